@@ -1,0 +1,225 @@
+/*
+ * rustyneedle.h — C ABI of the MI355X (gfx950) Needle token loop.
+ *
+ * The library replaces the CPU hot path of rustyneedle behind its own seams:
+ *   - the kernels API (QuantisedMatrix and the free functions re-exported at
+ *     crates/kernels/src/lib.rs:17-25),
+ *   - the model API (Model / Session, crates/model/src/session.rs:17-177),
+ *   - the greedy loop that the Engine trait drives
+ *     (crates/generate/src/generator.rs:199-265, crates/needle/src/engine.rs:14-18).
+ * Reference citations below are file:line in mcnairstudios/rustyneedle.
+ *
+ * Conventions
+ *   - Every entry point returns an int status: RN_OK (0) or a negative RN_ERR_*.
+ *     rn_last_error() returns the calling thread's last message. No C++
+ *     exception crosses the ABI. The reference panics on shape mismatches
+ *     (matrix.rs:156-157, neon.rs:44); here they are RN_ERR_ARGUMENT.
+ *   - Handles are opaque and freed by the caller. Device pointers passed to the
+ *     kernels API are caller-owned device memory (rn_malloc); `stream` is a
+ *     hipStream_t passed as void* (NULL = the default stream).
+ *   - Model / session entry points take host pointers for their inputs and
+ *     outputs and keep weights, caches and scratch resident in device memory.
+ *   - Numerics: int8 weight codes with one fp32 scale per `group` columns;
+ *     activations are quantised per row with an absmax scale (ops.rs:103-118);
+ *     the per-row product epilogue is sequential over groups, in the panel form
+ *     fmaf((float)acc, sW*sx, total) (panel.rs:184-188) for layer matrices and
+ *     the plane form total + ((float)acc*sW)*sx (neon.rs:180) for the tied
+ *     embedding. Integer accumulators and greedy token ids match the CPU
+ *     restatement bit for bit.
+ */
+#ifndef RUSTYNEEDLE_H
+#define RUSTYNEEDLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RN_ABI_VERSION 1
+
+enum {
+    RN_OK = 0,
+    RN_ERR_ARGUMENT = -1, /* bad shape, null pointer, unsupported geometry */
+    RN_ERR_DEVICE = -2,   /* a HIP call failed (no device, launch failure, ...) */
+    RN_ERR_CAPACITY = -3, /* a session would grow past its KV capacity */
+    RN_ERR_STATE = -4,    /* call out of order (e.g. logits before any push) */
+    RN_ERR_MEMORY = -5    /* device or host allocation failed */
+};
+
+/* Product epilogue form of a matrix (see the header comment). */
+enum { RN_FORM_PANEL = 0, RN_FORM_PLANE = 1 };
+
+const char* rn_last_error(void);
+int rn_abi_version(void);
+
+/* ---- device plumbing (no reference counterpart: the reference is host-only) ---- */
+int rn_device_count(int* count);
+int rn_device_set(int device);
+int rn_malloc(void** ptr, size_t bytes);
+int rn_free(void* ptr);
+int rn_memcpy_htod(void* dst, const void* src, size_t bytes);
+int rn_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int rn_memcpy_dtod(void* dst, const void* src, size_t bytes);
+int rn_stream_create(void** stream);
+int rn_stream_destroy(void* stream);
+int rn_stream_synchronize(void* stream);
+int rn_event_create(void** event);
+int rn_event_destroy(void* event);
+int rn_event_record(void* event, void* stream);
+int rn_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ---- kernels API: QuantisedMatrix (crates/kernels/src/matrix.rs:19-441) -------- */
+typedef struct rn_matrix rn_matrix;
+
+/* Replaces QuantisedMatrix::from_archive/from_parts (matrix.rs:35-59): host codes
+ * [rows][columns] int8 and scales [rows][columns/group] f32 are copied to the
+ * device. columns must be a multiple of 1024 or divide 1024 evenly with
+ * columns >= 512; group must be 32. */
+int rn_matrix_create_i8(const int8_t* codes, const float* scales, int rows, int columns, int group,
+                        int form, rn_matrix** out);
+int rn_matrix_free(rn_matrix* m);
+/* QuantisedMatrix::rows/columns/group (matrix.rs:61-75). */
+int rn_matrix_shape(const rn_matrix* m, int* rows, int* columns, int* group);
+
+/* QuantisedMatrix::multiply_vector (matrix.rs:155-165) with the activation
+ * quantisation of plane_input (matrix.rs:205-214) done on the device:
+ * y[rows] = W . quantise_int8(x[columns]). acc (nullable) receives the int32
+ * accumulator of every (row, group): [rows][columns/group]. Device pointers. */
+int rn_matrix_multiply_vector(const rn_matrix* m, const float* x, float* y, int32_t* acc, void* stream);
+
+/* QuantisedMatrix::multiply_fused (matrix.rs:167-193): one launch over `count`
+ * (<= 8) matrices of equal columns/group/form that share the input x. */
+int rn_matrix_multiply_fused(const rn_matrix* const* ms, int count, const float* x, float* const* ys,
+                             void* stream);
+
+/* QuantisedMatrix::multiply_batch (matrix.rs:330-389): x [count][columns],
+ * y [count][rows] token-major (matrix.rs:384-388). acc nullable:
+ * [count][rows][columns/group]. Runs on i8 MFMA. */
+int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, float* y, int32_t* acc,
+                             void* stream);
+
+/* QuantisedMatrix::dequantise_row (matrix.rs:140-153) for int8 codes: out[k] =
+ * code * scale(group of k). Host output of `columns` floats. */
+int rn_matrix_dequantise_row(const rn_matrix* m, int row, float* out);
+
+/* ops::quantise_int8 (ops.rs:112-118) for `count` rows of `columns` floats on
+ * the device: codes [count][columns], scales [count]. */
+int rn_quantise_int8(const float* x, int count, int columns, int8_t* codes, float* scales, void* stream);
+
+/* ops::fast_exp (ops.rs:82-90) and ops::silu (ops.rs:73-76) applied elementwise
+ * on the device (exposed for parity checks of the transcendental semantics). */
+int rn_fast_exp(const float* x, float* y, int n, void* stream);
+int rn_silu(const float* x, float* y, int n, void* stream);
+
+/* ops::zero_centred_norm (ops.rs:44-50) for `count` rows of `n` floats on the
+ * device (n a multiple of 8, <= 4096). */
+int rn_zero_centred_norm(const float* x, const float* gain, int count, int n, float* out, void* stream);
+
+/* kernels::attend_head (kernels/src/attention.rs:251-280) over an fp16 cache for
+ * `count` independent (query, cache) problems: q [count][head_dim] f32 (already
+ * rotated), K/V [count][stride][head_dim] fp16 bits, lengths [count] int32 (<=
+ * stride), out [count][head_dim]. head_dim must be 64. Device pointers. */
+int rn_attend_heads(const float* q, const uint16_t* K, const uint16_t* V, const int32_t* lengths,
+                    int count, int stride, int head_dim, float* out, void* stream);
+
+/* ---- model API: Model / Session (crates/model/src/model.rs, session.rs) -------- */
+typedef struct {
+    int layers, d_model, heads, head_dim, ffn, vocab, group, max_positions;
+    float rope_theta, norm_eps;
+} rn_config;
+
+typedef struct { const int8_t* codes; const float* scales; } rn_qmat_host;
+
+typedef struct {
+    rn_qmat_host qkv;     /* [3*d][d]: rows q (heads*head_dim), then k, then v */
+    rn_qmat_host out;     /* [d][d] */
+    rn_qmat_host gate_up; /* [2*ffn][d]: gate rows 0..ffn-1, up rows ffn..2*ffn-1 */
+    rn_qmat_host down;    /* [d][ffn] */
+    const float* norm_attn; /* [d] zero-centred gains */
+    const float* norm_ffn;  /* [d] */
+} rn_layer_host;
+
+typedef struct {
+    rn_qmat_host embedding;  /* [vocab][d], tied with the logits product */
+    const float* norm_final; /* [d] */
+    const rn_layer_host* layers;
+} rn_weights_host;
+
+typedef struct rn_model rn_model;
+typedef struct rn_session rn_session;
+typedef struct rn_batch rn_batch;
+
+/* Model::open / Model::build (model.rs:51-74): uploads all weights and the
+ * rotary table (ops.rs:127-141, tabulated for max_positions). Supported
+ * geometry: d_model 512, head_dim 64, heads*head_dim == d_model, ffn 2048,
+ * group 32, vocab a multiple of 64. */
+int rn_model_create(const rn_config* config, const rn_weights_host* weights, rn_model** out);
+/* The same model built from the seeded synthetic generators (rn_synth_*) with
+ * the tensor names listed at rn_synth_tensor_name. */
+int rn_model_create_synthetic(const rn_config* config, uint64_t seed, rn_model** out);
+int rn_model_free(rn_model* model);
+int rn_model_config(const rn_model* model, rn_config* out);
+/* The tabulated rotary cos/sin, [max_positions][head_dim/2] each (host out). */
+int rn_model_rotary_table(const rn_model* model, float* cos_out, float* sin_out);
+
+/* Session::new (session.rs:30-42) with a device KV cache of `capacity` positions
+ * per layer and head (fp16, [layers][heads][capacity][head_dim]). */
+int rn_session_create(const rn_model* model, int capacity, rn_session** out);
+int rn_session_free(rn_session* session);
+/* Session: Clone (session.rs:17; generator.rs:45) — a device-to-device copy. */
+int rn_session_clone(const rn_session* session, rn_session** out);
+/* Session::len (session.rs:44-46). */
+int rn_session_len(const rn_session* session, int* length);
+/* Keep only the first `length` (<= len) cached positions. No reference
+ * counterpart: the reference returns to a prefix by cloning a base session
+ * (generator.rs:45); this does it in place without a device allocation. The
+ * hidden state is cleared until the next push or feed. */
+int rn_session_truncate(rn_session* session, int length);
+/* Replace the cache contents with `length` positions (host fp16 bits,
+ * [layers][heads][length][head_dim]); used to pre-fill a context. */
+int rn_session_set_cache(rn_session* session, int length, const uint16_t* keys, const uint16_t* values);
+/* Read the first `length` cached positions back (same layout). */
+int rn_session_get_cache(const rn_session* session, int length, uint16_t* keys, uint16_t* values);
+/* Session::push (session.rs:72-148). */
+int rn_session_push(rn_session* session, uint32_t token);
+/* Session::feed (session.rs:56-70): batched prefill on i8 MFMA products. */
+int rn_session_feed(rn_session* session, const uint32_t* tokens, int count);
+/* The final-norm hidden state after the last push/feed (host out, d_model). */
+int rn_session_hidden(const rn_session* session, float* out);
+/* Session::logits (session.rs:166-177) (host out, vocab floats). */
+int rn_session_logits(rn_session* session, float* out);
+/* Generator::run_turn's greedy loop (generator.rs:199-230, argmax at 257-265)
+ * without grammar: token = first; `steps` times { push(token); logits;
+ * token = argmax; ids[i] = token }. Each step is one replay of a captured
+ * hipGraph; the argmax stays on the device and feeds the next embedding. */
+int rn_session_decode_greedy(rn_session* session, uint32_t first, int steps, uint32_t* ids);
+/* The stream the session's work runs on (hipStream_t as void*). */
+int rn_session_stream(const rn_session* session, void** stream);
+
+/* ---- batched decode: `count` independent sequences advanced together --------- */
+/* Like `count` Sessions, but each step runs the products as M=count i8-MFMA
+ * GEMMs and the attention over `count` ragged caches in one launch. */
+int rn_batch_create(const rn_model* model, int count, int capacity, rn_batch** out);
+int rn_batch_free(rn_batch* batch);
+int rn_batch_set_cache(rn_batch* batch, int sequence, int length, const uint16_t* keys,
+                       const uint16_t* values);
+/* ids [count][steps] (host out). */
+int rn_batch_decode_greedy(rn_batch* batch, const uint32_t* first, int steps, uint32_t* ids);
+/* Per-sequence rn_session_truncate: lengths [count], each <= its current length. */
+int rn_batch_truncate(rn_batch* batch, const int32_t* lengths);
+int rn_batch_stream(const rn_batch* batch, void** stream);
+
+/* ---- seeded synthetic inputs (host memory; no reference counterpart) ---------- */
+/* SplitMix64 stream per tensor: state0 = seed ^ FNV-1a-64(name). */
+int rn_synth_codes(uint64_t seed, const char* name, int8_t* out, size_t n);  /* U{-127..127} */
+int rn_synth_uniform(uint64_t seed, const char* name, float lo, float hi, float* out, size_t n);
+int rn_synth_normal(uint64_t seed, const char* name, float sigma, float* out, size_t n);
+int rn_synth_normal_f16(uint64_t seed, const char* name, uint16_t* out, size_t n);
+int rn_synth_tokens(uint64_t seed, const char* name, uint32_t vocab, uint32_t* out, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,304 @@
+"""CPU oracle for the Needle token loop — test infrastructure, not the product.
+
+A ctypes view of ``oracle/librn_oracle.so`` (built from ``rn_oracle.c`` by
+``oracle/Makefile``). Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker or as the timed CPU baseline.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librn_oracle.so")
+
+FORM_PANEL = 0
+FORM_PLANE = 1
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (always rebuilds when sources changed)."""
+    subprocess.run(["make", "-C", HERE, "-s"], check=True)
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"oracle library missing: {LIB_PATH} (run oracle/Makefile)")
+    return C.CDLL(LIB_PATH)
+
+
+lib = _load()
+
+_f = C.c_float
+_i = C.c_int
+_p = C.c_void_p
+
+lib.ro_fast_exp.restype = _f
+lib.ro_fast_exp.argtypes = [_f]
+lib.ro_silu.restype = _f
+lib.ro_silu.argtypes = [_f]
+lib.ro_peak_magnitude.restype = _f
+lib.ro_peak_magnitude.argtypes = [_p, _i]
+lib.ro_int8_scale.restype = _f
+lib.ro_int8_scale.argtypes = [_p, _i]
+lib.ro_quantise_int8.restype = _f
+lib.ro_quantise_int8.argtypes = [_p, _i, _p]
+lib.ro_fake_quantise_int8.argtypes = [_p, _i]
+lib.ro_sum_of_squares.restype = _f
+lib.ro_sum_of_squares.argtypes = [_p, _i]
+lib.ro_zero_centred_norm.argtypes = [_p, _p, _i, _p]
+lib.ro_softmax_in_place.argtypes = [_p, _i]
+lib.ro_rotary_frequencies.argtypes = [_i, _f, _p]
+lib.ro_rotary_table.argtypes = [_i, _f, _i, _p, _p]
+lib.ro_apply_rotary.argtypes = [_p, _i, _p, _p]
+lib.ro_f32_to_f16.restype = C.c_uint16
+lib.ro_f32_to_f16.argtypes = [_f]
+lib.ro_f16_to_f32.restype = _f
+lib.ro_f16_to_f32.argtypes = [C.c_uint16]
+lib.ro_argmax.restype = C.c_uint32
+lib.ro_argmax.argtypes = [_p, _i]
+lib.ro_product.argtypes = [_i, _p, _p, _i, _i, _i, _p, _p, _i, _p, _p]
+lib.ro_multiply.argtypes = [_i, _p, _p, _i, _i, _i, _p, _i, _p, _p, _p, _p]
+lib.ro_attend_head.argtypes = [_p, _p, _p, _i, _i, _p]
+lib.ro_set_threads.argtypes = [_i]
+lib.ro_get_threads.restype = _i
+
+
+class Config(C.Structure):
+    _fields_ = [
+        ("layers", _i), ("d_model", _i), ("heads", _i), ("head_dim", _i), ("ffn", _i),
+        ("vocab", _i), ("group", _i), ("max_positions", _i),
+        ("rope_theta", _f), ("norm_eps", _f),
+    ]
+
+
+class QMat(C.Structure):
+    _fields_ = [("codes", _p), ("scales", _p)]
+
+
+class Layer(C.Structure):
+    _fields_ = [("qkv", QMat), ("out", QMat), ("gate_up", QMat), ("down", QMat),
+                ("norm_attn", _p), ("norm_ffn", _p)]
+
+
+class Model(C.Structure):
+    _fields_ = [("embedding", QMat), ("norm_final", _p), ("layers", _p),
+                ("rope_cos", _p), ("rope_sin", _p)]
+
+
+class Session(C.Structure):
+    _fields_ = [("keys", _p), ("values", _p), ("hidden", _p), ("capacity", _i), ("length", _i)]
+
+
+lib.ro_embed.argtypes = [C.POINTER(Config), C.POINTER(Model), C.c_uint32, _p]
+lib.ro_session_push.argtypes = [C.POINTER(Config), C.POINTER(Model), C.POINTER(Session), C.c_uint32]
+lib.ro_session_prefill.argtypes = [C.POINTER(Config), C.POINTER(Model), C.POINTER(Session), _p, _i]
+lib.ro_session_logits.argtypes = [C.POINTER(Config), C.POINTER(Model), C.POINTER(Session), _p]
+lib.ro_greedy.argtypes = [C.POINTER(Config), C.POINTER(Model), C.POINTER(Session), C.c_uint32, _i, _p]
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def set_threads(n: int) -> None:
+    lib.ro_set_threads(int(n))
+
+
+def fast_exp(v: float) -> float:
+    return lib.ro_fast_exp(float(v))
+
+
+def silu(v: float) -> float:
+    return lib.ro_silu(float(v))
+
+
+def int8_scale(x) -> float:
+    x = _f32(x)
+    return lib.ro_int8_scale(_ptr(x), x.size)
+
+
+def quantise_int8(x):
+    x = _f32(x)
+    codes = np.empty(x.size, dtype=np.int8)
+    scale = lib.ro_quantise_int8(_ptr(x), x.size, _ptr(codes))
+    return codes, np.float32(scale)
+
+
+def fake_quantise_int8(x) -> np.ndarray:
+    x = _f32(x).copy()
+    lib.ro_fake_quantise_int8(_ptr(x), x.size)
+    return x
+
+
+def sum_of_squares(x) -> float:
+    x = _f32(x)
+    return lib.ro_sum_of_squares(_ptr(x), x.size)
+
+
+def zero_centred_norm(x, gain) -> np.ndarray:
+    x = _f32(x)
+    gain = _f32(gain)
+    out = np.empty_like(x)
+    lib.ro_zero_centred_norm(_ptr(x), _ptr(gain), x.size, _ptr(out))
+    return out
+
+
+def softmax(v) -> np.ndarray:
+    v = _f32(v).copy()
+    lib.ro_softmax_in_place(_ptr(v), v.size)
+    return v
+
+
+def rotary_frequencies(head_dim: int, theta: float) -> np.ndarray:
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    lib.ro_rotary_frequencies(head_dim, theta, _ptr(out))
+    return out
+
+
+def rotary_table(head_dim: int, theta: float, positions: int):
+    cos = np.empty((positions, head_dim // 2), dtype=np.float32)
+    sin = np.empty_like(cos)
+    lib.ro_rotary_table(head_dim, theta, positions, _ptr(cos), _ptr(sin))
+    return cos, sin
+
+
+def apply_rotary(head, cos_row, sin_row) -> np.ndarray:
+    head = _f32(head).copy()
+    cos_row, sin_row = _f32(cos_row), _f32(sin_row)
+    lib.ro_apply_rotary(_ptr(head), head.size, _ptr(cos_row), _ptr(sin_row))
+    return head
+
+
+def f32_to_f16(v: float) -> int:
+    return lib.ro_f32_to_f16(float(v))
+
+
+def f16_to_f32(bits: int) -> float:
+    return lib.ro_f16_to_f32(int(bits))
+
+
+def argmax(values) -> int:
+    values = _f32(values)
+    return int(lib.ro_argmax(_ptr(values), values.size))
+
+
+def product(form, W, sW, xq, sx, group=32, with_acc=False):
+    """y[count][rows] (and acc[count][rows][groups]) from pre-quantised inputs."""
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    sW = _f32(sW)
+    xq = np.ascontiguousarray(np.atleast_2d(xq), dtype=np.int8)
+    sx = _f32(np.atleast_1d(sx))
+    rows, cols = W.shape
+    count = xq.shape[0]
+    y = np.empty((count, rows), dtype=np.float32)
+    acc = np.empty((count, rows, cols // group), dtype=np.int32) if with_acc else None
+    lib.ro_product(form, _ptr(W), _ptr(sW), rows, cols, group, _ptr(xq), _ptr(sx), count, _ptr(y),
+                   _ptr(acc) if with_acc else None)
+    return (y, acc) if with_acc else y
+
+
+def multiply(form, W, sW, x, group=32, with_acc=False):
+    """Quantise each input row (quantise_int8) and multiply: returns y, acc, codes, scales."""
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    sW = _f32(sW)
+    x = _f32(np.atleast_2d(x))
+    rows, cols = W.shape
+    count = x.shape[0]
+    y = np.empty((count, rows), dtype=np.float32)
+    acc = np.empty((count, rows, cols // group), dtype=np.int32) if with_acc else None
+    codes = np.empty((count, cols), dtype=np.int8)
+    scales = np.empty(count, dtype=np.float32)
+    lib.ro_multiply(form, _ptr(W), _ptr(sW), rows, cols, group, _ptr(x), count, _ptr(y),
+                    _ptr(acc) if with_acc else None, _ptr(codes), _ptr(scales))
+    return y, acc, codes, scales
+
+
+def attend_head(q, K, V) -> np.ndarray:
+    """q: [hd] f32; K, V: [L][hd] float16 (or uint16 bits)."""
+    q = _f32(q)
+    K = np.ascontiguousarray(K).view(np.uint16)
+    V = np.ascontiguousarray(V).view(np.uint16)
+    L, hd = K.shape
+    out = np.empty(hd, dtype=np.float32)
+    lib.ro_attend_head(_ptr(q), _ptr(K), _ptr(V), hd, L, _ptr(out))
+    return out
+
+
+class OracleModel:
+    """Holds numpy weights (the same host arrays handed to the GPU model) and the
+    ctypes structs the oracle reads. `weights` is the dict produced by
+    rustyneedle_amd.synthetic_weights (or any dict with the same keys)."""
+
+    def __init__(self, config: dict, weights: dict):
+        self.config = dict(config)
+        c = self.config
+        self.cfg = Config(c["layers"], c["d_model"], c["heads"], c["head_dim"], c["ffn"], c["vocab"],
+                          c["group"], c["max_positions"], c["rope_theta"], c["norm_eps"])
+        self.w = weights
+        self.rope_cos, self.rope_sin = rotary_table(c["head_dim"], c["rope_theta"], c["max_positions"])
+        layers = (Layer * c["layers"])()
+        for l in range(c["layers"]):
+            lw = weights["layers"][l]
+            layers[l] = Layer(QMat(_ptr(lw["qkv"][0]), _ptr(lw["qkv"][1])),
+                              QMat(_ptr(lw["out"][0]), _ptr(lw["out"][1])),
+                              QMat(_ptr(lw["gate_up"][0]), _ptr(lw["gate_up"][1])),
+                              QMat(_ptr(lw["down"][0]), _ptr(lw["down"][1])),
+                              _ptr(lw["norm_attn"]), _ptr(lw["norm_ffn"]))
+        self._layers = layers
+        emb = weights["embedding"]
+        self.model = Model(QMat(_ptr(emb[0]), _ptr(emb[1])), _ptr(weights["norm_final"]),
+                           C.addressof(layers), _ptr(self.rope_cos), _ptr(self.rope_sin))
+
+    def session(self, capacity: int) -> "OracleSession":
+        return OracleSession(self, capacity)
+
+
+class OracleSession:
+    def __init__(self, model: OracleModel, capacity: int):
+        c = model.config
+        self.model = model
+        shape = (c["layers"], c["heads"], capacity, c["head_dim"])
+        self.keys = np.zeros(shape, dtype=np.uint16)
+        self.values = np.zeros(shape, dtype=np.uint16)
+        self.hidden = np.zeros(c["d_model"], dtype=np.float32)
+        self.s = Session(_ptr(self.keys), _ptr(self.values), _ptr(self.hidden), capacity, 0)
+
+    @property
+    def length(self) -> int:
+        return self.s.length
+
+    def set_cache(self, keys: np.ndarray, values: np.ndarray) -> None:
+        """keys/values: [layers][heads][length][hd] float16 or uint16 bits."""
+        length = keys.shape[2]
+        self.keys[:, :, :length] = np.asarray(keys).view(np.uint16)
+        self.values[:, :, :length] = np.asarray(values).view(np.uint16)
+        self.s.length = length
+
+    def push(self, token: int) -> None:
+        lib.ro_session_push(C.byref(self.model.cfg), C.byref(self.model.model), C.byref(self.s), token)
+
+    def feed(self, tokens) -> None:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        lib.ro_session_prefill(C.byref(self.model.cfg), C.byref(self.model.model), C.byref(self.s),
+                               _ptr(t), t.size)
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.model.config["vocab"], dtype=np.float32)
+        lib.ro_session_logits(C.byref(self.model.cfg), C.byref(self.model.model), C.byref(self.s), _ptr(out))
+        return out
+
+    def greedy(self, first: int, steps: int) -> np.ndarray:
+        ids = np.empty(steps, dtype=np.uint32)
+        lib.ro_greedy(C.byref(self.model.cfg), C.byref(self.model.model), C.byref(self.s), first, steps,
+                      _ptr(ids))
+        return ids

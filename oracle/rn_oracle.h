@@ -1,0 +1,140 @@
+/*
+ * rn_oracle.h — CPU oracle for the Needle token loop (test infrastructure).
+ *
+ * This is NOT part of the product. It is a plain-C restatement of the reference
+ * numerics (rustyneedle, crates/kernels, crates/model, crates/generate) at the
+ * synthetic int8 configuration: int8 weight codes with one fp32 scale per
+ * 32-element group along K, per-row int8 activation quantisation, an fp16 KV
+ * cache, a single residual stream and a gated FFN. Only tests/, the smoke check
+ * in __graft_entry__.py and the cpu_baseline leg of bench.py may load it, and
+ * only as the checker or as the timed CPU baseline — never as the product path.
+ *
+ * Every float operation is written out in the order the kernels use; the file
+ * is compiled with -ffp-contract=off so that `a * b + c` is two roundings and
+ * `fmaf` is the only fused operation. Reductions whose order the reference
+ * leaves platform-dependent (its NEON and x86 paths sum in different orders)
+ * are fixed here as the canonical trees below, and the HIP kernels implement
+ * exactly the same trees:
+ *
+ *   T1 sum of squares (RMSNorm): eight strided lanes, each summed in index
+ *      order, lanes then added 0..7, then the tail — ops.rs:7-17 verbatim.
+ *   T2 attention score q.k over head_dim = 16*c dims: sixteen sub-sums of c
+ *      consecutive dims (each 0 + q0k0 + q1k1 + ... in order), then a balanced
+ *      pairwise tree over the sixteen sub-sums in index order.
+ *   T3 softmax total and P.V over L positions: sixteen interleaved partial sums
+ *      (position p goes to partial p mod 16, added in increasing p, starting
+ *      from 0), then the sixteen partials added 0..15 starting from 0.
+ *   T4 product epilogue per (token, row): sequential over groups g = 0..G-1.
+ *      Panel form (layer matrices, panel.rs:184-188):
+ *          total = fmaf((float)acc_g, sW[g] * sx, total)
+ *      Plane form (tied embedding / logits, neon.rs:180):
+ *          total = total + ((float)acc_g * sW[g]) * sx
+ *   Integer accumulators are exact and therefore order-free.
+ *
+ * Parity pins (tests/test_oracle_*.py): integer accumulators against an int64
+ * brute force; fast_exp and softmax against the reference's own bounds
+ * (crates/kernels/tests/softmax.rs); quantisation against tie/clamp/zero
+ * known answers; RMSNorm, rotary, attention and the decoder step against
+ * float64 restatements within stated tolerances; argmax against the tie and
+ * NaN rules of generator.rs:257-265.
+ */
+#ifndef RN_ORACLE_H
+#define RN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar and vector primitives: crates/kernels/src/ops.rs ---------------- */
+float ro_fast_exp(float value);                                     /* ops.rs:82-90   */
+float ro_silu(float value);                                         /* ops.rs:73-76   */
+float ro_peak_magnitude(const float* x, int n);                     /* ops.rs:32-42   */
+float ro_int8_scale(const float* x, int n);                         /* ops.rs:103-110 */
+float ro_quantise_int8(const float* x, int n, int8_t* codes);       /* ops.rs:112-118 */
+void ro_fake_quantise_int8(float* x, int n);                        /* ops.rs:120-125 */
+float ro_sum_of_squares(const float* x, int n);                     /* ops.rs:7-17    */
+void ro_zero_centred_norm(const float* x, const float* gain, int n, float* out); /* ops.rs:44-50 */
+void ro_softmax_in_place(float* v, int n);                          /* ops.rs:92-101  */
+void ro_rotary_frequencies(int head_dim, float theta, float* freqs); /* ops.rs:127-129 */
+/* cos/sin of position * freq[i] for every position < positions: [positions][head_dim/2] */
+void ro_rotary_table(int head_dim, float theta, int positions, float* cos_tab, float* sin_tab);
+void ro_apply_rotary(float* head, int head_dim, const float* cos_row, const float* sin_row); /* ops.rs:131-141 */
+uint16_t ro_f32_to_f16(float value);
+float ro_f16_to_f32(uint16_t bits);
+uint32_t ro_argmax(const float* values, int n);                     /* generator.rs:257-265 */
+
+/* ---- quantised products ------------------------------------------------------ */
+enum { RO_FORM_PANEL = 0, RO_FORM_PLANE = 1 };
+/* y[t*rows + n] for t < count; acc (nullable) is [count][rows][cols/group] int32. */
+void ro_product(int form, const int8_t* W, const float* sW, int rows, int cols, int group,
+                const int8_t* xq, const float* sx, int count, float* y, int32_t* acc);
+/* quantise_int8 each of `count` input rows of `cols` floats, then ro_product.
+ * codes (nullable) receives [count][cols], scales (nullable) [count]. */
+void ro_multiply(int form, const int8_t* W, const float* sW, int rows, int cols, int group,
+                 const float* x, int count, float* y, int32_t* acc, int8_t* codes, float* scales);
+
+/* ---- attention over an fp16 cache (kernels/src/attention.rs:251-280 restated) -- */
+/* q: head_dim floats (already rotated); K, V: [length][head_dim] fp16 bits. */
+void ro_attend_head(const float* q, const uint16_t* K, const uint16_t* V, int head_dim, int length,
+                    float* out);
+
+/* ---- decoder model and session (crates/model/src/session.rs, prefill.rs) ------ */
+typedef struct {
+    int layers, d_model, heads, head_dim, ffn, vocab, group, max_positions;
+    float rope_theta, norm_eps;
+} ro_config;
+
+typedef struct { const int8_t* codes; const float* scales; } ro_qmat;
+
+typedef struct {
+    ro_qmat qkv;      /* [3*d][d]  rows: q (heads*head_dim), k, v            */
+    ro_qmat out;      /* [d][d]                                              */
+    ro_qmat gate_up;  /* [2*ffn][d] rows: gate 0..ffn-1, up ffn..2*ffn-1      */
+    ro_qmat down;     /* [d][ffn]                                            */
+    const float* norm_attn;  /* [d] zero-centred gains */
+    const float* norm_ffn;   /* [d] */
+} ro_layer;
+
+typedef struct {
+    ro_qmat embedding;         /* [vocab][d], tied with the logits product */
+    const float* norm_final;   /* [d] */
+    const ro_layer* layers;    /* [layers] */
+    const float* rope_cos;     /* [max_positions][head_dim/2] */
+    const float* rope_sin;
+} ro_model;
+
+/* A session owns its caches: keys/values are [layers][heads][capacity][head_dim]
+ * fp16 bits; hidden is [d_model]; length counts the cached positions. */
+typedef struct {
+    uint16_t* keys;
+    uint16_t* values;
+    float* hidden;
+    int capacity;
+    int length;
+} ro_session;
+
+void ro_embed(const ro_config* c, const ro_model* m, uint32_t token, float* x);
+/* Session::push_with (session.rs:76-148) for the config's block. */
+void ro_session_push(const ro_config* c, const ro_model* m, ro_session* s, uint32_t token);
+/* Session::prefill (prefill.rs:10-99): the same per-token arithmetic, batched. */
+void ro_session_prefill(const ro_config* c, const ro_model* m, ro_session* s,
+                        const uint32_t* tokens, int count);
+/* Session::logits (session.rs:166-177). */
+void ro_session_logits(const ro_config* c, const ro_model* m, const ro_session* s, float* logits);
+/* The greedy loop of generator.rs:199-230 without grammar: starting from
+ * token = first, `steps` times { push(token); logits; token = argmax; record }.
+ * The last recorded token is not pushed. */
+void ro_greedy(const ro_config* c, const ro_model* m, ro_session* s, uint32_t first, int steps,
+               uint32_t* ids);
+
+/* Threads used by products and head-parallel attention (1 = scalar). */
+void ro_set_threads(int threads);
+int ro_get_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

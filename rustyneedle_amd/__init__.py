@@ -1,0 +1,585 @@
+"""rustyneedle_amd — the Needle token loop on MI355X (gfx950).
+
+A thin Python view of ``librustyneedle_hip.so`` (the C ABI declared in
+``include/rustyneedle.h``). Names mirror the reference's kernels / model API
+(``QuantisedMatrix``, ``Model``, ``Session``) so that tests read like the
+reference's own. Loading fails loudly when the HIP library has not been built:
+there is no CPU fallback anywhere in this package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librustyneedle_hip.so")
+
+RN_OK = 0
+RN_ERR_ARGUMENT = -1
+RN_ERR_DEVICE = -2
+RN_ERR_CAPACITY = -3
+RN_ERR_STATE = -4
+RN_ERR_MEMORY = -5
+
+FORM_PANEL = 0
+FORM_PLANE = 1
+
+# The decoder of the decode / prefill / batch workloads: 20 layers, d_model 512,
+# 8 heads of 64, rotary base 10000, RMSNorm eps 1e-6, gated FFN 512->2048->512,
+# int8 codes with one fp32 scale per 32 columns, tied int8 vocab 8192.
+NEEDLE_DECODER = dict(layers=20, d_model=512, heads=8, head_dim=64, ffn=2048, vocab=8192, group=32,
+                      max_positions=1024, rope_theta=10000.0, norm_eps=1e-6)
+SEED = 20261201
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                          "(hipcc --offload-arch=gfx950); there is no CPU fallback")
+    return C.CDLL(LIB_PATH)
+
+
+lib = _load()
+
+_i, _f, _p, _u32, _u64, _sz = C.c_int, C.c_float, C.c_void_p, C.c_uint32, C.c_uint64, C.c_size_t
+
+
+class Config(C.Structure):
+    _fields_ = [("layers", _i), ("d_model", _i), ("heads", _i), ("head_dim", _i), ("ffn", _i),
+                ("vocab", _i), ("group", _i), ("max_positions", _i), ("rope_theta", _f), ("norm_eps", _f)]
+
+
+class QMatHost(C.Structure):
+    _fields_ = [("codes", _p), ("scales", _p)]
+
+
+class LayerHost(C.Structure):
+    _fields_ = [("qkv", QMatHost), ("out", QMatHost), ("gate_up", QMatHost), ("down", QMatHost),
+                ("norm_attn", _p), ("norm_ffn", _p)]
+
+
+class WeightsHost(C.Structure):
+    _fields_ = [("embedding", QMatHost), ("norm_final", _p), ("layers", _p)]
+
+
+# Every symbol of include/rustyneedle.h with its signature (restype int unless noted).
+SIGNATURES = {
+    "rn_last_error": (C.c_char_p, []),
+    "rn_abi_version": (_i, []),
+    "rn_device_count": (_i, [C.POINTER(_i)]),
+    "rn_device_set": (_i, [_i]),
+    "rn_malloc": (_i, [C.POINTER(_p), _sz]),
+    "rn_free": (_i, [_p]),
+    "rn_memcpy_htod": (_i, [_p, _p, _sz]),
+    "rn_memcpy_dtoh": (_i, [_p, _p, _sz]),
+    "rn_memcpy_dtod": (_i, [_p, _p, _sz]),
+    "rn_stream_create": (_i, [C.POINTER(_p)]),
+    "rn_stream_destroy": (_i, [_p]),
+    "rn_stream_synchronize": (_i, [_p]),
+    "rn_event_create": (_i, [C.POINTER(_p)]),
+    "rn_event_destroy": (_i, [_p]),
+    "rn_event_record": (_i, [_p, _p]),
+    "rn_event_elapsed_ms": (_i, [_p, _p, C.POINTER(_f)]),
+    "rn_matrix_create_i8": (_i, [_p, _p, _i, _i, _i, _i, C.POINTER(_p)]),
+    "rn_matrix_free": (_i, [_p]),
+    "rn_matrix_shape": (_i, [_p, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i)]),
+    "rn_matrix_multiply_vector": (_i, [_p, _p, _p, _p, _p]),
+    "rn_matrix_multiply_fused": (_i, [C.POINTER(_p), _i, _p, C.POINTER(_p), _p]),
+    "rn_matrix_multiply_batch": (_i, [_p, _p, _i, _p, _p, _p]),
+    "rn_matrix_dequantise_row": (_i, [_p, _i, _p]),
+    "rn_quantise_int8": (_i, [_p, _i, _i, _p, _p, _p]),
+    "rn_fast_exp": (_i, [_p, _p, _i, _p]),
+    "rn_silu": (_i, [_p, _p, _i, _p]),
+    "rn_zero_centred_norm": (_i, [_p, _p, _i, _i, _p, _p]),
+    "rn_attend_heads": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, _p]),
+    "rn_model_create": (_i, [C.POINTER(Config), C.POINTER(WeightsHost), C.POINTER(_p)]),
+    "rn_model_create_synthetic": (_i, [C.POINTER(Config), _u64, C.POINTER(_p)]),
+    "rn_model_free": (_i, [_p]),
+    "rn_model_config": (_i, [_p, C.POINTER(Config)]),
+    "rn_model_rotary_table": (_i, [_p, _p, _p]),
+    "rn_session_create": (_i, [_p, _i, C.POINTER(_p)]),
+    "rn_session_free": (_i, [_p]),
+    "rn_session_clone": (_i, [_p, C.POINTER(_p)]),
+    "rn_session_len": (_i, [_p, C.POINTER(_i)]),
+    "rn_session_truncate": (_i, [_p, _i]),
+    "rn_session_set_cache": (_i, [_p, _i, _p, _p]),
+    "rn_session_get_cache": (_i, [_p, _i, _p, _p]),
+    "rn_session_push": (_i, [_p, _u32]),
+    "rn_session_feed": (_i, [_p, _p, _i]),
+    "rn_session_hidden": (_i, [_p, _p]),
+    "rn_session_logits": (_i, [_p, _p]),
+    "rn_session_decode_greedy": (_i, [_p, _u32, _i, _p]),
+    "rn_session_stream": (_i, [_p, C.POINTER(_p)]),
+    "rn_batch_create": (_i, [_p, _i, _i, C.POINTER(_p)]),
+    "rn_batch_free": (_i, [_p]),
+    "rn_batch_set_cache": (_i, [_p, _i, _i, _p, _p]),
+    "rn_batch_decode_greedy": (_i, [_p, _p, _i, _p]),
+    "rn_batch_stream": (_i, [_p, C.POINTER(_p)]),
+    "rn_batch_truncate": (_i, [_p, _p]),
+    "rn_synth_codes": (_i, [_u64, C.c_char_p, _p, _sz]),
+    "rn_synth_uniform": (_i, [_u64, C.c_char_p, _f, _f, _p, _sz]),
+    "rn_synth_normal": (_i, [_u64, C.c_char_p, _f, _p, _sz]),
+    "rn_synth_normal_f16": (_i, [_u64, C.c_char_p, _p, _sz]),
+    "rn_synth_tokens": (_i, [_u64, C.c_char_p, _u32, _p, _sz]),
+}
+
+for _name, (_res, _args) in SIGNATURES.items():
+    _fn = getattr(lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+class RnError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+def check(rc: int) -> None:
+    if rc != RN_OK:
+        raise RnError(rc, lib.rn_last_error().decode(errors="replace"))
+
+
+def _ptr(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "arrays handed to the C ABI must be contiguous"
+    return a.ctypes.data
+
+
+def device_count() -> int:
+    n = _i(0)
+    check(lib.rn_device_count(C.byref(n)))
+    return n.value
+
+
+# ---- device plumbing --------------------------------------------------------------
+
+class DeviceBuffer:
+    """Device memory owned by Python (rn_malloc/rn_free)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _p()
+        check(lib.rn_malloc(C.byref(p), max(self.nbytes, 1)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(lib.rn_memcpy_htod(self.ptr, _ptr(a), a.nbytes))
+
+    def download(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        check(lib.rn_memcpy_dtoh(_ptr(out), self.ptr, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            check(lib.rn_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if getattr(self, "ptr", None):
+                lib.rn_free(self.ptr)
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        p = _p()
+        check(lib.rn_stream_create(C.byref(p)))
+        self.handle = p.value
+
+    def synchronize(self) -> None:
+        check(lib.rn_stream_synchronize(self.handle))
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_stream_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        p = _p()
+        check(lib.rn_event_create(C.byref(p)))
+        self.handle = p.value
+
+    def record(self, stream) -> None:
+        check(lib.rn_event_record(self.handle, stream))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = _f(0)
+        check(lib.rn_event_elapsed_ms(self.handle, end.handle, C.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+# ---- kernels API ------------------------------------------------------------------
+
+class QuantisedMatrix:
+    """crates/kernels/src/matrix.rs:19-441 for int8 codes and fp32 per-32 scales."""
+
+    def __init__(self, codes: np.ndarray, scales: np.ndarray, form: int = FORM_PANEL, group: int = 32):
+        codes = np.ascontiguousarray(codes, dtype=np.int8)
+        scales = np.ascontiguousarray(scales, dtype=np.float32)
+        rows, cols = codes.shape
+        assert scales.shape == (rows, cols // group)
+        h = _p()
+        check(lib.rn_matrix_create_i8(_ptr(codes), _ptr(scales), rows, cols, group, form, C.byref(h)))
+        self.handle = h.value
+        self.rows, self.columns, self.group, self.form = rows, cols, group, form
+
+    def multiply_vector(self, x_dev: int, y_dev: int, acc_dev: Optional[int] = None, stream=None) -> None:
+        check(lib.rn_matrix_multiply_vector(self.handle, x_dev, y_dev, acc_dev, stream))
+
+    def multiply_vector_host(self, x: np.ndarray, with_acc: bool = False):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        assert x.shape == (self.columns,)
+        xd = DeviceBuffer.from_array(x)
+        yd = DeviceBuffer(4 * self.rows)
+        ad = DeviceBuffer(4 * self.rows * (self.columns // self.group)) if with_acc else None
+        self.multiply_vector(xd.ptr, yd.ptr, ad.ptr if ad else None)
+        check(lib.rn_stream_synchronize(None))
+        y = yd.download(np.float32, (self.rows,))
+        if with_acc:
+            return y, ad.download(np.int32, (self.rows, self.columns // self.group))
+        return y
+
+    def multiply_batch_host(self, x: np.ndarray, with_acc: bool = False):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        count = x.shape[0]
+        assert x.shape == (count, self.columns)
+        xd = DeviceBuffer.from_array(x)
+        yd = DeviceBuffer(4 * count * self.rows)
+        ad = DeviceBuffer(4 * count * self.rows * (self.columns // self.group)) if with_acc else None
+        check(lib.rn_matrix_multiply_batch(self.handle, xd.ptr, count, yd.ptr, ad.ptr if ad else None, None))
+        check(lib.rn_stream_synchronize(None))
+        y = yd.download(np.float32, (count, self.rows))
+        if with_acc:
+            return y, ad.download(np.int32, (count, self.rows, self.columns // self.group))
+        return y
+
+    def dequantise_row(self, row: int) -> np.ndarray:
+        out = np.empty(self.columns, dtype=np.float32)
+        check(lib.rn_matrix_dequantise_row(self.handle, row, _ptr(out)))
+        return out
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_matrix_free(self.handle)
+        except Exception:
+            pass
+
+
+def multiply_fused_host(matrices, x: np.ndarray):
+    """QuantisedMatrix::multiply_fused (matrix.rs:167-193) on one shared input."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    xd = DeviceBuffer.from_array(x)
+    outs = [DeviceBuffer(4 * m.rows) for m in matrices]
+    hs = (_p * len(matrices))(*[m.handle for m in matrices])
+    ys = (_p * len(matrices))(*[o.ptr for o in outs])
+    check(lib.rn_matrix_multiply_fused(hs, len(matrices), xd.ptr, ys, None))
+    check(lib.rn_stream_synchronize(None))
+    return [o.download(np.float32, (m.rows,)) for o, m in zip(outs, matrices)]
+
+
+def _elementwise(fn, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    xd = DeviceBuffer.from_array(x)
+    yd = DeviceBuffer(x.nbytes)
+    check(fn(xd.ptr, yd.ptr, x.size, None))
+    check(lib.rn_stream_synchronize(None))
+    return yd.download(np.float32, x.shape)
+
+
+def fast_exp(x: np.ndarray) -> np.ndarray:
+    return _elementwise(lib.rn_fast_exp, x)
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    return _elementwise(lib.rn_silu, x)
+
+
+def quantise_int8(x: np.ndarray):
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    count, cols = x.shape
+    xd = DeviceBuffer.from_array(x)
+    cd = DeviceBuffer(count * cols)
+    sd = DeviceBuffer(4 * count)
+    check(lib.rn_quantise_int8(xd.ptr, count, cols, cd.ptr, sd.ptr, None))
+    check(lib.rn_stream_synchronize(None))
+    return cd.download(np.int8, (count, cols)), sd.download(np.float32, (count,))
+
+
+def zero_centred_norm(x: np.ndarray, gain: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    count, n = x.shape
+    xd = DeviceBuffer.from_array(x)
+    gd = DeviceBuffer.from_array(np.ascontiguousarray(gain, dtype=np.float32))
+    od = DeviceBuffer(x.nbytes)
+    check(lib.rn_zero_centred_norm(xd.ptr, gd.ptr, count, n, od.ptr, None))
+    check(lib.rn_stream_synchronize(None))
+    return od.download(np.float32, (count, n))
+
+
+def attend_heads(q: np.ndarray, K: np.ndarray, V: np.ndarray, lengths: np.ndarray) -> np.ndarray:
+    """q [count][64] f32; K, V [count][stride][64] float16; lengths [count]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    K = np.ascontiguousarray(K, dtype=np.float16)
+    V = np.ascontiguousarray(V, dtype=np.float16)
+    lengths = np.ascontiguousarray(lengths, dtype=np.int32)
+    count, stride, hd = K.shape
+    bufs = [DeviceBuffer.from_array(a) for a in (q, K, V, lengths)]
+    od = DeviceBuffer(4 * count * hd)
+    check(lib.rn_attend_heads(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, count, stride, hd, od.ptr, None))
+    check(lib.rn_stream_synchronize(None))
+    return od.download(np.float32, (count, hd))
+
+
+# ---- synthetic inputs ---------------------------------------------------------------
+
+def synth_codes(seed: int, name: str, shape) -> np.ndarray:
+    out = np.empty(shape, dtype=np.int8)
+    check(lib.rn_synth_codes(seed, name.encode(), _ptr(out), out.size))
+    return out
+
+
+def synth_uniform(seed: int, name: str, lo: float, hi: float, shape) -> np.ndarray:
+    out = np.empty(shape, dtype=np.float32)
+    check(lib.rn_synth_uniform(seed, name.encode(), lo, hi, _ptr(out), out.size))
+    return out
+
+
+def synth_normal(seed: int, name: str, sigma: float, shape) -> np.ndarray:
+    out = np.empty(shape, dtype=np.float32)
+    check(lib.rn_synth_normal(seed, name.encode(), sigma, _ptr(out), out.size))
+    return out
+
+
+def synth_normal_f16(seed: int, name: str, shape) -> np.ndarray:
+    out = np.empty(shape, dtype=np.uint16)
+    check(lib.rn_synth_normal_f16(seed, name.encode(), _ptr(out), out.size))
+    return out.view(np.float16)
+
+
+def synth_tokens(seed: int, name: str, vocab: int, shape) -> np.ndarray:
+    out = np.empty(shape, dtype=np.uint32)
+    check(lib.rn_synth_tokens(seed, name.encode(), vocab, _ptr(out), out.size))
+    return out
+
+
+def synthetic_weights(config: dict, seed: int = SEED) -> dict:
+    """The tensors rn_model_create_synthetic draws, by the same names: codes
+    U{-127..127}, scales U[1e-3, 1e-2], zero-centred gains N(0, 0.1)."""
+    d, f, vocab = config["d_model"], config["ffn"], config["vocab"]
+
+    def q(name, rows, cols):
+        return (synth_codes(seed, name + ".codes", (rows, cols)),
+                synth_uniform(seed, name + ".scales", 1e-3, 1e-2, (rows, cols // 32)))
+
+    layers = []
+    for l in range(config["layers"]):
+        p = f"layers.{l}."
+        layers.append(dict(qkv=q(p + "qkv", 3 * d, d), out=q(p + "out", d, d),
+                           gate_up=q(p + "gate_up", 2 * f, d), down=q(p + "down", d, f),
+                           norm_attn=synth_normal(seed, p + "norm_attn", 0.1, (d,)),
+                           norm_ffn=synth_normal(seed, p + "norm_ffn", 0.1, (d,))))
+    return dict(layers=layers, embedding=q("embedding", vocab, d),
+                norm_final=synth_normal(seed, "norm_final", 0.1, (d,)))
+
+
+def synthetic_cache(config: dict, length: int, name: str, seed: int = SEED):
+    """N(0,1) fp16 keys and values [layers][heads][length][head_dim]."""
+    shape = (config["layers"], config["heads"], length, config["head_dim"])
+    return synth_normal_f16(seed, name + ".k", shape), synth_normal_f16(seed, name + ".v", shape)
+
+
+# ---- model API ----------------------------------------------------------------------
+
+def _config_struct(config: dict) -> Config:
+    return Config(config["layers"], config["d_model"], config["heads"], config["head_dim"], config["ffn"],
+                  config["vocab"], config["group"], config["max_positions"], config["rope_theta"],
+                  config["norm_eps"])
+
+
+class Model:
+    """Model::open / Model::build (crates/model/src/model.rs:51-74)."""
+
+    def __init__(self, config: dict, weights: Optional[dict] = None, seed: Optional[int] = None):
+        self.config = dict(config)
+        self._cfg = _config_struct(self.config)
+        h = _p()
+        if weights is None:
+            check(lib.rn_model_create_synthetic(C.byref(self._cfg), SEED if seed is None else seed, C.byref(h)))
+        else:
+            layers = (LayerHost * self.config["layers"])()
+            keep = []
+            for l, lw in enumerate(weights["layers"]):
+                arrs = {k: (np.ascontiguousarray(v[0]), np.ascontiguousarray(v[1])) if isinstance(v, tuple)
+                        else np.ascontiguousarray(v) for k, v in lw.items()}
+                keep.append(arrs)
+                layers[l] = LayerHost(QMatHost(_ptr(arrs["qkv"][0]), _ptr(arrs["qkv"][1])),
+                                      QMatHost(_ptr(arrs["out"][0]), _ptr(arrs["out"][1])),
+                                      QMatHost(_ptr(arrs["gate_up"][0]), _ptr(arrs["gate_up"][1])),
+                                      QMatHost(_ptr(arrs["down"][0]), _ptr(arrs["down"][1])),
+                                      _ptr(arrs["norm_attn"]), _ptr(arrs["norm_ffn"]))
+            emb = (np.ascontiguousarray(weights["embedding"][0]), np.ascontiguousarray(weights["embedding"][1]))
+            nf = np.ascontiguousarray(weights["norm_final"])
+            w = WeightsHost(QMatHost(_ptr(emb[0]), _ptr(emb[1])), _ptr(nf), C.addressof(layers))
+            check(lib.rn_model_create(C.byref(self._cfg), C.byref(w), C.byref(h)))
+        self.handle = h.value
+
+    def rotary_table(self):
+        c = self.config
+        cos = np.empty((c["max_positions"], c["head_dim"] // 2), dtype=np.float32)
+        sin = np.empty_like(cos)
+        check(lib.rn_model_rotary_table(self.handle, _ptr(cos), _ptr(sin)))
+        return cos, sin
+
+    def session(self, capacity: int) -> "Session":
+        return Session(self, capacity)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_model_free(self.handle)
+        except Exception:
+            pass
+
+
+class Session:
+    """Session (crates/model/src/session.rs:17-177) with a device KV cache."""
+
+    def __init__(self, model: Model, capacity: int, _handle: Optional[int] = None):
+        self.model = model
+        self.capacity = capacity
+        if _handle is None:
+            h = _p()
+            check(lib.rn_session_create(model.handle, capacity, C.byref(h)))
+            _handle = h.value
+        self.handle = _handle
+
+    def __len__(self) -> int:
+        n = _i(0)
+        check(lib.rn_session_len(self.handle, C.byref(n)))
+        return n.value
+
+    def truncate(self, length: int) -> None:
+        check(lib.rn_session_truncate(self.handle, length))
+
+    def clone(self) -> "Session":
+        h = _p()
+        check(lib.rn_session_clone(self.handle, C.byref(h)))
+        return Session(self.model, self.capacity, h.value)
+
+    def set_cache(self, keys: np.ndarray, values: np.ndarray) -> None:
+        keys = np.ascontiguousarray(keys).view(np.uint16)
+        values = np.ascontiguousarray(values).view(np.uint16)
+        check(lib.rn_session_set_cache(self.handle, keys.shape[2], _ptr(keys), _ptr(values)))
+
+    def get_cache(self, length: Optional[int] = None):
+        c = self.model.config
+        length = len(self) if length is None else length
+        shape = (c["layers"], c["heads"], length, c["head_dim"])
+        k = np.empty(shape, dtype=np.uint16)
+        v = np.empty(shape, dtype=np.uint16)
+        check(lib.rn_session_get_cache(self.handle, length, _ptr(k), _ptr(v)))
+        return k.view(np.float16), v.view(np.float16)
+
+    def push(self, token: int) -> None:
+        check(lib.rn_session_push(self.handle, int(token)))
+
+    def feed(self, tokens) -> None:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        check(lib.rn_session_feed(self.handle, _ptr(t), t.size))
+
+    def hidden(self) -> np.ndarray:
+        out = np.empty(self.model.config["d_model"], dtype=np.float32)
+        check(lib.rn_session_hidden(self.handle, _ptr(out)))
+        return out
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.model.config["vocab"], dtype=np.float32)
+        check(lib.rn_session_logits(self.handle, _ptr(out)))
+        return out
+
+    def decode_greedy(self, first: int, steps: int) -> np.ndarray:
+        ids = np.empty(steps, dtype=np.uint32)
+        check(lib.rn_session_decode_greedy(self.handle, int(first), steps, _ptr(ids)))
+        return ids
+
+    def stream(self) -> int:
+        p = _p()
+        check(lib.rn_session_stream(self.handle, C.byref(p)))
+        return p.value
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_session_free(self.handle)
+        except Exception:
+            pass
+
+
+class Batch:
+    """`count` independent sequences decoded together (M=count MFMA products)."""
+
+    def __init__(self, model: Model, count: int, capacity: int):
+        self.model = model
+        self.count = count
+        h = _p()
+        check(lib.rn_batch_create(model.handle, count, capacity, C.byref(h)))
+        self.handle = h.value
+
+    def set_cache(self, sequence: int, keys: np.ndarray, values: np.ndarray) -> None:
+        keys = np.ascontiguousarray(keys).view(np.uint16)
+        values = np.ascontiguousarray(values).view(np.uint16)
+        check(lib.rn_batch_set_cache(self.handle, sequence, keys.shape[2], _ptr(keys), _ptr(values)))
+
+    def decode_greedy(self, first, steps: int) -> np.ndarray:
+        first = np.ascontiguousarray(first, dtype=np.uint32)
+        assert first.size == self.count
+        ids = np.empty((self.count, steps), dtype=np.uint32)
+        check(lib.rn_batch_decode_greedy(self.handle, _ptr(first), steps, _ptr(ids)))
+        return ids
+
+    def truncate(self, lengths) -> None:
+        lengths = np.ascontiguousarray(lengths, dtype=np.int32)
+        assert lengths.size == self.count
+        check(lib.rn_batch_truncate(self.handle, _ptr(lengths)))
+
+    def stream(self) -> int:
+        p = _p()
+        check(lib.rn_batch_stream(self.handle, C.byref(p)))
+        return p.value
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_batch_free(self.handle)
+        except Exception:
+            pass

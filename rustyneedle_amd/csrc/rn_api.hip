@@ -1,0 +1,1094 @@
+// rn_api.hip — the C ABI (include/rustyneedle.h): error reporting, device
+// plumbing, QuantisedMatrix, Model, Session and the multi-sequence batch.
+//
+// Device memory layout
+//   model  : one arena; per layer the fused QKV [3d][d], out [d][d], gate/up
+//            [2f][d] and down [d][f] int8 codes (row-major, rows = outputs),
+//            each followed by its [rows][cols/32] fp32 scales; the two norm
+//            gain vectors; the tied embedding [vocab][d] and its scales; the
+//            final gains; the rotary cos/sin table [max_positions][hd/2].
+//   session: one arena; K and V caches [layers][heads][capacity][hd] fp16
+//            (each (layer, head) a contiguous run of 128-byte rows), the
+//            residual x, the fused QKV output, the attention output, the FFN
+//            activation, the hidden state, the logits, a DecodeState and the
+//            greedy id buffer.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/rustyneedle.h"
+#include "rn_internal.hpp"
+
+using namespace rn;
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof g_error, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define RN_HIP(call)                                                                                 \
+    do {                                                                                             \
+        hipError_t e_ = (call);                                                                      \
+        if (e_ != hipSuccess)                                                                        \
+            return fail(RN_ERR_DEVICE, "%s: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, __LINE__); \
+    } while (0)
+
+#define RN_REQUIRE(cond, ...)                              \
+    do {                                                   \
+        if (!(cond)) return fail(RN_ERR_ARGUMENT, __VA_ARGS__); \
+    } while (0)
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Bump allocator over one device allocation.
+struct Arena {
+    char* base = nullptr;
+    size_t used = 0, size = 0;
+    void* take(size_t bytes) {
+        void* p = base + used;
+        used += align_up(bytes);
+        return p;
+    }
+};
+
+struct DevMatrix {
+    int8_t* W = nullptr;
+    float* sW = nullptr;
+};
+
+struct LayerDev {
+    DevMatrix qkv, out, gate_up, down;
+    float* norm_attn = nullptr;
+    float* norm_ffn = nullptr;
+};
+
+int check_supported(int columns) { return columns == 512 || columns == 1024 || columns == 2048; }
+
+}  // namespace
+
+struct rn_matrix {
+    int8_t* W = nullptr;
+    float* sW = nullptr;
+    int rows = 0, columns = 0, group = 0, form = 0;
+};
+
+struct rn_model {
+    rn_config cfg{};
+    void* arena = nullptr;
+    std::vector<LayerDev> layers;
+    DevMatrix embedding;
+    float* norm_final = nullptr;
+    float* rope_cos = nullptr;
+    float* rope_sin = nullptr;
+    std::vector<float> rope_cos_host, rope_sin_host;
+    float embed_scale = 0.0f;
+};
+
+struct rn_session {
+    const rn_model* model = nullptr;
+    int capacity = 0;
+    int length = 0;
+    bool has_hidden = false;
+    hipStream_t stream = nullptr;
+    void* arena = nullptr;
+    __half* kc = nullptr;
+    __half* vc = nullptr;
+    float* x = nullptr;
+    float* qkv = nullptr;
+    float* attn = nullptr;
+    float* ffh = nullptr;
+    float* hidden = nullptr;
+    float* logits = nullptr;
+    DecodeState* state = nullptr;
+    uint32_t* ids = nullptr;
+    hipGraphExec_t step_graph = nullptr;
+    // prefill scratch, grown on demand
+    void* scratch = nullptr;
+    int scratch_tokens = 0;
+};
+
+struct rn_batch {
+    const rn_model* model = nullptr;
+    int count = 0, capacity = 0;
+    std::vector<int> lengths;
+    hipStream_t stream = nullptr;
+    void* arena = nullptr;
+    __half* kc = nullptr;
+    __half* vc = nullptr;
+    int32_t* pos = nullptr;
+    float *X = nullptr, *QKV = nullptr, *A = nullptr, *F = nullptr, *logits = nullptr;
+    int8_t* Xq = nullptr;
+    float* sx = nullptr;
+    uint32_t* tokens = nullptr;
+    int32_t* error = nullptr;
+    uint32_t* ids = nullptr;
+    int ids_steps = 0;
+};
+
+// ------------------------------------------------------------------------------
+extern "C" {
+
+const char* rn_last_error(void) { return g_error; }
+int rn_abi_version(void) { return RN_ABI_VERSION; }
+
+int rn_device_count(int* count) {
+    RN_REQUIRE(count, "count is null");
+    RN_HIP(hipGetDeviceCount(count));
+    return RN_OK;
+}
+int rn_device_set(int device) {
+    RN_HIP(hipSetDevice(device));
+    return RN_OK;
+}
+int rn_malloc(void** ptr, size_t bytes) {
+    RN_REQUIRE(ptr, "ptr is null");
+    if (hipMalloc(ptr, bytes ? bytes : 1) != hipSuccess) return fail(RN_ERR_MEMORY, "hipMalloc(%zu) failed", bytes);
+    return RN_OK;
+}
+int rn_free(void* ptr) {
+    if (ptr) RN_HIP(hipFree(ptr));
+    return RN_OK;
+}
+int rn_memcpy_htod(void* dst, const void* src, size_t bytes) {
+    RN_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return RN_OK;
+}
+int rn_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+    RN_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return RN_OK;
+}
+int rn_memcpy_dtod(void* dst, const void* src, size_t bytes) {
+    RN_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    return RN_OK;
+}
+int rn_stream_create(void** stream) {
+    RN_REQUIRE(stream, "stream is null");
+    hipStream_t s;
+    RN_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return RN_OK;
+}
+int rn_stream_destroy(void* stream) {
+    if (stream) RN_HIP(hipStreamDestroy((hipStream_t)stream));
+    return RN_OK;
+}
+int rn_stream_synchronize(void* stream) {
+    RN_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return RN_OK;
+}
+int rn_event_create(void** event) {
+    RN_REQUIRE(event, "event is null");
+    hipEvent_t e;
+    RN_HIP(hipEventCreate(&e));
+    *event = e;
+    return RN_OK;
+}
+int rn_event_destroy(void* event) {
+    if (event) RN_HIP(hipEventDestroy((hipEvent_t)event));
+    return RN_OK;
+}
+int rn_event_record(void* event, void* stream) {
+    RN_HIP(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+    return RN_OK;
+}
+int rn_event_elapsed_ms(void* start, void* stop, float* ms) {
+    RN_REQUIRE(ms, "ms is null");
+    RN_HIP(hipEventSynchronize((hipEvent_t)stop));
+    RN_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return RN_OK;
+}
+
+// ---- QuantisedMatrix ------------------------------------------------------------
+
+int rn_matrix_create_i8(const int8_t* codes, const float* scales, int rows, int columns, int group, int form,
+                        rn_matrix** out) {
+    RN_REQUIRE(codes && scales && out, "null argument");
+    RN_REQUIRE(rows > 0, "rows must be positive (got %d)", rows);
+    RN_REQUIRE(group == kGroup, "group must be 32 (got %d)", group);
+    RN_REQUIRE(check_supported(columns), "columns must be 512, 1024 or 2048 (got %d)", columns);
+    RN_REQUIRE(form == RN_FORM_PANEL || form == RN_FORM_PLANE, "unknown form %d", form);
+    rn_matrix* m = new (std::nothrow) rn_matrix();
+    if (!m) return fail(RN_ERR_MEMORY, "out of host memory");
+    const size_t cb = (size_t)rows * columns, sb = (size_t)rows * (columns / group) * sizeof(float);
+    if (hipMalloc(&m->W, cb) != hipSuccess || hipMalloc(&m->sW, sb) != hipSuccess) {
+        (void)hipFree(m->W);
+        delete m;
+        return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", cb + sb);
+    }
+    m->rows = rows;
+    m->columns = columns;
+    m->group = group;
+    m->form = form;
+    if (hipMemcpy(m->W, codes, cb, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->sW, scales, sb, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(m->W);
+        (void)hipFree(m->sW);
+        delete m;
+        return fail(RN_ERR_DEVICE, "upload of matrix failed");
+    }
+    *out = m;
+    return RN_OK;
+}
+
+int rn_matrix_free(rn_matrix* m) {
+    if (!m) return RN_OK;
+    (void)hipFree(m->W);
+    (void)hipFree(m->sW);
+    delete m;
+    return RN_OK;
+}
+
+int rn_matrix_shape(const rn_matrix* m, int* rows, int* columns, int* group) {
+    RN_REQUIRE(m, "matrix is null");
+    if (rows) *rows = m->rows;
+    if (columns) *columns = m->columns;
+    if (group) *group = m->group;
+    return RN_OK;
+}
+
+int rn_matrix_multiply_vector(const rn_matrix* m, const float* x, float* y, int32_t* acc, void* stream) {
+    RN_REQUIRE(m && x && y, "null argument");
+    GemvParams p{};
+    const int rpb = gemv_rows_per_block(m->rows, m->columns, kStore);
+    const int blocks = (m->rows + rpb - 1) / rpb;
+    p.nseg = 1;
+    p.seg[0] = Segment{m->W, m->sW, y, acc, m->rows, 0};
+    p.x = x;
+    RN_HIP(launch_gemv(p, m->columns, kQuant, kStore, m->form, rpb, blocks, (hipStream_t)stream));
+    return RN_OK;
+}
+
+int rn_matrix_multiply_fused(const rn_matrix* const* ms, int count, const float* x, float* const* ys, void* stream) {
+    RN_REQUIRE(ms && x && ys, "null argument");
+    RN_REQUIRE(count >= 1 && count <= kMaxSegments, "count must be 1..%d (got %d)", kMaxSegments, count);
+    const rn_matrix* first = ms[0];
+    RN_REQUIRE(first, "matrix 0 is null");
+    int total_rows = 0;
+    for (int i = 0; i < count; ++i) {
+        RN_REQUIRE(ms[i] && ys[i], "matrix or output %d is null", i);
+        RN_REQUIRE(ms[i]->columns == first->columns && ms[i]->group == first->group && ms[i]->form == first->form,
+                   "fused matrices must share columns, group and form (matrix %d differs)", i);
+        total_rows += ms[i]->rows;
+    }
+    const int rpb = gemv_rows_per_block(total_rows, first->columns, kStore);
+    GemvParams p{};
+    p.nseg = count;
+    int block = 0;
+    for (int i = 0; i < count; ++i) {
+        p.seg[i] = Segment{ms[i]->W, ms[i]->sW, ys[i], nullptr, ms[i]->rows, block};
+        block += (ms[i]->rows + rpb - 1) / rpb;
+    }
+    p.x = x;
+    RN_HIP(launch_gemv(p, first->columns, kQuant, kStore, first->form, rpb, block, (hipStream_t)stream));
+    return RN_OK;
+}
+
+int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, float* y, int32_t* acc, void* stream) {
+    RN_REQUIRE(m && x && y, "null argument");
+    RN_REQUIRE(count >= 0, "count must be non-negative");
+    if (count == 0) return RN_OK;
+    hipStream_t s = (hipStream_t)stream;
+    void* scratch = nullptr;
+    const size_t codes = align_up((size_t)count * m->columns);
+    RN_HIP(hipMallocAsync(&scratch, codes + sizeof(float) * (size_t)count, s));
+    int8_t* xq = (int8_t*)scratch;
+    float* sx = (float*)((char*)scratch + codes);
+    hipError_t e = launch_norm_quantise(x, nullptr, count, m->columns, 1e-6f, xq, sx, nullptr, s);
+    if (e == hipSuccess) {
+        GemmParams p{xq, sx, m->W, m->sW, count, m->rows, m->columns, y, m->rows, acc, 0};
+        e = launch_gemm(p, kGemmStore, m->form, acc != nullptr, s);
+    }
+    hipError_t f = hipFreeAsync(scratch, s);
+    RN_HIP(e);
+    RN_HIP(f);
+    return RN_OK;
+}
+
+int rn_matrix_dequantise_row(const rn_matrix* m, int row, float* out) {
+    RN_REQUIRE(m && out, "null argument");
+    RN_REQUIRE(row >= 0 && row < m->rows, "row %d out of range [0, %d)", row, m->rows);
+    const int G = m->columns / m->group;
+    std::vector<int8_t> codes(m->columns);
+    std::vector<float> scales(G);
+    RN_HIP(hipMemcpy(codes.data(), m->W + (size_t)row * m->columns, m->columns, hipMemcpyDeviceToHost));
+    RN_HIP(hipMemcpy(scales.data(), m->sW + (size_t)row * G, sizeof(float) * G, hipMemcpyDeviceToHost));
+    for (int k = 0; k < m->columns; ++k) out[k] = (float)codes[k] * scales[k / m->group];
+    return RN_OK;
+}
+
+int rn_quantise_int8(const float* x, int count, int columns, int8_t* codes, float* scales, void* stream) {
+    RN_REQUIRE(x && codes && scales, "null argument");
+    RN_REQUIRE(count >= 0 && columns > 0, "bad shape");
+    RN_HIP(launch_quantise_rows(x, count, columns, codes, scales, (hipStream_t)stream));
+    return RN_OK;
+}
+
+int rn_fast_exp(const float* x, float* y, int n, void* stream) {
+    RN_REQUIRE(x && y && n >= 0, "bad argument");
+    RN_HIP(launch_fast_exp(x, y, n, 0, (hipStream_t)stream));
+    return RN_OK;
+}
+
+int rn_silu(const float* x, float* y, int n, void* stream) {
+    RN_REQUIRE(x && y && n >= 0, "bad argument");
+    RN_HIP(launch_fast_exp(x, y, n, 1, (hipStream_t)stream));
+    return RN_OK;
+}
+
+int rn_zero_centred_norm(const float* x, const float* gain, int count, int n, float* out, void* stream) {
+    RN_REQUIRE(x && gain && out, "null argument");
+    RN_REQUIRE(n > 0 && n % 8 == 0 && n <= 4096 && count >= 0, "n must be a multiple of 8 in 8..4096");
+    RN_HIP(launch_norm_rows(x, gain, count, n, 1e-6f, out, (hipStream_t)stream));
+    return RN_OK;
+}
+
+int rn_attend_heads(const float* q, const uint16_t* K, const uint16_t* V, const int32_t* lengths, int count,
+                    int stride, int head_dim, float* out, void* stream) {
+    RN_REQUIRE(q && K && V && lengths && out, "null argument");
+    RN_REQUIRE(head_dim == 64, "head_dim must be 64 (got %d)", head_dim);
+    RN_REQUIRE(stride >= 1 && stride <= 16384 && count >= 0, "stride must be 1..16384");
+    if (count == 0) return RN_OK;
+    hipStream_t s = (hipStream_t)stream;
+    int32_t* err = nullptr;
+    RN_HIP(hipMallocAsync((void**)&err, sizeof(int32_t), s));
+    RN_HIP(hipMemsetAsync(err, 0, sizeof(int32_t), s));
+    AttendParams p{};
+    p.q = q;
+    p.kc = (__half*)K;
+    p.vc = (__half*)V;
+    p.lengths = lengths;
+    p.stride = stride;
+    p.out = out;
+    p.error = err;
+    hipError_t e = launch_attend(p, kAttendRaw, count, 1, stride, s);
+    int32_t host_err = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&host_err, err, sizeof(int32_t), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFreeAsync(err, s);
+    RN_HIP(e);
+    if (host_err) return fail(RN_ERR_ARGUMENT, "a length is outside 1..stride");
+    return RN_OK;
+}
+
+// ---- Model ----------------------------------------------------------------------
+
+static int validate_config(const rn_config* c) {
+    RN_REQUIRE(c, "config is null");
+    RN_REQUIRE(c->d_model == 512, "d_model must be 512 (got %d)", c->d_model);
+    RN_REQUIRE(c->head_dim == 64, "head_dim must be 64 (got %d)", c->head_dim);
+    RN_REQUIRE(c->heads * c->head_dim == c->d_model, "heads * head_dim must equal d_model");
+    RN_REQUIRE(check_supported(c->ffn), "ffn must be 512, 1024 or 2048 (got %d)", c->ffn);
+    RN_REQUIRE(c->group == kGroup, "group must be 32 (got %d)", c->group);
+    RN_REQUIRE(c->layers >= 1 && c->layers <= 256, "layers must be 1..256 (got %d)", c->layers);
+    RN_REQUIRE(c->vocab >= 1, "vocab must be positive");
+    RN_REQUIRE(c->max_positions >= 1 && c->max_positions <= 16384, "max_positions must be 1..16384");
+    RN_REQUIRE(c->norm_eps == 1e-6f, "norm_eps must be 1e-6 (the reference's NORM_EPSILON)");
+    RN_REQUIRE(c->rope_theta > 0.0f, "rope_theta must be positive");
+    return RN_OK;
+}
+
+// ops.rs:127-141: frequencies 1/theta^(2i/hd) and the angle position*freq in f32.
+static void rotary_table(const rn_config& c, std::vector<float>& cs, std::vector<float>& sn) {
+    const int half = c.head_dim / 2;
+    std::vector<float> freqs(half);
+    for (int i = 0; i < half; ++i) freqs[i] = 1.0f / powf(c.rope_theta, (2.0f * (float)i) / (float)c.head_dim);
+    cs.resize((size_t)c.max_positions * half);
+    sn.resize(cs.size());
+    for (int p = 0; p < c.max_positions; ++p)
+        for (int i = 0; i < half; ++i) {
+            const float angle = (float)p * freqs[i];
+            cs[(size_t)p * half + i] = cosf(angle);
+            sn[(size_t)p * half + i] = sinf(angle);
+        }
+}
+
+int rn_model_create(const rn_config* config, const rn_weights_host* w, rn_model** out) {
+    int rc = validate_config(config);
+    if (rc) return rc;
+    RN_REQUIRE(w && out && w->layers && w->norm_final && w->embedding.codes && w->embedding.scales, "null weights");
+    const rn_config& c = *config;
+    const size_t d = c.d_model, f = c.ffn, G = d / kGroup, Gf = f / kGroup;
+    for (int l = 0; l < c.layers; ++l) {
+        const rn_layer_host& L = w->layers[l];
+        RN_REQUIRE(L.qkv.codes && L.qkv.scales && L.out.codes && L.out.scales && L.gate_up.codes && L.gate_up.scales &&
+                       L.down.codes && L.down.scales && L.norm_attn && L.norm_ffn,
+                   "null tensor in layer %d", l);
+    }
+    rn_model* m = new (std::nothrow) rn_model();
+    if (!m) return fail(RN_ERR_MEMORY, "out of host memory");
+    m->cfg = c;
+    rotary_table(c, m->rope_cos_host, m->rope_sin_host);
+    m->embed_scale = sqrtf((float)c.d_model);
+
+    auto qbytes = [](size_t rows, size_t cols) { return align_up(rows * cols) + align_up(rows * (cols / kGroup) * 4); };
+    size_t total = 0;
+    total += (size_t)c.layers * (qbytes(3 * d, d) + qbytes(d, d) + qbytes(2 * f, d) + qbytes(d, f) + 2 * align_up(4 * d));
+    total += qbytes(c.vocab, d) + align_up(4 * d) + 2 * align_up(m->rope_cos_host.size() * 4);
+    if (hipMalloc(&m->arena, total) != hipSuccess) {
+        delete m;
+        return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", total);
+    }
+    Arena a{(char*)m->arena, 0, total};
+    std::vector<std::pair<void*, std::pair<const void*, size_t>>> uploads;
+    auto place = [&](const void* src, size_t bytes) {
+        void* dst = a.take(bytes);
+        uploads.push_back({dst, {src, bytes}});
+        return dst;
+    };
+    auto placeq = [&](const rn_qmat_host& q, size_t rows, size_t cols) {
+        DevMatrix dm;
+        dm.W = (int8_t*)place(q.codes, rows * cols);
+        dm.sW = (float*)place(q.scales, rows * (cols / kGroup) * 4);
+        return dm;
+    };
+    m->layers.resize(c.layers);
+    for (int l = 0; l < c.layers; ++l) {
+        const rn_layer_host& L = w->layers[l];
+        LayerDev& D = m->layers[l];
+        D.qkv = placeq(L.qkv, 3 * d, d);
+        D.out = placeq(L.out, d, d);
+        D.gate_up = placeq(L.gate_up, 2 * f, d);
+        D.down = placeq(L.down, d, f);
+        D.norm_attn = (float*)place(L.norm_attn, 4 * d);
+        D.norm_ffn = (float*)place(L.norm_ffn, 4 * d);
+    }
+    m->embedding = placeq(w->embedding, c.vocab, d);
+    m->norm_final = (float*)place(w->norm_final, 4 * d);
+    m->rope_cos = (float*)place(m->rope_cos_host.data(), m->rope_cos_host.size() * 4);
+    m->rope_sin = (float*)place(m->rope_sin_host.data(), m->rope_sin_host.size() * 4);
+    (void)G;
+    (void)Gf;
+    for (auto& u : uploads) {
+        if (hipMemcpy(u.first, u.second.first, u.second.second, hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipFree(m->arena);
+            delete m;
+            return fail(RN_ERR_DEVICE, "weight upload failed");
+        }
+    }
+    *out = m;
+    return RN_OK;
+}
+
+int rn_model_create_synthetic(const rn_config* config, uint64_t seed, rn_model** out) {
+    int rc = validate_config(config);
+    if (rc) return rc;
+    RN_REQUIRE(out, "out is null");
+    const rn_config& c = *config;
+    const size_t d = c.d_model, f = c.ffn;
+    struct Q {
+        std::vector<int8_t> codes;
+        std::vector<float> scales;
+    };
+    auto gen_q = [&](const std::string& name, size_t rows, size_t cols) {
+        Q q;
+        q.codes.resize(rows * cols);
+        q.scales.resize(rows * (cols / kGroup));
+        rn_synth_codes(seed, (name + ".codes").c_str(), q.codes.data(), q.codes.size());
+        rn_synth_uniform(seed, (name + ".scales").c_str(), 1e-3f, 1e-2f, q.scales.data(), q.scales.size());
+        return q;
+    };
+    auto gen_gain = [&](const std::string& name) {
+        std::vector<float> g(d);
+        rn_synth_normal(seed, name.c_str(), 0.1f, g.data(), d);
+        return g;
+    };
+    std::vector<Q> qs;
+    std::vector<std::vector<float>> gains;
+    qs.reserve((size_t)c.layers * 4 + 1);
+    gains.reserve((size_t)c.layers * 2 + 1);
+    std::vector<rn_layer_host> layers(c.layers);
+    for (int l = 0; l < c.layers; ++l) {
+        const std::string p = "layers." + std::to_string(l) + ".";
+        qs.push_back(gen_q(p + "qkv", 3 * d, d));
+        qs.push_back(gen_q(p + "out", d, d));
+        qs.push_back(gen_q(p + "gate_up", 2 * f, d));
+        qs.push_back(gen_q(p + "down", d, f));
+        gains.push_back(gen_gain(p + "norm_attn"));
+        gains.push_back(gen_gain(p + "norm_ffn"));
+        const size_t qi = qs.size() - 4, gi = gains.size() - 2;
+        layers[l].qkv = {qs[qi].codes.data(), qs[qi].scales.data()};
+        layers[l].out = {qs[qi + 1].codes.data(), qs[qi + 1].scales.data()};
+        layers[l].gate_up = {qs[qi + 2].codes.data(), qs[qi + 2].scales.data()};
+        layers[l].down = {qs[qi + 3].codes.data(), qs[qi + 3].scales.data()};
+        layers[l].norm_attn = gains[gi].data();
+        layers[l].norm_ffn = gains[gi + 1].data();
+    }
+    qs.push_back(gen_q("embedding", c.vocab, d));
+    gains.push_back(gen_gain("norm_final"));
+    rn_weights_host w{};
+    w.embedding = {qs.back().codes.data(), qs.back().scales.data()};
+    w.norm_final = gains.back().data();
+    w.layers = layers.data();
+    return rn_model_create(config, &w, out);
+}
+
+int rn_model_free(rn_model* m) {
+    if (!m) return RN_OK;
+    (void)hipFree(m->arena);
+    delete m;
+    return RN_OK;
+}
+
+int rn_model_config(const rn_model* m, rn_config* out) {
+    RN_REQUIRE(m && out, "null argument");
+    *out = m->cfg;
+    return RN_OK;
+}
+
+int rn_model_rotary_table(const rn_model* m, float* cos_out, float* sin_out) {
+    RN_REQUIRE(m && cos_out && sin_out, "null argument");
+    memcpy(cos_out, m->rope_cos_host.data(), m->rope_cos_host.size() * 4);
+    memcpy(sin_out, m->rope_sin_host.data(), m->rope_sin_host.size() * 4);
+    return RN_OK;
+}
+
+// ---- Session --------------------------------------------------------------------
+
+static size_t cache_elems(const rn_config& c, int capacity) {
+    return (size_t)c.layers * c.heads * capacity * c.head_dim;
+}
+
+int rn_session_create(const rn_model* m, int capacity, rn_session** out) {
+    RN_REQUIRE(m && out, "null argument");
+    const rn_config& c = m->cfg;
+    RN_REQUIRE(capacity >= 1 && capacity <= c.max_positions, "capacity must be 1..max_positions (%d)", c.max_positions);
+    RN_REQUIRE(capacity <= 16384, "capacity must be at most 16384");
+    rn_session* s = new (std::nothrow) rn_session();
+    if (!s) return fail(RN_ERR_MEMORY, "out of host memory");
+    s->model = m;
+    s->capacity = capacity;
+    const size_t ce = cache_elems(c, capacity), d = c.d_model;
+    const size_t total = 2 * align_up(ce * 2) + align_up(4 * d) * 4 + align_up(4 * 3 * d) + align_up(4 * (size_t)c.ffn) +
+                         align_up(4 * (size_t)c.vocab) + align_up(sizeof(DecodeState)) + align_up(4 * (size_t)capacity);
+    if (hipMalloc(&s->arena, total) != hipSuccess) {
+        delete s;
+        return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", total);
+    }
+    Arena a{(char*)s->arena, 0, total};
+    s->kc = (__half*)a.take(ce * 2);
+    s->vc = (__half*)a.take(ce * 2);
+    s->x = (float*)a.take(4 * d);
+    s->qkv = (float*)a.take(4 * 3 * d);
+    s->attn = (float*)a.take(4 * d);
+    s->ffh = (float*)a.take(4 * (size_t)c.ffn);
+    s->hidden = (float*)a.take(4 * d);
+    s->logits = (float*)a.take(4 * (size_t)c.vocab);
+    s->state = (DecodeState*)a.take(sizeof(DecodeState));
+    s->ids = (uint32_t*)a.take(4 * (size_t)capacity);
+    if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipMemsetAsync(s->arena, 0, total, s->stream) != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess) {
+        if (s->stream) (void)hipStreamDestroy(s->stream);
+        (void)hipFree(s->arena);
+        delete s;
+        return fail(RN_ERR_DEVICE, "session initialisation failed");
+    }
+    *out = s;
+    return RN_OK;
+}
+
+int rn_session_free(rn_session* s) {
+    if (!s) return RN_OK;
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    if (s->step_graph) (void)hipGraphExecDestroy(s->step_graph);
+    if (s->scratch) (void)hipFree(s->scratch);
+    (void)hipFree(s->arena);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+    return RN_OK;
+}
+
+int rn_session_clone(const rn_session* s, rn_session** out) {
+    RN_REQUIRE(s && out, "null argument");
+    rn_session* t = nullptr;
+    int rc = rn_session_create(s->model, s->capacity, &t);
+    if (rc) return rc;
+    RN_HIP(hipStreamSynchronize(s->stream));
+    // Everything in the arena up to the id buffer is state; copy it wholesale.
+    const size_t bytes = (size_t)((char*)s->ids - (char*)s->arena);
+    RN_HIP(hipMemcpy(t->arena, s->arena, bytes, hipMemcpyDeviceToDevice));
+    t->length = s->length;
+    t->has_hidden = s->has_hidden;
+    *out = t;
+    return RN_OK;
+}
+
+int rn_session_len(const rn_session* s, int* length) {
+    RN_REQUIRE(s && length, "null argument");
+    *length = s->length;
+    return RN_OK;
+}
+
+int rn_session_truncate(rn_session* s, int length) {
+    RN_REQUIRE(s, "session is null");
+    RN_REQUIRE(length >= 0 && length <= s->length, "length %d outside 0..%d", length, s->length);
+    s->length = length;
+    s->has_hidden = false;
+    return RN_OK;
+}
+
+int rn_session_stream(const rn_session* s, void** stream) {
+    RN_REQUIRE(s && stream, "null argument");
+    *stream = s->stream;
+    return RN_OK;
+}
+
+int rn_session_set_cache(rn_session* s, int length, const uint16_t* keys, const uint16_t* values) {
+    RN_REQUIRE(s && (length == 0 || (keys && values)), "null argument");
+    RN_REQUIRE(length >= 0 && length <= s->capacity, "length %d outside 0..capacity (%d)", length, s->capacity);
+    const rn_config& c = s->model->cfg;
+    if (length > 0) {
+        const size_t row = (size_t)length * c.head_dim * 2, pitch = (size_t)s->capacity * c.head_dim * 2;
+        const size_t heads = (size_t)c.layers * c.heads;
+        RN_HIP(hipMemcpy2DAsync(s->kc, pitch, keys, row, row, heads, hipMemcpyHostToDevice, s->stream));
+        RN_HIP(hipMemcpy2DAsync(s->vc, pitch, values, row, row, heads, hipMemcpyHostToDevice, s->stream));
+        RN_HIP(hipStreamSynchronize(s->stream));
+    }
+    s->length = length;
+    s->has_hidden = false;
+    return RN_OK;
+}
+
+int rn_session_get_cache(const rn_session* s, int length, uint16_t* keys, uint16_t* values) {
+    RN_REQUIRE(s && keys && values, "null argument");
+    RN_REQUIRE(length >= 0 && length <= s->capacity, "length %d outside 0..capacity", length);
+    if (length == 0) return RN_OK;
+    const rn_config& c = s->model->cfg;
+    const size_t row = (size_t)length * c.head_dim * 2, pitch = (size_t)s->capacity * c.head_dim * 2;
+    const size_t heads = (size_t)c.layers * c.heads;
+    RN_HIP(hipStreamSynchronize(s->stream));
+    RN_HIP(hipMemcpy2D(keys, row, s->kc, pitch, row, heads, hipMemcpyDeviceToHost));
+    RN_HIP(hipMemcpy2D(values, row, s->vc, pitch, row, heads, hipMemcpyDeviceToHost));
+    return RN_OK;
+}
+
+// The kernels of one decode step (session.rs:76-148): per layer the norm+QKV
+// product (layer 0 gathers the embedding of state->token first), attention
+// with rotary and the fp16 append, the out product + residual, the
+// norm+gate/up product with silu(gate)*up, the down product + residual; then
+// the final norm into `hidden`. With `logits`, the tied-embedding product
+// follows, and with `greedy` its last block writes the argmax into the state.
+static int enqueue_step(rn_session* s, bool logits, bool greedy) {
+    const rn_model* m = s->model;
+    const rn_config& c = m->cfg;
+    const int d = c.d_model;
+    hipStream_t st = s->stream;
+    for (int l = 0; l < c.layers; ++l) {
+        const LayerDev& L = m->layers[l];
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.qkv.W, L.qkv.sW, s->qkv, nullptr, 3 * d, 0};
+            p.x = s->x;
+            p.gain = L.norm_attn;
+            p.eps = c.norm_eps;
+            p.embW = m->embedding.W;
+            p.embS = m->embedding.sW;
+            p.embed_scale = m->embed_scale;
+            p.vocab = c.vocab;
+            p.x_out = s->x;
+            p.state = s->state;
+            const int rpb = gemv_rows_per_block(3 * d, d, kStore);
+            RN_HIP(launch_gemv(p, d, l == 0 ? kEmbedNorm : kNorm, kStore, kPanel, rpb, (3 * d + rpb - 1) / rpb, st));
+        }
+        {
+            AttendParams a{};
+            a.qkv = s->qkv;
+            a.kc = s->kc;
+            a.vc = s->vc;
+            a.layer = l;
+            a.heads = c.heads;
+            a.capacity = s->capacity;
+            a.d_model = d;
+            a.pos = &s->state->pos;
+            a.pos_stride = 0;
+            a.rope_cos = m->rope_cos;
+            a.rope_sin = m->rope_sin;
+            a.out = s->attn;
+            a.error = &s->state->error;
+            RN_HIP(launch_attend(a, kAttendDecode, c.heads, 1, s->capacity, st));
+        }
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.out.W, L.out.sW, s->x, nullptr, d, 0};
+            p.x = s->attn;
+            const int rpb = gemv_rows_per_block(d, d, kResidual);
+            RN_HIP(launch_gemv(p, d, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
+        }
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.gate_up.W, L.gate_up.sW, s->ffh, nullptr, 2 * c.ffn, 0};
+            p.half_rows = c.ffn;
+            p.x = s->x;
+            p.gain = L.norm_ffn;
+            p.eps = c.norm_eps;
+            const int rpb = gemv_rows_per_block(2 * c.ffn, d, kSilu);
+            RN_HIP(launch_gemv(p, d, kNorm, kSilu, kPanel, rpb, (c.ffn + rpb / 2 - 1) / (rpb / 2), st));
+        }
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.down.W, L.down.sW, s->x, nullptr, d, 0};
+            p.x = s->ffh;
+            const int rpb = gemv_rows_per_block(d, c.ffn, kResidual);
+            RN_HIP(launch_gemv(p, c.ffn, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
+        }
+    }
+    RN_HIP(launch_finish_push(s->x, m->norm_final, d, c.norm_eps, s->hidden, s->state, st));
+    if (logits) {
+        GemvParams p{};
+        p.nseg = 1;
+        p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab, 0};
+        p.x = s->hidden;
+        p.state = s->state;
+        p.ids = s->ids;
+        const int rpb = gemv_rows_per_block(c.vocab, d, kStore);
+        RN_HIP(launch_gemv(p, d, kQuant, greedy ? kArgmax : kStore, kPlane, rpb, (c.vocab + rpb - 1) / rpb, st));
+    }
+    return RN_OK;
+}
+
+static int check_state_error(rn_session* s) {
+    int32_t err = 0;
+    RN_HIP(hipMemcpyAsync(&err, &s->state->error, sizeof err, hipMemcpyDeviceToHost, s->stream));
+    RN_HIP(hipStreamSynchronize(s->stream));
+    if (err) {
+        RN_HIP(hipMemsetAsync(&s->state->error, 0, sizeof(int32_t), s->stream));
+        RN_HIP(hipStreamSynchronize(s->stream));
+        return fail(RN_ERR_STATE, "device reported error flags 0x%x (1: token >= vocab, 2: position >= capacity)", err);
+    }
+    return RN_OK;
+}
+
+int rn_session_push(rn_session* s, uint32_t token) {
+    RN_REQUIRE(s, "session is null");
+    RN_REQUIRE(token < (uint32_t)s->model->cfg.vocab, "token %u outside the vocabulary (%d)", token,
+               s->model->cfg.vocab);
+    if (s->length >= s->capacity) return fail(RN_ERR_CAPACITY, "session is full (%d positions)", s->capacity);
+    RN_HIP(launch_set_state(s->state, token, s->length, 0, 0, s->stream));
+    int rc = enqueue_step(s, false, false);
+    if (rc) return rc;
+    s->length += 1;
+    s->has_hidden = true;
+    return RN_OK;
+}
+
+int rn_session_hidden(const rn_session* s, float* out) {
+    RN_REQUIRE(s && out, "null argument");
+    if (!s->has_hidden) return fail(RN_ERR_STATE, "no token has been pushed");
+    RN_HIP(hipMemcpyAsync(out, s->hidden, 4 * (size_t)s->model->cfg.d_model, hipMemcpyDeviceToHost, s->stream));
+    RN_HIP(hipStreamSynchronize(s->stream));
+    return RN_OK;
+}
+
+int rn_session_logits(rn_session* s, float* out) {
+    RN_REQUIRE(s && out, "null argument");
+    if (!s->has_hidden) return fail(RN_ERR_STATE, "no token has been pushed");
+    const rn_model* m = s->model;
+    const rn_config& c = m->cfg;
+    GemvParams p{};
+    p.nseg = 1;
+    p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab, 0};
+    p.x = s->hidden;
+    const int rpb = gemv_rows_per_block(c.vocab, c.d_model, kStore);
+    RN_HIP(launch_gemv(p, c.d_model, kQuant, kStore, kPlane, rpb, (c.vocab + rpb - 1) / rpb, s->stream));
+    RN_HIP(hipMemcpyAsync(out, s->logits, 4 * (size_t)c.vocab, hipMemcpyDeviceToHost, s->stream));
+    return check_state_error(s);
+}
+
+int rn_session_decode_greedy(rn_session* s, uint32_t first, int steps, uint32_t* ids) {
+    RN_REQUIRE(s && (ids || steps == 0), "null argument");
+    RN_REQUIRE(steps >= 0, "steps must be non-negative");
+    RN_REQUIRE(first < (uint32_t)s->model->cfg.vocab, "token %u outside the vocabulary", first);
+    if (steps == 0) return RN_OK;
+    if (s->length + steps > s->capacity)
+        return fail(RN_ERR_CAPACITY, "%d + %d positions exceed the capacity %d", s->length, steps, s->capacity);
+    if (!s->step_graph) {
+        hipGraph_t graph = nullptr;
+        RN_HIP(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_step(s, true, true);
+        hipError_t e = hipStreamEndCapture(s->stream, &graph);
+        if (rc) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        RN_HIP(e);
+        e = hipGraphInstantiate(&s->step_graph, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        RN_HIP(e);
+    }
+    RN_HIP(launch_set_state(s->state, first, s->length, 0, (uint32_t)s->capacity, s->stream));
+    for (int i = 0; i < steps; ++i) RN_HIP(hipGraphLaunch(s->step_graph, s->stream));
+    RN_HIP(hipMemcpyAsync(ids, s->ids, 4 * (size_t)steps, hipMemcpyDeviceToHost, s->stream));
+    s->length += steps;
+    s->has_hidden = true;
+    return check_state_error(s);
+}
+
+static int ensure_scratch(rn_session* s, int count) {
+    if (count <= s->scratch_tokens) return RN_OK;
+    const rn_config& c = s->model->cfg;
+    const size_t d = c.d_model, f = c.ffn;
+    const size_t bytes = align_up(4 * count * d) * 3 + align_up(4 * count * 3 * d) + align_up(4 * count * f) +
+                         align_up(count * (f > d ? f : d)) + align_up(4 * (size_t)count) + align_up(4 * (size_t)count);
+    RN_HIP(hipStreamSynchronize(s->stream));
+    if (s->scratch) RN_HIP(hipFree(s->scratch));
+    s->scratch = nullptr;
+    s->scratch_tokens = 0;
+    if (hipMalloc(&s->scratch, bytes) != hipSuccess) return fail(RN_ERR_MEMORY, "prefill scratch of %zu bytes", bytes);
+    s->scratch_tokens = count;
+    return RN_OK;
+}
+
+// Session::feed / prefill (session.rs:56-70, prefill.rs:10-99): all tokens of
+// the chunk go through each layer together; the products run on i8 MFMA.
+int rn_session_feed(rn_session* s, const uint32_t* tokens, int count) {
+    RN_REQUIRE(s && (tokens || count == 0), "null argument");
+    RN_REQUIRE(count >= 0, "count must be non-negative");
+    if (count == 0) return RN_OK;
+    const rn_model* m = s->model;
+    const rn_config& c = m->cfg;
+    for (int i = 0; i < count; ++i)
+        RN_REQUIRE(tokens[i] < (uint32_t)c.vocab, "token %u at %d outside the vocabulary", tokens[i], i);
+    if (s->length + count > s->capacity)
+        return fail(RN_ERR_CAPACITY, "%d + %d positions exceed the capacity %d", s->length, count, s->capacity);
+    int rc = ensure_scratch(s, count);
+    if (rc) return rc;
+    const int d = c.d_model, f = c.ffn;
+    Arena a{(char*)s->scratch, 0, 0};
+    float* X = (float*)a.take(4 * (size_t)count * d);
+    float* Q = (float*)a.take(4 * (size_t)count * d);
+    float* A = (float*)a.take(4 * (size_t)count * d);
+    float* QKV = (float*)a.take(4 * (size_t)count * 3 * d);
+    float* F = (float*)a.take(4 * (size_t)count * f);
+    int8_t* Xq = (int8_t*)a.take((size_t)count * (f > d ? f : d));
+    float* sx = (float*)a.take(4 * (size_t)count);
+    uint32_t* tok = (uint32_t*)a.take(4 * (size_t)count);
+    hipStream_t st = s->stream;
+    const int first = s->length;
+    RN_HIP(hipMemcpyAsync(tok, tokens, 4 * (size_t)count, hipMemcpyHostToDevice, st));
+    RN_HIP(launch_embed_rows(tok, count, m->embedding.W, m->embedding.sW, d, c.vocab, m->embed_scale, X,
+                             &s->state->error, st));
+    for (int l = 0; l < c.layers; ++l) {
+        const LayerDev& L = m->layers[l];
+        RN_HIP(launch_norm_quantise(X, L.norm_attn, count, d, c.norm_eps, Xq, sx, nullptr, st));
+        RN_HIP(launch_gemm(GemmParams{Xq, sx, L.qkv.W, L.qkv.sW, count, 3 * d, d, QKV, 3 * d, nullptr, 0}, kGemmStore,
+                           kPanel, false, st));
+        RN_HIP(launch_rope_append(QKV, Q, s->kc, s->vc, l, c.heads, s->capacity, d, first, count, m->rope_cos,
+                                  m->rope_sin, st));
+        AttendParams ap{};
+        ap.q = Q;
+        ap.kc = s->kc;
+        ap.vc = s->vc;
+        ap.layer = l;
+        ap.heads = c.heads;
+        ap.capacity = s->capacity;
+        ap.d_model = d;
+        ap.first = first;
+        ap.out = A;
+        ap.error = &s->state->error;
+        RN_HIP(launch_attend(ap, kAttendPrefill, c.heads, count, first + count, st));
+        RN_HIP(launch_norm_quantise(A, nullptr, count, d, c.norm_eps, Xq, sx, nullptr, st));
+        RN_HIP(launch_gemm(GemmParams{Xq, sx, L.out.W, L.out.sW, count, d, d, X, d, nullptr, 0}, kGemmResidual, kPanel,
+                           false, st));
+        RN_HIP(launch_norm_quantise(X, L.norm_ffn, count, d, c.norm_eps, Xq, sx, nullptr, st));
+        RN_HIP(launch_gemm(GemmParams{Xq, sx, L.gate_up.W, L.gate_up.sW, count, 2 * f, d, F, f, nullptr, f},
+                           kGemmSilu, kPanel, false, st));
+        RN_HIP(launch_norm_quantise(F, nullptr, count, f, c.norm_eps, Xq, sx, nullptr, st));
+        RN_HIP(launch_gemm(GemmParams{Xq, sx, L.down.W, L.down.sW, count, d, f, X, d, nullptr, 0}, kGemmResidual,
+                           kPanel, false, st));
+    }
+    RN_HIP(hipMemcpyAsync(s->x, X + (size_t)(count - 1) * d, 4 * (size_t)d, hipMemcpyDeviceToDevice, st));
+    RN_HIP(launch_norm_rows(s->x, m->norm_final, 1, d, c.norm_eps, s->hidden, st));
+    s->length += count;
+    s->has_hidden = true;
+    return check_state_error(s);
+}
+
+// ---- Batch ------------------------------------------------------------------------
+
+int rn_batch_create(const rn_model* m, int count, int capacity, rn_batch** out) {
+    RN_REQUIRE(m && out, "null argument");
+    const rn_config& c = m->cfg;
+    RN_REQUIRE(count >= 1 && count <= 4096, "count must be 1..4096");
+    RN_REQUIRE(capacity >= 1 && capacity <= c.max_positions && capacity <= 16384, "capacity must be 1..max_positions");
+    rn_batch* b = new (std::nothrow) rn_batch();
+    if (!b) return fail(RN_ERR_MEMORY, "out of host memory");
+    b->model = m;
+    b->count = count;
+    b->capacity = capacity;
+    b->lengths.assign(count, 0);
+    const size_t ce = cache_elems(c, capacity) * count, d = c.d_model, f = c.ffn, n = count;
+    const size_t total = 2 * align_up(ce * 2) + align_up(4 * n) + align_up(4 * n * d) * 2 + align_up(4 * n * 3 * d) +
+                         align_up(4 * n * f) + align_up(4 * n * c.vocab) + align_up(n * (f > d ? f : d)) +
+                         align_up(4 * n) * 3;
+    if (hipMalloc(&b->arena, total) != hipSuccess) {
+        delete b;
+        return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", total);
+    }
+    Arena a{(char*)b->arena, 0, total};
+    b->kc = (__half*)a.take(ce * 2);
+    b->vc = (__half*)a.take(ce * 2);
+    b->pos = (int32_t*)a.take(4 * n);
+    b->X = (float*)a.take(4 * n * d);
+    b->A = (float*)a.take(4 * n * d);
+    b->QKV = (float*)a.take(4 * n * 3 * d);
+    b->F = (float*)a.take(4 * n * f);
+    b->logits = (float*)a.take(4 * n * c.vocab);
+    b->Xq = (int8_t*)a.take(n * (f > d ? f : d));
+    b->sx = (float*)a.take(4 * n);
+    b->tokens = (uint32_t*)a.take(4 * n);
+    b->error = (int32_t*)a.take(4 * n);
+    if (hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipMemsetAsync(b->arena, 0, total, b->stream) != hipSuccess || hipStreamSynchronize(b->stream) != hipSuccess) {
+        if (b->stream) (void)hipStreamDestroy(b->stream);
+        (void)hipFree(b->arena);
+        delete b;
+        return fail(RN_ERR_DEVICE, "batch initialisation failed");
+    }
+    *out = b;
+    return RN_OK;
+}
+
+int rn_batch_free(rn_batch* b) {
+    if (!b) return RN_OK;
+    if (b->stream) (void)hipStreamSynchronize(b->stream);
+    if (b->ids) (void)hipFree(b->ids);
+    (void)hipFree(b->arena);
+    if (b->stream) (void)hipStreamDestroy(b->stream);
+    delete b;
+    return RN_OK;
+}
+
+int rn_batch_truncate(rn_batch* b, const int32_t* lengths) {
+    RN_REQUIRE(b && lengths, "null argument");
+    for (int i = 0; i < b->count; ++i)
+        RN_REQUIRE(lengths[i] >= 0 && lengths[i] <= b->lengths[i], "sequence %d: length %d outside 0..%d", i, lengths[i],
+                   b->lengths[i]);
+    for (int i = 0; i < b->count; ++i) b->lengths[i] = lengths[i];
+    return RN_OK;
+}
+
+int rn_batch_stream(const rn_batch* b, void** stream) {
+    RN_REQUIRE(b && stream, "null argument");
+    *stream = b->stream;
+    return RN_OK;
+}
+
+int rn_batch_set_cache(rn_batch* b, int sequence, int length, const uint16_t* keys, const uint16_t* values) {
+    RN_REQUIRE(b && (length == 0 || (keys && values)), "null argument");
+    RN_REQUIRE(sequence >= 0 && sequence < b->count, "sequence %d outside 0..%d", sequence, b->count);
+    RN_REQUIRE(length >= 0 && length <= b->capacity, "length %d outside 0..capacity", length);
+    const rn_config& c = b->model->cfg;
+    const size_t seq = cache_elems(c, b->capacity) * sequence;
+    if (length > 0) {
+        const size_t row = (size_t)length * c.head_dim * 2, pitch = (size_t)b->capacity * c.head_dim * 2;
+        const size_t heads = (size_t)c.layers * c.heads;
+        RN_HIP(hipMemcpy2DAsync(b->kc + seq, pitch, keys, row, row, heads, hipMemcpyHostToDevice, b->stream));
+        RN_HIP(hipMemcpy2DAsync(b->vc + seq, pitch, values, row, row, heads, hipMemcpyHostToDevice, b->stream));
+    }
+    b->lengths[sequence] = length;
+    RN_HIP(hipMemcpyAsync(b->pos + sequence, &b->lengths[sequence], 4, hipMemcpyHostToDevice, b->stream));
+    RN_HIP(hipStreamSynchronize(b->stream));
+    return RN_OK;
+}
+
+// One step for every sequence: embed the current tokens, the layer stack with
+// M=count MFMA products and ragged attention, the final norm, the tied logits
+// product and a per-row argmax that becomes the next tokens.
+static int enqueue_batch_step(rn_batch* b, int steps, int step) {
+    const rn_model* m = b->model;
+    const rn_config& c = m->cfg;
+    const int n = b->count, d = c.d_model, f = c.ffn;
+    hipStream_t st = b->stream;
+    RN_HIP(launch_embed_rows(b->tokens, n, m->embedding.W, m->embedding.sW, d, c.vocab, m->embed_scale, b->X, b->error,
+                             st));
+    for (int l = 0; l < c.layers; ++l) {
+        const LayerDev& L = m->layers[l];
+        RN_HIP(launch_norm_quantise(b->X, L.norm_attn, n, d, c.norm_eps, b->Xq, b->sx, nullptr, st));
+        RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, L.qkv.W, L.qkv.sW, n, 3 * d, d, b->QKV, 3 * d, nullptr, 0},
+                           kGemmStore, kPanel, false, st));
+        AttendParams ap{};
+        ap.qkv = b->QKV;
+        ap.kc = b->kc;
+        ap.vc = b->vc;
+        ap.seq_stride = cache_elems(c, b->capacity);
+        ap.layer = l;
+        ap.heads = c.heads;
+        ap.capacity = b->capacity;
+        ap.d_model = d;
+        ap.pos = b->pos;
+        ap.pos_stride = 1;
+        ap.rope_cos = m->rope_cos;
+        ap.rope_sin = m->rope_sin;
+        ap.out = b->A;
+        ap.error = b->error;
+        RN_HIP(launch_attend(ap, kAttendDecode, c.heads, n, b->capacity, st));
+        RN_HIP(launch_norm_quantise(b->A, nullptr, n, d, c.norm_eps, b->Xq, b->sx, nullptr, st));
+        RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, L.out.W, L.out.sW, n, d, d, b->X, d, nullptr, 0}, kGemmResidual,
+                           kPanel, false, st));
+        RN_HIP(launch_norm_quantise(b->X, L.norm_ffn, n, d, c.norm_eps, b->Xq, b->sx, nullptr, st));
+        RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, L.gate_up.W, L.gate_up.sW, n, 2 * f, d, b->F, f, nullptr, f},
+                           kGemmSilu, kPanel, false, st));
+        RN_HIP(launch_norm_quantise(b->F, nullptr, n, f, c.norm_eps, b->Xq, b->sx, nullptr, st));
+        RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, L.down.W, L.down.sW, n, d, f, b->X, d, nullptr, 0}, kGemmResidual,
+                           kPanel, false, st));
+    }
+    // final norm, then the per-row quantisation of the hidden state (session.rs:140-142, 166-177)
+    RN_HIP(launch_norm_quantise(b->X, m->norm_final, n, d, c.norm_eps, b->Xq, b->sx, nullptr, st));
+    RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, m->embedding.W, m->embedding.sW, n, c.vocab, d, b->logits, c.vocab,
+                                  nullptr, 0},
+                       kGemmStore, kPlane, false, st));
+    RN_HIP(launch_argmax_rows(b->logits, n, c.vocab, b->tokens, b->ids, steps, step, st));
+    RN_HIP(launch_advance_positions(b->pos, n, 1, st));
+    return RN_OK;
+}
+
+int rn_batch_decode_greedy(rn_batch* b, const uint32_t* first, int steps, uint32_t* ids) {
+    RN_REQUIRE(b && first && (ids || steps == 0), "null argument");
+    RN_REQUIRE(steps >= 0, "steps must be non-negative");
+    if (steps == 0) return RN_OK;
+    const rn_config& c = b->model->cfg;
+    for (int i = 0; i < b->count; ++i) {
+        RN_REQUIRE(first[i] < (uint32_t)c.vocab, "first token %u of sequence %d outside the vocabulary", first[i], i);
+        if (b->lengths[i] + steps > b->capacity)
+            return fail(RN_ERR_CAPACITY, "sequence %d: %d + %d positions exceed the capacity %d", i, b->lengths[i], steps,
+                        b->capacity);
+    }
+    if (b->ids_steps < steps) {
+        RN_HIP(hipStreamSynchronize(b->stream));
+        if (b->ids) RN_HIP(hipFree(b->ids));
+        b->ids = nullptr;
+        if (hipMalloc(&b->ids, 4 * (size_t)b->count * steps) != hipSuccess) return fail(RN_ERR_MEMORY, "id buffer");
+        b->ids_steps = steps;
+    }
+    RN_HIP(hipMemcpyAsync(b->tokens, first, 4 * (size_t)b->count, hipMemcpyHostToDevice, b->stream));
+    RN_HIP(hipMemcpyAsync(b->pos, b->lengths.data(), 4 * (size_t)b->count, hipMemcpyHostToDevice, b->stream));
+    for (int step = 0; step < steps; ++step) {
+        int rc = enqueue_batch_step(b, steps, step);
+        if (rc) return rc;
+    }
+    RN_HIP(hipMemcpyAsync(ids, b->ids, 4 * (size_t)b->count * steps, hipMemcpyDeviceToHost, b->stream));
+    int32_t err = 0;
+    RN_HIP(hipMemcpyAsync(&err, b->error, 4, hipMemcpyDeviceToHost, b->stream));
+    RN_HIP(hipStreamSynchronize(b->stream));
+    for (int i = 0; i < b->count; ++i) b->lengths[i] += steps;
+    if (err) return fail(RN_ERR_STATE, "device reported error flags 0x%x", err);
+    return RN_OK;
+}
+
+}  // extern "C"

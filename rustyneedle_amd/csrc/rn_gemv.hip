@@ -1,0 +1,325 @@
+// rn_gemv.hip — batch-1 quantised products for gfx950 (the decode GEMVs).
+//
+// Replaces the CPU row products of crates/kernels (matrix.rs:155-202 fan-out,
+// panel.rs:153-197 panel tile, neon.rs:126-183 row_dot) for int8 codes with one
+// fp32 scale per 32 columns.
+//
+// Shape of one block: a single wave (64 lanes) owns ROWS consecutive rows.
+//   1. Every lane issues its 128-bit weight loads first (NL loads of 16 codes),
+//      and the block stages its ROWS x G scales in LDS; the HBM latency of
+//      those loads overlaps the prologue.
+//   2. Prologue: the block reads the input vector and quantises it per row
+//      (ops.rs:112-118), optionally after the zero-centred RMSNorm
+//      (ops.rs:44-50, sum-of-squares tree of ops.rs:7-17) and, for layer 0 of a
+//      decode step, after gathering the embedding row of the current token.
+//      Every block repeats this small prologue instead of synchronising the
+//      grid: the vector is 2-8 KB and stays in L2.
+//   3. v_dot4_i32_i8 over the 16 codes of each load; lane pairs hold the two
+//      halves of one 32-code group and are added exactly with a lane shuffle.
+//   4. Group accumulators go through LDS to lane r, which runs row r's epilogue
+//      sequentially over groups (panel form fmaf(acc, sW*sx, total), or plane
+//      form total + (acc*sW)*sx), then the fused tail: store, residual add,
+//      silu(gate)*up, or logits + on-device argmax.
+#include "rn_device.hpp"
+#include "rn_internal.hpp"
+
+namespace rn {
+
+template <int K, int ROWS, int PRO, int EPI, int FORM>
+__global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
+    constexpr int G = K / kGroup;                       // groups per row
+    constexpr int CPR = K / 16;                         // 16-byte chunks per row
+    constexpr int RPL = CPR <= 64 ? 64 / CPR : 1;       // rows covered by one load instruction
+    constexpr int LPR = CPR <= 64 ? 1 : CPR / 64;       // load instructions per row
+    constexpr int NL = CPR <= 64 ? ROWS / RPL : ROWS * LPR;
+    constexpr int XC = LPR;                             // input chunks each lane needs
+    constexpr int E = K / 64;                           // input values per lane in the prologue
+    constexpr int H = ROWS / 2;
+    static_assert(ROWS % RPL == 0, "rows per block must cover whole load instructions");
+    static_assert(EPI != kSilu || ROWS % 2 == 0, "silu blocks pair gate and up rows");
+    static_assert(ROWS <= 64, "one lane per row in the epilogue");
+
+    constexpr bool NORM = PRO == kNorm || PRO == kEmbedNorm;
+    __shared__ __align__(16) int8_t xq_s[K];
+    __shared__ __align__(16) int acc_s[ROWS * G];
+    __shared__ __align__(16) float sq_s[NORM ? K : 4];
+
+    const int lane = threadIdx.x;
+    int si = 0;
+    for (int i = 1; i < p.nseg; ++i)
+        if ((int)blockIdx.x >= p.seg[i].block0) si = i;
+    const Segment sg = p.seg[si];
+    const int blk = (int)blockIdx.x - sg.block0;
+
+    auto row_of = [&](int rr) -> int {
+        if constexpr (EPI == kSilu) return rr < H ? blk * H + rr : p.half_rows + blk * H + (rr - H);
+        else return blk * ROWS + rr;
+    };
+    auto row_valid = [&](int rr) -> bool {
+        if constexpr (EPI == kSilu) return blk * H + (rr < H ? rr : rr - H) < p.half_rows;
+        else return blk * ROWS + rr < sg.rows;
+    };
+    // The row a lane loads from: past the end of the matrix it re-reads the last
+    // row (never stored), so loads need no condition.
+    auto row_load = [&](int rr) -> int {
+        if constexpr (EPI == kSilu) {
+            const int i = min(blk * H + (rr < H ? rr : rr - H), p.half_rows - 1);
+            return rr < H ? i : p.half_rows + i;
+        } else {
+            return min(blk * ROWS + rr, sg.rows - 1);
+        }
+    };
+    auto load_row = [&](int j) -> int { return CPR <= 64 ? j * RPL + lane / CPR : j / LPR; };
+    auto load_chunk = [&](int j) -> int { return CPR <= 64 ? lane % CPR : (j % LPR) * 64 + lane; };
+
+    // Memory-level order matters: loads complete in issue order for the wait
+    // counter, so the prologue inputs go first, then the weights, then the
+    // row scales; the prologue then waits only for its own inputs.
+    // 1a. prologue inputs
+    float v[E];
+    float gv[NORM ? E : 1];
+    if constexpr (PRO == kEmbedNorm) {
+        uint32_t token = p.state->token;
+        if (token >= (uint32_t)p.vocab) {
+            if (lane == 0 && blockIdx.x == 0) atomicOr(&p.state->error, 1);
+            token = 0;
+        }
+        const int8_t* er = p.embW + (size_t)token * K + lane * E;
+        const float scale = p.embS[(size_t)token * G + (lane * E) / kGroup];  // E divides 32
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = ((float)er[e] * scale) * p.embed_scale;
+    } else if constexpr (PRO != kCodes) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(p.x + lane * E + e);
+            v[e] = t.x;
+            v[e + 1] = t.y;
+            v[e + 2] = t.z;
+            v[e + 3] = t.w;
+        }
+    }
+    if constexpr (NORM) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(p.gain + lane * E + e);
+            gv[e] = t.x;
+            gv[e + 1] = t.y;
+            gv[e + 2] = t.z;
+            gv[e + 3] = t.w;
+        }
+    }
+
+    // 1b. weights: unconditional loads (a branch around a load would make the
+    // wait counter unknowable and force a full wait)
+    int4 w[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+        w[j] = *reinterpret_cast<const int4*>(sg.W + (size_t)row_load(load_row(j)) * K + load_chunk(j) * 16);
+    // 1c. lane r < ROWS holds the G scales of its row
+    float4 sv[G / 4];
+    const bool mine = lane < ROWS && row_valid(lane);
+    {
+        const float4* src = reinterpret_cast<const float4*>(sg.sW + (size_t)row_load(min(lane, ROWS - 1)) * G);
+#pragma unroll
+        for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
+    }
+    // keep the scheduler from sinking those loads below the prologue
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. prologue: the int8 codes of the input vector and its scale
+    float sx;
+    int4 xc[XC];
+    if constexpr (PRO == kCodes) {
+        sx = p.xs[0];
+#pragma unroll
+        for (int i = 0; i < XC; ++i) xc[i] = *reinterpret_cast<const int4*>(p.xq + load_chunk(i) * 16);
+    } else {
+        if constexpr (PRO == kEmbedNorm) {
+            if (blockIdx.x == 0)
+#pragma unroll
+                for (int e = 0; e < E; ++e) p.x_out[lane * E + e] = v[e];
+        }
+        if constexpr (NORM) {
+            // ops.rs:7-17: lane j of eight sums elements j, j+8, j+16, ... in index
+            // order. Squares are stored transposed (strided lane j's run is
+            // contiguous) so each of the eight lanes reads its run with 128-bit reads.
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const int idx = lane * E + e;
+                sq_s[(idx % 8) * (K / 8) + idx / 8] = v[e] * v[e];
+            }
+            __syncthreads();
+            float s = 0.0f;
+            if (lane < 8) {
+                const float4* run = reinterpret_cast<const float4*>(sq_s + lane * (K / 8));
+#pragma unroll
+                for (int c = 0; c < K / 32; ++c) {
+                    const float4 t = run[c];
+                    s = s + t.x;
+                    s = s + t.y;
+                    s = s + t.z;
+                    s = s + t.w;
+                }
+            }
+            float total = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) total = total + __shfl(s, j, 64);
+            total = total + 0.0f;  // the (empty) tail of ops.rs:15-16
+            const float mean_square = total / (float)K;
+            const float inverse = 1.0f / sqrtf(mean_square + p.eps);
+#pragma unroll
+            for (int e = 0; e < E; ++e) v[e] = ((1.0f + gv[e]) * v[e]) * inverse;
+            if (p.hidden_out != nullptr && blockIdx.x == 0)
+#pragma unroll
+                for (int e = 0; e < E; ++e) p.hidden_out[lane * E + e] = v[e];
+        }
+        float peak = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
+        peak = wave_max(peak);
+        sx = int8_scale_from_peak(peak);
+#pragma unroll
+        for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)quantise_one(v[e], sx);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < XC; ++i) xc[i] = *reinterpret_cast<const int4*>(xq_s + load_chunk(i) * 16);
+    }
+
+    // 3. exact int32 group accumulators
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        int part = dot16(w[j], xc[CPR <= 64 ? 0 : (j % LPR)], 0);
+        part = part + __shfl_xor(part, 1, 64);
+        if ((lane & 1) == 0) acc_s[load_row(j) * G + load_chunk(j) / 2] = part;
+    }
+    __syncthreads();
+
+    // 4. sequential per-row epilogue (tree T4), one lane per row
+    float total = 0.0f;
+    if (mine) {
+        const int4* arow = reinterpret_cast<const int4*>(acc_s + lane * G);
+#pragma unroll
+        for (int i = 0; i < G / 4; ++i) {
+            const int4 a4 = arow[i];
+            const float a[4] = {(float)a4.x, (float)a4.y, (float)a4.z, (float)a4.w};
+            const float s[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if constexpr (FORM == kPanel)
+                    total = fmaf(a[k], s[k] * sx, total);  // panel.rs:184-188
+                else
+                    total = total + (a[k] * s[k]) * sx;    // neon.rs:180
+            }
+        }
+    }
+    if (sg.acc != nullptr)
+        for (int idx = lane; idx < ROWS * G; idx += 64)
+            if (row_valid(idx / G)) sg.acc[(size_t)row_of(idx / G) * G + (idx % G)] = acc_s[idx];
+
+    if constexpr (EPI == kStore) {
+        if (mine) sg.y[row_of(lane)] = total;
+    } else if constexpr (EPI == kResidual) {
+        if (mine) {
+            const int r = row_of(lane);
+            sg.y[r] = sg.y[r] + total;
+        }
+    } else if constexpr (EPI == kSilu) {
+        const float up = __shfl(total, (lane + H) & 63, 64);
+        if (lane < H && mine) sg.y[blk * H + lane] = silu(total) * up;
+    } else {  // kArgmax: logits plus the greedy token (generator.rs:257-265)
+        if (mine) sg.y[row_of(lane)] = total;
+        uint64_t key = mine ? argmax_key(total, (uint32_t)row_of(lane)) : 0ull;
+        key = wave_max_u64(key);
+        if (lane == 0) {
+            DecodeState* st = p.state;
+            atomicMax(&st->key, (unsigned long long)key);
+            __threadfence();
+            const unsigned ticket = atomicAdd(&st->counter, 1u);
+            if (ticket == gridDim.x - 1) {  // last block: every other block's key is in
+                __threadfence();
+                const unsigned long long best = atomicAdd(&st->key, 0ull);
+                const float first = __hip_atomic_load(&sg.y[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint32_t index = (first != first) ? 0u : argmax_index(best);
+                st->token = index;
+                const uint32_t step = st->step;
+                if (p.ids != nullptr && step < st->ids_capacity) p.ids[step] = index;
+                st->step = step + 1;
+                st->key = 0ull;
+                st->counter = 0u;
+            }
+        }
+    }
+}
+
+template <int K, int ROWS, int PRO, int EPI, int FORM>
+static hipError_t launch_one(const GemvParams& p, int blocks, hipStream_t stream) {
+    hipLaunchKernelGGL((gemv_kernel<K, ROWS, PRO, EPI, FORM>), dim3(blocks), dim3(64), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <int K, int ROWS>
+static hipError_t dispatch_pe(const GemvParams& p, int prologue, int epilogue, int form, int blocks,
+                              hipStream_t s) {
+    // API products: quantise + store, either form.
+    if (prologue == kQuant && epilogue == kStore)
+        return form == kPanel ? launch_one<K, ROWS, kQuant, kStore, kPanel>(p, blocks, s)
+                              : launch_one<K, ROWS, kQuant, kStore, kPlane>(p, blocks, s);
+    if (prologue == kCodes && epilogue == kStore)
+        return form == kPanel ? launch_one<K, ROWS, kCodes, kStore, kPanel>(p, blocks, s)
+                              : launch_one<K, ROWS, kCodes, kStore, kPlane>(p, blocks, s);
+    if (form == kPanel) {
+        if (prologue == kQuant && epilogue == kResidual) return launch_one<K, ROWS, kQuant, kResidual, kPanel>(p, blocks, s);
+        if constexpr (K == 512) {
+            if (prologue == kNorm && epilogue == kStore) return launch_one<K, ROWS, kNorm, kStore, kPanel>(p, blocks, s);
+            if (prologue == kEmbedNorm && epilogue == kStore) return launch_one<K, ROWS, kEmbedNorm, kStore, kPanel>(p, blocks, s);
+            if (prologue == kNorm && epilogue == kSilu) return launch_one<K, ROWS, kNorm, kSilu, kPanel>(p, blocks, s);
+        }
+    } else {
+        if (prologue == kQuant && epilogue == kArgmax) return launch_one<K, ROWS, kQuant, kArgmax, kPlane>(p, blocks, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+int gemv_rows_per_block(int rows, int columns, int epilogue) {
+    if (epilogue == kSilu) return 8;
+    const int min_rows = columns == 512 ? 2 : 1;
+    int r = columns == 512 ? 32 : (columns == 1024 ? 16 : 8);
+    // Tall products: more rows per block amortise the input prologue, while
+    // keeping >= 2048 blocks (eight waves per CU) in flight.
+    while (r > 8 && (rows + r - 1) / r < 2048) r /= 2;
+    // Decode-sized products: enough blocks to cover all 256 CUs.
+    while (r > min_rows && (rows + r - 1) / r < 256) r /= 2;
+    return r;
+}
+
+hipError_t launch_gemv(const GemvParams& p, int columns, int prologue, int epilogue, int form, int rows_per_block,
+                       int blocks, hipStream_t stream) {
+    if (blocks <= 0) return hipSuccess;
+    switch (columns) {
+        case 512:
+            if (rows_per_block == 2) return dispatch_pe<512, 2>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 4) return dispatch_pe<512, 4>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 8) return dispatch_pe<512, 8>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 16) return dispatch_pe<512, 16>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 32) return dispatch_pe<512, 32>(p, prologue, epilogue, form, blocks, stream);
+            break;
+        case 1024:
+            if (rows_per_block == 1) return dispatch_pe<1024, 1>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 2) return dispatch_pe<1024, 2>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 4) return dispatch_pe<1024, 4>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 8) return dispatch_pe<1024, 8>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 16) return dispatch_pe<1024, 16>(p, prologue, epilogue, form, blocks, stream);
+            break;
+        case 2048:
+            if (rows_per_block == 1) return dispatch_pe<2048, 1>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 2) return dispatch_pe<2048, 2>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 4) return dispatch_pe<2048, 4>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 8) return dispatch_pe<2048, 8>(p, prologue, epilogue, form, blocks, stream);
+            break;
+        default:
+            break;
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace rn

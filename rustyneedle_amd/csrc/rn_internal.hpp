@@ -1,0 +1,138 @@
+// rn_internal.hpp — launch descriptors shared between the kernel translation
+// units and the C-ABI layer (rn_api.hip). Plain structs passed by value as
+// kernel arguments.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rn {
+
+constexpr int kGroup = 32;  // int8 codes per fp32 weight scale
+
+// Per-session decode state in device memory. The greedy step reads `token`,
+// the attention kernels read `pos`, the logits kernel's last block writes the
+// argmax back into `token` and `ids[step]`.
+struct DecodeState {
+    uint32_t token;
+    int32_t pos;
+    uint32_t step;
+    uint32_t counter;
+    unsigned long long key;
+    int32_t error;
+    uint32_t ids_capacity;
+};
+
+enum GemvPrologue { kQuant = 0, kNorm = 1, kEmbedNorm = 2, kCodes = 3 };
+enum GemvEpilogue { kStore = 0, kResidual = 1, kSilu = 2, kArgmax = 3 };
+enum ProductForm { kPanel = 0, kPlane = 1 };
+
+// One matrix of a (possibly fused) batch-1 product launch.
+struct Segment {
+    const int8_t* W;   // [rows][K]
+    const float* sW;   // [rows][K/32]
+    float* y;          // store target (kStore/kSilu/kArgmax) or residual x (kResidual)
+    int32_t* acc;      // nullable [rows][K/32]
+    int rows;          // rows of W (kSilu: 2*half_rows)
+    int block0;        // first block of this segment
+};
+constexpr int kMaxSegments = 8;
+
+struct GemvParams {
+    Segment seg[kMaxSegments];
+    int nseg;
+    int half_rows;        // kSilu: ffn width (gate rows 0..half-1, up rows half..2*half-1)
+    const float* x;       // input vector (kQuant/kNorm)
+    const float* gain;    // zero-centred norm gains (kNorm/kEmbedNorm)
+    float eps;
+    const int8_t* xq;     // kCodes: pre-quantised input
+    const float* xs;
+    const int8_t* embW;   // kEmbedNorm: embedding codes/scales, the token comes from state
+    const float* embS;
+    float embed_scale;    // sqrt(d_model)
+    int vocab;
+    float* x_out;         // kEmbedNorm: block 0 writes the embedded row (the residual)
+    float* hidden_out;    // kNorm: block 0 writes the normed input (nullable)
+    DecodeState* state;   // kEmbedNorm (token) / kArgmax (result)
+    uint32_t* ids;        // kArgmax: greedy ids written at state->step
+};
+
+// Launch one batch-1 product. `columns` in {512, 1024, 2048}; returns
+// hipErrorInvalidValue for an unsupported combination.
+hipError_t launch_gemv(const GemvParams& p, int columns, int prologue, int epilogue, int form,
+                       int rows_per_block, int blocks, hipStream_t stream);
+int gemv_rows_per_block(int rows, int columns, int epilogue);
+
+// ---- attention --------------------------------------------------------------
+enum AttendMode { kAttendDecode = 0, kAttendPrefill = 1, kAttendRaw = 2 };
+
+struct AttendParams {
+    // kAttendDecode: q/k/v rows come from qkv [batch][3*d]; rotary is applied and
+    //   k/v appended at pos[b]; grid (heads, batch).
+    // kAttendPrefill: rotated q from q [count][d], positions first+t; grid (heads, count).
+    // kAttendRaw: q [count][64], K/V [count][stride][64], lengths; grid (count).
+    const float* qkv;
+    const float* q;
+    __half* kc;
+    __half* vc;
+    size_t seq_stride;    // elements between sequences' caches (decode batch)
+    int layer, heads, capacity, d_model;
+    const int32_t* pos;   // decode: [batch] positions (state->pos for batch 1)
+    int pos_stride;       // int32 stride between positions (DecodeState vs plain array)
+    int first;            // prefill: position of token 0
+    const int32_t* lengths;
+    int stride;           // raw: positions per problem
+    const float* rope_cos;  // [max_positions][32]
+    const float* rope_sin;
+    float* out;
+    int32_t* error;
+};
+
+hipError_t launch_attend(const AttendParams& p, int mode, int grid_x, int grid_y, int max_length,
+                         hipStream_t stream);
+
+// Rotary + fp16 append for `count` tokens of one sequence (prefill): writes the
+// rotated queries to q_out [count][d] and keys/values into the cache.
+hipError_t launch_rope_append(const float* qkv, float* q_out, __half* kc, __half* vc, int layer, int heads,
+                              int capacity, int d_model, int first, int count, const float* rope_cos,
+                              const float* rope_sin, hipStream_t stream);
+
+// ---- multi-token products (i8 MFMA) ----------------------------------------------
+enum GemmEpilogue { kGemmStore = 0, kGemmResidual = 1, kGemmSilu = 2 };
+
+struct GemmParams {
+    const int8_t* X;   // [M][K] quantised tokens
+    const float* sx;   // [M] token scales
+    const int8_t* W;   // [N][K]
+    const float* sW;   // [N][K/32]
+    int M, N, K;
+    float* Y;          // [M][ldy] (kGemmSilu: [M][half])
+    int ldy;
+    int32_t* acc;      // dump only: [M][N][K/32]
+    int half;          // kGemmSilu: gate rows 0..half-1, up rows half..2*half-1 (N == 2*half)
+};
+
+hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, hipStream_t stream);
+hipError_t launch_norm_quantise(const float* x, const float* gain, int count, int n, float eps, int8_t* codes,
+                                float* scales, float* normed, hipStream_t stream);
+hipError_t launch_embed_rows(const uint32_t* tokens, int count, const int8_t* E, const float* sE, int d, int vocab,
+                             float scale, float* X, int32_t* error, hipStream_t stream);
+hipError_t launch_argmax_rows(const float* logits, int count, int n, uint32_t* tokens, uint32_t* ids, int steps,
+                              int step, hipStream_t stream);
+hipError_t launch_advance_positions(int32_t* pos, int count, int by, hipStream_t stream);
+
+// ---- elementwise / helpers ----------------------------------------------------
+hipError_t launch_quantise_rows(const float* x, int count, int columns, int8_t* codes, float* scales,
+                                hipStream_t stream);
+hipError_t launch_norm_rows(const float* x, const float* gain, int count, int n, float eps, float* out,
+                            hipStream_t stream);
+hipError_t launch_fast_exp(const float* x, float* y, int n, int silu, hipStream_t stream);
+hipError_t launch_finish_push(const float* x, const float* gain, int n, float eps, float* hidden,
+                              DecodeState* state, hipStream_t stream);
+// Overwrites token/pos/step/ids_capacity and clears the argmax key and ticket.
+hipError_t launch_set_state(DecodeState* state, uint32_t token, int32_t pos, uint32_t step, uint32_t ids_capacity,
+                            hipStream_t stream);
+
+}  // namespace rn

@@ -1,0 +1,209 @@
+"""GPU parity of the decoder (Session / Model / Batch) against the oracle.
+
+Bit-exact throughout: caches, hidden states, logits and greedy token ids.
+The full decode workload (20 layers, 256 cached positions, 64 greedy tokens)
+is checked against the oracle at full size; the batch workload is checked
+against single-sequence GPU sessions (bit-exact) and a subset against the
+oracle.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import rustyneedle_amd as rn
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tiny(tiny_config, tiny_weights):
+    return rn.Model(tiny_config, tiny_weights), oracle.OracleModel(tiny_config, tiny_weights)
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def test_rotary_table_matches_oracle(tiny, tiny_config):
+    gm, om = tiny
+    cos, sin = gm.rotary_table()
+    assert np.array_equal(_bits(cos), _bits(om.rope_cos))
+    assert np.array_equal(_bits(sin), _bits(om.rope_sin))
+
+
+def test_push_hidden_logits_and_cache(tiny, tiny_config):
+    gm, om = tiny
+    k, v = rn.synthetic_cache(tiny_config, 40, "push")
+    gs, os_ = gm.session(64), om.session(64)
+    gs.set_cache(k, v)
+    os_.set_cache(k, v)
+    for tok in (3, 999, 0, 512):
+        gs.push(tok)
+        os_.push(tok)
+        assert np.array_equal(_bits(gs.hidden()), _bits(os_.hidden))
+        assert np.array_equal(_bits(gs.logits()), _bits(os_.logits()))
+    assert len(gs) == os_.length == 44
+    gk, gv = gs.get_cache()
+    assert np.array_equal(gk.view(np.uint16), os_.keys[:, :, :44])
+    assert np.array_equal(gv.view(np.uint16), os_.values[:, :, :44])
+
+
+def test_push_from_empty_session(tiny):
+    gm, om = tiny
+    gs, os_ = gm.session(8), om.session(8)
+    for tok in (1, 2):
+        gs.push(tok)
+        os_.push(tok)
+    assert np.array_equal(_bits(gs.logits()), _bits(os_.logits()))
+
+
+def test_greedy_tiny_bit_identical(tiny, tiny_config):
+    gm, om = tiny
+    k, v = rn.synthetic_cache(tiny_config, 100, "greedy")
+    gs, os_ = gm.session(200), om.session(200)
+    gs.set_cache(k, v)
+    os_.set_cache(k, v)
+    ids = gs.decode_greedy(17, 40)
+    ref = os_.greedy(17, 40)
+    assert ids.tolist() == ref.tolist()
+    assert len(gs) == 140
+    # the session continues exactly like the oracle's after the greedy run
+    assert np.array_equal(_bits(gs.logits()), _bits(os_.logits()))
+
+
+def test_greedy_equals_push_logits_argmax(tiny, tiny_config):
+    """The on-device argmax of the captured step equals host argmax of logits."""
+    gm, _ = tiny
+    k, v = rn.synthetic_cache(tiny_config, 20, "loop")
+    a, b = gm.session(64), gm.session(64)
+    a.set_cache(k, v)
+    b.set_cache(k, v)
+    ids = a.decode_greedy(5, 12)
+    tok, manual = 5, []
+    for _ in range(12):
+        b.push(tok)
+        tok = oracle.argmax(b.logits())
+        manual.append(tok)
+    assert ids.tolist() == manual
+
+
+def test_feed_prefill_bit_exact_and_equals_pushes(tiny, tiny_config):
+    gm, om = tiny
+    k, v = rn.synthetic_cache(tiny_config, 30, "feed")
+    tokens = rn.synth_tokens(rn.SEED, "feed.tokens", tiny_config["vocab"], 70)
+    gs, os_, gp = gm.session(128), om.session(128), gm.session(128)
+    for s in (gs, os_, gp):
+        s.set_cache(k, v)
+    gs.feed(tokens)
+    os_.feed(tokens)
+    for t in tokens:
+        gp.push(int(t))
+    assert np.array_equal(_bits(gs.hidden()), _bits(os_.hidden))
+    assert np.array_equal(_bits(gs.hidden()), _bits(gp.hidden()))
+    assert np.array_equal(_bits(gs.logits()), _bits(os_.logits()))
+    ck, cv = gs.get_cache()
+    pk, pv = gp.get_cache()
+    assert np.array_equal(ck.view(np.uint16), pk.view(np.uint16))
+    assert np.array_equal(cv.view(np.uint16), pv.view(np.uint16))
+    assert np.array_equal(ck.view(np.uint16), os_.keys[:, :, :100])
+
+
+@pytest.mark.parametrize("count", [1, 3, 4, 65])
+def test_feed_small_and_ragged_counts(tiny, count):
+    gm, om = tiny
+    tokens = (np.arange(count) * 37 + 11) % 1000
+    gs, os_ = gm.session(96), om.session(96)
+    gs.feed(tokens)
+    os_.feed(tokens)
+    assert np.array_equal(_bits(gs.logits()), _bits(os_.logits()))
+
+
+def test_clone_is_independent(tiny, tiny_config):
+    gm, _ = tiny
+    k, v = rn.synthetic_cache(tiny_config, 10, "clone")
+    base = gm.session(32)
+    base.set_cache(k, v)
+    base.push(4)
+    c = base.clone()
+    assert len(c) == 11
+    assert np.array_equal(_bits(c.logits()), _bits(base.logits()))
+    c.push(9)
+    base.push(9)
+    assert np.array_equal(_bits(c.logits()), _bits(base.logits()))
+    c.push(1)
+    assert len(c) == 13 and len(base) == 12
+
+
+def test_capacity_and_argument_errors(tiny):
+    gm, _ = tiny
+    s = gm.session(4)
+    with pytest.raises(rn.RnError) as e:
+        s.push(1000)  # outside the vocabulary
+    assert e.value.code == rn.RN_ERR_ARGUMENT
+    s.feed([1, 2, 3])
+    with pytest.raises(rn.RnError) as e:
+        s.decode_greedy(1, 2)
+    assert e.value.code == rn.RN_ERR_CAPACITY
+    s.push(5)
+    with pytest.raises(rn.RnError) as e:
+        s.push(5)
+    assert e.value.code == rn.RN_ERR_CAPACITY
+    with pytest.raises(rn.RnError) as e:
+        gm.session(4).logits()
+    assert e.value.code == rn.RN_ERR_STATE
+
+
+def test_batch_decode_equals_sessions_and_oracle(tiny, tiny_config):
+    gm, om = tiny
+    count, steps = 9, 10
+    lengths = rn.synth_tokens(rn.SEED, "batch.lengths", 60, count) + 1
+    first = rn.synth_tokens(rn.SEED, "batch.first", tiny_config["vocab"], count)
+    b = rn.Batch(gm, count, 80)
+    caches = []
+    for i in range(count):
+        k, v = rn.synthetic_cache(tiny_config, int(lengths[i]), f"batch.{i}")
+        caches.append((k, v))
+        b.set_cache(i, k, v)
+    ids = b.decode_greedy(first, steps)
+    for i in range(count):
+        s = gm.session(80)
+        s.set_cache(*caches[i])
+        assert ids[i].tolist() == s.decode_greedy(int(first[i]), steps).tolist(), i
+        if i < 3:
+            o = om.session(80)
+            o.set_cache(*caches[i])
+            assert ids[i].tolist() == o.greedy(int(first[i]), steps).tolist(), i
+
+
+def test_full_decode_workload_bit_identical():
+    """The batch-1 decode workload at full size: 20 layers, d 512, vocab 8192,
+    fp16 cache pre-filled to 256, 64 greedy tokens — ids equal the oracle's."""
+    cfg = dict(rn.NEEDLE_DECODER)
+    w = rn.synthetic_weights(cfg)
+    gm, om = rn.Model(cfg, w), oracle.OracleModel(cfg, w)
+    k, v = rn.synthetic_cache(cfg, 256, "decode")
+    first = int(rn.synth_tokens(rn.SEED, "decode.first", cfg["vocab"], 1)[0])
+    gs = gm.session(320)
+    gs.set_cache(k, v)
+    ids = gs.decode_greedy(first, 64)
+    oracle.set_threads(8)
+    try:
+        os_ = om.session(320)
+        os_.set_cache(k, v)
+        ref = os_.greedy(first, 64)
+    finally:
+        oracle.set_threads(1)
+    assert ids.tolist() == ref.tolist()
+    assert np.array_equal(_bits(gs.logits()), _bits(os_.logits()))
+
+
+def test_synthetic_model_equals_host_weights():
+    """rn_model_create_synthetic draws the same tensors as synthetic_weights."""
+    cfg = dict(rn.NEEDLE_DECODER)
+    cfg.update(layers=2, vocab=512)
+    a = rn.Model(cfg, seed=99)
+    b = rn.Model(cfg, rn.synthetic_weights(cfg, seed=99))
+    sa, sb = a.session(8), b.session(8)
+    sa.push(3)
+    sb.push(3)
+    assert np.array_equal(_bits(sa.logits()), _bits(sb.logits()))
