@@ -16,6 +16,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <new>
@@ -114,6 +115,7 @@ struct rn_session {
     float* logits = nullptr;
     DecodeState* state = nullptr;
     uint32_t* ids = nullptr;
+    unsigned long long* keys = nullptr;  // per-block greedy keys of the logits product
     hipGraphExec_t step_graph = nullptr;
     // prefill scratch, grown on demand
     void* scratch = nullptr;
@@ -572,7 +574,8 @@ int rn_session_create(const rn_model* m, int capacity, rn_session** out) {
     s->capacity = capacity;
     const size_t ce = cache_elems(c, capacity), d = c.d_model;
     const size_t total = 2 * align_up(ce * 2) + align_up(4 * d) * 4 + align_up(4 * 3 * d) + align_up(4 * (size_t)c.ffn) +
-                         align_up(4 * (size_t)c.vocab) + align_up(sizeof(DecodeState)) + align_up(4 * (size_t)capacity);
+                         align_up(4 * (size_t)c.vocab) + align_up(sizeof(DecodeState)) + align_up(4 * (size_t)capacity) +
+                         align_up(8 * (size_t)c.vocab);
     if (hipMalloc(&s->arena, total) != hipSuccess) {
         delete s;
         return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", total);
@@ -588,6 +591,7 @@ int rn_session_create(const rn_model* m, int capacity, rn_session** out) {
     s->logits = (float*)a.take(4 * (size_t)c.vocab);
     s->state = (DecodeState*)a.take(sizeof(DecodeState));
     s->ids = (uint32_t*)a.take(4 * (size_t)capacity);
+    s->keys = (unsigned long long*)a.take(8 * (size_t)c.vocab);
     if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess ||
         hipMemsetAsync(s->arena, 0, total, s->stream) != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess) {
         if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -678,9 +682,9 @@ int rn_session_get_cache(const rn_session* s, int length, uint16_t* keys, uint16
 // product (layer 0 gathers the embedding of state->token first), attention
 // with rotary and the fp16 append, the out product + residual, the
 // norm+gate/up product with silu(gate)*up, the down product + residual; then
-// the final norm into `hidden`. With `logits`, the tied-embedding product
-// follows, and with `greedy` its last block writes the argmax into the state.
-static int enqueue_step(rn_session* s, bool logits, bool greedy) {
+// the final norm into `hidden`. With `greedy`, the tied-embedding product and
+// the on-device argmax follow and feed the next step's embedding.
+static int enqueue_step(rn_session* s, bool greedy) {
     const rn_model* m = s->model;
     const rn_config& c = m->cfg;
     const int d = c.d_model;
@@ -748,17 +752,25 @@ static int enqueue_step(rn_session* s, bool logits, bool greedy) {
             RN_HIP(launch_gemv(p, c.ffn, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
         }
     }
-    RN_HIP(launch_finish_push(s->x, m->norm_final, d, c.norm_eps, s->hidden, s->state, st));
-    if (logits) {
-        GemvParams p{};
-        p.nseg = 1;
-        p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab, 0};
-        p.x = s->hidden;
-        p.state = s->state;
-        p.ids = s->ids;
-        const int rpb = gemv_rows_per_block(c.vocab, d, kStore);
-        RN_HIP(launch_gemv(p, d, kQuant, greedy ? kArgmax : kStore, kPlane, rpb, (c.vocab + rpb - 1) / rpb, st));
+    if (!greedy) {
+        RN_HIP(launch_finish_push(s->x, m->norm_final, d, c.norm_eps, s->hidden, s->state, st));
+        return RN_OK;
     }
+    // Greedy: the logits product takes the final norm as its prologue (block 0
+    // also writes the hidden state), each block emits its greedy key, and a
+    // one-block kernel reduces them into the next token and advances the position.
+    GemvParams p{};
+    p.nseg = 1;
+    p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab, 0};
+    p.x = s->x;
+    p.gain = m->norm_final;
+    p.eps = c.norm_eps;
+    p.hidden_out = s->hidden;
+    p.keys = s->keys;
+    const int rpb = gemv_rows_per_block(c.vocab, d, kStore);
+    const int blocks = (c.vocab + rpb - 1) / rpb;
+    RN_HIP(launch_gemv(p, d, kNorm, kArgmax, kPlane, rpb, blocks, st));
+    RN_HIP(launch_argmax_finalize(s->keys, blocks, s->logits, s->state, s->ids, st));
     return RN_OK;
 }
 
@@ -780,7 +792,7 @@ int rn_session_push(rn_session* s, uint32_t token) {
                s->model->cfg.vocab);
     if (s->length >= s->capacity) return fail(RN_ERR_CAPACITY, "session is full (%d positions)", s->capacity);
     RN_HIP(launch_set_state(s->state, token, s->length, 0, 0, s->stream));
-    int rc = enqueue_step(s, false, false);
+    int rc = enqueue_step(s, false);
     if (rc) return rc;
     s->length += 1;
     s->has_hidden = true;
@@ -817,10 +829,27 @@ int rn_session_decode_greedy(rn_session* s, uint32_t first, int steps, uint32_t*
     if (steps == 0) return RN_OK;
     if (s->length + steps > s->capacity)
         return fail(RN_ERR_CAPACITY, "%d + %d positions exceed the capacity %d", s->length, steps, s->capacity);
+    // RN_DECODE_GRAPH=0 launches the step's kernels directly instead of replaying
+    // the captured graph (same kernels, same results; for kernel-level tracing).
+    static const bool use_graph = [] {
+        const char* e = getenv("RN_DECODE_GRAPH");
+        return !(e && e[0] == '0');
+    }();
+    if (!use_graph) {
+        RN_HIP(launch_set_state(s->state, first, s->length, 0, (uint32_t)s->capacity, s->stream));
+        for (int i = 0; i < steps; ++i) {
+            const int rc = enqueue_step(s, true);
+            if (rc) return rc;
+        }
+        RN_HIP(hipMemcpyAsync(ids, s->ids, 4 * (size_t)steps, hipMemcpyDeviceToHost, s->stream));
+        s->length += steps;
+        s->has_hidden = true;
+        return check_state_error(s);
+    }
     if (!s->step_graph) {
         hipGraph_t graph = nullptr;
         RN_HIP(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
-        const int rc = enqueue_step(s, true, true);
+        const int rc = enqueue_step(s, true);
         hipError_t e = hipStreamEndCapture(s->stream, &graph);
         if (rc) {
             if (graph) (void)hipGraphDestroy(graph);

@@ -226,29 +226,40 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     } else if constexpr (EPI == kSilu) {
         const float up = __shfl(total, (lane + H) & 63, 64);
         if (lane < H && mine) sg.y[blk * H + lane] = silu(total) * up;
-    } else {  // kArgmax: logits plus the greedy token (generator.rs:257-265)
+    } else {  // kArgmax: logits plus this block's greedy key (generator.rs:257-265);
+              // argmax_finalize reduces the keys (device atomics would serialise)
         if (mine) sg.y[row_of(lane)] = total;
         uint64_t key = mine ? argmax_key(total, (uint32_t)row_of(lane)) : 0ull;
         key = wave_max_u64(key);
-        if (lane == 0) {
-            DecodeState* st = p.state;
-            atomicMax(&st->key, (unsigned long long)key);
-            __threadfence();
-            const unsigned ticket = atomicAdd(&st->counter, 1u);
-            if (ticket == gridDim.x - 1) {  // last block: every other block's key is in
-                __threadfence();
-                const unsigned long long best = atomicAdd(&st->key, 0ull);
-                const float first = __hip_atomic_load(&sg.y[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint32_t index = (first != first) ? 0u : argmax_index(best);
-                st->token = index;
-                const uint32_t step = st->step;
-                if (p.ids != nullptr && step < st->ids_capacity) p.ids[step] = index;
-                st->step = step + 1;
-                st->key = 0ull;
-                st->counter = 0u;
-            }
-        }
+        if (lane == 0) p.keys[blockIdx.x] = (unsigned long long)key;
     }
+}
+
+__global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long* keys, int nkeys,
+                                                              const float* logits, DecodeState* st, uint32_t* ids) {
+    __shared__ unsigned long long best_s[4];
+    uint64_t key = 0ull;
+    for (int i = threadIdx.x; i < nkeys; i += 256) key = keys[i] > key ? keys[i] : key;
+    key = wave_max_u64(key);
+    if ((threadIdx.x & 63) == 0) best_s[threadIdx.x >> 6] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t k = best_s[0];
+        for (int w = 1; w < 4; ++w) k = best_s[w] > k ? best_s[w] : k;
+        const float first = logits[0];
+        const uint32_t index = (first != first) ? 0u : argmax_index(k);  // a NaN at 0 is never displaced
+        st->token = index;
+        const uint32_t step = st->step;
+        if (ids != nullptr && step < st->ids_capacity) ids[step] = index;
+        st->step = step + 1;
+        st->pos = st->pos + 1;
+    }
+}
+
+hipError_t launch_argmax_finalize(const unsigned long long* keys, int nkeys, const float* logits,
+                                  DecodeState* state, uint32_t* ids, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(256), 0, stream, keys, nkeys, logits, state, ids);
+    return hipGetLastError();
 }
 
 template <int K, int ROWS, int PRO, int EPI, int FORM>
@@ -275,7 +286,8 @@ static hipError_t dispatch_pe(const GemvParams& p, int prologue, int epilogue, i
             if (prologue == kNorm && epilogue == kSilu) return launch_one<K, ROWS, kNorm, kSilu, kPanel>(p, blocks, s);
         }
     } else {
-        if (prologue == kQuant && epilogue == kArgmax) return launch_one<K, ROWS, kQuant, kArgmax, kPlane>(p, blocks, s);
+        if constexpr (K == 512)
+            if (prologue == kNorm && epilogue == kArgmax) return launch_one<K, ROWS, kNorm, kArgmax, kPlane>(p, blocks, s);
     }
     return hipErrorInvalidValue;
 }

@@ -13,14 +13,12 @@ namespace rn {
 constexpr int kGroup = 32;  // int8 codes per fp32 weight scale
 
 // Per-session decode state in device memory. The greedy step reads `token`,
-// the attention kernels read `pos`, the logits kernel's last block writes the
-// argmax back into `token` and `ids[step]`.
+// the attention kernels read `pos`, the argmax finalize kernel writes the next
+// token back into `token` and `ids[step]`.
 struct DecodeState {
     uint32_t token;
     int32_t pos;
     uint32_t step;
-    uint32_t counter;
-    unsigned long long key;
     int32_t error;
     uint32_t ids_capacity;
 };
@@ -55,8 +53,8 @@ struct GemvParams {
     int vocab;
     float* x_out;         // kEmbedNorm: block 0 writes the embedded row (the residual)
     float* hidden_out;    // kNorm: block 0 writes the normed input (nullable)
-    DecodeState* state;   // kEmbedNorm (token) / kArgmax (result)
-    uint32_t* ids;        // kArgmax: greedy ids written at state->step
+    DecodeState* state;   // kEmbedNorm: the token to embed
+    unsigned long long* keys;  // kArgmax: one greedy key per block (argmax_key)
 };
 
 // Launch one batch-1 product. `columns` in {512, 1024, 2048}; returns
@@ -131,7 +129,11 @@ hipError_t launch_norm_rows(const float* x, const float* gain, int count, int n,
 hipError_t launch_fast_exp(const float* x, float* y, int n, int silu, hipStream_t stream);
 hipError_t launch_finish_push(const float* x, const float* gain, int n, float eps, float* hidden,
                               DecodeState* state, hipStream_t stream);
-// Overwrites token/pos/step/ids_capacity and clears the argmax key and ticket.
+// Second stage of the greedy argmax: reduces the per-block keys of the logits
+// product, writes the token into the state and ids[step], advances step and pos.
+hipError_t launch_argmax_finalize(const unsigned long long* keys, int nkeys, const float* logits,
+                                  DecodeState* state, uint32_t* ids, hipStream_t stream);
+// Overwrites token/pos/step/ids_capacity.
 hipError_t launch_set_state(DecodeState* state, uint32_t token, int32_t pos, uint32_t step, uint32_t ids_capacity,
                             hipStream_t stream);
 

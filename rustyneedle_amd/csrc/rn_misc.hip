@@ -95,8 +95,6 @@ __global__ void set_state_kernel(DecodeState* st, uint32_t token, int32_t pos, u
     st->pos = pos;
     st->step = step;
     st->ids_capacity = ids_capacity;
-    st->key = 0ull;
-    st->counter = 0u;
 }
 
 hipError_t launch_set_state(DecodeState* state, uint32_t token, int32_t pos, uint32_t step, uint32_t ids_capacity,
