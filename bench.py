@@ -32,6 +32,15 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 GEMV_UNIT_BYTES = 1_189_888    # one 2048x512 int8 matvec: W 1,048,576 + sW 131,072 + x 2,048 + y 8,192
 DECODE_TOKENS = 64
 CONTEXT = 256
+KERNEL_NAMES = {
+    "qkv": "gemv_kernel<512,4,norm,store,panel> (fused QKV)",
+    "attention": "attend_kernel<decode>",
+    "out": "gemv_kernel<512,2,quant,residual,panel> (out)",
+    "gate_up": "gemv_kernel<512,8,norm,silu,panel> (gate/up)",
+    "down": "gemv_kernel<2048,2,quant,residual,panel> (down)",
+    "logits": "gemv_kernel<512,8,norm,argmax,plane> (logits)",
+    "final": "argmax_finalize_kernel",
+}
 
 
 def log(msg: str) -> None:
@@ -75,6 +84,41 @@ def bench_decode(rn, model, cfg, steps: int, warmup: int):
     ms = start.elapsed_ms(stop)
     wall = time.perf_counter() - t0
     return ms, wall, ref, (keys, values, first)
+
+
+def decode_kernel_bytes(cfg, context: int, steps: int) -> dict:
+    """Algorithmic HBM bytes per launch of each decode-step kernel kind: weights,
+    scales, cache rows and vectors each read or written once."""
+    d, f, v, h, hd = cfg["d_model"], cfg["ffn"], cfg["vocab"], cfg["heads"], cfg["head_dim"]
+    q = lambda rows, cols: rows * cols + rows * (cols // 32) * 4   # codes + fp32 scales
+    mean_cached = context + (steps - 1) / 2.0                        # cache rows read per attention launch
+    blocks = (v + 7) // 8
+    return {
+        "qkv": q(3 * d, d) + 4 * d + 4 * d + 4 * 3 * d,               # W, x, gains, q/k/v out
+        "attention": h * 2 * mean_cached * hd * 2 + 4 * 3 * d + h * 2 * hd * 2 + 4 * d,
+        "out": q(d, d) + 4 * d + 2 * 4 * d,                           # W, attention in, residual read+write
+        "gate_up": q(2 * f, d) + 4 * d + 4 * d + 4 * f,               # W, x, gains, silu(gate)*up out
+        "down": q(d, f) + 4 * f + 2 * 4 * d,
+        "logits": q(v, d) + 4 * d + 4 * d + 4 * v + 4 * d + 8 * blocks,
+        "final": 8 * blocks + 4 * 4,
+    }
+
+
+def profile_decode(rn, model, cfg, cache, steps: int = DECODE_TOKENS):
+    """Per-kernel average durations of the decode step (events after every kernel)."""
+    keys, values, first = cache
+    sess = model.session(CONTEXT + DECODE_TOKENS)
+    sess.set_cache(keys, values)
+    sess.profile_step(first, steps)  # warm-up
+    sess.truncate(CONTEXT)
+    prof = sess.profile_step(first, steps)
+    # the roofline bytes assume the mean cache length of this run's positions
+    nbytes = decode_kernel_bytes(cfg, CONTEXT, steps)
+    for k, p in prof.items():
+        p["bytes_per_launch"] = nbytes[k]
+        p["gb_s"] = nbytes[k] / (p["us"] * 1e-6) / 1e9 if p["us"] > 0 else None
+        p["us_per_token"] = p["us"] * p["per_step"]
+    return prof
 
 
 def bench_batch(rn, model, cfg, count: int = 64, steps: int = 32, reps: int = 2):
@@ -181,6 +225,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="decode only")
+    ap.add_argument("--profile-steps", type=int, default=DECODE_TOKENS,
+                    help="greedy steps timed kernel by kernel for the roofline")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first copy this many MiB device-to-device (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); the decode path is single-GPU by design",
@@ -189,6 +237,12 @@ def main() -> int:
 
     import rustyneedle_amd as rn
 
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib << 20
+        src, dst = rn.DeviceBuffer(n), rn.DeviceBuffer(n)
+        rn.check(rn.lib.rn_memcpy_dtod(dst.ptr, src.ptr, n))
+        log(f"bench: copied {args.copy_probe_mib} MiB device to device")
+        del src, dst
     cfg = dict(rn.NEEDLE_DECODER)
     log("bench: building the synthetic 20-layer model on the device")
     model = rn.Model(cfg, seed=rn.SEED)
@@ -196,7 +250,9 @@ def main() -> int:
     ms, wall, ids, cache = bench_decode(rn, model, cfg, args.steps, args.warmup)
     ms_per_step = ms / args.steps
     tok_s = DECODE_TOKENS * args.steps / (ms / 1e3)
-    extra = {}
+    log("bench: per-kernel timing of the decode step")
+    kernels = profile_decode(rn, model, cfg, cache, args.profile_steps)
+    extra = {"decode_kernels": kernels}
     if not args.no_extra:
         for name, fn in (("gemv", lambda: bench_gemv(rn)),
                          ("prefill_256", lambda: bench_prefill(rn, model, cfg)),
@@ -215,13 +271,13 @@ def main() -> int:
                 base["mismatch"] = "CPU greedy ids differ from the GPU's"
         except Exception as e:
             base = {"error": repr(e)}
-    g = extra.get("gemv", {})
-    roofline = None
-    if "rotating_gb_s" in g:
-        roofline = dict(bound="hbm", kernel="gemv_kernel<512,32,quant,store,panel>",
-                        achieved=g["rotating_gb_s"], peak=HBM_PEAK_GBS, unit="GB/s",
-                        frac=g["rotating_gb_s"] / HBM_PEAK_GBS, traffic=None,
-                        units_per_launch=g["rotations"], bytes_per_unit=GEMV_UNIT_BYTES)
+    # the dominant kernel of the timed decode step: most microseconds per token
+    dom_kind = max(kernels, key=lambda k: kernels[k]["us_per_token"])
+    dom = kernels[dom_kind]
+    roofline = dict(bound="hbm", kernel=KERNEL_NAMES[dom_kind], achieved=dom["gb_s"], peak=HBM_PEAK_GBS,
+                    unit="GB/s", frac=dom["gb_s"] / HBM_PEAK_GBS, traffic=None,
+                    bytes_per_launch=dom["bytes_per_launch"], avg_launch_us=dom["us"],
+                    share_of_step=dom["us_per_token"] / (ms_per_step * 1e3 / DECODE_TOKENS))
     line = {
         "metric": "decode tokens/sec (batch 1, 64) + int8 GEMV GB/s and % HBM roofline",
         "value": tok_s,

@@ -198,6 +198,24 @@ int rn_session_decode_greedy(rn_session* session, uint32_t first, int steps, uin
 /* The stream the session's work runs on (hipStream_t as void*). */
 int rn_session_stream(const rn_session* session, void** stream);
 
+/* Per-kernel timing of greedy decode steps (no reference counterpart: the
+ * reference has no tracing; this is the build's tracing hook). Runs `steps`
+ * greedy steps like rn_session_decode_greedy, launching the step's kernels
+ * directly with a HIP event after each, and returns for every kernel kind the
+ * average microseconds per launch (kind_us) and launches per step (kind_count),
+ * both arrays of RN_PROFILE_KINDS entries in this order: */
+enum {
+    RN_PROFILE_QKV = 0,       /* norm + fused QKV product (layer 0: + embedding) */
+    RN_PROFILE_ATTENTION = 1, /* rotary + fp16 append + attention */
+    RN_PROFILE_OUT = 2,       /* quantise + out product + residual */
+    RN_PROFILE_GATE_UP = 3,   /* norm + gate/up product + silu(gate)*up */
+    RN_PROFILE_DOWN = 4,      /* quantise + down product + residual */
+    RN_PROFILE_LOGITS = 5,    /* final norm + tied logits product + per-block argmax */
+    RN_PROFILE_FINAL = 6,     /* argmax reduction, next token, position advance */
+    RN_PROFILE_KINDS = 7
+};
+int rn_session_profile_step(rn_session* session, uint32_t first, int steps, float* kind_us, int* kind_count);
+
 /* ---- batched decode: `count` independent sequences advanced together --------- */
 /* Like `count` Sessions, but each step runs the products as M=count i8-MFMA
  * GEMMs and the attention over `count` ragged caches in one launch. */

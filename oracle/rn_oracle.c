@@ -279,18 +279,19 @@ void ro_multiply(int form, const int8_t* W, const float* sW, int rows, int cols,
 
 /* ---- attention (trees T2 and T3) --------------------------------------------- */
 
-#define RO_LANES 16
+#define RO_SCORE_PARTS 16  /* T2: sub-sums of head_dim/16 consecutive dims */
+#define RO_CLASSES 32      /* T3: interleaved position classes p mod 32 */
 
 static float score_tree(const float* q, const uint16_t* k, int head_dim) {
-    int per = head_dim / RO_LANES;
-    float part[RO_LANES];
-    for (int j = 0; j < RO_LANES; ++j) {
+    int per = head_dim / RO_SCORE_PARTS;
+    float part[RO_SCORE_PARTS];
+    for (int j = 0; j < RO_SCORE_PARTS; ++j) {
         float s = 0.0f;
         for (int i = 0; i < per; ++i) s = s + q[j * per + i] * half_to_float(k[j * per + i]);
         part[j] = s;
     }
-    for (int width = 1; width < RO_LANES; width *= 2)
-        for (int j = 0; j < RO_LANES; j += 2 * width) part[j] = part[j] + part[j + width];
+    for (int width = 1; width < RO_SCORE_PARTS; width *= 2)
+        for (int j = 0; j < RO_SCORE_PARTS; j += 2 * width) part[j] = part[j] + part[j + width];
     return part[0];
 }
 
@@ -307,25 +308,25 @@ void ro_attend_head(const float* q, const uint16_t* K, const uint16_t* V, int he
         peak = fmaxf(peak, c[p]);
     }
     for (int p = 0; p < length; ++p) c[p] = ro_fast_exp(c[p] - peak);
-    float totals[RO_LANES];
-    for (int j = 0; j < RO_LANES; ++j) {
+    float totals[RO_CLASSES];
+    for (int j = 0; j < RO_CLASSES; ++j) {
         float t = 0.0f;
-        for (int p = j; p < length; p += RO_LANES) t = t + c[p];
+        for (int p = j; p < length; p += RO_CLASSES) t = t + c[p];
         totals[j] = t;
     }
     float total = 0.0f;
-    for (int j = 0; j < RO_LANES; ++j) total = total + totals[j];
+    for (int j = 0; j < RO_CLASSES; ++j) total = total + totals[j];
     float inverse = 1.0f / total;
-    /* part[j][d] accumulates positions p = j, j+16, ... in increasing p. */
-    float* part = (float*)calloc((size_t)RO_LANES * head_dim, sizeof(float));
+    /* part[j][d] accumulates positions p = j, j+32, ... in increasing p. */
+    float* part = (float*)calloc((size_t)RO_CLASSES * head_dim, sizeof(float));
     for (int p = 0; p < length; ++p) {
-        float* acc = part + (size_t)(p % RO_LANES) * head_dim;
+        float* acc = part + (size_t)(p % RO_CLASSES) * head_dim;
         const uint16_t* v = V + (size_t)p * head_dim;
         for (int d = 0; d < head_dim; ++d) acc[d] = acc[d] + c[p] * half_to_float(v[d]);
     }
     for (int d = 0; d < head_dim; ++d) {
         float o = 0.0f;
-        for (int j = 0; j < RO_LANES; ++j) o = o + part[(size_t)j * head_dim + d];
+        for (int j = 0; j < RO_CLASSES; ++j) o = o + part[(size_t)j * head_dim + d];
         out[d] = o * inverse;
     }
     free(part);

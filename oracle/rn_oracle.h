@@ -21,9 +21,9 @@
  *   T2 attention score q.k over head_dim = 16*c dims: sixteen sub-sums of c
  *      consecutive dims (each 0 + q0k0 + q1k1 + ... in order), then a balanced
  *      pairwise tree over the sixteen sub-sums in index order.
- *   T3 softmax total and P.V over L positions: sixteen interleaved partial sums
- *      (position p goes to partial p mod 16, added in increasing p, starting
- *      from 0), then the sixteen partials added 0..15 starting from 0.
+ *   T3 softmax total and P.V over L positions: thirty-two interleaved partial
+ *      sums (position p goes to partial p mod 32, added in increasing p,
+ *      starting from 0), then the partials added 0..31 starting from 0.
  *   T4 product epilogue per (token, row): sequential over groups g = 0..G-1.
  *      Panel form (layer matrices, panel.rs:184-188):
  *          total = fmaf((float)acc_g, sW[g] * sx, total)

@@ -27,6 +27,9 @@ RN_ERR_MEMORY = -5
 FORM_PANEL = 0
 FORM_PLANE = 1
 
+# Kernel kinds of rn_session_profile_step, in RN_PROFILE_* order.
+PROFILE_KINDS = ("qkv", "attention", "out", "gate_up", "down", "logits", "final")
+
 # The decoder of the decode / prefill / batch workloads: 20 layers, d_model 512,
 # 8 heads of 64, rotary base 10000, RMSNorm eps 1e-6, gated FFN 512->2048->512,
 # int8 codes with one fp32 scale per 32 columns, tied int8 vocab 8192.
@@ -113,6 +116,7 @@ SIGNATURES = {
     "rn_session_logits": (_i, [_p, _p]),
     "rn_session_decode_greedy": (_i, [_p, _u32, _i, _p]),
     "rn_session_stream": (_i, [_p, C.POINTER(_p)]),
+    "rn_session_profile_step": (_i, [_p, _u32, _i, _p, _p]),
     "rn_batch_create": (_i, [_p, _i, _i, C.POINTER(_p)]),
     "rn_batch_free": (_i, [_p]),
     "rn_batch_set_cache": (_i, [_p, _i, _i, _p, _p]),
@@ -536,6 +540,14 @@ class Session:
         p = _p()
         check(lib.rn_session_stream(self.handle, C.byref(p)))
         return p.value
+
+    def profile_step(self, first: int, steps: int) -> dict:
+        """Average microseconds per launch and launches per step of each kernel
+        kind of the greedy decode step (HIP events after every kernel)."""
+        us = np.zeros(len(PROFILE_KINDS), dtype=np.float32)
+        count = np.zeros(len(PROFILE_KINDS), dtype=np.int32)
+        check(lib.rn_session_profile_step(self.handle, int(first), steps, _ptr(us), _ptr(count)))
+        return {k: dict(us=float(us[i]), per_step=int(count[i])) for i, k in enumerate(PROFILE_KINDS)}
 
     def __del__(self):
         try:

@@ -684,11 +684,33 @@ int rn_session_get_cache(const rn_session* s, int length, uint16_t* keys, uint16
 // norm+gate/up product with silu(gate)*up, the down product + residual; then
 // the final norm into `hidden`. With `greedy`, the tied-embedding product and
 // the on-device argmax follow and feed the next step's embedding.
-static int enqueue_step(rn_session* s, bool greedy) {
+// Optional per-kernel timing of a decode step: every launch is armed with a
+// start/stop event pair that hipExtLaunchKernelGGL records around the kernel
+// itself; `kinds` gives each pair's kernel kind (RN_PROFILE_* order).
+struct StepProbe {
+    std::vector<hipEvent_t> events;  // 2 per launch
+    std::vector<int> kinds;
+    void arm() {
+        const size_t i = kinds.size();
+        if (2 * i + 1 < events.size()) {
+            launch_events().start = events[2 * i];
+            launch_events().stop = events[2 * i + 1];
+        }
+    }
+    void done(int kind) { kinds.push_back(kind); }
+};
+
+static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) {
     const rn_model* m = s->model;
     const rn_config& c = m->cfg;
     const int d = c.d_model;
     hipStream_t st = s->stream;
+#define RN_PROFILED(kind, call) \
+    do {                          \
+        if (probe) probe->arm();  \
+        RN_HIP(call);             \
+        if (probe) probe->done(kind); \
+    } while (0)
     for (int l = 0; l < c.layers; ++l) {
         const LayerDev& L = m->layers[l];
         {
@@ -705,7 +727,7 @@ static int enqueue_step(rn_session* s, bool greedy) {
             p.x_out = s->x;
             p.state = s->state;
             const int rpb = gemv_rows_per_block(3 * d, d, kStore);
-            RN_HIP(launch_gemv(p, d, l == 0 ? kEmbedNorm : kNorm, kStore, kPanel, rpb, (3 * d + rpb - 1) / rpb, st));
+            RN_PROFILED(RN_PROFILE_QKV, launch_gemv(p, d, l == 0 ? kEmbedNorm : kNorm, kStore, kPanel, rpb, (3 * d + rpb - 1) / rpb, st));
         }
         {
             AttendParams a{};
@@ -722,7 +744,7 @@ static int enqueue_step(rn_session* s, bool greedy) {
             a.rope_sin = m->rope_sin;
             a.out = s->attn;
             a.error = &s->state->error;
-            RN_HIP(launch_attend(a, kAttendDecode, c.heads, 1, s->capacity, st));
+            RN_PROFILED(RN_PROFILE_ATTENTION, launch_attend(a, kAttendDecode, c.heads, 1, s->capacity, st));
         }
         {
             GemvParams p{};
@@ -730,7 +752,7 @@ static int enqueue_step(rn_session* s, bool greedy) {
             p.seg[0] = Segment{L.out.W, L.out.sW, s->x, nullptr, d, 0};
             p.x = s->attn;
             const int rpb = gemv_rows_per_block(d, d, kResidual);
-            RN_HIP(launch_gemv(p, d, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
+            RN_PROFILED(RN_PROFILE_OUT, launch_gemv(p, d, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
         }
         {
             GemvParams p{};
@@ -741,7 +763,7 @@ static int enqueue_step(rn_session* s, bool greedy) {
             p.gain = L.norm_ffn;
             p.eps = c.norm_eps;
             const int rpb = gemv_rows_per_block(2 * c.ffn, d, kSilu);
-            RN_HIP(launch_gemv(p, d, kNorm, kSilu, kPanel, rpb, (c.ffn + rpb / 2 - 1) / (rpb / 2), st));
+            RN_PROFILED(RN_PROFILE_GATE_UP, launch_gemv(p, d, kNorm, kSilu, kPanel, rpb, (c.ffn + rpb / 2 - 1) / (rpb / 2), st));
         }
         {
             GemvParams p{};
@@ -749,11 +771,11 @@ static int enqueue_step(rn_session* s, bool greedy) {
             p.seg[0] = Segment{L.down.W, L.down.sW, s->x, nullptr, d, 0};
             p.x = s->ffh;
             const int rpb = gemv_rows_per_block(d, c.ffn, kResidual);
-            RN_HIP(launch_gemv(p, c.ffn, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
+            RN_PROFILED(RN_PROFILE_DOWN, launch_gemv(p, c.ffn, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
         }
     }
     if (!greedy) {
-        RN_HIP(launch_finish_push(s->x, m->norm_final, d, c.norm_eps, s->hidden, s->state, st));
+        RN_PROFILED(RN_PROFILE_FINAL, launch_finish_push(s->x, m->norm_final, d, c.norm_eps, s->hidden, s->state, st));
         return RN_OK;
     }
     // Greedy: the logits product takes the final norm as its prologue (block 0
@@ -769,9 +791,10 @@ static int enqueue_step(rn_session* s, bool greedy) {
     p.keys = s->keys;
     const int rpb = gemv_rows_per_block(c.vocab, d, kStore);
     const int blocks = (c.vocab + rpb - 1) / rpb;
-    RN_HIP(launch_gemv(p, d, kNorm, kArgmax, kPlane, rpb, blocks, st));
-    RN_HIP(launch_argmax_finalize(s->keys, blocks, s->logits, s->state, s->ids, st));
+    RN_PROFILED(RN_PROFILE_LOGITS, launch_gemv(p, d, kNorm, kArgmax, kPlane, rpb, blocks, st));
+    RN_PROFILED(RN_PROFILE_FINAL, launch_argmax_finalize(s->keys, blocks, s->logits, s->state, s->ids, st));
     return RN_OK;
+#undef RN_PROFILED
 }
 
 static int check_state_error(rn_session* s) {
@@ -863,6 +886,41 @@ int rn_session_decode_greedy(rn_session* s, uint32_t first, int steps, uint32_t*
     RN_HIP(launch_set_state(s->state, first, s->length, 0, (uint32_t)s->capacity, s->stream));
     for (int i = 0; i < steps; ++i) RN_HIP(hipGraphLaunch(s->step_graph, s->stream));
     RN_HIP(hipMemcpyAsync(ids, s->ids, 4 * (size_t)steps, hipMemcpyDeviceToHost, s->stream));
+    s->length += steps;
+    s->has_hidden = true;
+    return check_state_error(s);
+}
+
+int rn_session_profile_step(rn_session* s, uint32_t first, int steps, float* kind_us, int* kind_count) {
+    RN_REQUIRE(s && kind_us && kind_count, "null argument");
+    RN_REQUIRE(steps >= 1, "steps must be positive");
+    RN_REQUIRE(first < (uint32_t)s->model->cfg.vocab, "token %u outside the vocabulary", first);
+    if (s->length + steps > s->capacity)
+        return fail(RN_ERR_CAPACITY, "%d + %d positions exceed the capacity %d", s->length, steps, s->capacity);
+    const size_t launches = ((size_t)s->model->cfg.layers * 5 + 2) * steps;
+    StepProbe probe;
+    probe.events.resize(2 * launches);
+    for (auto& e : probe.events) RN_HIP(hipEventCreate(&e));
+    int rc = RN_OK;
+    hipError_t e = launch_set_state(s->state, first, s->length, 0, (uint32_t)s->capacity, s->stream);
+    for (int i = 0; i < steps && rc == RN_OK && e == hipSuccess; ++i) rc = enqueue_step(s, true, &probe);
+    launch_events() = LaunchEvents{};
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    double sum[RN_PROFILE_KINDS] = {0};
+    int count[RN_PROFILE_KINDS] = {0};
+    for (size_t i = 0; i < probe.kinds.size() && e == hipSuccess; ++i) {
+        float ms = 0.0f;
+        e = hipEventElapsedTime(&ms, probe.events[2 * i], probe.events[2 * i + 1]);
+        sum[probe.kinds[i]] += ms * 1000.0;
+        count[probe.kinds[i]] += 1;
+    }
+    for (auto& ev : probe.events) (void)hipEventDestroy(ev);
+    if (rc) return rc;
+    RN_HIP(e);
+    for (int k = 0; k < RN_PROFILE_KINDS; ++k) {
+        kind_us[k] = count[k] ? (float)(sum[k] / count[k]) : 0.0f;
+        kind_count[k] = count[k] / steps;
+    }
     s->length += steps;
     s->has_hidden = true;
     return check_state_error(s);

@@ -6,21 +6,20 @@
 // weighted values, one multiply by 1/total.
 //
 // One 256-thread block per (head, query). Latency is the enemy at these sizes
-// (a head's cache is 2 x L x 128 bytes), so every cache load that does not
-// depend on the current token is issued before anything else: the first chunk
-// of key rows (up to 384 positions) and of value rows goes out at once, and
-// only then does the block read its q/k/v row, apply the rotary and append the
-// new key/value. The new position is served from LDS.
+// (a head's cache is 2 x L x 128 bytes), so the first chunk of key rows and of
+// value rows (384 positions each) is loaded before the block even reads the
+// current position: only then does it read its q/k/v row, apply the rotary and
+// append the new key/value, which is served from LDS.
 //
-// Scores: 8 lanes per key row, 16 bytes (8 dims) each; a wave covers 8 rows per
-// load, the block 32 rows per pass. Values: 16 lanes per row, 8 bytes (4 dims)
-// each; thread (j, dg) walks positions j, j+16, j+32, ... The float reductions
-// follow the fixed trees of the CPU restatement:
+// Scores: 4 lanes per key row, 32 bytes (16 dims) each; the block covers 64
+// rows per pass. Values: 8 lanes per row, 16 bytes (8 dims) each; thread
+// (j, dg) walks positions j, j+32, j+64, ... The float reductions follow the
+// fixed trees of the CPU restatement:
 //   score (T2): per 4 dims 0 + q0k0 + ... + q3k3; the 16 sub-sums combined by a
-//               balanced pairwise tree (the first level inside a lane, then
-//               xor 1, 2, 4 across the 8 lanes);
-//   total and P.V (T3): sixteen running sums over positions j, j+16, ... in
-//               increasing order, then added j = 0..15.
+//               balanced pairwise tree (two levels inside a lane, then xor 1,
+//               xor 2 across the 4 lanes);
+//   total and P.V (T3): thirty-two running sums over positions j, j+32, ... in
+//               increasing order, then added j = 0..31.
 // Scores live in LDS (dynamic, one float per position).
 #include "rn_device.hpp"
 #include "rn_internal.hpp"
@@ -28,8 +27,9 @@
 namespace rn {
 
 constexpr int kHeadDim = 64;
-constexpr int kKChunk = 12;   // key passes of 32 rows issued together (384 positions)
-constexpr int kVChunk = 24;   // value positions per thread issued together (384 positions)
+constexpr int kKChunk = 6;    // key passes of 64 rows issued together (384 positions)
+constexpr int kVChunk = 12;   // value positions per thread issued together (384 positions)
+constexpr int kClasses = 32;  // T3 position classes (p mod 32)
 
 __device__ __forceinline__ void unpack8(const uint4& raw, float* out) {
     const __half2* h = reinterpret_cast<const __half2*>(&raw);
@@ -40,25 +40,24 @@ __device__ __forceinline__ void unpack8(const uint4& raw, float* out) {
     }
 }
 
-__device__ __forceinline__ void unpack4(const uint2& raw, float* out) {
-    const __half2* h = reinterpret_cast<const __half2*>(&raw);
-    out[0] = __low2float(h[0]);
-    out[1] = __high2float(h[0]);
-    out[2] = __low2float(h[1]);
-    out[3] = __high2float(h[1]);
-}
-
-// T2 for one key row held as 8 dims per lane (lane li owns dims 8li..8li+7).
-__device__ __forceinline__ float score_row(const float* q8, const float* k8) {
-    float a = 0.0f, b = 0.0f;
+// T2 for one key row held as 16 dims per lane (lane li owns dims 16li..16li+15,
+// i.e. the four 4-dim sub-sums 4li..4li+3): two tree levels inside the lane,
+// the last two across lanes (xor 1, xor 2).
+__device__ __forceinline__ float score_row(const float* q16, const uint4& ka, const uint4& kb) {
+    float k[16];
+    unpack8(ka, k);
+    unpack8(kb, k + 8);
+    float part[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a = a + q8[i] * k8[i];
+    for (int j = 0; j < 4; ++j) {
+        float s = 0.0f;
 #pragma unroll
-    for (int i = 4; i < 8; ++i) b = b + q8[i] * k8[i];
-    float s = a + b;
-    s = s + __shfl_xor(s, 1, 8);
-    s = s + __shfl_xor(s, 2, 8);
-    s = s + __shfl_xor(s, 4, 8);
+        for (int i = 0; i < 4; ++i) s = s + q16[4 * j + i] * k[4 * j + i];
+        part[j] = s;
+    }
+    float s = (part[0] + part[1]) + (part[2] + part[3]);
+    s = s + __shfl_xor(s, 1, 4);
+    s = s + __shfl_xor(s, 2, 4);
     return s;
 }
 
@@ -67,21 +66,61 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
     extern __shared__ float scores[];
     __shared__ float q_s[kHeadDim];
     __shared__ __align__(16) __half new_s[2][kHeadDim];  // decode: the appended key and value
-    __shared__ float part_s[16][kHeadDim];
-    __shared__ float total_s[16];
+    __shared__ float part_s[kClasses][kHeadDim];
+    __shared__ float total_s[kClasses];
     __shared__ float peak_s[4];
 
     const int tid = threadIdx.x;
-    const int r = tid >> 3, li = tid & 7;    // score layout: row slot, 8-dim lane
-    const int j = tid >> 4, dg = tid & 15;   // value layout: position class, 4-dim lane
+    const int r = tid >> 2, li = tid & 3;    // score layout: row slot (64 per pass), 16-dim lane
+    const int j = tid >> 3, dg = tid & 7;    // value layout: position class (32), 8-dim lane
 
     const __half* K;
     const __half* V;
     float* out;
     int nglobal;     // positions read from the cache in global memory
     bool has_new;    // decode: one more position (index nglobal) served from LDS
+    int rows;        // rows that exist in this (layer, head) cache: loads clamp to them
     int pos = 0;
 
+    if constexpr (MODE == kAttendDecode) {
+        const int h = blockIdx.x, b = blockIdx.y;
+        const size_t base = (size_t)b * p.seq_stride + ((size_t)p.layer * p.heads + h) * p.capacity * kHeadDim;
+        K = p.kc + base;
+        V = p.vc + base;
+        out = p.out + (size_t)b * p.d_model + h * kHeadDim;
+        rows = p.capacity;
+    } else if constexpr (MODE == kAttendPrefill) {
+        const int h = blockIdx.x, t = blockIdx.y;
+        const size_t base = ((size_t)p.layer * p.heads + h) * p.capacity * kHeadDim;
+        K = p.kc + base;
+        V = p.vc + base;
+        out = p.out + (size_t)t * p.d_model + h * kHeadDim;
+        rows = p.capacity;
+    } else {
+        const int i = blockIdx.x;
+        K = p.kc + (size_t)i * p.stride * kHeadDim;
+        V = p.vc + (size_t)i * p.stride * kHeadDim;
+        out = p.out + (size_t)i * kHeadDim;
+        rows = p.stride;
+    }
+
+    // 1. cache loads, issued before anything that depends on the current token
+    // or even on the length: rows past the valid ones are clamped into the
+    // cache and their results discarded by selects (never by branches, which
+    // would split the load stream and force a full wait).
+    uint4 kr[kKChunk][2];
+#pragma unroll
+    for (int c = 0; c < kKChunk; ++c) {
+        const __half* row = K + (size_t)min(r + 64 * c, rows - 1) * kHeadDim + 16 * li;
+        kr[c][0] = *reinterpret_cast<const uint4*>(row);
+        kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
+    }
+    uint4 vr[kVChunk];
+#pragma unroll
+    for (int c = 0; c < kVChunk; ++c)
+        vr[c] = *reinterpret_cast<const uint4*>(V + (size_t)min(j + kClasses * c, rows - 1) * kHeadDim + 8 * dg);
+
+    // 2. the length, the query and (decoding) the rotary + fp16 append of the new row
     if constexpr (MODE == kAttendDecode) {
         const int h = blockIdx.x, b = blockIdx.y;
         pos = p.pos[(size_t)b * p.pos_stride];
@@ -89,56 +128,8 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
             if (tid == 0) atomicOr(p.error, 2);
             return;
         }
-        const size_t base = (size_t)b * p.seq_stride + ((size_t)p.layer * p.heads + h) * p.capacity * kHeadDim;
-        K = p.kc + base;
-        V = p.vc + base;
-        out = p.out + (size_t)b * p.d_model + h * kHeadDim;
         nglobal = pos;
         has_new = true;
-    } else if constexpr (MODE == kAttendPrefill) {
-        const int h = blockIdx.x, t = blockIdx.y;
-        const size_t base = ((size_t)p.layer * p.heads + h) * p.capacity * kHeadDim;
-        K = p.kc + base;
-        V = p.vc + base;
-        out = p.out + (size_t)t * p.d_model + h * kHeadDim;
-        nglobal = p.first + t + 1;
-        has_new = false;
-    } else {
-        const int i = blockIdx.x;
-        const int length = p.lengths[i];
-        if (length < 1 || length > p.stride) {
-            if (tid == 0) atomicOr(p.error, 4);
-            return;
-        }
-        K = p.kc + (size_t)i * p.stride * kHeadDim;
-        V = p.vc + (size_t)i * p.stride * kHeadDim;
-        out = p.out + (size_t)i * kHeadDim;
-        nglobal = length;
-        has_new = false;
-    }
-    const int length = nglobal + (has_new ? 1 : 0);
-    // Loads past the last cached row re-read it (always inside the cache); their
-    // results are discarded by selects, never by branches, so no branch splits
-    // the load stream and forces a full wait.
-    const int last = nglobal > 0 ? nglobal - 1 : 0;
-
-    // 1. cache loads that do not depend on the current token, issued first
-    uint4 kr[kKChunk];
-#pragma unroll
-    for (int c = 0; c < kKChunk; ++c) {
-        const int pp = r + 32 * c;
-        kr[c] = *reinterpret_cast<const uint4*>(K + (size_t)min(pp, last) * kHeadDim + 8 * li);
-    }
-    uint2 vr[kVChunk];
-#pragma unroll
-    for (int c = 0; c < kVChunk; ++c) {
-        const int pp = j + 16 * c;
-        vr[c] = *reinterpret_cast<const uint2*>(V + (size_t)min(pp, last) * kHeadDim + 4 * dg);
-    }
-
-    // 2. the query (and, when decoding, the rotary + fp16 append of the new row)
-    if constexpr (MODE == kAttendDecode) {
-        const int h = blockIdx.x, b = blockIdx.y;
         const float* row = p.qkv + (size_t)b * 3 * p.d_model;
         if (tid < kHeadDim / 2) {  // ops.rs:131-141 rotate-half at `pos`
             const int i = tid, half = kHeadDim / 2;
@@ -163,38 +154,46 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
             Vw[i + half] = v1;
         }
     } else if constexpr (MODE == kAttendPrefill) {
+        nglobal = p.first + blockIdx.y + 1;
+        has_new = false;
         if (tid < kHeadDim) q_s[tid] = p.q[(size_t)blockIdx.y * p.d_model + blockIdx.x * kHeadDim + tid];
     } else {
+        nglobal = p.lengths[blockIdx.x];
+        has_new = false;
+        if (nglobal < 1 || nglobal > p.stride) {
+            if (tid == 0) atomicOr(p.error, 4);
+            return;
+        }
         if (tid < kHeadDim) q_s[tid] = p.q[(size_t)blockIdx.x * kHeadDim + tid];
     }
+    const int length = nglobal + (has_new ? 1 : 0);
     __syncthreads();
 
-    // 3. scores (T2)
+    // 3. scores (T2): one key row per 4-lane group, 64 rows per pass
     const float inverse_root = 1.0f / sqrtf((float)kHeadDim);
-    float q8[8];
+    float q16[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) q8[i] = q_s[8 * li + i];
-    for (int base = 0; base < nglobal; base += 32 * kKChunk) {
+    for (int i = 0; i < 16; ++i) q16[i] = q_s[16 * li + i];
+    for (int base = 0; base < nglobal; base += 64 * kKChunk) {
         if (base > 0) {
 #pragma unroll
             for (int c = 0; c < kKChunk; ++c) {
-                const int pp = base + r + 32 * c;
-                kr[c] = *reinterpret_cast<const uint4*>(K + (size_t)min(pp, last) * kHeadDim + 8 * li);
+                const __half* row = K + (size_t)min(base + r + 64 * c, rows - 1) * kHeadDim + 16 * li;
+                kr[c][0] = *reinterpret_cast<const uint4*>(row);
+                kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
             }
         }
 #pragma unroll
         for (int c = 0; c < kKChunk; ++c) {
-            const int pp = base + r + 32 * c;
-            float k8[8];
-            unpack8(kr[c], k8);
-            const float s = score_row(q8, k8);
+            const int pp = base + r + 64 * c;
+            const float s = score_row(q16, kr[c][0], kr[c][1]);
             if (li == 0 && pp < nglobal) scores[pp] = s * inverse_root;
         }
     }
-    if (has_new && tid < 8) {
-        float k8[8];
-        unpack8(*reinterpret_cast<const uint4*>(&new_s[0][8 * li]), k8);
-        const float s = score_row(q8, k8);
+    if (has_new && tid < 4) {
+        const uint4 ka = *reinterpret_cast<const uint4*>(&new_s[0][16 * li]);
+        const uint4 kb = *reinterpret_cast<const uint4*>(&new_s[0][16 * li + 8]);
+        const float s = score_row(q16, ka, kb);
         if (li == 0) scores[nglobal] = s * inverse_root;
     }
     __syncthreads();
@@ -209,49 +208,49 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
     for (int pp = tid; pp < length; pp += 256) scores[pp] = fast_exp(scores[pp] - peak);
     __syncthreads();
 
-    // 5. weighted values (T3): thread (j, dg) walks positions j, j+16, ... in order
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // 5. weighted values (T3): thread (j, dg) walks positions j, j+32, ... in order
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     float total = 0.0f;
-    for (int base = 0; base < nglobal; base += 16 * kVChunk) {
+    const int last = nglobal > 0 ? nglobal - 1 : 0;
+    for (int base = 0; base < nglobal; base += kClasses * kVChunk) {
         if (base > 0) {
 #pragma unroll
-            for (int c = 0; c < kVChunk; ++c) {
-                const int pp = base + j + 16 * c;
-                vr[c] = *reinterpret_cast<const uint2*>(V + (size_t)min(pp, last) * kHeadDim + 4 * dg);
-            }
+            for (int c = 0; c < kVChunk; ++c)
+                vr[c] = *reinterpret_cast<const uint4*>(V + (size_t)min(base + j + kClasses * c, rows - 1) * kHeadDim +
+                                                        8 * dg);
         }
 #pragma unroll
         for (int c = 0; c < kVChunk; ++c) {
-            const int pp = base + j + 16 * c;
+            const int pp = base + j + kClasses * c;
             const bool ok = pp < nglobal;
             const float e = scores[min(pp, last)];
-            float v4[4];
-            unpack4(vr[c], v4);
+            float v8[8];
+            unpack8(vr[c], v8);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float t = acc[i] + e * v4[i];
+            for (int i = 0; i < 8; ++i) {
+                const float t = acc[i] + e * v8[i];
                 acc[i] = ok ? t : acc[i];
             }
             const float tt = total + e;
             total = ok ? tt : total;
         }
     }
-    if (has_new && j == (nglobal & 15)) {  // the newest position closes its class's sequence
+    if (has_new && j == (nglobal & (kClasses - 1))) {  // the newest position closes its class
         const float e = scores[nglobal];
-        float v4[4];
-        unpack4(*reinterpret_cast<const uint2*>(&new_s[1][4 * dg]), v4);
+        float v8[8];
+        unpack8(*reinterpret_cast<const uint4*>(&new_s[1][8 * dg]), v8);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = acc[i] + e * v4[i];
+        for (int i = 0; i < 8; ++i) acc[i] = acc[i] + e * v8[i];
         total = total + e;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) part_s[j][4 * dg + i] = acc[i];
+    for (int i = 0; i < 8; ++i) part_s[j][8 * dg + i] = acc[i];
     if (dg == 0) total_s[j] = total;
     __syncthreads();
     if (tid < kHeadDim) {
         float o = 0.0f, t = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
+        for (int k = 0; k < kClasses; ++k) {
             o = o + part_s[k][tid];
             t = t + total_s[k];
         }
@@ -267,13 +266,13 @@ hipError_t launch_attend(const AttendParams& p, int mode, int grid_x, int grid_y
     const dim3 grid(grid_x, grid_y);
     switch (mode) {
         case kAttendDecode:
-            hipLaunchKernelGGL(attend_kernel<kAttendDecode>, grid, dim3(256), lds, stream, p);
+            rn_launch(attend_kernel<kAttendDecode>, grid, dim3(256), lds, stream, p);
             break;
         case kAttendPrefill:
-            hipLaunchKernelGGL(attend_kernel<kAttendPrefill>, grid, dim3(256), lds, stream, p);
+            rn_launch(attend_kernel<kAttendPrefill>, grid, dim3(256), lds, stream, p);
             break;
         case kAttendRaw:
-            hipLaunchKernelGGL(attend_kernel<kAttendRaw>, grid, dim3(256), lds, stream, p);
+            rn_launch(attend_kernel<kAttendRaw>, grid, dim3(256), lds, stream, p);
             break;
         default:
             return hipErrorInvalidValue;
@@ -309,7 +308,7 @@ hipError_t launch_rope_append(const float* qkv, float* q_out, __half* kc, __half
                               int capacity, int d_model, int first, int count, const float* rope_cos,
                               const float* rope_sin, hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    hipLaunchKernelGGL(rope_append_kernel, dim3(count), dim3(256), 0, stream, qkv, q_out, kc, vc, layer, heads,
+    rn_launch(rope_append_kernel, dim3(count), dim3(256), 0, stream, qkv, q_out, kc, vc, layer, heads,
                        capacity, d_model, first, rope_cos, rope_sin);
     return hipGetLastError();
 }

@@ -133,25 +133,25 @@ hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, h
     if (dump) {
         if (epilogue != kGemmStore) return hipErrorInvalidValue;
         if (form == kPanel)
-            hipLaunchKernelGGL((gemm_kernel<kGemmStore, kPanel, true>), grid, block, 0, stream, p);
+            rn_launch((gemm_kernel<kGemmStore, kPanel, true>), grid, block, 0, stream, p);
         else
-            hipLaunchKernelGGL((gemm_kernel<kGemmStore, kPlane, true>), grid, block, 0, stream, p);
+            rn_launch((gemm_kernel<kGemmStore, kPlane, true>), grid, block, 0, stream, p);
         return hipGetLastError();
     }
     if (form == kPlane) {
         if (epilogue != kGemmStore) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((gemm_kernel<kGemmStore, kPlane, false>), grid, block, 0, stream, p);
+        rn_launch((gemm_kernel<kGemmStore, kPlane, false>), grid, block, 0, stream, p);
         return hipGetLastError();
     }
     switch (epilogue) {
         case kGemmStore:
-            hipLaunchKernelGGL((gemm_kernel<kGemmStore, kPanel, false>), grid, block, 0, stream, p);
+            rn_launch((gemm_kernel<kGemmStore, kPanel, false>), grid, block, 0, stream, p);
             break;
         case kGemmResidual:
-            hipLaunchKernelGGL((gemm_kernel<kGemmResidual, kPanel, false>), grid, block, 0, stream, p);
+            rn_launch((gemm_kernel<kGemmResidual, kPanel, false>), grid, block, 0, stream, p);
             break;
         case kGemmSilu:
-            hipLaunchKernelGGL((gemm_kernel<kGemmSilu, kPanel, false>), grid, block, 0, stream, p);
+            rn_launch((gemm_kernel<kGemmSilu, kPanel, false>), grid, block, 0, stream, p);
             break;
         default:
             return hipErrorInvalidValue;
@@ -209,7 +209,7 @@ hipError_t launch_norm_quantise(const float* x, const float* gain, int count, in
                                 float* scales, float* normed, hipStream_t stream) {
     if (count <= 0) return hipSuccess;
     if (n <= 0 || n > kMaxWidth || n % 8 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(norm_quantise_kernel, dim3(count), dim3(64), 0, stream, x, gain, n, eps, codes, scales,
+    rn_launch(norm_quantise_kernel, dim3(count), dim3(64), 0, stream, x, gain, n, eps, codes, scales,
                        normed);
     return hipGetLastError();
 }
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const uint32_t* tokens,
 hipError_t launch_embed_rows(const uint32_t* tokens, int count, const int8_t* E, const float* sE, int d, int vocab,
                              float scale, float* X, int32_t* error, hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    hipLaunchKernelGGL(embed_rows_kernel, dim3(count), dim3(256), 0, stream, tokens, E, sE, d, vocab, scale, X, error);
+    rn_launch(embed_rows_kernel, dim3(count), dim3(256), 0, stream, tokens, E, sE, d, vocab, scale, X, error);
     return hipGetLastError();
 }
 
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* logits, i
 hipError_t launch_argmax_rows(const float* logits, int count, int n, uint32_t* tokens, uint32_t* ids, int steps,
                               int step, hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3(count), dim3(256), 0, stream, logits, n, tokens, ids, steps, step);
+    rn_launch(argmax_rows_kernel, dim3(count), dim3(256), 0, stream, logits, n, tokens, ids, steps, step);
     return hipGetLastError();
 }
 
@@ -274,7 +274,7 @@ __global__ void advance_positions_kernel(int32_t* pos, int count, int by) {
 
 hipError_t launch_advance_positions(int32_t* pos, int count, int by, hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    hipLaunchKernelGGL(advance_positions_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, pos, count, by);
+    rn_launch(advance_positions_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, pos, count, by);
     return hipGetLastError();
 }
 

@@ -258,13 +258,13 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
 
 hipError_t launch_argmax_finalize(const unsigned long long* keys, int nkeys, const float* logits,
                                   DecodeState* state, uint32_t* ids, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(256), 0, stream, keys, nkeys, logits, state, ids);
+    rn_launch(argmax_finalize_kernel, dim3(1), dim3(256), 0, stream, keys, nkeys, logits, state, ids);
     return hipGetLastError();
 }
 
 template <int K, int ROWS, int PRO, int EPI, int FORM>
 static hipError_t launch_one(const GemvParams& p, int blocks, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv_kernel<K, ROWS, PRO, EPI, FORM>), dim3(blocks), dim3(64), 0, stream, p);
+    rn_launch((gemv_kernel<K, ROWS, PRO, EPI, FORM>), dim3(blocks), dim3(64), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -3,12 +3,34 @@
 // kernel arguments.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
 namespace rn {
+
+// Launch hook of the per-kernel profiler: when a pair of events is armed, the
+// next launch records them around the kernel's own execution
+// (hipExtLaunchKernelGGL), so the interval excludes queueing gaps.
+struct LaunchEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+LaunchEvents& launch_events();  // per host thread
+
+template <typename F, typename... Args>
+inline void rn_launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
+    LaunchEvents& ev = launch_events();
+    if (ev.start != nullptr) {
+        hipEvent_t start = ev.start, stop = ev.stop;
+        ev.start = ev.stop = nullptr;
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, start, stop, 0u, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+    }
+}
 
 constexpr int kGroup = 32;  // int8 codes per fp32 weight scale
 

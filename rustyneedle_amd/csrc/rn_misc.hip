@@ -7,6 +7,11 @@
 
 namespace rn {
 
+LaunchEvents& launch_events() {
+    static thread_local LaunchEvents events;
+    return events;
+}
+
 constexpr int kRowThreads = 64;
 constexpr int kMaxRow = 4096;
 
@@ -72,21 +77,21 @@ hipError_t launch_norm_rows(const float* x, const float* gain, int count, int n,
                             hipStream_t stream) {
     if (n % 8 != 0 || n > kMaxRow || n <= 0) return hipErrorInvalidValue;
     if (count <= 0) return hipSuccess;
-    hipLaunchKernelGGL(norm_rows_kernel, dim3(count), dim3(kRowThreads), 0, stream, x, gain, n, eps, out);
+    rn_launch(norm_rows_kernel, dim3(count), dim3(kRowThreads), 0, stream, x, gain, n, eps, out);
     return hipGetLastError();
 }
 
 hipError_t launch_finish_push(const float* x, const float* gain, int n, float eps, float* hidden,
                               DecodeState* state, hipStream_t stream) {
     if (n % 8 != 0 || n > kMaxRow) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(finish_push_kernel, dim3(1), dim3(kRowThreads), 0, stream, x, gain, n, eps, hidden, state);
+    rn_launch(finish_push_kernel, dim3(1), dim3(kRowThreads), 0, stream, x, gain, n, eps, hidden, state);
     return hipGetLastError();
 }
 
 hipError_t launch_quantise_rows(const float* x, int count, int columns, int8_t* codes, float* scales,
                                 hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    hipLaunchKernelGGL(quantise_rows_kernel, dim3(count), dim3(kRowThreads), 0, stream, x, columns, codes, scales);
+    rn_launch(quantise_rows_kernel, dim3(count), dim3(kRowThreads), 0, stream, x, columns, codes, scales);
     return hipGetLastError();
 }
 
@@ -99,13 +104,13 @@ __global__ void set_state_kernel(DecodeState* st, uint32_t token, int32_t pos, u
 
 hipError_t launch_set_state(DecodeState* state, uint32_t token, int32_t pos, uint32_t step, uint32_t ids_capacity,
                             hipStream_t stream) {
-    hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, stream, state, token, pos, step, ids_capacity);
+    rn_launch(set_state_kernel, dim3(1), dim3(1), 0, stream, state, token, pos, step, ids_capacity);
     return hipGetLastError();
 }
 
 hipError_t launch_fast_exp(const float* x, float* y, int n, int apply_silu, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(fast_exp_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, y, n, apply_silu);
+    rn_launch(fast_exp_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, y, n, apply_silu);
     return hipGetLastError();
 }
 

@@ -87,6 +87,22 @@ def test_greedy_equals_push_logits_argmax(tiny, tiny_config):
     assert ids.tolist() == manual
 
 
+def test_profile_step_matches_greedy(tiny, tiny_config):
+    """The per-kernel profiling path runs the same kernels as the captured step."""
+    gm, _ = tiny
+    k, v = rn.synthetic_cache(tiny_config, 30, "profile")
+    a, b = gm.session(64), gm.session(64)
+    a.set_cache(k, v)
+    b.set_cache(k, v)
+    prof = a.profile_step(7, 6)
+    b.decode_greedy(7, 6)
+    assert len(a) == len(b) == 36
+    assert np.array_equal(_bits(a.logits()), _bits(b.logits()))
+    assert prof["attention"]["per_step"] == tiny_config["layers"]
+    assert prof["logits"]["per_step"] == 1 and prof["final"]["per_step"] == 1
+    assert all(p["us"] > 0 for p in prof.values())
+
+
 def test_feed_prefill_bit_exact_and_equals_pushes(tiny, tiny_config):
     gm, om = tiny
     k, v = rn.synthetic_cache(tiny_config, 30, "feed")
