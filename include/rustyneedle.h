@@ -199,7 +199,7 @@ int rn_session_decode_greedy(rn_session* session, uint32_t first, int steps, uin
 int rn_session_stream(const rn_session* session, void** stream);
 
 /* Per-kernel timing of greedy decode steps (no reference counterpart: the
- * reference has no tracing; this is the build's tracing hook). Runs `steps`
+ * reference has no tracing; it is this library's tracing hook). Runs `steps`
  * greedy steps like rn_session_decode_greedy, launching the step's kernels
  * directly with a HIP event after each, and returns for every kernel kind the
  * average microseconds per launch (kind_us) and launches per step (kind_count),
