@@ -39,6 +39,38 @@ __device__ __forceinline__ int quantise_one(float value, float scale) {
     return (int)q;
 }
 
+// The code of a quotient already divided by the scale: quantise_one's rounding.
+__device__ __forceinline__ int code_of_quotient(float y) {
+    float q = __builtin_rintf(y);
+    q = q < -128.0f ? -128.0f : (q > 127.0f ? 127.0f : q);
+    if (q != q) return 0;
+    return (int)q;
+}
+
+// The quotients value/scale of quantise_one for E values of a lane, without a
+// division per element: y = value * (1/scale) is within 1.5 * 2^-23 * |y| of
+// the exact quotient and the correctly rounded quotient within 2^-24 of it, so
+// unless y lies within |y| * 2^-21 of a half-integer both round to the same
+// integer (a tie would put y on the boundary). When any lane of the wave has a
+// value that close, the whole wave takes the exact division instead (a
+// wave-uniform branch, so the common path carries no division code). The codes
+// are bit-identical to quantise_one for every input, NaN and inf included.
+template <int E>
+__device__ __forceinline__ void quotients(const float* v, float scale, float* y) {
+    const float inv = 1.0f / scale;
+    bool near = false;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        y[e] = v[e] * inv;
+        const float h = floorf(y[e]) + 0.5f;
+        near = near || (fabsf(y[e] - h) <= fabsf(y[e]) * 0x1p-21f + 0x1p-30f);
+    }
+    if (__any(near)) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) y[e] = v[e] / scale;
+    }
+}
+
 // ops.rs:103-110
 __device__ __forceinline__ float int8_scale_from_peak(float peak) { return peak > 0.0f ? peak / 127.0f : 1.0f; }
 

@@ -6,152 +6,216 @@
 // (crates/kernels/src/panel.rs:136-198) for int8 codes with one fp32 scale per
 // 32 columns.
 //
-// One v_mfma_i32_32x32x32_i8 covers exactly one 32-column group for a 32-token
-// x 32-row tile, so every group's int32 accumulators come out of the matrix
+// One v_mfma_i32_16x16x32_i8 covers exactly one 32-column group for a
+// 16-token x 16-row tile, so every group's int32 sums come out of the matrix
 // core separately and feed the sequential group epilogue of the reference
 // (panel form fmaf(acc, sW*sx, total), or plane form total + (acc*sW)*sx).
-// A 256-thread block is 2x2 waves over a 64-token x 64-row output tile; each
-// wave streams its 32 token rows and 32 weight rows straight from global
-// memory with 128-bit loads (one per lane per group, prefetched one group
-// ahead). The finished tile goes through LDS for coalesced stores with the
-// fused tail: store, residual add, or silu(gate)*up.
-//
-// MFMA operand layout (32x32x32 i8): lane l supplies A row l%32 and B column
-// l%32, 16 bytes of K from half (l/32); any K permutation inside the
+// MFMA operand layout (16x16x32 i8): lane l supplies A row l%16 and B column
+// l%16 with 8 bytes of K from quarter l/16; any K permutation inside the
 // instruction is the same for A and B, so the group sum is exact regardless.
-// Output register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// Output register i of lane l holds row 4*(l/16) + i, column l%16.
 #include "rn_device.hpp"
 #include "rn_internal.hpp"
 
 namespace rn {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ v4i load16(const int8_t* p, bool ok) {
-    if (!ok) return v4i{0, 0, 0, 0};
-    const int4 t = *reinterpret_cast<const int4*>(p);
-    return v4i{t.x, t.y, t.z, t.w};
+// The integer work of a BM x BN output tile is spread over the 16 waves of a
+// 1024-thread block by group — every (16x16 sub-tile, group) MFMA is one job, each
+// wave issues all the loads of its 4 jobs at once — and the int32 group sums go
+// to LDS. Then one lane per output runs the sequential epilogue chain over the
+// groups, reading the sums and the weight scales from LDS. All of a tile's
+// loads are in flight together, so a launch costs about one memory round trip
+// plus the chain, whatever K is. LDS: G*BM*BN int32 (64 KB at the sizes used).
+template <int G, int BM, int BN>
+struct SplitShape {
+    static constexpr int kSub = (BM / 16) * (BN / 16);  // 16x16 sub-tiles
+    static constexpr int kJobs = kSub * G;
+    static constexpr int kPerWave = kJobs / 16;
+    static_assert(kJobs % 16 == 0, "jobs spread evenly over 16 waves");
+    static_assert(G % kPerWave == 0, "a wave's jobs stay in one sub-tile");
+    static_assert(BM * BN <= 1024, "one output per thread");
+};
+
+template <int G, int BM, int BN, int EPI, int FORM, bool DUMP>
+__global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
+    using S = SplitShape<G, BM, BN>;
+    constexpr bool kSilu = EPI == kGemmSilu;
+    constexpr int K = G * kGroup;
+    // Operand rows padded by 32 bytes: the 16 rows x 4 quarters of one MFMA
+    // fragment read then cover all 64 banks twice (the minimum for 512 bytes).
+    constexpr int KP = K + 32;
+    constexpr int kOperandBytes = (BM + BN) * KP;
+    constexpr int kAccBytes = G * BM * BN * 4;
+    // operand tiles first, then (after every wave has its fragments) the sums
+    __shared__ __align__(16) char ops_s[kOperandBytes > kAccBytes ? kOperandBytes : kAccBytes];
+    int8_t(*a_s)[KP] = reinterpret_cast<int8_t(*)[KP]>(ops_s);
+    int8_t(*b_s)[KP] = reinterpret_cast<int8_t(*)[KP]>(ops_s + BM * KP);
+    int(*acc_s)[BM][BN] = reinterpret_cast<int(*)[BM][BN]>(ops_s);
+    __shared__ float sw_s[BN][G + 1];
+    __shared__ float sx_s[BM];
+    __shared__ float tile[kSilu ? BM : 1][kSilu ? BN + 1 : 1];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int mtiles = (p.M + BM - 1) / BM;
+    int t = blockIdx.x;
+    if ((gridDim.x & 7) == 0) t = (t & 7) * (gridDim.x >> 3) + (t >> 3);
+    const int mt = t % mtiles, nt = t / mtiles;
+    const int m0 = mt * BM;
+
+    // output column of local column c (silu: first BN/2 gate rows, then the up rows)
+    auto column = [&](int c) -> int {
+        if constexpr (kSilu)
+            return c < BN / 2 ? nt * (BN / 2) + c : p.half + nt * (BN / 2) + (c - BN / 2);
+        else
+            return nt * BN + c;
+    };
+
+    // phase 1a: the tile's token rows and weight rows into LDS with 16-byte
+    // loads (a 64-lane load covers 1 KB of consecutive row bytes), all issued
+    // before any is waited for; rows past the matrix repeat its last row
+    constexpr int kRow16 = K / 16;  // 16-byte pieces per row
+    constexpr int kPieces = (BM + BN) * kRow16;
+    int4 piece[(kPieces + 1023) / 1024];
+#pragma unroll
+    for (int q = 0; q < (kPieces + 1023) / 1024; ++q) {
+        const int i = threadIdx.x + 1024 * q;
+        if (kPieces % 1024 == 0 || i < kPieces) {
+            const int row = i / kRow16, col = i - row * kRow16;
+            const int8_t* src = row < BM ? p.X + (size_t)min(m0 + row, p.M - 1) * K
+                                         : p.W + (size_t)min(column(row - BM), p.N - 1) * K;
+            piece[q] = *reinterpret_cast<const int4*>(src + 16 * col);
+        }
+    }
+    // scales of the tile's columns and rows
+    for (int i = threadIdx.x; i < BN * G; i += 1024) {
+        const int c = i / G, g = i - c * G;
+        sw_s[c][g] = p.sW[(size_t)min(column(c), p.N - 1) * G + g];
+    }
+    if (threadIdx.x < BM) sx_s[threadIdx.x] = p.sx[min(m0 + (int)threadIdx.x, p.M - 1)];
+#pragma unroll
+    for (int q = 0; q < (kPieces + 1023) / 1024; ++q) {
+        const int i = threadIdx.x + 1024 * q;
+        if (kPieces % 1024 == 0 || i < kPieces) {
+            const int row = i / kRow16, col = i - row * kRow16;
+            *reinterpret_cast<int4*>(&a_s[0][0] + (size_t)row * KP + 16 * col) = piece[q];
+        }
+    }
+    __syncthreads();
+
+    // phase 1b: this wave's jobs — one sub-tile, kPerWave consecutive groups
+    const int job0 = wave * S::kPerWave;
+    const int sub = job0 / G, g0 = job0 - sub * G;
+    const int sm = (sub / (BN / 16)) * 16, sn = (sub % (BN / 16)) * 16;
+    const int r16 = lane & 15, kq = lane >> 4;
+    long a[S::kPerWave], b[S::kPerWave];
+#pragma unroll
+    for (int q = 0; q < S::kPerWave; ++q) {
+        a[q] = *reinterpret_cast<const long*>(&a_s[sm + r16][(g0 + q) * kGroup + 8 * kq]);
+        b[q] = *reinterpret_cast<const long*>(&b_s[sn + r16][(g0 + q) * kGroup + 8 * kq]);
+    }
+    v4i r4[S::kPerWave];
+#pragma unroll
+    for (int q = 0; q < S::kPerWave; ++q)
+        r4[q] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[q], b[q], v4i{0, 0, 0, 0}, 0, 0, 0);
+    __syncthreads();  // every wave holds its fragments: the operand tiles may be overwritten
+#pragma unroll
+    for (int q = 0; q < S::kPerWave; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc_s[g0 + q][sm + 4 * kq + i][sn + r16] = r4[q][i];
+    __syncthreads();
+
+    // phase 2: one output per thread, the group chain in order
+    const int r = threadIdx.x / BN, c = threadIdx.x - r * BN;
+    float total = 0.0f;
+    if (r < BM) {
+        const float sx = sx_s[r];
+#pragma unroll 8
+        for (int g = 0; g < G; ++g) {
+            const int v = acc_s[g][r][c];
+            const float s = sw_s[c][g];
+            if constexpr (FORM == kPanel)
+                total = fmaf((float)v, s * sx, total);  // panel.rs:184-188
+            else
+                total = total + ((float)v * s) * sx;    // neon.rs:180
+        }
+        if constexpr (DUMP) {
+            const int m = m0 + r, n = column(c);
+            if (m < p.M && n < p.N)
+                for (int g = 0; g < G; ++g) p.acc[((size_t)m * p.N + n) * G + g] = acc_s[g][r][c];
+        }
+    }
+    if constexpr (kSilu) {
+        if (r < BM) tile[r][c] = total;
+        __syncthreads();
+        if (threadIdx.x < BM * (BN / 2)) {
+            const int mi = threadIdx.x / (BN / 2), ii = threadIdx.x - mi * (BN / 2);
+            const int m = m0 + mi, o = nt * (BN / 2) + ii;
+            if (m < p.M && o < p.half) p.Y[(size_t)m * p.ldy + o] = silu(tile[mi][ii]) * tile[mi][BN / 2 + ii];
+        }
+    } else if (r < BM) {
+        const int m = m0 + r, n = column(c);
+        if (m < p.M && n < p.N) {
+            float* dst = p.Y + (size_t)m * p.ldy + n;
+            if constexpr (EPI == kGemmResidual)
+                *dst = *dst + total;
+            else
+                *dst = total;
+        }
+    }
+}
+
+template <int G, int BM, int BN, int EPI, int FORM, bool DUMP>
+static void launch_split(const GemmParams& p, hipStream_t stream) {
+    const int mtiles = (p.M + BM - 1) / BM;
+    const int ntiles = EPI == kGemmSilu ? (p.half + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
+    rn_launch((gemm_split_kernel<G, BM, BN, EPI, FORM, DUMP>), dim3(mtiles * ntiles), dim3(1024), 0, stream, p);
 }
 
 template <int EPI, int FORM, bool DUMP>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
-    __shared__ float tile[64][65];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int G = p.K / kGroup;
-    const int m0 = blockIdx.y * 64 + wm * 32;
-    int n_base;
-    if constexpr (EPI == kGemmSilu)
-        n_base = (wn == 0 ? 0 : p.half) + blockIdx.x * 32;
-    else
-        n_base = blockIdx.x * 64 + wn * 32;
-    const int n = n_base + (lane & 31);
-    const bool b_ok = n < p.N;
-    const int mrow = m0 + (lane & 31);
-    const bool a_ok = mrow < p.M;
-    const int khalf = (lane >> 5) * 16;
-    const int8_t* xa = p.X + (size_t)(a_ok ? mrow : 0) * p.K + khalf;
-    const int8_t* wb = p.W + (size_t)(b_ok ? n : 0) * p.K + khalf;
-    const float* srow = p.sW + (size_t)(b_ok ? n : 0) * G;
-
-    float sxr[16];
-    float total[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int m = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        sxr[r] = m < p.M ? p.sx[m] : 0.0f;
-        total[r] = 0.0f;
-    }
-
-    v4i a = load16(xa, a_ok);
-    v4i b = load16(wb, b_ok);
-    for (int g = 0; g < G; ++g) {
-        v4i an = a, bn = b;
-        if (g + 1 < G) {
-            an = load16(xa + (g + 1) * kGroup, a_ok);
-            bn = load16(wb + (g + 1) * kGroup, b_ok);
-        }
-        v16i acc = {};
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
-        const float s = b_ok ? srow[g] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            if constexpr (FORM == kPanel)
-                total[r] = fmaf((float)acc[r], s * sxr[r], total[r]);  // panel.rs:184-188
-            else
-                total[r] = total[r] + ((float)acc[r] * s) * sxr[r];    // neon.rs:180
-        }
-        if constexpr (DUMP) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < p.M && b_ok) p.acc[((size_t)m * p.N + n) * G + g] = acc[r];
-            }
-        }
-        a = an;
-        b = bn;
-    }
-
-#pragma unroll
-    for (int r = 0; r < 16; ++r) tile[wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)][wn * 32 + (lane & 31)] = total[r];
-    __syncthreads();
-
-    if constexpr (EPI == kGemmSilu) {
-        for (int idx = threadIdx.x; idx < 64 * 32; idx += 256) {
-            const int mi = idx >> 5, ii = idx & 31;
-            const int m = blockIdx.y * 64 + mi, i = blockIdx.x * 32 + ii;
-            if (m < p.M && i < p.half) p.Y[(size_t)m * p.ldy + i] = silu(tile[mi][ii]) * tile[mi][32 + ii];
-        }
-    } else {
-        for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
-            const int mi = idx >> 6, ni = idx & 63;
-            const int m = blockIdx.y * 64 + mi, nn = blockIdx.x * 64 + ni;
-            if (m < p.M && nn < p.N) {
-                float* dst = p.Y + (size_t)m * p.ldy + nn;
-                if constexpr (EPI == kGemmResidual)
-                    *dst = *dst + tile[mi][ni];
-                else
-                    *dst = tile[mi][ni];
-            }
-        }
+static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
+    // tiles sized so that the int32 sums of a tile fill 64 KB of LDS
+    switch (p.K) {
+        case 512:
+            launch_split<16, 32, 32, EPI, FORM, DUMP>(p, stream);
+            break;
+        case 1024:
+            launch_split<32, 16, 32, EPI, FORM, DUMP>(p, stream);
+            break;
+        default:
+            launch_split<64, 16, 16, EPI, FORM, DUMP>(p, stream);
+            break;
     }
 }
 
 hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, hipStream_t stream) {
     if (p.M <= 0) return hipSuccess;
-    if (p.K % kGroup != 0 || p.K <= 0) return hipErrorInvalidValue;
-    const int gy = (p.M + 63) / 64;
-    int gx;
-    if (epilogue == kGemmSilu) {
-        if (p.half % 32 != 0 || p.N != 2 * p.half) return hipErrorInvalidValue;
-        gx = p.half / 32;
-    } else {
-        gx = (p.N + 63) / 64;
-    }
-    const dim3 grid(gx, gy), block(256);
+    // instantiated for the supported widths (the kernel is unrolled over groups)
+    if ((p.K != 512 && p.K != 1024 && p.K != 2048) || p.N <= 0) return hipErrorInvalidValue;
+    if (epilogue == kGemmSilu && (p.half % 16 != 0 || p.N != 2 * p.half)) return hipErrorInvalidValue;
     if (dump) {
         if (epilogue != kGemmStore) return hipErrorInvalidValue;
         if (form == kPanel)
-            rn_launch((gemm_kernel<kGemmStore, kPanel, true>), grid, block, 0, stream, p);
+            launch_by_rows<kGemmStore, kPanel, true>(p, stream);
         else
-            rn_launch((gemm_kernel<kGemmStore, kPlane, true>), grid, block, 0, stream, p);
+            launch_by_rows<kGemmStore, kPlane, true>(p, stream);
         return hipGetLastError();
     }
     if (form == kPlane) {
         if (epilogue != kGemmStore) return hipErrorInvalidValue;
-        rn_launch((gemm_kernel<kGemmStore, kPlane, false>), grid, block, 0, stream, p);
+        launch_by_rows<kGemmStore, kPlane, false>(p, stream);
         return hipGetLastError();
     }
     switch (epilogue) {
         case kGemmStore:
-            rn_launch((gemm_kernel<kGemmStore, kPanel, false>), grid, block, 0, stream, p);
+            launch_by_rows<kGemmStore, kPanel, false>(p, stream);
             break;
         case kGemmResidual:
-            rn_launch((gemm_kernel<kGemmResidual, kPanel, false>), grid, block, 0, stream, p);
+            launch_by_rows<kGemmResidual, kPanel, false>(p, stream);
             break;
         case kGemmSilu:
-            rn_launch((gemm_kernel<kGemmSilu, kPanel, false>), grid, block, 0, stream, p);
+            launch_by_rows<kGemmSilu, kPanel, false>(p, stream);
             break;
         default:
             return hipErrorInvalidValue;
@@ -161,56 +225,111 @@ hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, h
 
 // ---- row kernels for multi-token work -------------------------------------------
 
-constexpr int kMaxWidth = 4096;
-
 // Optional zero-centred norm (ops.rs:44-50 with the sum of ops.rs:7-17), then
-// the per-row int8 quantisation (ops.rs:112-118). One 64-lane block per row.
-// `normed` (nullable) receives the normed row.
-__global__ __launch_bounds__(64) void norm_quantise_kernel(const float* x, const float* gain, int n, float eps,
-                                                           int8_t* codes, float* scales, float* normed) {
-    __shared__ float v[kMaxWidth];
-    __shared__ float lanes_s[8];
-    const int lane = threadIdx.x;
-    const float* row = x + (size_t)blockIdx.x * n;
-    for (int i = lane; i < n; i += 64) v[i] = row[i];
-    __syncthreads();
+// the per-row int8 quantisation (ops.rs:112-118). One wave per row, four rows
+// per block; the row lives in registers (n/256 float4 per lane). The sum of
+// squares keeps the reference's order: 8 strided partial sums (element e goes
+// to partial e%8, each summed in element order), then the partials 0..7 in
+// order; the squares are staged transposed in LDS so that each of 8 lanes runs
+// one partial over contiguous memory. `normed` (nullable) receives the normed
+// rows. NV = n / 256 float4 per lane.
+template <int NV>
+__global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, const float* gain, int count, float eps,
+                                                            int8_t* codes, float* scales, float* normed) {
+    constexpr int n = NV * 256;
+    extern __shared__ float sq_s[];  // [4][n] when gain != nullptr
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + wave;
+    const bool live = row < count;
+    const float4* src = reinterpret_cast<const float4*>(x + (size_t)(live ? row : count - 1) * n);
+    float4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = src[lane + 64 * i];
     if (gain != nullptr) {
-        if (lane < 8) {
-            float s = 0.0f;
-            for (int c = 0; c < n / 8; ++c) {
-                const float t = v[8 * c + lane];
-                s = s + t * t;
-            }
-            lanes_s[lane] = s;
+        float* sq = sq_s + wave * n;
+        constexpr int run = n >> 3;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e = 4 * (lane + 64 * i);  // elements e..e+3; e % 8 is 0 or 4
+            const int p = e & 7, c = e >> 3;
+            sq[(p + 0) * run + c] = v[i].x * v[i].x;
+            sq[(p + 1) * run + c] = v[i].y * v[i].y;
+            sq[(p + 2) * run + c] = v[i].z * v[i].z;
+            sq[(p + 3) * run + c] = v[i].w * v[i].w;
         }
         __syncthreads();
+        float part = 0.0f;
+        if (lane < 8) {
+            const float4* r4 = reinterpret_cast<const float4*>(sq + lane * run);
+            for (int c = 0; c < run / 4; ++c) {
+                const float4 t = r4[c];
+                part = part + t.x;
+                part = part + t.y;
+                part = part + t.z;
+                part = part + t.w;
+            }
+        }
         float total = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) total = total + lanes_s[j];
-        total = total + 0.0f;
-        const float mean_square = total / (float)n;
-        const float inverse = 1.0f / sqrtf(mean_square + eps);
-        __syncthreads();
-        for (int i = lane; i < n; i += 64) v[i] = ((1.0f + gain[i]) * v[i]) * inverse;
-        __syncthreads();
-        if (normed != nullptr)
-            for (int i = lane; i < n; i += 64) normed[(size_t)blockIdx.x * n + i] = v[i];
+        for (int j = 0; j < 8; ++j) total = total + __shfl(part, j, kWave);
+        total = total + 0.0f;  // the empty tail of the 8-lane sum
+        const float inverse = 1.0f / sqrtf(total / (float)n + eps);
+        const float4* g4 = reinterpret_cast<const float4*>(gain);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const float4 g = g4[lane + 64 * i];
+            v[i].x = ((1.0f + g.x) * v[i].x) * inverse;
+            v[i].y = ((1.0f + g.y) * v[i].y) * inverse;
+            v[i].z = ((1.0f + g.z) * v[i].z) * inverse;
+            v[i].w = ((1.0f + g.w) * v[i].w) * inverse;
+            if (normed != nullptr && live) reinterpret_cast<float4*>(normed + (size_t)row * n)[lane + 64 * i] = v[i];
+        }
     }
     float peak = 0.0f;
-    for (int i = lane; i < n; i += 64) peak = fmaxf(peak, fabsf(v[i]));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        peak = fmaxf(peak, fabsf(v[i].x));
+        peak = fmaxf(peak, fabsf(v[i].y));
+        peak = fmaxf(peak, fabsf(v[i].z));
+        peak = fmaxf(peak, fabsf(v[i].w));
+    }
     peak = wave_max(peak);
     const float scale = int8_scale_from_peak(peak);
-    if (codes != nullptr)
-        for (int i = lane; i < n; i += 64) codes[(size_t)blockIdx.x * n + i] = (int8_t)quantise_one(v[i], scale);
-    if (lane == 0 && scales != nullptr) scales[blockIdx.x] = scale;
+    if (!live) return;  // the whole wave: one row per wave
+    if (codes != nullptr) {
+        float y[4 * NV];
+        quotients<4 * NV>(reinterpret_cast<const float*>(v), scale, y);
+        int* dst = reinterpret_cast<int*>(codes + (size_t)row * n);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t b0 = (uint8_t)code_of_quotient(y[4 * i + 0]);
+            const uint32_t b1 = (uint8_t)code_of_quotient(y[4 * i + 1]);
+            const uint32_t b2 = (uint8_t)code_of_quotient(y[4 * i + 2]);
+            const uint32_t b3 = (uint8_t)code_of_quotient(y[4 * i + 3]);
+            dst[lane + 64 * i] = (int)(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24));
+        }
+    }
+    if (lane == 0 && scales != nullptr) scales[row] = scale;
 }
 
 hipError_t launch_norm_quantise(const float* x, const float* gain, int count, int n, float eps, int8_t* codes,
                                 float* scales, float* normed, hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    if (n <= 0 || n > kMaxWidth || n % 8 != 0) return hipErrorInvalidValue;
-    rn_launch(norm_quantise_kernel, dim3(count), dim3(64), 0, stream, x, gain, n, eps, codes, scales,
-                       normed);
+    const size_t lds = gain != nullptr ? 4 * sizeof(float) * (size_t)n : 0;
+    const dim3 grid((count + 3) / 4), block(256);
+    switch (n) {
+        case 512:
+            rn_launch(norm_quantise_kernel<2>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed);
+            break;
+        case 1024:
+            rn_launch(norm_quantise_kernel<4>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed);
+            break;
+        case 2048:
+            rn_launch(norm_quantise_kernel<8>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

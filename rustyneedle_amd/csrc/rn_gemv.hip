@@ -178,8 +178,10 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
         peak = wave_max(peak);
         sx = int8_scale_from_peak(peak);
+        float y[E];
+        quotients<E>(v, sx, y);
 #pragma unroll
-        for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)quantise_one(v[e], sx);
+        for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)code_of_quotient(y[e]);
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < XC; ++i) xc[i] = *reinterpret_cast<const int4*>(xq_s + load_chunk(i) * 16);

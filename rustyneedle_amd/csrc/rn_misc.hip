@@ -63,8 +63,13 @@ __global__ __launch_bounds__(64) void quantise_rows_kernel(const float* x, int n
     for (int i = threadIdx.x; i < n; i += kRowThreads) peak = fmaxf(peak, fabsf(row[i]));
     peak = wave_max(peak);
     const float scale = int8_scale_from_peak(peak);
-    for (int i = threadIdx.x; i < n; i += kRowThreads)
-        codes[(size_t)blockIdx.x * n + i] = (int8_t)quantise_one(row[i], scale);
+    for (int i0 = 0; i0 < n; i0 += kRowThreads) {  // uniform trip count: every lane reaches the wave vote
+        const int i = i0 + threadIdx.x;
+        const float v = i < n ? row[i] : 0.0f;
+        float y;
+        quotients<1>(&v, scale, &y);
+        if (i < n) codes[(size_t)blockIdx.x * n + i] = (int8_t)code_of_quotient(y);
+    }
     if (threadIdx.x == 0) scales[blockIdx.x] = scale;
 }
 

@@ -148,3 +148,49 @@ def test_attend_heads_rejects_bad_length():
     K = np.zeros((1, 4, 64), np.float16)
     with pytest.raises(rn.RnError):
         rn.attend_heads(q, K, K, np.array([5]))
+
+
+def _near_boundary_rows(rng, count, cols):
+    """Rows whose quotients by their own scale sit within a few ulps of
+    half-integers: the inputs where a reciprocal-based quantiser could differ
+    from the division."""
+    rows = np.empty((count, cols), np.float32)
+    for t in range(count):
+        peak = np.float32(10.0 ** rng.uniform(-3, 3))
+        s = np.float32(peak / np.float32(127))
+        k = rng.integers(-127, 127, cols).astype(np.float32)
+        v = ((k + np.float32(0.5)) * s).astype(np.float32)
+        steps = rng.integers(-3, 4, cols)
+        for u in range(1, 4):
+            v = np.where(steps >= u, np.nextafter(v, np.float32(np.inf)), v)
+            v = np.where(steps <= -u, np.nextafter(v, np.float32(-np.inf)), v)
+        v[0] = peak
+        rows[t] = np.clip(v, -peak, peak)
+    return rows
+
+
+def test_quantise_near_rounding_boundaries():
+    rng = np.random.default_rng(41)
+    x = _near_boundary_rows(rng, 16, 2048)
+    codes, scales = rn.quantise_int8(x)
+    for t in range(x.shape[0]):
+        c, s = oracle.quantise_int8(x[t])
+        assert scales[t] == s
+        assert np.array_equal(codes[t], c), t
+
+
+@pytest.mark.parametrize("cols", [512, 2048])
+def test_products_quantise_near_rounding_boundaries(cols):
+    """The matvec prologue and the batched row quantiser on the same inputs."""
+    rng = np.random.default_rng(cols + 5)
+    W, sW = _matrix(rng, 256, cols)
+    x = _near_boundary_rows(rng, 8, cols)
+    m = rn.QuantisedMatrix(W, sW)
+    yo, acco, _, _ = oracle.multiply(rn.FORM_PANEL, W, sW, x, with_acc=True)
+    yb, accb = m.multiply_batch_host(x, with_acc=True)
+    assert np.array_equal(accb, acco)
+    assert np.array_equal(yb.view(np.uint32), yo.view(np.uint32))
+    for t in range(x.shape[0]):
+        y, acc = m.multiply_vector_host(x[t], with_acc=True)
+        assert np.array_equal(acc, acco[t])
+        assert np.array_equal(y.view(np.uint32), yo[t].view(np.uint32))
