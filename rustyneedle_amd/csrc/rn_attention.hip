@@ -27,8 +27,6 @@
 namespace rn {
 
 constexpr int kHeadDim = 64;
-constexpr int kKChunk = 6;    // key passes of 64 rows issued together (384 positions)
-constexpr int kVChunk = 12;   // value positions per thread issued together (384 positions)
 constexpr int kClasses = 32;  // T3 position classes (p mod 32)
 
 __device__ __forceinline__ void unpack8(const uint4& raw, float* out) {
@@ -61,7 +59,11 @@ __device__ __forceinline__ float score_row(const float* q16, const uint4& ka, co
     return s;
 }
 
-template <int MODE>
+// KC key passes of 64 rows and VC value positions per thread are issued
+// together (64*KC and 32*VC positions). POS_FIRST (decode of many sequences):
+// read the position before the cache loads and clamp them to it, instead of
+// to the capacity, so that short caches do not fetch the rows of long ones.
+template <int MODE, int KC, int VC, bool POS_FIRST>
 __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
     extern __shared__ float scores[];
     __shared__ float q_s[kHeadDim];
@@ -104,29 +106,40 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
         rows = p.stride;
     }
 
+    if constexpr (POS_FIRST) {
+        pos = p.pos[(size_t)blockIdx.y * p.pos_stride];
+        if (pos < 0 || pos >= p.capacity) {
+            if (tid == 0) atomicOr(p.error, 2);
+            return;
+        }
+        rows = pos > 0 ? pos : 1;  // the cached rows; the new one is served from LDS
+    }
+
     // 1. cache loads, issued before anything that depends on the current token
     // or even on the length: rows past the valid ones are clamped into the
     // cache and their results discarded by selects (never by branches, which
     // would split the load stream and force a full wait).
-    uint4 kr[kKChunk][2];
+    uint4 kr[KC][2];
 #pragma unroll
-    for (int c = 0; c < kKChunk; ++c) {
+    for (int c = 0; c < KC; ++c) {
         const __half* row = K + (size_t)min(r + 64 * c, rows - 1) * kHeadDim + 16 * li;
         kr[c][0] = *reinterpret_cast<const uint4*>(row);
         kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
     }
-    uint4 vr[kVChunk];
+    uint4 vr[VC];
 #pragma unroll
-    for (int c = 0; c < kVChunk; ++c)
+    for (int c = 0; c < VC; ++c)
         vr[c] = *reinterpret_cast<const uint4*>(V + (size_t)min(j + kClasses * c, rows - 1) * kHeadDim + 8 * dg);
 
     // 2. the length, the query and (decoding) the rotary + fp16 append of the new row
     if constexpr (MODE == kAttendDecode) {
         const int h = blockIdx.x, b = blockIdx.y;
-        pos = p.pos[(size_t)b * p.pos_stride];
-        if (pos < 0 || pos >= p.capacity) {
-            if (tid == 0) atomicOr(p.error, 2);
-            return;
+        if constexpr (!POS_FIRST) {
+            pos = p.pos[(size_t)b * p.pos_stride];
+            if (pos < 0 || pos >= p.capacity) {
+                if (tid == 0) atomicOr(p.error, 2);
+                return;
+            }
         }
         nglobal = pos;
         has_new = true;
@@ -174,17 +187,17 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
     float q16[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) q16[i] = q_s[16 * li + i];
-    for (int base = 0; base < nglobal; base += 64 * kKChunk) {
+    for (int base = 0; base < nglobal; base += 64 * KC) {
         if (base > 0) {
 #pragma unroll
-            for (int c = 0; c < kKChunk; ++c) {
+            for (int c = 0; c < KC; ++c) {
                 const __half* row = K + (size_t)min(base + r + 64 * c, rows - 1) * kHeadDim + 16 * li;
                 kr[c][0] = *reinterpret_cast<const uint4*>(row);
                 kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
             }
         }
 #pragma unroll
-        for (int c = 0; c < kKChunk; ++c) {
+        for (int c = 0; c < KC; ++c) {
             const int pp = base + r + 64 * c;
             const float s = score_row(q16, kr[c][0], kr[c][1]);
             if (li == 0 && pp < nglobal) scores[pp] = s * inverse_root;
@@ -212,15 +225,15 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
     float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     float total = 0.0f;
     const int last = nglobal > 0 ? nglobal - 1 : 0;
-    for (int base = 0; base < nglobal; base += kClasses * kVChunk) {
+    for (int base = 0; base < nglobal; base += kClasses * VC) {
         if (base > 0) {
 #pragma unroll
-            for (int c = 0; c < kVChunk; ++c)
+            for (int c = 0; c < VC; ++c)
                 vr[c] = *reinterpret_cast<const uint4*>(V + (size_t)min(base + j + kClasses * c, rows - 1) * kHeadDim +
                                                         8 * dg);
         }
 #pragma unroll
-        for (int c = 0; c < kVChunk; ++c) {
+        for (int c = 0; c < VC; ++c) {
             const int pp = base + j + kClasses * c;
             const bool ok = pp < nglobal;
             const float e = scores[min(pp, last)];
@@ -266,13 +279,16 @@ hipError_t launch_attend(const AttendParams& p, int mode, int grid_x, int grid_y
     const dim3 grid(grid_x, grid_y);
     switch (mode) {
         case kAttendDecode:
-            rn_launch(attend_kernel<kAttendDecode>, grid, dim3(256), lds, stream, p);
+            if (grid_y == 1)  // one sequence: its loads go out before its position is read
+                rn_launch((attend_kernel<kAttendDecode, 6, 12, false>), grid, dim3(256), lds, stream, p);
+            else              // many ragged sequences: exact clamps, one pass up to 576 positions
+                rn_launch((attend_kernel<kAttendDecode, 9, 18, true>), grid, dim3(256), lds, stream, p);
             break;
         case kAttendPrefill:
-            rn_launch(attend_kernel<kAttendPrefill>, grid, dim3(256), lds, stream, p);
+            rn_launch((attend_kernel<kAttendPrefill, 4, 8, false>), grid, dim3(256), lds, stream, p);
             break;
         case kAttendRaw:
-            rn_launch(attend_kernel<kAttendRaw>, grid, dim3(256), lds, stream, p);
+            rn_launch((attend_kernel<kAttendRaw, 6, 12, false>), grid, dim3(256), lds, stream, p);
             break;
         default:
             return hipErrorInvalidValue;
