@@ -302,3 +302,166 @@ class OracleSession:
         lib.ro_greedy(C.byref(self.model.cfg), C.byref(self.model.model), C.byref(self.s), first, steps,
                       _ptr(ids))
         return ids
+
+
+# ---- Whistle-style speech path (rn_whistle.c) ------------------------------------
+
+class WConfig(C.Structure):
+    _fields_ = [(n, _i) for n in ("mels", "frames", "d_model", "heads", "head_dim", "enc_layers", "dec_layers", "ffn",
+                                  "vocab", "max_positions", "group")] + [("rope_theta", _f), ("norm_eps", _f)]
+
+
+class WEncLayer(C.Structure):
+    _fields_ = [("qkv", QMat), ("out", QMat), ("gate_up", QMat), ("down", QMat), ("norm_attn", _p),
+                ("norm_ffn", _p), ("q_norm", _p), ("k_norm", _p)]
+
+
+class WDecLayer(C.Structure):
+    _fields_ = [("qkv", QMat), ("out", QMat), ("cross_q", QMat), ("cross_kv", QMat), ("cross_out", QMat),
+                ("gate_up", QMat), ("down", QMat), ("norm_attn", _p), ("norm_cross", _p), ("post_norm", _p),
+                ("norm_ffn", _p), ("q_norm", _p), ("k_norm", _p), ("cross_gain", _f)]
+
+
+class WModel(C.Structure):
+    _fields_ = [("conv1", _p), ("depthwise", _p), ("pointwise", QMat), ("enc", _p), ("enc_norm", _p),
+                ("cross_position", _p), ("embedding", QMat), ("dec", _p), ("dec_norm", _p), ("rope_cos", _p),
+                ("rope_sin", _p)]
+
+
+class WSession(C.Structure):
+    _fields_ = [("keys", _p), ("values", _p), ("mem_k", _p), ("mem_ks", _p), ("mem_v", _p), ("mem_vs", _p),
+                ("hidden", _p), ("capacity", _i), ("length", _i), ("frames", _i)]
+
+
+_WC, _WM, _WS = C.POINTER(WConfig), C.POINTER(WModel), C.POINTER(WSession)
+lib.ro_whistle_frames.restype = _i
+lib.ro_whistle_frames.argtypes = [_WC]
+lib.ro_sigmoid.restype = _f
+lib.ro_sigmoid.argtypes = [_f]
+lib.ro_whistle_position_table.argtypes = [_i, _i, _f, _p]
+lib.ro_whistle_stem.argtypes = [_WC, _WM, _p, _p]
+lib.ro_whistle_encoder_layer.argtypes = [_WC, _WM, _i, _p, _i]
+lib.ro_whistle_encode.argtypes = [_WC, _WM, _p, _p]
+lib.ro_whistle_memory.argtypes = [_WC, _WM, _p, _i, _p, _p, _p, _p]
+lib.ro_int8_attend.argtypes = [_p, _f, _p, _p, _p, _p, _i, _i, _i, _i, _p]
+lib.ro_whistle_push.argtypes = [_WC, _WM, _WS, C.c_uint32]
+lib.ro_whistle_logits.argtypes = [_WC, _WM, _WS, _p]
+lib.ro_whistle_greedy.argtypes = [_WC, _WM, _WS, C.c_uint32, _i, _p]
+
+
+def sigmoid(v: float) -> float:
+    return lib.ro_sigmoid(float(v))
+
+
+def whistle_position_table(frames: int, d: int, gate: float) -> np.ndarray:
+    out = np.empty((frames, d), dtype=np.float32)
+    lib.ro_whistle_position_table(frames, d, float(gate), _ptr(out))
+    return out
+
+
+def int8_attend(qc, query_scale, kc, ks, vc, vs) -> np.ndarray:
+    """One query head: qc [hd] int8; kc, vc [frames][hd] int8; ks, vs [frames]."""
+    qc = np.ascontiguousarray(qc, dtype=np.int8)
+    kc = np.ascontiguousarray(kc, dtype=np.int8)
+    vc = np.ascontiguousarray(vc, dtype=np.int8)
+    ks, vs = _f32(ks), _f32(vs)
+    frames, hd = kc.shape
+    out = np.empty(hd, dtype=np.float32)
+    lib.ro_int8_attend(_ptr(qc), float(query_scale), _ptr(kc), _ptr(ks), _ptr(vc), _ptr(vs), frames, hd, hd, 1,
+                       _ptr(out))
+    return out
+
+
+class OracleWhistle:
+    """The Whistle-style model over the numpy weights of
+    rustyneedle_amd.synthetic_whistle_weights (the same host arrays the GPU model
+    uploads)."""
+
+    def __init__(self, config: dict, weights: dict):
+        self.config = c = dict(config)
+        self.cfg = WConfig(*[c[n] for n in ("mels", "frames", "d_model", "heads", "head_dim", "enc_layers",
+                                            "dec_layers", "ffn", "vocab", "max_positions", "group")],
+                           c["rope_theta"], c["norm_eps"])
+        self.w = weights
+        self.frames = lib.ro_whistle_frames(C.byref(self.cfg))
+        self.rope_cos, self.rope_sin = rotary_table(c["head_dim"], c["rope_theta"],
+                                                    max(self.frames, c["max_positions"]))
+        self.position = whistle_position_table(self.frames, c["d_model"], sigmoid(weights["position_gate"]))
+        qm = lambda pair: QMat(_ptr(pair[0]), _ptr(pair[1]))
+        enc = (WEncLayer * c["enc_layers"])()
+        for l, lw in enumerate(weights["enc"]):
+            enc[l] = WEncLayer(qm(lw["qkv"]), qm(lw["out"]), qm(lw["gate_up"]), qm(lw["down"]), _ptr(lw["norm_attn"]),
+                               _ptr(lw["norm_ffn"]), _ptr(lw["q_norm"]), _ptr(lw["k_norm"]))
+        dec = (WDecLayer * c["dec_layers"])()
+        for l, lw in enumerate(weights["dec"]):
+            dec[l] = WDecLayer(qm(lw["qkv"]), qm(lw["out"]), qm(lw["cross_q"]), qm(lw["cross_kv"]), qm(lw["cross_out"]),
+                               qm(lw["gate_up"]), qm(lw["down"]), _ptr(lw["norm_attn"]), _ptr(lw["norm_cross"]),
+                               _ptr(lw["post_norm"]), _ptr(lw["norm_ffn"]), _ptr(lw["q_norm"]), _ptr(lw["k_norm"]),
+                               sigmoid(lw["gate"]))
+        self._enc, self._dec = enc, dec
+        self.model = WModel(_ptr(weights["conv1"]), _ptr(weights["depthwise"]), qm(weights["pointwise"]),
+                            C.addressof(enc), _ptr(weights["enc_norm"]), _ptr(self.position), qm(weights["embedding"]),
+                            C.addressof(dec), _ptr(weights["dec_norm"]), _ptr(self.rope_cos), _ptr(self.rope_sin))
+
+    def stem(self, mel: np.ndarray) -> np.ndarray:
+        mel = _f32(mel)
+        out = np.empty((self.frames, self.config["d_model"]), dtype=np.float32)
+        lib.ro_whistle_stem(C.byref(self.cfg), C.byref(self.model), _ptr(mel), _ptr(out))
+        return out
+
+    def encoder_layer(self, layer: int, x: np.ndarray) -> np.ndarray:
+        x = _f32(x).copy()
+        lib.ro_whistle_encoder_layer(C.byref(self.cfg), C.byref(self.model), layer, _ptr(x), x.shape[0])
+        return x
+
+    def encode(self, mel: np.ndarray) -> np.ndarray:
+        mel = _f32(mel)
+        out = np.empty((self.frames, self.config["d_model"]), dtype=np.float32)
+        lib.ro_whistle_encode(C.byref(self.cfg), C.byref(self.model), _ptr(mel), _ptr(out))
+        return out
+
+    def memory(self, encoded: np.ndarray):
+        encoded = _f32(encoded)
+        c = self.config
+        T = encoded.shape[0]
+        shape = (c["dec_layers"], T, c["heads"], c["head_dim"])
+        mk, mv = np.empty(shape, np.int8), np.empty(shape, np.int8)
+        ks, vs = np.empty(shape[:3], np.float32), np.empty(shape[:3], np.float32)
+        lib.ro_whistle_memory(C.byref(self.cfg), C.byref(self.model), _ptr(encoded), T, _ptr(mk), _ptr(ks), _ptr(mv),
+                              _ptr(vs))
+        return mk, ks, mv, vs
+
+    def session(self, capacity: int, memory) -> "OracleWhistleSession":
+        return OracleWhistleSession(self, capacity, memory)
+
+
+class OracleWhistleSession:
+    def __init__(self, model: OracleWhistle, capacity: int, memory):
+        c = model.config
+        self.model = model
+        shape = (c["dec_layers"], c["heads"], capacity, c["head_dim"])
+        self.keys = np.zeros(shape, dtype=np.uint16)
+        self.values = np.zeros(shape, dtype=np.uint16)
+        self.hidden = np.zeros(c["d_model"], dtype=np.float32)
+        self.memory = tuple(np.ascontiguousarray(a) for a in memory)
+        mk, ks, mv, vs = self.memory
+        self.s = WSession(_ptr(self.keys), _ptr(self.values), _ptr(mk), _ptr(ks), _ptr(mv), _ptr(vs),
+                          _ptr(self.hidden), capacity, 0, mk.shape[1])
+
+    @property
+    def length(self) -> int:
+        return self.s.length
+
+    def push(self, token: int) -> None:
+        lib.ro_whistle_push(C.byref(self.model.cfg), C.byref(self.model.model), C.byref(self.s), token)
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.model.config["vocab"], dtype=np.float32)
+        lib.ro_whistle_logits(C.byref(self.model.cfg), C.byref(self.model.model), C.byref(self.s), _ptr(out))
+        return out
+
+    def greedy(self, first: int, steps: int) -> np.ndarray:
+        ids = np.empty(steps, dtype=np.uint32)
+        lib.ro_whistle_greedy(C.byref(self.model.cfg), C.byref(self.model.model), C.byref(self.s), first, steps,
+                              _ptr(ids))
+        return ids

@@ -134,6 +134,93 @@ void ro_greedy(const ro_config* c, const ro_model* m, ro_session* s, uint32_t fi
 void ro_set_threads(int threads);
 int ro_get_threads(void);
 
+/* ---- Whistle-style speech path (rn_whistle.c) ---------------------------------
+ * crates/whistle: stem (stem.rs), encoder (encoder.rs), cross-attention
+ * memory and apply (cross.rs), and the decoder step with the cross hook
+ * (session.rs:76-148). The synthetic configuration keeps one residual stream
+ * and a gated FFN, like the decoder above: stem = fp32 conv (k3, s1, pad 1)
+ * + silu, then one stage of fp32 depthwise conv (k3, s2, pad 1) and an int8
+ * pointwise product, + silu; encoder layer = x += out(int8 attention over all
+ * frames of norm(x)), x += down(silu(gate) * up) of norm(x); final norm. */
+typedef struct {
+    int mels, frames, d_model, heads, head_dim, enc_layers, dec_layers, ffn, vocab, max_positions, group;
+    float rope_theta, norm_eps;
+} ro_wconfig;
+
+typedef struct {
+    ro_qmat qkv, out, gate_up, down;
+    const float *norm_attn, *norm_ffn;
+    const float *q_norm, *k_norm; /* [head_dim] per-head gains */
+} ro_wenc_layer;
+
+typedef struct {
+    ro_qmat qkv, out;           /* self-attention */
+    ro_qmat cross_q;            /* [d][d] */
+    ro_qmat cross_kv;           /* [2d][d]: key rows, then value rows, of the memory */
+    ro_qmat cross_out;          /* [d][d] */
+    ro_qmat gate_up, down;
+    const float *norm_attn, *norm_cross, *post_norm, *norm_ffn;
+    const float *q_norm, *k_norm; /* [head_dim] cross-attention head gains */
+    float cross_gain;           /* sigmoid(layer gate), cross.rs:176-180 */
+} ro_wdec_layer;
+
+typedef struct {
+    const float* conv1;          /* [d][3][mels] */
+    const float* depthwise;      /* [3][d] */
+    ro_qmat pointwise;           /* [d][d] */
+    const ro_wenc_layer* enc;
+    const float* enc_norm;       /* [d] */
+    const float* cross_position; /* [encoder frames][d]: sigmoid(gate) * sinusoid (cross.rs:62-72) */
+    ro_qmat embedding;           /* [vocab][d], tied */
+    const ro_wdec_layer* dec;
+    const float* dec_norm;       /* [d] */
+    const float* rope_cos;       /* [max(encoder frames, max_positions)][head_dim/2] */
+    const float* rope_sin;
+} ro_wmodel;
+
+/* Cross memory [dec_layers][frames][heads][head_dim] int8 codes with
+ * [dec_layers][frames][heads] scales; the self-attention cache as ro_session. */
+typedef struct {
+    uint16_t* keys;
+    uint16_t* values;
+    const int8_t* mem_k;
+    const float* mem_ks;
+    const int8_t* mem_v;
+    const float* mem_vs;
+    float* hidden;
+    int capacity, length, frames;
+} ro_wsession;
+
+int ro_whistle_frames(const ro_wconfig* c); /* (frames - 1) / 2 + 1 (stem.rs:23-25) */
+/* ops.rs:68-71 with the platform expf. */
+float ro_sigmoid(float value);
+/* cross.rs:62-72: gate * sin / cos of t * exp(rate * j) for frames 0..T-1, the
+ * sines in columns 0..d/2-1 and the cosines in d/2..d-1, rate = -ln(10000)/(d/2 - 1). */
+void ro_whistle_position_table(int T, int d, float gate, float* out);
+/* Stem::forward for the synthetic stem: mel [frames][mels] -> out [T][d]. */
+void ro_whistle_stem(const ro_wconfig* c, const ro_wmodel* m, const float* mel, float* out);
+/* One encoder layer over x [T][d] in place. */
+void ro_whistle_encoder_layer(const ro_wconfig* c, const ro_wmodel* m, int layer, float* x, int T);
+/* Whistle::encode: stem, the encoder layers, the final norm -> out [T][d]. */
+void ro_whistle_encode(const ro_wconfig* c, const ro_wmodel* m, const float* mel, float* out);
+/* CrossWeights::memory (cross.rs:62-99): per decoder layer, keys and values of
+ * the encoded frames (position added, quantised per row, key head norm) as int8
+ * codes per (frame, head) with their scales. */
+void ro_whistle_memory(const ro_wconfig* c, const ro_wmodel* m, const float* encoded, int T, int8_t* mem_k,
+                       float* mem_ks, int8_t* mem_v, float* mem_vs);
+/* One query head against `frames` int8 key/value rows (encoder.rs:232-258,
+ * cross.rs:147-170): scores ((float)dot * key_scale) * query_scale, fast_exp
+ * softmax with the totals in tree T3, weights times value scales, value codes
+ * summed in tree T3. Row j of keys/values starts at j * row_stride, its scales
+ * at j * scale_stride. */
+void ro_int8_attend(const int8_t* qc, float query_scale, const int8_t* kc, const float* ks, const int8_t* vc,
+                    const float* vs, int frames, int head_dim, int row_stride, int scale_stride, float* out);
+/* Session::push_with with the cross hook (session.rs:76-148, cross.rs:127-182). */
+void ro_whistle_push(const ro_wconfig* c, const ro_wmodel* m, ro_wsession* s, uint32_t token);
+void ro_whistle_logits(const ro_wconfig* c, const ro_wmodel* m, const ro_wsession* s, float* logits);
+void ro_whistle_greedy(const ro_wconfig* c, const ro_wmodel* m, ro_wsession* s, uint32_t first, int steps,
+                       uint32_t* ids);
+
 #ifdef __cplusplus
 }
 #endif

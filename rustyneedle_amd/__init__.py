@@ -35,6 +35,11 @@ PROFILE_KINDS = ("qkv", "attention", "out", "gate_up", "down", "logits", "final"
 # int8 codes with one fp32 scale per 32 columns, tied int8 vocab 8192.
 NEEDLE_DECODER = dict(layers=20, d_model=512, heads=8, head_dim=64, ffn=2048, vocab=8192, group=32,
                       max_positions=1024, rope_theta=10000.0, norm_eps=1e-6)
+# The Whistle-style speech path: 80-bin log-mel input of 3000 frames, stem to
+# d_model 384 over 1500 frames, 6 encoder layers, 4 decoder layers with
+# cross-attention over the encoded frames, tied int8 vocab 8192.
+WHISTLE = dict(mels=80, frames=3000, d_model=384, heads=6, head_dim=64, enc_layers=6, dec_layers=4, ffn=1536,
+               vocab=8192, max_positions=64, group=32, rope_theta=10000.0, norm_eps=1e-6)
 SEED = 20261201
 
 
@@ -414,6 +419,49 @@ def synthetic_weights(config: dict, seed: int = SEED) -> dict:
                            norm_ffn=synth_normal(seed, p + "norm_ffn", 0.1, (d,))))
     return dict(layers=layers, embedding=q("embedding", vocab, d),
                 norm_final=synth_normal(seed, "norm_final", 0.1, (d,)))
+
+
+def synthetic_whistle_weights(config: dict, seed: int = SEED) -> dict:
+    """The tensors rn_whistle_create_synthetic draws, by the same names: codes
+    U{-127..127}, scales U[1e-3, 1e-2], gains N(0, 0.1), the fp32 stem weights
+    N(0, 1/sqrt(fan-in)), the position and layer gates N(0, 1)."""
+    d, f, hd, M, V = config["d_model"], config["ffn"], config["head_dim"], config["mels"], config["vocab"]
+
+    def q(name, rows, cols):
+        return (synth_codes(seed, name + ".codes", (rows, cols)),
+                synth_uniform(seed, name + ".scales", 1e-3, 1e-2, (rows, cols // 32)))
+
+    def g(name, n):
+        return synth_normal(seed, name, 0.1, (n,))
+
+    enc = []
+    for l in range(config["enc_layers"]):
+        p = f"whistle.enc.{l}."
+        enc.append(dict(qkv=q(p + "qkv", 3 * d, d), out=q(p + "out", d, d), gate_up=q(p + "gate_up", 2 * f, d),
+                        down=q(p + "down", d, f), norm_attn=g(p + "norm_attn", d), norm_ffn=g(p + "norm_ffn", d),
+                        q_norm=g(p + "q_norm", hd), k_norm=g(p + "k_norm", hd)))
+    dec = []
+    for l in range(config["dec_layers"]):
+        p = f"whistle.dec.{l}."
+        dec.append(dict(qkv=q(p + "qkv", 3 * d, d), out=q(p + "out", d, d), cross_q=q(p + "cross_q", d, d),
+                        cross_kv=q(p + "cross_kv", 2 * d, d), cross_out=q(p + "cross_out", d, d),
+                        gate_up=q(p + "gate_up", 2 * f, d), down=q(p + "down", d, f),
+                        norm_attn=g(p + "norm_attn", d), norm_cross=g(p + "norm_cross", d),
+                        post_norm=g(p + "post_norm", d), norm_ffn=g(p + "norm_ffn", d),
+                        q_norm=g(p + "q_norm", hd), k_norm=g(p + "k_norm", hd),
+                        gate=float(synth_normal(seed, p + "gate", 1.0, (1,))[0])))
+    conv_sigma = float(np.float32(1.0) / np.sqrt(np.float32(3 * M)))
+    dw_sigma = float(np.float32(1.0) / np.sqrt(np.float32(3)))
+    return dict(conv1=synth_normal(seed, "whistle.conv1", conv_sigma, (d, 3, M)),
+                depthwise=synth_normal(seed, "whistle.depthwise", dw_sigma, (3, d)),
+                pointwise=q("whistle.pointwise", d, d), enc=enc, enc_norm=g("whistle.enc_norm", d),
+                position_gate=float(synth_normal(seed, "whistle.position_gate", 1.0, (1,))[0]),
+                embedding=q("whistle.embedding", V, d), dec=dec, dec_norm=g("whistle.dec_norm", d))
+
+
+def synthetic_mel(config: dict, name: str = "whistle.mel", seed: int = SEED) -> np.ndarray:
+    """N(0, 1) log-mel input [frames][mels]."""
+    return synth_normal(seed, name, 1.0, (config["frames"], config["mels"]))
 
 
 def synthetic_cache(config: dict, length: int, name: str, seed: int = SEED):
