@@ -75,8 +75,7 @@ typedef struct rn_matrix rn_matrix;
 
 /* Replaces QuantisedMatrix::from_archive/from_parts (matrix.rs:35-59): host codes
  * [rows][columns] int8 and scales [rows][columns/group] f32 are copied to the
- * device. columns must be a multiple of 1024 or divide 1024 evenly with
- * columns >= 512; group must be 32. */
+ * device. columns must be 384, 512, 1024, 1536 or 2048; group must be 32. */
 int rn_matrix_create_i8(const int8_t* codes, const float* scales, int rows, int columns, int group,
                         int form, rn_matrix** out);
 int rn_matrix_free(rn_matrix* m);
@@ -228,6 +227,53 @@ int rn_batch_decode_greedy(rn_batch* batch, const uint32_t* first, int steps, ui
 /* Per-sequence rn_session_truncate: lengths [count], each <= its current length. */
 int rn_batch_truncate(rn_batch* batch, const int32_t* lengths);
 int rn_batch_stream(const rn_batch* batch, void** stream);
+
+/* ---- Whistle-style speech path (crates/whistle) -------------------------------- */
+/* The synthetic configuration: a stem (fp32 conv kernel 3 stride 1 + silu, then
+ * an fp32 depthwise conv kernel 3 stride 2 and an int8 pointwise product +
+ * silu; stem.rs:39-115) to (frames - 1) / 2 + 1 encoder frames; encoder layers
+ * of int8 self-attention (encoder.rs:217-297) and a gated FFN; a decoder of
+ * the Session kind with cross-attention after each self-attention
+ * (session.rs:126-128, cross.rs:126-182); tied int8 logits. d_model 384 or
+ * 512 with heads of 64, ffn in {512, 1024, 1536, 2048}, mels <= 128. */
+typedef struct {
+    int mels, frames, d_model, heads, head_dim, enc_layers, dec_layers, ffn, vocab, max_positions, group;
+    float rope_theta, norm_eps;
+} rn_whistle_config;
+typedef struct rn_whistle rn_whistle;
+
+/* Whistle::open (lib.rs:101-140) with seeded synthetic weights drawn by name
+ * (the same draws as rn_synth_*): the model, its work buffers and one decoder
+ * session of max_positions positions, on their own stream. */
+int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, rn_whistle** out);
+int rn_whistle_free(rn_whistle* whistle);
+/* Encoder frames (frames - 1) / 2 + 1 (stem.rs:23-25). */
+int rn_whistle_frames(const rn_whistle* whistle, int* frames);
+/* The host-computed tables: the cross position term [frames][d_model]
+ * (cross.rs:61-72) and the per-decoder-layer cross gains sigmoid(gate)
+ * (cross.rs:178); both nullable. */
+int rn_whistle_tables(const rn_whistle* whistle, float* position, float* cross_gains);
+/* Stem::forward (stem.rs:39-115) alone: mel [frames][mels] -> out [T][d]. */
+int rn_whistle_stem(rn_whistle* whistle, const float* mel, float* out);
+/* Whistle::encode (lib.rs:155-161) then CrossWeights::memory (cross.rs:58-99):
+ * the encoded frames and every decoder layer's int8 key/value memory stay on
+ * the device; `encoded` (nullable) receives [T][d]. Resets the decoder. */
+int rn_whistle_encode(rn_whistle* whistle, const float* mel, float* encoded);
+/* The cross memory of the last encode: keys/values [dec_layers][T][heads][64]
+ * int8, scales [dec_layers][T][heads]. */
+int rn_whistle_memory(const rn_whistle* whistle, int8_t* keys, float* key_scales, int8_t* values,
+                      float* value_scales);
+/* Session::new for the decoder (an empty self-attention cache). */
+int rn_whistle_reset(rn_whistle* whistle);
+/* Session::push_with(token, Some(cross)) (session.rs:76-148). */
+int rn_whistle_push(rn_whistle* whistle, uint32_t token);
+/* Session::logits (session.rs:166-177) after the last push (host out, vocab). */
+int rn_whistle_logits(rn_whistle* whistle, float* out);
+/* The decode loop of Whistle::decode (lib.rs:240-295) without language,
+ * keywords or timestamps: token = first; `steps` times { push; token =
+ * argmax(logits); ids[i] = token }, the argmax on the device. */
+int rn_whistle_decode_greedy(rn_whistle* whistle, uint32_t first, int steps, uint32_t* ids);
+int rn_whistle_stream(const rn_whistle* whistle, void** stream);
 
 /* ---- seeded synthetic inputs (host memory; no reference counterpart) ---------- */
 /* SplitMix64 stream per tensor: state0 = seed ^ FNV-1a-64(name). */

@@ -161,7 +161,7 @@ typedef struct {
     ro_qmat gate_up, down;
     const float *norm_attn, *norm_cross, *post_norm, *norm_ffn;
     const float *q_norm, *k_norm; /* [head_dim] cross-attention head gains */
-    float cross_gain;           /* sigmoid(layer gate), cross.rs:176-180 */
+    float cross_gain;           /* sigmoid(layer gate), cross.rs:178 */
 } ro_wdec_layer;
 
 typedef struct {
@@ -170,7 +170,7 @@ typedef struct {
     ro_qmat pointwise;           /* [d][d] */
     const ro_wenc_layer* enc;
     const float* enc_norm;       /* [d] */
-    const float* cross_position; /* [encoder frames][d]: sigmoid(gate) * sinusoid (cross.rs:62-72) */
+    const float* cross_position; /* [encoder frames][d]: sigmoid(gate) * sinusoid (cross.rs:61-72) */
     ro_qmat embedding;           /* [vocab][d], tied */
     const ro_wdec_layer* dec;
     const float* dec_norm;       /* [d] */
@@ -191,10 +191,10 @@ typedef struct {
     int capacity, length, frames;
 } ro_wsession;
 
-int ro_whistle_frames(const ro_wconfig* c); /* (frames - 1) / 2 + 1 (stem.rs:23-25) */
+int ro_whistle_frames(const ro_wconfig* c); /* (frames - 1) / 2 + 1 (stem.rs:21-23) */
 /* ops.rs:68-71 with the platform expf. */
 float ro_sigmoid(float value);
-/* cross.rs:62-72: gate * sin / cos of t * exp(rate * j) for frames 0..T-1, the
+/* cross.rs:61-72: gate * sin / cos of t * exp(rate * j) for frames 0..T-1, the
  * sines in columns 0..d/2-1 and the cosines in d/2..d-1, rate = -ln(10000)/(d/2 - 1). */
 void ro_whistle_position_table(int T, int d, float gate, float* out);
 /* Stem::forward for the synthetic stem: mel [frames][mels] -> out [T][d]. */
@@ -203,19 +203,19 @@ void ro_whistle_stem(const ro_wconfig* c, const ro_wmodel* m, const float* mel, 
 void ro_whistle_encoder_layer(const ro_wconfig* c, const ro_wmodel* m, int layer, float* x, int T);
 /* Whistle::encode: stem, the encoder layers, the final norm -> out [T][d]. */
 void ro_whistle_encode(const ro_wconfig* c, const ro_wmodel* m, const float* mel, float* out);
-/* CrossWeights::memory (cross.rs:62-99): per decoder layer, keys and values of
+/* CrossWeights::memory (cross.rs:58-99): per decoder layer, keys and values of
  * the encoded frames (position added, quantised per row, key head norm) as int8
  * codes per (frame, head) with their scales. */
 void ro_whistle_memory(const ro_wconfig* c, const ro_wmodel* m, const float* encoded, int T, int8_t* mem_k,
                        float* mem_ks, int8_t* mem_v, float* mem_vs);
-/* One query head against `frames` int8 key/value rows (encoder.rs:232-258,
+/* One query head against `frames` int8 key/value rows (encoder.rs:266-285,
  * cross.rs:147-170): scores ((float)dot * key_scale) * query_scale, fast_exp
  * softmax with the totals in tree T3, weights times value scales, value codes
  * summed in tree T3. Row j of keys/values starts at j * row_stride, its scales
  * at j * scale_stride. */
 void ro_int8_attend(const int8_t* qc, float query_scale, const int8_t* kc, const float* ks, const int8_t* vc,
                     const float* vs, int frames, int head_dim, int row_stride, int scale_stride, float* out);
-/* Session::push_with with the cross hook (session.rs:76-148, cross.rs:127-182). */
+/* Session::push_with with the cross hook (session.rs:76-148, cross.rs:126-182). */
 void ro_whistle_push(const ro_wconfig* c, const ro_wmodel* m, ro_wsession* s, uint32_t token);
 void ro_whistle_logits(const ro_wconfig* c, const ro_wmodel* m, const ro_wsession* s, float* logits);
 void ro_whistle_greedy(const ro_wconfig* c, const ro_wmodel* m, ro_wsession* s, uint32_t first, int steps,

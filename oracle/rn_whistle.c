@@ -32,7 +32,7 @@ void ro_whistle_position_table(int T, int d, float gate, float* out) {
         }
 }
 
-/* stem.rs:36-58 and 59-96 for one dimension of time: the first convolution
+/* stem.rs:39-115 for one dimension of time: the first convolution
  * adds taps (k, m) in that order into a zero output, then silu; the stage's
  * depthwise convolution adds its three taps in order per channel; the
  * pointwise product quantises each position per row; silu closes the stem. */
@@ -72,7 +72,7 @@ void ro_whistle_stem(const ro_wconfig* c, const ro_wmodel* m, const float* mel, 
     free(h1);
 }
 
-/* Per-head preparation (encoder.rs:218-243, cross.rs:86-97 and 151-156): the
+/* Per-head preparation (encoder.rs:226-263, cross.rs:86-97 and 149-156): the
  * zero-centred norm with the head gains (when given), the rotary at the
  * frame's position (when given), then quantise_int8. Returns the scale. */
 static float head_codes(float* h, int hd, const float* gain, const float* cos_row, const float* sin_row,
@@ -107,7 +107,7 @@ void ro_int8_attend(const int8_t* qc, float query_scale, const int8_t* kc, const
     float total = 0.0f;
     for (int cl = 0; cl < RO_CLASSES; ++cl) total = total + part[cl];
     float inverse = 1.0f / total;
-    /* ops.rs:99-100 weights, then encoder.rs:250-256 scale = value_scale * weight */
+    /* ops.rs:99-100 weights, then encoder.rs:281 scale = value_scale * weight */
     for (int j = 0; j < frames; ++j) e[j] = vs[(size_t)j * scale_stride] * (e[j] * inverse);
     float* acc = (float*)calloc((size_t)RO_CLASSES * head_dim, sizeof(float));
     for (int j = 0; j < frames; ++j) {
@@ -140,7 +140,7 @@ static void gated_ffn(const ro_wconfig* c, ro_qmat gate_up, ro_qmat down, const 
     free(normed);
 }
 
-/* encoder.rs:204-262 for the synthetic layer: norm, fused q/k/v product, per
+/* encoder.rs:145-297 for the synthetic layer: norm, fused q/k/v product, per
  * head (q_norm | k_norm) + rotary at the frame position + int8 codes, values
  * quantised per head, attention of every frame over all frames, out product
  * + residual; then the gated FFN + residual. */
@@ -228,7 +228,7 @@ static size_t wcache_offset(const ro_wconfig* c, const ro_wsession* s, int layer
     return (((size_t)layer * c->heads + head) * (size_t)s->capacity + (size_t)pos) * (size_t)c->head_dim;
 }
 
-/* CrossState::apply (cross.rs:127-182) without the gate projection: norm,
+/* CrossState::apply (cross.rs:126-182) without the gate projection: norm,
  * q product, per head q_norm + int8 codes, int8 attention over the memory,
  * out product, post norm, x += gain * attended. */
 static void cross_apply(const ro_wconfig* c, const ro_wmodel* m, const ro_wsession* s, int layer, float* x) {

@@ -73,6 +73,11 @@ class WeightsHost(C.Structure):
     _fields_ = [("embedding", QMatHost), ("norm_final", _p), ("layers", _p)]
 
 
+class WhistleConfig(C.Structure):
+    _fields_ = [(n, _i) for n in ("mels", "frames", "d_model", "heads", "head_dim", "enc_layers", "dec_layers", "ffn",
+                                  "vocab", "max_positions", "group")] + [("rope_theta", _f), ("norm_eps", _f)]
+
+
 # Every symbol of include/rustyneedle.h with its signature (restype int unless noted).
 SIGNATURES = {
     "rn_last_error": (C.c_char_p, []),
@@ -128,6 +133,18 @@ SIGNATURES = {
     "rn_batch_decode_greedy": (_i, [_p, _p, _i, _p]),
     "rn_batch_stream": (_i, [_p, C.POINTER(_p)]),
     "rn_batch_truncate": (_i, [_p, _p]),
+    "rn_whistle_create_synthetic": (_i, [C.POINTER(WhistleConfig), _u64, C.POINTER(_p)]),
+    "rn_whistle_free": (_i, [_p]),
+    "rn_whistle_frames": (_i, [_p, C.POINTER(_i)]),
+    "rn_whistle_tables": (_i, [_p, _p, _p]),
+    "rn_whistle_stem": (_i, [_p, _p, _p]),
+    "rn_whistle_encode": (_i, [_p, _p, _p]),
+    "rn_whistle_memory": (_i, [_p, _p, _p, _p, _p]),
+    "rn_whistle_reset": (_i, [_p]),
+    "rn_whistle_push": (_i, [_p, _u32]),
+    "rn_whistle_logits": (_i, [_p, _p]),
+    "rn_whistle_decode_greedy": (_i, [_p, _u32, _i, _p]),
+    "rn_whistle_stream": (_i, [_p, C.POINTER(_p)]),
     "rn_synth_codes": (_i, [_u64, C.c_char_p, _p, _sz]),
     "rn_synth_uniform": (_i, [_u64, C.c_char_p, _f, _f, _p, _sz]),
     "rn_synth_normal": (_i, [_u64, C.c_char_p, _f, _p, _sz]),
@@ -641,5 +658,81 @@ class Batch:
         try:
             if self.handle:
                 lib.rn_batch_free(self.handle)
+        except Exception:
+            pass
+
+
+# ---- Whistle-style speech path ---------------------------------------------------
+
+class Whistle:
+    """crates/whistle Whistle (lib.rs:77-312) for the synthetic configuration: the
+    model, its encoder work buffers and one decoder session on the device."""
+
+    def __init__(self, config: dict, seed: int = SEED):
+        self.config = c = dict(config)
+        self._cfg = WhistleConfig(*[c[n] for n in ("mels", "frames", "d_model", "heads", "head_dim", "enc_layers",
+                                                   "dec_layers", "ffn", "vocab", "max_positions", "group")],
+                                  c["rope_theta"], c["norm_eps"])
+        h = _p()
+        check(lib.rn_whistle_create_synthetic(C.byref(self._cfg), seed, C.byref(h)))
+        self.handle = h.value
+        n = _i()
+        check(lib.rn_whistle_frames(self.handle, C.byref(n)))
+        self.frames = n.value
+
+    def tables(self):
+        pos = np.empty((self.frames, self.config["d_model"]), np.float32)
+        gains = np.empty(self.config["dec_layers"], np.float32)
+        check(lib.rn_whistle_tables(self.handle, _ptr(pos), _ptr(gains)))
+        return pos, gains
+
+    def stem(self, mel: np.ndarray) -> np.ndarray:
+        mel = np.ascontiguousarray(mel, dtype=np.float32)
+        assert mel.shape == (self.config["frames"], self.config["mels"])
+        out = np.empty((self.frames, self.config["d_model"]), np.float32)
+        check(lib.rn_whistle_stem(self.handle, _ptr(mel), _ptr(out)))
+        return out
+
+    def encode(self, mel: np.ndarray, copy_out: bool = True):
+        mel = np.ascontiguousarray(mel, dtype=np.float32)
+        assert mel.shape == (self.config["frames"], self.config["mels"])
+        out = np.empty((self.frames, self.config["d_model"]), np.float32) if copy_out else None
+        check(lib.rn_whistle_encode(self.handle, _ptr(mel), _ptr(out) if copy_out else None))
+        return out
+
+    def memory(self):
+        c = self.config
+        shape = (c["dec_layers"], self.frames, c["heads"], c["head_dim"])
+        mk, mv = np.empty(shape, np.int8), np.empty(shape, np.int8)
+        ks, vs = np.empty(shape[:3], np.float32), np.empty(shape[:3], np.float32)
+        check(lib.rn_whistle_memory(self.handle, _ptr(mk), _ptr(ks), _ptr(mv), _ptr(vs)))
+        return mk, ks, mv, vs
+
+    def reset(self) -> None:
+        check(lib.rn_whistle_reset(self.handle))
+
+    def push(self, token: int) -> None:
+        check(lib.rn_whistle_push(self.handle, int(token)))
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.config["vocab"], np.float32)
+        check(lib.rn_whistle_logits(self.handle, _ptr(out)))
+        return out
+
+    def decode_greedy(self, first: int, steps: int) -> np.ndarray:
+        ids = np.empty(steps, np.uint32)
+        check(lib.rn_whistle_decode_greedy(self.handle, int(first), int(steps), _ptr(ids)))
+        return ids
+
+    def stream(self) -> int:
+        s = _p()
+        check(lib.rn_whistle_stream(self.handle, C.byref(s)))
+        return s.value
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", None):
+                lib.rn_whistle_free(self.handle)
+                self.handle = None
         except Exception:
             pass

@@ -19,6 +19,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <new>
 #include <string>
 #include <vector>
@@ -76,7 +77,9 @@ struct LayerDev {
     float* norm_ffn = nullptr;
 };
 
-int check_supported(int columns) { return columns == 512 || columns == 1024 || columns == 2048; }
+int check_supported(int columns) {
+    return columns == 384 || columns == 512 || columns == 1024 || columns == 1536 || columns == 2048;
+}
 
 }  // namespace
 
@@ -220,7 +223,7 @@ int rn_matrix_create_i8(const int8_t* codes, const float* scales, int rows, int 
     RN_REQUIRE(codes && scales && out, "null argument");
     RN_REQUIRE(rows > 0, "rows must be positive (got %d)", rows);
     RN_REQUIRE(group == kGroup, "group must be 32 (got %d)", group);
-    RN_REQUIRE(check_supported(columns), "columns must be 512, 1024 or 2048 (got %d)", columns);
+    RN_REQUIRE(check_supported(columns), "columns must be 384, 512, 1024, 1536 or 2048 (got %d)", columns);
     RN_REQUIRE(form == RN_FORM_PANEL || form == RN_FORM_PLANE, "unknown form %d", form);
     rn_matrix* m = new (std::nothrow) rn_matrix();
     if (!m) return fail(RN_ERR_MEMORY, "out of host memory");
@@ -392,7 +395,7 @@ static int validate_config(const rn_config* c) {
     RN_REQUIRE(c->d_model == 512, "d_model must be 512 (got %d)", c->d_model);
     RN_REQUIRE(c->head_dim == 64, "head_dim must be 64 (got %d)", c->head_dim);
     RN_REQUIRE(c->heads * c->head_dim == c->d_model, "heads * head_dim must equal d_model");
-    RN_REQUIRE(check_supported(c->ffn), "ffn must be 512, 1024 or 2048 (got %d)", c->ffn);
+    RN_REQUIRE(c->ffn == 512 || c->ffn == 1024 || c->ffn == 2048, "ffn must be 512, 1024 or 2048 (got %d)", c->ffn);
     RN_REQUIRE(c->group == kGroup, "group must be 32 (got %d)", c->group);
     RN_REQUIRE(c->layers >= 1 && c->layers <= 256, "layers must be 1..256 (got %d)", c->layers);
     RN_REQUIRE(c->vocab >= 1, "vocab must be positive");
@@ -1176,6 +1179,657 @@ int rn_batch_decode_greedy(rn_batch* b, const uint32_t* first, int steps, uint32
     for (int i = 0; i < b->count; ++i) b->lengths[i] += steps;
     if (err) return fail(RN_ERR_STATE, "device reported error flags 0x%x", err);
     return RN_OK;
+}
+
+// ---- Whistle-style speech path --------------------------------------------------
+
+}  // extern "C"
+
+namespace {
+
+struct WEncLayerDev {
+    DevMatrix qkv, out, gate_up, down;
+    float *norm_attn = nullptr, *norm_ffn = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+struct WDecLayerDev {
+    DevMatrix qkv, out, cross_q, cross_kv, cross_out, gate_up, down;
+    float *norm_attn = nullptr, *norm_cross = nullptr, *post_norm = nullptr, *norm_ffn = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr;
+    float cross_gain = 0.0f;
+};
+
+// cross.rs:61-72 for frames 0..T-1 (host libm, as the CPU restatement).
+void whistle_position(int T, int d, float gate, std::vector<float>& out) {
+    const int half = d / 2;
+    const float rate = -logf(10000.0f) / ((float)half - 1.0f);
+    out.assign((size_t)T * d, 0.0f);
+    for (int t = 0; t < T; ++t)
+        for (int j = 0; j < half; ++j) {
+            const float angle = (float)t * expf(rate * (float)j);
+            out[(size_t)t * d + j] = gate * sinf(angle);
+            out[(size_t)t * d + half + j] = gate * cosf(angle);
+        }
+}
+
+float host_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }  // ops.rs:68-71
+
+}  // namespace
+
+struct rn_whistle {
+    rn_whistle_config cfg{};
+    int T = 0;  // encoder frames
+    hipStream_t stream = nullptr;
+    void* arena = nullptr;
+    float* conv1 = nullptr;
+    float* depthwise = nullptr;
+    DevMatrix pointwise;
+    std::vector<WEncLayerDev> enc;
+    float* enc_norm = nullptr;
+    float* position = nullptr;
+    DevMatrix embedding;
+    std::vector<WDecLayerDev> dec;
+    float* dec_norm = nullptr;
+    float* rope_cos = nullptr;
+    float* rope_sin = nullptr;
+    std::vector<float> position_host, gains_host;
+    float embed_scale = 0.0f;
+    // encoder work
+    float *mel = nullptr, *h1 = nullptr, *R = nullptr, *X = nullptr, *Y = nullptr, *F = nullptr, *ctx = nullptr;
+    float* encoded = nullptr;
+    int8_t* Xq = nullptr;
+    float* sx = nullptr;
+    int8_t *qc = nullptr, *kc = nullptr, *vc = nullptr;
+    float *qs = nullptr, *ks = nullptr, *vs = nullptr;
+    // cross memory [dec_layers][T][heads][64] and scales [dec_layers][T][heads]
+    int8_t *mem_k = nullptr, *mem_v = nullptr;
+    float *mem_ks = nullptr, *mem_vs = nullptr;
+    bool encoded_ready = false;
+    // the decoder session
+    __half *kcache = nullptr, *vcache = nullptr;
+    int capacity = 0, length = 0;
+    bool has_hidden = false;
+    float *x = nullptr, *qkv = nullptr, *attn = nullptr, *cq = nullptr, *cctx = nullptr, *catt = nullptr;
+    float *ffh = nullptr, *hidden = nullptr, *logits = nullptr;
+    int8_t* cqc = nullptr;
+    float* cqs = nullptr;
+    DecodeState* state = nullptr;
+    uint32_t* ids = nullptr;
+    unsigned long long* keys = nullptr;
+};
+
+extern "C" {
+
+static int validate_whistle(const rn_whistle_config* c) {
+    RN_REQUIRE(c, "config is null");
+    RN_REQUIRE(c->d_model == 384 || c->d_model == 512, "d_model must be 384 or 512 (got %d)", c->d_model);
+    RN_REQUIRE(c->head_dim == 64 && c->heads * 64 == c->d_model, "heads of 64 must tile d_model");
+    RN_REQUIRE(c->ffn == 512 || c->ffn == 1024 || c->ffn == 1536 || c->ffn == 2048, "ffn must be 512, 1024, 1536 or 2048");
+    RN_REQUIRE(c->group == kGroup, "group must be 32");
+    RN_REQUIRE(c->mels >= 1 && c->mels <= 128, "mels must be 1..128");
+    RN_REQUIRE(c->frames >= 2 && c->frames <= 65536, "frames must be 2..65536");
+    RN_REQUIRE(c->enc_layers >= 1 && c->enc_layers <= 64 && c->dec_layers >= 1 && c->dec_layers <= 64,
+               "layers must be 1..64");
+    RN_REQUIRE(c->vocab >= 1 && c->max_positions >= 1 && c->max_positions <= 16384, "vocab / max_positions");
+    RN_REQUIRE(c->norm_eps == 1e-6f, "norm_eps must be 1e-6 (the reference's NORM_EPSILON)");
+    return RN_OK;
+}
+
+int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, rn_whistle** out) {
+    int rc = validate_whistle(config);
+    if (rc) return rc;
+    RN_REQUIRE(out, "out is null");
+    const rn_whistle_config& c = *config;
+    const size_t d = c.d_model, f = c.ffn, H = c.heads, M = c.mels, Fr = c.frames, V = c.vocab;
+    const size_t T = (size_t)(c.frames - 1) / 2 + 1;
+    RN_REQUIRE(T * 4 <= 128 * 1024, "too many encoder frames for the attention's score buffer");
+    rn_whistle* w = new (std::nothrow) rn_whistle();
+    if (!w) return fail(RN_ERR_MEMORY, "out of host memory");
+    w->cfg = c;
+    w->T = (int)T;
+    w->embed_scale = sqrtf((float)d);
+    w->capacity = c.max_positions;
+
+    // host draws, by name (the same as rustyneedle_amd.synthetic_whistle_weights)
+    struct Q {
+        std::vector<int8_t> codes;
+        std::vector<float> scales;
+    };
+    auto gen_q = [&](const std::string& name, size_t rows, size_t cols) {
+        Q q;
+        q.codes.resize(rows * cols);
+        q.scales.resize(rows * (cols / kGroup));
+        rn_synth_codes(seed, (name + ".codes").c_str(), q.codes.data(), q.codes.size());
+        rn_synth_uniform(seed, (name + ".scales").c_str(), 1e-3f, 1e-2f, q.scales.data(), q.scales.size());
+        return q;
+    };
+    auto gen_normal = [&](const std::string& name, float sigma, size_t n) {
+        std::vector<float> g(n);
+        rn_synth_normal(seed, name.c_str(), sigma, g.data(), n);
+        return g;
+    };
+    std::vector<float> conv1 = gen_normal("whistle.conv1", 1.0f / sqrtf((float)(3 * M)), d * 3 * M);
+    std::vector<float> depthwise = gen_normal("whistle.depthwise", 1.0f / sqrtf(3.0f), 3 * d);
+    Q pointwise = gen_q("whistle.pointwise", d, d);
+    struct EncHost { Q qkv, out, gate_up, down; std::vector<float> norm_attn, norm_ffn, q_norm, k_norm; };
+    struct DecHost {
+        Q qkv, out, cross_q, cross_kv, cross_out, gate_up, down;
+        std::vector<float> norm_attn, norm_cross, post_norm, norm_ffn, q_norm, k_norm;
+        float gate;
+    };
+    std::vector<EncHost> eh(c.enc_layers);
+    for (int l = 0; l < c.enc_layers; ++l) {
+        const std::string p = "whistle.enc." + std::to_string(l) + ".";
+        eh[l].qkv = gen_q(p + "qkv", 3 * d, d);
+        eh[l].out = gen_q(p + "out", d, d);
+        eh[l].gate_up = gen_q(p + "gate_up", 2 * f, d);
+        eh[l].down = gen_q(p + "down", d, f);
+        eh[l].norm_attn = gen_normal(p + "norm_attn", 0.1f, d);
+        eh[l].norm_ffn = gen_normal(p + "norm_ffn", 0.1f, d);
+        eh[l].q_norm = gen_normal(p + "q_norm", 0.1f, 64);
+        eh[l].k_norm = gen_normal(p + "k_norm", 0.1f, 64);
+    }
+    std::vector<float> enc_norm = gen_normal("whistle.enc_norm", 0.1f, d);
+    const float position_gate = gen_normal("whistle.position_gate", 1.0f, 1)[0];
+    Q embedding = gen_q("whistle.embedding", V, d);
+    std::vector<DecHost> dh(c.dec_layers);
+    for (int l = 0; l < c.dec_layers; ++l) {
+        const std::string p = "whistle.dec." + std::to_string(l) + ".";
+        dh[l].qkv = gen_q(p + "qkv", 3 * d, d);
+        dh[l].out = gen_q(p + "out", d, d);
+        dh[l].cross_q = gen_q(p + "cross_q", d, d);
+        dh[l].cross_kv = gen_q(p + "cross_kv", 2 * d, d);
+        dh[l].cross_out = gen_q(p + "cross_out", d, d);
+        dh[l].gate_up = gen_q(p + "gate_up", 2 * f, d);
+        dh[l].down = gen_q(p + "down", d, f);
+        dh[l].norm_attn = gen_normal(p + "norm_attn", 0.1f, d);
+        dh[l].norm_cross = gen_normal(p + "norm_cross", 0.1f, d);
+        dh[l].post_norm = gen_normal(p + "post_norm", 0.1f, d);
+        dh[l].norm_ffn = gen_normal(p + "norm_ffn", 0.1f, d);
+        dh[l].q_norm = gen_normal(p + "q_norm", 0.1f, 64);
+        dh[l].k_norm = gen_normal(p + "k_norm", 0.1f, 64);
+        dh[l].gate = gen_normal(p + "gate", 1.0f, 1)[0];
+    }
+    std::vector<float> dec_norm = gen_normal("whistle.dec_norm", 0.1f, d);
+    whistle_position((int)T, (int)d, host_sigmoid(position_gate), w->position_host);
+    rn_config rc_rope{};
+    rc_rope.head_dim = 64;
+    rc_rope.rope_theta = c.rope_theta;
+    rc_rope.max_positions = (int)std::max(T, (size_t)c.max_positions);
+    std::vector<float> rope_cos, rope_sin;
+    rotary_table(rc_rope, rope_cos, rope_sin);
+
+    // one device arena: weights, tables, work buffers, the cross memory, the session
+    const size_t Dm = std::max(d, f), L = c.dec_layers, cap = c.max_positions;
+    auto qbytes = [](size_t rows, size_t cols) { return align_up(rows * cols) + align_up(rows * (cols / kGroup) * 4); };
+    size_t total = align_up(4 * conv1.size()) + align_up(4 * depthwise.size()) + qbytes(d, d);
+    total += (size_t)c.enc_layers * (qbytes(3 * d, d) + qbytes(d, d) + qbytes(2 * f, d) + qbytes(d, f) +
+                                     2 * align_up(4 * d) + 2 * align_up(4 * 64));
+    total += align_up(4 * d) + align_up(4 * T * d) + qbytes(V, d);
+    total += L * (qbytes(3 * d, d) + 3 * qbytes(d, d) + qbytes(2 * d, d) + qbytes(2 * f, d) + qbytes(d, f) +
+                  4 * align_up(4 * d) + 2 * align_up(4 * 64));
+    total += align_up(4 * d) + 2 * align_up(4 * rope_cos.size());
+    total += align_up(4 * Fr * M) + align_up(4 * Fr * d) + align_up(4 * T * d) * 4 + align_up(4 * T * 3 * d) +
+             align_up(4 * T * Dm) + align_up(T * Dm) + align_up(4 * T) + 3 * align_up(T * d) + 3 * align_up(4 * T * H);
+    total += 2 * align_up(L * T * d) + 2 * align_up(4 * L * T * H);
+    total += 2 * align_up(2 * L * H * cap * 64) + 6 * align_up(4 * d) + align_up(4 * 3 * d) + align_up(4 * f) +
+             align_up(4 * V) + align_up(d) + align_up(4 * H) + align_up(sizeof(DecodeState)) + align_up(4 * cap) +
+             align_up(8 * V);
+    if (hipMalloc(&w->arena, total) != hipSuccess) {
+        delete w;
+        return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", total);
+    }
+    Arena a{(char*)w->arena, 0, total};
+    std::vector<std::pair<void*, std::pair<const void*, size_t>>> uploads;
+    auto place = [&](const void* src, size_t bytes) {
+        void* dst = a.take(bytes);
+        uploads.push_back({dst, {src, bytes}});
+        return dst;
+    };
+    auto placeq = [&](const Q& q, size_t rows, size_t cols) {
+        DevMatrix dm;
+        dm.W = (int8_t*)place(q.codes.data(), rows * cols);
+        dm.sW = (float*)place(q.scales.data(), rows * (cols / kGroup) * 4);
+        return dm;
+    };
+    w->conv1 = (float*)place(conv1.data(), 4 * conv1.size());
+    w->depthwise = (float*)place(depthwise.data(), 4 * depthwise.size());
+    w->pointwise = placeq(pointwise, d, d);
+    w->enc.resize(c.enc_layers);
+    for (int l = 0; l < c.enc_layers; ++l) {
+        WEncLayerDev& D = w->enc[l];
+        D.qkv = placeq(eh[l].qkv, 3 * d, d);
+        D.out = placeq(eh[l].out, d, d);
+        D.gate_up = placeq(eh[l].gate_up, 2 * f, d);
+        D.down = placeq(eh[l].down, d, f);
+        D.norm_attn = (float*)place(eh[l].norm_attn.data(), 4 * d);
+        D.norm_ffn = (float*)place(eh[l].norm_ffn.data(), 4 * d);
+        D.q_norm = (float*)place(eh[l].q_norm.data(), 4 * 64);
+        D.k_norm = (float*)place(eh[l].k_norm.data(), 4 * 64);
+    }
+    w->enc_norm = (float*)place(enc_norm.data(), 4 * d);
+    w->position = (float*)place(w->position_host.data(), 4 * T * d);
+    w->embedding = placeq(embedding, V, d);
+    w->dec.resize(L);
+    w->gains_host.resize(L);
+    for (size_t l = 0; l < L; ++l) {
+        WDecLayerDev& D = w->dec[l];
+        D.qkv = placeq(dh[l].qkv, 3 * d, d);
+        D.out = placeq(dh[l].out, d, d);
+        D.cross_q = placeq(dh[l].cross_q, d, d);
+        D.cross_kv = placeq(dh[l].cross_kv, 2 * d, d);
+        D.cross_out = placeq(dh[l].cross_out, d, d);
+        D.gate_up = placeq(dh[l].gate_up, 2 * f, d);
+        D.down = placeq(dh[l].down, d, f);
+        D.norm_attn = (float*)place(dh[l].norm_attn.data(), 4 * d);
+        D.norm_cross = (float*)place(dh[l].norm_cross.data(), 4 * d);
+        D.post_norm = (float*)place(dh[l].post_norm.data(), 4 * d);
+        D.norm_ffn = (float*)place(dh[l].norm_ffn.data(), 4 * d);
+        D.q_norm = (float*)place(dh[l].q_norm.data(), 4 * 64);
+        D.k_norm = (float*)place(dh[l].k_norm.data(), 4 * 64);
+        D.cross_gain = w->gains_host[l] = host_sigmoid(dh[l].gate);
+    }
+    w->dec_norm = (float*)place(dec_norm.data(), 4 * d);
+    w->rope_cos = (float*)place(rope_cos.data(), 4 * rope_cos.size());
+    w->rope_sin = (float*)place(rope_sin.data(), 4 * rope_sin.size());
+    w->mel = (float*)a.take(4 * Fr * M);
+    w->h1 = (float*)a.take(4 * Fr * d);
+    w->R = (float*)a.take(4 * T * d);  // the stem's depthwise output, later the memory input
+    w->X = (float*)a.take(4 * T * d);
+    w->ctx = (float*)a.take(4 * T * d);
+    w->encoded = (float*)a.take(4 * T * d);
+    w->Y = (float*)a.take(4 * T * 3 * d);
+    w->F = (float*)a.take(4 * T * Dm);
+    w->Xq = (int8_t*)a.take(T * Dm);
+    w->sx = (float*)a.take(4 * T);
+    w->qc = (int8_t*)a.take(T * d);
+    w->kc = (int8_t*)a.take(T * d);
+    w->vc = (int8_t*)a.take(T * d);
+    w->qs = (float*)a.take(4 * T * H);
+    w->ks = (float*)a.take(4 * T * H);
+    w->vs = (float*)a.take(4 * T * H);
+    w->mem_k = (int8_t*)a.take(L * T * d);
+    w->mem_v = (int8_t*)a.take(L * T * d);
+    w->mem_ks = (float*)a.take(4 * L * T * H);
+    w->mem_vs = (float*)a.take(4 * L * T * H);
+    w->kcache = (__half*)a.take(2 * L * H * cap * 64);
+    w->vcache = (__half*)a.take(2 * L * H * cap * 64);
+    w->x = (float*)a.take(4 * d);
+    w->attn = (float*)a.take(4 * d);
+    w->cq = (float*)a.take(4 * d);
+    w->cctx = (float*)a.take(4 * d);
+    w->catt = (float*)a.take(4 * d);
+    w->hidden = (float*)a.take(4 * d);
+    w->qkv = (float*)a.take(4 * 3 * d);
+    w->ffh = (float*)a.take(4 * f);
+    w->logits = (float*)a.take(4 * V);
+    w->cqc = (int8_t*)a.take(d);
+    w->cqs = (float*)a.take(4 * H);
+    w->state = (DecodeState*)a.take(sizeof(DecodeState));
+    w->ids = (uint32_t*)a.take(4 * cap);
+    w->keys = (unsigned long long*)a.take(8 * V);
+    if (a.used > total || hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking) != hipSuccess) {
+        (void)hipFree(w->arena);
+        delete w;
+        return fail(RN_ERR_MEMORY, "arena layout (%zu of %zu bytes) or stream creation failed", a.used, total);
+    }
+    for (auto& u : uploads) {
+        if (hipMemcpy(u.first, u.second.first, u.second.second, hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipStreamDestroy(w->stream);
+            (void)hipFree(w->arena);
+            delete w;
+            return fail(RN_ERR_DEVICE, "weight upload failed");
+        }
+    }
+    if (hipMemsetAsync(w->state, 0, sizeof(DecodeState), w->stream) != hipSuccess ||
+        hipStreamSynchronize(w->stream) != hipSuccess) {
+        (void)hipStreamDestroy(w->stream);
+        (void)hipFree(w->arena);
+        delete w;
+        return fail(RN_ERR_DEVICE, "state initialisation failed");
+    }
+    *out = w;
+    return RN_OK;
+}
+
+int rn_whistle_free(rn_whistle* w) {
+    if (!w) return RN_OK;
+    if (w->stream) {
+        (void)hipStreamSynchronize(w->stream);
+        (void)hipStreamDestroy(w->stream);
+    }
+    (void)hipFree(w->arena);
+    delete w;
+    return RN_OK;
+}
+
+int rn_whistle_frames(const rn_whistle* w, int* frames) {
+    RN_REQUIRE(w && frames, "null argument");
+    *frames = w->T;
+    return RN_OK;
+}
+
+int rn_whistle_tables(const rn_whistle* w, float* position, float* cross_gains) {
+    RN_REQUIRE(w, "whistle is null");
+    if (position) memcpy(position, w->position_host.data(), 4 * w->position_host.size());
+    if (cross_gains) memcpy(cross_gains, w->gains_host.data(), 4 * w->gains_host.size());
+    return RN_OK;
+}
+
+int rn_whistle_stream(const rn_whistle* w, void** stream) {
+    RN_REQUIRE(w && stream, "null argument");
+    *stream = w->stream;
+    return RN_OK;
+}
+
+// stem.rs:39-115: first convolution + silu, the stage's depthwise convolution,
+// its pointwise product (rows quantised per frame) with silu, into w->X.
+static int whistle_stem(rn_whistle* w, const float* mel) {
+    const rn_whistle_config& c = w->cfg;
+    const int d = c.d_model, T = w->T;
+    hipStream_t st = w->stream;
+    RN_HIP(hipMemcpyAsync(w->mel, mel, 4 * (size_t)c.frames * c.mels, hipMemcpyHostToDevice, st));
+    RN_HIP(launch_stem(w->mel, w->conv1, w->depthwise, c.frames, c.mels, d, w->h1, w->R, st));
+    RN_HIP(launch_norm_quantise(w->R, nullptr, T, d, c.norm_eps, w->Xq, w->sx, nullptr, st));
+    RN_HIP(launch_gemm(GemmParams{w->Xq, w->sx, w->pointwise.W, w->pointwise.sW, T, d, d, w->X, d, nullptr, 0},
+                       kGemmStoreSilu, kPanel, false, st));
+    return RN_OK;
+}
+
+int rn_whistle_stem(rn_whistle* w, const float* mel, float* out) {
+    RN_REQUIRE(w && mel && out, "null argument");
+    int rc = whistle_stem(w, mel);
+    if (rc) return rc;
+    RN_HIP(hipMemcpyAsync(out, w->X, 4 * (size_t)w->T * w->cfg.d_model, hipMemcpyDeviceToHost, w->stream));
+    RN_HIP(hipStreamSynchronize(w->stream));
+    return RN_OK;
+}
+
+// encoder.rs:145-297 for one synthetic layer over w->X.
+static int whistle_encoder_layer(rn_whistle* w, int l) {
+    const rn_whistle_config& c = w->cfg;
+    const int d = c.d_model, T = w->T, H = c.heads, f = c.ffn;
+    const WEncLayerDev& L = w->enc[l];
+    hipStream_t st = w->stream;
+    RN_HIP(launch_norm_quantise(w->X, L.norm_attn, T, d, c.norm_eps, w->Xq, w->sx, nullptr, st));
+    RN_HIP(launch_gemm(GemmParams{w->Xq, w->sx, L.qkv.W, L.qkv.sW, T, 3 * d, d, w->Y, 3 * d, nullptr, 0}, kGemmStore,
+                       kPanel, false, st));
+    HeadCodesParams hp{};
+    hp.src = w->Y;
+    hp.src_stride = 3 * d;
+    hp.frames = T;
+    hp.heads = H;
+    hp.nsec = 3;
+    hp.sec[0] = HeadSection{0, L.q_norm, 1, 1.0f / sqrtf(64.0f), w->qc, w->qs};
+    hp.sec[1] = HeadSection{d, L.k_norm, 1, 1.0f, w->kc, w->ks};
+    hp.sec[2] = HeadSection{2 * d, nullptr, 0, 1.0f, w->vc, w->vs};
+    hp.rope_cos = w->rope_cos;
+    hp.rope_sin = w->rope_sin;
+    hp.pos0 = 0;
+    hp.eps = c.norm_eps;
+    RN_HIP(launch_head_codes(hp, st));
+    Int8AttendParams ap{w->qc, w->qs, w->kc, w->ks, w->vc, w->vs, T, H, w->ctx, d};
+    RN_HIP(launch_int8_attend(ap, T, st));
+    RN_HIP(launch_norm_quantise(w->ctx, nullptr, T, d, c.norm_eps, w->Xq, w->sx, nullptr, st));
+    RN_HIP(launch_gemm(GemmParams{w->Xq, w->sx, L.out.W, L.out.sW, T, d, d, w->X, d, nullptr, 0}, kGemmResidual, kPanel,
+                       false, st));
+    RN_HIP(launch_norm_quantise(w->X, L.norm_ffn, T, d, c.norm_eps, w->Xq, w->sx, nullptr, st));
+    RN_HIP(launch_gemm(GemmParams{w->Xq, w->sx, L.gate_up.W, L.gate_up.sW, T, 2 * f, d, w->F, f, nullptr, f},
+                       kGemmSilu, kPanel, false, st));
+    RN_HIP(launch_norm_quantise(w->F, nullptr, T, f, c.norm_eps, w->Xq, w->sx, nullptr, st));
+    RN_HIP(launch_gemm(GemmParams{w->Xq, w->sx, L.down.W, L.down.sW, T, d, f, w->X, d, nullptr, 0}, kGemmResidual,
+                       kPanel, false, st));
+    return RN_OK;
+}
+
+// cross.rs:58-99: position term added, rows quantised, then per decoder layer
+// the key/value product and their per-head codes (keys after k_norm).
+static int whistle_memory(rn_whistle* w) {
+    const rn_whistle_config& c = w->cfg;
+    const int d = c.d_model, T = w->T, H = c.heads;
+    hipStream_t st = w->stream;
+    RN_HIP(launch_add(w->encoded, w->position, (size_t)T * d, w->R, st));
+    RN_HIP(launch_norm_quantise(w->R, nullptr, T, d, c.norm_eps, w->Xq, w->sx, nullptr, st));
+    for (int l = 0; l < c.dec_layers; ++l) {
+        const WDecLayerDev& L = w->dec[l];
+        RN_HIP(launch_gemm(GemmParams{w->Xq, w->sx, L.cross_kv.W, L.cross_kv.sW, T, 2 * d, d, w->Y, 2 * d, nullptr, 0},
+                           kGemmStore, kPanel, false, st));
+        HeadCodesParams hp{};
+        hp.src = w->Y;
+        hp.src_stride = 2 * d;
+        hp.frames = T;
+        hp.heads = H;
+        hp.nsec = 2;
+        const size_t off = (size_t)l * T * d, soff = (size_t)l * T * H;
+        hp.sec[0] = HeadSection{0, L.k_norm, 0, 1.0f, w->mem_k + off, w->mem_ks + soff};
+        hp.sec[1] = HeadSection{d, nullptr, 0, 1.0f, w->mem_v + off, w->mem_vs + soff};
+        hp.eps = c.norm_eps;
+        RN_HIP(launch_head_codes(hp, st));
+    }
+    return RN_OK;
+}
+
+int rn_whistle_encode(rn_whistle* w, const float* mel, float* encoded) {
+    RN_REQUIRE(w && mel, "null argument");
+    const rn_whistle_config& c = w->cfg;
+    int rc = whistle_stem(w, mel);
+    if (rc) return rc;
+    for (int l = 0; l < c.enc_layers; ++l) {
+        rc = whistle_encoder_layer(w, l);
+        if (rc) return rc;
+    }
+    RN_HIP(launch_norm_rows(w->X, w->enc_norm, w->T, c.d_model, c.norm_eps, w->encoded, w->stream));
+    rc = whistle_memory(w);
+    if (rc) return rc;
+    if (encoded)
+        RN_HIP(hipMemcpyAsync(encoded, w->encoded, 4 * (size_t)w->T * c.d_model, hipMemcpyDeviceToHost, w->stream));
+    RN_HIP(hipStreamSynchronize(w->stream));
+    w->encoded_ready = true;
+    w->length = 0;
+    w->has_hidden = false;
+    return RN_OK;
+}
+
+int rn_whistle_memory(const rn_whistle* w, int8_t* keys, float* key_scales, int8_t* values, float* value_scales) {
+    RN_REQUIRE(w && keys && key_scales && values && value_scales, "null argument");
+    RN_REQUIRE(w->encoded_ready, "no audio has been encoded");
+    const size_t n = (size_t)w->cfg.dec_layers * w->T * w->cfg.d_model;
+    const size_t ns = (size_t)w->cfg.dec_layers * w->T * w->cfg.heads;
+    RN_HIP(hipMemcpyAsync(keys, w->mem_k, n, hipMemcpyDeviceToHost, w->stream));
+    RN_HIP(hipMemcpyAsync(values, w->mem_v, n, hipMemcpyDeviceToHost, w->stream));
+    RN_HIP(hipMemcpyAsync(key_scales, w->mem_ks, 4 * ns, hipMemcpyDeviceToHost, w->stream));
+    RN_HIP(hipMemcpyAsync(value_scales, w->mem_vs, 4 * ns, hipMemcpyDeviceToHost, w->stream));
+    RN_HIP(hipStreamSynchronize(w->stream));
+    return RN_OK;
+}
+
+int rn_whistle_reset(rn_whistle* w) {
+    RN_REQUIRE(w, "whistle is null");
+    w->length = 0;
+    w->has_hidden = false;
+    return RN_OK;
+}
+
+// One decoder step (session.rs:76-148 with the cross hook of cross.rs:126-182):
+// per layer the self-attention block, the cross-attention block and the gated
+// FFN; then either the final norm (push) or the logits product with the
+// on-device greedy argmax (decode).
+static int enqueue_whistle_step(rn_whistle* w, bool greedy) {
+    const rn_whistle_config& c = w->cfg;
+    const int d = c.d_model, H = c.heads, f = c.ffn, T = w->T;
+    hipStream_t st = w->stream;
+    for (int l = 0; l < c.dec_layers; ++l) {
+        const WDecLayerDev& L = w->dec[l];
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.qkv.W, L.qkv.sW, w->qkv, nullptr, 3 * d, 0};
+            p.x = w->x;
+            p.gain = L.norm_attn;
+            p.eps = c.norm_eps;
+            p.embW = w->embedding.W;
+            p.embS = w->embedding.sW;
+            p.embed_scale = w->embed_scale;
+            p.vocab = c.vocab;
+            p.x_out = w->x;
+            p.state = w->state;
+            const int rpb = gemv_rows_per_block(3 * d, d, kStore);
+            RN_HIP(launch_gemv(p, d, l == 0 ? kEmbedNorm : kNorm, kStore, kPanel, rpb, (3 * d + rpb - 1) / rpb, st));
+        }
+        {
+            AttendParams a{};
+            a.qkv = w->qkv;
+            a.kc = w->kcache;
+            a.vc = w->vcache;
+            a.layer = l;
+            a.heads = H;
+            a.capacity = w->capacity;
+            a.d_model = d;
+            a.pos = &w->state->pos;
+            a.pos_stride = 0;
+            a.rope_cos = w->rope_cos;
+            a.rope_sin = w->rope_sin;
+            a.out = w->attn;
+            a.error = &w->state->error;
+            RN_HIP(launch_attend(a, kAttendDecode, H, 1, w->capacity, st));
+        }
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.out.W, L.out.sW, w->x, nullptr, d, 0};
+            p.x = w->attn;
+            const int rpb = gemv_rows_per_block(d, d, kResidual);
+            RN_HIP(launch_gemv(p, d, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
+        }
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.cross_q.W, L.cross_q.sW, w->cq, nullptr, d, 0};
+            p.x = w->x;
+            p.gain = L.norm_cross;
+            p.eps = c.norm_eps;
+            const int rpb = gemv_rows_per_block(d, d, kStore);
+            RN_HIP(launch_gemv(p, d, kNorm, kStore, kPanel, rpb, (d + rpb - 1) / rpb, st));
+        }
+        {
+            HeadCodesParams hp{};
+            hp.src = w->cq;
+            hp.src_stride = d;
+            hp.frames = 1;
+            hp.heads = H;
+            hp.nsec = 1;
+            hp.sec[0] = HeadSection{0, L.q_norm, 0, 1.0f / sqrtf(64.0f), w->cqc, w->cqs};
+            hp.eps = c.norm_eps;
+            RN_HIP(launch_head_codes(hp, st));
+            const size_t off = (size_t)l * T * d, soff = (size_t)l * T * H;
+            Int8AttendParams ap{w->cqc, w->cqs, w->mem_k + off, w->mem_ks + soff, w->mem_v + off, w->mem_vs + soff,
+                                T, H, w->cctx, d};
+            RN_HIP(launch_int8_attend(ap, 1, st));
+        }
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.cross_out.W, L.cross_out.sW, w->catt, nullptr, d, 0};
+            p.x = w->cctx;
+            const int rpb = gemv_rows_per_block(d, d, kStore);
+            RN_HIP(launch_gemv(p, d, kQuant, kStore, kPanel, rpb, (d + rpb - 1) / rpb, st));
+            RN_HIP(launch_cross_residual(w->catt, L.post_norm, L.cross_gain, c.norm_eps, d, w->x, st));
+        }
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.gate_up.W, L.gate_up.sW, w->ffh, nullptr, 2 * f, 0};
+            p.half_rows = f;
+            p.x = w->x;
+            p.gain = L.norm_ffn;
+            p.eps = c.norm_eps;
+            const int rpb = gemv_rows_per_block(2 * f, d, kSilu);
+            RN_HIP(launch_gemv(p, d, kNorm, kSilu, kPanel, rpb, (f + rpb / 2 - 1) / (rpb / 2), st));
+        }
+        {
+            GemvParams p{};
+            p.nseg = 1;
+            p.seg[0] = Segment{L.down.W, L.down.sW, w->x, nullptr, d, 0};
+            p.x = w->ffh;
+            const int rpb = gemv_rows_per_block(d, f, kResidual);
+            RN_HIP(launch_gemv(p, f, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
+        }
+    }
+    if (!greedy) {
+        RN_HIP(launch_finish_push(w->x, w->dec_norm, d, c.norm_eps, w->hidden, w->state, st));
+        return RN_OK;
+    }
+    GemvParams p{};
+    p.nseg = 1;
+    p.seg[0] = Segment{w->embedding.W, w->embedding.sW, w->logits, nullptr, c.vocab, 0};
+    p.x = w->x;
+    p.gain = w->dec_norm;
+    p.eps = c.norm_eps;
+    p.hidden_out = w->hidden;
+    p.keys = w->keys;
+    const int rpb = gemv_rows_per_block(c.vocab, d, kStore);
+    const int blocks = (c.vocab + rpb - 1) / rpb;
+    RN_HIP(launch_gemv(p, d, kNorm, kArgmax, kPlane, rpb, blocks, st));
+    RN_HIP(launch_argmax_finalize(w->keys, blocks, w->logits, w->state, w->ids, st));
+    return RN_OK;
+}
+
+static int whistle_state_error(rn_whistle* w) {
+    int32_t err = 0;
+    RN_HIP(hipMemcpyAsync(&err, &w->state->error, sizeof err, hipMemcpyDeviceToHost, w->stream));
+    RN_HIP(hipStreamSynchronize(w->stream));
+    if (err) {
+        RN_HIP(hipMemsetAsync(&w->state->error, 0, sizeof(int32_t), w->stream));
+        RN_HIP(hipStreamSynchronize(w->stream));
+        return fail(RN_ERR_STATE, "device reported error flags 0x%x (1: token >= vocab, 2: position >= capacity)", err);
+    }
+    return RN_OK;
+}
+
+int rn_whistle_push(rn_whistle* w, uint32_t token) {
+    RN_REQUIRE(w, "whistle is null");
+    RN_REQUIRE(w->encoded_ready, "no audio has been encoded");
+    RN_REQUIRE(token < (uint32_t)w->cfg.vocab, "token %u outside the vocabulary (%d)", token, w->cfg.vocab);
+    if (w->length >= w->capacity) return fail(RN_ERR_CAPACITY, "decoder is full (%d positions)", w->capacity);
+    RN_HIP(launch_set_state(w->state, token, w->length, 0, 0, w->stream));
+    int rc = enqueue_whistle_step(w, false);
+    if (rc) return rc;
+    w->length += 1;
+    w->has_hidden = true;
+    return whistle_state_error(w);
+}
+
+int rn_whistle_logits(rn_whistle* w, float* out) {
+    RN_REQUIRE(w && out, "null argument");
+    if (!w->has_hidden) return fail(RN_ERR_STATE, "no token has been pushed");
+    const rn_whistle_config& c = w->cfg;
+    GemvParams p{};
+    p.nseg = 1;
+    p.seg[0] = Segment{w->embedding.W, w->embedding.sW, w->logits, nullptr, c.vocab, 0};
+    p.x = w->hidden;
+    const int rpb = gemv_rows_per_block(c.vocab, c.d_model, kStore);
+    RN_HIP(launch_gemv(p, c.d_model, kQuant, kStore, kPlane, rpb, (c.vocab + rpb - 1) / rpb, w->stream));
+    RN_HIP(hipMemcpyAsync(out, w->logits, 4 * (size_t)c.vocab, hipMemcpyDeviceToHost, w->stream));
+    return whistle_state_error(w);
+}
+
+int rn_whistle_decode_greedy(rn_whistle* w, uint32_t first, int steps, uint32_t* ids) {
+    RN_REQUIRE(w && (ids || steps == 0), "null argument");
+    RN_REQUIRE(w->encoded_ready, "no audio has been encoded");
+    RN_REQUIRE(steps >= 0, "steps must be non-negative");
+    RN_REQUIRE(first < (uint32_t)w->cfg.vocab, "token %u outside the vocabulary", first);
+    if (steps == 0) return RN_OK;
+    if (w->length + steps > w->capacity)
+        return fail(RN_ERR_CAPACITY, "%d + %d positions exceed the capacity %d", w->length, steps, w->capacity);
+    RN_HIP(launch_set_state(w->state, first, w->length, 0, (uint32_t)w->capacity, w->stream));
+    for (int i = 0; i < steps; ++i) {
+        const int rc = enqueue_whistle_step(w, true);
+        if (rc) return rc;
+    }
+    RN_HIP(hipMemcpyAsync(ids, w->ids, 4 * (size_t)steps, hipMemcpyDeviceToHost, w->stream));
+    w->length += steps;
+    w->has_hidden = true;
+    return whistle_state_error(w);
 }
 
 }  // extern "C"

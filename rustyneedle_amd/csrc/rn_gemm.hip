@@ -160,6 +160,8 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
             float* dst = p.Y + (size_t)m * p.ldy + n;
             if constexpr (EPI == kGemmResidual)
                 *dst = *dst + total;
+            else if constexpr (EPI == kGemmStoreSilu)
+                *dst = silu(total);  // stem.rs:76,99: silu after the stage
             else
                 *dst = total;
         }
@@ -177,11 +179,17 @@ template <int EPI, int FORM, bool DUMP>
 static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
     // tiles sized so that the int32 sums of a tile fill 64 KB of LDS
     switch (p.K) {
+        case 384:
+            launch_split<12, 32, 32, EPI, FORM, DUMP>(p, stream);
+            break;
         case 512:
             launch_split<16, 32, 32, EPI, FORM, DUMP>(p, stream);
             break;
         case 1024:
             launch_split<32, 16, 32, EPI, FORM, DUMP>(p, stream);
+            break;
+        case 1536:
+            launch_split<48, 16, 16, EPI, FORM, DUMP>(p, stream);
             break;
         default:
             launch_split<64, 16, 16, EPI, FORM, DUMP>(p, stream);
@@ -192,7 +200,7 @@ static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
 hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, hipStream_t stream) {
     if (p.M <= 0) return hipSuccess;
     // instantiated for the supported widths (the kernel is unrolled over groups)
-    if ((p.K != 512 && p.K != 1024 && p.K != 2048) || p.N <= 0) return hipErrorInvalidValue;
+    if ((p.K != 384 && p.K != 512 && p.K != 1024 && p.K != 1536 && p.K != 2048) || p.N <= 0) return hipErrorInvalidValue;
     if (epilogue == kGemmSilu && (p.half % 16 != 0 || p.N != 2 * p.half)) return hipErrorInvalidValue;
     if (dump) {
         if (epilogue != kGemmStore) return hipErrorInvalidValue;
@@ -217,6 +225,9 @@ hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, h
         case kGemmSilu:
             launch_by_rows<kGemmSilu, kPanel, false>(p, stream);
             break;
+        case kGemmStoreSilu:
+            launch_by_rows<kGemmStoreSilu, kPanel, false>(p, stream);
+            break;
         default:
             return hipErrorInvalidValue;
     }
@@ -227,22 +238,22 @@ hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, h
 
 // Optional zero-centred norm (ops.rs:44-50 with the sum of ops.rs:7-17), then
 // the per-row int8 quantisation (ops.rs:112-118). One wave per row, four rows
-// per block; the row lives in registers (n/256 float4 per lane). The sum of
+// per block; the row lives in registers (n/128 float2 per lane). The sum of
 // squares keeps the reference's order: 8 strided partial sums (element e goes
 // to partial e%8, each summed in element order), then the partials 0..7 in
 // order; the squares are staged transposed in LDS so that each of 8 lanes runs
 // one partial over contiguous memory. `normed` (nullable) receives the normed
-// rows. NV = n / 256 float4 per lane.
+// rows. NV = n / 128 float2 per lane.
 template <int NV>
 __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, const float* gain, int count, float eps,
                                                             int8_t* codes, float* scales, float* normed) {
-    constexpr int n = NV * 256;
+    constexpr int n = NV * 128;
     extern __shared__ float sq_s[];  // [4][n] when gain != nullptr
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + wave;
     const bool live = row < count;
-    const float4* src = reinterpret_cast<const float4*>(x + (size_t)(live ? row : count - 1) * n);
-    float4 v[NV];
+    const float2* src = reinterpret_cast<const float2*>(x + (size_t)(live ? row : count - 1) * n);
+    float2 v[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) v[i] = src[lane + 64 * i];
     if (gain != nullptr) {
@@ -250,39 +261,29 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
         constexpr int run = n >> 3;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int e = 4 * (lane + 64 * i);  // elements e..e+3; e % 8 is 0 or 4
+            const int e = 2 * (lane + 64 * i);  // elements e, e+1; e % 8 is 0, 2, 4 or 6
             const int p = e & 7, c = e >> 3;
             sq[(p + 0) * run + c] = v[i].x * v[i].x;
             sq[(p + 1) * run + c] = v[i].y * v[i].y;
-            sq[(p + 2) * run + c] = v[i].z * v[i].z;
-            sq[(p + 3) * run + c] = v[i].w * v[i].w;
         }
         __syncthreads();
         float part = 0.0f;
         if (lane < 8) {
-            const float4* r4 = reinterpret_cast<const float4*>(sq + lane * run);
-            for (int c = 0; c < run / 4; ++c) {
-                const float4 t = r4[c];
-                part = part + t.x;
-                part = part + t.y;
-                part = part + t.z;
-                part = part + t.w;
-            }
+            const float* r = sq + lane * run;
+            for (int c = 0; c < run; ++c) part = part + r[c];
         }
         float total = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) total = total + __shfl(part, j, kWave);
         total = total + 0.0f;  // the empty tail of the 8-lane sum
         const float inverse = 1.0f / sqrtf(total / (float)n + eps);
-        const float4* g4 = reinterpret_cast<const float4*>(gain);
+        const float2* g2 = reinterpret_cast<const float2*>(gain);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const float4 g = g4[lane + 64 * i];
+            const float2 g = g2[lane + 64 * i];
             v[i].x = ((1.0f + g.x) * v[i].x) * inverse;
             v[i].y = ((1.0f + g.y) * v[i].y) * inverse;
-            v[i].z = ((1.0f + g.z) * v[i].z) * inverse;
-            v[i].w = ((1.0f + g.w) * v[i].w) * inverse;
-            if (normed != nullptr && live) reinterpret_cast<float4*>(normed + (size_t)row * n)[lane + 64 * i] = v[i];
+            if (normed != nullptr && live) reinterpret_cast<float2*>(normed + (size_t)row * n)[lane + 64 * i] = v[i];
         }
     }
     float peak = 0.0f;
@@ -290,23 +291,19 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
     for (int i = 0; i < NV; ++i) {
         peak = fmaxf(peak, fabsf(v[i].x));
         peak = fmaxf(peak, fabsf(v[i].y));
-        peak = fmaxf(peak, fabsf(v[i].z));
-        peak = fmaxf(peak, fabsf(v[i].w));
     }
     peak = wave_max(peak);
     const float scale = int8_scale_from_peak(peak);
     if (!live) return;  // the whole wave: one row per wave
     if (codes != nullptr) {
-        float y[4 * NV];
-        quotients<4 * NV>(reinterpret_cast<const float*>(v), scale, y);
-        int* dst = reinterpret_cast<int*>(codes + (size_t)row * n);
+        float y[2 * NV];
+        quotients<2 * NV>(reinterpret_cast<const float*>(v), scale, y);
+        uint16_t* dst = reinterpret_cast<uint16_t*>(codes + (size_t)row * n);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const uint32_t b0 = (uint8_t)code_of_quotient(y[4 * i + 0]);
-            const uint32_t b1 = (uint8_t)code_of_quotient(y[4 * i + 1]);
-            const uint32_t b2 = (uint8_t)code_of_quotient(y[4 * i + 2]);
-            const uint32_t b3 = (uint8_t)code_of_quotient(y[4 * i + 3]);
-            dst[lane + 64 * i] = (int)(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24));
+            const uint32_t b0 = (uint8_t)code_of_quotient(y[2 * i + 0]);
+            const uint32_t b1 = (uint8_t)code_of_quotient(y[2 * i + 1]);
+            dst[lane + 64 * i] = (uint16_t)(b0 | (b1 << 8));
         }
     }
     if (lane == 0 && scales != nullptr) scales[row] = scale;
@@ -317,19 +314,16 @@ hipError_t launch_norm_quantise(const float* x, const float* gain, int count, in
     if (count <= 0) return hipSuccess;
     const size_t lds = gain != nullptr ? 4 * sizeof(float) * (size_t)n : 0;
     const dim3 grid((count + 3) / 4), block(256);
+#define RN_NQ(NV) rn_launch(norm_quantise_kernel<NV>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed)
     switch (n) {
-        case 512:
-            rn_launch(norm_quantise_kernel<2>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed);
-            break;
-        case 1024:
-            rn_launch(norm_quantise_kernel<4>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed);
-            break;
-        case 2048:
-            rn_launch(norm_quantise_kernel<8>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed);
-            break;
-        default:
-            return hipErrorInvalidValue;
+        case 384: RN_NQ(3); break;
+        case 512: RN_NQ(4); break;
+        case 1024: RN_NQ(8); break;
+        case 1536: RN_NQ(12); break;
+        case 2048: RN_NQ(16); break;
+        default: return hipErrorInvalidValue;
     }
+#undef RN_NQ
     return hipGetLastError();
 }
 

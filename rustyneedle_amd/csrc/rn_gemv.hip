@@ -25,17 +25,37 @@
 
 namespace rn {
 
+// E consecutive floats (E even) with the widest aligned loads.
+template <int E>
+__device__ __forceinline__ void load_floats(const float* src, float* v) {
+    if constexpr (E % 4 == 0) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(src + e);
+            v[e] = t.x;
+            v[e + 1] = t.y;
+            v[e + 2] = t.z;
+            v[e + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; e += 2) {
+            const float2 t = *reinterpret_cast<const float2*>(src + e);
+            v[e] = t.x;
+            v[e + 1] = t.y;
+        }
+    }
+}
+
 template <int K, int ROWS, int PRO, int EPI, int FORM>
 __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     constexpr int G = K / kGroup;                       // groups per row
     constexpr int CPR = K / 16;                         // 16-byte chunks per row
-    constexpr int RPL = CPR <= 64 ? 64 / CPR : 1;       // rows covered by one load instruction
-    constexpr int LPR = CPR <= 64 ? 1 : CPR / 64;       // load instructions per row
-    constexpr int NL = CPR <= 64 ? ROWS / RPL : ROWS * LPR;
-    constexpr int XC = LPR;                             // input chunks each lane needs
+    constexpr int NL = ROWS * CPR / 64;                 // load instructions per lane
     constexpr int E = K / 64;                           // input values per lane in the prologue
     constexpr int H = ROWS / 2;
-    static_assert(ROWS % RPL == 0, "rows per block must cover whole load instructions");
+    static_assert((ROWS * CPR) % 64 == 0, "rows per block must cover whole load instructions");
+    static_assert(E % 2 == 0 && G % 4 == 0, "input pairs per lane, scale quads per row");
     static_assert(EPI != kSilu || ROWS % 2 == 0, "silu blocks pair gate and up rows");
     static_assert(ROWS <= 64, "one lane per row in the epilogue");
 
@@ -69,8 +89,9 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
             return min(blk * ROWS + rr, sg.rows - 1);
         }
     };
-    auto load_row = [&](int j) -> int { return CPR <= 64 ? j * RPL + lane / CPR : j / LPR; };
-    auto load_chunk = [&](int j) -> int { return CPR <= 64 ? lane % CPR : (j % LPR) * 64 + lane; };
+    // load j of a lane covers chunk (64 j + lane) of the block's rows, in row-major order
+    auto load_row = [&](int j) -> int { return (64 * j + lane) / CPR; };
+    auto load_chunk = [&](int j) -> int { return (64 * j + lane) % CPR; };
 
     // Memory-level order matters: loads complete in issue order for the wait
     // counter, so the prologue inputs go first, then the weights, then the
@@ -85,29 +106,13 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
             token = 0;
         }
         const int8_t* er = p.embW + (size_t)token * K + lane * E;
-        const float scale = p.embS[(size_t)token * G + (lane * E) / kGroup];  // E divides 32
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = ((float)er[e] * scale) * p.embed_scale;
+        for (int e = 0; e < E; ++e)
+            v[e] = ((float)er[e] * p.embS[(size_t)token * G + (lane * E + e) / kGroup]) * p.embed_scale;
     } else if constexpr (PRO != kCodes) {
-#pragma unroll
-        for (int e = 0; e < E; e += 4) {
-            const float4 t = *reinterpret_cast<const float4*>(p.x + lane * E + e);
-            v[e] = t.x;
-            v[e + 1] = t.y;
-            v[e + 2] = t.z;
-            v[e + 3] = t.w;
-        }
+        load_floats<E>(p.x + lane * E, v);
     }
-    if constexpr (NORM) {
-#pragma unroll
-        for (int e = 0; e < E; e += 4) {
-            const float4 t = *reinterpret_cast<const float4*>(p.gain + lane * E + e);
-            gv[e] = t.x;
-            gv[e + 1] = t.y;
-            gv[e + 2] = t.z;
-            gv[e + 3] = t.w;
-        }
-    }
+    if constexpr (NORM) load_floats<E>(p.gain + lane * E, gv);
 
     // 1b. weights: unconditional loads (a branch around a load would make the
     // wait counter unknowable and force a full wait)
@@ -128,11 +133,11 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
 
     // 2. prologue: the int8 codes of the input vector and its scale
     float sx;
-    int4 xc[XC];
+    int4 xc[NL];
     if constexpr (PRO == kCodes) {
         sx = p.xs[0];
 #pragma unroll
-        for (int i = 0; i < XC; ++i) xc[i] = *reinterpret_cast<const int4*>(p.xq + load_chunk(i) * 16);
+        for (int j = 0; j < NL; ++j) xc[j] = *reinterpret_cast<const int4*>(p.xq + load_chunk(j) * 16);
     } else {
         if constexpr (PRO == kEmbedNorm) {
             if (blockIdx.x == 0)
@@ -184,13 +189,13 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)code_of_quotient(y[e]);
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < XC; ++i) xc[i] = *reinterpret_cast<const int4*>(xq_s + load_chunk(i) * 16);
+        for (int j = 0; j < NL; ++j) xc[j] = *reinterpret_cast<const int4*>(xq_s + load_chunk(j) * 16);
     }
 
     // 3. exact int32 group accumulators
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
-        int part = dot16(w[j], xc[CPR <= 64 ? 0 : (j % LPR)], 0);
+        int part = dot16(w[j], xc[j], 0);
         part = part + __shfl_xor(part, 1, 64);
         if ((lane & 1) == 0) acc_s[load_row(j) * G + load_chunk(j) / 2] = part;
     }
@@ -282,13 +287,13 @@ static hipError_t dispatch_pe(const GemvParams& p, int prologue, int epilogue, i
                               : launch_one<K, ROWS, kCodes, kStore, kPlane>(p, blocks, s);
     if (form == kPanel) {
         if (prologue == kQuant && epilogue == kResidual) return launch_one<K, ROWS, kQuant, kResidual, kPanel>(p, blocks, s);
-        if constexpr (K == 512) {
+        if constexpr (K == 512 || K == 384) {
             if (prologue == kNorm && epilogue == kStore) return launch_one<K, ROWS, kNorm, kStore, kPanel>(p, blocks, s);
             if (prologue == kEmbedNorm && epilogue == kStore) return launch_one<K, ROWS, kEmbedNorm, kStore, kPanel>(p, blocks, s);
             if (prologue == kNorm && epilogue == kSilu) return launch_one<K, ROWS, kNorm, kSilu, kPanel>(p, blocks, s);
         }
     } else {
-        if constexpr (K == 512)
+        if constexpr (K == 512 || K == 384)
             if (prologue == kNorm && epilogue == kArgmax) return launch_one<K, ROWS, kNorm, kArgmax, kPlane>(p, blocks, s);
     }
     return hipErrorInvalidValue;
@@ -296,8 +301,16 @@ static hipError_t dispatch_pe(const GemvParams& p, int prologue, int epilogue, i
 
 int gemv_rows_per_block(int rows, int columns, int epilogue) {
     if (epilogue == kSilu) return 8;
-    const int min_rows = columns == 512 ? 2 : 1;
-    int r = columns == 512 ? 32 : (columns == 1024 ? 16 : 8);
+    // rows x 16-byte chunks must fill whole 64-lane loads: 384 columns need
+    // multiples of 8 rows, 1536 multiples of 2
+    int r, min_rows;
+    switch (columns) {
+        case 384: r = 32; min_rows = 8; break;
+        case 512: r = 32; min_rows = 2; break;
+        case 1024: r = 16; min_rows = 1; break;
+        case 1536: r = 8; min_rows = 2; break;
+        default: r = 8; min_rows = 1; break;
+    }
     // Tall products: more rows per block amortise the input prologue, while
     // keeping >= 2048 blocks (eight waves per CU) in flight.
     while (r > 8 && (rows + r - 1) / r < 2048) r /= 2;
@@ -310,6 +323,16 @@ hipError_t launch_gemv(const GemvParams& p, int columns, int prologue, int epilo
                        int blocks, hipStream_t stream) {
     if (blocks <= 0) return hipSuccess;
     switch (columns) {
+        case 384:
+            if (rows_per_block == 8) return dispatch_pe<384, 8>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 16) return dispatch_pe<384, 16>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 32) return dispatch_pe<384, 32>(p, prologue, epilogue, form, blocks, stream);
+            break;
+        case 1536:
+            if (rows_per_block == 2) return dispatch_pe<1536, 2>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 4) return dispatch_pe<1536, 4>(p, prologue, epilogue, form, blocks, stream);
+            if (rows_per_block == 8) return dispatch_pe<1536, 8>(p, prologue, epilogue, form, blocks, stream);
+            break;
         case 512:
             if (rows_per_block == 2) return dispatch_pe<512, 2>(p, prologue, epilogue, form, blocks, stream);
             if (rows_per_block == 4) return dispatch_pe<512, 4>(p, prologue, epilogue, form, blocks, stream);

@@ -120,7 +120,7 @@ hipError_t launch_rope_append(const float* qkv, float* q_out, __half* kc, __half
                               const float* rope_sin, hipStream_t stream);
 
 // ---- multi-token products (i8 MFMA) ----------------------------------------------
-enum GemmEpilogue { kGemmStore = 0, kGemmResidual = 1, kGemmSilu = 2 };
+enum GemmEpilogue { kGemmStore = 0, kGemmResidual = 1, kGemmSilu = 2, kGemmStoreSilu = 3 };  // last: y = silu(total)
 
 struct GemmParams {
     const int8_t* X;   // [M][K] quantised tokens
@@ -142,6 +142,47 @@ hipError_t launch_embed_rows(const uint32_t* tokens, int count, const int8_t* E,
 hipError_t launch_argmax_rows(const float* logits, int count, int n, uint32_t* tokens, uint32_t* ids, int steps,
                               int step, hipStream_t stream);
 hipError_t launch_advance_positions(int32_t* pos, int count, int by, hipStream_t stream);
+
+// ---- speech path (rn_whistle.hip) ---------------------------------------------
+// First convolution (+ silu) into h1 [F][d], then the stage's depthwise
+// convolution into dw_out [(F - 1) / 2 + 1][d].
+hipError_t launch_stem(const float* mel, const float* conv1, const float* depthwise, int F, int M, int d, float* h1,
+                       float* dw_out, hipStream_t stream);
+
+struct HeadSection {
+    int col;             // first column of the section in a source row
+    const float* gain;   // head norm gains [64], or null
+    int rotary;          // rotate at position pos0 + frame
+    float scale_mul;     // multiplies the stored scale
+    int8_t* codes;       // [frames][heads][64]
+    float* scales;       // [frames][heads]
+};
+struct HeadCodesParams {
+    const float* src;    // [frames][src_stride]
+    int src_stride, frames, heads, nsec;
+    HeadSection sec[3];
+    const float* rope_cos;  // [positions][32]
+    const float* rope_sin;
+    int pos0;
+    float eps;
+};
+hipError_t launch_head_codes(const HeadCodesParams& p, hipStream_t stream);
+
+struct Int8AttendParams {
+    const int8_t* qc;    // [queries][heads][64]
+    const float* qs;     // [queries][heads] (times 1/sqrt(64))
+    const int8_t* kc;    // [frames][heads][64]
+    const float* ks;     // [frames][heads]
+    const int8_t* vc;
+    const float* vs;
+    int frames, heads;
+    float* out;          // [queries][out_stride], head h at column 64 h
+    int out_stride;
+};
+hipError_t launch_int8_attend(const Int8AttendParams& p, int queries, hipStream_t stream);
+hipError_t launch_cross_residual(const float* attended, const float* post_norm, float gain, float eps, int n, float* x,
+                                 hipStream_t stream);
+hipError_t launch_add(const float* a, const float* b, size_t n, float* out, hipStream_t stream);
 
 // ---- elementwise / helpers ----------------------------------------------------
 hipError_t launch_quantise_rows(const float* x, int count, int columns, int8_t* codes, float* scales,

@@ -5,7 +5,7 @@ encoder.rs, cross.rs; crates/model/src/session.rs:76-148), not from the
 oracle's code: float64 sums in NumPy's order, libm-exact exp in the softmax
 and silu. The discrete parts of the model are kept: int8 per-row activation
 quantisation before every product, int8 per-(frame, head) query/key/value codes
-in the attention (encoder.rs:218-258, cross.rs:86-170), the fp16 self-attention
+in the attention (encoder.rs:226-285, cross.rs:86-170), the fp16 self-attention
 cache of the decoder.
 """
 from __future__ import annotations
@@ -142,7 +142,7 @@ class Decoder:
                 p = np.exp(s - s.max())
                 att[sl] = (p / p.sum()) @ Vh
             x = x + product(*lw["out"], att)
-            # cross.rs:127-182 without the gate projection
+            # cross.rs:126-182 without the gate projection
             q = product(*lw["cross_q"], norm(x, lw["norm_cross"], 1e-6))
             kc, ks, vc, vs = self.mem[l]
             ctx = np.empty(d)

@@ -63,6 +63,11 @@ def test_zero_centred_norm_bit_exact(n):
     (100, 1024, rn.FORM_PANEL),    # ragged last block
     (7, 2048, rn.FORM_PLANE),
     (1, 512, rn.FORM_PANEL),
+    (1152, 384, rn.FORM_PANEL),    # the d_model 384 products of the speech path
+    (8192, 384, rn.FORM_PLANE),
+    (384, 1536, rn.FORM_PANEL),
+    (13, 384, rn.FORM_PANEL),
+    (5, 1536, rn.FORM_PLANE),
 ])
 def test_multiply_vector_bit_exact(rows, cols, form):
     rng = np.random.default_rng(rows * 7 + cols + form)
@@ -105,6 +110,9 @@ def test_multiply_fused_matches_separate():
     (256, 1536, 512, rn.FORM_PANEL),
     (65, 1000, 512, rn.FORM_PLANE),
     (3, 64, 1024, rn.FORM_PLANE),
+    (100, 1152, 384, rn.FORM_PANEL),
+    (33, 384, 1536, rn.FORM_PANEL),
+    (17, 8192, 384, rn.FORM_PLANE),
 ])
 def test_multiply_batch_mfma_bit_exact(count, rows, cols, form):
     rng = np.random.default_rng(count * 13 + rows + cols)

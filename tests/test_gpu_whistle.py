@@ -1,0 +1,78 @@
+"""The speech path on the GPU against the oracle, bit for bit, through the C ABI."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import rustyneedle_amd as rn
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def small():
+    cfg = dict(rn.WHISTLE)
+    cfg.update(frames=64, enc_layers=2, dec_layers=2, vocab=1000, max_positions=24)
+    w = rn.synthetic_whistle_weights(cfg, seed=11)
+    return cfg, oracle.OracleWhistle(cfg, w), rn.Whistle(cfg, seed=11), rn.synthetic_mel(cfg, seed=11)
+
+
+def test_host_tables(small):
+    cfg, o, g, _ = small
+    pos, gains = g.tables()
+    assert np.array_equal(_bits(pos), _bits(o.position))
+    ref = np.array([oracle.sigmoid(lw["gate"]) for lw in o.w["dec"]], np.float32)
+    assert np.array_equal(_bits(gains), _bits(ref))
+
+
+def test_stem(small):
+    cfg, o, g, mel = small
+    assert np.array_equal(_bits(g.stem(mel)), _bits(o.stem(mel)))
+
+
+def test_encode_and_memory(small):
+    cfg, o, g, mel = small
+    enc = g.encode(mel)
+    ref = o.encode(mel)
+    assert np.array_equal(_bits(enc), _bits(ref))
+    for a, b in zip(g.memory(), o.memory(ref)):
+        assert np.array_equal(a.view(np.uint8) if a.dtype == np.int8 else _bits(a),
+                              b.view(np.uint8) if b.dtype == np.int8 else _bits(b))
+
+
+def test_push_logits_and_greedy(small):
+    cfg, o, g, mel = small
+    enc = g.encode(mel)
+    mem = o.memory(o.encode(mel))
+    s = o.session(cfg["max_positions"], mem)
+    for tok in (3, 999, 0):
+        g.push(tok)
+        s.push(tok)
+        assert np.array_equal(_bits(g.logits()), _bits(s.logits()))
+    g.reset()
+    ids = g.decode_greedy(7, 12)
+    assert ids.tolist() == o.session(cfg["max_positions"], mem).greedy(7, 12).tolist()
+    with pytest.raises(rn.RnError):
+        g.decode_greedy(7, 13)  # 12 + 13 positions exceed the 24 of the session
+    assert enc.shape == (32, 384)
+
+
+def test_full_size_encode_and_48_tokens():
+    """The 3000-frame, 6-encoder-layer, 4-decoder-layer configuration."""
+    cfg = dict(rn.WHISTLE)
+    w = rn.synthetic_whistle_weights(cfg)
+    o = oracle.OracleWhistle(cfg, w)
+    g = rn.Whistle(cfg)
+    mel = rn.synthetic_mel(cfg)
+    oracle.set_threads(8)
+    enc = g.encode(mel)
+    ref = o.encode(mel)
+    assert np.array_equal(_bits(enc), _bits(ref))
+    first = int(rn.synth_tokens(rn.SEED, "whistle.first", cfg["vocab"], 1)[0])
+    ids = g.decode_greedy(first, 48)
+    assert ids.tolist() == o.session(cfg["max_positions"], o.memory(ref)).greedy(first, 48).tolist()
