@@ -11,8 +11,10 @@ Also reported: batch-64 decode tokens/s (64 sequences, ragged caches of 32..512
 positions, 32 greedy tokens), prefill tokens/s (one 256-token sequence), the
 single int8 matvec (2048 x 512) latency, a streaming int8 matvec over 512
 distinct 2048 x 512 matrices in one launch (609 MB, more than the 256 MB
-Infinity Cache: the HBM roofline of the product kernel), and the CPU oracle on
-the host cores as the baseline.
+Infinity Cache: the HBM roofline of the product kernel), the speech path (encode
+of a 3000-frame mel window through the stem and 6 encoder layers plus the cross
+memory, then 48 greedy tokens of the 4-layer cross-attention decoder), and the
+CPU oracle on the host cores as the baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -207,6 +209,53 @@ def bench_gemv(rn, rotations: int = 512):
                 rotating_frac=achieved / HBM_PEAK_GBS)
 
 
+def bench_whistle(rn, reps: int = 3, steps: int = 48, with_cpu: bool = True):
+    """The speech path: encode of a 3000-frame mel window (stem, 6 encoder
+    layers over 1500 frames, the cross memory of 4 decoder layers), then a
+    48-token greedy decode with cross-attention; HIP events on its stream."""
+    cfg = dict(rn.WHISTLE)
+    w = rn.Whistle(cfg)
+    mel = rn.synthetic_mel(cfg)
+    first = int(rn.synth_tokens(rn.SEED, "whistle.first", cfg["vocab"], 1)[0])
+    stream = w.stream()
+    w.encode(mel, copy_out=False)
+    ref = w.decode_greedy(first, steps)
+    enc_ms, dec_ms = [], []
+    for _ in range(reps):
+        t0, t1, t2 = rn.Event(), rn.Event(), rn.Event()
+        t0.record(stream)
+        w.encode(mel, copy_out=False)
+        t1.record(stream)
+        ids = w.decode_greedy(first, steps)
+        t2.record(stream)
+        if ids.tolist() != ref.tolist():
+            raise RuntimeError("speech decode is not deterministic")
+        enc_ms.append(t0.elapsed_ms(t1))
+        dec_ms.append(t1.elapsed_ms(t2))
+    T, d, f = w.frames, cfg["d_model"], cfg["ffn"]
+    per_layer = 2 * T * (3 * d * d + d * d + 2 * f * d + d * f)
+    ops = cfg["enc_layers"] * per_layer + 2 * T * d * d + cfg["dec_layers"] * 2 * T * 2 * d * d
+    out = dict(encode_ms=min(enc_ms), encode_int8_gops=ops / 1e9,
+               decode_tokens_per_s=steps / (min(dec_ms) / 1e3), decode_ms_per_token=min(dec_ms) / steps,
+               frames_in=cfg["frames"], encoder_frames=T, tokens=steps)
+    if with_cpu:
+        import oracle
+        cores = os.cpu_count() or 1
+        threads = max(1, min(cores - 1, 6))
+        oracle.set_threads(threads)
+        o = oracle.OracleWhistle(cfg, rn.synthetic_whistle_weights(cfg))
+        t = time.perf_counter()
+        encoded = o.encode(mel)
+        mem = o.memory(encoded)
+        cpu_enc = time.perf_counter() - t
+        t = time.perf_counter()
+        cpu_ids = o.session(cfg["max_positions"], mem).greedy(first, steps)
+        cpu_dec = time.perf_counter() - t
+        out["cpu"] = dict(encode_ms=cpu_enc * 1e3, decode_tokens_per_s=steps / cpu_dec, threads=threads,
+                          kind="port", ids_match=cpu_ids.tolist() == ref.tolist())
+    return out
+
+
 def cpu_baseline(rn, cfg, cache, budget_s: float = 10.0):
     """The oracle (C restatement of the reference path) on the host cores, with
     the reference's thread policy min(cores - 1, 6) (crates/kernels/src/pool.rs:48-52)."""
@@ -253,7 +302,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="decode only")
-    ap.add_argument("--extras", default="gemv,prefill_256,decode_batch64",
+    ap.add_argument("--extras", default="gemv,prefill_256,decode_batch64,whistle",
                     help="comma-separated secondary measurements to run")
     ap.add_argument("--profile-steps", type=int, default=DECODE_TOKENS,
                     help="greedy steps timed kernel by kernel for the roofline")
@@ -287,7 +336,8 @@ def main() -> int:
         wanted = {e.strip() for e in args.extras.split(",") if e.strip()}
         for name, fn in (("gemv", lambda: bench_gemv(rn)),
                          ("prefill_256", lambda: bench_prefill(rn, model, cfg)),
-                         ("decode_batch64", lambda: bench_batch(rn, model, cfg))):
+                         ("decode_batch64", lambda: bench_batch(rn, model, cfg)),
+                         ("whistle", lambda: bench_whistle(rn, with_cpu=not args.no_cpu))):
             if name not in wanted:
                 continue
             log(f"bench: {name}")
