@@ -36,8 +36,7 @@ GEMV_UNIT_BYTES = 1_189_888    # one 2048x512 int8 matvec: W 1,048,576 + sW 131,
 DECODE_TOKENS = 64
 CONTEXT = 256
 KERNEL_NAMES = {
-    "qkv": "gemv_kernel<512,4,norm,store,panel> (fused QKV)",
-    "attention": "attend_kernel<decode>",
+    "qkv_attention": "qkv_attend_kernel<512,norm> (norm + a head's q/k/v rows + rotary + fp16 append + attention)",
     "out": "gemv_kernel<512,2,quant,residual,panel> (out)",
     "gate_up": "gemv_kernel<512,8,norm,silu,panel> (gate/up)",
     "down": "gemv_kernel<2048,2,quant,residual,panel> (down)",
@@ -50,8 +49,6 @@ KERNEL_NAMES = {
 # (FETCH x2.000, WRITE x1.000). Recorded in profiles/decode_b1_needle20_traffic.md;
 # they describe the kernels as built when measured and are re-measured with them.
 PMC_TRAFFIC = {
-    "qkv": 1_004_397,
-    "attention": 828_295,
     "out": 391_312,
     "gate_up": 2_488_966,
     "down": 1_393_521,
@@ -111,8 +108,8 @@ def decode_kernel_bytes(cfg, context: int, steps: int) -> dict:
     mean_cached = context + (steps - 1) / 2.0                        # cache rows read per attention launch
     blocks = (v + 7) // 8
     return {
-        "qkv": q(3 * d, d) + 4 * d + 4 * d + 4 * 3 * d,               # W, x, gains, q/k/v out
-        "attention": h * 2 * mean_cached * hd * 2 + 4 * 3 * d + h * 2 * hd * 2 + 4 * d,
+        # W rows of every head, x, gains, K/V rows read, the new K/V row written, the output
+        "qkv_attention": q(3 * d, d) + 4 * d + 4 * d + h * 2 * mean_cached * hd * 2 + h * 2 * hd * 2 + 4 * d,
         "out": q(d, d) + 4 * d + 2 * 4 * d,                           # W, attention in, residual read+write
         "gate_up": q(2 * f, d) + 4 * d + 4 * d + 4 * f,               # W, x, gains, silu(gate)*up out
         "down": q(d, f) + 4 * f + 2 * 4 * d,

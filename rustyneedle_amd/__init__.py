@@ -28,7 +28,7 @@ FORM_PANEL = 0
 FORM_PLANE = 1
 
 # Kernel kinds of rn_session_profile_step, in RN_PROFILE_* order.
-PROFILE_KINDS = ("qkv", "attention", "out", "gate_up", "down", "logits", "final")
+PROFILE_KINDS = ("qkv_attention", "out", "gate_up", "down", "logits", "final")
 
 # The decoder of the decode / prefill / batch workloads: 20 layers, d_model 512,
 # 8 heads of 64, rotary base 10000, RMSNorm eps 1e-6, gated FFN 512->2048->512,

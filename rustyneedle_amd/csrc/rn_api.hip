@@ -111,7 +111,6 @@ struct rn_session {
     __half* kc = nullptr;
     __half* vc = nullptr;
     float* x = nullptr;
-    float* qkv = nullptr;
     float* attn = nullptr;
     float* ffh = nullptr;
     float* hidden = nullptr;
@@ -177,6 +176,7 @@ int rn_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
 }
 int rn_memcpy_dtod(void* dst, const void* src, size_t bytes) {
     RN_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    RN_HIP(hipStreamSynchronize(nullptr));  // a device-to-device copy may return before it ends
     return RN_OK;
 }
 int rn_stream_create(void** stream) {
@@ -576,7 +576,7 @@ int rn_session_create(const rn_model* m, int capacity, rn_session** out) {
     s->model = m;
     s->capacity = capacity;
     const size_t ce = cache_elems(c, capacity), d = c.d_model;
-    const size_t total = 2 * align_up(ce * 2) + align_up(4 * d) * 4 + align_up(4 * 3 * d) + align_up(4 * (size_t)c.ffn) +
+    const size_t total = 2 * align_up(ce * 2) + align_up(4 * d) * 4 + align_up(4 * (size_t)c.ffn) +
                          align_up(4 * (size_t)c.vocab) + align_up(sizeof(DecodeState)) + align_up(4 * (size_t)capacity) +
                          align_up(8 * (size_t)c.vocab);
     if (hipMalloc(&s->arena, total) != hipSuccess) {
@@ -587,7 +587,6 @@ int rn_session_create(const rn_model* m, int capacity, rn_session** out) {
     s->kc = (__half*)a.take(ce * 2);
     s->vc = (__half*)a.take(ce * 2);
     s->x = (float*)a.take(4 * d);
-    s->qkv = (float*)a.take(4 * 3 * d);
     s->attn = (float*)a.take(4 * d);
     s->ffh = (float*)a.take(4 * (size_t)c.ffn);
     s->hidden = (float*)a.take(4 * d);
@@ -623,9 +622,12 @@ int rn_session_clone(const rn_session* s, rn_session** out) {
     int rc = rn_session_create(s->model, s->capacity, &t);
     if (rc) return rc;
     RN_HIP(hipStreamSynchronize(s->stream));
-    // Everything in the arena up to the id buffer is state; copy it wholesale.
+    // Everything in the arena up to the id buffer is state; copy it wholesale,
+    // on the clone's stream (a device-to-device hipMemcpy may return before
+    // the copy ends, and the null stream does not order the session streams).
     const size_t bytes = (size_t)((char*)s->ids - (char*)s->arena);
-    RN_HIP(hipMemcpy(t->arena, s->arena, bytes, hipMemcpyDeviceToDevice));
+    RN_HIP(hipMemcpyAsync(t->arena, s->arena, bytes, hipMemcpyDeviceToDevice, t->stream));
+    RN_HIP(hipStreamSynchronize(t->stream));
     t->length = s->length;
     t->has_hidden = s->has_hidden;
     *out = t;
@@ -717,37 +719,27 @@ static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) 
     for (int l = 0; l < c.layers; ++l) {
         const LayerDev& L = m->layers[l];
         {
-            GemvParams p{};
-            p.nseg = 1;
-            p.seg[0] = Segment{L.qkv.W, L.qkv.sW, s->qkv, nullptr, 3 * d, 0};
-            p.x = s->x;
-            p.gain = L.norm_attn;
-            p.eps = c.norm_eps;
-            p.embW = m->embedding.W;
-            p.embS = m->embedding.sW;
-            p.embed_scale = m->embed_scale;
-            p.vocab = c.vocab;
-            p.x_out = s->x;
-            p.state = s->state;
-            const int rpb = gemv_rows_per_block(3 * d, d, kStore);
-            RN_PROFILED(RN_PROFILE_QKV, launch_gemv(p, d, l == 0 ? kEmbedNorm : kNorm, kStore, kPanel, rpb, (3 * d + rpb - 1) / rpb, st));
-        }
-        {
-            AttendParams a{};
-            a.qkv = s->qkv;
-            a.kc = s->kc;
-            a.vc = s->vc;
-            a.layer = l;
-            a.heads = c.heads;
+            QkvAttendParams a{};
+            a.W = L.qkv.W;
+            a.sW = L.qkv.sW;
+            a.x = s->x;
+            a.gain = L.norm_attn;
+            a.eps = c.norm_eps;
+            a.embW = m->embedding.W;
+            a.embS = m->embedding.sW;
+            a.embed_scale = m->embed_scale;
+            a.vocab = c.vocab;
+            a.x_out = s->x;
+            const size_t layer_base = (size_t)l * c.heads * s->capacity * c.head_dim;
+            a.kc = s->kc + layer_base;
+            a.vc = s->vc + layer_base;
             a.capacity = s->capacity;
-            a.d_model = d;
-            a.pos = &s->state->pos;
-            a.pos_stride = 0;
+            a.state = s->state;
             a.rope_cos = m->rope_cos;
             a.rope_sin = m->rope_sin;
             a.out = s->attn;
-            a.error = &s->state->error;
-            RN_PROFILED(RN_PROFILE_ATTENTION, launch_attend(a, kAttendDecode, c.heads, 1, s->capacity, st));
+            RN_PROFILED(RN_PROFILE_QKV_ATTENTION,
+                        launch_qkv_attend(a, d, l == 0 ? kEmbedNorm : kNorm, c.heads, st));
         }
         {
             GemvParams p{};
@@ -1249,7 +1241,7 @@ struct rn_whistle {
     __half *kcache = nullptr, *vcache = nullptr;
     int capacity = 0, length = 0;
     bool has_hidden = false;
-    float *x = nullptr, *qkv = nullptr, *attn = nullptr, *cq = nullptr, *cctx = nullptr, *catt = nullptr;
+    float *x = nullptr, *attn = nullptr, *cq = nullptr, *cctx = nullptr, *catt = nullptr;
     float *ffh = nullptr, *hidden = nullptr, *logits = nullptr;
     int8_t* cqc = nullptr;
     float* cqs = nullptr;
@@ -1460,7 +1452,6 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
     w->cctx = (float*)a.take(4 * d);
     w->catt = (float*)a.take(4 * d);
     w->hidden = (float*)a.take(4 * d);
-    w->qkv = (float*)a.take(4 * 3 * d);
     w->ffh = (float*)a.take(4 * f);
     w->logits = (float*)a.take(4 * V);
     w->cqc = (int8_t*)a.take(d);
@@ -1661,37 +1652,26 @@ static int enqueue_whistle_step(rn_whistle* w, bool greedy) {
     for (int l = 0; l < c.dec_layers; ++l) {
         const WDecLayerDev& L = w->dec[l];
         {
-            GemvParams p{};
-            p.nseg = 1;
-            p.seg[0] = Segment{L.qkv.W, L.qkv.sW, w->qkv, nullptr, 3 * d, 0};
-            p.x = w->x;
-            p.gain = L.norm_attn;
-            p.eps = c.norm_eps;
-            p.embW = w->embedding.W;
-            p.embS = w->embedding.sW;
-            p.embed_scale = w->embed_scale;
-            p.vocab = c.vocab;
-            p.x_out = w->x;
-            p.state = w->state;
-            const int rpb = gemv_rows_per_block(3 * d, d, kStore);
-            RN_HIP(launch_gemv(p, d, l == 0 ? kEmbedNorm : kNorm, kStore, kPanel, rpb, (3 * d + rpb - 1) / rpb, st));
-        }
-        {
-            AttendParams a{};
-            a.qkv = w->qkv;
-            a.kc = w->kcache;
-            a.vc = w->vcache;
-            a.layer = l;
-            a.heads = H;
+            QkvAttendParams a{};
+            a.W = L.qkv.W;
+            a.sW = L.qkv.sW;
+            a.x = w->x;
+            a.gain = L.norm_attn;
+            a.eps = c.norm_eps;
+            a.embW = w->embedding.W;
+            a.embS = w->embedding.sW;
+            a.embed_scale = w->embed_scale;
+            a.vocab = c.vocab;
+            a.x_out = w->x;
+            const size_t layer_base = (size_t)l * H * w->capacity * 64;
+            a.kc = w->kcache + layer_base;
+            a.vc = w->vcache + layer_base;
             a.capacity = w->capacity;
-            a.d_model = d;
-            a.pos = &w->state->pos;
-            a.pos_stride = 0;
+            a.state = w->state;
             a.rope_cos = w->rope_cos;
             a.rope_sin = w->rope_sin;
             a.out = w->attn;
-            a.error = &w->state->error;
-            RN_HIP(launch_attend(a, kAttendDecode, H, 1, w->capacity, st));
+            RN_HIP(launch_qkv_attend(a, d, l == 0 ? kEmbedNorm : kNorm, H, st));
         }
         {
             GemvParams p{};

@@ -40,7 +40,8 @@ __device__ __forceinline__ void unpack8(const uint4& raw, float* out) {
 
 // T2 for one key row held as 16 dims per lane (lane li owns dims 16li..16li+15,
 // i.e. the four 4-dim sub-sums 4li..4li+3): two tree levels inside the lane,
-// the last two across lanes (xor 1, xor 2).
+// the last two across lanes (xor 1, xor 2; the four lanes of a row are one
+// DPP quad).
 __device__ __forceinline__ float score_row(const float* q16, const uint4& ka, const uint4& kb) {
     float k[16];
     unpack8(ka, k);
@@ -54,8 +55,8 @@ __device__ __forceinline__ float score_row(const float* q16, const uint4& ka, co
         part[j] = s;
     }
     float s = (part[0] + part[1]) + (part[2] + part[3]);
-    s = s + __shfl_xor(s, 1, 4);
-    s = s + __shfl_xor(s, 2, 4);
+    s = s + __int_as_float(dpp_move<0xb1>(__float_as_int(s)));  // lane ^ 1
+    s = s + __int_as_float(dpp_move<0x4e>(__float_as_int(s)));  // lane ^ 2
     return s;
 }
 
@@ -326,6 +327,329 @@ hipError_t launch_rope_append(const float* qkv, float* q_out, __half* kc, __half
     if (count <= 0) return hipSuccess;
     rn_launch(rope_append_kernel, dim3(count), dim3(256), 0, stream, qkv, q_out, kc, vc, layer, heads,
                        capacity, d_model, first, rope_cos, rope_sin);
+    return hipGetLastError();
+}
+
+// Batch-1 decode: the norm + q/k/v product of one head, its rotary and fp16
+// append, and its attention, in one 512-thread block per head
+// (session.rs:94-120 with model/src/attention.rs:96-154 for one token).
+//
+// A head needs only its own 192 rows of the fused q/k/v matrix (q, k and v rows
+// 64h..64h+63), so the product splits by head with no exchange between blocks.
+// The block streams about 190 KB (weights, scales, K/V rows) through one CU, so
+// the wave that computes the input codes is kept free of that stream:
+//   1. wave 0: reads x (or gathers the embedding row times sqrt(d),
+//      session.rs:85-90), its zero-centred RMSNorm (eight-lane sum of
+//      ops.rs:7-17) and int8 codes (ops.rs:103-118) into LDS, while waves 1-7
+//      request the head's weight rows and scales; after the barrier every wave
+//      requests its share of the first KC x 128 key rows and 32 x VC value rows;
+//   2. waves 1-7: v_dot4 over 16-code chunks, lane pairs joined into 32-code
+//      group sums; thread 64 + r runs row r's group epilogue
+//      fmaf(acc, sW * sx, total) in group order (panel.rs:184-188);
+//   3. rotate-half rotary of q and k at the position (ops.rs:131-141), fp16
+//      append of k and v at that position;
+//   4. scores (tree T2 of score_row), peak, fast_exp weights, then the value
+//      sums in tree T3 (32 position classes, 4 dims per thread), one multiply
+//      by 1/total.
+// The float results are identical to the separate product + attend_kernel path.
+template <int K, int PRO, int KC, int VC>
+__global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
+    constexpr int NT = 512;
+    constexpr int G = K / kGroup;            // weight scales per row
+    constexpr int CPR = K / 16;              // 16-code chunks per row
+    constexpr int ROWS = 3 * kHeadDim;       // q, k and v rows of one head
+    constexpr int CHUNKS = ROWS * CPR;
+    constexpr int LW = NT - 64;                // weight-loading threads (waves 1-7)
+    constexpr int NLW = (CHUNKS + LW - 1) / LW;
+    constexpr int E = K / 64;                // prologue values per lane of wave 0
+    constexpr int KROWS = NT / 4;            // key rows per pass
+    static_assert(E % 2 == 0 && G % 4 == 0 && CPR % 2 == 0, "whole float pairs, scale quads, code pairs");
+    static_assert(64 + ROWS <= NT, "one epilogue thread per row in waves 1-7");
+    extern __shared__ float scores[];
+    __shared__ __align__(16) int8_t xq_s[K];
+    __shared__ __align__(16) float sq_s[K];
+    __shared__ __align__(16) int acc_s[ROWS * G];
+    __shared__ float qkv_s[ROWS];
+    __shared__ float q_s[kHeadDim];
+    __shared__ __align__(16) __half new_s[2][kHeadDim];
+    __shared__ __align__(16) float part_s[kClasses][kHeadDim];
+    __shared__ float total_s[kClasses];
+    __shared__ float peak_s[NT / 64];
+    __shared__ float sx_s;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = blockIdx.x;
+    const int r = tid >> 2, li = tid & 3;     // score layout: key row slot, 16-dim quarter
+    const int j = tid >> 4, dq = tid & 15;    // value layout: position class, dims 4dq..4dq+3
+    const size_t head_base = (size_t)h * p.capacity * kHeadDim;
+    const __half* Kc = p.kc + head_base;
+    const __half* Vc = p.vc + head_base;
+    const int rows = p.capacity;
+
+    const int pos = p.state->pos;
+    // 1. wave 0: the input row, its norm and its int8 codes (LDS traffic inside
+    // one wave: DS operations of a wave complete in order). Waves 1-7 request
+    // the head's weight rows and scales meanwhile.
+    auto global_row = [&](int hr) -> size_t {
+        return (size_t)(hr / kHeadDim) * K + (size_t)h * kHeadDim + (hr % kHeadDim);
+    };
+    int4 w[NLW];
+    float4 sv[G / 4];
+    if (wave == 0) {
+        float v[E];
+        float gv[E];
+        if constexpr (PRO == kEmbedNorm) {
+            uint32_t token = p.state->token;
+            if (token >= (uint32_t)p.vocab) {
+                if (lane == 0 && h == 0) atomicOr(&p.state->error, 1);
+                token = 0;
+            }
+            const int8_t* er = p.embW + (size_t)token * K + lane * E;
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                v[e] = ((float)er[e] * p.embS[(size_t)token * G + (lane * E + e) / kGroup]) * p.embed_scale;
+            if (h == 0)
+#pragma unroll
+                for (int e = 0; e < E; ++e) p.x_out[lane * E + e] = v[e];
+        } else {
+            load_floats<E>(p.x + lane * E, v);
+        }
+        load_floats<E>(p.gain + lane * E, gv);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int idx = lane * E + e;
+            sq_s[(idx % 8) * (K / 8) + idx / 8] = v[e] * v[e];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float s = 0.0f;
+        if (lane < 8) {
+            const float4* run = reinterpret_cast<const float4*>(sq_s + lane * (K / 8));
+            float4 t[K / 32];
+#pragma unroll
+            for (int c = 0; c < K / 32; ++c) t[c] = run[c];
+#pragma unroll
+            for (int c = 0; c < K / 32; ++c) {
+                s = s + t[c].x;
+                s = s + t[c].y;
+                s = s + t[c].z;
+                s = s + t[c].w;
+            }
+        }
+        float total = sum_lanes_0_to_7(s);
+        total = total + 0.0f;  // the (empty) tail of ops.rs:15-16
+        const float inverse = 1.0f / sqrtf(total / (float)K + p.eps);
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = ((1.0f + gv[e]) * v[e]) * inverse;
+        float peak = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
+        peak = wave_max(peak);
+        const float sx = int8_scale_from_peak(peak);
+        float y[E];
+        quotients<E>(v, sx, y);
+#pragma unroll
+        for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)code_of_quotient(y[e]);
+        if (lane == 0) sx_s = sx;
+    } else {
+        // chunk c = LW jj + (tid - 64) is chunk c % CPR of head row c / CPR
+        // (q rows 0..63, k rows 64..127, v rows 128..191); thread 64 + r holds
+        // row r's scales (threads past row 191 repeat row 191: one cache line)
+#pragma unroll
+        for (int jj = 0; jj < NLW; ++jj) {
+            const int c = min(LW * jj + tid - 64, CHUNKS - 1);
+            w[jj] = *reinterpret_cast<const int4*>(p.W + global_row(c / CPR) * K + (c % CPR) * 16);
+        }
+        const float4* src = reinterpret_cast<const float4*>(p.sW + global_row(min(tid - 64, ROWS - 1)) * G);
+#pragma unroll
+        for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
+    }
+    if (pos < 0 || pos >= p.capacity) {  // uniform over the block
+        if (tid == 0) atomicOr(&p.state->error, 2);
+        return;
+    }
+    __syncthreads();
+
+    // 2. every wave: its share of the first cache rows, clamped into the cache
+    // (no branch around these loads: it would make later wait counts
+    // conservative). Requested only now, so that wave 0's codes do not wait
+    // behind them; they arrive while waves 1-7 run the product.
+    uint4 kr[KC][2];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+        const __half* row = Kc + (size_t)min(r + KROWS * c, rows - 1) * kHeadDim + 16 * li;
+        kr[c][0] = *reinterpret_cast<const uint4*>(row);
+        kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
+    }
+    uint2 vr[VC];
+#pragma unroll
+    for (int c = 0; c < VC; ++c)
+        vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(j + kClasses * c, rows - 1) * kHeadDim + 4 * dq);
+
+    // 3. waves 1-7: exact int32 group sums of the 192 rows, then the row epilogues
+    if (wave != 0) {
+#pragma unroll
+        for (int jj = 0; jj < NLW; ++jj) {
+            const int c = LW * jj + tid - 64;
+            const int4 xc = *reinterpret_cast<const int4*>(xq_s + (min(c, CHUNKS - 1) % CPR) * 16);
+            int part = dot16(w[jj], xc, 0);
+            part = part + dpp_move<0xb1>(part);  // the pair partner (lane ^ 1: chunk c ^ 1)
+            if ((tid & 1) == 0 && c < CHUNKS) acc_s[(c / CPR) * G + (c % CPR) / 2] = part;
+        }
+    }
+    __syncthreads();
+    if (tid >= 64 && tid < 64 + ROWS) {
+        const int row = tid - 64;
+        const float sx = sx_s;
+        const int4* arow = reinterpret_cast<const int4*>(acc_s + row * G);
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < G / 4; ++i) {
+            const int4 a4 = arow[i];
+            total = fmaf((float)a4.x, sv[i].x * sx, total);
+            total = fmaf((float)a4.y, sv[i].y * sx, total);
+            total = fmaf((float)a4.z, sv[i].z * sx, total);
+            total = fmaf((float)a4.w, sv[i].w * sx, total);
+        }
+        qkv_s[row] = total;
+    }
+    __syncthreads();
+
+    // 4. rotary at `pos` and the fp16 append
+    if (tid < kHeadDim / 2) {
+        const int i = tid, half = kHeadDim / 2;
+        const float c = p.rope_cos[(size_t)pos * half + i];
+        const float s = p.rope_sin[(size_t)pos * half + i];
+        const float qa = qkv_s[i], qb = qkv_s[i + half];
+        q_s[i] = qa * c - qb * s;
+        q_s[i + half] = qb * c + qa * s;
+        const float ka = qkv_s[kHeadDim + i], kb = qkv_s[kHeadDim + i + half];
+        const __half k0 = __float2half_rn(ka * c - kb * s), k1 = __float2half_rn(kb * c + ka * s);
+        const __half v0 = __float2half_rn(qkv_s[2 * kHeadDim + i]);
+        const __half v1 = __float2half_rn(qkv_s[2 * kHeadDim + i + half]);
+        new_s[0][i] = k0;
+        new_s[0][i + half] = k1;
+        new_s[1][i] = v0;
+        new_s[1][i + half] = v1;
+        __half* Kw = const_cast<__half*>(Kc) + (size_t)pos * kHeadDim;
+        __half* Vw = const_cast<__half*>(Vc) + (size_t)pos * kHeadDim;
+        Kw[i] = k0;
+        Kw[i + half] = k1;
+        Vw[i] = v0;
+        Vw[i + half] = v1;
+    }
+    __syncthreads();
+
+    // 5. scores (T2), KROWS key rows per pass
+    const int nglobal = pos, length = pos + 1;
+    const float inverse_root = 1.0f / sqrtf((float)kHeadDim);
+    float q16[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q16[i] = q_s[16 * li + i];
+    for (int base = 0; base < nglobal; base += KROWS * KC) {
+        if (base > 0) {
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                const __half* row = Kc + (size_t)min(base + r + KROWS * c, rows - 1) * kHeadDim + 16 * li;
+                kr[c][0] = *reinterpret_cast<const uint4*>(row);
+                kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            const int pp = base + r + KROWS * c;
+            if (base + KROWS * c + 16 * wave < nglobal) {  // wave-uniform: the pass holds live rows
+                const float s = score_row(q16, kr[c][0], kr[c][1]);
+                if (li == 0 && pp < nglobal) scores[pp] = s * inverse_root;
+            }
+        }
+    }
+    if (tid < 4) {
+        const uint4 ka = *reinterpret_cast<const uint4*>(&new_s[0][16 * li]);
+        const uint4 kb = *reinterpret_cast<const uint4*>(&new_s[0][16 * li + 8]);
+        const float s = score_row(q16, ka, kb);
+        if (li == 0) scores[nglobal] = s * inverse_root;
+    }
+    __syncthreads();
+
+    // 6. peak (order-free) and the fast_exp weights
+    float m = -INFINITY;
+    for (int pp = tid; pp < length; pp += NT) m = fmaxf(m, scores[pp]);
+    m = wave_max(m);
+    if (lane == 0) peak_s[wave] = m;
+    __syncthreads();
+    float peak = peak_s[0];
+#pragma unroll
+    for (int w8 = 1; w8 < NT / 64; ++w8) peak = fmaxf(peak, peak_s[w8]);
+    for (int pp = tid; pp < length; pp += NT) scores[pp] = fast_exp(scores[pp] - peak);
+    __syncthreads();
+
+    // 7. weighted values (T3): thread (j, dq) walks positions j, j+32, ... in order
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float total = 0.0f;
+    const int last = nglobal > 0 ? nglobal - 1 : 0;
+    for (int base = 0; base < nglobal; base += kClasses * VC) {
+        if (base > 0) {
+#pragma unroll
+            for (int c = 0; c < VC; ++c)
+                vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(base + j + kClasses * c, rows - 1) * kHeadDim +
+                                                        4 * dq);
+        }
+#pragma unroll
+        for (int c = 0; c < VC; ++c) {
+            const int pp = base + j + kClasses * c;
+            const bool ok = pp < nglobal;
+            const float e = scores[min(pp, last)];
+            const __half2 h01 = *reinterpret_cast<const __half2*>(&vr[c].x);
+            const __half2 h23 = *reinterpret_cast<const __half2*>(&vr[c].y);
+            const float vv[4] = {__low2float(h01), __high2float(h01), __low2float(h23), __high2float(h23)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float t = a[i] + e * vv[i];
+                a[i] = ok ? t : a[i];
+            }
+            const float tt = total + e;
+            total = ok ? tt : total;
+        }
+    }
+    if (j == (nglobal & (kClasses - 1))) {  // the newest position closes its class
+        const float e = scores[nglobal];
+        const __half2 h01 = *reinterpret_cast<const __half2*>(&new_s[1][4 * dq]);
+        const __half2 h23 = *reinterpret_cast<const __half2*>(&new_s[1][4 * dq + 2]);
+        const float vv[4] = {__low2float(h01), __high2float(h01), __low2float(h23), __high2float(h23)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = a[i] + e * vv[i];
+        total = total + e;
+    }
+    *reinterpret_cast<float4*>(&part_s[j][4 * dq]) = make_float4(a[0], a[1], a[2], a[3]);
+    if (dq == 0) total_s[j] = total;
+    __syncthreads();
+    if (tid < kHeadDim) {
+        float o = 0.0f, t = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kClasses; ++k) {
+            o = o + part_s[k][tid];
+            t = t + total_s[k];
+        }
+        p.out[h * kHeadDim + tid] = o * (1.0f / t);
+    }
+}
+
+hipError_t launch_qkv_attend(const QkvAttendParams& p, int d_model, int prologue, int heads, hipStream_t stream) {
+    const size_t lds = sizeof(float) * (size_t)(p.capacity > 0 ? p.capacity : 1);
+    if (lds > 96 * 1024 || heads < 1 || d_model != heads * kHeadDim) return hipErrorInvalidValue;
+    const dim3 grid(heads), block(512);
+    if (d_model == 512) {
+        if (prologue == kNorm) rn_launch((qkv_attend_kernel<512, kNorm, 3, 10>), grid, block, lds, stream, p);
+        else if (prologue == kEmbedNorm) rn_launch((qkv_attend_kernel<512, kEmbedNorm, 3, 10>), grid, block, lds, stream, p);
+        else return hipErrorInvalidValue;
+    } else if (d_model == 384) {
+        if (prologue == kNorm) rn_launch((qkv_attend_kernel<384, kNorm, 3, 10>), grid, block, lds, stream, p);
+        else if (prologue == kEmbedNorm) rn_launch((qkv_attend_kernel<384, kEmbedNorm, 3, 10>), grid, block, lds, stream, p);
+        else return hipErrorInvalidValue;
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -48,17 +48,19 @@ __device__ __forceinline__ int code_of_quotient(float y) {
 }
 
 // The quotients value/scale of quantise_one for E values of a lane, without a
-// division per element: y = value * (1/scale) is within 1.5 * 2^-23 * |y| of
-// the exact quotient and the correctly rounded quotient within 2^-24 of it, so
+// division per element: with r = v_rcp_f32(scale), within 1 ulp of 1/scale for
+// scales in [2^-100, 2^100], y = value * r is within 1.5 * 2^-23 * |y| of the
+// exact quotient and the correctly rounded quotient within 2^-24 of it, so
 // unless y lies within |y| * 2^-21 of a half-integer both round to the same
 // integer (a tie would put y on the boundary). When any lane of the wave has a
-// value that close, the whole wave takes the exact division instead (a
-// wave-uniform branch, so the common path carries no division code). The codes
-// are bit-identical to quantise_one for every input, NaN and inf included.
+// value that close, or the scale lies outside that range, the whole wave takes
+// the exact division instead (a wave-uniform branch, so the common path carries
+// no division code). The codes are bit-identical to quantise_one for every
+// input, NaN and inf included.
 template <int E>
 __device__ __forceinline__ void quotients(const float* v, float scale, float* y) {
-    const float inv = 1.0f / scale;
-    bool near = false;
+    const float inv = __builtin_amdgcn_rcpf(scale);
+    bool near = !(scale >= 0x1p-100f && scale <= 0x1p+100f);
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         y[e] = v[e] * inv;
@@ -71,22 +73,67 @@ __device__ __forceinline__ void quotients(const float* v, float scale, float* y)
     }
 }
 
-// ops.rs:103-110
-__device__ __forceinline__ float int8_scale_from_peak(float peak) { return peak > 0.0f ? peak / 127.0f : 1.0f; }
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+// ops.rs:103-110: peak / 127 (1.0 when the peak is not positive). The quotient
+// is formed without a division: q0 = peak * RN(1/127), then one fma correction
+// with the exact residual peak - 127 q0; the result equals the correctly
+// rounded peak / 127 for every positive finite float (checked exhaustively on
+// the CPU over all 2^31 - 2^23 - 1 of them), and an infinite peak stays infinite.
+__device__ __forceinline__ float int8_scale_from_peak(float peak) {
+    constexpr float kInv127 = 1.0f / 127.0f;
+    const float q0 = peak * kInv127;
+    const float q = fmaf(fmaf(-q0, 127.0f, peak), kInv127, q0);
+    return peak > 0.0f ? (peak == __builtin_inff() ? peak : q) : 1.0f;
 }
 
+// Cross-lane moves inside rows of 16 lanes (DPP: no LDS round trip). CTRL:
+// quad_perm [1,0,3,2] = 0xb1, quad_perm [2,3,0,1] = 0x4e, row_half_mirror =
+// 0x141, row_mirror = 0x140. A lane whose source is invalid keeps its value.
+template <int CTRL>
+__device__ __forceinline__ int dpp_move(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float lane_float(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Maximum over the 64 lanes of a full wave, the same in every lane. The
+// maximum is order-free, so any reduction order gives the same value.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __int_as_float(dpp_move<0xb1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_move<0x4e>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_move<0x141>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_move<0x140>(__float_as_int(v))));
+    return fmaxf(fmaxf(lane_float(v, 0), lane_float(v, 16)), fmaxf(lane_float(v, 32), lane_float(v, 48)));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t max_with_dpp_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t)dpp_move<CTRL>((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)dpp_move<CTRL>((int)(uint32_t)(v >> 32));
+    const uint64_t other = ((uint64_t)hi << 32) | lo;
+    return other > v ? other : v;
+}
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int lane) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+    return ((uint64_t)hi << 32) | lo;
+}
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = max_with_dpp_u64<0xb1>(v);
+    v = max_with_dpp_u64<0x4e>(v);
+    v = max_with_dpp_u64<0x141>(v);
+    v = max_with_dpp_u64<0x140>(v);
+    const uint64_t a = lane_u64(v, 0), b = lane_u64(v, 16), c = lane_u64(v, 32), d = lane_u64(v, 48);
+    const uint64_t ab = b > a ? b : a, cd = d > c ? d : c;
+    return cd > ab ? cd : ab;
+}
+
+// ops.rs:14-16: the eight lane sums (held by lanes 0..7) added in lane order.
+__device__ __forceinline__ float sum_lanes_0_to_7(float s) {
+    float total = 0.0f;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        uint64_t other = __shfl_xor(v, o, kWave);
-        v = other > v ? other : v;
-    }
-    return v;
+    for (int q = 0; q < 8; ++q) total = total + lane_float(s, q);
+    return total;
 }
 
 // Four int8 x int8 products added to an int32 accumulator (v_dot4_i32_i8).
@@ -112,6 +159,28 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t index) {
 
 __device__ __forceinline__ uint32_t argmax_index(uint64_t key) {
     return key == 0ull ? 0u : 0xffffffffu - (uint32_t)(key & 0xffffffffull);
+}
+
+// E consecutive floats (E even) with the widest aligned loads.
+template <int E>
+__device__ __forceinline__ void load_floats(const float* src, float* v) {
+    if constexpr (E % 4 == 0) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(src + e);
+            v[e] = t.x;
+            v[e + 1] = t.y;
+            v[e + 2] = t.z;
+            v[e + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; e += 2) {
+            const float2 t = *reinterpret_cast<const float2*>(src + e);
+            v[e] = t.x;
+            v[e + 1] = t.y;
+        }
+    }
 }
 
 }  // namespace rn

@@ -272,9 +272,7 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
             const float* r = sq + lane * run;
             for (int c = 0; c < run; ++c) part = part + r[c];
         }
-        float total = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) total = total + __shfl(part, j, kWave);
+        float total = sum_lanes_0_to_7(part);
         total = total + 0.0f;  // the empty tail of the 8-lane sum
         const float inverse = 1.0f / sqrtf(total / (float)n + eps);
         const float2* g2 = reinterpret_cast<const float2*>(gain);

@@ -25,28 +25,6 @@
 
 namespace rn {
 
-// E consecutive floats (E even) with the widest aligned loads.
-template <int E>
-__device__ __forceinline__ void load_floats(const float* src, float* v) {
-    if constexpr (E % 4 == 0) {
-#pragma unroll
-        for (int e = 0; e < E; e += 4) {
-            const float4 t = *reinterpret_cast<const float4*>(src + e);
-            v[e] = t.x;
-            v[e + 1] = t.y;
-            v[e + 2] = t.z;
-            v[e + 3] = t.w;
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < E; e += 2) {
-            const float2 t = *reinterpret_cast<const float2*>(src + e);
-            v[e] = t.x;
-            v[e + 1] = t.y;
-        }
-    }
-}
-
 template <int K, int ROWS, int PRO, int EPI, int FORM>
 __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     constexpr int G = K / kGroup;                       // groups per row
@@ -166,9 +144,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
                     s = s + t.w;
                 }
             }
-            float total = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) total = total + __shfl(s, j, 64);
+            float total = sum_lanes_0_to_7(s);
             total = total + 0.0f;  // the (empty) tail of ops.rs:15-16
             const float mean_square = total / (float)K;
             const float inverse = 1.0f / sqrtf(mean_square + p.eps);

@@ -113,6 +113,29 @@ struct AttendParams {
 hipError_t launch_attend(const AttendParams& p, int mode, int grid_x, int grid_y, int max_length,
                          hipStream_t stream);
 
+// Batch-1 decode: norm + the q/k/v rows of each head + rotary + fp16 append +
+// attention, one block per head (grid = heads, d_model = 64 heads).
+struct QkvAttendParams {
+    const int8_t* W;      // fused q/k/v codes [3 d][d]
+    const float* sW;      // [3 d][d/32]
+    const float* x;       // residual stream [d] (kNorm)
+    const float* gain;    // norm gains [d]
+    float eps;
+    const int8_t* embW;   // kEmbedNorm: embedding codes/scales, token from state
+    const float* embS;
+    float embed_scale;
+    int vocab;
+    float* x_out;         // kEmbedNorm: block 0 writes the embedded row
+    __half* kc;           // this layer's cache [heads][capacity][64]
+    __half* vc;
+    int capacity;
+    DecodeState* state;   // token, pos, error flags
+    const float* rope_cos;
+    const float* rope_sin;
+    float* out;           // [d] attention output, head h at 64 h
+};
+hipError_t launch_qkv_attend(const QkvAttendParams& p, int d_model, int prologue, int heads, hipStream_t stream);
+
 // Rotary + fp16 append for `count` tokens of one sequence (prefill): writes the
 // rotated queries to q_out [count][d] and keys/values into the cache.
 hipError_t launch_rope_append(const float* qkv, float* q_out, __half* kc, __half* vc, int layer, int heads,

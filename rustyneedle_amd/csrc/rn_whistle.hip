@@ -104,9 +104,7 @@ __global__ __launch_bounds__(256) void head_codes_kernel(HeadCodesParams p) {
         float s = 0.0f;
 #pragma unroll
         for (int c = 0; c < 8; ++c) s = s + __shfl(sq, 8 * c + (lane & 7), kWave);
-        float total = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) total = total + __shfl(s, j, kWave);
+        float total = sum_lanes_0_to_7(s);
         total = total + 0.0f;
         const float inverse = 1.0f / sqrtf(total / 64.0f + p.eps);
         v = ((1.0f + sec.gain[lane]) * v) * inverse;
@@ -227,9 +225,7 @@ __global__ __launch_bounds__(64) void cross_residual_kernel(const float* attende
     float s = 0.0f;
     if (lane < 8)
         for (int c = 0; c < n / 8; ++c) s = s + sq_s[lane * (n / 8) + c];
-    float total = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) total = total + __shfl(s, j, kWave);
+    float total = sum_lanes_0_to_7(s);
     total = total + 0.0f;
     const float inverse = 1.0f / sqrtf(total / (float)n + eps);
 #pragma unroll

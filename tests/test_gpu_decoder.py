@@ -48,6 +48,20 @@ def test_push_hidden_logits_and_cache(tiny, tiny_config):
     assert np.array_equal(gv.view(np.uint16), os_.values[:, :, :44])
 
 
+def test_push_over_long_cache(tiny, tiny_config):
+    """Caches longer than one pass of the fused head kernel's preloaded key
+    (512) and value (320) rows, and a position that starts a new class of 32."""
+    gm, om = tiny
+    k, v = rn.synthetic_cache(tiny_config, 575, "long")
+    gs, os_ = gm.session(640), om.session(640)
+    gs.set_cache(k, v)
+    os_.set_cache(k, v)
+    for tok in (5, 999, 17):
+        gs.push(tok)
+        os_.push(tok)
+        assert np.array_equal(_bits(gs.logits()), _bits(os_.logits()))
+
+
 def test_push_from_empty_session(tiny):
     gm, om = tiny
     gs, os_ = gm.session(8), om.session(8)
@@ -98,7 +112,7 @@ def test_profile_step_matches_greedy(tiny, tiny_config):
     b.decode_greedy(7, 6)
     assert len(a) == len(b) == 36
     assert np.array_equal(_bits(a.logits()), _bits(b.logits()))
-    assert prof["attention"]["per_step"] == tiny_config["layers"]
+    assert prof["qkv_attention"]["per_step"] == tiny_config["layers"]
     assert prof["logits"]["per_step"] == 1 and prof["final"]["per_step"] == 1
     assert all(p["us"] > 0 for p in prof.values())
 

@@ -1,22 +1,38 @@
-"""The GPU quantiser multiplies by the reciprocal of the scale and falls back to
-the division only near a rounding boundary (quantise_one_r in
-rustyneedle_amd/csrc/rn_device.hpp). This restates that rule in IEEE float32
-(numpy) and checks it against the defining division of ops.rs:112-118 on random
-and adversarial inputs: quotients within a few ulps of every half-integer, for
-scales over sixty decades."""
+"""The GPU quantiser's two division-free shortcuts (rustyneedle_amd/csrc/rn_device.hpp),
+checked against the defining divisions of ops.rs:103-118 in IEEE float32:
+
+- quotients: multiply by v_rcp_f32(scale), which is within 1 ulp of 1/scale, and
+  fall back to the division near a rounding boundary or for scales outside
+  [2^-100, 2^100]. Restated in numpy for each of the three reciprocals a 1-ulp
+  error allows, on random and adversarial inputs (quotients within a few ulps of
+  every half-integer) for scales over sixty decades;
+- int8_scale_from_peak: peak / 127 as q0 = peak * RN(1/127) plus one fma
+  correction, compared with the division by a small C program (every 97th
+  positive float here; all of them with RN_EXHAUSTIVE=1)."""
 from __future__ import annotations
 
+import os
+import subprocess
+
 import numpy as np
+import pytest
 
 f32 = np.float32
+HERE = os.path.dirname(os.path.abspath(__file__))
 
 
-def reciprocal_rule(v: np.ndarray, s: np.float32) -> np.ndarray:
+def reciprocal_rule(v: np.ndarray, s: np.float32, ulps: int = 0) -> np.ndarray:
     r = f32(1) / s
+    for _ in range(abs(ulps)):
+        r = np.nextafter(r, f32(np.inf) if ulps > 0 else f32(-np.inf))
     y = (v * r).astype(f32)
     h = (np.floor(y) + f32(0.5)).astype(f32)
     thr = (np.abs(y) * f32(2.0 ** -21) + f32(2.0 ** -30)).astype(f32)
     near = np.abs((y - h).astype(f32)) <= thr
+    if not (f32(2.0 ** -100) <= s <= f32(2.0 ** 100)):
+        near = np.ones_like(near)
+    # per element: the device sends a whole wave to the division when any lane
+    # is near, which only replaces more quotients by the exact ones
     y = np.where(near, (v / s).astype(f32), y)
     return np.clip(np.rint(y), -128, 127)
 
@@ -39,6 +55,18 @@ def test_reciprocal_rule_equals_division():
                 near = np.where(steps >= u, np.nextafter(near, f32(np.inf)), near)
                 near = np.where(steps <= -u, np.nextafter(near, f32(-np.inf)), near)
             v = np.concatenate([v, near, np.array([peak, -peak, 0.0, -0.0, np.nan, np.inf], f32)])
-            a, b = reciprocal_rule(v, s), division_rule(v, s)
-            same = (a == b) | (np.isnan(a) & np.isnan(b))
-            assert same.all(), (peak, v[~same][:4])
+            b = division_rule(v, s)
+            for ulps in (-1, 0, 1):
+                a = reciprocal_rule(v, s, ulps)
+                same = (a == b) | (np.isnan(a) & np.isnan(b))
+                assert same.all(), (peak, ulps, v[~same][:4])
+
+
+def test_scale_without_division_matches_division(tmp_path):
+    exe = tmp_path / "scale127"
+    subprocess.run(["gcc", "-O2", "-march=x86-64-v3", "-ffp-contract=off", "-fopenmp",
+                    os.path.join(HERE, "c", "scale127.c"), "-o", str(exe), "-lm"], check=True)
+    stride = "1" if os.environ.get("RN_EXHAUSTIVE") else "97"
+    out = subprocess.run([str(exe), stride], check=True, capture_output=True, text=True).stdout.split()
+    bad, checked = int(out[0]), int(out[1])
+    assert checked > 2_000_000 and bad == 0
