@@ -235,7 +235,8 @@ int rn_batch_stream(const rn_batch* batch, void** stream);
  * of int8 self-attention (encoder.rs:217-297) and a gated FFN; a decoder of
  * the Session kind with cross-attention after each self-attention
  * (session.rs:126-128, cross.rs:126-182); tied int8 logits. d_model 384 or
- * 512 with heads of 64, ffn in {512, 1024, 1536, 2048}, mels <= 128. */
+ * 512 with heads of 64, ffn in {512, 1024, 1536, 2048}, mels <= 128, at most
+ * 3072 mel frames (1536 encoder frames). */
 typedef struct {
     int mels, frames, d_model, heads, head_dim, enc_layers, dec_layers, ffn, vocab, max_positions, group;
     float rope_theta, norm_eps;

@@ -1274,7 +1274,7 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
     const rn_whistle_config& c = *config;
     const size_t d = c.d_model, f = c.ffn, H = c.heads, M = c.mels, Fr = c.frames, V = c.vocab;
     const size_t T = (size_t)(c.frames - 1) / 2 + 1;
-    RN_REQUIRE(T * 4 <= 128 * 1024, "too many encoder frames for the attention's score buffer");
+    RN_REQUIRE(T <= 1536, "at most 1536 encoder frames (3072 mel frames): the attention stages a head's values in LDS");
     rn_whistle* w = new (std::nothrow) rn_whistle();
     if (!w) return fail(RN_ERR_MEMORY, "out of host memory");
     w->cfg = c;

@@ -131,42 +131,125 @@ hipError_t launch_head_codes(const HeadCodesParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// One (query, head) per 256-thread block over `frames` int8 key/value rows.
-// Scores ((float)dot * key_scale) * query_scale in LDS (dynamic: one float per
-// frame), the peak, fast_exp, class totals (thread c sums frames c, c+32, ...
-// in order), the weights value_scale * (e * (1 / total)), then thread
-// (class c, dims 8g..8g+7) sums its class's weighted value codes in frame
-// order and the classes are added 0..31.
-__global__ __launch_bounds__(256) void int8_attend_kernel(Int8AttendParams p) {
-    extern __shared__ float e_s[];
-    __shared__ float part_s[32][65];
+// Attention with int8 queries, keys and values (encoder.rs:262-285 for the
+// encoder's frames, cross.rs:136-170 for the decoder's cross-attention), for
+// one head over at most kMaxFrames frames:
+//   score_j = ((float)(q . k_j) * key_scale_j) * query_scale   (exact int32 dot)
+//   e_j = fast_exp(score_j - peak)
+//   class totals: class c sums e_j over j = c, c+32, ... in order; total adds
+//   the classes 0..31; inverse = 1 / total
+//   w_j = value_scale_j * (e_j * inverse)
+//   out_d = sum over classes 0..31 of (class c's sum over its j, in order, of
+//   w_j * (float)v_jd)
+// The head's value rows are staged in LDS once per block; scores and weights
+// live in LDS. Two block shapes: one query per 1024-thread block (the decoder's
+// cross-attention: every load of the block is issued before the first score),
+// and tiles of kTileQueries queries per 512-thread block (the encoder: a key
+// row or value row loaded once serves the whole tile).
+constexpr int kMaxFrames = 1536;
+constexpr int kTileQueries = 8;
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
+
+// The head's value rows into LDS with global_load_lds_dwordx4 (no registers:
+// each lane's 16 bytes land at the wave's LDS base + 16 * lane). Piece i of the
+// head is 16-byte quarter i % 4 of frame i / 4 and goes to v_s + 16 i, so a
+// wave's 64 pieces are 1 KB of consecutive LDS; frames past the end repeat the
+// last frame. The copies count on vmcnt: wait for them before a barrier.
+template <int NT>
+__device__ __forceinline__ void stage_values(const Int8AttendParams& p, int h, int8_t* v_s) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int c = 0; c < kMaxFrames * 4 / NT; ++c) {
+        const int base = NT * c + 64 * wave, id = base + lane, fr = min(id >> 2, p.frames - 1);
+        __builtin_amdgcn_global_load_lds((global_void*)(p.vc + ((size_t)fr * p.heads + h) * 64 + (id & 3) * 16),
+                                         (lds_void*)(v_s + (size_t)base * 16), 16, 0, 0);
+    }
+}
+
+// int8 pair (bytes 0, 1 of a 16-bit word) as floats
+__device__ __forceinline__ void int8x2_to_float(uint32_t w, float& a, float& b) {
+    a = (float)(int)(int8_t)(w & 0xff);
+    b = (float)(int)(int8_t)((w >> 8) & 0xff);
+}
+
+__global__ __launch_bounds__(1024) void int8_attend_one_kernel(Int8AttendParams p) {
+    constexpr int NT = 1024, KP = kMaxFrames / (NT / 4), EP = kMaxFrames / NT + 1;
+    __shared__ __align__(16) int8_t v_s[kMaxFrames * 64];
+    __shared__ float e_s[kMaxFrames];
+    __shared__ float part_s[32][64 + 1];
     __shared__ float tot_s[32];
-    __shared__ float peak_s[4];
-    const int q = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    __shared__ float red_s[NT / 64];
+    const int h = blockIdx.x, q = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int F = p.frames, H = p.heads;
-    const int4* qrow = reinterpret_cast<const int4*>(p.qc + ((size_t)q * H + h) * 64);
-    const int4 q0 = qrow[0], q1 = qrow[1], q2 = qrow[2], q3 = qrow[3];
+    const int li = tid & 3;
+    // 1. every load of the block: the query quarter, the key rows (4 lanes per
+    // frame), the value rows as 16-byte pieces, the scales; frames past the end
+    // repeat the last frame
+    const int4 qq = reinterpret_cast<const int4*>(p.qc + ((size_t)q * H + h) * 64)[li];
     const float qs = p.qs[(size_t)q * H + h];
+    int4 kr[KP];
+    float ksr[KP];
+#pragma unroll
+    for (int c = 0; c < KP; ++c) {
+        const int fr = min((tid >> 2) + (NT / 4) * c, F - 1);
+        kr[c] = reinterpret_cast<const int4*>(p.kc + ((size_t)fr * H + h) * 64)[li];
+        ksr[c] = p.ks[(size_t)fr * H + h];
+    }
+    // six 16-byte value pieces per thread, in named registers (an array this
+    // size beside the key rows would be kept in scratch memory)
+    static_assert(kMaxFrames * 4 / NT == 6, "six value pieces per thread");
+    auto vpiece = [&](int c) -> int4 {
+        const int id = tid + NT * c, fr = min(id >> 2, F - 1);
+        return reinterpret_cast<const int4*>(p.vc + ((size_t)fr * H + h) * 64)[id & 3];
+    };
+    const int4 vr0 = vpiece(0), vr1 = vpiece(1), vr2 = vpiece(2), vr3 = vpiece(3), vr4 = vpiece(4), vr5 = vpiece(5);
+    float vsr[EP];
+#pragma unroll
+    for (int c = 0; c < EP; ++c) vsr[c] = p.vs[(size_t)min(tid + NT * c, F - 1) * H + h];
+    __builtin_amdgcn_sched_barrier(0);  // every request before the first score
+
+    // 2. scores and the local peak
+    float sc[KP];
     float m = -INFINITY;
-    for (int j = tid; j < F; j += 256) {
-        const int4* krow = reinterpret_cast<const int4*>(p.kc + ((size_t)j * H + h) * 64);
-        int dot = dot16(krow[0], q0, 0);
-        dot = dot16(krow[1], q1, dot);
-        dot = dot16(krow[2], q2, dot);
-        dot = dot16(krow[3], q3, dot);
-        const float s = ((float)dot * p.ks[(size_t)j * H + h]) * qs;
-        e_s[j] = s;
-        m = fmaxf(m, s);
+#pragma unroll
+    for (int c = 0; c < KP; ++c) {
+        const int fr = (tid >> 2) + (NT / 4) * c;
+        int dot = dot16(kr[c], qq, 0);
+        dot = dot + dpp_move<0xb1>(dot);
+        dot = dot + dpp_move<0x4e>(dot);
+        sc[c] = ((float)dot * ksr[c]) * qs;
+        if (fr < F) m = fmaxf(m, sc[c]);
     }
     m = wave_max(m);
-    if ((tid & 63) == 0) peak_s[tid >> 6] = m;
+    // the value rows into LDS (piece id = quarter id % 4 of frame id / 4)
+    int4* vp = reinterpret_cast<int4*>(v_s) + tid;
+    vp[0] = vr0;
+    vp[NT] = vr1;
+    vp[2 * NT] = vr2;
+    vp[3 * NT] = vr3;
+    vp[4 * NT] = vr4;
+    vp[5 * NT] = vr5;
+    if (lane == 0) red_s[wave] = m;
     __syncthreads();
-    const float peak = fmaxf(fmaxf(peak_s[0], peak_s[1]), fmaxf(peak_s[2], peak_s[3]));
-    for (int j = tid; j < F; j += 256) e_s[j] = fast_exp(e_s[j] - peak);
+    float peak = red_s[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) peak = fmaxf(peak, red_s[w]);
+    // 3. fast_exp weights, the class totals, then the scaled weights
+#pragma unroll
+    for (int c = 0; c < KP; ++c) {
+        const int fr = (tid >> 2) + (NT / 4) * c;
+        if (li == 0 && fr < F) e_s[fr] = fast_exp(sc[c] - peak);
+    }
     __syncthreads();
     if (tid < 32) {
         float t = 0.0f;
-        for (int j = tid; j < F; j += 32) t = t + e_s[j];
+#pragma unroll
+        for (int k = 0; k < kMaxFrames / 32; ++k) {
+            const int j = tid + 32 * k;
+            if (j < F) t = t + e_s[j];
+        }
         tot_s[tid] = t;
     }
     __syncthreads();
@@ -174,20 +257,28 @@ __global__ __launch_bounds__(256) void int8_attend_kernel(Int8AttendParams p) {
 #pragma unroll
     for (int c = 0; c < 32; ++c) total = total + tot_s[c];
     const float inverse = 1.0f / total;
-    __syncthreads();  // every thread has read the class totals
-    for (int j = tid; j < F; j += 256) e_s[j] = p.vs[(size_t)j * H + h] * (e_s[j] * inverse);
-    __syncthreads();
-    const int c = tid >> 3, g = tid & 7;
-    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = c; j < F; j += 32) {
-        const int2 raw = *reinterpret_cast<const int2*>(p.vc + ((size_t)j * H + h) * 64 + 8 * g);
-        const float wj = e_s[j];
-        const int8_t* b = reinterpret_cast<const int8_t*>(&raw);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = acc[i] + wj * (float)b[i];
+    for (int c = 0; c < EP; ++c) {
+        const int j = tid + NT * c;
+        if (j < F) e_s[j] = vsr[c] * (e_s[j] * inverse);
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) part_s[c][8 * g + i] = acc[i];
+    __syncthreads();
+    // 4. value sums: thread (class c, dims 2 d2, 2 d2 + 1) walks c, c+32, ...
+    const int c = tid >> 5, d2 = tid & 31;
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < kMaxFrames / 32; ++k) {
+        const int j = c + 32 * k;
+        if (j < F) {
+            const float w = e_s[j];
+            float v0, v1;
+            int8x2_to_float(*reinterpret_cast<const uint16_t*>(v_s + j * 64 + 2 * d2), v0, v1);
+            a0 = a0 + w * v0;
+            a1 = a1 + w * v1;
+        }
+    }
+    part_s[c][2 * d2] = a0;
+    part_s[c][2 * d2 + 1] = a1;
     __syncthreads();
     if (tid < 64) {
         float o = 0.0f;
@@ -197,11 +288,163 @@ __global__ __launch_bounds__(256) void int8_attend_kernel(Int8AttendParams p) {
     }
 }
 
+__global__ __launch_bounds__(512) void int8_attend_tile_kernel(Int8AttendParams p, int queries) {
+    constexpr int NT = 512, Q = kTileQueries;
+    constexpr int KP = kMaxFrames / (NT / 4);
+    // LDS: the value rows (96 KB; reused for the class partials at the end),
+    // the tile's scores / weights [frame][query] (48 KB)
+    __shared__ __align__(16) int8_t v_s[kMaxFrames * 64];
+    __shared__ __align__(16) float e_s[kMaxFrames][Q];
+    __shared__ float vs_s[kMaxFrames];
+    __shared__ float tot_s[Q][32];
+    __shared__ float red_s[Q][NT / 64];
+    __shared__ float inv_s[Q];
+    static_assert(Q * 32 * 64 * 4 <= kMaxFrames * 64, "partials fit the value area");
+    float(*part_s)[32][64] = reinterpret_cast<float(*)[32][64]>(v_s);
+    const int q0 = blockIdx.x * Q, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int F = p.frames, H = p.heads;
+    const int li = tid & 3;
+    // 1. loads: the tile's query quarters and scales (queries past the end
+    // repeat the last one), key rows, value rows (into LDS), value scales
+    int4 qq[Q];
+    float qs[Q];
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+        const int qi = min(q0 + i, queries - 1);
+        qq[i] = reinterpret_cast<const int4*>(p.qc + ((size_t)qi * H + h) * 64)[li];
+        qs[i] = p.qs[(size_t)qi * H + h];
+    }
+    int4 kr[KP];
+    float ksr[KP];
+#pragma unroll
+    for (int c = 0; c < KP; ++c) {
+        const int fr = min((tid >> 2) + (NT / 4) * c, F - 1);
+        kr[c] = reinterpret_cast<const int4*>(p.kc + ((size_t)fr * H + h) * 64)[li];
+        ksr[c] = p.ks[(size_t)fr * H + h];
+    }
+    stage_values<NT>(p, h, v_s);
+    constexpr int SP = kMaxFrames / NT;
+    float vsr[SP];
+#pragma unroll
+    for (int c = 0; c < SP; ++c) vsr[c] = p.vs[(size_t)min(tid + NT * c, F - 1) * H + h];
+    // 2. scores for the tile's queries, and their local peaks
+    float m[Q];
+#pragma unroll
+    for (int i = 0; i < Q; ++i) m[i] = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < KP; ++c) {
+        const int fr = (tid >> 2) + (NT / 4) * c;
+        float s[Q];
+#pragma unroll
+        for (int i = 0; i < Q; ++i) {
+            int dot = dot16(kr[c], qq[i], 0);
+            dot = dot + dpp_move<0xb1>(dot);
+            dot = dot + dpp_move<0x4e>(dot);
+            s[i] = ((float)dot * ksr[c]) * qs[i];
+        }
+        if (fr < F) {
+            if (li == 0) {
+                *reinterpret_cast<float4*>(&e_s[fr][0]) = make_float4(s[0], s[1], s[2], s[3]);
+                *reinterpret_cast<float4*>(&e_s[fr][4]) = make_float4(s[4], s[5], s[6], s[7]);
+            }
+#pragma unroll
+            for (int i = 0; i < Q; ++i) m[i] = fmaxf(m[i], s[i]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < SP; ++c) vs_s[tid + NT * c] = vsr[c];
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+        const float mm = wave_max(m[i]);
+        if (lane == 0) red_s[i][wave] = mm;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's value rows are in LDS
+    __syncthreads();
+    // 3. fast_exp weights (element (frame, query) = (e / Q, e % Q))
+    {
+        const int i = tid % Q;  // NT is a multiple of Q: each thread keeps one query
+        float peak = red_s[i][0];
+#pragma unroll
+        for (int w = 1; w < NT / 64; ++w) peak = fmaxf(peak, red_s[i][w]);
+        for (int e = tid; e < F * Q; e += NT) {
+            float& x = e_s[e / Q][i];
+            x = fast_exp(x - peak);
+        }
+    }
+    __syncthreads();
+    if (tid < Q * 32) {  // class totals: thread (query i, class c)
+        const int i = tid >> 5, c = tid & 31;
+        float t = 0.0f;
+#pragma unroll 8
+        for (int k = 0; k < kMaxFrames / 32; ++k) {
+            const int j = c + 32 * k;
+            if (j < F) t = t + e_s[j][i];
+        }
+        tot_s[i][c] = t;
+    }
+    __syncthreads();
+    if (tid < Q) {
+        float total = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) total = total + tot_s[tid][c];
+        inv_s[tid] = 1.0f / total;
+    }
+    __syncthreads();
+    {
+        const int i = tid % Q;
+        const float inverse = inv_s[i];
+        for (int e = tid; e < F * Q; e += NT) {
+            const int j = e / Q;
+            e_s[j][i] = vs_s[j] * (e_s[j][i] * inverse);
+        }
+    }
+    __syncthreads();
+    // 4. value sums: thread (class c, dims 4 dq..4 dq + 3) for every query of the tile
+    const int c = tid >> 4, dq = tid & 15;
+    float a[Q][4];
+#pragma unroll
+    for (int i = 0; i < Q; ++i)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) a[i][d] = 0.0f;
+#pragma unroll 2
+    for (int k = 0; k < kMaxFrames / 32; ++k) {
+        const int j = c + 32 * k;
+        if (j < F) {
+            const uint32_t raw = *reinterpret_cast<const uint32_t*>(v_s + j * 64 + 4 * dq);
+            float v[4];
+            int8x2_to_float(raw, v[0], v[1]);
+            int8x2_to_float(raw >> 16, v[2], v[3]);
+            const float4 w0 = *reinterpret_cast<const float4*>(&e_s[j][0]);
+            const float4 w1 = *reinterpret_cast<const float4*>(&e_s[j][4]);
+            const float w[Q] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int i = 0; i < Q; ++i)
+#pragma unroll
+                for (int d = 0; d < 4; ++d) a[i][d] = a[i][d] + w[i] * v[d];
+        }
+    }
+    __syncthreads();  // every thread is done with the value rows: reuse them for the partials
+#pragma unroll
+    for (int i = 0; i < Q; ++i)
+        *reinterpret_cast<float4*>(&part_s[i][c][4 * dq]) = make_float4(a[i][0], a[i][1], a[i][2], a[i][3]);
+    __syncthreads();
+    {
+        const int i = tid >> 6, d = tid & 63;  // NT = Q * 64: one output per thread
+        float o = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) o = o + part_s[i][k][d];
+        if (q0 + i < queries) p.out[(size_t)(q0 + i) * p.out_stride + h * 64 + d] = o;
+    }
+}
+
 hipError_t launch_int8_attend(const Int8AttendParams& p, int queries, hipStream_t stream) {
     if (queries <= 0) return hipSuccess;
-    const size_t lds = sizeof(float) * (size_t)(p.frames > 0 ? p.frames : 1);
-    if (p.frames < 1 || lds > 128 * 1024) return hipErrorInvalidValue;
-    rn_launch(int8_attend_kernel, dim3(queries, p.heads), dim3(256), lds, stream, p);
+    if (p.frames < 1 || p.frames > kMaxFrames || p.heads < 1) return hipErrorInvalidValue;
+    if (queries < kTileQueries)
+        rn_launch(int8_attend_one_kernel, dim3(p.heads, queries), dim3(1024), 0, stream, p);
+    else
+        rn_launch(int8_attend_tile_kernel, dim3((queries + kTileQueries - 1) / kTileQueries, p.heads), dim3(512), 0,
+                  stream, p, queries);
     return hipGetLastError();
 }
 

@@ -76,3 +76,22 @@ def test_full_size_encode_and_48_tokens():
     first = int(rn.synth_tokens(rn.SEED, "whistle.first", cfg["vocab"], 1)[0])
     ids = g.decode_greedy(first, 48)
     assert ids.tolist() == o.session(cfg["max_positions"], o.memory(ref)).greedy(first, 48).tolist()
+
+
+@pytest.mark.parametrize("mel_frames", [2, 17, 100])
+def test_ragged_frame_counts(mel_frames):
+    """1, 9 and 50 encoder frames: a single frame, a last query tile of one, a
+    head's values shorter than one staging pass."""
+    cfg = dict(rn.WHISTLE)
+    cfg.update(frames=mel_frames, enc_layers=1, dec_layers=1, vocab=500, max_positions=8)
+    w = rn.synthetic_whistle_weights(cfg, seed=5)
+    o, g, mel = oracle.OracleWhistle(cfg, w), rn.Whistle(cfg, seed=5), rn.synthetic_mel(cfg, seed=5)
+    enc = g.encode(mel)
+    ref = o.encode(mel)
+    assert enc.shape == ((mel_frames - 1) // 2 + 1, 384)
+    assert np.array_equal(_bits(enc), _bits(ref))
+    s = o.session(cfg["max_positions"], o.memory(ref))
+    for tok in (4, 499):
+        g.push(tok)
+        s.push(tok)
+        assert np.array_equal(_bits(g.logits()), _bits(s.logits()))
