@@ -168,6 +168,228 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
     }
 }
 
+// ---- the chain GEMM: group chains kept in the MFMA result registers ----------
+//
+// A 256-thread block (4 waves, WAVES_M x (4 / WAVES_M)) owns a BM x BN output
+// tile; each wave owns SM x SN sub-tiles of 16 x 16, and each lane 4 outputs per
+// sub-tile (rows 4 (l / 16) .. +3, column l % 16). For every 32-column group the
+// wave issues one v_mfma_i32_16x16x32_i8 per sub-tile and folds the int32 group
+// sum straight into the lane's running totals in group order (panel form
+// fmaf(acc, sW * sx, total), plane form total + (acc * sW) * sx), so no sum
+// leaves the registers. K streams through LDS in chunks of 4 groups (128 bytes
+// of every tile row), double-buffered: the next chunk's operand pieces and
+// weight scales are requested before the current chunk's MFMAs, and written to
+// the other buffer after them; one barrier per chunk. For the gated FFN
+// (SN = 2) sub-tile column 0 holds gate rows and column 1 the matching up rows,
+// so silu(gate) * up needs no exchange.
+constexpr int kChunkGroups = 4;                  // groups per K chunk
+constexpr int kChunkBytes = kChunkGroups * kGroup;  // 128
+constexpr int kChunkPitch = kChunkBytes + 16;    // LDS row pitch: 16-byte aligned, rows start on different banks
+
+template <int SM, int SN, int WAVES_M, int EPI, int FORM, bool DUMP>
+__global__ __launch_bounds__(256) void gemm_chain_kernel(GemmParams p) {
+    constexpr int WAVES_N = 4 / WAVES_M;
+    constexpr int BM = WAVES_M * SM * 16, BN = WAVES_N * SN * 16;
+    constexpr bool kSilu = EPI == kGemmSilu;
+    static_assert(!kSilu || SN == 2, "the gated FFN pairs gate and up sub-tiles");
+    constexpr int kPieces = (BM + BN) * (kChunkBytes / 16);  // 16-byte pieces per chunk
+    constexpr int kPer = (kPieces + 255) / 256;
+    __shared__ __align__(16) int8_t a_s[2][BM][kChunkPitch];
+    __shared__ __align__(16) int8_t b_s[2][BN][kChunkPitch];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int mtiles = (p.M + BM - 1) / BM;
+    int t = blockIdx.x;
+    if ((gridDim.x & 7) == 0) t = (t & 7) * (gridDim.x >> 3) + (t >> 3);  // one weight panel per XCD
+    const int mt = t % mtiles, nt = t / mtiles;
+    const int m0 = mt * BM;
+    const int G = p.K / kGroup, chunks = G / kChunkGroups;
+
+    // weight row of local tile column c (silu: wave column block wn holds 16
+    // outputs; its sub-tile column 0 is their gate rows, column 1 their up rows)
+    auto weight_row = [&](int c) -> int {
+        if constexpr (kSilu) {
+            const int w = c / 32, j = (c / 16) & 1, o = nt * (BN / 2) + w * 16 + (c & 15);
+            return j == 0 ? o : p.half + o;
+        } else {
+            return nt * BN + c;
+        }
+    };
+    auto row_ok = [&](int c) -> bool {
+        if constexpr (kSilu) return nt * (BN / 2) + (c / 32) * 16 + (c & 15) < p.half;
+        else return nt * BN + c < p.N;
+    };
+
+    // the chunk's operand pieces: piece i is 16-byte column i % 8 of tile row
+    // i / 8 (rows 0..BM-1 tokens, then BN weight rows); rows past the matrix
+    // repeat its last row
+    v4i piece[kPer];
+    auto load_chunk = [&](int ch) {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = min((int)threadIdx.x + 256 * q, kPieces - 1);
+            const int row = i >> 3, col = i & 7;
+            const int8_t* src = row < BM ? p.X + (size_t)min(m0 + row, p.M - 1) * p.K
+                                         : p.W + (size_t)min(weight_row(row - BM), p.N - 1) * p.K;
+            piece[q] = *reinterpret_cast<const v4i*>(src + (size_t)ch * kChunkBytes + 16 * col);
+        }
+    };
+    auto store_chunk = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = (int)threadIdx.x + 256 * q;
+            if (kPieces % 256 == 0 || i < kPieces) {
+                const int row = i >> 3, col = i & 7;
+                int8_t* dst = row < BM ? &a_s[buf][row][16 * col] : &b_s[buf][row - BM][16 * col];
+                *reinterpret_cast<v4i*>(dst) = piece[q];
+            }
+        }
+    };
+    // this lane's weight rows (one per sub-tile column) and token rows
+    const int r16 = lane & 15, kq = lane >> 4;
+    int wrow[SN];
+#pragma unroll
+    for (int j = 0; j < SN; ++j) wrow[j] = min(weight_row(wn * SN * 16 + j * 16 + r16), p.N - 1);
+    float4 sw[SN];
+    auto load_scales = [&](int ch) {
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+            sw[j] = *reinterpret_cast<const float4*>(p.sW + (size_t)wrow[j] * G + ch * kChunkGroups);
+    };
+    float sx[SM][4];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sx[i][r] = p.sx[min(m0 + wm * SM * 16 + i * 16 + 4 * kq + r, p.M - 1)];
+
+    float total[SM][SN][4];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) total[i][j][r] = 0.0f;
+
+    load_chunk(0);
+    load_scales(0);
+    store_chunk(0);
+    __syncthreads();
+    for (int ch = 0; ch < chunks; ++ch) {
+        const int buf = ch & 1;
+        float4 swc[SN];
+#pragma unroll
+        for (int j = 0; j < SN; ++j) swc[j] = sw[j];
+        if (ch + 1 < chunks) {
+            load_chunk(ch + 1);
+            load_scales(ch + 1);
+        }
+#pragma unroll
+        for (int gk = 0; gk < kChunkGroups; ++gk) {
+            long a[SM], b[SN];
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+                a[i] = *reinterpret_cast<const long*>(&a_s[buf][wm * SM * 16 + i * 16 + r16][gk * kGroup + 8 * kq]);
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+                b[j] = *reinterpret_cast<const long*>(&b_s[buf][wn * SN * 16 + j * 16 + r16][gk * kGroup + 8 * kq]);
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+#pragma unroll
+                for (int j = 0; j < SN; ++j) {
+                    const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const float s = gk == 0 ? swc[j].x : gk == 1 ? swc[j].y : gk == 2 ? swc[j].z : swc[j].w;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if constexpr (FORM == kPanel)
+                            total[i][j][r] = fmaf((float)acc[r], s * sx[i][r], total[i][j][r]);  // panel.rs:184-188
+                        else
+                            total[i][j][r] = total[i][j][r] + ((float)acc[r] * s) * sx[i][r];  // neon.rs:180
+                    }
+                    if constexpr (DUMP) {
+                        const int n = nt * BN + wn * SN * 16 + j * 16 + r16;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int m = m0 + wm * SM * 16 + i * 16 + 4 * kq + r;
+                            if (m < p.M && n < p.N)
+                                p.acc[((size_t)m * p.N + n) * G + ch * kChunkGroups + gk] = acc[r];
+                        }
+                    }
+                }
+        }
+        if (ch + 1 < chunks) {
+            store_chunk(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    // epilogue
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * SM * 16 + i * 16 + 4 * kq + r;
+            if (m >= p.M) continue;
+            if constexpr (kSilu) {
+                const int o = nt * (BN / 2) + wn * 16 + r16;
+                if (o < p.half) p.Y[(size_t)m * p.ldy + o] = silu(total[i][0][r]) * total[i][1][r];
+            } else {
+#pragma unroll
+                for (int j = 0; j < SN; ++j) {
+                    const int c = wn * SN * 16 + j * 16 + r16;
+                    if (!row_ok(c)) continue;
+                    float* dst = p.Y + (size_t)m * p.ldy + nt * BN + c;
+                    if constexpr (EPI == kGemmResidual)
+                        *dst = *dst + total[i][j][r];
+                    else if constexpr (EPI == kGemmStoreSilu)
+                        *dst = silu(total[i][j][r]);  // stem.rs:76,99: silu after the stage
+                    else
+                        *dst = total[i][j][r];
+                }
+            }
+        }
+}
+
+template <int SM, int SN, int WAVES_M, int EPI, int FORM, bool DUMP>
+static void launch_chain(const GemmParams& p, hipStream_t stream) {
+    constexpr int BM = WAVES_M * SM * 16, BN = (4 / WAVES_M) * SN * 16;
+    const int mtiles = (p.M + BM - 1) / BM;
+    const int ntiles = EPI == kGemmSilu ? (p.half + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
+    rn_launch((gemm_chain_kernel<SM, SN, WAVES_M, EPI, FORM, DUMP>), dim3(mtiles * ntiles), dim3(256), 0, stream, p);
+}
+
+// Tile shape by grid size: the largest of 64 x 64, 64 x 32, 32 x 64, 32 x 32
+// (not for the gated FFN, whose waves pair gate and up sub-tiles) that still
+// gives at least 512 blocks (two per CU); when none does, the one with the
+// most blocks (the chains are sequential over K, so blocks are the parallelism).
+template <int EPI, int FORM, bool DUMP>
+static bool launch_chain_by_shape(const GemmParams& p, hipStream_t stream) {
+    const int n_eff = EPI == kGemmSilu ? 2 * p.half : p.N;
+    auto blocks = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((n_eff + bn - 1) / bn); };
+    struct Shape { int bm, bn; };
+    const Shape shapes[4] = {{64, 64}, {64, 32}, {32, 64}, {32, 32}};
+    const int count = EPI == kGemmSilu ? 3 : 4;
+    int pick = -1, best = 0;
+    for (int i = 0; i < count; ++i) {
+        const int b = blocks(shapes[i].bm, shapes[i].bn);
+        if (b >= 512) { pick = i; break; }
+        if (b > best) { best = b; pick = i; }
+    }
+    // Under 256 blocks the per-block chain over K is the critical path and the
+    // split kernel (all groups of a tile in flight at once) is faster.
+    if (blocks(shapes[pick].bm, shapes[pick].bn) < 256) return false;
+    switch (pick) {
+        case 0: launch_chain<2, 2, 2, EPI, FORM, DUMP>(p, stream); break;
+        case 1: launch_chain<1, 2, 4, EPI, FORM, DUMP>(p, stream); break;
+        case 2: launch_chain<1, 2, 2, EPI, FORM, DUMP>(p, stream); break;
+        default:
+            if constexpr (EPI != kGemmSilu) launch_chain<1, 1, 2, EPI, FORM, DUMP>(p, stream);
+            break;
+    }
+    return true;
+}
+
+
 template <int G, int BM, int BN, int EPI, int FORM, bool DUMP>
 static void launch_split(const GemmParams& p, hipStream_t stream) {
     const int mtiles = (p.M + BM - 1) / BM;
@@ -197,6 +419,12 @@ static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
     }
 }
 
+// The chain kernel for large grids, the split kernel for small ones.
+template <int EPI, int FORM, bool DUMP>
+static void launch_product(const GemmParams& p, hipStream_t stream) {
+    if (!launch_chain_by_shape<EPI, FORM, DUMP>(p, stream)) launch_by_rows<EPI, FORM, DUMP>(p, stream);
+}
+
 hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, hipStream_t stream) {
     if (p.M <= 0) return hipSuccess;
     // instantiated for the supported widths (the kernel is unrolled over groups)
@@ -205,28 +433,28 @@ hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, h
     if (dump) {
         if (epilogue != kGemmStore) return hipErrorInvalidValue;
         if (form == kPanel)
-            launch_by_rows<kGemmStore, kPanel, true>(p, stream);
+            launch_product<kGemmStore, kPanel, true>(p, stream);
         else
-            launch_by_rows<kGemmStore, kPlane, true>(p, stream);
+            launch_product<kGemmStore, kPlane, true>(p, stream);
         return hipGetLastError();
     }
     if (form == kPlane) {
         if (epilogue != kGemmStore) return hipErrorInvalidValue;
-        launch_by_rows<kGemmStore, kPlane, false>(p, stream);
+        launch_product<kGemmStore, kPlane, false>(p, stream);
         return hipGetLastError();
     }
     switch (epilogue) {
         case kGemmStore:
-            launch_by_rows<kGemmStore, kPanel, false>(p, stream);
+            launch_product<kGemmStore, kPanel, false>(p, stream);
             break;
         case kGemmResidual:
-            launch_by_rows<kGemmResidual, kPanel, false>(p, stream);
+            launch_product<kGemmResidual, kPanel, false>(p, stream);
             break;
         case kGemmSilu:
-            launch_by_rows<kGemmSilu, kPanel, false>(p, stream);
+            launch_product<kGemmSilu, kPanel, false>(p, stream);
             break;
         case kGemmStoreSilu:
-            launch_by_rows<kGemmStoreSilu, kPanel, false>(p, stream);
+            launch_product<kGemmStoreSilu, kPanel, false>(p, stream);
             break;
         default:
             return hipErrorInvalidValue;

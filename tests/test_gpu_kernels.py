@@ -113,6 +113,11 @@ def test_multiply_fused_matches_separate():
     (100, 1152, 384, rn.FORM_PANEL),
     (33, 384, 1536, rn.FORM_PANEL),
     (17, 8192, 384, rn.FORM_PLANE),
+    # grids of 256 blocks or more take the register-chain kernel: ragged token
+    # and row tiles, a long K, the plane form
+    (300, 1000, 512, rn.FORM_PANEL),
+    (1500, 384, 1536, rn.FORM_PANEL),
+    (600, 1000, 384, rn.FORM_PLANE),
 ])
 def test_multiply_batch_mfma_bit_exact(count, rows, cols, form):
     rng = np.random.default_rng(count * 13 + rows + cols)
