@@ -358,10 +358,10 @@ static void launch_chain(const GemmParams& p, hipStream_t stream) {
     rn_launch((gemm_chain_kernel<SM, SN, WAVES_M, EPI, FORM, DUMP>), dim3(mtiles * ntiles), dim3(256), 0, stream, p);
 }
 
-// Tile shape by grid size: the largest of 64 x 64, 64 x 32, 32 x 64, 32 x 32
-// (not for the gated FFN, whose waves pair gate and up sub-tiles) that still
-// gives at least 512 blocks (two per CU); when none does, the one with the
-// most blocks (the chains are sequential over K, so blocks are the parallelism).
+// Tile shape: the one with the most blocks among 64 x 64, 64 x 32, 32 x 64 and
+// 32 x 32 (not for the gated FFN, whose waves pair gate and up sub-tiles). The
+// chains are sequential over K, so blocks are the parallelism, and small tiles
+// measured faster than large ones at every size used here.
 template <int EPI, int FORM, bool DUMP>
 static bool launch_chain_by_shape(const GemmParams& p, hipStream_t stream) {
     const int n_eff = EPI == kGemmSilu ? 2 * p.half : p.N;
@@ -372,7 +372,6 @@ static bool launch_chain_by_shape(const GemmParams& p, hipStream_t stream) {
     int pick = -1, best = 0;
     for (int i = 0; i < count; ++i) {
         const int b = blocks(shapes[i].bm, shapes[i].bn);
-        if (b >= 512) { pick = i; break; }
         if (b > best) { best = b; pick = i; }
     }
     // Under 256 blocks the per-block chain over K is the critical path and the
