@@ -1241,10 +1241,9 @@ struct rn_whistle {
     __half *kcache = nullptr, *vcache = nullptr;
     int capacity = 0, length = 0;
     bool has_hidden = false;
-    float *x = nullptr, *attn = nullptr, *cq = nullptr, *cctx = nullptr, *catt = nullptr;
+    float *x = nullptr, *attn = nullptr, *catt = nullptr;
+    float* cpart = nullptr;  // cross-attention value sums per position class [32][d]
     float *ffh = nullptr, *hidden = nullptr, *logits = nullptr;
-    int8_t* cqc = nullptr;
-    float* cqs = nullptr;
     DecodeState* state = nullptr;
     uint32_t* ids = nullptr;
     unsigned long long* keys = nullptr;
@@ -1364,9 +1363,8 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
     total += align_up(4 * Fr * M) + align_up(4 * Fr * d) + align_up(4 * T * d) * 4 + align_up(4 * T * 3 * d) +
              align_up(4 * T * Dm) + align_up(T * Dm) + align_up(4 * T) + 3 * align_up(T * d) + 3 * align_up(4 * T * H);
     total += 2 * align_up(L * T * d) + 2 * align_up(4 * L * T * H);
-    total += 2 * align_up(2 * L * H * cap * 64) + 6 * align_up(4 * d) + align_up(4 * 3 * d) + align_up(4 * f) +
-             align_up(4 * V) + align_up(d) + align_up(4 * H) + align_up(sizeof(DecodeState)) + align_up(4 * cap) +
-             align_up(8 * V);
+    total += 2 * align_up(2 * L * H * cap * 64) + 4 * align_up(4 * d) + align_up(4 * 32 * d) + align_up(4 * 3 * d) +
+             align_up(4 * f) + align_up(4 * V) + align_up(sizeof(DecodeState)) + align_up(4 * cap) + align_up(8 * V);
     if (hipMalloc(&w->arena, total) != hipSuccess) {
         delete w;
         return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", total);
@@ -1448,14 +1446,11 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
     w->vcache = (__half*)a.take(2 * L * H * cap * 64);
     w->x = (float*)a.take(4 * d);
     w->attn = (float*)a.take(4 * d);
-    w->cq = (float*)a.take(4 * d);
-    w->cctx = (float*)a.take(4 * d);
+    w->cpart = (float*)a.take(4 * 32 * d);
     w->catt = (float*)a.take(4 * d);
     w->hidden = (float*)a.take(4 * d);
     w->ffh = (float*)a.take(4 * f);
     w->logits = (float*)a.take(4 * V);
-    w->cqc = (int8_t*)a.take(d);
-    w->cqs = (float*)a.take(4 * H);
     w->state = (DecodeState*)a.take(sizeof(DecodeState));
     w->ids = (uint32_t*)a.take(4 * cap);
     w->keys = (unsigned long long*)a.take(8 * V);
@@ -1682,37 +1677,21 @@ static int enqueue_whistle_step(rn_whistle* w, bool greedy) {
             RN_HIP(launch_gemv(p, d, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
         }
         {
-            GemvParams p{};
-            p.nseg = 1;
-            p.seg[0] = Segment{L.cross_q.W, L.cross_q.sW, w->cq, nullptr, d, 0};
-            p.x = w->x;
-            p.gain = L.norm_cross;
-            p.eps = c.norm_eps;
-            const int rpb = gemv_rows_per_block(d, d, kStore);
-            RN_HIP(launch_gemv(p, d, kNorm, kStore, kPanel, rpb, (d + rpb - 1) / rpb, st));
-        }
-        {
-            HeadCodesParams hp{};
-            hp.src = w->cq;
-            hp.src_stride = d;
-            hp.frames = 1;
-            hp.heads = H;
-            hp.nsec = 1;
-            hp.sec[0] = HeadSection{0, L.q_norm, 0, 1.0f / sqrtf(64.0f), w->cqc, w->cqs};
-            hp.eps = c.norm_eps;
-            RN_HIP(launch_head_codes(hp, st));
+            // norm, q product, q codes and attention in one launch; it leaves
+            // the value sums per position class, which the out product adds
             const size_t off = (size_t)l * T * d, soff = (size_t)l * T * H;
-            Int8AttendParams ap{w->cqc, w->cqs, w->mem_k + off, w->mem_ks + soff, w->mem_v + off, w->mem_vs + soff,
-                                T, H, w->cctx, d};
-            RN_HIP(launch_int8_attend(ap, 1, st));
+            CrossAttendParams ap{L.cross_q.W, L.cross_q.sW, w->x, L.norm_cross, L.q_norm, c.norm_eps,
+                                 w->mem_k + off, w->mem_ks + soff, w->mem_v + off, w->mem_vs + soff,
+                                 T, H, w->cpart};
+            RN_HIP(launch_cross_attend(ap, d, st));
         }
         {
             GemvParams p{};
             p.nseg = 1;
             p.seg[0] = Segment{L.cross_out.W, L.cross_out.sW, w->catt, nullptr, d, 0};
-            p.x = w->cctx;
+            p.x = w->cpart;
             const int rpb = gemv_rows_per_block(d, d, kStore);
-            RN_HIP(launch_gemv(p, d, kQuant, kStore, kPanel, rpb, (d + rpb - 1) / rpb, st));
+            RN_HIP(launch_gemv(p, d, kClassSum, kStore, kPanel, rpb, (d + rpb - 1) / rpb, st));
             RN_HIP(launch_cross_residual(w->catt, L.post_norm, L.cross_gain, c.norm_eps, d, w->x, st));
         }
         {

@@ -87,6 +87,19 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
 #pragma unroll
         for (int e = 0; e < E; ++e)
             v[e] = ((float)er[e] * p.embS[(size_t)token * G + (lane * E + e) / kGroup]) * p.embed_scale;
+    } else if constexpr (PRO == kClassSum) {
+        // element i is the sum of the 32 class partials x[c][i] in class order
+        // (tree T3 of the cross-attention's value sums); all 32 rows requested
+        // before the first add
+        float t[32][E];
+#pragma unroll
+        for (int c = 0; c < 32; ++c) load_floats<E>(p.x + (size_t)c * K + lane * E, t[c]);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            v[e] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 32; ++c) v[e] = v[e] + t[c][e];
+        }
     } else if constexpr (PRO != kCodes) {
         load_floats<E>(p.x + lane * E, v);
     }
@@ -264,6 +277,7 @@ static hipError_t dispatch_pe(const GemvParams& p, int prologue, int epilogue, i
     if (form == kPanel) {
         if (prologue == kQuant && epilogue == kResidual) return launch_one<K, ROWS, kQuant, kResidual, kPanel>(p, blocks, s);
         if constexpr (K == 512 || K == 384) {
+            if (prologue == kClassSum && epilogue == kStore) return launch_one<K, ROWS, kClassSum, kStore, kPanel>(p, blocks, s);
             if (prologue == kNorm && epilogue == kStore) return launch_one<K, ROWS, kNorm, kStore, kPanel>(p, blocks, s);
             if (prologue == kEmbedNorm && epilogue == kStore) return launch_one<K, ROWS, kEmbedNorm, kStore, kPanel>(p, blocks, s);
             if (prologue == kNorm && epilogue == kSilu) return launch_one<K, ROWS, kNorm, kSilu, kPanel>(p, blocks, s);

@@ -45,7 +45,10 @@ struct DecodeState {
     uint32_t ids_capacity;
 };
 
-enum GemvPrologue { kQuant = 0, kNorm = 1, kEmbedNorm = 2, kCodes = 3 };
+// kClassSum: the input is 32 partial vectors [32][K] (the per-class value sums
+// of the decoder's cross-attention), added in class order 0..31 before the
+// quantisation of kQuant.
+enum GemvPrologue { kQuant = 0, kNorm = 1, kEmbedNorm = 2, kCodes = 3, kClassSum = 4 };
 enum GemvEpilogue { kStore = 0, kResidual = 1, kSilu = 2, kArgmax = 3 };
 enum ProductForm { kPanel = 0, kPlane = 1 };
 
@@ -203,6 +206,27 @@ struct Int8AttendParams {
     int out_stride;
 };
 hipError_t launch_int8_attend(const Int8AttendParams& p, int queries, hipStream_t stream);
+
+// The decoder's cross-attention for one token (cross.rs:126-170 up to the
+// attention output): zero-centred norm of x with the cross gains, the head's
+// 64 rows of the cross q product, per-head q norm and int8 codes, int8 scores
+// over the layer's memory, softmax, and the value sums of the 32 position
+// classes, written per class (part[c][64 h + i]); a kClassSum product adds them.
+struct CrossAttendParams {
+    const int8_t* W;     // cross q codes [d][d]
+    const float* sW;     // [d][d/32]
+    const float* x;      // residual stream [d]
+    const float* gain;   // norm_cross [d]
+    const float* q_gain; // q_norm [64]
+    float eps;
+    const int8_t* kc;    // layer memory [frames][heads][64] and scales [frames][heads]
+    const float* ks;
+    const int8_t* vc;
+    const float* vs;
+    int frames, heads;
+    float* part;         // [32][d]
+};
+hipError_t launch_cross_attend(const CrossAttendParams& p, int d_model, hipStream_t stream);
 hipError_t launch_cross_residual(const float* attended, const float* post_norm, float gain, float eps, int n, float* x,
                                  hipStream_t stream);
 hipError_t launch_add(const float* a, const float* b, size_t n, float* out, hipStream_t stream);

@@ -448,6 +448,271 @@ hipError_t launch_int8_attend(const Int8AttendParams& p, int queries, hipStream_
     return hipGetLastError();
 }
 
+// The decoder's cross-attention of one token (cross.rs:126-170 up to the
+// attention output) in 1024-thread blocks, kCrossGroups per head: block b
+// serves head b % 8 and position-class group g = b / 8 (classes 8g..8g+7).
+// Blocks are dealt to the XCDs round-robin, so a head's blocks share one L2
+// for the key rows every one of them reads; blocks of heads the model lacks
+// exit at once. One block per head would be bound by its value sums (about
+// 4600 wave instructions through one CU); split four ways, the redundant part
+// (keys, scores, softmax total) costs less than the split saves.
+//   1. wave 0: x, its zero-centred norm with the cross gains (eight-lane sum of
+//      ops.rs:7-17) and int8 codes (ops.rs:103-118) into LDS, while waves 1-15
+//      request the head's 64 rows of the cross q matrix and wave 1 their scales;
+//   2. every thread requests its memory rows: the keys of frames tid and
+//      tid + 1024, 64 bytes each; 16-byte pieces of the value rows of the
+//      group's 384 frames; their value scales;
+//   3. waves 1-15: v_dot4 group sums (lane pairs joined into 32-code groups);
+//      wave 1 lane r: row r's panel epilogue fmaf(acc, sW * sx, total)
+//      (panel.rs:184-188), then the head's zero-centred q norm with the q_norm
+//      gains, its int8 codes and scale times 1/sqrt(64) (encoder.rs:239-244);
+//   4. scores ((float)(q . k) * key_scale) * query_scale (exact int32 dot), the
+//      peak, fast_exp(score - peak) for every frame (0 past the last);
+//   5. wave 0: the 32 class totals (frames c, c+32, ... in order), their sum
+//      over classes 0..31, inverse = 1/total, and the group's weights
+//      value_scale * (e * inverse) (ops.rs:92-101, encoder.rs:278-285);
+//   6. waves 0-7: class 8g + wave, lane = dim: the weighted value sum over the
+//      class's frames in order, stored as part[class][64 h + lane].
+// Frames past the last add exact zeros: a weight of +0 adds +-0 to a running
+// sum that starts at +0, which leaves it unchanged, so the loops need no
+// bounds. The rows of frame j of group g: value row r holds frame
+// 32 (r / 8) + 8 g + r % 8.
+constexpr int kCrossGroups = 4;
+constexpr int kCrossRows = kMaxFrames / kCrossGroups;  // value rows per block
+
+template <int K>
+__global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p) {
+    constexpr int NT = 1024;
+    constexpr int G = K / kGroup, CPR = K / 16, CHUNKS = kWave * CPR, LW = NT - kWave;
+    constexpr int NLW = (CHUNKS + LW - 1) / LW;
+    constexpr int E = K / kWave;
+    constexpr int SLOTS = (kMaxFrames + NT - 1) / NT;   // key frames per thread
+    constexpr int VP = (kCrossRows * 4 + NT - 1) / NT;  // value pieces per thread
+    static_assert(kCrossRows * kCrossGroups == kMaxFrames && kCrossRows % 8 == 0, "whole classes per group");
+    static_assert(kCrossGroups * 8 == 32 && kCrossRows <= NT, "8 classes per group, one weight per thread");
+    static_assert(E % 2 == 0 && G % 4 == 0 && CPR % 2 == 0, "float pairs, scale quads, code pairs");
+    __shared__ __align__(16) int8_t v_s[kCrossRows * 64];
+    __shared__ float e_s[kMaxFrames];
+    __shared__ float w_s[kCrossRows];
+    __shared__ __align__(16) int8_t xq_s[K];
+    __shared__ __align__(16) float sq_s[K];
+    __shared__ __align__(16) int acc_s[kWave * G];
+    __shared__ __align__(16) int8_t qc_s[kWave];
+    __shared__ float red_s[NT / kWave];
+    __shared__ float sx_s, qs_s;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x & 7, g = blockIdx.x >> 3;
+    const int H = p.heads, F = p.frames;
+    if (h >= H) return;  // uniform over the block, before any barrier
+    auto frame_of_row = [&](int r) -> int { return 32 * (r >> 3) + 8 * g + (r & 7); };
+
+    // 1. the input codes (wave 0) and the head's weight rows (waves 1-15)
+    int4 w[NLW];
+    float4 sv[G / 4];
+    float qgain = 0.0f;
+    if (wave == 0) {
+        float v[E], gv[E];
+        load_floats<E>(p.x + lane * E, v);
+        load_floats<E>(p.gain + lane * E, gv);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int idx = lane * E + e;
+            sq_s[(idx % 8) * (K / 8) + idx / 8] = v[e] * v[e];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float s = 0.0f;
+        if (lane < 8) {
+            const float4* run = reinterpret_cast<const float4*>(sq_s + lane * (K / 8));
+            float4 t[K / 32];
+#pragma unroll
+            for (int c = 0; c < K / 32; ++c) t[c] = run[c];
+#pragma unroll
+            for (int c = 0; c < K / 32; ++c) {
+                s = s + t[c].x;
+                s = s + t[c].y;
+                s = s + t[c].z;
+                s = s + t[c].w;
+            }
+        }
+        float total = sum_lanes_0_to_7(s);
+        total = total + 0.0f;  // the (empty) tail of ops.rs:15-16
+        const float inverse = 1.0f / sqrtf(total / (float)K + p.eps);
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = ((1.0f + gv[e]) * v[e]) * inverse;
+        float peak = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
+        peak = wave_max(peak);
+        const float sx = int8_scale_from_peak(peak);
+        float y[E];
+        quotients<E>(v, sx, y);
+#pragma unroll
+        for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)code_of_quotient(y[e]);
+        if (lane == 0) sx_s = sx;
+    } else {
+        // chunk c = LW jj + (tid - 64): chunk c % CPR of head row c / CPR
+#pragma unroll
+        for (int jj = 0; jj < NLW; ++jj) {
+            const int c = min(LW * jj + tid - kWave, CHUNKS - 1);
+            w[jj] = *reinterpret_cast<const int4*>(p.W + (size_t)(kWave * h + c / CPR) * K + (c % CPR) * 16);
+        }
+        if (wave == 1) {
+            const float4* src = reinterpret_cast<const float4*>(p.sW + (size_t)(kWave * h + lane) * G);
+#pragma unroll
+            for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
+            qgain = p.q_gain[lane];
+        }
+    }
+    __syncthreads();
+
+    // 2. the memory rows (frames past the last repeat the last frame); offsets
+    // fit 32 bits (at most 1536 x 8 x 64 bytes)
+    int4 kr[SLOTS][4];
+    float ksr[SLOTS];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const uint32_t fh = (uint32_t)(min(tid + NT * s, F - 1) * H + h);
+        const int4* row = reinterpret_cast<const int4*>(p.kc + fh * 64u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[s][i] = row[i];
+        ksr[s] = p.ks[fh];
+    }
+    // two named pieces (an array here would be moved to LDS, behind a full wait)
+    static_assert(VP == 2, "two value pieces per thread");
+    auto vpiece = [&](int s) -> int4 {
+        const int id = min(tid + NT * s, kCrossRows * 4 - 1);
+        const uint32_t fh = (uint32_t)(min(frame_of_row(id >> 2), F - 1) * H + h);
+        return *reinterpret_cast<const int4*>(p.vc + fh * 64u + (uint32_t)(id & 3) * 16u);
+    };
+    const int4 vr0 = vpiece(0), vr1 = vpiece(1);
+    const int vrow = min(tid, kCrossRows - 1);
+    const float vsr = p.vs[(uint32_t)(min(frame_of_row(vrow), F - 1) * H + h)];
+    __builtin_amdgcn_sched_barrier(0);  // requested before the product, not sunk below it
+
+    // 3. the head's q rows: group sums, then wave 1's row epilogues and head codes
+    if (wave != 0) {
+#pragma unroll
+        for (int jj = 0; jj < NLW; ++jj) {
+            const int c = LW * jj + tid - kWave;
+            const int4 xc = *reinterpret_cast<const int4*>(xq_s + (min(c, CHUNKS - 1) % CPR) * 16);
+            int part = dot16(w[jj], xc, 0);
+            part = part + dpp_move<0xb1>(part);  // the pair partner (lane ^ 1: chunk c ^ 1)
+            if ((tid & 1) == 0 && c < CHUNKS) acc_s[(c / CPR) * G + (c % CPR) / 2] = part;
+        }
+    }
+    __syncthreads();
+    if (wave == 1) {
+        const float sx = sx_s;
+        const int4* arow = reinterpret_cast<const int4*>(acc_s + lane * G);
+        float q = 0.0f;
+#pragma unroll
+        for (int i = 0; i < G / 4; ++i) {
+            const int4 a4 = arow[i];
+            q = fmaf((float)a4.x, sv[i].x * sx, q);
+            q = fmaf((float)a4.y, sv[i].y * sx, q);
+            q = fmaf((float)a4.z, sv[i].z * sx, q);
+            q = fmaf((float)a4.w, sv[i].w * sx, q);
+        }
+        // per-head q norm (lane j < 8 of the eight-lane sum gathers j, j+8, ...)
+        const float sq = q * q;
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) s = s + __shfl(sq, 8 * c + (lane & 7), kWave);
+        float total = sum_lanes_0_to_7(s);
+        total = total + 0.0f;
+        const float inverse = 1.0f / sqrtf(total / 64.0f + p.eps);
+        q = ((1.0f + qgain) * q) * inverse;
+        const float scale = int8_scale_from_peak(wave_max(fabsf(q)));
+        float y;
+        quotients<1>(&q, scale, &y);
+        qc_s[lane] = (int8_t)code_of_quotient(y);
+        if (lane == 0) qs_s = scale * (1.0f / sqrtf(64.0f));
+    }
+    __syncthreads();
+
+    // 4. scores and their peak; the group's value rows into LDS
+    int4 qv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qv[i] = reinterpret_cast<const int4*>(qc_s)[i];
+    const float qs = qs_s;
+    float sc[SLOTS];
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        int dot = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dot = dot16(kr[s][i], qv[i], dot);
+        sc[s] = ((float)dot * ksr[s]) * qs;
+        if (tid + NT * s < F) m = fmaxf(m, sc[s]);
+    }
+    m = wave_max(m);
+    if (lane == 0) red_s[wave] = m;
+    reinterpret_cast<int4*>(v_s)[tid] = vr0;
+    if (tid + NT < kCrossRows * 4) reinterpret_cast<int4*>(v_s)[tid + NT] = vr1;
+    if (tid < kCrossRows) w_s[tid] = frame_of_row(tid) < F ? vsr : 0.0f;  // value scales for now
+    __syncthreads();
+    float peak = red_s[0];
+#pragma unroll
+    for (int i = 1; i < NT / kWave; ++i) peak = fmaxf(peak, red_s[i]);
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int fr = tid + NT * s;
+        if (fr < kMaxFrames) e_s[fr] = fr < F ? fast_exp(sc[s] - peak) : 0.0f;
+    }
+    __syncthreads();
+
+    // 5. class totals, total, and the group's weights (wave 0)
+    if (wave == 0) {
+        float t[kMaxFrames / 32];
+#pragma unroll
+        for (int k = 0; k < kMaxFrames / 32; ++k) t[k] = e_s[(lane & 31) + 32 * k];
+        float ct = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kMaxFrames / 32; ++k) ct = ct + t[k];
+        float total = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) total = total + lane_float(ct, c);
+        const float inverse = 1.0f / total;
+#pragma unroll
+        for (int k = 0; k < kCrossRows / kWave; ++k) {
+            const int r = lane + kWave * k;
+            w_s[r] = w_s[r] * (e_s[frame_of_row(r)] * inverse);
+        }
+    }
+    __syncthreads();
+
+    // 6. the value sums of class 8 g + wave (lane = dim), frames in order
+    if (wave < 8) {
+        float a = 0.0f;
+#pragma unroll 16
+        for (int k = 0; k < kMaxFrames / 32; ++k) {
+            const int r = 8 * k + wave;
+            a = a + w_s[r] * (float)v_s[r * 64 + lane];
+        }
+        p.part[(size_t)(8 * g + wave) * (H * 64) + h * 64 + lane] = a;
+    }
+}
+
+hipError_t launch_cross_attend(const CrossAttendParams& p, int d_model, hipStream_t stream) {
+    if (p.frames < 1 || p.frames > kMaxFrames || p.heads < 1 || p.heads > 8 || d_model != p.heads * 64)
+        return hipErrorInvalidValue;
+    const dim3 grid(8 * kCrossGroups);
+    switch (d_model) {
+        case 384:
+            rn_launch(cross_attend_kernel<384>, grid, dim3(1024), 0, stream, p);
+            break;
+        case 512:
+            rn_launch(cross_attend_kernel<512>, grid, dim3(1024), 0, stream, p);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // cross.rs:176-181: x += gain * zero_centred_norm(attended, post_norm), one
 // wave over the whole vector (E values per lane).
 template <int E>
