@@ -1241,7 +1241,7 @@ struct rn_whistle {
     __half *kcache = nullptr, *vcache = nullptr;
     int capacity = 0, length = 0;
     bool has_hidden = false;
-    float *x = nullptr, *attn = nullptr, *catt = nullptr;
+    float *x = nullptr, *x2 = nullptr, *attn = nullptr, *catt = nullptr;
     float* cpart = nullptr;  // cross-attention value sums per position class [32][d]
     float *ffh = nullptr, *hidden = nullptr, *logits = nullptr;
     DecodeState* state = nullptr;
@@ -1363,7 +1363,7 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
     total += align_up(4 * Fr * M) + align_up(4 * Fr * d) + align_up(4 * T * d) * 4 + align_up(4 * T * 3 * d) +
              align_up(4 * T * Dm) + align_up(T * Dm) + align_up(4 * T) + 3 * align_up(T * d) + 3 * align_up(4 * T * H);
     total += 2 * align_up(L * T * d) + 2 * align_up(4 * L * T * H);
-    total += 2 * align_up(2 * L * H * cap * 64) + 4 * align_up(4 * d) + align_up(4 * 32 * d) + align_up(4 * 3 * d) +
+    total += 2 * align_up(2 * L * H * cap * 64) + 5 * align_up(4 * d) + align_up(4 * 32 * d) + align_up(4 * 3 * d) +
              align_up(4 * f) + align_up(4 * V) + align_up(sizeof(DecodeState)) + align_up(4 * cap) + align_up(8 * V);
     if (hipMalloc(&w->arena, total) != hipSuccess) {
         delete w;
@@ -1445,6 +1445,7 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
     w->kcache = (__half*)a.take(2 * L * H * cap * 64);
     w->vcache = (__half*)a.take(2 * L * H * cap * 64);
     w->x = (float*)a.take(4 * d);
+    w->x2 = (float*)a.take(4 * d);
     w->attn = (float*)a.take(4 * d);
     w->cpart = (float*)a.take(4 * 32 * d);
     w->catt = (float*)a.take(4 * d);
@@ -1692,23 +1693,30 @@ static int enqueue_whistle_step(rn_whistle* w, bool greedy) {
             p.x = w->cpart;
             const int rpb = gemv_rows_per_block(d, d, kStore);
             RN_HIP(launch_gemv(p, d, kClassSum, kStore, kPanel, rpb, (d + rpb - 1) / rpb, st));
-            RN_HIP(launch_cross_residual(w->catt, L.post_norm, L.cross_gain, c.norm_eps, d, w->x, st));
         }
         {
+            // the cross residual in every block's prologue (block 0 keeps the sum
+            // in x2, read by the down product as its residual: x itself is read
+            // by the other blocks of this launch), then the FFN norm
             GemvParams p{};
             p.nseg = 1;
             p.seg[0] = Segment{L.gate_up.W, L.gate_up.sW, w->ffh, nullptr, 2 * f, 0};
             p.half_rows = f;
             p.x = w->x;
+            p.attended = w->catt;
+            p.post_gain = L.post_norm;
+            p.cross_gain = L.cross_gain;
+            p.x_out = w->x2;
             p.gain = L.norm_ffn;
             p.eps = c.norm_eps;
             const int rpb = gemv_rows_per_block(2 * f, d, kSilu);
-            RN_HIP(launch_gemv(p, d, kNorm, kSilu, kPanel, rpb, (f + rpb / 2 - 1) / (rpb / 2), st));
+            RN_HIP(launch_gemv(p, d, kCrossNorm, kSilu, kPanel, rpb, (f + rpb / 2 - 1) / (rpb / 2), st));
         }
         {
             GemvParams p{};
             p.nseg = 1;
             p.seg[0] = Segment{L.down.W, L.down.sW, w->x, nullptr, d, 0};
+            p.res = w->x2;
             p.x = w->ffh;
             const int rpb = gemv_rows_per_block(d, f, kResidual);
             RN_HIP(launch_gemv(p, f, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));

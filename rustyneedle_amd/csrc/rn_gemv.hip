@@ -37,7 +37,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     static_assert(EPI != kSilu || ROWS % 2 == 0, "silu blocks pair gate and up rows");
     static_assert(ROWS <= 64, "one lane per row in the epilogue");
 
-    constexpr bool NORM = PRO == kNorm || PRO == kEmbedNorm;
+    constexpr bool NORM = PRO == kNorm || PRO == kEmbedNorm || PRO == kCrossNorm;
     __shared__ __align__(16) int8_t xq_s[K];
     __shared__ __align__(16) int acc_s[ROWS * G];
     __shared__ __align__(16) float sq_s[NORM ? K : 4];
@@ -103,6 +103,12 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     } else if constexpr (PRO != kCodes) {
         load_floats<E>(p.x + lane * E, v);
     }
+    constexpr int CE = PRO == kCrossNorm ? E : 1;
+    float av[CE], pg[CE];
+    if constexpr (PRO == kCrossNorm) {
+        load_floats<E>(p.attended + lane * E, av);
+        load_floats<E>(p.post_gain + lane * E, pg);
+    }
     if constexpr (NORM) load_floats<E>(p.gain + lane * E, gv);
 
     // 1b. weights: unconditional loads (a branch around a load would make the
@@ -130,19 +136,15 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
 #pragma unroll
         for (int j = 0; j < NL; ++j) xc[j] = *reinterpret_cast<const int4*>(p.xq + load_chunk(j) * 16);
     } else {
-        if constexpr (PRO == kEmbedNorm) {
-            if (blockIdx.x == 0)
-#pragma unroll
-                for (int e = 0; e < E; ++e) p.x_out[lane * E + e] = v[e];
-        }
-        if constexpr (NORM) {
-            // ops.rs:7-17: lane j of eight sums elements j, j+8, j+16, ... in index
-            // order. Squares are stored transposed (strided lane j's run is
-            // contiguous) so each of the eight lanes reads its run with 128-bit reads.
+        // ops.rs:7-17 for the E values of every lane: lane j of eight sums elements
+        // j, j+8, j+16, ... in index order. Squares are stored transposed
+        // (strided lane j's run is contiguous) so each of the eight lanes reads
+        // its run with 128-bit reads. Returns 1 / sqrt(mean square + eps).
+        auto norm_inverse = [&](const float* vals) -> float {
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 const int idx = lane * E + e;
-                sq_s[(idx % 8) * (K / 8) + idx / 8] = v[e] * v[e];
+                sq_s[(idx % 8) * (K / 8) + idx / 8] = vals[e] * vals[e];
             }
             __syncthreads();
             float s = 0.0f;
@@ -160,7 +162,25 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
             float total = sum_lanes_0_to_7(s);
             total = total + 0.0f;  // the (empty) tail of ops.rs:15-16
             const float mean_square = total / (float)K;
-            const float inverse = 1.0f / sqrtf(mean_square + p.eps);
+            return 1.0f / sqrtf(mean_square + p.eps);
+        };
+        if constexpr (PRO == kEmbedNorm) {
+            if (blockIdx.x == 0)
+#pragma unroll
+                for (int e = 0; e < E; ++e) p.x_out[lane * E + e] = v[e];
+        }
+        if constexpr (PRO == kCrossNorm) {
+            // cross.rs:176-181: x += cross_gain * zero_centred_norm(attended, post_gain)
+            const float inverse = norm_inverse(av);
+#pragma unroll
+            for (int e = 0; e < E; ++e) v[e] = v[e] + p.cross_gain * (((1.0f + pg[e]) * av[e]) * inverse);
+            if (blockIdx.x == 0)
+#pragma unroll
+                for (int e = 0; e < E; ++e) p.x_out[lane * E + e] = v[e];
+            __syncthreads();  // the runs are read before the next squares replace them
+        }
+        if constexpr (NORM) {
+            const float inverse = norm_inverse(v);
 #pragma unroll
             for (int e = 0; e < E; ++e) v[e] = ((1.0f + gv[e]) * v[e]) * inverse;
             if (p.hidden_out != nullptr && blockIdx.x == 0)
@@ -217,7 +237,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     } else if constexpr (EPI == kResidual) {
         if (mine) {
             const int r = row_of(lane);
-            sg.y[r] = sg.y[r] + total;
+            sg.y[r] = (p.res != nullptr ? p.res[r] : sg.y[r]) + total;
         }
     } else if constexpr (EPI == kSilu) {
         const float up = __shfl(total, (lane + H) & 63, 64);
@@ -281,6 +301,7 @@ static hipError_t dispatch_pe(const GemvParams& p, int prologue, int epilogue, i
             if (prologue == kNorm && epilogue == kStore) return launch_one<K, ROWS, kNorm, kStore, kPanel>(p, blocks, s);
             if (prologue == kEmbedNorm && epilogue == kStore) return launch_one<K, ROWS, kEmbedNorm, kStore, kPanel>(p, blocks, s);
             if (prologue == kNorm && epilogue == kSilu) return launch_one<K, ROWS, kNorm, kSilu, kPanel>(p, blocks, s);
+            if (prologue == kCrossNorm && epilogue == kSilu) return launch_one<K, ROWS, kCrossNorm, kSilu, kPanel>(p, blocks, s);
         }
     } else {
         if constexpr (K == 512 || K == 384)

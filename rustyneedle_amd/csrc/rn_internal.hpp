@@ -47,8 +47,10 @@ struct DecodeState {
 
 // kClassSum: the input is 32 partial vectors [32][K] (the per-class value sums
 // of the decoder's cross-attention), added in class order 0..31 before the
-// quantisation of kQuant.
-enum GemvPrologue { kQuant = 0, kNorm = 1, kEmbedNorm = 2, kCodes = 3, kClassSum = 4 };
+// quantisation of kQuant. kCrossNorm: the cross-attention residual first
+// (x + cross_gain * zero_centred_norm(attended, post_gain), cross.rs:176-181;
+// block 0 writes it to x_out), then kNorm on that sum.
+enum GemvPrologue { kQuant = 0, kNorm = 1, kEmbedNorm = 2, kCodes = 3, kClassSum = 4, kCrossNorm = 5 };
 enum GemvEpilogue { kStore = 0, kResidual = 1, kSilu = 2, kArgmax = 3 };
 enum ProductForm { kPanel = 0, kPlane = 1 };
 
@@ -76,10 +78,14 @@ struct GemvParams {
     const float* embS;
     float embed_scale;    // sqrt(d_model)
     int vocab;
-    float* x_out;         // kEmbedNorm: block 0 writes the embedded row (the residual)
+    float* x_out;         // kEmbedNorm / kCrossNorm: block 0 writes the new residual row
     float* hidden_out;    // kNorm: block 0 writes the normed input (nullable)
     DecodeState* state;   // kEmbedNorm: the token to embed
     unsigned long long* keys;  // kArgmax: one greedy key per block (argmax_key)
+    const float* attended;     // kCrossNorm: the cross-attention output and its post-norm gains
+    const float* post_gain;
+    float cross_gain;
+    const float* res;     // kResidual: the residual read (nullable: the stored row itself)
 };
 
 // Launch one batch-1 product. `columns` in {512, 1024, 2048}; returns
@@ -227,8 +233,6 @@ struct CrossAttendParams {
     float* part;         // [32][d]
 };
 hipError_t launch_cross_attend(const CrossAttendParams& p, int d_model, hipStream_t stream);
-hipError_t launch_cross_residual(const float* attended, const float* post_norm, float gain, float eps, int n, float* x,
-                                 hipStream_t stream);
 hipError_t launch_add(const float* a, const float* b, size_t n, float* out, hipStream_t stream);
 
 // ---- elementwise / helpers ----------------------------------------------------

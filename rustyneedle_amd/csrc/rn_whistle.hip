@@ -1,11 +1,12 @@
 // rn_whistle.hip — the speech path's own kernels for gfx950: the fp32 stem
 // convolutions, per-head norm/rotary/int8 codes, attention with int8 queries,
-// keys and values, and the cross-attention residual.
+// keys and values, and the decoder's fused cross-attention.
 //
 // Replaces crates/whistle/src/stem.rs:39-115 (first convolution, one
 // depthwise + pointwise stage), encoder.rs:217-297 (the attention's integer
 // scores and int8 values) and cross.rs:58-182 (memory, apply). Products go
-// through the shared int8 kernels (rn_gemm.hip, rn_gemv.hip).
+// through the shared int8 kernels (rn_gemm.hip, rn_gemv.hip); the cross
+// residual (cross.rs:176-181) is the prologue of the gated FFN's product.
 //
 // Float orders (identical to the CPU restatement): the first convolution adds
 // its taps (k, m) in order into a zero output per (frame, channel); the
@@ -450,34 +451,41 @@ hipError_t launch_int8_attend(const Int8AttendParams& p, int queries, hipStream_
 
 // The decoder's cross-attention of one token (cross.rs:126-170 up to the
 // attention output) in 1024-thread blocks, kCrossGroups per head: block b
-// serves head b % 8 and position-class group g = b / 8 (classes 8g..8g+7).
-// Blocks are dealt to the XCDs round-robin, so a head's blocks share one L2
-// for the key rows every one of them reads; blocks of heads the model lacks
-// exit at once. One block per head would be bound by its value sums (about
-// 4600 wave instructions through one CU); split four ways, the redundant part
-// (keys, scores, softmax total) costs less than the split saves.
-//   1. wave 0: x, its zero-centred norm with the cross gains (eight-lane sum of
-//      ops.rs:7-17) and int8 codes (ops.rs:103-118) into LDS, while waves 1-15
-//      request the head's 64 rows of the cross q matrix and wave 1 their scales;
-//   2. every thread requests its memory rows: the keys of frames tid and
-//      tid + 1024, 64 bytes each; 16-byte pieces of the value rows of the
-//      group's 384 frames; their value scales;
+// serves head b % 8 and position-class group g = b / 8 (classes
+// kGroupClasses g .. kGroupClasses g + kGroupClasses - 1). Blocks are dealt to
+// the XCDs round-robin, so a head's blocks share one L2 for the key rows every
+// one of them reads; blocks of heads the model lacks exit at once. One block
+// per head would be bound by its value sums (about 4600 wave instructions
+// through one CU); split eight ways, the redundant part (keys, scores, softmax
+// total) costs less than the split saves. The block's loads (about 150 KB,
+// the bound of the front half: one CU takes about 64 bytes a clock) are all
+// requested at the start, behind wave 0's input vector:
+//   1. wave 0 requests x and the cross gains, waves 1-15 the head's 64 rows of
+//      the cross q matrix (wave 1 also their scales and the q_norm gains); then
+//      every thread its memory rows: the key row of frame tid (64 bytes), half
+//      the key row of frame 1024 + tid / 2 (32 bytes), a 16-byte piece of the
+//      group's value rows, a value scale;
+//   2. wave 0: the zero-centred norm of x (eight-lane sum of ops.rs:7-17) and
+//      its int8 codes (ops.rs:103-118) into LDS;
 //   3. waves 1-15: v_dot4 group sums (lane pairs joined into 32-code groups);
 //      wave 1 lane r: row r's panel epilogue fmaf(acc, sW * sx, total)
 //      (panel.rs:184-188), then the head's zero-centred q norm with the q_norm
 //      gains, its int8 codes and scale times 1/sqrt(64) (encoder.rs:239-244);
-//   4. scores ((float)(q . k) * key_scale) * query_scale (exact int32 dot), the
-//      peak, fast_exp(score - peak) for every frame (0 past the last);
+//   4. scores ((float)(q . k) * key_scale) * query_scale (exact int32 dot; the
+//      half rows joined across the lane pair), the peak, fast_exp(score - peak)
+//      for every frame (0 past the last);
 //   5. wave 0: the 32 class totals (frames c, c+32, ... in order), their sum
 //      over classes 0..31, inverse = 1/total, and the group's weights
-//      value_scale * (e * inverse) (ops.rs:92-101, encoder.rs:278-285);
-//   6. waves 0-7: class 8g + wave, lane = dim: the weighted value sum over the
-//      class's frames in order, stored as part[class][64 h + lane].
+//      value_scale * (e * inverse) (ops.rs:92-101, encoder.rs:278-285), while
+//      waves 1..kGroupClasses convert their class's int8 values to floats;
+//   6. those waves, lane = dim: the weighted value sum over the class's frames
+//      in order, stored as part[class][64 h + lane].
 // Frames past the last add exact zeros: a weight of +0 adds +-0 to a running
 // sum that starts at +0, which leaves it unchanged, so the loops need no
-// bounds. The rows of frame j of group g: value row r holds frame
-// 32 (r / 8) + 8 g + r % 8.
-constexpr int kCrossGroups = 4;
+// bounds. Value row r of group g holds frame
+// 32 (r / kGroupClasses) + kGroupClasses g + r % kGroupClasses.
+constexpr int kCrossGroups = 8;
+constexpr int kGroupClasses = 32 / kCrossGroups;
 constexpr int kCrossRows = kMaxFrames / kCrossGroups;  // value rows per block
 
 template <int K>
@@ -486,10 +494,10 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
     constexpr int G = K / kGroup, CPR = K / 16, CHUNKS = kWave * CPR, LW = NT - kWave;
     constexpr int NLW = (CHUNKS + LW - 1) / LW;
     constexpr int E = K / kWave;
-    constexpr int SLOTS = (kMaxFrames + NT - 1) / NT;   // key frames per thread
-    constexpr int VP = (kCrossRows * 4 + NT - 1) / NT;  // value pieces per thread
-    static_assert(kCrossRows * kCrossGroups == kMaxFrames && kCrossRows % 8 == 0, "whole classes per group");
-    static_assert(kCrossGroups * 8 == 32 && kCrossRows <= NT, "8 classes per group, one weight per thread");
+    constexpr int FPC = kMaxFrames / 32;  // frame slots per class
+    static_assert(kMaxFrames == NT + NT / 2, "a full key row and half a key row per thread");
+    static_assert(kCrossRows * 4 <= NT && kCrossRows % kWave == 0, "one value piece per thread, whole weight rows");
+    static_assert(kGroupClasses + 1 <= NT / kWave, "value-sum waves besides wave 0");
     static_assert(E % 2 == 0 && G % 4 == 0 && CPR % 2 == 0, "float pairs, scale quads, code pairs");
     __shared__ __align__(16) int8_t v_s[kCrossRows * 64];
     __shared__ float e_s[kMaxFrames];
@@ -499,22 +507,49 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
     __shared__ __align__(16) int acc_s[kWave * G];
     __shared__ __align__(16) int8_t qc_s[kWave];
     __shared__ float red_s[NT / kWave];
+    __shared__ __align__(16) float4 sw_s[kWave][G / 4];
+    __shared__ float qg_s[kWave];
     __shared__ float sx_s, qs_s;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x & 7, g = blockIdx.x >> 3;
     const int H = p.heads, F = p.frames;
     if (h >= H) return;  // uniform over the block, before any barrier
-    auto frame_of_row = [&](int r) -> int { return 32 * (r >> 3) + 8 * g + (r & 7); };
+    auto frame_of_row = [&](int r) -> int {
+        return 32 * (r / kGroupClasses) + kGroupClasses * g + r % kGroupClasses;
+    };
 
-    // 1. the input codes (wave 0) and the head's weight rows (waves 1-15)
+    // 1. requests: the prologue inputs (wave 0) or the head's weight rows
+    // (waves 1-15) first, then every thread's memory rows
+    typedef float v4f __attribute__((ext_vector_type(4)));  // kept in registers, unlike float4 arrays
     int4 w[NLW];
-    float4 sv[G / 4];
+    v4f sv[G / 4];
     float qgain = 0.0f;
+    float v[E], gv[E];
     if (wave == 0) {
-        float v[E], gv[E];
+        // also the q rows' scales (lane r: row r) and the q_norm gains, staged
+        // in LDS for wave 1's epilogue: a wave of the product that waits on
+        // loads of its own before its memory requests would hold them back
         load_floats<E>(p.x + lane * E, v);
         load_floats<E>(p.gain + lane * E, gv);
+        const v4f* src = reinterpret_cast<const v4f*>(p.sW + (size_t)(kWave * h + lane) * G);
+#pragma unroll
+        for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
+        qgain = p.q_gain[lane];
+    } else {
+        // chunk c = LW jj + (tid - 64): chunk c % CPR of head row c / CPR
+#pragma unroll
+        for (int jj = 0; jj < NLW; ++jj) {
+            const int c = min(LW * jj + tid - kWave, CHUNKS - 1);
+            w[jj] = *reinterpret_cast<const int4*>(p.W + (size_t)(kWave * h + c / CPR) * K + (c % CPR) * 16);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. wave 0: the input's norm and int8 codes, before its memory requests
+    // (a wave issues in order, and the memory requests queue behind the other
+    // waves' for about a microsecond)
+    if (wave == 0) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const int idx = lane * E + e;
@@ -525,16 +560,22 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float s = 0.0f;
         if (lane < 8) {
+            // the run in quarters of four float4s (all memory loads are still
+            // in flight, so registers are short here)
             const float4* run = reinterpret_cast<const float4*>(sq_s + lane * (K / 8));
-            float4 t[K / 32];
 #pragma unroll
-            for (int c = 0; c < K / 32; ++c) t[c] = run[c];
+            for (int c0 = 0; c0 < K / 32; c0 += 4) {
+                float4 t[4];
 #pragma unroll
-            for (int c = 0; c < K / 32; ++c) {
-                s = s + t[c].x;
-                s = s + t[c].y;
-                s = s + t[c].z;
-                s = s + t[c].w;
+                for (int c = 0; c < 4; ++c) t[c] = run[c0 + c];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    s = s + t[c].x;
+                    s = s + t[c].y;
+                    s = s + t[c].z;
+                    s = s + t[c].w;
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         float total = sum_lanes_0_to_7(s);
@@ -552,45 +593,28 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
 #pragma unroll
         for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)code_of_quotient(y[e]);
         if (lane == 0) sx_s = sx;
-    } else {
-        // chunk c = LW jj + (tid - 64): chunk c % CPR of head row c / CPR
 #pragma unroll
-        for (int jj = 0; jj < NLW; ++jj) {
-            const int c = min(LW * jj + tid - kWave, CHUNKS - 1);
-            w[jj] = *reinterpret_cast<const int4*>(p.W + (size_t)(kWave * h + c / CPR) * K + (c % CPR) * 16);
-        }
-        if (wave == 1) {
-            const float4* src = reinterpret_cast<const float4*>(p.sW + (size_t)(kWave * h + lane) * G);
-#pragma unroll
-            for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
-            qgain = p.q_gain[lane];
-        }
+        for (int i = 0; i < G / 4; ++i) sw_s[lane][i] = make_float4(sv[i].x, sv[i].y, sv[i].z, sv[i].w);
+        qg_s[lane] = qgain;
     }
-    __syncthreads();
-
-    // 2. the memory rows (frames past the last repeat the last frame); offsets
-    // fit 32 bits (at most 1536 x 8 x 64 bytes)
-    int4 kr[SLOTS][4];
-    float ksr[SLOTS];
+    // every thread's memory rows: frames past the last repeat the last frame;
+    // offsets fit 32 bits (at most 1536 x 8 x 64 bytes)
+    const int half = tid & 1;
+    const uint32_t fh0 = (uint32_t)(min(tid, F - 1) * H + h);
+    const uint32_t fh1 = (uint32_t)(min(NT + (tid >> 1), F - 1) * H + h);
+    int4 k0[4], k1[2];
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        const uint32_t fh = (uint32_t)(min(tid + NT * s, F - 1) * H + h);
-        const int4* row = reinterpret_cast<const int4*>(p.kc + fh * 64u);
+    for (int i = 0; i < 4; ++i) k0[i] = reinterpret_cast<const int4*>(p.kc + fh0 * 64u)[i];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) kr[s][i] = row[i];
-        ksr[s] = p.ks[fh];
-    }
-    // two named pieces (an array here would be moved to LDS, behind a full wait)
-    static_assert(VP == 2, "two value pieces per thread");
-    auto vpiece = [&](int s) -> int4 {
-        const int id = min(tid + NT * s, kCrossRows * 4 - 1);
-        const uint32_t fh = (uint32_t)(min(frame_of_row(id >> 2), F - 1) * H + h);
-        return *reinterpret_cast<const int4*>(p.vc + fh * 64u + (uint32_t)(id & 3) * 16u);
-    };
-    const int4 vr0 = vpiece(0), vr1 = vpiece(1);
+    for (int i = 0; i < 2; ++i) k1[i] = reinterpret_cast<const int4*>(p.kc + fh1 * 64u + 32u * half)[i];
+    const float ks0 = p.ks[fh0], ks1 = p.ks[fh1];
+    const int vpiece = min(tid, kCrossRows * 4 - 1);
+    const int4 vr = *reinterpret_cast<const int4*>(
+        p.vc + (uint32_t)(min(frame_of_row(vpiece >> 2), F - 1) * H + h) * 64u + (uint32_t)(vpiece & 3) * 16u);
     const int vrow = min(tid, kCrossRows - 1);
     const float vsr = p.vs[(uint32_t)(min(frame_of_row(vrow), F - 1) * H + h)];
     __builtin_amdgcn_sched_barrier(0);  // requested before the product, not sunk below it
+    __syncthreads();
 
     // 3. the head's q rows: group sums, then wave 1's row epilogues and head codes
     if (wave != 0) {
@@ -611,11 +635,13 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
 #pragma unroll
         for (int i = 0; i < G / 4; ++i) {
             const int4 a4 = arow[i];
-            q = fmaf((float)a4.x, sv[i].x * sx, q);
-            q = fmaf((float)a4.y, sv[i].y * sx, q);
-            q = fmaf((float)a4.z, sv[i].z * sx, q);
-            q = fmaf((float)a4.w, sv[i].w * sx, q);
+            const float4 s4 = sw_s[lane][i];
+            q = fmaf((float)a4.x, s4.x * sx, q);
+            q = fmaf((float)a4.y, s4.y * sx, q);
+            q = fmaf((float)a4.z, s4.z * sx, q);
+            q = fmaf((float)a4.w, s4.w * sx, q);
         }
+        const float qgain = qg_s[lane];
         // per-head q norm (lane j < 8 of the eight-lane sum gathers j, j+8, ...)
         const float sq = q * q;
         float s = 0.0f;
@@ -634,44 +660,43 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
     __syncthreads();
 
     // 4. scores and their peak; the group's value rows into LDS
-    int4 qv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qv[i] = reinterpret_cast<const int4*>(qc_s)[i];
     const float qs = qs_s;
-    float sc[SLOTS];
-    float m = -INFINITY;
+    float sc0, sc1;
+    {
+        int d0 = 0, d1 = 0;
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        int dot = 0;
+        for (int i = 0; i < 4; ++i) d0 = dot16(k0[i], reinterpret_cast<const int4*>(qc_s)[i], d0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dot = dot16(kr[s][i], qv[i], dot);
-        sc[s] = ((float)dot * ksr[s]) * qs;
-        if (tid + NT * s < F) m = fmaxf(m, sc[s]);
+        for (int i = 0; i < 2; ++i) d1 = dot16(k1[i], reinterpret_cast<const int4*>(qc_s)[2 * half + i], d1);
+        d1 = d1 + dpp_move<0xb1>(d1);  // the other half row (lane ^ 1)
+        sc0 = ((float)d0 * ks0) * qs;
+        sc1 = ((float)d1 * ks1) * qs;
     }
+    float m = tid < F ? sc0 : -INFINITY;
+    if (NT + (tid >> 1) < F) m = fmaxf(m, sc1);
     m = wave_max(m);
     if (lane == 0) red_s[wave] = m;
-    reinterpret_cast<int4*>(v_s)[tid] = vr0;
-    if (tid + NT < kCrossRows * 4) reinterpret_cast<int4*>(v_s)[tid + NT] = vr1;
+    if (tid < kCrossRows * 4) reinterpret_cast<int4*>(v_s)[tid] = vr;
     if (tid < kCrossRows) w_s[tid] = frame_of_row(tid) < F ? vsr : 0.0f;  // value scales for now
     __syncthreads();
     float peak = red_s[0];
 #pragma unroll
     for (int i = 1; i < NT / kWave; ++i) peak = fmaxf(peak, red_s[i]);
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        const int fr = tid + NT * s;
-        if (fr < kMaxFrames) e_s[fr] = fr < F ? fast_exp(sc[s] - peak) : 0.0f;
-    }
+    e_s[tid] = tid < F ? fast_exp(sc0 - peak) : 0.0f;
+    if (half == 0) e_s[NT + (tid >> 1)] = NT + (tid >> 1) < F ? fast_exp(sc1 - peak) : 0.0f;
     __syncthreads();
 
-    // 5. class totals, total, and the group's weights (wave 0)
+    // 5. wave 0: class totals, total, and the group's weights; the value-sum
+    // waves meanwhile take their int8 values out of LDS as floats
+    float vf[FPC];
+    const int cls = wave - 1;  // the value-sum waves' class within the group
     if (wave == 0) {
-        float t[kMaxFrames / 32];
+        float t[FPC];
 #pragma unroll
-        for (int k = 0; k < kMaxFrames / 32; ++k) t[k] = e_s[(lane & 31) + 32 * k];
+        for (int k = 0; k < FPC; ++k) t[k] = e_s[(lane & 31) + 32 * k];
         float ct = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kMaxFrames / 32; ++k) ct = ct + t[k];
+        for (int k = 0; k < FPC; ++k) ct = ct + t[k];
         float total = 0.0f;
 #pragma unroll
         for (int c = 0; c < 32; ++c) total = total + lane_float(ct, c);
@@ -681,18 +706,18 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
             const int r = lane + kWave * k;
             w_s[r] = w_s[r] * (e_s[frame_of_row(r)] * inverse);
         }
+    } else if (cls < kGroupClasses) {
+#pragma unroll
+        for (int k = 0; k < FPC; ++k) vf[k] = (float)v_s[(kGroupClasses * k + cls) * 64 + lane];
     }
     __syncthreads();
 
-    // 6. the value sums of class 8 g + wave (lane = dim), frames in order
-    if (wave < 8) {
+    // 6. the value sums of class kGroupClasses g + cls (lane = dim), frames in order
+    if (wave >= 1 && cls < kGroupClasses) {
         float a = 0.0f;
-#pragma unroll 16
-        for (int k = 0; k < kMaxFrames / 32; ++k) {
-            const int r = 8 * k + wave;
-            a = a + w_s[r] * (float)v_s[r * 64 + lane];
-        }
-        p.part[(size_t)(8 * g + wave) * (H * 64) + h * 64 + lane] = a;
+#pragma unroll
+        for (int k = 0; k < FPC; ++k) a = a + w_s[kGroupClasses * k + cls] * vf[k];
+        p.part[(size_t)(kGroupClasses * g + cls) * (H * 64) + h * 64 + lane] = a;
     }
 }
 
@@ -706,52 +731,6 @@ hipError_t launch_cross_attend(const CrossAttendParams& p, int d_model, hipStrea
             break;
         case 512:
             rn_launch(cross_attend_kernel<512>, grid, dim3(1024), 0, stream, p);
-            break;
-        default:
-            return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
-// cross.rs:176-181: x += gain * zero_centred_norm(attended, post_norm), one
-// wave over the whole vector (E values per lane).
-template <int E>
-__global__ __launch_bounds__(64) void cross_residual_kernel(const float* attended, const float* gain_vec, float gain,
-                                                           float eps, float* x) {
-    constexpr int n = 64 * E;
-    __shared__ float sq_s[n];
-    const int lane = threadIdx.x;
-    float v[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) v[e] = attended[lane * E + e];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int idx = lane * E + e;
-        sq_s[(idx % 8) * (n / 8) + idx / 8] = v[e] * v[e];
-    }
-    __syncthreads();
-    float s = 0.0f;
-    if (lane < 8)
-        for (int c = 0; c < n / 8; ++c) s = s + sq_s[lane * (n / 8) + c];
-    float total = sum_lanes_0_to_7(s);
-    total = total + 0.0f;
-    const float inverse = 1.0f / sqrtf(total / (float)n + eps);
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int idx = lane * E + e;
-        const float normed = ((1.0f + gain_vec[idx]) * v[e]) * inverse;
-        x[idx] = x[idx] + gain * normed;
-    }
-}
-
-hipError_t launch_cross_residual(const float* attended, const float* post_norm, float gain, float eps, int n, float* x,
-                                 hipStream_t stream) {
-    switch (n) {
-        case 384:
-            rn_launch(cross_residual_kernel<6>, dim3(1), dim3(64), 0, stream, attended, post_norm, gain, eps, x);
-            break;
-        case 512:
-            rn_launch(cross_residual_kernel<8>, dim3(1), dim3(64), 0, stream, attended, post_norm, gain, eps, x);
             break;
         default:
             return hipErrorInvalidValue;
