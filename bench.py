@@ -49,11 +49,12 @@ KERNEL_NAMES = {
 # (FETCH x2.000, WRITE x1.000). Recorded in profiles/decode_b1_needle20_traffic.md;
 # they describe the kernels as built when measured and are re-measured with them.
 PMC_TRAFFIC = {
-    "out": 391_312,
-    "gate_up": 2_488_966,
-    "down": 1_393_521,
-    "logits": 4_895_005,
-    "final": 11_838,
+    "qkv_attention": 1_712_282,
+    "out": 400_530,
+    "gate_up": 2_488_974,
+    "down": 1_384_447,
+    "logits": 4_906_489,
+    "final": 11_979,
 }
 
 

@@ -383,7 +383,6 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
     const size_t head_base = (size_t)h * p.capacity * kHeadDim;
     const __half* Kc = p.kc + head_base;
     const __half* Vc = p.vc + head_base;
-    const int rows = p.capacity;
 
     const int pos = p.state->pos;
     // 1. wave 0: the input row, its norm and its int8 codes (LDS traffic inside
@@ -468,23 +467,24 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
         if (tid == 0) atomicOr(&p.state->error, 2);
         return;
     }
+    const int last_row = pos > 0 ? pos - 1 : 0;  // the last cached row (rows past it are never used)
     __syncthreads();
 
-    // 2. every wave: its share of the first cache rows, clamped into the cache
-    // (no branch around these loads: it would make later wait counts
+    // 2. every wave: its share of the first cache rows, clamped to the last
+    // cached row (no branch around these loads: it would make later wait counts
     // conservative). Requested only now, so that wave 0's codes do not wait
     // behind them; they arrive while waves 1-7 run the product.
     uint4 kr[KC][2];
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-        const __half* row = Kc + (size_t)min(r + KROWS * c, rows - 1) * kHeadDim + 16 * li;
+        const __half* row = Kc + (size_t)min(r + KROWS * c, last_row) * kHeadDim + 16 * li;
         kr[c][0] = *reinterpret_cast<const uint4*>(row);
         kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
     }
     uint2 vr[VC];
 #pragma unroll
     for (int c = 0; c < VC; ++c)
-        vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(j + kClasses * c, rows - 1) * kHeadDim + 4 * dq);
+        vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(j + kClasses * c, last_row) * kHeadDim + 4 * dq);
 
     // 3. waves 1-7: exact int32 group sums of the 192 rows, then the row epilogues
     if (wave != 0) {
@@ -550,7 +550,7 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
         if (base > 0) {
 #pragma unroll
             for (int c = 0; c < KC; ++c) {
-                const __half* row = Kc + (size_t)min(base + r + KROWS * c, rows - 1) * kHeadDim + 16 * li;
+                const __half* row = Kc + (size_t)min(base + r + KROWS * c, last_row) * kHeadDim + 16 * li;
                 kr[c][0] = *reinterpret_cast<const uint4*>(row);
                 kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
             }
@@ -592,8 +592,8 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
         if (base > 0) {
 #pragma unroll
             for (int c = 0; c < VC; ++c)
-                vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(base + j + kClasses * c, rows - 1) * kHeadDim +
-                                                        4 * dq);
+                vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(base + j + kClasses * c, last_row) *
+                                                        kHeadDim + 4 * dq);
         }
 #pragma unroll
         for (int c = 0; c < VC; ++c) {
