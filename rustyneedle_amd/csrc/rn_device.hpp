@@ -14,6 +14,10 @@ namespace rn {
 
 constexpr int kWave = 64;
 
+// Native 4-int vector: the i8 MFMA accumulator; arrays of it stay in registers
+// where arrays of HIP's int4 struct can be moved to scratch or LDS.
+typedef int v4i __attribute__((ext_vector_type(4)));
+
 // ops.rs:82-90 — clamp, scale by log2(e), round half away from zero, degree-5
 // Horner polynomial in the fraction, times 2^whole assembled from its bits.
 __device__ __forceinline__ float fast_exp(float value) {

@@ -19,8 +19,6 @@
 
 namespace rn {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
 // The integer work of a BM x BN output tile is spread over the 16 waves of a
 // 1024-thread block by group — every (16x16 sub-tile, group) MFMA is one job, each
 // wave issues all the loads of its 4 jobs at once — and the int32 group sums go

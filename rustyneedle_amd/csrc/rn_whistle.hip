@@ -289,98 +289,118 @@ __global__ __launch_bounds__(1024) void int8_attend_one_kernel(Int8AttendParams 
     }
 }
 
+// One 512-thread block per (slice, head) runs the tiles slice, slice + slices,
+// ... of its head: the head's key rows (registers) and value rows (LDS) are
+// loaded once per block and serve every tile it runs; per tile only the
+// queries' codes are loaded.
 __global__ __launch_bounds__(512) void int8_attend_tile_kernel(Int8AttendParams p, int queries) {
     constexpr int NT = 512, Q = kTileQueries;
-    constexpr int KP = kMaxFrames / (NT / 4);
-    // LDS: the value rows (96 KB; reused for the class partials at the end),
-    // the tile's scores / weights [frame][query] (48 KB)
+    constexpr int KT = kMaxFrames / 16 / (NT / 64);  // 16-frame key tiles per wave
+    constexpr int QH = Q / 2;  // queries per pass of the final class sum
+    static_assert(Q == 8, "two groups of 4 output rows of the 16-row MFMA operand");
+    // LDS: the value rows (96 KB), a tile's scores / weights [frame][query]
+    // (48 KB; after the value sums it takes half a tile's class partials)
     __shared__ __align__(16) int8_t v_s[kMaxFrames * 64];
     __shared__ __align__(16) float e_s[kMaxFrames][Q];
     __shared__ float vs_s[kMaxFrames];
     __shared__ float tot_s[Q][32];
     __shared__ float red_s[Q][NT / 64];
     __shared__ float inv_s[Q];
-    static_assert(Q * 32 * 64 * 4 <= kMaxFrames * 64, "partials fit the value area");
-    float(*part_s)[32][64] = reinterpret_cast<float(*)[32][64]>(v_s);
-    const int q0 = blockIdx.x * Q, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    static_assert(QH * 32 * 64 <= kMaxFrames * Q, "half a tile's partials fit the weight area");
+    float(*part_s)[32][64] = reinterpret_cast<float(*)[32][64]>(&e_s[0][0]);
+    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int F = p.frames, H = p.heads;
-    const int li = tid & 3;
-    // 1. loads: the tile's query quarters and scales (queries past the end
-    // repeat the last one), key rows, value rows (into LDS), value scales
-    int4 qq[Q];
-    float qs[Q];
+    const int tiles = (queries + Q - 1) / Q;
+    // 1. once per block: key rows and scales, value rows (into LDS), value
+    // scales; frames past the last repeat the last frame. The keys are held as
+    // i8 MFMA fragments: wave w owns frame tiles w, w + 8, ... (16 frames each);
+    // lane l holds frame 16 t + l % 16, bytes 8 (l / 16) and 32 + 8 (l / 16)
+    const int r16 = lane & 15, kq = lane >> 4;
+    long kf[KT][2];
+    float kfs[KT];
 #pragma unroll
-    for (int i = 0; i < Q; ++i) {
-        const int qi = min(q0 + i, queries - 1);
-        qq[i] = reinterpret_cast<const int4*>(p.qc + ((size_t)qi * H + h) * 64)[li];
-        qs[i] = p.qs[(size_t)qi * H + h];
-    }
-    int4 kr[KP];
-    float ksr[KP];
-#pragma unroll
-    for (int c = 0; c < KP; ++c) {
-        const int fr = min((tid >> 2) + (NT / 4) * c, F - 1);
-        kr[c] = reinterpret_cast<const int4*>(p.kc + ((size_t)fr * H + h) * 64)[li];
-        ksr[c] = p.ks[(size_t)fr * H + h];
+    for (int t = 0; t < KT; ++t) {
+        const int fr = min(16 * (wave + (NT / 64) * t) + r16, F - 1);
+        const int8_t* row = p.kc + ((size_t)fr * H + h) * 64;
+        kf[t][0] = *reinterpret_cast<const long*>(row + 8 * kq);
+        kf[t][1] = *reinterpret_cast<const long*>(row + 32 + 8 * kq);
+        kfs[t] = p.ks[(size_t)fr * H + h];
     }
     stage_values<NT>(p, h, v_s);
     constexpr int SP = kMaxFrames / NT;
-    float vsr[SP];
 #pragma unroll
-    for (int c = 0; c < SP; ++c) vsr[c] = p.vs[(size_t)min(tid + NT * c, F - 1) * H + h];
-    // 2. scores for the tile's queries, and their local peaks
-    float m[Q];
-#pragma unroll
-    for (int i = 0; i < Q; ++i) m[i] = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < KP; ++c) {
-        const int fr = (tid >> 2) + (NT / 4) * c;
-        float s[Q];
-#pragma unroll
-        for (int i = 0; i < Q; ++i) {
-            int dot = dot16(kr[c], qq[i], 0);
-            dot = dot + dpp_move<0xb1>(dot);
-            dot = dot + dpp_move<0x4e>(dot);
-            s[i] = ((float)dot * ksr[c]) * qs[i];
-        }
-        if (fr < F) {
-            if (li == 0) {
-                *reinterpret_cast<float4*>(&e_s[fr][0]) = make_float4(s[0], s[1], s[2], s[3]);
-                *reinterpret_cast<float4*>(&e_s[fr][4]) = make_float4(s[4], s[5], s[6], s[7]);
-            }
-#pragma unroll
-            for (int i = 0; i < Q; ++i) m[i] = fmaxf(m[i], s[i]);
-        }
-    }
-#pragma unroll
-    for (int c = 0; c < SP; ++c) vs_s[tid + NT * c] = vsr[c];
-#pragma unroll
-    for (int i = 0; i < Q; ++i) {
-        const float mm = wave_max(m[i]);
-        if (lane == 0) red_s[i][wave] = mm;
-    }
+    for (int c = 0; c < SP; ++c) vs_s[tid + NT * c] = p.vs[(size_t)min(tid + NT * c, F - 1) * H + h];
     __builtin_amdgcn_s_waitcnt(0);  // this wave's value rows are in LDS
     __syncthreads();
-    // 3. fast_exp weights (element (frame, query) = (e / Q, e % Q))
+
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int q0 = tile * Q;
+    // the tile's query fragments: lane l holds query min(l % 16, Q - 1) (rows 8-15
+    // of the 16-row operand repeat query 7 and are never read), bytes 8 (l / 16)
+    // and 32 + 8 (l / 16); queries past the end repeat the last. Output row
+    // 4 (l / 16) + i of lane l is query 4 (l / 16) + i: lanes 0-31 hold the tile.
+    long qa0, qa1;
+    float qsv[4];
+    {
+        const int qi = min(q0 + min(r16, Q - 1), queries - 1);
+        const int8_t* qrow = p.qc + ((size_t)qi * H + h) * 64;
+        qa0 = *reinterpret_cast<const long*>(qrow + 8 * kq);
+        qa1 = *reinterpret_cast<const long*>(qrow + 32 + 8 * kq);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qsv[i] = p.qs[(size_t)min(q0 + min(4 * kq + i, Q - 1), queries - 1) * H + h];
+    }
+    // 2. scores for the tile's queries (exact int32 dots on the matrix cores, two
+    // 32-byte halves of the head), and their local peaks
+    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa0, kf[t][0], v4i{0, 0, 0, 0}, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa1, kf[t][1], acc, 0, 0, 0);
+        const int fr = 16 * (wave + (NT / 64) * t) + r16;
+        float s[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] = ((float)acc[i] * kfs[t]) * qsv[i];
+        if (kq < 2) {
+            *reinterpret_cast<float4*>(&e_s[fr][4 * kq]) = make_float4(s[0], s[1], s[2], s[3]);
+            if (fr < F)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) m[i] = fmaxf(m[i], s[i]);
+        }
+    }
+    // the peak of each query over the 16 lanes of its row group (lanes 0-15:
+    // queries 0-3, lanes 16-31: queries 4-7)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float mm = m[i];
+        mm = fmaxf(mm, __int_as_float(dpp_move<0xb1>(__float_as_int(mm))));
+        mm = fmaxf(mm, __int_as_float(dpp_move<0x4e>(__float_as_int(mm))));
+        mm = fmaxf(mm, __int_as_float(dpp_move<0x141>(__float_as_int(mm))));
+        mm = fmaxf(mm, __int_as_float(dpp_move<0x140>(__float_as_int(mm))));
+        if (lane == 0 || lane == 16) red_s[4 * kq + i][wave] = mm;
+    }
+    __syncthreads();
+    // 3. fast_exp weights (element (frame, query) = (e / Q, e % Q)); frames past
+    // the last get weight 0, so the loops below run over every frame slot: an
+    // exact +0 addend leaves a running sum that started at +0 unchanged (and
+    // those slots' value rows repeat the last frame, so they are finite)
+    static_assert((kMaxFrames * Q) % NT == 0, "whole weight passes");
     {
         const int i = tid % Q;  // NT is a multiple of Q: each thread keeps one query
         float peak = red_s[i][0];
 #pragma unroll
         for (int w = 1; w < NT / 64; ++w) peak = fmaxf(peak, red_s[i][w]);
-        for (int e = tid; e < F * Q; e += NT) {
+#pragma unroll 4
+        for (int e = tid; e < kMaxFrames * Q; e += NT) {
             float& x = e_s[e / Q][i];
-            x = fast_exp(x - peak);
+            x = e / Q < F ? fast_exp(x - peak) : 0.0f;
         }
     }
     __syncthreads();
     if (tid < Q * 32) {  // class totals: thread (query i, class c)
         const int i = tid >> 5, c = tid & 31;
         float t = 0.0f;
-#pragma unroll 8
-        for (int k = 0; k < kMaxFrames / 32; ++k) {
-            const int j = c + 32 * k;
-            if (j < F) t = t + e_s[j][i];
-        }
+#pragma unroll
+        for (int k = 0; k < kMaxFrames / 32; ++k) t = t + e_s[c + 32 * k][i];
         tot_s[i][c] = t;
     }
     __syncthreads();
@@ -394,7 +414,8 @@ __global__ __launch_bounds__(512) void int8_attend_tile_kernel(Int8AttendParams 
     {
         const int i = tid % Q;
         const float inverse = inv_s[i];
-        for (int e = tid; e < F * Q; e += NT) {
+#pragma unroll 4
+        for (int e = tid; e < kMaxFrames * Q; e += NT) {
             const int j = e / Q;
             e_s[j][i] = vs_s[j] * (e_s[j][i] * inverse);
         }
@@ -407,45 +428,64 @@ __global__ __launch_bounds__(512) void int8_attend_tile_kernel(Int8AttendParams 
     for (int i = 0; i < Q; ++i)
 #pragma unroll
         for (int d = 0; d < 4; ++d) a[i][d] = 0.0f;
-#pragma unroll 2
+#pragma unroll 4
     for (int k = 0; k < kMaxFrames / 32; ++k) {
         const int j = c + 32 * k;
-        if (j < F) {
-            const uint32_t raw = *reinterpret_cast<const uint32_t*>(v_s + j * 64 + 4 * dq);
-            float v[4];
-            int8x2_to_float(raw, v[0], v[1]);
-            int8x2_to_float(raw >> 16, v[2], v[3]);
-            const float4 w0 = *reinterpret_cast<const float4*>(&e_s[j][0]);
-            const float4 w1 = *reinterpret_cast<const float4*>(&e_s[j][4]);
-            const float w[Q] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const uint32_t raw = *reinterpret_cast<const uint32_t*>(v_s + j * 64 + 4 * dq);
+        float v[4];
+        int8x2_to_float(raw, v[0], v[1]);
+        int8x2_to_float(raw >> 16, v[2], v[3]);
+        const float4 w0 = *reinterpret_cast<const float4*>(&e_s[j][0]);
+        const float4 w1 = *reinterpret_cast<const float4*>(&e_s[j][4]);
+        const float w[Q] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-            for (int i = 0; i < Q; ++i)
+        for (int i = 0; i < Q; ++i)
 #pragma unroll
-                for (int d = 0; d < 4; ++d) a[i][d] = a[i][d] + w[i] * v[d];
+            for (int d = 0; d < 4; ++d) a[i][d] = a[i][d] + w[i] * v[d];
+    }
+    // 5. out = the class partials added in class order, half a tile at a time
+    // through the weight area (the value rows stay for the next tile)
+    static_assert(NT == QH * 2 * 64, "one output per thread of each half pass");
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        __syncthreads();  // the area's previous contents are read
+#pragma unroll
+        for (int i = 0; i < QH; ++i) {
+            const float* ai = a[QH * half + i];
+            *reinterpret_cast<float4*>(&part_s[i][c][4 * dq]) = make_float4(ai[0], ai[1], ai[2], ai[3]);
+        }
+        __syncthreads();
+        if (tid < QH * 64) {
+            const int i = tid >> 6, d = tid & 63;
+            float o = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) o = o + part_s[i][k][d];
+            const int qi = q0 + QH * half + i;
+            if (qi < queries) p.out[(size_t)qi * p.out_stride + h * 64 + d] = o;
         }
     }
-    __syncthreads();  // every thread is done with the value rows: reuse them for the partials
-#pragma unroll
-    for (int i = 0; i < Q; ++i)
-        *reinterpret_cast<float4*>(&part_s[i][c][4 * dq]) = make_float4(a[i][0], a[i][1], a[i][2], a[i][3]);
-    __syncthreads();
-    {
-        const int i = tid >> 6, d = tid & 63;  // NT = Q * 64: one output per thread
-        float o = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 32; ++k) o = o + part_s[i][k][d];
-        if (q0 + i < queries) p.out[(size_t)(q0 + i) * p.out_stride + h * 64 + d] = o;
+    __syncthreads();  // the partials are read before the next tile's scores
     }
 }
 
 hipError_t launch_int8_attend(const Int8AttendParams& p, int queries, hipStream_t stream) {
     if (queries <= 0) return hipSuccess;
     if (p.frames < 1 || p.frames > kMaxFrames || p.heads < 1) return hipErrorInvalidValue;
-    if (queries < kTileQueries)
+    if (queries < kTileQueries) {
         rn_launch(int8_attend_one_kernel, dim3(p.heads, queries), dim3(1024), 0, stream, p);
-    else
-        rn_launch(int8_attend_tile_kernel, dim3((queries + kTileQueries - 1) / kTileQueries, p.heads), dim3(512), 0,
-                  stream, p, queries);
+    } else {
+        // one block per CU: as few slices per head as keep the rounds of tiles per
+        // CU at their minimum
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        const int tiles = (queries + kTileQueries - 1) / kTileQueries;
+        const long work = (long)tiles * p.heads;
+        const int rounds = (int)((work + cus - 1) / cus);
+        const int slices = (tiles + rounds - 1) / rounds;
+        rn_launch(int8_attend_tile_kernel, dim3(slices, p.heads), dim3(512), 0, stream, p, queries);
+    }
     return hipGetLastError();
 }
 
