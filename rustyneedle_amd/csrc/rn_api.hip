@@ -965,11 +965,18 @@ int rn_session_feed(rn_session* s, const uint32_t* tokens, int count) {
     RN_HIP(hipMemcpyAsync(tok, tokens, 4 * (size_t)count, hipMemcpyHostToDevice, st));
     RN_HIP(launch_embed_rows(tok, count, m->embedding.W, m->embedding.sW, d, c.vocab, m->embed_scale, X,
                              &s->state->error, st));
+    // a product over float rows (quantised by the product, after the norm when
+    // `gain` is set); Xq / sx take the codes where a separate quantise runs
+    auto rows = [&](const float* in, const float* gain, const DevMatrix& w, int N, int K, float* Y, int ldy, int half) {
+        GemmParams g{Xq, sx, w.W, w.sW, count, N, K, Y, ldy, nullptr, half};
+        g.Xf = in;
+        g.gain = gain;
+        g.eps = c.norm_eps;
+        return g;
+    };
     for (int l = 0; l < c.layers; ++l) {
         const LayerDev& L = m->layers[l];
-        RN_HIP(launch_norm_quantise(X, L.norm_attn, count, d, c.norm_eps, Xq, sx, nullptr, st));
-        RN_HIP(launch_gemm(GemmParams{Xq, sx, L.qkv.W, L.qkv.sW, count, 3 * d, d, QKV, 3 * d, nullptr, 0}, kGemmStore,
-                           kPanel, false, st));
+        RN_HIP(launch_gemm(rows(X, L.norm_attn, L.qkv, 3 * d, d, QKV, 3 * d, 0), kGemmStore, kPanel, false, st));
         RN_HIP(launch_rope_append(QKV, Q, s->kc, s->vc, l, c.heads, s->capacity, d, first, count, m->rope_cos,
                                   m->rope_sin, st));
         AttendParams ap{};
@@ -984,15 +991,9 @@ int rn_session_feed(rn_session* s, const uint32_t* tokens, int count) {
         ap.out = A;
         ap.error = &s->state->error;
         RN_HIP(launch_attend(ap, kAttendPrefill, c.heads, count, first + count, st));
-        RN_HIP(launch_norm_quantise(A, nullptr, count, d, c.norm_eps, Xq, sx, nullptr, st));
-        RN_HIP(launch_gemm(GemmParams{Xq, sx, L.out.W, L.out.sW, count, d, d, X, d, nullptr, 0}, kGemmResidual, kPanel,
-                           false, st));
-        RN_HIP(launch_norm_quantise(X, L.norm_ffn, count, d, c.norm_eps, Xq, sx, nullptr, st));
-        RN_HIP(launch_gemm(GemmParams{Xq, sx, L.gate_up.W, L.gate_up.sW, count, 2 * f, d, F, f, nullptr, f},
-                           kGemmSilu, kPanel, false, st));
-        RN_HIP(launch_norm_quantise(F, nullptr, count, f, c.norm_eps, Xq, sx, nullptr, st));
-        RN_HIP(launch_gemm(GemmParams{Xq, sx, L.down.W, L.down.sW, count, d, f, X, d, nullptr, 0}, kGemmResidual,
-                           kPanel, false, st));
+        RN_HIP(launch_gemm(rows(A, nullptr, L.out, d, d, X, d, 0), kGemmResidual, kPanel, false, st));
+        RN_HIP(launch_gemm(rows(X, L.norm_ffn, L.gate_up, 2 * f, d, F, f, f), kGemmSilu, kPanel, false, st));
+        RN_HIP(launch_gemm(rows(F, nullptr, L.down, d, f, X, d, 0), kGemmResidual, kPanel, false, st));
     }
     RN_HIP(hipMemcpyAsync(s->x, X + (size_t)(count - 1) * d, 4 * (size_t)d, hipMemcpyDeviceToDevice, st));
     RN_HIP(launch_norm_rows(s->x, m->norm_final, 1, d, c.norm_eps, s->hidden, st));
@@ -1099,11 +1100,18 @@ static int enqueue_batch_step(rn_batch* b, int steps, int step) {
     hipStream_t st = b->stream;
     RN_HIP(launch_embed_rows(b->tokens, n, m->embedding.W, m->embedding.sW, d, c.vocab, m->embed_scale, b->X, b->error,
                              st));
+    // a product over float rows (quantised by the product, after the norm when
+    // `gain` is set); Xq / sx take the codes where a separate quantise runs
+    auto rows = [&](const float* in, const float* gain, const DevMatrix& w, int N, int K, float* Y, int ldy, int half) {
+        GemmParams g{b->Xq, b->sx, w.W, w.sW, n, N, K, Y, ldy, nullptr, half};
+        g.Xf = in;
+        g.gain = gain;
+        g.eps = c.norm_eps;
+        return g;
+    };
     for (int l = 0; l < c.layers; ++l) {
         const LayerDev& L = m->layers[l];
-        RN_HIP(launch_norm_quantise(b->X, L.norm_attn, n, d, c.norm_eps, b->Xq, b->sx, nullptr, st));
-        RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, L.qkv.W, L.qkv.sW, n, 3 * d, d, b->QKV, 3 * d, nullptr, 0},
-                           kGemmStore, kPanel, false, st));
+        RN_HIP(launch_gemm(rows(b->X, L.norm_attn, L.qkv, 3 * d, d, b->QKV, 3 * d, 0), kGemmStore, kPanel, false, st));
         AttendParams ap{};
         ap.qkv = b->QKV;
         ap.kc = b->kc;
@@ -1120,15 +1128,9 @@ static int enqueue_batch_step(rn_batch* b, int steps, int step) {
         ap.out = b->A;
         ap.error = b->error;
         RN_HIP(launch_attend(ap, kAttendDecode, c.heads, n, b->capacity, st));
-        RN_HIP(launch_norm_quantise(b->A, nullptr, n, d, c.norm_eps, b->Xq, b->sx, nullptr, st));
-        RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, L.out.W, L.out.sW, n, d, d, b->X, d, nullptr, 0}, kGemmResidual,
-                           kPanel, false, st));
-        RN_HIP(launch_norm_quantise(b->X, L.norm_ffn, n, d, c.norm_eps, b->Xq, b->sx, nullptr, st));
-        RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, L.gate_up.W, L.gate_up.sW, n, 2 * f, d, b->F, f, nullptr, f},
-                           kGemmSilu, kPanel, false, st));
-        RN_HIP(launch_norm_quantise(b->F, nullptr, n, f, c.norm_eps, b->Xq, b->sx, nullptr, st));
-        RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, L.down.W, L.down.sW, n, d, f, b->X, d, nullptr, 0}, kGemmResidual,
-                           kPanel, false, st));
+        RN_HIP(launch_gemm(rows(b->A, nullptr, L.out, d, d, b->X, d, 0), kGemmResidual, kPanel, false, st));
+        RN_HIP(launch_gemm(rows(b->X, L.norm_ffn, L.gate_up, 2 * f, d, b->F, f, f), kGemmSilu, kPanel, false, st));
+        RN_HIP(launch_gemm(rows(b->F, nullptr, L.down, d, f, b->X, d, 0), kGemmResidual, kPanel, false, st));
     }
     // final norm, then the per-row quantisation of the hidden state (session.rs:140-142, 166-177)
     RN_HIP(launch_norm_quantise(b->X, m->norm_final, n, d, c.norm_eps, b->Xq, b->sx, nullptr, st));

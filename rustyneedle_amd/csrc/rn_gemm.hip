@@ -36,11 +36,18 @@ struct SplitShape {
     static_assert(BM * BN <= 1024, "one output per thread");
 };
 
-template <int G, int BM, int BN, int EPI, int FORM, bool DUMP>
+// Token rows of the split kernel: int8 codes and scales given (kRowsCodes), or
+// float rows quantised in the prologue (kRowsQuant: quantise_int8 of
+// ops.rs:103-118, identical to norm_quantise_kernel without gains). One wave
+// per row: lane l holds elements E l .. E l + E - 1.
+enum RowsIn { kRowsCodes = 0, kRowsQuant = 1 };
+
+template <int G, int BM, int BN, int EPI, int FORM, bool DUMP, int AIN>
 __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
     using S = SplitShape<G, BM, BN>;
     constexpr bool kSilu = EPI == kGemmSilu;
     constexpr int K = G * kGroup;
+    static_assert(AIN == kRowsCodes || (BM % 16 == 0 && K % 64 == 0), "whole rows per wave, whole elements per lane");
     // Operand rows padded by 32 bytes: the 16 rows x 4 quarters of one MFMA
     // fragment read then cover all 64 banks twice (the minimum for 512 bytes).
     constexpr int KP = K + 32;
@@ -62,6 +69,17 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
     const int mt = t % mtiles, nt = t / mtiles;
     const int m0 = mt * BM;
 
+    // float token rows (kRowsQuant): requested first, wave w owns rows w,
+    // w + 16, ...; rows past the matrix repeat its last row
+    constexpr int E = AIN != kRowsCodes ? K / 64 : 1;
+    constexpr int RPW = AIN != kRowsCodes ? BM / 16 : 1;
+    float xv[RPW][E];
+    if constexpr (AIN != kRowsCodes) {
+#pragma unroll
+        for (int rr = 0; rr < RPW; ++rr)
+            load_floats<E>(p.Xf + (size_t)min(m0 + wave + 16 * rr, p.M - 1) * K + lane * E, xv[rr]);
+    }
+
     // output column of local column c (silu: first BN/2 gate rows, then the up rows)
     auto column = [&](int c) -> int {
         if constexpr (kSilu)
@@ -74,16 +92,17 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
     // loads (a 64-lane load covers 1 KB of consecutive row bytes), all issued
     // before any is waited for; rows past the matrix repeat its last row
     constexpr int kRow16 = K / 16;  // 16-byte pieces per row
-    constexpr int kPieces = (BM + BN) * kRow16;
-    int4 piece[(kPieces + 1023) / 1024];
+    constexpr int kFirst = AIN != kRowsCodes ? BM * kRow16 : 0;  // float rows: weight pieces only
+    constexpr int kPieces = (BM + BN) * kRow16 - kFirst;
+    v4i piece[(kPieces + 1023) / 1024];  // native vectors stay in registers
 #pragma unroll
     for (int q = 0; q < (kPieces + 1023) / 1024; ++q) {
-        const int i = threadIdx.x + 1024 * q;
-        if (kPieces % 1024 == 0 || i < kPieces) {
+        const int i = kFirst + threadIdx.x + 1024 * q;
+        if (kPieces % 1024 == 0 || i < kFirst + kPieces) {
             const int row = i / kRow16, col = i - row * kRow16;
             const int8_t* src = row < BM ? p.X + (size_t)min(m0 + row, p.M - 1) * K
                                          : p.W + (size_t)min(column(row - BM), p.N - 1) * K;
-            piece[q] = *reinterpret_cast<const int4*>(src + 16 * col);
+            piece[q] = *reinterpret_cast<const v4i*>(src + 16 * col);
         }
     }
     // scales of the tile's columns and rows
@@ -91,13 +110,35 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
         const int c = i / G, g = i - c * G;
         sw_s[c][g] = p.sW[(size_t)min(column(c), p.N - 1) * G + g];
     }
-    if (threadIdx.x < BM) sx_s[threadIdx.x] = p.sx[min(m0 + (int)threadIdx.x, p.M - 1)];
+    if (AIN == kRowsCodes && threadIdx.x < BM) sx_s[threadIdx.x] = p.sx[min(m0 + (int)threadIdx.x, p.M - 1)];
 #pragma unroll
     for (int q = 0; q < (kPieces + 1023) / 1024; ++q) {
-        const int i = threadIdx.x + 1024 * q;
-        if (kPieces % 1024 == 0 || i < kPieces) {
+        const int i = kFirst + threadIdx.x + 1024 * q;
+        if (kPieces % 1024 == 0 || i < kFirst + kPieces) {
             const int row = i / kRow16, col = i - row * kRow16;
-            *reinterpret_cast<int4*>(&a_s[0][0] + (size_t)row * KP + 16 * col) = piece[q];
+            *reinterpret_cast<v4i*>(&a_s[0][0] + (size_t)row * KP + 16 * col) = piece[q];
+        }
+    }
+    if constexpr (AIN != kRowsCodes) {
+        // the token rows' codes and scales, one wave per row
+#pragma unroll
+        for (int rr = 0; rr < RPW; ++rr) {
+            const int row = wave + 16 * rr;
+            const float* v = xv[rr];
+            float peak = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
+            const float scale = int8_scale_from_peak(wave_max(peak));
+            float y[E];
+            quotients<E>(v, scale, y);
+            int8_t* dst = &a_s[row][lane * E];
+#pragma unroll
+            for (int e = 0; e < E; e += 2) {
+                const uint32_t lo = (uint32_t)(uint8_t)(int8_t)code_of_quotient(y[e]);
+                const uint32_t hi = (uint32_t)(uint8_t)(int8_t)code_of_quotient(y[e + 1]);
+                *reinterpret_cast<uint16_t*>(dst + e) = (uint16_t)(lo | (hi << 8));
+            }
+            if (lane == 0) sx_s[row] = scale;
         }
     }
     __syncthreads();
@@ -360,8 +401,9 @@ static void launch_chain(const GemmParams& p, hipStream_t stream) {
 // 32 x 32 (not for the gated FFN, whose waves pair gate and up sub-tiles). The
 // chains are sequential over K, so blocks are the parallelism, and small tiles
 // measured faster than large ones at every size used here.
-template <int EPI, int FORM, bool DUMP>
-static bool launch_chain_by_shape(const GemmParams& p, hipStream_t stream) {
+// Returns the chain shape to use (0-3), or -1 for the split kernel.
+template <int EPI>
+static int chain_pick(const GemmParams& p) {
     const int n_eff = EPI == kGemmSilu ? 2 * p.half : p.N;
     auto blocks = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((n_eff + bn - 1) / bn); };
     struct Shape { int bm, bn; };
@@ -374,7 +416,11 @@ static bool launch_chain_by_shape(const GemmParams& p, hipStream_t stream) {
     }
     // Under 256 blocks the per-block chain over K is the critical path and the
     // split kernel (all groups of a tile in flight at once) is faster.
-    if (blocks(shapes[pick].bm, shapes[pick].bn) < 256) return false;
+    return best < 256 ? -1 : pick;
+}
+
+template <int EPI, int FORM, bool DUMP>
+static void launch_chain_shape(const GemmParams& p, int pick, hipStream_t stream) {
     switch (pick) {
         case 0: launch_chain<2, 2, 2, EPI, FORM, DUMP>(p, stream); break;
         case 1: launch_chain<1, 2, 4, EPI, FORM, DUMP>(p, stream); break;
@@ -383,43 +429,70 @@ static bool launch_chain_by_shape(const GemmParams& p, hipStream_t stream) {
             if constexpr (EPI != kGemmSilu) launch_chain<1, 1, 2, EPI, FORM, DUMP>(p, stream);
             break;
     }
-    return true;
 }
 
-
-template <int G, int BM, int BN, int EPI, int FORM, bool DUMP>
+template <int G, int BM, int BN, int EPI, int FORM, bool DUMP, int AIN>
 static void launch_split(const GemmParams& p, hipStream_t stream) {
     const int mtiles = (p.M + BM - 1) / BM;
     const int ntiles = EPI == kGemmSilu ? (p.half + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
-    rn_launch((gemm_split_kernel<G, BM, BN, EPI, FORM, DUMP>), dim3(mtiles * ntiles), dim3(1024), 0, stream, p);
+    rn_launch((gemm_split_kernel<G, BM, BN, EPI, FORM, DUMP, AIN>), dim3(mtiles * ntiles), dim3(1024), 0, stream, p);
 }
 
-template <int EPI, int FORM, bool DUMP>
+// tiles sized so that the int32 sums of a tile fill 64 KB of LDS
+template <int EPI, int FORM, bool DUMP, int AIN>
 static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
-    // tiles sized so that the int32 sums of a tile fill 64 KB of LDS
     switch (p.K) {
         case 384:
-            launch_split<12, 32, 32, EPI, FORM, DUMP>(p, stream);
+            launch_split<12, 32, 32, EPI, FORM, DUMP, AIN>(p, stream);
             break;
         case 512:
-            launch_split<16, 32, 32, EPI, FORM, DUMP>(p, stream);
+            launch_split<16, 32, 32, EPI, FORM, DUMP, AIN>(p, stream);
             break;
         case 1024:
-            launch_split<32, 16, 32, EPI, FORM, DUMP>(p, stream);
+            launch_split<32, 16, 32, EPI, FORM, DUMP, AIN>(p, stream);
             break;
         case 1536:
-            launch_split<48, 16, 16, EPI, FORM, DUMP>(p, stream);
+            launch_split<48, 16, 16, EPI, FORM, DUMP, AIN>(p, stream);
             break;
         default:
-            launch_split<64, 16, 16, EPI, FORM, DUMP>(p, stream);
+            launch_split<64, 16, 16, EPI, FORM, DUMP, AIN>(p, stream);
             break;
     }
 }
 
-// The chain kernel for large grids, the split kernel for small ones.
-template <int EPI, int FORM, bool DUMP>
-static void launch_product(const GemmParams& p, hipStream_t stream) {
-    if (!launch_chain_by_shape<EPI, FORM, DUMP>(p, stream)) launch_by_rows<EPI, FORM, DUMP>(p, stream);
+// The chain kernel for large grids, the split kernel for small ones. Float
+// input rows without a norm are quantised inside the split kernel when that
+// re-reads little: every column tile of the grid quantises its own rows
+// again, so the fused form is taken for rows of at most 512 and at most 8 MB of
+// re-read floats per launch (measured: the batch-64 and 256-token out products
+// gain about 1.8 us; wider or taller grids, and the normed inputs, do not).
+// Otherwise a quantise launch (with the norm when `gain` is set) writes the
+// codes to X / sx first.
+template <int EPI, int FORM, bool DUMP, int AIN>
+static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
+    const int pick = chain_pick<EPI>(p);
+    const int n_eff = EPI == kGemmSilu ? 2 * p.half : p.N;
+    const size_t reread = (size_t)((n_eff + 31) / 32) * (size_t)p.M * (size_t)p.K * sizeof(float);
+    const bool fused =
+        AIN != kRowsCodes && p.gain == nullptr && pick < 0 && p.K <= 512 && reread <= ((size_t)8 << 20);
+    if (AIN != kRowsCodes && !fused) {
+        const hipError_t e = launch_norm_quantise(p.Xf, p.gain, p.M, p.K, p.eps, const_cast<int8_t*>(p.X),
+                                                  const_cast<float*>(p.sx), nullptr, stream);
+        if (e != hipSuccess) return e;
+    }
+    if (pick >= 0)
+        launch_chain_shape<EPI, FORM, DUMP>(p, pick, stream);
+    else if (fused)
+        launch_by_rows<EPI, FORM, DUMP, kRowsQuant>(p, stream);
+    else
+        launch_by_rows<EPI, FORM, DUMP, kRowsCodes>(p, stream);
+    return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_panel(const GemmParams& p, int ain, hipStream_t stream) {
+    return ain == kRowsQuant ? launch_product<EPI, kPanel, false, kRowsQuant>(p, stream)
+                             : launch_product<EPI, kPanel, false, kRowsCodes>(p, stream);
 }
 
 hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, hipStream_t stream) {
@@ -427,36 +500,28 @@ hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, h
     // instantiated for the supported widths (the kernel is unrolled over groups)
     if ((p.K != 384 && p.K != 512 && p.K != 1024 && p.K != 1536 && p.K != 2048) || p.N <= 0) return hipErrorInvalidValue;
     if (epilogue == kGemmSilu && (p.half % 16 != 0 || p.N != 2 * p.half)) return hipErrorInvalidValue;
-    if (dump) {
+    if (p.Xf != nullptr && (p.X == nullptr || p.sx == nullptr)) return hipErrorInvalidValue;
+    const int ain = p.Xf == nullptr ? kRowsCodes : kRowsQuant;
+    if (dump || form == kPlane) {
+        // the dump and plane-form products take codes: float rows are quantised first
         if (epilogue != kGemmStore) return hipErrorInvalidValue;
-        if (form == kPanel)
-            launch_product<kGemmStore, kPanel, true>(p, stream);
-        else
-            launch_product<kGemmStore, kPlane, true>(p, stream);
-        return hipGetLastError();
-    }
-    if (form == kPlane) {
-        if (epilogue != kGemmStore) return hipErrorInvalidValue;
-        launch_product<kGemmStore, kPlane, false>(p, stream);
-        return hipGetLastError();
+        if (ain != kRowsCodes) {
+            const hipError_t e = launch_norm_quantise(p.Xf, p.gain, p.M, p.K, p.eps, const_cast<int8_t*>(p.X),
+                                                      const_cast<float*>(p.sx), nullptr, stream);
+            if (e != hipSuccess) return e;
+        }
+        if (dump)
+            return form == kPanel ? launch_product<kGemmStore, kPanel, true, kRowsCodes>(p, stream)
+                                  : launch_product<kGemmStore, kPlane, true, kRowsCodes>(p, stream);
+        return launch_product<kGemmStore, kPlane, false, kRowsCodes>(p, stream);
     }
     switch (epilogue) {
-        case kGemmStore:
-            launch_product<kGemmStore, kPanel, false>(p, stream);
-            break;
-        case kGemmResidual:
-            launch_product<kGemmResidual, kPanel, false>(p, stream);
-            break;
-        case kGemmSilu:
-            launch_product<kGemmSilu, kPanel, false>(p, stream);
-            break;
-        case kGemmStoreSilu:
-            launch_product<kGemmStoreSilu, kPanel, false>(p, stream);
-            break;
-        default:
-            return hipErrorInvalidValue;
+        case kGemmStore: return launch_panel<kGemmStore>(p, ain, stream);
+        case kGemmResidual: return launch_panel<kGemmResidual>(p, ain, stream);
+        case kGemmSilu: return launch_panel<kGemmSilu>(p, ain, stream);
+        case kGemmStoreSilu: return launch_panel<kGemmStoreSilu>(p, ain, stream);
+        default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 // ---- row kernels for multi-token work -------------------------------------------

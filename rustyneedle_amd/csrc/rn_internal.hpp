@@ -164,6 +164,13 @@ struct GemmParams {
     int ldy;
     int32_t* acc;      // dump only: [M][N][K/32]
     int half;          // kGemmSilu: gate rows 0..half-1, up rows half..2*half-1 (N == 2*half)
+    // Optional float input rows [M][K] (nullable): the product quantises them
+    // itself, after the zero-centred norm with `gain` when that is set
+    // (ops.rs:44-58, 103-118). X and sx then receive the codes only where a
+    // separate quantise launch is used (large grids); they must be valid.
+    const float* Xf;
+    const float* gain;
+    float eps;
 };
 
 hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, hipStream_t stream);
