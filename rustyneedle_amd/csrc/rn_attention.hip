@@ -5,14 +5,14 @@
 // an fp16 cache: score = q.k / sqrt(head_dim), peak-subtracted fast_exp weights,
 // weighted values, one multiply by 1/total.
 //
-// One 256-thread block per (head, query). Latency is the enemy at these sizes
-// (a head's cache is 2 x L x 128 bytes), so the first chunk of key rows and of
-// value rows (384 positions each) is loaded before the block even reads the
-// current position: only then does it read its q/k/v row, apply the rotary and
-// append the new key/value, which is served from LDS.
+// One block per (head, query): 256 threads, or 512 for the decode of many
+// sequences. Latency is the enemy at these sizes (a head's cache is
+// 2 x L x 128 bytes), so the first chunk of key rows and of value rows is
+// loaded before the block even reads its q/k/v row, applies the rotary and
+// appends the new key/value, which is served from LDS.
 //
-// Scores: 4 lanes per key row, 32 bytes (16 dims) each; the block covers 64
-// rows per pass. Values: 8 lanes per row, 16 bytes (8 dims) each; thread
+// Scores: 4 lanes per key row, 32 bytes (16 dims) each; the block covers NT/4
+// rows per pass. Values: NT/32 lanes per row (8 or 4 dims each); thread
 // (j, dg) walks positions j, j+32, j+64, ... The float reductions follow the
 // fixed trees of the CPU restatement:
 //   score (T2): per 4 dims 0 + q0k0 + ... + q3k3; the 16 sub-sums combined by a
@@ -33,6 +33,20 @@ __device__ __forceinline__ void unpack8(const uint4& raw, float* out) {
     const __half2* h = reinterpret_cast<const __half2*>(&raw);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+        out[2 * i] = __low2float(h[i]);
+        out[2 * i + 1] = __high2float(h[i]);
+    }
+}
+
+// DPV consecutive fp16 values of one value row: the load type and its floats
+template <int DPV> struct ValuePiece;
+template <> struct ValuePiece<8> { using T = uint4; };
+template <> struct ValuePiece<4> { using T = uint2; };
+template <int DPV>
+__device__ __forceinline__ void unpack_values(const typename ValuePiece<DPV>::T& raw, float* out) {
+    const __half2* h = reinterpret_cast<const __half2*>(&raw);
+#pragma unroll
+    for (int i = 0; i < DPV / 2; ++i) {
         out[2 * i] = __low2float(h[i]);
         out[2 * i + 1] = __high2float(h[i]);
     }
@@ -60,22 +74,30 @@ __device__ __forceinline__ float score_row(const float* q16, const uint4& ka, co
     return s;
 }
 
-// KC key passes of 64 rows and VC value positions per thread are issued
-// together (64*KC and 32*VC positions). POS_FIRST (decode of many sequences):
-// read the position before the cache loads and clamp them to it, instead of
-// to the capacity, so that short caches do not fetch the rows of long ones.
-template <int MODE, int KC, int VC, bool POS_FIRST>
-__global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
+// KC key passes of NT/4 rows and VC value positions per thread are issued
+// together (NT/4*KC and 32*VC positions); NT threads, 4 lanes per key row and
+// NT/32 lanes per position class. POS_FIRST (decode of many sequences): read
+// the position before the cache loads and clamp them to it, instead of to the
+// capacity, so that short caches do not fetch the rows of long ones. Passes and
+// value slots past the length are skipped per wave (they add nothing).
+template <int MODE, int KC, int VC, bool POS_FIRST, int NT = 256>
+// (512-thread blocks are held to 128 VGPRs, so that two blocks share a CU)
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 512 ? 4 : 1))) void attend_kernel(
+    AttendParams p) {
+    constexpr int KROWS = NT / 4;         // key rows per pass (4 lanes per row)
+    constexpr int TPC = NT / kClasses;    // value threads per position class
+    constexpr int DPV = kHeadDim / TPC;   // value dims per thread
+    using VPiece = typename ValuePiece<DPV>::T;
     extern __shared__ float scores[];
     __shared__ float q_s[kHeadDim];
     __shared__ __align__(16) __half new_s[2][kHeadDim];  // decode: the appended key and value
     __shared__ float part_s[kClasses][kHeadDim];
     __shared__ float total_s[kClasses];
-    __shared__ float peak_s[4];
+    __shared__ float peak_s[NT / 64];
 
-    const int tid = threadIdx.x;
-    const int r = tid >> 2, li = tid & 3;    // score layout: row slot (64 per pass), 16-dim lane
-    const int j = tid >> 3, dg = tid & 7;    // value layout: position class (32), 8-dim lane
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int r = tid >> 2, li = tid & 3;     // score layout: row slot (KROWS per pass), 16-dim lane
+    const int j = tid / TPC, dg = tid % TPC;  // value layout: position class (32), DPV-dim lane
 
     const __half* K;
     const __half* V;
@@ -123,14 +145,14 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
     uint4 kr[KC][2];
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-        const __half* row = K + (size_t)min(r + 64 * c, rows - 1) * kHeadDim + 16 * li;
+        const __half* row = K + (size_t)min(r + KROWS * c, rows - 1) * kHeadDim + 16 * li;
         kr[c][0] = *reinterpret_cast<const uint4*>(row);
         kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
     }
-    uint4 vr[VC];
+    VPiece vr[VC];
 #pragma unroll
     for (int c = 0; c < VC; ++c)
-        vr[c] = *reinterpret_cast<const uint4*>(V + (size_t)min(j + kClasses * c, rows - 1) * kHeadDim + 8 * dg);
+        vr[c] = *reinterpret_cast<const VPiece*>(V + (size_t)min(j + kClasses * c, rows - 1) * kHeadDim + DPV * dg);
 
     // 2. the length, the query and (decoding) the rotary + fp16 append of the new row
     if constexpr (MODE == kAttendDecode) {
@@ -188,20 +210,22 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
     float q16[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) q16[i] = q_s[16 * li + i];
-    for (int base = 0; base < nglobal; base += 64 * KC) {
+    for (int base = 0; base < nglobal; base += KROWS * KC) {
         if (base > 0) {
 #pragma unroll
             for (int c = 0; c < KC; ++c) {
-                const __half* row = K + (size_t)min(base + r + 64 * c, rows - 1) * kHeadDim + 16 * li;
+                const __half* row = K + (size_t)min(base + r + KROWS * c, rows - 1) * kHeadDim + 16 * li;
                 kr[c][0] = *reinterpret_cast<const uint4*>(row);
                 kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
             }
         }
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
-            const int pp = base + r + 64 * c;
-            const float s = score_row(q16, kr[c][0], kr[c][1]);
-            if (li == 0 && pp < nglobal) scores[pp] = s * inverse_root;
+            const int pp = base + r + KROWS * c;
+            if (base + KROWS * c + 16 * wave < nglobal) {  // wave-uniform: the wave's rows hold live positions
+                const float s = score_row(q16, kr[c][0], kr[c][1]);
+                if (li == 0 && pp < nglobal) scores[pp] = s * inverse_root;
+            }
         }
     }
     if (has_new && tid < 4) {
@@ -214,35 +238,41 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
 
     // 4. peak (order-free) and the fast_exp weights
     float m = -INFINITY;
-    for (int pp = tid; pp < length; pp += 256) m = fmaxf(m, scores[pp]);
+    for (int pp = tid; pp < length; pp += NT) m = fmaxf(m, scores[pp]);
     m = wave_max(m);
-    if ((tid & 63) == 0) peak_s[tid >> 6] = m;
+    if ((tid & 63) == 0) peak_s[wave] = m;
     __syncthreads();
-    const float peak = fmaxf(fmaxf(peak_s[0], peak_s[1]), fmaxf(peak_s[2], peak_s[3]));
-    for (int pp = tid; pp < length; pp += 256) scores[pp] = fast_exp(scores[pp] - peak);
+    float peak = peak_s[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) peak = fmaxf(peak, peak_s[w]);
+    for (int pp = tid; pp < length; pp += NT) scores[pp] = fast_exp(scores[pp] - peak);
     __syncthreads();
 
     // 5. weighted values (T3): thread (j, dg) walks positions j, j+32, ... in order
-    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[DPV];
+#pragma unroll
+    for (int i = 0; i < DPV; ++i) acc[i] = 0.0f;
     float total = 0.0f;
     const int last = nglobal > 0 ? nglobal - 1 : 0;
     for (int base = 0; base < nglobal; base += kClasses * VC) {
         if (base > 0) {
 #pragma unroll
             for (int c = 0; c < VC; ++c)
-                vr[c] = *reinterpret_cast<const uint4*>(V + (size_t)min(base + j + kClasses * c, rows - 1) * kHeadDim +
-                                                        8 * dg);
+                vr[c] = *reinterpret_cast<const VPiece*>(V + (size_t)min(base + j + kClasses * c, rows - 1) * kHeadDim +
+                                                         DPV * dg);
         }
 #pragma unroll
         for (int c = 0; c < VC; ++c) {
             const int pp = base + j + kClasses * c;
+            // wave-uniform: the wave's classes hold no live position in this slot
+            if (base + kClasses * c + (64 / TPC) * wave >= nglobal) continue;
             const bool ok = pp < nglobal;
             const float e = scores[min(pp, last)];
-            float v8[8];
-            unpack8(vr[c], v8);
+            float vv[DPV];
+            unpack_values<DPV>(vr[c], vv);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float t = acc[i] + e * v8[i];
+            for (int i = 0; i < DPV; ++i) {
+                const float t = acc[i] + e * vv[i];
                 acc[i] = ok ? t : acc[i];
             }
             const float tt = total + e;
@@ -251,14 +281,14 @@ __global__ __launch_bounds__(256) void attend_kernel(AttendParams p) {
     }
     if (has_new && j == (nglobal & (kClasses - 1))) {  // the newest position closes its class
         const float e = scores[nglobal];
-        float v8[8];
-        unpack8(*reinterpret_cast<const uint4*>(&new_s[1][8 * dg]), v8);
+        float vv[DPV];
+        unpack_values<DPV>(*reinterpret_cast<const VPiece*>(&new_s[1][DPV * dg]), vv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = acc[i] + e * v8[i];
+        for (int i = 0; i < DPV; ++i) acc[i] = acc[i] + e * vv[i];
         total = total + e;
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) part_s[j][8 * dg + i] = acc[i];
+    for (int i = 0; i < DPV; ++i) part_s[j][DPV * dg + i] = acc[i];
     if (dg == 0) total_s[j] = total;
     __syncthreads();
     if (tid < kHeadDim) {
@@ -283,7 +313,7 @@ hipError_t launch_attend(const AttendParams& p, int mode, int grid_x, int grid_y
             if (grid_y == 1)  // one sequence: its loads go out before its position is read
                 rn_launch((attend_kernel<kAttendDecode, 6, 12, false>), grid, dim3(256), lds, stream, p);
             else              // many ragged sequences: exact clamps, one pass up to 576 positions
-                rn_launch((attend_kernel<kAttendDecode, 9, 18, true>), grid, dim3(256), lds, stream, p);
+                rn_launch((attend_kernel<kAttendDecode, 5, 18, true, 512>), grid, dim3(512), lds, stream, p);
             break;
         case kAttendPrefill:
             rn_launch((attend_kernel<kAttendPrefill, 4, 8, false>), grid, dim3(256), lds, stream, p);
