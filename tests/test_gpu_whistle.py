@@ -78,6 +78,27 @@ def test_full_size_encode_and_48_tokens():
     assert ids.tolist() == o.session(cfg["max_positions"], o.memory(ref)).greedy(first, 48).tolist()
 
 
+def test_d512_eight_heads():
+    """d_model 512 (8 heads, FFN 2048): the 512-wide cross kernel, class-sum and
+    cross-norm prologues and the 8-head encoder attention, against the oracle."""
+    cfg = dict(rn.WHISTLE)
+    cfg.update(d_model=512, heads=8, ffn=2048, frames=80, enc_layers=1, dec_layers=2, vocab=1000, max_positions=16)
+    w = rn.synthetic_whistle_weights(cfg, seed=13)
+    o, g, mel = oracle.OracleWhistle(cfg, w), rn.Whistle(cfg, seed=13), rn.synthetic_mel(cfg, seed=13)
+    enc = g.encode(mel)
+    ref = o.encode(mel)
+    assert enc.shape == (40, 512)
+    assert np.array_equal(_bits(enc), _bits(ref))
+    mem = o.memory(ref)
+    s = o.session(cfg["max_positions"], mem)
+    for tok in (2, 999, 31):
+        g.push(tok)
+        s.push(tok)
+        assert np.array_equal(_bits(g.logits()), _bits(s.logits()))
+    g.reset()
+    assert g.decode_greedy(5, 10).tolist() == o.session(cfg["max_positions"], mem).greedy(5, 10).tolist()
+
+
 @pytest.mark.parametrize("mel_frames", [2, 17, 100])
 def test_ragged_frame_counts(mel_frames):
     """1, 9 and 50 encoder frames: a single frame, a last query tile of one, a
