@@ -151,6 +151,14 @@ __device__ __forceinline__ int dot16(const int4& w, const int4& x, int c) {
     return c;
 }
 
+__device__ __forceinline__ int dot16(const v4i& w, const int4& x, int c) {
+    c = dot4(w.x, x.x, c);
+    c = dot4(w.y, x.y, c);
+    c = dot4(w.z, x.z, c);
+    c = dot4(w.w, x.w, c);
+    return c;
+}
+
 // Greedy key for generator.rs:257-265: larger float first, then lower index.
 // NaN maps to 0 so it never wins; a NaN at index 0 is handled by the caller.
 __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t index) {

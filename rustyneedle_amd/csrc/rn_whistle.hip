@@ -499,21 +499,24 @@ hipError_t launch_int8_attend(const Int8AttendParams& p, int queries, hipStream_
 // through one CU); split eight ways, the redundant part (keys, scores, softmax
 // total) costs less than the split saves. The block's loads (about 150 KB,
 // the bound of the front half: one CU takes about 64 bytes a clock) are all
-// requested at the start, behind wave 0's input vector:
-//   1. wave 0 requests x and the cross gains, waves 1-15 the head's 64 rows of
-//      the cross q matrix (wave 1 also their scales and the q_norm gains); then
-//      every thread its memory rows: the key row of frame tid (64 bytes), half
-//      the key row of frame 1024 + tid / 2 (32 bytes), a 16-byte piece of the
-//      group's value rows, a value scale;
+// requested at the start, each by the wave that uses it, and no barrier
+// separates the q product from them:
+//   1. wave 0 requests x, the cross gains, the q rows' scales and the q_norm
+//      gains; waves 1..kProductWaves the head's 64 rows of the cross q matrix;
+//      each thread t of the memory waves (kProductWaves + 1 .. 15) the key rows
+//      of frames t and t + 768, a 16-byte piece of the group's value rows and
+//      a value scale;
 //   2. wave 0: the zero-centred norm of x (eight-lane sum of ops.rs:7-17) and
-//      its int8 codes (ops.rs:103-118) into LDS;
-//   3. waves 1-15: v_dot4 group sums (lane pairs joined into 32-code groups);
-//      wave 1 lane r: row r's panel epilogue fmaf(acc, sW * sx, total)
-//      (panel.rs:184-188), then the head's zero-centred q norm with the q_norm
-//      gains, its int8 codes and scale times 1/sqrt(64) (encoder.rs:239-244);
-//   4. scores ((float)(q . k) * key_scale) * query_scale (exact int32 dot; the
-//      half rows joined across the lane pair), the peak, fast_exp(score - peak)
-//      for every frame (0 past the last);
+//      its int8 codes (ops.rs:103-118) into LDS, then it raises an LDS flag;
+//   3. the product waves, once the flag is up: v_dot4 group sums (lane pairs
+//      joined into 32-code groups), each then counting itself done in LDS;
+//      wave 1, once all have: lane r runs row r's panel epilogue
+//      fmaf(acc, sW * sx, total) (panel.rs:184-188), then the head's
+//      zero-centred q norm with the q_norm gains, its int8 codes and scale
+//      times 1/sqrt(64) (encoder.rs:239-244);
+//   4. the memory waves: scores ((float)(q . k) * key_scale) * query_scale
+//      (exact int32 dot), the peak, fast_exp(score - peak) for every frame (0
+//      past the last);
 //   5. wave 0: the 32 class totals (frames c, c+32, ... in order), their sum
 //      over classes 0..31, inverse = 1/total, and the group's weights
 //      value_scale * (e * inverse) (ops.rs:92-101, encoder.rs:278-285), while
@@ -527,16 +530,21 @@ hipError_t launch_int8_attend(const Int8AttendParams& p, int queries, hipStream_
 constexpr int kCrossGroups = 8;
 constexpr int kGroupClasses = 32 / kCrossGroups;
 constexpr int kCrossRows = kMaxFrames / kCrossGroups;  // value rows per block
+constexpr int kProductWaves = 3;                        // waves 1..3 take the q product
 
 template <int K>
 __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p) {
     constexpr int NT = 1024;
-    constexpr int G = K / kGroup, CPR = K / 16, CHUNKS = kWave * CPR, LW = NT - kWave;
+    constexpr int G = K / kGroup, CPR = K / 16, CHUNKS = kWave * CPR;
+    constexpr int LW = kProductWaves * kWave;   // threads of the q product (waves 1..kProductWaves)
     constexpr int NLW = (CHUNKS + LW - 1) / LW;
+    constexpr int MW0 = 1 + kProductWaves;      // first memory wave
+    constexpr int MT = NT - MW0 * kWave;        // memory threads
     constexpr int E = K / kWave;
     constexpr int FPC = kMaxFrames / 32;  // frame slots per class
-    static_assert(kMaxFrames == NT + NT / 2, "a full key row and half a key row per thread");
-    static_assert(kCrossRows * 4 <= NT && kCrossRows % kWave == 0, "one value piece per thread, whole weight rows");
+    static_assert(kMaxFrames == 2 * MT, "two key rows per memory thread");
+    static_assert(kCrossRows * 4 <= MT && kCrossRows <= MT && kCrossRows % kWave == 0,
+                  "one value piece and one value scale per memory thread, whole weight rows");
     static_assert(kGroupClasses + 1 <= NT / kWave, "value-sum waves besides wave 0");
     static_assert(E % 2 == 0 && G % 4 == 0 && CPR % 2 == 0, "float pairs, scale quads, code pairs");
     __shared__ __align__(16) int8_t v_s[kCrossRows * 64];
@@ -550,6 +558,7 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
     __shared__ __align__(16) float4 sw_s[kWave][G / 4];
     __shared__ float qg_s[kWave];
     __shared__ float sx_s, qs_s;
+    __shared__ int codes_ready_s, rows_done_s;  // LDS flags between waves 0 and 1..kProductWaves
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x & 7, g = blockIdx.x >> 3;
@@ -558,37 +567,59 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
     auto frame_of_row = [&](int r) -> int {
         return 32 * (r / kGroupClasses) + kGroupClasses * g + r % kGroupClasses;
     };
+    if (tid == 0) {
+        codes_ready_s = 0;
+        rows_done_s = 0;
+    }
+    __syncthreads();  // the flags start at zero before any wave waits on them
 
-    // 1. requests: the prologue inputs (wave 0) or the head's weight rows
-    // (waves 1-15) first, then every thread's memory rows
+    // 1. requests: wave 0 the prologue inputs (and the q rows' scales and the
+    // q_norm gains, staged in LDS for wave 1); the product waves the head's 64
+    // rows of the cross q matrix; the memory waves the key rows of frames t and
+    // t + MT (t = tid - 64 MW0), a 16-byte piece of the group's value rows and a
+    // value scale. Frames past the last repeat the last frame; offsets fit 32
+    // bits (at most 1536 x 8 x 64 bytes).
+    // The product waves' chunks and the memory waves' rows share one register
+    // array r: every variable set in one branch of this phase stays live past
+    // it, so separate arrays would each take registers in every wave.
     typedef float v4f __attribute__((ext_vector_type(4)));  // kept in registers, unlike float4 arrays
-    int4 w[NLW];
+    constexpr int RW = NLW > 9 ? NLW : 9;  // product: r[0..NLW); memory: keys r[0..8), values r[8]
+    v4i r[RW];
     v4f sv[G / 4];
     float qgain = 0.0f;
     float v[E], gv[E];
+    const int t = tid - MW0 * kWave;  // memory thread index (memory waves only)
+    float ks0 = 0.0f, ks1 = 0.0f, vsr = 0.0f;
     if (wave == 0) {
-        // also the q rows' scales (lane r: row r) and the q_norm gains, staged
-        // in LDS for wave 1's epilogue: a wave of the product that waits on
-        // loads of its own before its memory requests would hold them back
         load_floats<E>(p.x + lane * E, v);
         load_floats<E>(p.gain + lane * E, gv);
         const v4f* src = reinterpret_cast<const v4f*>(p.sW + (size_t)(kWave * h + lane) * G);
 #pragma unroll
         for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
         qgain = p.q_gain[lane];
-    } else {
+    } else if (wave < MW0) {
         // chunk c = LW jj + (tid - 64): chunk c % CPR of head row c / CPR
 #pragma unroll
         for (int jj = 0; jj < NLW; ++jj) {
             const int c = min(LW * jj + tid - kWave, CHUNKS - 1);
-            w[jj] = *reinterpret_cast<const int4*>(p.W + (size_t)(kWave * h + c / CPR) * K + (c % CPR) * 16);
+            r[jj] = *reinterpret_cast<const v4i*>(p.W + (size_t)(kWave * h + c / CPR) * K + (c % CPR) * 16);
         }
+    } else {
+        const uint32_t fh0 = (uint32_t)(min(t, F - 1) * H + h);
+        const uint32_t fh1 = (uint32_t)(min(MT + t, F - 1) * H + h);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = reinterpret_cast<const v4i*>(p.kc + fh0 * 64u)[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[4 + i] = reinterpret_cast<const v4i*>(p.kc + fh1 * 64u)[i];
+        ks0 = p.ks[fh0];
+        ks1 = p.ks[fh1];
+        r[8] = *reinterpret_cast<const v4i*>(p.vc + (uint32_t)(min(frame_of_row(t >> 2), F - 1) * H + h) * 64u +
+                                             (uint32_t)(t & 3) * 16u);
+        vsr = p.vs[(uint32_t)(min(frame_of_row(min(t, kCrossRows - 1)), F - 1) * H + h)];
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. wave 0: the input's norm and int8 codes, before its memory requests
-    // (a wave issues in order, and the memory requests queue behind the other
-    // waves' for about a microsecond)
+    // 2. wave 0: the input's norm and int8 codes; then it raises codes_ready_s
     if (wave == 0) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -636,39 +667,40 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
 #pragma unroll
         for (int i = 0; i < G / 4; ++i) sw_s[lane][i] = make_float4(sv[i].x, sv[i].y, sv[i].z, sv[i].w);
         qg_s[lane] = qgain;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_store(&codes_ready_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    // every thread's memory rows: frames past the last repeat the last frame;
-    // offsets fit 32 bits (at most 1536 x 8 x 64 bytes)
-    const int half = tid & 1;
-    const uint32_t fh0 = (uint32_t)(min(tid, F - 1) * H + h);
-    const uint32_t fh1 = (uint32_t)(min(NT + (tid >> 1), F - 1) * H + h);
-    int4 k0[4], k1[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) k0[i] = reinterpret_cast<const int4*>(p.kc + fh0 * 64u)[i];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) k1[i] = reinterpret_cast<const int4*>(p.kc + fh1 * 64u + 32u * half)[i];
-    const float ks0 = p.ks[fh0], ks1 = p.ks[fh1];
-    const int vpiece = min(tid, kCrossRows * 4 - 1);
-    const int4 vr = *reinterpret_cast<const int4*>(
-        p.vc + (uint32_t)(min(frame_of_row(vpiece >> 2), F - 1) * H + h) * 64u + (uint32_t)(vpiece & 3) * 16u);
-    const int vrow = min(tid, kCrossRows - 1);
-    const float vsr = p.vs[(uint32_t)(min(frame_of_row(vrow), F - 1) * H + h)];
-    __builtin_amdgcn_sched_barrier(0);  // requested before the product, not sunk below it
-    __syncthreads();
 
-    // 3. the head's q rows: group sums, then wave 1's row epilogues and head codes
-    if (wave != 0) {
+    // 3. the head's q rows: the product waves wait for the codes on the LDS flag
+    // (not a barrier: the memory waves may still be issuing their requests), add
+    // their group sums, and count themselves done; wave 1 then runs the row
+    // epilogues and the head's q codes. Both waits end once the waves they wait
+    // for have passed the flag writes above and below, which no branch skips;
+    // the spin is bounded all the same.
+    if (wave >= 1 && wave < MW0) {
+        for (int spin = 0; spin < (1 << 22); ++spin) {
+            if (__hip_atomic_load(&codes_ready_s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 #pragma unroll
         for (int jj = 0; jj < NLW; ++jj) {
             const int c = LW * jj + tid - kWave;
             const int4 xc = *reinterpret_cast<const int4*>(xq_s + (min(c, CHUNKS - 1) % CPR) * 16);
-            int part = dot16(w[jj], xc, 0);
+            int part = dot16(r[jj], xc, 0);
             part = part + dpp_move<0xb1>(part);  // the pair partner (lane ^ 1: chunk c ^ 1)
             if ((tid & 1) == 0 && c < CHUNKS) acc_s[(c / CPR) * G + (c % CPR) / 2] = part;
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&rows_done_s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    __syncthreads();
     if (wave == 1) {
+        for (int spin = 0; spin < (1 << 22); ++spin) {
+            if (__hip_atomic_load(&rows_done_s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == kProductWaves)
+                break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         const float sx = sx_s;
         const int4* arow = reinterpret_cast<const int4*>(acc_s + lane * G);
         float q = 0.0f;
@@ -699,31 +731,35 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
     }
     __syncthreads();
 
-    // 4. scores and their peak; the group's value rows into LDS
-    const float qs = qs_s;
-    float sc0, sc1;
-    {
+    // 4. the memory waves: scores of frames t and t + MT and their peak; the
+    // group's value rows and scales into LDS
+    float sc0 = 0.0f, sc1 = 0.0f, m = -INFINITY;
+    if (wave >= MW0) {
+        const float qs = qs_s;
         int d0 = 0, d1 = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) d0 = dot16(k0[i], reinterpret_cast<const int4*>(qc_s)[i], d0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) d1 = dot16(k1[i], reinterpret_cast<const int4*>(qc_s)[2 * half + i], d1);
-        d1 = d1 + dpp_move<0xb1>(d1);  // the other half row (lane ^ 1)
+        for (int i = 0; i < 4; ++i) {
+            const int4 qv = reinterpret_cast<const int4*>(qc_s)[i];
+            d0 = dot16(r[i], qv, d0);
+            d1 = dot16(r[4 + i], qv, d1);
+        }
         sc0 = ((float)d0 * ks0) * qs;
         sc1 = ((float)d1 * ks1) * qs;
+        if (t < F) m = sc0;
+        if (MT + t < F) m = fmaxf(m, sc1);
+        reinterpret_cast<v4i*>(v_s)[t] = r[8];
+        if (t < kCrossRows) w_s[t] = frame_of_row(t) < F ? vsr : 0.0f;  // value scales for now
     }
-    float m = tid < F ? sc0 : -INFINITY;
-    if (NT + (tid >> 1) < F) m = fmaxf(m, sc1);
     m = wave_max(m);
     if (lane == 0) red_s[wave] = m;
-    if (tid < kCrossRows * 4) reinterpret_cast<int4*>(v_s)[tid] = vr;
-    if (tid < kCrossRows) w_s[tid] = frame_of_row(tid) < F ? vsr : 0.0f;  // value scales for now
     __syncthreads();
     float peak = red_s[0];
 #pragma unroll
     for (int i = 1; i < NT / kWave; ++i) peak = fmaxf(peak, red_s[i]);
-    e_s[tid] = tid < F ? fast_exp(sc0 - peak) : 0.0f;
-    if (half == 0) e_s[NT + (tid >> 1)] = NT + (tid >> 1) < F ? fast_exp(sc1 - peak) : 0.0f;
+    if (wave >= MW0) {
+        e_s[t] = t < F ? fast_exp(sc0 - peak) : 0.0f;
+        e_s[MT + t] = MT + t < F ? fast_exp(sc1 - peak) : 0.0f;
+    }
     __syncthreads();
 
     // 5. wave 0: class totals, total, and the group's weights; the value-sum
