@@ -100,8 +100,31 @@ int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, floa
                              void* stream);
 
 /* QuantisedMatrix::dequantise_row (matrix.rs:140-153) for int8 codes: out[k] =
- * code * scale(group of k). Host output of `columns` floats. */
+ * code * scale(group of k); for codebook matrices (level[index] * norm) then
+ * the Walsh-Hadamard transform of each group, on the device. Host output of
+ * `columns` floats. */
 int rn_matrix_dequantise_row(const rn_matrix* m, int row, float* out);
+
+/* ---- the codebook weight format (docs/format.md "Codebook-quantised matrices") ----
+ * Replaces QuantisedMatrix::from_archive/from_parts (matrix.rs:35-59) for a
+ * kind-3 record (cact record.rs:7-84): `blob` is the record's bytes as the
+ * archive holds them (packed indices LSB first, rows x padded x index_bits / 8
+ * bytes, then rows x padded / group fp16 norms), `codebook` the archive's 28
+ * levels (2-bit 0..3, 3-bit 4..11, 4-bit 12..27). bits 2, 4 or 5 (ternary
+ * crumbs); group 64, 128 or 256. The blob is copied to the device as is.
+ * The multiply entry points above then take the ROTATED input of
+ * rn_matrix_prepare ([count][padded] floats), quantise it per group and run
+ * the integer path: 2-bit matrices the panel form (panel.rs:153-197), 4-bit and
+ * ternary ones the plane form (neon.rs:126-183). multiply_fused on codebook
+ * matrices launches once per matrix. */
+int rn_matrix_create_codebook(const uint8_t* blob, size_t blob_bytes, int rows, int columns, int group, int bits,
+                              const float* codebook, int codebook_len, rn_matrix** out);
+/* QuantisedMatrix::padded_columns (matrix.rs:69-71); columns for int8 matrices. */
+int rn_matrix_padded_columns(const rn_matrix* m, int* padded);
+/* QuantisedMatrix::prepare / prepare_batch (matrix.rs:123-138): x [count][columns]
+ * -> rotated [count][padded], zero-padded and rotated group by group
+ * (walsh.rs:41-80). Codebook matrices only. Device pointers. */
+int rn_matrix_prepare(const rn_matrix* m, const float* x, int count, float* rotated, void* stream);
 
 /* ops::quantise_int8 (ops.rs:112-118) for `count` rows of `columns` floats on
  * the device: codes [count][columns], scales [count]. */

@@ -465,3 +465,96 @@ class OracleWhistleSession:
         lib.ro_whistle_greedy(C.byref(self.model.cfg), C.byref(self.model.model), C.byref(self.s), first, steps,
                               _ptr(ids))
         return ids
+
+
+# ---- codebook weight format (rn_codebook.c) ------------------------------------
+lib.ro_walsh_transform.argtypes = [_p, _i]
+lib.ro_codebook_prepare.argtypes = [_p, _i, _i, _i, _p]
+lib.ro_codebook_levels.restype = _i
+lib.ro_codebook_levels.argtypes = [_p, _i, _i, _p]
+lib.ro_integer_levels.restype = _f
+lib.ro_integer_levels.argtypes = [_p, _i, _p]
+lib.ro_group_codes.argtypes = [_p, _i, _i, _p, _p]
+lib.ro_codebook_product.argtypes = [_p, _p, _i, _i, _i, _i, _p, _f, _p, _p, _i, _p, _p]
+lib.ro_codebook_dequantise_row.argtypes = [_p, _p, _i, _i, _i, _i, _p, _i, _p]
+
+
+def walsh_transform(v) -> np.ndarray:
+    v = _f32(v).copy()
+    lib.ro_walsh_transform(_ptr(v), v.size)
+    return v
+
+
+def codebook_prepare(x, padded: int, group: int) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty(padded, np.float32)
+    lib.ro_codebook_prepare(_ptr(x), x.size, padded, group, _ptr(out))
+    return out
+
+
+def codebook_levels(codebook, bits: int, group: int):
+    cb = _f32(codebook)
+    levels = np.empty(16, np.float32)
+    count = lib.ro_codebook_levels(_ptr(cb), bits, group, _ptr(levels))
+    return levels, count
+
+
+def integer_levels(levels, count: int):
+    levels = _f32(levels)
+    table = np.empty(16, np.int8)
+    scale = lib.ro_integer_levels(_ptr(levels), count, _ptr(table))
+    return table, np.float32(scale)
+
+
+def group_codes(rotated, group: int):
+    r = _f32(rotated)
+    codes = np.empty(r.size, np.int8)
+    scales = np.empty(r.size // group, np.float32)
+    lib.ro_group_codes(_ptr(r), r.size, group, _ptr(codes), _ptr(scales))
+    return codes, scales
+
+
+class OracleCodebookMatrix:
+    """A codebook-quantised matrix from its archive blob (packed indices, then
+    fp16 norms), restating QuantisedMatrix's integer path."""
+
+    def __init__(self, blob, rows: int, columns: int, group: int, bits: int, codebook):
+        self.rows, self.columns, self.group, self.bits = rows, columns, group, bits
+        self.padded = -(-columns // group) * group
+        ib = 2 if bits == 5 else bits
+        packed_len = rows * self.padded * ib // 8
+        blob = np.ascontiguousarray(blob, dtype=np.uint8)
+        self.packed = np.ascontiguousarray(blob[:packed_len])
+        self.norms = np.ascontiguousarray(blob[packed_len:packed_len + rows * (self.padded // group) * 2]).view(np.uint16)
+        self.levels, self.count = codebook_levels(codebook, bits, group)
+        self.table, self.lscale = integer_levels(self.levels, self.count)
+
+    def prepare(self, x) -> np.ndarray:
+        return codebook_prepare(x, self.padded, self.group)
+
+    def multiply_rotated(self, rotated, with_acc: bool = False):
+        """rotated [count][padded] -> y [count][rows] (acc [count][rows][groups])."""
+        rotated = _f32(rotated).reshape(-1, self.padded)
+        count = rotated.shape[0]
+        codes = np.empty(rotated.shape, np.int8)
+        scales = np.empty((count, self.padded // self.group), np.float32)
+        for t in range(count):
+            codes[t], scales[t] = group_codes(rotated[t], self.group)
+        y = np.empty((count, self.rows), np.float32)
+        acc = np.empty((count, self.rows, self.padded // self.group), np.int32) if with_acc else None
+        lib.ro_codebook_product(_ptr(self.packed), _ptr(self.norms), self.rows, self.padded, self.group, self.bits,
+                                _ptr(self.table), float(self.lscale), _ptr(codes), _ptr(scales), count, _ptr(y),
+                                _ptr(acc) if acc is not None else None)
+        return (y, acc) if with_acc else y
+
+    def multiply(self, x, with_acc: bool = False):
+        """Unrotated inputs [count][columns]: prepare, then the product."""
+        x = _f32(x).reshape(-1, self.columns)
+        rotated = np.stack([self.prepare(row) for row in x])
+        return self.multiply_rotated(rotated, with_acc)
+
+    def dequantise_row(self, row: int) -> np.ndarray:
+        out = np.empty(self.columns, np.float32)
+        lib.ro_codebook_dequantise_row(_ptr(self.packed), _ptr(self.norms), self.padded, self.columns, self.group,
+                                       self.bits, _ptr(self.levels), row, _ptr(out))
+        return out

@@ -134,6 +134,20 @@ void ro_greedy(const ro_config* c, const ro_model* m, ro_session* s, uint32_t fi
 void ro_set_threads(int threads);
 int ro_get_threads(void);
 
+/* ---- codebook weight format (rn_codebook.c) ----------------------------------
+ * Packed 2-bit / 4-bit / ternary indices with fp16 group norms, rotated input
+ * (walsh.rs, matrix.rs, neon.rs, panel.rs); bits 5 marks ternary crumbs. */
+void ro_walsh_transform(float* v, int n);                                        /* walsh.rs:41-76 */
+void ro_codebook_prepare(const float* x, int columns, int padded, int group, float* rotated); /* matrix.rs:123-138 */
+int ro_codebook_levels(const float* codebook, int bits, int group, float levels[16]); /* matrix.rs:499-508 */
+float ro_integer_levels(const float levels[16], int count, int8_t table[16]);    /* neon.rs:114-124 */
+void ro_group_codes(const float* rotated, int n, int group, int8_t* codes, float* scales); /* panel.rs:52-66 */
+void ro_codebook_product(const uint8_t* packed, const uint16_t* norms, int rows, int padded, int group,
+                         int bits, const int8_t table[16], float lscale, const int8_t* xcodes,
+                         const float* xscales, int count, float* y, int32_t* acc);
+void ro_codebook_dequantise_row(const uint8_t* packed, const uint16_t* norms, int padded, int columns,
+                                int group, int bits, const float levels[16], int row, float* out); /* matrix.rs:140-153 */
+
 /* ---- Whistle-style speech path (rn_whistle.c) ---------------------------------
  * crates/whistle: stem (stem.rs), encoder (encoder.rs), cross-attention
  * memory and apply (cross.rs), and the decoder step with the cross hook

@@ -103,6 +103,9 @@ SIGNATURES = {
     "rn_matrix_multiply_fused": (_i, [C.POINTER(_p), _i, _p, C.POINTER(_p), _p]),
     "rn_matrix_multiply_batch": (_i, [_p, _p, _i, _p, _p, _p]),
     "rn_matrix_dequantise_row": (_i, [_p, _i, _p]),
+    "rn_matrix_create_codebook": (_i, [_p, _sz, _i, _i, _i, _i, _p, _i, C.POINTER(_p)]),
+    "rn_matrix_padded_columns": (_i, [_p, C.POINTER(_i)]),
+    "rn_matrix_prepare": (_i, [_p, _p, _i, _p, _p]),
     "rn_quantise_int8": (_i, [_p, _i, _i, _p, _p, _p]),
     "rn_fast_exp": (_i, [_p, _p, _i, _p]),
     "rn_silu": (_i, [_p, _p, _i, _p]),
@@ -319,6 +322,92 @@ class QuantisedMatrix:
                 lib.rn_matrix_free(self.handle)
         except Exception:
             pass
+
+
+class CodebookMatrix:
+    """QuantisedMatrix (crates/kernels/src/matrix.rs:19-441) over a codebook-quantised
+    record: the archive blob (packed indices LSB first, then fp16 group norms), the
+    archive's 28 codebook levels, bits 2, 4 or 5 (ternary)."""
+
+    def __init__(self, blob: np.ndarray, rows: int, columns: int, group: int, bits: int, codebook: np.ndarray):
+        blob = np.ascontiguousarray(blob, dtype=np.uint8)
+        codebook = np.ascontiguousarray(codebook, dtype=np.float32)
+        h = _p()
+        check(lib.rn_matrix_create_codebook(_ptr(blob), blob.size, rows, columns, group, bits, _ptr(codebook),
+                                            codebook.size, C.byref(h)))
+        self.handle = h.value
+        self.rows, self.columns, self.group, self.bits = rows, columns, group, bits
+        padded = _i()
+        check(lib.rn_matrix_padded_columns(self.handle, C.byref(padded)))
+        self.padded = padded.value
+        self.groups = self.padded // group
+
+    def prepare(self, x_dev: int, count: int, rotated_dev: int, stream=None) -> None:
+        check(lib.rn_matrix_prepare(self.handle, x_dev, count, rotated_dev, stream))
+
+    def prepare_host(self, x: np.ndarray) -> np.ndarray:
+        """QuantisedMatrix::prepare(_batch) (matrix.rs:123-138): [count][columns] -> [count][padded]."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, self.columns)
+        xd = DeviceBuffer.from_array(x)
+        rd = DeviceBuffer(4 * x.shape[0] * self.padded)
+        self.prepare(xd.ptr, x.shape[0], rd.ptr)
+        check(lib.rn_stream_synchronize(None))
+        return rd.download(np.float32, (x.shape[0], self.padded))
+
+    def multiply_batch_host(self, rotated: np.ndarray, with_acc: bool = False):
+        """multiply_vector (one row) or multiply_batch over rotated inputs [count][padded]."""
+        rotated = np.ascontiguousarray(rotated, dtype=np.float32).reshape(-1, self.padded)
+        count = rotated.shape[0]
+        xd = DeviceBuffer.from_array(rotated)
+        yd = DeviceBuffer(4 * count * self.rows)
+        ad = DeviceBuffer(4 * count * self.rows * self.groups) if with_acc else None
+        if count == 1:
+            check(lib.rn_matrix_multiply_vector(self.handle, xd.ptr, yd.ptr, ad.ptr if ad else None, None))
+        else:
+            check(lib.rn_matrix_multiply_batch(self.handle, xd.ptr, count, yd.ptr, ad.ptr if ad else None, None))
+        check(lib.rn_stream_synchronize(None))
+        y = yd.download(np.float32, (count, self.rows))
+        if with_acc:
+            return y, ad.download(np.int32, (count, self.rows, self.groups))
+        return y
+
+    def dequantise_row(self, row: int) -> np.ndarray:
+        out = np.empty(self.columns, dtype=np.float32)
+        check(lib.rn_matrix_dequantise_row(self.handle, row, _ptr(out)))
+        return out
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_matrix_free(self.handle)
+        except Exception:
+            pass
+
+
+# Lloyd-Max levels of a unit Gaussian for 2, 3 and 4 bits (ascending); divided by
+# sqrt(group) they approximate the coordinates of a unit vector of that length.
+_LLOYD_MAX = {
+    2: [-1.5104, -0.4528, 0.4528, 1.5104],
+    3: [-2.1520, -1.3439, -0.7560, -0.2451, 0.2451, 0.7560, 1.3439, 2.1520],
+    4: [-2.7326, -2.0690, -1.6181, -1.2562, -0.9424, -0.6568, -0.3881, -0.1284,
+        0.1284, 0.3881, 0.6568, 0.9424, 1.2562, 1.6181, 2.0690, 2.7326],
+}
+
+
+def synthetic_codebook(group: int) -> np.ndarray:
+    """28 archive levels (2-bit, 3-bit, 4-bit) for unit-sphere groups of `group`."""
+    s = np.float32(1.0) / np.sqrt(np.float32(group))
+    return np.concatenate([np.float32(_LLOYD_MAX[b]) * s for b in (2, 3, 4)]).astype(np.float32)
+
+
+def synthetic_codebook_blob(rows: int, columns: int, group: int, bits: int, seed: int = SEED,
+                            name: str = "codebook") -> np.ndarray:
+    """A record blob of seeded random indices (every byte but 0x80) and fp16 norms in [0.5, 2)."""
+    padded = -(-columns // group) * group
+    ib = 2 if bits == 5 else bits
+    packed = synth_codes(seed, name + ".packed", (rows * padded * ib // 8,)).view(np.uint8)
+    norms = synth_uniform(seed, name + ".norms", 0.5, 2.0, (rows * (padded // group),)).astype(np.float16)
+    return np.concatenate([packed, norms.view(np.uint8)])
 
 
 def multiply_fused_host(matrices, x: np.ndarray):

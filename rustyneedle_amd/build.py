@@ -14,7 +14,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librustyneedle_hip.so")
-SOURCES = ["rn_gemv.hip", "rn_attention.hip", "rn_gemm.hip", "rn_misc.hip", "rn_whistle.hip", "rn_api.hip",
+SOURCES = ["rn_gemv.hip", "rn_attention.hip", "rn_gemm.hip", "rn_misc.hip", "rn_whistle.hip", "rn_codebook.hip",
+           "rn_api.hip",
            "rn_synth.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -87,6 +87,9 @@ struct rn_matrix {
     int8_t* W = nullptr;
     float* sW = nullptr;
     int rows = 0, columns = 0, group = 0, form = 0;
+    int bits = 0;                  // 0: int8 codes; 2, 4 or 5 (ternary): codebook indices
+    unsigned char* blob = nullptr;  // codebook blob: packed indices, fp16 norms, padding
+    CodebookParams cb{};
 };
 
 struct rn_model {
@@ -248,11 +251,105 @@ int rn_matrix_create_i8(const int8_t* codes, const float* scales, int rows, int 
     return RN_OK;
 }
 
+// QuantisedMatrix::from_parts (matrix.rs:41-59) for a codebook-quantised record.
+// The levels follow lookup_table (matrix.rs:499-508, codebook.rs:12-43), the
+// integer table IntegerLevels::new (neon.rs:114-124): scale = peak / 127 (1.0
+// for a zero peak), entry = level / scale rounded half away from zero.
+int rn_matrix_create_codebook(const uint8_t* blob, size_t blob_bytes, int rows, int columns, int group, int bits,
+                              const float* codebook, int codebook_len, rn_matrix** out) {
+    RN_REQUIRE(blob && codebook && out, "null argument");
+    RN_REQUIRE(rows > 0 && columns > 0, "rows and columns must be positive (got %d x %d)", rows, columns);
+    RN_REQUIRE(group == 64 || group == 128 || group == 256, "group must be 64, 128 or 256 (got %d)", group);
+    RN_REQUIRE(bits == 2 || bits == 4 || bits == 5,
+               "bits must be 2, 4 or 5 (ternary); 1- and 3-bit records have no integer path (got %d)", bits);
+    RN_REQUIRE(codebook_len >= 28, "the codebook holds 28 levels (got %d)", codebook_len);
+    const int padded = (columns + group - 1) / group * group;
+    const int ib = bits == 5 ? 2 : bits;
+    const size_t row_bytes = (size_t)padded * ib / 8;
+    const size_t packed = (size_t)rows * row_bytes, norms = (size_t)rows * (padded / group) * 2;
+    RN_REQUIRE(padded <= 49152, "padded columns above 49152 are not supported (got %d)", padded);
+    RN_REQUIRE(blob_bytes >= packed + norms, "blob of %zu bytes is shorter than indices + norms (%zu)", blob_bytes,
+               packed + norms);
+    float levels[16] = {0};
+    int count = 0;
+    if (bits == 2) {
+        std::copy(codebook, codebook + 4, levels);
+        count = 4;
+    } else if (bits == 4) {
+        std::copy(codebook + 12, codebook + 28, levels);
+        count = 16;
+    } else {
+        const float level = 1.2240064f / sqrtf((float)group);  // codebook.rs:39-42
+        levels[1] = level;
+        levels[3] = -level;
+        count = 4;
+    }
+    float peak = 0.0f;
+    for (int i = 0; i < count; ++i) peak = fmaxf(peak, fabsf(levels[i]));
+    const float lscale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    uint8_t table[16] = {0};
+    for (int i = 0; i < count; ++i) table[i] = (uint8_t)(int8_t)roundf(levels[i] / lscale);
+
+    rn_matrix* m = new (std::nothrow) rn_matrix();
+    if (!m) return fail(RN_ERR_MEMORY, "out of host memory");
+    const size_t bytes = packed + norms + 4096;  // kernels read norms in 3 KB windows past a block's start
+    if (hipMalloc(&m->blob, bytes) != hipSuccess) {
+        delete m;
+        return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", bytes);
+    }
+    if (hipMemset(m->blob, 0, bytes) != hipSuccess || hipMemcpy(m->blob, blob, packed + norms, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(m->blob);
+        delete m;
+        return fail(RN_ERR_DEVICE, "upload of matrix failed");
+    }
+    m->rows = rows;
+    m->columns = columns;
+    m->group = group;
+    m->bits = bits;
+    m->form = bits == 2 ? RN_FORM_PANEL : RN_FORM_PLANE;
+    CodebookParams& c = m->cb;
+    c.packed = m->blob;
+    c.norms = reinterpret_cast<const uint16_t*>(m->blob + packed);
+    c.rows = rows;
+    c.columns = columns;
+    c.padded = padded;
+    c.group = group;
+    c.bits = bits;
+    c.row_bytes = (int)row_bytes;
+    c.cpr = (int)(row_bytes / 16);
+    c.inv_cpr = 1.0f / (float)c.cpr;
+    for (int i = 0; i < 4; ++i)
+        c.lut[i] = (uint32_t)table[4 * i] | ((uint32_t)table[4 * i + 1] << 8) | ((uint32_t)table[4 * i + 2] << 16) |
+                   ((uint32_t)table[4 * i + 3] << 24);
+    c.lscale = lscale;
+    std::copy(levels, levels + 16, c.levels);
+    c.wht_scale = 1.0f / sqrtf((float)group);  // walsh.rs:74
+    *out = m;
+    return RN_OK;
+}
+
 int rn_matrix_free(rn_matrix* m) {
     if (!m) return RN_OK;
     (void)hipFree(m->W);
     (void)hipFree(m->sW);
+    (void)hipFree(m->blob);
     delete m;
+    return RN_OK;
+}
+
+int rn_matrix_padded_columns(const rn_matrix* m, int* padded) {
+    RN_REQUIRE(m && padded, "null argument");
+    *padded = m->bits ? m->cb.padded : m->columns;
+    return RN_OK;
+}
+
+int rn_matrix_prepare(const rn_matrix* m, const float* x, int count, float* rotated, void* stream) {
+    RN_REQUIRE(m && x && rotated, "null argument");
+    RN_REQUIRE(m->bits != 0, "int8 matrices take their input unrotated; prepare applies to codebook matrices");
+    RN_REQUIRE(count >= 0, "count must be non-negative");
+    if (count == 0) return RN_OK;
+    RN_HIP(launch_codebook_rotate(x, count, m->columns, m->cb.padded, m->group, m->cb.wht_scale, rotated,
+                                  (hipStream_t)stream));
     return RN_OK;
 }
 
@@ -266,6 +363,10 @@ int rn_matrix_shape(const rn_matrix* m, int* rows, int* columns, int* group) {
 
 int rn_matrix_multiply_vector(const rn_matrix* m, const float* x, float* y, int32_t* acc, void* stream) {
     RN_REQUIRE(m && x && y, "null argument");
+    if (m->bits) {
+        RN_HIP(launch_codebook_product(m->cb, x, 1, y, acc, (hipStream_t)stream));
+        return RN_OK;
+    }
     GemvParams p{};
     const int rpb = gemv_rows_per_block(m->rows, m->columns, kStore);
     const int blocks = (m->rows + rpb - 1) / rpb;
@@ -281,6 +382,17 @@ int rn_matrix_multiply_fused(const rn_matrix* const* ms, int count, const float*
     RN_REQUIRE(count >= 1 && count <= kMaxSegments, "count must be 1..%d (got %d)", kMaxSegments, count);
     const rn_matrix* first = ms[0];
     RN_REQUIRE(first, "matrix 0 is null");
+    if (first->bits) {
+        // codebook matrices sharing the rotated input: one launch each
+        for (int i = 0; i < count; ++i) {
+            RN_REQUIRE(ms[i] && ys[i], "matrix or output %d is null", i);
+            RN_REQUIRE(ms[i]->bits && ms[i]->cb.padded == first->cb.padded && ms[i]->group == first->group,
+                       "fused matrices must share padded columns and group (matrix %d differs)", i);
+        }
+        for (int i = 0; i < count; ++i)
+            RN_HIP(launch_codebook_product(ms[i]->cb, x, 1, ys[i], nullptr, (hipStream_t)stream));
+        return RN_OK;
+    }
     int total_rows = 0;
     for (int i = 0; i < count; ++i) {
         RN_REQUIRE(ms[i] && ys[i], "matrix or output %d is null", i);
@@ -306,6 +418,10 @@ int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, floa
     RN_REQUIRE(count >= 0, "count must be non-negative");
     if (count == 0) return RN_OK;
     hipStream_t s = (hipStream_t)stream;
+    if (m->bits) {
+        RN_HIP(launch_codebook_product(m->cb, x, count, y, acc, s));
+        return RN_OK;
+    }
     void* scratch = nullptr;
     const size_t codes = align_up((size_t)count * m->columns);
     RN_HIP(hipMallocAsync(&scratch, codes + sizeof(float) * (size_t)count, s));
@@ -325,6 +441,15 @@ int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, floa
 int rn_matrix_dequantise_row(const rn_matrix* m, int row, float* out) {
     RN_REQUIRE(m && out, "null argument");
     RN_REQUIRE(row >= 0 && row < m->rows, "row %d out of range [0, %d)", row, m->rows);
+    if (m->bits) {
+        float* dev = nullptr;
+        RN_HIP(hipMalloc(&dev, sizeof(float) * m->cb.padded));
+        hipError_t e = launch_codebook_dequantise(m->cb, row, dev, nullptr);
+        if (e == hipSuccess) e = hipMemcpy(out, dev, sizeof(float) * m->columns, hipMemcpyDeviceToHost);
+        (void)hipFree(dev);
+        RN_HIP(e);
+        return RN_OK;
+    }
     const int G = m->columns / m->group;
     std::vector<int8_t> codes(m->columns);
     std::vector<float> scales(G);

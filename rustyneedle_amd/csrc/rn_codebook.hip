@@ -1,0 +1,450 @@
+// rn_codebook.hip — products over the codebook weight format for gfx950.
+//
+// A codebook-quantised [rows][columns] matrix (docs/format.md "Codebook-quantised
+// matrices", cact record.rs:57-84) pads columns to a multiple of the group
+// size. Its blob holds the packed indices, least-significant bits first, then
+// one fp16 L2 norm per (row, group). The device keeps that blob as the
+// archive stores it (2 or 4 bits a weight, 4-8x fewer bytes than int8 codes).
+//
+// Replaces, for the integer path the reference takes on aarch64:
+//   walsh::rotate_groups (walsh.rs:41-80) under QuantisedMatrix::prepare
+//     (matrix.rs:123-138)                                   -> cb_rotate_kernel
+//   plane_input / NaturalInput::new per-group input codes (matrix.rs:205-214,
+//     neon.rs:63-106, panel.rs:52-66), PanelMatrix::tile (panel.rs:153-197,
+//     2-bit) and row_dot_two_bit / row_dot_four_bit (neon.rs:126-183, 4-bit
+//     and ternary crumbs)                                    -> cb_product_kernel
+//   QuantisedMatrix::dequantise_row (matrix.rs:140-153)      -> cb_dequantise_kernel
+//
+// Product arithmetic (bit-exact with the reference order):
+//   - per group of the rotated input: scale = peak / 127 (1.0 for a zero
+//     peak), code = round-half-even(x / scale) (clamped to +-127; |x| <= peak
+//     keeps every quotient within +-127.5, so no clamp is reached);
+//   - the integer levels (IntegerLevels, neon.rs:114-124: an int8 table and
+//     one scale lscale, computed on the host) decode each index with
+//     v_perm_b32 from a table held in registers, and v_dot4_i32_i8 adds the
+//     exact int32 group sum (order-free);
+//   - per row, sequentially over the groups:
+//       2-bit (panel.rs:184-188):   total = fmaf(acc, (norm * lscale) * xs, total)
+//       4-bit and ternary (neon.rs:158,180):
+//                                   total = total + (((acc * norm) * lscale) * xs)
+//
+// Input codes live in LDS in "plane" order so that one decoded weight dword
+// meets one code dword: for 2-bit indices, a dword of 16 indices holds element
+// 4b + k at bits 2k of byte b, so (dword >> 2k) & 0x03030303 selects elements
+// {k, 4+k, 8+k, 12+k}; the codes of each run of 16 elements are stored as the
+// 4x4 byte transpose. For 4-bit indices a dword holds 8 elements and
+// (dword >> 4k) & 0x0f0f0f0f selects {k, 2+k, 4+k, 6+k}.
+#include "rn_device.hpp"
+#include "rn_internal.hpp"
+
+namespace rn {
+
+namespace {
+
+// The Walsh-Hadamard transform of one group held as runs of 16 consecutive
+// elements, one run per lane, GROUP / 16 aligned lanes per group (walsh.rs:41-76):
+// butterflies of span 1, 2, 4, 8 inside the lane, then spans 16 .. GROUP/2
+// across lanes (partner lane ^ span/16); the low element becomes a + b, the
+// high one a - b; then every value times `scale` = 1 / sqrt(GROUP).
+template <int GROUP>
+__device__ __forceinline__ void wht_run(float (&v)[16], int lane, float scale) {
+#pragma unroll
+    for (int span = 1; span < 16; span *= 2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if ((i & span) == 0) {
+                const float a = v[i], b = v[i + span];
+                v[i] = a + b;
+                v[i + span] = a - b;
+            }
+#pragma unroll
+    for (int m = 1; m < GROUP / 16; m *= 2) {
+        const bool high = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float p = __shfl_xor(v[i], m, 64);
+            v[i] = high ? p - v[i] : v[i] + p;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = v[i] * scale;
+}
+
+// Maximum over aligned sets of L lanes (L = 1, 2, 4, 8 or 16), the same in
+// every lane of the set (DPP inside rows of 16; the maximum is order-free).
+template <int L>
+__device__ __forceinline__ float set_max(float v) {
+    if constexpr (L >= 2) v = fmaxf(v, __int_as_float(dpp_move<0xb1>(__float_as_int(v))));
+    if constexpr (L >= 4) v = fmaxf(v, __int_as_float(dpp_move<0x4e>(__float_as_int(v))));
+    if constexpr (L >= 8) v = fmaxf(v, __int_as_float(dpp_move<0x141>(__float_as_int(v))));
+    if constexpr (L >= 16) v = fmaxf(v, __int_as_float(dpp_move<0x140>(__float_as_int(v))));
+    return v;
+}
+
+// Integer sum over aligned sets of L lanes, the same in every lane of the set.
+template <int L>
+__device__ __forceinline__ int set_sum(int v) {
+    if constexpr (L >= 2) v = v + dpp_move<0xb1>(v);
+    if constexpr (L >= 4) v = v + dpp_move<0x4e>(v);
+    if constexpr (L >= 8) v = v + dpp_move<0x141>(v);
+    return v;
+}
+
+// The codes of one run of 16 elements in plane order for BITS-bit indices.
+template <int BITS>
+__device__ __forceinline__ int4 plane_pack(const int (&c)[16]) {
+    auto b4 = [](int a, int b, int x, int d) -> int {
+        return (a & 0xff) | ((b & 0xff) << 8) | ((x & 0xff) << 16) | ((d & 0xff) << 24);
+    };
+    if constexpr (BITS == 2)  // dword k = elements k, 4+k, 8+k, 12+k
+        return make_int4(b4(c[0], c[4], c[8], c[12]), b4(c[1], c[5], c[9], c[13]), b4(c[2], c[6], c[10], c[14]),
+                         b4(c[3], c[7], c[11], c[15]));
+    else  // two blocks of 8: dword 2h + k = elements 8h + k, 8h+2+k, 8h+4+k, 8h+6+k
+        return make_int4(b4(c[0], c[2], c[4], c[6]), b4(c[1], c[3], c[5], c[7]), b4(c[8], c[10], c[12], c[14]),
+                         b4(c[9], c[11], c[13], c[15]));
+}
+
+// The int8 levels of four indices (one per byte of sel, 0..3 or 0..15).
+template <int BITS>
+__device__ __forceinline__ int decode4(uint32_t sel, const uint32_t (&lut)[4]) {
+    if constexpr (BITS == 2) {
+        return (int)__builtin_amdgcn_perm(0u, lut[0], sel);
+    } else {
+        const uint32_t s7 = sel & 0x07070707u;
+        const uint32_t lo = __builtin_amdgcn_perm(lut[1], lut[0], s7);
+        const uint32_t hi = __builtin_amdgcn_perm(lut[3], lut[2], s7);
+        const uint32_t m = ((sel >> 3) & 0x01010101u) * 0xffu;
+        return (int)((hi & m) | (lo & ~m));
+    }
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+}  // namespace
+
+// QuantisedMatrix::prepare / prepare_batch (matrix.rs:123-138): x [count][columns]
+// -> rotated [count][padded], zero past `columns`, each group rotated. One
+// lane per run of 16 elements.
+template <int GROUP>
+__global__ __launch_bounds__(256) void cb_rotate_kernel(const float* x, int count, int columns, int padded,
+                                                        float scale, float* rotated) {
+    const int lane = threadIdx.x & 63;
+    const int runs = padded / 16;
+    const int f = blockIdx.x * 256 + threadIdx.x;  // flat run index over [count][runs]
+    // every lane of a group set runs the shuffles, also past the end (whole
+    // sets only: runs is a multiple of GROUP / 16)
+    const int ff = min(f, count * runs - 1);
+    const int t = ff / runs, u = ff - t * runs;
+    float v[16];
+    const float* src = x + (size_t)t * columns;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int e = 16 * u + i;
+        v[i] = e < columns ? src[e] : 0.0f;
+    }
+    wht_run<GROUP>(v, lane, scale);
+    if (f < count * runs) {
+        float4* dst = reinterpret_cast<float4*>(rotated + (size_t)t * padded + 16 * u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    }
+}
+
+// QuantisedMatrix::dequantise_row (matrix.rs:140-153): per group
+// (level[index] * norm) then the group's Walsh-Hadamard transform; the first
+// `columns` values. One block of padded / 16 lanes (at most 1024).
+template <int BITS, int GROUP>
+__global__ __launch_bounds__(1024) void cb_dequantise_kernel(CodebookParams p, int row, float* out) {
+    constexpr int IB = BITS == 5 ? 2 : BITS;
+    const int u = threadIdx.x, lane = u & 63;
+    const int runs = p.padded / 16, G = p.padded / GROUP;
+    const int uu = min(u, runs - 1);
+    const uint8_t* r = p.packed + (size_t)row * p.row_bytes + (size_t)uu * 2 * IB;  // 16 indices = 2 * IB bytes
+    const float norm = half_bits_to_float(p.norms[(size_t)row * G + (16 * uu) / GROUP]);
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int bit = i * IB;
+        const int idx = (r[bit / 8] >> (bit % 8)) & ((1 << IB) - 1);
+        v[i] = p.levels[idx] * norm;
+    }
+    wht_run<GROUP>(v, lane, p.wht_scale);
+    if (u < runs)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (16 * u + i < p.columns) out[16 * u + i] = v[i];
+}
+
+// The row products of T tokens at a time (token tile blockIdx.y) over
+// p.rows_per_block rows (blockIdx.x), one wave per block.
+//   1. The first runs of the block's input rows are requested, then the
+//      block's weight chunks (NL 16-byte loads per lane: chunk 64 j + lane of
+//      the block's rows in row-major order, clamped to the matrix, so no load
+//      is conditional), then the block's norms.
+//   2. Prologue: per run of 16 rotated values, the group's peak over its
+//      GROUP/16 lanes (DPP), scale, codes (quotients without a division unless
+//      a quotient lies near a rounding boundary), stored in plane order.
+//   3. Per chunk and token: decoded dwords meet code dwords in v_dot4; the
+//      chunks of one group join across their lanes (DPP) into acc_s.
+//   4. One lane per (token, row): the sequential group epilogue.
+template <int BITS, int GROUP, int FORM, int NL, int T>
+__global__ __launch_bounds__(64) void cb_product_kernel(CodebookParams p, const float* x, int count, float* y,
+                                                        int32_t* acc_out) {
+    constexpr int IB = BITS == 5 ? 2 : BITS;        // index bits (ternary crumbs are 2)
+    constexpr int EPC = 128 / IB;                    // elements per 16-byte chunk
+    constexpr int CPG = GROUP / EPC;                 // chunks per group
+    constexpr int RPG = GROUP / 16;                  // runs of 16 per group
+    constexpr int XB = 2;                            // input runs per lane per batch
+    static_assert(CPG >= 1 && CPG <= 8 && RPG <= 16, "group of 64, 128 or 256");
+    extern __shared__ __align__(16) unsigned char lds[];
+
+    const int lane = threadIdx.x;
+    const int R = p.rows_per_block, CPR = p.cpr, G = p.padded / GROUP, runs = p.padded / 16;
+    const int row0 = blockIdx.x * R, t0 = blockIdx.y * T;
+    uint16_t* nm_s = reinterpret_cast<uint16_t*>(lds);                          // 3 KB of norms
+    int8_t* xq_s = reinterpret_cast<int8_t*>(lds + 3072);                       // [T][padded]
+    int* acc_s = reinterpret_cast<int*>(lds + 3072 + (size_t)T * p.padded);    // [T][R][G]
+    float* sx_s = reinterpret_cast<float*>(acc_s + (size_t)T * R * G);         // [T][G]
+
+    // 1. requests
+    const int xruns = T * runs;  // flat (token, run) index of the tile
+    auto run_src = [&](int f) -> const float* {
+        const int ff = min(f, xruns - 1);
+        const int t = ff / runs;
+        return x + (size_t)min(t0 + t, count - 1) * p.padded + 16 * (ff - t * runs);
+    };
+    float xv[XB][16];
+#pragma unroll
+    for (int k = 0; k < XB; ++k) {
+        const float4* s = reinterpret_cast<const float4*>(run_src(64 * k + lane));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 q = s[i];
+            xv[k][4 * i] = q.x;
+            xv[k][4 * i + 1] = q.y;
+            xv[k][4 * i + 2] = q.z;
+            xv[k][4 * i + 3] = q.w;
+        }
+    }
+    v4i w[NL];
+    int wrow[NL], wchunk[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int idx = 64 * j + lane;
+        const int rl = (int)(((float)idx + 0.5f) * p.inv_cpr);  // exact idx / CPR for idx < 4096
+        wrow[j] = rl;
+        wchunk[j] = idx - rl * CPR;
+        const int row = min(row0 + rl, p.rows - 1);
+        w[j] = *reinterpret_cast<const v4i*>(p.packed + (size_t)row * p.row_bytes + (size_t)wchunk[j] * 16);
+    }
+    // the block's norms: contiguous halves [row0 * G, (row0 + R) * G), read
+    // from a 16-byte aligned start (the allocation is padded past its end)
+    const size_t nbase = (size_t)row0 * G * 2, nal = nbase & ~(size_t)15;
+    v4i nv[3];  // native vectors stay in registers (arrays of int4 structs may not)
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        nv[i] = *reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(p.norms) + nal +
+                                              16 * (size_t)(lane + 64 * i));
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. prologue: per-group input codes and scales
+    auto quantise_runs = [&](float (&v)[16], int f) {
+        float peak = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) peak = fmaxf(peak, fabsf(v[i]));
+        peak = set_max<RPG>(peak);
+        const float sx = int8_scale_from_peak(peak);
+        float q[16];
+        quotients<16>(v, sx, q);
+        int c[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) c[i] = code_of_quotient(q[i]);
+        if (f < xruns) {
+            reinterpret_cast<int4*>(xq_s)[f] = plane_pack<IB>(c);
+            const int t = f / runs, u = f - t * runs;
+            if (u % RPG == 0) sx_s[t * G + u / RPG] = sx;
+        }
+    };
+#pragma unroll
+    for (int k = 0; k < XB; ++k) quantise_runs(xv[k], 64 * k + lane);
+    for (int base = 64 * XB; base < xruns; base += 64 * XB) {  // wide inputs or many tokens
+#pragma unroll
+        for (int k = 0; k < XB; ++k) {
+            const float4* s = reinterpret_cast<const float4*>(run_src(base + 64 * k + lane));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 q = s[i];
+                xv[k][4 * i] = q.x;
+                xv[k][4 * i + 1] = q.y;
+                xv[k][4 * i + 2] = q.z;
+                xv[k][4 * i + 3] = q.w;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < XB; ++k) quantise_runs(xv[k], base + 64 * k + lane);
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) reinterpret_cast<v4i*>(nm_s)[lane + 64 * i] = nv[i];
+    __syncthreads();
+
+    // 3. exact int32 group sums
+    const uint32_t lut[4] = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int c = wchunk[j];
+        int part[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) part[t] = 0;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t wd = (uint32_t)w[j][d];
+            if constexpr (IB == 2) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int lv = decode4<2>((wd >> (2 * k)) & 0x03030303u, lut);
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        const int a = *reinterpret_cast<const int*>(xq_s + (size_t)t * p.padded + 64 * c + 16 * d + 4 * k);
+                        part[t] = dot4(lv, a, part[t]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int lv = decode4<4>((wd >> (4 * k)) & 0x0f0f0f0fu, lut);
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        const int a = *reinterpret_cast<const int*>(xq_s + (size_t)t * p.padded + 32 * c + 8 * d + 4 * k);
+                        part[t] = dot4(lv, a, part[t]);
+                    }
+                }
+            }
+        }
+        const int rl = wrow[j];
+        const bool store = (lane % CPG) == 0 && 64 * j + lane < R * CPR && row0 + rl < p.rows;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int s = set_sum<CPG>(part[t]);
+            if (store) acc_s[((size_t)t * R + rl) * G + c / CPG] = s;
+        }
+    }
+    __syncthreads();
+
+    // 4. sequential epilogue per (token, row)
+    const int nhalf0 = (int)((nbase - nal) / 2);
+    for (int e = lane; e < T * R; e += 64) {
+        const int t = e / R, r = e - t * R;
+        if (row0 + r >= p.rows || t0 + t >= count) continue;
+        const int* a = acc_s + ((size_t)t * R + r) * G;
+        const uint16_t* nm = nm_s + nhalf0 + r * G;
+        const float* xs = sx_s + t * G;
+        float total = 0.0f;
+        for (int g = 0; g < G; ++g) {
+            const float norm = half_bits_to_float(nm[g]);
+            if constexpr (FORM == kPanel)
+                total = fmaf((float)a[g], (norm * p.lscale) * xs[g], total);  // panel.rs:184-188
+            else
+                total = total + ((((float)a[g] * norm) * p.lscale) * xs[g]);  // neon.rs:158,180
+        }
+        y[(size_t)(t0 + t) * p.rows + row0 + r] = total;
+        if (acc_out != nullptr)
+            for (int g = 0; g < G; ++g) acc_out[((size_t)(t0 + t) * p.rows + row0 + r) * G + g] = a[g];
+    }
+}
+
+namespace {
+
+// LDS of a product block: norms window, [T][padded] codes, [T][R][G] sums, [T][G] scales
+inline size_t product_lds(const CodebookParams& p, int T, int R) {
+    const size_t G = (size_t)(p.padded / p.group);
+    return 3072 + (size_t)T * p.padded + 4 * ((size_t)T * R * G + (size_t)T * G);
+}
+inline int product_loads(const CodebookParams& p) { return p.cpr <= 512 ? 8 : 16; }
+inline int product_rows(const CodebookParams& p) { return min(64, 64 * product_loads(p) / p.cpr); }
+constexpr size_t kProductMaxLds = 64 * 1024;
+
+template <int BITS, int GROUP, int FORM, int T>
+hipError_t launch_product_t(const CodebookParams& p, const float* x, int count, float* y, int32_t* acc,
+                            hipStream_t stream) {
+    const int nl = product_loads(p);
+    CodebookParams q = p;
+    q.rows_per_block = product_rows(p);
+    const size_t lds = product_lds(p, T, q.rows_per_block);
+    if (lds > kProductMaxLds) return hipErrorInvalidValue;
+    const dim3 grid((p.rows + q.rows_per_block - 1) / q.rows_per_block, (count + T - 1) / T);
+    if (nl == 8)
+        rn_launch(cb_product_kernel<BITS, GROUP, FORM, 8, T>, grid, dim3(64), lds, stream, q, x, count, y, acc);
+    else
+        rn_launch(cb_product_kernel<BITS, GROUP, FORM, 16, T>, grid, dim3(64), lds, stream, q, x, count, y, acc);
+    return hipGetLastError();
+}
+
+template <int BITS, int GROUP, int FORM>
+hipError_t launch_product_g(const CodebookParams& p, const float* x, int count, float* y, int32_t* acc,
+                            hipStream_t stream) {
+    // token tiles of 8 share each block's weight loads; one token a block when
+    // 8 tokens' codes would not fit the LDS budget
+    const bool tile = count > 1 && product_lds(p, 8, product_rows(p)) <= kProductMaxLds;
+    return tile ? launch_product_t<BITS, GROUP, FORM, 8>(p, x, count, y, acc, stream)
+                : launch_product_t<BITS, GROUP, FORM, 1>(p, x, count, y, acc, stream);
+}
+
+template <int BITS, int FORM>
+hipError_t launch_product_b(const CodebookParams& p, const float* x, int count, float* y, int32_t* acc,
+                            hipStream_t stream) {
+    switch (p.group) {
+        case 64: return launch_product_g<BITS, 64, FORM>(p, x, count, y, acc, stream);
+        case 128: return launch_product_g<BITS, 128, FORM>(p, x, count, y, acc, stream);
+        case 256: return launch_product_g<BITS, 256, FORM>(p, x, count, y, acc, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_codebook_product(const CodebookParams& p, const float* x, int count, float* y, int32_t* acc,
+                                   hipStream_t stream) {
+    if (count < 1 || p.rows < 1 || p.cpr < 1 || p.cpr > 1024) return hipErrorInvalidValue;
+    switch (p.bits) {
+        case 2: return launch_product_b<2, kPanel>(p, x, count, y, acc, stream);
+        case 4: return launch_product_b<4, kPlane>(p, x, count, y, acc, stream);
+        case 5: return launch_product_b<5, kPlane>(p, x, count, y, acc, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_codebook_rotate(const float* x, int count, int columns, int padded, int group, float scale,
+                                  float* rotated, hipStream_t stream) {
+    if (count < 1 || padded % group != 0 || columns > padded) return hipErrorInvalidValue;
+    const long long runs = (long long)count * (padded / 16);
+    const dim3 grid((unsigned)((runs + 255) / 256));
+    switch (group) {
+        case 64: rn_launch(cb_rotate_kernel<64>, grid, dim3(256), 0, stream, x, count, columns, padded, scale, rotated); break;
+        case 128: rn_launch(cb_rotate_kernel<128>, grid, dim3(256), 0, stream, x, count, columns, padded, scale, rotated); break;
+        case 256: rn_launch(cb_rotate_kernel<256>, grid, dim3(256), 0, stream, x, count, columns, padded, scale, rotated); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_codebook_dequantise(const CodebookParams& p, int row, float* out, hipStream_t stream) {
+    const int threads = ((p.padded / 16 + 63) / 64) * 64;
+    if (row < 0 || row >= p.rows || threads > 1024) return hipErrorInvalidValue;
+#define RN_DQ(B, GR) rn_launch(cb_dequantise_kernel<B, GR>, dim3(1), dim3(threads), 0, stream, p, row, out)
+    switch (p.bits * 1000 + p.group) {
+        case 2064: RN_DQ(2, 64); break;
+        case 2128: RN_DQ(2, 128); break;
+        case 2256: RN_DQ(2, 256); break;
+        case 4064: RN_DQ(4, 64); break;
+        case 4128: RN_DQ(4, 128); break;
+        case 4256: RN_DQ(4, 256); break;
+        case 5064: RN_DQ(5, 64); break;
+        case 5128: RN_DQ(5, 128); break;
+        case 5256: RN_DQ(5, 256); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef RN_DQ
+    return hipGetLastError();
+}
+
+}  // namespace rn

@@ -240,6 +240,29 @@ struct CrossAttendParams {
     float* part;         // [32][d]
 };
 hipError_t launch_cross_attend(const CrossAttendParams& p, int d_model, hipStream_t stream);
+
+// A codebook-quantised matrix on the device: the archive blob as stored
+// (packed indices [rows][row_bytes], then fp16 norms [rows][padded/group]; the
+// allocation runs at least 4 KB past the norms) and the host-derived tables.
+struct CodebookParams {
+    const uint8_t* packed;
+    const uint16_t* norms;
+    int rows, columns, padded, group, bits;  // bits 5: ternary crumbs
+    int row_bytes;                           // padded * index_bits / 8
+    int cpr;                                 // 16-byte chunks per row
+    float inv_cpr;                           // 1 / cpr
+    int rows_per_block;                      // set by the launcher
+    uint32_t lut[4];                         // IntegerLevels table, 16 int8
+    float lscale;                            // IntegerLevels scale
+    float levels[16];                        // float levels (dequantise_row)
+    float wht_scale;                         // 1 / sqrt(group)
+};
+// rotated [count][padded] inputs -> y [count][rows] (acc nullable: [count][rows][groups])
+hipError_t launch_codebook_product(const CodebookParams& p, const float* x, int count, float* y, int32_t* acc,
+                                   hipStream_t stream);
+hipError_t launch_codebook_rotate(const float* x, int count, int columns, int padded, int group, float scale,
+                                  float* rotated, hipStream_t stream);
+hipError_t launch_codebook_dequantise(const CodebookParams& p, int row, float* out, hipStream_t stream);
 hipError_t launch_add(const float* a, const float* b, size_t n, float* out, hipStream_t stream);
 
 // ---- elementwise / helpers ----------------------------------------------------

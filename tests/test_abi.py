@@ -118,3 +118,12 @@ def test_synth_streams_are_named_and_seeded():
     assert not np.array_equal(a, rn.synth_codes(1, "b", (64,)))
     h = rn.synth_normal_f16(3, "h", (4096,))
     assert np.array_equal(h, rn.synth_normal(3, "h", 1.0, (4096,)).astype(np.float16))
+
+
+def test_codebook_argument_errors_need_no_device():
+    cb = rn.synthetic_codebook(128)
+    blob = rn.synthetic_codebook_blob(4, 128, 128, 2)
+    for bits, group, size, columns in ((3, 128, blob.size, 128), (2, 96, blob.size, 128),
+                                       (2, 128, blob.size - 1, 128), (2, 128, blob.size, 50000)):
+        with pytest.raises(rn.RnError):
+            rn.CodebookMatrix(blob[:size], 4, columns, group, bits, cb)
