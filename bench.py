@@ -207,6 +207,42 @@ def bench_gemv(rn, rotations: int = 512):
                 rotating_frac=achieved / HBM_PEAK_GBS)
 
 
+def codebook_bytes(rows: int, columns: int, group: int, bits: int) -> int:
+    """Algorithmic HBM bytes of one codebook matvec: indices, fp16 norms, the
+    rotated input and the output."""
+    padded = -(-columns // group) * group
+    ib = 2 if bits == 5 else bits
+    return rows * padded * ib // 8 + rows * (padded // group) * 2 + 4 * padded + 4 * rows
+
+
+def bench_codebook(rn, shapes=((2, 128, 2048, 512), (2, 128, 2097152, 512), (4, 128, 1048576, 512),
+                                (2, 128, 131072, 8192))):
+    """Codebook-format matvecs (2-bit panel form, 4-bit plane form) on rotated
+    inputs: the 2048 x 512 layer shape, and matrices of 264-272 MB (more than
+    the 256 MB Infinity Cache) that stream from HBM."""
+    stream = rn.Stream()
+    out = {}
+    for bits, group, rows, columns in shapes:
+        cb = rn.synthetic_codebook(group)
+        blob = rn.synthetic_codebook_blob(rows, columns, group, bits, name=f"bench.codebook.{bits}.{columns}")
+        m = rn.CodebookMatrix(blob, rows, columns, group, bits, cb)
+        del blob
+        x = rn.synth_normal(rn.SEED, "bench.codebook.x", 1.0, (1, columns))
+        xd = rn.DeviceBuffer.from_array(x)
+        rd, yd = rn.DeviceBuffer(4 * m.padded), rn.DeviceBuffer(4 * rows)
+        m.prepare(xd.ptr, 1, rd.ptr, stream.handle)
+        call = lambda: rn.check(rn.lib.rn_matrix_multiply_vector(m.handle, rd.ptr, yd.ptr, None, stream.handle))
+        for _ in range(3):
+            call()
+        n = 2000 if rows * columns <= (1 << 22) else 20
+        ms = time_events(rn, stream.handle, call, n)
+        nbytes = codebook_bytes(rows, columns, group, bits)
+        gbs = nbytes / (ms / 1e3) / 1e9
+        out[f"{bits}bit_{rows}x{columns}"] = dict(us=ms * 1e3, bytes=nbytes, gb_s=gbs, frac=gbs / HBM_PEAK_GBS)
+        del m, xd, rd, yd
+    return out
+
+
 def bench_whistle(rn, reps: int = 3, steps: int = 48, with_cpu: bool = True):
     """The speech path: encode of a 3000-frame mel window (stem, 6 encoder
     layers over 1500 frames, the cross memory of 4 decoder layers), then a
@@ -300,7 +336,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="decode only")
-    ap.add_argument("--extras", default="gemv,prefill_256,decode_batch64,whistle",
+    ap.add_argument("--extras", default="gemv,prefill_256,decode_batch64,whistle,codebook",
                     help="comma-separated secondary measurements to run")
     ap.add_argument("--profile-steps", type=int, default=DECODE_TOKENS,
                     help="greedy steps timed kernel by kernel for the roofline")
@@ -335,7 +371,8 @@ def main() -> int:
         for name, fn in (("gemv", lambda: bench_gemv(rn)),
                          ("prefill_256", lambda: bench_prefill(rn, model, cfg)),
                          ("decode_batch64", lambda: bench_batch(rn, model, cfg)),
-                         ("whistle", lambda: bench_whistle(rn, with_cpu=not args.no_cpu))):
+                         ("whistle", lambda: bench_whistle(rn, with_cpu=not args.no_cpu)),
+                         ("codebook", lambda: bench_codebook(rn))):
             if name not in wanted:
                 continue
             log(f"bench: {name}")

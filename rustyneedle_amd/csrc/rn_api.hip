@@ -292,7 +292,7 @@ int rn_matrix_create_codebook(const uint8_t* blob, size_t blob_bytes, int rows, 
 
     rn_matrix* m = new (std::nothrow) rn_matrix();
     if (!m) return fail(RN_ERR_MEMORY, "out of host memory");
-    const size_t bytes = packed + norms + 4096;  // kernels read norms in 3 KB windows past a block's start
+    const size_t bytes = packed + norms + 16384;  // kernels read norms in 12 KB windows past a block's start
     if (hipMalloc(&m->blob, bytes) != hipSuccess) {
         delete m;
         return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", bytes);

@@ -120,6 +120,8 @@ __device__ __forceinline__ int decode4(uint32_t sel, const uint32_t (&lut)[4]) {
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
+constexpr int kNormWindow = 12288;  // bytes of norms staged per row group (3 x 16 B a thread)
+
 }  // namespace
 
 // QuantisedMatrix::prepare / prepare_batch (matrix.rs:123-138): x [count][columns]
@@ -175,189 +177,207 @@ __global__ __launch_bounds__(1024) void cb_dequantise_kernel(CodebookParams p, i
             if (16 * u + i < p.columns) out[16 * u + i] = v[i];
 }
 
-// The row products of T tokens at a time (token tile blockIdx.y) over
-// p.rows_per_block rows (blockIdx.x), one wave per block.
-//   1. The first runs of the block's input rows are requested, then the
-//      block's weight chunks (NL 16-byte loads per lane: chunk 64 j + lane of
-//      the block's rows in row-major order, clamped to the matrix, so no load
-//      is conditional), then the block's norms.
-//   2. Prologue: per run of 16 rotated values, the group's peak over its
-//      GROUP/16 lanes (DPP), scale, codes (quotients without a division unless
-//      a quotient lies near a rounding boundary), stored in plane order.
-//   3. Per chunk and token: decoded dwords meet code dwords in v_dot4; the
-//      chunks of one group join across their lanes (DPP) into acc_s.
-//   4. One lane per (token, row): the sequential group epilogue.
+// The row products of T tokens at a time (token tile blockIdx.y). A block of
+// four waves shares one prologue; each wave owns R = p.rows_per_block rows of a
+// row group of 4R rows, and the block runs p.iters consecutive row groups so
+// that a wide input is quantised once for many rows.
+//   1. The first 256 runs of 16 input values are requested, then row group 0's
+//      weight chunks (NL 16-byte loads a lane: chunk 64 j + lane of the wave's
+//      rows in row-major order, clamped to the matrix, so no load is
+//      conditional) and its norms (a 12 KB window from a 16-byte aligned
+//      start; the allocation runs 16 KB past the norms).
+//   2. Prologue: per run, the group's peak over its GROUP/16 lanes (DPP),
+//      scale, codes (quotients without a division unless one lies near a
+//      rounding boundary), stored in plane order.
+//   3. Per row group: decoded dwords meet code dwords in v_dot4 and the chunks
+//      of one group join across their lanes (DPP) into the wave's acc_s; the
+//      next row group's loads are issued before this one's epilogue;
+//   4. one lane per (token, row): the sequential group epilogue.
 template <int BITS, int GROUP, int FORM, int NL, int T>
-__global__ __launch_bounds__(64) void cb_product_kernel(CodebookParams p, const float* x, int count, float* y,
-                                                        int32_t* acc_out) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NL == 8 && T == 1 ? 4 : 1)))
+void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, int32_t* acc_out) {
     constexpr int IB = BITS == 5 ? 2 : BITS;        // index bits (ternary crumbs are 2)
     constexpr int EPC = 128 / IB;                    // elements per 16-byte chunk
     constexpr int CPG = GROUP / EPC;                 // chunks per group
     constexpr int RPG = GROUP / 16;                  // runs of 16 per group
-    constexpr int XB = 2;                            // input runs per lane per batch
+    constexpr int NW = 4, NT = NW * 64;
     static_assert(CPG >= 1 && CPG <= 8 && RPG <= 16, "group of 64, 128 or 256");
     extern __shared__ __align__(16) unsigned char lds[];
 
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int R = p.rows_per_block, CPR = p.cpr, G = p.padded / GROUP, runs = p.padded / 16;
-    const int row0 = blockIdx.x * R, t0 = blockIdx.y * T;
-    uint16_t* nm_s = reinterpret_cast<uint16_t*>(lds);                          // 3 KB of norms
-    int8_t* xq_s = reinterpret_cast<int8_t*>(lds + 3072);                       // [T][padded]
-    int* acc_s = reinterpret_cast<int*>(lds + 3072 + (size_t)T * p.padded);    // [T][R][G]
-    float* sx_s = reinterpret_cast<float*>(acc_s + (size_t)T * R * G);         // [T][G]
+    const int BR = NW * R, t0 = blockIdx.y * T;
+    uint16_t* nm_s = reinterpret_cast<uint16_t*>(lds);                                 // 12 KB of norms
+    int8_t* xq_s = reinterpret_cast<int8_t*>(lds + kNormWindow);                      // [T][padded]
+    int* acc_all = reinterpret_cast<int*>(lds + kNormWindow + (size_t)T * p.padded);  // [NW][T][R][G]
+    float* sx_s = reinterpret_cast<float*>(acc_all + (size_t)NW * T * R * G);         // [T][G]
+    int* acc_s = acc_all + (size_t)wv * T * R * G;
 
     // 1. requests
     const int xruns = T * runs;  // flat (token, run) index of the tile
-    auto run_src = [&](int f) -> const float* {
+    auto load_run = [&](int f, float (&v)[16]) {
         const int ff = min(f, xruns - 1);
         const int t = ff / runs;
-        return x + (size_t)min(t0 + t, count - 1) * p.padded + 16 * (ff - t * runs);
-    };
-    float xv[XB][16];
-#pragma unroll
-    for (int k = 0; k < XB; ++k) {
-        const float4* s = reinterpret_cast<const float4*>(run_src(64 * k + lane));
+        const float4* s = reinterpret_cast<const float4*>(x + (size_t)min(t0 + t, count - 1) * p.padded +
+                                                          16 * (ff - t * runs));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float4 q = s[i];
-            xv[k][4 * i] = q.x;
-            xv[k][4 * i + 1] = q.y;
-            xv[k][4 * i + 2] = q.z;
-            xv[k][4 * i + 3] = q.w;
+            v[4 * i] = q.x;
+            v[4 * i + 1] = q.y;
+            v[4 * i + 2] = q.z;
+            v[4 * i + 3] = q.w;
         }
-    }
+    };
+    float xv[16];
+    load_run(tid, xv);
     v4i w[NL];
-    int wrow[NL], wchunk[NL];
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        const int idx = 64 * j + lane;
-        const int rl = (int)(((float)idx + 0.5f) * p.inv_cpr);  // exact idx / CPR for idx < 4096
-        wrow[j] = rl;
-        wchunk[j] = idx - rl * CPR;
-        const int row = min(row0 + rl, p.rows - 1);
-        w[j] = *reinterpret_cast<const v4i*>(p.packed + (size_t)row * p.row_bytes + (size_t)wchunk[j] * 16);
-    }
-    // the block's norms: contiguous halves [row0 * G, (row0 + R) * G), read
-    // from a 16-byte aligned start (the allocation is padded past its end)
-    const size_t nbase = (size_t)row0 * G * 2, nal = nbase & ~(size_t)15;
     v4i nv[3];  // native vectors stay in registers (arrays of int4 structs may not)
+    auto group_row0 = [&](int it) -> int { return (blockIdx.x * p.iters + it) * BR; };
+    auto issue = [&](int it) {
+        const int rw = group_row0(it) + wv * R;
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
-        nv[i] = *reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(p.norms) + nal +
-                                              16 * (size_t)(lane + 64 * i));
+        for (int j = 0; j < NL; ++j) {
+            const int idx = 64 * j + lane;
+            const int rl = (int)(((float)idx + 0.5f) * p.inv_cpr);  // exact idx / CPR for idx < 4096
+            const int row = min(rw + rl, p.rows - 1);
+            w[j] = *reinterpret_cast<const v4i*>(p.packed + (size_t)row * p.row_bytes + (size_t)(idx - rl * CPR) * 16);
+        }
+    };
+    // the norms are wanted only by the epilogue: requested after the prologue,
+    // so their registers are not held through it
+    auto issue_norms = [&](int it) {
+        const size_t nal = ((size_t)min(group_row0(it), p.rows - 1) * G * 2) & ~(size_t)15;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            nv[i] = *reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(p.norms) + nal +
+                                                  16 * (size_t)(tid + NT * i));
+    };
+    issue(0);
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. prologue: per-group input codes and scales
-    auto quantise_runs = [&](float (&v)[16], int f) {
+    auto quantise_run = [&](float (&v)[16], int f) {
         float peak = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) peak = fmaxf(peak, fabsf(v[i]));
         peak = set_max<RPG>(peak);
         const float sx = int8_scale_from_peak(peak);
-        float q[16];
-        quotients<16>(v, sx, q);
+        // quotients four at a time: the weight loads in flight hold registers,
+        // and sixteen interleaved boundary checks would add sixty more
         int c[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) c[i] = code_of_quotient(q[i]);
+        for (int c4 = 0; c4 < 16; c4 += 4) {
+            float q[4];
+            quotients<4>(v + c4, sx, q);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[c4 + i] = code_of_quotient(q[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         if (f < xruns) {
             reinterpret_cast<int4*>(xq_s)[f] = plane_pack<IB>(c);
             const int t = f / runs, u = f - t * runs;
             if (u % RPG == 0) sx_s[t * G + u / RPG] = sx;
         }
     };
-#pragma unroll
-    for (int k = 0; k < XB; ++k) quantise_runs(xv[k], 64 * k + lane);
-    for (int base = 64 * XB; base < xruns; base += 64 * XB) {  // wide inputs or many tokens
-#pragma unroll
-        for (int k = 0; k < XB; ++k) {
-            const float4* s = reinterpret_cast<const float4*>(run_src(base + 64 * k + lane));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 q = s[i];
-                xv[k][4 * i] = q.x;
-                xv[k][4 * i + 1] = q.y;
-                xv[k][4 * i + 2] = q.z;
-                xv[k][4 * i + 3] = q.w;
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < XB; ++k) quantise_runs(xv[k], base + 64 * k + lane);
+    quantise_run(xv, tid);
+    for (int base = NT; base < xruns; base += NT) {  // wide inputs or many tokens
+        load_run(base + tid, xv);
+        quantise_run(xv, base + tid);
     }
-#pragma unroll
-    for (int i = 0; i < 3; ++i) reinterpret_cast<v4i*>(nm_s)[lane + 64 * i] = nv[i];
-    __syncthreads();
 
-    // 3. exact int32 group sums
+    issue_norms(0);
     const uint32_t lut[4] = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
+    for (int it = 0; it < p.iters; ++it) {
+        const int gr0 = group_row0(it), rw = gr0 + wv * R;
+        const int nhalf0 = (int)((((size_t)min(gr0, p.rows - 1) * G * 2) & 15) / 2);
 #pragma unroll
-    for (int j = 0; j < NL; ++j) {
-        const int c = wchunk[j];
-        int part[T];
+        for (int i = 0; i < 3; ++i) reinterpret_cast<v4i*>(nm_s)[tid + NT * i] = nv[i];
+        __syncthreads();  // codes, scales and this row group's norms
+
+        // 3. exact int32 group sums
 #pragma unroll
-        for (int t = 0; t < T; ++t) part[t] = 0;
+        for (int j = 0; j < NL; ++j) {
+            const int idx = 64 * j + lane;
+            const int rl = (int)(((float)idx + 0.5f) * p.inv_cpr);
+            const int c = idx - rl * CPR;
+            int part[T];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const uint32_t wd = (uint32_t)w[j][d];
-            if constexpr (IB == 2) {
+            for (int t = 0; t < T; ++t) part[t] = 0;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int lv = decode4<2>((wd >> (2 * k)) & 0x03030303u, lut);
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t wd = (uint32_t)w[j][d];
+                if constexpr (IB == 2) {
 #pragma unroll
-                    for (int t = 0; t < T; ++t) {
-                        const int a = *reinterpret_cast<const int*>(xq_s + (size_t)t * p.padded + 64 * c + 16 * d + 4 * k);
-                        part[t] = dot4(lv, a, part[t]);
+                    for (int k = 0; k < 4; ++k) {
+                        const int lv = decode4<2>((wd >> (2 * k)) & 0x03030303u, lut);
+#pragma unroll
+                        for (int t = 0; t < T; ++t) {
+                            const int a =
+                                *reinterpret_cast<const int*>(xq_s + (size_t)t * p.padded + 64 * c + 16 * d + 4 * k);
+                            part[t] = dot4(lv, a, part[t]);
+                        }
                     }
-                }
-            } else {
+                } else {
 #pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                    const int lv = decode4<4>((wd >> (4 * k)) & 0x0f0f0f0fu, lut);
+                    for (int k = 0; k < 2; ++k) {
+                        const int lv = decode4<4>((wd >> (4 * k)) & 0x0f0f0f0fu, lut);
 #pragma unroll
-                    for (int t = 0; t < T; ++t) {
-                        const int a = *reinterpret_cast<const int*>(xq_s + (size_t)t * p.padded + 32 * c + 8 * d + 4 * k);
-                        part[t] = dot4(lv, a, part[t]);
+                        for (int t = 0; t < T; ++t) {
+                            const int a =
+                                *reinterpret_cast<const int*>(xq_s + (size_t)t * p.padded + 32 * c + 8 * d + 4 * k);
+                            part[t] = dot4(lv, a, part[t]);
+                        }
                     }
                 }
             }
-        }
-        const int rl = wrow[j];
-        const bool store = (lane % CPG) == 0 && 64 * j + lane < R * CPR && row0 + rl < p.rows;
+            const bool store = (lane % CPG) == 0 && idx < R * CPR && rw + rl < p.rows;
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const int s = set_sum<CPG>(part[t]);
-            if (store) acc_s[((size_t)t * R + rl) * G + c / CPG] = s;
+            for (int t = 0; t < T; ++t) {
+                const int s = set_sum<CPG>(part[t]);
+                if (store) acc_s[((size_t)t * R + rl) * G + c / CPG] = s;
+            }
+            // one chunk's code reads at a time: hoisting them all would hold
+            // 16 registers a chunk and cut the waves a CU keeps in flight
+            __builtin_amdgcn_sched_barrier(0);
         }
-    }
-    __syncthreads();
+        if (it + 1 < p.iters) {  // w and nv are free: in flight during the epilogue
+            issue(it + 1);
+            issue_norms(it + 1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // acc_s is this wave's own
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // 4. sequential epilogue per (token, row)
-    const int nhalf0 = (int)((nbase - nal) / 2);
-    for (int e = lane; e < T * R; e += 64) {
-        const int t = e / R, r = e - t * R;
-        if (row0 + r >= p.rows || t0 + t >= count) continue;
-        const int* a = acc_s + ((size_t)t * R + r) * G;
-        const uint16_t* nm = nm_s + nhalf0 + r * G;
-        const float* xs = sx_s + t * G;
-        float total = 0.0f;
-        for (int g = 0; g < G; ++g) {
-            const float norm = half_bits_to_float(nm[g]);
-            if constexpr (FORM == kPanel)
-                total = fmaf((float)a[g], (norm * p.lscale) * xs[g], total);  // panel.rs:184-188
-            else
-                total = total + ((((float)a[g] * norm) * p.lscale) * xs[g]);  // neon.rs:158,180
+        // 4. sequential epilogue per (token, row)
+        for (int e = lane; e < T * R; e += 64) {
+            const int t = e / R, r = e - t * R;
+            if (rw + r >= p.rows || t0 + t >= count) continue;
+            const int* a = acc_s + ((size_t)t * R + r) * G;
+            const uint16_t* nm = nm_s + nhalf0 + (wv * R + r) * G;
+            const float* xs = sx_s + t * G;
+            float total = 0.0f;
+            for (int g = 0; g < G; ++g) {
+                const float norm = half_bits_to_float(nm[g]);
+                if constexpr (FORM == kPanel)
+                    total = fmaf((float)a[g], (norm * p.lscale) * xs[g], total);  // panel.rs:184-188
+                else
+                    total = total + ((((float)a[g] * norm) * p.lscale) * xs[g]);  // neon.rs:158,180
+            }
+            y[(size_t)(t0 + t) * p.rows + rw + r] = total;
+            if (acc_out != nullptr)
+                for (int g = 0; g < G; ++g) acc_out[((size_t)(t0 + t) * p.rows + rw + r) * G + g] = a[g];
         }
-        y[(size_t)(t0 + t) * p.rows + row0 + r] = total;
-        if (acc_out != nullptr)
-            for (int g = 0; g < G; ++g) acc_out[((size_t)(t0 + t) * p.rows + row0 + r) * G + g] = a[g];
+        __syncthreads();  // the norms window and acc_s are read before the next row group replaces them
     }
 }
 
 namespace {
 
-// LDS of a product block: norms window, [T][padded] codes, [T][R][G] sums, [T][G] scales
+// LDS of a product block: norms window, [T][padded] codes, [4][T][R][G] sums, [T][G] scales
 inline size_t product_lds(const CodebookParams& p, int T, int R) {
     const size_t G = (size_t)(p.padded / p.group);
-    return 3072 + (size_t)T * p.padded + 4 * ((size_t)T * R * G + (size_t)T * G);
+    return kNormWindow + (size_t)T * p.padded + 4 * (4 * (size_t)T * R * G + (size_t)T * G);
 }
 inline int product_loads(const CodebookParams& p) { return p.cpr <= 512 ? 8 : 16; }
 inline int product_rows(const CodebookParams& p) { return min(64, 64 * product_loads(p) / p.cpr); }
@@ -371,11 +391,15 @@ hipError_t launch_product_t(const CodebookParams& p, const float* x, int count, 
     q.rows_per_block = product_rows(p);
     const size_t lds = product_lds(p, T, q.rows_per_block);
     if (lds > kProductMaxLds) return hipErrorInvalidValue;
-    const dim3 grid((p.rows + q.rows_per_block - 1) / q.rows_per_block, (count + T - 1) / T);
+    // consecutive row groups per block: a wide input's prologue then serves
+    // up to padded / 1024 groups, while the grid keeps at least 512 blocks
+    const int groups = (p.rows + 4 * q.rows_per_block - 1) / (4 * q.rows_per_block);
+    q.iters = max(1, min(p.padded / 1024, groups / 512));
+    const dim3 grid((groups + q.iters - 1) / q.iters, (count + T - 1) / T);
     if (nl == 8)
-        rn_launch(cb_product_kernel<BITS, GROUP, FORM, 8, T>, grid, dim3(64), lds, stream, q, x, count, y, acc);
+        rn_launch(cb_product_kernel<BITS, GROUP, FORM, 8, T>, grid, dim3(256), lds, stream, q, x, count, y, acc);
     else
-        rn_launch(cb_product_kernel<BITS, GROUP, FORM, 16, T>, grid, dim3(64), lds, stream, q, x, count, y, acc);
+        rn_launch(cb_product_kernel<BITS, GROUP, FORM, 16, T>, grid, dim3(256), lds, stream, q, x, count, y, acc);
     return hipGetLastError();
 }
 

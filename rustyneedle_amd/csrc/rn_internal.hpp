@@ -243,7 +243,7 @@ hipError_t launch_cross_attend(const CrossAttendParams& p, int d_model, hipStrea
 
 // A codebook-quantised matrix on the device: the archive blob as stored
 // (packed indices [rows][row_bytes], then fp16 norms [rows][padded/group]; the
-// allocation runs at least 4 KB past the norms) and the host-derived tables.
+// allocation runs at least 16 KB past the norms) and the host-derived tables.
 struct CodebookParams {
     const uint8_t* packed;
     const uint16_t* norms;
@@ -251,7 +251,8 @@ struct CodebookParams {
     int row_bytes;                           // padded * index_bits / 8
     int cpr;                                 // 16-byte chunks per row
     float inv_cpr;                           // 1 / cpr
-    int rows_per_block;                      // set by the launcher
+    int rows_per_block;                      // rows of a wave's row group (set by the launcher)
+    int iters;                               // row groups per block (set by the launcher)
     uint32_t lut[4];                         // IntegerLevels table, 16 int8
     float lscale;                            // IntegerLevels scale
     float levels[16];                        // float levels (dequantise_row)
