@@ -126,6 +126,47 @@ int rn_matrix_padded_columns(const rn_matrix* m, int* padded);
  * (walsh.rs:41-80). Codebook matrices only. Device pointers. */
 int rn_matrix_prepare(const rn_matrix* m, const float* x, int count, float* rotated, void* stream);
 
+/* ---- the .cact archive (crates/cact; docs/format.md) ---------------------------
+ * A memory-mapped, little-endian archive: 196-byte header, codebook levels, a
+ * directory of 44-byte tensor records, 64-byte aligned blobs. Host-side; the
+ * pointers returned stay valid until rn_archive_close. */
+typedef struct rn_archive rn_archive;
+/* Geometry (geometry.rs:10-37): the header fields in file order; global_layers
+ * joins global_mask_lo/hi; only the first engram_order_count orders and
+ * engram_site_count sites are meaningful. */
+typedef struct {
+    uint32_t tensor_count, codebook_len, kv_window, kv_bits, vocab, out_vocab, d_model, num_heads, num_kv_heads,
+        num_layers, qk_head_dim, v_head_dim, max_seq_len, hada_n, mhc_lanes, sliding_window;
+    uint64_t global_layers;
+    uint32_t qkv_conv_taps, engram_slots, engram_sub_dim, engram_tables, engram_conv_taps, engram_conv_dilation,
+        engram_seed_heads, engram_order_count, engram_orders[4], engram_site_count, engram_sites[16];
+    float rope_theta;
+} rn_geometry;
+/* ElementKind (record.rs:7-25) */
+enum { RN_KIND_HALF = 1, RN_KIND_SINGLE = 2, RN_KIND_CODEBOOK = 3, RN_KIND_RAW = 4 };
+/* TensorRecord (record.rs:27-51): shape[rank..4) is 0; bits 5 marks ternary crumbs. */
+typedef struct {
+    int kind, rank;
+    uint32_t shape[4];
+    uint64_t offset, nbytes;
+    uint32_t group_size, bits;
+} rn_tensor_record;
+/* Archive::open (archive.rs:37-41) with the checks of Archive::from_map
+ * (archive.rs:43-70): format tag, truncation, element kinds, every tensor inside
+ * the file and aligned to its element width. Errors carry the reference's
+ * messages (error.rs:15-26). */
+int rn_archive_open(const char* path, rn_archive** out);
+/* The same over bytes in memory (copied). */
+int rn_archive_from_memory(const uint8_t* bytes, size_t nbytes, rn_archive** out);
+int rn_archive_close(rn_archive* archive);
+int rn_archive_geometry(const rn_archive* archive, rn_geometry* out);     /* Archive::geometry (archive.rs:72-74) */
+int rn_archive_codebook(const rn_archive* archive, const float** values, int* count); /* archive.rs:76-78 */
+int rn_archive_record(const rn_archive* archive, int index, rn_tensor_record* out);  /* archive.rs:80-82 */
+int rn_archive_tensor_bytes(const rn_archive* archive, int index, const uint8_t** data, size_t* nbytes); /* archive.rs:88-91 */
+/* QuantisedMatrix::from_archive (matrix.rs:35-40): a kind-3 record to the device
+ * (rn_matrix_create_codebook with the record's shape, group and bits). */
+int rn_matrix_from_archive(const rn_archive* archive, int index, rn_matrix** out);
+
 /* ops::quantise_int8 (ops.rs:112-118) for `count` rows of `columns` floats on
  * the device: codes [count][columns], scales [count]. */
 int rn_quantise_int8(const float* x, int count, int columns, int8_t* codes, float* scales, void* stream);

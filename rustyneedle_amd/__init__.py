@@ -73,6 +73,24 @@ class WeightsHost(C.Structure):
     _fields_ = [("embedding", QMatHost), ("norm_final", _p), ("layers", _p)]
 
 
+class Geometry(C.Structure):
+    """rn_geometry: the .cact header (geometry.rs:10-37)."""
+    _fields_ = [(n, C.c_uint32) for n in (
+        "tensor_count", "codebook_len", "kv_window", "kv_bits", "vocab", "out_vocab", "d_model", "num_heads",
+        "num_kv_heads", "num_layers", "qk_head_dim", "v_head_dim", "max_seq_len", "hada_n", "mhc_lanes",
+        "sliding_window")] + [("global_layers", C.c_uint64)] + [(n, C.c_uint32) for n in (
+        "qkv_conv_taps", "engram_slots", "engram_sub_dim", "engram_tables", "engram_conv_taps",
+        "engram_conv_dilation", "engram_seed_heads", "engram_order_count")] + [
+        ("engram_orders", C.c_uint32 * 4), ("engram_site_count", C.c_uint32), ("engram_sites", C.c_uint32 * 16),
+        ("rope_theta", C.c_float)]
+
+
+class TensorRecord(C.Structure):
+    """rn_tensor_record (record.rs:27-51)."""
+    _fields_ = [("kind", C.c_int), ("rank", C.c_int), ("shape", C.c_uint32 * 4), ("offset", C.c_uint64),
+                ("nbytes", C.c_uint64), ("group_size", C.c_uint32), ("bits", C.c_uint32)]
+
+
 class WhistleConfig(C.Structure):
     _fields_ = [(n, _i) for n in ("mels", "frames", "d_model", "heads", "head_dim", "enc_layers", "dec_layers", "ffn",
                                   "vocab", "max_positions", "group")] + [("rope_theta", _f), ("norm_eps", _f)]
@@ -106,6 +124,14 @@ SIGNATURES = {
     "rn_matrix_create_codebook": (_i, [_p, _sz, _i, _i, _i, _i, _p, _i, C.POINTER(_p)]),
     "rn_matrix_padded_columns": (_i, [_p, C.POINTER(_i)]),
     "rn_matrix_prepare": (_i, [_p, _p, _i, _p, _p]),
+    "rn_archive_open": (_i, [C.c_char_p, C.POINTER(_p)]),
+    "rn_archive_from_memory": (_i, [_p, _sz, C.POINTER(_p)]),
+    "rn_archive_close": (_i, [_p]),
+    "rn_archive_geometry": (_i, [_p, C.POINTER(Geometry)]),
+    "rn_archive_codebook": (_i, [_p, C.POINTER(C.POINTER(_f)), C.POINTER(_i)]),
+    "rn_archive_record": (_i, [_p, _i, C.POINTER(TensorRecord)]),
+    "rn_archive_tensor_bytes": (_i, [_p, _i, C.POINTER(C.POINTER(C.c_uint8)), C.POINTER(_sz)]),
+    "rn_matrix_from_archive": (_i, [_p, _i, C.POINTER(_p)]),
     "rn_quantise_int8": (_i, [_p, _i, _i, _p, _p, _p]),
     "rn_fast_exp": (_i, [_p, _p, _i, _p]),
     "rn_silu": (_i, [_p, _p, _i, _p]),
@@ -335,7 +361,16 @@ class CodebookMatrix:
         h = _p()
         check(lib.rn_matrix_create_codebook(_ptr(blob), blob.size, rows, columns, group, bits, _ptr(codebook),
                                             codebook.size, C.byref(h)))
-        self.handle = h.value
+        self._adopt(h.value, rows, columns, group, bits)
+
+    @classmethod
+    def from_handle(cls, handle: int, rows: int, columns: int, group: int, bits: int) -> "CodebookMatrix":
+        m = cls.__new__(cls)
+        m._adopt(handle, rows, columns, group, bits)
+        return m
+
+    def _adopt(self, handle: int, rows: int, columns: int, group: int, bits: int) -> None:
+        self.handle = handle
         self.rows, self.columns, self.group, self.bits = rows, columns, group, bits
         padded = _i()
         check(lib.rn_matrix_padded_columns(self.handle, C.byref(padded)))
@@ -380,6 +415,58 @@ class CodebookMatrix:
         try:
             if self.handle:
                 lib.rn_matrix_free(self.handle)
+        except Exception:
+            pass
+
+
+class Archive:
+    """cact::Archive (crates/cact/src/archive.rs): a memory-mapped .cact file."""
+
+    def __init__(self, path: Optional[str] = None, data: Optional[bytes] = None):
+        h = _p()
+        if data is not None:
+            buf = np.frombuffer(data, dtype=np.uint8)
+            check(lib.rn_archive_from_memory(_ptr(buf) if buf.size else None, buf.size, C.byref(h)))
+        else:
+            check(lib.rn_archive_open(os.fsencode(path), C.byref(h)))
+        self.handle = h.value
+
+    def geometry(self) -> dict:
+        g = Geometry()
+        check(lib.rn_archive_geometry(self.handle, C.byref(g)))
+        out = {name: getattr(g, name) for name, _ in Geometry._fields_}
+        out["engram_orders"] = list(g.engram_orders)[:g.engram_order_count]
+        out["engram_sites"] = list(g.engram_sites)[:g.engram_site_count]
+        return out
+
+    def codebook(self) -> np.ndarray:
+        ptr, n = C.POINTER(_f)(), _i()
+        check(lib.rn_archive_codebook(self.handle, C.byref(ptr), C.byref(n)))
+        return np.ctypeslib.as_array(ptr, (n.value,)).copy() if n.value else np.zeros(0, np.float32)
+
+    def record(self, index: int) -> dict:
+        r = TensorRecord()
+        check(lib.rn_archive_record(self.handle, index, C.byref(r)))
+        return dict(kind=r.kind, shape=list(r.shape)[:r.rank], offset=r.offset, nbytes=r.nbytes,
+                    group_size=r.group_size, bits=r.bits)
+
+    def tensor_bytes(self, index: int) -> np.ndarray:
+        ptr, n = C.POINTER(C.c_uint8)(), _sz()
+        check(lib.rn_archive_tensor_bytes(self.handle, index, C.byref(ptr), C.byref(n)))
+        return np.ctypeslib.as_array(ptr, (n.value,)).copy() if n.value else np.zeros(0, np.uint8)
+
+    def matrix(self, index: int) -> "CodebookMatrix":
+        """QuantisedMatrix::from_archive (matrix.rs:35-40)."""
+        h = _p()
+        check(lib.rn_matrix_from_archive(self.handle, index, C.byref(h)))
+        r = self.record(index)
+        return CodebookMatrix.from_handle(h.value, r["shape"][0], r["shape"][1] if len(r["shape"]) > 1 else 1,
+                                          r["group_size"], r["bits"])
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_archive_close(self.handle)
         except Exception:
             pass
 

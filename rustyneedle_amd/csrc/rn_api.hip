@@ -83,6 +83,10 @@ int check_supported(int columns) {
 
 }  // namespace
 
+namespace rn {
+int set_error(int code, const char* message) { return fail(code, "%s", message); }
+}  // namespace rn
+
 struct rn_matrix {
     int8_t* W = nullptr;
     float* sW = nullptr;

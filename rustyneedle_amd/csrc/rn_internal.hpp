@@ -20,6 +20,9 @@ struct LaunchEvents {
 };
 LaunchEvents& launch_events();  // per host thread
 
+// Records `message` as the calling thread's last error (rn_last_error); returns `code`.
+int set_error(int code, const char* message);
+
 template <typename F, typename... Args>
 inline void rn_launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
     LaunchEvents& ev = launch_events();

@@ -87,3 +87,21 @@ def test_fused_products_share_the_rotated_input():
     for (g, o), y in zip(pairs, ys):
         assert np.array_equal(_bits(y), _bits(o.multiply_rotated(rotated)[0]))
 
+
+
+def test_matrix_from_an_archive_record():
+    """QuantisedMatrix::from_archive: the record's blob, shape, group and bits, and
+    the archive's codebook, give the same product as the blob given directly."""
+    from cact_writer import write
+    cb = rn.synthetic_codebook(128)
+    blobs = {bits: rn.synthetic_codebook_blob(96, 300, 128, bits, seed=bits) for bits in (2, 4, 5)}
+    data = write([(1, (8,), np.zeros(8, np.float16).tobytes(), 0, 0)] +
+                 [(3, (96, 300), blobs[b].tobytes(), 128, b) for b in (2, 4, 5)], cb)
+    a = rn.Archive(data=data)
+    x = rn.synth_normal(4, "cbarch", 1.0, (300,))
+    for index, bits in ((1, 2), (2, 4), (3, 5)):
+        g = a.matrix(index)
+        o = oracle.OracleCodebookMatrix(blobs[bits], 96, 300, 128, bits, cb)
+        rotated = g.prepare_host(x)
+        assert np.array_equal(_bits(g.multiply_batch_host(rotated)), _bits(o.multiply_rotated(rotated)))
+        assert np.array_equal(_bits(g.dequantise_row(95)), _bits(o.dequantise_row(95)))
