@@ -194,7 +194,7 @@ __global__ __launch_bounds__(1024) void cb_dequantise_kernel(CodebookParams p, i
 //      next row group's loads are issued before this one's epilogue;
 //   4. one lane per (token, row): the sequential group epilogue.
 template <int BITS, int GROUP, int FORM, int NL, int T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NL == 8 && T == 1 ? 4 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NL == 8 && T == 1 ? 3 : 1)))
 void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, int32_t* acc_out) {
     constexpr int IB = BITS == 5 ? 2 : BITS;        // index bits (ternary crumbs are 2)
     constexpr int EPC = 128 / IB;                    // elements per 16-byte chunk
@@ -231,10 +231,14 @@ void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, in
     };
     float xv[16];
     load_run(tid, xv);
-    v4i w[NL];
+    // With DB, row groups alternate between two sets of weight registers and a
+    // group's weights are requested before the previous group's decode;
+    // otherwise (wide rows, token tiles: no registers to spare) after it.
+    constexpr bool DB = NL == 8 && T == 1;
+    v4i wa[NL], wb[DB ? NL : 1];
     v4i nv[3];  // native vectors stay in registers (arrays of int4 structs may not)
     auto group_row0 = [&](int it) -> int { return (blockIdx.x * p.iters + it) * BR; };
-    auto issue = [&](int it) {
+    auto issue = [&](int it, auto& w) {
         const int rw = group_row0(it) + wv * R;
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
@@ -246,14 +250,18 @@ void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, in
     };
     // the norms are wanted only by the epilogue: requested after the prologue,
     // so their registers are not held through it
+    // (only the pieces the row group's norms cover: a full window per group
+    // would fetch up to six times the norm bytes)
     auto issue_norms = [&](int it) {
-        const size_t nal = ((size_t)min(group_row0(it), p.rows - 1) * G * 2) & ~(size_t)15;
+        const size_t nbase = (size_t)min(group_row0(it), p.rows - 1) * G * 2, nal = nbase & ~(size_t)15;
+        const int need = (int)(nbase - nal) + BR * G * 2;
 #pragma unroll
         for (int i = 0; i < 3; ++i)
-            nv[i] = *reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(p.norms) + nal +
-                                                  16 * (size_t)(tid + NT * i));
+            if (16 * (tid + NT * i) < need)
+                nv[i] = *reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(p.norms) + nal +
+                                                      16 * (size_t)(tid + NT * i));
     };
-    issue(0);
+    issue(0, wa);
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. prologue: per-group input codes and scales
@@ -288,12 +296,16 @@ void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, in
 
     issue_norms(0);
     const uint32_t lut[4] = {p.lut[0], p.lut[1], p.lut[2], p.lut[3]};
-    for (int it = 0; it < p.iters; ++it) {
+    // one row group: its norms to LDS, the next group's requests (into the
+    // other register set, so they are in flight through this decode), the
+    // group sums, the epilogue
+    auto step = [&](int it, v4i (&w)[NL], auto& w_next) {
         const int gr0 = group_row0(it), rw = gr0 + wv * R;
         const int nhalf0 = (int)((((size_t)min(gr0, p.rows - 1) * G * 2) & 15) / 2);
 #pragma unroll
         for (int i = 0; i < 3; ++i) reinterpret_cast<v4i*>(nm_s)[tid + NT * i] = nv[i];
         __syncthreads();  // codes, scales and this row group's norms
+        if (DB && it + 1 < p.iters) issue(it + 1, w_next);
 
         // 3. exact int32 group sums
 #pragma unroll
@@ -341,8 +353,8 @@ void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, in
             // 16 registers a chunk and cut the waves a CU keeps in flight
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (it + 1 < p.iters) {  // w and nv are free: in flight during the epilogue
-            issue(it + 1);
+        if (it + 1 < p.iters) {  // the registers are free now
+            if (!DB) issue(it + 1, w_next);
             issue_norms(it + 1);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -369,6 +381,14 @@ void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, in
                 for (int g = 0; g < G; ++g) acc_out[((size_t)(t0 + t) * p.rows + rw + r) * G + g] = a[g];
         }
         __syncthreads();  // the norms window and acc_s are read before the next row group replaces them
+    };
+    if constexpr (DB) {
+        for (int it = 0; it < p.iters; it += 2) {
+            step(it, wa, wb);
+            if (it + 1 < p.iters) step(it + 1, wb, wa);
+        }
+    } else {
+        for (int it = 0; it < p.iters; ++it) step(it, wa, wa);
     }
 }
 
@@ -379,7 +399,7 @@ inline size_t product_lds(const CodebookParams& p, int T, int R) {
     const size_t G = (size_t)(p.padded / p.group);
     return kNormWindow + (size_t)T * p.padded + 4 * (4 * (size_t)T * R * G + (size_t)T * G);
 }
-inline int product_loads(const CodebookParams& p) { return p.cpr <= 512 ? 8 : 16; }
+inline int product_loads(const CodebookParams& p) { return p.cpr < 64 ? 8 : 16; }
 inline int product_rows(const CodebookParams& p) { return min(64, 64 * product_loads(p) / p.cpr); }
 constexpr size_t kProductMaxLds = 64 * 1024;
 
@@ -391,10 +411,12 @@ hipError_t launch_product_t(const CodebookParams& p, const float* x, int count, 
     q.rows_per_block = product_rows(p);
     const size_t lds = product_lds(p, T, q.rows_per_block);
     if (lds > kProductMaxLds) return hipErrorInvalidValue;
-    // consecutive row groups per block: a wide input's prologue then serves
-    // up to padded / 1024 groups, while the grid keeps at least 512 blocks
+    // consecutive row groups per block (at least 4, or padded / 1024 for a wide
+    // input, whose prologue then serves them all), while the grid keeps at
+    // least 512 blocks; each group's loads are in flight during the previous
+    // group's decode
     const int groups = (p.rows + 4 * q.rows_per_block - 1) / (4 * q.rows_per_block);
-    q.iters = max(1, min(p.padded / 1024, groups / 512));
+    q.iters = max(1, min(max(4, p.padded / 1024), groups / 512));
     const dim3 grid((groups + q.iters - 1) / q.iters, (count + T - 1) / T);
     if (nl == 8)
         rn_launch(cb_product_kernel<BITS, GROUP, FORM, 8, T>, grid, dim3(256), lds, stream, q, x, count, y, acc);
