@@ -258,6 +258,28 @@ int rn_session_logits(rn_session* session, float* out);
  * token = argmax; ids[i] = token }. Each step is one replay of a captured
  * hipGraph; the argmax stays on the device and feeds the next embedding. */
 int rn_session_decode_greedy(rn_session* session, uint32_t first, int steps, uint32_t* ids);
+
+/* ---- grammar-constrained choice (generator.rs:99-117, 147-194) ----------------
+ * While a tool-call grammar is active the generator picks
+ * argmax_allowed(logits, allowed) (the first allowed index of the largest
+ * allowed value; a NaN wins only as the first allowed value), falls back to
+ * argmax when nothing is allowed, and accumulates allowed_statistics of the
+ * choice: probability = fast_exp(l[t] - peak_allowed) / total_allowed and
+ * mass = total_allowed * fast_exp(peak_allowed - peak_all) / total_all, the
+ * totals summed sequentially in index order as the reference does. */
+typedef struct {
+    uint32_t token;      /* the choice (or the token asked for) */
+    int32_t constrained; /* 1: argmax_allowed found a token; 0: nothing allowed, argmax */
+    float probability;
+    float mass;
+} rn_choice;
+/* logits [n] f32, allowed [n] bytes (non-zero = allowed) and out are device
+ * pointers; token < 0 chooses, token >= 0 gives the statistics of that token. */
+int rn_choose_allowed(const float* logits, const uint8_t* allowed, int n, int token, rn_choice* out, void* stream);
+/* The session's logits (as rn_session_logits, left on the device) and the
+ * constrained choice over them: allowed is a host mask of vocab bytes (the
+ * grammar's TokenBytes::allowed, generator.rs:104), out a host rn_choice. */
+int rn_session_choose_allowed(rn_session* session, const uint8_t* allowed, rn_choice* out);
 /* The stream the session's work runs on (hipStream_t as void*). */
 int rn_session_stream(const rn_session* session, void** stream);
 

@@ -558,3 +558,32 @@ class OracleCodebookMatrix:
         lib.ro_codebook_dequantise_row(_ptr(self.packed), _ptr(self.norms), self.padded, self.columns, self.group,
                                        self.bits, _ptr(self.levels), row, _ptr(out))
         return out
+
+
+# ---- grammar-constrained choice (rn_generate.c) ---------------------------------
+lib.ro_argmax_allowed.restype = C.c_int32
+lib.ro_argmax_allowed.argtypes = [_p, _p, _i]
+lib.ro_allowed_statistics.argtypes = [_p, _p, _i, _i, C.POINTER(_f), C.POINTER(_f)]
+
+
+def argmax_allowed(values, allowed) -> int:
+    """generator.rs:147-155; -1 where the reference returns None."""
+    v = _f32(values)
+    a = np.ascontiguousarray(allowed, dtype=np.uint8)
+    return int(lib.ro_argmax_allowed(_ptr(v), _ptr(a), v.size))
+
+
+def allowed_statistics(logits, allowed, token: int):
+    v = _f32(logits)
+    a = np.ascontiguousarray(allowed, dtype=np.uint8)
+    p, m = _f(), _f()
+    lib.ro_allowed_statistics(_ptr(v), _ptr(a), v.size, token, C.byref(p), C.byref(m))
+    return np.float32(p.value), np.float32(m.value)
+
+
+def choose_allowed(logits, allowed):
+    """generator.rs:99-117: argmax_allowed, else argmax; and the statistics of the choice."""
+    token = argmax_allowed(logits, allowed)
+    if token < 0:
+        token = argmax(logits)
+    return (token,) + allowed_statistics(logits, allowed, token)

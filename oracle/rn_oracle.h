@@ -148,6 +148,11 @@ void ro_codebook_product(const uint8_t* packed, const uint16_t* norms, int rows,
 void ro_codebook_dequantise_row(const uint8_t* packed, const uint16_t* norms, int padded, int columns,
                                 int group, int bits, const float levels[16], int row, float* out); /* matrix.rs:140-153 */
 
+/* ---- grammar-constrained choice (rn_generate.c) ------------------------------ */
+int32_t ro_argmax_allowed(const float* values, const uint8_t* allowed, int n);   /* generator.rs:147-155 */
+void ro_allowed_statistics(const float* logits, const uint8_t* allowed, int n, int token, float* probability,
+                           float* mass);                                         /* generator.rs:182-194 */
+
 /* ---- Whistle-style speech path (rn_whistle.c) ---------------------------------
  * crates/whistle: stem (stem.rs), encoder (encoder.rs), cross-attention
  * memory and apply (cross.rs), and the decoder step with the cross hook

@@ -91,6 +91,11 @@ class TensorRecord(C.Structure):
                 ("nbytes", C.c_uint64), ("group_size", C.c_uint32), ("bits", C.c_uint32)]
 
 
+class Choice(C.Structure):
+    """rn_choice: the constrained choice and its allowed_statistics (generator.rs:99-194)."""
+    _fields_ = [("token", C.c_uint32), ("constrained", C.c_int32), ("probability", C.c_float), ("mass", C.c_float)]
+
+
 class WhistleConfig(C.Structure):
     _fields_ = [(n, _i) for n in ("mels", "frames", "d_model", "heads", "head_dim", "enc_layers", "dec_layers", "ffn",
                                   "vocab", "max_positions", "group")] + [("rope_theta", _f), ("norm_eps", _f)]
@@ -132,6 +137,8 @@ SIGNATURES = {
     "rn_archive_record": (_i, [_p, _i, C.POINTER(TensorRecord)]),
     "rn_archive_tensor_bytes": (_i, [_p, _i, C.POINTER(C.POINTER(C.c_uint8)), C.POINTER(_sz)]),
     "rn_matrix_from_archive": (_i, [_p, _i, C.POINTER(_p)]),
+    "rn_choose_allowed": (_i, [_p, _p, _i, _i, _p, _p]),
+    "rn_session_choose_allowed": (_i, [_p, _p, C.POINTER(Choice)]),
     "rn_quantise_int8": (_i, [_p, _i, _i, _p, _p, _p]),
     "rn_fast_exp": (_i, [_p, _p, _i, _p]),
     "rn_silu": (_i, [_p, _p, _i, _p]),
@@ -772,6 +779,14 @@ class Session:
         check(lib.rn_session_logits(self.handle, _ptr(out)))
         return out
 
+    def choose_allowed(self, allowed: np.ndarray):
+        """generator.rs:99-117: (token, constrained, probability, mass) over this step's logits."""
+        mask = np.ascontiguousarray(allowed, dtype=np.uint8)
+        assert mask.shape == (self.model.config["vocab"],)
+        c = Choice()
+        check(lib.rn_session_choose_allowed(self.handle, _ptr(mask), C.byref(c)))
+        return int(c.token), bool(c.constrained), np.float32(c.probability), np.float32(c.mass)
+
     def decode_greedy(self, first: int, steps: int) -> np.ndarray:
         ids = np.empty(steps, dtype=np.uint32)
         check(lib.rn_session_decode_greedy(self.handle, int(first), steps, _ptr(ids)))
@@ -912,3 +927,15 @@ class Whistle:
                 self.handle = None
         except Exception:
             pass
+
+
+def choose_allowed(logits: np.ndarray, allowed: np.ndarray, token: int = -1):
+    """rn_choose_allowed on host arrays: (token, constrained, probability, mass)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    mask = np.ascontiguousarray(allowed, dtype=np.uint8)
+    ld, md, od = DeviceBuffer.from_array(logits), DeviceBuffer.from_array(mask), DeviceBuffer(C.sizeof(Choice))
+    check(lib.rn_choose_allowed(ld.ptr, md.ptr, logits.size, token, od.ptr, None))
+    check(lib.rn_stream_synchronize(None))
+    raw = od.download(np.uint8, (C.sizeof(Choice),))
+    c = Choice.from_buffer_copy(raw.tobytes())
+    return int(c.token), bool(c.constrained), np.float32(c.probability), np.float32(c.mass)

@@ -129,6 +129,8 @@ struct rn_session {
     // prefill scratch, grown on demand
     void* scratch = nullptr;
     int scratch_tokens = 0;
+    // constrained choice: the vocabulary mask and the result, allocated on first use
+    void* choice_buf = nullptr;
 };
 
 struct rn_batch {
@@ -739,6 +741,7 @@ int rn_session_free(rn_session* s) {
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     if (s->step_graph) (void)hipGraphExecDestroy(s->step_graph);
     if (s->scratch) (void)hipFree(s->scratch);
+    if (s->choice_buf) (void)hipFree(s->choice_buf);
     (void)hipFree(s->arena);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
@@ -966,6 +969,38 @@ int rn_session_logits(rn_session* s, float* out) {
     const int rpb = gemv_rows_per_block(c.vocab, c.d_model, kStore);
     RN_HIP(launch_gemv(p, c.d_model, kQuant, kStore, kPlane, rpb, (c.vocab + rpb - 1) / rpb, s->stream));
     RN_HIP(hipMemcpyAsync(out, s->logits, 4 * (size_t)c.vocab, hipMemcpyDeviceToHost, s->stream));
+    return check_state_error(s);
+}
+
+static_assert(sizeof(rn_choice) == sizeof(Choice), "rn_choice mirrors rn::Choice");
+
+int rn_choose_allowed(const float* logits, const uint8_t* allowed, int n, int token, rn_choice* out, void* stream) {
+    RN_REQUIRE(logits && allowed && out, "null argument");
+    RN_REQUIRE(n >= 1, "n must be positive (got %d)", n);
+    RN_REQUIRE(token < n, "token %d outside the %d logits", token, n);
+    RN_HIP(launch_constrained_choice(logits, allowed, n, token < 0 ? -1 : token, reinterpret_cast<Choice*>(out),
+                                     (hipStream_t)stream));
+    return RN_OK;
+}
+
+int rn_session_choose_allowed(rn_session* s, const uint8_t* allowed, rn_choice* out) {
+    RN_REQUIRE(s && allowed && out, "null argument");
+    if (!s->has_hidden) return fail(RN_ERR_STATE, "no token has been pushed");
+    const rn_model* m = s->model;
+    const rn_config& c = m->cfg;
+    if (!s->choice_buf) RN_HIP(hipMalloc(&s->choice_buf, align_up((size_t)c.vocab) + sizeof(Choice)));
+    uint8_t* mask = (uint8_t*)s->choice_buf;
+    Choice* choice = (Choice*)((char*)s->choice_buf + align_up((size_t)c.vocab));
+    GemvParams p{};
+    p.nseg = 1;
+    p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab, 0};
+    p.x = s->hidden;
+    const int rpb = gemv_rows_per_block(c.vocab, c.d_model, kStore);
+    RN_HIP(launch_gemv(p, c.d_model, kQuant, kStore, kPlane, rpb, (c.vocab + rpb - 1) / rpb, s->stream));
+    RN_HIP(hipMemcpyAsync(mask, allowed, (size_t)c.vocab, hipMemcpyHostToDevice, s->stream));
+    RN_HIP(launch_constrained_choice(s->logits, mask, c.vocab, -1, choice, s->stream));
+    RN_HIP(hipMemcpyAsync(out, choice, sizeof(Choice), hipMemcpyDeviceToHost, s->stream));
+    RN_HIP(hipStreamSynchronize(s->stream));
     return check_state_error(s);
 }
 

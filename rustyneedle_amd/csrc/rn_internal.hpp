@@ -267,6 +267,17 @@ hipError_t launch_codebook_product(const CodebookParams& p, const float* x, int 
 hipError_t launch_codebook_rotate(const float* x, int count, int columns, int padded, int group, float scale,
                                   float* rotated, hipStream_t stream);
 hipError_t launch_codebook_dequantise(const CodebookParams& p, int row, float* out, hipStream_t stream);
+
+// The grammar-constrained choice (generator.rs:99-117): the chosen token (or
+// the given one), whether an allowed token existed, and allowed_statistics.
+struct Choice {
+    uint32_t token;
+    int32_t constrained;
+    float probability;
+    float mass;
+};
+hipError_t launch_constrained_choice(const float* logits, const uint8_t* allowed, int n, int token, Choice* out,
+                                     hipStream_t stream);
 hipError_t launch_add(const float* a, const float* b, size_t n, float* out, hipStream_t stream);
 
 // ---- elementwise / helpers ----------------------------------------------------

@@ -119,4 +119,126 @@ hipError_t launch_fast_exp(const float* x, float* y, int n, int apply_silu, hipS
     return hipGetLastError();
 }
 
+// The grammar-constrained choice of generator.rs:99-117 over n logits, one
+// 1024-thread block.
+//   1. Peaks (max is order-free: DPP within waves, then LDS), the greedy keys
+//      of all and of allowed values (argmax_key: larger value, then lower
+//      index) and the first allowed index. argmax_allowed (generator.rs:147-155)
+//      is the first allowed index when its value is NaN, else the best allowed
+//      key; with nothing allowed the choice falls back to argmax
+//      (generator.rs:157-165).
+//   2. allowed_statistics (generator.rs:182-194): the two totals are sequential
+//      sums in index order, so the block computes fast_exp terms for 4096
+//      values at a time into LDS and lanes 0 and 1 of wave 0 add them in order
+//      (lane 0 the total over all values, lane 1 the allowed total, where a
+//      disallowed term is multiplied by 0 as the reference does).
+// token >= 0 asks for the statistics of that token instead of the choice.
+__global__ __launch_bounds__(1024) void constrained_choice_kernel(const float* logits, const uint8_t* allowed, int n,
+                                                                  int token, Choice* out) {
+    constexpr int NT = 1024, NW = NT / 64, CH = 4096;
+    __shared__ __align__(16) float ea_s[CH];
+    __shared__ __align__(16) float ek_s[CH];
+    __shared__ float pa_s[NW], pk_s[NW];
+    __shared__ unsigned long long key_s[NW], akey_s[NW];
+    __shared__ int first_s[NW];
+    __shared__ float peaks_s[2];
+    __shared__ int token_s, found_s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    float pa = -INFINITY, pk = -INFINITY;
+    uint64_t key = 0, akey = 0;
+    int first = n;
+    for (int i = tid; i < n; i += NT) {
+        const float v = logits[i];
+        const bool ok = allowed[i] != 0;
+        pa = fmaxf(pa, v);
+        const uint64_t k = argmax_key(v, (uint32_t)i);
+        key = k > key ? k : key;
+        if (ok) {
+            pk = fmaxf(pk, v);
+            akey = k > akey ? k : akey;
+            first = min(first, i);
+        }
+    }
+    pa = wave_max(pa);
+    pk = wave_max(pk);
+    key = wave_max_u64(key);
+    akey = wave_max_u64(akey);
+    for (int o = 32; o >= 1; o >>= 1) first = min(first, __shfl_xor(first, o, 64));
+    if (lane == 0) {
+        pa_s[wave] = pa;
+        pk_s[wave] = pk;
+        key_s[wave] = key;
+        akey_s[wave] = akey;
+        first_s[wave] = first;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < NW; ++w) {
+            pa = fmaxf(pa, pa_s[w]);
+            pk = fmaxf(pk, pk_s[w]);
+            key = key_s[w] > key ? key_s[w] : key;
+            akey = akey_s[w] > akey ? akey_s[w] : akey;
+            first = min(first, first_s[w]);
+        }
+        peaks_s[0] = pa;
+        peaks_s[1] = pk;
+        int t = token;
+        const bool found = first < n;
+        if (t < 0) {
+            if (found)
+                t = logits[first] != logits[first] ? first : (int)argmax_index(akey);
+            else
+                t = logits[0] != logits[0] ? 0 : (int)argmax_index(key);
+        }
+        token_s = t;
+        found_s = found ? 1 : 0;
+    }
+    __syncthreads();
+    const float peak_all = peaks_s[0], peak_allowed = peaks_s[1];
+
+    float total = 0.0f;  // lane 0: over all values; lane 1: over allowed ones
+    for (int base = 0; base < n; base += CH) {
+        const int m = min(CH, n - base);
+        for (int i = tid; i < m; i += NT) {
+            const float v = logits[base + i];
+            ea_s[i] = fast_exp(v - peak_all);
+            ek_s[i] = fast_exp(v - peak_allowed) * (allowed[base + i] != 0 ? 1.0f : 0.0f);
+        }
+        __syncthreads();
+        if (wave == 0 && lane < 2) {
+            const float* src = lane == 0 ? ea_s : ek_s;
+            int i = 0;
+            for (; i + 4 <= m; i += 4) {
+                const float4 q = *reinterpret_cast<const float4*>(src + i);
+                total = total + q.x;
+                total = total + q.y;
+                total = total + q.z;
+                total = total + q.w;
+            }
+            for (; i < m; ++i) total = total + src[i];
+        }
+        __syncthreads();
+    }
+    if (wave == 0) {
+        const float total_allowed = __shfl(total, 1, 64);
+        if (lane == 0) {
+            const int t = token_s;
+            Choice c;
+            c.token = (uint32_t)t;
+            c.constrained = found_s;
+            c.probability = fast_exp(logits[t] - peak_allowed) / total_allowed;
+            c.mass = (total_allowed * fast_exp(peak_allowed - peak_all)) / total;
+            *out = c;
+        }
+    }
+}
+
+hipError_t launch_constrained_choice(const float* logits, const uint8_t* allowed, int n, int token, Choice* out,
+                                     hipStream_t stream) {
+    if (n < 1 || token >= n) return hipErrorInvalidValue;
+    rn_launch(constrained_choice_kernel, dim3(1), dim3(1024), 0, stream, logits, allowed, n, token, out);
+    return hipGetLastError();
+}
+
 }  // namespace rn
