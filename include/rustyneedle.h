@@ -329,6 +329,23 @@ typedef struct {
 } rn_whistle_config;
 typedef struct rn_whistle rn_whistle;
 
+/* The front end (crates/whistle/src/frontend.rs): Frontend::new (frontend.rs:31-40)
+ * with the archive's mel filterbank [fft_size/2 + 1][mels] (host floats); the
+ * Hann window and FFT twiddles are built on the host in float from cosf/sinf.
+ * fft_size a power of two <= 4096, mels <= 256. */
+typedef struct rn_frontend rn_frontend;
+int rn_frontend_create(int mels, int fft_size, int window, int hop, const float* mel_weights, rn_frontend** out);
+int rn_frontend_free(rn_frontend* frontend);
+/* Frontend::log_mel (frontend.rs:72-102) on the device: samples (host, n) ->
+ * features (host, [n/hop + 1][mels]) normalised per mel over the valid
+ * frames (frames past them 0), *frames = n/hop + 1, *valid = n/hop, *spread
+ * (Frontend::spread of the un-normalised log-mel, frontend.rs:104-116). The FFT,
+ * power spectrum, mel sums and normalisation follow the reference's float
+ * order; ln is the device logf where the reference calls the host libm's, so
+ * features agree with it within 5e-5 (1 + |x|), not bit for bit. */
+int rn_frontend_log_mel(rn_frontend* frontend, const float* samples, int n, float* features, int* frames,
+                        int* valid, float* spread);
+
 /* Whistle::open (lib.rs:101-140) with seeded synthetic weights drawn by name
  * (the same draws as rn_synth_*): the model, its work buffers and one decoder
  * session of max_positions positions, on their own stream. */

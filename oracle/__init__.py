@@ -587,3 +587,35 @@ def choose_allowed(logits, allowed):
     if token < 0:
         token = argmax(logits)
     return (token,) + allowed_statistics(logits, allowed, token)
+
+
+# ---- speech front end (rn_frontend.c) -------------------------------------------
+lib.ro_frontend_tables.argtypes = [_i, _i, _p, _p, _p]
+lib.ro_power_spectrum.argtypes = [_p, _p, _i, _p, _p, _p]
+lib.ro_log_mel.restype = _i
+lib.ro_log_mel.argtypes = [_p, _i, _i, _i, _i, _i, _p, _p, C.POINTER(_i), C.POINTER(_f)]
+
+
+def frontend_tables(fft_size: int, window: int):
+    win, tc, ts = np.empty(window, np.float32), np.empty(fft_size // 2, np.float32), np.empty(fft_size // 2, np.float32)
+    lib.ro_frontend_tables(fft_size, window, _ptr(win), _ptr(tc), _ptr(ts))
+    return win, tc, ts
+
+
+def power_spectrum(real, imaginary):
+    re, im = _f32(real).copy(), _f32(imaginary).copy()
+    _, tc, ts = frontend_tables(re.size, 2)
+    out = np.empty(re.size // 2 + 1, np.float32)
+    lib.ro_power_spectrum(_ptr(re), _ptr(im), re.size, _ptr(tc), _ptr(ts), _ptr(out))
+    return out
+
+
+def log_mel(samples, mels: int, fft_size: int, window: int, hop: int, mel_weights):
+    """Frontend::log_mel: (features [frames][mels], valid, spread)."""
+    x = _f32(samples)
+    w = _f32(mel_weights)
+    data = np.empty((x.size // hop + 1, mels), np.float32)
+    valid, spread = _i(), _f()
+    lib.ro_log_mel(_ptr(x) if x.size else None, x.size, mels, fft_size, window, hop, _ptr(w), _ptr(data),
+                   C.byref(valid), C.byref(spread))
+    return data, valid.value, np.float32(spread.value)

@@ -148,6 +148,17 @@ void ro_codebook_product(const uint8_t* packed, const uint16_t* norms, int rows,
 void ro_codebook_dequantise_row(const uint8_t* packed, const uint16_t* norms, int padded, int columns,
                                 int group, int bits, const float levels[16], int row, float* out); /* matrix.rs:140-153 */
 
+/* ---- speech front end (rn_frontend.c): crates/whistle/src/frontend.rs ---------- */
+void ro_frontend_tables(int fft_size, int window, float* win, float* twiddle_cos, float* twiddle_sin); /* :32-39 */
+void ro_power_spectrum(float* real, float* imaginary, int size, const float* twiddle_cos, const float* twiddle_sin,
+                       float* power);                                                                  /* :42-70 */
+int ro_log_mel_raw(const float* samples, int n, int mels, int fft_size, int window, int hop,
+                   const float* mel_weights, float* data);
+float ro_spread(const float* data, int valid, int mels);                                               /* :104-116 */
+void ro_normalise(float* data, int frames, int valid, int mels);                                       /* :118-133 */
+int ro_log_mel(const float* samples, int n, int mels, int fft_size, int window, int hop, const float* mel_weights,
+               float* data, int* valid, float* spread);                                                /* :72-102 */
+
 /* ---- grammar-constrained choice (rn_generate.c) ------------------------------ */
 int32_t ro_argmax_allowed(const float* values, const uint8_t* allowed, int n);   /* generator.rs:147-155 */
 void ro_allowed_statistics(const float* logits, const uint8_t* allowed, int n, int token, float* probability,

@@ -138,6 +138,9 @@ SIGNATURES = {
     "rn_archive_tensor_bytes": (_i, [_p, _i, C.POINTER(C.POINTER(C.c_uint8)), C.POINTER(_sz)]),
     "rn_matrix_from_archive": (_i, [_p, _i, C.POINTER(_p)]),
     "rn_choose_allowed": (_i, [_p, _p, _i, _i, _p, _p]),
+    "rn_frontend_create": (_i, [_i, _i, _i, _i, _p, C.POINTER(_p)]),
+    "rn_frontend_free": (_i, [_p]),
+    "rn_frontend_log_mel": (_i, [_p, _p, _i, _p, C.POINTER(_i), C.POINTER(_i), C.POINTER(_f)]),
     "rn_session_choose_allowed": (_i, [_p, _p, C.POINTER(Choice)]),
     "rn_quantise_int8": (_i, [_p, _i, _i, _p, _p, _p]),
     "rn_fast_exp": (_i, [_p, _p, _i, _p]),
@@ -939,3 +942,45 @@ def choose_allowed(logits: np.ndarray, allowed: np.ndarray, token: int = -1):
     raw = od.download(np.uint8, (C.sizeof(Choice),))
     c = Choice.from_buffer_copy(raw.tobytes())
     return int(c.token), bool(c.constrained), np.float32(c.probability), np.float32(c.mass)
+
+
+class Frontend:
+    """crates/whistle/src/frontend.rs: the log-mel front end on the device."""
+
+    def __init__(self, mels: int, fft_size: int, window: int, hop: int, mel_weights: np.ndarray):
+        w = np.ascontiguousarray(mel_weights, dtype=np.float32)
+        assert w.shape == (fft_size // 2 + 1, mels)
+        h = _p()
+        check(lib.rn_frontend_create(mels, fft_size, window, hop, _ptr(w), C.byref(h)))
+        self.handle = h.value
+        self.mels, self.hop = mels, hop
+
+    def log_mel(self, samples: np.ndarray):
+        """Frontend::log_mel: (features [frames][mels], valid, spread)."""
+        x = np.ascontiguousarray(samples, dtype=np.float32)
+        out = np.empty((x.size // self.hop + 1, self.mels), np.float32)
+        frames, valid, spread = _i(), _i(), _f()
+        check(lib.rn_frontend_log_mel(self.handle, _ptr(x) if x.size else None, x.size, _ptr(out), C.byref(frames),
+                                      C.byref(valid), C.byref(spread)))
+        return out, valid.value, np.float32(spread.value)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_frontend_free(self.handle)
+        except Exception:
+            pass
+
+
+def synthetic_mel_filters(mels: int, fft_size: int, sample_rate: int = 16000) -> np.ndarray:
+    """Triangular mel filters [fft_size/2 + 1][mels] on the HTK mel scale (a
+    stand-in for the archive's filterbank)."""
+    bins = fft_size // 2 + 1
+    hz = np.linspace(0, sample_rate / 2, bins)
+    mel = lambda f: 2595.0 * np.log10(1.0 + f / 700.0)
+    edges = 700.0 * (10 ** (np.linspace(mel(0.0), mel(sample_rate / 2), mels + 2) / 2595.0) - 1.0)
+    w = np.zeros((bins, mels))
+    for m in range(mels):
+        lo, c, hi = edges[m], edges[m + 1], edges[m + 2]
+        w[:, m] = np.maximum(0.0, np.minimum((hz - lo) / (c - lo), (hi - hz) / (hi - c)))
+    return w.astype(np.float32)

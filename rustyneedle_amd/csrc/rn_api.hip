@@ -972,6 +972,81 @@ int rn_session_logits(rn_session* s, float* out) {
     return check_state_error(s);
 }
 
+// ---- speech front end -------------------------------------------------------------
+
+struct rn_frontend {
+    FrontendParams p{};
+    float* tables = nullptr;  // window gains, twiddles, mel weights
+};
+
+// Frontend::new (frontend.rs:31-40): the Hann window and the twiddles in float
+// from cosf / sinf, computed here on the host as the reference does.
+int rn_frontend_create(int mels, int fft_size, int window, int hop, const float* mel_weights, rn_frontend** out) {
+    RN_REQUIRE(mel_weights && out, "null argument");
+    RN_REQUIRE(mels >= 1 && mels <= 256, "mels must be 1..256 (got %d)", mels);
+    RN_REQUIRE(fft_size >= 2 && fft_size <= 4096 && (fft_size & (fft_size - 1)) == 0,
+               "fft_size must be a power of two in 2..4096 (got %d)", fft_size);
+    RN_REQUIRE(window >= 2 && hop >= 1, "window must be at least 2 and hop positive");
+    const int bins = fft_size / 2 + 1, half = fft_size / 2;
+    std::vector<float> host((size_t)window + 2 * half + (size_t)bins * mels);
+    float* win = host.data();
+    float* tc = win + window;
+    float* ts = tc + half;
+    const float pi = 3.14159265358979323846f;
+    for (int n = 0; n < window; ++n) win[n] = 0.5f - 0.5f * cosf(((2.0f * pi) * (float)n) / (float)(window - 1));
+    for (int k = 0; k < half; ++k) {
+        tc[k] = cosf(((2.0f * pi) * (float)k) / (float)fft_size);
+        ts[k] = -sinf(((2.0f * pi) * (float)k) / (float)fft_size);
+    }
+    std::copy(mel_weights, mel_weights + (size_t)bins * mels, ts + half);
+    rn_frontend* f = new (std::nothrow) rn_frontend();
+    if (!f) return fail(RN_ERR_MEMORY, "out of host memory");
+    if (hipMalloc(&f->tables, sizeof(float) * host.size()) != hipSuccess) {
+        delete f;
+        return fail(RN_ERR_MEMORY, "device allocation failed");
+    }
+    if (hipMemcpy(f->tables, host.data(), sizeof(float) * host.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(f->tables);
+        delete f;
+        return fail(RN_ERR_DEVICE, "upload of the front-end tables failed");
+    }
+    int log2 = 0;
+    while ((1 << log2) < fft_size) ++log2;
+    f->p = FrontendParams{mels, fft_size, log2, window, hop, f->tables, f->tables + window, f->tables + window + half,
+                          f->tables + window + 2 * half};
+    *out = f;
+    return RN_OK;
+}
+
+int rn_frontend_free(rn_frontend* f) {
+    if (!f) return RN_OK;
+    (void)hipFree(f->tables);
+    delete f;
+    return RN_OK;
+}
+
+int rn_frontend_log_mel(rn_frontend* f, const float* samples, int n, float* features, int* frames, int* valid,
+                        float* spread) {
+    RN_REQUIRE(f && (samples || n == 0) && features && frames && valid && spread, "null argument");
+    RN_REQUIRE(n >= 0, "n must be non-negative");
+    const int nf = n / f->p.hop + 1;
+    const size_t fb = sizeof(float) * (size_t)nf * f->p.mels;
+    char* dev = nullptr;
+    RN_HIP(hipMalloc(&dev, align_up(sizeof(float) * (size_t)n + 4) + fb + 4));
+    float* ds = (float*)dev;
+    float* dd = (float*)(dev + align_up(sizeof(float) * (size_t)n + 4));
+    float* dspread = (float*)((char*)dd + fb);
+    hipError_t e = n ? hipMemcpy(ds, samples, sizeof(float) * (size_t)n, hipMemcpyHostToDevice) : hipSuccess;
+    if (e == hipSuccess) e = launch_log_mel(f->p, ds, n, dd, dspread, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(features, dd, fb, hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(spread, dspread, sizeof(float), hipMemcpyDeviceToHost);
+    (void)hipFree(dev);
+    RN_HIP(e);
+    *frames = nf;
+    *valid = n / f->p.hop;
+    return RN_OK;
+}
+
 static_assert(sizeof(rn_choice) == sizeof(Choice), "rn_choice mirrors rn::Choice");
 
 int rn_choose_allowed(const float* logits, const uint8_t* allowed, int n, int token, rn_choice* out, void* stream) {

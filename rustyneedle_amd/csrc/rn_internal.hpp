@@ -268,6 +268,18 @@ hipError_t launch_codebook_rotate(const float* x, int count, int columns, int pa
                                   float* rotated, hipStream_t stream);
 hipError_t launch_codebook_dequantise(const CodebookParams& p, int row, float* out, hipStream_t stream);
 
+// The speech front end (frontend.rs): device tables built on the host.
+struct FrontendParams {
+    int mels, fft_size, log2_size, window, hop;
+    const float* window_gain;  // [window] Hann gains
+    const float* twiddle_cos;  // [fft_size / 2]
+    const float* twiddle_sin;
+    const float* mel_weights;  // [fft_size / 2 + 1][mels]
+};
+// samples [n] -> data [n / hop + 1][mels] normalised, spread (device scalar)
+hipError_t launch_log_mel(const FrontendParams& p, const float* samples, int n, float* data, float* spread,
+                          hipStream_t stream);
+
 // The grammar-constrained choice (generator.rs:99-117): the chosen token (or
 // the given one), whether an allowed token existed, and allowed_statistics.
 struct Choice {

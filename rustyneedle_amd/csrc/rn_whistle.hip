@@ -2,9 +2,11 @@
 // convolutions, per-head norm/rotary/int8 codes, attention with int8 queries,
 // keys and values, and the decoder's fused cross-attention.
 //
-// Replaces crates/whistle/src/stem.rs:39-115 (first convolution, one
-// depthwise + pointwise stage), encoder.rs:217-297 (the attention's integer
-// scores and int8 values) and cross.rs:58-182 (memory, apply). Products go
+// Replaces crates/whistle/src/frontend.rs:42-133 (FFT, power spectrum, mel
+// projection, log, spread and normalisation), stem.rs:39-115 (first
+// convolution, one depthwise + pointwise stage), encoder.rs:217-297 (the
+// attention's integer scores and int8 values) and cross.rs:58-182 (memory,
+// apply). Products go
 // through the shared int8 kernels (rn_gemm.hip, rn_gemv.hip); the cross
 // residual (cross.rs:176-181) is the prologue of the gated FFN's product.
 //
@@ -822,6 +824,102 @@ __global__ void add_rows_kernel(const float* a, const float* b, size_t n, float*
 hipError_t launch_add(const float* a, const float* b, size_t n, float* out, hipStream_t stream) {
     if (n == 0) return hipSuccess;
     rn_launch(add_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, b, n, out);
+    return hipGetLastError();
+}
+
+}  // namespace rn
+
+namespace rn {
+
+// Frontend::log_mel (frontend.rs:72-102) up to the log: one 256-thread block per
+// frame. The windowed samples go straight to their bit-reversed slots (the swap
+// loop of frontend.rs:44-50 leaves slot i holding input rev(i)); the
+// butterflies of each span run one per thread with the reference's float
+// operations (frontend.rs:52-66); the power spectrum, then per mel the
+// projection summed bin by bin and ln(value + FLOOR).
+__global__ __launch_bounds__(256) void log_mel_kernel(FrontendParams p, const float* samples, int n, float* data) {
+    extern __shared__ __align__(16) float fft_s[];
+    float* re = fft_s;
+    float* im = fft_s + p.fft_size;
+    float* power = fft_s + 2 * p.fft_size;
+    const int tid = threadIdx.x, frame = blockIdx.x, size = p.fft_size;
+    const int bins = size / 2 + 1, half = p.window / 2;
+    for (int i = tid; i < size; i += 256) {
+        re[i] = 0.0f;
+        im[i] = 0.0f;
+    }
+    __syncthreads();
+    for (int pos = tid; pos < p.window && pos < size; pos += 256) {
+        const long long source = (long long)frame * p.hop + pos - half;
+        if (source >= 0 && source < n) re[__brev((unsigned)pos) >> (32 - p.log2_size)] = samples[source] * p.window_gain[pos];
+    }
+    for (int span = 1; span < size; span *= 2) {
+        __syncthreads();
+        const int stride = size / (span * 2);
+        for (int j = tid; j < size / 2; j += 256) {
+            const int offset = j % span, a = (j / span) * 2 * span + offset, b = a + span;
+            const float c = p.twiddle_cos[offset * stride], s = p.twiddle_sin[offset * stride];
+            const float tr = re[b] * c - im[b] * s;
+            const float ti = re[b] * s + im[b] * c;
+            re[b] = re[a] - tr;
+            im[b] = im[a] - ti;
+            re[a] = re[a] + tr;
+            im[a] = im[a] + ti;
+        }
+    }
+    __syncthreads();
+    for (int bin = tid; bin < bins; bin += 256) power[bin] = re[bin] * re[bin] + im[bin] * im[bin];
+    __syncthreads();
+    for (int m = tid; m < p.mels; m += 256) {
+        float row = 0.0f;
+        for (int bin = 0; bin < bins; ++bin) row = row + power[bin] * p.mel_weights[(size_t)bin * p.mels + m];
+        data[(size_t)frame * p.mels + m] = logf(row + 5.9604645e-8f);  // FLOOR, frontend.rs:3
+    }
+}
+
+// Frontend::spread and normalise (frontend.rs:104-133), one thread per mel: the
+// mean and squared deviations summed over the valid frames in order (from -0.0,
+// as Iterator::sum does), then the spread's per-mel deviations summed in mel
+// order by thread 0, and the normalised column (0 past the valid frames).
+__global__ __launch_bounds__(256) void normalise_mels_kernel(float* data, int frames, int valid, int mels,
+                                                             float* spread) {
+    __shared__ float dev_s[256];
+    const int m = threadIdx.x;
+    if (m < mels) {
+        float sum = -0.0f;
+        for (int f = 0; f < valid; ++f) sum = sum + data[(size_t)f * mels + m];
+        const float count = (float)(valid > 1 ? valid : 1);
+        const float mean = sum / count;  // = sum / valid whenever valid >= 1
+        float sq = -0.0f;
+        for (int f = 0; f < valid; ++f) {
+            const float d = data[(size_t)f * mels + m] - mean;
+            sq = sq + d * d;
+        }
+        if (valid >= 2) dev_s[m] = sqrtf(sq / (float)(valid - 1));
+        const float denominator = fmaxf((float)(valid > 1 ? valid : 1) - 1.0f, 1.0f);
+        const float scale = 1.0f / (sqrtf(sq / denominator) + 1e-5f);  // NORMALISER_EPSILON, frontend.rs:4
+        for (int f = 0; f < frames; ++f) {
+            float* slot = data + (size_t)f * mels + m;
+            *slot = f < valid ? (*slot - mean) * scale : 0.0f;
+        }
+    }
+    __syncthreads();
+    if (m == 0) {
+        float total = 0.0f;
+        if (valid >= 2)
+            for (int i = 0; i < mels; ++i) total = total + dev_s[i];
+        *spread = valid >= 2 ? total / (float)mels : 0.0f;
+    }
+}
+
+hipError_t launch_log_mel(const FrontendParams& p, const float* samples, int n, float* data, float* spread,
+                          hipStream_t stream) {
+    if (n < 0 || p.mels < 1 || p.mels > 256 || p.fft_size < 2 || p.fft_size > 4096 || p.hop < 1)
+        return hipErrorInvalidValue;
+    const int frames = n / p.hop + 1, valid = n / p.hop;
+    const size_t lds = sizeof(float) * (2 * (size_t)p.fft_size + p.fft_size / 2 + 1);
+    rn_launch(log_mel_kernel, dim3(frames), dim3(256), lds, stream, p, samples, n, data);
+    rn_launch(normalise_mels_kernel, dim3(1), dim3(256), 0, stream, data, frames, valid, p.mels, spread);
     return hipGetLastError();
 }
 
