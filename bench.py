@@ -243,6 +243,22 @@ def bench_codebook(rn, shapes=((2, 128, 2048, 512), (2, 128, 2097152, 512), (4, 
     return out
 
 
+def bench_frontend(rn, seconds: int = 30, reps: int = 5):
+    """The speech front end over a 30 s, 16 kHz input (3001 frames of 80 mels,
+    FFT 512, window 400, hop 160): wall time of rn_frontend_log_mel including
+    the sample upload and feature download (the kernels alone are in the trace)."""
+    n = 16000 * seconds
+    x = rn.synth_normal(rn.SEED, "bench.frontend", 0.1, (n,))
+    f = rn.Frontend(80, 512, 400, 160, rn.synthetic_mel_filters(80, 512))
+    f.log_mel(x)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        f.log_mel(x)
+        times.append(time.perf_counter() - t0)
+    return dict(samples=n, frames=n // 160 + 1, ms_with_transfers=min(times) * 1e3)
+
+
 def bench_whistle(rn, reps: int = 3, steps: int = 48, with_cpu: bool = True):
     """The speech path: encode of a 3000-frame mel window (stem, 6 encoder
     layers over 1500 frames, the cross memory of 4 decoder layers), then a
@@ -336,7 +352,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="decode only")
-    ap.add_argument("--extras", default="gemv,prefill_256,decode_batch64,whistle,codebook",
+    ap.add_argument("--extras", default="gemv,prefill_256,decode_batch64,whistle,codebook,frontend",
                     help="comma-separated secondary measurements to run")
     ap.add_argument("--profile-steps", type=int, default=DECODE_TOKENS,
                     help="greedy steps timed kernel by kernel for the roofline")
@@ -372,7 +388,8 @@ def main() -> int:
                          ("prefill_256", lambda: bench_prefill(rn, model, cfg)),
                          ("decode_batch64", lambda: bench_batch(rn, model, cfg)),
                          ("whistle", lambda: bench_whistle(rn, with_cpu=not args.no_cpu)),
-                         ("codebook", lambda: bench_codebook(rn))):
+                         ("codebook", lambda: bench_codebook(rn)),
+                         ("frontend", lambda: bench_frontend(rn))):
             if name not in wanted:
                 continue
             log(f"bench: {name}")

@@ -1032,7 +1032,7 @@ int rn_frontend_log_mel(rn_frontend* f, const float* samples, int n, float* feat
     const int nf = n / f->p.hop + 1;
     const size_t fb = sizeof(float) * (size_t)nf * f->p.mels;
     char* dev = nullptr;
-    RN_HIP(hipMalloc(&dev, align_up(sizeof(float) * (size_t)n + 4) + fb + 4));
+    RN_HIP(hipMalloc(&dev, align_up(sizeof(float) * (size_t)n + 4) + fb + 4 * (1 + (size_t)f->p.mels)));
     float* ds = (float*)dev;
     float* dd = (float*)(dev + align_up(sizeof(float) * (size_t)n + 4));
     float* dspread = (float*)((char*)dd + fb);

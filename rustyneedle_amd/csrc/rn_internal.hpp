@@ -276,7 +276,8 @@ struct FrontendParams {
     const float* twiddle_sin;
     const float* mel_weights;  // [fft_size / 2 + 1][mels]
 };
-// samples [n] -> data [n / hop + 1][mels] normalised, spread (device scalar)
+// samples [n] -> data [n / hop + 1][mels] normalised; spread[0] the spread,
+// spread[1 .. mels] scratch for the per-mel deviations
 hipError_t launch_log_mel(const FrontendParams& p, const float* samples, int n, float* data, float* spread,
                           hipStream_t stream);
 

@@ -877,39 +877,82 @@ __global__ __launch_bounds__(256) void log_mel_kernel(FrontendParams p, const fl
     }
 }
 
-// Frontend::spread and normalise (frontend.rs:104-133), one thread per mel: the
-// mean and squared deviations summed over the valid frames in order (from -0.0,
-// as Iterator::sum does), then the spread's per-mel deviations summed in mel
-// order by thread 0, and the normalised column (0 past the valid frames).
-__global__ __launch_bounds__(256) void normalise_mels_kernel(float* data, int frames, int valid, int mels,
-                                                             float* spread) {
-    __shared__ float dev_s[256];
-    const int m = threadIdx.x;
-    if (m < mels) {
-        float sum = -0.0f;
-        for (int f = 0; f < valid; ++f) sum = sum + data[(size_t)f * mels + m];
-        const float count = (float)(valid > 1 ? valid : 1);
-        const float mean = sum / count;  // = sum / valid whenever valid >= 1
-        float sq = -0.0f;
-        for (int f = 0; f < valid; ++f) {
-            const float d = data[(size_t)f * mels + m] - mean;
-            sq = sq + d * d;
+// Frontend::spread and normalise (frontend.rs:104-133), one wave per mel: the
+// wave stages the mel's column in LDS (4096 frames at a time, every load
+// independent), lane 0 adds the mean and the squared deviations over the valid
+// frames in order (from -0.0, as Iterator::sum does), and the wave writes the
+// normalised column (0 past the valid frames). dev[m] keeps the spread's
+// per-mel deviation for spread_kernel.
+constexpr int kColumnChunk = 4096;
+
+__global__ __launch_bounds__(64) void normalise_mels_kernel(float* data, int frames, int valid, int mels, float* dev) {
+    __shared__ __align__(16) float col_s[kColumnChunk];
+    __shared__ float stats_s[2];
+    const int lane = threadIdx.x, m = blockIdx.x;
+    auto column_sum = [&](float mean, bool squares) -> float {
+        float total = -0.0f;
+        for (int f0 = 0; f0 < valid; f0 += kColumnChunk) {
+            const int rows = min(kColumnChunk, valid - f0);
+            for (int r0 = 0; r0 < rows; r0 += 64 * 16) {  // sixteen loads in flight a lane
+                float t[16];
+#pragma unroll
+                for (int k = 0; k < 16; ++k) t[k] = data[(size_t)(f0 + min(r0 + 64 * k + lane, rows - 1)) * mels + m];
+#pragma unroll
+                for (int k = 0; k < 16; ++k)
+                    if (r0 + 64 * k + lane < rows) col_s[r0 + 64 * k + lane] = t[k];
+            }
+            __syncthreads();
+            if (squares) {  // the squared deviations in parallel; only their sum is sequential
+                for (int r = lane; r < rows; r += 64) {
+                    const float d = col_s[r] - mean;
+                    col_s[r] = d * d;
+                }
+                __syncthreads();
+            }
+            if (lane == 0) {
+                int r = 0;
+                for (; r + 16 <= rows; r += 16) {  // sixteen values read ahead, added in order
+                    float4 q[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) q[i] = reinterpret_cast<const float4*>(col_s + r)[i];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        total = total + q[i].x;
+                        total = total + q[i].y;
+                        total = total + q[i].z;
+                        total = total + q[i].w;
+                    }
+                }
+                for (; r < rows; ++r) total = total + col_s[r];
+            }
+            __syncthreads();
         }
-        if (valid >= 2) dev_s[m] = sqrtf(sq / (float)(valid - 1));
+        return total;
+    };
+    const float sum = column_sum(0.0f, false);
+    if (lane == 0) stats_s[0] = sum / (float)(valid > 1 ? valid : 1);  // = sum / valid whenever valid >= 1
+    __syncthreads();
+    const float mean = stats_s[0];
+    const float sq = column_sum(mean, true);
+    if (lane == 0) {
+        dev[m] = valid >= 2 ? sqrtf(sq / (float)(valid - 1)) : 0.0f;
         const float denominator = fmaxf((float)(valid > 1 ? valid : 1) - 1.0f, 1.0f);
-        const float scale = 1.0f / (sqrtf(sq / denominator) + 1e-5f);  // NORMALISER_EPSILON, frontend.rs:4
-        for (int f = 0; f < frames; ++f) {
-            float* slot = data + (size_t)f * mels + m;
-            *slot = f < valid ? (*slot - mean) * scale : 0.0f;
-        }
+        stats_s[1] = 1.0f / (sqrtf(sq / denominator) + 1e-5f);  // NORMALISER_EPSILON, frontend.rs:4
     }
     __syncthreads();
-    if (m == 0) {
-        float total = 0.0f;
-        if (valid >= 2)
-            for (int i = 0; i < mels; ++i) total = total + dev_s[i];
-        *spread = valid >= 2 ? total / (float)mels : 0.0f;
+    const float scale = stats_s[1];
+    for (int f = lane; f < frames; f += 64) {
+        float* slot = data + (size_t)f * mels + m;
+        *slot = f < valid ? (*slot - mean) * scale : 0.0f;
     }
+}
+
+// frontend.rs:110-115: the per-mel deviations added in mel order, over mels.
+__global__ void spread_kernel(const float* dev, int valid, int mels, float* spread) {
+    if (threadIdx.x != 0) return;
+    float total = 0.0f;
+    for (int i = 0; i < mels; ++i) total = total + dev[i];
+    *spread = valid >= 2 ? total / (float)mels : 0.0f;
 }
 
 hipError_t launch_log_mel(const FrontendParams& p, const float* samples, int n, float* data, float* spread,
@@ -919,7 +962,8 @@ hipError_t launch_log_mel(const FrontendParams& p, const float* samples, int n, 
     const int frames = n / p.hop + 1, valid = n / p.hop;
     const size_t lds = sizeof(float) * (2 * (size_t)p.fft_size + p.fft_size / 2 + 1);
     rn_launch(log_mel_kernel, dim3(frames), dim3(256), lds, stream, p, samples, n, data);
-    rn_launch(normalise_mels_kernel, dim3(1), dim3(256), 0, stream, data, frames, valid, p.mels, spread);
+    rn_launch(normalise_mels_kernel, dim3(p.mels), dim3(64), 0, stream, data, frames, valid, p.mels, spread + 1);
+    rn_launch(spread_kernel, dim3(1), dim3(64), 0, stream, spread + 1, valid, p.mels, spread);
     return hipGetLastError();
 }
 
