@@ -457,11 +457,13 @@ int rn_matrix_dequantise_row(const rn_matrix* m, int row, float* out) {
         return RN_OK;
     }
     const int G = m->columns / m->group;
-    std::vector<int8_t> codes(m->columns);
-    std::vector<float> scales(G);
-    RN_HIP(hipMemcpy(codes.data(), m->W + (size_t)row * m->columns, m->columns, hipMemcpyDeviceToHost));
-    RN_HIP(hipMemcpy(scales.data(), m->sW + (size_t)row * G, sizeof(float) * G, hipMemcpyDeviceToHost));
-    for (int k = 0; k < m->columns; ++k) out[k] = (float)codes[k] * scales[k / m->group];
+    float* dev = nullptr;
+    RN_HIP(hipMalloc(&dev, sizeof(float) * m->columns));
+    hipError_t e = launch_dequantise_i8(m->W + (size_t)row * m->columns, m->sW + (size_t)row * G, m->columns,
+                                        m->group, dev, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, dev, sizeof(float) * m->columns, hipMemcpyDeviceToHost);
+    (void)hipFree(dev);
+    RN_HIP(e);
     return RN_OK;
 }
 

@@ -268,6 +268,10 @@ hipError_t launch_codebook_rotate(const float* x, int count, int columns, int pa
                                   float* rotated, hipStream_t stream);
 hipError_t launch_codebook_dequantise(const CodebookParams& p, int row, float* out, hipStream_t stream);
 
+// One int8 row dequantised: out[k] = codes[k] * scales[k / group].
+hipError_t launch_dequantise_i8(const int8_t* codes, const float* scales, int columns, int group, float* out,
+                                hipStream_t stream);
+
 // The speech front end (frontend.rs): device tables built on the host.
 struct FrontendParams {
     int mels, fft_size, log2_size, window, hop;

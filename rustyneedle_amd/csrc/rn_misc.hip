@@ -119,6 +119,21 @@ hipError_t launch_fast_exp(const float* x, float* y, int n, int apply_silu, hipS
     return hipGetLastError();
 }
 
+// QuantisedMatrix::dequantise_row (matrix.rs:140-153) for int8 codes: code x
+// the scale of its group.
+__global__ void dequantise_i8_kernel(const int8_t* codes, const float* scales, int columns, int group, float* out) {
+    const int k = blockIdx.x * 256 + threadIdx.x;
+    if (k < columns) out[k] = (float)codes[k] * scales[k / group];
+}
+
+hipError_t launch_dequantise_i8(const int8_t* codes, const float* scales, int columns, int group, float* out,
+                                hipStream_t stream) {
+    if (columns < 1 || group < 1) return hipErrorInvalidValue;
+    rn_launch(dequantise_i8_kernel, dim3((columns + 255) / 256), dim3(256), 0, stream, codes, scales, columns, group,
+              out);
+    return hipGetLastError();
+}
+
 // The grammar-constrained choice of generator.rs:99-117 over n logits, one
 // 1024-thread block.
 //   1. Peaks (max is order-free: DPP within waves, then LDS), the greedy keys
