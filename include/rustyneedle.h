@@ -167,6 +167,14 @@ int rn_archive_tensor_bytes(const rn_archive* archive, int index, const uint8_t*
  * (rn_matrix_create_codebook with the record's shape, group and bits). */
 int rn_matrix_from_archive(const rn_archive* archive, int index, rn_matrix** out);
 
+/* ops::kronecker_apply (ops.rs:166-217), the factor product of the Hadamard MLP
+ * (hadamard.rs:100-106): out = L^T . X . R for each of `count` inputs X
+ * [32][32] (device pointers, [count][1024] in and out; L and R [32][32]). Only
+ * 32 x 32 factors: those the reference runs on its aarch64 path
+ * (ops.rs:220-297), whose fused multiply-adds in index order this follows. */
+int rn_kronecker_apply(const float* input, const float* left, int left_size, const float* right, int right_size,
+                       int count, float* output, void* stream);
+
 /* ops::quantise_int8 (ops.rs:112-118) for `count` rows of `columns` floats on
  * the device: codes [count][columns], scales [count]. */
 int rn_quantise_int8(const float* x, int count, int columns, int8_t* codes, float* scales, void* stream);

@@ -619,3 +619,15 @@ def log_mel(samples, mels: int, fft_size: int, window: int, hop: int, mel_weight
     lib.ro_log_mel(_ptr(x) if x.size else None, x.size, mels, fft_size, window, hop, _ptr(w), _ptr(data),
                    C.byref(valid), C.byref(spread))
     return data, valid.value, np.float32(spread.value)
+
+
+# ---- Kronecker apply (rn_hadamard.c) ----------------------------------------------
+lib.ro_kronecker_apply_32.argtypes = [_p, _p, _p, _p]
+
+
+def kronecker_apply_32(x, left, right) -> np.ndarray:
+    """ops.rs:220-297: L^T . X . R for 32 x 32 factors, fused multiply-adds in index order."""
+    x, left, right = _f32(x), _f32(left), _f32(right)
+    out = np.empty(1024, np.float32)
+    lib.ro_kronecker_apply_32(_ptr(x), _ptr(left), _ptr(right), _ptr(out))
+    return out

@@ -159,6 +159,9 @@ void ro_normalise(float* data, int frames, int valid, int mels);                
 int ro_log_mel(const float* samples, int n, int mels, int fft_size, int window, int hop, const float* mel_weights,
                float* data, int* valid, float* spread);                                                /* :72-102 */
 
+/* ---- Kronecker apply (rn_hadamard.c): ops.rs:220-297, 32 x 32 factors ---------- */
+void ro_kronecker_apply_32(const float* input, const float* left, const float* right, float* output);
+
 /* ---- grammar-constrained choice (rn_generate.c) ------------------------------ */
 int32_t ro_argmax_allowed(const float* values, const uint8_t* allowed, int n);   /* generator.rs:147-155 */
 void ro_allowed_statistics(const float* logits, const uint8_t* allowed, int n, int token, float* probability,

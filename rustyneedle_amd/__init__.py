@@ -138,6 +138,7 @@ SIGNATURES = {
     "rn_archive_tensor_bytes": (_i, [_p, _i, C.POINTER(C.POINTER(C.c_uint8)), C.POINTER(_sz)]),
     "rn_matrix_from_archive": (_i, [_p, _i, C.POINTER(_p)]),
     "rn_choose_allowed": (_i, [_p, _p, _i, _i, _p, _p]),
+    "rn_kronecker_apply": (_i, [_p, _p, _i, _p, _i, _i, _p, _p]),
     "rn_frontend_create": (_i, [_i, _i, _i, _i, _p, C.POINTER(_p)]),
     "rn_frontend_free": (_i, [_p]),
     "rn_frontend_log_mel": (_i, [_p, _p, _i, _p, C.POINTER(_i), C.POINTER(_i), C.POINTER(_f)]),
@@ -984,3 +985,13 @@ def synthetic_mel_filters(mels: int, fft_size: int, sample_rate: int = 16000) ->
         lo, c, hi = edges[m], edges[m + 1], edges[m + 2]
         w[:, m] = np.maximum(0.0, np.minimum((hz - lo) / (c - lo), (hi - hz) / (hi - c)))
     return w.astype(np.float32)
+
+
+def kronecker_apply(x: np.ndarray, left: np.ndarray, right: np.ndarray) -> np.ndarray:
+    """ops::kronecker_apply for 32 x 32 factors over inputs [count][1024]."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, 1024)
+    xd, ld, rd = (DeviceBuffer.from_array(np.ascontiguousarray(a, dtype=np.float32)) for a in (x, left, right))
+    od = DeviceBuffer(4 * x.size)
+    check(lib.rn_kronecker_apply(xd.ptr, ld.ptr, 32, rd.ptr, 32, x.shape[0], od.ptr, None))
+    check(lib.rn_stream_synchronize(None))
+    return od.download(np.float32, x.shape)

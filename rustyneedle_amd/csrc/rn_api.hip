@@ -1049,6 +1049,15 @@ int rn_frontend_log_mel(rn_frontend* f, const float* samples, int n, float* feat
     return RN_OK;
 }
 
+int rn_kronecker_apply(const float* input, const float* left, int left_size, const float* right, int right_size,
+                       int count, float* output, void* stream) {
+    RN_REQUIRE(input && left && right && output, "null argument");
+    RN_REQUIRE(left_size == 32 && right_size == 32, "factors must be 32 x 32 (got %d and %d)", left_size, right_size);
+    RN_REQUIRE(count >= 0, "count must be non-negative");
+    RN_HIP(launch_kronecker32(input, left, right, count, output, (hipStream_t)stream));
+    return RN_OK;
+}
+
 static_assert(sizeof(rn_choice) == sizeof(Choice), "rn_choice mirrors rn::Choice");
 
 int rn_choose_allowed(const float* logits, const uint8_t* allowed, int n, int token, rn_choice* out, void* stream) {

@@ -268,6 +268,10 @@ hipError_t launch_codebook_rotate(const float* x, int count, int columns, int pa
                                   float* rotated, hipStream_t stream);
 hipError_t launch_codebook_dequantise(const CodebookParams& p, int row, float* out, hipStream_t stream);
 
+// kronecker_apply for 32 x 32 factors over `count` inputs [count][1024].
+hipError_t launch_kronecker32(const float* input, const float* left, const float* right, int count, float* output,
+                              hipStream_t stream);
+
 // One int8 row dequantised: out[k] = codes[k] * scales[k / group].
 hipError_t launch_dequantise_i8(const int8_t* codes, const float* scales, int columns, int group, float* out,
                                 hipStream_t stream);

@@ -134,6 +134,40 @@ hipError_t launch_dequantise_i8(const int8_t* codes, const float* scales, int co
     return hipGetLastError();
 }
 
+// kronecker_apply (ops.rs:166-217) for 32 x 32 factors, as the reference's
+// aarch64 path computes it (ops.rs:220-297): one 1024-thread block per input
+// [32][32]; thread (i, c) forms mixed[i][c] = sum over j of x[i][j] r[j][c]
+// with fused multiply-adds in j order, then thread (k, c) out[k][c] = sum over
+// i of l[i][k] mixed[i][c] with fused multiply-adds in i order. The input and
+// both factors are staged in LDS.
+__global__ __launch_bounds__(1024) void kronecker32_kernel(const float* input, const float* left, const float* right,
+                                                           float* output) {
+    __shared__ float x_s[1024], l_s[1024], r_s[1024], m_s[1024];
+    const int t = threadIdx.x, row = t >> 5, col = t & 31;
+    const float* x = input + (size_t)blockIdx.x * 1024;
+    x_s[t] = x[t];
+    l_s[t] = left[t];
+    r_s[t] = right[t];
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) acc = fmaf(r_s[j * 32 + col], x_s[row * 32 + j], acc);
+    m_s[t] = acc;
+    __syncthreads();
+    acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc = fmaf(m_s[i * 32 + col], l_s[i * 32 + row], acc);
+    output[(size_t)blockIdx.x * 1024 + t] = acc;
+}
+
+hipError_t launch_kronecker32(const float* input, const float* left, const float* right, int count, float* output,
+                              hipStream_t stream) {
+    if (count < 0) return hipErrorInvalidValue;
+    if (count == 0) return hipSuccess;
+    rn_launch(kronecker32_kernel, dim3(count), dim3(1024), 0, stream, input, left, right, output);
+    return hipGetLastError();
+}
+
 // The grammar-constrained choice of generator.rs:99-117 over n logits, one
 // 1024-thread block.
 //   1. Peaks (max is order-free: DPP within waves, then LDS), the greedy keys
