@@ -167,6 +167,28 @@ int rn_archive_tensor_bytes(const rn_archive* archive, int index, const uint8_t*
  * (rn_matrix_create_codebook with the record's shape, group and bits). */
 int rn_matrix_from_archive(const rn_archive* archive, int index, rn_matrix** out);
 
+/* ---- the multi-lane hyper-connection (crates/model/src/lanes.rs) ----------------
+ * LaneWeights::load (lanes.rs:31-45): the lane tensors a_pre/a_post/a_res
+ * [layers], b_pre/b_post [layers][lanes], b_res [layers][lanes][lanes] (host
+ * floats, copied) and the three codebook routing matrices (kept by reference:
+ * phi_pre and phi_post of layers x lanes rows, phi_res of layers x lanes^2
+ * rows, all over the lanes x width stream). lanes <= 16. */
+typedef struct rn_lanes rn_lanes;
+int rn_lanes_create(int lanes, int width, int layers, const float* a_pre, const float* a_post, const float* a_res,
+                    const float* b_pre, const float* b_post, const float* b_res, const rn_matrix* phi_pre,
+                    const rn_matrix* phi_post, const rn_matrix* phi_res, rn_lanes** out);
+int rn_lanes_free(rn_lanes* lanes);
+/* LaneWeights::route (lanes.rs:48-84) on device pointers: stream [lanes][width]
+ * -> input [width], post [lanes], residual [lanes][lanes]. unit_rms,
+ * fake_quantise_int8, prepare and the products follow the reference's order
+ * bit for bit; the gates (sigmoid) and sinkhorn_in_place use the device expf
+ * where the reference calls the host libm's. */
+int rn_lanes_route(rn_lanes* lanes, int layer, int slot, const float* stream, float* input, float* post,
+                   float* residual, void* stream_handle);
+/* LaneWeights::combine_into (lanes.rs:86-98): next [lanes][width]. */
+int rn_lanes_combine(const rn_lanes* lanes, const float* post, const float* residual, const float* stream,
+                     const float* block_delta, float* next, void* stream_handle);
+
 /* ops::kronecker_apply (ops.rs:166-217), the factor product of the Hadamard MLP
  * (hadamard.rs:100-106): out = L^T . X . R for each of `count` inputs X
  * [32][32] (device pointers, [count][1024] in and out; L and R [32][32]). Only

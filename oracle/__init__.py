@@ -631,3 +631,46 @@ def kronecker_apply_32(x, left, right) -> np.ndarray:
     out = np.empty(1024, np.float32)
     lib.ro_kronecker_apply_32(_ptr(x), _ptr(left), _ptr(right), _ptr(out))
     return out
+
+
+# ---- lanes hyper-connection (rn_lanes.c) ------------------------------------------
+lib.ro_unit_rms.argtypes = [_p, _i, _p]
+lib.ro_sinkhorn.argtypes = [_p, _i, _i]
+lib.ro_lanes_route_tail.argtypes = [_i, _i, _i, _i] + [_p] * 11
+lib.ro_lanes_combine.argtypes = [_i, _i] + [_p] * 5
+
+
+def unit_rms(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib.ro_unit_rms(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def sinkhorn(m, iterations: int = 20) -> np.ndarray:
+    m = _f32(m).copy()
+    lib.ro_sinkhorn(_ptr(m), int(round(m.size ** 0.5)), iterations)
+    return m
+
+
+def lanes_route(lanes, width, layer, slot, t, stream, phis):
+    """lanes.rs:48-84 with the routing matrices as OracleCodebookMatrix (t: dict of the lane tensors)."""
+    stream = _f32(stream).reshape(-1)
+    normalised = fake_quantise_int8(unit_rms(stream))
+    rotated = phis[0].prepare(normalised)
+    pre = phis[0].multiply_rotated(rotated)[0][layer * lanes:(layer + 1) * lanes].copy()
+    post = phis[1].multiply_rotated(rotated)[0][layer * lanes:(layer + 1) * lanes].copy()
+    residual = phis[2].multiply_rotated(rotated)[0][layer * lanes * lanes:(layer + 1) * lanes * lanes].copy()
+    a = {k: _f32(v) for k, v in t.items()}
+    inp = np.empty(width, np.float32)
+    lib.ro_lanes_route_tail(lanes, width, layer, slot, _ptr(a["a_pre"]), _ptr(a["a_post"]), _ptr(a["a_res"]),
+                            _ptr(a["b_pre"]), _ptr(a["b_post"]), _ptr(a["b_res"]), _ptr(stream), _ptr(pre),
+                            _ptr(post), _ptr(residual), _ptr(inp))
+    return inp, post, residual.reshape(lanes, lanes)
+
+
+def lanes_combine(lanes, width, post, residual, stream, delta) -> np.ndarray:
+    post, residual, stream, delta = _f32(post), _f32(residual), _f32(stream), _f32(delta)
+    out = np.empty((lanes, width), np.float32)
+    lib.ro_lanes_combine(lanes, width, _ptr(post), _ptr(residual), _ptr(stream), _ptr(delta), _ptr(out))
+    return out

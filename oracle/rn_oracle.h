@@ -162,6 +162,15 @@ int ro_log_mel(const float* samples, int n, int mels, int fft_size, int window, 
 /* ---- Kronecker apply (rn_hadamard.c): ops.rs:220-297, 32 x 32 factors ---------- */
 void ro_kronecker_apply_32(const float* input, const float* left, const float* right, float* output);
 
+/* ---- lanes hyper-connection (rn_lanes.c): crates/model/src/lanes.rs ------------ */
+void ro_unit_rms(const float* x, int n, float* out);                                   /* ops.rs:60-66 */
+void ro_sinkhorn(float* m, int size, int iterations);                                   /* ops.rs:198-217 */
+void ro_lanes_route_tail(int lanes, int width, int layer, int slot, const float* a_pre, const float* a_post,
+                         const float* a_res, const float* b_pre, const float* b_post, const float* b_res,
+                         const float* stream, const float* pre, float* post, float* residual, float* input);
+void ro_lanes_combine(int lanes, int width, const float* post, const float* residual, const float* stream,
+                      const float* delta, float* next);                                 /* lanes.rs:86-98 */
+
 /* ---- grammar-constrained choice (rn_generate.c) ------------------------------ */
 int32_t ro_argmax_allowed(const float* values, const uint8_t* allowed, int n);   /* generator.rs:147-155 */
 void ro_allowed_statistics(const float* logits, const uint8_t* allowed, int n, int token, float* probability,

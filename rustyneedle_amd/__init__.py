@@ -139,6 +139,10 @@ SIGNATURES = {
     "rn_matrix_from_archive": (_i, [_p, _i, C.POINTER(_p)]),
     "rn_choose_allowed": (_i, [_p, _p, _i, _i, _p, _p]),
     "rn_kronecker_apply": (_i, [_p, _p, _i, _p, _i, _i, _p, _p]),
+    "rn_lanes_create": (_i, [_i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, C.POINTER(_p)]),
+    "rn_lanes_free": (_i, [_p]),
+    "rn_lanes_route": (_i, [_p, _i, _i, _p, _p, _p, _p, _p]),
+    "rn_lanes_combine": (_i, [_p, _p, _p, _p, _p, _p, _p]),
     "rn_frontend_create": (_i, [_i, _i, _i, _i, _p, C.POINTER(_p)]),
     "rn_frontend_free": (_i, [_p]),
     "rn_frontend_log_mel": (_i, [_p, _p, _i, _p, C.POINTER(_i), C.POINTER(_i), C.POINTER(_f)]),
@@ -995,3 +999,41 @@ def kronecker_apply(x: np.ndarray, left: np.ndarray, right: np.ndarray) -> np.nd
     check(lib.rn_kronecker_apply(xd.ptr, ld.ptr, 32, rd.ptr, 32, x.shape[0], od.ptr, None))
     check(lib.rn_stream_synchronize(None))
     return od.download(np.float32, x.shape)
+
+
+class Lanes:
+    """LaneWeights (crates/model/src/lanes.rs) over three CodebookMatrix routing matrices."""
+
+    def __init__(self, lanes: int, width: int, layers: int, a_pre, a_post, a_res, b_pre, b_post, b_res,
+                 phi_pre: "CodebookMatrix", phi_post: "CodebookMatrix", phi_res: "CodebookMatrix"):
+        arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (a_pre, a_post, a_res, b_pre, b_post, b_res)]
+        h = _p()
+        check(lib.rn_lanes_create(lanes, width, layers, *[_ptr(a) for a in arrs], phi_pre.handle, phi_post.handle,
+                                  phi_res.handle, C.byref(h)))
+        self.handle = h.value
+        self.lanes, self.width = lanes, width
+        self._keep = (phi_pre, phi_post, phi_res)
+
+    def route(self, layer: int, slot: int, stream: np.ndarray):
+        """(input [width], post [lanes], residual [lanes][lanes])."""
+        x = np.ascontiguousarray(stream, dtype=np.float32).reshape(-1)
+        xd = DeviceBuffer.from_array(x)
+        ind, pd, rd = DeviceBuffer(4 * self.width), DeviceBuffer(4 * self.lanes), DeviceBuffer(4 * self.lanes ** 2)
+        check(lib.rn_lanes_route(self.handle, layer, slot, xd.ptr, ind.ptr, pd.ptr, rd.ptr, None))
+        check(lib.rn_stream_synchronize(None))
+        return (ind.download(np.float32, (self.width,)), pd.download(np.float32, (self.lanes,)),
+                rd.download(np.float32, (self.lanes, self.lanes)))
+
+    def combine(self, post, residual, stream, delta) -> np.ndarray:
+        bufs = [DeviceBuffer.from_array(np.ascontiguousarray(a, dtype=np.float32)) for a in (post, residual, stream, delta)]
+        nd = DeviceBuffer(4 * self.lanes * self.width)
+        check(lib.rn_lanes_combine(self.handle, *[b.ptr for b in bufs], nd.ptr, None))
+        check(lib.rn_stream_synchronize(None))
+        return nd.download(np.float32, (self.lanes, self.width))
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.rn_lanes_free(self.handle)
+        except Exception:
+            pass

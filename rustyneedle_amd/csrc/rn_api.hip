@@ -1049,6 +1049,117 @@ int rn_frontend_log_mel(rn_frontend* f, const float* samples, int n, float* feat
     return RN_OK;
 }
 
+// ---- the multi-lane hyper-connection (lanes.rs) -------------------------------------
+
+struct rn_lanes {
+    int lanes = 0, width = 0, layers = 0;
+    const rn_matrix* phi[3] = {nullptr, nullptr, nullptr};
+    float* buf = nullptr;  // a_pre, a_post, a_res, b_pre, b_post, b_res, then scratch
+    float *a_pre, *a_post, *a_res, *b_pre, *b_post, *b_res, *normalised, *rotated, *pre;
+};
+
+int rn_lanes_create(int lanes, int width, int layers, const float* a_pre, const float* a_post, const float* a_res,
+                    const float* b_pre, const float* b_post, const float* b_res, const rn_matrix* phi_pre,
+                    const rn_matrix* phi_post, const rn_matrix* phi_res, rn_lanes** out) {
+    RN_REQUIRE(a_pre && a_post && a_res && b_pre && b_post && b_res && phi_pre && phi_post && phi_res && out,
+               "null argument");
+    RN_REQUIRE(lanes >= 1 && lanes <= kMaxLanes, "lanes must be 1..%d (got %d)", kMaxLanes, lanes);
+    RN_REQUIRE(width >= 1 && layers >= 1 && (lanes * width) % 8 == 0 && lanes * width <= 49152,
+               "lanes * width must be a multiple of 8 up to 49152");
+    const rn_matrix* phis[3] = {phi_pre, phi_post, phi_res};
+    const int need[3] = {layers * lanes, layers * lanes, layers * lanes * lanes};
+    for (int i = 0; i < 3; ++i) {
+        RN_REQUIRE(phis[i]->bits != 0, "the routing matrices are codebook matrices");
+        RN_REQUIRE(phis[i]->columns == lanes * width, "routing matrix %d has %d columns, the stream %d", i,
+                   phis[i]->columns, lanes * width);
+        RN_REQUIRE(phis[i]->rows >= need[i], "routing matrix %d has %d rows, %d needed", i, phis[i]->rows, need[i]);
+        RN_REQUIRE(phis[i]->cb.padded == phi_pre->cb.padded && phis[i]->group == phi_pre->group,
+                   "the routing matrices share padded columns and group (multiply_fused)");
+    }
+    rn_lanes* l = new (std::nothrow) rn_lanes();
+    if (!l) return fail(RN_ERR_MEMORY, "out of host memory");
+    const size_t nA = layers, nB = (size_t)layers * lanes, nR = (size_t)layers * lanes * lanes;
+    const size_t n = (size_t)lanes * width, padded = (size_t)phi_pre->cb.padded;
+    const size_t total = 3 * nA + 2 * nB + nR + n + padded + lanes;
+    if (hipMalloc(&l->buf, sizeof(float) * total) != hipSuccess) {
+        delete l;
+        return fail(RN_ERR_MEMORY, "device allocation failed");
+    }
+    float* p = l->buf;
+    l->a_pre = p; p += nA;
+    l->a_post = p; p += nA;
+    l->a_res = p; p += nA;
+    l->b_pre = p; p += nB;
+    l->b_post = p; p += nB;
+    l->b_res = p; p += nR;
+    l->normalised = p; p += n;
+    l->rotated = p; p += padded;
+    l->pre = p;
+    const std::pair<float*, const float*> up[6] = {{l->a_pre, a_pre}, {l->a_post, a_post}, {l->a_res, a_res},
+                                                   {l->b_pre, b_pre}, {l->b_post, b_post}, {l->b_res, b_res}};
+    const size_t sizes[6] = {nA, nA, nA, nB, nB, nR};
+    for (int i = 0; i < 6; ++i)
+        if (hipMemcpy(up[i].first, up[i].second, sizeof(float) * sizes[i], hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipFree(l->buf);
+            delete l;
+            return fail(RN_ERR_DEVICE, "upload of the lane tensors failed");
+        }
+    l->lanes = lanes;
+    l->width = width;
+    l->layers = layers;
+    l->phi[0] = phi_pre;
+    l->phi[1] = phi_post;
+    l->phi[2] = phi_res;
+    *out = l;
+    return RN_OK;
+}
+
+int rn_lanes_free(rn_lanes* l) {
+    if (!l) return RN_OK;
+    (void)hipFree(l->buf);
+    delete l;
+    return RN_OK;
+}
+
+// LaneWeights::route (lanes.rs:48-84): unit_rms + fake_quantise_int8 of the
+// stream, prepare with phi_pre, the three products over this layer's rows
+// (multiply_fused, matrix.rs:167-193, one launch each), then the gates, the
+// post gains and the Sinkhorn-normalised residual mix.
+int rn_lanes_route(rn_lanes* l, int layer, int slot, const float* stream, float* input, float* post, float* residual,
+                   void* stream_handle) {
+    RN_REQUIRE(l && stream && input && post && residual, "null argument");
+    RN_REQUIRE(layer >= 0 && layer < l->layers, "layer %d out of range [0, %d)", layer, l->layers);
+    RN_REQUIRE(slot >= 0, "slot must be non-negative");
+    hipStream_t s = (hipStream_t)stream_handle;
+    const int L = l->lanes, n = L * l->width;
+    RN_HIP(launch_lanes_prologue(stream, n, l->normalised, s));
+    const rn_matrix* pre_m = l->phi[0];
+    RN_HIP(launch_codebook_rotate(l->normalised, 1, n, pre_m->cb.padded, pre_m->group, pre_m->cb.wht_scale, l->rotated,
+                                  s));
+    float* outs[3] = {l->pre, post, residual};
+    const int first[3] = {layer * L, layer * L, layer * L * L}, count[3] = {L, L, L * L};
+    for (int i = 0; i < 3; ++i) {  // a row range of the matrix: the same blob from its first row
+        CodebookParams v = l->phi[i]->cb;
+        const int G = v.padded / v.group;
+        v.packed += (size_t)first[i] * v.row_bytes;
+        v.norms += (size_t)first[i] * G;
+        v.rows = count[i];
+        RN_HIP(launch_codebook_product(v, l->rotated, 1, outs[i], nullptr, s));
+    }
+    LanesRouteParams p{L, l->width, layer, slot, l->a_pre, l->a_post, l->a_res, l->b_pre, l->b_post, l->b_res,
+                       stream, l->pre, post, residual, input};
+    RN_HIP(launch_lanes_route(p, s));
+    return RN_OK;
+}
+
+int rn_lanes_combine(const rn_lanes* l, const float* post, const float* residual, const float* stream,
+                     const float* block_delta, float* next, void* stream_handle) {
+    RN_REQUIRE(l && post && residual && stream && block_delta && next, "null argument");
+    RN_HIP(launch_lanes_combine(l->lanes, l->width, post, residual, stream, block_delta, next,
+                                (hipStream_t)stream_handle));
+    return RN_OK;
+}
+
 int rn_kronecker_apply(const float* input, const float* left, int left_size, const float* right, int right_size,
                        int count, float* output, void* stream) {
     RN_REQUIRE(input && left && right && output, "null argument");

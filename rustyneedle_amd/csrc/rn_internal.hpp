@@ -268,6 +268,27 @@ hipError_t launch_codebook_rotate(const float* x, int count, int columns, int pa
                                   float* rotated, hipStream_t stream);
 hipError_t launch_codebook_dequantise(const CodebookParams& p, int row, float* out, hipStream_t stream);
 
+// The multi-lane hyper-connection (lanes.rs): route after the three products.
+constexpr int kMaxLanes = 16;
+struct LanesRouteParams {
+    int lanes, width, layer, slot;
+    const float* a_pre;    // [layers]
+    const float* a_post;
+    const float* a_res;
+    const float* b_pre;    // [layers][lanes]
+    const float* b_post;
+    const float* b_res;    // [layers][lanes][lanes]
+    const float* stream;   // [lanes][width]
+    const float* pre;      // [lanes] the phi_pre rows of this layer
+    float* post;           // [lanes] in: the phi_post rows; out: the post gains
+    float* residual;       // [lanes][lanes] in: the phi_res rows; out: the Sinkhorn mix
+    float* input;          // [width]
+};
+hipError_t launch_lanes_prologue(const float* stream, int n, float* out, hipStream_t s);
+hipError_t launch_lanes_route(const LanesRouteParams& p, hipStream_t s);
+hipError_t launch_lanes_combine(int lanes, int width, const float* post, const float* residual, const float* stream,
+                                const float* delta, float* next, hipStream_t s);
+
 // kronecker_apply for 32 x 32 factors over `count` inputs [count][1024].
 hipError_t launch_kronecker32(const float* input, const float* left, const float* right, int count, float* output,
                               hipStream_t stream);

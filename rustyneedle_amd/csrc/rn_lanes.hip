@@ -1,0 +1,129 @@
+// rn_lanes.hip — the multi-lane hyper-connection of Needle 3 (crates/model/src/
+// lanes.rs) on gfx950: LaneWeights::route and combine_into around the three
+// codebook products of the routing matrices.
+//
+//   lanes_prologue_kernel: unit_rms of the whole stream (ops.rs:60-66, the
+//     eight-lane sum of squares of ops.rs:7-17) and fake_quantise_int8
+//     (ops.rs:120-125), one block;
+//   the products: rn_codebook.hip on row ranges of phi_pre, phi_post, phi_res;
+//   lanes_route_kernel: the gates (sigmoid, ops.rs:68-71), the gated input
+//     mix, the post gains, the residual mixing logits and sinkhorn_in_place
+//     (ops.rs:198-217), lanes.rs:62-83;
+//   lanes_combine_kernel: lanes.rs:86-98.
+// sigmoid and sinkhorn use expf, where the reference calls the host libm's.
+#include "rn_device.hpp"
+#include "rn_internal.hpp"
+
+namespace rn {
+
+constexpr int kLaneThreads = 256;
+
+__global__ __launch_bounds__(256) void lanes_prologue_kernel(const float* stream, int n, float* out) {
+    __shared__ float lanes_s[8];
+    __shared__ float peak_s[kLaneThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < 8) {  // ops.rs:7-17: lane j sums x[8c + j]^2 over c in order
+        float s = 0.0f;
+        for (int c = 0; c < n / 8; ++c) {
+            const float x = stream[8 * c + tid];
+            s = s + x * x;
+        }
+        lanes_s[tid] = s;
+    }
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) total = total + lanes_s[j];
+    total = total + 0.0f;  // the empty tail (n is a multiple of 8)
+    const float inverse = 1.0f / sqrtf(total / (float)n + 1e-6f);
+    float peak = 0.0f;
+    for (int i = tid; i < n; i += kLaneThreads) peak = fmaxf(peak, fabsf(stream[i] * inverse));
+    peak = wave_max(peak);
+    if (lane == 0) peak_s[wave] = peak;
+    __syncthreads();
+    peak = fmaxf(fmaxf(peak_s[0], peak_s[1]), fmaxf(peak_s[2], peak_s[3]));
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    for (int i = tid; i < n; i += kLaneThreads) {
+        float q = __builtin_rintf((stream[i] * inverse) / scale);
+        q = q < -128.0f ? -128.0f : (q > 127.0f ? 127.0f : q);
+        out[i] = q * scale;
+    }
+}
+
+__device__ __forceinline__ float sigmoid_exp(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+__global__ __launch_bounds__(256) void lanes_route_kernel(LanesRouteParams p) {
+    __shared__ float gate_s[kMaxLanes];
+    const int tid = threadIdx.x, L = p.lanes, own = p.slot % L;
+    if (tid == 0) {
+        for (int lane = 0; lane < L; ++lane) {
+            const float pre_offset = lane == own ? 8.0f + -4.0f : -4.0f;  // PRE_LANE_BOOST, PRE_LANE_FLOOR
+            gate_s[lane] = sigmoid_exp(p.a_pre[p.layer] * p.pre[lane] + p.b_pre[p.layer * L + lane] + pre_offset);
+            const float post_offset = lane == own ? 0.0f : -4.0f;  // POST_LANE_FLOOR
+            p.post[lane] = 2.0f * sigmoid_exp(p.a_post[p.layer] * p.post[lane] + p.b_post[p.layer * L + lane] +
+                                              post_offset);
+        }
+        float* m = p.residual;
+        const int base = p.layer * L * L;
+        for (int i = 0; i < L * L; ++i) m[i] = p.a_res[p.layer] * m[i] + p.b_res[base + i];
+        for (int r = 0; r < L; ++r) {  // ops.rs:199-202
+            float peak = -INFINITY;
+            for (int c = 0; c < L; ++c) peak = fmaxf(peak, m[r * L + c]);
+            for (int c = 0; c < L; ++c) m[r * L + c] = expf(m[r * L + c] - peak);
+        }
+        for (int it = 0; it < 20; ++it) {  // SINKHORN_ITERATIONS; sums fold from -0.0
+            for (int r = 0; r < L; ++r) {
+                float total = -0.0f;
+                for (int c = 0; c < L; ++c) total = total + m[r * L + c];
+                const float inv = 1.0f / fmaxf(total, 1.17549435e-38f);
+                for (int c = 0; c < L; ++c) m[r * L + c] = m[r * L + c] * inv;
+            }
+            for (int c = 0; c < L; ++c) {
+                float total = -0.0f;
+                for (int r = 0; r < L; ++r) total = total + m[r * L + c];
+                const float inv = 1.0f / fmaxf(total, 1.17549435e-38f);
+                for (int r = 0; r < L; ++r) m[r * L + c] = m[r * L + c] * inv;
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < p.width; i += kLaneThreads) {
+        float acc = 0.0f;
+        for (int lane = 0; lane < L; ++lane) acc = acc + gate_s[lane] * p.stream[(size_t)lane * p.width + i];
+        p.input[i] = acc;
+    }
+}
+
+__global__ __launch_bounds__(256) void lanes_combine_kernel(int lanes, int width, const float* post,
+                                                            const float* residual, const float* stream,
+                                                            const float* delta, float* next) {
+    const int idx = blockIdx.x * kLaneThreads + threadIdx.x;
+    if (idx >= lanes * width) return;
+    const int lane = idx / width, i = idx - lane * width;
+    float acc = 0.0f;
+    for (int source = 0; source < lanes; ++source) acc = acc + residual[lane * lanes + source] * stream[(size_t)source * width + i];
+    next[idx] = acc + post[lane] * delta[i];
+}
+
+hipError_t launch_lanes_prologue(const float* stream, int n, float* out, hipStream_t s) {
+    if (n < 8 || n % 8 != 0) return hipErrorInvalidValue;
+    rn_launch(lanes_prologue_kernel, dim3(1), dim3(kLaneThreads), 0, s, stream, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_lanes_route(const LanesRouteParams& p, hipStream_t s) {
+    if (p.lanes < 1 || p.lanes > kMaxLanes || p.width < 1) return hipErrorInvalidValue;
+    rn_launch(lanes_route_kernel, dim3(1), dim3(kLaneThreads), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_lanes_combine(int lanes, int width, const float* post, const float* residual, const float* stream,
+                                const float* delta, float* next, hipStream_t s) {
+    const long long n = (long long)lanes * width;
+    if (lanes < 1 || width < 1) return hipErrorInvalidValue;
+    rn_launch(lanes_combine_kernel, dim3((unsigned)((n + kLaneThreads - 1) / kLaneThreads)), dim3(kLaneThreads), 0, s,
+              lanes, width, post, residual, stream, delta, next);
+    return hipGetLastError();
+}
+
+}  // namespace rn
