@@ -13,8 +13,10 @@ single int8 matvec (2048 x 512) latency, a streaming int8 matvec over 512
 distinct 2048 x 512 matrices in one launch (609 MB, more than the 256 MB
 Infinity Cache: the HBM roofline of the product kernel), the speech path (encode
 of a 3000-frame mel window through the stem and 6 encoder layers plus the cross
-memory, then 48 greedy tokens of the 4-layer cross-attention decoder), and the
-CPU oracle on the host cores as the baseline.
+memory, then 48 greedy tokens of the 4-layer cross-attention decoder), the
+codebook-format matvecs (2-bit and 4-bit streams larger than the Infinity Cache,
+and the 2048 x 512 layer shape), the speech front end over 30 s of audio, and
+the CPU oracle on the host cores as the baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
