@@ -172,7 +172,9 @@ int rn_matrix_from_archive(const rn_archive* archive, int index, rn_matrix** out
  * [layers], b_pre/b_post [layers][lanes], b_res [layers][lanes][lanes] (host
  * floats, copied) and the three codebook routing matrices (kept by reference:
  * phi_pre and phi_post of layers x lanes rows, phi_res of layers x lanes^2
- * rows, all over the lanes x width stream). lanes <= 16. */
+ * rows, all over the lanes x width stream). lanes <= 16. An rn_lanes holds
+ * the scratch of its route (normalised and rotated stream, pre gains): calls
+ * on one rn_lanes must not overlap. */
 typedef struct rn_lanes rn_lanes;
 int rn_lanes_create(int lanes, int width, int layers, const float* a_pre, const float* a_post, const float* a_res,
                     const float* b_pre, const float* b_post, const float* b_res, const rn_matrix* phi_pre,
