@@ -191,6 +191,14 @@ int rn_lanes_route(rn_lanes* lanes, int layer, int slot, const float* stream, fl
 int rn_lanes_combine(const rn_lanes* lanes, const float* post, const float* residual, const float* stream,
                      const float* block_delta, float* next, void* stream_handle);
 
+/* ---- the depth ladder (crates/model/src/ladder.rs) -------------------------------
+ * ladder::order (ladder.rs:1-20): the order in which layers join as depth grows
+ * (host). ladder::select (ladder.rs:22-29): the sorted first `depth` of them;
+ * RN_ERR_ARGUMENT where the reference returns None (depth outside
+ * [min(2, layers), layers]). */
+int rn_ladder_order(int layers, int32_t* order);
+int rn_ladder_select(int layers, int depth, int32_t* chosen);
+
 /* ops::kronecker_apply (ops.rs:166-217), the factor product of the Hadamard MLP
  * (hadamard.rs:100-106): out = L^T . X . R for each of `count` inputs X
  * [32][32] (device pointers, [count][1024] in and out; L and R [32][32]). Only

@@ -139,6 +139,8 @@ SIGNATURES = {
     "rn_matrix_from_archive": (_i, [_p, _i, C.POINTER(_p)]),
     "rn_choose_allowed": (_i, [_p, _p, _i, _i, _p, _p]),
     "rn_kronecker_apply": (_i, [_p, _p, _i, _p, _i, _i, _p, _p]),
+    "rn_ladder_order": (_i, [_i, _p]),
+    "rn_ladder_select": (_i, [_i, _i, _p]),
     "rn_lanes_create": (_i, [_i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, C.POINTER(_p)]),
     "rn_lanes_free": (_i, [_p]),
     "rn_lanes_route": (_i, [_p, _i, _i, _p, _p, _p, _p, _p]),
@@ -1037,3 +1039,17 @@ class Lanes:
                 lib.rn_lanes_free(self.handle)
         except Exception:
             pass
+
+
+def ladder_order(layers: int) -> list:
+    """ladder::order (crates/model/src/ladder.rs:1-20)."""
+    out = np.empty(max(layers, 1), np.int32)
+    check(lib.rn_ladder_order(layers, _ptr(out)))
+    return out[:layers].tolist()
+
+
+def ladder_select(layers: int, depth: int):
+    """ladder::select (ladder.rs:22-29); None where the reference returns None."""
+    out = np.empty(max(depth, 1), np.int32)
+    rc = lib.rn_ladder_select(layers, depth, _ptr(out))
+    return None if rc == RN_ERR_ARGUMENT else out[:depth].tolist()

@@ -1160,6 +1160,52 @@ int rn_lanes_combine(const rn_lanes* l, const float* post, const float* residual
     return RN_OK;
 }
 
+// ---- the depth ladder (ladder.rs) ----------------------------------------------------
+
+// ladder::order (ladder.rs:1-20): the first and last layer, then repeatedly the
+// midpoint of the widest gap between chosen layers (the leftmost of equal gaps).
+int rn_ladder_order(int layers, int32_t* order) {
+    RN_REQUIRE(layers >= 0 && (order || layers == 0), "bad argument");
+    if (layers <= 1) {
+        for (int i = 0; i < layers; ++i) order[i] = i;
+        return RN_OK;
+    }
+    std::vector<int> selected = {0, layers - 1};
+    order[0] = 0;
+    order[1] = layers - 1;
+    for (int n = 2; n < layers; ++n) {
+        std::sort(selected.begin(), selected.end());
+        int best_gap = 0, best_left = 0, best_right = 0;
+        for (size_t i = 0; i + 1 < selected.size(); ++i) {
+            const int gap = selected[i + 1] - selected[i];
+            if (gap > 1 && gap > best_gap) {  // ties keep the leftmost (the larger Reverse(left))
+                best_gap = gap;
+                best_left = selected[i];
+                best_right = selected[i + 1];
+            }
+        }
+        const int candidate = (best_left + best_right) / 2;
+        selected.push_back(candidate);
+        order[n] = candidate;
+    }
+    return RN_OK;
+}
+
+// ladder::select (ladder.rs:22-29): the first `depth` layers of the order, sorted;
+// RN_ERR_ARGUMENT where the reference returns None.
+int rn_ladder_select(int layers, int depth, int32_t* chosen) {
+    RN_REQUIRE(chosen || depth == 0, "null argument");
+    RN_REQUIRE(layers >= 0, "layers must be non-negative");
+    if (depth < std::min(2, layers) || depth > layers)
+        return fail(RN_ERR_ARGUMENT, "depth %d outside [%d, %d]", depth, std::min(2, layers), layers);
+    std::vector<int32_t> order(layers);
+    const int rc = rn_ladder_order(layers, order.data());
+    if (rc != RN_OK) return rc;
+    std::copy(order.begin(), order.begin() + depth, chosen);
+    std::sort(chosen, chosen + depth);
+    return RN_OK;
+}
+
 int rn_kronecker_apply(const float* input, const float* left, int left_size, const float* right, int right_size,
                        int count, float* output, void* stream) {
     RN_REQUIRE(input && left && right && output, "null argument");
