@@ -99,6 +99,24 @@ int rn_matrix_multiply_fused(const rn_matrix* const* ms, int count, const float*
 int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, float* y, int32_t* acc,
                              void* stream);
 
+/* Host-slice forms, with the reference's signatures: the input slice is host
+ * memory, the output slice host memory the call fills before it returns.
+ * Each copies the input to a staging buffer the matrix owns, runs the device
+ * entry point above on the matrix's own stream, copies the output back and
+ * synchronises; calls on one matrix from several threads are serialised
+ * (QuantisedMatrix is Send + Sync). The staging buffer is allocated on the
+ * first call and grown as needed.
+ *   QuantisedMatrix::multiply_vector(&self, rotated: &[f32], output: &mut [f32])
+ *     (matrix.rs:155-165): x [padded columns], y [rows].
+ *   QuantisedMatrix::multiply_batch(&self, rotated: &[f32], count, output: &mut [f32])
+ *     (matrix.rs:330-389): x [count][padded columns], y [count][rows].
+ *   QuantisedMatrix::prepare_batch (matrix.rs:123-138), codebook matrices:
+ *     x [count][columns] -> rotated [count][padded columns].
+ * For int8 matrices the padded columns are the columns. */
+int rn_matrix_multiply_vector_host(const rn_matrix* m, const float* x, float* y);
+int rn_matrix_multiply_batch_host(const rn_matrix* m, const float* x, int count, float* y);
+int rn_matrix_prepare_host(const rn_matrix* m, const float* x, int count, float* rotated);
+
 /* QuantisedMatrix::dequantise_row (matrix.rs:140-153) for int8 codes: out[k] =
  * code * scale(group of k); for codebook matrices (level[index] * norm) then
  * the Walsh-Hadamard transform of each group, on the device. Host output of
@@ -352,6 +370,12 @@ int rn_batch_set_cache(rn_batch* batch, int sequence, int length, const uint16_t
 int rn_batch_decode_greedy(rn_batch* batch, const uint32_t* first, int steps, uint32_t* ids);
 /* Per-sequence rn_session_truncate: lengths [count], each <= its current length. */
 int rn_batch_truncate(rn_batch* batch, const int32_t* lengths);
+/* Session::logits (session.rs:166-177) of every sequence after the last
+ * decoded step: out [count][vocab] (host). RN_ERR_STATE before any step. */
+int rn_batch_logits(const rn_batch* batch, float* out);
+/* rn_session_get_cache for one sequence: the first `length` (<= its length)
+ * cached positions, [layers][heads][length][head_dim] fp16 bits (host out). */
+int rn_batch_get_cache(const rn_batch* batch, int sequence, int length, uint16_t* keys, uint16_t* values);
 int rn_batch_stream(const rn_batch* batch, void** stream);
 
 /* ---- Whistle-style speech path (crates/whistle) -------------------------------- */

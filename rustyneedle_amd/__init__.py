@@ -126,6 +126,9 @@ SIGNATURES = {
     "rn_matrix_multiply_fused": (_i, [C.POINTER(_p), _i, _p, C.POINTER(_p), _p]),
     "rn_matrix_multiply_batch": (_i, [_p, _p, _i, _p, _p, _p]),
     "rn_matrix_dequantise_row": (_i, [_p, _i, _p]),
+    "rn_matrix_multiply_vector_host": (_i, [_p, _p, _p]),
+    "rn_matrix_multiply_batch_host": (_i, [_p, _p, _i, _p]),
+    "rn_matrix_prepare_host": (_i, [_p, _p, _i, _p]),
     "rn_matrix_create_codebook": (_i, [_p, _sz, _i, _i, _i, _i, _p, _i, C.POINTER(_p)]),
     "rn_matrix_padded_columns": (_i, [_p, C.POINTER(_i)]),
     "rn_matrix_prepare": (_i, [_p, _p, _i, _p, _p]),
@@ -179,6 +182,8 @@ SIGNATURES = {
     "rn_batch_decode_greedy": (_i, [_p, _p, _i, _p]),
     "rn_batch_stream": (_i, [_p, C.POINTER(_p)]),
     "rn_batch_truncate": (_i, [_p, _p]),
+    "rn_batch_logits": (_i, [_p, _p]),
+    "rn_batch_get_cache": (_i, [_p, _i, _i, _p, _p]),
     "rn_whistle_create_synthetic": (_i, [C.POINTER(WhistleConfig), _u64, C.POINTER(_p)]),
     "rn_whistle_free": (_i, [_p]),
     "rn_whistle_frames": (_i, [_p, C.POINTER(_i)]),
@@ -849,6 +854,20 @@ class Batch:
         lengths = np.ascontiguousarray(lengths, dtype=np.int32)
         assert lengths.size == self.count
         check(lib.rn_batch_truncate(self.handle, _ptr(lengths)))
+
+    def logits(self) -> np.ndarray:
+        """The last decoded step's logits of every sequence, [count][vocab]."""
+        out = np.empty((self.count, self.model.config["vocab"]), dtype=np.float32)
+        check(lib.rn_batch_logits(self.handle, _ptr(out)))
+        return out
+
+    def get_cache(self, sequence: int, length: int):
+        c = self.model.config
+        shape = (c["layers"], c["heads"], length, c["head_dim"])
+        k = np.empty(shape, dtype=np.uint16)
+        v = np.empty(shape, dtype=np.uint16)
+        check(lib.rn_batch_get_cache(self.handle, sequence, length, _ptr(k), _ptr(v)))
+        return k.view(np.float16), v.view(np.float16)
 
     def stream(self) -> int:
         p = _p()

@@ -20,6 +20,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -94,6 +95,12 @@ struct rn_matrix {
     int bits = 0;                  // 0: int8 codes; 2, 4 or 5 (ternary): codebook indices
     unsigned char* blob = nullptr;  // codebook blob: packed indices, fp16 norms, padding
     CodebookParams cb{};
+    // staging of the host-slice entry points: a stream and a device buffer for
+    // the input and output slices, made on first use; calls hold the mutex
+    mutable std::mutex host_mu;
+    mutable hipStream_t host_stream = nullptr;
+    mutable char* host_buf = nullptr;
+    mutable size_t host_bytes = 0;
 };
 
 struct rn_model {
@@ -149,6 +156,7 @@ struct rn_batch {
     int32_t* error = nullptr;
     uint32_t* ids = nullptr;
     int ids_steps = 0;
+    bool has_logits = false;
 };
 
 // ------------------------------------------------------------------------------
@@ -336,6 +344,11 @@ int rn_matrix_create_codebook(const uint8_t* blob, size_t blob_bytes, int rows, 
 
 int rn_matrix_free(rn_matrix* m) {
     if (!m) return RN_OK;
+    if (m->host_stream) {
+        (void)hipStreamSynchronize(m->host_stream);
+        (void)hipStreamDestroy(m->host_stream);
+    }
+    (void)hipFree(m->host_buf);
     (void)hipFree(m->W);
     (void)hipFree(m->sW);
     (void)hipFree(m->blob);
@@ -441,6 +454,79 @@ int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, floa
     hipError_t f = hipFreeAsync(scratch, s);
     RN_HIP(e);
     RN_HIP(f);
+    return RN_OK;
+}
+
+// ---- host-slice products (the reference's &[f32] / &mut [f32] signatures) -------
+// The input slice is copied to the matrix's staging buffer, the device entry
+// point runs on the matrix's own stream, the output is copied back and the
+// stream is synchronised before returning. Caller holds m->host_mu.
+static int host_stage(const rn_matrix* m, size_t in_bytes, size_t out_bytes, float** din, float** dout) {
+    const size_t need = align_up(in_bytes) + align_up(out_bytes);
+    if (!m->host_stream) RN_HIP(hipStreamCreateWithFlags(&m->host_stream, hipStreamNonBlocking));
+    if (need > m->host_bytes) {
+        RN_HIP(hipStreamSynchronize(m->host_stream));
+        if (m->host_buf) RN_HIP(hipFree(m->host_buf));
+        m->host_buf = nullptr;
+        m->host_bytes = 0;
+        if (hipMalloc(&m->host_buf, need) != hipSuccess)
+            return fail(RN_ERR_MEMORY, "staging buffer of %zu bytes", need);
+        m->host_bytes = need;
+    }
+    *din = (float*)m->host_buf;
+    *dout = (float*)(m->host_buf + align_up(in_bytes));
+    return RN_OK;
+}
+
+static int matrix_width(const rn_matrix* m) { return m->bits ? m->cb.padded : m->columns; }
+
+int rn_matrix_multiply_vector_host(const rn_matrix* m, const float* x, float* y) {
+    RN_REQUIRE(m && x && y, "null argument");
+    std::lock_guard<std::mutex> lock(m->host_mu);
+    const size_t in = sizeof(float) * matrix_width(m), out = sizeof(float) * m->rows;
+    float *dx = nullptr, *dy = nullptr;
+    int rc = host_stage(m, in, out, &dx, &dy);
+    if (rc) return rc;
+    RN_HIP(hipMemcpyAsync(dx, x, in, hipMemcpyHostToDevice, m->host_stream));
+    rc = rn_matrix_multiply_vector(m, dx, dy, nullptr, m->host_stream);
+    if (rc) return rc;
+    RN_HIP(hipMemcpyAsync(y, dy, out, hipMemcpyDeviceToHost, m->host_stream));
+    RN_HIP(hipStreamSynchronize(m->host_stream));
+    return RN_OK;
+}
+
+int rn_matrix_multiply_batch_host(const rn_matrix* m, const float* x, int count, float* y) {
+    RN_REQUIRE(m && (count == 0 || (x && y)), "null argument");
+    RN_REQUIRE(count >= 0, "count must be non-negative");
+    if (count == 0) return RN_OK;
+    std::lock_guard<std::mutex> lock(m->host_mu);
+    const size_t in = sizeof(float) * (size_t)count * matrix_width(m), out = sizeof(float) * (size_t)count * m->rows;
+    float *dx = nullptr, *dy = nullptr;
+    int rc = host_stage(m, in, out, &dx, &dy);
+    if (rc) return rc;
+    RN_HIP(hipMemcpyAsync(dx, x, in, hipMemcpyHostToDevice, m->host_stream));
+    rc = rn_matrix_multiply_batch(m, dx, count, dy, nullptr, m->host_stream);
+    if (rc) return rc;
+    RN_HIP(hipMemcpyAsync(y, dy, out, hipMemcpyDeviceToHost, m->host_stream));
+    RN_HIP(hipStreamSynchronize(m->host_stream));
+    return RN_OK;
+}
+
+int rn_matrix_prepare_host(const rn_matrix* m, const float* x, int count, float* rotated) {
+    RN_REQUIRE(m && (count == 0 || (x && rotated)), "null argument");
+    RN_REQUIRE(m->bits != 0, "int8 matrices take their input unrotated; prepare applies to codebook matrices");
+    RN_REQUIRE(count >= 0, "count must be non-negative");
+    if (count == 0) return RN_OK;
+    std::lock_guard<std::mutex> lock(m->host_mu);
+    const size_t in = sizeof(float) * (size_t)count * m->columns, out = sizeof(float) * (size_t)count * m->cb.padded;
+    float *dx = nullptr, *dy = nullptr;
+    int rc = host_stage(m, in, out, &dx, &dy);
+    if (rc) return rc;
+    RN_HIP(hipMemcpyAsync(dx, x, in, hipMemcpyHostToDevice, m->host_stream));
+    rc = rn_matrix_prepare(m, dx, count, dy, m->host_stream);
+    if (rc) return rc;
+    RN_HIP(hipMemcpyAsync(rotated, dy, out, hipMemcpyDeviceToHost, m->host_stream));
+    RN_HIP(hipStreamSynchronize(m->host_stream));
     return RN_OK;
 }
 
@@ -1578,7 +1664,31 @@ int rn_batch_decode_greedy(rn_batch* b, const uint32_t* first, int steps, uint32
     RN_HIP(hipMemcpyAsync(&err, b->error, 4, hipMemcpyDeviceToHost, b->stream));
     RN_HIP(hipStreamSynchronize(b->stream));
     for (int i = 0; i < b->count; ++i) b->lengths[i] += steps;
+    b->has_logits = true;
     if (err) return fail(RN_ERR_STATE, "device reported error flags 0x%x", err);
+    return RN_OK;
+}
+
+int rn_batch_logits(const rn_batch* b, float* out) {
+    RN_REQUIRE(b && out, "null argument");
+    if (!b->has_logits) return fail(RN_ERR_STATE, "no decode step has run on this batch");
+    RN_HIP(hipStreamSynchronize(b->stream));
+    RN_HIP(hipMemcpy(out, b->logits, sizeof(float) * (size_t)b->count * b->model->cfg.vocab, hipMemcpyDeviceToHost));
+    return RN_OK;
+}
+
+int rn_batch_get_cache(const rn_batch* b, int sequence, int length, uint16_t* keys, uint16_t* values) {
+    RN_REQUIRE(b && keys && values, "null argument");
+    RN_REQUIRE(sequence >= 0 && sequence < b->count, "sequence %d outside 0..%d", sequence, b->count);
+    RN_REQUIRE(length >= 0 && length <= b->lengths[sequence], "length %d outside 0..%d", length, b->lengths[sequence]);
+    if (length == 0) return RN_OK;
+    const rn_config& c = b->model->cfg;
+    const size_t seq = cache_elems(c, b->capacity) * sequence;
+    const size_t row = (size_t)length * c.head_dim * 2, pitch = (size_t)b->capacity * c.head_dim * 2;
+    const size_t heads = (size_t)c.layers * c.heads;
+    RN_HIP(hipStreamSynchronize(b->stream));
+    RN_HIP(hipMemcpy2D(keys, row, b->kc + seq, pitch, row, heads, hipMemcpyDeviceToHost));
+    RN_HIP(hipMemcpy2D(values, row, b->vc + seq, pitch, row, heads, hipMemcpyDeviceToHost));
     return RN_OK;
 }
 

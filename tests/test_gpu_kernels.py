@@ -108,6 +108,10 @@ def test_multiply_fused_matches_separate():
     (64, 4096, 512, rn.FORM_PANEL),
     (64, 512, 2048, rn.FORM_PANEL),
     (256, 1536, 512, rn.FORM_PANEL),
+    # the 256-token prefill shapes: fused gate/up, out and down
+    (256, 4096, 512, rn.FORM_PANEL),
+    (256, 512, 512, rn.FORM_PANEL),
+    (256, 512, 2048, rn.FORM_PANEL),
     (65, 1000, 512, rn.FORM_PLANE),
     (3, 64, 1024, rn.FORM_PLANE),
     (100, 1152, 384, rn.FORM_PANEL),

@@ -1,0 +1,100 @@
+"""The prefill and batched-decode workloads at full size against the oracle.
+
+The model is the 20-layer decoder (d_model 512, 8 heads of 64, FFN 2048,
+vocab 8192, int8 codes with per-32 scales, fp16 cache) the benchmark runs,
+with the benchmark's own seeded inputs:
+- prefill: one 256-token `feed` of ids U{0..8191} into an empty session
+  (crates/model/src/session.rs:56-70, crates/model/src/prefill.rs:10-99),
+  compared bit for bit (hidden state, logits, the whole cache) with the
+  oracle and with 256 single-token pushes on the GPU;
+- batched decode: 64 sequences with caches of U[32, 512] positions, 32 greedy
+  steps (crates/generate/src/generator.rs:199-265 per sequence), every id,
+  every sequence's final logits and a sample of the caches compared bit for
+  bit with the oracle run one sequence at a time.
+"""
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+
+import oracle
+import rustyneedle_amd as rn
+
+pytestmark = pytest.mark.gpu
+
+# oracle sessions run concurrently, one thread each (ctypes releases the GIL)
+WORKERS = 12
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def needle():
+    cfg = dict(rn.NEEDLE_DECODER)
+    w = rn.synthetic_weights(cfg)
+    return cfg, rn.Model(cfg, w), oracle.OracleModel(cfg, w)
+
+
+def test_prefill_256_tokens_full_model(needle):
+    cfg, gm, om = needle
+    tokens = rn.synth_tokens(rn.SEED, "prefill.tokens", cfg["vocab"], 256)
+    gs = gm.session(256)
+    gs.feed(tokens)
+    oracle.set_threads(WORKERS)
+    try:
+        os_ = om.session(256)
+        os_.feed(tokens)
+    finally:
+        oracle.set_threads(1)
+    assert len(gs) == os_.length == 256
+    assert np.array_equal(_bits(gs.hidden()), _bits(os_.hidden))
+    assert np.array_equal(_bits(gs.logits()), _bits(os_.logits()))
+    k, v = gs.get_cache()
+    assert np.array_equal(k.view(np.uint16), os_.keys)
+    assert np.array_equal(v.view(np.uint16), os_.values)
+    # the same positions one token at a time (the decode kernels) on the GPU
+    gp = gm.session(256)
+    for t in tokens:
+        gp.push(int(t))
+    assert np.array_equal(_bits(gp.hidden()), _bits(os_.hidden))
+    pk, pv = gp.get_cache()
+    assert np.array_equal(pk.view(np.uint16), os_.keys)
+    assert np.array_equal(pv.view(np.uint16), os_.values)
+
+
+def test_batch64_ragged_32_steps_full_model(needle):
+    cfg, gm, om = needle
+    count, steps = 64, 32
+    lengths = (rn.synth_tokens(rn.SEED, "batch.lengths", 481, count) + 32).astype(np.int32)
+    first = rn.synth_tokens(rn.SEED, "batch.first", cfg["vocab"], count)
+    assert lengths.min() >= 32 and lengths.max() <= 512
+    with ThreadPoolExecutor(WORKERS) as ex:
+        caches = list(ex.map(lambda i: rn.synthetic_cache(cfg, int(lengths[i]), f"batch.{i}"), range(count)))
+    b = rn.Batch(gm, count, int(lengths.max()) + steps)
+    for i in range(count):
+        b.set_cache(i, *caches[i])
+    ids = b.decode_greedy(first, steps)
+    logits = b.logits()
+
+    oracle.set_threads(1)
+
+    def run(i):
+        o = om.session(int(lengths[i]) + steps)
+        o.set_cache(*caches[i])
+        return o.greedy(int(first[i]), steps), o.logits(), o
+
+    with ThreadPoolExecutor(WORKERS) as ex:
+        ref = list(ex.map(run, range(count)))
+    bad = [i for i in range(count) if ids[i].tolist() != ref[i][0].tolist()]
+    assert not bad, f"sequences whose greedy ids differ from the oracle: {bad}"
+    bad = [i for i in range(count) if not np.array_equal(_bits(logits[i]), _bits(ref[i][1]))]
+    assert not bad, f"sequences whose final logits differ from the oracle: {bad}"
+    # caches: the shortest, the longest and two in between, all positions
+    for i in {int(np.argmin(lengths)), int(np.argmax(lengths)), 0, count - 1}:
+        n = int(lengths[i]) + steps
+        k, v = b.get_cache(i, n)
+        o = ref[i][2]
+        assert np.array_equal(k.view(np.uint16), o.keys[:, :, :n]), i
+        assert np.array_equal(v.view(np.uint16), o.values[:, :, :n]), i

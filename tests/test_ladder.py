@@ -28,3 +28,17 @@ def test_select():
     assert rn.ladder_select(8, 8) == list(range(8))
     assert rn.ladder_select(8, 1) is None and rn.ladder_select(8, 9) is None
     assert rn.ladder_select(1, 1) == [0] and rn.ladder_select(0, 0) == []
+
+
+def test_reference_known_answers():
+    """crates/model/tests/ladder.rs:3-29, the reference's own expected values."""
+    assert rn.ladder_order(20) == [0, 19, 9, 14, 4, 6, 11, 16, 2, 7, 12, 17, 1, 3, 5, 8, 10, 13, 15, 18]
+    assert rn.ladder_select(20, 2) == [0, 19]
+    assert rn.ladder_select(20, 4) == [0, 9, 14, 19]
+    assert rn.ladder_select(20, 8) == [0, 4, 6, 9, 11, 14, 16, 19]
+    assert rn.ladder_select(20, 12) == [0, 2, 4, 6, 7, 9, 11, 12, 14, 16, 17, 19]
+    assert rn.ladder_select(20, 20) == list(range(20))
+    assert rn.ladder_select(20, 1) is None and rn.ladder_select(20, 21) is None
+    eight, four = rn.ladder_select(8, 8), rn.ladder_select(8, 4)
+    assert all(layer in eight for layer in four)
+    assert rn.ladder_select(8, 2) == [0, 7]
