@@ -99,6 +99,19 @@ int rn_matrix_multiply_fused(const rn_matrix* const* ms, int count, const float*
 int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, float* y, int32_t* acc,
                              void* stream);
 
+/* rn_matrix_multiply_batch without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The input rows' int8 codes and scales go to a fixed scratch array that the
+ * library holds on each GPU until the process ends (4 MiB of codes + 4096
+ * scales): count <= 4096 and count * columns rounded up to 256 <= 4 MiB, or
+ * RN_ERR_ARGUMENT. Every call on one GPU shares that GPU's array, so calls
+ * whose work overlaps on one GPU (several streams, several threads) race;
+ * serialise them. Codebook matrices need no scratch and run as
+ * rn_matrix_multiply_batch. Device pointers, as rn_matrix_multiply_batch. */
+int rn_matrix_multiply_batch_noalloc(const rn_matrix* m, const float* x, int count, float* y, int32_t* acc,
+                                     void* stream);
+
 /* Host-slice forms, with the reference's signatures: the input slice is host
  * memory, the output slice host memory the call fills before it returns.
  * Each copies the input to a staging buffer the matrix owns, runs the device

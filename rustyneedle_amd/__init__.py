@@ -125,6 +125,7 @@ SIGNATURES = {
     "rn_matrix_multiply_vector": (_i, [_p, _p, _p, _p, _p]),
     "rn_matrix_multiply_fused": (_i, [C.POINTER(_p), _i, _p, C.POINTER(_p), _p]),
     "rn_matrix_multiply_batch": (_i, [_p, _p, _i, _p, _p, _p]),
+    "rn_matrix_multiply_batch_noalloc": (_i, [_p, _p, _i, _p, _p, _p]),
     "rn_matrix_dequantise_row": (_i, [_p, _i, _p]),
     "rn_matrix_multiply_vector_host": (_i, [_p, _p, _p]),
     "rn_matrix_multiply_batch_host": (_i, [_p, _p, _i, _p]),

@@ -159,6 +159,38 @@ struct rn_batch {
     bool has_logits = false;
 };
 
+// ---- the fixed scratch of rn_matrix_multiply_batch_noalloc ------------------------
+// The input rows' int8 codes (first kNoAllocCodeBytes bytes) and their scales
+// (kNoAllocTokens floats after them). One copy per GPU, at its own address,
+// held until the process ends. Host code never passes `scratch` itself to a
+// kernel: on the host the name is a stand-in, not a device address. It uses
+// the device address that hipGetSymbolAddress returns, looked up once per
+// device on the entry point's first call there.
+constexpr size_t kNoAllocCodeBytes = size_t(4) << 20;
+constexpr int kNoAllocTokens = 4096;
+static __device__ __align__(256) unsigned char scratch[kNoAllocCodeBytes + sizeof(float) * kNoAllocTokens];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // per device ordinal
+
+int scratch_address(void** out) {
+    int device = -1;
+    RN_HIP(hipGetDevice(&device));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if ((size_t)device >= g_scratch_ptr.size()) g_scratch_ptr.resize(device + 1, nullptr);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(RN_ERR_DEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return RN_OK;
+}
+}  // namespace
+
 // ------------------------------------------------------------------------------
 extern "C" {
 
@@ -432,6 +464,16 @@ int rn_matrix_multiply_fused(const rn_matrix* const* ms, int count, const float*
     return RN_OK;
 }
 
+// The int8 batch product once the input rows have a place for their codes:
+// per-row quantisation into xq / sx, then the i8 MFMA product.
+static hipError_t batch_product_i8(const rn_matrix* m, const float* x, int count, float* y, int32_t* acc, int8_t* xq,
+                                   float* sx, hipStream_t s) {
+    hipError_t e = launch_norm_quantise(x, nullptr, count, m->columns, 1e-6f, xq, sx, nullptr, s);
+    if (e != hipSuccess) return e;
+    GemmParams p{xq, sx, m->W, m->sW, count, m->rows, m->columns, y, m->rows, acc, 0};
+    return launch_gemm(p, kGemmStore, m->form, acc != nullptr, s);
+}
+
 int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, float* y, int32_t* acc, void* stream) {
     RN_REQUIRE(m && x && y, "null argument");
     RN_REQUIRE(count >= 0, "count must be non-negative");
@@ -444,16 +486,33 @@ int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, floa
     void* scratch = nullptr;
     const size_t codes = align_up((size_t)count * m->columns);
     RN_HIP(hipMallocAsync(&scratch, codes + sizeof(float) * (size_t)count, s));
-    int8_t* xq = (int8_t*)scratch;
-    float* sx = (float*)((char*)scratch + codes);
-    hipError_t e = launch_norm_quantise(x, nullptr, count, m->columns, 1e-6f, xq, sx, nullptr, s);
-    if (e == hipSuccess) {
-        GemmParams p{xq, sx, m->W, m->sW, count, m->rows, m->columns, y, m->rows, acc, 0};
-        e = launch_gemm(p, kGemmStore, m->form, acc != nullptr, s);
-    }
+    hipError_t e = batch_product_i8(m, x, count, y, acc, (int8_t*)scratch, (float*)((char*)scratch + codes), s);
     hipError_t f = hipFreeAsync(scratch, s);
     RN_HIP(e);
     RN_HIP(f);
+    return RN_OK;
+}
+
+int rn_matrix_multiply_batch_noalloc(const rn_matrix* m, const float* x, int count, float* y, int32_t* acc,
+                                     void* stream) {
+    RN_REQUIRE(m && x && y, "null argument");
+    RN_REQUIRE(count >= 0, "count must be non-negative");
+    if (count == 0) return RN_OK;
+    hipStream_t s = (hipStream_t)stream;
+    if (m->bits) {  // the codebook product quantises inside its kernel: no scratch
+        RN_HIP(launch_codebook_product(m->cb, x, count, y, acc, s));
+        return RN_OK;
+    }
+    const size_t codes = align_up((size_t)count * m->columns);
+    RN_REQUIRE(count <= kNoAllocTokens && codes <= kNoAllocCodeBytes,
+               "count %d x columns %d exceeds the fixed scratch (at most %d rows and %zu code bytes)", count,
+               m->columns, kNoAllocTokens, kNoAllocCodeBytes);
+    void* base = nullptr;
+    int rc = scratch_address(&base);
+    if (rc) return rc;
+    int8_t* xq = (int8_t*)base;
+    float* sx = (float*)((char*)base + kNoAllocCodeBytes);
+    RN_HIP(batch_product_i8(m, x, count, y, acc, xq, sx, s));
     return RN_OK;
 }
 
