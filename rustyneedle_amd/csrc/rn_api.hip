@@ -1040,12 +1040,12 @@ static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) 
             RN_PROFILED(RN_PROFILE_GATE_UP, launch_gemv(p, d, kNorm, kSilu, kPanel, rpb, (c.ffn + rpb / 2 - 1) / (rpb / 2), st));
         }
         {
+            // the 2048-wide input: four waves split the columns (quantise + product + residual)
             GemvParams p{};
             p.nseg = 1;
             p.seg[0] = Segment{L.down.W, L.down.sW, s->x, nullptr, d, 0};
             p.x = s->ffh;
-            const int rpb = gemv_rows_per_block(d, c.ffn, kResidual);
-            RN_PROFILED(RN_PROFILE_DOWN, launch_gemv(p, c.ffn, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
+            RN_PROFILED(RN_PROFILE_DOWN, launch_gemv_splitk(p, c.ffn, d, st));
         }
     }
     if (!greedy) {

@@ -251,6 +251,107 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     }
 }
 
+// The wide decode product (down, K 2048): four waves split the columns, so
+// each wave quantises and dots a quarter of the input (K / 256 values a lane)
+// instead of one wave doing the whole row; the per-row scale needs the peak
+// of all four quarters (one exchange through LDS). A lane owns one 16-code
+// chunk of one row per load; lane pairs join a 32-code group by DPP; the
+// group sums meet in LDS and lane r of wave 0 runs row r's sequential
+// epilogue over all K / 32 groups (tree T4), then the residual add.
+template <int K, int ROWS, int FORM>
+__global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
+    constexpr int W = 4;                  // waves
+    constexpr int KW = K / W;             // columns per wave
+    constexpr int G = K / kGroup;         // groups per row
+    constexpr int GW = KW / kGroup;       // groups per row and wave
+    constexpr int CW = KW / 16;           // 16-code chunks per row and wave
+    constexpr int NL = ROWS * CW / 64;    // loads per lane
+    constexpr int E = KW / 64;            // input values per lane
+    static_assert((ROWS * CW) % 64 == 0 && E % 4 == 0 && G % 4 == 0, "whole loads, float4 inputs, scale quads");
+    static_assert(ROWS <= 64, "one lane per row in the epilogue");
+    __shared__ __align__(16) int8_t xq_s[K];
+    __shared__ __align__(16) int acc_s[ROWS * G];
+    __shared__ float peak_s[W];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const Segment sg = p.seg[0];
+    const int r0 = (int)blockIdx.x * ROWS;
+    // load j of a lane: chunk (64 j + lane) % CW of row (64 j + lane) / CW, in this wave's columns
+    auto load_row = [&](int j) -> int { return (64 * j + lane) / CW; };
+    auto load_chunk = [&](int j) -> int { return (64 * j + lane) % CW; };
+
+    float v[E];
+    load_floats<E>(p.x + wave * KW + lane * E, v);
+    int4 w[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+        w[j] = *reinterpret_cast<const int4*>(sg.W + (size_t)min(r0 + load_row(j), sg.rows - 1) * K + wave * KW +
+                                              load_chunk(j) * 16);
+    const bool mine = wave == 0 && lane < ROWS && r0 + lane < sg.rows;
+    float4 sv[G / 4];
+    {
+        const float4* src = reinterpret_cast<const float4*>(sg.sW + (size_t)min(r0 + min(lane, ROWS - 1), sg.rows - 1) * G);
+        if (wave == 0) {
+#pragma unroll
+            for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // the row scale from the peak of all four quarters (ops.rs:103-118)
+    float peak = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
+    peak = wave_max(peak);
+    if (lane == 0) peak_s[wave] = peak;
+    __syncthreads();
+    peak = fmaxf(fmaxf(peak_s[0], peak_s[1]), fmaxf(peak_s[2], peak_s[3]));
+    const float sx = int8_scale_from_peak(peak);
+    float y[E];
+    quotients<E>(v, sx, y);
+#pragma unroll
+    for (int e = 0; e < E; ++e) xq_s[wave * KW + lane * E + e] = (int8_t)code_of_quotient(y[e]);
+    // the codes a lane dots were written by lanes of its own wave
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int4 xc = *reinterpret_cast<const int4*>(xq_s + wave * KW + load_chunk(j) * 16);
+        int part = dot16(w[j], xc, 0);
+        part = part + dpp_move<0xb1>(part);  // lane ^ 1 holds the other half of the group
+        if ((lane & 1) == 0) acc_s[load_row(j) * G + wave * GW + load_chunk(j) / 2] = part;
+    }
+    __syncthreads();
+    if (mine) {
+        const int4* arow = reinterpret_cast<const int4*>(acc_s + lane * G);
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < G / 4; ++i) {
+            const int4 a4 = arow[i];
+            const float a[4] = {(float)a4.x, (float)a4.y, (float)a4.z, (float)a4.w};
+            const float s[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if constexpr (FORM == kPanel)
+                    total = fmaf(a[k], s[k] * sx, total);  // panel.rs:184-188
+                else
+                    total = total + (a[k] * s[k]) * sx;    // neon.rs:180
+            }
+        }
+        const int r = r0 + lane;
+        sg.y[r] = (p.res != nullptr ? p.res[r] : sg.y[r]) + total;
+    }
+}
+
+hipError_t launch_gemv_splitk(const GemvParams& p, int columns, int rows, hipStream_t stream) {
+    if (columns == 2048) {
+        rn_launch((gemv_splitk_kernel<2048, 2, kPanel>), dim3((rows + 1) / 2), dim3(256), 0, stream, p);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+}
+
 __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long* keys, int nkeys,
                                                               const float* logits, DecodeState* st, uint32_t* ids) {
     __shared__ unsigned long long best_s[4];

@@ -97,6 +97,10 @@ hipError_t launch_gemv(const GemvParams& p, int columns, int prologue, int epilo
                        int rows_per_block, int blocks, hipStream_t stream);
 int gemv_rows_per_block(int rows, int columns, int epilogue);
 
+// The decode product with four waves splitting the columns (quantise prologue,
+// residual epilogue with p.res, panel form); columns 2048.
+hipError_t launch_gemv_splitk(const GemvParams& p, int columns, int rows, hipStream_t stream);
+
 // ---- attention --------------------------------------------------------------
 enum AttendMode { kAttendDecode = 0, kAttendPrefill = 1, kAttendRaw = 2 };
 
