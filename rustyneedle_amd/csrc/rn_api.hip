@@ -1542,7 +1542,7 @@ int rn_session_feed(rn_session* s, const uint32_t* tokens, int count) {
         ap.first = first;
         ap.out = A;
         ap.error = &s->state->error;
-        RN_HIP(launch_attend(ap, kAttendPrefill, c.heads, count, first + count, st));
+        RN_HIP(launch_attend_prefill(ap, c.heads, count, st));
         RN_HIP(launch_gemm(rows(A, nullptr, L.out, d, d, X, d, 0), kGemmResidual, kPanel, false, st));
         RN_HIP(launch_gemm(rows(X, L.norm_ffn, L.gate_up, 2 * f, d, F, f, f), kGemmSilu, kPanel, false, st));
         RN_HIP(launch_gemm(rows(F, nullptr, L.down, d, f, X, d, 0), kGemmResidual, kPanel, false, st));

@@ -327,6 +327,194 @@ hipError_t launch_attend(const AttendParams& p, int mode, int grid_x, int grid_y
     return hipGetLastError();
 }
 
+// Causal prefill attention over query tiles: one 256-thread block per (head,
+// QT consecutive queries), so each key and value row is read from L2 once per
+// tile instead of once per query. Rows go to LDS in chunks of 256 positions
+// (global_load_lds: no registers); the scores of the QT queries live in LDS
+// [QT][length]. The float order is the per-query kernel's: scores in tree T2
+// (4 lanes per key row, the row's 16 dims per lane reused for all QT
+// queries), peak, fast_exp weights, then the value sums in tree T3 (thread
+// (class j, 8 dims) walks positions j, j + 32, ... in order for every query),
+// classes added 0..31, one multiply by 1/total.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
+
+constexpr int kTileRows = 256;  // positions per staged chunk
+
+template <int QT>
+__global__ __launch_bounds__(256) void attend_prefill_tile_kernel(AttendParams p, int count) {
+    constexpr int NT = 256;
+    extern __shared__ float scores[];  // [QT][max length]
+    __shared__ __align__(16) __half k_s[kTileRows * kHeadDim];  // a chunk of key rows
+    __shared__ __align__(16) __half v_s[kTileRows * kHeadDim];  // a chunk of value rows
+    __shared__ float q_s[QT][kHeadDim];
+    __shared__ float total_s[QT][kClasses];
+    float(*part_s)[kClasses][kHeadDim] = reinterpret_cast<float(*)[kClasses][kHeadDim]>(k_s);
+    static_assert(QT * kClasses * kHeadDim * 4 <= kTileRows * kHeadDim * 2, "class sums fit in the key buffer");
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the last tiles attend the most positions: they go first
+    const int h = blockIdx.x, t0 = (gridDim.y - 1 - blockIdx.y) * QT;
+    const int stride = p.first + count;  // scores row pitch
+    const size_t base = ((size_t)p.layer * p.heads + h) * p.capacity * kHeadDim;
+    const __half* K = p.kc + base;
+    const __half* V = p.vc + base;
+    int len[QT];  // positions each query attends (0: a query past the end)
+#pragma unroll
+    for (int q = 0; q < QT; ++q) len[q] = t0 + q < count ? p.first + t0 + q + 1 : 0;
+    const int L = p.first + min(t0 + QT, count);  // rows the tile needs (t0 < count)
+
+    // a chunk of rows [c0, c0 + 256) of K or V into dst; rows past L repeat row L - 1
+    auto stage = [&](const __half* src, __half* dst, int c0) {
+#pragma unroll
+        for (int i = 0; i < kTileRows * 8 / NT; ++i) {
+            const int piece = NT * i + 64 * wave + lane, row = min(c0 + piece / 8, L - 1);
+            __builtin_amdgcn_global_load_lds((global_void*)(src + (size_t)row * kHeadDim + 8 * (piece % 8)),
+                                             (lds_void*)(dst + 8 * (NT * i + 64 * wave)), 16, 0, 0);
+        }
+    };
+    // the first chunks of keys and values are requested together
+    stage(K, k_s, 0);
+    stage(V, v_s, 0);
+    if (tid < QT * kHeadDim) {
+        const int q = tid / kHeadDim, d = tid % kHeadDim;
+        q_s[q][d] = p.q[(size_t)min(t0 + q, count - 1) * p.d_model + h * kHeadDim + d];
+    }
+
+    // 1. scores (T2): key row r of a pass in lanes 4 r .. 4 r + 3, 16 dims each
+    const int r = tid >> 2, li = tid & 3;
+    const float inverse_root = 1.0f / sqrtf((float)kHeadDim);
+    float qr[QT][16];  // this lane's 16 query dims of every query
+    for (int c0 = 0; c0 < L; c0 += kTileRows) {
+        if (c0 > 0) {
+            __syncthreads();  // the previous chunk is consumed
+            stage(K, k_s, c0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (c0 == 0) {
+#pragma unroll
+            for (int q = 0; q < QT; ++q)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) qr[q][i] = q_s[q][16 * li + i];
+        }
+        for (int pass = 0; pass < kTileRows && c0 + pass < L; pass += NT / 4) {
+            const int pp = c0 + pass + r;
+            const uint4* kr = reinterpret_cast<const uint4*>(k_s + (pass + r) * kHeadDim + 16 * li);
+            float k[16];
+            unpack8(kr[0], k);
+            unpack8(kr[1], k + 8);
+#pragma unroll
+            for (int q = 0; q < QT; ++q) {
+                float part[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) sum = sum + qr[q][4 * jj + i] * k[4 * jj + i];
+                    part[jj] = sum;
+                }
+                float sc = (part[0] + part[1]) + (part[2] + part[3]);
+                sc = sc + __int_as_float(dpp_move<0xb1>(__float_as_int(sc)));  // lane ^ 1
+                sc = sc + __int_as_float(dpp_move<0x4e>(__float_as_int(sc)));  // lane ^ 2
+                if (li == 0 && pp < len[q]) scores[q * stride + pp] = sc * inverse_root;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. peak (order-free) and the fast_exp weights: wave q serves query q
+    for (int q = wave; q < QT; q += NT / 64) {
+        const int n = len[q];
+        float m = -INFINITY;
+        for (int pp = lane; pp < n; pp += 64) m = fmaxf(m, scores[q * stride + pp]);
+        m = wave_max(m);
+        for (int pp = lane; pp < n; pp += 64) scores[q * stride + pp] = fast_exp(scores[q * stride + pp] - m);
+    }
+
+    // 3. weighted values (T3): thread (j, dg) walks positions j, j + 32, ... for every query
+    const int j = tid >> 3, dg = tid & 7;
+    float acc[QT][8];
+    float total[QT];
+#pragma unroll
+    for (int q = 0; q < QT; ++q) {
+        total[q] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[q][i] = 0.0f;
+    }
+    for (int c0 = 0; c0 < L; c0 += kTileRows) {
+        __syncthreads();  // weights written; the previous chunk is consumed
+        if (c0 > 0) {
+            stage(V, v_s, c0);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+        // positions every query of the tile attends, then the tile's last QT - 1
+        const int all = min(c0 + kTileRows, len[0]), end = min(c0 + kTileRows, L);
+        int pp = c0 + j;
+        for (; pp < all; pp += kClasses) {
+            float vv[8];
+            unpack8(*reinterpret_cast<const uint4*>(v_s + (pp - c0) * kHeadDim + 8 * dg), vv);
+#pragma unroll
+            for (int q = 0; q < QT; ++q) {
+                const float e = scores[q * stride + pp];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[q][i] = acc[q][i] + e * vv[i];
+                total[q] = total[q] + e;
+            }
+        }
+        for (; pp < end; pp += kClasses) {
+            float vv[8];
+            unpack8(*reinterpret_cast<const uint4*>(v_s + (pp - c0) * kHeadDim + 8 * dg), vv);
+#pragma unroll
+            for (int q = 0; q < QT; ++q) {
+                if (pp < len[q]) {
+                    const float e = scores[q * stride + pp];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[q][i] = acc[q][i] + e * vv[i];
+                    total[q] = total[q] + e;
+                }
+            }
+        }
+    }
+    // the key buffer becomes the class sums (its last readers passed the barrier above)
+#pragma unroll
+    for (int q = 0; q < QT; ++q) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part_s[q][j][8 * dg + i] = acc[q][i];
+        if (dg == 0) total_s[q][j] = total[q];
+    }
+    __syncthreads();
+    if (tid < QT * kHeadDim) {
+        const int q = tid / kHeadDim, d = tid % kHeadDim;
+        if (t0 + q < count) {
+            float o = 0.0f, t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kClasses; ++k) {
+                o = o + part_s[q][k][d];
+                t = t + total_s[q][k];
+            }
+            const float inverse = 1.0f / t;
+            p.out[(size_t)(t0 + q) * p.d_model + h * kHeadDim + d] = o * inverse;
+        }
+    }
+}
+
+// The tiled kernel holds the scores of QT queries over the whole length in LDS;
+// longer contexts take the per-query kernel.
+constexpr int kPrefillTileQueries = 4;
+constexpr int kPrefillTileMaxLength = 6144;
+
+hipError_t launch_attend_prefill(const AttendParams& p, int heads, int count, hipStream_t stream) {
+    if (count <= 0) return hipSuccess;
+    const int length = p.first + count;
+    if (length > kPrefillTileMaxLength) return launch_attend(p, kAttendPrefill, heads, count, length, stream);
+    const size_t lds = sizeof(float) * (size_t)kPrefillTileQueries * length;
+    const dim3 grid(heads, (count + kPrefillTileQueries - 1) / kPrefillTileQueries);
+    rn_launch(attend_prefill_tile_kernel<kPrefillTileQueries>, grid, dim3(256), lds, stream, p, count);
+    return hipGetLastError();
+}
+
 // Prefill rotary + append: one block per token, one thread per (head, pair).
 __global__ __launch_bounds__(256) void rope_append_kernel(const float* qkv, float* q_out, __half* kc, __half* vc,
                                                           int layer, int heads, int capacity, int d_model, int first,

@@ -129,6 +129,10 @@ struct AttendParams {
 hipError_t launch_attend(const AttendParams& p, int mode, int grid_x, int grid_y, int max_length,
                          hipStream_t stream);
 
+// Causal attention of `count` prefill tokens at positions first.. (q [count][d]
+// rotated, keys and values already appended): grid (heads, query tiles).
+hipError_t launch_attend_prefill(const AttendParams& p, int heads, int count, hipStream_t stream);
+
 // Batch-1 decode: norm + the q/k/v rows of each head + rotary + fp16 append +
 // attention, one block per head (grid = heads, d_model = 64 heads).
 struct QkvAttendParams {
