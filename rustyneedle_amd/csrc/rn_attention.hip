@@ -129,6 +129,20 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 512 ? 
         rows = p.stride;
     }
 
+    // the new q/k/v row and its rotary factors (decoding many sequences): requested
+    // before the cache rows, so that the query is ready when the keys arrive
+    float nq[2] = {0.0f, 0.0f}, nk[2] = {0.0f, 0.0f}, nv[2] = {0.0f, 0.0f}, rc = 0.0f, rsn = 0.0f;
+    if constexpr (MODE == kAttendDecode && POS_FIRST) {
+        if (tid < kHeadDim / 2) {
+            const float* row = p.qkv + (size_t)blockIdx.y * 3 * p.d_model + blockIdx.x * kHeadDim + tid;
+            nq[0] = row[0];
+            nq[1] = row[kHeadDim / 2];
+            nk[0] = row[p.d_model];
+            nk[1] = row[p.d_model + kHeadDim / 2];
+            nv[0] = row[2 * p.d_model];
+            nv[1] = row[2 * p.d_model + kHeadDim / 2];
+        }
+    }
     if constexpr (POS_FIRST) {
         pos = p.pos[(size_t)blockIdx.y * p.pos_stride];
         if (pos < 0 || pos >= p.capacity) {
@@ -136,6 +150,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 512 ? 
             return;
         }
         rows = pos > 0 ? pos : 1;  // the cached rows; the new one is served from LDS
+        if constexpr (MODE == kAttendDecode) {
+            if (tid < kHeadDim / 2) {
+                rc = p.rope_cos[(size_t)pos * (kHeadDim / 2) + tid];
+                rsn = p.rope_sin[(size_t)pos * (kHeadDim / 2) + tid];
+            }
+        }
     }
 
     // 1. cache loads, issued before anything that depends on the current token
@@ -169,15 +189,21 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 512 ? 
         const float* row = p.qkv + (size_t)b * 3 * p.d_model;
         if (tid < kHeadDim / 2) {  // ops.rs:131-141 rotate-half at `pos`
             const int i = tid, half = kHeadDim / 2;
-            const float c = p.rope_cos[(size_t)pos * half + i];
-            const float s = p.rope_sin[(size_t)pos * half + i];
-            const float qa = row[h * kHeadDim + i], qb = row[h * kHeadDim + i + half];
+            float c, s, qa, qb, ka, kb, va, vb;
+            if constexpr (POS_FIRST) {  // requested before the cache rows
+                c = rc, s = rsn, qa = nq[0], qb = nq[1], ka = nk[0], kb = nk[1], va = nv[0], vb = nv[1];
+            } else {
+                c = p.rope_cos[(size_t)pos * half + i];
+                s = p.rope_sin[(size_t)pos * half + i];
+                qa = row[h * kHeadDim + i], qb = row[h * kHeadDim + i + half];
+                ka = row[p.d_model + h * kHeadDim + i], kb = row[p.d_model + h * kHeadDim + i + half];
+                va = row[2 * p.d_model + h * kHeadDim + i], vb = row[2 * p.d_model + h * kHeadDim + i + half];
+            }
             q_s[i] = qa * c - qb * s;
             q_s[i + half] = qb * c + qa * s;
-            const float ka = row[p.d_model + h * kHeadDim + i], kb = row[p.d_model + h * kHeadDim + i + half];
             const __half k0 = __float2half_rn(ka * c - kb * s), k1 = __float2half_rn(kb * c + ka * s);
-            const __half v0 = __float2half_rn(row[2 * p.d_model + h * kHeadDim + i]);
-            const __half v1 = __float2half_rn(row[2 * p.d_model + h * kHeadDim + i + half]);
+            const __half v0 = __float2half_rn(va);
+            const __half v1 = __float2half_rn(vb);
             new_s[0][i] = k0;
             new_s[0][i + half] = k1;
             new_s[1][i] = v0;

@@ -389,12 +389,183 @@ __global__ __launch_bounds__(256) void gemm_chain_kernel(GemmParams p) {
         }
 }
 
+// ---- the panel GEMM: the tile's whole K panel in LDS ----------------------------
+//
+// The chain kernel's arithmetic (a 16 x 16 x 32 i8 MFMA per sub-tile and group,
+// folded into the lane's running totals in group order), with every operand
+// byte of the block requested at once: the BM token rows and BN weight rows of
+// all K columns, and the tile's weight scales, go straight to LDS
+// (global_load_lds_dwordx4, no registers), so a block waits for one memory
+// round trip instead of one per K chunk, then runs its group chains back to
+// back from LDS. Rows are padded by 16 bytes, so the 16 rows of an MFMA
+// fragment read start on 16 different 16-byte bank slots.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void global_void;
+
+template <int K, int BM, int BN>
+struct PanelShape {
+    static constexpr int kPitch = K + 16;             // LDS bytes per row
+    static constexpr int kSlotsPerRow = kPitch / 16;  // the last slot of a row is padding
+    static constexpr int kSlots = (BM + BN) * kSlotsPerRow;
+    static constexpr int kG = K / kGroup;
+    static constexpr int kScaleSlots = BN * kG / 4;   // 16-byte pieces of the tile's weight scales
+};
+
+template <int K, int SM, int SN, int WAVES_M, int EPI, int FORM>
+__global__ __launch_bounds__(256) void gemm_panel_kernel(GemmParams p) {
+    constexpr int WAVES_N = 4 / WAVES_M;
+    constexpr int BM = WAVES_M * SM * 16, BN = WAVES_N * SN * 16;
+    using S = PanelShape<K, BM, BN>;
+    constexpr int G = S::kG, PITCH = S::kPitch;
+    constexpr bool kSilu = EPI == kGemmSilu;
+    static_assert(!kSilu || SN == 2, "the gated FFN pairs gate and up sub-tiles");
+    static_assert(K % 32 == 0 && G % 4 == 0, "whole groups, scale quads");
+    __shared__ __align__(16) int8_t panel_s[(BM + BN) * PITCH];
+    __shared__ __align__(16) float sw_s[BN * G];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int mtiles = (p.M + BM - 1) / BM;
+    int t = blockIdx.x;
+    if ((gridDim.x & 7) == 0) t = (t & 7) * (gridDim.x >> 3) + (t >> 3);  // one weight panel per XCD
+    const int mt = t % mtiles, nt = t / mtiles;
+    const int m0 = mt * BM;
+
+    // weight row of local tile column c (silu: wave column block wn holds 16
+    // outputs; its sub-tile column 0 is their gate rows, column 1 their up rows)
+    auto weight_row = [&](int c) -> int {
+        if constexpr (kSilu) {
+            const int w = c / 32, j = (c / 16) & 1, o = nt * (BN / 2) + w * 16 + (c & 15);
+            return j == 0 ? o : p.half + o;
+        } else {
+            return nt * BN + c;
+        }
+    };
+    auto row_ok = [&](int c) -> bool {
+        if constexpr (kSilu) return nt * (BN / 2) + (c / 32) * 16 + (c & 15) < p.half;
+        else return nt * BN + c < p.N;
+    };
+
+    // 1. the panel: slot s of the LDS image is 16-byte piece s % kSlotsPerRow of
+    // tile row s / kSlotsPerRow (rows 0..BM-1 tokens, then BN weight rows; rows
+    // past the matrix repeat its last row; a padding slot repeats piece 0). A
+    // lane copies to slot (round base + lane): lanes past the image stay idle.
+#pragma unroll
+    for (int q = 0; q < (S::kSlots + 255) / 256; ++q) {
+        const int sl = 256 * q + 64 * wave + lane;
+        if (sl < S::kSlots) {
+            const int row = sl / S::kSlotsPerRow, col = sl - row * S::kSlotsPerRow;
+            const int piece = col < S::kSlotsPerRow - 1 ? col : 0;
+            const int8_t* src = row < BM ? p.X + (size_t)min(m0 + row, p.M - 1) * K
+                                         : p.W + (size_t)min(weight_row(row - BM), p.N - 1) * K;
+            __builtin_amdgcn_global_load_lds((global_void*)(src + 16 * piece),
+                                             (lds_void*)(panel_s + 16 * (256 * q + 64 * wave)), 16, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < (S::kScaleSlots + 255) / 256; ++q) {
+        const int sl = 256 * q + 64 * wave + lane;
+        if (sl < S::kScaleSlots) {
+            const int c = sl / (G / 4), quad = sl - c * (G / 4);
+            __builtin_amdgcn_global_load_lds((global_void*)(p.sW + (size_t)min(weight_row(c), p.N - 1) * G + 4 * quad),
+                                             (lds_void*)(sw_s + 4 * (256 * q + 64 * wave)), 16, 0, 0);
+        }
+    }
+    const int r16 = lane & 15, kq = lane >> 4;
+    float sx[SM][4];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sx[i][r] = p.sx[min(m0 + wm * SM * 16 + i * 16 + 4 * kq + r, p.M - 1)];
+    float total[SM][SN][4];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) total[i][j][r] = 0.0f;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's panel pieces are in LDS
+    __syncthreads();
+
+    // 2. the group chains, in group order
+    const int8_t* arow[SM];
+    const int8_t* brow[SN];
+    const float* srow[SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i) arow[i] = panel_s + (wm * SM * 16 + i * 16 + r16) * PITCH + 8 * kq;
+#pragma unroll
+    for (int j = 0; j < SN; ++j) {
+        brow[j] = panel_s + (BM + wn * SN * 16 + j * 16 + r16) * PITCH + 8 * kq;
+        srow[j] = sw_s + (wn * SN * 16 + j * 16 + r16) * G;
+    }
+#pragma unroll 4
+    for (int g = 0; g < G; ++g) {
+        long a[SM], b[SN];
+        float sv[SN];
+#pragma unroll
+        for (int i = 0; i < SM; ++i) a[i] = *reinterpret_cast<const long*>(arow[i] + g * kGroup);
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+            b[j] = *reinterpret_cast<const long*>(brow[j] + g * kGroup);
+            sv[j] = srow[j][g];
+        }
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j) {
+                const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (FORM == kPanel)
+                        total[i][j][r] = fmaf((float)acc[r], sv[j] * sx[i][r], total[i][j][r]);  // panel.rs:184-188
+                    else
+                        total[i][j][r] = total[i][j][r] + ((float)acc[r] * sv[j]) * sx[i][r];  // neon.rs:180
+                }
+            }
+    }
+
+    // 3. epilogue
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm * SM * 16 + i * 16 + 4 * kq + r;
+            if (m >= p.M) continue;
+            if constexpr (kSilu) {
+                const int o = nt * (BN / 2) + wn * 16 + r16;
+                if (o < p.half) p.Y[(size_t)m * p.ldy + o] = silu(total[i][0][r]) * total[i][1][r];
+            } else {
+#pragma unroll
+                for (int j = 0; j < SN; ++j) {
+                    const int c = wn * SN * 16 + j * 16 + r16;
+                    if (!row_ok(c)) continue;
+                    float* dst = p.Y + (size_t)m * p.ldy + nt * BN + c;
+                    if constexpr (EPI == kGemmResidual)
+                        *dst = *dst + total[i][j][r];
+                    else if constexpr (EPI == kGemmStoreSilu)
+                        *dst = silu(total[i][j][r]);  // stem.rs:76,99: silu after the stage
+                    else
+                        *dst = total[i][j][r];
+                }
+            }
+        }
+}
+
 template <int SM, int SN, int WAVES_M, int EPI, int FORM, bool DUMP>
 static void launch_chain(const GemmParams& p, hipStream_t stream) {
     constexpr int BM = WAVES_M * SM * 16, BN = (4 / WAVES_M) * SN * 16;
     const int mtiles = (p.M + BM - 1) / BM;
     const int ntiles = EPI == kGemmSilu ? (p.half + BN / 2 - 1) / (BN / 2) : (p.N + BN - 1) / BN;
-    rn_launch((gemm_chain_kernel<SM, SN, WAVES_M, EPI, FORM, DUMP>), dim3(mtiles * ntiles), dim3(256), 0, stream, p);
+    const dim3 grid(mtiles * ntiles), block(256);
+    if constexpr (!DUMP) {
+        // the whole K panel in LDS for the widths it fits
+        switch (p.K) {
+            case 384: rn_launch((gemm_panel_kernel<384, SM, SN, WAVES_M, EPI, FORM>), grid, block, 0, stream, p); return;
+            case 512: rn_launch((gemm_panel_kernel<512, SM, SN, WAVES_M, EPI, FORM>), grid, block, 0, stream, p); return;
+            default: break;
+        }
+    }
+    rn_launch((gemm_chain_kernel<SM, SN, WAVES_M, EPI, FORM, DUMP>), grid, block, 0, stream, p);
 }
 
 // Tile shape: the one with the most blocks among 64 x 64, 64 x 32, 32 x 64 and
