@@ -286,7 +286,8 @@ def bench_whistle(rn, reps: int = 3, steps: int = 48, with_cpu: bool = True):
         dec_ms.append(t1.elapsed_ms(t2))
     T, d, f = w.frames, cfg["d_model"], cfg["ffn"]
     per_layer = 2 * T * (3 * d * d + d * d + 2 * f * d + d * f)
-    ops = cfg["enc_layers"] * per_layer + 2 * T * d * d + cfg["dec_layers"] * 2 * T * 2 * d * d
+    # encoder layers, the stem's second convolution (im2col rows of 3 d) and the cross memory
+    ops = cfg["enc_layers"] * per_layer + 2 * T * d * 3 * d + cfg["dec_layers"] * 2 * T * 2 * d * d
     out = dict(encode_ms=min(enc_ms), encode_int8_gops=ops / 1e9,
                decode_tokens_per_s=steps / (min(dec_ms) / 1e3), decode_ms_per_token=min(dec_ms) / steps,
                frames_in=cfg["frames"], encoder_frames=T, tokens=steps)

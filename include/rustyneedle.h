@@ -392,9 +392,10 @@ int rn_batch_get_cache(const rn_batch* batch, int sequence, int length, uint16_t
 int rn_batch_stream(const rn_batch* batch, void** stream);
 
 /* ---- Whistle-style speech path (crates/whistle) -------------------------------- */
-/* The synthetic configuration: a stem (fp32 conv kernel 3 stride 1 + silu, then
- * an fp32 depthwise conv kernel 3 stride 2 and an int8 pointwise product +
- * silu; stem.rs:39-115) to (frames - 1) / 2 + 1 encoder frames; encoder layers
+/* The configuration: a stem of two conv1d layers (stem.rs:39-115 in one
+ * dimension of time: an fp32 conv mels -> d, kernel 3 stride 1 + silu, then a
+ * conv d -> d, kernel 3 stride 2, as an int8 product over im2col rows of three
+ * frames + silu) to (frames - 1) / 2 + 1 encoder frames; encoder layers
  * of int8 self-attention (encoder.rs:217-297) and a gated FFN; a decoder of
  * the Session kind with cross-attention after each self-attention
  * (session.rs:126-128, cross.rs:126-182); tied int8 logits. d_model 384 or
@@ -423,9 +424,43 @@ int rn_frontend_free(rn_frontend* frontend);
 int rn_frontend_log_mel(rn_frontend* frontend, const float* samples, int n, float* features, int* frames,
                         int* valid, float* spread);
 
-/* Whistle::open (lib.rs:101-140) with seeded synthetic weights drawn by name
- * (the same draws as rn_synth_*): the model, its work buffers and one decoder
- * session of max_positions positions, on their own stream. */
+/* Host weights of the speech model (int8 codes with fp32 per-32 scales, fp32
+ * gains; every pointer host memory, copied at creation). */
+typedef struct {
+    rn_qmat_host qkv;                  /* [3 d][d]: q rows, k rows, v rows */
+    rn_qmat_host out;                  /* [d][d] */
+    rn_qmat_host gate_up;              /* [2 ffn][d] */
+    rn_qmat_host down;                 /* [d][ffn] */
+    const float *norm_attn, *norm_ffn; /* [d] */
+    const float *q_norm, *k_norm;      /* [64] per-head gains (encoder.rs:226-244) */
+} rn_whistle_enc_host;
+typedef struct {
+    rn_qmat_host qkv, out;             /* self-attention, as the encoder's */
+    rn_qmat_host cross_q;              /* [d][d] */
+    rn_qmat_host cross_kv;             /* [2 d][d]: key rows, then value rows of the memory */
+    rn_qmat_host cross_out;            /* [d][d] */
+    rn_qmat_host gate_up, down;
+    const float *norm_attn, *norm_cross, *post_norm, *norm_ffn; /* [d] */
+    const float *q_norm, *k_norm;      /* [64] cross-attention head gains */
+    float gate;                        /* the layer gate; the residual gain is sigmoid(gate) (cross.rs:178) */
+} rn_whistle_dec_host;
+typedef struct {
+    const float* conv1;                /* [d][3][mels] fp32 */
+    rn_qmat_host conv2;                /* [d][3 d]: column k d + i is tap k of input channel i */
+    const rn_whistle_enc_host* enc;    /* [enc_layers] */
+    const float* enc_norm;             /* [d] */
+    float position_gate;               /* the cross position term's gain is sigmoid(position_gate) (cross.rs:61-72) */
+    rn_qmat_host embedding;            /* [vocab][d], tied with the logits */
+    const rn_whistle_dec_host* dec;    /* [dec_layers] */
+    const float* dec_norm;             /* [d] */
+} rn_whistle_weights_host;
+
+/* Whistle::open (lib.rs:101-140) over host weights: the model, its work
+ * buffers and one decoder session of max_positions positions, on their own
+ * stream. */
+int rn_whistle_create(const rn_whistle_config* config, const rn_whistle_weights_host* weights, rn_whistle** out);
+/* The same with seeded synthetic weights drawn by name (the same draws as
+ * rn_synth_*). */
 int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, rn_whistle** out);
 int rn_whistle_free(rn_whistle* whistle);
 /* Encoder frames (frames - 1) / 2 + 1 (stem.rs:23-25). */

@@ -323,7 +323,7 @@ class WDecLayer(C.Structure):
 
 
 class WModel(C.Structure):
-    _fields_ = [("conv1", _p), ("depthwise", _p), ("pointwise", QMat), ("enc", _p), ("enc_norm", _p),
+    _fields_ = [("conv1", _p), ("conv2", QMat), ("enc", _p), ("enc_norm", _p),
                 ("cross_position", _p), ("embedding", QMat), ("dec", _p), ("dec_norm", _p), ("rope_cos", _p),
                 ("rope_sin", _p)]
 
@@ -399,7 +399,7 @@ class OracleWhistle:
                                _ptr(lw["post_norm"]), _ptr(lw["norm_ffn"]), _ptr(lw["q_norm"]), _ptr(lw["k_norm"]),
                                sigmoid(lw["gate"]))
         self._enc, self._dec = enc, dec
-        self.model = WModel(_ptr(weights["conv1"]), _ptr(weights["depthwise"]), qm(weights["pointwise"]),
+        self.model = WModel(_ptr(weights["conv1"]), qm(weights["conv2"]),
                             C.addressof(enc), _ptr(weights["enc_norm"]), _ptr(self.position), qm(weights["embedding"]),
                             C.addressof(dec), _ptr(weights["dec_norm"]), _ptr(self.rope_cos), _ptr(self.rope_sin))
 

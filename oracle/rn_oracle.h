@@ -180,10 +180,11 @@ void ro_allowed_statistics(const float* logits, const uint8_t* allowed, int n, i
  * crates/whistle: stem (stem.rs), encoder (encoder.rs), cross-attention
  * memory and apply (cross.rs), and the decoder step with the cross hook
  * (session.rs:76-148). The synthetic configuration keeps one residual stream
- * and a gated FFN, like the decoder above: stem = fp32 conv (k3, s1, pad 1)
- * + silu, then one stage of fp32 depthwise conv (k3, s2, pad 1) and an int8
- * pointwise product, + silu; encoder layer = x += out(int8 attention over all
- * frames of norm(x)), x += down(silu(gate) * up) of norm(x); final norm. */
+ * and a gated FFN, like the decoder above: stem = two conv1d layers, fp32
+ * conv (mels -> d, k3, s1, pad 1) + silu, then conv (d -> d, k3, s2, pad 1)
+ * as an int8 product over the im2col rows (three consecutive frames, each
+ * row quantised per row) + silu; encoder layer = x += out(int8 attention over
+ * all frames of norm(x)), x += down(silu(gate) * up) of norm(x); final norm. */
 typedef struct {
     int mels, frames, d_model, heads, head_dim, enc_layers, dec_layers, ffn, vocab, max_positions, group;
     float rope_theta, norm_eps;
@@ -208,8 +209,7 @@ typedef struct {
 
 typedef struct {
     const float* conv1;          /* [d][3][mels] */
-    const float* depthwise;      /* [3][d] */
-    ro_qmat pointwise;           /* [d][d] */
+    ro_qmat conv2;               /* [d][3 d]: column k d + i is tap k of input channel i */
     const ro_wenc_layer* enc;
     const float* enc_norm;       /* [d] */
     const float* cross_position; /* [encoder frames][d]: sigmoid(gate) * sinusoid (cross.rs:61-72) */

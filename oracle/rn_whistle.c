@@ -32,10 +32,12 @@ void ro_whistle_position_table(int T, int d, float gate, float* out) {
         }
 }
 
-/* stem.rs:39-115 for one dimension of time: the first convolution
- * adds taps (k, m) in that order into a zero output, then silu; the stage's
- * depthwise convolution adds its three taps in order per channel; the
- * pointwise product quantises each position per row; silu closes the stem. */
+/* The stem as two conv1d layers (stem.rs:39-115 keeps the reference's order of
+ * operations: convolution, silu after each stage, an int8 product for the
+ * learned projection). The first convolution adds taps (k, m) in that order
+ * into a zero output, then silu. The second is the int8 product of conv2 with
+ * the im2col rows: row t is frames 2t-1, 2t, 2t+1 of the first output (zero
+ * outside the input), quantised per row like every product input; then silu. */
 void ro_whistle_stem(const ro_wconfig* c, const ro_wmodel* m, const float* mel, float* out) {
     const int F = c->frames, M = c->mels, d = c->d_model, T = ro_whistle_frames(c);
     float* h1 = fbuf((size_t)F * d);
@@ -54,21 +56,19 @@ void ro_whistle_stem(const ro_wconfig* c, const ro_wmodel* m, const float* mel, 
             h1[(size_t)t * d + ch] = ro_silu(acc);
         }
     }
-    float* dw = fbuf((size_t)T * d);
-    for (int t = 0; t < T; ++t) {
-        for (int ch = 0; ch < d; ++ch) {
-            float acc = 0.0f;
-            for (int k = 0; k < 3; ++k) {
-                int src = 2 * t + k - 1;
-                if (src < 0 || src >= F) continue;
-                acc = acc + h1[(size_t)src * d + ch] * m->depthwise[(size_t)k * d + ch];
-            }
-            dw[(size_t)t * d + ch] = acc;
+    float* cols = fbuf((size_t)T * 3 * d);
+    for (int t = 0; t < T; ++t)
+        for (int k = 0; k < 3; ++k) {
+            const int src = 2 * t + k - 1;
+            float* dst = cols + ((size_t)t * 3 + k) * d;
+            if (src < 0 || src >= F)
+                memset(dst, 0, sizeof(float) * (size_t)d);
+            else
+                memcpy(dst, h1 + (size_t)src * d, sizeof(float) * (size_t)d);
         }
-    }
-    ro_multiply(RO_FORM_PANEL, m->pointwise.codes, m->pointwise.scales, d, d, c->group, dw, T, out, NULL, NULL, NULL);
+    ro_multiply(RO_FORM_PANEL, m->conv2.codes, m->conv2.scales, d, 3 * d, c->group, cols, T, out, NULL, NULL, NULL);
     for (size_t i = 0; i < (size_t)T * d; ++i) out[i] = ro_silu(out[i]);
-    free(dw);
+    free(cols);
     free(h1);
 }
 

@@ -101,6 +101,23 @@ class WhistleConfig(C.Structure):
                                   "vocab", "max_positions", "group")] + [("rope_theta", _f), ("norm_eps", _f)]
 
 
+class WhistleEncHost(C.Structure):
+    _fields_ = [("qkv", QMatHost), ("out", QMatHost), ("gate_up", QMatHost), ("down", QMatHost),
+                ("norm_attn", _p), ("norm_ffn", _p), ("q_norm", _p), ("k_norm", _p)]
+
+
+class WhistleDecHost(C.Structure):
+    _fields_ = [("qkv", QMatHost), ("out", QMatHost), ("cross_q", QMatHost), ("cross_kv", QMatHost),
+                ("cross_out", QMatHost), ("gate_up", QMatHost), ("down", QMatHost), ("norm_attn", _p),
+                ("norm_cross", _p), ("post_norm", _p), ("norm_ffn", _p), ("q_norm", _p), ("k_norm", _p),
+                ("gate", _f)]
+
+
+class WhistleWeightsHost(C.Structure):
+    _fields_ = [("conv1", _p), ("conv2", QMatHost), ("enc", _p), ("enc_norm", _p), ("position_gate", _f),
+                ("embedding", QMatHost), ("dec", _p), ("dec_norm", _p)]
+
+
 # Every symbol of include/rustyneedle.h with its signature (restype int unless noted).
 SIGNATURES = {
     "rn_last_error": (C.c_char_p, []),
@@ -186,6 +203,7 @@ SIGNATURES = {
     "rn_batch_logits": (_i, [_p, _p]),
     "rn_batch_get_cache": (_i, [_p, _i, _i, _p, _p]),
     "rn_whistle_create_synthetic": (_i, [C.POINTER(WhistleConfig), _u64, C.POINTER(_p)]),
+    "rn_whistle_create": (_i, [C.POINTER(WhistleConfig), C.POINTER(WhistleWeightsHost), C.POINTER(_p)]),
     "rn_whistle_free": (_i, [_p]),
     "rn_whistle_frames": (_i, [_p, C.POINTER(_i)]),
     "rn_whistle_tables": (_i, [_p, _p, _p]),
@@ -639,8 +657,8 @@ def synthetic_weights(config: dict, seed: int = SEED) -> dict:
 
 def synthetic_whistle_weights(config: dict, seed: int = SEED) -> dict:
     """The tensors rn_whistle_create_synthetic draws, by the same names: codes
-    U{-127..127}, scales U[1e-3, 1e-2], gains N(0, 0.1), the fp32 stem weights
-    N(0, 1/sqrt(fan-in)), the position and layer gates N(0, 1)."""
+    U{-127..127}, scales U[1e-3, 1e-2], gains N(0, 0.1), the fp32 first stem
+    convolution N(0, 1/sqrt(fan-in)), the position and layer gates N(0, 1)."""
     d, f, hd, M, V = config["d_model"], config["ffn"], config["head_dim"], config["mels"], config["vocab"]
 
     def q(name, rows, cols):
@@ -667,10 +685,8 @@ def synthetic_whistle_weights(config: dict, seed: int = SEED) -> dict:
                         q_norm=g(p + "q_norm", hd), k_norm=g(p + "k_norm", hd),
                         gate=float(synth_normal(seed, p + "gate", 1.0, (1,))[0])))
     conv_sigma = float(np.float32(1.0) / np.sqrt(np.float32(3 * M)))
-    dw_sigma = float(np.float32(1.0) / np.sqrt(np.float32(3)))
     return dict(conv1=synth_normal(seed, "whistle.conv1", conv_sigma, (d, 3, M)),
-                depthwise=synth_normal(seed, "whistle.depthwise", dw_sigma, (3, d)),
-                pointwise=q("whistle.pointwise", d, d), enc=enc, enc_norm=g("whistle.enc_norm", d),
+                conv2=q("whistle.conv2", d, 3 * d), enc=enc, enc_norm=g("whistle.enc_norm", d),
                 position_gate=float(synth_normal(seed, "whistle.position_gate", 1.0, (1,))[0]),
                 embedding=q("whistle.embedding", V, d), dec=dec, dec_norm=g("whistle.dec_norm", d))
 
@@ -886,16 +902,35 @@ class Batch:
 # ---- Whistle-style speech path ---------------------------------------------------
 
 class Whistle:
-    """crates/whistle Whistle (lib.rs:77-312) for the synthetic configuration: the
-    model, its encoder work buffers and one decoder session on the device."""
+    """crates/whistle Whistle (lib.rs:77-312): the model, its encoder work buffers
+    and one decoder session on the device, from host weights (the dict of
+    synthetic_whistle_weights) or drawn on the library side from `seed`."""
 
-    def __init__(self, config: dict, seed: int = SEED):
+    def __init__(self, config: dict, seed: int = SEED, weights: Optional[dict] = None):
         self.config = c = dict(config)
         self._cfg = WhistleConfig(*[c[n] for n in ("mels", "frames", "d_model", "heads", "head_dim", "enc_layers",
                                                    "dec_layers", "ffn", "vocab", "max_positions", "group")],
                                   c["rope_theta"], c["norm_eps"])
         h = _p()
-        check(lib.rn_whistle_create_synthetic(C.byref(self._cfg), seed, C.byref(h)))
+        if weights is None:
+            check(lib.rn_whistle_create_synthetic(C.byref(self._cfg), seed, C.byref(h)))
+        else:
+            qm = lambda pair: QMatHost(_ptr(pair[0]), _ptr(pair[1]))
+            enc = (WhistleEncHost * c["enc_layers"])()
+            for l, lw in enumerate(weights["enc"]):
+                enc[l] = WhistleEncHost(qm(lw["qkv"]), qm(lw["out"]), qm(lw["gate_up"]), qm(lw["down"]),
+                                        _ptr(lw["norm_attn"]), _ptr(lw["norm_ffn"]), _ptr(lw["q_norm"]),
+                                        _ptr(lw["k_norm"]))
+            dec = (WhistleDecHost * c["dec_layers"])()
+            for l, lw in enumerate(weights["dec"]):
+                dec[l] = WhistleDecHost(qm(lw["qkv"]), qm(lw["out"]), qm(lw["cross_q"]), qm(lw["cross_kv"]),
+                                        qm(lw["cross_out"]), qm(lw["gate_up"]), qm(lw["down"]), _ptr(lw["norm_attn"]),
+                                        _ptr(lw["norm_cross"]), _ptr(lw["post_norm"]), _ptr(lw["norm_ffn"]),
+                                        _ptr(lw["q_norm"]), _ptr(lw["k_norm"]), float(lw["gate"]))
+            wh = WhistleWeightsHost(_ptr(weights["conv1"]), qm(weights["conv2"]), C.addressof(enc),
+                                    _ptr(weights["enc_norm"]), float(weights["position_gate"]),
+                                    qm(weights["embedding"]), C.addressof(dec), _ptr(weights["dec_norm"]))
+            check(lib.rn_whistle_create(C.byref(self._cfg), C.byref(wh), C.byref(h)))
         self.handle = h.value
         n = _i()
         check(lib.rn_whistle_frames(self.handle, C.byref(n)))

@@ -1792,8 +1792,7 @@ struct rn_whistle {
     hipStream_t stream = nullptr;
     void* arena = nullptr;
     float* conv1 = nullptr;
-    float* depthwise = nullptr;
-    DevMatrix pointwise;
+    DevMatrix conv2;  // [d][3 d]
     std::vector<WEncLayerDev> enc;
     float* enc_norm = nullptr;
     float* position = nullptr;
@@ -1844,25 +1843,18 @@ static int validate_whistle(const rn_whistle_config* c) {
     return RN_OK;
 }
 
+// The synthetic weights drawn by name (the same draws as
+// rustyneedle_amd.synthetic_whistle_weights), then rn_whistle_create.
 int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, rn_whistle** out) {
     int rc = validate_whistle(config);
     if (rc) return rc;
     RN_REQUIRE(out, "out is null");
     const rn_whistle_config& c = *config;
-    const size_t d = c.d_model, f = c.ffn, H = c.heads, M = c.mels, Fr = c.frames, V = c.vocab;
-    const size_t T = (size_t)(c.frames - 1) / 2 + 1;
-    RN_REQUIRE(T <= 1536, "at most 1536 encoder frames (3072 mel frames): the attention stages a head's values in LDS");
-    rn_whistle* w = new (std::nothrow) rn_whistle();
-    if (!w) return fail(RN_ERR_MEMORY, "out of host memory");
-    w->cfg = c;
-    w->T = (int)T;
-    w->embed_scale = sqrtf((float)d);
-    w->capacity = c.max_positions;
-
-    // host draws, by name (the same as rustyneedle_amd.synthetic_whistle_weights)
+    const size_t d = c.d_model, f = c.ffn, M = c.mels, V = c.vocab;
     struct Q {
         std::vector<int8_t> codes;
         std::vector<float> scales;
+        rn_qmat_host host() const { return rn_qmat_host{codes.data(), scales.data()}; }
     };
     auto gen_q = [&](const std::string& name, size_t rows, size_t cols) {
         Q q;
@@ -1878,8 +1870,7 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
         return g;
     };
     std::vector<float> conv1 = gen_normal("whistle.conv1", 1.0f / sqrtf((float)(3 * M)), d * 3 * M);
-    std::vector<float> depthwise = gen_normal("whistle.depthwise", 1.0f / sqrtf(3.0f), 3 * d);
-    Q pointwise = gen_q("whistle.pointwise", d, d);
+    Q conv2 = gen_q("whistle.conv2", d, 3 * d);
     struct EncHost { Q qkv, out, gate_up, down; std::vector<float> norm_attn, norm_ffn, q_norm, k_norm; };
     struct DecHost {
         Q qkv, out, cross_q, cross_kv, cross_out, gate_up, down;
@@ -1887,6 +1878,7 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
         float gate;
     };
     std::vector<EncHost> eh(c.enc_layers);
+    std::vector<rn_whistle_enc_host> ew(c.enc_layers);
     for (int l = 0; l < c.enc_layers; ++l) {
         const std::string p = "whistle.enc." + std::to_string(l) + ".";
         eh[l].qkv = gen_q(p + "qkv", 3 * d, d);
@@ -1897,11 +1889,15 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
         eh[l].norm_ffn = gen_normal(p + "norm_ffn", 0.1f, d);
         eh[l].q_norm = gen_normal(p + "q_norm", 0.1f, 64);
         eh[l].k_norm = gen_normal(p + "k_norm", 0.1f, 64);
+        ew[l] = rn_whistle_enc_host{eh[l].qkv.host(), eh[l].out.host(), eh[l].gate_up.host(), eh[l].down.host(),
+                                    eh[l].norm_attn.data(), eh[l].norm_ffn.data(), eh[l].q_norm.data(),
+                                    eh[l].k_norm.data()};
     }
     std::vector<float> enc_norm = gen_normal("whistle.enc_norm", 0.1f, d);
     const float position_gate = gen_normal("whistle.position_gate", 1.0f, 1)[0];
     Q embedding = gen_q("whistle.embedding", V, d);
     std::vector<DecHost> dh(c.dec_layers);
+    std::vector<rn_whistle_dec_host> dw(c.dec_layers);
     for (int l = 0; l < c.dec_layers; ++l) {
         const std::string p = "whistle.dec." + std::to_string(l) + ".";
         dh[l].qkv = gen_q(p + "qkv", 3 * d, d);
@@ -1918,9 +1914,49 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
         dh[l].q_norm = gen_normal(p + "q_norm", 0.1f, 64);
         dh[l].k_norm = gen_normal(p + "k_norm", 0.1f, 64);
         dh[l].gate = gen_normal(p + "gate", 1.0f, 1)[0];
+        dw[l] = rn_whistle_dec_host{dh[l].qkv.host(), dh[l].out.host(), dh[l].cross_q.host(), dh[l].cross_kv.host(),
+                                    dh[l].cross_out.host(), dh[l].gate_up.host(), dh[l].down.host(),
+                                    dh[l].norm_attn.data(), dh[l].norm_cross.data(), dh[l].post_norm.data(),
+                                    dh[l].norm_ffn.data(), dh[l].q_norm.data(), dh[l].k_norm.data(), dh[l].gate};
     }
     std::vector<float> dec_norm = gen_normal("whistle.dec_norm", 0.1f, d);
-    whistle_position((int)T, (int)d, host_sigmoid(position_gate), w->position_host);
+    rn_whistle_weights_host wh{conv1.data(), conv2.host(), ew.data(), enc_norm.data(), position_gate,
+                               embedding.host(), dw.data(), dec_norm.data()};
+    return rn_whistle_create(config, &wh, out);
+}
+
+int rn_whistle_create(const rn_whistle_config* config, const rn_whistle_weights_host* wh, rn_whistle** out) {
+    int rc = validate_whistle(config);
+    if (rc) return rc;
+    RN_REQUIRE(out && wh, "null argument");
+    RN_REQUIRE(wh->conv1 && wh->conv2.codes && wh->conv2.scales && wh->enc && wh->enc_norm && wh->embedding.codes &&
+                   wh->embedding.scales && wh->dec && wh->dec_norm,
+               "null weight pointer");
+    const rn_whistle_config& c = *config;
+    auto qok = [](const rn_qmat_host& q) { return q.codes != nullptr && q.scales != nullptr; };
+    for (int l = 0; l < c.enc_layers; ++l) {
+        const rn_whistle_enc_host& e = wh->enc[l];
+        RN_REQUIRE(qok(e.qkv) && qok(e.out) && qok(e.gate_up) && qok(e.down) && e.norm_attn && e.norm_ffn && e.q_norm &&
+                       e.k_norm,
+                   "encoder layer %d has a null weight pointer", l);
+    }
+    for (int l = 0; l < c.dec_layers; ++l) {
+        const rn_whistle_dec_host& e = wh->dec[l];
+        RN_REQUIRE(qok(e.qkv) && qok(e.out) && qok(e.cross_q) && qok(e.cross_kv) && qok(e.cross_out) &&
+                       qok(e.gate_up) && qok(e.down) && e.norm_attn && e.norm_cross && e.post_norm && e.norm_ffn &&
+                       e.q_norm && e.k_norm,
+                   "decoder layer %d has a null weight pointer", l);
+    }
+    const size_t d = c.d_model, f = c.ffn, H = c.heads, M = c.mels, Fr = c.frames, V = c.vocab;
+    const size_t T = (size_t)(c.frames - 1) / 2 + 1;
+    RN_REQUIRE(T <= 1536, "at most 1536 encoder frames (3072 mel frames): the attention stages a head's values in LDS");
+    rn_whistle* w = new (std::nothrow) rn_whistle();
+    if (!w) return fail(RN_ERR_MEMORY, "out of host memory");
+    w->cfg = c;
+    w->T = (int)T;
+    w->embed_scale = sqrtf((float)d);
+    w->capacity = c.max_positions;
+    whistle_position((int)T, (int)d, host_sigmoid(wh->position_gate), w->position_host);
     rn_config rc_rope{};
     rc_rope.head_dim = 64;
     rc_rope.rope_theta = c.rope_theta;
@@ -1929,16 +1965,17 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
     rotary_table(rc_rope, rope_cos, rope_sin);
 
     // one device arena: weights, tables, work buffers, the cross memory, the session
-    const size_t Dm = std::max(d, f), L = c.dec_layers, cap = c.max_positions;
+    const size_t Dm = std::max(std::max(d, f), 3 * d), L = c.dec_layers, cap = c.max_positions;
     auto qbytes = [](size_t rows, size_t cols) { return align_up(rows * cols) + align_up(rows * (cols / kGroup) * 4); };
-    size_t total = align_up(4 * conv1.size()) + align_up(4 * depthwise.size()) + qbytes(d, d);
+    const size_t conv1_floats = d * 3 * M;
+    size_t total = align_up(4 * conv1_floats) + qbytes(d, 3 * d);
     total += (size_t)c.enc_layers * (qbytes(3 * d, d) + qbytes(d, d) + qbytes(2 * f, d) + qbytes(d, f) +
                                      2 * align_up(4 * d) + 2 * align_up(4 * 64));
     total += align_up(4 * d) + align_up(4 * T * d) + qbytes(V, d);
     total += L * (qbytes(3 * d, d) + 3 * qbytes(d, d) + qbytes(2 * d, d) + qbytes(2 * f, d) + qbytes(d, f) +
                   4 * align_up(4 * d) + 2 * align_up(4 * 64));
     total += align_up(4 * d) + 2 * align_up(4 * rope_cos.size());
-    total += align_up(4 * Fr * M) + align_up(4 * Fr * d) + align_up(4 * T * d) * 4 + align_up(4 * T * 3 * d) +
+    total += align_up(4 * Fr * M) + align_up(4 * (Fr + 2) * d) + align_up(4 * T * d) * 4 + align_up(4 * T * 3 * d) +
              align_up(4 * T * Dm) + align_up(T * Dm) + align_up(4 * T) + 3 * align_up(T * d) + 3 * align_up(4 * T * H);
     total += 2 * align_up(L * T * d) + 2 * align_up(4 * L * T * H);
     total += 2 * align_up(2 * L * H * cap * 64) + 5 * align_up(4 * d) + align_up(4 * 32 * d) + align_up(4 * 3 * d) +
@@ -1954,55 +1991,56 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
         uploads.push_back({dst, {src, bytes}});
         return dst;
     };
-    auto placeq = [&](const Q& q, size_t rows, size_t cols) {
+    auto placeq = [&](const rn_qmat_host& q, size_t rows, size_t cols) {
         DevMatrix dm;
-        dm.W = (int8_t*)place(q.codes.data(), rows * cols);
-        dm.sW = (float*)place(q.scales.data(), rows * (cols / kGroup) * 4);
+        dm.W = (int8_t*)place(q.codes, rows * cols);
+        dm.sW = (float*)place(q.scales, rows * (cols / kGroup) * 4);
         return dm;
     };
-    w->conv1 = (float*)place(conv1.data(), 4 * conv1.size());
-    w->depthwise = (float*)place(depthwise.data(), 4 * depthwise.size());
-    w->pointwise = placeq(pointwise, d, d);
+    w->conv1 = (float*)place(wh->conv1, 4 * conv1_floats);
+    w->conv2 = placeq(wh->conv2, d, 3 * d);
     w->enc.resize(c.enc_layers);
     for (int l = 0; l < c.enc_layers; ++l) {
+        const rn_whistle_enc_host& e = wh->enc[l];
         WEncLayerDev& D = w->enc[l];
-        D.qkv = placeq(eh[l].qkv, 3 * d, d);
-        D.out = placeq(eh[l].out, d, d);
-        D.gate_up = placeq(eh[l].gate_up, 2 * f, d);
-        D.down = placeq(eh[l].down, d, f);
-        D.norm_attn = (float*)place(eh[l].norm_attn.data(), 4 * d);
-        D.norm_ffn = (float*)place(eh[l].norm_ffn.data(), 4 * d);
-        D.q_norm = (float*)place(eh[l].q_norm.data(), 4 * 64);
-        D.k_norm = (float*)place(eh[l].k_norm.data(), 4 * 64);
+        D.qkv = placeq(e.qkv, 3 * d, d);
+        D.out = placeq(e.out, d, d);
+        D.gate_up = placeq(e.gate_up, 2 * f, d);
+        D.down = placeq(e.down, d, f);
+        D.norm_attn = (float*)place(e.norm_attn, 4 * d);
+        D.norm_ffn = (float*)place(e.norm_ffn, 4 * d);
+        D.q_norm = (float*)place(e.q_norm, 4 * 64);
+        D.k_norm = (float*)place(e.k_norm, 4 * 64);
     }
-    w->enc_norm = (float*)place(enc_norm.data(), 4 * d);
+    w->enc_norm = (float*)place(wh->enc_norm, 4 * d);
     w->position = (float*)place(w->position_host.data(), 4 * T * d);
-    w->embedding = placeq(embedding, V, d);
+    w->embedding = placeq(wh->embedding, V, d);
     w->dec.resize(L);
     w->gains_host.resize(L);
     for (size_t l = 0; l < L; ++l) {
+        const rn_whistle_dec_host& e = wh->dec[l];
         WDecLayerDev& D = w->dec[l];
-        D.qkv = placeq(dh[l].qkv, 3 * d, d);
-        D.out = placeq(dh[l].out, d, d);
-        D.cross_q = placeq(dh[l].cross_q, d, d);
-        D.cross_kv = placeq(dh[l].cross_kv, 2 * d, d);
-        D.cross_out = placeq(dh[l].cross_out, d, d);
-        D.gate_up = placeq(dh[l].gate_up, 2 * f, d);
-        D.down = placeq(dh[l].down, d, f);
-        D.norm_attn = (float*)place(dh[l].norm_attn.data(), 4 * d);
-        D.norm_cross = (float*)place(dh[l].norm_cross.data(), 4 * d);
-        D.post_norm = (float*)place(dh[l].post_norm.data(), 4 * d);
-        D.norm_ffn = (float*)place(dh[l].norm_ffn.data(), 4 * d);
-        D.q_norm = (float*)place(dh[l].q_norm.data(), 4 * 64);
-        D.k_norm = (float*)place(dh[l].k_norm.data(), 4 * 64);
-        D.cross_gain = w->gains_host[l] = host_sigmoid(dh[l].gate);
+        D.qkv = placeq(e.qkv, 3 * d, d);
+        D.out = placeq(e.out, d, d);
+        D.cross_q = placeq(e.cross_q, d, d);
+        D.cross_kv = placeq(e.cross_kv, 2 * d, d);
+        D.cross_out = placeq(e.cross_out, d, d);
+        D.gate_up = placeq(e.gate_up, 2 * f, d);
+        D.down = placeq(e.down, d, f);
+        D.norm_attn = (float*)place(e.norm_attn, 4 * d);
+        D.norm_cross = (float*)place(e.norm_cross, 4 * d);
+        D.post_norm = (float*)place(e.post_norm, 4 * d);
+        D.norm_ffn = (float*)place(e.norm_ffn, 4 * d);
+        D.q_norm = (float*)place(e.q_norm, 4 * 64);
+        D.k_norm = (float*)place(e.k_norm, 4 * 64);
+        D.cross_gain = w->gains_host[l] = host_sigmoid(e.gate);
     }
-    w->dec_norm = (float*)place(dec_norm.data(), 4 * d);
+    w->dec_norm = (float*)place(wh->dec_norm, 4 * d);
     w->rope_cos = (float*)place(rope_cos.data(), 4 * rope_cos.size());
     w->rope_sin = (float*)place(rope_sin.data(), 4 * rope_sin.size());
     w->mel = (float*)a.take(4 * Fr * M);
-    w->h1 = (float*)a.take(4 * Fr * d);
-    w->R = (float*)a.take(4 * T * d);  // the stem's depthwise output, later the memory input
+    w->h1 = (float*)a.take(4 * (Fr + 2) * d);  // the first convolution's output, one zero row before and after
+    w->R = (float*)a.take(4 * T * d);  // the memory input
     w->X = (float*)a.take(4 * T * d);
     w->ctx = (float*)a.take(4 * T * d);
     w->encoded = (float*)a.take(4 * T * d);
@@ -2046,7 +2084,10 @@ int rn_whistle_create_synthetic(const rn_whistle_config* config, uint64_t seed, 
             return fail(RN_ERR_DEVICE, "weight upload failed");
         }
     }
-    if (hipMemsetAsync(w->state, 0, sizeof(DecodeState), w->stream) != hipSuccess ||
+    // the zero rows around the first convolution's output, and the decoder state
+    if (hipMemsetAsync(w->h1, 0, 4 * d, w->stream) != hipSuccess ||
+        hipMemsetAsync(w->h1 + (Fr + 1) * d, 0, 4 * d, w->stream) != hipSuccess ||
+        hipMemsetAsync(w->state, 0, sizeof(DecodeState), w->stream) != hipSuccess ||
         hipStreamSynchronize(w->stream) != hipSuccess) {
         (void)hipStreamDestroy(w->stream);
         (void)hipFree(w->arena);
@@ -2087,16 +2128,19 @@ int rn_whistle_stream(const rn_whistle* w, void** stream) {
     return RN_OK;
 }
 
-// stem.rs:39-115: first convolution + silu, the stage's depthwise convolution,
-// its pointwise product (rows quantised per frame) with silu, into w->X.
+// stem.rs:39-115 as two conv1d layers: the first convolution + silu into rows
+// 1..F of h1 (rows 0 and F + 1 stay zero), then the second (kernel 3, stride 2)
+// as the int8 product of conv2 with the im2col rows: row t is h1 rows 2t..2t+2
+// (frames 2t-1..2t+1), contiguous, so the rows are read in place with a
+// stride of two frames and quantised per row; silu, into w->X.
 static int whistle_stem(rn_whistle* w, const float* mel) {
     const rn_whistle_config& c = w->cfg;
     const int d = c.d_model, T = w->T;
     hipStream_t st = w->stream;
     RN_HIP(hipMemcpyAsync(w->mel, mel, 4 * (size_t)c.frames * c.mels, hipMemcpyHostToDevice, st));
-    RN_HIP(launch_stem(w->mel, w->conv1, w->depthwise, c.frames, c.mels, d, w->h1, w->R, st));
-    RN_HIP(launch_norm_quantise(w->R, nullptr, T, d, c.norm_eps, w->Xq, w->sx, nullptr, st));
-    RN_HIP(launch_gemm(GemmParams{w->Xq, w->sx, w->pointwise.W, w->pointwise.sW, T, d, d, w->X, d, nullptr, 0},
+    RN_HIP(launch_stem(w->mel, w->conv1, c.frames, c.mels, d, w->h1 + d, st));
+    RN_HIP(launch_quantise_strided(w->h1, 2 * (size_t)d, T, 3 * d, w->Xq, w->sx, st));
+    RN_HIP(launch_gemm(GemmParams{w->Xq, w->sx, w->conv2.W, w->conv2.sW, T, d, 3 * d, w->X, d, nullptr, 0},
                        kGemmStoreSilu, kPanel, false, st));
     return RN_OK;
 }

@@ -641,7 +641,7 @@ static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
 // codes to X / sx first.
 template <int EPI, int FORM, bool DUMP, int AIN>
 static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
-    const int pick = chain_pick<EPI>(p);
+    const int pick = p.K == 1152 ? (EPI == kGemmSilu ? 2 : 3) : chain_pick<EPI>(p);
     const int n_eff = EPI == kGemmSilu ? 2 * p.half : p.N;
     const size_t reread = (size_t)((n_eff + 31) / 32) * (size_t)p.M * (size_t)p.K * sizeof(float);
     const bool fused =
@@ -669,7 +669,10 @@ static hipError_t launch_panel(const GemmParams& p, int ain, hipStream_t stream)
 hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, hipStream_t stream) {
     if (p.M <= 0) return hipSuccess;
     // instantiated for the supported widths (the kernel is unrolled over groups)
-    if ((p.K != 384 && p.K != 512 && p.K != 1024 && p.K != 1536 && p.K != 2048) || p.N <= 0) return hipErrorInvalidValue;
+    if ((p.K != 384 && p.K != 512 && p.K != 1024 && p.K != 1152 && p.K != 1536 && p.K != 2048) || p.N <= 0)
+        return hipErrorInvalidValue;
+    // 1152 columns (the stem's im2col rows at d 384) have no split-kernel tile: codes only, chain kernel
+    if (p.K == 1152 && (p.Xf != nullptr || dump)) return hipErrorInvalidValue;
     if (epilogue == kGemmSilu && (p.half % 16 != 0 || p.N != 2 * p.half)) return hipErrorInvalidValue;
     if (p.Xf != nullptr && (p.X == nullptr || p.sx == nullptr)) return hipErrorInvalidValue;
     const int ain = p.Xf == nullptr ? kRowsCodes : kRowsQuant;
@@ -707,13 +710,14 @@ hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, h
 // rows. NV = n / 128 float2 per lane.
 template <int NV>
 __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, const float* gain, int count, float eps,
-                                                            int8_t* codes, float* scales, float* normed) {
+                                                            int8_t* codes, float* scales, float* normed,
+                                                            size_t x_stride) {
     constexpr int n = NV * 128;
     extern __shared__ float sq_s[];  // [4][n] when gain != nullptr
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + wave;
     const bool live = row < count;
-    const float2* src = reinterpret_cast<const float2*>(x + (size_t)(live ? row : count - 1) * n);
+    const float2* src = reinterpret_cast<const float2*>(x + (size_t)(live ? row : count - 1) * x_stride);
     float2 v[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) v[i] = src[lane + 64 * i];
@@ -773,16 +777,35 @@ hipError_t launch_norm_quantise(const float* x, const float* gain, int count, in
     if (count <= 0) return hipSuccess;
     const size_t lds = gain != nullptr ? 4 * sizeof(float) * (size_t)n : 0;
     const dim3 grid((count + 3) / 4), block(256);
-#define RN_NQ(NV) rn_launch(norm_quantise_kernel<NV>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed)
+#define RN_NQ(NV) \
+    rn_launch(norm_quantise_kernel<NV>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed, (size_t)n)
     switch (n) {
         case 384: RN_NQ(3); break;
         case 512: RN_NQ(4); break;
         case 1024: RN_NQ(8); break;
+        case 1152: RN_NQ(9); break;
         case 1536: RN_NQ(12); break;
         case 2048: RN_NQ(16); break;
         default: return hipErrorInvalidValue;
     }
 #undef RN_NQ
+    return hipGetLastError();
+}
+
+hipError_t launch_quantise_strided(const float* x, size_t x_stride, int count, int n, int8_t* codes, float* scales,
+                                   hipStream_t stream) {
+    if (count <= 0) return hipSuccess;
+    const dim3 grid((count + 3) / 4), block(256);
+    const float* no_gain = nullptr;
+    float* no_normed = nullptr;
+#define RN_QS(NV) \
+    rn_launch(norm_quantise_kernel<NV>, grid, block, 0, stream, x, no_gain, count, 0.0f, codes, scales, no_normed, x_stride)
+    switch (n) {
+        case 1152: RN_QS(9); break;
+        case 1536: RN_QS(12); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef RN_QS
     return hipGetLastError();
 }
 

@@ -187,6 +187,10 @@ struct GemmParams {
 hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, hipStream_t stream);
 hipError_t launch_norm_quantise(const float* x, const float* gain, int count, int n, float eps, int8_t* codes,
                                 float* scales, float* normed, hipStream_t stream);
+// quantise_int8 of `count` rows of n floats that start x_stride floats apart
+// (rows may overlap: the im2col rows of a strided convolution)
+hipError_t launch_quantise_strided(const float* x, size_t x_stride, int count, int n, int8_t* codes, float* scales,
+                                   hipStream_t stream);
 hipError_t launch_embed_rows(const uint32_t* tokens, int count, const int8_t* E, const float* sE, int d, int vocab,
                              float scale, float* X, int32_t* error, hipStream_t stream);
 hipError_t launch_argmax_rows(const float* logits, int count, int n, uint32_t* tokens, uint32_t* ids, int steps,
@@ -194,10 +198,8 @@ hipError_t launch_argmax_rows(const float* logits, int count, int n, uint32_t* t
 hipError_t launch_advance_positions(int32_t* pos, int count, int by, hipStream_t stream);
 
 // ---- speech path (rn_whistle.hip) ---------------------------------------------
-// First convolution (+ silu) into h1 [F][d], then the stage's depthwise
-// convolution into dw_out [(F - 1) / 2 + 1][d].
-hipError_t launch_stem(const float* mel, const float* conv1, const float* depthwise, int F, int M, int d, float* h1,
-                       float* dw_out, hipStream_t stream);
+// The stem's first convolution (kernel 3, stride 1, pad 1) + silu into h1 [F][d].
+hipError_t launch_stem(const float* mel, const float* conv1, int F, int M, int d, float* h1, hipStream_t stream);
 
 struct HeadSection {
     int col;             // first column of the section in a source row

@@ -3,16 +3,17 @@
 // keys and values, and the decoder's fused cross-attention.
 //
 // Replaces crates/whistle/src/frontend.rs:42-133 (FFT, power spectrum, mel
-// projection, log, spread and normalisation), stem.rs:39-115 (first
-// convolution, one depthwise + pointwise stage), encoder.rs:217-297 (the
+// projection, log, spread and normalisation), stem.rs:39-115 (the two
+// conv1d layers of the stem; the second runs as an int8 product over im2col
+// rows), encoder.rs:217-297 (the
 // attention's integer scores and int8 values) and cross.rs:58-182 (memory,
 // apply). Products go
 // through the shared int8 kernels (rn_gemm.hip, rn_gemv.hip); the cross
 // residual (cross.rs:176-181) is the prologue of the gated FFN's product.
 //
 // Float orders (identical to the CPU restatement): the first convolution adds
-// its taps (k, m) in order into a zero output per (frame, channel); the
-// depthwise convolution adds its three taps in order; the head norm uses the
+// its taps (k, m) in order into a zero output per (frame, channel); the head
+// norm uses the
 // eight-lane sum of ops.rs:7-17; softmax totals and value sums use 32
 // interleaved frame classes (frame j goes to class j mod 32, classes summed
 // 0..31), with the weights normalised first and scaled by the value scale
@@ -61,29 +62,11 @@ __global__ __launch_bounds__(256) void stem_conv_kernel(const float* mel, const 
     }
 }
 
-// stem.rs:64-94, the stage's depthwise convolution (kernel 3, stride 2, pad 1).
-__global__ __launch_bounds__(256) void stem_depthwise_kernel(const float* h, const float* dw, int F, int T, int d,
-                                                             float* out) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= T * d) return;
-    const int t = i / d, c = i - t * d;
-    float acc = 0.0f;
-    for (int k = 0; k < 3; ++k) {
-        const int src = 2 * t + k - 1;
-        if (src < 0 || src >= F) continue;
-        acc = acc + h[(size_t)src * d + c] * dw[(size_t)k * d + c];
-    }
-    out[i] = acc;
-}
-
-hipError_t launch_stem(const float* mel, const float* conv1, const float* depthwise, int F, int M, int d, float* h1,
-                       float* dw_out, hipStream_t stream) {
+hipError_t launch_stem(const float* mel, const float* conv1, int F, int M, int d, float* h1, hipStream_t stream) {
     if (M < 1 || M > kMaxMels || F < 1 || d < 1) return hipErrorInvalidValue;
-    const int T = (F - 1) / 2 + 1;
     const size_t lds = sizeof(float) * ((size_t)kStemChan * (3 * M + 1) + (size_t)(kStemTime + 2) * M);
     rn_launch(stem_conv_kernel, dim3((F + kStemTime - 1) / kStemTime, (d + kStemChan - 1) / kStemChan), dim3(256), lds,
               stream, mel, conv1, F, M, d, h1);
-    rn_launch(stem_depthwise_kernel, dim3((T * d + 255) / 256), dim3(256), 0, stream, h1, depthwise, F, T, d, dw_out);
     return hipGetLastError();
 }
 

@@ -45,14 +45,13 @@ def stem(cfg, w, mel):
     for k in range(3):
         h1 += pad[k:k + F] @ W1[:, k, :].T
     h1 = silu(h1)
+    # second conv1d (d -> d, kernel 3, stride 2, pad 1) as an int8 product of the
+    # three input frames of each output frame, quantised per row like any input
     T = (F - 1) // 2 + 1
-    hp = np.zeros((F + 2, d))
-    hp[1:-1] = h1
-    dw = w["depthwise"].astype(np.float64)
-    out = np.zeros((T, d))
-    for k in range(3):
-        out += hp[k:k + 2 * T:2][:T] * dw[k]
-    y = np.stack([product(*w["pointwise"], out[t]) for t in range(T)])
+    hp = np.zeros((F + 3, d))
+    hp[1:F + 1] = h1
+    cols = np.stack([hp[2 * t:2 * t + 3].reshape(-1) for t in range(T)])
+    y = np.stack([product(*w["conv2"], cols[t]) for t in range(T)])
     return silu(y)
 
 

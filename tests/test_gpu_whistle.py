@@ -116,3 +116,27 @@ def test_ragged_frame_counts(mel_frames):
         g.push(tok)
         s.push(tok)
         assert np.array_equal(_bits(g.logits()), _bits(s.logits()))
+
+
+def test_host_weights_equal_synthetic_and_oracle():
+    """rn_whistle_create over host weights (Whistle::open's role, lib.rs:101-140)
+    builds the same model as the library's seeded draws: stem, encode and greedy
+    ids equal, and equal to the oracle; weights perturbed on the host change the
+    result (the host arrays are the ones used)."""
+    cfg = dict(rn.WHISTLE)
+    cfg.update(frames=40, enc_layers=1, dec_layers=1, vocab=500, max_positions=16)
+    w = rn.synthetic_whistle_weights(cfg, seed=5)
+    a, b = rn.Whistle(cfg, seed=5), rn.Whistle(cfg, weights=w)
+    mel = rn.synthetic_mel(cfg, seed=5)
+    o = oracle.OracleWhistle(cfg, w)
+    assert np.array_equal(_bits(a.stem(mel)), _bits(b.stem(mel)))
+    enc = b.encode(mel)
+    assert np.array_equal(_bits(a.encode(mel)), _bits(enc))
+    assert np.array_equal(_bits(enc), _bits(o.encode(mel)))
+    ids = b.decode_greedy(3, 6)
+    assert ids.tolist() == a.decode_greedy(3, 6).tolist()
+    assert ids.tolist() == o.session(cfg["max_positions"], o.memory(o.encode(mel))).greedy(3, 6).tolist()
+    w2 = dict(w)
+    w2["conv2"] = (w["conv2"][0].copy(), w["conv2"][1] * np.float32(2.0))
+    c = rn.Whistle(cfg, weights=w2)
+    assert not np.array_equal(_bits(c.stem(mel)), _bits(b.stem(mel)))

@@ -58,7 +58,7 @@ def test_stem_against_float64(small):
     st, ref = o.stem(mel), nw.stem(cfg, w, mel)
     assert st.shape == (32, 384)
     rel = row_rel(st, ref)
-    # a pointwise-input code within float32 rounding of a rounding boundary may
+    # a second-convolution input code within float32 rounding of a rounding boundary may
     # flip (the model is discontinuous there); every other row agrees to float32
     assert np.mean(rel < 1e-5) >= 0.9, rel
     assert np.all(rel < 2e-2), rel
