@@ -242,6 +242,40 @@ def bench_codebook(rn, shapes=((2, 128, 2048, 512), (2, 128, 2097152, 512), (4, 
         gbs = nbytes / (ms / 1e3) / 1e9
         out[f"{bits}bit_{rows}x{columns}"] = dict(us=ms * 1e3, bytes=nbytes, gb_s=gbs, frac=gbs / HBM_PEAK_GBS)
         del m, xd, rd, yd
+    out["float_path"] = bench_codebook_float(rn, stream)
+    return out
+
+
+def bench_codebook_float(rn, stream, rows: int = 2048, columns: int = 512, group: int = 128):
+    """The float path (fill_rows_float, crates/kernels/src/matrix.rs:427-440): what
+    the reference runs on x86-64 for every width, and everywhere for 1- and 3-bit
+    matrices. The device kernel per width, and the oracle's restatement of it on
+    one host core beside it (about 0.5 s of CPU work per width)."""
+    import oracle
+    out = {}
+    for bits in (1, 2, 3, 4):
+        cb = rn.synthetic_codebook(group)
+        blob = rn.synthetic_codebook_blob(rows, columns, group, bits, name=f"bench.float.{bits}")
+        m = rn.CodebookMatrix(blob, rows, columns, group, bits, cb)
+        om = oracle.OracleCodebookMatrix(blob, rows, columns, group, bits, cb)
+        x = rn.synth_normal(rn.SEED, "bench.float.x", 1.0, (1, m.padded))
+        xd, yd = rn.DeviceBuffer.from_array(x), rn.DeviceBuffer(4 * rows)
+        call = lambda: rn.check(rn.lib.rn_matrix_multiply_vector_float(m.handle, xd.ptr, yd.ptr, stream.handle))
+        for _ in range(3):
+            call()
+        gpu_ms = time_events(rn, stream.handle, call, 200)
+        oracle.set_threads(1)
+        reps, spent = 0, 0.0
+        ref = None
+        while spent < 0.5 or reps < 3:
+            t0 = time.perf_counter()
+            ref = om.multiply_float(x)
+            spent += time.perf_counter() - t0
+            reps += 1
+        same = np.array_equal(yd.download(np.float32, (1, rows)).view(np.uint32), ref.view(np.uint32))
+        out[f"{bits}bit_{rows}x{columns}"] = dict(gpu_us=gpu_ms * 1e3, cpu_us=spent / reps * 1e6, cpu_cores=1,
+                                                 cpu_kind="port", bit_identical=bool(same))
+        del m, xd, yd
     return out
 
 

@@ -141,15 +141,30 @@ int rn_matrix_dequantise_row(const rn_matrix* m, int row, float* out);
  * kind-3 record (cact record.rs:7-84): `blob` is the record's bytes as the
  * archive holds them (packed indices LSB first, rows x padded x index_bits / 8
  * bytes, then rows x padded / group fp16 norms), `codebook` the archive's 28
- * levels (2-bit 0..3, 3-bit 4..11, 4-bit 12..27). bits 2, 4 or 5 (ternary
+ * levels (2-bit 0..3, 3-bit 4..11, 4-bit 12..27). bits 1..4 or 5 (ternary
  * crumbs); group 64, 128 or 256. The blob is copied to the device as is.
  * The multiply entry points above then take the ROTATED input of
  * rn_matrix_prepare ([count][padded] floats), quantise it per group and run
  * the integer path: 2-bit matrices the panel form (panel.rs:153-197), 4-bit and
  * ternary ones the plane form (neon.rs:126-183). multiply_fused on codebook
- * matrices launches once per matrix. */
+ * matrices launches once per matrix. 1- and 3-bit matrices have no integer
+ * levels in the reference (matrix.rs:559-563): their products are the float
+ * path below (no acc). */
 int rn_matrix_create_codebook(const uint8_t* blob, size_t blob_bytes, int rows, int columns, int group, int bits,
                               const float* codebook, int codebook_len, rn_matrix** out);
+/* The float path of a codebook matrix, the one the reference takes on x86-64
+ * for every width (docs/portability.md:10) and everywhere for 1- and 3-bit
+ * ones. Rotated inputs (not quantised), device pointers.
+ *   vector: fill_rows_float (matrix.rs:427-440) with LookupTable::dot_group
+ *     (matrix.rs:610-620): per group, each of the 8 / index_bits lanes of a
+ *     byte sums level * input over the group's bytes in order, the lanes are
+ *     summed in order (3-bit: one sum over the positions), then
+ *     total += partial * norm over the groups in order.
+ *   batch: multiply_batch's float tile (matrix.rs:356-378): the row expanded
+ *     as level * norm (matrix.rs:390-399) and dotted with each input in
+ *     eight lanes (matrix.rs:488-497). */
+int rn_matrix_multiply_vector_float(const rn_matrix* m, const float* rotated, float* y, void* stream);
+int rn_matrix_multiply_batch_float(const rn_matrix* m, const float* rotated, int count, float* y, void* stream);
 /* QuantisedMatrix::padded_columns (matrix.rs:69-71); columns for int8 matrices. */
 int rn_matrix_padded_columns(const rn_matrix* m, int* padded);
 /* QuantisedMatrix::prepare / prepare_batch (matrix.rs:123-138): x [count][columns]

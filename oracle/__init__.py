@@ -477,6 +477,8 @@ lib.ro_integer_levels.argtypes = [_p, _i, _p]
 lib.ro_group_codes.argtypes = [_p, _i, _i, _p, _p]
 lib.ro_codebook_product.argtypes = [_p, _p, _i, _i, _i, _i, _p, _f, _p, _p, _i, _p, _p]
 lib.ro_codebook_dequantise_row.argtypes = [_p, _p, _i, _i, _i, _i, _p, _i, _p]
+lib.ro_codebook_float_vector.argtypes = [_p, _p, _i, _i, _i, _i, _p, _p, _i, _p]
+lib.ro_codebook_float_batch.argtypes = [_p, _p, _i, _i, _i, _i, _p, _p, _i, _p]
 
 
 def walsh_transform(v) -> np.ndarray:
@@ -552,6 +554,18 @@ class OracleCodebookMatrix:
         x = _f32(x).reshape(-1, self.columns)
         rotated = np.stack([self.prepare(row) for row in x])
         return self.multiply_rotated(rotated, with_acc)
+
+    def multiply_float(self, rotated, batch: bool = False) -> np.ndarray:
+        """The float path on rotated inputs [count][padded]: fill_rows_float
+        (multiply_vector on x86-64, matrix.rs:427-440) or, with batch, the float
+        tile of multiply_batch (matrix.rs:356-378)."""
+        rotated = _f32(rotated).reshape(-1, self.padded)
+        count = rotated.shape[0]
+        y = np.empty((count, self.rows), np.float32)
+        fn = lib.ro_codebook_float_batch if batch else lib.ro_codebook_float_vector
+        fn(_ptr(self.packed), _ptr(self.norms), self.rows, self.padded, self.group, self.bits, _ptr(self.levels),
+           _ptr(rotated), count, _ptr(y))
+        return y
 
     def dequantise_row(self, row: int) -> np.ndarray:
         out = np.empty(self.columns, np.float32)

@@ -21,8 +21,11 @@
  *     (matrix.rs:113-121, 205-214: 2-bit matrices take the panel path, 4-bit
  *     and ternary ones the plane path).
  * 1-bit and 3-bit matrices have no integer path in the reference
- * (matrix.rs:559-563: integer levels for 2 and 4 bits only) and are not
- * restated here.
+ * (matrix.rs:559-563: integer levels for 2 and 4 bits only); they, and every
+ * width on x86-64, take the float path, restated by ro_codebook_float_vector
+ * (fill_rows_float, matrix.rs:427-440, with LookupTable::dot_group,
+ * matrix.rs:610-620) and ro_codebook_float_batch (multiply_batch's float tile,
+ * matrix.rs:356-378: expand_row_scaled then the eight-lane dot, matrix.rs:488-497).
  */
 #include <math.h>
 #include <stdint.h>
@@ -120,6 +123,8 @@ void ro_group_codes(const float* rotated, int n, int group, int8_t* codes, float
     }
 }
 
+static float level_at(const uint8_t* row, int e, int ib, const float levels[16]);
+
 /* record.rs:66-72: the index width in the blob (ternary crumbs are 2 bits) */
 static int index_bits(int bits) { return bits == 5 ? 2 : bits; }
 
@@ -170,9 +175,86 @@ void ro_codebook_dequantise_row(const uint8_t* packed, const uint16_t* norms, in
     float* full = (float*)malloc((size_t)padded * sizeof(float));
     for (int g = 0; g < groups; ++g) {
         const float norm = ro_f16_to_f32(norms[(size_t)row * groups + g]);
-        for (int i = 0; i < group; ++i) full[g * group + i] = levels[code_at(r, g * group + i, ib)] * norm;
+        for (int i = 0; i < group; ++i) full[g * group + i] = level_at(r, g * group + i, ib, levels) * norm;
         ro_walsh_transform(full + g * group, group);
     }
     memcpy(out, full, (size_t)columns * sizeof(float));
     free(full);
+}
+
+/* matrix.rs:623-631: the level of element e of a packed row, LSB first; a
+ * 3-bit index may straddle two bytes */
+static float level_at(const uint8_t* row, int e, int ib, const float levels[16]) {
+    const int bit = e * ib, byte = bit / 8, shift = bit % 8;
+    uint32_t raw = row[byte];
+    if (shift + ib > 8) raw |= (uint32_t)row[byte + 1] << 8;
+    return levels[(raw >> shift) & ((1u << ib) - 1)];
+}
+
+/* LookupTable::dot_group (matrix.rs:610-620). 1-, 2- and 4-bit indices (and
+ * ternary crumbs) go through per-byte tables: lane l of the 8 / index_bits
+ * values of a byte sums entry * input over the group's bytes in order from
+ * 0.0 (dot_with, matrix.rs:540-549), then the lanes are summed in order;
+ * 3-bit indices sum value * input over the group's positions in order
+ * (Bitwise). Iterator::sum of f32 folds from -0.0 (Rust 1.87). */
+static float dot_group(const uint8_t* row, int g, int group, int ib, const float levels[16], const float* x) {
+    if (ib == 3) {
+        float s = -0.0f;
+        for (int p = 0; p < group; ++p) s = s + level_at(row, g * group + p, ib, levels) * x[p];
+        return s;
+    }
+    const int n = 8 / ib;
+    float lanes[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < group / n; ++b)
+        for (int l = 0; l < n; ++l) lanes[l] = lanes[l] + level_at(row, g * group + b * n + l, ib, levels) * x[b * n + l];
+    float s = -0.0f;
+    for (int l = 0; l < n; ++l) s = s + lanes[l];
+    return s;
+}
+
+/* fill_rows_float (matrix.rs:427-440) for `count` rotated inputs [t][padded]:
+ * per row, total = 0, then total += dot_group * norm over the groups in order. */
+void ro_codebook_float_vector(const uint8_t* packed, const uint16_t* norms, int rows, int padded, int group, int bits,
+                              const float levels[16], const float* rotated, int count, float* y) {
+    const int ib = index_bits(bits), groups = padded / group;
+    const size_t row_bytes = (size_t)padded * ib / 8;
+#pragma omp parallel for schedule(static) if ((size_t)rows * padded * count >= (1u << 22))
+    for (int r = 0; r < rows; ++r) {
+        const uint8_t* row = packed + (size_t)r * row_bytes;
+        for (int t = 0; t < count; ++t) {
+            const float* x = rotated + (size_t)t * padded;
+            float total = 0.0f;
+            for (int g = 0; g < groups; ++g)
+                total = total + dot_group(row, g, group, ib, levels, x + (size_t)g * group) *
+                                    ro_f16_to_f32(norms[(size_t)r * groups + g]);
+            y[(size_t)t * rows + r] = total;
+        }
+    }
+}
+
+/* multiply_batch's float tile (matrix.rs:356-378): the row expanded and scaled
+ * (expand_row_scaled, matrix.rs:390-399: level * norm per element), then
+ * dot (matrix.rs:488-497): eight lanes over chunks of 8 from 0.0, the lanes
+ * summed in order from -0.0. */
+void ro_codebook_float_batch(const uint8_t* packed, const uint16_t* norms, int rows, int padded, int group, int bits,
+                             const float levels[16], const float* rotated, int count, float* y) {
+    const int ib = index_bits(bits), groups = padded / group;
+    const size_t row_bytes = (size_t)padded * ib / 8;
+#pragma omp parallel for schedule(static) if ((size_t)rows * padded * count >= (1u << 22))
+    for (int r = 0; r < rows; ++r) {
+        const uint8_t* row = packed + (size_t)r * row_bytes;
+        float* w = (float*)malloc((size_t)padded * sizeof(float));
+        for (int e = 0; e < padded; ++e)
+            w[e] = level_at(row, e, ib, levels) * ro_f16_to_f32(norms[(size_t)r * groups + e / group]);
+        for (int t = 0; t < count; ++t) {
+            const float* x = rotated + (size_t)t * padded;
+            float lanes[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            for (int c = 0; c < padded / 8; ++c)
+                for (int l = 0; l < 8; ++l) lanes[l] = lanes[l] + w[8 * c + l] * x[8 * c + l];
+            float s = -0.0f;
+            for (int l = 0; l < 8; ++l) s = s + lanes[l];
+            y[(size_t)t * rows + r] = s;
+        }
+        free(w);
+    }
 }

@@ -147,6 +147,12 @@ void ro_codebook_product(const uint8_t* packed, const uint16_t* norms, int rows,
                          const float* xscales, int count, float* y, int32_t* acc);
 void ro_codebook_dequantise_row(const uint8_t* packed, const uint16_t* norms, int padded, int columns,
                                 int group, int bits, const float levels[16], int row, float* out); /* matrix.rs:140-153 */
+/* the float path: fill_rows_float (matrix.rs:427-440) and multiply_batch's
+ * float tile (matrix.rs:356-378); any width 1-5, rotated [count][padded] in */
+void ro_codebook_float_vector(const uint8_t* packed, const uint16_t* norms, int rows, int padded, int group, int bits,
+                              const float levels[16], const float* rotated, int count, float* y);
+void ro_codebook_float_batch(const uint8_t* packed, const uint16_t* norms, int rows, int padded, int group, int bits,
+                             const float levels[16], const float* rotated, int count, float* y);
 
 /* ---- speech front end (rn_frontend.c): crates/whistle/src/frontend.rs ---------- */
 void ro_frontend_tables(int fft_size, int window, float* win, float* twiddle_cos, float* twiddle_sin); /* :32-39 */

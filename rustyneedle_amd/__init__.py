@@ -145,6 +145,8 @@ SIGNATURES = {
     "rn_matrix_multiply_batch_noalloc": (_i, [_p, _p, _i, _p, _p, _p]),
     "rn_matrix_dequantise_row": (_i, [_p, _i, _p]),
     "rn_matrix_multiply_vector_host": (_i, [_p, _p, _p]),
+    "rn_matrix_multiply_vector_float": (_i, [_p, _p, _p, _p]),
+    "rn_matrix_multiply_batch_float": (_i, [_p, _p, _i, _p, _p]),
     "rn_matrix_multiply_batch_host": (_i, [_p, _p, _i, _p]),
     "rn_matrix_prepare_host": (_i, [_p, _p, _i, _p]),
     "rn_matrix_create_codebook": (_i, [_p, _sz, _i, _i, _i, _i, _p, _i, C.POINTER(_p)]),
@@ -446,6 +448,22 @@ class CodebookMatrix:
         if with_acc:
             return y, ad.download(np.int32, (count, self.rows, self.groups))
         return y
+
+    def multiply_float_host(self, rotated: np.ndarray, batch: bool = False) -> np.ndarray:
+        """The float path on rotated inputs [count][padded]: fill_rows_float, or
+        with batch multiply_batch's float tile (matrix.rs:356-440)."""
+        rotated = np.ascontiguousarray(rotated, dtype=np.float32).reshape(-1, self.padded)
+        count = rotated.shape[0]
+        xd = DeviceBuffer.from_array(rotated)
+        yd = DeviceBuffer(4 * count * self.rows)
+        if batch:
+            check(lib.rn_matrix_multiply_batch_float(self.handle, xd.ptr, count, yd.ptr, None))
+        else:
+            for t in range(count):
+                check(lib.rn_matrix_multiply_vector_float(self.handle, xd.ptr + 4 * t * self.padded,
+                                                          yd.ptr + 4 * t * self.rows, None))
+        check(lib.rn_stream_synchronize(None))
+        return yd.download(np.float32, (count, self.rows))
 
     def dequantise_row(self, row: int) -> np.ndarray:
         out = np.empty(self.columns, dtype=np.float32)

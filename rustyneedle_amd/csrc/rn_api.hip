@@ -306,8 +306,7 @@ int rn_matrix_create_codebook(const uint8_t* blob, size_t blob_bytes, int rows, 
     RN_REQUIRE(blob && codebook && out, "null argument");
     RN_REQUIRE(rows > 0 && columns > 0, "rows and columns must be positive (got %d x %d)", rows, columns);
     RN_REQUIRE(group == 64 || group == 128 || group == 256, "group must be 64, 128 or 256 (got %d)", group);
-    RN_REQUIRE(bits == 2 || bits == 4 || bits == 5,
-               "bits must be 2, 4 or 5 (ternary); 1- and 3-bit records have no integer path (got %d)", bits);
+    RN_REQUIRE(bits >= 1 && bits <= 5, "bits must be 1..4 or 5 (ternary crumbs) (got %d)", bits);
     RN_REQUIRE(codebook_len >= 28, "the codebook holds 28 levels (got %d)", codebook_len);
     const int padded = (columns + group - 1) / group * group;
     const int ib = bits == 5 ? 2 : bits;
@@ -318,9 +317,17 @@ int rn_matrix_create_codebook(const uint8_t* blob, size_t blob_bytes, int rows, 
                packed + norms);
     float levels[16] = {0};
     int count = 0;
-    if (bits == 2) {
+    if (bits == 1) {  // codebook.rs:34-37
+        const float level = sqrtf(2.0f / 3.14159265358979323846f) / sqrtf((float)group);
+        levels[0] = -level;
+        levels[1] = level;
+        count = 2;
+    } else if (bits == 2) {
         std::copy(codebook, codebook + 4, levels);
         count = 4;
+    } else if (bits == 3) {
+        std::copy(codebook + 4, codebook + 12, levels);
+        count = 8;
     } else if (bits == 4) {
         std::copy(codebook + 12, codebook + 28, levels);
         count = 16;
@@ -412,8 +419,17 @@ int rn_matrix_shape(const rn_matrix* m, int* rows, int* columns, int* group) {
     return RN_OK;
 }
 
+// 1- and 3-bit matrices have integer levels nowhere in the reference
+// (matrix.rs:559-563): every product of theirs is the float path.
+static bool float_only(const rn_matrix* m) { return m->bits == 1 || m->bits == 3; }
+
 int rn_matrix_multiply_vector(const rn_matrix* m, const float* x, float* y, int32_t* acc, void* stream) {
     RN_REQUIRE(m && x && y, "null argument");
+    if (float_only(m)) {
+        RN_REQUIRE(acc == nullptr, "1- and 3-bit matrices have no integer accumulators (the float path)");
+        RN_HIP(launch_codebook_float(m->cb, x, 1, y, false, (hipStream_t)stream));
+        return RN_OK;
+    }
     if (m->bits) {
         RN_HIP(launch_codebook_product(m->cb, x, 1, y, acc, (hipStream_t)stream));
         return RN_OK;
@@ -440,8 +456,12 @@ int rn_matrix_multiply_fused(const rn_matrix* const* ms, int count, const float*
             RN_REQUIRE(ms[i]->bits && ms[i]->cb.padded == first->cb.padded && ms[i]->group == first->group,
                        "fused matrices must share padded columns and group (matrix %d differs)", i);
         }
-        for (int i = 0; i < count; ++i)
-            RN_HIP(launch_codebook_product(ms[i]->cb, x, 1, ys[i], nullptr, (hipStream_t)stream));
+        for (int i = 0; i < count; ++i) {
+            if (float_only(ms[i]))
+                RN_HIP(launch_codebook_float(ms[i]->cb, x, 1, ys[i], false, (hipStream_t)stream));
+            else
+                RN_HIP(launch_codebook_product(ms[i]->cb, x, 1, ys[i], nullptr, (hipStream_t)stream));
+        }
         return RN_OK;
     }
     int total_rows = 0;
@@ -479,6 +499,11 @@ int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, floa
     RN_REQUIRE(count >= 0, "count must be non-negative");
     if (count == 0) return RN_OK;
     hipStream_t s = (hipStream_t)stream;
+    if (float_only(m)) {
+        RN_REQUIRE(acc == nullptr, "1- and 3-bit matrices have no integer accumulators (the float path)");
+        RN_HIP(launch_codebook_float(m->cb, x, count, y, true, s));
+        return RN_OK;
+    }
     if (m->bits) {
         RN_HIP(launch_codebook_product(m->cb, x, count, y, acc, s));
         return RN_OK;
@@ -499,6 +524,11 @@ int rn_matrix_multiply_batch_noalloc(const rn_matrix* m, const float* x, int cou
     RN_REQUIRE(count >= 0, "count must be non-negative");
     if (count == 0) return RN_OK;
     hipStream_t s = (hipStream_t)stream;
+    if (float_only(m)) {  // the float path needs no scratch
+        RN_REQUIRE(acc == nullptr, "1- and 3-bit matrices have no integer accumulators (the float path)");
+        RN_HIP(launch_codebook_float(m->cb, x, count, y, true, s));
+        return RN_OK;
+    }
     if (m->bits) {  // the codebook product quantises inside its kernel: no scratch
         RN_HIP(launch_codebook_product(m->cb, x, count, y, acc, s));
         return RN_OK;
@@ -513,6 +543,22 @@ int rn_matrix_multiply_batch_noalloc(const rn_matrix* m, const float* x, int cou
     int8_t* xq = (int8_t*)base;
     float* sx = (float*)((char*)base + kNoAllocCodeBytes);
     RN_HIP(batch_product_i8(m, x, count, y, acc, xq, sx, s));
+    return RN_OK;
+}
+
+int rn_matrix_multiply_vector_float(const rn_matrix* m, const float* rotated, float* y, void* stream) {
+    RN_REQUIRE(m && rotated && y, "null argument");
+    RN_REQUIRE(m->bits != 0, "the float path is a codebook matrix's (int8 matrices have only the integer path)");
+    RN_HIP(launch_codebook_float(m->cb, rotated, 1, y, false, (hipStream_t)stream));
+    return RN_OK;
+}
+
+int rn_matrix_multiply_batch_float(const rn_matrix* m, const float* rotated, int count, float* y, void* stream) {
+    RN_REQUIRE(m && (count == 0 || (rotated && y)), "null argument");
+    RN_REQUIRE(m->bits != 0, "the float path is a codebook matrix's (int8 matrices have only the integer path)");
+    RN_REQUIRE(count >= 0, "count must be non-negative");
+    if (count == 0) return RN_OK;
+    RN_HIP(launch_codebook_float(m->cb, rotated, count, y, true, (hipStream_t)stream));
     return RN_OK;
 }
 

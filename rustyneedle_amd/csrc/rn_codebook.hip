@@ -167,7 +167,9 @@ __global__ __launch_bounds__(1024) void cb_dequantise_kernel(CodebookParams p, i
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int bit = i * IB;
-        const int idx = (r[bit / 8] >> (bit % 8)) & ((1 << IB) - 1);
+        uint32_t raw = r[bit / 8];
+        if ((bit % 8) + IB > 8) raw |= (uint32_t)r[bit / 8 + 1] << 8;  // a 3-bit index may straddle two bytes
+        const int idx = (raw >> (bit % 8)) & ((1 << IB) - 1);
         v[i] = p.levels[idx] * norm;
     }
     wht_run<GROUP>(v, lane, p.wht_scale);
@@ -446,7 +448,108 @@ hipError_t launch_product_b(const CodebookParams& p, const float* x, int count, 
     }
 }
 
+// ---- the float path (x86-64 and the 1- and 3-bit widths) ----------------------
+//
+// The level of element e of a packed row, LSB first (matrix.rs:623-631); a
+// 3-bit index may straddle two bytes.
+__device__ __forceinline__ float cb_level(const uint8_t* row, int e, int ib, const float* levels) {
+    const int bit = e * ib, byte = bit >> 3, shift = bit & 7;
+    uint32_t raw = row[byte];
+    if (shift + ib > 8) raw |= (uint32_t)row[byte + 1] << 8;
+    return levels[(raw >> shift) & ((1u << ib) - 1)];
+}
+
+// fill_rows_float (matrix.rs:427-440) for one token (blockIdx.y) and rb rows
+// (blockIdx.x): a chain is (row, group, lane) of LookupTable::dot_group
+// (matrix.rs:610-620): lane l of the N = 8 / index_bits values of a byte sums
+// level * input over the group's bytes in order from 0.0; 3-bit groups are one
+// chain over the positions from -0.0 (N = 1). The lanes of a group are summed
+// in order from -0.0 (Iterator::sum), then one thread per row adds
+// partial * norm over the groups in order from 0.0.
+__global__ __launch_bounds__(256) void cb_float_vector_kernel(CodebookParams p, const float* x, float* y, int rb,
+                                                              int nl) {
+    extern __shared__ float sh[];  // [rb][groups][nl] lane sums, then [rb][groups] partials
+    const int ib = p.bits == 5 ? 2 : p.bits, groups = p.padded / p.group;
+    const int row0 = blockIdx.x * rb, token = blockIdx.y;
+    const float* xt = x + (size_t)token * p.padded;
+    const int per_row = groups * nl, chains = rb * per_row;
+    float* lane_s = sh;
+    float* part_s = sh + chains;
+    for (int c = threadIdx.x; c < chains; c += blockDim.x) {
+        const int r = c / per_row, rem = c - r * per_row, g = rem / nl, l = rem - g * nl;
+        const uint8_t* row = p.packed + (size_t)min(row0 + r, p.rows - 1) * p.row_bytes;
+        const int base = g * p.group;
+        float acc = nl == 1 ? -0.0f : 0.0f;
+        for (int b = 0; b < p.group / nl; ++b) {
+            const int e = base + b * nl + l;
+            acc = acc + cb_level(row, e, ib, p.levels) * xt[e];
+        }
+        lane_s[c] = acc;
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < rb * groups; q += blockDim.x) {
+        float s = lane_s[q * nl];
+        if (nl > 1) {
+            s = -0.0f;
+            for (int l = 0; l < nl; ++l) s = s + lane_s[q * nl + l];
+        }
+        part_s[q] = s;
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < rb; r += blockDim.x) {
+        const int row = row0 + r;
+        if (row >= p.rows) continue;
+        float total = 0.0f;
+        for (int g = 0; g < groups; ++g)
+            total = total + part_s[r * groups + g] * half_bits_to_float(p.norms[(size_t)row * groups + g]);
+        y[(size_t)token * p.rows + row] = total;
+    }
+}
+
+// multiply_batch's float tile (matrix.rs:356-378): the expanded row
+// (expand_row_scaled: level * norm per element, matrix.rs:390-399) dotted with
+// the input in eight lanes over chunks of 8 from 0.0 (dot, matrix.rs:488-497),
+// the lanes summed in order from -0.0. Eight threads per (token, row), one per lane.
+__global__ __launch_bounds__(256) void cb_float_batch_kernel(CodebookParams p, const float* x, int count, float* y) {
+    const int ib = p.bits == 5 ? 2 : p.bits, groups = p.padded / p.group;
+    const int l = threadIdx.x & 7;
+    const long long pair = (long long)blockIdx.x * 32 + (threadIdx.x >> 3);
+    const bool live = pair < (long long)count * p.rows;
+    const int token = live ? (int)(pair / p.rows) : 0, row = live ? (int)(pair % p.rows) : 0;
+    const uint8_t* packed = p.packed + (size_t)row * p.row_bytes;
+    const uint16_t* norms = p.norms + (size_t)row * groups;
+    const float* xt = x + (size_t)token * p.padded;
+    float acc = 0.0f;
+    for (int c = 0; c < p.padded / 8; ++c) {
+        const int e = 8 * c + l;
+        const float w = cb_level(packed, e, ib, p.levels) * half_bits_to_float(norms[e / p.group]);
+        acc = acc + w * xt[e];
+    }
+    float s = -0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s = s + __shfl(acc, (threadIdx.x & ~7) + j, 64);
+    if (live && l == 0) y[(size_t)token * p.rows + row] = s;
+}
+
 }  // namespace
+
+hipError_t launch_codebook_float(const CodebookParams& p, const float* x, int count, float* y, bool batch,
+                                 hipStream_t stream) {
+    if (count < 1 || p.rows < 1 || p.padded % p.group != 0) return hipErrorInvalidValue;
+    if (p.bits < 1 || p.bits > 5) return hipErrorInvalidValue;
+    if (batch) {
+        const long long pairs = (long long)count * p.rows;
+        rn_launch(cb_float_batch_kernel, dim3((unsigned)((pairs + 31) / 32)), dim3(256), 0, stream, p, x, count, y);
+    } else {
+        const int ib = p.bits == 5 ? 2 : p.bits, nl = ib == 3 ? 1 : 8 / ib;
+        const int per_row = (p.padded / p.group) * nl;
+        const int rb = per_row >= 256 ? 1 : 256 / per_row;
+        const size_t lds = sizeof(float) * ((size_t)rb * per_row + (size_t)rb * (p.padded / p.group));
+        if (lds > 64 * 1024) return hipErrorInvalidValue;
+        rn_launch(cb_float_vector_kernel, dim3((p.rows + rb - 1) / rb, count), dim3(256), lds, stream, p, x, y, rb, nl);
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_codebook_product(const CodebookParams& p, const float* x, int count, float* y, int32_t* acc,
                                    hipStream_t stream) {
@@ -478,6 +581,12 @@ hipError_t launch_codebook_dequantise(const CodebookParams& p, int row, float* o
     if (row < 0 || row >= p.rows || threads > 1024) return hipErrorInvalidValue;
 #define RN_DQ(B, GR) rn_launch(cb_dequantise_kernel<B, GR>, dim3(1), dim3(threads), 0, stream, p, row, out)
     switch (p.bits * 1000 + p.group) {
+        case 1064: RN_DQ(1, 64); break;
+        case 1128: RN_DQ(1, 128); break;
+        case 1256: RN_DQ(1, 256); break;
+        case 3064: RN_DQ(3, 64); break;
+        case 3128: RN_DQ(3, 128); break;
+        case 3256: RN_DQ(3, 256); break;
         case 2064: RN_DQ(2, 64); break;
         case 2128: RN_DQ(2, 128); break;
         case 2256: RN_DQ(2, 256); break;

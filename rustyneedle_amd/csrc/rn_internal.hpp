@@ -274,6 +274,11 @@ struct CodebookParams {
 // rotated [count][padded] inputs -> y [count][rows] (acc nullable: [count][rows][groups])
 hipError_t launch_codebook_product(const CodebookParams& p, const float* x, int count, float* y, int32_t* acc,
                                    hipStream_t stream);
+// The float products of any width (1-5): fill_rows_float (batch false, one
+// result per token and row in the vector order) or multiply_batch's float tile
+// (batch true); rotated [count][padded] -> y [count][rows].
+hipError_t launch_codebook_float(const CodebookParams& p, const float* x, int count, float* y, bool batch,
+                                 hipStream_t stream);
 hipError_t launch_codebook_rotate(const float* x, int count, int columns, int padded, int group, float scale,
                                   float* rotated, hipStream_t stream);
 hipError_t launch_codebook_dequantise(const CodebookParams& p, int row, float* out, hipStream_t stream);

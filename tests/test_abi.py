@@ -123,7 +123,8 @@ def test_synth_streams_are_named_and_seeded():
 def test_codebook_argument_errors_need_no_device():
     cb = rn.synthetic_codebook(128)
     blob = rn.synthetic_codebook_blob(4, 128, 128, 2)
-    for bits, group, size, columns in ((3, 128, blob.size, 128), (2, 96, blob.size, 128),
+    for bits, group, size, columns in ((6, 128, blob.size, 128), (0, 128, blob.size, 128), (3, 128, blob.size, 128),
+                                       (2, 96, blob.size, 128),
                                        (2, 128, blob.size - 1, 128), (2, 128, blob.size, 50000)):
         with pytest.raises(rn.RnError):
             rn.CodebookMatrix(blob[:size], 4, columns, group, bits, cb)
