@@ -262,6 +262,13 @@ int rn_quantise_int8(const float* x, int count, int columns, int8_t* codes, floa
 int rn_fast_exp(const float* x, float* y, int n, void* stream);
 int rn_silu(const float* x, float* y, int n, void* stream);
 
+/* f32::exp as the reference calls it (the C library's expf: ops::sigmoid,
+ * ops.rs:68-71, sinkhorn_in_place, ops.rs:198-217, ProbeHead::observe,
+ * heads.rs:138-150) and ops::sigmoid over it, elementwise on the device; equal
+ * bit for bit to glibc's x86-64 expf. Exposed for parity checks. */
+int rn_libm_exp(const float* x, float* y, int n, void* stream);
+int rn_sigmoid(const float* x, float* y, int n, void* stream);
+
 /* ops::zero_centred_norm (ops.rs:44-50) for `count` rows of `n` floats on the
  * device (n a multiple of 8, <= 4096). */
 int rn_zero_centred_norm(const float* x, const float* gain, int count, int n, float* out, void* stream);

@@ -118,6 +118,18 @@ def fast_exp(v: float) -> float:
     return lib.ro_fast_exp(float(v))
 
 
+lib.ro_libm_exp_array.restype = None
+lib.ro_libm_exp_array.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+
+
+def libm_exp_array(x: np.ndarray, sigmoid: bool = False) -> np.ndarray:
+    """The C library's expf (f32::exp), or ops::sigmoid over it, elementwise."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib.ro_libm_exp_array(x.ctypes.data, y.ctypes.data, x.size, int(sigmoid))
+    return y
+
+
 def silu(v: float) -> float:
     return lib.ro_silu(float(v))
 

@@ -42,6 +42,13 @@ float ro_fast_exp(float value) {
 /* ops.rs:73-76 */
 float ro_silu(float value) { return value / (1.0f + ro_fast_exp(-value)); }
 
+/* f32::exp and ops::sigmoid (ops.rs:68-71) over arrays: the C library's expf,
+ * which the reference's f32::exp calls. */
+void ro_libm_exp_array(const float* x, float* y, size_t n, int sigmoid) {
+#pragma omp parallel for schedule(static) num_threads(ro_get_threads())
+    for (size_t i = 0; i < n; ++i) y[i] = sigmoid ? 1.0f / (1.0f + expf(-x[i])) : expf(x[i]);
+}
+
 /* ops.rs:32-42 — max is order-free (NaN operands are ignored like f32::max). */
 float ro_peak_magnitude(const float* x, int n) {
     float peak = 0.0f;

@@ -175,6 +175,8 @@ SIGNATURES = {
     "rn_quantise_int8": (_i, [_p, _i, _i, _p, _p, _p]),
     "rn_fast_exp": (_i, [_p, _p, _i, _p]),
     "rn_silu": (_i, [_p, _p, _i, _p]),
+    "rn_libm_exp": (_i, [_p, _p, _i, _p]),
+    "rn_sigmoid": (_i, [_p, _p, _i, _p]),
     "rn_zero_centred_norm": (_i, [_p, _p, _i, _i, _p, _p]),
     "rn_attend_heads": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, _p]),
     "rn_model_create": (_i, [C.POINTER(Config), C.POINTER(WeightsHost), C.POINTER(_p)]),
@@ -583,6 +585,15 @@ def fast_exp(x: np.ndarray) -> np.ndarray:
 
 def silu(x: np.ndarray) -> np.ndarray:
     return _elementwise(lib.rn_silu, x)
+
+
+def libm_exp(x: np.ndarray) -> np.ndarray:
+    """f32::exp (the C library's expf) on the device."""
+    return _elementwise(lib.rn_libm_exp, x)
+
+
+def sigmoid(x: np.ndarray) -> np.ndarray:
+    return _elementwise(lib.rn_sigmoid, x)
 
 
 def quantise_int8(x: np.ndarray):

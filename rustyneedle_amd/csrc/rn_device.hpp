@@ -35,6 +35,53 @@ __device__ __forceinline__ float fast_exp(float value) {
 // ops.rs:73-76
 __device__ __forceinline__ float silu(float value) { return value / (1.0f + fast_exp(-value)); }
 
+// 2^(i/32) rounded to double, each less i << 47 so that adding k << 47 to the
+// entry of k mod 32 gives the bits of 2^(k/32).
+static __device__ __constant__ const uint64_t kExp2Table[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+// The C library's expf, which the reference's f32::exp calls (sigmoid,
+// ops.rs:68-71; sinkhorn_in_place, ops.rs:198-217; the probe heads' online
+// softmax, heads.rs:138-150), as glibc builds it for x86-64 with FMA: the
+// method of ARM's optimized-routines expf (Szabolcs Nagy, 2017). With
+// z = x * 32/ln2 and k = round(z), exp(x) = 2^(k/32) * 2^(r/32) for r = z - k,
+// the second factor a cubic in r; all in double, the reduction and the
+// polynomial as fused multiply-adds, one rounding to float at the end. Equal to
+// glibc 2.35's expf on every one of the 2^32 inputs.
+__device__ __forceinline__ float libm_expf(float x) {
+    const uint32_t bits = __float_as_uint(x), magnitude = bits & 0x7fffffffu;
+    if (magnitude >= 0x42b00000u) {  // |x| >= 88, infinities, NaN
+        if (bits == 0xff800000u) return 0.0f;
+        if (magnitude >= 0x7f800000u) return x + x;
+        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32.0, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32768.0, c1 = 0x1.ebfce50fac4f3p-3 / 1024.0,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_32, xd, shift);  // k in the low mantissa bits
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_32, xd, -kd);
+    const double s = __longlong_as_double((long long)(kExp2Table[ki % 32] + (ki << 47)));
+    const double z = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    return (float)(y * s);
+}
+
+// ops.rs:68-71 with the C library's expf.
+__device__ __forceinline__ float libm_sigmoid(float value) { return 1.0f / (1.0f + libm_expf(-value)); }
+
 // ops.rs:112-118 per element: round half to even, clamp to [-128, 127]; NaN -> 0.
 __device__ __forceinline__ int quantise_one(float value, float scale) {
     float q = __builtin_rintf(value / scale);

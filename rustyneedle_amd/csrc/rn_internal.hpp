@@ -342,7 +342,7 @@ hipError_t launch_quantise_rows(const float* x, int count, int columns, int8_t* 
                                 hipStream_t stream);
 hipError_t launch_norm_rows(const float* x, const float* gain, int count, int n, float eps, float* out,
                             hipStream_t stream);
-hipError_t launch_fast_exp(const float* x, float* y, int n, int silu, hipStream_t stream);
+hipError_t launch_fast_exp(const float* x, float* y, int n, int op, hipStream_t stream);  // op 0..3: fast_exp, silu, expf, sigmoid
 hipError_t launch_finish_push(const float* x, const float* gain, int n, float eps, float* hidden,
                               DecodeState* state, hipStream_t stream);
 // Second stage of the greedy argmax: reduces the per-block keys of the logits

@@ -10,7 +10,7 @@
 //     mix, the post gains, the residual mixing logits and sinkhorn_in_place
 //     (ops.rs:198-217), lanes.rs:62-83;
 //   lanes_combine_kernel: lanes.rs:86-98.
-// sigmoid and sinkhorn use expf, where the reference calls the host libm's.
+// sigmoid and sinkhorn use libm_expf, the C library's expf the reference calls.
 #include "rn_device.hpp"
 #include "rn_internal.hpp"
 
@@ -50,17 +50,15 @@ __global__ __launch_bounds__(256) void lanes_prologue_kernel(const float* stream
     }
 }
 
-__device__ __forceinline__ float sigmoid_exp(float v) { return 1.0f / (1.0f + expf(-v)); }
-
 __global__ __launch_bounds__(256) void lanes_route_kernel(LanesRouteParams p) {
     __shared__ float gate_s[kMaxLanes];
     const int tid = threadIdx.x, L = p.lanes, own = p.slot % L;
     if (tid == 0) {
         for (int lane = 0; lane < L; ++lane) {
             const float pre_offset = lane == own ? 8.0f + -4.0f : -4.0f;  // PRE_LANE_BOOST, PRE_LANE_FLOOR
-            gate_s[lane] = sigmoid_exp(p.a_pre[p.layer] * p.pre[lane] + p.b_pre[p.layer * L + lane] + pre_offset);
+            gate_s[lane] = libm_sigmoid(p.a_pre[p.layer] * p.pre[lane] + p.b_pre[p.layer * L + lane] + pre_offset);
             const float post_offset = lane == own ? 0.0f : -4.0f;  // POST_LANE_FLOOR
-            p.post[lane] = 2.0f * sigmoid_exp(p.a_post[p.layer] * p.post[lane] + p.b_post[p.layer * L + lane] +
+            p.post[lane] = 2.0f * libm_sigmoid(p.a_post[p.layer] * p.post[lane] + p.b_post[p.layer * L + lane] +
                                               post_offset);
         }
         float* m = p.residual;
@@ -69,7 +67,7 @@ __global__ __launch_bounds__(256) void lanes_route_kernel(LanesRouteParams p) {
         for (int r = 0; r < L; ++r) {  // ops.rs:199-202
             float peak = -INFINITY;
             for (int c = 0; c < L; ++c) peak = fmaxf(peak, m[r * L + c]);
-            for (int c = 0; c < L; ++c) m[r * L + c] = expf(m[r * L + c] - peak);
+            for (int c = 0; c < L; ++c) m[r * L + c] = libm_expf(m[r * L + c] - peak);
         }
         for (int it = 0; it < 20; ++it) {  // SINKHORN_ITERATIONS; sums fold from -0.0
             for (int r = 0; r < L; ++r) {

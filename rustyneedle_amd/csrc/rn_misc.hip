@@ -1,6 +1,7 @@
 // rn_misc.hip — small row kernels: per-row int8 quantisation (ops.rs:112-118),
 // the zero-centred RMSNorm (ops.rs:44-50) with the eight-lane sum of squares of
-// ops.rs:7-17, elementwise fast_exp / silu (ops.rs:73-90), and the end of a
+// ops.rs:7-17, elementwise fast_exp / silu (ops.rs:73-90), the C library's expf
+// and sigmoid over it (ops.rs:68-71), and the end of a
 // push (final norm into the session's hidden state, position advance).
 #include "rn_device.hpp"
 #include "rn_internal.hpp"
@@ -73,9 +74,12 @@ __global__ __launch_bounds__(64) void quantise_rows_kernel(const float* x, int n
     if (threadIdx.x == 0) scales[blockIdx.x] = scale;
 }
 
-__global__ void fast_exp_kernel(const float* x, float* y, int n, int apply_silu) {
+// op: 0 fast_exp, 1 silu, 2 the C library's expf, 3 sigmoid over it.
+__global__ void fast_exp_kernel(const float* x, float* y, int n, int op) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = apply_silu ? silu(x[i]) : fast_exp(x[i]);
+    if (i >= n) return;
+    const float v = x[i];
+    y[i] = op == 0 ? fast_exp(v) : op == 1 ? silu(v) : op == 2 ? libm_expf(v) : libm_sigmoid(v);
 }
 
 hipError_t launch_norm_rows(const float* x, const float* gain, int count, int n, float eps, float* out,
@@ -113,9 +117,10 @@ hipError_t launch_set_state(DecodeState* state, uint32_t token, int32_t pos, uin
     return hipGetLastError();
 }
 
-hipError_t launch_fast_exp(const float* x, float* y, int n, int apply_silu, hipStream_t stream) {
+hipError_t launch_fast_exp(const float* x, float* y, int n, int op, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    rn_launch(fast_exp_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, y, n, apply_silu);
+    if (op < 0 || op > 3) return hipErrorInvalidValue;
+    rn_launch(fast_exp_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, y, n, op);
     return hipGetLastError();
 }
 
