@@ -237,6 +237,43 @@ int rn_lanes_route(rn_lanes* lanes, int layer, int slot, const float* stream, fl
 int rn_lanes_combine(const rn_lanes* lanes, const float* post, const float* residual, const float* stream,
                      const float* block_delta, float* next, void* stream_handle);
 
+/* ---- Needle 3 (crates/model/src) --------------------------------------------------
+ * Model::from_archive + with_depth (model.rs:50-78) over an open archive: the
+ * canonical tensor order (layout.rs:176-257) with the probe heads and no audio
+ * encoder; every codebook matrix and float tensor goes to the device (the
+ * archive may be closed afterwards). depth <= 0 keeps every layer; otherwise
+ * ladder::select (RN_ERR_ARGUMENT where it returns None). Head dimensions of
+ * 64, a Hadamard size of 1024 (32 x 32 factors), d_model <= 1024. */
+typedef struct rn_n3_model rn_n3_model;
+typedef struct rn_n3_session rn_n3_session;
+int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out);
+int rn_n3_model_free(rn_n3_model* model);
+int rn_n3_model_active_layers(const rn_n3_model* model, int* layers, int* count); /* Model::active_layers */
+int rn_n3_model_output_vocab(const rn_n3_model* model, int* count);               /* geometry.rs:117-123 */
+/* Session::new (session.rs:30-42) with room for `capacity` tokens (<= 8192). */
+int rn_n3_session_create(const rn_n3_model* model, int capacity, rn_n3_session** out);
+int rn_n3_session_free(rn_n3_session* session);
+/* Session::push (session.rs:76-148) and Session::feed (session.rs:58-74). Tokens
+ * below the vocabulary; RN_ERR_ARGUMENT past the capacity. */
+int rn_n3_session_push(rn_n3_session* session, uint32_t token);
+int rn_n3_session_feed(rn_n3_session* session, const uint32_t* tokens, int count);
+int rn_n3_session_length(const rn_n3_session* session, int* length);
+/* Session::logits (session.rs:151-165): output_vocab floats (host). */
+int rn_n3_session_logits(rn_n3_session* session, float* logits);
+/* The final hidden state [d_model] and Session::cells [active + 1][d_model] (host). */
+int rn_n3_session_hidden(rn_n3_session* session, float* hidden);
+int rn_n3_session_cells(rn_n3_session* session, float* cells);
+/* Session::head_output / pooled_readout (session.rs:125-135): the head with
+ * `code`; *count is 0 when there is none (the reference's None). Host output
+ * of `capacity` floats. */
+int rn_n3_session_head_output(rn_n3_session* session, int code, float* out, int capacity, int* count);
+int rn_n3_session_pooled_readout(rn_n3_session* session, int code, float* out, int capacity, int* count);
+/* The int8 cache of a layer (attention.rs:36-44): keys / values [length][kv][64],
+ * scales [kv][length] (host). */
+int rn_n3_session_cache(rn_n3_session* session, int layer, int8_t* keys, float* key_scales, int8_t* values,
+                        float* value_scales);
+int rn_n3_session_stream(const rn_n3_session* session, void** stream);
+
 /* ---- the depth ladder (crates/model/src/ladder.rs) -------------------------------
  * ladder::order (ladder.rs:1-20): the order in which layers join as depth grows
  * (host). ladder::select (ladder.rs:22-29): the sorted first `depth` of them;

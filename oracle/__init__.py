@@ -700,3 +700,163 @@ def lanes_combine(lanes, width, post, residual, stream, delta) -> np.ndarray:
     out = np.empty((lanes, width), np.float32)
     lib.ro_lanes_combine(lanes, width, _ptr(post), _ptr(residual), _ptr(stream), _ptr(delta), _ptr(out))
     return out
+
+
+# ---- Needle 3 (rn_needle3.c) ------------------------------------------------------
+class N3Config(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("vocab", "output_vocab", "d_model", "num_heads", "num_kv_heads", "num_layers",
+                                        "qk_head_dim", "v_head_dim", "max_seq_len", "lanes", "sliding_window",
+                                        "conv_taps", "hadamard_size")] + [
+        ("global_layers", C.c_uint64), ("rope_theta", C.c_float)] + [
+        (n, C.c_int) for n in ("engram_slots", "engram_sub_dim", "engram_tables", "engram_conv_taps",
+                                "engram_dilation", "engram_seed_heads", "engram_order_count")] + [
+        ("engram_orders", C.c_int * 4), ("engram_heads_per_order", C.c_int), ("engram_site_count", C.c_int),
+        ("engram_sites", C.c_int * 16)]
+
+
+lib.ro_n3_open.restype = C.c_int
+lib.ro_n3_open.argtypes = [_p, C.c_size_t, C.c_int, C.POINTER(_p)]
+lib.ro_n3_close.argtypes = [_p]
+lib.ro_n3_config_of.restype = C.POINTER(N3Config)
+lib.ro_n3_config_of.argtypes = [_p]
+lib.ro_n3_active.restype = C.c_int
+lib.ro_n3_active.argtypes = [_p, _p]
+lib.ro_n3_session_new.restype = C.c_int
+lib.ro_n3_session_new.argtypes = [_p, C.c_int, C.POINTER(_p)]
+lib.ro_n3_session_free.argtypes = [_p]
+lib.ro_n3_push.argtypes = [_p, C.c_uint32]
+lib.ro_n3_logits.argtypes = [_p, _p]
+lib.ro_n3_pooled_readout.restype = C.c_int
+lib.ro_n3_pooled_readout.argtypes = [_p, C.c_int, _p]
+lib.ro_n3_head_output.restype = C.c_int
+lib.ro_n3_head_output.argtypes = [_p, C.c_int, _p]
+lib.ro_n3_table_indices.argtypes = [C.POINTER(N3Config), _p, C.c_int, _p]
+lib.ro_n3_attend_head.argtypes = [_p, _f, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p]
+
+
+class N3Session(C.Structure):
+    _fields_ = [("m", _p), ("length", C.c_int), ("capacity", C.c_int), ("tokens", _p), ("caches", _p),
+                ("engram_history", _p), ("engram_count", _p), ("cos_tab", _p), ("sin_tab", _p), ("hidden", _p),
+                ("cells", _p), ("peak", _p), ("total", _p), ("weighted", _p)]
+
+
+class N3Cache(C.Structure):
+    _fields_ = [("keys", _p), ("values", _p), ("key_scales", _p), ("value_scales", _p), ("history", _p),
+                ("history_count", C.c_int), ("length", C.c_int)]
+
+
+class OracleNeedle3:
+    """Model::open + with_depth over archive bytes (crates/model/src/model.rs)."""
+
+    def __init__(self, archive: bytes, depth: int = 0):
+        self._bytes = np.frombuffer(archive, np.uint8).copy()
+        h = _p()
+        rc = lib.ro_n3_open(_ptr(self._bytes), self._bytes.size, depth, C.byref(h))
+        if rc != 0:
+            raise ValueError("depth outside the ladder" if rc == -2 else "malformed or unsupported archive")
+        self.handle = h.value
+        self.config = lib.ro_n3_config_of(self.handle).contents
+        n = self.config.num_layers
+        layers = (C.c_int * n)()
+        count = lib.ro_n3_active(self.handle, layers)
+        self.active = [layers[i] for i in range(count)]
+
+    def session(self, capacity: int = 512) -> "OracleNeedle3Session":
+        return OracleNeedle3Session(self, capacity)
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            lib.ro_n3_close(self.handle)
+            self.handle = None
+
+
+class OracleNeedle3Session:
+    """Session (session.rs): push / feed (feeding equals pushing in order: the
+    batched prefill, prefill.rs:10-99, runs the same arithmetic per token),
+    logits, hidden, cells, the probe heads, and the int8 caches."""
+
+    def __init__(self, model: OracleNeedle3, capacity: int):
+        self.model = model
+        h = _p()
+        lib.ro_n3_session_new(model.handle, capacity, C.byref(h))
+        self.handle = h.value
+        self.capacity = capacity
+
+    def push(self, token: int) -> None:
+        s = C.cast(self.handle, C.POINTER(N3Session)).contents
+        if s.length >= self.capacity:
+            raise ValueError("session is full")
+        lib.ro_n3_push(self.handle, int(token))
+
+    def feed(self, tokens) -> None:
+        for t in tokens:
+            self.push(int(t))
+
+    def __len__(self) -> int:
+        return C.cast(self.handle, C.POINTER(N3Session)).contents.length
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.model.config.output_vocab, np.float32)
+        lib.ro_n3_logits(self.handle, _ptr(out))
+        return out
+
+    def hidden(self) -> np.ndarray:
+        s = C.cast(self.handle, C.POINTER(N3Session)).contents
+        d = self.model.config.d_model
+        return np.ctypeslib.as_array(C.cast(s.hidden, C.POINTER(_f)), (d,)).copy()
+
+    def cells(self) -> np.ndarray:
+        s = C.cast(self.handle, C.POINTER(N3Session)).contents
+        d = self.model.config.d_model
+        n = len(self.model.active) + 1
+        return np.ctypeslib.as_array(C.cast(s.cells, C.POINTER(_f)), (n, d)).copy()
+
+    def head_output(self, code: int) -> Optional[np.ndarray]:
+        out = np.empty(65536, np.float32)
+        n = lib.ro_n3_head_output(self.handle, code, _ptr(out))
+        return None if n < 0 else out[:n].copy()
+
+    def pooled_readout(self, code: int) -> Optional[np.ndarray]:
+        out = np.empty(1 << 20, np.float32)
+        n = lib.ro_n3_pooled_readout(self.handle, code, _ptr(out))
+        return None if n < 0 else out[:n].copy()
+
+    def cache(self, layer: int):
+        """keys [length][kv][qk] int8, key_scales [kv][length], values, value_scales."""
+        c = self.model.config
+        s = C.cast(self.handle, C.POINTER(N3Session)).contents
+        k = C.cast(s.caches, C.POINTER(N3Cache))[layer]
+        n = s.length
+        cap = self.capacity
+        keys = np.ctypeslib.as_array(C.cast(k.keys, C.POINTER(C.c_int8)), (cap, c.num_kv_heads, c.qk_head_dim))
+        values = np.ctypeslib.as_array(C.cast(k.values, C.POINTER(C.c_int8)), (cap, c.num_kv_heads, c.v_head_dim))
+        ks = np.ctypeslib.as_array(C.cast(k.key_scales, C.POINTER(_f)), (c.num_kv_heads, cap))
+        vs = np.ctypeslib.as_array(C.cast(k.value_scales, C.POINTER(_f)), (c.num_kv_heads, cap))
+        return keys[:n].copy(), ks[:, :n].copy(), values[:n].copy(), vs[:, :n].copy()
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            lib.ro_n3_session_free(self.handle)
+            self.handle = None
+
+
+def n3_table_indices(config: N3Config, tokens, position: int) -> list:
+    t = np.ascontiguousarray(tokens, np.uint32)
+    n = config.engram_order_count * config.engram_heads_per_order
+    out = np.empty(max(n, 1), np.int32)
+    lib.ro_n3_table_indices(C.byref(config), _ptr(t), position, _ptr(out))
+    return out[:n].tolist()
+
+
+def n3_attend_head(query, query_scale, keys, key_scales, values, value_scales) -> np.ndarray:
+    """kernels/src/attention.rs:53-80 over int8 keys [count][qk], values [count][vd]."""
+    q = np.ascontiguousarray(query, np.int8)
+    k = np.ascontiguousarray(keys, np.int8)
+    v = np.ascontiguousarray(values, np.int8)
+    ks, vs = _f32(key_scales), _f32(value_scales)
+    count, qk = k.shape
+    vd = v.shape[1]
+    out = np.empty(vd, np.float32)
+    lib.ro_n3_attend_head(_ptr(q), float(query_scale), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), count, qk, vd, qk, vd,
+                          _ptr(out))
+    return out

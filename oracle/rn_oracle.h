@@ -270,6 +270,102 @@ void ro_whistle_logits(const ro_wconfig* c, const ro_wmodel* m, const ro_wsessio
 void ro_whistle_greedy(const ro_wconfig* c, const ro_wmodel* m, ro_wsession* s, uint32_t first, int steps,
                        uint32_t* ids);
 
+/* ---- Needle 3 (rn_needle3.c): crates/model/src, crates/cact/src --------------- */
+/* A codebook matrix (QuantisedMatrix, matrix.rs:14-59) over the archive's blob. */
+typedef struct {
+    const uint8_t* packed;
+    const uint16_t* norms;
+    int rows, columns, padded, group, bits, groups;
+    size_t row_bytes;
+    float levels[16];
+    int8_t table[16];
+    float lscale;
+    int integer; /* the integer path (2-, 4-bit, ternary) */
+} ro_cbm;
+void ro_cbm_init(ro_cbm* m, const uint8_t* blob, int rows, int columns, int group, int bits, const float* codebook);
+void ro_cbm_prepare(const ro_cbm* m, const float* x, float* rotated);                    /* matrix.rs:123-128 */
+void ro_cbm_rows(const ro_cbm* m, int first, int n, const float* rotated, float* y);    /* matrix.rs:402-421 */
+void ro_cbm_dequantise_row(const ro_cbm* m, int row, float* out);                       /* matrix.rs:140-153 */
+
+typedef struct { /* ModelConfig (config.rs:17-35) */
+    int vocab, output_vocab, d_model, num_heads, num_kv_heads, num_layers, qk_head_dim, v_head_dim, max_seq_len;
+    int lanes, sliding_window, conv_taps, hadamard_size;
+    uint64_t global_layers;
+    float rope_theta;
+    int engram_slots, engram_sub_dim, engram_tables, engram_conv_taps, engram_dilation, engram_seed_heads;
+    int engram_order_count, engram_orders[4], engram_heads_per_order, engram_site_count, engram_sites[16];
+} ro_n3_config;
+typedef struct { /* HadamardWeights (hadamard.rs:8-21) */
+    int size, rank;
+    float *d1, *d2, *b2, *d3, *d4, *cond_v, *cond_u;
+    float* factors[6]; /* w1a w1b w2a w2b w3a w3b */
+    int factor_sizes[6];
+} ro_n3_hadamard;
+typedef struct { /* LayerWeights + AttentionWeights (weights.rs:11-18, attention.rs:11-20) */
+    float *norm_in, *q_norm, *k_norm, *post_norm, *pre_hadamard_norm;
+    float attention_gate;
+    float* taps[3];
+    ro_cbm q, k, v, gate, out;
+    ro_n3_hadamard hadamard;
+} ro_n3_layer;
+typedef struct { ro_cbm tables, key, value; float* taps; } ro_n3_engram; /* engram.rs:13-18 */
+typedef struct { /* ProbeHead after with_rows (heads.rs:6-18) */
+    int code, layers, probes_per_layer, queries, width;
+    float *probes, *gain, *query, *row_bias, *bias;
+    ro_cbm projection;
+} ro_n3_head;
+typedef struct {
+    ro_n3_config config;
+    float codebook[28];
+    void* records;
+    ro_cbm embedding;
+    ro_n3_layer* layers;
+    float *a_pre, *a_post, *a_res, *b_pre, *b_post, *b_res;
+    ro_cbm phi_pre, phi_post, phi_res;
+    int32_t* permutations[2];
+    ro_n3_engram* engrams;
+    float* final_norm;
+    ro_n3_head* heads;
+    int head_count;
+    int* active;
+    int active_count;
+} ro_n3_model;
+typedef struct { /* AttentionCache (attention.rs:36-44), dense: keys [cap][kv][qk], scales [kv][cap] */
+    int8_t *keys, *values;
+    float *key_scales, *value_scales;
+    float* history; /* [conv_taps][q | k | v] newest first */
+    int history_count, length;
+} ro_n3_cache;
+typedef struct {
+    const ro_n3_model* m;
+    int length, capacity;
+    uint32_t* tokens;
+    ro_n3_cache* caches;
+    float** engram_history;
+    int* engram_count;
+    float *cos_tab, *sin_tab;
+    float *hidden, *cells;
+    float **peak, **total, **weighted;
+} ro_n3_session;
+/* Model::open over archive bytes (kept by the caller), then with_depth (depth
+ * <= 0: every layer). 0, -1 malformed or unsupported, -2 depth outside the ladder. */
+int ro_n3_open(const uint8_t* bytes, size_t size, int depth, ro_n3_model** out);
+void ro_n3_close(ro_n3_model* m);
+const ro_n3_config* ro_n3_config_of(const ro_n3_model* m);
+int ro_n3_active(const ro_n3_model* m, int* layers);
+int ro_n3_session_new(const ro_n3_model* m, int capacity, ro_n3_session** out);
+void ro_n3_session_free(ro_n3_session* s);
+void ro_n3_push(ro_n3_session* s, uint32_t token);                                  /* session.rs:76-148 */
+void ro_n3_logits(const ro_n3_session* s, float* logits);                           /* session.rs:151-165 */
+int ro_n3_pooled_readout(const ro_n3_session* s, int code, float* pooled);          /* heads.rs:99-125 */
+int ro_n3_head_output(const ro_n3_session* s, int code, float* out);                /* heads.rs:127-136 */
+void ro_n3_table_indices(const ro_n3_config* c, const uint32_t* tokens, int position, int* indices); /* engram.rs:30-46 */
+void ro_n3_hadamard_apply(const ro_n3_hadamard* h, const int32_t* first_perm, const int32_t* second_perm,
+                          const float* input, int width, float* output);            /* hadamard.rs:55-107 */
+void ro_n3_attend_head(const int8_t* query, float query_scale, const int8_t* keys, const float* key_scales,
+                       const int8_t* values, const float* value_scales, int count, int qk, int vd, int key_stride,
+                       int value_stride, float* out);                                /* kernels/src/attention.rs:53-80 */
+
 #ifdef __cplusplus
 }
 #endif

@@ -219,6 +219,22 @@ SIGNATURES = {
     "rn_whistle_logits": (_i, [_p, _p]),
     "rn_whistle_decode_greedy": (_i, [_p, _u32, _i, _p]),
     "rn_whistle_stream": (_i, [_p, C.POINTER(_p)]),
+    "rn_n3_model_open": (_i, [_p, _i, C.POINTER(_p)]),
+    "rn_n3_model_free": (_i, [_p]),
+    "rn_n3_model_active_layers": (_i, [_p, _p, C.POINTER(_i)]),
+    "rn_n3_model_output_vocab": (_i, [_p, C.POINTER(_i)]),
+    "rn_n3_session_create": (_i, [_p, _i, C.POINTER(_p)]),
+    "rn_n3_session_free": (_i, [_p]),
+    "rn_n3_session_push": (_i, [_p, _u32]),
+    "rn_n3_session_feed": (_i, [_p, _p, _i]),
+    "rn_n3_session_length": (_i, [_p, C.POINTER(_i)]),
+    "rn_n3_session_logits": (_i, [_p, _p]),
+    "rn_n3_session_hidden": (_i, [_p, _p]),
+    "rn_n3_session_cells": (_i, [_p, _p]),
+    "rn_n3_session_head_output": (_i, [_p, _i, _p, _i, C.POINTER(_i)]),
+    "rn_n3_session_pooled_readout": (_i, [_p, _i, _p, _i, C.POINTER(_i)]),
+    "rn_n3_session_cache": (_i, [_p, _i, _p, _p, _p, _p]),
+    "rn_n3_session_stream": (_i, [_p, C.POINTER(_p)]),
     "rn_synth_codes": (_i, [_u64, C.c_char_p, _p, _sz]),
     "rn_synth_uniform": (_i, [_u64, C.c_char_p, _f, _f, _p, _sz]),
     "rn_synth_normal": (_i, [_u64, C.c_char_p, _f, _p, _sz]),

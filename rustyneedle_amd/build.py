@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librustyneedle_hip.so")
 SOURCES = ["rn_gemv.hip", "rn_attention.hip", "rn_gemm.hip", "rn_misc.hip", "rn_whistle.hip", "rn_codebook.hip",
-           "rn_lanes.hip", "rn_api.hip", "rn_archive.cpp", "rn_synth.cpp"]
+           "rn_lanes.hip", "rn_needle3.hip", "rn_api.hip", "rn_archive.cpp", "rn_synth.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math",

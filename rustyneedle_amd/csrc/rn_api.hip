@@ -27,6 +27,7 @@
 
 #include "../../include/rustyneedle.h"
 #include "rn_internal.hpp"
+#include "rn_matrix.hpp"
 
 using namespace rn;
 
@@ -87,21 +88,6 @@ int check_supported(int columns) {
 namespace rn {
 int set_error(int code, const char* message) { return fail(code, "%s", message); }
 }  // namespace rn
-
-struct rn_matrix {
-    int8_t* W = nullptr;
-    float* sW = nullptr;
-    int rows = 0, columns = 0, group = 0, form = 0;
-    int bits = 0;                  // 0: int8 codes; 2, 4 or 5 (ternary): codebook indices
-    unsigned char* blob = nullptr;  // codebook blob: packed indices, fp16 norms, padding
-    CodebookParams cb{};
-    // staging of the host-slice entry points: a stream and a device buffer for
-    // the input and output slices, made on first use; calls hold the mutex
-    mutable std::mutex host_mu;
-    mutable hipStream_t host_stream = nullptr;
-    mutable char* host_buf = nullptr;
-    mutable size_t host_bytes = 0;
-};
 
 struct rn_model {
     rn_config cfg{};

@@ -1,0 +1,1548 @@
+// rn_needle3.hip — the Needle 3 token step (crates/model/src) on gfx950: the
+// model read from a .cact archive in its canonical order (crates/cact/src/
+// layout.rs:176-257), Session::push / feed / logits (session.rs:58-165) and the
+// probe heads (heads.rs:84-150), every float in the reference's order.
+//
+// Device memory
+//   model   : every codebook matrix as its archive blob (rn_matrix); the float
+//             tensors (norm gains, conv taps, Hadamard diagonals, factors and
+//             condition matrices, lane tensors, engram taps, final gains, the
+//             dense probe and query rows of the heads) in one allocation each;
+//             the two permutations as int32.
+//   session : per layer the int8 cache, keys and values [kv][capacity][64]
+//             with their scales [kv][capacity], and the conv-tap ring
+//             [taps][q | k | v] (slot = position mod taps); per engram site
+//             the ring of raw values [(taps - 1) * dilation + 1][d_model]; two
+//             lane streams [lanes][d_model]; the cells [active + 1][d_model];
+//             the head accumulators; the rotary table [capacity][32] (host
+//             cosf / sinf, as the reference's sin_cos); scratch.
+//
+// Kernels of one push (host-driven, on the session's stream)
+//   n3_stream_init    embedding row times sqrt(d) into every lane, cell 0;
+//   n3_gather         engram: the tables' rows of the hashed slots, dequantised
+//                     and fake-quantised (engram.rs:66-82);
+//   n3_engram_conv    the value taps over the site's ring (engram.rs:84-111);
+//   lanes route       rn_lanes (lanes.rs:48-84);
+//   n3_block_in       add_engram (session.rs:175-188), the input norm and the
+//                     fake quantisation before the projections;
+//   n3_qkv            conv taps (attention.rs:84-94), q/k norms, rotary, the
+//                     per-head int8 codes and the cache append;
+//   n3_attend         attend_head per query head (kernels/src/attention.rs:
+//                     53-80 as the aarch64 build runs it) times sigmoid(gate);
+//   n3_fake_quantise  the gated attention before the output projection;
+//   n3_block_out      post norm and gate, the Hadamard MLP (hadamard.rs:55-107,
+//                     three 32 x 32 Kronecker products), block delta, lane
+//                     combine and the cell (lanes.rs:86-104);
+//   n3_final          lane mean and the final norm;
+//   n3_observe        the heads' online softmax (heads.rs:138-155).
+// The products are rn_codebook.hip's launches on rotated inputs.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/rustyneedle.h"
+#include "rn_device.hpp"
+#include "rn_internal.hpp"
+#include "rn_matrix.hpp"
+
+namespace rn {
+
+constexpr int kN3Block = 1024;
+constexpr int kN3MaxWidth = 4096;     // stream, gathered rows, attention width
+constexpr int kN3MaxAttend = 8192;    // positions one head attends
+constexpr int kN3Head = 64;           // qk_head_dim = v_head_dim
+constexpr int kN3MaxTables = 16;
+constexpr int kN3Hadamard = 1024;     // 32 x 32
+
+namespace {
+
+// The maximum over the block (every thread calls; all get the result).
+__device__ float n3_block_max(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = (blockDim.x + 63) >> 6;
+    v = wave_max(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int w = 1; w < waves; ++w) r = fmaxf(r, red[w]);
+    __syncthreads();
+    return r;
+}
+
+// ops.rs:7-17 over n values in LDS: eight strided lanes, summed in lane order,
+// then the tail. Every thread calls; all get the result.
+__device__ float n3_sum_of_squares(const float* v, int n, float* red) {
+    const int tid = threadIdx.x;
+    if (tid < 8) {
+        float s = 0.0f;
+        for (int c = 0; c < n / 8; ++c) {
+            const float x = v[8 * c + tid];
+            s = s + x * x;
+        }
+        red[tid] = s;
+    }
+    __syncthreads();
+    float total = 0.0f;
+    for (int j = 0; j < 8; ++j) total = total + red[j];
+    float tail = -0.0f;
+    for (int i = n / 8 * 8; i < n; ++i) tail = tail + v[i] * v[i];
+    __syncthreads();
+    return total + tail;
+}
+
+// ops.rs:44-58: out = ((1 + gain) * x) * inverse (out may be x)
+__device__ void n3_norm(const float* x, const float* gain, int n, float* out, float* red) {
+    const float mean_square = n3_sum_of_squares(x, n, red) / (float)n;
+    const float inverse = 1.0f / sqrtf(mean_square + 1e-6f);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = ((1.0f + gain[i]) * x[i]) * inverse;
+    __syncthreads();
+}
+
+// ops.rs:60-66
+__device__ void n3_unit_rms(const float* x, int n, float* out, float* red) {
+    const float inverse = 1.0f / sqrtf(n3_sum_of_squares(x, n, red) / (float)n + 1e-6f);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inverse;
+    __syncthreads();
+}
+
+// ops.rs:120-125 in place over LDS
+__device__ void n3_fake_quantise(float* v, int n, float* red) {
+    float peak = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) peak = fmaxf(peak, fabsf(v[i]));
+    peak = n3_block_max(peak, red);
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float q = __builtin_rintf(v[i] / scale);
+        q = q < -128.0f ? -128.0f : (q > 127.0f ? 127.0f : q);
+        v[i] = q * scale;
+    }
+    __syncthreads();
+}
+
+// the level index of element e of a packed row (LSB first; 3-bit indices may
+// straddle two bytes)
+__device__ __forceinline__ int n3_index(const uint8_t* row, int e, int ib) {
+    const int bit = e * ib;
+    uint32_t raw = row[bit / 8];
+    if ((bit % 8) + ib > 8) raw |= (uint32_t)row[bit / 8 + 1] << 8;
+    return (raw >> (bit % 8)) & ((1 << ib) - 1);
+}
+
+}  // namespace
+
+// ---- kernels ---------------------------------------------------------------
+
+// session.rs:89-97: every lane holds the embedding row times sqrt(d); cell 0 is
+// their lane mean (session.rs:190-200).
+__global__ void n3_stream_init_kernel(const float* row, int d, int lanes, float scale, float* stream, float* cell) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= d) return;
+    const float v = row[i] * scale;
+    float mean = 0.0f;
+    for (int l = 0; l < lanes; ++l) {
+        stream[(size_t)l * d + i] = v;
+        mean = mean + v / (float)lanes;
+    }
+    cell[i] = mean;
+}
+
+struct N3GatherParams {
+    CodebookParams tables;
+    int count, sub, slots, position;
+    int index[kN3MaxTables];
+    int order[kN3MaxTables];
+    float* out;  // [count * sub]
+};
+
+// engram.rs:66-82: row table * slots + index of each table (zeros while the
+// position is shorter than the table's order), dequantised (matrix.rs:140-153),
+// then fake_quantise_int8 over the whole gathered vector.
+__global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherParams p) {
+    __shared__ float buf[kN3MaxWidth];
+    __shared__ float red[32];
+    const CodebookParams& c = p.tables;
+    const int n = p.count * p.sub, ib = c.bits == 5 ? 2 : c.bits, G = c.padded / c.group;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        const int t = e / p.sub, j = e - t * p.sub;
+        float v = 0.0f;
+        if (p.position + 1 >= p.order[t]) {
+            const int row = t * p.slots + p.index[t];
+            const float norm = __half2float(__ushort_as_half(c.norms[(size_t)row * G + j / c.group]));
+            v = c.levels[n3_index(c.packed + (size_t)row * c.row_bytes, j, ib)] * norm;
+        }
+        buf[e] = v;
+    }
+    __syncthreads();
+    // walsh.rs:41-76 per group of the rows: butterflies of span 1, 2, 4, ...
+    // (low a + b, high a - b), then every value times 1 / sqrt(group)
+    const int half = c.group / 2;
+    for (int span = 1; span < c.group; span *= 2) {
+        for (int q = threadIdx.x; q < n / 2; q += blockDim.x) {
+            const int g = q / half, w = q - g * half;
+            const int lo = g * c.group + (w / span) * 2 * span + (w % span), hi = lo + span;
+            const float a = buf[lo], b = buf[hi];
+            buf[lo] = a + b;
+            buf[hi] = a - b;
+        }
+        __syncthreads();
+    }
+    for (int e = threadIdx.x; e < n; e += blockDim.x) buf[e] = buf[e] * c.wht_scale;
+    __syncthreads();
+    n3_fake_quantise(buf, n, red);
+    for (int e = threadIdx.x; e < n; e += blockDim.x) p.out[e] = buf[e];
+}
+
+// engram.rs:84-111: the raw value joins the ring (slot position mod keep);
+// value = sum over taps of gain * the raw value `tap * dilation` back.
+__global__ void n3_engram_conv_kernel(const float* raw, float* ring, const float* taps, int position, int keep,
+                                      int ntaps, int dilation, int width, float* value) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= width) return;
+    const float r = raw[i];
+    ring[(size_t)(position % keep) * width + i] = r;
+    float v = 0.0f;
+    for (int tap = 0; tap < ntaps; ++tap) {
+        const int back = tap * dilation;
+        if (position < back) continue;
+        const float sample = back == 0 ? r : ring[(size_t)((position - back) % keep) * width + i];
+        v = v + taps[(size_t)tap * width + i] * sample;
+    }
+    value[i] = v;
+}
+
+struct N3BlockInParams {
+    const float* input;   // the routed input [d]
+    const float* key;     // engram key [d] or null
+    const float* value;   // engram value [d]
+    const float* norm_in;
+    int d;
+    float* x;             // [d]
+    float* quantised;     // [d] fake-quantised norm of x
+};
+
+// session.rs:112-118 with add_engram (session.rs:175-188).
+__global__ __launch_bounds__(kN3Block) void n3_block_in_kernel(N3BlockInParams p) {
+    __shared__ float xs[kN3MaxWidth], ta[kN3MaxWidth], tb[kN3MaxWidth];
+    __shared__ float red[32];
+    __shared__ float alpha_s;
+    const int d = p.d;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) xs[i] = p.input[i];
+    __syncthreads();
+    if (p.key != nullptr) {
+        n3_unit_rms(xs, d, ta, red);
+        for (int i = threadIdx.x; i < d; i += blockDim.x) tb[i] = p.key[i];
+        __syncthreads();
+        n3_unit_rms(tb, d, tb, red);
+        if (threadIdx.x == 0) {  // Iterator::sum: in order from -0.0
+            float dot = -0.0f;
+            for (int i = 0; i < d; ++i) dot = dot + ta[i] * tb[i];
+            alpha_s = libm_sigmoid(dot / sqrtf((float)d));
+        }
+        __syncthreads();
+        const float alpha = alpha_s;
+        for (int i = threadIdx.x; i < d; i += blockDim.x) xs[i] = xs[i] + alpha * p.value[i];
+        __syncthreads();
+    }
+    n3_norm(xs, p.norm_in, d, ta, red);
+    n3_fake_quantise(ta, d, red);
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        p.x[i] = xs[i];
+        p.quantised[i] = ta[i];
+    }
+}
+
+struct N3QkvParams {
+    const float* prod;     // q | k | v | gate projections of this token
+    float* hist;           // conv-tap ring [taps][q | k | v]
+    const float* taps[3];  // [taps][width] for q, k, v
+    int ntaps, position, H, KV, cap;
+    const float* q_norm;
+    const float* k_norm;
+    const float* cos_row;  // [32] at this position
+    const float* sin_row;
+    int8_t* qcodes;        // [H][64]
+    float* qscales;        // [H]
+    int8_t* keys;          // [KV][cap][64]
+    float* key_scales;     // [KV][cap]
+    int8_t* values;
+    float* value_scales;
+};
+
+// attention.rs:110-141: conv taps over the raw q/k/v ring, per-head norms and
+// rotary for q and k, int8 codes per head, the cache append. One wave per head
+// (blocks 0..H-1 the queries, then the key and value heads).
+__global__ __launch_bounds__(64) void n3_qkv_kernel(N3QkvParams p) {
+    __shared__ float v_s[kN3Head];
+    __shared__ float red[8];
+    const int b = blockIdx.x, lane = threadIdx.x;
+    const int which = b < p.H ? 0 : (b < p.H + p.KV ? 1 : 2);
+    const int h = which == 0 ? b : (which == 1 ? b - p.H : b - p.H - p.KV);
+    const int qw = p.H * kN3Head, kw = p.KV * kN3Head, total = qw + 2 * kw;
+    const int width = which == 0 ? qw : kw, off = which == 0 ? 0 : (which == 1 ? qw : qw + kw);
+    const int col = h * kN3Head + lane;
+    const float raw = p.prod[off + col];
+    float v = raw;
+    if (p.ntaps > 0) {
+        p.hist[(size_t)(p.position % p.ntaps) * total + off + col] = raw;
+        const int n = min(p.ntaps, p.position + 1);
+        v = 0.0f;
+        for (int tap = 0; tap < n; ++tap) {
+            const float sample = tap == 0 ? raw : p.hist[(size_t)((p.position - tap) % p.ntaps) * total + off + col];
+            v = v + p.taps[which][(size_t)tap * width + col] * sample;
+        }
+    }
+    if (which < 2) {
+        // ops.rs:52-58 over the head, then ops.rs:131-141
+        v_s[lane] = v;
+        __syncthreads();
+        if (lane < 8) {
+            float s = 0.0f;
+            for (int c = 0; c < kN3Head / 8; ++c) s = s + v_s[8 * c + lane] * v_s[8 * c + lane];
+            red[lane] = s;
+        }
+        __syncthreads();
+        float ss = 0.0f;
+        for (int j = 0; j < 8; ++j) ss = ss + red[j];
+        const float inverse = 1.0f / sqrtf(ss / (float)kN3Head + 1e-6f);
+        const float* gain = which == 0 ? p.q_norm : p.k_norm;
+        v = ((1.0f + gain[lane]) * v) * inverse;
+        __syncthreads();
+        v_s[lane] = v;
+        __syncthreads();
+        const int half = kN3Head / 2;
+        if (lane < half) {
+            const float a = v_s[lane], bb = v_s[lane + half];
+            v = a * p.cos_row[lane] - bb * p.sin_row[lane];
+        } else {
+            const int i = lane - half;
+            const float a = v_s[i], bb = v_s[lane];
+            v = bb * p.cos_row[i] + a * p.sin_row[i];
+        }
+    }
+    // ops.rs:112-118
+    const float peak = wave_max(fabsf(v));
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const int8_t code = (int8_t)quantise_one(v, scale);
+    if (which == 0) {
+        p.qcodes[col] = code;
+        if (lane == 0) p.qscales[h] = scale;
+    } else {
+        const size_t row = (size_t)h * p.cap + p.position;
+        (which == 1 ? p.keys : p.values)[row * kN3Head + lane] = code;
+        if (lane == 0) (which == 1 ? p.key_scales : p.value_scales)[row] = scale;
+    }
+}
+
+struct N3AttendParams {
+    const int8_t* qcodes;
+    const float* qscales;
+    const int8_t* keys;    // [KV][cap][64]
+    const float* key_scales;
+    const int8_t* values;
+    const float* value_scales;
+    const float* gate;     // [H][64] gate projections
+    int cap, first, count, group;
+    float inverse_root;
+    float* out;            // [H][64]
+};
+
+// kernels/src/attention.rs:53-80 for query head blockIdx.x over positions
+// [first, first + count), then times sigmoid(gate) (attention.rs:147-149).
+// Scores are exact; coefficients ((float)score * key_scale) * query_scale; the
+// exponent total is the aarch64 build's: four lane sums over the first
+// count - count % 4 positions (position p in lane p % 4, in order), added as
+// (l0 + l1) + (l2 + l3), then the remaining positions in order
+// (neon.rs:278-311). The weights round(c / (peak / 2047)) (half away from
+// zero) times the value codes sum exactly in int32 (neon.rs:347-438).
+__global__ __launch_bounds__(256) void n3_attend_kernel(N3AttendParams p) {
+    __shared__ float c_s[kN3MaxAttend];  // scores, then the exponents
+    __shared__ int part[16][kN3Head];
+    __shared__ float red[8];
+    __shared__ float lanes_s[4];
+    const int h = blockIdx.x, tid = threadIdx.x, kvh = h / p.group, count = p.count;
+    const float query_scale = p.qscales[h] * p.inverse_root;
+    int4 q[4];
+    const int4* qs = reinterpret_cast<const int4*>(p.qcodes + (size_t)h * kN3Head);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = qs[i];
+    const int8_t* kbase = p.keys + ((size_t)kvh * p.cap + p.first) * kN3Head;
+    const float* ks = p.key_scales + (size_t)kvh * p.cap + p.first;
+    const float* vs = p.value_scales + (size_t)kvh * p.cap + p.first;
+    float peak = -INFINITY;
+    for (int pp = tid; pp < count; pp += 256) {
+        const int4* k = reinterpret_cast<const int4*>(kbase + (size_t)pp * kN3Head);
+        int score = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) score = dot16(q[i], k[i], score);
+        const float c = ((float)score * ks[pp]) * query_scale;
+        c_s[pp] = c;
+        peak = fmaxf(peak, c);
+    }
+    peak = n3_block_max(peak, red);
+    // the exponents, and the peak of the coefficients e * value_scale
+    float cpeak = 0.0f;
+    for (int pp = tid; pp < count; pp += 256) {
+        const float e = fast_exp(c_s[pp] - peak);
+        c_s[pp] = e;
+        cpeak = fmaxf(cpeak, fabsf(e * vs[pp]));
+    }
+    cpeak = n3_block_max(cpeak, red);  // its barrier orders the exponents before the reads below
+    const int vector_count = count - count % 4;
+    if (tid < 4) {
+        float s = 0.0f;
+        for (int pp = tid; pp < vector_count; pp += 4) s = s + c_s[pp];
+        lanes_s[tid] = s;
+    }
+    const float scale = cpeak / 2047.0f;
+    const int dg = tid & 15, pc = tid >> 4;
+    int acc[4] = {0, 0, 0, 0};
+    if (cpeak > 0.0f) {
+        const int8_t* vbase = p.values + ((size_t)kvh * p.cap + p.first) * kN3Head + 4 * dg;
+        for (int pp = pc; pp < count; pp += 16) {
+            const int w = (int)__builtin_roundf((c_s[pp] * vs[pp]) / scale);
+            if (w == 0) continue;
+            const int packed = *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[k] += w * (int)(int8_t)(packed >> (8 * k));
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) part[pc][4 * dg + k] = acc[k];
+    __syncthreads();
+    if (tid < kN3Head) {
+        int sum = 0;
+        for (int c = 0; c < 16; ++c) sum += part[c][tid];
+        float total = (lanes_s[0] + lanes_s[1]) + (lanes_s[2] + lanes_s[3]);
+        for (int pp = vector_count; pp < count; ++pp) total = total + c_s[pp];
+        float o = cpeak > 0.0f ? (float)sum * scale : 0.0f;
+        o = o * (1.0f / total);
+        o = o * libm_sigmoid(p.gate[(size_t)h * kN3Head + tid]);
+        p.out[(size_t)h * kN3Head + tid] = o;
+    }
+}
+
+// ops.rs:120-125 over n <= 4096 values (one block)
+__global__ __launch_bounds__(kN3Block) void n3_fake_quantise_kernel(const float* in, int n, float* out) {
+    __shared__ float buf[kN3MaxWidth];
+    __shared__ float red[32];
+    for (int i = threadIdx.x; i < n; i += blockDim.x) buf[i] = in[i];
+    __syncthreads();
+    n3_fake_quantise(buf, n, red);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = buf[i];
+}
+
+struct N3BlockOutParams {
+    const float* attention;    // out projection [d]
+    const float* post_norm;
+    float gate;                // sigmoid(attention_gate)
+    const float* pre_norm;
+    const float *d1, *d2, *b2, *d3, *d4;
+    const float* factors[6];   // w1a w1b w2a w2b w3a w3b, [32][32]
+    const float* cond_v;       // [d][rank]
+    const float* cond_u;       // [rank][1024]
+    int rank;
+    const int32_t* perm1;
+    const int32_t* perm2;
+    const float* x;            // block input after the attention input norm
+    const float* input;        // routed input
+    const float* post;         // [lanes]
+    const float* residual;     // [lanes][lanes]
+    const float* stream;       // [lanes][d]
+    int d, lanes;
+    float* next;               // [lanes][d]
+    float* cell;               // [d]
+};
+
+// kronecker_apply for 32 x 32 factors (ops.rs:220-297): mixed = X . R, then
+// out = L^T . mixed, each a chain of fused multiply-adds in index order.
+// 1024 threads; x and out in LDS (distinct), mixed LDS scratch.
+__device__ void n3_kronecker32(const float* x, const float* left, const float* right, float* mixed, float* out) {
+    const int tid = threadIdx.x, i = tid >> 5, c = tid & 31;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int j = 0; j < 32; ++j) acc = __builtin_fmaf(right[j * 32 + c], x[i * 32 + j], acc);
+    mixed[tid] = acc;
+    __syncthreads();
+    acc = 0.0f;
+#pragma unroll 8
+    for (int r = 0; r < 32; ++r) acc = __builtin_fmaf(mixed[r * 32 + c], left[r * 32 + i], acc);
+    out[tid] = acc;
+    __syncthreads();
+}
+
+// session.rs:119-146 from the output projection: post norm, gated residual,
+// the pre-Hadamard norm, HadamardWeights::apply, the block delta, the lane
+// combine and the next cell. One block of 1024 threads (the Hadamard size).
+__global__ __launch_bounds__(kN3Block) void n3_block_out_kernel(N3BlockOutParams p) {
+    __shared__ float xs[kN3Hadamard], a[kN3Hadamard], sc[kN3Hadamard], st[kN3Hadamard], mx[kN3Hadamard];
+    __shared__ float modulation[kN3Hadamard];
+    __shared__ float chains[4][8];
+    __shared__ float weights[64];
+    __shared__ float red[32];
+    const int tid = threadIdx.x, d = p.d;
+    for (int i = tid; i < d; i += blockDim.x) {
+        a[i] = p.attention[i];
+        xs[i] = p.x[i];
+    }
+    __syncthreads();
+    n3_norm(a, p.post_norm, d, a, red);
+    for (int i = tid; i < d; i += blockDim.x) xs[i] = xs[i] + p.gate * a[i];
+    __syncthreads();
+    n3_norm(xs, p.pre_norm, d, a, red);  // a = pre
+    // condition weights (hadamard.rs:57-79)
+    if (p.rank == 8) {
+        if (tid < 32) {
+            const int j = tid >> 3, r = tid & 7;
+            float s = 0.0f;
+            for (int g0 = 0; g0 + j < d; g0 += 4) s = s + a[g0 + j] * p.cond_v[(size_t)(g0 + j) * 8 + r];
+            chains[j][r] = s;
+        }
+        __syncthreads();
+        if (tid < 8) weights[tid] = (((0.0f + chains[0][tid]) + chains[1][tid]) + chains[2][tid]) + chains[3][tid];
+    } else if (tid < p.rank) {
+        float s = 0.0f;
+        for (int i = 0; i < d; ++i) s = s + a[i] * p.cond_v[(size_t)i * p.rank + tid];
+        weights[tid] = s;
+    }
+    __syncthreads();
+    if (tid == 0) {  // ops.rs:92-101
+        float peak = -INFINITY;
+        for (int r = 0; r < p.rank; ++r) peak = fmaxf(peak, weights[r]);
+        float total = 0.0f;
+        for (int r = 0; r < p.rank; ++r) {
+            weights[r] = fast_exp(weights[r] - peak);
+            total = total + weights[r];
+        }
+        const float inverse = 1.0f / total;
+        for (int r = 0; r < p.rank; ++r) weights[r] = weights[r] * inverse;
+    }
+    __syncthreads();
+    {
+        float m = 1.0f;
+        for (int r = 0; r < p.rank; ++r) m = m + weights[r] * p.cond_u[(size_t)r * kN3Hadamard + tid];
+        modulation[tid] = m;
+        sc[tid] = (tid < d ? a[tid] : 0.0f) * p.d1[tid];
+    }
+    __syncthreads();
+    n3_kronecker32(sc, p.factors[0], p.factors[1], mx, st);
+    sc[tid] = silu(((p.d2[tid] * modulation[tid]) * st[p.perm1[tid]]) + p.b2[tid]);
+    __syncthreads();
+    n3_kronecker32(sc, p.factors[2], p.factors[3], mx, st);
+    sc[tid] = st[p.perm2[tid]] * p.d3[tid];
+    __syncthreads();
+    n3_kronecker32(sc, p.factors[4], p.factors[5], mx, st);
+    // block output, delta (lanes.rs:100-104), combine (lanes.rs:86-98), cell
+    for (int i = tid; i < d; i += blockDim.x) {
+        const float xo = xs[i] + st[i] * p.d4[i];
+        const float delta = xo - p.input[i];
+        float mean = 0.0f;
+        for (int l = 0; l < p.lanes; ++l) {
+            float o = 0.0f;
+            for (int s = 0; s < p.lanes; ++s) o = o + p.residual[l * p.lanes + s] * p.stream[(size_t)s * d + i];
+            o = o + p.post[l] * delta;
+            p.next[(size_t)l * d + i] = o;
+            mean = mean + o / (float)p.lanes;
+        }
+        p.cell[i] = mean;
+    }
+}
+
+// session.rs:141-144: lane mean and the final norm
+__global__ __launch_bounds__(kN3Block) void n3_final_kernel(const float* stream, int d, int lanes, const float* gain,
+                                                            float* hidden) {
+    __shared__ float m[kN3MaxWidth];
+    __shared__ float red[32];
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        float v = 0.0f;
+        for (int l = 0; l < lanes; ++l) v = v + stream[(size_t)l * d + i] / (float)lanes;
+        m[i] = v;
+    }
+    __syncthreads();
+    n3_norm(m, gain, d, m, red);
+    for (int i = threadIdx.x; i < d; i += blockDim.x) hidden[i] = m[i];
+}
+
+// ops.rs:19-30 by one block: eight strided lanes (threads 0..7), summed in lane
+// order from -0.0, plus the tail from -0.0. All threads get the value.
+__device__ float n3_dot_product(const float* a, const float* b, int n, float* red) {
+    const int tid = threadIdx.x;
+    if (tid < 8) {
+        float s = 0.0f;
+        for (int c = 0; c < n / 8; ++c) s = s + a[8 * c + tid] * b[8 * c + tid];
+        red[tid] = s;
+    }
+    __syncthreads();
+    float total = -0.0f;
+    for (int j = 0; j < 8; ++j) total = total + red[j];
+    float tail = -0.0f;
+    for (int i = n / 8 * 8; i < n; ++i) tail = tail + a[i] * b[i];
+    __syncthreads();
+    return total + tail;
+}
+
+// heads.rs:138-155: one block per slot (layer * k + probe)
+__global__ __launch_bounds__(256) void n3_observe_kernel(const float* cells, const float* probes, int k, int width,
+                                                         float* peak, float* total, float* weighted) {
+    __shared__ float red[8];
+    __shared__ float rw[2];
+    const int slot = blockIdx.x, layer = slot / k;
+    const float* cell = cells + (size_t)layer * width;
+    const float dot = n3_dot_product(cell, probes + (size_t)slot * width, width, red);
+    if (threadIdx.x == 0) {
+        const float score = dot / sqrtf((float)width);
+        const float old = peak[slot];
+        const float pk = fmaxf(old, score);
+        const float rescale = old == -INFINITY ? 0.0f : libm_expf(old - pk);
+        const float weight = libm_expf(score - pk);
+        total[slot] = total[slot] * rescale + weight;
+        peak[slot] = pk;
+        rw[0] = rescale;
+        rw[1] = weight;
+    }
+    __syncthreads();
+    const float rescale = rw[0], weight = rw[1];
+    float* target = weighted + (size_t)slot * width;
+    for (int i = threadIdx.x; i < width; i += blockDim.x) target[i] = target[i] * rescale + weight * cell[i];
+}
+
+// heads.rs:102-110: per slot, the average over the online total, unit_rms,
+// times the slot's gain
+__global__ __launch_bounds__(256) void n3_readout_kernel(const float* weighted, const float* total, const float* gain,
+                                                         int width, float* readouts) {
+    __shared__ float v[kN3MaxWidth];
+    __shared__ float red[32];
+    const int slot = blockIdx.x;
+    const float inverse = 1.0f / total[slot];
+    for (int i = threadIdx.x; i < width; i += blockDim.x) v[i] = weighted[(size_t)slot * width + i] * inverse;
+    __syncthreads();
+    n3_unit_rms(v, width, v, red);
+    const float g = gain[slot];
+    for (int i = threadIdx.x; i < width; i += blockDim.x) readouts[(size_t)slot * width + i] = v[i] * g;
+}
+
+// heads.rs:111-124 for query blockIdx.x
+__global__ __launch_bounds__(256) void n3_pool_kernel(const float* readouts, int slots, const float* query,
+                                                      const float* row_bias, int width, float* pooled) {
+    __shared__ float w[1024];
+    __shared__ float red[8];
+    const int q = blockIdx.x;
+    const float root = sqrtf((float)width);
+    for (int s = 0; s < slots; ++s) {
+        const float dot = n3_dot_product(readouts + (size_t)s * width, query + (size_t)q * width, width, red);
+        if (threadIdx.x == 0) w[s] = dot / root + row_bias[(size_t)q * slots + s];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float peak = -INFINITY;
+        for (int s = 0; s < slots; ++s) peak = fmaxf(peak, w[s]);
+        float t = 0.0f;
+        for (int s = 0; s < slots; ++s) {
+            w[s] = fast_exp(w[s] - peak);
+            t = t + w[s];
+        }
+        const float inverse = 1.0f / t;
+        for (int s = 0; s < slots; ++s) w[s] = w[s] * inverse;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < width; i += blockDim.x) {
+        float o = 0.0f;
+        for (int s = 0; s < slots; ++s) o = o + w[s] * readouts[(size_t)s * width + i];
+        pooled[(size_t)q * width + i] = o;
+    }
+}
+
+__global__ void n3_add_kernel(float* y, const float* bias, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = y[i] + bias[i];
+}
+
+}  // namespace rn
+
+using namespace rn;
+
+// ---- host ---------------------------------------------------------------------
+
+namespace {
+
+int n3_fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    return rn::set_error(code, buf);
+}
+
+#define N3_HIP(call)                                                                                            \
+    do {                                                                                                        \
+        hipError_t e_ = (call);                                                                                 \
+        if (e_ != hipSuccess)                                                                                   \
+            return n3_fail(RN_ERR_DEVICE, "%s: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, __LINE__); \
+    } while (0)
+
+#define N3_REQUIRE(cond, ...)                                    \
+    do {                                                         \
+        if (!(cond)) return n3_fail(RN_ERR_ARGUMENT, __VA_ARGS__); \
+    } while (0)
+
+#define N3_CALL(call)               \
+    do {                            \
+        int rc_ = (call);           \
+        if (rc_ != RN_OK) return rc_; \
+    } while (0)
+
+float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31, exponent = (h >> 10) & 0x1f, mantissa = h & 0x3ff;
+    uint32_t bits;
+    if (exponent == 0) {
+        if (mantissa == 0) {
+            bits = sign;
+        } else {  // subnormal: normalise
+            int e = -1;
+            uint32_t m = mantissa;
+            do {
+                ++e;
+                m <<= 1;
+            } while ((m & 0x400) == 0);
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((m & 0x3ff) << 13);
+        }
+    } else if (exponent == 31) {
+        bits = sign | 0x7f800000u | (mantissa << 13);
+    } else {
+        bits = sign | ((exponent + 127 - 15) << 23) | (mantissa << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+// The canonical tensor order (layout.rs:176-257), walked over the directory.
+struct Walk {
+    const rn_archive* archive;
+    int next = 0, end = 0;
+    bool failed = false;
+    int take() {
+        if (next >= end) {
+            failed = true;
+            return 0;
+        }
+        return next++;
+    }
+    int kind(int index) const {
+        rn_tensor_record r;
+        return rn_archive_record(archive, index, &r) == RN_OK ? r.kind : 0;
+    }
+};
+
+}  // namespace
+
+struct N3Layer {
+    rn_matrix *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *out = nullptr;
+    float *norm_in = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_norm = nullptr, *pre_norm = nullptr;
+    float* taps[3] = {nullptr, nullptr, nullptr};
+    float gate_sigmoid = 0.0f;
+    float *d1 = nullptr, *d2 = nullptr, *b2 = nullptr, *d3 = nullptr, *d4 = nullptr;
+    float* factors[6] = {};
+    float *cond_v = nullptr, *cond_u = nullptr;
+    int rank = 0;
+};
+
+struct N3Engram {
+    rn_matrix *tables = nullptr, *key = nullptr, *value = nullptr;
+    float* taps = nullptr;
+};
+
+struct N3Head {
+    int code = 0, layers = 0, per_layer = 0, queries = 0, width = 0;
+    float *probes = nullptr, *gain = nullptr, *query = nullptr, *row_bias = nullptr, *bias = nullptr;
+    rn_matrix* projection = nullptr;
+};
+
+struct rn_n3_model {
+    rn_geometry g{};
+    int output_vocab = 0;
+    rn_matrix* embedding = nullptr;
+    std::vector<N3Layer> layers;
+    float *a_pre = nullptr, *a_post = nullptr, *a_res = nullptr, *b_pre = nullptr, *b_post = nullptr,
+          *b_res = nullptr;
+    std::vector<float> a_pre_h, a_post_h, a_res_h, b_pre_h, b_post_h, b_res_h;
+    rn_matrix *phi_pre = nullptr, *phi_post = nullptr, *phi_res = nullptr;
+    int32_t* perm[2] = {nullptr, nullptr};
+    std::vector<N3Engram> engrams;
+    float* final_norm = nullptr;
+    std::vector<N3Head> heads;
+    std::vector<int> active;
+    std::vector<void*> allocations;
+    std::vector<rn_matrix*> matrices;
+};
+
+namespace {
+
+int upload_floats(rn_n3_model* m, const std::vector<float>& v, float** out) {
+    void* p = nullptr;
+    N3_HIP(hipMalloc(&p, std::max<size_t>(4, v.size() * sizeof(float))));
+    m->allocations.push_back(p);
+    if (!v.empty()) N3_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+    *out = (float*)p;
+    return RN_OK;
+}
+
+// tensors.rs:3-13: half or single records as floats
+int host_floats(const rn_archive* a, int index, std::vector<float>& out) {
+    rn_tensor_record r;
+    N3_CALL(rn_archive_record(a, index, &r));
+    const uint8_t* data = nullptr;
+    size_t n = 0;
+    N3_CALL(rn_archive_tensor_bytes(a, index, &data, &n));
+    if (r.kind == RN_KIND_HALF) {
+        out.resize(n / 2);
+        for (size_t i = 0; i < out.size(); ++i) {
+            uint16_t h;
+            memcpy(&h, data + 2 * i, 2);
+            out[i] = half_to_float(h);
+        }
+    } else if (r.kind == RN_KIND_SINGLE) {
+        out.resize(n / 4);
+        memcpy(out.data(), data, out.size() * 4);
+    } else {
+        return n3_fail(RN_ERR_ARGUMENT, "tensor %d holds kind %d, not floating point values", index, r.kind);
+    }
+    return RN_OK;
+}
+
+// a float tensor of exactly `count` values (count < 0: any) to the device
+int device_floats(rn_n3_model* m, const rn_archive* a, int index, float** out, long count,
+                  std::vector<float>* keep = nullptr) {
+    std::vector<float> v;
+    N3_CALL(host_floats(a, index, v));
+    if (count >= 0 && (long)v.size() != count)
+        return n3_fail(RN_ERR_ARGUMENT, "tensor %d holds %zu values, %ld expected", index, v.size(), count);
+    if (keep) *keep = v;
+    return upload_floats(m, v, out);
+}
+
+int matrix(rn_n3_model* m, const rn_archive* a, int index, rn_matrix** out) {
+    N3_CALL(rn_matrix_from_archive(a, index, out));
+    m->matrices.push_back(*out);
+    return RN_OK;
+}
+
+// rows of a matrix dequantised on the device, gathered on the host
+int dense_rows(const rn_matrix* mat, const std::vector<int>& rows, std::vector<float>& out) {
+    out.resize(rows.size() * (size_t)mat->columns);
+    for (size_t i = 0; i < rows.size(); ++i)
+        N3_CALL(rn_matrix_dequantise_row(mat, rows[i], out.data() + i * mat->columns));
+    return RN_OK;
+}
+
+// ladder.rs:1-29, through the public entry point
+int ladder(int layers, int depth, std::vector<int>& active) {
+    std::vector<int32_t> chosen((size_t)std::max(layers, 1));
+    N3_CALL(rn_ladder_select(layers, depth, chosen.data()));
+    active.assign(chosen.begin(), chosen.begin() + depth);
+    return RN_OK;
+}
+
+}  // namespace
+
+int rn_n3_model_free(rn_n3_model* m) {
+    if (!m) return RN_OK;
+    for (rn_matrix* x : m->matrices) rn_matrix_free(x);
+    for (void* p : m->allocations) (void)hipFree(p);
+    delete m;
+    return RN_OK;
+}
+
+int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out) {
+    N3_REQUIRE(archive && out, "null argument");
+    *out = nullptr;
+    rn_n3_model* m = new (std::nothrow) rn_n3_model();
+    if (!m) return n3_fail(RN_ERR_MEMORY, "out of host memory");
+    int rc = [&]() -> int {
+        rn_geometry& g = m->g;
+        N3_CALL(rn_archive_geometry(archive, &g));
+        N3_REQUIRE(g.qk_head_dim == 64 && g.v_head_dim == 64, "head dimensions must be 64 (got %u / %u)", g.qk_head_dim,
+                   g.v_head_dim);
+        N3_REQUIRE(g.num_kv_heads > 0 && g.num_heads % g.num_kv_heads == 0, "heads must be a multiple of kv heads");
+        N3_REQUIRE(g.hada_n == (uint32_t)kN3Hadamard, "the Hadamard size must be 1024 (32 x 32 factors; got %u)",
+                   g.hada_n);
+        N3_REQUIRE(g.d_model % 8 == 0 && g.d_model <= (uint32_t)kN3Hadamard, "d_model must be a multiple of 8, <= 1024");
+        N3_REQUIRE(g.mhc_lanes >= 1 && g.mhc_lanes * g.d_model <= (uint32_t)kN3MaxWidth, "lanes x d_model above %d",
+                   kN3MaxWidth);
+        N3_REQUIRE(g.num_heads * 64 <= (uint32_t)kN3MaxWidth, "too many heads");
+        N3_REQUIRE(g.engram_order_count * (g.engram_order_count ? g.engram_tables / g.engram_order_count : 0) <=
+                       (uint32_t)kN3MaxTables,
+                   "more than %d engram tables", kN3MaxTables);
+        m->output_vocab = g.out_vocab ? (int)g.out_vocab : (int)g.vocab;
+        Walk w{archive};
+        w.end = (int)g.tensor_count - 1;
+        N3_REQUIRE(g.tensor_count >= 1 && w.kind((int)g.tensor_count - 1) == RN_KIND_RAW, "no trailing tokenizer blob");
+        N3_CALL(matrix(m, archive, w.take(), &m->embedding));
+        const int L = (int)g.num_layers, d = (int)g.d_model;
+        N3_REQUIRE(m->embedding->rows >= (int)g.vocab && m->embedding->rows >= m->output_vocab &&
+                       m->embedding->columns == d,
+                   "embedding [%d][%d] does not cover the vocabulary x d_model", m->embedding->rows,
+                   m->embedding->columns);
+        m->layers.resize((size_t)L);
+        std::vector<float> scalar;
+        for (int l = 0; l < L; ++l) {
+            N3Layer& y = m->layers[(size_t)l];
+            N3_CALL(device_floats(m, archive, w.take(), &y.norm_in, d));
+            N3_CALL(matrix(m, archive, w.take(), &y.q));
+            N3_CALL(matrix(m, archive, w.take(), &y.k));
+            N3_CALL(matrix(m, archive, w.take(), &y.v));
+            if (g.qkv_conv_taps > 0)
+                for (int t = 0; t < 3; ++t)
+                    N3_CALL(device_floats(m, archive, w.take(), &y.taps[t],
+                                          (long)g.qkv_conv_taps * (t == 0 ? g.num_heads : g.num_kv_heads) * 64));
+            N3_CALL(device_floats(m, archive, w.take(), &y.q_norm, 64));
+            N3_CALL(device_floats(m, archive, w.take(), &y.k_norm, 64));
+            N3_CALL(matrix(m, archive, w.take(), &y.gate));
+            N3_CALL(matrix(m, archive, w.take(), &y.out));
+            N3_CALL(device_floats(m, archive, w.take(), &y.post_norm, d));
+            N3_CALL(host_floats(archive, w.take(), scalar));
+            N3_REQUIRE(!scalar.empty(), "attention gate of layer %d is empty", l);
+            y.gate_sigmoid = 1.0f / (1.0f + expf(-scalar[0]));  // ops.rs:68-71 with the host's expf
+            N3_CALL(device_floats(m, archive, w.take(), &y.pre_norm, d));
+            float** diag[5] = {&y.d1, &y.d2, &y.b2, &y.d3, &y.d4};
+            for (int i = 0; i < 5; ++i) N3_CALL(device_floats(m, archive, w.take(), diag[i], kN3Hadamard));
+            for (int f = 0; f < 6; ++f) {
+                std::vector<float> v;
+                const int idx = w.take();
+                N3_CALL(host_floats(archive, idx, v));
+                N3_REQUIRE(v.size() == 1024, "Hadamard factors must be 32 x 32 (layer %d factor %d)", l, f);
+                N3_CALL(upload_floats(m, v, &y.factors[f]));
+            }
+            std::vector<float> cu;
+            std::vector<float> cv;
+            N3_CALL(device_floats(m, archive, w.take(), &y.cond_v, -1, &cv));
+            N3_CALL(device_floats(m, archive, w.take(), &y.cond_u, -1, &cu));
+            y.rank = (int)(cu.size() / kN3Hadamard);  // hadamard.rs:39
+            N3_REQUIRE(y.rank >= 1 && y.rank <= 64 && cu.size() == (size_t)y.rank * kN3Hadamard &&
+                           cv.size() == (size_t)y.rank * d,
+                       "condition tensors of layer %d: rank %d (1..64), cond_v [d_model][rank]", l, y.rank);
+            const bool same = y.q->columns == d && y.k->columns == d && y.v->columns == d && y.gate->columns == d;
+            N3_REQUIRE(same, "projections of layer %d must take d_model columns", l);
+            N3_REQUIRE(y.q->rows == (int)(g.num_heads * 64) && y.k->rows == (int)(g.num_kv_heads * 64) &&
+                           y.v->rows == (int)(g.num_kv_heads * 64) && y.gate->rows == (int)(g.num_heads * 64) &&
+                           y.out->rows == d,
+                       "projection shapes of layer %d do not match the geometry", l);
+            N3_REQUIRE(y.q->cb.padded == y.k->cb.padded && y.q->cb.padded == y.v->cb.padded &&
+                           y.q->cb.padded == y.gate->cb.padded,
+                       "projections of layer %d must share their padded width", l);
+        }
+        N3_CALL(device_floats(m, archive, w.take(), &m->a_pre, L, &m->a_pre_h));
+        N3_CALL(device_floats(m, archive, w.take(), &m->a_post, L, &m->a_post_h));
+        N3_CALL(device_floats(m, archive, w.take(), &m->a_res, L, &m->a_res_h));
+        N3_CALL(device_floats(m, archive, w.take(), &m->b_pre, (long)L * g.mhc_lanes, &m->b_pre_h));
+        N3_CALL(device_floats(m, archive, w.take(), &m->b_post, (long)L * g.mhc_lanes, &m->b_post_h));
+        N3_CALL(device_floats(m, archive, w.take(), &m->b_res, (long)L * g.mhc_lanes * g.mhc_lanes, &m->b_res_h));
+        N3_CALL(matrix(m, archive, w.take(), &m->phi_pre));
+        N3_CALL(matrix(m, archive, w.take(), &m->phi_post));
+        N3_CALL(matrix(m, archive, w.take(), &m->phi_res));
+        const int lanes = (int)g.mhc_lanes;
+        N3_REQUIRE(m->phi_pre->rows == L * lanes && m->phi_post->rows == L * lanes &&
+                       m->phi_res->rows == L * lanes * lanes && m->phi_pre->columns == lanes * d &&
+                       m->phi_post->columns == lanes * d && m->phi_res->columns == lanes * d,
+                   "routing matrices do not match layers x lanes over the lane stream");
+        for (int p = 0; p < 2; ++p) {  // hadamard.rs:36: floats, `as usize`
+            std::vector<float> v;
+            N3_CALL(host_floats(archive, w.take(), v));
+            N3_REQUIRE(v.size() == (size_t)kN3Hadamard, "permutation %d has %zu entries", p, v.size());
+            std::vector<int32_t> perm(v.size());
+            for (size_t i = 0; i < v.size(); ++i) {
+                perm[i] = (int32_t)v[i];
+                N3_REQUIRE(perm[i] >= 0 && perm[i] < kN3Hadamard, "permutation %d entry out of range", p);
+            }
+            void* dp = nullptr;
+            N3_HIP(hipMalloc(&dp, perm.size() * 4));
+            m->allocations.push_back(dp);
+            N3_HIP(hipMemcpy(dp, perm.data(), perm.size() * 4, hipMemcpyHostToDevice));
+            m->perm[p] = (int32_t*)dp;
+        }
+        m->engrams.resize(g.engram_site_count);
+        for (N3Engram& e : m->engrams) {
+            N3_CALL(matrix(m, archive, w.take(), &e.tables));
+            N3_CALL(matrix(m, archive, w.take(), &e.key));
+            N3_CALL(matrix(m, archive, w.take(), &e.value));
+            N3_CALL(device_floats(m, archive, w.take(), &e.taps, (long)g.engram_conv_taps * d));
+            N3_REQUIRE(e.key->rows == d && e.value->rows == d, "engram projections must give d_model rows");
+            N3_REQUIRE(e.key->cb.padded == e.value->cb.padded, "engram projections must share their width");
+            N3_REQUIRE(e.tables->columns == (int)g.engram_sub_dim && e.tables->cb.padded == e.tables->columns,
+                       "engram tables must hold sub_dim columns, a whole number of groups");
+        }
+        N3_CALL(device_floats(m, archive, w.take(), &m->final_norm, d));
+        if (w.failed) return n3_fail(RN_ERR_ARGUMENT, "directory ends before the canonical tensor list");
+        if (depth <= 0) depth = L;
+        N3_CALL(ladder(L, depth, m->active));
+        N3_REQUIRE(!m->active.empty(), "depth %d selects no layers", depth);
+        // probe heads (layout.rs:228-246; heads.rs:33-82 with with_rows)
+        if (w.next < w.end && w.kind(w.next) == RN_KIND_HALF) {
+            std::vector<float> codes;
+            N3_CALL(host_floats(archive, w.take(), codes));
+            for (float cf : codes) {
+                const int code = (int)lroundf(cf);
+                N3_REQUIRE(code >= 1 && code <= 3, "unrecognised head manifest code");
+                N3Head h;
+                h.code = code;
+                rn_matrix *probes = nullptr, *query = nullptr;
+                N3_CALL(matrix(m, archive, w.take(), &probes));
+                std::vector<float> gain, row_bias;
+                N3_CALL(host_floats(archive, w.take(), gain));
+                N3_CALL(matrix(m, archive, w.take(), &query));
+                N3_CALL(host_floats(archive, w.take(), row_bias));
+                N3_CALL(matrix(m, archive, w.take(), &h.projection));
+                N3_CALL(device_floats(m, archive, w.take(), &h.bias, h.projection->rows));
+                if (code == 3) w.take();  // calibration
+                const int rows_all = L + 1, k = probes->rows / rows_all;
+                h.width = probes->columns;
+                h.per_layer = k;
+                h.queries = query->rows;
+                h.layers = (int)m->active.size() + 1;
+                N3_REQUIRE(h.width == d && k >= 1 && probes->rows == rows_all * k, "probe head rows must be layers x k over d_model");
+                N3_REQUIRE(query->columns == d && h.projection->columns == h.queries * d &&
+                               gain.size() == (size_t)rows_all * k && row_bias.size() == (size_t)h.queries * rows_all * k,
+                           "probe head tensors do not match its probes and queries");
+                N3_REQUIRE(h.queries * d <= kN3MaxWidth * 16, "too many probe queries");
+                N3_REQUIRE(h.layers * k <= 1024, "more than 1024 probe slots");
+                std::vector<int> rows, qrows;
+                std::vector<float> sel_gain, sel_bias;
+                const int old_slots = rows_all * k;
+                for (int ri = 0; ri < h.layers; ++ri) {
+                    const int row = ri == 0 ? 0 : m->active[(size_t)ri - 1] + 1;
+                    for (int p = 0; p < k; ++p) {
+                        rows.push_back(row * k + p);
+                        sel_gain.push_back(gain[(size_t)row * k + p]);
+                    }
+                }
+                for (int q = 0; q < h.queries; ++q) {
+                    qrows.push_back(q);
+                    for (int ri = 0; ri < h.layers; ++ri) {
+                        const int row = ri == 0 ? 0 : m->active[(size_t)ri - 1] + 1;
+                        for (int p = 0; p < k; ++p) sel_bias.push_back(row_bias[(size_t)q * old_slots + row * k + p]);
+                    }
+                }
+                std::vector<float> dense;
+                N3_CALL(dense_rows(probes, rows, dense));
+                N3_CALL(upload_floats(m, dense, &h.probes));
+                N3_CALL(dense_rows(query, qrows, dense));
+                N3_CALL(upload_floats(m, dense, &h.query));
+                N3_CALL(upload_floats(m, sel_gain, &h.gain));
+                N3_CALL(upload_floats(m, sel_bias, &h.row_bias));
+                m->heads.push_back(h);
+            }
+        }
+        if (w.failed) return n3_fail(RN_ERR_ARGUMENT, "directory ends inside the probe heads");
+        N3_REQUIRE(w.next == w.end, "%d tensors follow the heads (an audio encoder is not part of this model)",
+                   w.end - w.next);
+        return RN_OK;
+    }();
+    if (rc != RN_OK) {
+        rn_n3_model_free(m);
+        return rc;
+    }
+    *out = m;
+    return RN_OK;
+}
+
+int rn_n3_model_active_layers(const rn_n3_model* m, int* layers, int* count) {
+    N3_REQUIRE(m && count, "null argument");
+    *count = (int)m->active.size();
+    if (layers) std::copy(m->active.begin(), m->active.end(), layers);
+    return RN_OK;
+}
+
+int rn_n3_model_output_vocab(const rn_n3_model* m, int* count) {
+    N3_REQUIRE(m && count, "null argument");
+    *count = m->output_vocab;
+    return RN_OK;
+}
+
+struct N3CacheDev {
+    int8_t *keys = nullptr, *values = nullptr;
+    float *key_scales = nullptr, *value_scales = nullptr, *hist = nullptr;
+};
+
+struct rn_n3_session {
+    const rn_n3_model* m = nullptr;
+    int capacity = 0, length = 0;
+    hipStream_t stream = nullptr;
+    std::vector<uint32_t> tokens;
+    rn_lanes* lanes = nullptr;
+    std::vector<N3CacheDev> caches;
+    std::vector<float*> rings, ekey, evalue;
+    std::vector<void*> allocations;
+    float *stream_a = nullptr, *stream_b = nullptr, *input = nullptr, *post = nullptr, *residual = nullptr;
+    float *x = nullptr, *quantised = nullptr, *rotated = nullptr, *prod = nullptr, *attended = nullptr;
+    float *attn_out = nullptr, *row = nullptr, *gathered = nullptr, *eraw = nullptr, *qscales = nullptr;
+    int8_t* qcodes = nullptr;
+    float *cells = nullptr, *hidden = nullptr, *logits = nullptr, *cos = nullptr, *sin = nullptr;
+    std::vector<float*> peak, total, weighted;
+    float *readouts = nullptr, *pooled = nullptr, *head_out = nullptr;
+};
+
+namespace {
+
+int alloc(rn_n3_session* s, size_t bytes, void** out) {
+    void* p = nullptr;
+    N3_HIP(hipMalloc(&p, std::max<size_t>(bytes, 256)));
+    s->allocations.push_back(p);
+    N3_HIP(hipMemsetAsync(p, 0, std::max<size_t>(bytes, 256), s->stream));
+    *out = p;
+    return RN_OK;
+}
+template <typename T>
+int alloc_n(rn_n3_session* s, size_t n, T** out) {
+    void* p = nullptr;
+    N3_CALL(alloc(s, n * sizeof(T), &p));
+    *out = (T*)p;
+    return RN_OK;
+}
+
+// QuantisedMatrix::multiply_vector on a rotated input (matrix.rs:155-165): the
+// integer path for 2-, 4-bit and ternary matrices, the float path otherwise
+int product(const rn_matrix* mat, const float* rotated, float* y, hipStream_t st) {
+    if (mat->bits == 1 || mat->bits == 3)
+        N3_HIP(launch_codebook_float(mat->cb, rotated, 1, y, false, st));
+    else
+        N3_HIP(launch_codebook_product(mat->cb, rotated, 1, y, nullptr, st));
+    return RN_OK;
+}
+
+int rotate(const rn_matrix* mat, const float* x, float* rotated, hipStream_t st) {
+    N3_HIP(launch_codebook_rotate(x, 1, mat->columns, mat->cb.padded, mat->group, mat->cb.wht_scale, rotated, st));
+    return RN_OK;
+}
+
+int site_of(const rn_n3_model* m, int layer) {  // config.rs:89-91
+    for (uint32_t e = 0; e < m->g.engram_site_count; ++e)
+        if ((int)m->g.engram_sites[e] == layer) return (int)e;
+    return -1;
+}
+
+bool site_active(const rn_n3_model* m, int site) {
+    return std::find(m->active.begin(), m->active.end(), (int)m->g.engram_sites[site]) != m->active.end();
+}
+
+int heads_per_order(const rn_geometry& g) { return (int)g.engram_tables / (g.engram_order_count > 1 ? (int)g.engram_order_count : 1); }
+
+// engram.rs:30-46
+void table_indices(const rn_geometry& g, const std::vector<uint32_t>& tokens, int position, int* out) {
+    const int hpo = heads_per_order(g), stride = g.engram_seed_heads == 0 ? hpo : (int)g.engram_seed_heads;
+    int n = 0;
+    for (int o = 0; o < (int)g.engram_order_count; ++o)
+        for (int head = 0; head < hpo; ++head) {
+            uint32_t acc = 0x9E3779B9u * (uint32_t)(o * stride + head + 1);
+            for (int back = 0; back < (int)g.engram_orders[o]; ++back) {
+                const uint32_t token = position >= back ? tokens[(size_t)(position - back)] : 0u;
+                acc = (acc ^ token) * 0x01000193u;
+            }
+            acc ^= acc >> 15;
+            out[n++] = (int)(acc % g.engram_slots);
+        }
+}
+
+}  // namespace
+
+int rn_n3_session_free(rn_n3_session* s) {
+    if (!s) return RN_OK;
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    if (s->lanes) rn_lanes_free(s->lanes);
+    for (void* p : s->allocations) (void)hipFree(p);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+    return RN_OK;
+}
+
+int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out) {
+    N3_REQUIRE(m && out, "null argument");
+    N3_REQUIRE(capacity >= 1 && capacity <= kN3MaxAttend, "capacity must be 1..%d (got %d)", kN3MaxAttend, capacity);
+    *out = nullptr;
+    rn_n3_session* s = new (std::nothrow) rn_n3_session();
+    if (!s) return n3_fail(RN_ERR_MEMORY, "out of host memory");
+    s->m = m;
+    s->capacity = capacity;
+    int rc = [&]() -> int {
+        const rn_geometry& g = m->g;
+        const int d = (int)g.d_model, L = (int)g.num_layers, lanes = (int)g.mhc_lanes, H = (int)g.num_heads,
+                  KV = (int)g.num_kv_heads;
+        N3_HIP(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+        N3_CALL(rn_lanes_create(lanes, d, L, m->a_pre_h.data(), m->a_post_h.data(), m->a_res_h.data(),
+                                m->b_pre_h.data(), m->b_post_h.data(), m->b_res_h.data(), m->phi_pre, m->phi_post,
+                                m->phi_res, &s->lanes));
+        s->caches.resize((size_t)L);
+        const int qkv = (H + 2 * KV) * 64, taps = std::max(1, (int)g.qkv_conv_taps);
+        for (N3CacheDev& c : s->caches) {
+            N3_CALL(alloc_n(s, (size_t)KV * capacity * 64, &c.keys));
+            N3_CALL(alloc_n(s, (size_t)KV * capacity * 64, &c.values));
+            N3_CALL(alloc_n(s, (size_t)KV * capacity, &c.key_scales));
+            N3_CALL(alloc_n(s, (size_t)KV * capacity, &c.value_scales));
+            N3_CALL(alloc_n(s, (size_t)taps * qkv, &c.hist));
+        }
+        const int keep = std::max(1, ((int)g.engram_conv_taps - 1) * (int)g.engram_conv_dilation + 1);
+        s->rings.resize(g.engram_site_count);
+        s->ekey.resize(g.engram_site_count);
+        s->evalue.resize(g.engram_site_count);
+        for (uint32_t e = 0; e < g.engram_site_count; ++e) {
+            N3_CALL(alloc_n(s, (size_t)keep * d, &s->rings[e]));
+            N3_CALL(alloc_n(s, (size_t)d, &s->ekey[e]));
+            N3_CALL(alloc_n(s, (size_t)d, &s->evalue[e]));
+        }
+        int widest = std::max(lanes * d, qkv + H * 64);
+        for (const N3Engram& e : m->engrams) widest = std::max(widest, e.key->cb.padded);
+        for (const N3Head& h : m->heads) widest = std::max(widest, h.projection->cb.padded);
+        widest = std::max(widest, m->embedding->cb.padded);
+        N3_CALL(alloc_n(s, (size_t)lanes * d, &s->stream_a));
+        N3_CALL(alloc_n(s, (size_t)lanes * d, &s->stream_b));
+        N3_CALL(alloc_n(s, (size_t)d, &s->input));
+        N3_CALL(alloc_n(s, 64, &s->post));
+        N3_CALL(alloc_n(s, 256, &s->residual));
+        N3_CALL(alloc_n(s, (size_t)d, &s->x));
+        N3_CALL(alloc_n(s, (size_t)widest, &s->quantised));
+        N3_CALL(alloc_n(s, (size_t)widest, &s->rotated));
+        N3_CALL(alloc_n(s, (size_t)qkv + H * 64, &s->prod));
+        N3_CALL(alloc_n(s, (size_t)H * 64, &s->attended));
+        N3_CALL(alloc_n(s, (size_t)d, &s->attn_out));
+        N3_CALL(alloc_n(s, (size_t)std::max(d, m->embedding->cb.padded), &s->row));
+        N3_CALL(alloc_n(s, (size_t)kN3MaxWidth, &s->gathered));
+        N3_CALL(alloc_n(s, (size_t)d, &s->eraw));
+        N3_CALL(alloc_n(s, (size_t)H, &s->qscales));
+        N3_CALL(alloc_n(s, (size_t)H * 64, &s->qcodes));
+        N3_CALL(alloc_n(s, (size_t)(m->active.size() + 1) * d, &s->cells));
+        N3_CALL(alloc_n(s, (size_t)d, &s->hidden));
+        N3_CALL(alloc_n(s, (size_t)m->output_vocab, &s->logits));
+        // the rotary table (ops.rs:127-141): angle = position as f32 * frequency
+        std::vector<float> cs((size_t)capacity * 32), sn((size_t)capacity * 32);
+        for (int p = 0; p < capacity; ++p)
+            for (int i = 0; i < 32; ++i) {
+                const float freq = 1.0f / powf(g.rope_theta, (2.0f * (float)i) / 64.0f);
+                const float angle = (float)p * freq;
+                cs[(size_t)p * 32 + i] = cosf(angle);
+                sn[(size_t)p * 32 + i] = sinf(angle);
+            }
+        N3_CALL(alloc_n(s, cs.size(), &s->cos));
+        N3_CALL(alloc_n(s, sn.size(), &s->sin));
+        N3_HIP(hipMemcpyAsync(s->cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, s->stream));
+        N3_HIP(hipMemcpyAsync(s->sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, s->stream));
+        size_t readouts = 0, pooled = 0, outs = 0;
+        for (const N3Head& h : m->heads) {
+            const int slots = h.layers * h.per_layer;
+            float *pk = nullptr, *tt = nullptr, *wt = nullptr;
+            N3_CALL(alloc_n(s, (size_t)slots, &pk));
+            N3_CALL(alloc_n(s, (size_t)slots, &tt));
+            N3_CALL(alloc_n(s, (size_t)slots * h.width, &wt));
+            std::vector<float> ninf((size_t)slots, -INFINITY);
+            N3_HIP(hipMemcpyAsync(pk, ninf.data(), ninf.size() * 4, hipMemcpyHostToDevice, s->stream));
+            s->peak.push_back(pk);
+            s->total.push_back(tt);
+            s->weighted.push_back(wt);
+            readouts = std::max(readouts, (size_t)slots * h.width);
+            pooled = std::max(pooled, (size_t)h.queries * h.width);
+            outs = std::max(outs, (size_t)h.projection->rows);
+        }
+        N3_CALL(alloc_n(s, std::max<size_t>(readouts, 1), &s->readouts));
+        N3_CALL(alloc_n(s, std::max<size_t>(pooled, 1), &s->pooled));
+        N3_CALL(alloc_n(s, std::max<size_t>(outs, 1), &s->head_out));
+        N3_HIP(hipStreamSynchronize(s->stream));
+        return RN_OK;
+    }();
+    if (rc != RN_OK) {
+        rn_n3_session_free(s);
+        return rc;
+    }
+    *out = s;
+    return RN_OK;
+}
+
+// Session::push (session.rs:76-148)
+int rn_n3_session_push(rn_n3_session* s, uint32_t token) {
+    N3_REQUIRE(s, "null session");
+    const rn_n3_model* m = s->m;
+    const rn_geometry& g = m->g;
+    N3_REQUIRE(token < g.vocab, "token %u is outside the vocabulary of %u", token, g.vocab);
+    N3_REQUIRE(s->length < s->capacity, "session is full (capacity %d)", s->capacity);
+    const int d = (int)g.d_model, lanes = (int)g.mhc_lanes, H = (int)g.num_heads, KV = (int)g.num_kv_heads;
+    const int position = s->length;
+    hipStream_t st = s->stream;
+    s->tokens.push_back(token);
+
+    N3_HIP(launch_codebook_dequantise(m->embedding->cb, (int)token, s->row, st));
+    float* cur = s->stream_a;
+    float* nxt = s->stream_b;
+    rn_launch(n3_stream_init_kernel, dim3((d + 255) / 256), dim3(256), 0, st, (const float*)s->row, d, lanes,
+              sqrtf((float)d), cur, s->cells);
+    N3_HIP(hipGetLastError());
+
+    // engram sites (engram.rs:30-112), before the layers
+    int indices[kN3MaxTables] = {0};
+    table_indices(g, s->tokens, position, indices);
+    const int hpo = heads_per_order(g), tables = (int)g.engram_order_count * hpo;
+    const int keep = std::max(1, ((int)g.engram_conv_taps - 1) * (int)g.engram_conv_dilation + 1);
+    for (uint32_t e = 0; e < g.engram_site_count; ++e) {
+        if (!site_active(m, (int)e)) continue;
+        const N3Engram& eg = m->engrams[e];
+        N3GatherParams gp{};
+        gp.tables = eg.tables->cb;
+        gp.count = tables;
+        gp.sub = (int)g.engram_sub_dim;
+        gp.slots = (int)g.engram_slots;
+        gp.position = position;
+        for (int t = 0; t < tables; ++t) {
+            gp.index[t] = indices[t];
+            gp.order[t] = (int)g.engram_orders[t / hpo];
+        }
+        gp.out = s->gathered;
+        N3_REQUIRE(tables * gp.sub <= kN3MaxWidth && eg.key->columns == tables * gp.sub,
+                   "engram key projection must take tables x sub_dim columns");
+        rn_launch(n3_gather_kernel, dim3(1), dim3(kN3Block), 0, st, gp);
+        N3_HIP(hipGetLastError());
+        N3_CALL(rotate(eg.key, s->gathered, s->rotated, st));
+        N3_CALL(product(eg.key, s->rotated, s->ekey[e], st));
+        N3_CALL(product(eg.value, s->rotated, s->eraw, st));
+        rn_launch(n3_engram_conv_kernel, dim3((d + 255) / 256), dim3(256), 0, st, (const float*)s->eraw, s->rings[e],
+                  (const float*)eg.taps, position, keep, (int)g.engram_conv_taps, (int)g.engram_conv_dilation, d,
+                  s->evalue[e]);
+        N3_HIP(hipGetLastError());
+    }
+
+    const int qw = H * 64, kw = KV * 64, qkv = qw + 2 * kw;
+    for (size_t slot = 0; slot < m->active.size(); ++slot) {
+        const int layer = m->active[slot];
+        const N3Layer& y = m->layers[(size_t)layer];
+        N3CacheDev& c = s->caches[(size_t)layer];
+        N3_CALL(rn_lanes_route(s->lanes, layer, (int)slot, cur, s->input, s->post, s->residual, st));
+        const int site = site_of(m, layer);
+        N3BlockInParams bi{s->input, site >= 0 ? s->ekey[(size_t)site] : nullptr,
+                           site >= 0 ? s->evalue[(size_t)site] : nullptr, y.norm_in, d, s->x, s->quantised};
+        rn_launch(n3_block_in_kernel, dim3(1), dim3(kN3Block), 0, st, bi);
+        N3_HIP(hipGetLastError());
+        N3_CALL(rotate(y.q, s->quantised, s->rotated, st));
+        N3_CALL(product(y.q, s->rotated, s->prod, st));
+        N3_CALL(product(y.k, s->rotated, s->prod + qw, st));
+        N3_CALL(product(y.v, s->rotated, s->prod + qw + kw, st));
+        N3_CALL(product(y.gate, s->rotated, s->prod + qkv, st));
+        N3QkvParams qp{};
+        qp.prod = s->prod;
+        qp.hist = c.hist;
+        for (int t = 0; t < 3; ++t) qp.taps[t] = y.taps[t];
+        qp.ntaps = (int)g.qkv_conv_taps;
+        qp.position = position;
+        qp.H = H;
+        qp.KV = KV;
+        qp.cap = s->capacity;
+        qp.q_norm = y.q_norm;
+        qp.k_norm = y.k_norm;
+        qp.cos_row = s->cos + (size_t)position * 32;
+        qp.sin_row = s->sin + (size_t)position * 32;
+        qp.qcodes = s->qcodes;
+        qp.qscales = s->qscales;
+        qp.keys = c.keys;
+        qp.key_scales = c.key_scales;
+        qp.values = c.values;
+        qp.value_scales = c.value_scales;
+        rn_launch(n3_qkv_kernel, dim3(H + 2 * KV), dim3(64), 0, st, qp);
+        N3_HIP(hipGetLastError());
+        // attention.rs:172-178: the window unless the layer is global
+        const int total = position + 1;
+        int first = 0;
+        if (g.sliding_window > 0 && !((g.global_layers >> layer) & 1))
+            first = total > (int)g.sliding_window ? total - (int)g.sliding_window : 0;
+        N3AttendParams ap{s->qcodes, s->qscales, c.keys, c.key_scales, c.values, c.value_scales, s->prod + qkv,
+                          s->capacity, first, total - first, H / KV, 1.0f / sqrtf(64.0f), s->attended};
+        rn_launch(n3_attend_kernel, dim3(H), dim3(256), 0, st, ap);
+        N3_HIP(hipGetLastError());
+        rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->attended, H * 64,
+                  s->quantised);
+        N3_HIP(hipGetLastError());
+        N3_CALL(rotate(y.out, s->quantised, s->rotated, st));
+        N3_CALL(product(y.out, s->rotated, s->attn_out, st));
+        N3BlockOutParams bo{};
+        bo.attention = s->attn_out;
+        bo.post_norm = y.post_norm;
+        bo.gate = y.gate_sigmoid;
+        bo.pre_norm = y.pre_norm;
+        bo.d1 = y.d1;
+        bo.d2 = y.d2;
+        bo.b2 = y.b2;
+        bo.d3 = y.d3;
+        bo.d4 = y.d4;
+        for (int f = 0; f < 6; ++f) bo.factors[f] = y.factors[f];
+        bo.cond_v = y.cond_v;
+        bo.cond_u = y.cond_u;
+        bo.rank = y.rank;
+        bo.perm1 = m->perm[0];
+        bo.perm2 = m->perm[1];
+        bo.x = s->x;
+        bo.input = s->input;
+        bo.post = s->post;
+        bo.residual = s->residual;
+        bo.stream = cur;
+        bo.d = d;
+        bo.lanes = lanes;
+        bo.next = nxt;
+        bo.cell = s->cells + (slot + 1) * (size_t)d;
+        rn_launch(n3_block_out_kernel, dim3(1), dim3(kN3Block), 0, st, bo);
+        N3_HIP(hipGetLastError());
+        std::swap(cur, nxt);
+    }
+    rn_launch(n3_final_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)cur, d, lanes,
+              (const float*)m->final_norm, s->hidden);
+    N3_HIP(hipGetLastError());
+    for (size_t i = 0; i < m->heads.size(); ++i) {
+        const N3Head& h = m->heads[i];
+        rn_launch(n3_observe_kernel, dim3(h.layers * h.per_layer), dim3(256), 0, st, (const float*)s->cells,
+                  (const float*)h.probes, h.per_layer, h.width, s->peak[i], s->total[i], s->weighted[i]);
+        N3_HIP(hipGetLastError());
+    }
+    s->length++;
+    return RN_OK;
+}
+
+// Session::feed (session.rs:58-74): the batched prefill runs the same
+// arithmetic per token as pushing them in order.
+int rn_n3_session_feed(rn_n3_session* s, const uint32_t* tokens, int count) {
+    N3_REQUIRE(s && (tokens || count == 0), "null argument");
+    N3_REQUIRE(count >= 0 && s->length + count <= s->capacity, "feed of %d tokens overflows the capacity", count);
+    for (int i = 0; i < count; ++i) N3_REQUIRE(tokens[i] < s->m->g.vocab, "token %u outside the vocabulary", tokens[i]);
+    for (int i = 0; i < count; ++i) N3_CALL(rn_n3_session_push(s, tokens[i]));
+    return RN_OK;
+}
+
+int rn_n3_session_length(const rn_n3_session* s, int* length) {
+    N3_REQUIRE(s && length, "null argument");
+    *length = s->length;
+    return RN_OK;
+}
+
+// Session::logits (session.rs:151-165): logits [output_vocab] on the host
+int rn_n3_session_logits(rn_n3_session* s, float* logits) {
+    N3_REQUIRE(s && logits, "null argument");
+    const rn_n3_model* m = s->m;
+    const int d = (int)m->g.d_model;
+    hipStream_t st = s->stream;
+    rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->hidden, d, s->quantised);
+    N3_HIP(hipGetLastError());
+    N3_CALL(rotate(m->embedding, s->quantised, s->rotated, st));
+    CodebookParams p = m->embedding->cb;
+    p.rows = m->output_vocab;  // multiply_rows(0, ..) over the first output_vocab rows
+    if (m->embedding->bits == 1 || m->embedding->bits == 3)
+        N3_HIP(launch_codebook_float(p, s->rotated, 1, s->logits, false, st));
+    else
+        N3_HIP(launch_codebook_product(p, s->rotated, 1, s->logits, nullptr, st));
+    N3_HIP(hipMemcpyAsync(logits, s->logits, (size_t)m->output_vocab * 4, hipMemcpyDeviceToHost, st));
+    N3_HIP(hipStreamSynchronize(st));
+    return RN_OK;
+}
+
+int rn_n3_session_hidden(rn_n3_session* s, float* hidden) {
+    N3_REQUIRE(s && hidden, "null argument");
+    N3_HIP(hipMemcpyAsync(hidden, s->hidden, (size_t)s->m->g.d_model * 4, hipMemcpyDeviceToHost, s->stream));
+    N3_HIP(hipStreamSynchronize(s->stream));
+    return RN_OK;
+}
+
+// Session::cells (session.rs:137-139): [active + 1][d_model] of the last push
+int rn_n3_session_cells(rn_n3_session* s, float* cells) {
+    N3_REQUIRE(s && cells, "null argument");
+    const size_t n = (s->m->active.size() + 1) * (size_t)s->m->g.d_model;
+    N3_HIP(hipMemcpyAsync(cells, s->cells, n * 4, hipMemcpyDeviceToHost, s->stream));
+    N3_HIP(hipStreamSynchronize(s->stream));
+    return RN_OK;
+}
+
+namespace {
+int pooled_into(rn_n3_session* s, size_t i) {
+    const N3Head& h = s->m->heads[i];
+    const int slots = h.layers * h.per_layer;
+    rn_launch(n3_readout_kernel, dim3(slots), dim3(256), 0, s->stream, (const float*)s->weighted[i],
+              (const float*)s->total[i], (const float*)h.gain, h.width, s->readouts);
+    N3_HIP(hipGetLastError());
+    rn_launch(n3_pool_kernel, dim3(h.queries), dim3(256), 0, s->stream, (const float*)s->readouts, slots,
+              (const float*)h.query, (const float*)h.row_bias, h.width, s->pooled);
+    N3_HIP(hipGetLastError());
+    return RN_OK;
+}
+int head_index(const rn_n3_model* m, int code) {
+    for (size_t i = 0; i < m->heads.size(); ++i)
+        if (m->heads[i].code == code) return (int)i;
+    return -1;
+}
+}  // namespace
+
+// Session::pooled_readout (session.rs:131-135; heads.rs:99-125): queries x width
+// floats on the host; *count is 0 when no head has the code.
+int rn_n3_session_pooled_readout(rn_n3_session* s, int code, float* out, int capacity, int* count) {
+    N3_REQUIRE(s && count, "null argument");
+    const int i = head_index(s->m, code);
+    *count = 0;
+    if (i < 0) return RN_OK;
+    const N3Head& h = s->m->heads[(size_t)i];
+    N3_REQUIRE(s->length > 0, "no token has been observed");
+    const int n = h.queries * h.width;
+    N3_REQUIRE(out && capacity >= n, "output holds %d floats, %d needed", capacity, n);
+    N3_CALL(pooled_into(s, (size_t)i));
+    N3_HIP(hipMemcpyAsync(out, s->pooled, (size_t)n * 4, hipMemcpyDeviceToHost, s->stream));
+    N3_HIP(hipStreamSynchronize(s->stream));
+    *count = n;
+    return RN_OK;
+}
+
+// Session::head_output (session.rs:125-129; heads.rs:127-136)
+int rn_n3_session_head_output(rn_n3_session* s, int code, float* out, int capacity, int* count) {
+    N3_REQUIRE(s && count, "null argument");
+    const int i = head_index(s->m, code);
+    *count = 0;
+    if (i < 0) return RN_OK;
+    const N3Head& h = s->m->heads[(size_t)i];
+    N3_REQUIRE(s->length > 0, "no token has been observed");
+    const int rows = h.projection->rows;
+    N3_REQUIRE(out && capacity >= rows, "output holds %d floats, %d needed", capacity, rows);
+    N3_CALL(pooled_into(s, (size_t)i));
+    N3_CALL(rotate(h.projection, s->pooled, s->rotated, s->stream));
+    N3_CALL(product(h.projection, s->rotated, s->head_out, s->stream));
+    rn_launch(n3_add_kernel, dim3((rows + 255) / 256), dim3(256), 0, s->stream, s->head_out, (const float*)h.bias, rows);
+    N3_HIP(hipGetLastError());
+    N3_HIP(hipMemcpyAsync(out, s->head_out, (size_t)rows * 4, hipMemcpyDeviceToHost, s->stream));
+    N3_HIP(hipStreamSynchronize(s->stream));
+    *count = rows;
+    return RN_OK;
+}
+
+// The int8 cache of one layer for the first `length` positions, on the host:
+// keys / values [length][kv][64] (the reference's order), scales [kv][length].
+int rn_n3_session_cache(rn_n3_session* s, int layer, int8_t* keys, float* key_scales, int8_t* values,
+                        float* value_scales) {
+    N3_REQUIRE(s && keys && key_scales && values && value_scales, "null argument");
+    N3_REQUIRE(layer >= 0 && layer < (int)s->m->g.num_layers, "layer %d out of range", layer);
+    const int KV = (int)s->m->g.num_kv_heads, n = s->length, cap = s->capacity;
+    const N3CacheDev& c = s->caches[(size_t)layer];
+    std::vector<int8_t> k((size_t)KV * cap * 64), v(k.size());
+    std::vector<float> ks((size_t)KV * cap), vs(ks.size());
+    N3_HIP(hipStreamSynchronize(s->stream));
+    N3_HIP(hipMemcpy(k.data(), c.keys, k.size(), hipMemcpyDeviceToHost));
+    N3_HIP(hipMemcpy(v.data(), c.values, v.size(), hipMemcpyDeviceToHost));
+    N3_HIP(hipMemcpy(ks.data(), c.key_scales, ks.size() * 4, hipMemcpyDeviceToHost));
+    N3_HIP(hipMemcpy(vs.data(), c.value_scales, vs.size() * 4, hipMemcpyDeviceToHost));
+    for (int p = 0; p < n; ++p)
+        for (int h = 0; h < KV; ++h) {
+            memcpy(keys + ((size_t)p * KV + h) * 64, k.data() + ((size_t)h * cap + p) * 64, 64);
+            memcpy(values + ((size_t)p * KV + h) * 64, v.data() + ((size_t)h * cap + p) * 64, 64);
+        }
+    for (int h = 0; h < KV; ++h) {
+        memcpy(key_scales + (size_t)h * n, ks.data() + (size_t)h * cap, (size_t)n * 4);
+        memcpy(value_scales + (size_t)h * n, vs.data() + (size_t)h * cap, (size_t)n * 4);
+    }
+    return RN_OK;
+}
+
+int rn_n3_session_stream(const rn_n3_session* s, void** stream) {
+    N3_REQUIRE(s && stream, "null argument");
+    *stream = s->stream;
+    return RN_OK;
+}
