@@ -860,3 +860,22 @@ def n3_attend_head(query, query_scale, keys, key_scales, values, value_scales) -
     lib.ro_n3_attend_head(_ptr(q), float(query_scale), _ptr(k), _ptr(ks), _ptr(v), _ptr(vs), count, qk, vd, qk, vd,
                           _ptr(out))
     return out
+
+
+lib.ro_n3_hadamard_arrays.argtypes = [_i, _i] + [_p] * 11 + [_i, _p]
+
+
+def n3_hadamard(t: dict, first_perm, second_perm, x) -> np.ndarray:
+    """hadamard.rs:55-107: t holds d1 d2 b2 d3 d4 [size], factors [6][32][32],
+    cond_v [width][rank], cond_u [rank][size]."""
+    size = t["d1"].size
+    rank = t["cond_u"].size // size
+    a = {k: _f32(v) for k, v in t.items()}
+    p1 = np.ascontiguousarray(first_perm, np.int32)
+    p2 = np.ascontiguousarray(second_perm, np.int32)
+    x = _f32(x)
+    out = np.empty(x.size, np.float32)
+    lib.ro_n3_hadamard_arrays(size, rank, _ptr(a["d1"]), _ptr(a["d2"]), _ptr(a["b2"]), _ptr(a["d3"]), _ptr(a["d4"]),
+                              _ptr(a["factors"]), _ptr(a["cond_v"]), _ptr(a["cond_u"]), _ptr(p1), _ptr(p2), _ptr(x),
+                              x.size, _ptr(out))
+    return out

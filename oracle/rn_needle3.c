@@ -179,8 +179,10 @@ static float* floats_of(const n3_seq* s, int index, int* count) {
 
 static int matrix_of(const n3_seq* s, int index, const float* codebook, ro_cbm* m) {
     const n3_record* r = &s->records[index];
-    if (r->kind != 3 || r->rank != 2) return -1;
+    if (r->kind != 3 || r->rank != 2 || r->bits < 1 || r->bits > 5) return -1;
+    if (r->group != 64 && r->group != 128 && r->group != 256) return -1;
     ro_cbm_init(m, s->bytes + r->offset, (int)r->shape[0], (int)r->shape[1], (int)r->group, (int)r->bits, codebook);
+    if (m->row_bytes * (size_t)m->rows + (size_t)m->rows * m->groups * 2 > r->nbytes) return -1;
     return 0;
 }
 
@@ -266,6 +268,7 @@ static int ladder_select(int layers, int depth, int* out) {
 int ro_n3_open(const uint8_t* bytes, size_t size, int depth, ro_n3_model** out) {
     *out = NULL;
     if (size < N3_HEADER || rd32(bytes) != 0x05E12A84u) return -1;
+    if ((size_t)N3_HEADER + 4 * (size_t)rd32(bytes + 8) + 44 * (size_t)rd32(bytes + 4) > size) return -1;
     ro_n3_model* m = (ro_n3_model*)calloc(1, sizeof(ro_n3_model));
     ro_n3_config* c = &m->config;
     const uint8_t* h = bytes + 4;
@@ -312,6 +315,12 @@ int ro_n3_open(const uint8_t* bytes, size_t size, int depth, ro_n3_model** out) 
         rec[i].nbytes = rd64(r + 28);
         rec[i].group = rd32(r + 36);
         rec[i].bits = rd32(r + 40);
+        /* archive.rs:52-66: every tensor inside the file */
+        if ((size_t)(dir - bytes) + 44 * (size_t)(i + 1) > size || rec[i].offset > size ||
+            rec[i].nbytes > size - rec[i].offset) {
+            m->records = rec;
+            goto bad;
+        }
     }
     m->records = rec;
     if (tensor_count < 1 || rec[tensor_count - 1].kind != 4) goto bad; /* the trailing tokenizer blob */
@@ -548,6 +557,30 @@ void ro_n3_hadamard_apply(const ro_n3_hadamard* h, const int32_t* first_perm, co
     free(scaled);
     free(modulation);
     free(weights);
+}
+
+/* hadamard.rs:55-107 over explicit arrays: factors [6][32][32] (w1a w1b w2a w2b
+ * w3a w3b), cond_v [width][rank], cond_u [rank][size] */
+void ro_n3_hadamard_arrays(int size, int rank, const float* d1, const float* d2, const float* b2, const float* d3,
+                           const float* d4, const float* factors, const float* cond_v, const float* cond_u,
+                           const int32_t* first_perm, const int32_t* second_perm, const float* input, int width,
+                           float* output) {
+    ro_n3_hadamard h;
+    memset(&h, 0, sizeof h);
+    h.size = size;
+    h.rank = rank;
+    h.d1 = (float*)d1;
+    h.d2 = (float*)d2;
+    h.b2 = (float*)b2;
+    h.d3 = (float*)d3;
+    h.d4 = (float*)d4;
+    for (int f = 0; f < 6; ++f) {
+        h.factors[f] = (float*)(factors + (size_t)f * 1024);
+        h.factor_sizes[f] = 32;
+    }
+    h.cond_v = (float*)cond_v;
+    h.cond_u = (float*)cond_u;
+    ro_n3_hadamard_apply(&h, first_perm, second_perm, input, width, output);
 }
 
 /* attend_head (kernels/src/attention.rs:53-80) as its aarch64 build runs it:

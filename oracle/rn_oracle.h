@@ -362,6 +362,10 @@ int ro_n3_head_output(const ro_n3_session* s, int code, float* out);            
 void ro_n3_table_indices(const ro_n3_config* c, const uint32_t* tokens, int position, int* indices); /* engram.rs:30-46 */
 void ro_n3_hadamard_apply(const ro_n3_hadamard* h, const int32_t* first_perm, const int32_t* second_perm,
                           const float* input, int width, float* output);            /* hadamard.rs:55-107 */
+void ro_n3_hadamard_arrays(int size, int rank, const float* d1, const float* d2, const float* b2, const float* d3,
+                           const float* d4, const float* factors, const float* cond_v, const float* cond_u,
+                           const int32_t* first_perm, const int32_t* second_perm, const float* input, int width,
+                           float* output);
 void ro_n3_attend_head(const int8_t* query, float query_scale, const int8_t* keys, const float* key_scales,
                        const int8_t* values, const float* value_scales, int count, int qk, int vd, int key_stride,
                        int value_stride, float* out);                                /* kernels/src/attention.rs:53-80 */
