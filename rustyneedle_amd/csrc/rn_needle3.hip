@@ -23,23 +23,26 @@
 //                     and fake-quantised (engram.rs:66-82);
 //   n3_engram_conv    the value taps over the site's ring (engram.rs:84-111);
 //   lanes route       rn_lanes (lanes.rs:48-84);
-//   n3_block_in       add_engram (session.rs:175-188), the input norm and the
-//                     fake quantisation before the projections;
+//   n3_block_in       add_engram (session.rs:175-188), the input norm, the fake
+//                     quantisation and the rotation before the projections;
 //   n3_qkv            conv taps (attention.rs:84-94), q/k norms, rotary, the
 //                     per-head int8 codes and the cache append;
 //   n3_attend         attend_head per query head (kernels/src/attention.rs:
 //                     53-80 as the aarch64 build runs it) times sigmoid(gate);
-//   n3_fake_quantise  the gated attention before the output projection;
+//   n3_fake_quantise  the gated attention, fake-quantised and rotated for the
+//                     output projection;
 //   n3_block_out      post norm and gate, the Hadamard MLP (hadamard.rs:55-107,
 //                     three 32 x 32 Kronecker products), block delta, lane
 //                     combine and the cell (lanes.rs:86-104);
 //   n3_final          lane mean and the final norm;
 //   n3_observe        the heads' online softmax (heads.rs:138-155).
-// The products are rn_codebook.hip's launches on rotated inputs.
+// The products are rn_codebook.hip's launches on rotated inputs; a layer's
+// q, k, v and gate projections are one stacked matrix (one launch).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -75,18 +78,36 @@ __device__ float n3_block_max(float v, float* red) {
     return r;
 }
 
+// Sequential folds s = s + f(a[i], b[i]) over i = 0..count-1 at a stride, in
+// order; the loads of sixteen elements are issued before their adds, so the
+// chain waits on the adds and not on each load.
+template <bool SQUARE>
+__device__ __forceinline__ float n3_fold(float s, const float* a, const float* b, int count, int stride,
+                                         int b_stride = -1) {
+    const int sb = b_stride < 0 ? stride : b_stride;
+    int i = 0;
+    for (; i + 16 <= count; i += 16) {
+        float x[16], y[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            x[j] = a[(size_t)(i + j) * stride];
+            y[j] = SQUARE ? x[j] : b[(size_t)(i + j) * sb];
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s = s + x[j] * y[j];
+    }
+    for (; i < count; ++i) {
+        const float x = a[(size_t)i * stride];
+        s = s + x * (SQUARE ? x : b[(size_t)i * sb]);
+    }
+    return s;
+}
+
 // ops.rs:7-17 over n values in LDS: eight strided lanes, summed in lane order,
 // then the tail. Every thread calls; all get the result.
 __device__ float n3_sum_of_squares(const float* v, int n, float* red) {
     const int tid = threadIdx.x;
-    if (tid < 8) {
-        float s = 0.0f;
-        for (int c = 0; c < n / 8; ++c) {
-            const float x = v[8 * c + tid];
-            s = s + x * x;
-        }
-        red[tid] = s;
-    }
+    if (tid < 8) red[tid] = n3_fold<true>(0.0f, v + tid, nullptr, n / 8, 8);
     __syncthreads();
     float total = 0.0f;
     for (int j = 0; j < 8; ++j) total = total + red[j];
@@ -134,6 +155,43 @@ __device__ __forceinline__ int n3_index(const uint8_t* row, int e, int ib) {
     return (raw >> (bit % 8)) & ((1 << ib) - 1);
 }
 
+// QuantisedMatrix::prepare (matrix.rs:123-128) in LDS: v [padded] (zero past
+// the columns) rotated group by group (walsh.rs:41-76): butterflies of span 1,
+// 2, 4, ... (low a + b, high a - b), then every value times `scale`.
+__device__ void n3_rotate(float* v, int padded, int group, float scale) {
+    const int half = group / 2;
+    for (int span = 1; span < group; span *= 2) {
+        for (int q = threadIdx.x; q < padded / 2; q += blockDim.x) {
+            const int g = q / half, w = q - g * half;
+            const int lo = g * group + (w / span) * 2 * span + (w % span), hi = lo + span;
+            const float a = v[lo], b = v[hi];
+            v[lo] = a + b;
+            v[hi] = a - b;
+        }
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < padded; i += blockDim.x) v[i] = v[i] * scale;
+    __syncthreads();
+}
+
+// dst[i] = src[i] for i < n, eight loads a thread issued before their stores
+// (the stores may alias the loads as far as the compiler knows)
+__device__ void n3_copy(float* dst, const float* src, int n) {
+    for (int base = 0; base < n; base += 8 * blockDim.x) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = base + j * blockDim.x + threadIdx.x;
+            t[j] = i < n ? src[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = base + j * blockDim.x + threadIdx.x;
+            if (i < n) dst[i] = t[j];
+        }
+    }
+}
+
 }  // namespace
 
 // ---- kernels ---------------------------------------------------------------
@@ -179,21 +237,7 @@ __global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherParams p) {
         buf[e] = v;
     }
     __syncthreads();
-    // walsh.rs:41-76 per group of the rows: butterflies of span 1, 2, 4, ...
-    // (low a + b, high a - b), then every value times 1 / sqrt(group)
-    const int half = c.group / 2;
-    for (int span = 1; span < c.group; span *= 2) {
-        for (int q = threadIdx.x; q < n / 2; q += blockDim.x) {
-            const int g = q / half, w = q - g * half;
-            const int lo = g * c.group + (w / span) * 2 * span + (w % span), hi = lo + span;
-            const float a = buf[lo], b = buf[hi];
-            buf[lo] = a + b;
-            buf[hi] = a - b;
-        }
-        __syncthreads();
-    }
-    for (int e = threadIdx.x; e < n; e += blockDim.x) buf[e] = buf[e] * c.wht_scale;
-    __syncthreads();
+    n3_rotate(buf, n, c.group, c.wht_scale);  // each table row's groups (dequantise_row)
     n3_fake_quantise(buf, n, red);
     for (int e = threadIdx.x; e < n; e += blockDim.x) p.out[e] = buf[e];
 }
@@ -223,7 +267,9 @@ struct N3BlockInParams {
     const float* norm_in;
     int d;
     float* x;             // [d]
-    float* quantised;     // [d] fake-quantised norm of x
+    int padded, group;    // of the projections
+    float wht_scale;
+    float* rotated;       // [padded] the fake-quantised norm of x, rotated (prepare)
 };
 
 // session.rs:112-118 with add_engram (session.rs:175-188).
@@ -240,8 +286,7 @@ __global__ __launch_bounds__(kN3Block) void n3_block_in_kernel(N3BlockInParams p
         __syncthreads();
         n3_unit_rms(tb, d, tb, red);
         if (threadIdx.x == 0) {  // Iterator::sum: in order from -0.0
-            float dot = -0.0f;
-            for (int i = 0; i < d; ++i) dot = dot + ta[i] * tb[i];
+            const float dot = n3_fold<false>(-0.0f, ta, tb, d, 1);
             alpha_s = libm_sigmoid(dot / sqrtf((float)d));
         }
         __syncthreads();
@@ -251,10 +296,11 @@ __global__ __launch_bounds__(kN3Block) void n3_block_in_kernel(N3BlockInParams p
     }
     n3_norm(xs, p.norm_in, d, ta, red);
     n3_fake_quantise(ta, d, red);
-    for (int i = threadIdx.x; i < d; i += blockDim.x) {
-        p.x[i] = xs[i];
-        p.quantised[i] = ta[i];
-    }
+    for (int i = d + threadIdx.x; i < p.padded; i += blockDim.x) ta[i] = 0.0f;
+    __syncthreads();
+    n3_rotate(ta, p.padded, p.group, p.wht_scale);
+    for (int i = threadIdx.x; i < d; i += blockDim.x) p.x[i] = xs[i];
+    for (int i = threadIdx.x; i < p.padded; i += blockDim.x) p.rotated[i] = ta[i];
 }
 
 struct N3QkvParams {
@@ -396,7 +442,15 @@ __global__ __launch_bounds__(256) void n3_attend_kernel(N3AttendParams p) {
     const int vector_count = count - count % 4;
     if (tid < 4) {
         float s = 0.0f;
-        for (int pp = tid; pp < vector_count; pp += 4) s = s + c_s[pp];
+        int pp = tid;
+        for (; pp + 64 <= vector_count; pp += 64) {
+            float e[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) e[j] = c_s[pp + 4 * j];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s = s + e[j];
+        }
+        for (; pp < vector_count; pp += 4) s = s + c_s[pp];
         lanes_s[tid] = s;
     }
     const float scale = cpeak / 2047.0f;
@@ -427,14 +481,23 @@ __global__ __launch_bounds__(256) void n3_attend_kernel(N3AttendParams p) {
     }
 }
 
-// ops.rs:120-125 over n <= 4096 values (one block)
-__global__ __launch_bounds__(kN3Block) void n3_fake_quantise_kernel(const float* in, int n, float* out) {
+// ops.rs:120-125 over n <= 4096 values (one block), then, for group > 0,
+// prepare for a matrix of that group and padded width (matrix.rs:123-128)
+__global__ __launch_bounds__(kN3Block) void n3_fake_quantise_kernel(const float* in, int n, int padded, int group,
+                                                                    float wht_scale, float* out) {
     __shared__ float buf[kN3MaxWidth];
     __shared__ float red[32];
     for (int i = threadIdx.x; i < n; i += blockDim.x) buf[i] = in[i];
     __syncthreads();
     n3_fake_quantise(buf, n, red);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = buf[i];
+    if (group > 0) {
+        for (int i = n + threadIdx.x; i < padded; i += blockDim.x) buf[i] = 0.0f;
+        __syncthreads();
+        n3_rotate(buf, padded, group, wht_scale);
+    } else {
+        padded = n;
+    }
+    for (int i = threadIdx.x; i < padded; i += blockDim.x) out[i] = buf[i];
 }
 
 struct N3BlockOutParams {
@@ -464,32 +527,68 @@ struct N3BlockOutParams {
 // 1024 threads; x and out in LDS (distinct), mixed LDS scratch.
 __device__ void n3_kronecker32(const float* x, const float* left, const float* right, float* mixed, float* out) {
     const int tid = threadIdx.x, i = tid >> 5, c = tid & 31;
+    float a[32], b[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        a[j] = right[j * 32 + c];
+        b[j] = x[i * 32 + j];
+    }
     float acc = 0.0f;
-#pragma unroll 8
-    for (int j = 0; j < 32; ++j) acc = __builtin_fmaf(right[j * 32 + c], x[i * 32 + j], acc);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) acc = __builtin_fmaf(a[j], b[j], acc);
     mixed[tid] = acc;
     __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+        a[r] = mixed[r * 32 + c];
+        b[r] = left[r * 32 + i];
+    }
     acc = 0.0f;
-#pragma unroll 8
-    for (int r = 0; r < 32; ++r) acc = __builtin_fmaf(mixed[r * 32 + c], left[r * 32 + i], acc);
+#pragma unroll
+    for (int r = 0; r < 32; ++r) acc = __builtin_fmaf(a[r], b[r], acc);
     out[tid] = acc;
     __syncthreads();
 }
 
+// LDS of the block tail: six Hadamard-sized arrays, the rank-8 condition rows
+struct N3TailLds {
+    float *xs, *a, *sc, *st, *mx, *modulation, *cv, *chains, *weights, *red;
+};
+
+// A thread's elementwise Hadamard tensors, read at kernel start so that their
+// latency overlaps the work before the MLP.
+struct N3TailPre {
+    float d1, d2, b2, d3, d4, cond_u[8];
+    int perm1, perm2;
+};
+
+__device__ N3TailPre n3_tail_prefetch(const N3BlockOutParams& p) {
+    const int tid = threadIdx.x;
+    N3TailPre t;
+    t.d1 = p.d1[tid];
+    t.d2 = p.d2[tid];
+    t.b2 = p.b2[tid];
+    t.d3 = p.d3[tid];
+    t.d4 = p.d4[tid];
+    t.perm1 = p.perm1[tid];
+    t.perm2 = p.perm2[tid];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) t.cond_u[r] = r < p.rank ? p.cond_u[(size_t)r * kN3Hadamard + tid] : 0.0f;
+    return t;
+}
+
 // session.rs:119-146 from the output projection: post norm, gated residual,
 // the pre-Hadamard norm, HadamardWeights::apply, the block delta, the lane
-// combine and the next cell. One block of 1024 threads (the Hadamard size).
-__global__ __launch_bounds__(kN3Block) void n3_block_out_kernel(N3BlockOutParams p) {
-    __shared__ float xs[kN3Hadamard], a[kN3Hadamard], sc[kN3Hadamard], st[kN3Hadamard], mx[kN3Hadamard];
-    __shared__ float modulation[kN3Hadamard];
-    __shared__ float chains[4][8];
-    __shared__ float weights[64];
-    __shared__ float red[32];
+// combine and the next cell; the next stream also into `keep` (LDS) when set.
+// 1024 threads (the Hadamard size).
+__device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* keep, const N3TailPre& pre) {
+    float *xs = l.xs, *a = l.a, *sc = l.sc, *st = l.st, *mx = l.mx, *modulation = l.modulation;
+    float *cv = l.cv, *weights = l.weights, *red = l.red;
+    float(*chains)[8] = reinterpret_cast<float(*)[8]>(l.chains);
     const int tid = threadIdx.x, d = p.d;
-    for (int i = tid; i < d; i += blockDim.x) {
-        a[i] = p.attention[i];
-        xs[i] = p.x[i];
-    }
+    n3_copy(a, p.attention, d);
+    n3_copy(xs, p.x, d);
+    if (p.rank == 8) n3_copy(cv, p.cond_v, d * 8);
     __syncthreads();
     n3_norm(a, p.post_norm, d, a, red);
     for (int i = tid; i < d; i += blockDim.x) xs[i] = xs[i] + p.gate * a[i];
@@ -499,9 +598,7 @@ __global__ __launch_bounds__(kN3Block) void n3_block_out_kernel(N3BlockOutParams
     if (p.rank == 8) {
         if (tid < 32) {
             const int j = tid >> 3, r = tid & 7;
-            float s = 0.0f;
-            for (int g0 = 0; g0 + j < d; g0 += 4) s = s + a[g0 + j] * p.cond_v[(size_t)(g0 + j) * 8 + r];
-            chains[j][r] = s;
+            chains[j][r] = n3_fold<false>(0.0f, a + j, cv + j * 8 + r, (d - j + 3) / 4, 4, 32);
         }
         __syncthreads();
         if (tid < 8) weights[tid] = (((0.0f + chains[0][tid]) + chains[1][tid]) + chains[2][tid]) + chains[3][tid];
@@ -525,32 +622,54 @@ __global__ __launch_bounds__(kN3Block) void n3_block_out_kernel(N3BlockOutParams
     __syncthreads();
     {
         float m = 1.0f;
-        for (int r = 0; r < p.rank; ++r) m = m + weights[r] * p.cond_u[(size_t)r * kN3Hadamard + tid];
+        if (p.rank <= 8) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (r < p.rank) m = m + weights[r] * pre.cond_u[r];
+        } else {
+            for (int r = 0; r < p.rank; ++r) m = m + weights[r] * p.cond_u[(size_t)r * kN3Hadamard + tid];
+        }
         modulation[tid] = m;
-        sc[tid] = (tid < d ? a[tid] : 0.0f) * p.d1[tid];
+        sc[tid] = (tid < d ? a[tid] : 0.0f) * pre.d1;
     }
     __syncthreads();
     n3_kronecker32(sc, p.factors[0], p.factors[1], mx, st);
-    sc[tid] = silu(((p.d2[tid] * modulation[tid]) * st[p.perm1[tid]]) + p.b2[tid]);
+    sc[tid] = silu(((pre.d2 * modulation[tid]) * st[pre.perm1]) + pre.b2);
     __syncthreads();
     n3_kronecker32(sc, p.factors[2], p.factors[3], mx, st);
-    sc[tid] = st[p.perm2[tid]] * p.d3[tid];
+    sc[tid] = st[pre.perm2] * pre.d3;
     __syncthreads();
     n3_kronecker32(sc, p.factors[4], p.factors[5], mx, st);
+    mx[tid] = st[tid] * pre.d4;  // mlp
+    __syncthreads();
     // block output, delta (lanes.rs:100-104), combine (lanes.rs:86-98), cell
     for (int i = tid; i < d; i += blockDim.x) {
-        const float xo = xs[i] + st[i] * p.d4[i];
+        const float xo = xs[i] + mx[i];
         const float delta = xo - p.input[i];
         float mean = 0.0f;
-        for (int l = 0; l < p.lanes; ++l) {
+        for (int ln = 0; ln < p.lanes; ++ln) {
             float o = 0.0f;
-            for (int s = 0; s < p.lanes; ++s) o = o + p.residual[l * p.lanes + s] * p.stream[(size_t)s * d + i];
-            o = o + p.post[l] * delta;
-            p.next[(size_t)l * d + i] = o;
+            for (int s = 0; s < p.lanes; ++s) o = o + p.residual[ln * p.lanes + s] * p.stream[(size_t)s * d + i];
+            o = o + p.post[ln] * delta;
+            p.next[(size_t)ln * d + i] = o;
+            if (keep) keep[(size_t)ln * d + i] = o;
             mean = mean + o / (float)p.lanes;
         }
         p.cell[i] = mean;
     }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kN3Block) void n3_block_out_kernel(N3BlockOutParams p) {
+    __shared__ float xs[kN3Hadamard], a[kN3Hadamard], sc[kN3Hadamard], st[kN3Hadamard], mx[kN3Hadamard];
+    __shared__ float modulation[kN3Hadamard];
+    __shared__ float chains[32];
+    __shared__ float weights[64];
+    __shared__ float red[32];
+    __shared__ float cv[kN3Hadamard * 8];  // cond_v of rank 8
+    const N3TailLds l{xs, a, sc, st, mx, modulation, cv, chains, weights, red};
+    const N3TailPre pre = n3_tail_prefetch(p);
+    n3_tail(p, l, nullptr, pre);
 }
 
 // session.rs:141-144: lane mean and the final norm
@@ -572,11 +691,7 @@ __global__ __launch_bounds__(kN3Block) void n3_final_kernel(const float* stream,
 // order from -0.0, plus the tail from -0.0. All threads get the value.
 __device__ float n3_dot_product(const float* a, const float* b, int n, float* red) {
     const int tid = threadIdx.x;
-    if (tid < 8) {
-        float s = 0.0f;
-        for (int c = 0; c < n / 8; ++c) s = s + a[8 * c + tid] * b[8 * c + tid];
-        red[tid] = s;
-    }
+    if (tid < 8) red[tid] = n3_fold<false>(0.0f, a + tid, b + tid, n / 8, 8);
     __syncthreads();
     float total = -0.0f;
     for (int j = 0; j < 8; ++j) total = total + red[j];
@@ -662,6 +777,645 @@ __global__ void n3_add_kernel(float* y, const float* bias, int n) {
     if (i < n) y[i] = y[i] + bias[i];
 }
 
+// ---- the fused step: three kernels a layer -------------------------------------
+//
+//   n3_attention_kernel  one block a query head: the head's q, its kv head's k
+//                        and v, and its gate rows of the stacked projection
+//                        (integer path on the block's own group codes of the
+//                        rotated input), conv taps, norms, rotary, codes, the
+//                        cache append (the blocks of a kv group write the same
+//                        bytes), attention and the gate;
+//   n3_out_kernel        each block fake-quantises and rotates the gated
+//                        attention itself, then 64 rows of the output
+//                        projection;
+//   n3_boundary_kernel   one block: the tail of a layer (n3_tail), the final
+//                        norm after the last, or the routing of the next layer
+//                        (its routing rows on the block's own group codes),
+//                        add_engram, the input norm, fake quantisation and
+//                        rotation.
+
+// The int8 levels of four indices (one per byte of sel) from the sixteen-entry
+// table in lut (v_perm_b32).
+template <int IB>
+__device__ __forceinline__ int n3_decode4(uint32_t sel, const uint32_t (&lut)[4]) {
+    if constexpr (IB == 2) {
+        return (int)__builtin_amdgcn_perm(0u, lut[0], sel);
+    } else {
+        const uint32_t s7 = sel & 0x07070707u;
+        const uint32_t lo = __builtin_amdgcn_perm(lut[1], lut[0], s7);
+        const uint32_t hi = __builtin_amdgcn_perm(lut[3], lut[2], s7);
+        const uint32_t m = ((sel >> 3) & 0x01010101u) * 0xffu;
+        return (int)((hi & m) | (lo & ~m));
+    }
+}
+
+__device__ __forceinline__ int n3_b4(int a, int b, int c, int d) {
+    return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | ((d & 0xff) << 24);
+}
+
+// Per-group int8 codes of an LDS input (panel.rs:52-66): scale = peak / 127 (1
+// for a zero peak), code = round-half-even(v / scale) clamped. A lane per run
+// of 16; the group's peak over its aligned lanes. Codes are stored in the
+// order the packed indices decode: for 2-bit dword k of a run holds elements
+// k, 4+k, 8+k, 12+k; for 4-bit dword 2h+k holds 8h+k, 8h+2+k, 8h+4+k, 8h+6+k.
+__device__ void n3_group_codes(const float* v, int P, int group, int ib, int4* xq, float* xs) {
+    const int runs = P / 16, rpg = group / 16;
+    for (int base = 0; base < runs; base += blockDim.x) {
+        const int u = base + threadIdx.x;
+        const bool valid = u < runs;
+        float x[16];
+        float peak = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            x[i] = valid ? v[16 * u + i] : 0.0f;
+            peak = fmaxf(peak, fabsf(x[i]));
+        }
+        for (int m = 1; m < rpg; m <<= 1) peak = fmaxf(peak, __shfl_xor(peak, m, 64));
+        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+        int c[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) c[i] = quantise_one(x[i], scale);
+        if (valid) {
+            xq[u] = ib == 2 ? make_int4(n3_b4(c[0], c[4], c[8], c[12]), n3_b4(c[1], c[5], c[9], c[13]),
+                                        n3_b4(c[2], c[6], c[10], c[14]), n3_b4(c[3], c[7], c[11], c[15]))
+                            : make_int4(n3_b4(c[0], c[2], c[4], c[6]), n3_b4(c[1], c[3], c[5], c[7]),
+                                        n3_b4(c[8], c[10], c[12], c[14]), n3_b4(c[9], c[11], c[13], c[15]));
+            if (u % rpg == 0) xs[u / rpg] = scale;
+        }
+    }
+    __syncthreads();
+}
+
+// Rows row_of(0..R) of a codebook matrix into LDS: the packed bytes (R x
+// row_bytes, row r at r * row_bytes) and the fp16 norms (R x groups). Four
+// 16-byte loads a thread are issued before their stores.
+template <typename RowOf>
+__device__ void n3_stage_rows(const CodebookParams& c, RowOf row_of, int R, uint8_t* w, uint16_t* nm) {
+    const int chunks = c.row_bytes / 16, total = R * chunks;
+    for (int base = 0; base < total; base += 4 * blockDim.x) {
+        int4 t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = base + j * blockDim.x + threadIdx.x;
+            if (i < total) {
+                const int r = i / chunks, k = i - r * chunks;
+                t[j] = reinterpret_cast<const int4*>(c.packed + (size_t)row_of(r) * c.row_bytes)[k];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = base + j * blockDim.x + threadIdx.x;
+            if (i < total) reinterpret_cast<int4*>(w)[i] = t[j];
+        }
+    }
+    const int G = c.padded / c.group;
+    for (int i = threadIdx.x; i < R * G; i += blockDim.x) {
+        const int r = i / G;
+        nm[i] = c.norms[(size_t)row_of(r) * G + (i - r * G)];
+    }
+}
+
+// The integer path of a codebook matrix (panel.rs:153-197 for 2-bit,
+// neon.rs:126-183 for 4-bit and ternary) over R rows staged in LDS (w, nm) for
+// one input quantised per group in LDS (xq, xs): exact group sums of level *
+// code, then per row the epilogue over the groups in order. Lanes hold runs
+// of 16 elements; a group's runs sit on aligned lanes and join by shuffles.
+__device__ void n3_rows(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R, const int4* xq,
+                        const float* xs, int* acc, float* y) {
+    const int ib = c.bits == 5 ? 2 : c.bits, runs = c.padded / 16, rpg = c.group / 16, G = c.padded / c.group;
+    const uint32_t lut[4] = {c.lut[0], c.lut[1], c.lut[2], c.lut[3]};
+    const int total = R * runs;
+    for (int base = 0; base < total; base += 4 * blockDim.x) {
+        int sum[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int idx = base + k * blockDim.x + threadIdx.x;
+            sum[k] = 0;
+            if (idx < total) {
+                const int r = idx / runs, u = idx - r * runs;
+                const uint8_t* bytes = w + (size_t)r * c.row_bytes + (size_t)u * 2 * ib;
+                const int4 x = xq[u];
+                int sm = 0;
+                if (ib == 2) {
+                    const uint32_t wd = *reinterpret_cast<const uint32_t*>(bytes);
+                    sm = dot4(n3_decode4<2>(wd & 0x03030303u, lut), x.x, sm);
+                    sm = dot4(n3_decode4<2>((wd >> 2) & 0x03030303u, lut), x.y, sm);
+                    sm = dot4(n3_decode4<2>((wd >> 4) & 0x03030303u, lut), x.z, sm);
+                    sm = dot4(n3_decode4<2>((wd >> 6) & 0x03030303u, lut), x.w, sm);
+                } else {
+                    const uint2 wd = *reinterpret_cast<const uint2*>(bytes);
+                    sm = dot4(n3_decode4<4>(wd.x & 0x0f0f0f0fu, lut), x.x, sm);
+                    sm = dot4(n3_decode4<4>((wd.x >> 4) & 0x0f0f0f0fu, lut), x.y, sm);
+                    sm = dot4(n3_decode4<4>(wd.y & 0x0f0f0f0fu, lut), x.z, sm);
+                    sm = dot4(n3_decode4<4>((wd.y >> 4) & 0x0f0f0f0fu, lut), x.w, sm);
+                }
+                sum[k] = sm;
+            }
+        }
+        // the runs of a group sit on rpg aligned lanes (DPP: exact integer sums)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            int v = sum[k];
+            v = v + dpp_move<0xb1>(v);
+            if (rpg >= 4) v = v + dpp_move<0x4e>(v);
+            if (rpg >= 8) v = v + dpp_move<0x141>(v);
+            if (rpg >= 16) v = v + dpp_move<0x140>(v);
+            const int idx = base + k * blockDim.x + threadIdx.x;
+            if (idx < total) {
+                const int r = idx / runs, u = idx - r * runs;
+                if (u % rpg == 0) acc[r * G + u / rpg] = v;
+            }
+        }
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < R; r += blockDim.x) {
+        float t = 0.0f;
+        for (int g = 0; g < G; ++g) {
+            const float norm = __half2float(__ushort_as_half(nm[r * G + g]));
+            const float a = (float)acc[r * G + g];
+            if (c.bits == 2)
+                t = fmaf(a, (norm * c.lscale) * xs[g], t);  // panel.rs:184-188
+            else
+                t = t + (((a * norm) * c.lscale) * xs[g]);  // neon.rs:158,180
+        }
+        y[r] = t;
+    }
+    __syncthreads();
+}
+
+struct N3AttentionParams {
+    CodebookParams qkvg;   // rows q [H*64] | k [KV*64] | v [KV*64] | gate [H*64]
+    const float* rotated;  // [padded] the prepared input of the projections
+    float* hist;           // conv-tap ring [taps][q | k | v]
+    const float* taps[3];
+    int ntaps, position, H, KV, cap, first, count;
+    const float* q_norm;
+    const float* k_norm;
+    const float* cos_row;
+    const float* sin_row;
+    int8_t* keys;
+    float* key_scales;
+    int8_t* values;
+    float* value_scales;
+    float* out;  // [H][64], times sigmoid(gate)
+};
+
+constexpr int kN3AttendThreads = 1024;
+constexpr int kN3HeadRowBytes = 256;  // the head's 256 staged rows, each at most 256 bytes (2-bit, 1024 columns)
+
+__global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3AttentionParams p) {
+    __shared__ __align__(16) uint8_t w_s[256 * kN3HeadRowBytes];
+    __shared__ uint16_t nm_s[256 * 16];
+    __shared__ float x_s[kN3Hadamard];
+    __shared__ int4 xq[kN3Hadamard / 16];
+    __shared__ float xs[64];
+    __shared__ int acc[64 * kN3Head];  // the row group sums, then the value sums
+    __shared__ float y_s[256];
+    __shared__ float v_s[3][kN3Head];
+    __shared__ float red_s[3][8];
+    __shared__ __align__(16) int8_t qc_s[kN3Head];
+    __shared__ float qscale_s;
+    __shared__ float c_s[kN3MaxAttend];
+    __shared__ float red[16];
+    __shared__ float lanes_s[4];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int group = p.H / p.KV, kvh = h / group, P = p.qkvg.padded;
+    const int qw = p.H * kN3Head, kw = p.KV * kN3Head, width_all = qw + 2 * kw;
+    auto row_of = [&](int r) -> int {
+        return r < 64 ? h * 64 + r
+                      : r < 128 ? qw + kvh * 64 + (r - 64)
+                                : r < 192 ? qw + kw + kvh * 64 + (r - 128) : qw + 2 * kw + h * 64 + (r - 192);
+    };
+    n3_stage_rows(p.qkvg, row_of, 256, w_s, nm_s);
+    for (int i = tid; i < P; i += blockDim.x) x_s[i] = p.rotated[i];
+    __syncthreads();
+    n3_group_codes(x_s, P, p.qkvg.group, p.qkvg.bits == 5 ? 2 : p.qkvg.bits, xq, xs);
+    n3_rows(p.qkvg, w_s, nm_s, 256, xq, xs, acc, y_s);
+    // waves 0, 1, 2: the query head, then its key and value heads (attention.rs:110-141)
+    const int which = wave < 3 ? wave : 0;
+    const int head = which == 0 ? h : kvh;
+    const int width = which == 0 ? qw : kw, off = which == 0 ? 0 : (which == 1 ? qw : qw + kw);
+    const int col = head * kN3Head + lane;
+    float v = 0.0f;
+    if (wave < 3) {
+        const float raw = y_s[which * 64 + lane];
+        v = raw;
+        if (p.ntaps > 0) {
+            p.hist[(size_t)(p.position % p.ntaps) * width_all + off + col] = raw;
+            const int n = min(p.ntaps, p.position + 1);
+            v = 0.0f;
+            for (int tap = 0; tap < n; ++tap) {
+                const float sample =
+                    tap == 0 ? raw : p.hist[(size_t)((p.position - tap) % p.ntaps) * width_all + off + col];
+                v = v + p.taps[which][(size_t)tap * width + col] * sample;
+            }
+        }
+        v_s[which][lane] = v;
+    }
+    __syncthreads();
+    if (wave < 2 && lane < 8) {
+        float s = 0.0f;
+        for (int c = 0; c < kN3Head / 8; ++c) s = s + v_s[which][8 * c + lane] * v_s[which][8 * c + lane];
+        red_s[which][lane] = s;
+    }
+    __syncthreads();
+    if (wave < 2) {
+        float ss = 0.0f;
+        for (int j = 0; j < 8; ++j) ss = ss + red_s[which][j];
+        const float inverse = 1.0f / sqrtf(ss / (float)kN3Head + 1e-6f);
+        const float* gain = which == 0 ? p.q_norm : p.k_norm;
+        v = ((1.0f + gain[lane]) * v) * inverse;
+    }
+    __syncthreads();
+    if (wave < 2) v_s[which][lane] = v;
+    __syncthreads();
+    if (wave < 2) {
+        const int half = kN3Head / 2;
+        if (lane < half) {
+            const float a = v_s[which][lane], bb = v_s[which][lane + half];
+            v = a * p.cos_row[lane] - bb * p.sin_row[lane];
+        } else {
+            const int i = lane - half;
+            const float a = v_s[which][i], bb = v_s[which][lane];
+            v = bb * p.cos_row[i] + a * p.sin_row[i];
+        }
+    }
+    if (wave < 3) {  // ops.rs:112-118 per head
+        const float peak = wave_max(fabsf(v));
+        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+        const int8_t code = (int8_t)quantise_one(v, scale);
+        if (which == 0) {
+            qc_s[lane] = code;
+            if (lane == 0) qscale_s = scale;
+        } else {
+            const size_t row = (size_t)kvh * p.cap + p.position;
+            (which == 1 ? p.keys : p.values)[row * kN3Head + lane] = code;
+            if (lane == 0) (which == 1 ? p.key_scales : p.value_scales)[row] = scale;
+        }
+    }
+    __syncthreads();  // the cache row of this position, written above, is read below
+    // kernels/src/attention.rs:53-80 (as n3_attend_kernel)
+    const int count = p.count;
+    const float query_scale = qscale_s * (1.0f / sqrtf((float)kN3Head));
+    int4 q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = reinterpret_cast<const int4*>(qc_s)[i];
+    const int8_t* kbase = p.keys + ((size_t)kvh * p.cap + p.first) * kN3Head;
+    const float* ks = p.key_scales + (size_t)kvh * p.cap + p.first;
+    const float* vsc = p.value_scales + (size_t)kvh * p.cap + p.first;
+    float peak = -INFINITY;
+    for (int pp = tid; pp < count; pp += kN3AttendThreads) {
+        const int4* k = reinterpret_cast<const int4*>(kbase + (size_t)pp * kN3Head);
+        int score = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) score = dot16(q[i], k[i], score);
+        const float c = ((float)score * ks[pp]) * query_scale;
+        c_s[pp] = c;
+        peak = fmaxf(peak, c);
+    }
+    peak = n3_block_max(peak, red);
+    float cpeak = 0.0f;
+    for (int pp = tid; pp < count; pp += kN3AttendThreads) {
+        const float e = fast_exp(c_s[pp] - peak);
+        c_s[pp] = e;
+        cpeak = fmaxf(cpeak, fabsf(e * vsc[pp]));
+    }
+    cpeak = n3_block_max(cpeak, red);
+    const int vector_count = count - count % 4;
+    if (tid < 4) {
+        float s = 0.0f;
+        int pp = tid;
+        for (; pp + 64 <= vector_count; pp += 64) {
+            float e[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) e[j] = c_s[pp + 4 * j];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s = s + e[j];
+        }
+        for (; pp < vector_count; pp += 4) s = s + c_s[pp];
+        lanes_s[tid] = s;
+    }
+    // the values: thread (dims 4 dg .. 4 dg + 3, positions pc mod 64), four
+    // positions' loads issued before their weights are applied
+    const float scale = cpeak / 2047.0f;
+    const int dg = tid & 15, pc = tid >> 4;
+    int av[4] = {0, 0, 0, 0};
+    if (cpeak > 0.0f) {
+        const int8_t* vbase = p.values + ((size_t)kvh * p.cap + p.first) * kN3Head + 4 * dg;
+        for (int pp0 = pc; pp0 < count; pp0 += 4 * 64) {
+            int packed[4];
+            float sv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pp = pp0 + 64 * j;
+                packed[j] = pp < count ? *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head) : 0;
+                sv[j] = pp < count ? vsc[pp] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pp = pp0 + 64 * j;
+                if (pp >= count) continue;
+                const int wgt = (int)__builtin_roundf((c_s[pp] * sv[j]) / scale);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) av[k] += wgt * (int)(int8_t)(packed[j] >> (8 * k));
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[pc * kN3Head + 4 * dg + k] = av[k];
+    __syncthreads();
+    if (tid < kN3Head) {
+        int sum = 0;
+        for (int c = 0; c < 64; ++c) sum += acc[c * kN3Head + tid];
+        float total = (lanes_s[0] + lanes_s[1]) + (lanes_s[2] + lanes_s[3]);
+        for (int pp = vector_count; pp < count; ++pp) total = total + c_s[pp];
+        float o = cpeak > 0.0f ? (float)sum * scale : 0.0f;
+        o = o * (1.0f / total);
+        o = o * libm_sigmoid(y_s[192 + tid]);
+        p.out[(size_t)h * kN3Head + tid] = o;
+    }
+}
+
+struct N3OutParams {
+    CodebookParams out;
+    const float* attended;  // [n] gated attention
+    int n;
+    float* y;               // [rows]
+};
+
+constexpr int kN3OutRowBytes = 1024;  // 4-bit over 2048 columns or 2-bit over 4096
+
+// fake_quantise_int8 of the gated attention, prepare, then rows
+// [64 * blockIdx.x, + 64) of the output projection (attention.rs:150-153)
+__global__ __launch_bounds__(256) void n3_out_kernel(N3OutParams p) {
+    __shared__ __align__(16) uint8_t w_s[64 * kN3OutRowBytes];
+    __shared__ uint16_t nm_s[64 * 64];
+    __shared__ float v[kN3MaxWidth];
+    __shared__ int4 xq[kN3MaxWidth / 16];
+    __shared__ float xs[64];
+    __shared__ int acc[64 * 64];
+    __shared__ float y_s[64];
+    __shared__ float red[8];
+    const int P = p.out.padded;
+    const int r0 = blockIdx.x * 64, R = min(64, p.out.rows - r0);
+    n3_stage_rows(p.out, [&](int r) { return r0 + r; }, R, w_s, nm_s);
+    for (int i = threadIdx.x; i < p.n; i += blockDim.x) v[i] = p.attended[i];
+    for (int i = p.n + threadIdx.x; i < P; i += blockDim.x) v[i] = 0.0f;
+    __syncthreads();
+    n3_fake_quantise(v, p.n, red);
+    n3_rotate(v, P, p.out.group, p.out.wht_scale);
+    n3_group_codes(v, P, p.out.group, p.out.bits == 5 ? 2 : p.out.bits, xq, xs);
+    n3_rows(p.out, w_s, nm_s, R, xq, xs, acc, y_s);
+    for (int r = threadIdx.x; r < R; r += blockDim.x) p.y[r0 + r] = y_s[r];
+}
+
+struct N3BoundaryParams {
+    int tail, final, route;
+    N3BlockOutParams t;          // the tail of the previous layer
+    const float* final_norm;
+    float* hidden;
+    // the routing of layer `layer` at `slot` (lanes.rs:48-84)
+    int layer, slot;
+    const float* stream;         // when there is no tail: the lanes stream
+    CodebookParams phi_pre, phi_post, phi_res;
+    const float *a_pre, *a_post, *a_res, *b_pre, *b_post, *b_res;
+    float* input;                // [d]
+    float* post;                 // [lanes]
+    float* residual;             // [lanes][lanes]
+    // the block input (session.rs:112-118)
+    const float* key;
+    const float* value;
+    const float* norm_in;
+    float* x;
+    int qpadded, qgroup;
+    float qscale;
+    float* rotated;
+    int d, lanes;
+};
+
+constexpr int kN3RouteRows = 24;         // 2 lanes + lanes^2 for four lanes
+constexpr int kN3RouteRowBytes = 768;    // 2-bit over 3072 columns
+
+__global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams p) {
+    __shared__ float xs_[kN3Hadamard], a_[kN3Hadamard], sc_[kN3Hadamard], st_[kN3Hadamard], mx_[kN3Hadamard];
+    __shared__ float mod_[kN3Hadamard];
+    __shared__ float chains_[32];
+    __shared__ float weights_[64];
+    __shared__ float red[32];
+    __shared__ float cv_[kN3Hadamard * 8];
+    __shared__ float stream_s[kN3MaxWidth];
+    __shared__ float rv[kN3MaxWidth];
+    __shared__ int4 rq[kN3MaxWidth / 16];
+    __shared__ float rs[64];
+    __shared__ int racc[kN3RouteRows * 64];
+    __shared__ float ry[kN3RouteRows];
+    __shared__ __align__(16) uint8_t pw[kN3RouteRows * kN3RouteRowBytes];
+    __shared__ uint16_t pn[kN3RouteRows * 64];
+    __shared__ float factors_s[6][kN3Hadamard];
+    __shared__ float tin_s[3][kN3Hadamard];  // the tail's attention, x and input
+    __shared__ float lane_s[2 * kMaxLanes + kMaxLanes * kMaxLanes];  // post, residual of the tail
+    __shared__ float small_s[4 * kMaxLanes + 2 * 64];  // a_pre a_post a_res (one each), b_pre, b_post, b_res
+    __shared__ float gate_s[kMaxLanes];
+    __shared__ float alpha_s;
+    const int tid = threadIdx.x, d = p.d, L = p.lanes, S = L * d;
+    // everything this block reads from memory, requested first
+    const int route_rows = 2 * L + L * L, G = p.phi_pre.padded / p.phi_pre.group;
+    if (p.route) {
+        const int layer = p.layer;
+        // the layer's rows of phi_pre, phi_post and phi_res, one after another
+        auto route_row = [&](int r) -> const uint8_t* {
+            return r < L ? p.phi_pre.packed + (size_t)(layer * L + r) * p.phi_pre.row_bytes
+                         : r < 2 * L ? p.phi_post.packed + (size_t)(layer * L + r - L) * p.phi_pre.row_bytes
+                                     : p.phi_res.packed + (size_t)(layer * L * L + r - 2 * L) * p.phi_pre.row_bytes;
+        };
+        auto route_norms = [&](int r) -> const uint16_t* {
+            return r < L ? p.phi_pre.norms + (size_t)(layer * L + r) * G
+                         : r < 2 * L ? p.phi_post.norms + (size_t)(layer * L + r - L) * G
+                                     : p.phi_res.norms + (size_t)(layer * L * L + r - 2 * L) * G;
+        };
+        const int chunks = p.phi_pre.row_bytes / 16, total = route_rows * chunks;
+        int4 tw[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = j * blockDim.x + tid;
+            if (i < total) tw[j] = reinterpret_cast<const int4*>(route_row(i / chunks))[i % chunks];
+        }
+        uint16_t tn = tid < route_rows * G ? route_norms(tid / G)[tid % G] : 0;
+        if (tid < L) {
+            small_s[3 + tid] = p.b_pre[layer * L + tid];
+            small_s[3 + L + tid] = p.b_post[layer * L + tid];
+        }
+        if (tid < L * L) small_s[3 + 2 * L + tid] = p.b_res[layer * L * L + tid];
+        if (tid == 0) {
+            small_s[0] = p.a_pre[layer];
+            small_s[1] = p.a_post[layer];
+            small_s[2] = p.a_res[layer];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = j * blockDim.x + tid;
+            if (i < total) reinterpret_cast<int4*>(pw)[i] = tw[j];
+        }
+        if (tid < route_rows * G) pn[tid] = tn;
+    }
+    N3BlockOutParams t = p.t;
+    N3TailPre pre{};
+    if (p.tail) {
+        pre = n3_tail_prefetch(t);
+        n3_copy(&factors_s[0][0], t.factors[0], kN3Hadamard);
+        for (int f = 1; f < 6; ++f) n3_copy(&factors_s[f][0], t.factors[f], kN3Hadamard);
+        n3_copy(tin_s[0], t.attention, d);
+        n3_copy(tin_s[1], t.x, d);
+        n3_copy(tin_s[2], t.input, d);
+        n3_copy(stream_s, t.stream, S);
+        if (tid < L) lane_s[tid] = t.post[tid];
+        if (tid < L * L) lane_s[kMaxLanes + tid] = t.residual[tid];
+        // the tail reads its copies
+        for (int f = 0; f < 6; ++f) t.factors[f] = factors_s[f];
+        t.attention = tin_s[0];
+        t.x = tin_s[1];
+        t.input = tin_s[2];
+        t.stream = stream_s;
+        t.post = lane_s;
+        t.residual = lane_s + kMaxLanes;
+    } else {
+        n3_copy(stream_s, p.stream, S);
+    }
+    __syncthreads();
+    const N3TailLds l{xs_, a_, sc_, st_, mx_, mod_, cv_, chains_, weights_, red};
+    if (p.tail) n3_tail(t, l, rv, pre);  // the next stream into rv, then into stream_s
+    if (p.tail) {
+        for (int i = tid; i < S; i += blockDim.x) stream_s[i] = rv[i];
+        __syncthreads();
+    }
+    if (p.final) {  // session.rs:141-144
+        for (int i = tid; i < d; i += blockDim.x) {
+            float v = 0.0f;
+            for (int ln = 0; ln < L; ++ln) v = v + stream_s[(size_t)ln * d + i] / (float)L;
+            a_[i] = v;
+        }
+        __syncthreads();
+        n3_norm(a_, p.final_norm, d, a_, red);
+        for (int i = tid; i < d; i += blockDim.x) p.hidden[i] = a_[i];
+    }
+    if (!p.route) return;
+    // the block input's tensors, requested before the routing work
+    float norm_in_r[1], key_r[1], value_r[1];
+    norm_in_r[0] = tid < d ? p.norm_in[tid] : 0.0f;
+    key_r[0] = (p.key != nullptr && tid < d) ? p.key[tid] : 0.0f;
+    value_r[0] = (p.key != nullptr && tid < d) ? p.value[tid] : 0.0f;
+    // lanes.rs:49-53: unit_rms, fake_quantise_int8, prepare (phi_pre's groups)
+    n3_unit_rms(stream_s, S, rv, red);
+    n3_fake_quantise(rv, S, red);
+    const int P = p.phi_pre.padded;
+    for (int i = S + tid; i < P; i += blockDim.x) rv[i] = 0.0f;
+    __syncthreads();
+    n3_rotate(rv, P, p.phi_pre.group, p.phi_pre.wht_scale);
+    // the routing matrices share their format, so one set of codes serves the
+    // three (matrix.rs:167-193 shares a plane input per format)
+    const int ib_pre = p.phi_pre.bits == 5 ? 2 : p.phi_pre.bits;
+    n3_group_codes(rv, P, p.phi_pre.group, ib_pre, rq, rs);
+    // lanes.rs:56-63: the layer's rows of the three routing matrices
+    n3_rows(p.phi_pre, pw, pn, route_rows, rq, rs, racc, ry);
+    // lanes.rs:64-83 (as lanes_route_kernel)
+    const int own = p.slot % L, n = L * L;
+    if (tid < 64) {
+        if (tid < L) {
+            const int lane = tid;
+            const float pre_offset = lane == own ? 8.0f + -4.0f : -4.0f;
+            gate_s[lane] = libm_sigmoid(small_s[0] * ry[lane] + small_s[3 + lane] + pre_offset);
+            const float post_offset = lane == own ? 0.0f : -4.0f;
+            p.post[lane] = 2.0f * libm_sigmoid(small_s[1] * ry[L + lane] + small_s[3 + L + lane] + post_offset);
+        }
+        const int i = tid;
+        const bool live = i < n;
+        const int r = live ? i / L : 0, c = live ? i % L : 0;
+        float m = live ? small_s[2] * ry[2 * L + i] + small_s[3 + 2 * L + i] : 0.0f;
+        if (L == 4) {
+            // lane 4r + c: a row's entries by quad broadcasts (DPP quad_perm
+            // [j,j,j,j]), a column's by rotations of the 16-lane row by 4, 8
+            // and 12 (row_ror), each put in row order
+            auto row_j = [](float v, int j) {
+                const int b = __float_as_int(v);
+                const int o = j == 0 ? dpp_move<0x00>(b) : j == 1 ? dpp_move<0x55>(b) : j == 2 ? dpp_move<0xaa>(b)
+                                                                                                : dpp_move<0xff>(b);
+                return __int_as_float(o);
+            };
+            // the row each rotation brings, rotated with the values
+            const int from4 = dpp_move<0x124>(r), from8 = dpp_move<0x128>(r);
+            auto col4 = [&](float v, float (&out)[4]) {
+                const int b = __float_as_int(v);
+                const float r4 = __int_as_float(dpp_move<0x124>(b)), r8 = __int_as_float(dpp_move<0x128>(b)),
+                            r12 = __int_as_float(dpp_move<0x12c>(b));
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    out[j] = j == r ? v : (j == from4 ? r4 : (j == from8 ? r8 : r12));
+            };
+            float peak = -INFINITY;  // ops.rs:199-202
+#pragma unroll
+            for (int j = 0; j < 4; ++j) peak = fmaxf(peak, row_j(m, j));
+            m = libm_expf(m - peak);
+            for (int it = 0; it < 20; ++it) {
+                float total = -0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) total = total + row_j(m, j);
+                m = m * (1.0f / fmaxf(total, 1.17549435e-38f));
+                float col[4];
+                col4(m, col);
+                total = -0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) total = total + col[j];
+                m = m * (1.0f / fmaxf(total, 1.17549435e-38f));
+            }
+        } else {
+            float peak = -INFINITY;
+            for (int j = 0; j < L; ++j) peak = fmaxf(peak, __shfl(m, r * L + j, 64));
+            m = libm_expf(m - peak);
+            for (int it = 0; it < 20; ++it) {
+                float total = -0.0f;
+                for (int j = 0; j < L; ++j) total = total + __shfl(m, r * L + j, 64);
+                m = m * (1.0f / fmaxf(total, 1.17549435e-38f));
+                total = -0.0f;
+                for (int j = 0; j < L; ++j) total = total + __shfl(m, j * L + c, 64);
+                m = m * (1.0f / fmaxf(total, 1.17549435e-38f));
+            }
+        }
+        if (live) p.residual[i] = m;
+    }
+    __syncthreads();
+    for (int i = tid; i < d; i += blockDim.x) {
+        float v = 0.0f;
+        for (int ln = 0; ln < L; ++ln) v = v + gate_s[ln] * stream_s[(size_t)ln * d + i];
+        xs_[i] = v;
+        p.input[i] = v;
+    }
+    __syncthreads();
+    // session.rs:112-118 with add_engram (session.rs:175-188)
+    if (p.key != nullptr) {
+        n3_unit_rms(xs_, d, a_, red);
+        if (tid < d) sc_[tid] = key_r[0];
+        __syncthreads();
+        n3_unit_rms(sc_, d, sc_, red);
+        if (tid == 0) {  // Iterator::sum: in order from -0.0
+            const float dot = n3_fold<false>(-0.0f, a_, sc_, d, 1);
+            alpha_s = libm_sigmoid(dot / sqrtf((float)d));
+        }
+        __syncthreads();
+        const float alpha = alpha_s;
+        if (tid < d) xs_[tid] = xs_[tid] + alpha * value_r[0];
+        __syncthreads();
+    }
+    if (tid < d) mx_[tid] = norm_in_r[0];
+    __syncthreads();
+    n3_norm(xs_, mx_, d, a_, red);
+    n3_fake_quantise(a_, d, red);
+    for (int i = d + tid; i < p.qpadded; i += blockDim.x) a_[i] = 0.0f;
+    __syncthreads();
+    n3_rotate(a_, p.qpadded, p.qgroup, p.qscale);
+    for (int i = tid; i < d; i += blockDim.x) p.x[i] = xs_[i];
+    for (int i = tid; i < p.qpadded; i += blockDim.x) p.rotated[i] = a_[i];
+}
+
 }  // namespace rn
 
 using namespace rn;
@@ -744,6 +1498,7 @@ struct Walk {
 
 struct N3Layer {
     rn_matrix *q = nullptr, *k = nullptr, *v = nullptr, *gate = nullptr, *out = nullptr;
+    rn_matrix* qkvg = nullptr;  // q | k | v | gate rows stacked, when the four share a format
     float *norm_in = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_norm = nullptr, *pre_norm = nullptr;
     float* taps[3] = {nullptr, nullptr, nullptr};
     float gate_sigmoid = 0.0f;
@@ -780,6 +1535,7 @@ struct rn_n3_model {
     std::vector<int> active;
     std::vector<void*> allocations;
     std::vector<rn_matrix*> matrices;
+    bool fused = false;  // the three-kernel step applies (integer-path formats, sizes in range)
 };
 
 namespace {
@@ -841,6 +1597,66 @@ int dense_rows(const rn_matrix* mat, const std::vector<int>& rows, std::vector<f
     return RN_OK;
 }
 
+// The four projections of a layer that share bits and group as one matrix:
+// their packed rows in order, then their norms in order (the same row
+// arithmetic; one launch instead of four, QuantisedMatrix::multiply_fused).
+int stack_projections(rn_n3_model* m, const rn_archive* a, const int idx[4], N3Layer& y) {
+    const rn_matrix* mats[4] = {y.q, y.k, y.v, y.gate};
+    for (const rn_matrix* x : mats)
+        if (x->bits != y.q->bits || x->group != y.q->group) return RN_OK;
+    std::vector<uint8_t> packed, norms;
+    int rows = 0;
+    for (int i = 0; i < 4; ++i) {
+        const uint8_t* data = nullptr;
+        size_t n = 0;
+        N3_CALL(rn_archive_tensor_bytes(a, idx[i], &data, &n));
+        const size_t pb = (size_t)mats[i]->rows * mats[i]->cb.row_bytes;
+        const size_t nb = (size_t)mats[i]->rows * (mats[i]->cb.padded / mats[i]->group) * 2;
+        packed.insert(packed.end(), data, data + pb);
+        norms.insert(norms.end(), data + pb, data + pb + nb);
+        rows += mats[i]->rows;
+    }
+    packed.insert(packed.end(), norms.begin(), norms.end());
+    const float* codebook = nullptr;
+    int count = 0;
+    N3_CALL(rn_archive_codebook(a, &codebook, &count));
+    N3_CALL(rn_matrix_create_codebook(packed.data(), packed.size(), rows, y.q->columns, y.q->group, y.q->bits, codebook,
+                                      count, &y.qkvg));
+    m->matrices.push_back(y.qkvg);
+    return RN_OK;
+}
+
+bool integer_path(const rn_matrix* x) { return x->bits == 2 || x->bits == 4 || x->bits == 5; }
+
+// The three-kernel step needs integer-path formats whose rows start where the
+// reference takes the panel form (2-bit rows on panels of four), at most four
+// lanes, and rows that fit its LDS tiles.
+bool fused_applies(const rn_n3_model* m) {
+    const rn_geometry& g = m->g;
+    const int L = (int)g.mhc_lanes;
+    if (2 * L + L * L > kN3RouteRows || g.d_model > (uint32_t)kN3Hadamard) return false;
+    if (m->phi_pre->cb.row_bytes > kN3RouteRowBytes || m->phi_pre->cb.padded / m->phi_pre->group > 64) return false;
+    if ((2 * L + L * L) * (m->phi_pre->cb.padded / m->phi_pre->group) > kN3Block ||
+        (2 * L + L * L) * (m->phi_pre->cb.row_bytes / 16) > 2 * kN3Block)
+        return false;
+    const rn_matrix* phis[3] = {m->phi_pre, m->phi_post, m->phi_res};
+    for (const rn_matrix* x : phis) {
+        if (!integer_path(x) || x->cb.padded > kN3MaxWidth || x->group != m->phi_pre->group ||
+            x->cb.padded != m->phi_pre->cb.padded || x->bits != m->phi_pre->bits)
+            return false;
+        if (x->bits == 2 && L % 4 != 0) return false;
+    }
+    for (const N3Layer& y : m->layers) {
+        if (y.qkvg == nullptr || !integer_path(y.qkvg) || y.qkvg->cb.padded > kN3Hadamard ||
+            y.qkvg->cb.row_bytes > kN3HeadRowBytes)
+            return false;
+        if (!integer_path(y.out) || y.out->cb.padded > kN3MaxWidth || y.out->cb.row_bytes > kN3OutRowBytes ||
+            y.out->cb.padded / y.out->group > 64)
+            return false;
+    }
+    return true;
+}
+
 // ladder.rs:1-29, through the public entry point
 int ladder(int layers, int depth, std::vector<int>& active) {
     std::vector<int32_t> chosen((size_t)std::max(layers, 1));
@@ -894,16 +1710,21 @@ int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out) {
         for (int l = 0; l < L; ++l) {
             N3Layer& y = m->layers[(size_t)l];
             N3_CALL(device_floats(m, archive, w.take(), &y.norm_in, d));
-            N3_CALL(matrix(m, archive, w.take(), &y.q));
-            N3_CALL(matrix(m, archive, w.take(), &y.k));
-            N3_CALL(matrix(m, archive, w.take(), &y.v));
+            int proj[4];
+            proj[0] = w.take();
+            N3_CALL(matrix(m, archive, proj[0], &y.q));
+            proj[1] = w.take();
+            N3_CALL(matrix(m, archive, proj[1], &y.k));
+            proj[2] = w.take();
+            N3_CALL(matrix(m, archive, proj[2], &y.v));
             if (g.qkv_conv_taps > 0)
                 for (int t = 0; t < 3; ++t)
                     N3_CALL(device_floats(m, archive, w.take(), &y.taps[t],
                                           (long)g.qkv_conv_taps * (t == 0 ? g.num_heads : g.num_kv_heads) * 64));
             N3_CALL(device_floats(m, archive, w.take(), &y.q_norm, 64));
             N3_CALL(device_floats(m, archive, w.take(), &y.k_norm, 64));
-            N3_CALL(matrix(m, archive, w.take(), &y.gate));
+            proj[3] = w.take();
+            N3_CALL(matrix(m, archive, proj[3], &y.gate));
             N3_CALL(matrix(m, archive, w.take(), &y.out));
             N3_CALL(device_floats(m, archive, w.take(), &y.post_norm, d));
             N3_CALL(host_floats(archive, w.take(), scalar));
@@ -936,6 +1757,7 @@ int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out) {
             N3_REQUIRE(y.q->cb.padded == y.k->cb.padded && y.q->cb.padded == y.v->cb.padded &&
                            y.q->cb.padded == y.gate->cb.padded,
                        "projections of layer %d must share their padded width", l);
+            N3_CALL(stack_projections(m, archive, proj, y));
         }
         N3_CALL(device_floats(m, archive, w.take(), &m->a_pre, L, &m->a_pre_h));
         N3_CALL(device_floats(m, archive, w.take(), &m->a_post, L, &m->a_post_h));
@@ -1039,6 +1861,7 @@ int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out) {
             }
         }
         if (w.failed) return n3_fail(RN_ERR_ARGUMENT, "directory ends inside the probe heads");
+        m->fused = fused_applies(m);
         N3_REQUIRE(w.next == w.end, "%d tensors follow the heads (an audio encoder is not part of this model)",
                    w.end - w.next);
         return RN_OK;
@@ -1072,6 +1895,7 @@ struct N3CacheDev {
 struct rn_n3_session {
     const rn_n3_model* m = nullptr;
     int capacity = 0, length = 0;
+    bool fused = false;  // three kernels a layer; RN_N3_PATH=stepwise forces one launch per piece
     hipStream_t stream = nullptr;
     std::vector<uint32_t> tokens;
     rn_lanes* lanes = nullptr;
@@ -1079,7 +1903,7 @@ struct rn_n3_session {
     std::vector<float*> rings, ekey, evalue;
     std::vector<void*> allocations;
     float *stream_a = nullptr, *stream_b = nullptr, *input = nullptr, *post = nullptr, *residual = nullptr;
-    float *x = nullptr, *quantised = nullptr, *rotated = nullptr, *prod = nullptr, *attended = nullptr;
+    float *x = nullptr, *rotated = nullptr, *prod = nullptr, *attended = nullptr;
     float *attn_out = nullptr, *row = nullptr, *gathered = nullptr, *eraw = nullptr, *qscales = nullptr;
     int8_t* qcodes = nullptr;
     float *cells = nullptr, *hidden = nullptr, *logits = nullptr, *cos = nullptr, *sin = nullptr;
@@ -1118,6 +1942,13 @@ int product(const rn_matrix* mat, const float* rotated, float* y, hipStream_t st
 int rotate(const rn_matrix* mat, const float* x, float* rotated, hipStream_t st) {
     N3_HIP(launch_codebook_rotate(x, 1, mat->columns, mat->cb.padded, mat->group, mat->cb.wht_scale, rotated, st));
     return RN_OK;
+}
+
+// attention.rs:172-178: the window's first position unless the layer is global
+int window_first(const rn_geometry& g, int layer, int total) {
+    if (g.sliding_window > 0 && !((g.global_layers >> layer) & 1))
+        return total > (int)g.sliding_window ? total - (int)g.sliding_window : 0;
+    return 0;
 }
 
 int site_of(const rn_n3_model* m, int layer) {  // config.rs:89-91
@@ -1168,6 +1999,10 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
     if (!s) return n3_fail(RN_ERR_MEMORY, "out of host memory");
     s->m = m;
     s->capacity = capacity;
+    {
+        const char* path = getenv("RN_N3_PATH");
+        s->fused = m->fused && !(path && strcmp(path, "stepwise") == 0);
+    }
     int rc = [&]() -> int {
         const rn_geometry& g = m->g;
         const int d = (int)g.d_model, L = (int)g.num_layers, lanes = (int)g.mhc_lanes, H = (int)g.num_heads,
@@ -1204,7 +2039,6 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
         N3_CALL(alloc_n(s, 64, &s->post));
         N3_CALL(alloc_n(s, 256, &s->residual));
         N3_CALL(alloc_n(s, (size_t)d, &s->x));
-        N3_CALL(alloc_n(s, (size_t)widest, &s->quantised));
         N3_CALL(alloc_n(s, (size_t)widest, &s->rotated));
         N3_CALL(alloc_n(s, (size_t)qkv + H * 64, &s->prod));
         N3_CALL(alloc_n(s, (size_t)H * 64, &s->attended));
@@ -1260,6 +2094,222 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
     return RN_OK;
 }
 
+namespace {
+
+// The layers of one push, one launch per piece (any format); the hidden state
+// at the end.
+int stepwise_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
+    const rn_n3_model* m = s->m;
+    const rn_geometry& g = m->g;
+    const int d = (int)g.d_model, lanes = (int)g.mhc_lanes, H = (int)g.num_heads, KV = (int)g.num_kv_heads;
+    hipStream_t st = s->stream;
+    const int qw = H * 64, kw = KV * 64, qkv = qw + 2 * kw;
+    for (size_t slot = 0; slot < m->active.size(); ++slot) {
+        const int layer = m->active[slot];
+        const N3Layer& y = m->layers[(size_t)layer];
+        N3CacheDev& c = s->caches[(size_t)layer];
+        N3_CALL(rn_lanes_route(s->lanes, layer, (int)slot, cur, s->input, s->post, s->residual, st));
+        const int site = site_of(m, layer);
+        N3BlockInParams bi{s->input, site >= 0 ? s->ekey[(size_t)site] : nullptr,
+                           site >= 0 ? s->evalue[(size_t)site] : nullptr, y.norm_in, d, s->x, y.q->cb.padded,
+                           y.q->group, y.q->cb.wht_scale, s->rotated};
+        rn_launch(n3_block_in_kernel, dim3(1), dim3(kN3Block), 0, st, bi);
+        N3_HIP(hipGetLastError());
+        if (y.qkvg != nullptr) {
+            N3_CALL(product(y.qkvg, s->rotated, s->prod, st));
+        } else {
+            N3_CALL(product(y.q, s->rotated, s->prod, st));
+            N3_CALL(product(y.k, s->rotated, s->prod + qw, st));
+            N3_CALL(product(y.v, s->rotated, s->prod + qw + kw, st));
+            N3_CALL(product(y.gate, s->rotated, s->prod + qkv, st));
+        }
+        N3QkvParams qp{};
+        qp.prod = s->prod;
+        qp.hist = c.hist;
+        for (int t = 0; t < 3; ++t) qp.taps[t] = y.taps[t];
+        qp.ntaps = (int)g.qkv_conv_taps;
+        qp.position = position;
+        qp.H = H;
+        qp.KV = KV;
+        qp.cap = s->capacity;
+        qp.q_norm = y.q_norm;
+        qp.k_norm = y.k_norm;
+        qp.cos_row = s->cos + (size_t)position * 32;
+        qp.sin_row = s->sin + (size_t)position * 32;
+        qp.qcodes = s->qcodes;
+        qp.qscales = s->qscales;
+        qp.keys = c.keys;
+        qp.key_scales = c.key_scales;
+        qp.values = c.values;
+        qp.value_scales = c.value_scales;
+        rn_launch(n3_qkv_kernel, dim3(H + 2 * KV), dim3(64), 0, st, qp);
+        N3_HIP(hipGetLastError());
+        const int total = position + 1, first = window_first(g, layer, total);
+        N3AttendParams ap{s->qcodes, s->qscales, c.keys, c.key_scales, c.values, c.value_scales, s->prod + qkv,
+                          s->capacity, first, total - first, H / KV, 1.0f / sqrtf(64.0f), s->attended};
+        rn_launch(n3_attend_kernel, dim3(H), dim3(256), 0, st, ap);
+        N3_HIP(hipGetLastError());
+        rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->attended, H * 64,
+                  y.out->cb.padded, y.out->group, y.out->cb.wht_scale, s->rotated);
+        N3_HIP(hipGetLastError());
+        N3_CALL(product(y.out, s->rotated, s->attn_out, st));
+        N3BlockOutParams bo{};
+        bo.attention = s->attn_out;
+        bo.post_norm = y.post_norm;
+        bo.gate = y.gate_sigmoid;
+        bo.pre_norm = y.pre_norm;
+        bo.d1 = y.d1;
+        bo.d2 = y.d2;
+        bo.b2 = y.b2;
+        bo.d3 = y.d3;
+        bo.d4 = y.d4;
+        for (int f = 0; f < 6; ++f) bo.factors[f] = y.factors[f];
+        bo.cond_v = y.cond_v;
+        bo.cond_u = y.cond_u;
+        bo.rank = y.rank;
+        bo.perm1 = m->perm[0];
+        bo.perm2 = m->perm[1];
+        bo.x = s->x;
+        bo.input = s->input;
+        bo.post = s->post;
+        bo.residual = s->residual;
+        bo.stream = cur;
+        bo.d = d;
+        bo.lanes = lanes;
+        bo.next = nxt;
+        bo.cell = s->cells + (slot + 1) * (size_t)d;
+        rn_launch(n3_block_out_kernel, dim3(1), dim3(kN3Block), 0, st, bo);
+        N3_HIP(hipGetLastError());
+        std::swap(cur, nxt);
+    }
+    rn_launch(n3_final_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)cur, d, lanes,
+              (const float*)m->final_norm, s->hidden);
+    N3_HIP(hipGetLastError());
+    return RN_OK;
+}
+
+// The layers of one push in three kernels a layer (n3_attention, n3_out,
+// n3_boundary); the routing of the first layer by a boundary without a tail.
+int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
+    const rn_n3_model* m = s->m;
+    const rn_geometry& g = m->g;
+    const int d = (int)g.d_model, lanes = (int)g.mhc_lanes, H = (int)g.num_heads, KV = (int)g.num_kv_heads;
+    hipStream_t st = s->stream;
+    const size_t layers = m->active.size();
+    auto route_into = [&](N3BoundaryParams& b, size_t slot) {
+        const int layer = m->active[slot];
+        const N3Layer& y = m->layers[(size_t)layer];
+        const int site = site_of(m, layer);
+        b.route = 1;
+        b.layer = layer;
+        b.slot = (int)slot;
+        b.phi_pre = m->phi_pre->cb;
+        b.phi_post = m->phi_post->cb;
+        b.phi_res = m->phi_res->cb;
+        b.a_pre = m->a_pre;
+        b.a_post = m->a_post;
+        b.a_res = m->a_res;
+        b.b_pre = m->b_pre;
+        b.b_post = m->b_post;
+        b.b_res = m->b_res;
+        b.input = s->input;
+        b.post = s->post;
+        b.residual = s->residual;
+        b.key = site >= 0 ? s->ekey[(size_t)site] : nullptr;
+        b.value = site >= 0 ? s->evalue[(size_t)site] : nullptr;
+        b.norm_in = y.norm_in;
+        b.x = s->x;
+        b.qpadded = y.qkvg->cb.padded;
+        b.qgroup = y.qkvg->group;
+        b.qscale = y.qkvg->cb.wht_scale;
+        b.rotated = s->rotated;
+    };
+    {
+        N3BoundaryParams b{};
+        b.stream = cur;
+        b.d = d;
+        b.lanes = lanes;
+        route_into(b, 0);
+        rn_launch(n3_boundary_kernel, dim3(1), dim3(kN3Block), 0, st, b);
+        N3_HIP(hipGetLastError());
+    }
+    const int qw = H * 64;
+    for (size_t slot = 0; slot < layers; ++slot) {
+        const int layer = m->active[slot];
+        const N3Layer& y = m->layers[(size_t)layer];
+        N3CacheDev& c = s->caches[(size_t)layer];
+        const int total = position + 1, first = window_first(g, layer, total);
+        N3AttentionParams ap{};
+        ap.qkvg = y.qkvg->cb;
+        ap.rotated = s->rotated;
+        ap.hist = c.hist;
+        for (int t = 0; t < 3; ++t) ap.taps[t] = y.taps[t];
+        ap.ntaps = (int)g.qkv_conv_taps;
+        ap.position = position;
+        ap.H = H;
+        ap.KV = KV;
+        ap.cap = s->capacity;
+        ap.first = first;
+        ap.count = total - first;
+        ap.q_norm = y.q_norm;
+        ap.k_norm = y.k_norm;
+        ap.cos_row = s->cos + (size_t)position * 32;
+        ap.sin_row = s->sin + (size_t)position * 32;
+        ap.keys = c.keys;
+        ap.key_scales = c.key_scales;
+        ap.values = c.values;
+        ap.value_scales = c.value_scales;
+        ap.out = s->attended;
+        rn_launch(n3_attention_kernel, dim3(H), dim3(kN3AttendThreads), 0, st, ap);
+        N3_HIP(hipGetLastError());
+        N3OutParams op{y.out->cb, s->attended, qw, s->attn_out};
+        rn_launch(n3_out_kernel, dim3((unsigned)((y.out->rows + 63) / 64)), dim3(256), 0, st, op);
+        N3_HIP(hipGetLastError());
+        N3BoundaryParams b{};
+        b.tail = 1;
+        N3BlockOutParams& bo = b.t;
+        bo.attention = s->attn_out;
+        bo.post_norm = y.post_norm;
+        bo.gate = y.gate_sigmoid;
+        bo.pre_norm = y.pre_norm;
+        bo.d1 = y.d1;
+        bo.d2 = y.d2;
+        bo.b2 = y.b2;
+        bo.d3 = y.d3;
+        bo.d4 = y.d4;
+        for (int f = 0; f < 6; ++f) bo.factors[f] = y.factors[f];
+        bo.cond_v = y.cond_v;
+        bo.cond_u = y.cond_u;
+        bo.rank = y.rank;
+        bo.perm1 = m->perm[0];
+        bo.perm2 = m->perm[1];
+        bo.x = s->x;
+        bo.input = s->input;
+        bo.post = s->post;
+        bo.residual = s->residual;
+        bo.stream = cur;
+        bo.d = d;
+        bo.lanes = lanes;
+        bo.next = nxt;
+        bo.cell = s->cells + (slot + 1) * (size_t)d;
+        b.d = d;
+        b.lanes = lanes;
+        if (slot + 1 < layers) {
+            route_into(b, slot + 1);
+        } else {
+            b.final = 1;
+            b.final_norm = m->final_norm;
+            b.hidden = s->hidden;
+        }
+        rn_launch(n3_boundary_kernel, dim3(1), dim3(kN3Block), 0, st, b);
+        N3_HIP(hipGetLastError());
+        std::swap(cur, nxt);
+    }
+    return RN_OK;
+}
+
+}  // namespace
+
 // Session::push (session.rs:76-148)
 int rn_n3_session_push(rn_n3_session* s, uint32_t token) {
     N3_REQUIRE(s, "null session");
@@ -1267,7 +2317,7 @@ int rn_n3_session_push(rn_n3_session* s, uint32_t token) {
     const rn_geometry& g = m->g;
     N3_REQUIRE(token < g.vocab, "token %u is outside the vocabulary of %u", token, g.vocab);
     N3_REQUIRE(s->length < s->capacity, "session is full (capacity %d)", s->capacity);
-    const int d = (int)g.d_model, lanes = (int)g.mhc_lanes, H = (int)g.num_heads, KV = (int)g.num_kv_heads;
+    const int d = (int)g.d_model, lanes = (int)g.mhc_lanes;
     const int position = s->length;
     hipStream_t st = s->stream;
     s->tokens.push_back(token);
@@ -1311,89 +2361,7 @@ int rn_n3_session_push(rn_n3_session* s, uint32_t token) {
         N3_HIP(hipGetLastError());
     }
 
-    const int qw = H * 64, kw = KV * 64, qkv = qw + 2 * kw;
-    for (size_t slot = 0; slot < m->active.size(); ++slot) {
-        const int layer = m->active[slot];
-        const N3Layer& y = m->layers[(size_t)layer];
-        N3CacheDev& c = s->caches[(size_t)layer];
-        N3_CALL(rn_lanes_route(s->lanes, layer, (int)slot, cur, s->input, s->post, s->residual, st));
-        const int site = site_of(m, layer);
-        N3BlockInParams bi{s->input, site >= 0 ? s->ekey[(size_t)site] : nullptr,
-                           site >= 0 ? s->evalue[(size_t)site] : nullptr, y.norm_in, d, s->x, s->quantised};
-        rn_launch(n3_block_in_kernel, dim3(1), dim3(kN3Block), 0, st, bi);
-        N3_HIP(hipGetLastError());
-        N3_CALL(rotate(y.q, s->quantised, s->rotated, st));
-        N3_CALL(product(y.q, s->rotated, s->prod, st));
-        N3_CALL(product(y.k, s->rotated, s->prod + qw, st));
-        N3_CALL(product(y.v, s->rotated, s->prod + qw + kw, st));
-        N3_CALL(product(y.gate, s->rotated, s->prod + qkv, st));
-        N3QkvParams qp{};
-        qp.prod = s->prod;
-        qp.hist = c.hist;
-        for (int t = 0; t < 3; ++t) qp.taps[t] = y.taps[t];
-        qp.ntaps = (int)g.qkv_conv_taps;
-        qp.position = position;
-        qp.H = H;
-        qp.KV = KV;
-        qp.cap = s->capacity;
-        qp.q_norm = y.q_norm;
-        qp.k_norm = y.k_norm;
-        qp.cos_row = s->cos + (size_t)position * 32;
-        qp.sin_row = s->sin + (size_t)position * 32;
-        qp.qcodes = s->qcodes;
-        qp.qscales = s->qscales;
-        qp.keys = c.keys;
-        qp.key_scales = c.key_scales;
-        qp.values = c.values;
-        qp.value_scales = c.value_scales;
-        rn_launch(n3_qkv_kernel, dim3(H + 2 * KV), dim3(64), 0, st, qp);
-        N3_HIP(hipGetLastError());
-        // attention.rs:172-178: the window unless the layer is global
-        const int total = position + 1;
-        int first = 0;
-        if (g.sliding_window > 0 && !((g.global_layers >> layer) & 1))
-            first = total > (int)g.sliding_window ? total - (int)g.sliding_window : 0;
-        N3AttendParams ap{s->qcodes, s->qscales, c.keys, c.key_scales, c.values, c.value_scales, s->prod + qkv,
-                          s->capacity, first, total - first, H / KV, 1.0f / sqrtf(64.0f), s->attended};
-        rn_launch(n3_attend_kernel, dim3(H), dim3(256), 0, st, ap);
-        N3_HIP(hipGetLastError());
-        rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->attended, H * 64,
-                  s->quantised);
-        N3_HIP(hipGetLastError());
-        N3_CALL(rotate(y.out, s->quantised, s->rotated, st));
-        N3_CALL(product(y.out, s->rotated, s->attn_out, st));
-        N3BlockOutParams bo{};
-        bo.attention = s->attn_out;
-        bo.post_norm = y.post_norm;
-        bo.gate = y.gate_sigmoid;
-        bo.pre_norm = y.pre_norm;
-        bo.d1 = y.d1;
-        bo.d2 = y.d2;
-        bo.b2 = y.b2;
-        bo.d3 = y.d3;
-        bo.d4 = y.d4;
-        for (int f = 0; f < 6; ++f) bo.factors[f] = y.factors[f];
-        bo.cond_v = y.cond_v;
-        bo.cond_u = y.cond_u;
-        bo.rank = y.rank;
-        bo.perm1 = m->perm[0];
-        bo.perm2 = m->perm[1];
-        bo.x = s->x;
-        bo.input = s->input;
-        bo.post = s->post;
-        bo.residual = s->residual;
-        bo.stream = cur;
-        bo.d = d;
-        bo.lanes = lanes;
-        bo.next = nxt;
-        bo.cell = s->cells + (slot + 1) * (size_t)d;
-        rn_launch(n3_block_out_kernel, dim3(1), dim3(kN3Block), 0, st, bo);
-        N3_HIP(hipGetLastError());
-        std::swap(cur, nxt);
-    }
-    rn_launch(n3_final_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)cur, d, lanes,
-              (const float*)m->final_norm, s->hidden);
-    N3_HIP(hipGetLastError());
+    N3_CALL(s->fused ? fused_layers(s, position, cur, nxt) : stepwise_layers(s, position, cur, nxt));
     for (size_t i = 0; i < m->heads.size(); ++i) {
         const N3Head& h = m->heads[i];
         rn_launch(n3_observe_kernel, dim3(h.layers * h.per_layer), dim3(256), 0, st, (const float*)s->cells,
@@ -1426,9 +2394,9 @@ int rn_n3_session_logits(rn_n3_session* s, float* logits) {
     const rn_n3_model* m = s->m;
     const int d = (int)m->g.d_model;
     hipStream_t st = s->stream;
-    rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->hidden, d, s->quantised);
+    rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->hidden, d,
+              m->embedding->cb.padded, m->embedding->group, m->embedding->cb.wht_scale, s->rotated);
     N3_HIP(hipGetLastError());
-    N3_CALL(rotate(m->embedding, s->quantised, s->rotated, st));
     CodebookParams p = m->embedding->cb;
     p.rows = m->output_vocab;  // multiply_rows(0, ..) over the first output_vocab rows
     if (m->embedding->bits == 1 || m->embedding->bits == 3)

@@ -42,15 +42,25 @@ def _compare_session(gs, os_, label):
     assert gs.head_output(3) is None and os_.head_output(3) is None
 
 
+@pytest.fixture(params=["fused", "stepwise"])
+def path(request, monkeypatch):
+    """The three-kernel step and the one-launch-a-piece step (RN_N3_PATH)."""
+    if request.param == "stepwise":
+        monkeypatch.setenv("RN_N3_PATH", "stepwise")
+    else:
+        monkeypatch.delenv("RN_N3_PATH", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("depth", [0, 2])
-def test_push_bit_exact(archive, depth):
+def test_push_bit_exact(archive, depth, path):
     gm = needle3.Model(archive, depth)
     om = oracle.OracleNeedle3(archive, depth)
     assert gm.active == om.active
     gs, os_ = gm.session(64), om.session(64)
     tokens = _tokens(40)
     for i, t in enumerate(tokens):
-        print(f"needle3 depth {depth} push {i}", flush=True)
+        print(f"needle3 {path} depth {depth} push {i}", flush=True)
         gs.push(int(t))
         os_.push(int(t))
         assert np.array_equal(_bits(gs.hidden()), _bits(os_.hidden())), f"hidden at step {i}"
@@ -63,7 +73,7 @@ def test_push_bit_exact(archive, depth):
             assert a.shape == b.shape and np.array_equal(a.view(np.uint8), b.view(np.uint8)), layer
 
 
-def test_feed_equals_push(archive):
+def test_feed_equals_push(archive, path):
     gm = needle3.Model(archive)
     a, b = gm.session(64), gm.session(64)
     tokens = _tokens(21, seed=5)
