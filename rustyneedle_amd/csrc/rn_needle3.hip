@@ -86,15 +86,15 @@ __device__ __forceinline__ float n3_fold(float s, const float* a, const float* b
                                          int b_stride = -1) {
     const int sb = b_stride < 0 ? stride : b_stride;
     int i = 0;
-    for (; i + 16 <= count; i += 16) {
-        float x[16], y[16];
+    for (; i + 32 <= count; i += 32) {
+        float x[32], y[32];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < 32; ++j) {
             x[j] = a[(size_t)(i + j) * stride];
             y[j] = SQUARE ? x[j] : b[(size_t)(i + j) * sb];
         }
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s = s + x[j] * y[j];
+        for (int j = 0; j < 32; ++j) s = s + x[j] * y[j];
     }
     for (; i < count; ++i) {
         const float x = a[(size_t)i * stride];
@@ -529,9 +529,14 @@ __device__ void n3_kronecker32(const float* x, const float* left, const float* r
     const int tid = threadIdx.x, i = tid >> 5, c = tid & 31;
     float a[32], b[32];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        a[j] = right[j * 32 + c];
-        b[j] = x[i * 32 + j];
+    for (int j = 0; j < 32; ++j) a[j] = right[j * 32 + c];
+#pragma unroll
+    for (int j = 0; j < 32; j += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(x + i * 32 + j);
+        b[j] = q.x;
+        b[j + 1] = q.y;
+        b[j + 2] = q.z;
+        b[j + 3] = q.w;
     }
     float acc = 0.0f;
 #pragma unroll
@@ -581,14 +586,15 @@ __device__ N3TailPre n3_tail_prefetch(const N3BlockOutParams& p) {
 // the pre-Hadamard norm, HadamardWeights::apply, the block delta, the lane
 // combine and the next cell; the next stream also into `keep` (LDS) when set.
 // 1024 threads (the Hadamard size).
-__device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* keep, const N3TailPre& pre) {
+__device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* keep, const N3TailPre& pre,
+                        bool cv_staged = false) {
     float *xs = l.xs, *a = l.a, *sc = l.sc, *st = l.st, *mx = l.mx, *modulation = l.modulation;
     float *cv = l.cv, *weights = l.weights, *red = l.red;
     float(*chains)[8] = reinterpret_cast<float(*)[8]>(l.chains);
     const int tid = threadIdx.x, d = p.d;
     n3_copy(a, p.attention, d);
     n3_copy(xs, p.x, d);
-    if (p.rank == 8) n3_copy(cv, p.cond_v, d * 8);
+    if (p.rank == 8 && !cv_staged) n3_copy(cv, p.cond_v, d * 8);
     __syncthreads();
     n3_norm(a, p.post_norm, d, a, red);
     for (int i = tid; i < d; i += blockDim.x) xs[i] = xs[i] + p.gate * a[i];
@@ -661,7 +667,7 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
 }
 
 __global__ __launch_bounds__(kN3Block) void n3_block_out_kernel(N3BlockOutParams p) {
-    __shared__ float xs[kN3Hadamard], a[kN3Hadamard], sc[kN3Hadamard], st[kN3Hadamard], mx[kN3Hadamard];
+    __shared__ __align__(16) float xs[kN3Hadamard], a[kN3Hadamard], sc[kN3Hadamard], st[kN3Hadamard], mx[kN3Hadamard];
     __shared__ float modulation[kN3Hadamard];
     __shared__ float chains[32];
     __shared__ float weights[64];
@@ -813,6 +819,65 @@ __device__ __forceinline__ int n3_b4(int a, int b, int c, int d) {
     return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | ((d & 0xff) << 24);
 }
 
+// Pack sixteen codes of a run in the order its packed indices decode: for
+// 2-bit dword k holds elements k, 4+k, 8+k, 12+k; for 4-bit dword 2h+k holds
+// 8h+k, 8h+2+k, 8h+4+k, 8h+6+k.
+__device__ __forceinline__ int4 n3_pack_codes(const int (&c)[16], int ib) {
+    return ib == 2 ? make_int4(n3_b4(c[0], c[4], c[8], c[12]), n3_b4(c[1], c[5], c[9], c[13]),
+                               n3_b4(c[2], c[6], c[10], c[14]), n3_b4(c[3], c[7], c[11], c[15]))
+                   : make_int4(n3_b4(c[0], c[2], c[4], c[6]), n3_b4(c[1], c[3], c[5], c[7]),
+                               n3_b4(c[8], c[10], c[12], c[14]), n3_b4(c[9], c[11], c[13], c[15]));
+}
+
+// prepare and the per-group codes in one pass (matrix.rs:123-128 then
+// panel.rs:52-66): lane u holds run u (16 elements of v [P], zero past the
+// columns), runs the group's Walsh-Hadamard butterflies (spans 1..8 in the
+// lane, then 16 .. group / 2 with the partner lane u ^ (span / 16); low a + b,
+// high a - b; walsh.rs:41-76), scales, then quantises with the group's peak.
+// Codes to xq (plane order) and scales to xs, LDS or global.
+__device__ void n3_prepare_codes(const float* v, int P, int group, float wht_scale, int ib, int4* xq, float* xs) {
+    const int runs = P / 16, rpg = group / 16;
+    for (int base = 0; base < runs; base += blockDim.x) {
+        const int u = base + threadIdx.x;
+        const bool valid = u < runs;
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = valid ? v[16 * u + i] : 0.0f;
+#pragma unroll
+        for (int span = 1; span < 16; span *= 2)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if ((i & span) == 0) {
+                    const float a = x[i], b = x[i + span];
+                    x[i] = a + b;
+                    x[i + span] = a - b;
+                }
+        for (int m = 1; m < rpg; m <<= 1) {
+            const bool high = (u & m) != 0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float q = __shfl_xor(x[i], m, 64);
+                x[i] = high ? q - x[i] : x[i] + q;
+            }
+        }
+        float peak = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            x[i] = x[i] * wht_scale;
+            peak = fmaxf(peak, fabsf(x[i]));
+        }
+        for (int m = 1; m < rpg; m <<= 1) peak = fmaxf(peak, __shfl_xor(peak, m, 64));
+        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+        int c[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) c[i] = quantise_one(x[i], scale);
+        if (valid) {
+            xq[u] = n3_pack_codes(c, ib);
+            if ((u & (rpg - 1)) == 0) xs[u / rpg] = scale;
+        }
+    }
+}
+
 // Per-group int8 codes of an LDS input (panel.rs:52-66): scale = peak / 127 (1
 // for a zero peak), code = round-half-even(v / scale) clamped. A lane per run
 // of 16; the group's peak over its aligned lanes. Codes are stored in the
@@ -878,75 +943,97 @@ __device__ void n3_stage_rows(const CodebookParams& c, RowOf row_of, int R, uint
 // The integer path of a codebook matrix (panel.rs:153-197 for 2-bit,
 // neon.rs:126-183 for 4-bit and ternary) over R rows staged in LDS (w, nm) for
 // one input quantised per group in LDS (xq, xs): exact group sums of level *
-// code, then per row the epilogue over the groups in order. Lanes hold runs
-// of 16 elements; a group's runs sit on aligned lanes and join by shuffles.
-__device__ void n3_rows(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R, const int4* xq,
-                        const float* xs, int* acc, float* y) {
-    const int ib = c.bits == 5 ? 2 : c.bits, runs = c.padded / 16, rpg = c.group / 16, G = c.padded / c.group;
+// code, then per row the epilogue over the groups in order. Lane l of every
+// wave holds the codes of run u = l (+ 64 per pass) in registers; the waves
+// take the rows in turn, four at a time. A group's runs sit on aligned lanes
+// and join by DPP.
+template <int IB>
+__device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R, const int4* xq,
+                           const float* xs, int* acc, float* y) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const int runs = c.padded / 16, rpg = c.group / 16, G = c.padded / c.group;
+    const int rpg_shift = rpg == 4 ? 2 : (rpg == 8 ? 3 : 4);
     const uint32_t lut[4] = {c.lut[0], c.lut[1], c.lut[2], c.lut[3]};
-    const int total = R * runs;
-    for (int base = 0; base < total; base += 4 * blockDim.x) {
-        int sum[4];
+    for (int u0 = 0; u0 < runs; u0 += 64) {
+        const int u = u0 + lane;
+        const bool live = u < runs;
+        const int4 x = live ? xq[u] : make_int4(0, 0, 0, 0);
+        const uint8_t* base = w + (size_t)(live ? u : 0) * 2 * IB;
+        const bool leader = live && (u & (rpg - 1)) == 0;
+        for (int r0 = wave; r0 < R; r0 += 4 * waves) {
+            int sum[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int idx = base + k * blockDim.x + threadIdx.x;
-            sum[k] = 0;
-            if (idx < total) {
-                const int r = idx / runs, u = idx - r * runs;
-                const uint8_t* bytes = w + (size_t)r * c.row_bytes + (size_t)u * 2 * ib;
-                const int4 x = xq[u];
+            for (int k = 0; k < 4; ++k) {
+                const int r = r0 + k * waves;
                 int sm = 0;
-                if (ib == 2) {
-                    const uint32_t wd = *reinterpret_cast<const uint32_t*>(bytes);
-                    sm = dot4(n3_decode4<2>(wd & 0x03030303u, lut), x.x, sm);
-                    sm = dot4(n3_decode4<2>((wd >> 2) & 0x03030303u, lut), x.y, sm);
-                    sm = dot4(n3_decode4<2>((wd >> 4) & 0x03030303u, lut), x.z, sm);
-                    sm = dot4(n3_decode4<2>((wd >> 6) & 0x03030303u, lut), x.w, sm);
-                } else {
-                    const uint2 wd = *reinterpret_cast<const uint2*>(bytes);
-                    sm = dot4(n3_decode4<4>(wd.x & 0x0f0f0f0fu, lut), x.x, sm);
-                    sm = dot4(n3_decode4<4>((wd.x >> 4) & 0x0f0f0f0fu, lut), x.y, sm);
-                    sm = dot4(n3_decode4<4>(wd.y & 0x0f0f0f0fu, lut), x.z, sm);
-                    sm = dot4(n3_decode4<4>((wd.y >> 4) & 0x0f0f0f0fu, lut), x.w, sm);
+                if (r < R && live) {
+                    if constexpr (IB == 2) {
+                        const uint32_t wd = *reinterpret_cast<const uint32_t*>(base + (size_t)r * c.row_bytes);
+                        sm = dot4(n3_decode4<2>(wd & 0x03030303u, lut), x.x, sm);
+                        sm = dot4(n3_decode4<2>((wd >> 2) & 0x03030303u, lut), x.y, sm);
+                        sm = dot4(n3_decode4<2>((wd >> 4) & 0x03030303u, lut), x.z, sm);
+                        sm = dot4(n3_decode4<2>((wd >> 6) & 0x03030303u, lut), x.w, sm);
+                    } else {
+                        const uint2 wd = *reinterpret_cast<const uint2*>(base + (size_t)r * c.row_bytes);
+                        sm = dot4(n3_decode4<4>(wd.x & 0x0f0f0f0fu, lut), x.x, sm);
+                        sm = dot4(n3_decode4<4>((wd.x >> 4) & 0x0f0f0f0fu, lut), x.y, sm);
+                        sm = dot4(n3_decode4<4>(wd.y & 0x0f0f0f0fu, lut), x.z, sm);
+                        sm = dot4(n3_decode4<4>((wd.y >> 4) & 0x0f0f0f0fu, lut), x.w, sm);
+                    }
                 }
                 sum[k] = sm;
             }
-        }
-        // the runs of a group sit on rpg aligned lanes (DPP: exact integer sums)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            int v = sum[k];
-            v = v + dpp_move<0xb1>(v);
-            if (rpg >= 4) v = v + dpp_move<0x4e>(v);
-            if (rpg >= 8) v = v + dpp_move<0x141>(v);
-            if (rpg >= 16) v = v + dpp_move<0x140>(v);
-            const int idx = base + k * blockDim.x + threadIdx.x;
-            if (idx < total) {
-                const int r = idx / runs, u = idx - r * runs;
-                if (u % rpg == 0) acc[r * G + u / rpg] = v;
+            for (int k = 0; k < 4; ++k) {
+                int v = sum[k];
+                v = v + dpp_move<0xb1>(v);
+                v = v + dpp_move<0x4e>(v);
+                if (rpg >= 8) v = v + dpp_move<0x141>(v);
+                if (rpg >= 16) v = v + dpp_move<0x140>(v);
+                const int r = r0 + k * waves;
+                if (leader && r < R) acc[r * G + (u >> rpg_shift)] = v;
             }
         }
     }
     __syncthreads();
     for (int r = threadIdx.x; r < R; r += blockDim.x) {
         float t = 0.0f;
-        for (int g = 0; g < G; ++g) {
-            const float norm = __half2float(__ushort_as_half(nm[r * G + g]));
-            const float a = (float)acc[r * G + g];
-            if (c.bits == 2)
-                t = fmaf(a, (norm * c.lscale) * xs[g], t);  // panel.rs:184-188
-            else
-                t = t + (((a * norm) * c.lscale) * xs[g]);  // neon.rs:158,180
+        for (int g0 = 0; g0 < G; g0 += 8) {
+            float nv[8], av[8], sv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int g = min(g0 + k, G - 1);
+                nv[k] = __half2float(__ushort_as_half(nm[r * G + g]));
+                av[k] = (float)acc[r * G + g];
+                sv[k] = xs[g];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (g0 + k >= G) break;
+                if (c.bits == 2)
+                    t = fmaf(av[k], (nv[k] * c.lscale) * sv[k], t);  // panel.rs:184-188
+                else
+                    t = t + (((av[k] * nv[k]) * c.lscale) * sv[k]);  // neon.rs:158,180
+            }
         }
         y[r] = t;
     }
     __syncthreads();
 }
 
+__device__ void n3_rows(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R, const int4* xq,
+                        const float* xs, int* acc, float* y) {
+    if (c.bits == 4)
+        n3_rows_ib<4>(c, w, nm, R, xq, xs, acc, y);
+    else
+        n3_rows_ib<2>(c, w, nm, R, xq, xs, acc, y);
+}
+
 struct N3AttentionParams {
-    CodebookParams qkvg;   // rows q [H*64] | k [KV*64] | v [KV*64] | gate [H*64]
-    const float* rotated;  // [padded] the prepared input of the projections
-    float* hist;           // conv-tap ring [taps][q | k | v]
+    CodebookParams qkvg;       // rows q [H*64] | k [KV*64] | v [KV*64] | gate [H*64]
+    const int4* codes;         // [padded / 16] the projections' input, prepared and quantised (plane order)
+    const float* code_scales;  // [groups]
+    float* hist;               // conv-tap ring [taps][q | k | v]
     const float* taps[3];
     int ntaps, position, H, KV, cap, first, count;
     const float* q_norm;
@@ -962,11 +1049,16 @@ struct N3AttentionParams {
 
 constexpr int kN3AttendThreads = 1024;
 constexpr int kN3HeadRowBytes = 256;  // the head's 256 staged rows, each at most 256 bytes (2-bit, 1024 columns)
+constexpr int kN3MaxTaps = 4;
 
+// One block a query head (attention.rs:96-149 for that head): every load this
+// block needs is issued first (its 256 projection rows and norms, the input
+// codes, the conv taps and ring samples, the norm gains and rotary row, and
+// the cached keys and values of the earlier positions, which no block writes
+// here); the new position's key and value come from LDS.
 __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3AttentionParams p) {
     __shared__ __align__(16) uint8_t w_s[256 * kN3HeadRowBytes];
     __shared__ uint16_t nm_s[256 * 16];
-    __shared__ float x_s[kN3Hadamard];
     __shared__ int4 xq[kN3Hadamard / 16];
     __shared__ float xs[64];
     __shared__ int acc[64 * kN3Head];  // the row group sums, then the value sums
@@ -974,41 +1066,98 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     __shared__ float v_s[3][kN3Head];
     __shared__ float red_s[3][8];
     __shared__ __align__(16) int8_t qc_s[kN3Head];
-    __shared__ float qscale_s;
+    __shared__ __align__(16) int8_t kc_s[kN3Head];
+    __shared__ __align__(16) int8_t vc_s[kN3Head];
+    __shared__ float scale_s[3];
     __shared__ float c_s[kN3MaxAttend];
     __shared__ float red[16];
     __shared__ float lanes_s[4];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int group = p.H / p.KV, kvh = h / group, P = p.qkvg.padded;
+    const int group = p.H / p.KV, kvh = h / group, P = p.qkvg.padded, G = P / p.qkvg.group;
     const int qw = p.H * kN3Head, kw = p.KV * kN3Head, width_all = qw + 2 * kw;
+    const int count = p.count, last = count - 1;  // the new position is first + last
     auto row_of = [&](int r) -> int {
         return r < 64 ? h * 64 + r
                       : r < 128 ? qw + kvh * 64 + (r - 64)
                                 : r < 192 ? qw + kw + kvh * 64 + (r - 128) : qw + 2 * kw + h * 64 + (r - 192);
     };
-    n3_stage_rows(p.qkvg, row_of, 256, w_s, nm_s);
-    for (int i = tid; i < P; i += blockDim.x) x_s[i] = p.rotated[i];
-    __syncthreads();
-    n3_group_codes(x_s, P, p.qkvg.group, p.qkvg.bits == 5 ? 2 : p.qkvg.bits, xq, xs);
-    n3_rows(p.qkvg, w_s, nm_s, 256, xq, xs, acc, y_s);
-    // waves 0, 1, 2: the query head, then its key and value heads (attention.rs:110-141)
+    // ---- loads
+    const int chunks = p.qkvg.row_bytes / 16;
+    int4 rw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = j * kN3AttendThreads + tid;
+        if (i < 256 * chunks) rw[j] = reinterpret_cast<const int4*>(p.qkvg.packed + (size_t)row_of(i / chunks) * p.qkvg.row_bytes)[i % chunks];
+    }
+    uint16_t rn[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = j * kN3AttendThreads + tid;
+        rn[j] = i < 256 * G ? p.qkvg.norms[(size_t)row_of(i / G) * G + i % G] : 0;
+    }
+    int4 code = make_int4(0, 0, 0, 0);
+    if (tid < P / 16) code = p.codes[tid];
+    const float code_scale = tid < G ? p.code_scales[tid] : 0.0f;
+    // conv taps, ring samples, norm gain and rotary row of waves 0, 1, 2 (q, k, v)
     const int which = wave < 3 ? wave : 0;
     const int head = which == 0 ? h : kvh;
     const int width = which == 0 ? qw : kw, off = which == 0 ? 0 : (which == 1 ? qw : qw + kw);
     const int col = head * kN3Head + lane;
+    const int ntap = min(p.ntaps, p.position + 1);
+    float gains[kN3MaxTaps], samples[kN3MaxTaps];
+#pragma unroll
+    for (int t = 0; t < kN3MaxTaps; ++t) {
+        gains[t] = (wave < 3 && t < ntap) ? p.taps[which][(size_t)t * width + col] : 0.0f;
+        samples[t] = (wave < 3 && t >= 1 && t < ntap)
+                         ? p.hist[(size_t)((p.position - t) % p.ntaps) * width_all + off + col]
+                         : 0.0f;
+    }
+    const float gain = wave < 2 ? (which == 0 ? p.q_norm : p.k_norm)[lane] : 0.0f;
+    const float cs = p.cos_row[lane & 31], sn = p.sin_row[lane & 31];
+    // the earlier positions' keys (thread: position tid) and values (thread:
+    // dims 4 dg .. 4 dg + 3 of positions pc + 64 j)
+    const int8_t* kbase = p.keys + ((size_t)kvh * p.cap + p.first) * kN3Head;
+    const int8_t* vbase = p.values + ((size_t)kvh * p.cap + p.first) * kN3Head;
+    const float* ks = p.key_scales + (size_t)kvh * p.cap + p.first;
+    const float* vsc = p.value_scales + (size_t)kvh * p.cap + p.first;
+    int4 kr[4];
+    float kscale = 0.0f;
+    if (tid < last) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const int4*>(kbase + (size_t)tid * kN3Head)[i];
+        kscale = ks[tid];
+    }
+    const int dg = tid & 15, pc = tid >> 4;
+    int vr[16];
+    float vsr[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int pp = pc + 64 * j;
+        vr[j] = pp < last ? *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head + 4 * dg) : 0;
+        vsr[j] = pp < last ? vsc[pp] : 0.0f;
+    }
+    // ---- the head's projection rows
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = j * kN3AttendThreads + tid;
+        if (i < 256 * chunks) reinterpret_cast<int4*>(w_s)[i] = rw[j];
+        if (i < 256 * G) nm_s[i] = rn[j];
+    }
+    if (tid < P / 16) xq[tid] = code;
+    if (tid < G) xs[tid] = code_scale;
+    __syncthreads();
+    n3_rows(p.qkvg, w_s, nm_s, 256, xq, xs, acc, y_s);
+    // ---- conv taps, norms, rotary, codes (attention.rs:110-141)
     float v = 0.0f;
     if (wave < 3) {
         const float raw = y_s[which * 64 + lane];
         v = raw;
         if (p.ntaps > 0) {
             p.hist[(size_t)(p.position % p.ntaps) * width_all + off + col] = raw;
-            const int n = min(p.ntaps, p.position + 1);
             v = 0.0f;
-            for (int tap = 0; tap < n; ++tap) {
-                const float sample =
-                    tap == 0 ? raw : p.hist[(size_t)((p.position - tap) % p.ntaps) * width_all + off + col];
-                v = v + p.taps[which][(size_t)tap * width + col] * sample;
-            }
+#pragma unroll
+            for (int t = 0; t < kN3MaxTaps; ++t)
+                if (t < ntap) v = v + gains[t] * (t == 0 ? raw : samples[t]);
         }
         v_s[which][lane] = v;
     }
@@ -1023,8 +1172,7 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         float ss = 0.0f;
         for (int j = 0; j < 8; ++j) ss = ss + red_s[which][j];
         const float inverse = 1.0f / sqrtf(ss / (float)kN3Head + 1e-6f);
-        const float* gain = which == 0 ? p.q_norm : p.k_norm;
-        v = ((1.0f + gain[lane]) * v) * inverse;
+        v = ((1.0f + gain) * v) * inverse;
     }
     __syncthreads();
     if (wave < 2) v_s[which][lane] = v;
@@ -1033,43 +1181,51 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         const int half = kN3Head / 2;
         if (lane < half) {
             const float a = v_s[which][lane], bb = v_s[which][lane + half];
-            v = a * p.cos_row[lane] - bb * p.sin_row[lane];
+            v = a * cs - bb * sn;
         } else {
-            const int i = lane - half;
-            const float a = v_s[which][i], bb = v_s[which][lane];
-            v = bb * p.cos_row[i] + a * p.sin_row[i];
+            const float a = v_s[which][lane - half], bb = v_s[which][lane];
+            v = bb * cs + a * sn;
         }
     }
     if (wave < 3) {  // ops.rs:112-118 per head
         const float peak = wave_max(fabsf(v));
         const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-        const int8_t code = (int8_t)quantise_one(v, scale);
-        if (which == 0) {
-            qc_s[lane] = code;
-            if (lane == 0) qscale_s = scale;
-        } else {
+        const int8_t code8 = (int8_t)quantise_one(v, scale);
+        (which == 0 ? qc_s : which == 1 ? kc_s : vc_s)[lane] = code8;
+        if (lane == 0) scale_s[which] = scale;
+        if (which > 0) {  // the cache append (the blocks of a kv group write the same bytes)
             const size_t row = (size_t)kvh * p.cap + p.position;
-            (which == 1 ? p.keys : p.values)[row * kN3Head + lane] = code;
+            (which == 1 ? p.keys : p.values)[row * kN3Head + lane] = code8;
             if (lane == 0) (which == 1 ? p.key_scales : p.value_scales)[row] = scale;
         }
     }
-    __syncthreads();  // the cache row of this position, written above, is read below
-    // kernels/src/attention.rs:53-80 (as n3_attend_kernel)
-    const int count = p.count;
-    const float query_scale = qscale_s * (1.0f / sqrtf((float)kN3Head));
+    __syncthreads();
+    // ---- kernels/src/attention.rs:53-80 (as n3_attend_kernel)
+    const float query_scale = scale_s[0] * (1.0f / sqrtf((float)kN3Head));
     int4 q[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) q[i] = reinterpret_cast<const int4*>(qc_s)[i];
-    const int8_t* kbase = p.keys + ((size_t)kvh * p.cap + p.first) * kN3Head;
-    const float* ks = p.key_scales + (size_t)kvh * p.cap + p.first;
-    const float* vsc = p.value_scales + (size_t)kvh * p.cap + p.first;
     float peak = -INFINITY;
     for (int pp = tid; pp < count; pp += kN3AttendThreads) {
-        const int4* k = reinterpret_cast<const int4*>(kbase + (size_t)pp * kN3Head);
+        int4 k[4];
+        float kscl;
+        if (pp == last) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) k[i] = reinterpret_cast<const int4*>(kc_s)[i];
+            kscl = scale_s[1];
+        } else if (pp == tid) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) k[i] = kr[i];
+            kscl = kscale;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) k[i] = reinterpret_cast<const int4*>(kbase + (size_t)pp * kN3Head)[i];
+            kscl = ks[pp];
+        }
         int score = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) score = dot16(q[i], k[i], score);
-        const float c = ((float)score * ks[pp]) * query_scale;
+        const float c = ((float)score * kscl) * query_scale;
         c_s[pp] = c;
         peak = fmaxf(peak, c);
     }
@@ -1078,7 +1234,7 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     for (int pp = tid; pp < count; pp += kN3AttendThreads) {
         const float e = fast_exp(c_s[pp] - peak);
         c_s[pp] = e;
-        cpeak = fmaxf(cpeak, fabsf(e * vsc[pp]));
+        cpeak = fmaxf(cpeak, fabsf(e * (pp == last ? scale_s[2] : vsc[pp])));
     }
     cpeak = n3_block_max(cpeak, red);
     const int vector_count = count - count % 4;
@@ -1095,29 +1251,29 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         for (; pp < vector_count; pp += 4) s = s + c_s[pp];
         lanes_s[tid] = s;
     }
-    // the values: thread (dims 4 dg .. 4 dg + 3, positions pc mod 64), four
-    // positions' loads issued before their weights are applied
     const float scale = cpeak / 2047.0f;
-    const int dg = tid & 15, pc = tid >> 4;
     int av[4] = {0, 0, 0, 0};
     if (cpeak > 0.0f) {
-        const int8_t* vbase = p.values + ((size_t)kvh * p.cap + p.first) * kN3Head + 4 * dg;
-        for (int pp0 = pc; pp0 < count; pp0 += 4 * 64) {
-            int packed[4];
-            float sv[4];
+        for (int pp0 = pc; pp0 < count; pp0 += 16 * 64) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < 16; ++j) {
                 const int pp = pp0 + 64 * j;
-                packed[j] = pp < count ? *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head) : 0;
-                sv[j] = pp < count ? vsc[pp] : 0.0f;
-            }
+                if (pp >= count) break;
+                int packed;
+                float sv;
+                if (pp == last) {
+                    packed = reinterpret_cast<const int*>(vc_s)[dg];
+                    sv = scale_s[2];
+                } else if (pp0 == pc) {
+                    packed = vr[j];
+                    sv = vsr[j];
+                } else {
+                    packed = *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head + 4 * dg);
+                    sv = vsc[pp];
+                }
+                const int wgt = (int)__builtin_roundf((c_s[pp] * sv) / scale);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int pp = pp0 + 64 * j;
-                if (pp >= count) continue;
-                const int wgt = (int)__builtin_roundf((c_s[pp] * sv[j]) / scale);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) av[k] += wgt * (int)(int8_t)(packed[j] >> (8 * k));
+                for (int k = 0; k < 4; ++k) av[k] += wgt * (int)(int8_t)(packed >> (8 * k));
             }
         }
     }
@@ -1146,7 +1302,8 @@ struct N3OutParams {
 constexpr int kN3OutRowBytes = 1024;  // 4-bit over 2048 columns or 2-bit over 4096
 
 // fake_quantise_int8 of the gated attention, prepare, then rows
-// [64 * blockIdx.x, + 64) of the output projection (attention.rs:150-153)
+// [64 * blockIdx.x, + 64) of the output projection (attention.rs:150-153).
+// The block's rows, norms and the attention are requested together first.
 __global__ __launch_bounds__(256) void n3_out_kernel(N3OutParams p) {
     __shared__ __align__(16) uint8_t w_s[64 * kN3OutRowBytes];
     __shared__ uint16_t nm_s[64 * 64];
@@ -1156,17 +1313,45 @@ __global__ __launch_bounds__(256) void n3_out_kernel(N3OutParams p) {
     __shared__ int acc[64 * 64];
     __shared__ float y_s[64];
     __shared__ float red[8];
-    const int P = p.out.padded;
+    const int P = p.out.padded, G = P / p.out.group, tid = threadIdx.x;
     const int r0 = blockIdx.x * 64, R = min(64, p.out.rows - r0);
-    n3_stage_rows(p.out, [&](int r) { return r0 + r; }, R, w_s, nm_s);
-    for (int i = threadIdx.x; i < p.n; i += blockDim.x) v[i] = p.attended[i];
-    for (int i = p.n + threadIdx.x; i < P; i += blockDim.x) v[i] = 0.0f;
+    const int chunks = p.out.row_bytes / 16;
+    constexpr int kLoads = 64 * kN3OutRowBytes / 16 / 256;
+    int4 rw[kLoads];
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+        const int i = j * 256 + tid;
+        if (i < R * chunks) rw[j] = reinterpret_cast<const int4*>(p.out.packed + (size_t)(r0 + i / chunks) * p.out.row_bytes)[i % chunks];
+    }
+    uint16_t rn[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int i = j * 256 + tid;
+        rn[j] = i < R * G ? p.out.norms[(size_t)(r0 + i / G) * G + i % G] : 0;
+    }
+    float a[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int i = j * 256 + tid;
+        a[j] = i < p.n ? p.attended[i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+        const int i = j * 256 + tid;
+        if (i < R * chunks) reinterpret_cast<int4*>(w_s)[i] = rw[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int i = j * 256 + tid;
+        if (i < R * G) nm_s[i] = rn[j];
+        if (i < P) v[i] = a[j];
+    }
     __syncthreads();
     n3_fake_quantise(v, p.n, red);
-    n3_rotate(v, P, p.out.group, p.out.wht_scale);
-    n3_group_codes(v, P, p.out.group, p.out.bits == 5 ? 2 : p.out.bits, xq, xs);
+    n3_prepare_codes(v, P, p.out.group, p.out.wht_scale, p.out.bits == 5 ? 2 : p.out.bits, xq, xs);
+    __syncthreads();
     n3_rows(p.out, w_s, nm_s, R, xq, xs, acc, y_s);
-    for (int r = threadIdx.x; r < R; r += blockDim.x) p.y[r0 + r] = y_s[r];
+    for (int r = tid; r < R; r += blockDim.x) p.y[r0 + r] = y_s[r];
 }
 
 struct N3BoundaryParams {
@@ -1187,9 +1372,10 @@ struct N3BoundaryParams {
     const float* value;
     const float* norm_in;
     float* x;
-    int qpadded, qgroup;
+    int qpadded, qgroup, qib;
     float qscale;
-    float* rotated;
+    int4* codes;          // [qpadded / 16] the projections' input, prepared and quantised
+    float* code_scales;   // [qpadded / qgroup]
     int d, lanes;
 };
 
@@ -1197,7 +1383,7 @@ constexpr int kN3RouteRows = 24;         // 2 lanes + lanes^2 for four lanes
 constexpr int kN3RouteRowBytes = 768;    // 2-bit over 3072 columns
 
 __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams p) {
-    __shared__ float xs_[kN3Hadamard], a_[kN3Hadamard], sc_[kN3Hadamard], st_[kN3Hadamard], mx_[kN3Hadamard];
+    __shared__ __align__(16) float xs_[kN3Hadamard], a_[kN3Hadamard], sc_[kN3Hadamard], st_[kN3Hadamard], mx_[kN3Hadamard];
     __shared__ float mod_[kN3Hadamard];
     __shared__ float chains_[32];
     __shared__ float weights_[64];
@@ -1260,6 +1446,8 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     }
     N3BlockOutParams t = p.t;
     N3TailPre pre{};
+    const bool cv_staged = p.tail && t.rank == 8;
+    if (cv_staged) n3_copy(cv_, t.cond_v, d * 8);
     if (p.tail) {
         pre = n3_tail_prefetch(t);
         n3_copy(&factors_s[0][0], t.factors[0], kN3Hadamard);
@@ -1283,7 +1471,7 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     }
     __syncthreads();
     const N3TailLds l{xs_, a_, sc_, st_, mx_, mod_, cv_, chains_, weights_, red};
-    if (p.tail) n3_tail(t, l, rv, pre);  // the next stream into rv, then into stream_s
+    if (p.tail) n3_tail(t, l, rv, pre, cv_staged);  // the next stream into rv, then into stream_s
     if (p.tail) {
         for (int i = tid; i < S; i += blockDim.x) stream_s[i] = rv[i];
         __syncthreads();
@@ -1310,11 +1498,11 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     const int P = p.phi_pre.padded;
     for (int i = S + tid; i < P; i += blockDim.x) rv[i] = 0.0f;
     __syncthreads();
-    n3_rotate(rv, P, p.phi_pre.group, p.phi_pre.wht_scale);
     // the routing matrices share their format, so one set of codes serves the
     // three (matrix.rs:167-193 shares a plane input per format)
     const int ib_pre = p.phi_pre.bits == 5 ? 2 : p.phi_pre.bits;
-    n3_group_codes(rv, P, p.phi_pre.group, ib_pre, rq, rs);
+    n3_prepare_codes(rv, P, p.phi_pre.group, p.phi_pre.wht_scale, ib_pre, rq, rs);
+    __syncthreads();
     // lanes.rs:56-63: the layer's rows of the three routing matrices
     n3_rows(p.phi_pre, pw, pn, route_rows, rq, rs, racc, ry);
     // lanes.rs:64-83 (as lanes_route_kernel)
@@ -1411,9 +1599,8 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     n3_fake_quantise(a_, d, red);
     for (int i = d + tid; i < p.qpadded; i += blockDim.x) a_[i] = 0.0f;
     __syncthreads();
-    n3_rotate(a_, p.qpadded, p.qgroup, p.qscale);
+    n3_prepare_codes(a_, p.qpadded, p.qgroup, p.qscale, p.qib, p.codes, p.code_scales);
     for (int i = tid; i < d; i += blockDim.x) p.x[i] = xs_[i];
-    for (int i = tid; i < p.qpadded; i += blockDim.x) p.rotated[i] = a_[i];
 }
 
 }  // namespace rn
@@ -1635,6 +1822,7 @@ bool fused_applies(const rn_n3_model* m) {
     const rn_geometry& g = m->g;
     const int L = (int)g.mhc_lanes;
     if (2 * L + L * L > kN3RouteRows || g.d_model > (uint32_t)kN3Hadamard) return false;
+    if (g.qkv_conv_taps > (uint32_t)kN3MaxTaps) return false;
     if (m->phi_pre->cb.row_bytes > kN3RouteRowBytes || m->phi_pre->cb.padded / m->phi_pre->group > 64) return false;
     if ((2 * L + L * L) * (m->phi_pre->cb.padded / m->phi_pre->group) > kN3Block ||
         (2 * L + L * L) * (m->phi_pre->cb.row_bytes / 16) > 2 * kN3Block)
@@ -1904,6 +2092,8 @@ struct rn_n3_session {
     std::vector<void*> allocations;
     float *stream_a = nullptr, *stream_b = nullptr, *input = nullptr, *post = nullptr, *residual = nullptr;
     float *x = nullptr, *rotated = nullptr, *prod = nullptr, *attended = nullptr;
+    void* codes = nullptr;         // the projections' input codes (int4 a run of 16)
+    float* code_scales = nullptr;
     float *attn_out = nullptr, *row = nullptr, *gathered = nullptr, *eraw = nullptr, *qscales = nullptr;
     int8_t* qcodes = nullptr;
     float *cells = nullptr, *hidden = nullptr, *logits = nullptr, *cos = nullptr, *sin = nullptr;
@@ -2042,6 +2232,8 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
         N3_CALL(alloc_n(s, (size_t)widest, &s->rotated));
         N3_CALL(alloc_n(s, (size_t)qkv + H * 64, &s->prod));
         N3_CALL(alloc_n(s, (size_t)H * 64, &s->attended));
+        N3_CALL(alloc(s, (size_t)kN3Hadamard, &s->codes));
+        N3_CALL(alloc_n(s, 64, &s->code_scales));
         N3_CALL(alloc_n(s, (size_t)d, &s->attn_out));
         N3_CALL(alloc_n(s, (size_t)std::max(d, m->embedding->cb.padded), &s->row));
         N3_CALL(alloc_n(s, (size_t)kN3MaxWidth, &s->gathered));
@@ -2221,8 +2413,10 @@ int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
         b.x = s->x;
         b.qpadded = y.qkvg->cb.padded;
         b.qgroup = y.qkvg->group;
+        b.qib = y.qkvg->bits == 5 ? 2 : y.qkvg->bits;
         b.qscale = y.qkvg->cb.wht_scale;
-        b.rotated = s->rotated;
+        b.codes = reinterpret_cast<int4*>(s->codes);
+        b.code_scales = s->code_scales;
     };
     {
         N3BoundaryParams b{};
@@ -2241,7 +2435,8 @@ int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
         const int total = position + 1, first = window_first(g, layer, total);
         N3AttentionParams ap{};
         ap.qkvg = y.qkvg->cb;
-        ap.rotated = s->rotated;
+        ap.codes = reinterpret_cast<const int4*>(s->codes);
+        ap.code_scales = s->code_scales;
         ap.hist = c.hist;
         for (int t = 0; t < 3; ++t) ap.taps[t] = y.taps[t];
         ap.ntaps = (int)g.qkv_conv_taps;
