@@ -257,6 +257,11 @@ int rn_n3_session_free(rn_n3_session* session);
  * below the vocabulary; RN_ERR_ARGUMENT past the capacity. */
 int rn_n3_session_push(rn_n3_session* session, uint32_t token);
 int rn_n3_session_feed(rn_n3_session* session, const uint32_t* tokens, int count);
+/* Generator::run_turn's greedy loop (generator.rs:199-230, argmax at 257-265)
+ * without grammar: token = first; `steps` times { push(token); logits; token =
+ * argmax over output_vocab; ids[i] = token } (host ids). The argmax stays on
+ * the device and feeds the next push. */
+int rn_n3_session_decode_greedy(rn_n3_session* session, uint32_t first, int steps, uint32_t* ids);
 int rn_n3_session_length(const rn_n3_session* session, int* length);
 /* Session::logits (session.rs:151-165): output_vocab floats (host). */
 int rn_n3_session_logits(rn_n3_session* session, float* logits);

@@ -792,6 +792,16 @@ class OracleNeedle3Session:
         for t in tokens:
             self.push(int(t))
 
+    def greedy(self, first: int, steps: int) -> np.ndarray:
+        """generator.rs:199-230 without grammar: push, logits, argmax (generator.rs:257-265)."""
+        ids = np.empty(steps, np.uint32)
+        token = int(first)
+        for i in range(steps):
+            self.push(token)
+            token = argmax(self.logits())
+            ids[i] = token
+        return ids
+
     def __len__(self) -> int:
         return C.cast(self.handle, C.POINTER(N3Session)).contents.length
 

@@ -227,6 +227,7 @@ SIGNATURES = {
     "rn_n3_session_free": (_i, [_p]),
     "rn_n3_session_push": (_i, [_p, _u32]),
     "rn_n3_session_feed": (_i, [_p, _p, _i]),
+    "rn_n3_session_decode_greedy": (_i, [_p, _u32, _i, _p]),
     "rn_n3_session_length": (_i, [_p, C.POINTER(_i)]),
     "rn_n3_session_logits": (_i, [_p, _p]),
     "rn_n3_session_hidden": (_i, [_p, _p]),

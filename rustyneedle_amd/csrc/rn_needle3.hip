@@ -196,25 +196,63 @@ __device__ void n3_copy(float* dst, const float* src, int n) {
 
 // ---- kernels ---------------------------------------------------------------
 
-// session.rs:89-97: every lane holds the embedding row times sqrt(d); cell 0 is
-// their lane mean (session.rs:190-200).
-__global__ void n3_stream_init_kernel(const float* row, int d, int lanes, float scale, float* stream, float* cell) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= d) return;
-    const float v = row[i] * scale;
-    float mean = 0.0f;
-    for (int l = 0; l < lanes; ++l) {
-        stream[(size_t)l * d + i] = v;
-        mean = mean + v / (float)lanes;
+// tokens[position] = *source, or the host's token when source is null
+__global__ void n3_set_token_kernel(uint32_t* tokens, int position, uint32_t token, const uint32_t* source) {
+    if (threadIdx.x == 0) tokens[position] = source != nullptr ? *source : token;
+}
+
+// session.rs:86-97: the embedding row of tokens[position] (dequantise_row,
+// matrix.rs:140-153: level * norm, then each group's Walsh-Hadamard transform
+// in registers, lane u holding run u) times sqrt(d) into every lane; cell 0 is
+// their lane mean (session.rs:190-200). One block of 64 * ceil(runs / 64).
+__global__ __launch_bounds__(1024) void n3_embed_kernel(CodebookParams c, const uint32_t* tokens, int position, int d,
+                                                        int lanes, float scale, float* stream, float* cell) {
+    const int u = threadIdx.x, runs = c.padded / 16, rpg = c.group / 16, G = c.padded / c.group;
+    const int ib = c.bits == 5 ? 2 : c.bits;
+    const bool valid = u < runs;
+    const uint32_t token = tokens[position];
+    const uint8_t* row = c.packed + (size_t)token * c.row_bytes;
+    const float norm = valid ? __half2float(__ushort_as_half(c.norms[(size_t)token * G + (16 * u) / c.group])) : 0.0f;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = valid ? c.levels[n3_index(row, 16 * u + i, ib)] * norm : 0.0f;
+#pragma unroll
+    for (int span = 1; span < 16; span *= 2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if ((i & span) == 0) {
+                const float a = x[i], b = x[i + span];
+                x[i] = a + b;
+                x[i + span] = a - b;
+            }
+    for (int m = 1; m < rpg; m <<= 1) {
+        const bool high = (u & m) != 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float q = __shfl_xor(x[i], m, 64);
+            x[i] = high ? q - x[i] : x[i] + q;
+        }
     }
-    cell[i] = mean;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int e = 16 * u + i;
+        if (!valid || e >= d) continue;
+        const float v = (x[i] * c.wht_scale) * scale;
+        float mean = 0.0f;
+        for (int l = 0; l < lanes; ++l) {
+            stream[(size_t)l * d + e] = v;
+            mean = mean + v / (float)lanes;
+        }
+        cell[e] = mean;
+    }
 }
 
 struct N3GatherParams {
     CodebookParams tables;
     int count, sub, slots, position;
-    int index[kN3MaxTables];
-    int order[kN3MaxTables];
+    const uint32_t* tokens;  // the session's tokens [capacity]
+    int heads_per_order, stride;
+    int orders[4];
     float* out;  // [count * sub]
 };
 
@@ -224,13 +262,26 @@ struct N3GatherParams {
 __global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherParams p) {
     __shared__ float buf[kN3MaxWidth];
     __shared__ float red[32];
+    __shared__ int index_s[kN3MaxTables], order_s[kN3MaxTables];
     const CodebookParams& c = p.tables;
     const int n = p.count * p.sub, ib = c.bits == 5 ? 2 : c.bits, G = c.padded / c.group;
+    if (threadIdx.x < p.count) {  // engram.rs:30-46: table (order o, head) hashes the last `order` tokens
+        const int t = threadIdx.x, o = t / p.heads_per_order, head = t - o * p.heads_per_order;
+        uint32_t acc = 0x9E3779B9u * (uint32_t)(o * p.stride + head + 1);
+        for (int back = 0; back < p.orders[o]; ++back) {
+            const uint32_t token = p.position >= back ? p.tokens[p.position - back] : 0u;
+            acc = (acc ^ token) * 0x01000193u;
+        }
+        acc ^= acc >> 15;
+        index_s[t] = (int)(acc % (uint32_t)p.slots);
+        order_s[t] = p.orders[o];
+    }
+    __syncthreads();
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         const int t = e / p.sub, j = e - t * p.sub;
         float v = 0.0f;
-        if (p.position + 1 >= p.order[t]) {
-            const int row = t * p.slots + p.index[t];
+        if (p.position + 1 >= order_s[t]) {
+            const int row = t * p.slots + index_s[t];
             const float norm = __half2float(__ushort_as_half(c.norms[(size_t)row * G + j / c.group]));
             v = c.levels[n3_index(c.packed + (size_t)row * c.row_bytes, j, ib)] * norm;
         }
@@ -1813,6 +1864,9 @@ int stack_projections(rn_n3_model* m, const rn_archive* a, const int idx[4], N3L
     return RN_OK;
 }
 
+// config.rs:61: tables over the orders
+int heads_per_order(const rn_geometry& g) { return (int)g.engram_tables / (g.engram_order_count > 1 ? (int)g.engram_order_count : 1); }
+
 bool integer_path(const rn_matrix* x) { return x->bits == 2 || x->bits == 4 || x->bits == 5; }
 
 // The three-kernel step needs integer-path formats whose rows start where the
@@ -1986,6 +2040,10 @@ int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out) {
             N3_REQUIRE(e.key->cb.padded == e.value->cb.padded, "engram projections must share their width");
             N3_REQUIRE(e.tables->columns == (int)g.engram_sub_dim && e.tables->cb.padded == e.tables->columns,
                        "engram tables must hold sub_dim columns, a whole number of groups");
+            const int tables = (int)g.engram_order_count * heads_per_order(g);
+            N3_REQUIRE(e.key->columns == tables * (int)g.engram_sub_dim && tables * (int)g.engram_sub_dim <= kN3MaxWidth &&
+                           e.tables->rows >= tables * (int)g.engram_slots && g.engram_slots > 0,
+                       "engram projections must take tables x sub_dim columns (at most %d)", kN3MaxWidth);
         }
         N3_CALL(device_floats(m, archive, w.take(), &m->final_norm, d));
         if (w.failed) return n3_fail(RN_ERR_ARGUMENT, "directory ends before the canonical tensor list");
@@ -2085,7 +2143,6 @@ struct rn_n3_session {
     int capacity = 0, length = 0;
     bool fused = false;  // three kernels a layer; RN_N3_PATH=stepwise forces one launch per piece
     hipStream_t stream = nullptr;
-    std::vector<uint32_t> tokens;
     rn_lanes* lanes = nullptr;
     std::vector<N3CacheDev> caches;
     std::vector<float*> rings, ekey, evalue;
@@ -2094,7 +2151,10 @@ struct rn_n3_session {
     float *x = nullptr, *rotated = nullptr, *prod = nullptr, *attended = nullptr;
     void* codes = nullptr;         // the projections' input codes (int4 a run of 16)
     float* code_scales = nullptr;
-    float *attn_out = nullptr, *row = nullptr, *gathered = nullptr, *eraw = nullptr, *qscales = nullptr;
+    uint32_t* tokens_dev = nullptr;  // the tokens pushed so far [capacity]
+    uint32_t* next_dev = nullptr;    // the greedy argmax of the last logits
+    uint32_t* ids_dev = nullptr;     // greedy ids [capacity]
+    float *attn_out = nullptr, *gathered = nullptr, *eraw = nullptr, *qscales = nullptr;
     int8_t* qcodes = nullptr;
     float *cells = nullptr, *hidden = nullptr, *logits = nullptr, *cos = nullptr, *sin = nullptr;
     std::vector<float*> peak, total, weighted;
@@ -2151,23 +2211,7 @@ bool site_active(const rn_n3_model* m, int site) {
     return std::find(m->active.begin(), m->active.end(), (int)m->g.engram_sites[site]) != m->active.end();
 }
 
-int heads_per_order(const rn_geometry& g) { return (int)g.engram_tables / (g.engram_order_count > 1 ? (int)g.engram_order_count : 1); }
 
-// engram.rs:30-46
-void table_indices(const rn_geometry& g, const std::vector<uint32_t>& tokens, int position, int* out) {
-    const int hpo = heads_per_order(g), stride = g.engram_seed_heads == 0 ? hpo : (int)g.engram_seed_heads;
-    int n = 0;
-    for (int o = 0; o < (int)g.engram_order_count; ++o)
-        for (int head = 0; head < hpo; ++head) {
-            uint32_t acc = 0x9E3779B9u * (uint32_t)(o * stride + head + 1);
-            for (int back = 0; back < (int)g.engram_orders[o]; ++back) {
-                const uint32_t token = position >= back ? tokens[(size_t)(position - back)] : 0u;
-                acc = (acc ^ token) * 0x01000193u;
-            }
-            acc ^= acc >> 15;
-            out[n++] = (int)(acc % g.engram_slots);
-        }
-}
 
 }  // namespace
 
@@ -2233,9 +2277,11 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
         N3_CALL(alloc_n(s, (size_t)qkv + H * 64, &s->prod));
         N3_CALL(alloc_n(s, (size_t)H * 64, &s->attended));
         N3_CALL(alloc(s, (size_t)kN3Hadamard, &s->codes));
+        N3_CALL(alloc_n(s, (size_t)capacity, &s->tokens_dev));
+        N3_CALL(alloc_n(s, 64, &s->next_dev));
+        N3_CALL(alloc_n(s, (size_t)capacity, &s->ids_dev));
         N3_CALL(alloc_n(s, 64, &s->code_scales));
         N3_CALL(alloc_n(s, (size_t)d, &s->attn_out));
-        N3_CALL(alloc_n(s, (size_t)std::max(d, m->embedding->cb.padded), &s->row));
         N3_CALL(alloc_n(s, (size_t)kN3MaxWidth, &s->gathered));
         N3_CALL(alloc_n(s, (size_t)d, &s->eraw));
         N3_CALL(alloc_n(s, (size_t)H, &s->qscales));
@@ -2505,28 +2551,26 @@ int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
 
 }  // namespace
 
-// Session::push (session.rs:76-148)
-int rn_n3_session_push(rn_n3_session* s, uint32_t token) {
-    N3_REQUIRE(s, "null session");
+namespace {
+
+// Session::push (session.rs:76-148) of tokens[position], which the host writes
+// (source null) or a device value (source: the greedy argmax) supplies.
+int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
     const rn_n3_model* m = s->m;
     const rn_geometry& g = m->g;
-    N3_REQUIRE(token < g.vocab, "token %u is outside the vocabulary of %u", token, g.vocab);
-    N3_REQUIRE(s->length < s->capacity, "session is full (capacity %d)", s->capacity);
     const int d = (int)g.d_model, lanes = (int)g.mhc_lanes;
     const int position = s->length;
     hipStream_t st = s->stream;
-    s->tokens.push_back(token);
-
-    N3_HIP(launch_codebook_dequantise(m->embedding->cb, (int)token, s->row, st));
+    rn_launch(n3_set_token_kernel, dim3(1), dim3(64), 0, st, s->tokens_dev, position, token, source);
+    N3_HIP(hipGetLastError());
     float* cur = s->stream_a;
     float* nxt = s->stream_b;
-    rn_launch(n3_stream_init_kernel, dim3((d + 255) / 256), dim3(256), 0, st, (const float*)s->row, d, lanes,
-              sqrtf((float)d), cur, s->cells);
+    const int embed_threads = ((m->embedding->cb.padded / 16 + 63) / 64) * 64;
+    rn_launch(n3_embed_kernel, dim3(1), dim3(embed_threads), 0, st, m->embedding->cb, (const uint32_t*)s->tokens_dev,
+              position, d, lanes, sqrtf((float)d), cur, s->cells);
     N3_HIP(hipGetLastError());
 
     // engram sites (engram.rs:30-112), before the layers
-    int indices[kN3MaxTables] = {0};
-    table_indices(g, s->tokens, position, indices);
     const int hpo = heads_per_order(g), tables = (int)g.engram_order_count * hpo;
     const int keep = std::max(1, ((int)g.engram_conv_taps - 1) * (int)g.engram_conv_dilation + 1);
     for (uint32_t e = 0; e < g.engram_site_count; ++e) {
@@ -2538,13 +2582,11 @@ int rn_n3_session_push(rn_n3_session* s, uint32_t token) {
         gp.sub = (int)g.engram_sub_dim;
         gp.slots = (int)g.engram_slots;
         gp.position = position;
-        for (int t = 0; t < tables; ++t) {
-            gp.index[t] = indices[t];
-            gp.order[t] = (int)g.engram_orders[t / hpo];
-        }
+        gp.tokens = s->tokens_dev;
+        gp.heads_per_order = hpo;
+        gp.stride = g.engram_seed_heads == 0 ? hpo : (int)g.engram_seed_heads;
+        for (int o = 0; o < 4; ++o) gp.orders[o] = (int)g.engram_orders[o];
         gp.out = s->gathered;
-        N3_REQUIRE(tables * gp.sub <= kN3MaxWidth && eg.key->columns == tables * gp.sub,
-                   "engram key projection must take tables x sub_dim columns");
         rn_launch(n3_gather_kernel, dim3(1), dim3(kN3Block), 0, st, gp);
         N3_HIP(hipGetLastError());
         N3_CALL(rotate(eg.key, s->gathered, s->rotated, st));
@@ -2567,6 +2609,52 @@ int rn_n3_session_push(rn_n3_session* s, uint32_t token) {
     return RN_OK;
 }
 
+// Session::logits (session.rs:151-165) into s->logits on the device
+int enqueue_logits(rn_n3_session* s) {
+    const rn_n3_model* m = s->m;
+    hipStream_t st = s->stream;
+    rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->hidden, (int)m->g.d_model,
+              m->embedding->cb.padded, m->embedding->group, m->embedding->cb.wht_scale, s->rotated);
+    N3_HIP(hipGetLastError());
+    CodebookParams p = m->embedding->cb;
+    p.rows = m->output_vocab;  // multiply_rows(0, ..) over the first output_vocab rows
+    if (m->embedding->bits == 1 || m->embedding->bits == 3)
+        N3_HIP(launch_codebook_float(p, s->rotated, 1, s->logits, false, st));
+    else
+        N3_HIP(launch_codebook_product(p, s->rotated, 1, s->logits, nullptr, st));
+    return RN_OK;
+}
+
+}  // namespace
+
+int rn_n3_session_push(rn_n3_session* s, uint32_t token) {
+    N3_REQUIRE(s, "null session");
+    N3_REQUIRE(token < s->m->g.vocab, "token %u is outside the vocabulary of %u", token, s->m->g.vocab);
+    N3_REQUIRE(s->length < s->capacity, "session is full (capacity %d)", s->capacity);
+    return enqueue_push(s, token, nullptr);
+}
+
+// Generator::run_turn's greedy loop (generator.rs:199-230, argmax at 257-265)
+// without grammar: token = first; `steps` times { push(token); logits; token =
+// argmax; ids[i] = token }. The argmax stays on the device and feeds the next
+// push; the host waits once, for the ids.
+int rn_n3_session_decode_greedy(rn_n3_session* s, uint32_t first, int steps, uint32_t* ids) {
+    N3_REQUIRE(s && (ids || steps == 0), "null argument");
+    N3_REQUIRE(steps >= 0, "steps must be non-negative");
+    N3_REQUIRE(first < s->m->g.vocab, "token %u is outside the vocabulary of %u", first, s->m->g.vocab);
+    N3_REQUIRE(s->length + steps <= s->capacity, "%d steps overflow the capacity", steps);
+    if (steps == 0) return RN_OK;
+    N3_REQUIRE(steps <= s->capacity, "steps above the capacity");
+    for (int i = 0; i < steps; ++i) {
+        N3_CALL(enqueue_push(s, first, i == 0 ? nullptr : s->next_dev));
+        N3_CALL(enqueue_logits(s));
+        N3_HIP(launch_argmax_rows(s->logits, 1, s->m->output_vocab, s->next_dev, s->ids_dev, steps, i, s->stream));
+    }
+    N3_HIP(hipMemcpyAsync(ids, s->ids_dev, (size_t)steps * 4, hipMemcpyDeviceToHost, s->stream));
+    N3_HIP(hipStreamSynchronize(s->stream));
+    return RN_OK;
+}
+
 // Session::feed (session.rs:58-74): the batched prefill runs the same
 // arithmetic per token as pushing them in order.
 int rn_n3_session_feed(rn_n3_session* s, const uint32_t* tokens, int count) {
@@ -2586,20 +2674,9 @@ int rn_n3_session_length(const rn_n3_session* s, int* length) {
 // Session::logits (session.rs:151-165): logits [output_vocab] on the host
 int rn_n3_session_logits(rn_n3_session* s, float* logits) {
     N3_REQUIRE(s && logits, "null argument");
-    const rn_n3_model* m = s->m;
-    const int d = (int)m->g.d_model;
-    hipStream_t st = s->stream;
-    rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->hidden, d,
-              m->embedding->cb.padded, m->embedding->group, m->embedding->cb.wht_scale, s->rotated);
-    N3_HIP(hipGetLastError());
-    CodebookParams p = m->embedding->cb;
-    p.rows = m->output_vocab;  // multiply_rows(0, ..) over the first output_vocab rows
-    if (m->embedding->bits == 1 || m->embedding->bits == 3)
-        N3_HIP(launch_codebook_float(p, s->rotated, 1, s->logits, false, st));
-    else
-        N3_HIP(launch_codebook_product(p, s->rotated, 1, s->logits, nullptr, st));
-    N3_HIP(hipMemcpyAsync(logits, s->logits, (size_t)m->output_vocab * 4, hipMemcpyDeviceToHost, st));
-    N3_HIP(hipStreamSynchronize(st));
+    N3_CALL(enqueue_logits(s));
+    N3_HIP(hipMemcpyAsync(logits, s->logits, (size_t)s->m->output_vocab * 4, hipMemcpyDeviceToHost, s->stream));
+    N3_HIP(hipStreamSynchronize(s->stream));
     return RN_OK;
 }
 

@@ -84,6 +84,22 @@ def test_feed_equals_push(archive, path):
     assert np.array_equal(_bits(a.cells()), _bits(b.cells()))
 
 
+def test_decode_greedy(archive, path):
+    """Generator::run_turn's loop with the argmax on the device: the ids, then
+    the state after them, against the oracle."""
+    gm, om = needle3.Model(archive), oracle.OracleNeedle3(archive)
+    gs, os_ = gm.session(64), om.session(64)
+    prompt = _tokens(9, seed=11)
+    gs.feed(prompt)
+    os_.feed(prompt)
+    ids = gs.decode_greedy(7, 24)
+    want = os_.greedy(7, 24)
+    assert ids.tolist() == want.tolist()
+    assert len(gs) == len(os_) == 9 + 24
+    assert np.array_equal(_bits(gs.hidden()), _bits(os_.hidden()))
+    assert np.array_equal(_bits(gs.logits()), _bits(os_.logits()))
+
+
 def test_errors(archive):
     gm = needle3.Model(archive)
     s = gm.session(4)
