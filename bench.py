@@ -343,6 +343,54 @@ def bench_whistle(rn, reps: int = 3, steps: int = 48, with_cpu: bool = True):
     return out
 
 
+def bench_needle3(rn, with_cpu: bool = True, context: int = 600, steps: int = 64):
+    """The Needle 3 block (crates/model/src/session.rs) at its documented shape
+    (d_model 768, 20 layers, 12 heads over 4 kv heads, four lanes, two engram
+    sites, 32 x 32 Hadamard factors, 2-bit projections, 4-bit 8192 x 768
+    logits) from a synthetic archive: a 600-token feed, then greedy decode
+    (push, logits, argmax) at that context, HIP events on the session's stream;
+    the first pushes checked bit for bit against the oracle."""
+    import oracle
+    from rustyneedle_amd import needle3
+    archive = needle3.synthetic_archive(needle3.NEEDLE3)
+    model = needle3.Model(archive)
+    prompt = rn.synth_tokens(rn.SEED, "needle3.prompt", needle3.NEEDLE3["vocab"], (context,))
+    # bit identity with the oracle on the first pushes
+    om = oracle.OracleNeedle3(archive)
+    gs, os_ = model.session(16), om.session(16)
+    identical = True
+    for t in prompt[:4]:
+        gs.push(int(t))
+        os_.push(int(t))
+        identical &= bool(np.array_equal(gs.hidden().view(np.uint32), os_.hidden().view(np.uint32)))
+    s = model.session(context + steps + 8)
+    stream = s.stream()
+    t0, t1, t2, t3 = rn.Event(), rn.Event(), rn.Event(), rn.Event()
+    t0.record(stream)
+    s.feed(prompt)
+    t1.record(stream)
+    s.decode_greedy(int(prompt[-1]), 4)  # warm
+    t2.record(stream)
+    s.decode_greedy(int(prompt[-1]), steps)
+    t3.record(stream)
+    feed_ms, dec_ms = t0.elapsed_ms(t1), t2.elapsed_ms(t3)
+    out = dict(decode_tokens_per_s=steps / (dec_ms / 1e3), decode_ms_per_token=dec_ms / steps, context=context + 4,
+               feed_tokens_per_s=context / (feed_ms / 1e3), layers=needle3.NEEDLE3["num_layers"],
+               d_model=needle3.NEEDLE3["d_model"], bit_identical=identical,
+               reference_published="decode about 830-860 tokens/s at 600 tokens of context on an Apple M1 Max "
+                                   "(docs/architecture.md, Performance)")
+    if with_cpu:
+        oracle.set_threads(1)
+        cs = om.session(24)
+        t = time.perf_counter()
+        for tok in prompt[:16]:
+            cs.push(int(tok))
+        dt = (time.perf_counter() - t) / 16
+        out["cpu"] = dict(ms_per_push=dt * 1e3, tokens_per_s=1.0 / dt, cores=1, kind="port",
+                          sample="16 pushes from an empty session, C oracle on one thread")
+    return out
+
+
 def cpu_baseline(rn, cfg, cache, budget_s: float = 10.0):
     """The oracle (C restatement of the reference path) on the host cores, with
     the reference's thread policy min(cores - 1, 6) (crates/kernels/src/pool.rs:48-52)."""
@@ -389,7 +437,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="decode only")
-    ap.add_argument("--extras", default="gemv,prefill_256,decode_batch64,whistle,codebook,frontend",
+    ap.add_argument("--extras", default="gemv,prefill_256,decode_batch64,whistle,codebook,frontend,needle3",
                     help="comma-separated secondary measurements to run")
     ap.add_argument("--profile-steps", type=int, default=DECODE_TOKENS,
                     help="greedy steps timed kernel by kernel for the roofline")
@@ -426,7 +474,8 @@ def main() -> int:
                          ("decode_batch64", lambda: bench_batch(rn, model, cfg)),
                          ("whistle", lambda: bench_whistle(rn, with_cpu=not args.no_cpu)),
                          ("codebook", lambda: bench_codebook(rn)),
-                         ("frontend", lambda: bench_frontend(rn))):
+                         ("frontend", lambda: bench_frontend(rn)),
+                         ("needle3", lambda: bench_needle3(rn, with_cpu=not args.no_cpu))):
             if name not in wanted:
                 continue
             log(f"bench: {name}")

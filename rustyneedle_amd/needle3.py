@@ -196,6 +196,11 @@ class Session:
         t = np.ascontiguousarray(tokens, np.uint32)
         check(lib.rn_n3_session_feed(self.handle, _ptr(t), t.size))
 
+    def stream(self) -> int:
+        h = _p()
+        check(lib.rn_n3_session_stream(self.handle, _C.byref(h)))
+        return h.value
+
     def decode_greedy(self, first: int, steps: int) -> np.ndarray:
         ids = np.empty(steps, np.uint32)
         check(lib.rn_n3_session_decode_greedy(self.handle, int(first), steps, _ptr(ids)))
