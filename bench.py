@@ -51,12 +51,12 @@ KERNEL_NAMES = {
 # (FETCH x2.000, WRITE x1.000). Recorded in profiles/decode_b1_needle20_traffic.md;
 # they describe the kernels as built when measured and are re-measured with them.
 PMC_TRAFFIC = {
-    "qkv_attention": 1_712_282,
-    "out": 400_530,
-    "gate_up": 2_488_974,
-    "down": None,  # re-measured with the four-wave kernel
-    "logits": 4_906_489,
-    "final": 11_979,
+    "qkv_attention": 1_723_522,
+    "out": 400_320,
+    "gate_up": 2_503_276,
+    "down": 1_345_319,
+    "logits": 4_914_412,
+    "final": 10_341,
 }
 
 
