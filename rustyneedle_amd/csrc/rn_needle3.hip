@@ -104,30 +104,56 @@ __device__ __forceinline__ float n3_fold(float s, const float* a, const float* b
 }
 
 // ops.rs:7-17 over n values in LDS: eight strided lanes, summed in lane order,
-// then the tail. Every thread calls; all get the result.
-__device__ float n3_sum_of_squares(const float* v, int n, float* red) {
-    const int tid = threadIdx.x;
-    if (tid < 8) red[tid] = n3_fold<true>(0.0f, v + tid, nullptr, n / 8, 8);
+// then the tail. Every thread calls; all get the result. With `sq` (LDS
+// scratch of n + 64 floats, 16-byte aligned, n / 8 a multiple of 4) the squares
+// are first computed by every thread into sq, lane j's at row j (stride n / 8
+// + 8, so the writes of a wave fall in distinct banks), and the eight chains
+// only add, four squares a read.
+__device__ float n3_sum_of_squares(const float* v, int n, float* red, float* sq = nullptr) {
+    const int tid = threadIdx.x, n8 = n / 8;
+    if (sq != nullptr && (n8 & 3) == 0) {
+        const int stride = n8 + 8;
+        for (int i = tid; i < n8 * 8; i += blockDim.x) {
+            const float x = v[i];
+            sq[(i & 7) * stride + (i >> 3)] = x * x;
+        }
+        __syncthreads();
+        if (tid < 8) {
+            const float4* q = reinterpret_cast<const float4*>(sq + tid * stride);
+            float s = 0.0f;
+#pragma unroll 8
+            for (int k = 0; k < n8 / 4; ++k) {
+                const float4 t = q[k];
+                s = s + t.x;
+                s = s + t.y;
+                s = s + t.z;
+                s = s + t.w;
+            }
+            red[tid] = s;
+        }
+    } else if (tid < 8) {
+        red[tid] = n3_fold<true>(0.0f, v + tid, nullptr, n8, 8);
+    }
     __syncthreads();
     float total = 0.0f;
     for (int j = 0; j < 8; ++j) total = total + red[j];
     float tail = -0.0f;
-    for (int i = n / 8 * 8; i < n; ++i) tail = tail + v[i] * v[i];
+    for (int i = n8 * 8; i < n; ++i) tail = tail + v[i] * v[i];
     __syncthreads();
     return total + tail;
 }
 
 // ops.rs:44-58: out = ((1 + gain) * x) * inverse (out may be x)
-__device__ void n3_norm(const float* x, const float* gain, int n, float* out, float* red) {
-    const float mean_square = n3_sum_of_squares(x, n, red) / (float)n;
+__device__ void n3_norm(const float* x, const float* gain, int n, float* out, float* red, float* sq = nullptr) {
+    const float mean_square = n3_sum_of_squares(x, n, red, sq) / (float)n;
     const float inverse = 1.0f / sqrtf(mean_square + 1e-6f);
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = ((1.0f + gain[i]) * x[i]) * inverse;
     __syncthreads();
 }
 
 // ops.rs:60-66
-__device__ void n3_unit_rms(const float* x, int n, float* out, float* red) {
-    const float inverse = 1.0f / sqrtf(n3_sum_of_squares(x, n, red) / (float)n + 1e-6f);
+__device__ void n3_unit_rms(const float* x, int n, float* out, float* red, float* sq = nullptr) {
+    const float inverse = 1.0f / sqrtf(n3_sum_of_squares(x, n, red, sq) / (float)n + 1e-6f);
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inverse;
     __syncthreads();
 }
@@ -189,6 +215,39 @@ __device__ void n3_copy(float* dst, const float* src, int n) {
             const int i = base + j * blockDim.x + threadIdx.x;
             if (i < n) dst[i] = t[j];
         }
+    }
+}
+
+// One region of a staging pass: `count` 16-byte units from global `src` to
+// LDS `dst` (count 0: nothing, src may be null).
+struct N3Span {
+    const void* src;
+    void* dst;
+    int count;
+};
+
+typedef __attribute__((address_space(3))) void n3_lds_void;
+typedef __attribute__((address_space(1))) void n3_global_void;
+
+// Everything a block stages, in one pass that holds no registers: the regions'
+// 16-byte units go global -> LDS by global_load_lds_dwordx4 (lane l of a wave
+// lands at the wave's LDS base + 16 l), in chunks of 64 units dealt to the
+// waves in turn. The copies count on vmcnt: every wave waits for its own
+// (s_waitcnt) before the barrier that publishes them.
+template <int N>
+__device__ __forceinline__ void n3_stage(const N3Span (&s)[N]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    int c0 = 0;  // the first chunk of region j
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const int count = s[j].count, chunks = (count + 63) / 64;
+        for (int c = c0 + (wave - c0 % waves + waves) % waves; c < c0 + chunks; c += waves) {
+            const int q = c - c0, unit = 64 * q + lane;
+            if (unit < count)
+                __builtin_amdgcn_global_load_lds((n3_global_void*)(reinterpret_cast<const int4*>(s[j].src) + unit),
+                                                 (n3_lds_void*)(reinterpret_cast<int4*>(s[j].dst) + 64 * q), 16, 0, 0);
+        }
+        c0 += chunks;
     }
 }
 
@@ -575,34 +634,57 @@ struct N3BlockOutParams {
 
 // kronecker_apply for 32 x 32 factors (ops.rs:220-297): mixed = X . R, then
 // out = L^T . mixed, each a chain of fused multiply-adds in index order.
-// 1024 threads; x and out in LDS (distinct), mixed LDS scratch.
-__device__ void n3_kronecker32(const float* x, const float* left, const float* right, float* mixed, float* out) {
-    const int tid = threadIdx.x, i = tid >> 5, c = tid & 31;
-    float a[32], b[32];
+// Every thread of the block calls (256 or more); x and out in LDS (distinct),
+// mixed LDS scratch; x and left 16-byte aligned.
+__device__ __forceinline__ void n3_kronecker32(const float* x, const float* left, const float* right, float* mixed, float* out) {
+    // threads 0..255: column c of rows 4 q .. 4 q + 3, so that a column of the
+    // right factor (stage one) or of the mixed matrix (stage two) read once
+    // serves four outputs; each output's chain stays in index order
+    const int tid = threadIdx.x, c = tid & 31, i0 = (tid >> 5) * 4;
+    if (tid < 256) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < 32; ++j) a[j] = right[j * 32 + c];
+        for (int j = 0; j < 32; j += 4) {
+            float r[4];
+            float4 q[4];
 #pragma unroll
-    for (int j = 0; j < 32; j += 4) {
-        const float4 q = *reinterpret_cast<const float4*>(x + i * 32 + j);
-        b[j] = q.x;
-        b[j + 1] = q.y;
-        b[j + 2] = q.z;
-        b[j + 3] = q.w;
+            for (int k = 0; k < 4; ++k) r[k] = right[(j + k) * 32 + c];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) q[m] = *reinterpret_cast<const float4*>(x + (i0 + m) * 32 + j);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                acc[m] = __builtin_fmaf(r[0], q[m].x, acc[m]);
+                acc[m] = __builtin_fmaf(r[1], q[m].y, acc[m]);
+                acc[m] = __builtin_fmaf(r[2], q[m].z, acc[m]);
+                acc[m] = __builtin_fmaf(r[3], q[m].w, acc[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) mixed[(i0 + m) * 32 + c] = acc[m];
     }
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 32; ++j) acc = __builtin_fmaf(a[j], b[j], acc);
-    mixed[tid] = acc;
     __syncthreads();
+    if (tid < 256) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int r = 0; r < 32; ++r) {
-        a[r] = mixed[r * 32 + c];
-        b[r] = left[r * 32 + i];
+        for (int r = 0; r < 32; r += 4) {
+            float mv[4];
+            float4 l[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                mv[k] = mixed[(r + k) * 32 + c];
+                l[k] = *reinterpret_cast<const float4*>(left + (r + k) * 32 + i0);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                acc[0] = __builtin_fmaf(mv[k], l[k].x, acc[0]);
+                acc[1] = __builtin_fmaf(mv[k], l[k].y, acc[1]);
+                acc[2] = __builtin_fmaf(mv[k], l[k].z, acc[2]);
+                acc[3] = __builtin_fmaf(mv[k], l[k].w, acc[3]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) out[(i0 + m) * 32 + c] = acc[m];
     }
-    acc = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 32; ++r) acc = __builtin_fmaf(a[r], b[r], acc);
-    out[tid] = acc;
     __syncthreads();
 }
 
@@ -647,10 +729,10 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
     n3_copy(xs, p.x, d);
     if (p.rank == 8 && !cv_staged) n3_copy(cv, p.cond_v, d * 8);
     __syncthreads();
-    n3_norm(a, p.post_norm, d, a, red);
+    n3_norm(a, p.post_norm, d, a, red, st);
     for (int i = tid; i < d; i += blockDim.x) xs[i] = xs[i] + p.gate * a[i];
     __syncthreads();
-    n3_norm(xs, p.pre_norm, d, a, red);  // a = pre
+    n3_norm(xs, p.pre_norm, d, a, red, st);  // a = pre
     // condition weights (hadamard.rs:57-79)
     if (p.rank == 8) {
         if (tid < 32) {
@@ -1012,27 +1094,33 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
         const uint8_t* base = w + (size_t)(live ? u : 0) * 2 * IB;
         const bool leader = live && (u & (rpg - 1)) == 0;
         for (int r0 = wave; r0 < R; r0 += 4 * waves) {
+            // the four rows' words first (rows past R repeat the last; a lane past
+            // the runs has zero codes, so its sums are zero), then the sums
             int sum[4];
+            if constexpr (IB == 2) {
+                uint32_t wd[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int r = r0 + k * waves;
-                int sm = 0;
-                if (r < R && live) {
-                    if constexpr (IB == 2) {
-                        const uint32_t wd = *reinterpret_cast<const uint32_t*>(base + (size_t)r * c.row_bytes);
-                        sm = dot4(n3_decode4<2>(wd & 0x03030303u, lut), x.x, sm);
-                        sm = dot4(n3_decode4<2>((wd >> 2) & 0x03030303u, lut), x.y, sm);
-                        sm = dot4(n3_decode4<2>((wd >> 4) & 0x03030303u, lut), x.z, sm);
-                        sm = dot4(n3_decode4<2>((wd >> 6) & 0x03030303u, lut), x.w, sm);
-                    } else {
-                        const uint2 wd = *reinterpret_cast<const uint2*>(base + (size_t)r * c.row_bytes);
-                        sm = dot4(n3_decode4<4>(wd.x & 0x0f0f0f0fu, lut), x.x, sm);
-                        sm = dot4(n3_decode4<4>((wd.x >> 4) & 0x0f0f0f0fu, lut), x.y, sm);
-                        sm = dot4(n3_decode4<4>(wd.y & 0x0f0f0f0fu, lut), x.z, sm);
-                        sm = dot4(n3_decode4<4>((wd.y >> 4) & 0x0f0f0f0fu, lut), x.w, sm);
-                    }
+                for (int k = 0; k < 4; ++k)
+                    wd[k] = *reinterpret_cast<const uint32_t*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    int sm = dot4(n3_decode4<2>(wd[k] & 0x03030303u, lut), x.x, 0);
+                    sm = dot4(n3_decode4<2>((wd[k] >> 2) & 0x03030303u, lut), x.y, sm);
+                    sm = dot4(n3_decode4<2>((wd[k] >> 4) & 0x03030303u, lut), x.z, sm);
+                    sum[k] = dot4(n3_decode4<2>((wd[k] >> 6) & 0x03030303u, lut), x.w, sm);
                 }
-                sum[k] = sm;
+            } else {
+                uint2 wd[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    wd[k] = *reinterpret_cast<const uint2*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    int sm = dot4(n3_decode4<4>(wd[k].x & 0x0f0f0f0fu, lut), x.x, 0);
+                    sm = dot4(n3_decode4<4>((wd[k].x >> 4) & 0x0f0f0f0fu, lut), x.y, sm);
+                    sm = dot4(n3_decode4<4>(wd[k].y & 0x0f0f0f0fu, lut), x.z, sm);
+                    sum[k] = dot4(n3_decode4<4>((wd[k].y >> 4) & 0x0f0f0f0fu, lut), x.w, sm);
+                }
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -1127,24 +1215,25 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     const int group = p.H / p.KV, kvh = h / group, P = p.qkvg.padded, G = P / p.qkvg.group;
     const int qw = p.H * kN3Head, kw = p.KV * kN3Head, width_all = qw + 2 * kw;
     const int count = p.count, last = count - 1;  // the new position is first + last
-    auto row_of = [&](int r) -> int {
-        return r < 64 ? h * 64 + r
-                      : r < 128 ? qw + kvh * 64 + (r - 64)
-                                : r < 192 ? qw + kw + kvh * 64 + (r - 128) : qw + 2 * kw + h * 64 + (r - 192);
-    };
-    // ---- loads
-    const int chunks = p.qkvg.row_bytes / 16;
+    // ---- loads: none conditional (indices clamped), so that the values stay in
+    // registers and every request is out before the first wait. The head's rows
+    // are four ranges of 64 (q rows, its kv head's k and v rows, gate rows),
+    // staged one after another.
+    const int chunks = p.qkvg.row_bytes / 16, per_range = 64 * chunks;
+    auto range_row = [&](int j) { return j == 0 ? h * 64 : j == 1 ? qw + kvh * 64 : j == 2 ? qw + kw + kvh * 64 : qw + 2 * kw + h * 64; };
     int4 rw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int i = j * kN3AttendThreads + tid;
-        if (i < 256 * chunks) rw[j] = reinterpret_cast<const int4*>(p.qkvg.packed + (size_t)row_of(i / chunks) * p.qkvg.row_bytes)[i % chunks];
+        const int i = min(j * kN3AttendThreads + tid, 4 * per_range - 1);
+        const int rj = (i >= per_range) + (i >= 2 * per_range) + (i >= 3 * per_range);
+        rw[j] = reinterpret_cast<const int4*>(p.qkvg.packed + (size_t)range_row(rj) * p.qkvg.row_bytes)[i - rj * per_range];
     }
     uint16_t rn[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int i = j * kN3AttendThreads + tid;
-        rn[j] = i < 256 * G ? p.qkvg.norms[(size_t)row_of(i / G) * G + i % G] : 0;
+        const int i = min(j * kN3AttendThreads + tid, 256 * G - 1), per = 64 * G;
+        const int rj = (i >= per) + (i >= 2 * per) + (i >= 3 * per);
+        rn[j] = p.qkvg.norms[(size_t)range_row(rj) * G + (i - rj * per)];
     }
     int4 code = make_int4(0, 0, 0, 0);
     if (tid < P / 16) code = p.codes[tid];
@@ -1171,21 +1260,21 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     const int8_t* vbase = p.values + ((size_t)kvh * p.cap + p.first) * kN3Head;
     const float* ks = p.key_scales + (size_t)kvh * p.cap + p.first;
     const float* vsc = p.value_scales + (size_t)kvh * p.cap + p.first;
+    // (a thread past the earlier positions reads the last of them, or the new
+    // position's row when there is none, and does not use it)
+    const int kp = min(tid, max(last - 1, 0));
     int4 kr[4];
-    float kscale = 0.0f;
-    if (tid < last) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const int4*>(kbase + (size_t)tid * kN3Head)[i];
-        kscale = ks[tid];
-    }
+    for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const int4*>(kbase + (size_t)kp * kN3Head)[i];
+    const float kscale = ks[kp];
     const int dg = tid & 15, pc = tid >> 4;
     int vr[16];
     float vsr[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        const int pp = pc + 64 * j;
-        vr[j] = pp < last ? *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head + 4 * dg) : 0;
-        vsr[j] = pp < last ? vsc[pp] : 0.0f;
+        const int vp = min(pc + 64 * j, max(last - 1, 0));  // used only below last
+        vr[j] = *reinterpret_cast<const int*>(vbase + (size_t)vp * kN3Head + 4 * dg);
+        vsr[j] = vsc[vp];
     }
     // ---- the head's projection rows
 #pragma unroll
@@ -1355,54 +1444,42 @@ constexpr int kN3OutRowBytes = 1024;  // 4-bit over 2048 columns or 2-bit over 4
 // fake_quantise_int8 of the gated attention, prepare, then rows
 // [64 * blockIdx.x, + 64) of the output projection (attention.rs:150-153).
 // The block's rows, norms and the attention are requested together first.
-__global__ __launch_bounds__(256) void n3_out_kernel(N3OutParams p) {
+template <int LPT>
+__global__ __launch_bounds__(1024) void n3_out_kernel(N3OutParams p) {
     __shared__ __align__(16) uint8_t w_s[64 * kN3OutRowBytes];
-    __shared__ uint16_t nm_s[64 * 64];
-    __shared__ float v[kN3MaxWidth];
+    __shared__ __align__(16) uint16_t nm_s[64 * 64 + 8];
+    __shared__ __align__(16) float v[kN3MaxWidth];
     __shared__ int4 xq[kN3MaxWidth / 16];
     __shared__ float xs[64];
     __shared__ int acc[64 * 64];
     __shared__ float y_s[64];
-    __shared__ float red[8];
+    __shared__ float red[16];
+    constexpr int T = 1024;
     const int P = p.out.padded, G = P / p.out.group, tid = threadIdx.x;
     const int r0 = blockIdx.x * 64, R = min(64, p.out.rows - r0);
-    const int chunks = p.out.row_bytes / 16;
-    constexpr int kLoads = 64 * kN3OutRowBytes / 16 / 256;
-    int4 rw[kLoads];
+    // the block's rows are contiguous: LPT 16-byte loads a thread, then the
+    // norms and the input vector, none conditional (indices clamped; the last
+    // norm unit may run into the next rows' norms or the blob's padding)
+    const int units = R * (p.out.row_bytes / 16);
+    const int4* wsrc = reinterpret_cast<const int4*>(p.out.packed + (size_t)r0 * p.out.row_bytes);
+    int4 rw[LPT];
 #pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-        const int i = j * 256 + tid;
-        if (i < R * chunks) rw[j] = reinterpret_cast<const int4*>(p.out.packed + (size_t)(r0 + i / chunks) * p.out.row_bytes)[i % chunks];
-    }
-    uint16_t rn[16];
+    for (int j = 0; j < LPT; ++j) rw[j] = wsrc[min(j * T + tid, units - 1)];
+    const int nn = (R * G * 2 + 15) / 16, n4 = p.n / 4;
+    const int4 rn = reinterpret_cast<const int4*>(p.out.norms + (size_t)r0 * G)[min(tid, nn - 1)];
+    const float4 a = reinterpret_cast<const float4*>(p.attended)[min(tid, n4 - 1)];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int i = j * 256 + tid;
-        rn[j] = i < R * G ? p.out.norms[(size_t)(r0 + i / G) * G + i % G] : 0;
-    }
-    float a[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int i = j * 256 + tid;
-        a[j] = i < p.n ? p.attended[i] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-        const int i = j * 256 + tid;
-        if (i < R * chunks) reinterpret_cast<int4*>(w_s)[i] = rw[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int i = j * 256 + tid;
-        if (i < R * G) nm_s[i] = rn[j];
-        if (i < P) v[i] = a[j];
-    }
+    for (int j = 0; j < LPT; ++j)
+        if (j * T + tid < units) reinterpret_cast<int4*>(w_s)[j * T + tid] = rw[j];
+    if (tid < nn) reinterpret_cast<int4*>(nm_s)[tid] = rn;
+    if (tid < n4) reinterpret_cast<float4*>(v)[tid] = a;
+    for (int i = p.n + tid; i < P; i += T) v[i] = 0.0f;
     __syncthreads();
     n3_fake_quantise(v, p.n, red);
     n3_prepare_codes(v, P, p.out.group, p.out.wht_scale, p.out.bits == 5 ? 2 : p.out.bits, xq, xs);
     __syncthreads();
     n3_rows(p.out, w_s, nm_s, R, xq, xs, acc, y_s);
-    for (int r = tid; r < R; r += blockDim.x) p.y[r0 + r] = y_s[r];
+    if (tid < R) p.y[r0 + tid] = y_s[tid];
 }
 
 struct N3BoundaryParams {
@@ -1439,8 +1516,8 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     __shared__ float chains_[32];
     __shared__ float weights_[64];
     __shared__ float red[32];
-    __shared__ float cv_[kN3Hadamard * 8];
-    __shared__ float stream_s[kN3MaxWidth];
+    __shared__ __align__(16) float cv_[kN3Hadamard * 8];
+    __shared__ __align__(16) float stream_s[kN3MaxWidth];
     __shared__ float rv[kN3MaxWidth];
     __shared__ int4 rq[kN3MaxWidth / 16];
     __shared__ float rs[64];
@@ -1448,8 +1525,8 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     __shared__ float ry[kN3RouteRows];
     __shared__ __align__(16) uint8_t pw[kN3RouteRows * kN3RouteRowBytes];
     __shared__ uint16_t pn[kN3RouteRows * 64];
-    __shared__ float factors_s[6][kN3Hadamard];
-    __shared__ float tin_s[3][kN3Hadamard];  // the tail's attention, x and input
+    __shared__ __align__(16) float factors_s[6][kN3Hadamard];
+    __shared__ __align__(16) float tin_s[3][kN3Hadamard];  // the tail's attention, x and input
     __shared__ float lane_s[2 * kMaxLanes + kMaxLanes * kMaxLanes];  // post, residual of the tail
     __shared__ float small_s[4 * kMaxLanes + 2 * 64];  // a_pre a_post a_res (one each), b_pre, b_post, b_res
     __shared__ float gate_s[kMaxLanes];
@@ -1457,27 +1534,40 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     const int tid = threadIdx.x, d = p.d, L = p.lanes, S = L * d;
     // everything this block reads from memory, requested first
     const int route_rows = 2 * L + L * L, G = p.phi_pre.padded / p.phi_pre.group;
+    const int layer = p.layer, chunks = p.phi_pre.row_bytes / 16;
+    N3BlockOutParams t = p.t;
+    N3TailPre pre{};
+    const bool cv_staged = p.tail && t.rank == 8;
+    {
+        const int tc = p.tail ? 1 : 0, rc = p.route ? 1 : 0;
+        const size_t rb = p.phi_pre.row_bytes;
+        const N3Span spans[14] = {
+            {t.cond_v, cv_, cv_staged ? d * 2 : 0},
+            {t.factors[0], factors_s[0], tc * kN3Hadamard / 4},
+            {t.factors[1], factors_s[1], tc * kN3Hadamard / 4},
+            {t.factors[2], factors_s[2], tc * kN3Hadamard / 4},
+            {t.factors[3], factors_s[3], tc * kN3Hadamard / 4},
+            {t.factors[4], factors_s[4], tc * kN3Hadamard / 4},
+            {t.factors[5], factors_s[5], tc * kN3Hadamard / 4},
+            {t.attention, tin_s[0], tc * d / 4},
+            {t.x, tin_s[1], tc * d / 4},
+            {t.input, tin_s[2], tc * d / 4},
+            {p.tail ? t.stream : p.stream, stream_s, S / 4},
+            {p.phi_pre.packed + (size_t)layer * L * rb, pw, rc * L * chunks},
+            {p.phi_post.packed + (size_t)layer * L * rb, pw + (size_t)L * rb, rc * L * chunks},
+            {p.phi_res.packed + (size_t)layer * L * L * rb, pw + (size_t)2 * L * rb, rc * L * L * chunks},
+        };
+        n3_stage(spans);
+    }
+    if (p.tail) pre = n3_tail_prefetch(t);
+    // the layer's norms of phi_pre, phi_post and phi_res (rows one after another)
+    uint16_t tn = 0;
     if (p.route) {
-        const int layer = p.layer;
-        // the layer's rows of phi_pre, phi_post and phi_res, one after another
-        auto route_row = [&](int r) -> const uint8_t* {
-            return r < L ? p.phi_pre.packed + (size_t)(layer * L + r) * p.phi_pre.row_bytes
-                         : r < 2 * L ? p.phi_post.packed + (size_t)(layer * L + r - L) * p.phi_pre.row_bytes
-                                     : p.phi_res.packed + (size_t)(layer * L * L + r - 2 * L) * p.phi_pre.row_bytes;
-        };
-        auto route_norms = [&](int r) -> const uint16_t* {
-            return r < L ? p.phi_pre.norms + (size_t)(layer * L + r) * G
-                         : r < 2 * L ? p.phi_post.norms + (size_t)(layer * L + r - L) * G
-                                     : p.phi_res.norms + (size_t)(layer * L * L + r - 2 * L) * G;
-        };
-        const int chunks = p.phi_pre.row_bytes / 16, total = route_rows * chunks;
-        int4 tw[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int i = j * blockDim.x + tid;
-            if (i < total) tw[j] = reinterpret_cast<const int4*>(route_row(i / chunks))[i % chunks];
-        }
-        uint16_t tn = tid < route_rows * G ? route_norms(tid / G)[tid % G] : 0;
+        const int i = min(tid, route_rows * G - 1), r = i / G;
+        const uint16_t* nsrc = r < L ? p.phi_pre.norms + (size_t)(layer * L + r) * G
+                                     : r < 2 * L ? p.phi_post.norms + (size_t)(layer * L + r - L) * G
+                                                 : p.phi_res.norms + (size_t)(layer * L * L + r - 2 * L) * G;
+        tn = nsrc[i - r * G];
         if (tid < L) {
             small_s[3 + tid] = p.b_pre[layer * L + tid];
             small_s[3 + L + tid] = p.b_post[layer * L + tid];
@@ -1488,27 +1578,14 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
             small_s[1] = p.a_post[layer];
             small_s[2] = p.a_res[layer];
         }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int i = j * blockDim.x + tid;
-            if (i < total) reinterpret_cast<int4*>(pw)[i] = tw[j];
-        }
-        if (tid < route_rows * G) pn[tid] = tn;
     }
-    N3BlockOutParams t = p.t;
-    N3TailPre pre{};
-    const bool cv_staged = p.tail && t.rank == 8;
-    if (cv_staged) n3_copy(cv_, t.cond_v, d * 8);
     if (p.tail) {
-        pre = n3_tail_prefetch(t);
-        n3_copy(&factors_s[0][0], t.factors[0], kN3Hadamard);
-        for (int f = 1; f < 6; ++f) n3_copy(&factors_s[f][0], t.factors[f], kN3Hadamard);
-        n3_copy(tin_s[0], t.attention, d);
-        n3_copy(tin_s[1], t.x, d);
-        n3_copy(tin_s[2], t.input, d);
-        n3_copy(stream_s, t.stream, S);
         if (tid < L) lane_s[tid] = t.post[tid];
         if (tid < L * L) lane_s[kMaxLanes + tid] = t.residual[tid];
+    }
+    if (p.route && tid < route_rows * G) pn[tid] = tn;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's staged units are in LDS
+    if (p.tail) {
         // the tail reads its copies
         for (int f = 0; f < 6; ++f) t.factors[f] = factors_s[f];
         t.attention = tin_s[0];
@@ -1517,8 +1594,6 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
         t.stream = stream_s;
         t.post = lane_s;
         t.residual = lane_s + kMaxLanes;
-    } else {
-        n3_copy(stream_s, p.stream, S);
     }
     __syncthreads();
     const N3TailLds l{xs_, a_, sc_, st_, mx_, mod_, cv_, chains_, weights_, red};
@@ -1534,7 +1609,7 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
             a_[i] = v;
         }
         __syncthreads();
-        n3_norm(a_, p.final_norm, d, a_, red);
+        n3_norm(a_, p.final_norm, d, a_, red, cv_);
         for (int i = tid; i < d; i += blockDim.x) p.hidden[i] = a_[i];
     }
     if (!p.route) return;
@@ -1544,7 +1619,7 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     key_r[0] = (p.key != nullptr && tid < d) ? p.key[tid] : 0.0f;
     value_r[0] = (p.key != nullptr && tid < d) ? p.value[tid] : 0.0f;
     // lanes.rs:49-53: unit_rms, fake_quantise_int8, prepare (phi_pre's groups)
-    n3_unit_rms(stream_s, S, rv, red);
+    n3_unit_rms(stream_s, S, rv, red, cv_);
     n3_fake_quantise(rv, S, red);
     const int P = p.phi_pre.padded;
     for (int i = S + tid; i < P; i += blockDim.x) rv[i] = 0.0f;
@@ -1631,10 +1706,10 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     __syncthreads();
     // session.rs:112-118 with add_engram (session.rs:175-188)
     if (p.key != nullptr) {
-        n3_unit_rms(xs_, d, a_, red);
+        n3_unit_rms(xs_, d, a_, red, cv_);
         if (tid < d) sc_[tid] = key_r[0];
         __syncthreads();
-        n3_unit_rms(sc_, d, sc_, red);
+        n3_unit_rms(sc_, d, sc_, red, cv_);
         if (tid == 0) {  // Iterator::sum: in order from -0.0
             const float dot = n3_fold<false>(-0.0f, a_, sc_, d, 1);
             alpha_s = libm_sigmoid(dot / sqrtf((float)d));
@@ -1646,7 +1721,7 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     }
     if (tid < d) mx_[tid] = norm_in_r[0];
     __syncthreads();
-    n3_norm(xs_, mx_, d, a_, red);
+    n3_norm(xs_, mx_, d, a_, red, cv_);
     n3_fake_quantise(a_, d, red);
     for (int i = d + tid; i < p.qpadded; i += blockDim.x) a_[i] = 0.0f;
     __syncthreads();
@@ -1757,6 +1832,12 @@ struct N3Head {
     rn_matrix* projection = nullptr;
 };
 
+// the bump allocator's state (arena_take)
+struct N3Arena {
+    char* cur = nullptr;
+    size_t left = 0;
+};
+
 struct rn_n3_model {
     rn_geometry g{};
     int output_vocab = 0;
@@ -1772,16 +1853,38 @@ struct rn_n3_model {
     std::vector<N3Head> heads;
     std::vector<int> active;
     std::vector<void*> allocations;
+    N3Arena arena;
     std::vector<rn_matrix*> matrices;
     bool fused = false;  // the three-kernel step applies (integer-path formats, sizes in range)
 };
 
 namespace {
 
+// A bump allocator over a few large device allocations, so that the many small
+// tensors of a model or a session share pages and address-translation entries
+// instead of taking one allocation each. Pieces are 256-byte aligned.
+int arena_take(std::vector<void*>& owned, N3Arena& a, size_t bytes, size_t chunk, void** out) {
+    bytes = (std::max<size_t>(bytes, 256) + 255) & ~(size_t)255;
+    if (bytes > a.left) {
+        const size_t size = std::max(chunk, bytes);
+        void* p = nullptr;
+        N3_HIP(hipMalloc(&p, size));
+        owned.push_back(p);
+        a.cur = static_cast<char*>(p);
+        a.left = size;
+    }
+    *out = a.cur;
+    a.cur += bytes;
+    a.left -= bytes;
+    return RN_OK;
+}
+
+constexpr size_t kN3ModelChunk = (size_t)8 << 20;
+constexpr size_t kN3SessionChunk = (size_t)32 << 20;
+
 int upload_floats(rn_n3_model* m, const std::vector<float>& v, float** out) {
     void* p = nullptr;
-    N3_HIP(hipMalloc(&p, std::max<size_t>(4, v.size() * sizeof(float))));
-    m->allocations.push_back(p);
+    N3_CALL(arena_take(m->allocations, m->arena, v.size() * sizeof(float), kN3ModelChunk, &p));
     if (!v.empty()) N3_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
     *out = (float*)p;
     return RN_OK;
@@ -1869,6 +1972,15 @@ int heads_per_order(const rn_geometry& g) { return (int)g.engram_tables / (g.eng
 
 bool integer_path(const rn_matrix* x) { return x->bits == 2 || x->bits == 4 || x->bits == 5; }
 
+// 16-byte loads a thread of n3_out_kernel for rows of `row_bytes` (64 rows,
+// 1024 threads), rounded up to a power of two
+int n3_out_loads(int row_bytes) {
+    const int need = (64 * (row_bytes / 16) + 1023) / 1024;
+    int l = 1;
+    while (l < need) l *= 2;
+    return l;
+}
+
 // The three-kernel step needs integer-path formats whose rows start where the
 // reference takes the panel form (2-bit rows on panels of four), at most four
 // lanes, and rows that fit its LDS tiles.
@@ -1878,9 +1990,11 @@ bool fused_applies(const rn_n3_model* m) {
     if (2 * L + L * L > kN3RouteRows || g.d_model > (uint32_t)kN3Hadamard) return false;
     if (g.qkv_conv_taps > (uint32_t)kN3MaxTaps) return false;
     if (m->phi_pre->cb.row_bytes > kN3RouteRowBytes || m->phi_pre->cb.padded / m->phi_pre->group > 64) return false;
-    if ((2 * L + L * L) * (m->phi_pre->cb.padded / m->phi_pre->group) > kN3Block ||
-        (2 * L + L * L) * (m->phi_pre->cb.row_bytes / 16) > 2 * kN3Block)
-        return false;
+    if ((2 * L + L * L) * (m->phi_pre->cb.padded / m->phi_pre->group) > kN3Block) return false;
+    // the layer boundary stages cond_v, the factors, its vectors, the stream and
+    // the routing rows in 16-byte units
+    if (m->phi_pre->cb.row_bytes % 16 != 0) return false;
+    auto aligned = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     const rn_matrix* phis[3] = {m->phi_pre, m->phi_post, m->phi_res};
     for (const rn_matrix* x : phis) {
         if (!integer_path(x) || x->cb.padded > kN3MaxWidth || x->group != m->phi_pre->group ||
@@ -1888,12 +2002,19 @@ bool fused_applies(const rn_n3_model* m) {
             return false;
         if (x->bits == 2 && L % 4 != 0) return false;
     }
+    for (const rn_matrix* x : phis)
+        if (!aligned(x->cb.packed)) return false;
     for (const N3Layer& y : m->layers) {
+        if (y.qkvg == nullptr) return false;
+        for (int f = 0; f < 6; ++f)
+            if (!aligned(y.factors[f])) return false;
+        if (y.rank == 8 && !aligned(y.cond_v)) return false;
+        if (!aligned(y.out->cb.packed) || !aligned(y.out->cb.norms) || !aligned(y.qkvg->cb.packed)) return false;
         if (y.qkvg == nullptr || !integer_path(y.qkvg) || y.qkvg->cb.padded > kN3Hadamard ||
             y.qkvg->cb.row_bytes > kN3HeadRowBytes)
             return false;
         if (!integer_path(y.out) || y.out->cb.padded > kN3MaxWidth || y.out->cb.row_bytes > kN3OutRowBytes ||
-            y.out->cb.padded / y.out->group > 64)
+            y.out->cb.padded / y.out->group > 64 || y.out->cb.row_bytes % 16 != 0)
             return false;
     }
     return true;
@@ -2025,8 +2146,7 @@ int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out) {
                 N3_REQUIRE(perm[i] >= 0 && perm[i] < kN3Hadamard, "permutation %d entry out of range", p);
             }
             void* dp = nullptr;
-            N3_HIP(hipMalloc(&dp, perm.size() * 4));
-            m->allocations.push_back(dp);
+            N3_CALL(arena_take(m->allocations, m->arena, perm.size() * 4, kN3ModelChunk, &dp));
             N3_HIP(hipMemcpy(dp, perm.data(), perm.size() * 4, hipMemcpyHostToDevice));
             m->perm[p] = (int32_t*)dp;
         }
@@ -2147,6 +2267,7 @@ struct rn_n3_session {
     std::vector<N3CacheDev> caches;
     std::vector<float*> rings, ekey, evalue;
     std::vector<void*> allocations;
+    N3Arena arena;
     float *stream_a = nullptr, *stream_b = nullptr, *input = nullptr, *post = nullptr, *residual = nullptr;
     float *x = nullptr, *rotated = nullptr, *prod = nullptr, *attended = nullptr;
     void* codes = nullptr;         // the projections' input codes (int4 a run of 16)
@@ -2165,8 +2286,7 @@ namespace {
 
 int alloc(rn_n3_session* s, size_t bytes, void** out) {
     void* p = nullptr;
-    N3_HIP(hipMalloc(&p, std::max<size_t>(bytes, 256)));
-    s->allocations.push_back(p);
+    N3_CALL(arena_take(s->allocations, s->arena, bytes, kN3SessionChunk, &p));
     N3_HIP(hipMemsetAsync(p, 0, std::max<size_t>(bytes, 256), s->stream));
     *out = p;
     return RN_OK;
@@ -2504,7 +2624,12 @@ int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
         rn_launch(n3_attention_kernel, dim3(H), dim3(kN3AttendThreads), 0, st, ap);
         N3_HIP(hipGetLastError());
         N3OutParams op{y.out->cb, s->attended, qw, s->attn_out};
-        rn_launch(n3_out_kernel, dim3((unsigned)((y.out->rows + 63) / 64)), dim3(256), 0, st, op);
+        const dim3 out_grid((unsigned)((y.out->rows + 63) / 64));
+        switch (n3_out_loads(y.out->cb.row_bytes)) {
+            case 1: rn_launch(n3_out_kernel<1>, out_grid, dim3(1024), 0, st, op); break;
+            case 2: rn_launch(n3_out_kernel<2>, out_grid, dim3(1024), 0, st, op); break;
+            default: rn_launch(n3_out_kernel<4>, out_grid, dim3(1024), 0, st, op); break;
+        }
         N3_HIP(hipGetLastError());
         N3BoundaryParams b{};
         b.tail = 1;
