@@ -151,6 +151,15 @@ __device__ void n3_norm(const float* x, const float* gain, int n, float* out, fl
     __syncthreads();
 }
 
+// n3_norm for n <= blockDim.x with thread i's gain in a register
+__device__ void n3_norm_gain(const float* x, float gain, int n, float* out, float* red, float* sq) {
+    const float mean_square = n3_sum_of_squares(x, n, red, sq) / (float)n;
+    const float inverse = 1.0f / sqrtf(mean_square + 1e-6f);
+    const int i = threadIdx.x;
+    if (i < n) out[i] = ((1.0f + gain) * x[i]) * inverse;
+    __syncthreads();
+}
+
 // ops.rs:60-66
 __device__ void n3_unit_rms(const float* x, int n, float* out, float* red, float* sq = nullptr) {
     const float inverse = 1.0f / sqrtf(n3_sum_of_squares(x, n, red, sq) / (float)n + 1e-6f);
@@ -158,16 +167,21 @@ __device__ void n3_unit_rms(const float* x, int n, float* out, float* red, float
     __syncthreads();
 }
 
-// ops.rs:120-125 in place over LDS
+// ops.rs:120-125 in place over LDS; the quotient v / scale without a division
+// (quotients<1>: the same rounding), NaN kept as the reference keeps it
 __device__ void n3_fake_quantise(float* v, int n, float* red) {
     float peak = 0.0f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) peak = fmaxf(peak, fabsf(v[i]));
     peak = n3_block_max(peak, red);
-    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float q = __builtin_rintf(v[i] / scale);
+    const float scale = int8_scale_from_peak(peak);
+    for (int base = 0; base < n; base += blockDim.x) {
+        const int i = base + threadIdx.x;
+        const float x = v[min(i, n - 1)];
+        float y;
+        quotients<1>(&x, scale, &y);
+        float q = __builtin_rintf(y);
         q = q < -128.0f ? -128.0f : (q > 127.0f ? 127.0f : q);
-        v[i] = q * scale;
+        if (i < n) v[i] = q * scale;
     }
     __syncthreads();
 }
@@ -215,39 +229,6 @@ __device__ void n3_copy(float* dst, const float* src, int n) {
             const int i = base + j * blockDim.x + threadIdx.x;
             if (i < n) dst[i] = t[j];
         }
-    }
-}
-
-// One region of a staging pass: `count` 16-byte units from global `src` to
-// LDS `dst` (count 0: nothing, src may be null).
-struct N3Span {
-    const void* src;
-    void* dst;
-    int count;
-};
-
-typedef __attribute__((address_space(3))) void n3_lds_void;
-typedef __attribute__((address_space(1))) void n3_global_void;
-
-// Everything a block stages, in one pass that holds no registers: the regions'
-// 16-byte units go global -> LDS by global_load_lds_dwordx4 (lane l of a wave
-// lands at the wave's LDS base + 16 l), in chunks of 64 units dealt to the
-// waves in turn. The copies count on vmcnt: every wave waits for its own
-// (s_waitcnt) before the barrier that publishes them.
-template <int N>
-__device__ __forceinline__ void n3_stage(const N3Span (&s)[N]) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    int c0 = 0;  // the first chunk of region j
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-        const int count = s[j].count, chunks = (count + 63) / 64;
-        for (int c = c0 + (wave - c0 % waves + waves) % waves; c < c0 + chunks; c += waves) {
-            const int q = c - c0, unit = 64 * q + lane;
-            if (unit < count)
-                __builtin_amdgcn_global_load_lds((n3_global_void*)(reinterpret_cast<const int4*>(s[j].src) + unit),
-                                                 (n3_lds_void*)(reinterpret_cast<int4*>(s[j].dst) + 64 * q), 16, 0, 0);
-        }
-        c0 += chunks;
     }
 }
 
@@ -697,6 +678,7 @@ struct N3TailLds {
 // latency overlaps the work before the MLP.
 struct N3TailPre {
     float d1, d2, b2, d3, d4, cond_u[8];
+    float post_gain, pre_gain;  // element threadIdx.x of post_norm and pre_norm (0 past d)
     int perm1, perm2;
 };
 
@@ -710,6 +692,8 @@ __device__ N3TailPre n3_tail_prefetch(const N3BlockOutParams& p) {
     t.d4 = p.d4[tid];
     t.perm1 = p.perm1[tid];
     t.perm2 = p.perm2[tid];
+    t.post_gain = p.post_norm[min(tid, p.d - 1)];
+    t.pre_gain = p.pre_norm[min(tid, p.d - 1)];
 #pragma unroll
     for (int r = 0; r < 8; ++r) t.cond_u[r] = r < p.rank ? p.cond_u[(size_t)r * kN3Hadamard + tid] : 0.0f;
     return t;
@@ -720,24 +704,44 @@ __device__ N3TailPre n3_tail_prefetch(const N3BlockOutParams& p) {
 // combine and the next cell; the next stream also into `keep` (LDS) when set.
 // 1024 threads (the Hadamard size).
 __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* keep, const N3TailPre& pre,
-                        bool cv_staged = false) {
+                        bool staged = false) {
     float *xs = l.xs, *a = l.a, *sc = l.sc, *st = l.st, *mx = l.mx, *modulation = l.modulation;
     float *cv = l.cv, *weights = l.weights, *red = l.red;
     float(*chains)[8] = reinterpret_cast<float(*)[8]>(l.chains);
     const int tid = threadIdx.x, d = p.d;
-    n3_copy(a, p.attention, d);
-    n3_copy(xs, p.x, d);
-    if (p.rank == 8 && !cv_staged) n3_copy(cv, p.cond_v, d * 8);
+    if (staged) {  // attention, x and (rank 8) cond_v already in LDS: work on them in place
+        a = const_cast<float*>(p.attention);
+        xs = const_cast<float*>(p.x);
+    } else {
+        n3_copy(a, p.attention, d);
+        n3_copy(xs, p.x, d);
+        if (p.rank == 8) n3_copy(cv, p.cond_v, d * 8);
+        __syncthreads();
+    }
+    n3_norm_gain(a, pre.post_gain, d, a, red, st);
+    if (tid < d) xs[tid] = xs[tid] + p.gate * a[tid];
     __syncthreads();
-    n3_norm(a, p.post_norm, d, a, red, st);
-    for (int i = tid; i < d; i += blockDim.x) xs[i] = xs[i] + p.gate * a[i];
-    __syncthreads();
-    n3_norm(xs, p.pre_norm, d, a, red, st);  // a = pre
-    // condition weights (hadamard.rs:57-79)
+    n3_norm_gain(xs, pre.pre_gain, d, a, red, st);  // a = pre
+    // condition weights (hadamard.rs:57-79): the products value * factor by
+    // every thread (in place over cv), then the 32 chains (lane j of rank r:
+    // rows 4k + j in order) only add
     if (p.rank == 8) {
+        for (int e = tid; e < d * 8; e += blockDim.x) cv[e] = a[e >> 3] * cv[e];
+        __syncthreads();
         if (tid < 32) {
-            const int j = tid >> 3, r = tid & 7;
-            chains[j][r] = n3_fold<false>(0.0f, a + j, cv + j * 8 + r, (d - j + 3) / 4, 4, 32);
+            const int j = tid >> 3, r = tid & 7, n = (d - j + 3) / 4;
+            const float* q = cv + j * 8 + r;
+            float sum = 0.0f;
+            int k = 0;
+            for (; k + 16 <= n; k += 16) {
+                float t[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) t[u] = q[(k + u) * 32];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) sum = sum + t[u];
+            }
+            for (; k < n; ++k) sum = sum + q[k * 32];
+            chains[j][r] = sum;
         }
         __syncthreads();
         if (tid < 8) weights[tid] = (((0.0f + chains[0][tid]) + chains[1][tid]) + chains[2][tid]) + chains[3][tid];
@@ -963,50 +967,64 @@ __device__ __forceinline__ int4 n3_pack_codes(const int (&c)[16], int ib) {
 }
 
 // prepare and the per-group codes in one pass (matrix.rs:123-128 then
-// panel.rs:52-66): lane u holds run u (16 elements of v [P], zero past the
-// columns), runs the group's Walsh-Hadamard butterflies (spans 1..8 in the
-// lane, then 16 .. group / 2 with the partner lane u ^ (span / 16); low a + b,
-// high a - b; walsh.rs:41-76), scales, then quantises with the group's peak.
-// Codes to xq (plane order) and scales to xs, LDS or global.
-__device__ void n3_prepare_codes(const float* v, int P, int group, float wht_scale, int ib, int4* xq, float* xs) {
-    const int runs = P / 16, rpg = group / 16;
-    for (int base = 0; base < runs; base += blockDim.x) {
-        const int u = base + threadIdx.x;
-        const bool valid = u < runs;
-        float x[16];
+// panel.rs:52-66) over v [P] in LDS (zero past the columns), four lanes per
+// run of 16 (groups of at most 256): lane L holds elements 4L .. 4L + 3 of v;
+// the Walsh-Hadamard butterflies (walsh.rs:41-76) of spans 1 and 2 in the lane, spans
+// 4 .. group / 2 with the partner lane L ^ (span / 4) (low a + b, high a - b),
+// scales, the group's peak over its group / 4 lanes, quotients without a
+// division (quotients<4>: the codes of quantise_one), then the run's four
+// lanes (a quad) exchange their codes by DPP broadcasts so that lane d of the
+// run writes dword d of its plane-order int4.
+__device__ __forceinline__ void n3_prepare_codes(const float* v, int P, int group, float wht_scale, int ib, int4* xq, float* xs) {
+    const int lanes = P / 4, lpg = group / 4;
+    int* xqw = reinterpret_cast<int*>(xq);
+    for (int base = 0; base < lanes; base += blockDim.x) {
+        const int L = base + threadIdx.x;
+        const bool valid = L < lanes;
+        const float4 t = reinterpret_cast<const float4*>(v)[valid ? L : 0];
+        float x[4] = {t.x, t.y, t.z, t.w};
+        float a0 = x[0], b0 = x[1], a1 = x[2], b1 = x[3];
+        x[0] = a0 + b0;
+        x[1] = a0 - b0;
+        x[2] = a1 + b1;
+        x[3] = a1 - b1;
+        a0 = x[0], b0 = x[2], a1 = x[1], b1 = x[3];
+        x[0] = a0 + b0;
+        x[2] = a0 - b0;
+        x[1] = a1 + b1;
+        x[3] = a1 - b1;
+        for (int m = 1; m < lpg; m <<= 1) {
+            const bool high = (L & m) != 0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) x[i] = valid ? v[16 * u + i] : 0.0f;
-#pragma unroll
-        for (int span = 1; span < 16; span *= 2)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-                if ((i & span) == 0) {
-                    const float a = x[i], b = x[i + span];
-                    x[i] = a + b;
-                    x[i + span] = a - b;
-                }
-        for (int m = 1; m < rpg; m <<= 1) {
-            const bool high = (u & m) != 0;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float q = __shfl_xor(x[i], m, 64);
-                x[i] = high ? q - x[i] : x[i] + q;
+            for (int e = 0; e < 4; ++e) {
+                const float q = __shfl_xor(x[e], m, 64);
+                x[e] = high ? q - x[e] : x[e] + q;
             }
         }
         float peak = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            x[i] = x[i] * wht_scale;
-            peak = fmaxf(peak, fabsf(x[i]));
+        for (int e = 0; e < 4; ++e) {
+            x[e] = x[e] * wht_scale;
+            peak = fmaxf(peak, fabsf(x[e]));
         }
-        for (int m = 1; m < rpg; m <<= 1) peak = fmaxf(peak, __shfl_xor(peak, m, 64));
-        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-        int c[16];
+        for (int m = 1; m < lpg; m <<= 1) peak = fmaxf(peak, __shfl_xor(peak, m, 64));
+        const float scale = int8_scale_from_peak(peak);
+        float y[4];
+        quotients<4>(x, scale, y);
+        const int w = n3_b4(code_of_quotient(y[0]), code_of_quotient(y[1]), code_of_quotient(y[2]),
+                            code_of_quotient(y[3]));
+        const int w0 = dpp_move<0x00>(w), w1 = dpp_move<0x55>(w), w2 = dpp_move<0xaa>(w), w3 = dpp_move<0xff>(w);
+        const int d = L & 3;
+        int out = 0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) c[i] = quantise_one(x[i], scale);
+        for (int j = 0; j < 4; ++j) {
+            const int e = ib == 2 ? 4 * j + d : 8 * (d >> 1) + 2 * j + (d & 1);
+            const int src = e >> 2, ws = src == 0 ? w0 : src == 1 ? w1 : src == 2 ? w2 : w3;
+            out |= ((ws >> (8 * (e & 3))) & 0xff) << (8 * j);
+        }
         if (valid) {
-            xq[u] = n3_pack_codes(c, ib);
-            if ((u & (rpg - 1)) == 0) xs[u / rpg] = scale;
+            xqw[L] = out;
+            if ((L & (lpg - 1)) == 0) xs[L / lpg] = scale;
         }
     }
 }
@@ -1086,6 +1104,8 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     const int runs = c.padded / 16, rpg = c.group / 16, G = c.padded / c.group;
     const int rpg_shift = rpg == 4 ? 2 : (rpg == 8 ? 3 : 4);
+    // rows a wave takes at a time: four, or fewer when the rows do not fill the waves
+    const int kr = min(4, (R + waves - 1) / waves);
     const uint32_t lut[4] = {c.lut[0], c.lut[1], c.lut[2], c.lut[3]};
     for (int u0 = 0; u0 < runs; u0 += 64) {
         const int u = u0 + lane;
@@ -1093,17 +1113,18 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
         const int4 x = live ? xq[u] : make_int4(0, 0, 0, 0);
         const uint8_t* base = w + (size_t)(live ? u : 0) * 2 * IB;
         const bool leader = live && (u & (rpg - 1)) == 0;
-        for (int r0 = wave; r0 < R; r0 += 4 * waves) {
-            // the four rows' words first (rows past R repeat the last; a lane past
+        for (int r0 = wave; r0 < R; r0 += kr * waves) {
+            // the kr rows' words first (rows past R repeat the last; a lane past
             // the runs has zero codes, so its sums are zero), then the sums
             int sum[4];
             if constexpr (IB == 2) {
                 uint32_t wd[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    wd[k] = *reinterpret_cast<const uint32_t*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
+                    if (k < kr) wd[k] = *reinterpret_cast<const uint32_t*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
+                    if (k >= kr) break;
                     int sm = dot4(n3_decode4<2>(wd[k] & 0x03030303u, lut), x.x, 0);
                     sm = dot4(n3_decode4<2>((wd[k] >> 2) & 0x03030303u, lut), x.y, sm);
                     sm = dot4(n3_decode4<2>((wd[k] >> 4) & 0x03030303u, lut), x.z, sm);
@@ -1113,9 +1134,10 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
                 uint2 wd[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    wd[k] = *reinterpret_cast<const uint2*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
+                    if (k < kr) wd[k] = *reinterpret_cast<const uint2*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
+                    if (k >= kr) break;
                     int sm = dot4(n3_decode4<4>(wd[k].x & 0x0f0f0f0fu, lut), x.x, 0);
                     sm = dot4(n3_decode4<4>((wd[k].x >> 4) & 0x0f0f0f0fu, lut), x.y, sm);
                     sm = dot4(n3_decode4<4>(wd[k].y & 0x0f0f0f0fu, lut), x.z, sm);
@@ -1124,6 +1146,7 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
+                if (k >= kr) break;
                 int v = sum[k];
                 v = v + dpp_move<0xb1>(v);
                 v = v + dpp_move<0x4e>(v);
@@ -1504,6 +1527,7 @@ struct N3BoundaryParams {
     float qscale;
     int4* codes;          // [qpadded / 16] the projections' input, prepared and quantised
     float* code_scales;   // [qpadded / qgroup]
+    const uint8_t* phi_rows;  // the route layer's rows of phi_pre, phi_post, phi_res, one after another
     int d, lanes;
 };
 
@@ -1516,17 +1540,16 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     __shared__ float chains_[32];
     __shared__ float weights_[64];
     __shared__ float red[32];
-    __shared__ __align__(16) float cv_[kN3Hadamard * 8];
+    __shared__ __align__(16) float tailw_s[6 * kN3Hadamard + kN3Hadamard * 8];  // the six factors, then cond_v
     __shared__ __align__(16) float stream_s[kN3MaxWidth];
-    __shared__ float rv[kN3MaxWidth];
+    __shared__ __align__(16) float rv[kN3MaxWidth];
     __shared__ int4 rq[kN3MaxWidth / 16];
     __shared__ float rs[64];
     __shared__ int racc[kN3RouteRows * 64];
     __shared__ float ry[kN3RouteRows];
     __shared__ __align__(16) uint8_t pw[kN3RouteRows * kN3RouteRowBytes];
     __shared__ uint16_t pn[kN3RouteRows * 64];
-    __shared__ __align__(16) float factors_s[6][kN3Hadamard];
-    __shared__ __align__(16) float tin_s[3][kN3Hadamard];  // the tail's attention, x and input
+    __shared__ __align__(16) float tin_s[3 * kN3Hadamard];  // the tail's attention, x and input ([3][d])
     __shared__ float lane_s[2 * kMaxLanes + kMaxLanes * kMaxLanes];  // post, residual of the tail
     __shared__ float small_s[4 * kMaxLanes + 2 * 64];  // a_pre a_post a_res (one each), b_pre, b_post, b_res
     __shared__ float gate_s[kMaxLanes];
@@ -1538,26 +1561,33 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     N3BlockOutParams t = p.t;
     N3TailPre pre{};
     const bool cv_staged = p.tail && t.rank == 8;
+    float* const cv_ = tailw_s + 6 * kN3Hadamard;
+    // the inputs in four ranges, each loaded by waves of its own (at most 384
+    // 16-byte units a wave, six a lane, all requested before the first LDS
+    // store): the factors and cond_v, the projection output with x and the
+    // routed input, the stream, the route layer's rows
     {
-        const int tc = p.tail ? 1 : 0, rc = p.route ? 1 : 0;
-        const size_t rb = p.phi_pre.row_bytes;
-        const N3Span spans[14] = {
-            {t.cond_v, cv_, cv_staged ? d * 2 : 0},
-            {t.factors[0], factors_s[0], tc * kN3Hadamard / 4},
-            {t.factors[1], factors_s[1], tc * kN3Hadamard / 4},
-            {t.factors[2], factors_s[2], tc * kN3Hadamard / 4},
-            {t.factors[3], factors_s[3], tc * kN3Hadamard / 4},
-            {t.factors[4], factors_s[4], tc * kN3Hadamard / 4},
-            {t.factors[5], factors_s[5], tc * kN3Hadamard / 4},
-            {t.attention, tin_s[0], tc * d / 4},
-            {t.x, tin_s[1], tc * d / 4},
-            {t.input, tin_s[2], tc * d / 4},
-            {p.tail ? t.stream : p.stream, stream_s, S / 4},
-            {p.phi_pre.packed + (size_t)layer * L * rb, pw, rc * L * chunks},
-            {p.phi_post.packed + (size_t)layer * L * rb, pw + (size_t)L * rb, rc * L * chunks},
-            {p.phi_res.packed + (size_t)layer * L * L * rb, pw + (size_t)2 * L * rb, rc * L * L * chunks},
-        };
-        n3_stage(spans);
+        const int u0 = p.tail ? (6 * kN3Hadamard + (cv_staged ? 8 * d : 0)) / 4 : 0, u1 = p.tail ? 3 * d / 4 : 0;
+        const int u2 = S / 4, u3 = p.route ? route_rows * chunks : 0;
+        const int n0 = (u0 + 383) / 384, n1 = (u1 + 383) / 384, n2 = (u2 + 383) / 384, n3 = (u3 + 383) / 384;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+        const int j = wave < n0 ? 0 : wave < n0 + n1 ? 1 : wave < n0 + n1 + n2 ? 2 : wave < n0 + n1 + n2 + n3 ? 3 : 4;
+        if (j < 4) {
+            const int w0 = j == 0 ? 0 : j == 1 ? n0 : j == 2 ? n0 + n1 : n0 + n1 + n2;
+            const int nw = j == 0 ? n0 : j == 1 ? n1 : j == 2 ? n2 : n3, cnt = j == 0 ? u0 : j == 1 ? u1 : j == 2 ? u2 : u3;
+            const int4* src = reinterpret_cast<const int4*>(
+                j == 0 ? (const void*)t.factors[0]
+                       : j == 1 ? (const void*)t.attention : j == 2 ? (const void*)(p.tail ? t.stream : p.stream) : (const void*)p.phi_rows);
+            int4* dst = reinterpret_cast<int4*>(j == 0 ? (void*)tailw_s : j == 1 ? (void*)tin_s : j == 2 ? (void*)stream_s : (void*)pw);
+            int4 v[6];
+#pragma unroll
+            for (int k = 0; k < 6; ++k) v[k] = src[min((k * nw + wave - w0) * 64 + lane, cnt - 1)];
+#pragma unroll
+            for (int k = 0; k < 6; ++k) {
+                const int u = (k * nw + wave - w0) * 64 + lane;
+                if (u < cnt) dst[u] = v[k];
+            }
+        }
     }
     if (p.tail) pre = n3_tail_prefetch(t);
     // the layer's norms of phi_pre, phi_post and phi_res (rows one after another)
@@ -1584,20 +1614,19 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
         if (tid < L * L) lane_s[kMaxLanes + tid] = t.residual[tid];
     }
     if (p.route && tid < route_rows * G) pn[tid] = tn;
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's staged units are in LDS
     if (p.tail) {
         // the tail reads its copies
-        for (int f = 0; f < 6; ++f) t.factors[f] = factors_s[f];
-        t.attention = tin_s[0];
-        t.x = tin_s[1];
-        t.input = tin_s[2];
+        for (int f = 0; f < 6; ++f) t.factors[f] = tailw_s + f * kN3Hadamard;
+        t.attention = tin_s;
+        t.x = tin_s + d;
+        t.input = tin_s + 2 * d;
         t.stream = stream_s;
         t.post = lane_s;
         t.residual = lane_s + kMaxLanes;
     }
     __syncthreads();
     const N3TailLds l{xs_, a_, sc_, st_, mx_, mod_, cv_, chains_, weights_, red};
-    if (p.tail) n3_tail(t, l, rv, pre, cv_staged);  // the next stream into rv, then into stream_s
+    if (p.tail) n3_tail(t, l, rv, pre, true);  // the next stream into rv, then into stream_s
     if (p.tail) {
         for (int i = tid; i < S; i += blockDim.x) stream_s[i] = rv[i];
         __syncthreads();
@@ -1847,6 +1876,9 @@ struct rn_n3_model {
           *b_res = nullptr;
     std::vector<float> a_pre_h, a_post_h, a_res_h, b_pre_h, b_post_h, b_res_h;
     rn_matrix *phi_pre = nullptr, *phi_post = nullptr, *phi_res = nullptr;
+    // the fused step's routing rows by layer, [pre (lanes) | post (lanes) | res
+    // (lanes^2)] rows of phi_pre's row bytes each
+    uint8_t* phi_stack = nullptr;
     int32_t* perm[2] = {nullptr, nullptr};
     std::vector<N3Engram> engrams;
     float* final_norm = nullptr;
@@ -1972,6 +2004,23 @@ int heads_per_order(const rn_geometry& g) { return (int)g.engram_tables / (g.eng
 
 bool integer_path(const rn_matrix* x) { return x->bits == 2 || x->bits == 4 || x->bits == 5; }
 
+// phi_stack (device to device copies at open)
+int stack_routing_rows(rn_n3_model* m) {
+    const int L = (int)m->g.mhc_lanes, layers = (int)m->g.num_layers;
+    const size_t rb = m->phi_pre->cb.row_bytes, per = (size_t)(2 * L + L * L) * rb;
+    void* q = nullptr;
+    N3_CALL(arena_take(m->allocations, m->arena, per * layers, kN3ModelChunk, &q));
+    m->phi_stack = static_cast<uint8_t*>(q);
+    for (int l = 0; l < layers; ++l) {
+        uint8_t* dst = m->phi_stack + per * l;
+        N3_HIP(hipMemcpy(dst, m->phi_pre->cb.packed + (size_t)l * L * rb, L * rb, hipMemcpyDeviceToDevice));
+        N3_HIP(hipMemcpy(dst + L * rb, m->phi_post->cb.packed + (size_t)l * L * rb, L * rb, hipMemcpyDeviceToDevice));
+        N3_HIP(hipMemcpy(dst + 2 * L * rb, m->phi_res->cb.packed + (size_t)l * L * L * rb, (size_t)L * L * rb,
+                         hipMemcpyDeviceToDevice));
+    }
+    return RN_OK;
+}
+
 // 16-byte loads a thread of n3_out_kernel for rows of `row_bytes` (64 rows,
 // 1024 threads), rounded up to a power of two
 int n3_out_loads(int row_bytes) {
@@ -1990,10 +2039,16 @@ bool fused_applies(const rn_n3_model* m) {
     if (2 * L + L * L > kN3RouteRows || g.d_model > (uint32_t)kN3Hadamard) return false;
     if (g.qkv_conv_taps > (uint32_t)kN3MaxTaps) return false;
     if (m->phi_pre->cb.row_bytes > kN3RouteRowBytes || m->phi_pre->cb.padded / m->phi_pre->group > 64) return false;
+    // the input codes four lanes a run: groups of at most 256
+    if (m->phi_pre->group > 256) return false;
     if ((2 * L + L * L) * (m->phi_pre->cb.padded / m->phi_pre->group) > kN3Block) return false;
-    // the layer boundary stages cond_v, the factors, its vectors, the stream and
-    // the routing rows in 16-byte units
+    // the layer boundary stages the factors and cond_v, three vectors, the
+    // stream and the routing rows in 16-byte units, at most 384 a wave
+    const int d = (int)g.d_model;
     if (m->phi_pre->cb.row_bytes % 16 != 0) return false;
+    const int waves = (6 * kN3Hadamard + 8 * d + 1535) / 1536 + (3 * d + 1535) / 1536 + (L * d + 1535) / 1536 +
+                      ((2 * L + L * L) * (int)(m->phi_pre->cb.row_bytes / 16) + 383) / 384;
+    if (waves > kN3Block / 64) return false;
     auto aligned = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     const rn_matrix* phis[3] = {m->phi_pre, m->phi_post, m->phi_res};
     for (const rn_matrix* x : phis) {
@@ -2010,6 +2065,7 @@ bool fused_applies(const rn_n3_model* m) {
             if (!aligned(y.factors[f])) return false;
         if (y.rank == 8 && !aligned(y.cond_v)) return false;
         if (!aligned(y.out->cb.packed) || !aligned(y.out->cb.norms) || !aligned(y.qkvg->cb.packed)) return false;
+        if (y.qkvg->group > 256 || y.out->group > 256) return false;
         if (y.qkvg == nullptr || !integer_path(y.qkvg) || y.qkvg->cb.padded > kN3Hadamard ||
             y.qkvg->cb.row_bytes > kN3HeadRowBytes)
             return false;
@@ -2096,16 +2152,24 @@ int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out) {
             N3_CALL(device_floats(m, archive, w.take(), &y.pre_norm, d));
             float** diag[5] = {&y.d1, &y.d2, &y.b2, &y.d3, &y.d4};
             for (int i = 0; i < 5; ++i) N3_CALL(device_floats(m, archive, w.take(), diag[i], kN3Hadamard));
+            // the six factors and cond_v in one allocation, [w1a .. w3b | cond_v]:
+            // the layer boundary stages them as one range
+            std::vector<float> tail;
             for (int f = 0; f < 6; ++f) {
                 std::vector<float> v;
                 const int idx = w.take();
                 N3_CALL(host_floats(archive, idx, v));
                 N3_REQUIRE(v.size() == 1024, "Hadamard factors must be 32 x 32 (layer %d factor %d)", l, f);
-                N3_CALL(upload_floats(m, v, &y.factors[f]));
+                tail.insert(tail.end(), v.begin(), v.end());
             }
             std::vector<float> cu;
             std::vector<float> cv;
-            N3_CALL(device_floats(m, archive, w.take(), &y.cond_v, -1, &cv));
+            N3_CALL(host_floats(archive, w.take(), cv));
+            tail.insert(tail.end(), cv.begin(), cv.end());
+            float* tail_dev = nullptr;
+            N3_CALL(upload_floats(m, tail, &tail_dev));
+            for (int f = 0; f < 6; ++f) y.factors[f] = tail_dev + (size_t)f * kN3Hadamard;
+            y.cond_v = tail_dev + (size_t)6 * kN3Hadamard;
             N3_CALL(device_floats(m, archive, w.take(), &y.cond_u, -1, &cu));
             y.rank = (int)(cu.size() / kN3Hadamard);  // hadamard.rs:39
             N3_REQUIRE(y.rank >= 1 && y.rank <= 64 && cu.size() == (size_t)y.rank * kN3Hadamard &&
@@ -2228,6 +2292,7 @@ int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out) {
         }
         if (w.failed) return n3_fail(RN_ERR_ARGUMENT, "directory ends inside the probe heads");
         m->fused = fused_applies(m);
+        if (m->fused) N3_CALL(stack_routing_rows(m));
         N3_REQUIRE(w.next == w.end, "%d tensors follow the heads (an audio encoder is not part of this model)",
                    w.end - w.next);
         return RN_OK;
@@ -2389,10 +2454,8 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
         widest = std::max(widest, m->embedding->cb.padded);
         N3_CALL(alloc_n(s, (size_t)lanes * d, &s->stream_a));
         N3_CALL(alloc_n(s, (size_t)lanes * d, &s->stream_b));
-        N3_CALL(alloc_n(s, (size_t)d, &s->input));
         N3_CALL(alloc_n(s, 64, &s->post));
         N3_CALL(alloc_n(s, 256, &s->residual));
-        N3_CALL(alloc_n(s, (size_t)d, &s->x));
         N3_CALL(alloc_n(s, (size_t)widest, &s->rotated));
         N3_CALL(alloc_n(s, (size_t)qkv + H * 64, &s->prod));
         N3_CALL(alloc_n(s, (size_t)H * 64, &s->attended));
@@ -2401,7 +2464,11 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
         N3_CALL(alloc_n(s, 64, &s->next_dev));
         N3_CALL(alloc_n(s, (size_t)capacity, &s->ids_dev));
         N3_CALL(alloc_n(s, 64, &s->code_scales));
-        N3_CALL(alloc_n(s, (size_t)d, &s->attn_out));
+        // the output projection, x and the routed input one after another: the
+        // layer boundary stages them as one range
+        N3_CALL(alloc_n(s, (size_t)3 * d, &s->attn_out));
+        s->x = s->attn_out + d;
+        s->input = s->attn_out + 2 * (size_t)d;
         N3_CALL(alloc_n(s, (size_t)kN3MaxWidth, &s->gathered));
         N3_CALL(alloc_n(s, (size_t)d, &s->eraw));
         N3_CALL(alloc_n(s, (size_t)H, &s->qscales));
@@ -2583,6 +2650,7 @@ int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
         b.qscale = y.qkvg->cb.wht_scale;
         b.codes = reinterpret_cast<int4*>(s->codes);
         b.code_scales = s->code_scales;
+        b.phi_rows = m->phi_stack + (size_t)layer * (2 * lanes + lanes * lanes) * m->phi_pre->cb.row_bytes;
     };
     {
         N3BoundaryParams b{};
