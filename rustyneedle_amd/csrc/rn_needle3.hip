@@ -186,6 +186,9 @@ __device__ void n3_fake_quantise(float* v, int n, float* red) {
     __syncthreads();
 }
 
+typedef __attribute__((address_space(3))) void n3_lds_void;
+typedef __attribute__((address_space(1))) void n3_global_void;
+
 // the level index of element e of a packed row (LSB first; 3-bit indices may
 // straddle two bytes)
 __device__ __forceinline__ int n3_index(const uint8_t* row, int e, int ib) {
@@ -1210,6 +1213,7 @@ struct N3AttentionParams {
 };
 
 constexpr int kN3AttendThreads = 1024;
+constexpr int kN3StagedPositions = 1024;  // earlier positions whose keys and values the attention block holds
 constexpr int kN3HeadRowBytes = 256;  // the head's 256 staged rows, each at most 256 bytes (2-bit, 1024 columns)
 constexpr int kN3MaxTaps = 4;
 
@@ -1267,37 +1271,36 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     const int width = which == 0 ? qw : kw, off = which == 0 ? 0 : (which == 1 ? qw : qw + kw);
     const int col = head * kN3Head + lane;
     const int ntap = min(p.ntaps, p.position + 1);
+    const float* const tap = which == 0 ? p.taps[0] : which == 1 ? p.taps[1] : p.taps[2];
     float gains[kN3MaxTaps], samples[kN3MaxTaps];
 #pragma unroll
     for (int t = 0; t < kN3MaxTaps; ++t) {
-        gains[t] = (wave < 3 && t < ntap) ? p.taps[which][(size_t)t * width + col] : 0.0f;
+        gains[t] = (wave < 3 && t < ntap) ? tap[(size_t)t * width + col] : 0.0f;
         samples[t] = (wave < 3 && t >= 1 && t < ntap)
                          ? p.hist[(size_t)((p.position - t) % p.ntaps) * width_all + off + col]
                          : 0.0f;
     }
     const float gain = wave < 2 ? (which == 0 ? p.q_norm : p.k_norm)[lane] : 0.0f;
     const float cs = p.cos_row[lane & 31], sn = p.sin_row[lane & 31];
-    // the earlier positions' keys (thread: position tid) and values (thread:
-    // dims 4 dg .. 4 dg + 3 of positions pc + 64 j)
+    // the first 1024 earlier positions' keys and values as 16-byte units (unit u
+    // = 1024 k + tid: quarter u % 4 of position u / 4, so a wave's request is 1
+    // KB in a row and a position's four quarters sit on one quad), and each
+    // unit's key scale; thread t's value scale of position t. A unit past the
+    // earlier positions reads the last of them, or the new position's row when
+    // there is none, and is not used. Later positions are read from memory as
+    // they are needed.
     const int8_t* kbase = p.keys + ((size_t)kvh * p.cap + p.first) * kN3Head;
     const int8_t* vbase = p.values + ((size_t)kvh * p.cap + p.first) * kN3Head;
     const float* ks = p.key_scales + (size_t)kvh * p.cap + p.first;
     const float* vsc = p.value_scales + (size_t)kvh * p.cap + p.first;
-    // (a thread past the earlier positions reads the last of them, or the new
-    // position's row when there is none, and does not use it)
-    const int kp = min(tid, max(last - 1, 0));
-    int4 kr[4];
+    const int early = min(last, kN3StagedPositions), clampp = max(last - 1, 0);
+    int4 ku[4];
+    float ksr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kr[i] = reinterpret_cast<const int4*>(kbase + (size_t)kp * kN3Head)[i];
-    const float kscale = ks[kp];
-    const int dg = tid & 15, pc = tid >> 4;
-    int vr[16];
-    float vsr[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int vp = min(pc + 64 * j, max(last - 1, 0));  // used only below last
-        vr[j] = *reinterpret_cast<const int*>(vbase + (size_t)vp * kN3Head + 4 * dg);
-        vsr[j] = vsc[vp];
+    for (int k = 0; k < 4; ++k) {
+        const int u = k * kN3AttendThreads + tid, pos = min(u >> 2, clampp);
+        ku[k] = reinterpret_cast<const int4*>(kbase + (size_t)pos * kN3Head)[u & 3];
+        ksr[k] = ks[pos];
     }
     // ---- the head's projection rows
 #pragma unroll
@@ -1310,6 +1313,19 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     if (tid < G) xs[tid] = code_scale;
     __syncthreads();
     n3_rows(p.qkvg, w_s, nm_s, 256, xq, xs, acc, y_s);
+    // the rows are done: the values of the staged positions are requested now
+    // (they arrive during the next phases; w_s then takes them, [position][64],
+    // and nm_s their scales)
+    int8_t* const val_s = reinterpret_cast<int8_t*>(w_s);
+    float* const vsc_s = reinterpret_cast<float*>(nm_s);
+    {  // global_load_lds: wave w copies 1 KB chunks w, w + 16, ... (lane l: unit 64 c + l)
+        const int units = 4 * early, wv = __builtin_amdgcn_readfirstlane(wave);
+        for (int c = wv; c < (units + 63) / 64; c += kN3AttendThreads / 64)
+            if (64 * c + lane < units)
+                __builtin_amdgcn_global_load_lds((n3_global_void*)(vbase + (size_t)(64 * c + lane) * 16),
+                                                 (n3_lds_void*)(val_s + (size_t)c * 1024), 16, 0, 0);
+    }
+    const float vsr = vsc[min(tid, clampp)];
     // ---- conv taps, norms, rotary, codes (attention.rs:110-141)
     float v = 0.0f;
     if (wave < 3) {
@@ -1365,21 +1381,30 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     __syncthreads();
     // ---- kernels/src/attention.rs:53-80 (as n3_attend_kernel)
     const float query_scale = scale_s[0] * (1.0f / sqrtf((float)kN3Head));
-    int4 q[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) q[i] = reinterpret_cast<const int4*>(qc_s)[i];
     float peak = -INFINITY;
-    for (int pp = tid; pp < count; pp += kN3AttendThreads) {
+    {  // the staged positions: a quad a position, each lane one quarter's dot
+        const int4 qq = reinterpret_cast<const int4*>(qc_s)[tid & 3];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int u = k * kN3AttendThreads + tid, pos = u >> 2;
+            int sc = dot16(qq, ku[k], 0);
+            sc = sc + dpp_move<0xb1>(sc);
+            sc = sc + dpp_move<0x4e>(sc);
+            if (pos < early) {
+                const float c = ((float)sc * ksr[k]) * query_scale;
+                if ((u & 3) == 0) c_s[pos] = c;
+                peak = fmaxf(peak, c);
+            }
+        }
+    }
+    // the new position, and earlier positions past the staged ones
+    for (int pp = early + tid; pp < count; pp += kN3AttendThreads) {
         int4 k[4];
         float kscl;
         if (pp == last) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) k[i] = reinterpret_cast<const int4*>(kc_s)[i];
             kscl = scale_s[1];
-        } else if (pp == tid) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) k[i] = kr[i];
-            kscl = kscale;
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) k[i] = reinterpret_cast<const int4*>(kbase + (size_t)pp * kN3Head)[i];
@@ -1387,19 +1412,39 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         }
         int score = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) score = dot16(q[i], k[i], score);
+        for (int i = 0; i < 4; ++i) score = dot16(reinterpret_cast<const int4*>(qc_s)[i], k[i], score);
         const float c = ((float)score * kscl) * query_scale;
         c_s[pp] = c;
         peak = fmaxf(peak, c);
     }
     peak = n3_block_max(peak, red);
+    // (a thread's first position is its own: its value scale is in vsr)
+    auto value_scale = [&](int pp) {
+        return pp == last ? scale_s[2] : pp == tid ? vsr : pp < early ? vsc_s[pp] : vsc[pp];
+    };
     float cpeak = 0.0f;
     for (int pp = tid; pp < count; pp += kN3AttendThreads) {
         const float e = fast_exp(c_s[pp] - peak);
         c_s[pp] = e;
-        cpeak = fmaxf(cpeak, fabsf(e * (pp == last ? scale_s[2] : vsc[pp])));
+        cpeak = fmaxf(cpeak, fabsf(e * value_scale(pp)));
     }
+    if (tid < early) vsc_s[tid] = vsr;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's value chunks are in LDS (published by the barriers below)
     cpeak = n3_block_max(cpeak, red);
+    // the coefficients round((e * value scale) / scale), once a position
+    // (quotients<1>: rounds as the division; in acc, free until the sums)
+    const float scale = cpeak / 2047.0f;
+    int* const wgt_s = acc;
+    const bool pre_w = count <= 64 * kN3Head;
+    if (pre_w && cpeak > 0.0f) {
+        for (int pp = tid; pp < count; pp += kN3AttendThreads) {
+            const float x = c_s[pp] * value_scale(pp);
+            float y;
+            quotients<1>(&x, scale, &y);
+            wgt_s[pp] = (int)__builtin_roundf(y);
+        }
+    }
+    __syncthreads();
     const int vector_count = count - count % 4;
     if (tid < 4) {
         float s = 0.0f;
@@ -1414,7 +1459,9 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         for (; pp < vector_count; pp += 4) s = s + c_s[pp];
         lanes_s[tid] = s;
     }
-    const float scale = cpeak / 2047.0f;
+    // the value sums: thread (dg, pc) takes dims 4 dg .. 4 dg + 3 of positions
+    // pc, pc + 64, ... (integer sums: any order)
+    const int dg = tid & 15, pc = tid >> 4;
     int av[4] = {0, 0, 0, 0};
     if (cpeak > 0.0f) {
         for (int pp0 = pc; pp0 < count; pp0 += 16 * 64) {
@@ -1422,24 +1469,16 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
             for (int j = 0; j < 16; ++j) {
                 const int pp = pp0 + 64 * j;
                 if (pp >= count) break;
-                int packed;
-                float sv;
-                if (pp == last) {
-                    packed = reinterpret_cast<const int*>(vc_s)[dg];
-                    sv = scale_s[2];
-                } else if (pp0 == pc) {
-                    packed = vr[j];
-                    sv = vsr[j];
-                } else {
-                    packed = *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head + 4 * dg);
-                    sv = vsc[pp];
-                }
-                const int wgt = (int)__builtin_roundf((c_s[pp] * sv) / scale);
+                const int packed = pp == last ? reinterpret_cast<const int*>(vc_s)[dg]
+                                   : pp < early ? reinterpret_cast<const int*>(val_s + (size_t)pp * kN3Head)[dg]
+                                                : *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head + 4 * dg);
+                const int wgt = pre_w ? wgt_s[pp] : (int)__builtin_roundf((c_s[pp] * value_scale(pp)) / scale);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) av[k] += wgt * (int)(int8_t)(packed >> (8 * k));
             }
         }
     }
+    __syncthreads();  // the coefficients are read: acc takes the sums
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc[pc * kN3Head + 4 * dg + k] = av[k];
     __syncthreads();
