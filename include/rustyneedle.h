@@ -227,10 +227,10 @@ int rn_lanes_create(int lanes, int width, int layers, const float* a_pre, const 
                     const rn_matrix* phi_post, const rn_matrix* phi_res, rn_lanes** out);
 int rn_lanes_free(rn_lanes* lanes);
 /* LaneWeights::route (lanes.rs:48-84) on device pointers: stream [lanes][width]
- * -> input [width], post [lanes], residual [lanes][lanes]. unit_rms,
- * fake_quantise_int8, prepare and the products follow the reference's order
- * bit for bit; the gates (sigmoid) and sinkhorn_in_place use the device expf
- * where the reference calls the host libm's. */
+ * -> input [width], post [lanes], residual [lanes][lanes], bit for bit:
+ * unit_rms, fake_quantise_int8, prepare and the products in the reference's
+ * order, the gates (sigmoid) and sinkhorn_in_place over the device restatement
+ * of the C library's expf (rn_libm_exp). */
 int rn_lanes_route(rn_lanes* lanes, int layer, int slot, const float* stream, float* input, float* post,
                    float* residual, void* stream_handle);
 /* LaneWeights::combine_into (lanes.rs:86-98): next [lanes][width]. */
