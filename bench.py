@@ -199,14 +199,23 @@ def bench_gemv(rn, rotations: int = 512):
     mr = rn.QuantisedMatrix(Wr, sWr)
     del Wr, sWr
     yr = rn.DeviceBuffer(4 * rows)
-    call_r = lambda: mr.multiply_vector(xd.ptr, yr.ptr, None, stream.handle)
-    for _ in range(3):
-        call_r()
-    rot_ms = time_events(rn, stream.handle, call_r, 20)
+    # the stream: `rotations` distinct 2048 x 512 matrices one after another in
+    # memory (609 MB, past the Infinity Cache), one launch of the kernel instance
+    # the single 2048 x 512 product runs (8 rows a block), then of the 32-row
+    # instance the library picks for a matrix this tall
+    def stream_ms(rows_per_block):
+        call = lambda: mr.multiply_vector_rows(xd.ptr, yr.ptr, rows_per_block, stream.handle)
+        for _ in range(3):
+            call()
+        return time_events(rn, stream.handle, call, 20)
+    rot_ms = stream_ms(8)
+    rot32_ms = stream_ms(32)
     achieved = GEMV_UNIT_BYTES * rotations / (rot_ms / 1e3) / 1e9
+    achieved32 = GEMV_UNIT_BYTES * rotations / (rot32_ms / 1e3) / 1e9
     return dict(single_us=single_ms * 1e3, single_gb_s=GEMV_UNIT_BYTES / (single_ms / 1e3) / 1e9,
                 rotations=rotations, rotating_ms=rot_ms, rotating_gb_s=achieved,
-                rotating_frac=achieved / HBM_PEAK_GBS)
+                rotating_frac=achieved / HBM_PEAK_GBS, rotating_kernel="gemv_kernel<512,8,quant,store,panel>",
+                rotating32_ms=rot32_ms, rotating32_gb_s=achieved32, rotating32_frac=achieved32 / HBM_PEAK_GBS)
 
 
 def codebook_bytes(rows: int, columns: int, group: int, bits: int) -> int:

@@ -87,6 +87,11 @@ int rn_matrix_shape(const rn_matrix* m, int* rows, int* columns, int* group);
  * y[rows] = W . quantise_int8(x[columns]). acc (nullable) receives the int32
  * accumulator of every (row, group): [rows][columns/group]. Device pointers. */
 int rn_matrix_multiply_vector(const rn_matrix* m, const float* x, float* y, int32_t* acc, void* stream);
+/* The same product (int8 matrices of 384 or 512 columns) with the kernel
+ * instance of `rows_per_block` output rows a block (8, 16 or 32) instead of the
+ * one rn_matrix_multiply_vector picks from the shape; the results are the same.
+ * For measurement: the instance a 2048-row product runs (8) over a tall matrix. */
+int rn_matrix_multiply_vector_rows(const rn_matrix* m, const float* x, float* y, int rows_per_block, void* stream);
 
 /* QuantisedMatrix::multiply_fused (matrix.rs:167-193): one launch over `count`
  * (<= 8) matrices of equal columns/group/form that share the input x. */

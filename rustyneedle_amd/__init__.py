@@ -140,6 +140,7 @@ SIGNATURES = {
     "rn_matrix_free": (_i, [_p]),
     "rn_matrix_shape": (_i, [_p, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i)]),
     "rn_matrix_multiply_vector": (_i, [_p, _p, _p, _p, _p]),
+    "rn_matrix_multiply_vector_rows": (_i, [_p, _p, _p, _i, _p]),
     "rn_matrix_multiply_fused": (_i, [C.POINTER(_p), _i, _p, C.POINTER(_p), _p]),
     "rn_matrix_multiply_batch": (_i, [_p, _p, _i, _p, _p, _p]),
     "rn_matrix_multiply_batch_noalloc": (_i, [_p, _p, _i, _p, _p, _p]),
@@ -371,6 +372,10 @@ class QuantisedMatrix:
 
     def multiply_vector(self, x_dev: int, y_dev: int, acc_dev: Optional[int] = None, stream=None) -> None:
         check(lib.rn_matrix_multiply_vector(self.handle, x_dev, y_dev, acc_dev, stream))
+
+    def multiply_vector_rows(self, x_dev: int, y_dev: int, rows_per_block: int, stream=None) -> None:
+        """The same product with the kernel instance of `rows_per_block` rows a block."""
+        check(lib.rn_matrix_multiply_vector_rows(self.handle, x_dev, y_dev, int(rows_per_block), stream))
 
     def multiply_vector_host(self, x: np.ndarray, with_acc: bool = False):
         x = np.ascontiguousarray(x, dtype=np.float32)

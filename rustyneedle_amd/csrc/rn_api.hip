@@ -430,6 +430,21 @@ int rn_matrix_multiply_vector(const rn_matrix* m, const float* x, float* y, int3
     return RN_OK;
 }
 
+int rn_matrix_multiply_vector_rows(const rn_matrix* m, const float* x, float* y, int rows_per_block, void* stream) {
+    RN_REQUIRE(m && x && y, "null argument");
+    RN_REQUIRE(m->bits == 0, "an int8 matrix (codebook matrices have their own kernels)");
+    RN_REQUIRE(rows_per_block == 8 || rows_per_block == 16 || rows_per_block == 32, "rows_per_block must be 8, 16 or 32");
+    RN_REQUIRE(m->columns == 512 || (m->columns == 384 && rows_per_block >= 8),
+               "columns must be 512 or 384 (got %d)", m->columns);
+    GemvParams p{};
+    const int blocks = (m->rows + rows_per_block - 1) / rows_per_block;
+    p.nseg = 1;
+    p.seg[0] = Segment{m->W, m->sW, y, nullptr, m->rows, 0};
+    p.x = x;
+    RN_HIP(launch_gemv(p, m->columns, kQuant, kStore, m->form, rows_per_block, blocks, (hipStream_t)stream));
+    return RN_OK;
+}
+
 int rn_matrix_multiply_fused(const rn_matrix* const* ms, int count, const float* x, float* const* ys, void* stream) {
     RN_REQUIRE(ms && x && ys, "null argument");
     RN_REQUIRE(count >= 1 && count <= kMaxSegments, "count must be 1..%d (got %d)", kMaxSegments, count);

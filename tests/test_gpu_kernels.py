@@ -80,6 +80,25 @@ def test_multiply_vector_bit_exact(rows, cols, form):
     assert np.array_equal(y.view(np.uint32), yo[0].view(np.uint32))
 
 
+@pytest.mark.parametrize("rows", [2048, 1000])
+@pytest.mark.parametrize("rows_per_block", [8, 16, 32])
+def test_multiply_vector_rows_instances(rows, rows_per_block):
+    """The product's 8-, 16- and 32-row kernel instances give the oracle's bits
+    (the 8-row one is the instance a 2048 x 512 product runs)."""
+    rng = np.random.default_rng(rows + rows_per_block)
+    W, sW = _matrix(rng, rows, 512)
+    x = rng.standard_normal(512).astype(np.float32)
+    m = rn.QuantisedMatrix(W, sW)
+    xd, yd = rn.DeviceBuffer.from_array(x), rn.DeviceBuffer(4 * rows)
+    m.multiply_vector_rows(xd.ptr, yd.ptr, rows_per_block)
+    rn.check(rn.lib.rn_stream_synchronize(None))
+    y = yd.download(np.float32, (rows,))
+    yo = oracle.multiply(0, W, sW, x)[0][0]
+    assert np.array_equal(y.view(np.uint32), yo.view(np.uint32))
+    with pytest.raises(rn.RnError):
+        m.multiply_vector_rows(xd.ptr, yd.ptr, 12)
+
+
 def test_multiply_vector_edge_inputs():
     rng = np.random.default_rng(5)
     W, sW = _matrix(rng, 256, 512)
