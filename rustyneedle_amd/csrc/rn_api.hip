@@ -1279,11 +1279,19 @@ int rn_lanes_create(int lanes, int width, int layers, const float* a_pre, const 
         RN_REQUIRE(phis[i]->rows >= need[i], "routing matrix %d has %d rows, %d needed", i, phis[i]->rows, need[i]);
         RN_REQUIRE(phis[i]->cb.padded == phi_pre->cb.padded && phis[i]->group == phi_pre->group,
                    "the routing matrices share padded columns and group (multiply_fused)");
+        // a layer's rows start at layer * lanes (layer * lanes^2): for 2-bit
+        // matrices the reference takes the integer panel path only from rows on
+        // panels of four (matrix.rs:404-409), the only path built here
+        RN_REQUIRE(phis[i]->bits != 2 || lanes % 4 == 0,
+                   "2-bit routing matrices need lanes a multiple of 4 (got %d): the reference takes the float path", lanes);
     }
     rn_lanes* l = new (std::nothrow) rn_lanes();
     if (!l) return fail(RN_ERR_MEMORY, "out of host memory");
-    const size_t nA = layers, nB = (size_t)layers * lanes, nR = (size_t)layers * lanes * lanes;
-    const size_t n = (size_t)lanes * width, padded = (size_t)phi_pre->cb.padded;
+    // every slice starts on a 256-byte boundary (the kernels read the stream and
+    // the rotated input as float4)
+    auto round64 = [](size_t v) { return (v + 63) / 64 * 64; };
+    const size_t nA = round64(layers), nB = round64((size_t)layers * lanes), nR = round64((size_t)layers * lanes * lanes);
+    const size_t n = round64((size_t)lanes * width), padded = round64((size_t)phi_pre->cb.padded);
     const size_t total = 3 * nA + 2 * nB + nR + n + padded + lanes;
     if (hipMalloc(&l->buf, sizeof(float) * total) != hipSuccess) {
         delete l;
@@ -1301,7 +1309,8 @@ int rn_lanes_create(int lanes, int width, int layers, const float* a_pre, const 
     l->pre = p;
     const std::pair<float*, const float*> up[6] = {{l->a_pre, a_pre}, {l->a_post, a_post}, {l->a_res, a_res},
                                                    {l->b_pre, b_pre}, {l->b_post, b_post}, {l->b_res, b_res}};
-    const size_t sizes[6] = {nA, nA, nA, nB, nB, nR};
+    const size_t sizes[6] = {(size_t)layers, (size_t)layers, (size_t)layers, (size_t)layers * lanes,
+                             (size_t)layers * lanes, (size_t)layers * lanes * lanes};
     for (int i = 0; i < 6; ++i)
         if (hipMemcpy(up[i].first, up[i].second, sizeof(float) * sizes[i], hipMemcpyHostToDevice) != hipSuccess) {
             (void)hipFree(l->buf);

@@ -43,7 +43,7 @@ def test_combine_against_float64():
     assert np.max(np.abs(got - want)) < 1e-5
 
 
-def _setup():
+def _setup(bits=4):
     rng = np.random.default_rng(4)
     t = dict(a_pre=rng.normal(0, 1, LAYERS), a_post=rng.normal(0, 1, LAYERS), a_res=rng.normal(0, 1, LAYERS),
              b_pre=rng.normal(0, 1, LAYERS * LANES), b_post=rng.normal(0, 1, LAYERS * LANES),
@@ -51,15 +51,18 @@ def _setup():
     t = {k: v.astype(np.float32) for k, v in t.items()}
     cb = rn.synthetic_codebook(128)
     rows = (LAYERS * LANES, LAYERS * LANES, LAYERS * LANES * LANES)
-    blobs = [rn.synthetic_codebook_blob(r, LANES * WIDTH, 128, 4, seed=10 + i) for i, r in enumerate(rows)]
+    blobs = [rn.synthetic_codebook_blob(r, LANES * WIDTH, 128, bits, seed=10 + i) for i, r in enumerate(rows)]
     return t, cb, rows, blobs
 
 
 @pytest.mark.gpu
-def test_route_and_combine_on_the_gpu():
-    t, cb, rows, blobs = _setup()
-    gphis = [rn.CodebookMatrix(b, r, LANES * WIDTH, 128, 4, cb) for b, r in zip(blobs, rows)]
-    ophis = [oracle.OracleCodebookMatrix(b, r, LANES * WIDTH, 128, 4, cb) for b, r in zip(blobs, rows)]
+@pytest.mark.parametrize("bits", [2, 4, 5])
+def test_route_and_combine_on_the_gpu(bits):
+    """Every output bit for 2-bit (panel form), 4-bit and ternary (plane form)
+    routing matrices, at layer 0 and at layer 1 (rows past the first layer's)."""
+    t, cb, rows, blobs = _setup(bits)
+    gphis = [rn.CodebookMatrix(b, r, LANES * WIDTH, 128, bits, cb) for b, r in zip(blobs, rows)]
+    ophis = [oracle.OracleCodebookMatrix(b, r, LANES * WIDTH, 128, bits, cb) for b, r in zip(blobs, rows)]
     lanes = rn.Lanes(LANES, WIDTH, LAYERS, t["a_pre"], t["a_post"], t["a_res"], t["b_pre"], t["b_post"], t["b_res"],
                      *gphis)
     stream = np.random.default_rng(5).normal(0, 1, (LANES, WIDTH)).astype(np.float32)
