@@ -244,16 +244,32 @@ __global__ void n3_set_token_kernel(uint32_t* tokens, int position, uint32_t tok
     if (threadIdx.x == 0) tokens[position] = source != nullptr ? *source : token;
 }
 
+constexpr int kN3FeedChunk = 256;  // tokens a batched feed runs together
+
+// the ids of a run of tokens, passed by value
+struct N3TokenRun {
+    uint32_t ids[kN3FeedChunk];
+};
+
+__global__ void n3_set_tokens_kernel(uint32_t* tokens, int position, int count, N3TokenRun run) {
+    for (int i = threadIdx.x; i < count; i += blockDim.x) tokens[position + i] = run.ids[i];
+}
+
 // session.rs:86-97: the embedding row of tokens[position] (dequantise_row,
 // matrix.rs:140-153: level * norm, then each group's Walsh-Hadamard transform
 // in registers, lane u holding run u) times sqrt(d) into every lane; cell 0 is
-// their lane mean (session.rs:190-200). One block of 64 * ceil(runs / 64).
+// their lane mean (session.rs:190-200). One block of 64 * ceil(runs / 64) a
+// token: block b embeds position + b into stream + b * stream_stride and
+// cell + b * cell_stride (prefill.rs:21-29 for a run of tokens).
 __global__ __launch_bounds__(1024) void n3_embed_kernel(CodebookParams c, const uint32_t* tokens, int position, int d,
-                                                        int lanes, float scale, float* stream, float* cell) {
+                                                        int lanes, float scale, float* stream, float* cell,
+                                                        int stream_stride, int cell_stride) {
     const int u = threadIdx.x, runs = c.padded / 16, rpg = c.group / 16, G = c.padded / c.group;
     const int ib = c.bits == 5 ? 2 : c.bits;
     const bool valid = u < runs;
-    const uint32_t token = tokens[position];
+    stream += (size_t)blockIdx.x * stream_stride;
+    cell += (size_t)blockIdx.x * cell_stride;
+    const uint32_t token = tokens[position + blockIdx.x];
     const uint8_t* row = c.packed + (size_t)token * c.row_bytes;
     const float norm = valid ? __half2float(__ushort_as_half(c.norms[(size_t)token * G + (16 * u) / c.group])) : 0.0f;
     float x[16];
@@ -296,23 +312,27 @@ struct N3GatherParams {
     const uint32_t* tokens;  // the session's tokens [capacity]
     int heads_per_order, stride;
     int orders[4];
-    float* out;  // [count * sub]
+    float* out;  // [count * sub] a position, out_stride apart
+    int out_stride;
 };
 
 // engram.rs:66-82: row table * slots + index of each table (zeros while the
 // position is shorter than the table's order), dequantised (matrix.rs:140-153),
-// then fake_quantise_int8 over the whole gathered vector.
+// then fake_quantise_int8 over the whole gathered vector. Block b gathers
+// position p.position + b (engram.rs:122-133 for a run of positions).
 __global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherParams p) {
     __shared__ float buf[kN3MaxWidth];
     __shared__ float red[32];
     __shared__ int index_s[kN3MaxTables], order_s[kN3MaxTables];
     const CodebookParams& c = p.tables;
     const int n = p.count * p.sub, ib = c.bits == 5 ? 2 : c.bits, G = c.padded / c.group;
+    const int position = p.position + (int)blockIdx.x;
+    float* const out = p.out + (size_t)blockIdx.x * p.out_stride;
     if (threadIdx.x < p.count) {  // engram.rs:30-46: table (order o, head) hashes the last `order` tokens
         const int t = threadIdx.x, o = t / p.heads_per_order, head = t - o * p.heads_per_order;
         uint32_t acc = 0x9E3779B9u * (uint32_t)(o * p.stride + head + 1);
         for (int back = 0; back < p.orders[o]; ++back) {
-            const uint32_t token = p.position >= back ? p.tokens[p.position - back] : 0u;
+            const uint32_t token = position >= back ? p.tokens[position - back] : 0u;
             acc = (acc ^ token) * 0x01000193u;
         }
         acc ^= acc >> 15;
@@ -323,7 +343,7 @@ __global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherParams p) {
     for (int e = threadIdx.x; e < n; e += blockDim.x) {
         const int t = e / p.sub, j = e - t * p.sub;
         float v = 0.0f;
-        if (p.position + 1 >= order_s[t]) {
+        if (position + 1 >= order_s[t]) {
             const int row = t * p.slots + index_s[t];
             const float norm = __half2float(__ushort_as_half(c.norms[(size_t)row * G + j / c.group]));
             v = c.levels[n3_index(c.packed + (size_t)row * c.row_bytes, j, ib)] * norm;
@@ -333,25 +353,42 @@ __global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherParams p) {
     __syncthreads();
     n3_rotate(buf, n, c.group, c.wht_scale);  // each table row's groups (dequantise_row)
     n3_fake_quantise(buf, n, red);
-    for (int e = threadIdx.x; e < n; e += blockDim.x) p.out[e] = buf[e];
+    for (int e = threadIdx.x; e < n; e += blockDim.x) out[e] = buf[e];
 }
 
-// engram.rs:84-111: the raw value joins the ring (slot position mod keep);
-// value = sum over taps of gain * the raw value `tap * dilation` back.
+// engram.rs:84-111: value = sum over taps of gain * the raw value `tap *
+// dilation` back. Token t = blockIdx.y is position + t, its raw value at raw +
+// t * width; a raw value `back` positions earlier comes from the same run when
+// back <= t (engram.rs:140-153), else from the ring (slot position mod keep).
+// With write_ring (one token) the raw value joins the ring here; a run's
+// values join it afterwards (n3_ring_store_kernel), once every block has read.
 __global__ void n3_engram_conv_kernel(const float* raw, float* ring, const float* taps, int position, int keep,
-                                      int ntaps, int dilation, int width, float* value) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+                                      int ntaps, int dilation, int width, float* value, int write_ring) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y, pos = position + t;
     if (i >= width) return;
-    const float r = raw[i];
-    ring[(size_t)(position % keep) * width + i] = r;
+    const float r = raw[(size_t)t * width + i];
+    if (write_ring) ring[(size_t)(pos % keep) * width + i] = r;
     float v = 0.0f;
     for (int tap = 0; tap < ntaps; ++tap) {
         const int back = tap * dilation;
-        if (position < back) continue;
-        const float sample = back == 0 ? r : ring[(size_t)((position - back) % keep) * width + i];
+        if (pos < back) continue;
+        const float sample = back == 0 ? r
+                             : back <= t ? raw[(size_t)(t - back) * width + i]
+                                         : ring[(size_t)((pos - back) % keep) * width + i];
         v = v + taps[(size_t)tap * width + i] * sample;
     }
-    value[i] = v;
+    value[(size_t)t * width + i] = v;
+}
+
+// The last min(count, keep) rows of a run of positions [position, position +
+// count) into their ring slots (slot position mod keep, ring_stride apart):
+// the history the next position's taps read (engram.rs:155-159,
+// attention.rs:265-273).
+__global__ void n3_ring_store_kernel(const float* rows, int row_stride, int count, int position, int keep, int width,
+                                     float* ring, int ring_stride) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, t = count - min(count, keep) + (int)blockIdx.y;
+    if (i >= width) return;
+    ring[(size_t)((position + t) % keep) * ring_stride + i] = rows[(size_t)t * row_stride + i];
 }
 
 struct N3BlockInParams {
@@ -412,29 +449,40 @@ struct N3QkvParams {
     float* key_scales;     // [KV][cap]
     int8_t* values;
     float* value_scales;
+    int prod_stride;       // a run of tokens: token t's projections at prod + t * prod_stride
+    int run;               // a run: taps of earlier tokens of the run from prod, the ring left alone
 };
 
 // attention.rs:110-141: conv taps over the raw q/k/v ring, per-head norms and
 // rotary for q and k, int8 codes per head, the cache append. One wave per head
-// (blocks 0..H-1 the queries, then the key and value heads).
+// (blocks 0..H-1 the queries, then the key and value heads) and token
+// (blockIdx.y: position + t; attention.rs:242-318 for a run of tokens, whose
+// raw rows join the ring afterwards, n3_ring_store_kernel).
 __global__ __launch_bounds__(64) void n3_qkv_kernel(N3QkvParams p) {
     __shared__ float v_s[kN3Head];
     __shared__ float red[8];
-    const int b = blockIdx.x, lane = threadIdx.x;
+    const int b = blockIdx.x, lane = threadIdx.x, t = blockIdx.y;
     const int which = b < p.H ? 0 : (b < p.H + p.KV ? 1 : 2);
     const int h = which == 0 ? b : (which == 1 ? b - p.H : b - p.H - p.KV);
     const int qw = p.H * kN3Head, kw = p.KV * kN3Head, total = qw + 2 * kw;
     const int width = which == 0 ? qw : kw, off = which == 0 ? 0 : (which == 1 ? qw : qw + kw);
     const int col = h * kN3Head + lane;
-    const float raw = p.prod[off + col];
+    const int position = p.position + t;
+    const float* const prod = p.prod + (size_t)t * p.prod_stride;
+    const float* const cos_row = p.cos_row + (size_t)t * 32;
+    const float* const sin_row = p.sin_row + (size_t)t * 32;
+    const float* const taps = which == 0 ? p.taps[0] : (which == 1 ? p.taps[1] : p.taps[2]);
+    const float raw = prod[off + col];
     float v = raw;
     if (p.ntaps > 0) {
-        p.hist[(size_t)(p.position % p.ntaps) * total + off + col] = raw;
-        const int n = min(p.ntaps, p.position + 1);
+        if (!p.run) p.hist[(size_t)(position % p.ntaps) * total + off + col] = raw;
+        const int n = min(p.ntaps, position + 1);
         v = 0.0f;
         for (int tap = 0; tap < n; ++tap) {
-            const float sample = tap == 0 ? raw : p.hist[(size_t)((p.position - tap) % p.ntaps) * total + off + col];
-            v = v + p.taps[which][(size_t)tap * width + col] * sample;
+            const float sample = tap == 0 ? raw
+                                 : (p.run && tap <= t) ? prod[off + col - (ptrdiff_t)tap * p.prod_stride]
+                                                       : p.hist[(size_t)((position - tap) % p.ntaps) * total + off + col];
+            v = v + taps[(size_t)tap * width + col] * sample;
         }
     }
     if (which < 2) {
@@ -458,11 +506,11 @@ __global__ __launch_bounds__(64) void n3_qkv_kernel(N3QkvParams p) {
         const int half = kN3Head / 2;
         if (lane < half) {
             const float a = v_s[lane], bb = v_s[lane + half];
-            v = a * p.cos_row[lane] - bb * p.sin_row[lane];
+            v = a * cos_row[lane] - bb * sin_row[lane];
         } else {
             const int i = lane - half;
             const float a = v_s[i], bb = v_s[lane];
-            v = bb * p.cos_row[i] + a * p.sin_row[i];
+            v = bb * cos_row[i] + a * sin_row[i];
         }
     }
     // ops.rs:112-118
@@ -470,10 +518,10 @@ __global__ __launch_bounds__(64) void n3_qkv_kernel(N3QkvParams p) {
     const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
     const int8_t code = (int8_t)quantise_one(v, scale);
     if (which == 0) {
-        p.qcodes[col] = code;
-        if (lane == 0) p.qscales[h] = scale;
+        p.qcodes[(size_t)t * qw + col] = code;
+        if (lane == 0) p.qscales[(size_t)t * p.H + h] = scale;
     } else {
-        const size_t row = (size_t)h * p.cap + p.position;
+        const size_t row = (size_t)h * p.cap + position;
         (which == 1 ? p.keys : p.values)[row * kN3Head + lane] = code;
         if (lane == 0) (which == 1 ? p.key_scales : p.value_scales)[row] = scale;
     }
@@ -487,13 +535,16 @@ struct N3AttendParams {
     const int8_t* values;
     const float* value_scales;
     const float* gate;     // [H][64] gate projections
-    int cap, first, count, group;
+    int cap, position, window, group;  // window: positions a non-global layer sees (0: all)
     float inverse_root;
     float* out;            // [H][64]
+    int gate_stride;       // a run of tokens: token t's gates at gate + t * gate_stride
 };
 
-// kernels/src/attention.rs:53-80 for query head blockIdx.x over positions
-// [first, first + count), then times sigmoid(gate) (attention.rs:147-149).
+// kernels/src/attention.rs:53-80 for query head blockIdx.x of the token at
+// position + blockIdx.y over positions [first, position + 1) (first from the
+// window, attention.rs:171-177), then times sigmoid(gate)
+// (attention.rs:147-149; attention.rs:319-330 for a run of tokens).
 // Scores are exact; coefficients ((float)score * key_scale) * query_scale; the
 // exponent total is the aarch64 build's: four lane sums over the first
 // count - count % 4 positions (position p in lane p % 4, in order), added as
@@ -505,15 +556,20 @@ __global__ __launch_bounds__(256) void n3_attend_kernel(N3AttendParams p) {
     __shared__ int part[16][kN3Head];
     __shared__ float red[8];
     __shared__ float lanes_s[4];
-    const int h = blockIdx.x, tid = threadIdx.x, kvh = h / p.group, count = p.count;
-    const float query_scale = p.qscales[h] * p.inverse_root;
+    const int t = blockIdx.y, total_positions = p.position + t + 1;
+    const int first = p.window > 0 && total_positions > p.window ? total_positions - p.window : 0;
+    const int8_t* const qcodes = p.qcodes + (size_t)t * gridDim.x * kN3Head;
+    const float* const gate = p.gate + (size_t)t * p.gate_stride;
+    float* const out = p.out + (size_t)t * gridDim.x * kN3Head;
+    const int h = blockIdx.x, tid = threadIdx.x, kvh = h / p.group, count = total_positions - first;
+    const float query_scale = p.qscales[(size_t)t * gridDim.x + h] * p.inverse_root;
     int4 q[4];
-    const int4* qs = reinterpret_cast<const int4*>(p.qcodes + (size_t)h * kN3Head);
+    const int4* qs = reinterpret_cast<const int4*>(qcodes + (size_t)h * kN3Head);
 #pragma unroll
     for (int i = 0; i < 4; ++i) q[i] = qs[i];
-    const int8_t* kbase = p.keys + ((size_t)kvh * p.cap + p.first) * kN3Head;
-    const float* ks = p.key_scales + (size_t)kvh * p.cap + p.first;
-    const float* vs = p.value_scales + (size_t)kvh * p.cap + p.first;
+    const int8_t* kbase = p.keys + ((size_t)kvh * p.cap + first) * kN3Head;
+    const float* ks = p.key_scales + (size_t)kvh * p.cap + first;
+    const float* vs = p.value_scales + (size_t)kvh * p.cap + first;
     float peak = -INFINITY;
     for (int pp = tid; pp < count; pp += 256) {
         const int4* k = reinterpret_cast<const int4*>(kbase + (size_t)pp * kN3Head);
@@ -551,7 +607,7 @@ __global__ __launch_bounds__(256) void n3_attend_kernel(N3AttendParams p) {
     const int dg = tid & 15, pc = tid >> 4;
     int acc[4] = {0, 0, 0, 0};
     if (cpeak > 0.0f) {
-        const int8_t* vbase = p.values + ((size_t)kvh * p.cap + p.first) * kN3Head + 4 * dg;
+        const int8_t* vbase = p.values + ((size_t)kvh * p.cap + first) * kN3Head + 4 * dg;
         for (int pp = pc; pp < count; pp += 16) {
             const int w = (int)__builtin_roundf((c_s[pp] * vs[pp]) / scale);
             if (w == 0) continue;
@@ -570,17 +626,20 @@ __global__ __launch_bounds__(256) void n3_attend_kernel(N3AttendParams p) {
         for (int pp = vector_count; pp < count; ++pp) total = total + c_s[pp];
         float o = cpeak > 0.0f ? (float)sum * scale : 0.0f;
         o = o * (1.0f / total);
-        o = o * libm_sigmoid(p.gate[(size_t)h * kN3Head + tid]);
-        p.out[(size_t)h * kN3Head + tid] = o;
+        o = o * libm_sigmoid(gate[(size_t)h * kN3Head + tid]);
+        out[(size_t)h * kN3Head + tid] = o;
     }
 }
 
-// ops.rs:120-125 over n <= 4096 values (one block), then, for group > 0,
-// prepare for a matrix of that group and padded width (matrix.rs:123-128)
+// ops.rs:120-125 over n <= 4096 values (one block a vector: block b reads in +
+// b * n), then, for group > 0, prepare for a matrix of that group and padded
+// width (matrix.rs:123-128) into out + b * padded (else out + b * n)
 __global__ __launch_bounds__(kN3Block) void n3_fake_quantise_kernel(const float* in, int n, int padded, int group,
                                                                     float wht_scale, float* out) {
     __shared__ float buf[kN3MaxWidth];
     __shared__ float red[32];
+    in += (size_t)blockIdx.x * n;
+    out += (size_t)blockIdx.x * (group > 0 ? padded : n);
     for (int i = threadIdx.x; i < n; i += blockDim.x) buf[i] = in[i];
     __syncthreads();
     n3_fake_quantise(buf, n, red);
@@ -870,6 +929,55 @@ __global__ __launch_bounds__(256) void n3_observe_kernel(const float* cells, con
     const float rescale = rw[0], weight = rw[1];
     float* target = weighted + (size_t)slot * width;
     for (int i = threadIdx.x; i < width; i += blockDim.x) target[i] = target[i] * rescale + weight * cell[i];
+}
+
+// n3_observe_kernel over a run of tokens in order (prefill.rs:92-96): one
+// block per slot; the run's scores first (ops.rs:19-30, 32 tokens at a time,
+// eight lanes each), since they do not depend on the accumulator, then the
+// online updates token by token (heads.rs:138-155).
+__global__ __launch_bounds__(256) void n3_observe_run_kernel(const float* cells, int cell_stride, int count,
+                                                             const float* probes, int k, int width, float* peak,
+                                                             float* total, float* weighted) {
+    __shared__ float score_s[kN3FeedChunk], rescale_s[kN3FeedChunk], weight_s[kN3FeedChunk];
+    __shared__ float red[256];
+    const int slot = blockIdx.x, layer = slot / k, tid = threadIdx.x;
+    const float* probe = probes + (size_t)slot * width;
+    const float* first_cell = cells + (size_t)layer * width;
+    for (int t0 = 0; t0 < count; t0 += 32) {
+        const int tt = t0 + (tid >> 3), j = tid & 7;
+        if (tt < count) red[tid] = n3_fold<false>(0.0f, first_cell + (size_t)tt * cell_stride + j, probe + j, width / 8, 8);
+        __syncthreads();
+        if (tid < 32 && t0 + tid < count) {
+            const float* cell = first_cell + (size_t)(t0 + tid) * cell_stride;
+            float sum = -0.0f;
+            for (int q = 0; q < 8; ++q) sum = sum + red[8 * tid + q];
+            float tail = -0.0f;
+            for (int i = width / 8 * 8; i < width; ++i) tail = tail + cell[i] * probe[i];
+            score_s[t0 + tid] = (sum + tail) / sqrtf((float)width);
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        float pk = peak[slot], tot = total[slot];
+        for (int t = 0; t < count; ++t) {
+            const float score = score_s[t], next = fmaxf(pk, score);
+            const float rescale = pk == -INFINITY ? 0.0f : libm_expf(pk - next);
+            const float weight = libm_expf(score - next);
+            tot = tot * rescale + weight;
+            pk = next;
+            rescale_s[t] = rescale;
+            weight_s[t] = weight;
+        }
+        peak[slot] = pk;
+        total[slot] = tot;
+    }
+    __syncthreads();
+    float* target = weighted + (size_t)slot * width;
+    for (int i = tid; i < width; i += blockDim.x) {
+        float w = target[i];
+        for (int t = 0; t < count; ++t) w = w * rescale_s[t] + weight_s[t] * first_cell[(size_t)t * cell_stride + i];
+        target[i] = w;
+    }
 }
 
 // heads.rs:102-110: per slot, the average over the online total, unit_rms,
@@ -1568,6 +1676,13 @@ struct N3BoundaryParams {
     float* code_scales;   // [qpadded / qgroup]
     const uint8_t* phi_rows;  // the route layer's rows of phi_pre, phi_post, phi_res, one after another
     int d, lanes;
+    // a run of tokens, one block each (prefill.rs:45-88): block b's vectors
+    // sit b strides on (stream and next lanes * d, attention, x, input, key
+    // and value d, post kMaxLanes, residual kMaxLanes^2, cell cell_stride,
+    // rotated qpadded); with `rotated` the block input is written prepared
+    // (matrix.rs:123-128) instead of as codes; the last block writes hidden
+    float* rotated;
+    int cell_stride;
 };
 
 constexpr int kN3RouteRows = 24;         // 2 lanes + lanes^2 for four lanes
@@ -1598,6 +1713,28 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     const int route_rows = 2 * L + L * L, G = p.phi_pre.padded / p.phi_pre.group;
     const int layer = p.layer, chunks = p.phi_pre.row_bytes / 16;
     N3BlockOutParams t = p.t;
+    {  // this block's token of a run
+        const size_t b = blockIdx.x;
+        t.attention += b * d;
+        t.x += b * d;
+        t.input += b * d;
+        t.post += b * kMaxLanes;
+        t.residual += b * kMaxLanes * kMaxLanes;
+        t.stream += b * S;
+        t.next += b * S;
+        t.cell += b * p.cell_stride;
+    }
+    // (the kernel arguments stay as passed: a changed argument struct is copied
+    // to scratch memory)
+    const size_t tb = blockIdx.x;
+    const float* const in_stream = p.stream + tb * S;
+    float* const out_input = p.input + tb * d;
+    float* const out_post = p.post + tb * kMaxLanes;
+    float* const out_residual = p.residual + tb * kMaxLanes * kMaxLanes;
+    const float* const e_key = p.key != nullptr ? p.key + tb * d : nullptr;
+    const float* const e_value = p.key != nullptr ? p.value + tb * d : nullptr;
+    float* const out_x = p.x + tb * d;
+    float* const out_rotated = p.rotated != nullptr ? p.rotated + tb * p.qpadded : nullptr;
     N3TailPre pre{};
     const bool cv_staged = p.tail && t.rank == 8;
     float* const cv_ = tailw_s + 6 * kN3Hadamard;
@@ -1616,11 +1753,18 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
             const int nw = j == 0 ? n0 : j == 1 ? n1 : j == 2 ? n2 : n3, cnt = j == 0 ? u0 : j == 1 ? u1 : j == 2 ? u2 : u3;
             const int4* src = reinterpret_cast<const int4*>(
                 j == 0 ? (const void*)t.factors[0]
-                       : j == 1 ? (const void*)t.attention : j == 2 ? (const void*)(p.tail ? t.stream : p.stream) : (const void*)p.phi_rows);
+                       : j == 1 ? (const void*)t.attention : j == 2 ? (const void*)(p.tail ? t.stream : in_stream) : (const void*)p.phi_rows);
             int4* dst = reinterpret_cast<int4*>(j == 0 ? (void*)tailw_s : j == 1 ? (void*)tin_s : j == 2 ? (void*)stream_s : (void*)pw);
+            // range 1 is three vectors of d / 4 units (attention, x, input)
+            const int d4 = d / 4;
+            const int4* x4 = reinterpret_cast<const int4*>(t.x) - d4;
+            const int4* in4 = reinterpret_cast<const int4*>(t.input) - 2 * d4;
             int4 v[6];
 #pragma unroll
-            for (int k = 0; k < 6; ++k) v[k] = src[min((k * nw + wave - w0) * 64 + lane, cnt - 1)];
+            for (int k = 0; k < 6; ++k) {
+                const int u = min((k * nw + wave - w0) * 64 + lane, cnt - 1);
+                v[k] = (j == 1 && u >= d4 ? (u >= 2 * d4 ? in4 : x4) : src)[u];
+            }
 #pragma unroll
             for (int k = 0; k < 6; ++k) {
                 const int u = (k * nw + wave - w0) * 64 + lane;
@@ -1678,14 +1822,15 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
         }
         __syncthreads();
         n3_norm(a_, p.final_norm, d, a_, red, cv_);
-        for (int i = tid; i < d; i += blockDim.x) p.hidden[i] = a_[i];
+        if (blockIdx.x == gridDim.x - 1)
+            for (int i = tid; i < d; i += blockDim.x) p.hidden[i] = a_[i];
     }
     if (!p.route) return;
     // the block input's tensors, requested before the routing work
     float norm_in_r[1], key_r[1], value_r[1];
     norm_in_r[0] = tid < d ? p.norm_in[tid] : 0.0f;
-    key_r[0] = (p.key != nullptr && tid < d) ? p.key[tid] : 0.0f;
-    value_r[0] = (p.key != nullptr && tid < d) ? p.value[tid] : 0.0f;
+    key_r[0] = (e_key != nullptr && tid < d) ? e_key[tid] : 0.0f;
+    value_r[0] = (e_key != nullptr && tid < d) ? e_value[tid] : 0.0f;
     // lanes.rs:49-53: unit_rms, fake_quantise_int8, prepare (phi_pre's groups)
     n3_unit_rms(stream_s, S, rv, red, cv_);
     n3_fake_quantise(rv, S, red);
@@ -1707,7 +1852,7 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
             const float pre_offset = lane == own ? 8.0f + -4.0f : -4.0f;
             gate_s[lane] = libm_sigmoid(small_s[0] * ry[lane] + small_s[3 + lane] + pre_offset);
             const float post_offset = lane == own ? 0.0f : -4.0f;
-            p.post[lane] = 2.0f * libm_sigmoid(small_s[1] * ry[L + lane] + small_s[3 + L + lane] + post_offset);
+            out_post[lane] = 2.0f * libm_sigmoid(small_s[1] * ry[L + lane] + small_s[3 + L + lane] + post_offset);
         }
         const int i = tid;
         const bool live = i < n;
@@ -1762,18 +1907,18 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
                 m = m * (1.0f / fmaxf(total, 1.17549435e-38f));
             }
         }
-        if (live) p.residual[i] = m;
+        if (live) out_residual[i] = m;
     }
     __syncthreads();
     for (int i = tid; i < d; i += blockDim.x) {
         float v = 0.0f;
         for (int ln = 0; ln < L; ++ln) v = v + gate_s[ln] * stream_s[(size_t)ln * d + i];
         xs_[i] = v;
-        p.input[i] = v;
+        out_input[i] = v;
     }
     __syncthreads();
     // session.rs:112-118 with add_engram (session.rs:175-188)
-    if (p.key != nullptr) {
+    if (e_key != nullptr) {
         n3_unit_rms(xs_, d, a_, red, cv_);
         if (tid < d) sc_[tid] = key_r[0];
         __syncthreads();
@@ -1793,8 +1938,13 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     n3_fake_quantise(a_, d, red);
     for (int i = d + tid; i < p.qpadded; i += blockDim.x) a_[i] = 0.0f;
     __syncthreads();
-    n3_prepare_codes(a_, p.qpadded, p.qgroup, p.qscale, p.qib, p.codes, p.code_scales);
-    for (int i = tid; i < d; i += blockDim.x) p.x[i] = xs_[i];
+    if (out_rotated != nullptr) {
+        n3_rotate(a_, p.qpadded, p.qgroup, p.qscale);
+        for (int i = tid; i < p.qpadded; i += blockDim.x) out_rotated[i] = a_[i];
+    } else {
+        n3_prepare_codes(a_, p.qpadded, p.qgroup, p.qscale, p.qib, p.codes, p.code_scales);
+    }
+    for (int i = tid; i < d; i += blockDim.x) out_x[i] = xs_[i];
 }
 
 }  // namespace rn
@@ -2384,6 +2534,15 @@ struct rn_n3_session {
     float *cells = nullptr, *hidden = nullptr, *logits = nullptr, *cos = nullptr, *sin = nullptr;
     std::vector<float*> peak, total, weighted;
     float *readouts = nullptr, *pooled = nullptr, *head_out = nullptr;
+    // a batched feed's vectors, kN3FeedChunk tokens of each (taken on the first feed)
+    struct Run {
+        bool ready = false;
+        float *stream_a = nullptr, *stream_b = nullptr, *attn = nullptr, *x = nullptr, *input = nullptr;
+        float *post = nullptr, *residual = nullptr, *rotated = nullptr, *prod = nullptr, *attended = nullptr;
+        float *qscales = nullptr, *cells = nullptr, *gathered = nullptr, *eraw = nullptr;
+        int8_t* qcodes = nullptr;
+        std::vector<float*> ekey, evalue;
+    } run;
 };
 
 namespace {
@@ -2413,6 +2572,16 @@ int product(const rn_matrix* mat, const float* rotated, float* y, hipStream_t st
     return RN_OK;
 }
 
+// QuantisedMatrix::multiply_batch (matrix.rs:330-389) of count rotated inputs:
+// the integer path per token, the float path's batch tile otherwise
+int product_run(const rn_matrix* mat, const float* rotated, int count, float* y, hipStream_t st) {
+    if (mat->bits == 1 || mat->bits == 3)
+        N3_HIP(launch_codebook_float(mat->cb, rotated, count, y, true, st));
+    else
+        N3_HIP(launch_codebook_product(mat->cb, rotated, count, y, nullptr, st));
+    return RN_OK;
+}
+
 int rotate(const rn_matrix* mat, const float* x, float* rotated, hipStream_t st) {
     N3_HIP(launch_codebook_rotate(x, 1, mat->columns, mat->cb.padded, mat->group, mat->cb.wht_scale, rotated, st));
     return RN_OK;
@@ -2423,6 +2592,11 @@ int window_first(const rn_geometry& g, int layer, int total) {
     if (g.sliding_window > 0 && !((g.global_layers >> layer) & 1))
         return total > (int)g.sliding_window ? total - (int)g.sliding_window : 0;
     return 0;
+}
+
+// the positions a layer's query sees (0: all of them)
+int layer_window(const rn_geometry& g, int layer) {
+    return g.sliding_window > 0 && !((g.global_layers >> layer) & 1) ? (int)g.sliding_window : 0;
 }
 
 int site_of(const rn_n3_model* m, int layer) {  // config.rs:89-91
@@ -2608,9 +2782,8 @@ int stepwise_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
         qp.value_scales = c.value_scales;
         rn_launch(n3_qkv_kernel, dim3(H + 2 * KV), dim3(64), 0, st, qp);
         N3_HIP(hipGetLastError());
-        const int total = position + 1, first = window_first(g, layer, total);
         N3AttendParams ap{s->qcodes, s->qscales, c.keys, c.key_scales, c.values, c.value_scales, s->prod + qkv,
-                          s->capacity, first, total - first, H / KV, 1.0f / sqrtf(64.0f), s->attended};
+                          s->capacity, position, layer_window(g, layer), H / KV, 1.0f / sqrtf(64.0f), s->attended, 0};
         rn_launch(n3_attend_kernel, dim3(H), dim3(256), 0, st, ap);
         N3_HIP(hipGetLastError());
         rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->attended, H * 64,
@@ -2799,7 +2972,7 @@ int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
     float* nxt = s->stream_b;
     const int embed_threads = ((m->embedding->cb.padded / 16 + 63) / 64) * 64;
     rn_launch(n3_embed_kernel, dim3(1), dim3(embed_threads), 0, st, m->embedding->cb, (const uint32_t*)s->tokens_dev,
-              position, d, lanes, sqrtf((float)d), cur, s->cells);
+              position, d, lanes, sqrtf((float)d), cur, s->cells, 0, 0);
     N3_HIP(hipGetLastError());
 
     // engram sites (engram.rs:30-112), before the layers
@@ -2826,7 +2999,7 @@ int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
         N3_CALL(product(eg.value, s->rotated, s->eraw, st));
         rn_launch(n3_engram_conv_kernel, dim3((d + 255) / 256), dim3(256), 0, st, (const float*)s->eraw, s->rings[e],
                   (const float*)eg.taps, position, keep, (int)g.engram_conv_taps, (int)g.engram_conv_dilation, d,
-                  s->evalue[e]);
+                  s->evalue[e], 1);
         N3_HIP(hipGetLastError());
     }
 
@@ -2855,6 +3028,267 @@ int enqueue_logits(rn_n3_session* s) {
     else
         N3_HIP(launch_codebook_product(p, s->rotated, 1, s->logits, nullptr, st));
     return RN_OK;
+}
+
+// The vectors of a batched feed, once a session
+int run_buffers(rn_n3_session* s) {
+    rn_n3_session::Run& r = s->run;
+    if (r.ready) return RN_OK;
+    const rn_n3_model* m = s->m;
+    const rn_geometry& g = m->g;
+    const size_t C = kN3FeedChunk, d = g.d_model, S = (size_t)g.mhc_lanes * d, H = g.num_heads;
+    const size_t A = m->active.size();
+    size_t widest = 0, rows = 0, gathered = 1;
+    for (const N3Layer& y : m->layers) {
+        widest = std::max({widest, (size_t)y.qkvg->cb.padded, (size_t)y.out->cb.padded});
+        rows = std::max(rows, (size_t)y.qkvg->rows);
+    }
+    for (const N3Engram& e : m->engrams) {
+        widest = std::max(widest, (size_t)e.key->cb.padded);
+        gathered = std::max(gathered, (size_t)e.key->columns);
+    }
+    N3_CALL(alloc_n(s, C * S, &r.stream_a));
+    N3_CALL(alloc_n(s, C * S, &r.stream_b));
+    N3_CALL(alloc_n(s, C * d, &r.attn));
+    N3_CALL(alloc_n(s, C * d, &r.x));
+    N3_CALL(alloc_n(s, C * d, &r.input));
+    N3_CALL(alloc_n(s, C * kMaxLanes, &r.post));
+    N3_CALL(alloc_n(s, C * kMaxLanes * kMaxLanes, &r.residual));
+    N3_CALL(alloc_n(s, C * widest, &r.rotated));
+    N3_CALL(alloc_n(s, C * rows, &r.prod));
+    N3_CALL(alloc_n(s, C * H * 64, &r.attended));
+    N3_CALL(alloc_n(s, C * H * 64, &r.qcodes));
+    N3_CALL(alloc_n(s, C * H, &r.qscales));
+    N3_CALL(alloc_n(s, C * (A + 1) * d, &r.cells));
+    N3_CALL(alloc_n(s, C * gathered, &r.gathered));
+    N3_CALL(alloc_n(s, C * d, &r.eraw));
+    r.ekey.assign(g.engram_site_count, nullptr);
+    r.evalue.assign(g.engram_site_count, nullptr);
+    for (uint32_t e = 0; e < g.engram_site_count; ++e) {
+        N3_CALL(alloc_n(s, C * d, &r.ekey[e]));
+        N3_CALL(alloc_n(s, C * d, &r.evalue[e]));
+    }
+    r.ready = true;
+    return RN_OK;
+}
+
+// Session::prefill (prefill.rs:10-99) of count (<= kN3FeedChunk) tokens at
+// positions [length, length + count): the per-token work of a layer runs as
+// one launch over the tokens (a block or a grid row each), the projections as
+// batched products, the attention per (head, token) after every token's key
+// and value joined the cache; each token's arithmetic is the push's, so the
+// state after the run equals that after pushing the tokens in order.
+int enqueue_run(rn_n3_session* s, const uint32_t* tokens, int count) {
+    N3_CALL(run_buffers(s));
+    const rn_n3_model* m = s->m;
+    const rn_geometry& g = m->g;
+    rn_n3_session::Run& r = s->run;
+    const int d = (int)g.d_model, lanes = (int)g.mhc_lanes, H = (int)g.num_heads, KV = (int)g.num_kv_heads;
+    const int S = lanes * d, T = count, P0 = s->length;
+    const size_t layers = m->active.size();
+    const int cell_stride = (int)(layers + 1) * d;
+    hipStream_t st = s->stream;
+    {
+        N3TokenRun ids{};
+        for (int i = 0; i < T; ++i) ids.ids[i] = tokens[i];
+        rn_launch(n3_set_tokens_kernel, dim3(1), dim3(256), 0, st, s->tokens_dev, P0, T, ids);
+        N3_HIP(hipGetLastError());
+    }
+    const int embed_threads = ((m->embedding->cb.padded / 16 + 63) / 64) * 64;
+    rn_launch(n3_embed_kernel, dim3(T), dim3(embed_threads), 0, st, m->embedding->cb, (const uint32_t*)s->tokens_dev,
+              P0, d, lanes, sqrtf((float)d), r.stream_a, r.cells, S, cell_stride);
+    N3_HIP(hipGetLastError());
+
+    // engram sites (engram.rs:113-162)
+    const int hpo = heads_per_order(g), tables = (int)g.engram_order_count * hpo;
+    const int keep = std::max(1, ((int)g.engram_conv_taps - 1) * (int)g.engram_conv_dilation + 1);
+    for (uint32_t e = 0; e < g.engram_site_count; ++e) {
+        if (!site_active(m, (int)e)) continue;
+        const N3Engram& eg = m->engrams[e];
+        N3GatherParams gp{};
+        gp.tables = eg.tables->cb;
+        gp.count = tables;
+        gp.sub = (int)g.engram_sub_dim;
+        gp.slots = (int)g.engram_slots;
+        gp.position = P0;
+        gp.tokens = s->tokens_dev;
+        gp.heads_per_order = hpo;
+        gp.stride = g.engram_seed_heads == 0 ? hpo : (int)g.engram_seed_heads;
+        for (int o = 0; o < 4; ++o) gp.orders[o] = (int)g.engram_orders[o];
+        gp.out = r.gathered;
+        gp.out_stride = (int)eg.key->columns;
+        rn_launch(n3_gather_kernel, dim3(T), dim3(kN3Block), 0, st, gp);
+        N3_HIP(hipGetLastError());
+        N3_HIP(launch_codebook_rotate(r.gathered, T, eg.key->columns, eg.key->cb.padded, eg.key->group,
+                                      eg.key->cb.wht_scale, r.rotated, st));
+        N3_CALL(product_run(eg.key, r.rotated, T, r.ekey[e], st));
+        N3_CALL(product_run(eg.value, r.rotated, T, r.eraw, st));
+        rn_launch(n3_engram_conv_kernel, dim3((d + 255) / 256, T), dim3(256), 0, st, (const float*)r.eraw, s->rings[e],
+                  (const float*)eg.taps, P0, keep, (int)g.engram_conv_taps, (int)g.engram_conv_dilation, d, r.evalue[e],
+                  0);
+        N3_HIP(hipGetLastError());
+        rn_launch(n3_ring_store_kernel, dim3((d + 255) / 256, std::min(T, keep)), dim3(256), 0, st, (const float*)r.eraw,
+                  d, T, P0, keep, d, s->rings[e], d);
+        N3_HIP(hipGetLastError());
+    }
+
+    float* cur = r.stream_a;
+    float* nxt = r.stream_b;
+    auto route_into = [&](N3BoundaryParams& b, size_t slot) {
+        const int layer = m->active[slot];
+        const N3Layer& y = m->layers[(size_t)layer];
+        const int site = site_of(m, layer);
+        b.route = 1;
+        b.layer = layer;
+        b.slot = (int)slot;
+        b.phi_pre = m->phi_pre->cb;
+        b.phi_post = m->phi_post->cb;
+        b.phi_res = m->phi_res->cb;
+        b.a_pre = m->a_pre;
+        b.a_post = m->a_post;
+        b.a_res = m->a_res;
+        b.b_pre = m->b_pre;
+        b.b_post = m->b_post;
+        b.b_res = m->b_res;
+        b.input = r.input;
+        b.post = r.post;
+        b.residual = r.residual;
+        b.key = site >= 0 ? r.ekey[(size_t)site] : nullptr;
+        b.value = site >= 0 ? r.evalue[(size_t)site] : nullptr;
+        b.norm_in = y.norm_in;
+        b.x = r.x;
+        b.qpadded = y.qkvg->cb.padded;
+        b.qgroup = y.qkvg->group;
+        b.qib = y.qkvg->bits == 5 ? 2 : y.qkvg->bits;
+        b.qscale = y.qkvg->cb.wht_scale;
+        b.rotated = r.rotated;
+        b.phi_rows = m->phi_stack + (size_t)layer * (2 * lanes + lanes * lanes) * m->phi_pre->cb.row_bytes;
+    };
+    {
+        N3BoundaryParams b{};
+        b.stream = cur;
+        b.d = d;
+        b.lanes = lanes;
+        b.cell_stride = cell_stride;
+        route_into(b, 0);
+        rn_launch(n3_boundary_kernel, dim3(T), dim3(kN3Block), 0, st, b);
+        N3_HIP(hipGetLastError());
+    }
+    const int qw = H * 64, qkv = (H + 2 * KV) * 64;
+    for (size_t slot = 0; slot < layers; ++slot) {
+        const int layer = m->active[slot];
+        const N3Layer& y = m->layers[(size_t)layer];
+        N3CacheDev& c = s->caches[(size_t)layer];
+        const int rows = (int)y.qkvg->rows;
+        N3_CALL(product_run(y.qkvg, r.rotated, T, r.prod, st));
+        N3QkvParams qp{};
+        qp.prod = r.prod;
+        qp.hist = c.hist;
+        for (int t = 0; t < 3; ++t) qp.taps[t] = y.taps[t];
+        qp.ntaps = (int)g.qkv_conv_taps;
+        qp.position = P0;
+        qp.H = H;
+        qp.KV = KV;
+        qp.cap = s->capacity;
+        qp.q_norm = y.q_norm;
+        qp.k_norm = y.k_norm;
+        qp.cos_row = s->cos + (size_t)P0 * 32;
+        qp.sin_row = s->sin + (size_t)P0 * 32;
+        qp.qcodes = r.qcodes;
+        qp.qscales = r.qscales;
+        qp.keys = c.keys;
+        qp.key_scales = c.key_scales;
+        qp.values = c.values;
+        qp.value_scales = c.value_scales;
+        qp.prod_stride = rows;
+        qp.run = 1;
+        rn_launch(n3_qkv_kernel, dim3(H + 2 * KV, T), dim3(64), 0, st, qp);
+        N3_HIP(hipGetLastError());
+        if (qp.ntaps > 0) {
+            rn_launch(n3_ring_store_kernel, dim3((qkv + 255) / 256, std::min(T, qp.ntaps)), dim3(256), 0, st,
+                      (const float*)r.prod, rows, T, P0, qp.ntaps, qkv, c.hist, qkv);
+            N3_HIP(hipGetLastError());
+        }
+        N3AttendParams ap{r.qcodes, r.qscales, c.keys, c.key_scales, c.values, c.value_scales, r.prod + qkv,
+                          s->capacity, P0, layer_window(g, layer), H / KV, 1.0f / sqrtf(64.0f), r.attended, rows};
+        rn_launch(n3_attend_kernel, dim3(H, T), dim3(256), 0, st, ap);
+        N3_HIP(hipGetLastError());
+        rn_launch(n3_fake_quantise_kernel, dim3(T), dim3(kN3Block), 0, st, (const float*)r.attended, qw,
+                  y.out->cb.padded, y.out->group, y.out->cb.wht_scale, r.rotated);
+        N3_HIP(hipGetLastError());
+        N3_CALL(product_run(y.out, r.rotated, T, r.attn, st));
+        N3BoundaryParams b{};
+        b.tail = 1;
+        N3BlockOutParams& bo = b.t;
+        bo.attention = r.attn;
+        bo.post_norm = y.post_norm;
+        bo.gate = y.gate_sigmoid;
+        bo.pre_norm = y.pre_norm;
+        bo.d1 = y.d1;
+        bo.d2 = y.d2;
+        bo.b2 = y.b2;
+        bo.d3 = y.d3;
+        bo.d4 = y.d4;
+        for (int f = 0; f < 6; ++f) bo.factors[f] = y.factors[f];
+        bo.cond_v = y.cond_v;
+        bo.cond_u = y.cond_u;
+        bo.rank = y.rank;
+        bo.perm1 = m->perm[0];
+        bo.perm2 = m->perm[1];
+        bo.x = r.x;
+        bo.input = r.input;
+        bo.post = r.post;
+        bo.residual = r.residual;
+        bo.stream = cur;
+        bo.d = d;
+        bo.lanes = lanes;
+        bo.next = nxt;
+        bo.cell = r.cells + (slot + 1) * (size_t)d;
+        b.d = d;
+        b.lanes = lanes;
+        b.cell_stride = cell_stride;
+        if (slot + 1 < layers) {
+            route_into(b, slot + 1);
+        } else {
+            b.final = 1;
+            b.final_norm = m->final_norm;
+            b.hidden = s->hidden;
+        }
+        rn_launch(n3_boundary_kernel, dim3(T), dim3(kN3Block), 0, st, b);
+        N3_HIP(hipGetLastError());
+        std::swap(cur, nxt);
+    }
+    // the heads observe the tokens in order (prefill.rs:92-96)
+    for (size_t i = 0; i < m->heads.size(); ++i) {
+        const N3Head& h = m->heads[i];
+        rn_launch(n3_observe_run_kernel, dim3(h.layers * h.per_layer), dim3(256), 0, st, (const float*)r.cells,
+                  cell_stride, T, (const float*)h.probes, h.per_layer, h.width, s->peak[i], s->total[i],
+                  s->weighted[i]);
+        N3_HIP(hipGetLastError());
+    }
+    // the last token's cells (prefill.rs:98)
+    N3_HIP(hipMemcpyAsync(s->cells, r.cells + (size_t)(T - 1) * cell_stride, (size_t)cell_stride * 4,
+                          hipMemcpyDeviceToDevice, st));
+    s->length += T;
+    return RN_OK;
+}
+
+// A run of tokens can take the batched path: the one-launch boundary, integer
+// projections, and vectors on 16-byte boundaries.
+bool run_applies(const rn_n3_session* s) {
+    const rn_n3_model* m = s->m;
+    const rn_geometry& g = m->g;
+    const int d = (int)g.d_model;
+    if (!s->fused || d % 4 != 0) return false;
+    for (const N3Head& h : m->heads)
+        if (h.width != d) return false;
+    const int gathered = (int)(g.engram_order_count * heads_per_order(g) * g.engram_sub_dim);
+    for (const N3Engram& e : m->engrams)
+        if ((int)e.key->columns != gathered || (int)e.key->rows != d || (int)e.value->rows != d) return false;
+    for (const N3Layer& y : m->layers)
+        if ((int)y.out->rows != d || (int)y.qkvg->rows < ((int)g.num_heads * 2 + 2 * (int)g.num_kv_heads) * 64)
+            return false;
+    return true;
 }
 
 }  // namespace
@@ -2887,13 +3321,30 @@ int rn_n3_session_decode_greedy(rn_n3_session* s, uint32_t first, int steps, uin
     return RN_OK;
 }
 
-// Session::feed (session.rs:58-74): the batched prefill runs the same
-// arithmetic per token as pushing them in order.
+// Session::feed (session.rs:58-74): at least BATCH_THRESHOLD (4) tokens run
+// as batched prefills of up to kN3FeedChunk tokens (a shorter last chunk of
+// fewer than 4 is pushed), fewer are pushed. The batched prefill runs each
+// token's arithmetic as a push does, so the chunk size changes nothing but
+// speed (RN_N3_FEED_CHUNK, 4..256, sets it).
 int rn_n3_session_feed(rn_n3_session* s, const uint32_t* tokens, int count) {
+    constexpr int kBatchThreshold = 4;
     N3_REQUIRE(s && (tokens || count == 0), "null argument");
     N3_REQUIRE(count >= 0 && s->length + count <= s->capacity, "feed of %d tokens overflows the capacity", count);
     for (int i = 0; i < count; ++i) N3_REQUIRE(tokens[i] < s->m->g.vocab, "token %u outside the vocabulary", tokens[i]);
-    for (int i = 0; i < count; ++i) N3_CALL(rn_n3_session_push(s, tokens[i]));
+    int chunk = kN3FeedChunk;
+    if (const char* e = getenv("RN_N3_FEED_CHUNK")) chunk = std::min(kN3FeedChunk, std::max(kBatchThreshold, atoi(e)));
+    if (count < kBatchThreshold || !run_applies(s)) {
+        for (int i = 0; i < count; ++i) N3_CALL(rn_n3_session_push(s, tokens[i]));
+        return RN_OK;
+    }
+    for (int i = 0; i < count; i += chunk) {
+        const int n = std::min(chunk, count - i);
+        if (n >= kBatchThreshold) {
+            N3_CALL(enqueue_run(s, tokens + i, n));
+        } else {
+            for (int j = 0; j < n; ++j) N3_CALL(rn_n3_session_push(s, tokens[i + j]));
+        }
+    }
     return RN_OK;
 }
 

@@ -110,3 +110,37 @@ def test_errors(archive):
         s.push(5)
     with pytest.raises(rn.RnError):
         needle3.Model(archive, depth=1)
+
+
+def _compare_all(gs, os_, gm, label):
+    assert len(gs) == len(os_), label
+    assert np.array_equal(_bits(gs.hidden()), _bits(os_.hidden())), f"hidden {label}"
+    assert np.array_equal(_bits(gs.cells()), _bits(os_.cells())), f"cells {label}"
+    _compare_session(gs, os_, label)
+    for layer in gm.active:
+        for a, b in zip(gs.cache(layer), os_.cache(layer)):
+            assert a.shape == b.shape and np.array_equal(a.view(np.uint8), b.view(np.uint8)), (label, layer)
+
+
+@pytest.mark.parametrize("chunk", [4, 7, 256])
+@pytest.mark.parametrize("depth", [0, 2])
+def test_batched_feed_bit_exact(archive, depth, chunk, monkeypatch):
+    """Session::feed's batched prefill (prefill.rs:10-99): runs of up to
+    `chunk` tokens (a last run under four tokens pushed), against the oracle
+    pushing the same tokens, after each of three feeds (21 tokens, 3 tokens,
+    which are pushed, then 30, past the 16-token window); with chunks of 4 and
+    7 the conv-tap and engram rings (3 and 5 positions) cross run boundaries."""
+    monkeypatch.delenv("RN_N3_PATH", raising=False)
+    monkeypatch.setenv("RN_N3_FEED_CHUNK", str(chunk))
+    gm, om = needle3.Model(archive, depth), oracle.OracleNeedle3(archive, depth)
+    gs, os_ = gm.session(64), om.session(64)
+    tokens = _tokens(54, seed=17)
+    for a, b in ((0, 21), (21, 24), (24, 54)):
+        print(f"needle3 batched feed depth {depth} chunk {chunk} tokens {a}..{b}", flush=True)
+        gs.feed(tokens[a:b])
+        os_.feed(tokens[a:b])
+        _compare_all(gs, os_, gm, f"depth {depth} chunk {chunk} after {b}")
+    # the session goes on by pushes and greedy decoding from the fed state
+    ids = gs.decode_greedy(5, 6)
+    assert ids.tolist() == os_.greedy(5, 6).tolist()
+    _compare_all(gs, os_, gm, f"depth {depth} chunk {chunk} after greedy")

@@ -98,3 +98,33 @@ def test_batch64_ragged_32_steps_full_model(needle):
         o = ref[i][2]
         assert np.array_equal(k.view(np.uint16), o.keys[:, :, :n]), i
         assert np.array_equal(v.view(np.uint16), o.values[:, :, :n]), i
+
+
+def test_needle3_full_size_feed_equals_pushes(monkeypatch):
+    """The Needle 3 block at its documented shape (d_model 768, 20 layers, 12
+    heads over 4 kv heads, four lanes, two engram sites, a 1024 window with
+    four global layers): a 300-token feed (a 256-token run, then 44) leaves
+    the same state, bit for bit, as 300 pushes (each push is pinned to the
+    oracle in test_gpu_needle3.py); then 8 greedy tokens from both."""
+    from rustyneedle_amd import needle3
+    monkeypatch.delenv("RN_N3_PATH", raising=False)
+    monkeypatch.delenv("RN_N3_FEED_CHUNK", raising=False)
+    g = needle3.NEEDLE3
+    model = needle3.Model(needle3.synthetic_archive(g))
+    tokens = rn.synth_tokens(rn.SEED, "needle3.feed", g["vocab"], (300,))
+    fed, pushed = model.session(320), model.session(320)
+    print("needle3 full-size feed of 300 tokens", flush=True)
+    fed.feed(tokens)
+    print("needle3 full-size 300 pushes", flush=True)
+    for t in tokens:
+        pushed.push(int(t))
+    bits = lambda a: np.ascontiguousarray(a, np.float32).view(np.uint32)
+    assert np.array_equal(bits(fed.hidden()), bits(pushed.hidden()))
+    assert np.array_equal(bits(fed.cells()), bits(pushed.cells()))
+    assert np.array_equal(bits(fed.logits()), bits(pushed.logits()))
+    for code in (1, 2):
+        assert np.array_equal(bits(fed.pooled_readout(code)), bits(pushed.pooled_readout(code))), code
+    for layer in (0, 1, 10, 19):
+        for a, b in zip(fed.cache(layer), pushed.cache(layer)):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), layer
+    assert fed.decode_greedy(7, 8).tolist() == pushed.decode_greedy(7, 8).tolist()
