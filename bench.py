@@ -357,8 +357,10 @@ def bench_needle3(rn, with_cpu: bool = True, context: int = 600, steps: int = 64
     (d_model 768, 20 layers, 12 heads over 4 kv heads, four lanes, two engram
     sites, 32 x 32 Hadamard factors, 2-bit projections, 4-bit 8192 x 768
     logits) from a synthetic archive: a 600-token feed, then greedy decode
-    (push, logits, argmax) at that context, HIP events on the session's stream;
-    the first pushes checked bit for bit against the oracle."""
+    (push, logits, argmax) at that context; a 4000-token feed; greedy decode
+    after 1100 tokens (the reference bench's `decode --context 600`, `prefill
+    --tokens 4000`); HIP events on the session's stream; the first pushes
+    checked bit for bit against the oracle."""
     import oracle
     from rustyneedle_amd import needle3
     archive = needle3.synthetic_archive(needle3.NEEDLE3)
@@ -383,10 +385,32 @@ def bench_needle3(rn, with_cpu: bool = True, context: int = 600, steps: int = 64
     s.decode_greedy(int(prompt[-1]), steps)
     t3.record(stream)
     feed_ms, dec_ms = t0.elapsed_ms(t1), t2.elapsed_ms(t3)
+    del s
+    # the reference's other two figures: a 4000-token prefill, and decode at
+    # 1100 tokens of context
+    long_prompt = rn.synth_tokens(rn.SEED, "needle3.prompt4000", needle3.NEEDLE3["vocab"], (4000,))
+    s = model.session(4000 + 8)
+    stream = s.stream()
+    t0.record(stream)
+    s.feed(long_prompt)
+    t1.record(stream)
+    feed4000_ms = t0.elapsed_ms(t1)
+    del s
+    s = model.session(1100 + steps + 8)
+    stream = s.stream()
+    s.feed(long_prompt[:1100])
+    s.decode_greedy(int(long_prompt[1099]), 4)
+    t2.record(stream)
+    s.decode_greedy(int(long_prompt[1099]), steps)
+    t3.record(stream)
+    dec1100_ms = t2.elapsed_ms(t3)
+    del s
     out = dict(decode_tokens_per_s=steps / (dec_ms / 1e3), decode_ms_per_token=dec_ms / steps, context=context + 4,
-               feed_tokens_per_s=context / (feed_ms / 1e3), layers=needle3.NEEDLE3["num_layers"],
-               d_model=needle3.NEEDLE3["d_model"], bit_identical=identical,
-               reference_published="decode about 830-860 tokens/s at 600 tokens of context on an Apple M1 Max "
+               feed_tokens_per_s=context / (feed_ms / 1e3), feed_4000_tokens_per_s=4000 / (feed4000_ms / 1e3),
+               feed_4000_ms=feed4000_ms, decode_1100_tokens_per_s=steps / (dec1100_ms / 1e3),
+               layers=needle3.NEEDLE3["num_layers"], d_model=needle3.NEEDLE3["d_model"], bit_identical=identical,
+               reference_published="decode about 830-860 tokens/s at 600 tokens of context, about 720 at 1100; "
+                                   "prefill of 4000 tokens about 1800 tokens/s; on an Apple M1 Max "
                                    "(docs/architecture.md, Performance)")
     if with_cpu:
         oracle.set_threads(1)

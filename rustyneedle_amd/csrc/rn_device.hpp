@@ -147,6 +147,40 @@ __device__ __forceinline__ float lane_float(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// The value of lane (this lane ^ M) of a wave, M a power of two up to 32,
+// without an LDS round trip: quad_perm for 1 and 2, row rotations by 4 and 12
+// (bit 2 picks) and by 8 inside rows of 16, the gfx950 lane swaps for 16
+// (v_permlane16_swap: odd rows read the first result, even rows the second)
+// and 32 (v_permlane32_swap: the upper half reads the first result, the lower
+// the second). Every lane of the wave must be active (a DPP source lane that
+// is off yields the lane's own value).
+template <int M>
+__device__ __forceinline__ int lane_xor_i(int v) {
+    if constexpr (M == 1) {
+        return dpp_move<0xb1>(v);
+    } else if constexpr (M == 2) {
+        return dpp_move<0x4e>(v);
+    } else if constexpr (M == 4) {
+        const int a = dpp_move<0x124>(v), b = dpp_move<0x12c>(v), m = -(((int)threadIdx.x >> 2) & 1);
+        return (a & m) | (b & ~m);
+    } else if constexpr (M == 8) {
+        return dpp_move<0x128>(v);
+    } else if constexpr (M == 16) {
+        const auto s = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        const int m = -(((int)threadIdx.x >> 4) & 1);
+        return ((int)s[0] & m) | ((int)s[1] & ~m);
+    } else {
+        static_assert(M == 32, "lane_xor: 1, 2, 4, 8, 16 or 32");
+        const auto s = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+        const int m = -(((int)threadIdx.x >> 5) & 1);
+        return ((int)s[0] & m) | ((int)s[1] & ~m);
+    }
+}
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+    return __int_as_float(lane_xor_i<M>(__float_as_int(v)));
+}
+
 // Maximum over the 64 lanes of a full wave, the same in every lane. The
 // maximum is order-free, so any reduction order gives the same value.
 __device__ __forceinline__ float wave_max(float v) {

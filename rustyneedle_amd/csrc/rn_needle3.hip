@@ -66,15 +66,23 @@ constexpr int kN3Hadamard = 1024;     // 32 x 32
 
 namespace {
 
-// The maximum over the block (every thread calls; all get the result).
+// The maximum over the block (every thread calls; all get the result). With
+// TAIL false the caller's next barrier must come before red is written again.
+template <bool TAIL = true>
 __device__ float n3_block_max(float v, float* red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = (blockDim.x + 63) >> 6;
     v = wave_max(v);
     if (lane == 0) red[wave] = v;
     __syncthreads();
-    float r = red[0];
-    for (int w = 1; w < waves; ++w) r = fmaxf(r, red[w]);
-    __syncthreads();
+    // the waves' maxima (at most 16) on a row of lanes (the rest repeat the
+    // last), joined inside the row
+    float r = red[min(lane, waves - 1)];
+    r = fmaxf(r, lane_xor<1>(r));
+    r = fmaxf(r, lane_xor<2>(r));
+    r = fmaxf(r, lane_xor<4>(r));
+    r = fmaxf(r, lane_xor<8>(r));
+    r = lane_float(r, 0);
+    if (TAIL) __syncthreads();
     return r;
 }
 
@@ -172,9 +180,10 @@ __device__ void n3_unit_rms(const float* x, int n, float* out, float* red, float
 __device__ void n3_fake_quantise(float* v, int n, float* red) {
     float peak = 0.0f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) peak = fmaxf(peak, fabsf(v[i]));
-    peak = n3_block_max(peak, red);
+    peak = n3_block_max<false>(peak, red);  // red is next written after the barrier below
     const float scale = int8_scale_from_peak(peak);
     for (int base = 0; base < n; base += blockDim.x) {
+        if (base + (int)(threadIdx.x & ~63u) >= n) break;  // a wave past the values
         const int i = base + threadIdx.x;
         const float x = v[min(i, n - 1)];
         float y;
@@ -1077,6 +1086,17 @@ __device__ __forceinline__ int4 n3_pack_codes(const int (&c)[16], int ib) {
                                n3_b4(c[8], c[10], c[12], c[14]), n3_b4(c[9], c[11], c[13], c[15]));
 }
 
+// One butterfly level across lanes: partner lane L ^ M holds the other half
+// of each pair (low a + b, high a - b, walsh.rs:41-76).
+template <int M>
+__device__ __forceinline__ void n3_butterfly_lanes(float (&x)[4], bool high) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float q = lane_xor<M>(x[e]);
+        x[e] = high ? q - x[e] : x[e] + q;
+    }
+}
+
 // prepare and the per-group codes in one pass (matrix.rs:123-128 then
 // panel.rs:52-66) over v [P] in LDS (zero past the columns), four lanes per
 // run of 16 (groups of at most 256): lane L holds elements 4L .. 4L + 3 of v;
@@ -1085,11 +1105,13 @@ __device__ __forceinline__ int4 n3_pack_codes(const int (&c)[16], int ib) {
 // scales, the group's peak over its group / 4 lanes, quotients without a
 // division (quotients<4>: the codes of quantise_one), then the run's four
 // lanes (a quad) exchange their codes by DPP broadcasts so that lane d of the
-// run writes dword d of its plane-order int4.
+// run writes dword d of its plane-order int4. The exchanges between lanes are
+// DPP moves and lane swaps (lane_xor), with every lane of the block active.
 __device__ __forceinline__ void n3_prepare_codes(const float* v, int P, int group, float wht_scale, int ib, int4* xq, float* xs) {
     const int lanes = P / 4, lpg = group / 4;
     int* xqw = reinterpret_cast<int*>(xq);
     for (int base = 0; base < lanes; base += blockDim.x) {
+        if (base + (int)(threadIdx.x & ~63u) >= lanes) break;  // a wave past the runs
         const int L = base + threadIdx.x;
         const bool valid = L < lanes;
         const float4 t = reinterpret_cast<const float4*>(v)[valid ? L : 0];
@@ -1104,21 +1126,24 @@ __device__ __forceinline__ void n3_prepare_codes(const float* v, int P, int grou
         x[2] = a0 - b0;
         x[1] = a1 + b1;
         x[3] = a1 - b1;
-        for (int m = 1; m < lpg; m <<= 1) {
-            const bool high = (L & m) != 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float q = __shfl_xor(x[e], m, 64);
-                x[e] = high ? q - x[e] : x[e] + q;
-            }
-        }
+        if (lpg > 1) n3_butterfly_lanes<1>(x, (L & 1) != 0);
+        if (lpg > 2) n3_butterfly_lanes<2>(x, (L & 2) != 0);
+        if (lpg > 4) n3_butterfly_lanes<4>(x, (L & 4) != 0);
+        if (lpg > 8) n3_butterfly_lanes<8>(x, (L & 8) != 0);
+        if (lpg > 16) n3_butterfly_lanes<16>(x, (L & 16) != 0);
+        if (lpg > 32) n3_butterfly_lanes<32>(x, (L & 32) != 0);
         float peak = 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             x[e] = x[e] * wht_scale;
             peak = fmaxf(peak, fabsf(x[e]));
         }
-        for (int m = 1; m < lpg; m <<= 1) peak = fmaxf(peak, __shfl_xor(peak, m, 64));
+        if (lpg > 1) peak = fmaxf(peak, lane_xor<1>(peak));
+        if (lpg > 2) peak = fmaxf(peak, lane_xor<2>(peak));
+        if (lpg > 4) peak = fmaxf(peak, lane_xor<4>(peak));
+        if (lpg > 8) peak = fmaxf(peak, lane_xor<8>(peak));
+        if (lpg > 16) peak = fmaxf(peak, lane_xor<16>(peak));
+        if (lpg > 32) peak = fmaxf(peak, lane_xor<32>(peak));
         const float scale = int8_scale_from_peak(peak);
         float y[4];
         quotients<4>(x, scale, y);
@@ -1207,48 +1232,46 @@ __device__ void n3_stage_rows(const CodebookParams& c, RowOf row_of, int R, uint
 // one input quantised per group in LDS (xq, xs): exact group sums of level *
 // code, then per row the epilogue over the groups in order. Lane l of every
 // wave holds the codes of run u = l (+ 64 per pass) in registers; the waves
-// take the rows in turn, four at a time. A group's runs sit on aligned lanes
-// and join by DPP.
-template <int IB>
+// take the rows in turn, KR at a time. A group's runs sit on aligned lanes
+// and join by DPP. No branch inside the loops but uniform ones: groups past
+// the row's last add an exact zero (level, norm and scale all zero).
+template <int IB, int KR>
 __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R, const int4* xq,
                            const float* xs, int* acc, float* y) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     const int runs = c.padded / 16, rpg = c.group / 16, G = c.padded / c.group;
     const int rpg_shift = rpg == 4 ? 2 : (rpg == 8 ? 3 : 4);
-    // rows a wave takes at a time: four, or fewer when the rows do not fill the waves
-    const int kr = min(4, (R + waves - 1) / waves);
     const uint32_t lut[4] = {c.lut[0], c.lut[1], c.lut[2], c.lut[3]};
     for (int u0 = 0; u0 < runs; u0 += 64) {
         const int u = u0 + lane;
         const bool live = u < runs;
-        const int4 x = live ? xq[u] : make_int4(0, 0, 0, 0);
-        const uint8_t* base = w + (size_t)(live ? u : 0) * 2 * IB;
+        int4 x = xq[min(u, runs - 1)];
+        if (!live) x = make_int4(0, 0, 0, 0);
+        const uint8_t* base = w + (size_t)min(u, runs - 1) * 2 * IB;
         const bool leader = live && (u & (rpg - 1)) == 0;
-        for (int r0 = wave; r0 < R; r0 += kr * waves) {
-            // the kr rows' words first (rows past R repeat the last; a lane past
+        for (int r0 = wave; r0 < R; r0 += KR * waves) {
+            // the KR rows' words first (rows past R repeat the last; a lane past
             // the runs has zero codes, so its sums are zero), then the sums
-            int sum[4];
+            int sum[KR];
             if constexpr (IB == 2) {
-                uint32_t wd[4];
+                uint32_t wd[KR];
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (k < kr) wd[k] = *reinterpret_cast<const uint32_t*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
+                for (int k = 0; k < KR; ++k)
+                    wd[k] = *reinterpret_cast<const uint32_t*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    if (k >= kr) break;
+                for (int k = 0; k < KR; ++k) {
                     int sm = dot4(n3_decode4<2>(wd[k] & 0x03030303u, lut), x.x, 0);
                     sm = dot4(n3_decode4<2>((wd[k] >> 2) & 0x03030303u, lut), x.y, sm);
                     sm = dot4(n3_decode4<2>((wd[k] >> 4) & 0x03030303u, lut), x.z, sm);
                     sum[k] = dot4(n3_decode4<2>((wd[k] >> 6) & 0x03030303u, lut), x.w, sm);
                 }
             } else {
-                uint2 wd[4];
+                uint2 wd[KR];
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (k < kr) wd[k] = *reinterpret_cast<const uint2*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
+                for (int k = 0; k < KR; ++k)
+                    wd[k] = *reinterpret_cast<const uint2*>(base + (size_t)min(r0 + k * waves, R - 1) * c.row_bytes);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    if (k >= kr) break;
+                for (int k = 0; k < KR; ++k) {
                     int sm = dot4(n3_decode4<4>(wd[k].x & 0x0f0f0f0fu, lut), x.x, 0);
                     sm = dot4(n3_decode4<4>((wd[k].x >> 4) & 0x0f0f0f0fu, lut), x.y, sm);
                     sm = dot4(n3_decode4<4>(wd[k].y & 0x0f0f0f0fu, lut), x.z, sm);
@@ -1256,19 +1279,26 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
                 }
             }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (k >= kr) break;
+            for (int k = 0; k < KR; ++k) {
                 int v = sum[k];
                 v = v + dpp_move<0xb1>(v);
                 v = v + dpp_move<0x4e>(v);
-                if (rpg >= 8) v = v + dpp_move<0x141>(v);
-                if (rpg >= 16) v = v + dpp_move<0x140>(v);
+                const int v8 = dpp_move<0x141>(v);
+                v = rpg >= 8 ? v + v8 : v;
+                const int v16 = dpp_move<0x140>(v);
+                v = rpg >= 16 ? v + v16 : v;
+                sum[k] = v;
+            }
+#pragma unroll
+            for (int k = 0; k < KR; ++k) {
                 const int r = r0 + k * waves;
-                if (leader && r < R) acc[r * G + (u >> rpg_shift)] = v;
+                if (leader && r < R) acc[r * G + (u >> rpg_shift)] = sum[k];
             }
         }
     }
     __syncthreads();
+    const bool fma_form = c.bits == 2;  // panel.rs:184-188; else neon.rs:158,180
+    const float lscale = c.lscale;
     for (int r = threadIdx.x; r < R; r += blockDim.x) {
         float t = 0.0f;
         for (int g0 = 0; g0 < G; g0 += 8) {
@@ -1276,17 +1306,17 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const int g = min(g0 + k, G - 1);
-                nv[k] = __half2float(__ushort_as_half(nm[r * G + g]));
-                av[k] = (float)acc[r * G + g];
-                sv[k] = xs[g];
+                const bool in = g0 + k < G;
+                nv[k] = in ? __half2float(__ushort_as_half(nm[r * G + g])) : 0.0f;
+                av[k] = in ? (float)acc[r * G + g] : 0.0f;
+                sv[k] = in ? xs[g] : 0.0f;
             }
+            if (fma_form) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                if (g0 + k >= G) break;
-                if (c.bits == 2)
-                    t = fmaf(av[k], (nv[k] * c.lscale) * sv[k], t);  // panel.rs:184-188
-                else
-                    t = t + (((av[k] * nv[k]) * c.lscale) * sv[k]);  // neon.rs:158,180
+                for (int k = 0; k < 8; ++k) t = fmaf(av[k], (nv[k] * lscale) * sv[k], t);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) t = t + (((av[k] * nv[k]) * lscale) * sv[k]);
             }
         }
         y[r] = t;
@@ -1294,12 +1324,24 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
     __syncthreads();
 }
 
+template <int IB>
+__device__ __forceinline__ void n3_rows_kr(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R,
+                                           const int4* xq, const float* xs, int* acc, float* y) {
+    const int waves = blockDim.x >> 6, kr = (R + waves - 1) / waves;
+    if (kr <= 1)
+        n3_rows_ib<IB, 1>(c, w, nm, R, xq, xs, acc, y);
+    else if (kr <= 2)
+        n3_rows_ib<IB, 2>(c, w, nm, R, xq, xs, acc, y);
+    else
+        n3_rows_ib<IB, 4>(c, w, nm, R, xq, xs, acc, y);
+}
+
 __device__ void n3_rows(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R, const int4* xq,
                         const float* xs, int* acc, float* y) {
     if (c.bits == 4)
-        n3_rows_ib<4>(c, w, nm, R, xq, xs, acc, y);
+        n3_rows_kr<4>(c, w, nm, R, xq, xs, acc, y);
     else
-        n3_rows_ib<2>(c, w, nm, R, xq, xs, acc, y);
+        n3_rows_kr<2>(c, w, nm, R, xq, xs, acc, y);
 }
 
 struct N3AttentionParams {
