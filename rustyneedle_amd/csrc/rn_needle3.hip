@@ -1098,8 +1098,9 @@ __device__ __forceinline__ void n3_butterfly_lanes(float (&x)[4], bool high) {
 }
 
 // prepare and the per-group codes in one pass (matrix.rs:123-128 then
-// panel.rs:52-66) over v [P] in LDS (zero past the columns), four lanes per
-// run of 16 (groups of at most 256): lane L holds elements 4L .. 4L + 3 of v;
+// panel.rs:52-66) over P values (zero past the columns) that load(L, x) gives
+// four a lane, four lanes per run of 16 (groups of at most 256): lane L holds
+// elements 4L .. 4L + 3;
 // the Walsh-Hadamard butterflies (walsh.rs:41-76) of spans 1 and 2 in the lane, spans
 // 4 .. group / 2 with the partner lane L ^ (span / 4) (low a + b, high a - b),
 // scales, the group's peak over its group / 4 lanes, quotients without a
@@ -1107,15 +1108,16 @@ __device__ __forceinline__ void n3_butterfly_lanes(float (&x)[4], bool high) {
 // lanes (a quad) exchange their codes by DPP broadcasts so that lane d of the
 // run writes dword d of its plane-order int4. The exchanges between lanes are
 // DPP moves and lane swaps (lane_xor), with every lane of the block active.
-__device__ __forceinline__ void n3_prepare_codes(const float* v, int P, int group, float wht_scale, int ib, int4* xq, float* xs) {
+template <typename Load>
+__device__ __forceinline__ void n3_codes_from(Load load, int P, int group, float wht_scale, int ib, int4* xq, float* xs) {
     const int lanes = P / 4, lpg = group / 4;
     int* xqw = reinterpret_cast<int*>(xq);
     for (int base = 0; base < lanes; base += blockDim.x) {
         if (base + (int)(threadIdx.x & ~63u) >= lanes) break;  // a wave past the runs
         const int L = base + threadIdx.x;
         const bool valid = L < lanes;
-        const float4 t = reinterpret_cast<const float4*>(v)[valid ? L : 0];
-        float x[4] = {t.x, t.y, t.z, t.w};
+        float x[4];
+        load(valid ? L : 0, x);
         float a0 = x[0], b0 = x[1], a1 = x[2], b1 = x[3];
         x[0] = a0 + b0;
         x[1] = a0 - b0;
@@ -1163,6 +1165,99 @@ __device__ __forceinline__ void n3_prepare_codes(const float* v, int P, int grou
             if ((L & (lpg - 1)) == 0) xs[L / lpg] = scale;
         }
     }
+}
+
+// n3_codes_from over v [P] in LDS (16-byte aligned, zero past the columns)
+__device__ __forceinline__ void n3_prepare_codes(const float* v, int P, int group, float wht_scale, int ib, int4* xq, float* xs) {
+    n3_codes_from(
+        [&](int L, float (&x)[4]) {
+            const float4 t = reinterpret_cast<const float4*>(v)[L];
+            x[0] = t.x;
+            x[1] = t.y;
+            x[2] = t.z;
+            x[3] = t.w;
+        },
+        P, group, wht_scale, ib, xq, xs);
+}
+
+// ops.rs:120-125 for four values of a vector whose scale is known:
+// round(value / scale) clamped to the int8 range, times scale (NaN kept)
+__device__ __forceinline__ void n3_fake_quantise4(float (&x)[4], float scale) {
+    float y[4];
+    quotients<4>(x, scale, y);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float q = __builtin_rintf(y[e]);
+        q = q < -128.0f ? -128.0f : (q > 127.0f ? 127.0f : q);
+        x[e] = q * scale;
+    }
+}
+
+// zero_centred_norm (GAIN: ops.rs:44-50) or unit_rms (ops.rs:60-66) of v [n]
+// in LDS, then fake_quantise_int8 (ops.rs:120-125), then prepare and the codes
+// (n3_codes_from), without writing the normalised vector: one pass computes
+// the squares for the eight chains of ops.rs:7-17 and the peak of m_i = (1 +
+// gain_i) * v_i (v_i without the gain); since rounding is monotone, the peak
+// of the normalised m_i * inverse is fl(peak_m * inverse) exactly, so the
+// quantisation scale is known when the inverse is. v and gain 16-byte aligned,
+// n a multiple of 32 (the eight chains' squares four a read), sq LDS scratch of
+// n + 64 floats, red of at least 32.
+template <bool GAIN>
+__device__ void n3_norm_codes(const float* v, const float* gain, int n, float* red, float* sq, int P, int group,
+                              float wht_scale, int ib, int4* xq, float* xs) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6, n8 = n / 8;
+    const int stride = n8 + 8;
+    float pk = 0.0f;
+    for (int i = tid; i < n; i += blockDim.x) {
+        const float x = v[i];
+        sq[(i & 7) * stride + (i >> 3)] = x * x;
+        pk = fmaxf(pk, fabsf(GAIN ? (1.0f + gain[i]) * x : x));
+    }
+    pk = wave_max(pk);
+    if (lane == 0) red[16 + wave] = pk;
+    __syncthreads();
+    if (tid < 8) {
+        const float4* q = reinterpret_cast<const float4*>(sq + tid * stride);
+        float s = 0.0f;
+#pragma unroll 8
+        for (int k = 0; k < n8 / 4; ++k) {
+            const float4 t = q[k];
+            s = s + t.x;
+            s = s + t.y;
+            s = s + t.z;
+            s = s + t.w;
+        }
+        red[tid] = s;
+    }
+    __syncthreads();
+    float total = 0.0f;
+    for (int j = 0; j < 8; ++j) total = total + red[j];
+    const float inverse = 1.0f / sqrtf(total / (float)n + 1e-6f);
+    float r = red[16 + min(lane, waves - 1)];
+    r = fmaxf(r, lane_xor<1>(r));
+    r = fmaxf(r, lane_xor<2>(r));
+    r = fmaxf(r, lane_xor<4>(r));
+    r = fmaxf(r, lane_xor<8>(r));
+    const float scale = int8_scale_from_peak(lane_float(r, 0) * inverse);
+    n3_codes_from(
+        [&](int L, float (&x)[4]) {
+            const float4 t = reinterpret_cast<const float4*>(v)[L];
+            x[0] = t.x;
+            x[1] = t.y;
+            x[2] = t.z;
+            x[3] = t.w;
+            if (GAIN) {
+                const float4 g = reinterpret_cast<const float4*>(gain)[L];
+                x[0] = (1.0f + g.x) * x[0];
+                x[1] = (1.0f + g.y) * x[1];
+                x[2] = (1.0f + g.z) * x[2];
+                x[3] = (1.0f + g.w) * x[3];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = 4 * L + e < n ? x[e] * inverse : 0.0f;  // fake quantised: still zero
+            n3_fake_quantise4(x, scale);
+        },
+        P, group, wht_scale, ib, xq, xs);
 }
 
 // Per-group int8 codes of an LDS input (panel.rs:52-66): scale = peak / 127 (1
@@ -1685,10 +1780,31 @@ __global__ __launch_bounds__(1024) void n3_out_kernel(N3OutParams p) {
         if (j * T + tid < units) reinterpret_cast<int4*>(w_s)[j * T + tid] = rw[j];
     if (tid < nn) reinterpret_cast<int4*>(nm_s)[tid] = rn;
     if (tid < n4) reinterpret_cast<float4*>(v)[tid] = a;
-    for (int i = p.n + tid; i < P; i += T) v[i] = 0.0f;
+    // the peak of the attention from the registers (ops.rs:32-43, order-free)
+    {
+        float pk = tid < n4 ? fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))) : 0.0f;
+        pk = wave_max(pk);
+        if ((tid & 63) == 0) red[tid >> 6] = pk;
+    }
     __syncthreads();
-    n3_fake_quantise(v, p.n, red);
-    n3_prepare_codes(v, P, p.out.group, p.out.wht_scale, p.out.bits == 5 ? 2 : p.out.bits, xq, xs);
+    // fake_quantise_int8 (ops.rs:120-125) as the values are loaded for prepare and the codes
+    float peak = red[min(tid & 63, T / 64 - 1)];
+    peak = fmaxf(peak, lane_xor<1>(peak));
+    peak = fmaxf(peak, lane_xor<2>(peak));
+    peak = fmaxf(peak, lane_xor<4>(peak));
+    peak = fmaxf(peak, lane_xor<8>(peak));
+    const float scale = int8_scale_from_peak(lane_float(peak, 0));
+    const int n = p.n;
+    n3_codes_from(
+        [&](int L, float (&x)[4]) {
+            const float4 t = reinterpret_cast<const float4*>(v)[L];
+            x[0] = 4 * L < n ? t.x : 0.0f;
+            x[1] = 4 * L + 1 < n ? t.y : 0.0f;
+            x[2] = 4 * L + 2 < n ? t.z : 0.0f;
+            x[3] = 4 * L + 3 < n ? t.w : 0.0f;
+            n3_fake_quantise4(x, scale);
+        },
+        P, p.out.group, p.out.wht_scale, p.out.bits == 5 ? 2 : p.out.bits, xq, xs);
     __syncthreads();
     n3_rows(p.out, w_s, nm_s, R, xq, xs, acc, y_s);
     if (tid < R) p.y[r0 + tid] = y_s[tid];
@@ -1873,16 +1989,12 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     norm_in_r[0] = tid < d ? p.norm_in[tid] : 0.0f;
     key_r[0] = (e_key != nullptr && tid < d) ? e_key[tid] : 0.0f;
     value_r[0] = (e_key != nullptr && tid < d) ? e_value[tid] : 0.0f;
-    // lanes.rs:49-53: unit_rms, fake_quantise_int8, prepare (phi_pre's groups)
-    n3_unit_rms(stream_s, S, rv, red, cv_);
-    n3_fake_quantise(rv, S, red);
-    const int P = p.phi_pre.padded;
-    for (int i = S + tid; i < P; i += blockDim.x) rv[i] = 0.0f;
-    __syncthreads();
+    // lanes.rs:49-53: unit_rms, fake_quantise_int8, prepare (phi_pre's groups);
     // the routing matrices share their format, so one set of codes serves the
     // three (matrix.rs:167-193 shares a plane input per format)
+    const int P = p.phi_pre.padded;
     const int ib_pre = p.phi_pre.bits == 5 ? 2 : p.phi_pre.bits;
-    n3_prepare_codes(rv, P, p.phi_pre.group, p.phi_pre.wht_scale, ib_pre, rq, rs);
+    n3_norm_codes<false>(stream_s, nullptr, S, red, cv_, P, p.phi_pre.group, p.phi_pre.wht_scale, ib_pre, rq, rs);
     __syncthreads();
     // lanes.rs:56-63: the layer's rows of the three routing matrices
     n3_rows(p.phi_pre, pw, pn, route_rows, rq, rs, racc, ry);
@@ -1976,15 +2088,15 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     }
     if (tid < d) mx_[tid] = norm_in_r[0];
     __syncthreads();
-    n3_norm(xs_, mx_, d, a_, red, cv_);
-    n3_fake_quantise(a_, d, red);
-    for (int i = d + tid; i < p.qpadded; i += blockDim.x) a_[i] = 0.0f;
-    __syncthreads();
     if (out_rotated != nullptr) {
+        n3_norm(xs_, mx_, d, a_, red, cv_);
+        n3_fake_quantise(a_, d, red);
+        for (int i = d + tid; i < p.qpadded; i += blockDim.x) a_[i] = 0.0f;
+        __syncthreads();
         n3_rotate(a_, p.qpadded, p.qgroup, p.qscale);
         for (int i = tid; i < p.qpadded; i += blockDim.x) out_rotated[i] = a_[i];
     } else {
-        n3_prepare_codes(a_, p.qpadded, p.qgroup, p.qscale, p.qib, p.codes, p.code_scales);
+        n3_norm_codes<true>(xs_, mx_, d, red, cv_, p.qpadded, p.qgroup, p.qscale, p.qib, p.codes, p.code_scales);
     }
     for (int i = tid; i < d; i += blockDim.x) out_x[i] = xs_[i];
 }
@@ -2274,8 +2386,10 @@ bool fused_applies(const rn_n3_model* m) {
     if (m->phi_pre->group > 256) return false;
     if ((2 * L + L * L) * (m->phi_pre->cb.padded / m->phi_pre->group) > kN3Block) return false;
     // the layer boundary stages the factors and cond_v, three vectors, the
-    // stream and the routing rows in 16-byte units, at most 384 a wave
+    // stream and the routing rows in 16-byte units, at most 384 a wave; its
+    // norms take squares four a read (d a multiple of 32)
     const int d = (int)g.d_model;
+    if (d % 32 != 0) return false;
     if (m->phi_pre->cb.row_bytes % 16 != 0) return false;
     const int waves = (6 * kN3Hadamard + 8 * d + 1535) / 1536 + (3 * d + 1535) / 1536 + (L * d + 1535) / 1536 +
                       ((2 * L + L * L) * (int)(m->phi_pre->cb.row_bytes / 16) + 383) / 384;
