@@ -48,6 +48,7 @@
 #include <algorithm>
 #include <new>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/rustyneedle.h"
@@ -249,10 +250,6 @@ __device__ void n3_copy(float* dst, const float* src, int n) {
 // ---- kernels ---------------------------------------------------------------
 
 // tokens[position] = *source, or the host's token when source is null
-__global__ void n3_set_token_kernel(uint32_t* tokens, int position, uint32_t token, const uint32_t* source) {
-    if (threadIdx.x == 0) tokens[position] = source != nullptr ? *source : token;
-}
-
 constexpr int kN3FeedChunk = 256;  // tokens a batched feed runs together
 
 // the ids of a run of tokens, passed by value
@@ -269,16 +266,20 @@ __global__ void n3_set_tokens_kernel(uint32_t* tokens, int position, int count, 
 // in registers, lane u holding run u) times sqrt(d) into every lane; cell 0 is
 // their lane mean (session.rs:190-200). One block of 64 * ceil(runs / 64) a
 // token: block b embeds position + b into stream + b * stream_stride and
-// cell + b * cell_stride (prefill.rs:21-29 for a run of tokens).
-__global__ __launch_bounds__(1024) void n3_embed_kernel(CodebookParams c, const uint32_t* tokens, int position, int d,
+// cell + b * cell_stride (prefill.rs:21-29 for a run of tokens). With `set`
+// (one token) the token is *source (the greedy argmax) or `value`, and the
+// block records it at tokens[position].
+__global__ __launch_bounds__(1024) void n3_embed_kernel(CodebookParams c, uint32_t* tokens, int position, int d,
                                                         int lanes, float scale, float* stream, float* cell,
-                                                        int stream_stride, int cell_stride) {
+                                                        int stream_stride, int cell_stride, int set,
+                                                        const uint32_t* source, uint32_t value) {
     const int u = threadIdx.x, runs = c.padded / 16, rpg = c.group / 16, G = c.padded / c.group;
     const int ib = c.bits == 5 ? 2 : c.bits;
     const bool valid = u < runs;
     stream += (size_t)blockIdx.x * stream_stride;
     cell += (size_t)blockIdx.x * cell_stride;
-    const uint32_t token = tokens[position + blockIdx.x];
+    const uint32_t token = set ? (source != nullptr ? *source : value) : tokens[position + blockIdx.x];
+    if (set && u == 0) tokens[position] = token;
     const uint8_t* row = c.packed + (size_t)token * c.row_bytes;
     const float norm = valid ? __half2float(__ushort_as_half(c.norms[(size_t)token * G + (16 * u) / c.group])) : 0.0f;
     float x[16];
@@ -293,14 +294,19 @@ __global__ __launch_bounds__(1024) void n3_embed_kernel(CodebookParams c, const 
                 x[i] = a + b;
                 x[i + span] = a - b;
             }
-    for (int m = 1; m < rpg; m <<= 1) {
-        const bool high = (u & m) != 0;
+    // spans 16 .. group / 2 with the partner lane u ^ (span / 16) (every lane active)
+    auto level = [&](auto m) {
+        const bool high = (u & decltype(m)::value) != 0;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float q = __shfl_xor(x[i], m, 64);
+            const float q = lane_xor<decltype(m)::value>(x[i]);
             x[i] = high ? q - x[i] : x[i] + q;
         }
-    }
+    };
+    if (rpg > 1) level(std::integral_constant<int, 1>{});
+    if (rpg > 2) level(std::integral_constant<int, 2>{});
+    if (rpg > 4) level(std::integral_constant<int, 4>{});
+    if (rpg > 8) level(std::integral_constant<int, 8>{});
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int e = 16 * u + i;
@@ -793,6 +799,10 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
     if (tid < d) xs[tid] = xs[tid] + p.gate * a[tid];
     __syncthreads();
     n3_norm_gain(xs, pre.pre_gain, d, a, red, st);  // a = pre
+    if (staged) {  // the factors and cond_v, copied into LDS as the tail began
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
     // condition weights (hadamard.rs:57-79): the products value * factor by
     // every thread (in place over cv), then the 32 chains (lane j of rank r:
     // rows 4k + j in order) only add
@@ -1841,6 +1851,12 @@ struct N3BoundaryParams {
     // (matrix.rs:123-128) instead of as codes; the last block writes hidden
     float* rotated;
     int cell_stride;
+    // with the final norm: the logits' input (fake_quantise_int8 of the hidden
+    // state, then prepare for the embedding matrix: session.rs:151-165) into
+    // logits_in [lpadded] as well
+    float* logits_in;
+    int lpadded, lgroup;
+    float lwht;
 };
 
 constexpr int kN3RouteRows = 24;         // 2 lanes + lanes^2 for four lanes
@@ -1896,40 +1912,28 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     N3TailPre pre{};
     const bool cv_staged = p.tail && t.rank == 8;
     float* const cv_ = tailw_s + 6 * kN3Hadamard;
-    // the inputs in four ranges, each loaded by waves of its own (at most 384
-    // 16-byte units a wave, six a lane, all requested before the first LDS
-    // store): the factors and cond_v, the projection output with x and the
-    // routed input, the stream, the route layer's rows
-    {
-        const int u0 = p.tail ? (6 * kN3Hadamard + (cv_staged ? 8 * d : 0)) / 4 : 0, u1 = p.tail ? 3 * d / 4 : 0;
-        const int u2 = S / 4, u3 = p.route ? route_rows * chunks : 0;
-        const int n0 = (u0 + 383) / 384, n1 = (u1 + 383) / 384, n2 = (u2 + 383) / 384, n3 = (u3 + 383) / 384;
-        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-        const int j = wave < n0 ? 0 : wave < n0 + n1 ? 1 : wave < n0 + n1 + n2 ? 2 : wave < n0 + n1 + n2 + n3 ? 3 : 4;
-        if (j < 4) {
-            const int w0 = j == 0 ? 0 : j == 1 ? n0 : j == 2 ? n0 + n1 : n0 + n1 + n2;
-            const int nw = j == 0 ? n0 : j == 1 ? n1 : j == 2 ? n2 : n3, cnt = j == 0 ? u0 : j == 1 ? u1 : j == 2 ? u2 : u3;
-            const int4* src = reinterpret_cast<const int4*>(
-                j == 0 ? (const void*)t.factors[0]
-                       : j == 1 ? (const void*)t.attention : j == 2 ? (const void*)(p.tail ? t.stream : in_stream) : (const void*)p.phi_rows);
-            int4* dst = reinterpret_cast<int4*>(j == 0 ? (void*)tailw_s : j == 1 ? (void*)tin_s : j == 2 ? (void*)stream_s : (void*)pw);
-            // range 1 is three vectors of d / 4 units (attention, x, input)
-            const int d4 = d / 4;
-            const int4* x4 = reinterpret_cast<const int4*>(t.x) - d4;
-            const int4* in4 = reinterpret_cast<const int4*>(t.input) - 2 * d4;
-            int4 v[6];
-#pragma unroll
-            for (int k = 0; k < 6; ++k) {
-                const int u = min((k * nw + wave - w0) * 64 + lane, cnt - 1);
-                v[k] = (j == 1 && u >= d4 ? (u >= 2 * d4 ? in4 : x4) : src)[u];
-            }
-#pragma unroll
-            for (int k = 0; k < 6; ++k) {
-                const int u = (k * nw + wave - w0) * 64 + lane;
-                if (u < cnt) dst[u] = v[k];
-            }
-        }
-    }
+    // The vectors the tail reads first (attention, x and input; the stream)
+    // through registers, two 16-byte units a thread; the later-used ranges (the
+    // factors and cond_v, the route layer's rows) go straight to LDS once these
+    // are stored, 1 KB a wave instruction, and are waited for before their first
+    // use (the condition products, the routing rows), while the tail runs.
+    const int u0 = p.tail ? (6 * kN3Hadamard + (cv_staged ? 8 * d : 0)) / 4 : 0, u1 = p.tail ? 3 * d / 4 : 0;
+    const int u2 = S / 4, u3 = p.route ? route_rows * chunks : 0, d4 = d / 4;
+    // 64-unit chunks, each inside one vector (d a multiple of 256): chunk c of
+    // wave c % 16, its source and destination uniform over the wave
+    const int cd = d4 / 64, c1 = u1 / 64, cn = (u1 + u2) / 64;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    auto chunk_src = [&](int c) {
+        const float* b = c >= c1 ? (p.tail ? t.stream : in_stream) : c < cd ? t.attention : c < 2 * cd ? t.x : t.input;
+        const int first = c >= c1 ? c1 : c < cd ? 0 : c < 2 * cd ? cd : 2 * cd;
+        return reinterpret_cast<const int4*>(b) + (c - first) * 64;
+    };
+    auto chunk_dst = [&](int c) {
+        return c >= c1 ? reinterpret_cast<int4*>(stream_s) + (c - c1) * 64 : reinterpret_cast<int4*>(tin_s) + c * 64;
+    };
+    int4 v0 = make_int4(0, 0, 0, 0), v1 = make_int4(0, 0, 0, 0);
+    if (wv < cn) v0 = chunk_src(wv)[lane];
+    if (wv + 16 < cn) v1 = chunk_src(wv + 16)[lane];
     if (p.tail) pre = n3_tail_prefetch(t);
     // the layer's norms of phi_pre, phi_post and phi_res (rows one after another)
     uint16_t tn = 0;
@@ -1955,6 +1959,22 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
         if (tid < L * L) lane_s[kMaxLanes + tid] = t.residual[tid];
     }
     if (p.route && tid < route_rows * G) pn[tid] = tn;
+    if (wv < cn) chunk_dst(wv)[lane] = v0;
+    if (wv + 16 < cn) chunk_dst(wv + 16)[lane] = v1;
+    {
+        const int c0 = (u0 + 63) / 64, c3 = (u3 + 63) / 64;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+        for (int ch = wave; ch < c0 + c3; ch += kN3Block / 64) {
+            const bool first = ch < c0;
+            const int k = first ? ch : ch - c0, cnt = first ? u0 : u3;
+            const char* src = first ? reinterpret_cast<const char*>(t.factors[0]) : reinterpret_cast<const char*>(p.phi_rows);
+            char* dst = first ? reinterpret_cast<char*>(tailw_s) : reinterpret_cast<char*>(pw);
+            const int u = 64 * k + lane;
+            if (u < cnt)
+                __builtin_amdgcn_global_load_lds((n3_global_void*)(src + (size_t)u * 16), (n3_lds_void*)(dst + (size_t)k * 1024),
+                                                 16, 0, 0);
+        }
+    }
     if (p.tail) {
         // the tail reads its copies
         for (int f = 0; f < 6; ++f) t.factors[f] = tailw_s + f * kN3Hadamard;
@@ -1982,6 +2002,14 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
         n3_norm(a_, p.final_norm, d, a_, red, cv_);
         if (blockIdx.x == gridDim.x - 1)
             for (int i = tid; i < d; i += blockDim.x) p.hidden[i] = a_[i];
+        if (p.logits_in != nullptr) {
+            n3_fake_quantise(a_, d, red);
+            for (int i = d + tid; i < p.lpadded; i += blockDim.x) a_[i] = 0.0f;
+            __syncthreads();
+            n3_rotate(a_, p.lpadded, p.lgroup, p.lwht);
+            if (blockIdx.x == gridDim.x - 1)
+                for (int i = tid; i < p.lpadded; i += blockDim.x) p.logits_in[i] = a_[i];
+        }
     }
     if (!p.route) return;
     // the block input's tensors, requested before the routing work
@@ -1995,6 +2023,7 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     const int P = p.phi_pre.padded;
     const int ib_pre = p.phi_pre.bits == 5 ? 2 : p.phi_pre.bits;
     n3_norm_codes<false>(stream_s, nullptr, S, red, cv_, P, p.phi_pre.group, p.phi_pre.wht_scale, ib_pre, rq, rs);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the routing rows, copied into LDS at the start
     __syncthreads();
     // lanes.rs:56-63: the layer's rows of the three routing matrices
     n3_rows(p.phi_pre, pw, pn, route_rows, rq, rs, racc, ry);
@@ -2385,15 +2414,13 @@ bool fused_applies(const rn_n3_model* m) {
     // the input codes four lanes a run: groups of at most 256
     if (m->phi_pre->group > 256) return false;
     if ((2 * L + L * L) * (m->phi_pre->cb.padded / m->phi_pre->group) > kN3Block) return false;
-    // the layer boundary stages the factors and cond_v, three vectors, the
-    // stream and the routing rows in 16-byte units, at most 384 a wave; its
-    // norms take squares four a read (d a multiple of 32)
+    // the layer boundary stages three vectors and the stream in 1 KB chunks,
+    // two a wave (d a multiple of 256), and copies the factors, cond_v and the
+    // routing rows in 16-byte units; its norms take squares four a read
     const int d = (int)g.d_model;
-    if (d % 32 != 0) return false;
+    if (d % 256 != 0 || (3 * d + L * d) / 256 > 2 * (kN3Block / 64)) return false;
+    if (m->embedding->cb.padded > kN3Hadamard || m->embedding->group > 256) return false;  // the logits' input
     if (m->phi_pre->cb.row_bytes % 16 != 0) return false;
-    const int waves = (6 * kN3Hadamard + 8 * d + 1535) / 1536 + (3 * d + 1535) / 1536 + (L * d + 1535) / 1536 +
-                      ((2 * L + L * L) * (int)(m->phi_pre->cb.row_bytes / 16) + 383) / 384;
-    if (waves > kN3Block / 64) return false;
     auto aligned = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
     const rn_matrix* phis[3] = {m->phi_pre, m->phi_post, m->phi_res};
     for (const rn_matrix* x : phis) {
@@ -2682,6 +2709,8 @@ struct rn_n3_session {
     float *x = nullptr, *rotated = nullptr, *prod = nullptr, *attended = nullptr;
     void* codes = nullptr;         // the projections' input codes (int4 a run of 16)
     float* code_scales = nullptr;
+    float* lrot = nullptr;     // the logits' input prepared by the last fused push (lrot_ready)
+    bool lrot_ready = false;
     uint32_t* tokens_dev = nullptr;  // the tokens pushed so far [capacity]
     uint32_t* next_dev = nullptr;    // the greedy argmax of the last logits
     uint32_t* ids_dev = nullptr;     // greedy ids [capacity]
@@ -2826,6 +2855,7 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
         N3_CALL(alloc_n(s, 64, &s->post));
         N3_CALL(alloc_n(s, 256, &s->residual));
         N3_CALL(alloc_n(s, (size_t)widest, &s->rotated));
+        N3_CALL(alloc_n(s, (size_t)m->embedding->cb.padded, &s->lrot));
         N3_CALL(alloc_n(s, (size_t)qkv + H * 64, &s->prod));
         N3_CALL(alloc_n(s, (size_t)H * 64, &s->attended));
         N3_CALL(alloc(s, (size_t)kN3Hadamard, &s->codes));
@@ -3102,6 +3132,10 @@ int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
             b.final = 1;
             b.final_norm = m->final_norm;
             b.hidden = s->hidden;
+            b.logits_in = s->lrot;
+            b.lpadded = m->embedding->cb.padded;
+            b.lgroup = m->embedding->group;
+            b.lwht = m->embedding->cb.wht_scale;
         }
         rn_launch(n3_boundary_kernel, dim3(1), dim3(kN3Block), 0, st, b);
         N3_HIP(hipGetLastError());
@@ -3122,13 +3156,11 @@ int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
     const int d = (int)g.d_model, lanes = (int)g.mhc_lanes;
     const int position = s->length;
     hipStream_t st = s->stream;
-    rn_launch(n3_set_token_kernel, dim3(1), dim3(64), 0, st, s->tokens_dev, position, token, source);
-    N3_HIP(hipGetLastError());
     float* cur = s->stream_a;
     float* nxt = s->stream_b;
     const int embed_threads = ((m->embedding->cb.padded / 16 + 63) / 64) * 64;
-    rn_launch(n3_embed_kernel, dim3(1), dim3(embed_threads), 0, st, m->embedding->cb, (const uint32_t*)s->tokens_dev,
-              position, d, lanes, sqrtf((float)d), cur, s->cells, 0, 0);
+    rn_launch(n3_embed_kernel, dim3(1), dim3(embed_threads), 0, st, m->embedding->cb, s->tokens_dev, position, d, lanes,
+              sqrtf((float)d), cur, s->cells, 0, 0, 1, source, token);
     N3_HIP(hipGetLastError());
 
     // engram sites (engram.rs:30-112), before the layers
@@ -3160,6 +3192,7 @@ int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
     }
 
     N3_CALL(s->fused ? fused_layers(s, position, cur, nxt) : stepwise_layers(s, position, cur, nxt));
+    s->lrot_ready = s->fused;
     for (size_t i = 0; i < m->heads.size(); ++i) {
         const N3Head& h = m->heads[i];
         rn_launch(n3_observe_kernel, dim3(h.layers * h.per_layer), dim3(256), 0, st, (const float*)s->cells,
@@ -3174,15 +3207,19 @@ int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
 int enqueue_logits(rn_n3_session* s) {
     const rn_n3_model* m = s->m;
     hipStream_t st = s->stream;
-    rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->hidden, (int)m->g.d_model,
-              m->embedding->cb.padded, m->embedding->group, m->embedding->cb.wht_scale, s->rotated);
-    N3_HIP(hipGetLastError());
+    const float* in = s->lrot;
+    if (!s->lrot_ready) {
+        rn_launch(n3_fake_quantise_kernel, dim3(1), dim3(kN3Block), 0, st, (const float*)s->hidden, (int)m->g.d_model,
+                  m->embedding->cb.padded, m->embedding->group, m->embedding->cb.wht_scale, s->rotated);
+        N3_HIP(hipGetLastError());
+        in = s->rotated;
+    }
     CodebookParams p = m->embedding->cb;
     p.rows = m->output_vocab;  // multiply_rows(0, ..) over the first output_vocab rows
     if (m->embedding->bits == 1 || m->embedding->bits == 3)
-        N3_HIP(launch_codebook_float(p, s->rotated, 1, s->logits, false, st));
+        N3_HIP(launch_codebook_float(p, in, 1, s->logits, false, st));
     else
-        N3_HIP(launch_codebook_product(p, s->rotated, 1, s->logits, nullptr, st));
+        N3_HIP(launch_codebook_product(p, in, 1, s->logits, nullptr, st));
     return RN_OK;
 }
 
@@ -3251,8 +3288,8 @@ int enqueue_run(rn_n3_session* s, const uint32_t* tokens, int count) {
         N3_HIP(hipGetLastError());
     }
     const int embed_threads = ((m->embedding->cb.padded / 16 + 63) / 64) * 64;
-    rn_launch(n3_embed_kernel, dim3(T), dim3(embed_threads), 0, st, m->embedding->cb, (const uint32_t*)s->tokens_dev,
-              P0, d, lanes, sqrtf((float)d), r.stream_a, r.cells, S, cell_stride);
+    rn_launch(n3_embed_kernel, dim3(T), dim3(embed_threads), 0, st, m->embedding->cb, s->tokens_dev, P0, d, lanes,
+              sqrtf((float)d), r.stream_a, r.cells, S, cell_stride, 0, (const uint32_t*)nullptr, 0u);
     N3_HIP(hipGetLastError());
 
     // engram sites (engram.rs:113-162)
@@ -3426,6 +3463,7 @@ int enqueue_run(rn_n3_session* s, const uint32_t* tokens, int count) {
     N3_HIP(hipMemcpyAsync(s->cells, r.cells + (size_t)(T - 1) * cell_stride, (size_t)cell_stride * 4,
                           hipMemcpyDeviceToDevice, st));
     s->length += T;
+    s->lrot_ready = false;
     return RN_OK;
 }
 
