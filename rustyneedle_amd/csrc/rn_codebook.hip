@@ -196,8 +196,8 @@ __global__ __launch_bounds__(1024) void cb_dequantise_kernel(CodebookParams p, i
 //      next row group's loads are issued before this one's epilogue;
 //   4. one lane per (token, row): the sequential group epilogue.
 template <int BITS, int GROUP, int FORM, int NL, int T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NL == 8 && T == 1 ? 3 : 1)))
-void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, int32_t* acc_out) {
+__device__ __forceinline__ void cb_product_body(const CodebookParams& p, const float* x, int count, float* y,
+                                                int32_t* acc_out) {
     constexpr int IB = BITS == 5 ? 2 : BITS;        // index bits (ternary crumbs are 2)
     constexpr int EPC = 128 / IB;                    // elements per 16-byte chunk
     constexpr int CPG = GROUP / EPC;                 // chunks per group
@@ -394,6 +394,21 @@ void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, in
     }
 }
 
+template <int BITS, int GROUP, int FORM, int NL, int T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NL == 8 && T == 1 ? 3 : 1)))
+void cb_product_kernel(CodebookParams p, const float* x, int count, float* y, int32_t* acc_out) {
+    cb_product_body<BITS, GROUP, FORM, NL, T>(p, x, count, y, acc_out);
+}
+
+// Up to four products of one shape in one launch (blockIdx.z picks the job):
+// matrices that share rows, width, format and group, one input vector each.
+template <int BITS, int GROUP, int FORM, int NL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NL == 8 ? 3 : 1)))
+void cb_product_jobs_kernel(CodebookJobs jobs) {
+    const CodebookJob& j = jobs.job[blockIdx.z];
+    cb_product_body<BITS, GROUP, FORM, NL, 1>(j.p, j.x, 1, j.y, nullptr);
+}
+
 namespace {
 
 // LDS of a product block: norms window, [T][padded] codes, [4][T][R][G] sums, [T][G] scales
@@ -558,6 +573,57 @@ hipError_t launch_codebook_product(const CodebookParams& p, const float* x, int 
         case 2: return launch_product_b<2, kPanel>(p, x, count, y, acc, stream);
         case 4: return launch_product_b<4, kPlane>(p, x, count, y, acc, stream);
         case 5: return launch_product_b<5, kPlane>(p, x, count, y, acc, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+namespace {
+
+template <int BITS, int GROUP, int FORM>
+hipError_t launch_jobs_t(CodebookJobs jobs, int n, hipStream_t stream) {
+    const CodebookParams& p = jobs.job[0].p;
+    const int nl = product_loads(p), R = product_rows(p);
+    const size_t lds = product_lds(p, 1, R);
+    if (lds > kProductMaxLds) return hipErrorInvalidValue;
+    const int groups = (p.rows + 4 * R - 1) / (4 * R);
+    const int iters = max(1, min(max(4, p.padded / 1024), groups / 512));
+    for (int i = 0; i < n; ++i) {
+        jobs.job[i].p.rows_per_block = R;
+        jobs.job[i].p.iters = iters;
+    }
+    const dim3 grid((groups + iters - 1) / iters, 1, n);
+    if (nl == 8)
+        rn_launch(cb_product_jobs_kernel<BITS, GROUP, FORM, 8>, grid, dim3(256), lds, stream, jobs);
+    else
+        rn_launch(cb_product_jobs_kernel<BITS, GROUP, FORM, 16>, grid, dim3(256), lds, stream, jobs);
+    return hipGetLastError();
+}
+
+template <int BITS, int FORM>
+hipError_t launch_jobs_b(const CodebookJobs& jobs, int n, hipStream_t stream) {
+    switch (jobs.job[0].p.group) {
+        case 64: return launch_jobs_t<BITS, 64, FORM>(jobs, n, stream);
+        case 128: return launch_jobs_t<BITS, 128, FORM>(jobs, n, stream);
+        case 256: return launch_jobs_t<BITS, 256, FORM>(jobs, n, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_codebook_product_jobs(const CodebookJobs& jobs, int n, hipStream_t stream) {
+    if (n < 1 || n > kCodebookJobs) return hipErrorInvalidValue;
+    const CodebookParams& p = jobs.job[0].p;
+    if (p.rows < 1 || p.cpr < 1 || p.cpr > 1024) return hipErrorInvalidValue;
+    for (int i = 1; i < n; ++i) {
+        const CodebookParams& q = jobs.job[i].p;
+        if (q.bits != p.bits || q.group != p.group || q.padded != p.padded || q.rows != p.rows || q.cpr != p.cpr)
+            return hipErrorInvalidValue;
+    }
+    switch (p.bits) {
+        case 2: return launch_jobs_b<2, kPanel>(jobs, n, stream);
+        case 4: return launch_jobs_b<4, kPlane>(jobs, n, stream);
+        case 5: return launch_jobs_b<5, kPlane>(jobs, n, stream);
         default: return hipErrorInvalidValue;
     }
 }

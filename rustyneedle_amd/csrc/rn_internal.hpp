@@ -274,6 +274,18 @@ struct CodebookParams {
 // rotated [count][padded] inputs -> y [count][rows] (acc nullable: [count][rows][groups])
 hipError_t launch_codebook_product(const CodebookParams& p, const float* x, int count, float* y, int32_t* acc,
                                    hipStream_t stream);
+// up to kCodebookJobs products of one vector each, in one launch: the matrices
+// share rows, padded width, bits and group (the integer path)
+constexpr int kCodebookJobs = 4;
+struct CodebookJob {
+    CodebookParams p;
+    const float* x;  // rotated [padded]
+    float* y;        // [rows]
+};
+struct CodebookJobs {
+    CodebookJob job[kCodebookJobs];
+};
+hipError_t launch_codebook_product_jobs(const CodebookJobs& jobs, int n, hipStream_t stream);
 // The float products of any width (1-5): fill_rows_float (batch false, one
 // result per token and row in the vector order) or multiply_batch's float tile
 // (batch true); rotated [count][padded] -> y [count][rows].

@@ -329,16 +329,29 @@ struct N3GatherParams {
     int orders[4];
     float* out;  // [count * sub] a position, out_stride apart
     int out_stride;
+    // with `rotated`: prepare for the key matrix (matrix.rs:123-128: zero to
+    // rpadded, each group of rgroup rotated, times rwht) into rotated [rpadded]
+    // instead of writing out
+    float* rotated;
+    int rpadded, rgroup;
+    float rwht;
+};
+
+constexpr int kN3MaxSites = 4;  // engram sites one launch serves
+
+struct N3GatherSites {
+    N3GatherParams site[kN3MaxSites];
 };
 
 // engram.rs:66-82: row table * slots + index of each table (zeros while the
 // position is shorter than the table's order), dequantised (matrix.rs:140-153),
 // then fake_quantise_int8 over the whole gathered vector. Block b gathers
 // position p.position + b (engram.rs:122-133 for a run of positions).
-__global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherParams p) {
+__global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherSites sites) {
     __shared__ float buf[kN3MaxWidth];
     __shared__ float red[32];
     __shared__ int index_s[kN3MaxTables], order_s[kN3MaxTables];
+    const N3GatherParams& p = sites.site[blockIdx.y];  // the site (one launch serves a push's sites)
     const CodebookParams& c = p.tables;
     const int n = p.count * p.sub, ib = c.bits == 5 ? 2 : c.bits, G = c.padded / c.group;
     const int position = p.position + (int)blockIdx.x;
@@ -368,7 +381,14 @@ __global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherParams p) {
     __syncthreads();
     n3_rotate(buf, n, c.group, c.wht_scale);  // each table row's groups (dequantise_row)
     n3_fake_quantise(buf, n, red);
-    for (int e = threadIdx.x; e < n; e += blockDim.x) out[e] = buf[e];
+    if (p.rotated != nullptr) {
+        for (int e = n + threadIdx.x; e < p.rpadded; e += blockDim.x) buf[e] = 0.0f;
+        __syncthreads();
+        n3_rotate(buf, p.rpadded, p.rgroup, p.rwht);
+        for (int e = threadIdx.x; e < p.rpadded; e += blockDim.x) p.rotated[e] = buf[e];
+    } else {
+        for (int e = threadIdx.x; e < n; e += blockDim.x) out[e] = buf[e];
+    }
 }
 
 // engram.rs:84-111: value = sum over taps of gain * the raw value `tap *
@@ -377,9 +397,20 @@ __global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherParams p) {
 // back <= t (engram.rs:140-153), else from the ring (slot position mod keep).
 // With write_ring (one token) the raw value joins the ring here; a run's
 // values join it afterwards (n3_ring_store_kernel), once every block has read.
-__global__ void n3_engram_conv_kernel(const float* raw, float* ring, const float* taps, int position, int keep,
-                                      int ntaps, int dilation, int width, float* value, int write_ring) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y, pos = position + t;
+struct N3ConvSites {
+    const float* raw[kN3MaxSites];
+    float* ring[kN3MaxSites];
+    const float* taps[kN3MaxSites];
+    float* value[kN3MaxSites];
+};
+
+__global__ void n3_engram_conv_kernel(N3ConvSites sites, int position, int keep, int ntaps, int dilation, int width,
+                                      int write_ring) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y, pos = position + t, e = blockIdx.z;
+    const float* const raw = sites.raw[e];
+    float* const ring = sites.ring[e];
+    const float* const taps = sites.taps[e];
+    float* const value = sites.value[e];
     if (i >= width) return;
     const float r = raw[(size_t)t * width + i];
     if (write_ring) ring[(size_t)(pos % keep) * width + i] = r;
@@ -925,12 +956,30 @@ __device__ float n3_dot_product(const float* a, const float* b, int n, float* re
     return total + tail;
 }
 
-// heads.rs:138-155: one block per slot (layer * k + probe)
-__global__ __launch_bounds__(256) void n3_observe_kernel(const float* cells, const float* probes, int k, int width,
-                                                         float* peak, float* total, float* weighted) {
+constexpr int kN3MaxHeads = 4;  // probe heads one launch serves
+
+struct N3ObserveHeads {
+    const float* probes[kN3MaxHeads];
+    float* peak[kN3MaxHeads];
+    float* total[kN3MaxHeads];
+    float* weighted[kN3MaxHeads];
+    int k[kN3MaxHeads], width[kN3MaxHeads], first[kN3MaxHeads + 1];  // first slot (block) of each head
+    int count;
+};
+
+// heads.rs:138-155: one block per slot (layer * k + probe) of each head
+__global__ __launch_bounds__(256) void n3_observe_kernel(const float* cells, N3ObserveHeads hs) {
     __shared__ float red[8];
     __shared__ float rw[2];
-    const int slot = blockIdx.x, layer = slot / k;
+    int hh = 0;
+    for (int j = 1; j < hs.count; ++j) hh = (int)blockIdx.x >= hs.first[j] ? j : hh;
+    const int h = __builtin_amdgcn_readfirstlane(hh);
+    const int k = hs.k[h], width = hs.width[h];
+    const float* const probes = hs.probes[h];
+    float* const peak = hs.peak[h];
+    float* const total = hs.total[h];
+    float* const weighted = hs.weighted[h];
+    const int slot = (int)blockIdx.x - hs.first[h], layer = slot / k;
     const float* cell = cells + (size_t)layer * width;
     const float dot = n3_dot_product(cell, probes + (size_t)slot * width, width, red);
     if (threadIdx.x == 0) {
@@ -2702,7 +2751,7 @@ struct rn_n3_session {
     hipStream_t stream = nullptr;
     rn_lanes* lanes = nullptr;
     std::vector<N3CacheDev> caches;
-    std::vector<float*> rings, ekey, evalue;
+    std::vector<float*> rings, ekey, evalue, site_rot, site_raw;  // per engram site
     std::vector<void*> allocations;
     N3Arena arena;
     float *stream_a = nullptr, *stream_b = nullptr, *input = nullptr, *post = nullptr, *residual = nullptr;
@@ -2841,10 +2890,14 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
         s->rings.resize(g.engram_site_count);
         s->ekey.resize(g.engram_site_count);
         s->evalue.resize(g.engram_site_count);
+        s->site_rot.resize(g.engram_site_count);
+        s->site_raw.resize(g.engram_site_count);
         for (uint32_t e = 0; e < g.engram_site_count; ++e) {
             N3_CALL(alloc_n(s, (size_t)keep * d, &s->rings[e]));
             N3_CALL(alloc_n(s, (size_t)d, &s->ekey[e]));
             N3_CALL(alloc_n(s, (size_t)d, &s->evalue[e]));
+            N3_CALL(alloc_n(s, (size_t)m->engrams[e].key->cb.padded, &s->site_rot[e]));
+            N3_CALL(alloc_n(s, (size_t)d, &s->site_raw[e]));
         }
         int widest = std::max(lanes * d, qkv + H * 64);
         for (const N3Engram& e : m->engrams) widest = std::max(widest, e.key->cb.padded);
@@ -3148,6 +3201,109 @@ int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
 
 namespace {
 
+// The engram sites of a push at `position` (engram.rs:30-112)
+int enqueue_sites(rn_n3_session* s, int position) {
+    const rn_n3_model* m = s->m;
+    const rn_geometry& g = m->g;
+    const int d = (int)g.d_model;
+    hipStream_t st = s->stream;
+    const int hpo = heads_per_order(g), tables = (int)g.engram_order_count * hpo;
+    const int keep = std::max(1, ((int)g.engram_conv_taps - 1) * (int)g.engram_conv_dilation + 1);
+    std::vector<int> act;
+    for (uint32_t e = 0; e < g.engram_site_count; ++e)
+        if (site_active(m, (int)e)) act.push_back((int)e);
+    for (size_t b0 = 0; b0 < act.size(); b0 += kN3MaxSites / 2) {  // two products a site, four a launch
+        const int ns = (int)std::min(act.size() - b0, (size_t)kN3MaxSites / 2);
+        N3GatherSites gs{};
+        N3ConvSites cs{};
+        CodebookJobs jobs{};
+        bool joint = true;
+        for (int k = 0; k < ns; ++k) {
+            const int e = act[b0 + (size_t)k];
+            const N3Engram& eg = m->engrams[(size_t)e];
+            N3GatherParams& gp = gs.site[k];
+            gp.tables = eg.tables->cb;
+            gp.count = tables;
+            gp.sub = (int)g.engram_sub_dim;
+            gp.slots = (int)g.engram_slots;
+            gp.position = position;
+            gp.tokens = s->tokens_dev;
+            gp.heads_per_order = hpo;
+            gp.stride = g.engram_seed_heads == 0 ? hpo : (int)g.engram_seed_heads;
+            for (int o = 0; o < 4; ++o) gp.orders[o] = (int)g.engram_orders[o];
+            gp.rotated = s->site_rot[(size_t)e];
+            gp.rpadded = eg.key->cb.padded;
+            gp.rgroup = eg.key->group;
+            gp.rwht = eg.key->cb.wht_scale;
+            jobs.job[2 * k] = CodebookJob{eg.key->cb, s->site_rot[(size_t)e], s->ekey[(size_t)e]};
+            jobs.job[2 * k + 1] = CodebookJob{eg.value->cb, s->site_rot[(size_t)e], s->site_raw[(size_t)e]};
+            joint = joint && integer_path(eg.key) && integer_path(eg.value);
+            cs.raw[k] = s->site_raw[(size_t)e];
+            cs.ring[k] = s->rings[(size_t)e];
+            cs.taps[k] = eg.taps;
+            cs.value[k] = s->evalue[(size_t)e];
+        }
+        rn_launch(n3_gather_kernel, dim3(1, ns), dim3(kN3Block), 0, st, gs);
+        N3_HIP(hipGetLastError());
+        bool same = joint;
+        for (int j = 1; j < 2 * ns; ++j) {
+            const CodebookParams &a = jobs.job[0].p, &b = jobs.job[j].p;
+            same = same && a.bits == b.bits && a.group == b.group && a.padded == b.padded && a.rows == b.rows &&
+                   a.cpr == b.cpr;
+        }
+        if (same && launch_codebook_product_jobs(jobs, 2 * ns, st) == hipSuccess) {
+        } else {
+            (void)hipGetLastError();
+            for (int k = 0; k < ns; ++k) {
+                const N3Engram& eg = m->engrams[(size_t)act[b0 + (size_t)k]];
+                N3_CALL(product(eg.key, jobs.job[2 * k].x, jobs.job[2 * k].y, st));
+                N3_CALL(product(eg.value, jobs.job[2 * k + 1].x, jobs.job[2 * k + 1].y, st));
+            }
+        }
+        rn_launch(n3_engram_conv_kernel, dim3((d + 255) / 256, 1, ns), dim3(256), 0, st, cs, position, keep,
+                  (int)g.engram_conv_taps, (int)g.engram_conv_dilation, d, 1);
+        N3_HIP(hipGetLastError());
+    }
+    return RN_OK;
+}
+
+// The probe heads observe the cells of `count` tokens in order (heads.rs:138-155),
+// kN3MaxHeads heads a launch
+int enqueue_observe(rn_n3_session* s, const float* cells, int cell_stride, int count) {
+    const rn_n3_model* m = s->m;
+    hipStream_t st = s->stream;
+    for (size_t b0 = 0; b0 < m->heads.size(); b0 += kN3MaxHeads) {
+        if (count > 1) {
+            for (size_t i = b0; i < std::min(m->heads.size(), b0 + kN3MaxHeads); ++i) {
+                const N3Head& h = m->heads[i];
+                rn_launch(n3_observe_run_kernel, dim3(h.layers * h.per_layer), dim3(256), 0, st, cells, cell_stride,
+                          count, (const float*)h.probes, h.per_layer, h.width, s->peak[i], s->total[i],
+                          s->weighted[i]);
+                N3_HIP(hipGetLastError());
+            }
+            continue;
+        }
+        N3ObserveHeads hs{};
+        int blocks = 0;
+        for (size_t i = b0; i < std::min(m->heads.size(), b0 + kN3MaxHeads); ++i) {
+            const N3Head& h = m->heads[i];
+            const int k = hs.count++;
+            hs.probes[k] = h.probes;
+            hs.peak[k] = s->peak[i];
+            hs.total[k] = s->total[i];
+            hs.weighted[k] = s->weighted[i];
+            hs.k[k] = h.per_layer;
+            hs.width[k] = h.width;
+            hs.first[k] = blocks;
+            blocks += h.layers * h.per_layer;
+        }
+        hs.first[hs.count] = blocks;
+        rn_launch(n3_observe_kernel, dim3(blocks), dim3(256), 0, st, cells, hs);
+        N3_HIP(hipGetLastError());
+    }
+    return RN_OK;
+}
+
 // Session::push (session.rs:76-148) of tokens[position], which the host writes
 // (source null) or a device value (source: the greedy argmax) supplies.
 int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
@@ -3163,42 +3319,14 @@ int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
               sqrtf((float)d), cur, s->cells, 0, 0, 1, source, token);
     N3_HIP(hipGetLastError());
 
-    // engram sites (engram.rs:30-112), before the layers
-    const int hpo = heads_per_order(g), tables = (int)g.engram_order_count * hpo;
-    const int keep = std::max(1, ((int)g.engram_conv_taps - 1) * (int)g.engram_conv_dilation + 1);
-    for (uint32_t e = 0; e < g.engram_site_count; ++e) {
-        if (!site_active(m, (int)e)) continue;
-        const N3Engram& eg = m->engrams[e];
-        N3GatherParams gp{};
-        gp.tables = eg.tables->cb;
-        gp.count = tables;
-        gp.sub = (int)g.engram_sub_dim;
-        gp.slots = (int)g.engram_slots;
-        gp.position = position;
-        gp.tokens = s->tokens_dev;
-        gp.heads_per_order = hpo;
-        gp.stride = g.engram_seed_heads == 0 ? hpo : (int)g.engram_seed_heads;
-        for (int o = 0; o < 4; ++o) gp.orders[o] = (int)g.engram_orders[o];
-        gp.out = s->gathered;
-        rn_launch(n3_gather_kernel, dim3(1), dim3(kN3Block), 0, st, gp);
-        N3_HIP(hipGetLastError());
-        N3_CALL(rotate(eg.key, s->gathered, s->rotated, st));
-        N3_CALL(product(eg.key, s->rotated, s->ekey[e], st));
-        N3_CALL(product(eg.value, s->rotated, s->eraw, st));
-        rn_launch(n3_engram_conv_kernel, dim3((d + 255) / 256), dim3(256), 0, st, (const float*)s->eraw, s->rings[e],
-                  (const float*)eg.taps, position, keep, (int)g.engram_conv_taps, (int)g.engram_conv_dilation, d,
-                  s->evalue[e], 1);
-        N3_HIP(hipGetLastError());
-    }
+    // engram sites (engram.rs:30-112), before the layers: one launch gathers
+    // and prepares the active sites' inputs, one runs their key and value
+    // products, one their value convolutions
+    N3_CALL(enqueue_sites(s, position));
 
     N3_CALL(s->fused ? fused_layers(s, position, cur, nxt) : stepwise_layers(s, position, cur, nxt));
     s->lrot_ready = s->fused;
-    for (size_t i = 0; i < m->heads.size(); ++i) {
-        const N3Head& h = m->heads[i];
-        rn_launch(n3_observe_kernel, dim3(h.layers * h.per_layer), dim3(256), 0, st, (const float*)s->cells,
-                  (const float*)h.probes, h.per_layer, h.width, s->peak[i], s->total[i], s->weighted[i]);
-        N3_HIP(hipGetLastError());
-    }
+    N3_CALL(enqueue_observe(s, s->cells, 0, 1));
     s->length++;
     return RN_OK;
 }
@@ -3310,15 +3438,21 @@ int enqueue_run(rn_n3_session* s, const uint32_t* tokens, int count) {
         for (int o = 0; o < 4; ++o) gp.orders[o] = (int)g.engram_orders[o];
         gp.out = r.gathered;
         gp.out_stride = (int)eg.key->columns;
-        rn_launch(n3_gather_kernel, dim3(T), dim3(kN3Block), 0, st, gp);
+        N3GatherSites gs{};
+        gs.site[0] = gp;
+        rn_launch(n3_gather_kernel, dim3(T, 1), dim3(kN3Block), 0, st, gs);
         N3_HIP(hipGetLastError());
         N3_HIP(launch_codebook_rotate(r.gathered, T, eg.key->columns, eg.key->cb.padded, eg.key->group,
                                       eg.key->cb.wht_scale, r.rotated, st));
         N3_CALL(product_run(eg.key, r.rotated, T, r.ekey[e], st));
         N3_CALL(product_run(eg.value, r.rotated, T, r.eraw, st));
-        rn_launch(n3_engram_conv_kernel, dim3((d + 255) / 256, T), dim3(256), 0, st, (const float*)r.eraw, s->rings[e],
-                  (const float*)eg.taps, P0, keep, (int)g.engram_conv_taps, (int)g.engram_conv_dilation, d, r.evalue[e],
-                  0);
+        N3ConvSites cs{};
+        cs.raw[0] = r.eraw;
+        cs.ring[0] = s->rings[e];
+        cs.taps[0] = eg.taps;
+        cs.value[0] = r.evalue[e];
+        rn_launch(n3_engram_conv_kernel, dim3((d + 255) / 256, T, 1), dim3(256), 0, st, cs, P0, keep,
+                  (int)g.engram_conv_taps, (int)g.engram_conv_dilation, d, 0);
         N3_HIP(hipGetLastError());
         rn_launch(n3_ring_store_kernel, dim3((d + 255) / 256, std::min(T, keep)), dim3(256), 0, st, (const float*)r.eraw,
                   d, T, P0, keep, d, s->rings[e], d);
@@ -3452,13 +3586,7 @@ int enqueue_run(rn_n3_session* s, const uint32_t* tokens, int count) {
         std::swap(cur, nxt);
     }
     // the heads observe the tokens in order (prefill.rs:92-96)
-    for (size_t i = 0; i < m->heads.size(); ++i) {
-        const N3Head& h = m->heads[i];
-        rn_launch(n3_observe_run_kernel, dim3(h.layers * h.per_layer), dim3(256), 0, st, (const float*)r.cells,
-                  cell_stride, T, (const float*)h.probes, h.per_layer, h.width, s->peak[i], s->total[i],
-                  s->weighted[i]);
-        N3_HIP(hipGetLastError());
-    }
+    N3_CALL(enqueue_observe(s, r.cells, cell_stride, T));
     // the last token's cells (prefill.rs:98)
     N3_HIP(hipMemcpyAsync(s->cells, r.cells + (size_t)(T - 1) * cell_stride, (size_t)cell_stride * 4,
                           hipMemcpyDeviceToDevice, st));
