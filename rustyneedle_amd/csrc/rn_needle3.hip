@@ -112,6 +112,55 @@ __device__ __forceinline__ float n3_fold(float s, const float* a, const float* b
     return s;
 }
 
+// 0.0 + q[0].x + q[0].y + ... in order over `count` float4 values in LDS (a
+// chain of dependent adds): the next eight values' loads are issued before
+// the current eight's adds (two register sets in turn), so the chain waits on
+// the adds and not on the LDS.
+__device__ __forceinline__ float n3_chain4(const float4* q, int count) {
+    float s = 0.0f;
+    auto add8 = [&](const float4 (&v)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            s = s + v[j].x;
+            s = s + v[j].y;
+            s = s + v[j].z;
+            s = s + v[j].w;
+        }
+    };
+    const int full = count / 8 * 8;
+    if (full > 0) {
+        float4 a[8], b[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = q[j];
+        for (int k = 0;;) {
+            const bool more = k + 8 < full;
+            if (more) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) b[j] = q[k + 8 + j];
+            }
+            add8(a);
+            k += 8;
+            if (!more) break;
+            const bool more2 = k + 8 < full;
+            if (more2) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) a[j] = q[k + 8 + j];
+            }
+            add8(b);
+            k += 8;
+            if (!more2) break;
+        }
+    }
+    for (int k = full; k < count; ++k) {
+        const float4 t = q[k];
+        s = s + t.x;
+        s = s + t.y;
+        s = s + t.z;
+        s = s + t.w;
+    }
+    return s;
+}
+
 // ops.rs:7-17 over n values in LDS: eight strided lanes, summed in lane order,
 // then the tail. Every thread calls; all get the result. With `sq` (LDS
 // scratch of n + 64 floats, 16-byte aligned, n / 8 a multiple of 4) the squares
@@ -128,17 +177,7 @@ __device__ float n3_sum_of_squares(const float* v, int n, float* red, float* sq 
         }
         __syncthreads();
         if (tid < 8) {
-            const float4* q = reinterpret_cast<const float4*>(sq + tid * stride);
-            float s = 0.0f;
-#pragma unroll 8
-            for (int k = 0; k < n8 / 4; ++k) {
-                const float4 t = q[k];
-                s = s + t.x;
-                s = s + t.y;
-                s = s + t.z;
-                s = s + t.w;
-            }
-            red[tid] = s;
+            red[tid] = n3_chain4(reinterpret_cast<const float4*>(sq + tid * stride), n8 / 4);
         }
     } else if (tid < 8) {
         red[tid] = n3_fold<true>(0.0f, v + tid, nullptr, n8, 8);
@@ -1276,17 +1315,7 @@ __device__ void n3_norm_codes(const float* v, const float* gain, int n, float* r
     if (lane == 0) red[16 + wave] = pk;
     __syncthreads();
     if (tid < 8) {
-        const float4* q = reinterpret_cast<const float4*>(sq + tid * stride);
-        float s = 0.0f;
-#pragma unroll 8
-        for (int k = 0; k < n8 / 4; ++k) {
-            const float4 t = q[k];
-            s = s + t.x;
-            s = s + t.y;
-            s = s + t.z;
-            s = s + t.w;
-        }
-        red[tid] = s;
+        red[tid] = n3_chain4(reinterpret_cast<const float4*>(sq + tid * stride), n8 / 4);
     }
     __syncthreads();
     float total = 0.0f;
