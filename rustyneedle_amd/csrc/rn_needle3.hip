@@ -882,16 +882,36 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
         if (tid < 32) {
             const int j = tid >> 3, r = tid & 7, n = (d - j + 3) / 4;
             const float* q = cv + j * 8 + r;
+            // 0.0 + q[0] + q[32] + ... in order; the next sixteen loads are
+            // issued before the current sixteen adds (two register sets in turn)
             float sum = 0.0f;
-            int k = 0;
-            for (; k + 16 <= n; k += 16) {
-                float t[16];
+            const int full = n / 16 * 16;
+            if (full > 0) {
+                float ta[16], tb[16];
 #pragma unroll
-                for (int u = 0; u < 16; ++u) t[u] = q[(k + u) * 32];
+                for (int u = 0; u < 16; ++u) ta[u] = q[u * 32];
+                for (int k = 0;;) {
+                    const bool more = k + 16 < full;
+                    if (more) {
 #pragma unroll
-                for (int u = 0; u < 16; ++u) sum = sum + t[u];
+                        for (int u = 0; u < 16; ++u) tb[u] = q[(k + 16 + u) * 32];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) sum = sum + ta[u];
+                    k += 16;
+                    if (!more) break;
+                    const bool more2 = k + 16 < full;
+                    if (more2) {
+#pragma unroll
+                        for (int u = 0; u < 16; ++u) ta[u] = q[(k + 16 + u) * 32];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) sum = sum + tb[u];
+                    k += 16;
+                    if (!more2) break;
+                }
             }
-            for (; k < n; ++k) sum = sum + q[k * 32];
+            for (int k = full; k < n; ++k) sum = sum + q[k * 32];
             chains[j][r] = sum;
         }
         __syncthreads();
