@@ -1955,6 +1955,13 @@ struct N3BoundaryParams {
     float* logits_in;
     int lpadded, lgroup;
     float lwht;
+    // with `raw` (one token at `position`), the engram value is the site's
+    // convolution (engram.rs:84-111) of its raw value over the ring, computed
+    // here, and the raw value joins the ring (slot position mod keep)
+    const float* raw;
+    float* ring;
+    const float* taps;
+    int position, keep, ntaps, dilation;
 };
 
 constexpr int kN3RouteRows = 24;         // 2 lanes + lanes^2 for four lanes
@@ -2111,10 +2118,32 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     }
     if (!p.route) return;
     // the block input's tensors, requested before the routing work
-    float norm_in_r[1], key_r[1], value_r[1];
-    norm_in_r[0] = tid < d ? p.norm_in[tid] : 0.0f;
-    key_r[0] = (e_key != nullptr && tid < d) ? e_key[tid] : 0.0f;
-    value_r[0] = (e_key != nullptr && tid < d) ? e_value[tid] : 0.0f;
+    float norm_in_r, key_r, value_r;
+    norm_in_r = tid < d ? p.norm_in[tid] : 0.0f;
+    key_r = (e_key != nullptr && tid < d) ? e_key[tid] : 0.0f;
+    if (p.raw != nullptr) {
+        // engram.rs:84-111: value = sum over taps of gain * the raw value
+        // `tap * dilation` positions back (the ring holds the earlier ones)
+        // (taps of the positions that exist, at most kN3MaxTaps, read first)
+        const int i = min(tid, d - 1);
+        const float r = p.raw[i];
+        float gain[kN3MaxTaps], sample[kN3MaxTaps];
+#pragma unroll
+        for (int tap = 0; tap < kN3MaxTaps; ++tap) {
+            const int back = tap * p.dilation;
+            const bool on = tap < p.ntaps && p.position >= back;
+            gain[tap] = on ? p.taps[(size_t)tap * d + i] : 0.0f;
+            sample[tap] = (on && tap > 0) ? p.ring[(size_t)((p.position - back) % p.keep) * d + i] : r;
+        }
+        float v = 0.0f;
+#pragma unroll
+        for (int tap = 0; tap < kN3MaxTaps; ++tap)
+            if (tap < p.ntaps && p.position >= tap * p.dilation) v = v + gain[tap] * sample[tap];
+        if (tid < d) p.ring[(size_t)(p.position % p.keep) * d + i] = r;
+        value_r = v;
+    } else {
+        value_r = (e_key != nullptr && tid < d) ? e_value[tid] : 0.0f;
+    }
     // lanes.rs:49-53: unit_rms, fake_quantise_int8, prepare (phi_pre's groups);
     // the routing matrices share their format, so one set of codes serves the
     // three (matrix.rs:167-193 shares a plane input per format)
@@ -2201,7 +2230,7 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     // session.rs:112-118 with add_engram (session.rs:175-188)
     if (e_key != nullptr) {
         n3_unit_rms(xs_, d, a_, red, cv_);
-        if (tid < d) sc_[tid] = key_r[0];
+        if (tid < d) sc_[tid] = key_r;
         __syncthreads();
         n3_unit_rms(sc_, d, sc_, red, cv_);
         if (tid == 0) {  // Iterator::sum: in order from -0.0
@@ -2210,10 +2239,10 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
         }
         __syncthreads();
         const float alpha = alpha_s;
-        if (tid < d) xs_[tid] = xs_[tid] + alpha * value_r[0];
+        if (tid < d) xs_[tid] = xs_[tid] + alpha * value_r;
         __syncthreads();
     }
-    if (tid < d) mx_[tid] = norm_in_r[0];
+    if (tid < d) mx_[tid] = norm_in_r;
     __syncthreads();
     if (out_rotated != nullptr) {
         n3_norm(xs_, mx_, d, a_, red, cv_);
@@ -2517,6 +2546,7 @@ bool fused_applies(const rn_n3_model* m) {
     // routing rows in 16-byte units; its norms take squares four a read
     const int d = (int)g.d_model;
     if (d % 256 != 0 || (3 * d + L * d) / 256 > 2 * (kN3Block / 64)) return false;
+    if (g.engram_conv_taps > (uint32_t)kN3MaxTaps) return false;  // the boundary's site convolution
     if (m->embedding->cb.padded > kN3Hadamard || m->embedding->group > 256) return false;  // the logits' input
     if (m->phi_pre->cb.row_bytes % 16 != 0) return false;
     auto aligned = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
@@ -3142,6 +3172,15 @@ int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
         b.residual = s->residual;
         b.key = site >= 0 ? s->ekey[(size_t)site] : nullptr;
         b.value = site >= 0 ? s->evalue[(size_t)site] : nullptr;
+        if (site >= 0) {  // the site's convolution in the boundary (enqueue_sites leaves it)
+            b.raw = s->site_raw[(size_t)site];
+            b.ring = s->rings[(size_t)site];
+            b.taps = m->engrams[(size_t)site].taps;
+            b.position = position;
+            b.keep = std::max(1, ((int)g.engram_conv_taps - 1) * (int)g.engram_conv_dilation + 1);
+            b.ntaps = (int)g.engram_conv_taps;
+            b.dilation = (int)g.engram_conv_dilation;
+        }
         b.norm_in = y.norm_in;
         b.x = s->x;
         b.qpadded = y.qkvg->cb.padded;
@@ -3250,8 +3289,9 @@ int fused_layers(rn_n3_session* s, int position, float* cur, float* nxt) {
 
 namespace {
 
-// The engram sites of a push at `position` (engram.rs:30-112)
-int enqueue_sites(rn_n3_session* s, int position) {
+// The engram sites of a push at `position` (engram.rs:30-112); the value
+// convolutions only with `conv`
+int enqueue_sites(rn_n3_session* s, int position, bool conv) {
     const rn_n3_model* m = s->m;
     const rn_geometry& g = m->g;
     const int d = (int)g.d_model;
@@ -3309,9 +3349,11 @@ int enqueue_sites(rn_n3_session* s, int position) {
                 N3_CALL(product(eg.value, jobs.job[2 * k + 1].x, jobs.job[2 * k + 1].y, st));
             }
         }
-        rn_launch(n3_engram_conv_kernel, dim3((d + 255) / 256, 1, ns), dim3(256), 0, st, cs, position, keep,
-                  (int)g.engram_conv_taps, (int)g.engram_conv_dilation, d, 1);
-        N3_HIP(hipGetLastError());
+        if (conv) {
+            rn_launch(n3_engram_conv_kernel, dim3((d + 255) / 256, 1, ns), dim3(256), 0, st, cs, position, keep,
+                      (int)g.engram_conv_taps, (int)g.engram_conv_dilation, d, 1);
+            N3_HIP(hipGetLastError());
+        }
     }
     return RN_OK;
 }
@@ -3371,7 +3413,7 @@ int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
     // engram sites (engram.rs:30-112), before the layers: one launch gathers
     // and prepares the active sites' inputs, one runs their key and value
     // products, one their value convolutions
-    N3_CALL(enqueue_sites(s, position));
+    N3_CALL(enqueue_sites(s, position, !s->fused));  // (the fused layers convolve in their boundary)
 
     N3_CALL(s->fused ? fused_layers(s, position, cur, nxt) : stepwise_layers(s, position, cur, nxt));
     s->lrot_ready = s->fused;
