@@ -308,17 +308,11 @@ __global__ void n3_set_tokens_kernel(uint32_t* tokens, int position, int count, 
 // cell + b * cell_stride (prefill.rs:21-29 for a run of tokens). With `set`
 // (one token) the token is *source (the greedy argmax) or `value`, and the
 // block records it at tokens[position].
-__global__ __launch_bounds__(1024) void n3_embed_kernel(CodebookParams c, uint32_t* tokens, int position, int d,
-                                                        int lanes, float scale, float* stream, float* cell,
-                                                        int stream_stride, int cell_stride, int set,
-                                                        const uint32_t* source, uint32_t value) {
+__device__ __forceinline__ void n3_embed_body(const CodebookParams& c, uint32_t token, int d, int lanes, float scale,
+                                              float* stream, float* cell) {
     const int u = threadIdx.x, runs = c.padded / 16, rpg = c.group / 16, G = c.padded / c.group;
     const int ib = c.bits == 5 ? 2 : c.bits;
     const bool valid = u < runs;
-    stream += (size_t)blockIdx.x * stream_stride;
-    cell += (size_t)blockIdx.x * cell_stride;
-    const uint32_t token = set ? (source != nullptr ? *source : value) : tokens[position + blockIdx.x];
-    if (set && u == 0) tokens[position] = token;
     const uint8_t* row = c.packed + (size_t)token * c.row_bytes;
     const float norm = valid ? __half2float(__ushort_as_half(c.norms[(size_t)token * G + (16 * u) / c.group])) : 0.0f;
     float x[16];
@@ -360,6 +354,16 @@ __global__ __launch_bounds__(1024) void n3_embed_kernel(CodebookParams c, uint32
     }
 }
 
+__global__ __launch_bounds__(1024) void n3_embed_kernel(CodebookParams c, uint32_t* tokens, int position, int d,
+                                                        int lanes, float scale, float* stream, float* cell,
+                                                        int stream_stride, int cell_stride, int set,
+                                                        const uint32_t* source, uint32_t value) {
+    const uint32_t token = set ? (source != nullptr ? *source : value) : tokens[position + blockIdx.x];
+    if (set && threadIdx.x == 0) tokens[position] = token;
+    n3_embed_body(c, token, d, lanes, scale, stream + (size_t)blockIdx.x * stream_stride,
+                  cell + (size_t)blockIdx.x * cell_stride);
+}
+
 struct N3GatherParams {
     CodebookParams tables;
     int count, sub, slots, position;
@@ -380,6 +384,17 @@ constexpr int kN3MaxSites = 4;  // engram sites one launch serves
 
 struct N3GatherSites {
     N3GatherParams site[kN3MaxSites];
+    int sites;  // blocks 0 .. sites - 1 (blockIdx.y) gather; with `embed`, block `sites` embeds
+    // the push's token: *source (the greedy argmax) or value, recorded at
+    // tokens[position] by the embedding block; the gathers take it from here
+    int embed;
+    CodebookParams table;
+    uint32_t* tokens;
+    int position, d, lanes;
+    float scale;
+    float *stream, *cell;
+    const uint32_t* source;
+    uint32_t value;
 };
 
 // engram.rs:66-82: row table * slots + index of each table (zeros while the
@@ -390,6 +405,13 @@ __global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherSites sites
     __shared__ float buf[kN3MaxWidth];
     __shared__ float red[32];
     __shared__ int index_s[kN3MaxTables], order_s[kN3MaxTables];
+    const bool mine = sites.embed != 0;  // the push's token comes from the launch
+    const uint32_t now = mine ? (sites.source != nullptr ? *sites.source : sites.value) : 0u;
+    if (mine && (int)blockIdx.y == sites.sites) {  // session.rs:86-97 for the push's token
+        if (threadIdx.x == 0) sites.tokens[sites.position] = now;
+        n3_embed_body(sites.table, now, sites.d, sites.lanes, sites.scale, sites.stream, sites.cell);
+        return;
+    }
     const N3GatherParams& p = sites.site[blockIdx.y];  // the site (one launch serves a push's sites)
     const CodebookParams& c = p.tables;
     const int n = p.count * p.sub, ib = c.bits == 5 ? 2 : c.bits, G = c.padded / c.group;
@@ -399,7 +421,7 @@ __global__ __launch_bounds__(kN3Block) void n3_gather_kernel(N3GatherSites sites
         const int t = threadIdx.x, o = t / p.heads_per_order, head = t - o * p.heads_per_order;
         uint32_t acc = 0x9E3779B9u * (uint32_t)(o * p.stride + head + 1);
         for (int back = 0; back < p.orders[o]; ++back) {
-            const uint32_t token = position >= back ? p.tokens[position - back] : 0u;
+            const uint32_t token = position >= back ? (mine && back == 0 ? now : p.tokens[position - back]) : 0u;
             acc = (acc ^ token) * 0x01000193u;
         }
         acc ^= acc >> 15;
@@ -3291,7 +3313,7 @@ namespace {
 
 // The engram sites of a push at `position` (engram.rs:30-112); the value
 // convolutions only with `conv`
-int enqueue_sites(rn_n3_session* s, int position, bool conv) {
+int enqueue_sites(rn_n3_session* s, int position, bool conv, const N3GatherSites* embed) {
     const rn_n3_model* m = s->m;
     const rn_geometry& g = m->g;
     const int d = (int)g.d_model;
@@ -3301,9 +3323,11 @@ int enqueue_sites(rn_n3_session* s, int position, bool conv) {
     std::vector<int> act;
     for (uint32_t e = 0; e < g.engram_site_count; ++e)
         if (site_active(m, (int)e)) act.push_back((int)e);
-    for (size_t b0 = 0; b0 < act.size(); b0 += kN3MaxSites / 2) {  // two products a site, four a launch
-        const int ns = (int)std::min(act.size() - b0, (size_t)kN3MaxSites / 2);
+    for (size_t b0 = 0; b0 < std::max<size_t>(act.size(), 1); b0 += kN3MaxSites / 2) {  // two products a site
+        const int ns = (int)std::min(act.size() - std::min(b0, act.size()), (size_t)kN3MaxSites / 2);
         N3GatherSites gs{};
+        if (embed != nullptr && b0 == 0) gs = *embed;  // the first launch also embeds the push's token
+        gs.sites = ns;
         N3ConvSites cs{};
         CodebookJobs jobs{};
         bool joint = true;
@@ -3332,8 +3356,9 @@ int enqueue_sites(rn_n3_session* s, int position, bool conv) {
             cs.taps[k] = eg.taps;
             cs.value[k] = s->evalue[(size_t)e];
         }
-        rn_launch(n3_gather_kernel, dim3(1, ns), dim3(kN3Block), 0, st, gs);
+        rn_launch(n3_gather_kernel, dim3(1, ns + (gs.embed ? 1 : 0)), dim3(kN3Block), 0, st, gs);
         N3_HIP(hipGetLastError());
+        if (ns == 0) continue;
         bool same = joint;
         for (int j = 1; j < 2 * ns; ++j) {
             const CodebookParams &a = jobs.job[0].p, &b = jobs.job[j].p;
@@ -3402,18 +3427,25 @@ int enqueue_push(rn_n3_session* s, uint32_t token, const uint32_t* source) {
     const rn_geometry& g = m->g;
     const int d = (int)g.d_model, lanes = (int)g.mhc_lanes;
     const int position = s->length;
-    hipStream_t st = s->stream;
     float* cur = s->stream_a;
     float* nxt = s->stream_b;
-    const int embed_threads = ((m->embedding->cb.padded / 16 + 63) / 64) * 64;
-    rn_launch(n3_embed_kernel, dim3(1), dim3(embed_threads), 0, st, m->embedding->cb, s->tokens_dev, position, d, lanes,
-              sqrtf((float)d), cur, s->cells, 0, 0, 1, source, token);
-    N3_HIP(hipGetLastError());
-
-    // engram sites (engram.rs:30-112), before the layers: one launch gathers
-    // and prepares the active sites' inputs, one runs their key and value
-    // products, one their value convolutions
-    N3_CALL(enqueue_sites(s, position, !s->fused));  // (the fused layers convolve in their boundary)
+    // the embedding (session.rs:86-97) and the engram sites (engram.rs:30-112)
+    // before the layers: one launch embeds the token and gathers and prepares
+    // the active sites' inputs, one runs their key and value products, one
+    // their value convolutions (the fused layers convolve in their boundary)
+    N3GatherSites em{};
+    em.embed = 1;
+    em.table = m->embedding->cb;
+    em.tokens = s->tokens_dev;
+    em.position = position;
+    em.d = d;
+    em.lanes = lanes;
+    em.scale = sqrtf((float)d);
+    em.stream = cur;
+    em.cell = s->cells;
+    em.source = source;
+    em.value = token;
+    N3_CALL(enqueue_sites(s, position, !s->fused, &em));
 
     N3_CALL(s->fused ? fused_layers(s, position, cur, nxt) : stepwise_layers(s, position, cur, nxt));
     s->lrot_ready = s->fused;
