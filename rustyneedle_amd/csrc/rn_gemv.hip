@@ -205,7 +205,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
         int part = dot16(w[j], xc[j], 0);
-        part = part + __shfl_xor(part, 1, 64);
+        part = part + lane_xor_i<1>(part);  // the lane pair of a chunk (DPP)
         if ((lane & 1) == 0) acc_s[load_row(j) * G + load_chunk(j) / 2] = part;
     }
     __syncthreads();
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
             sg.y[r] = (p.res != nullptr ? p.res[r] : sg.y[r]) + total;
         }
     } else if constexpr (EPI == kSilu) {
-        const float up = __shfl(total, (lane + H) & 63, 64);
+        const float up = lane_xor<H>(total);  // lane + H for the lanes below H (DPP / lane swap)
         if (lane < H && mine) sg.y[blk * H + lane] = silu(total) * up;
     } else {  // kArgmax: logits plus this block's greedy key (generator.rs:257-265);
               // argmax_finalize reduces the keys (device atomics would serialise)
