@@ -258,8 +258,10 @@ int rn_n3_model_output_vocab(const rn_n3_model* model, int* count);             
 /* Session::new (session.rs:30-42) with room for `capacity` tokens (<= 8192). */
 int rn_n3_session_create(const rn_n3_model* model, int capacity, rn_n3_session** out);
 int rn_n3_session_free(rn_n3_session* session);
-/* Session::push (session.rs:76-148) and Session::feed (session.rs:58-74). Tokens
- * below the vocabulary; RN_ERR_ARGUMENT past the capacity. */
+/* Session::push (session.rs:76-148) and Session::feed (session.rs:58-74; at
+ * least 4 tokens run as batched prefills, prefill.rs:10-99, of up to 256 tokens,
+ * with each token's arithmetic a push's). Tokens below the vocabulary;
+ * RN_ERR_ARGUMENT past the capacity. */
 int rn_n3_session_push(rn_n3_session* session, uint32_t token);
 int rn_n3_session_feed(rn_n3_session* session, const uint32_t* tokens, int count);
 /* Generator::run_turn's greedy loop (generator.rs:199-230, argmax at 257-265)
