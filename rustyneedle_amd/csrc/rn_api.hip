@@ -1596,9 +1596,16 @@ int rn_session_feed(rn_session* s, const uint32_t* tokens, int count) {
     };
     for (int l = 0; l < c.layers; ++l) {
         const LayerDev& L = m->layers[l];
-        RN_HIP(launch_gemm(rows(X, L.norm_attn, L.qkv, 3 * d, d, QKV, 3 * d, 0), kGemmStore, kPanel, false, st));
-        RN_HIP(launch_rope_append(QKV, Q, s->kc, s->vc, l, c.heads, s->capacity, d, first, count, m->rope_cos,
-                                  m->rope_sin, st));
+        GemmParams qkv = rows(X, L.norm_attn, L.qkv, 3 * d, d, QKV, 3 * d, 0);
+        if ((d == 384 || d == 512) && c.heads * 64 == d) {
+            // the product's epilogue rotates q and k and appends k and v
+            qkv.rope = GemmRope{Q, s->kc, s->vc, m->rope_cos, m->rope_sin, l, c.heads, s->capacity, first};
+            RN_HIP(launch_gemm(qkv, kGemmRope, kPanel, false, st));
+        } else {
+            RN_HIP(launch_gemm(qkv, kGemmStore, kPanel, false, st));
+            RN_HIP(launch_rope_append(QKV, Q, s->kc, s->vc, l, c.heads, s->capacity, d, first, count, m->rope_cos,
+                                      m->rope_sin, st));
+        }
         AttendParams ap{};
         ap.q = Q;
         ap.kc = s->kc;

@@ -418,10 +418,13 @@ __global__ __launch_bounds__(256) void gemm_panel_kernel(GemmParams p) {
     using S = PanelShape<K, BM, BN>;
     constexpr int G = S::kG, PITCH = S::kPitch;
     constexpr bool kSilu = EPI == kGemmSilu;
+    constexpr bool kRope = EPI == kGemmRope;
     static_assert(!kSilu || SN == 2, "the gated FFN pairs gate and up sub-tiles");
+    static_assert(!kRope || (SM == 1 && SN == 1 && WAVES_M == 2), "rotary: wave column 0 the first halves, 1 the second");
     static_assert(K % 32 == 0 && G % 4 == 0, "whole groups, scale quads");
     __shared__ __align__(16) int8_t panel_s[(BM + BN) * PITCH];
     __shared__ __align__(16) float sw_s[BN * G];
+    __shared__ float pair_s[kRope ? BM : 1][kRope ? BN + 1 : 1];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -432,17 +435,22 @@ __global__ __launch_bounds__(256) void gemm_panel_kernel(GemmParams p) {
     const int m0 = mt * BM;
 
     // weight row of local tile column c (silu: wave column block wn holds 16
-    // outputs; its sub-tile column 0 is their gate rows, column 1 their up rows)
+    // outputs; its sub-tile column 0 is their gate rows, column 1 their up rows;
+    // rotary: tiles nt = 2 hp + s cover pairs 16 s .. 16 s + 15 of head row
+    // block hp, wave column 0 their first halves, wave column 1 their second)
     auto weight_row = [&](int c) -> int {
         if constexpr (kSilu) {
             const int w = c / 32, j = (c / 16) & 1, o = nt * (BN / 2) + w * 16 + (c & 15);
             return j == 0 ? o : p.half + o;
+        } else if constexpr (kRope) {
+            return (nt >> 1) * 64 + (c >> 4) * 32 + (nt & 1) * 16 + (c & 15);
         } else {
             return nt * BN + c;
         }
     };
     auto row_ok = [&](int c) -> bool {
         if constexpr (kSilu) return nt * (BN / 2) + (c / 32) * 16 + (c & 15) < p.half;
+        else if constexpr (kRope) return (nt >> 1) * 64 < p.N;
         else return nt * BN + c < p.N;
     };
 
@@ -525,6 +533,38 @@ __global__ __launch_bounds__(256) void gemm_panel_kernel(GemmParams p) {
     }
 
     // 3. epilogue
+    if constexpr (kRope) {
+        // the rotate-half pairs (i, i + 32) of one head meet in LDS; then a
+        // thread per (row, pair) as rope_append_kernel does for one token
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pair_s[wm * 16 + 4 * kq + r][wn * 16 + r16] = total[0][0][r];
+        __syncthreads();
+        const int hp = nt >> 1, part = hp / p.rope.heads, h = hp - part * p.rope.heads;
+        const int d = p.rope.heads * 64;
+#pragma unroll
+        for (int e = tid; e < BM * 16; e += 256) {
+            const int lr = e >> 4, pi = e & 15, m = m0 + lr;
+            if (m >= p.M || part > 2) continue;
+            const int i = (nt & 1) * 16 + pi, pos = p.rope.first + m;
+            const float a = pair_s[lr][pi], b = pair_s[lr][16 + pi];
+            const size_t base = (((size_t)p.rope.layer * p.rope.heads + h) * p.rope.capacity + pos) * 64;
+            if (part == 2) {
+                p.rope.vc[base + i] = __float2half_rn(a);
+                p.rope.vc[base + i + 32] = __float2half_rn(b);
+            } else {
+                const float c = p.rope.cos[(size_t)pos * 32 + i], s = p.rope.sin[(size_t)pos * 32 + i];
+                const float x0 = a * c - b * s, x1 = b * c + a * s;
+                if (part == 0) {
+                    p.rope.q_out[(size_t)m * d + h * 64 + i] = x0;
+                    p.rope.q_out[(size_t)m * d + h * 64 + i + 32] = x1;
+                } else {
+                    p.rope.kc[base + i] = __float2half_rn(x0);
+                    p.rope.kc[base + i + 32] = __float2half_rn(x1);
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < SM; ++i)
 #pragma unroll
@@ -565,7 +605,7 @@ static void launch_chain(const GemmParams& p, hipStream_t stream) {
             default: break;
         }
     }
-    rn_launch((gemm_chain_kernel<SM, SN, WAVES_M, EPI, FORM, DUMP>), grid, block, 0, stream, p);
+    if constexpr (EPI != kGemmRope) rn_launch((gemm_chain_kernel<SM, SN, WAVES_M, EPI, FORM, DUMP>), grid, block, 0, stream, p);
 }
 
 // Tile shape: the one with the most blocks among 64 x 64, 64 x 32, 32 x 64 and
@@ -641,6 +681,16 @@ static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
 // codes to X / sx first.
 template <int EPI, int FORM, bool DUMP, int AIN>
 static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
+    if constexpr (EPI == kGemmRope) {
+        // the 32 x 32 panel tile at every size (its epilogue pairs the two wave columns)
+        if (AIN != kRowsCodes) {
+            const hipError_t e = launch_norm_quantise(p.Xf, p.gain, p.M, p.K, p.eps, const_cast<int8_t*>(p.X),
+                                                      const_cast<float*>(p.sx), nullptr, stream);
+            if (e != hipSuccess) return e;
+        }
+        launch_chain<1, 1, 2, kGemmRope, FORM, false>(p, stream);
+        return hipGetLastError();
+    } else {
     const int pick = p.K == 1152 ? (EPI == kGemmSilu ? 2 : 3) : chain_pick<EPI>(p);
     const int n_eff = EPI == kGemmSilu ? 2 * p.half : p.N;
     const size_t reread = (size_t)((n_eff + 31) / 32) * (size_t)p.M * (size_t)p.K * sizeof(float);
@@ -658,6 +708,7 @@ static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
     else
         launch_by_rows<EPI, FORM, DUMP, kRowsCodes>(p, stream);
     return hipGetLastError();
+    }
 }
 
 template <int EPI>
@@ -674,6 +725,11 @@ hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, h
     // 1152 columns (the stem's im2col rows at d 384) have no split-kernel tile: codes only, chain kernel
     if (p.K == 1152 && (p.Xf != nullptr || dump)) return hipErrorInvalidValue;
     if (epilogue == kGemmSilu && (p.half % 16 != 0 || p.N != 2 * p.half)) return hipErrorInvalidValue;
+    if (epilogue == kGemmRope &&
+        (dump || form != kPanel || (p.K != 384 && p.K != 512) || p.rope.heads <= 0 || p.N != 3 * 64 * p.rope.heads ||
+         p.rope.q_out == nullptr || p.rope.kc == nullptr || p.rope.vc == nullptr || p.rope.cos == nullptr ||
+         p.rope.sin == nullptr || p.rope.first < 0 || p.rope.first + p.M > p.rope.capacity))
+        return hipErrorInvalidValue;
     if (p.Xf != nullptr && (p.X == nullptr || p.sx == nullptr)) return hipErrorInvalidValue;
     const int ain = p.Xf == nullptr ? kRowsCodes : kRowsQuant;
     if (dump || form == kPlane) {
@@ -694,6 +750,7 @@ hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, h
         case kGemmResidual: return launch_panel<kGemmResidual>(p, ain, stream);
         case kGemmSilu: return launch_panel<kGemmSilu>(p, ain, stream);
         case kGemmStoreSilu: return launch_panel<kGemmStoreSilu>(p, ain, stream);
+        case kGemmRope: return launch_panel<kGemmRope>(p, ain, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -163,7 +163,23 @@ hipError_t launch_rope_append(const float* qkv, float* q_out, __half* kc, __half
                               const float* rope_sin, hipStream_t stream);
 
 // ---- multi-token products (i8 MFMA) ----------------------------------------------
-enum GemmEpilogue { kGemmStore = 0, kGemmResidual = 1, kGemmSilu = 2, kGemmStoreSilu = 3 };  // last: y = silu(total)
+// kGemmStoreSilu: y = silu(total); kGemmRope: the fused q/k/v rows of one
+// layer, rotated and appended to the cache instead of stored (GemmParams::rope)
+enum GemmEpilogue { kGemmStore = 0, kGemmResidual = 1, kGemmSilu = 2, kGemmStoreSilu = 3, kGemmRope = 4 };
+
+// The q/k/v epilogue of a prefill product (kGemmRope): output columns are the q,
+// k and v rows of `heads` heads of 64 (N == 3 * heads * 64); row m is position
+// first + m. q is rotated into q_out [M][heads * 64], k rotated and v copied
+// into this layer's fp16 caches [layers][heads][capacity][64]
+// (crates/model/src/prefill.rs:10-99 with the rotary of ops.rs:131-141).
+struct GemmRope {
+    float* q_out;
+    __half* kc;
+    __half* vc;
+    const float* cos;  // [positions][32]
+    const float* sin;
+    int layer, heads, capacity, first;
+};
 
 struct GemmParams {
     const int8_t* X;   // [M][K] quantised tokens
@@ -182,6 +198,7 @@ struct GemmParams {
     const float* Xf;
     const float* gain;
     float eps;
+    GemmRope rope;     // kGemmRope only
 };
 
 hipError_t launch_gemm(const GemmParams& p, int epilogue, int form, bool dump, hipStream_t stream);
