@@ -770,7 +770,7 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
                                                             int8_t* codes, float* scales, float* normed,
                                                             size_t x_stride) {
     constexpr int n = NV * 128;
-    extern __shared__ float sq_s[];  // [4][n] when gain != nullptr
+    extern __shared__ float sq_s[];  // [4][n + 8] when gain != nullptr
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + wave;
     const bool live = row < count;
@@ -778,41 +778,52 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
     float2 v[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) v[i] = src[lane + 64 * i];
+    float peak = 0.0f;
     if (gain != nullptr) {
-        float* sq = sq_s + wave * n;
+        // run r of the squares at sq[r * (run + 1)]: the 8 chain lanes read 8 banks
         constexpr int run = n >> 3;
+        float* sq = sq_s + wave * (n + 8);
+        const float2* g2 = reinterpret_cast<const float2*>(gain);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int e = 2 * (lane + 64 * i);  // elements e, e+1; e % 8 is 0, 2, 4 or 6
             const int p = e & 7, c = e >> 3;
-            sq[(p + 0) * run + c] = v[i].x * v[i].x;
-            sq[(p + 1) * run + c] = v[i].y * v[i].y;
+            sq[(p + 0) * (run + 1) + c] = v[i].x * v[i].x;
+            sq[(p + 1) * (run + 1) + c] = v[i].y * v[i].y;
         }
+        // the gained values and their peak while the squares are summed: the
+        // normed value is fl(m * inverse) with inverse > 0 and rounding is
+        // monotone, so the normed peak is fl(peak(|m|) * inverse)
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const float2 g = g2[lane + 64 * i];
+            v[i].x = (1.0f + g.x) * v[i].x;
+            v[i].y = (1.0f + g.y) * v[i].y;
+            peak = fmaxf(peak, fmaxf(fabsf(v[i].x), fabsf(v[i].y)));
+        }
+        peak = wave_max(peak);
         __syncthreads();
         float part = 0.0f;
         if (lane < 8) {
-            const float* r = sq + lane * run;
+            const float* r = sq + lane * (run + 1);
+#pragma unroll 16
             for (int c = 0; c < run; ++c) part = part + r[c];
         }
         float total = sum_lanes_0_to_7(part);
         total = total + 0.0f;  // the empty tail of the 8-lane sum
         const float inverse = 1.0f / sqrtf(total / (float)n + eps);
-        const float2* g2 = reinterpret_cast<const float2*>(gain);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const float2 g = g2[lane + 64 * i];
-            v[i].x = ((1.0f + g.x) * v[i].x) * inverse;
-            v[i].y = ((1.0f + g.y) * v[i].y) * inverse;
+            v[i].x = v[i].x * inverse;
+            v[i].y = v[i].y * inverse;
             if (normed != nullptr && live) reinterpret_cast<float2*>(normed + (size_t)row * n)[lane + 64 * i] = v[i];
         }
-    }
-    float peak = 0.0f;
+        peak = peak * inverse;
+    } else {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        peak = fmaxf(peak, fabsf(v[i].x));
-        peak = fmaxf(peak, fabsf(v[i].y));
+        for (int i = 0; i < NV; ++i) peak = fmaxf(peak, fmaxf(fabsf(v[i].x), fabsf(v[i].y)));
+        peak = wave_max(peak);
     }
-    peak = wave_max(peak);
     const float scale = int8_scale_from_peak(peak);
     if (!live) return;  // the whole wave: one row per wave
     if (codes != nullptr) {
@@ -832,7 +843,7 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
 hipError_t launch_norm_quantise(const float* x, const float* gain, int count, int n, float eps, int8_t* codes,
                                 float* scales, float* normed, hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    const size_t lds = gain != nullptr ? 4 * sizeof(float) * (size_t)n : 0;
+    const size_t lds = gain != nullptr ? 4 * sizeof(float) * (size_t)(n + 8) : 0;
     const dim3 grid((count + 3) / 4), block(256);
 #define RN_NQ(NV) \
     rn_launch(norm_quantise_kernel<NV>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed, (size_t)n)
