@@ -649,7 +649,9 @@ static void launch_split(const GemmParams& p, hipStream_t stream) {
     rn_launch((gemm_split_kernel<G, BM, BN, EPI, FORM, DUMP, AIN>), dim3(mtiles * ntiles), dim3(1024), 0, stream, p);
 }
 
-// tiles sized so that the int32 sums of a tile fill 64 KB of LDS
+// 16-row tiles where the 16 waves divide the jobs: these grids are small, and
+// at 512 columns twice the blocks of 32-row tiles measured faster at 64 and
+// 256 rows (16 x 16 tiles did not)
 template <int EPI, int FORM, bool DUMP, int AIN>
 static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
     switch (p.K) {
@@ -657,7 +659,7 @@ static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
             launch_split<12, 32, 32, EPI, FORM, DUMP, AIN>(p, stream);
             break;
         case 512:
-            launch_split<16, 32, 32, EPI, FORM, DUMP, AIN>(p, stream);
+            launch_split<16, 16, 32, EPI, FORM, DUMP, AIN>(p, stream);
             break;
         case 1024:
             launch_split<32, 16, 32, EPI, FORM, DUMP, AIN>(p, stream);
