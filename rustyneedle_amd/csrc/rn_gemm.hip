@@ -39,8 +39,10 @@ struct SplitShape {
 // Token rows of the split kernel: int8 codes and scales given (kRowsCodes), or
 // float rows quantised in the prologue (kRowsQuant: quantise_int8 of
 // ops.rs:103-118, identical to norm_quantise_kernel without gains). One wave
-// per row: lane l holds elements E l .. E l + E - 1.
-enum RowsIn { kRowsCodes = 0, kRowsQuant = 1 };
+// per row: lane l holds elements E l .. E l + E - 1. kRowsNormQuant: the same
+// after the zero-centred norm with `gain` (identical to norm_quantise_kernel
+// with gains; 16-row tiles, one row per wave).
+enum RowsIn { kRowsCodes = 0, kRowsQuant = 1, kRowsNormQuant = 2 };
 
 template <int G, int BM, int BN, int EPI, int FORM, bool DUMP, int AIN>
 __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
@@ -48,6 +50,7 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
     constexpr bool kSilu = EPI == kGemmSilu;
     constexpr int K = G * kGroup;
     static_assert(AIN == kRowsCodes || (BM % 16 == 0 && K % 64 == 0), "whole rows per wave, whole elements per lane");
+    static_assert(AIN != kRowsNormQuant || BM == 16, "one normed row per wave");
     // Operand rows padded by 32 bytes: the 16 rows x 4 quarters of one MFMA
     // fragment read then cover all 64 banks twice (the minimum for 512 bytes).
     constexpr int KP = K + 32;
@@ -61,6 +64,8 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
     __shared__ float sw_s[BN][G + 1];
     __shared__ float sx_s[BM];
     __shared__ float tile[kSilu ? BM : 1][kSilu ? BN + 1 : 1];
+    // kRowsNormQuant: a wave's squares, run r (elements e = r mod 8) at r * (K / 8 + 1)
+    __shared__ float sq_s[AIN == kRowsNormQuant ? 16 : 1][AIN == kRowsNormQuant ? K + 8 : 1];
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int mtiles = (p.M + BM - 1) / BM;
@@ -124,11 +129,46 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
 #pragma unroll
         for (int rr = 0; rr < RPW; ++rr) {
             const int row = wave + 16 * rr;
-            const float* v = xv[rr];
+            float* v = xv[rr];
             float peak = 0.0f;
+            if constexpr (AIN == kRowsNormQuant) {
+                // the ordered 8-run sum of squares of norm_quantise_kernel (ops.rs:7-17),
+                // the gained values m = (1 + g) x and their peak beside it; the normed
+                // peak is fl(peak(|m|) * inverse) (rounding is monotone, inverse > 0)
+                constexpr int run = K / 8;
+                float* sq = sq_s[wave];
 #pragma unroll
-            for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
-            const float scale = int8_scale_from_peak(wave_max(peak));
+                for (int e = 0; e < E; ++e) {
+                    const int ge = lane * E + e;
+                    sq[(ge & 7) * (run + 1) + (ge >> 3)] = v[e] * v[e];
+                }
+                float g[E];
+                load_floats<E>(p.gain + lane * E, g);
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    v[e] = (1.0f + g[e]) * v[e];
+                    peak = fmaxf(peak, fabsf(v[e]));
+                }
+                peak = wave_max(peak);
+                __syncthreads();
+                float part = 0.0f;
+                if (lane < 8) {
+                    const float* r = sq + lane * (run + 1);
+#pragma unroll 16
+                    for (int c = 0; c < run; ++c) part = part + r[c];
+                }
+                float total = sum_lanes_0_to_7(part);
+                total = total + 0.0f;  // the empty tail of the 8-lane sum
+                const float inverse = 1.0f / sqrtf(total / (float)K + p.eps);
+#pragma unroll
+                for (int e = 0; e < E; ++e) v[e] = v[e] * inverse;
+                peak = peak * inverse;
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
+                peak = wave_max(peak);
+            }
+            const float scale = int8_scale_from_peak(peak);
             float y[E];
             quotients<E>(v, scale, y);
             int8_t* dst = &a_s[row][lane * E];
@@ -698,7 +738,9 @@ static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
     const size_t reread = (size_t)((n_eff + 31) / 32) * (size_t)p.M * (size_t)p.K * sizeof(float);
     const bool fused =
         AIN != kRowsCodes && p.gain == nullptr && pick < 0 && p.K <= 512 && reread <= ((size_t)8 << 20);
-    if (AIN != kRowsCodes && !fused) {
+    const bool fused_norm =
+        AIN != kRowsCodes && p.gain != nullptr && pick < 0 && p.K == 512 && reread <= ((size_t)16 << 20);
+    if (AIN != kRowsCodes && !fused && !fused_norm) {
         const hipError_t e = launch_norm_quantise(p.Xf, p.gain, p.M, p.K, p.eps, const_cast<int8_t*>(p.X),
                                                   const_cast<float*>(p.sx), nullptr, stream);
         if (e != hipSuccess) return e;
@@ -707,6 +749,8 @@ static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
         launch_chain_shape<EPI, FORM, DUMP>(p, pick, stream);
     else if (fused)
         launch_by_rows<EPI, FORM, DUMP, kRowsQuant>(p, stream);
+    else if (fused_norm)
+        launch_split<16, 16, 32, EPI, FORM, DUMP, kRowsNormQuant>(p, stream);
     else
         launch_by_rows<EPI, FORM, DUMP, kRowsCodes>(p, stream);
     return hipGetLastError();
