@@ -718,9 +718,10 @@ static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
 // re-reads little: every column tile of the grid quantises its own rows
 // again, so the fused form is taken for rows of at most 512 and at most 8 MB of
 // re-read floats per launch (measured: the batch-64 and 256-token out products
-// gain about 1.8 us; wider or taller grids, and the normed inputs, do not).
-// Otherwise a quantise launch (with the norm when `gain` is set) writes the
-// codes to X / sx first.
+// gain about 1.8 us; wider or taller grids do not). Normed rows of 512 are
+// normed and quantised in the prologue up to 16 MB of re-read (batch-64 QKV
+// and gate/up: 0.93 -> 0.91 ms per step). Otherwise a quantise launch (with
+// the norm when `gain` is set) writes the codes to X / sx first.
 template <int EPI, int FORM, bool DUMP, int AIN>
 static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
     if constexpr (EPI == kGemmRope) {
