@@ -718,10 +718,12 @@ static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
 // re-reads little: every column tile of the grid quantises its own rows
 // again, so the fused form is taken for rows of at most 512 and at most 8 MB of
 // re-read floats per launch (measured: the batch-64 and 256-token out products
-// gain about 1.8 us; wider or taller grids do not). Normed rows of 512 are
-// normed and quantised in the prologue up to 16 MB of re-read (batch-64 QKV
-// and gate/up: 0.93 -> 0.91 ms per step). Otherwise a quantise launch (with
-// the norm when `gain` is set) writes the codes to X / sx first.
+// gain about 1.8 us; wider or taller grids do not). Float rows of 512 with a
+// norm are normed and quantised in the prologue under the same 8 MB limit
+// (the batch-64 QKV product: 6.9 us against 4.5 + 3.8 us for the product and
+// the norm launch; its gate/up product at 16 MB measured 9.8 against 9.5 us).
+// Otherwise a quantise launch (with the norm when `gain` is set) writes the
+// codes to X / sx first.
 template <int EPI, int FORM, bool DUMP, int AIN>
 static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
     if constexpr (EPI == kGemmRope) {
@@ -740,7 +742,7 @@ static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
     const bool fused =
         AIN != kRowsCodes && p.gain == nullptr && pick < 0 && p.K <= 512 && reread <= ((size_t)8 << 20);
     const bool fused_norm =
-        AIN != kRowsCodes && p.gain != nullptr && pick < 0 && p.K == 512 && reread <= ((size_t)16 << 20);
+        AIN != kRowsCodes && p.gain != nullptr && pick < 0 && p.K == 512 && reread <= ((size_t)8 << 20);
     if (AIN != kRowsCodes && !fused && !fused_norm) {
         const hipError_t e = launch_norm_quantise(p.Xf, p.gain, p.M, p.K, p.eps, const_cast<int8_t*>(p.X),
                                                   const_cast<float*>(p.sx), nullptr, stream);
