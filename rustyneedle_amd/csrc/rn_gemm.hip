@@ -719,11 +719,12 @@ static void launch_by_rows(const GemmParams& p, hipStream_t stream) {
 // again, so the fused form is taken for rows of at most 512 and at most 8 MB of
 // re-read floats per launch (measured: the batch-64 and 256-token out products
 // gain about 1.8 us; wider or taller grids do not). Float rows of 512 with a
-// norm are normed and quantised in the prologue under the same 8 MB limit
-// (the batch-64 QKV product: 6.9 us against 4.5 + 3.8 us for the product and
-// the norm launch; its gate/up product at 16 MB measured 9.8 against 9.5 us).
-// Otherwise a quantise launch (with the norm when `gain` is set) writes the
-// codes to X / sx first.
+// norm are normed and quantised in the prologue up to 16 MB of re-read at
+// 32-column tiles, on 64-column tiles above 8 MB (the batch-64 QKV product: 6.9
+// us against 4.5 + 3.8 us for the product and the norm launch; its gate/up
+// product on 64-column tiles: 0.90 -> 0.88 ms per step, where 32-column tiles
+// measured a loss). Otherwise a quantise launch (with the norm when `gain` is
+// set) writes the codes to X / sx first.
 template <int EPI, int FORM, bool DUMP, int AIN>
 static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
     if constexpr (EPI == kGemmRope) {
@@ -742,7 +743,7 @@ static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
     const bool fused =
         AIN != kRowsCodes && p.gain == nullptr && pick < 0 && p.K <= 512 && reread <= ((size_t)8 << 20);
     const bool fused_norm =
-        AIN != kRowsCodes && p.gain != nullptr && pick < 0 && p.K == 512 && reread <= ((size_t)8 << 20);
+        AIN != kRowsCodes && p.gain != nullptr && pick < 0 && p.K == 512 && reread <= ((size_t)16 << 20);
     if (AIN != kRowsCodes && !fused && !fused_norm) {
         const hipError_t e = launch_norm_quantise(p.Xf, p.gain, p.M, p.K, p.eps, const_cast<int8_t*>(p.X),
                                                   const_cast<float*>(p.sx), nullptr, stream);
@@ -752,8 +753,10 @@ static hipError_t launch_product(const GemmParams& p, hipStream_t stream) {
         launch_chain_shape<EPI, FORM, DUMP>(p, pick, stream);
     else if (fused)
         launch_by_rows<EPI, FORM, DUMP, kRowsQuant>(p, stream);
-    else if (fused_norm)
+    else if (fused_norm && reread <= ((size_t)8 << 20))
         launch_split<16, 16, 32, EPI, FORM, DUMP, kRowsNormQuant>(p, stream);
+    else if (fused_norm)  // 64-column tiles: half the re-read of 32-column tiles
+        launch_split<16, 16, 64, EPI, FORM, DUMP, kRowsNormQuant>(p, stream);
     else
         launch_by_rows<EPI, FORM, DUMP, kRowsCodes>(p, stream);
     return hipGetLastError();
