@@ -138,7 +138,10 @@ def test_feed_prefill_bit_exact_and_equals_pushes(tiny, tiny_config):
     assert np.array_equal(ck.view(np.uint16), os_.keys[:, :, :100])
 
 
-@pytest.mark.parametrize("count", [1, 3, 4, 65])
+# 40 tokens: the normed products quantise their rows in their own prologue,
+# gate/up on 64-column tiles, with a partial last row tile; 65: the gate/up
+# input through the separate norm launch
+@pytest.mark.parametrize("count", [1, 3, 4, 40, 65])
 def test_feed_small_and_ragged_counts(tiny, count):
     gm, om = tiny
     tokens = (np.arange(count) * 37 + 11) % 1000
