@@ -110,10 +110,14 @@ int rn_matrix_multiply_batch(const rn_matrix* m, const float* x, int count, floa
  * The input rows' int8 codes and scales go to a fixed scratch array that the
  * library holds on each GPU until the process ends (4 MiB of codes + 4096
  * scales): count <= 4096 and count * columns rounded up to 256 <= 4 MiB, or
- * RN_ERR_ARGUMENT. Every call on one GPU shares that GPU's array, so calls
- * whose work overlaps on one GPU (several streams, several threads) race;
- * serialise them. Codebook matrices need no scratch and run as
- * rn_matrix_multiply_batch. Device pointers, as rn_matrix_multiply_batch. */
+ * RN_ERR_ARGUMENT. Every call on one GPU shares that GPU's array, which keeps
+ * the last call's contents. Calls outside stream capture are ordered on the
+ * device: each call's stream waits for the previous call's kernels (an event
+ * per GPU, recorded under a lock), so calls from several threads or streams
+ * run one after another. Under stream capture no such wait is recorded: the
+ * graphs captured from this call must not run concurrently with each other or
+ * with other calls on the same GPU. Codebook matrices need no scratch and run
+ * as rn_matrix_multiply_batch. Device pointers, as rn_matrix_multiply_batch. */
 int rn_matrix_multiply_batch_noalloc(const rn_matrix* m, const float* x, int count, float* y, int32_t* acc,
                                      void* stream);
 
@@ -269,6 +273,29 @@ int rn_n3_session_feed(rn_n3_session* session, const uint32_t* tokens, int count
  * argmax over output_vocab; ids[i] = token } (host ids). The argmax stays on
  * the device and feeds the next push. */
 int rn_n3_session_decode_greedy(rn_n3_session* session, uint32_t first, int steps, uint32_t* ids);
+/* #[derive(Clone)] on Session (session.rs:17): a new session holding a copy of
+ * the whole state, which then continues independently. Generator::new keeps a
+ * base session with the system prompt and clones it per turn and on reset
+ * (generator.rs:41-46). */
+int rn_n3_session_clone(const rn_n3_session* session, rn_n3_session** out);
+/* The token loop of Generator::run_turn (generator.rs:99-130) while no grammar
+ * is active: while n < max_tokens && len + 1 < window { next = argmax(logits)
+ * (generator.rs:157-165); ids[n++] = next; push(next); a token of stops
+ * (im_end, eos) ends the loop after its push }. run_turn counts the think_start
+ * token it fed in `generated`, so its max_new_tokens is max_tokens + 1 here.
+ * window <= 0 takes the archive's max_seq_len. *count = n; *finished = 1 when a
+ * stop token ended the loop. The argmax feeds the push on the device; the host
+ * reads each token (for the stop test) while the push of it runs. Needs a
+ * pushed token; RN_ERR_ARGUMENT when the loop could pass the capacity. */
+int rn_n3_session_run_turn(rn_n3_session* session, int max_tokens, int window, const uint32_t* stops, int stop_count,
+                           uint32_t* ids, int* count, int* finished);
+/* generator.rs:104-116 while a tool-call grammar is active: the session's
+ * logits, argmax_allowed over `allowed` (output_vocab host bytes, non-zero =
+ * allowed; the grammar's TokenBytes::allowed), the argmax where nothing is
+ * allowed, and allowed_statistics of the choice (rn_choice below, host). The
+ * caller pushes out->token with rn_n3_session_push. */
+typedef struct rn_choice rn_choice;
+int rn_n3_session_choose_allowed(rn_n3_session* session, const uint8_t* allowed, rn_choice* out);
 int rn_n3_session_length(const rn_n3_session* session, int* length);
 /* Session::logits (session.rs:151-165): output_vocab floats (host). */
 int rn_n3_session_logits(rn_n3_session* session, float* logits);
@@ -281,7 +308,8 @@ int rn_n3_session_cells(rn_n3_session* session, float* cells);
 int rn_n3_session_head_output(rn_n3_session* session, int code, float* out, int capacity, int* count);
 int rn_n3_session_pooled_readout(rn_n3_session* session, int code, float* out, int capacity, int* count);
 /* The int8 cache of a layer (attention.rs:36-44): keys / values [length][kv][64],
- * scales [kv][length] (host). */
+ * scales [kv][length] (host). RN_ERR_ARGUMENT for a layer outside the active
+ * ladder selection (whose cache the reference never fills). */
 int rn_n3_session_cache(rn_n3_session* session, int layer, int8_t* keys, float* key_scales, int8_t* values,
                         float* value_scales);
 int rn_n3_session_stream(const rn_n3_session* session, void** stream);
@@ -409,12 +437,12 @@ int rn_session_decode_greedy(rn_session* session, uint32_t first, int steps, uin
  * choice: probability = fast_exp(l[t] - peak_allowed) / total_allowed and
  * mass = total_allowed * fast_exp(peak_allowed - peak_all) / total_all, the
  * totals summed sequentially in index order as the reference does. */
-typedef struct {
+struct rn_choice {
     uint32_t token;      /* the choice (or the token asked for) */
     int32_t constrained; /* 1: argmax_allowed found a token; 0: nothing allowed, argmax */
     float probability;
     float mass;
-} rn_choice;
+};
 /* logits [n] f32, allowed [n] bytes (non-zero = allowed) and out are device
  * pointers; token < 0 chooses, token >= 0 gives the statistics of that token. */
 int rn_choose_allowed(const float* logits, const uint8_t* allowed, int n, int token, rn_choice* out, void* stream);

@@ -724,6 +724,8 @@ lib.ro_n3_active.argtypes = [_p, _p]
 lib.ro_n3_session_new.restype = C.c_int
 lib.ro_n3_session_new.argtypes = [_p, C.c_int, C.POINTER(_p)]
 lib.ro_n3_session_free.argtypes = [_p]
+lib.ro_n3_session_clone.restype = C.c_int
+lib.ro_n3_session_clone.argtypes = [_p, C.POINTER(_p)]
 lib.ro_n3_push.argtypes = [_p, C.c_uint32]
 lib.ro_n3_logits.argtypes = [_p, _p]
 lib.ro_n3_pooled_readout.restype = C.c_int
@@ -801,6 +803,39 @@ class OracleNeedle3Session:
             token = argmax(self.logits())
             ids[i] = token
         return ids
+
+    def clone(self) -> "OracleNeedle3Session":
+        """#[derive(Clone)] on Session (session.rs:17)."""
+        h = _p()
+        if lib.ro_n3_session_clone(self.handle, C.byref(h)) != 0:
+            raise MemoryError("clone failed")
+        t = OracleNeedle3Session.__new__(OracleNeedle3Session)
+        t.model, t.handle, t.capacity = self.model, h.value, self.capacity
+        return t
+
+    def run_turn(self, max_tokens: int, window: int, stops) -> tuple:
+        """The loop of Generator::run_turn without a grammar (generator.rs:99-130):
+        while n < max_tokens and len + 1 < window: next = argmax(logits);
+        push(next); stop after pushing a token of `stops`. Returns (ids, finished)."""
+        ids, finished = [], False
+        stops = set(int(t) for t in stops)
+        while len(ids) < max_tokens and len(self) + 1 < window:
+            token = argmax(self.logits())
+            ids.append(token)
+            self.push(token)
+            if token in stops:
+                finished = True
+                break
+        return np.array(ids, np.uint32), finished
+
+    def choose_allowed(self, allowed) -> tuple:
+        """generator.rs:104-116 on this session's logits: (token, constrained,
+        probability, mass), as rn_n3_session_choose_allowed returns them."""
+        logits = self.logits()
+        best = argmax_allowed(logits, allowed)
+        token = best if best >= 0 else argmax(logits)
+        probability, mass = allowed_statistics(logits, allowed, token)
+        return token, int(best >= 0), probability, mass
 
     def __len__(self) -> int:
         return C.cast(self.handle, C.POINTER(N3Session)).contents.length

@@ -709,6 +709,48 @@ void ro_n3_session_free(ro_n3_session* s) {
     free(s);
 }
 
+/* #[derive(Clone)] on Session (session.rs:17): every field copied, so the two
+ * sessions continue independently (Generator::new/reset, generator.rs:41-46) */
+int ro_n3_session_clone(const ro_n3_session* s, ro_n3_session** out) {
+    const ro_n3_model* m = s->m;
+    const ro_n3_config* c = &m->config;
+    ro_n3_session* t = NULL;
+    if (ro_n3_session_new(m, s->capacity, &t) != 0) return -1;
+    const size_t cap = (size_t)s->capacity;
+    const int qk = c->qk_head_dim, vd = c->v_head_dim, kv = c->num_kv_heads;
+    const int qkv = c->num_heads * qk + kv * qk + kv * vd;
+    t->length = s->length;
+    memcpy(t->tokens, s->tokens, cap * sizeof(uint32_t));
+    for (int l = 0; l < c->num_layers; ++l) {
+        const ro_n3_cache* a = &s->caches[l];
+        ro_n3_cache* b = &t->caches[l];
+        memcpy(b->keys, a->keys, cap * kv * qk);
+        memcpy(b->values, a->values, cap * kv * vd);
+        memcpy(b->key_scales, a->key_scales, cap * kv * sizeof(float));
+        memcpy(b->value_scales, a->value_scales, cap * kv * sizeof(float));
+        memcpy(b->history, a->history, (size_t)(c->conv_taps > 0 ? c->conv_taps : 1) * qkv * sizeof(float));
+        b->history_count = a->history_count;
+        b->length = a->length;
+    }
+    const int keep = (c->engram_conv_taps - 1) * c->engram_dilation + 1;
+    for (int e = 0; e < c->engram_site_count; ++e) {
+        memcpy(t->engram_history[e], s->engram_history[e],
+               (size_t)(keep > 0 ? keep : 1) * m->engrams[e].value.rows * sizeof(float));
+        t->engram_count[e] = s->engram_count[e];
+    }
+    memcpy(t->hidden, s->hidden, (size_t)c->d_model * sizeof(float));
+    memcpy(t->cells, s->cells, (size_t)(m->active_count + 1) * c->d_model * sizeof(float));
+    for (int i = 0; i < m->head_count; ++i) {
+        const ro_n3_head* h = &m->heads[i];
+        const size_t slots = (size_t)h->layers * h->probes_per_layer;
+        memcpy(t->peak[i], s->peak[i], slots * sizeof(float));
+        memcpy(t->total[i], s->total[i], slots * sizeof(float));
+        memcpy(t->weighted[i], s->weighted[i], slots * h->width * sizeof(float));
+    }
+    *out = t;
+    return 0;
+}
+
 /* engram.rs:66-112: contribute for one site */
 static void engram_contribute(ro_n3_session* s, int site, const int* indices, int position, float* key, float* value) {
     const ro_n3_model* m = s->m;

@@ -229,6 +229,9 @@ SIGNATURES = {
     "rn_n3_session_push": (_i, [_p, _u32]),
     "rn_n3_session_feed": (_i, [_p, _p, _i]),
     "rn_n3_session_decode_greedy": (_i, [_p, _u32, _i, _p]),
+    "rn_n3_session_clone": (_i, [_p, C.POINTER(_p)]),
+    "rn_n3_session_run_turn": (_i, [_p, _i, _i, _p, _i, _p, C.POINTER(_i), C.POINTER(_i)]),
+    "rn_n3_session_choose_allowed": (_i, [_p, _p, C.POINTER(Choice)]),
     "rn_n3_session_length": (_i, [_p, C.POINTER(_i)]),
     "rn_n3_session_logits": (_i, [_p, _p]),
     "rn_n3_session_hidden": (_i, [_p, _p]),

@@ -157,22 +157,34 @@ constexpr int kNoAllocTokens = 4096;
 static __device__ __align__(256) unsigned char scratch[kNoAllocCodeBytes + sizeof(float) * kNoAllocTokens];
 
 namespace {
+// Per device: the scratch's device address and an event marking the end of
+// the last call's kernels there. Calls on one device take g_scratch_mu for
+// their whole enqueue, and each call's stream first waits for the previous
+// call's event, so calls from several threads and streams run one after
+// another on the device instead of racing on the scratch.
+struct NoAllocDevice {
+    void* ptr = nullptr;
+    hipEvent_t last = nullptr;
+};
 std::mutex g_scratch_mu;
-std::vector<void*> g_scratch_ptr;  // per device ordinal
+std::vector<NoAllocDevice> g_scratch;  // per device ordinal
 
-int scratch_address(void** out) {
+// Set-up on a device's first call (caller holds g_scratch_mu): the symbol's
+// address and the ordering event (an event is no device-memory allocation).
+int scratch_device(NoAllocDevice** out) {
     int device = -1;
     RN_HIP(hipGetDevice(&device));
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if ((size_t)device >= g_scratch_ptr.size()) g_scratch_ptr.resize(device + 1, nullptr);
-    if (!g_scratch_ptr[device]) {
+    if ((size_t)device >= g_scratch.size()) g_scratch.resize(device + 1);
+    NoAllocDevice& d = g_scratch[device];
+    if (!d.ptr) {
         void* ptr = nullptr;
         const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !ptr)
             return fail(RN_ERR_DEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
-        g_scratch_ptr[device] = ptr;
+        RN_HIP(hipEventCreateWithFlags(&d.last, hipEventDisableTiming));
+        d.ptr = ptr;
     }
-    *out = g_scratch_ptr[device];
+    *out = &d;
     return RN_OK;
 }
 }  // namespace
@@ -538,12 +550,20 @@ int rn_matrix_multiply_batch_noalloc(const rn_matrix* m, const float* x, int cou
     RN_REQUIRE(count <= kNoAllocTokens && codes <= kNoAllocCodeBytes,
                "count %d x columns %d exceeds the fixed scratch (at most %d rows and %zu code bytes)", count,
                m->columns, kNoAllocTokens, kNoAllocCodeBytes);
-    void* base = nullptr;
-    int rc = scratch_address(&base);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    NoAllocDevice* dev = nullptr;
+    int rc = scratch_device(&dev);
     if (rc) return rc;
-    int8_t* xq = (int8_t*)base;
-    float* sx = (float*)((char*)base + kNoAllocCodeBytes);
+    // Under stream capture the caller's graph orders its own replays; an event
+    // recorded outside the capture cannot be waited on inside it.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    RN_HIP(hipStreamIsCapturing(s, &capture));
+    const bool ordered = capture == hipStreamCaptureStatusNone;
+    if (ordered) RN_HIP(hipStreamWaitEvent(s, dev->last, 0));
+    int8_t* xq = (int8_t*)dev->ptr;
+    float* sx = (float*)((char*)dev->ptr + kNoAllocCodeBytes);
     RN_HIP(batch_product_i8(m, x, count, y, acc, xq, sx, s));
+    if (ordered) RN_HIP(hipEventRecord(dev->last, s));
     return RN_OK;
 }
 

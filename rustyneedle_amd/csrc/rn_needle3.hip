@@ -2416,13 +2416,15 @@ namespace {
 // A bump allocator over a few large device allocations, so that the many small
 // tensors of a model or a session share pages and address-translation entries
 // instead of taking one allocation each. Pieces are 256-byte aligned.
-int arena_take(std::vector<void*>& owned, N3Arena& a, size_t bytes, size_t chunk, void** out) {
+int arena_take(std::vector<void*>& owned, N3Arena& a, size_t bytes, size_t chunk, void** out,
+               std::vector<size_t>* sizes = nullptr) {
     bytes = (std::max<size_t>(bytes, 256) + 255) & ~(size_t)255;
     if (bytes > a.left) {
         const size_t size = std::max(chunk, bytes);
         void* p = nullptr;
         N3_HIP(hipMalloc(&p, size));
         owned.push_back(p);
+        if (sizes) sizes->push_back(size);
         a.cur = static_cast<char*>(p);
         a.left = size;
     }
@@ -2853,7 +2855,8 @@ struct rn_n3_session {
     rn_lanes* lanes = nullptr;
     std::vector<N3CacheDev> caches;
     std::vector<float*> rings, ekey, evalue, site_rot, site_raw;  // per engram site
-    std::vector<void*> allocations;
+    std::vector<void*> allocations;  // every device buffer of the session lives in these chunks
+    std::vector<size_t> allocation_bytes;
     N3Arena arena;
     float *stream_a = nullptr, *stream_b = nullptr, *input = nullptr, *post = nullptr, *residual = nullptr;
     float *x = nullptr, *rotated = nullptr, *prod = nullptr, *attended = nullptr;
@@ -2864,6 +2867,10 @@ struct rn_n3_session {
     uint32_t* tokens_dev = nullptr;  // the tokens pushed so far [capacity]
     uint32_t* next_dev = nullptr;    // the greedy argmax of the last logits
     uint32_t* ids_dev = nullptr;     // greedy ids [capacity]
+    uint8_t* allowed_dev = nullptr;  // the grammar's mask [output_vocab] (rn_n3_session_choose_allowed)
+    Choice* choice_dev = nullptr;
+    uint32_t* turn_host = nullptr;   // pinned: the last two greedy tokens of a turn (rn_n3_session_run_turn)
+    hipEvent_t turn_done[2] = {nullptr, nullptr};
     float *attn_out = nullptr, *gathered = nullptr, *eraw = nullptr, *qscales = nullptr;
     int8_t* qcodes = nullptr;
     float *cells = nullptr, *hidden = nullptr, *logits = nullptr, *cos = nullptr, *sin = nullptr;
@@ -2884,7 +2891,7 @@ namespace {
 
 int alloc(rn_n3_session* s, size_t bytes, void** out) {
     void* p = nullptr;
-    N3_CALL(arena_take(s->allocations, s->arena, bytes, kN3SessionChunk, &p));
+    N3_CALL(arena_take(s->allocations, s->arena, bytes, kN3SessionChunk, &p, &s->allocation_bytes));
     N3_HIP(hipMemsetAsync(p, 0, std::max<size_t>(bytes, 256), s->stream));
     *out = p;
     return RN_OK;
@@ -2953,6 +2960,9 @@ int rn_n3_session_free(rn_n3_session* s) {
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     if (s->lanes) rn_lanes_free(s->lanes);
     for (void* p : s->allocations) (void)hipFree(p);
+    for (hipEvent_t e : s->turn_done)
+        if (e) (void)hipEventDestroy(e);
+    if (s->turn_host) (void)hipHostFree(s->turn_host);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
     return RN_OK;
@@ -3016,6 +3026,8 @@ int rn_n3_session_create(const rn_n3_model* m, int capacity, rn_n3_session** out
         N3_CALL(alloc_n(s, (size_t)capacity, &s->tokens_dev));
         N3_CALL(alloc_n(s, 64, &s->next_dev));
         N3_CALL(alloc_n(s, (size_t)capacity, &s->ids_dev));
+        N3_CALL(alloc_n(s, (size_t)m->output_vocab, &s->allowed_dev));
+        N3_CALL(alloc_n(s, 1, &s->choice_dev));
         N3_CALL(alloc_n(s, 64, &s->code_scales));
         // the output projection, x and the routed input one after another: the
         // layer boundary stages them as one range
@@ -3766,18 +3778,129 @@ int rn_n3_session_decode_greedy(rn_n3_session* s, uint32_t first, int steps, uin
     return RN_OK;
 }
 
+// #[derive(Clone)] on Session (session.rs:17), the Generator's prefix cache
+// (generator.rs:41-46: the base session with the system prompt is cloned per
+// turn and on reset). A new session of the same capacity takes its chunks in
+// the same order, so every buffer sits at the same offset of the same chunk;
+// copying the chunks copies the whole state (caches, conv and engram rings,
+// lanes stream, token history, cells, probe-head accumulators, hidden state
+// and logits' input). No session buffer holds a device pointer.
+int rn_n3_session_clone(const rn_n3_session* s, rn_n3_session** out) {
+    N3_REQUIRE(s && out, "null argument");
+    *out = nullptr;
+    rn_n3_session* t = nullptr;
+    N3_CALL(rn_n3_session_create(s->m, s->capacity, &t));
+    auto fail_with = [&](int rc) {
+        rn_n3_session_free(t);
+        return rc;
+    };
+    t->fused = s->fused;
+    if (s->run.ready) {
+        const int rc = run_buffers(t);
+        if (rc) return fail_with(rc);
+    }
+    if (t->allocation_bytes != s->allocation_bytes)
+        return fail_with(n3_fail(RN_ERR_STATE, "the clone's buffers do not line up with the session's"));
+    hipError_t e = hipStreamSynchronize(s->stream);
+    for (size_t i = 0; i < s->allocations.size() && e == hipSuccess; ++i)
+        e = hipMemcpyAsync(t->allocations[i], s->allocations[i], s->allocation_bytes[i], hipMemcpyDeviceToDevice,
+                           t->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(t->stream);
+    if (e != hipSuccess) return fail_with(n3_fail(RN_ERR_DEVICE, "clone: %s", hipGetErrorString(e)));
+    t->length = s->length;
+    t->lrot_ready = s->lrot_ready;
+    *out = t;
+    return RN_OK;
+}
+
+// The loop of Generator::run_turn (generator.rs:99-130) with no grammar active:
+//   while n < max_tokens && len + 1 < window { next = argmax(logits);
+//     ids[n++] = next; push(next); if next is a stop token { finished; break } }
+// The logits, argmax and push stay on the device (the push reads the argmax
+// there). The host learns each token while the push of it runs: the next
+// token's logits and argmax are queued before the host waits for the
+// previous token, so the device never waits for the stop test. A stop token
+// is pushed, nothing after it. *count gets n, *finished 1 after a stop token.
+int rn_n3_session_run_turn(rn_n3_session* s, int max_tokens, int window, const uint32_t* stops, int stop_count,
+                           uint32_t* ids, int* count, int* finished) {
+    N3_REQUIRE(s && count && finished && (ids || max_tokens == 0) && (stops || stop_count == 0), "null argument");
+    N3_REQUIRE(max_tokens >= 0 && stop_count >= 0, "max_tokens and stop_count must be non-negative");
+    *count = 0;
+    *finished = 0;
+    N3_REQUIRE(s->length > 0, "no token has been pushed (the turn's logits need one)");
+    if (window <= 0) window = (int)s->m->g.max_seq_len;  // ModelConfig::max_seq_len, as run_turn takes it
+    const int room = std::max(0, std::min(max_tokens, window - 1 - s->length));
+    N3_REQUIRE(s->length + room <= s->capacity, "a turn of up to %d tokens overflows the capacity %d", room,
+               s->capacity);
+    if (room == 0) return RN_OK;
+    if (!s->turn_host) {
+        N3_HIP(hipHostMalloc((void**)&s->turn_host, 2 * sizeof(uint32_t), hipHostMallocDefault));
+        for (hipEvent_t& e : s->turn_done) N3_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    hipStream_t st = s->stream;
+    // the logits of the state after n pushes, the argmax into next_dev and
+    // ids_dev[n], its copy to the host slot n % 2
+    auto choose = [&](int n) -> int {
+        N3_CALL(enqueue_logits(s));
+        N3_HIP(launch_argmax_rows(s->logits, 1, s->m->output_vocab, s->next_dev, s->ids_dev, room, n, st));
+        N3_HIP(hipMemcpyAsync(s->turn_host + (n & 1), s->next_dev, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+        N3_HIP(hipEventRecord(s->turn_done[n & 1], st));
+        return RN_OK;
+    };
+    N3_CALL(choose(0));
+    int n = 0;
+    while (n < room) {
+        N3_CALL(enqueue_push(s, 0, s->next_dev));
+        ++n;
+        if (n < room) N3_CALL(choose(n));
+        N3_HIP(hipEventSynchronize(s->turn_done[(n - 1) & 1]));
+        const uint32_t token = s->turn_host[(n - 1) & 1];
+        if (std::find(stops, stops + stop_count, token) != stops + stop_count) {
+            *finished = 1;
+            break;
+        }
+    }
+    N3_HIP(hipMemcpyAsync(ids, s->ids_dev, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+    N3_HIP(hipStreamSynchronize(st));
+    *count = n;
+    return RN_OK;
+}
+
+// generator.rs:104-116 while a tool-call grammar is active: the session's
+// logits (Session::logits), argmax_allowed over the host's mask with the
+// argmax fallback, and allowed_statistics of the choice, on the device.
+int rn_n3_session_choose_allowed(rn_n3_session* s, const uint8_t* allowed, rn_choice* out) {
+    N3_REQUIRE(s && allowed && out, "null argument");
+    N3_REQUIRE(s->length > 0, "no token has been pushed");
+    static_assert(sizeof(rn_choice) == sizeof(Choice), "rn_choice mirrors rn::Choice");
+    const int n = s->m->output_vocab;
+    N3_CALL(enqueue_logits(s));
+    N3_HIP(hipMemcpyAsync(s->allowed_dev, allowed, (size_t)n, hipMemcpyHostToDevice, s->stream));
+    N3_HIP(launch_constrained_choice(s->logits, s->allowed_dev, n, -1, s->choice_dev, s->stream));
+    N3_HIP(hipMemcpyAsync(out, s->choice_dev, sizeof(Choice), hipMemcpyDeviceToHost, s->stream));
+    N3_HIP(hipStreamSynchronize(s->stream));
+    return RN_OK;
+}
+
 // Session::feed (session.rs:58-74): at least BATCH_THRESHOLD (4) tokens run
-// as batched prefills of up to kN3FeedChunk tokens (a shorter last chunk of
-// fewer than 4 is pushed), fewer are pushed. The batched prefill runs each
+// as batched prefills (a shorter last chunk of fewer than 4 is pushed), fewer
+// are pushed. With integer-path engram matrices the batched prefill runs each
 // token's arithmetic as a push does, so the chunk size changes nothing but
-// speed (RN_N3_FEED_CHUNK, 4..256, sets it).
+// speed, and runs take up to kN3FeedChunk tokens (RN_N3_FEED_CHUNK, 4..256,
+// sets it). A 1- or 3-bit engram key or value matrix takes the float path,
+// whose batch tile (multiply_batch, matrix.rs:330-389) rounds differently from
+// its vector path: then the chunks are the reference's PREFILL_CHUNK of 128
+// (session.rs:11), so that the same tokens run batched and pushed as there.
 int rn_n3_session_feed(rn_n3_session* s, const uint32_t* tokens, int count) {
-    constexpr int kBatchThreshold = 4;
+    constexpr int kBatchThreshold = 4, kPrefillChunk = 128;
     N3_REQUIRE(s && (tokens || count == 0), "null argument");
     N3_REQUIRE(count >= 0 && s->length + count <= s->capacity, "feed of %d tokens overflows the capacity", count);
     for (int i = 0; i < count; ++i) N3_REQUIRE(tokens[i] < s->m->g.vocab, "token %u outside the vocabulary", tokens[i]);
-    int chunk = kN3FeedChunk;
-    if (const char* e = getenv("RN_N3_FEED_CHUNK")) chunk = std::min(kN3FeedChunk, std::max(kBatchThreshold, atoi(e)));
+    bool float_engram = false;
+    for (const N3Engram& e : s->m->engrams) float_engram |= !integer_path(e.key) || !integer_path(e.value);
+    int chunk = float_engram ? kPrefillChunk : kN3FeedChunk;
+    if (const char* e = getenv("RN_N3_FEED_CHUNK"))
+        if (!float_engram) chunk = std::min(kN3FeedChunk, std::max(kBatchThreshold, atoi(e)));
     if (count < kBatchThreshold || !run_applies(s)) {
         for (int i = 0; i < count; ++i) N3_CALL(rn_n3_session_push(s, tokens[i]));
         return RN_OK;
@@ -3888,6 +4011,10 @@ int rn_n3_session_cache(rn_n3_session* s, int layer, int8_t* keys, float* key_sc
                         float* value_scales) {
     N3_REQUIRE(s && keys && key_scales && values && value_scales, "null argument");
     N3_REQUIRE(layer >= 0 && layer < (int)s->m->g.num_layers, "layer %d out of range", layer);
+    // the cache of a layer outside the ladder's selection stays empty in the
+    // reference (session.rs:99-101 never visits it): refuse it here
+    N3_REQUIRE(std::find(s->m->active.begin(), s->m->active.end(), layer) != s->m->active.end(),
+               "layer %d is not an active layer at this depth", layer);
     const int KV = (int)s->m->g.num_kv_heads, n = s->length, cap = s->capacity;
     const N3CacheDev& c = s->caches[(size_t)layer];
     std::vector<int8_t> k((size_t)KV * cap * 64), v(k.size());

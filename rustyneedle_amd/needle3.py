@@ -143,7 +143,7 @@ def synthetic_archive(geometry: dict, seed: int = 20261202) -> bytes:
 
 
 # ---- the device model and session ------------------------------------------------
-from . import Archive, _ptr, check, lib  # noqa: E402
+from . import Archive, Choice, _ptr, check, lib  # noqa: E402
 
 _p = __import__("ctypes").c_void_p
 _C = __import__("ctypes")
@@ -205,6 +205,32 @@ class Session:
         ids = np.empty(steps, np.uint32)
         check(lib.rn_n3_session_decode_greedy(self.handle, int(first), steps, _ptr(ids)))
         return ids
+
+    def clone(self) -> "Session":
+        """#[derive(Clone)] on Session (session.rs:17): an independent copy."""
+        h = _p()
+        check(lib.rn_n3_session_clone(self.handle, _C.byref(h)))
+        t = Session.__new__(Session)
+        t.model, t.handle, t.capacity = self.model, h.value, self.capacity
+        return t
+
+    def run_turn(self, max_tokens: int, stops=(), window: int = 0):
+        """Generator::run_turn's loop with no grammar (generator.rs:99-130):
+        (ids, finished); window 0 takes the archive's max_seq_len."""
+        ids = np.empty(max(1, max_tokens), np.uint32)
+        st = np.ascontiguousarray(list(stops) or [0], np.uint32)
+        n, fin = _C.c_int(), _C.c_int()
+        check(lib.rn_n3_session_run_turn(self.handle, int(max_tokens), int(window), _ptr(st), len(stops), _ptr(ids),
+                                         _C.byref(n), _C.byref(fin)))
+        return ids[:n.value].copy(), bool(fin.value)
+
+    def choose_allowed(self, allowed: np.ndarray):
+        """generator.rs:104-116: (token, constrained, probability, mass) over this session's logits."""
+        mask = np.ascontiguousarray(allowed, dtype=np.uint8)
+        assert mask.shape == (self.model.output_vocab,)
+        c = Choice()
+        check(lib.rn_n3_session_choose_allowed(self.handle, _ptr(mask), _C.byref(c)))
+        return int(c.token), bool(c.constrained), np.float32(c.probability), np.float32(c.mass)
 
     def __len__(self) -> int:
         n = _C.c_int()

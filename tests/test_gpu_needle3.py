@@ -71,6 +71,10 @@ def test_push_bit_exact(archive, depth, path):
         g, o = gs.cache(layer), os_.cache(layer)
         for a, b in zip(g, o):
             assert a.shape == b.shape and np.array_equal(a.view(np.uint8), b.view(np.uint8)), layer
+    # a layer the ladder leaves out has no cache (the reference never fills it)
+    for layer in set(range(GEOMETRY["num_layers"])) - set(gm.active):
+        with pytest.raises(rn.RnError):
+            gs.cache(layer)
 
 
 def test_feed_equals_push(archive, path):
@@ -144,3 +148,91 @@ def test_batched_feed_bit_exact(archive, depth, chunk, monkeypatch):
     ids = gs.decode_greedy(5, 6)
     assert ids.tolist() == os_.greedy(5, 6).tolist()
     _compare_all(gs, os_, gm, f"depth {depth} chunk {chunk} after greedy")
+
+
+def test_clone_diverges_independently(archive, path):
+    """#[derive(Clone)] on Session (session.rs:17), the Generator's prefix
+    cache (generator.rs:41-46): after a batched feed the session is cloned;
+    base and clone then take different tokens, and each matches an oracle
+    session that took the same ones (state, heads, caches); a clone of the
+    clone then feeds again while the clone stays as it was."""
+    gm, om = needle3.Model(archive), oracle.OracleNeedle3(archive)
+    gs, os_ = gm.session(96), om.session(96)
+    prompt = _tokens(20, seed=23)
+    gs.feed(prompt)
+    os_.feed(prompt)
+    gc, oc = gs.clone(), os_.clone()
+    _compare_all(gc, oc, gm, "fresh clone")
+    for t in _tokens(6, seed=29):
+        gs.push(int(t))
+        os_.push(int(t))
+    for t in _tokens(9, seed=31):
+        gc.push(int(t))
+        oc.push(int(t))
+    _compare_all(gs, os_, gm, "base after its tokens")
+    _compare_all(gc, oc, gm, "clone after its tokens")
+    gc2, oc2 = gc.clone(), oc.clone()
+    more = _tokens(12, seed=37)
+    gc2.feed(more)
+    oc2.feed(more)
+    _compare_all(gc2, oc2, gm, "clone of the clone after a feed")
+    _compare_all(gc, oc, gm, "clone left as it was")
+    assert gc2.decode_greedy(3, 5).tolist() == oc2.greedy(3, 5).tolist()
+
+
+def test_run_turn_stops_like_the_generator(archive, path):
+    """Generator::run_turn's loop (generator.rs:99-130): a turn without a stop
+    token runs max_tokens; with a stop token planted from that turn's ids a
+    turn from the same prefix (a clone) ends after pushing its first
+    occurrence; a short window ends the loop at len + 1 == window. Ids,
+    length, finished and the whole state (head_output(2) included, which the
+    reference reads after the loop) against the oracle."""
+    gm, om = needle3.Model(archive), oracle.OracleNeedle3(archive)
+    gs, os_ = gm.session(96), om.session(96)
+    prompt = _tokens(10, seed=41)
+    gs.feed(prompt)
+    os_.feed(prompt)
+    base_g, base_o = gs.clone(), os_.clone()
+    want, fin = os_.run_turn(20, 4096, [])
+    got, gfin = gs.run_turn(20, window=4096)
+    assert got.tolist() == want.tolist() and not fin and not gfin and len(want) == 20
+    _compare_all(gs, os_, gm, "turn of 20")
+    for k in (0, 7):
+        stop = int(want[k])
+        g2, o2 = base_g.clone(), base_o.clone()
+        want2, fin2 = o2.run_turn(20, 4096, [GEOMETRY["vocab"] - 1, stop])
+        got2, gfin2 = g2.run_turn(20, stops=[GEOMETRY["vocab"] - 1, stop], window=4096)
+        assert fin2 and gfin2 and got2.tolist() == want2.tolist(), (k, got2, want2)
+        stops_at = [i for i, t in enumerate(want.tolist()) if t in (stop, GEOMETRY["vocab"] - 1)]
+        assert len(got2) == stops_at[0] + 1
+        _compare_all(g2, o2, gm, f"stopped turn {k}")
+        assert np.array_equal(_bits(g2.head_output(2)), _bits(o2.head_output(2)))
+    g3, o3 = base_g.clone(), base_o.clone()
+    want3, fin3 = o3.run_turn(50, len(o3) + 6, [])
+    got3, gfin3 = g3.run_turn(50, window=len(g3) + 6)
+    assert len(want3) == 5 and got3.tolist() == want3.tolist() and not gfin3
+    _compare_all(g3, o3, gm, "window")
+    with pytest.raises(rn.RnError):
+        g3.run_turn(200, window=4096)  # 200 more tokens cannot fit the capacity of 96
+
+
+def test_choose_allowed_on_the_session(archive):
+    """generator.rs:104-116 on the Needle 3 session's logits: argmax_allowed
+    with the argmax fallback and allowed_statistics, bit for bit; the chosen
+    token is pushed and the next choice compared again."""
+    gm, om = needle3.Model(archive), oracle.OracleNeedle3(archive)
+    gs, os_ = gm.session(64), om.session(64)
+    prompt = _tokens(12, seed=43)
+    gs.feed(prompt)
+    os_.feed(prompt)
+    rng = np.random.default_rng(5)
+    n = gm.output_vocab
+    for mask in ((rng.random(n) < 0.3).astype(np.uint8), np.zeros(n, np.uint8), np.ones(n, np.uint8),
+                 (rng.random(n) < 0.01).astype(np.uint8)):
+        got = gs.choose_allowed(mask)
+        want = os_.choose_allowed(mask)
+        assert got[0] == want[0] and got[1] == bool(want[1]), (got, want)
+        assert np.array_equal(_bits([got[2], got[3]]), _bits([want[2], want[3]]))
+        gs.push(got[0])
+        os_.push(want[0])
+    _compare_all(gs, os_, gm, "after constrained steps")

@@ -128,3 +128,52 @@ def test_needle3_full_size_feed_equals_pushes(monkeypatch):
         for a, b in zip(fed.cache(layer), pushed.cache(layer)):
             assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), layer
     assert fed.decode_greedy(7, 8).tolist() == pushed.decode_greedy(7, 8).tolist()
+
+
+@pytest.mark.timeout(600)
+def test_needle3_documented_geometry_against_the_oracle(monkeypatch):
+    """The Needle 3 block at its documented shape (d_model 768, 20 layers, 12
+    heads over 4 kv heads, four lanes, two engram sites at layers 1 and 10, a
+    1024-token window with layers 4, 9, 14 and 19 global) against the oracle,
+    bit for bit: a 1040-token feed (batched runs; the last 16 positions are past
+    the window of the 16 non-global layers, attention.rs:171-177), then 8 greedy
+    tokens (session.rs:76-148 per push). Compared: hidden state, cells, logits,
+    both probe heads' pooled readouts and outputs, and the int8 caches (codes and
+    scales) of layers 0, 1, 4, 10 and 19, after the feed and after the tokens."""
+    from rustyneedle_amd import needle3
+    monkeypatch.delenv("RN_N3_PATH", raising=False)
+    monkeypatch.delenv("RN_N3_FEED_CHUNK", raising=False)
+    g = needle3.NEEDLE3
+    archive = needle3.synthetic_archive(g)
+    gm, om = needle3.Model(archive), oracle.OracleNeedle3(archive)
+    tokens = rn.synth_tokens(rn.SEED, "needle3.window", g["vocab"], (1040,))
+    gs, os_ = gm.session(1056), om.session(1056)
+
+    def oracle_feed():
+        for a in range(0, tokens.size, 130):
+            print(f"needle3 documented geometry: oracle pushes {a}..{min(a + 130, tokens.size)}", flush=True)
+            os_.feed(tokens[a:a + 130])
+
+    with ThreadPoolExecutor(1) as pool:
+        done = pool.submit(oracle_feed)
+        print("needle3 documented geometry: device feed of 1040 tokens", flush=True)
+        gs.feed(tokens)
+        done.result()
+
+    def compare(label):
+        assert len(gs) == len(os_), label
+        assert np.array_equal(_bits(gs.hidden()), _bits(os_.hidden())), f"hidden {label}"
+        assert np.array_equal(_bits(gs.cells()), _bits(os_.cells())), f"cells {label}"
+        assert np.array_equal(_bits(gs.logits()), _bits(os_.logits())), f"logits {label}"
+        for code in (1, 2):
+            assert np.array_equal(_bits(gs.pooled_readout(code)), _bits(os_.pooled_readout(code))), (label, code)
+            assert np.array_equal(_bits(gs.head_output(code)), _bits(os_.head_output(code))), (label, code)
+        for layer in (0, 1, 4, 10, 19):
+            for a, b in zip(gs.cache(layer), os_.cache(layer)):
+                assert a.shape == b.shape and np.array_equal(a.view(np.uint8), b.view(np.uint8)), (label, layer)
+
+    compare("after the 1040-token feed")
+    print("needle3 documented geometry: 8 greedy tokens", flush=True)
+    ids = gs.decode_greedy(7, 8)
+    assert ids.tolist() == os_.greedy(7, 8).tolist()
+    compare("after 8 greedy tokens")
