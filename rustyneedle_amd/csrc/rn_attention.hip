@@ -580,40 +580,44 @@ hipError_t launch_rope_append(const float* qkv, float* q_out, __half* kc, __half
 //
 // A head needs only its own 192 rows of the fused q/k/v matrix (q, k and v rows
 // 64h..64h+63), so the product splits by head with no exchange between blocks.
-// The block streams about 190 KB (weights, scales, K/V rows) through one CU, so
-// the wave that computes the input codes is kept free of that stream:
-//   1. wave 0: reads x (or gathers the embedding row times sqrt(d),
-//      session.rs:85-90), its zero-centred RMSNorm (eight-lane sum of
-//      ops.rs:7-17) and int8 codes (ops.rs:103-118) into LDS, while waves 1-7
-//      request the head's weight rows and scales; after the barrier every wave
-//      requests its share of the first KC x 128 key rows and 32 x VC value rows;
-//   2. waves 1-7: v_dot4 over 16-code chunks, lane pairs joined into 32-code
-//      group sums; thread 64 + r runs row r's group epilogue
-//      fmaf(acc, sW * sx, total) in group order (panel.rs:184-188);
-//   3. rotate-half rotary of q and k at the position (ops.rs:131-141), fp16
-//      append of k and v at that position;
-//   4. scores (tree T2 of score_row), peak, fast_exp weights, then the value
-//      sums in tree T3 (32 position classes, 4 dims per thread), one multiply
-//      by 1/total.
+// The kernel is a chain of dependent steps, so it is laid out to keep global
+// loads and barriers off that chain:
+//   1. every load is requested at the start: wave 0 the input row (or the
+//      embedding row of the token times sqrt(d), session.rs:85-90) and the
+//      norm gains; waves 1-6 the head's weight rows and scales; every wave its
+//      share of the first KC x 128 key rows and 32 x VC value rows (clamped to
+//      the capacity, so that they need not wait for the position); once the
+//      position is known (one scalar load), waves 1-4 the rotary angles of
+//      their rows;
+//   2. wave 0: zero-centred RMSNorm (eight-lane sum of ops.rs:7-17) and int8
+//      codes (ops.rs:103-118) into LDS (barrier 1);
+//   3. waves 1-6, 32 rows each, two lanes a row: each lane owns half a row's
+//      codes, so its group sums never leave the lane; the panel epilogue
+//      fmaf(acc, sW * sx, total) runs in group order over the first half's
+//      groups in the even lane and continues in the odd lane (panel.rs:184-188);
+//      a wave holds rows i and i + 32 of its section in lanes l and l ^ 32, so
+//      the rotate-half rotary (ops.rs:131-141) is a lane swap; q goes to LDS,
+//      k and v to LDS and to the cache as fp16 (barrier 2);
+//   4. scores (tree T2 of score_row) into LDS with each thread's running peak,
+//      the block peak through one barrier (barrier 3), the fast_exp weights
+//      (barrier 4), then the value sums in tree T3 (32 position classes, 4 dims
+//      per thread, barrier 5) and the class combine with one multiply by
+//      1/total.
 // The float results are identical to the separate product + attend_kernel path.
 template <int K, int PRO, int KC, int VC>
 __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
     constexpr int NT = 512;
     constexpr int G = K / kGroup;            // weight scales per row
     constexpr int CPR = K / 16;              // 16-code chunks per row
-    constexpr int ROWS = 3 * kHeadDim;       // q, k and v rows of one head
-    constexpr int CHUNKS = ROWS * CPR;
-    constexpr int LW = NT - 64;                // weight-loading threads (waves 1-7)
-    constexpr int NLW = (CHUNKS + LW - 1) / LW;
+    constexpr int HC = CPR / 2;              // chunks per lane: half a row
+    constexpr int HG = G / 2;                // groups per lane
     constexpr int E = K / 64;                // prologue values per lane of wave 0
     constexpr int KROWS = NT / 4;            // key rows per pass
-    static_assert(E % 2 == 0 && G % 4 == 0 && CPR % 2 == 0, "whole float pairs, scale quads, code pairs");
-    static_assert(64 + ROWS <= NT, "one epilogue thread per row in waves 1-7");
+    static_assert(E % 2 == 0 && HG % 2 == 0 && HC == 2 * HG, "whole float pairs, scale pairs, two chunks a group");
     extern __shared__ float scores[];
     __shared__ __align__(16) int8_t xq_s[K];
     __shared__ __align__(16) float sq_s[K];
-    __shared__ __align__(16) int acc_s[ROWS * G];
-    __shared__ float qkv_s[ROWS];
+    __shared__ __align__(16) int acc_s[6 * 32 * CPR];  // chunk sums, 32 rows a product wave
     __shared__ float q_s[kHeadDim];
     __shared__ __align__(16) __half new_s[2][kHeadDim];
     __shared__ __align__(16) float part_s[kClasses][kHeadDim];
@@ -627,19 +631,21 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
     const size_t head_base = (size_t)h * p.capacity * kHeadDim;
     const __half* Kc = p.kc + head_base;
     const __half* Vc = p.vc + head_base;
+    // product layout (waves 1-6): section q / k / v, the lane pair of row
+    // slot lr, half hh of the row; slots lr and lr ^ 16 hold dims i and i + 32
+    const int section = (wave - 1) >> 1, sub = (wave - 1) & 1, lr = lane >> 1, hh = lane & 1;
+    auto dim_of = [&](int slot) { return (slot & 15) + 16 * sub + 32 * (slot >> 4); };
+    auto slot_row = [&](int slot) { return (size_t)section * K + (size_t)h * kHeadDim + dim_of(slot); };
+    const int dim = dim_of(lr);
+    const int rot = (lr & 15) + 16 * sub;     // rotary pair index of this row
+    const bool rows_wave = wave >= 1 && wave <= 6;
 
-    const int pos = p.state->pos;
-    // 1. wave 0: the input row, its norm and its int8 codes (LDS traffic inside
-    // one wave: DS operations of a wave complete in order). Waves 1-7 request
-    // the head's weight rows and scales meanwhile.
-    auto global_row = [&](int hr) -> size_t {
-        return (size_t)(hr / kHeadDim) * K + (size_t)h * kHeadDim + (hr % kHeadDim);
-    };
-    int4 w[NLW];
-    float4 sv[G / 4];
+    // 1. requests: the prologue input first (wave 0), the weights and scales
+    // (waves 1-6), then everything that needs the position
+    float v[E], gv[E];
+    int4 w[HC];
+    float sv[HG];
     if (wave == 0) {
-        float v[E];
-        float gv[E];
         if constexpr (PRO == kEmbedNorm) {
             uint32_t token = p.state->token;
             if (token >= (uint32_t)p.vocab) {
@@ -657,6 +663,48 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
             load_floats<E>(p.x + lane * E, v);
         }
         load_floats<E>(p.gain + lane * E, gv);
+    } else if (rows_wave) {
+        // load c covers chunk 64 c + lane of the wave's 32 rows taken slot by
+        // slot: consecutive lanes read consecutive 16-byte chunks of a row
+#pragma unroll
+        for (int c = 0; c < HC; ++c) {
+            const int chunk = 64 * c + lane, slot = chunk / CPR;
+            w[c] = *reinterpret_cast<const int4*>(p.W + slot_row(slot) * K + (chunk % CPR) * 16);
+        }
+        load_floats<HG>(p.sW + slot_row(lr) * G + hh * HG, sv);
+    }
+    // The first pass of key and value rows does not wait for the position: a
+    // load that needed it would start only when the position's own load came
+    // back. The rows are clamped to the capacity instead; rows past the cached
+    // ones are read but never used. No branch around these loads (it would
+    // make later wait counts conservative).
+    const int top = p.capacity - 1;
+    uint4 kr[KC][2];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+        const __half* row = Kc + (size_t)min(r + KROWS * c, top) * kHeadDim + 16 * li;
+        kr[c][0] = *reinterpret_cast<const uint4*>(row);
+        kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
+    }
+    uint2 vr[VC];
+#pragma unroll
+    for (int c = 0; c < VC; ++c)
+        vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(j + kClasses * c, top) * kHeadDim + 4 * dq);
+    const int pos = p.state->pos;
+    if (pos < 0 || pos >= p.capacity) {  // uniform over the block
+        if (tid == 0) atomicOr(&p.state->error, 2);
+        return;
+    }
+    float rc = 1.0f, rs = 0.0f;
+    if (rows_wave && section < 2) {
+        rc = p.rope_cos[(size_t)pos * (kHeadDim / 2) + rot];
+        rs = p.rope_sin[(size_t)pos * (kHeadDim / 2) + rot];
+    }
+    const int last_row = pos > 0 ? pos - 1 : 0;  // the last cached row (later passes clamp to it)
+
+    // 2. wave 0: the norm and the int8 codes (DS operations of a wave complete
+    // in order, so the squares need only a wave barrier)
+    if (wave == 0) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const int idx = lane * E + e;
@@ -694,102 +742,74 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
 #pragma unroll
         for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)code_of_quotient(y[e]);
         if (lane == 0) sx_s = sx;
-    } else {
-        // chunk c = LW jj + (tid - 64) is chunk c % CPR of head row c / CPR
-        // (q rows 0..63, k rows 64..127, v rows 128..191); thread 64 + r holds
-        // row r's scales (threads past row 191 repeat row 191: one cache line)
-#pragma unroll
-        for (int jj = 0; jj < NLW; ++jj) {
-            const int c = min(LW * jj + tid - 64, CHUNKS - 1);
-            w[jj] = *reinterpret_cast<const int4*>(p.W + global_row(c / CPR) * K + (c % CPR) * 16);
-        }
-        const float4* src = reinterpret_cast<const float4*>(p.sW + global_row(min(tid - 64, ROWS - 1)) * G);
-#pragma unroll
-        for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
-    }
-    if (pos < 0 || pos >= p.capacity) {  // uniform over the block
-        if (tid == 0) atomicOr(&p.state->error, 2);
-        return;
-    }
-    const int last_row = pos > 0 ? pos - 1 : 0;  // the last cached row (rows past it are never used)
-    __syncthreads();
-
-    // 2. every wave: its share of the first cache rows, clamped to the last
-    // cached row (no branch around these loads: it would make later wait counts
-    // conservative). Requested only now, so that wave 0's codes do not wait
-    // behind them; they arrive while waves 1-7 run the product.
-    uint4 kr[KC][2];
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-        const __half* row = Kc + (size_t)min(r + KROWS * c, last_row) * kHeadDim + 16 * li;
-        kr[c][0] = *reinterpret_cast<const uint4*>(row);
-        kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
-    }
-    uint2 vr[VC];
-#pragma unroll
-    for (int c = 0; c < VC; ++c)
-        vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(j + kClasses * c, last_row) * kHeadDim + 4 * dq);
-
-    // 3. waves 1-7: exact int32 group sums of the 192 rows, then the row epilogues
-    if (wave != 0) {
-#pragma unroll
-        for (int jj = 0; jj < NLW; ++jj) {
-            const int c = LW * jj + tid - 64;
-            const int4 xc = *reinterpret_cast<const int4*>(xq_s + (min(c, CHUNKS - 1) % CPR) * 16);
-            int part = dot16(w[jj], xc, 0);
-            part = part + dpp_move<0xb1>(part);  // the pair partner (lane ^ 1: chunk c ^ 1)
-            if ((tid & 1) == 0 && c < CHUNKS) acc_s[(c / CPR) * G + (c % CPR) / 2] = part;
-        }
     }
     __syncthreads();
-    if (tid >= 64 && tid < 64 + ROWS) {
-        const int row = tid - 64;
+
+    // 3. waves 1-6: a row's exact group sums inside its lane pair, the epilogue
+    // chain over the even lane's groups continued by the odd lane, the rotary
+    // by lane swap, and the stores of q, k and v
+    if (rows_wave) {
+        // exact int32 sums of 16-code chunks, through this wave's own LDS rows
+        // (DS operations of a wave complete in order) to the lane pair of each
+        // row, which adds a group's two chunks
+        int* wacc = acc_s + (wave - 1) * 32 * CPR;
+#pragma unroll
+        for (int c = 0; c < HC; ++c) {
+            const int chunk = 64 * c + lane;
+            wacc[chunk] = dot16(w[c], *reinterpret_cast<const int4*>(xq_s + (chunk % CPR) * 16), 0);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        int acc[HG];
+#pragma unroll
+        for (int g = 0; g < HG; g += 2) {
+            const int4 a4 = *reinterpret_cast<const int4*>(wacc + lr * CPR + hh * HC + 2 * g);
+            acc[g] = a4.x + a4.y;
+            acc[g + 1] = a4.z + a4.w;
+        }
         const float sx = sx_s;
-        const int4* arow = reinterpret_cast<const int4*>(acc_s + row * G);
-        float total = 0.0f;
+        float scale[HG];
 #pragma unroll
-        for (int i = 0; i < G / 4; ++i) {
-            const int4 a4 = arow[i];
-            total = fmaf((float)a4.x, sv[i].x * sx, total);
-            total = fmaf((float)a4.y, sv[i].y * sx, total);
-            total = fmaf((float)a4.z, sv[i].z * sx, total);
-            total = fmaf((float)a4.w, sv[i].w * sx, total);
+        for (int g = 0; g < HG; ++g) scale[g] = sv[g] * sx;
+        float first = 0.0f;  // groups 0..HG-1 (meaningful in even lanes)
+#pragma unroll
+        for (int g = 0; g < HG; ++g) first = fmaf((float)acc[g], scale[g], first);
+        float total = lane_xor<1>(first);  // odd lanes continue from the even lane's total
+#pragma unroll
+        for (int g = 0; g < HG; ++g) total = fmaf((float)acc[g], scale[g], total);
+        // lane exchanges run in every lane (a DPP source lane that is off would
+        // give the lane its own value), then the selects
+        const float from_odd = lane_xor<1>(total);
+        const float value = hh ? total : from_odd;  // the row in both lanes of its pair
+        const float other = lane_xor<32>(value);    // dim i + 32 for dim i, and back
+        if (hh == 0) {
+            if (section == 2) {
+                const __half vh = __float2half_rn(value);
+                new_s[1][dim] = vh;
+                const_cast<__half*>(Vc)[(size_t)pos * kHeadDim + dim] = vh;
+            } else {
+                // rotate-half: (a, b) = (dim i, dim i + 32) -> (a c - b s, b c + a s)
+                const float rotated = lr < 16 ? value * rc - other * rs : value * rc + other * rs;
+                if (section == 0) {
+                    q_s[dim] = rotated;
+                } else {
+                    const __half kh = __float2half_rn(rotated);
+                    new_s[0][dim] = kh;
+                    const_cast<__half*>(Kc)[(size_t)pos * kHeadDim + dim] = kh;
+                }
+            }
         }
-        qkv_s[row] = total;
     }
     __syncthreads();
 
-    // 4. rotary at `pos` and the fp16 append
-    if (tid < kHeadDim / 2) {
-        const int i = tid, half = kHeadDim / 2;
-        const float c = p.rope_cos[(size_t)pos * half + i];
-        const float s = p.rope_sin[(size_t)pos * half + i];
-        const float qa = qkv_s[i], qb = qkv_s[i + half];
-        q_s[i] = qa * c - qb * s;
-        q_s[i + half] = qb * c + qa * s;
-        const float ka = qkv_s[kHeadDim + i], kb = qkv_s[kHeadDim + i + half];
-        const __half k0 = __float2half_rn(ka * c - kb * s), k1 = __float2half_rn(kb * c + ka * s);
-        const __half v0 = __float2half_rn(qkv_s[2 * kHeadDim + i]);
-        const __half v1 = __float2half_rn(qkv_s[2 * kHeadDim + i + half]);
-        new_s[0][i] = k0;
-        new_s[0][i + half] = k1;
-        new_s[1][i] = v0;
-        new_s[1][i + half] = v1;
-        __half* Kw = const_cast<__half*>(Kc) + (size_t)pos * kHeadDim;
-        __half* Vw = const_cast<__half*>(Vc) + (size_t)pos * kHeadDim;
-        Kw[i] = k0;
-        Kw[i + half] = k1;
-        Vw[i] = v0;
-        Vw[i + half] = v1;
-    }
-    __syncthreads();
-
-    // 5. scores (T2), KROWS key rows per pass
+    // 4. scores (T2), KROWS key rows per pass, and each thread's peak
     const int nglobal = pos, length = pos + 1;
     const float inverse_root = 1.0f / sqrtf((float)kHeadDim);
     float q16[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) q16[i] = q_s[16 * li + i];
+    float m = -INFINITY;
     for (int base = 0; base < nglobal; base += KROWS * KC) {
         if (base > 0) {
 #pragma unroll
@@ -803,32 +823,33 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
         for (int c = 0; c < KC; ++c) {
             const int pp = base + r + KROWS * c;
             if (base + KROWS * c + 16 * wave < nglobal) {  // wave-uniform: the pass holds live rows
-                const float s = score_row(q16, kr[c][0], kr[c][1]);
-                if (li == 0 && pp < nglobal) scores[pp] = s * inverse_root;
+                const float s = score_row(q16, kr[c][0], kr[c][1]) * inverse_root;
+                if (pp < nglobal) {
+                    m = fmaxf(m, s);
+                    if (li == 0) scores[pp] = s;
+                }
             }
         }
     }
     if (tid < 4) {
         const uint4 ka = *reinterpret_cast<const uint4*>(&new_s[0][16 * li]);
         const uint4 kb = *reinterpret_cast<const uint4*>(&new_s[0][16 * li + 8]);
-        const float s = score_row(q16, ka, kb);
-        if (li == 0) scores[nglobal] = s * inverse_root;
+        const float s = score_row(q16, ka, kb) * inverse_root;
+        m = fmaxf(m, s);
+        if (li == 0) scores[nglobal] = s;
     }
-    __syncthreads();
-
-    // 6. peak (order-free) and the fast_exp weights
-    float m = -INFINITY;
-    for (int pp = tid; pp < length; pp += NT) m = fmaxf(m, scores[pp]);
     m = wave_max(m);
     if (lane == 0) peak_s[wave] = m;
     __syncthreads();
+
+    // 5. the fast_exp weights (the peak is order-free)
     float peak = peak_s[0];
 #pragma unroll
     for (int w8 = 1; w8 < NT / 64; ++w8) peak = fmaxf(peak, peak_s[w8]);
     for (int pp = tid; pp < length; pp += NT) scores[pp] = fast_exp(scores[pp] - peak);
     __syncthreads();
 
-    // 7. weighted values (T3): thread (j, dq) walks positions j, j+32, ... in order
+    // 6. weighted values (T3): thread (j, dq) walks positions j, j+32, ... in order
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float total = 0.0f;
     const int last = nglobal > 0 ? nglobal - 1 : 0;

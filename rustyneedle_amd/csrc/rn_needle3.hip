@@ -2425,6 +2425,12 @@ int arena_take(std::vector<void*>& owned, N3Arena& a, size_t bytes, size_t chunk
         N3_HIP(hipMalloc(&p, size));
         owned.push_back(p);
         if (sizes) sizes->push_back(size);
+        // a whole chunk starts zeroed (also the part no buffer takes), so that
+        // nothing a kernel reads depends on what the memory held before
+        // (on the null stream, waited for here: the session streams do not
+        // synchronise with it)
+        N3_HIP(hipMemset(p, 0, size));
+        N3_HIP(hipStreamSynchronize(nullptr));
         a.cur = static_cast<char*>(p);
         a.left = size;
     }
