@@ -129,6 +129,7 @@ def profile_decode(rn, model, cfg, cache, steps: int = DECODE_TOKENS):
     sess.profile_step(first, steps)  # warm-up
     sess.truncate(CONTEXT)
     prof = sess.profile_step(first, steps)
+    prof = {k: p for k, p in prof.items() if p["per_step"] > 0}  # kinds the step launches
     # the roofline bytes assume the mean cache length of this run's positions
     nbytes = decode_kernel_bytes(cfg, CONTEXT, steps)
     for k, p in prof.items():

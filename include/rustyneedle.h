@@ -461,12 +461,14 @@ int rn_session_stream(const rn_session* session, void** stream);
  * both arrays of RN_PROFILE_KINDS entries in this order: */
 enum {
     RN_PROFILE_QKV_ATTENTION = 0, /* norm + each head's q/k/v rows + rotary + fp16 append + attention
-                                     (layer 0: + embedding), one block per head */
+                                     (layer 0: + the previous step's argmax and the embedding), one
+                                     block per head */
     RN_PROFILE_OUT = 1,           /* quantise + out product + residual */
     RN_PROFILE_GATE_UP = 2,       /* norm + gate/up product + silu(gate)*up */
     RN_PROFILE_DOWN = 3,          /* quantise + down product + residual */
-    RN_PROFILE_LOGITS = 4,        /* final norm + tied logits product + per-block argmax */
-    RN_PROFILE_FINAL = 5,         /* argmax reduction, next token, position advance */
+    RN_PROFILE_LOGITS = 4,        /* final norm + tied logits product + per-block argmax keys + position
+                                     advance (the next step's first kernel reduces the keys) */
+    RN_PROFILE_FINAL = 5,         /* a separate argmax reduction (0 launches a step in this build) */
     RN_PROFILE_KINDS = 6
 };
 int rn_session_profile_step(rn_session* session, uint32_t first, int steps, float* kind_us, int* kind_count);

@@ -1063,6 +1063,18 @@ struct StepProbe {
     void done(int kind) { kinds.push_back(kind); }
 };
 
+// The blocks of the logits product of a greedy step: one argmax key each.
+static int logits_blocks(const rn_config& c) {
+    const int rpb = gemv_rows_per_block(c.vocab, c.d_model, kStore);
+    return (c.vocab + rpb - 1) / rpb;
+}
+
+// A greedy step is: the head kernel of layer 0 reduces the previous step's
+// block keys into the token it embeds (and records it in ids), the layers,
+// then the logits product, which leaves its block keys and moves pos and step
+// on. The choice of the last step is collected after the run
+// (launch_argmax_finalize mode 1); the first step's token is planted as keys
+// by launch_greedy_start.
 static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) {
     const rn_model* m = s->model;
     const rn_config& c = m->cfg;
@@ -1096,8 +1108,12 @@ static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) 
             a.rope_cos = m->rope_cos;
             a.rope_sin = m->rope_sin;
             a.out = s->attn;
-            RN_PROFILED(RN_PROFILE_QKV_ATTENTION,
-                        launch_qkv_attend(a, d, l == 0 ? kEmbedNorm : kNorm, c.heads, st));
+            a.keys = s->keys;
+            a.nkeys = logits_blocks(c);
+            a.logits = s->logits;
+            a.ids = s->ids;
+            const int pro = l > 0 ? kNorm : (greedy ? kEmbedArgmax : kEmbedNorm);
+            RN_PROFILED(RN_PROFILE_QKV_ATTENTION, launch_qkv_attend(a, d, pro, c.heads, st));
         }
         {
             GemvParams p{};
@@ -1132,8 +1148,8 @@ static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) 
         return RN_OK;
     }
     // Greedy: the logits product takes the final norm as its prologue (block 0
-    // also writes the hidden state), each block emits its greedy key, and a
-    // one-block kernel reduces them into the next token and advances the position.
+    // also writes the hidden state), each block emits its greedy key, and block
+    // 0 moves the position on; the next step's first kernel reduces the keys.
     GemvParams p{};
     p.nseg = 1;
     p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab, 0};
@@ -1142,10 +1158,9 @@ static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) 
     p.eps = c.norm_eps;
     p.hidden_out = s->hidden;
     p.keys = s->keys;
+    p.advance = s->state;
     const int rpb = gemv_rows_per_block(c.vocab, d, kStore);
-    const int blocks = (c.vocab + rpb - 1) / rpb;
-    RN_PROFILED(RN_PROFILE_LOGITS, launch_gemv(p, d, kNorm, kArgmax, kPlane, rpb, blocks, st));
-    RN_PROFILED(RN_PROFILE_FINAL, launch_argmax_finalize(s->keys, blocks, s->logits, s->state, s->ids, st));
+    RN_PROFILED(RN_PROFILE_LOGITS, launch_gemv(p, d, kNorm, kArgmax, kPlane, rpb, logits_blocks(c), st));
     return RN_OK;
 #undef RN_PROFILED
 }
@@ -1493,12 +1508,15 @@ int rn_session_decode_greedy(rn_session* s, uint32_t first, int steps, uint32_t*
         const char* e = getenv("RN_DECODE_GRAPH");
         return !(e && e[0] == '0');
     }();
+    const int nkeys = logits_blocks(s->model->cfg);
     if (!use_graph) {
-        RN_HIP(launch_set_state(s->state, first, s->length, 0, (uint32_t)s->capacity, s->stream));
+        RN_HIP(launch_greedy_start(s->state, first, s->length, (uint32_t)s->capacity, s->keys, nkeys, s->logits,
+                                   s->stream));
         for (int i = 0; i < steps; ++i) {
             const int rc = enqueue_step(s, true);
             if (rc) return rc;
         }
+        RN_HIP(launch_argmax_finalize(s->keys, nkeys, s->logits, s->state, s->ids, s->stream, 1));
         RN_HIP(hipMemcpyAsync(ids, s->ids, 4 * (size_t)steps, hipMemcpyDeviceToHost, s->stream));
         s->length += steps;
         s->has_hidden = true;
@@ -1518,8 +1536,10 @@ int rn_session_decode_greedy(rn_session* s, uint32_t first, int steps, uint32_t*
         (void)hipGraphDestroy(graph);
         RN_HIP(e);
     }
-    RN_HIP(launch_set_state(s->state, first, s->length, 0, (uint32_t)s->capacity, s->stream));
+    RN_HIP(launch_greedy_start(s->state, first, s->length, (uint32_t)s->capacity, s->keys, nkeys, s->logits,
+                               s->stream));
     for (int i = 0; i < steps; ++i) RN_HIP(hipGraphLaunch(s->step_graph, s->stream));
+    RN_HIP(launch_argmax_finalize(s->keys, nkeys, s->logits, s->state, s->ids, s->stream, 1));
     RN_HIP(hipMemcpyAsync(ids, s->ids, 4 * (size_t)steps, hipMemcpyDeviceToHost, s->stream));
     s->length += steps;
     s->has_hidden = true;
@@ -1537,9 +1557,13 @@ int rn_session_profile_step(rn_session* s, uint32_t first, int steps, float* kin
     probe.events.resize(2 * launches);
     for (auto& e : probe.events) RN_HIP(hipEventCreate(&e));
     int rc = RN_OK;
-    hipError_t e = launch_set_state(s->state, first, s->length, 0, (uint32_t)s->capacity, s->stream);
+    const int nkeys = logits_blocks(s->model->cfg);
+    hipError_t e = launch_greedy_start(s->state, first, s->length, (uint32_t)s->capacity, s->keys, nkeys, s->logits,
+                                       s->stream);
     for (int i = 0; i < steps && rc == RN_OK && e == hipSuccess; ++i) rc = enqueue_step(s, true, &probe);
     launch_events() = LaunchEvents{};
+    if (e == hipSuccess && rc == RN_OK)
+        e = launch_argmax_finalize(s->keys, nkeys, s->logits, s->state, s->ids, s->stream, 1);
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
     double sum[RN_PROFILE_KINDS] = {0};
     int count[RN_PROFILE_KINDS] = {0};

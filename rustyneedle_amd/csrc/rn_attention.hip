@@ -646,8 +646,28 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
     int4 w[HC];
     float sv[HG];
     if (wave == 0) {
-        if constexpr (PRO == kEmbedNorm) {
-            uint32_t token = p.state->token;
+        if constexpr (PRO == kEmbedNorm || PRO == kEmbedArgmax) {
+            uint32_t token;
+            if constexpr (PRO == kEmbedArgmax) {
+                // the previous step's greedy choice (generator.rs:257-265): the
+                // largest of the logits kernel's block keys (the lowest index
+                // among equal values); a NaN at index 0 is never displaced
+                uint64_t key = 0ull;
+                for (int i = lane; i < p.nkeys; i += 64) {
+                    const uint64_t k = p.keys[i];
+                    key = k > key ? k : key;
+                }
+                key = wave_max_u64(key);
+                const float first = p.logits[0];
+                token = (first != first) ? 0u : argmax_index(key);
+                if (h == 0 && lane == 0) {
+                    p.state->token = token;
+                    const uint32_t step = p.state->step;
+                    if (step > 0 && step - 1 < p.state->ids_capacity) p.ids[step - 1] = token;
+                }
+            } else {
+                token = p.state->token;
+            }
             if (token >= (uint32_t)p.vocab) {
                 if (lane == 0 && h == 0) atomicOr(&p.state->error, 1);
                 token = 0;
@@ -907,6 +927,7 @@ hipError_t launch_qkv_attend(const QkvAttendParams& p, int d_model, int prologue
     if (d_model == 512) {
         if (prologue == kNorm) rn_launch((qkv_attend_kernel<512, kNorm, 3, 10>), grid, block, lds, stream, p);
         else if (prologue == kEmbedNorm) rn_launch((qkv_attend_kernel<512, kEmbedNorm, 3, 10>), grid, block, lds, stream, p);
+        else if (prologue == kEmbedArgmax) rn_launch((qkv_attend_kernel<512, kEmbedArgmax, 3, 10>), grid, block, lds, stream, p);
         else return hipErrorInvalidValue;
     } else if (d_model == 384) {
         if (prologue == kNorm) rn_launch((qkv_attend_kernel<384, kNorm, 3, 10>), grid, block, lds, stream, p);

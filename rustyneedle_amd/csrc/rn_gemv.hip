@@ -248,6 +248,11 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         uint64_t key = mine ? argmax_key(total, (uint32_t)row_of(lane)) : 0ull;
         key = wave_max_u64(key);
         if (lane == 0) p.keys[blockIdx.x] = (unsigned long long)key;
+        // the last kernel of a greedy step (no other block reads the state)
+        if (p.advance != nullptr && blockIdx.x == 0 && lane == 0) {
+            p.advance->pos = p.advance->pos + 1;
+            p.advance->step = p.advance->step + 1;
+        }
     }
 }
 
@@ -353,7 +358,8 @@ hipError_t launch_gemv_splitk(const GemvParams& p, int columns, int rows, hipStr
 }
 
 __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned long long* keys, int nkeys,
-                                                              const float* logits, DecodeState* st, uint32_t* ids) {
+                                                              const float* logits, DecodeState* st, uint32_t* ids,
+                                                              int mode) {
     __shared__ unsigned long long best_s[4];
     uint64_t key = 0ull;
     for (int i = threadIdx.x; i < nkeys; i += 256) key = keys[i] > key ? keys[i] : key;
@@ -367,15 +373,38 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
         const uint32_t index = (first != first) ? 0u : argmax_index(k);  // a NaN at 0 is never displaced
         st->token = index;
         const uint32_t step = st->step;
-        if (ids != nullptr && step < st->ids_capacity) ids[step] = index;
-        st->step = step + 1;
-        st->pos = st->pos + 1;
+        if (mode == 0) {
+            if (ids != nullptr && step < st->ids_capacity) ids[step] = index;
+            st->step = step + 1;
+            st->pos = st->pos + 1;
+        } else if (ids != nullptr && step > 0 && step - 1 < st->ids_capacity) {
+            ids[step - 1] = index;
+        }
     }
 }
 
 hipError_t launch_argmax_finalize(const unsigned long long* keys, int nkeys, const float* logits,
-                                  DecodeState* state, uint32_t* ids, hipStream_t stream) {
-    rn_launch(argmax_finalize_kernel, dim3(1), dim3(256), 0, stream, keys, nkeys, logits, state, ids);
+                                  DecodeState* state, uint32_t* ids, hipStream_t stream, int mode) {
+    rn_launch(argmax_finalize_kernel, dim3(1), dim3(256), 0, stream, keys, nkeys, logits, state, ids, mode);
+    return hipGetLastError();
+}
+
+__global__ void greedy_start_kernel(DecodeState* st, uint32_t token, int32_t pos, uint32_t ids_capacity,
+                                    unsigned long long* keys, int nkeys, float* logits) {
+    for (int i = threadIdx.x; i < nkeys; i += blockDim.x) keys[i] = argmax_key(0.0f, token);
+    if (threadIdx.x == 0) {
+        st->token = token;
+        st->pos = pos;
+        st->step = 0;
+        st->ids_capacity = ids_capacity;
+        logits[0] = 0.0f;
+    }
+}
+
+hipError_t launch_greedy_start(DecodeState* state, uint32_t token, int32_t pos, uint32_t ids_capacity,
+                               unsigned long long* keys, int nkeys, float* logits, hipStream_t stream) {
+    rn_launch(greedy_start_kernel, dim3(1), dim3(256), 0, stream, state, token, pos, ids_capacity, keys, nkeys,
+              logits);
     return hipGetLastError();
 }
 

@@ -53,7 +53,9 @@ struct DecodeState {
 // quantisation of kQuant. kCrossNorm: the cross-attention residual first
 // (x + cross_gain * zero_centred_norm(attended, post_gain), cross.rs:176-181;
 // block 0 writes it to x_out), then kNorm on that sum.
-enum GemvPrologue { kQuant = 0, kNorm = 1, kEmbedNorm = 2, kCodes = 3, kClassSum = 4, kCrossNorm = 5 };
+// kEmbedArgmax (the batch-1 head kernel only): the token is the greedy choice
+// of the previous step's logits, reduced from the logits kernel's block keys.
+enum GemvPrologue { kQuant = 0, kNorm = 1, kEmbedNorm = 2, kCodes = 3, kClassSum = 4, kCrossNorm = 5, kEmbedArgmax = 6 };
 enum GemvEpilogue { kStore = 0, kResidual = 1, kSilu = 2, kArgmax = 3 };
 enum ProductForm { kPanel = 0, kPlane = 1 };
 
@@ -85,6 +87,7 @@ struct GemvParams {
     float* hidden_out;    // kNorm: block 0 writes the normed input (nullable)
     DecodeState* state;   // kEmbedNorm: the token to embed
     unsigned long long* keys;  // kArgmax: one greedy key per block (argmax_key)
+    DecodeState* advance;      // kArgmax: when set, block 0 moves pos and step on by one
     const float* attended;     // kCrossNorm: the cross-attention output and its post-norm gains
     const float* post_gain;
     float cross_gain;
@@ -153,6 +156,10 @@ struct QkvAttendParams {
     const float* rope_cos;
     const float* rope_sin;
     float* out;           // [d] attention output, head h at 64 h
+    const unsigned long long* keys;  // kEmbedArgmax: the previous logits' block keys [nkeys]
+    int nkeys;
+    const float* logits;  // kEmbedArgmax: the previous logits (index 0 for the NaN rule)
+    uint32_t* ids;        // kEmbedArgmax: block 0 writes ids[step - 1]
 };
 hipError_t launch_qkv_attend(const QkvAttendParams& p, int d_model, int prologue, int heads, hipStream_t stream);
 
@@ -376,8 +383,16 @@ hipError_t launch_finish_push(const float* x, const float* gain, int n, float ep
                               DecodeState* state, hipStream_t stream);
 // Second stage of the greedy argmax: reduces the per-block keys of the logits
 // product, writes the token into the state and ids[step], advances step and pos.
+// mode 0: token = the keys' choice; ids[step] = token; step and pos move on.
+// mode 1 (after a greedy run whose steps moved pos and step themselves): the
+// last step's choice into ids[step - 1], nothing moved.
 hipError_t launch_argmax_finalize(const unsigned long long* keys, int nkeys, const float* logits,
-                                  DecodeState* state, uint32_t* ids, hipStream_t stream);
+                                  DecodeState* state, uint32_t* ids, hipStream_t stream, int mode = 0);
+// The start of a greedy run with the choice folded into the next step's first
+// kernel: the state (token, pos, step 0, ids capacity), every block key set to
+// the key of `token` and logits[0] to 0, so that step 0 chooses `token`.
+hipError_t launch_greedy_start(DecodeState* state, uint32_t token, int32_t pos, uint32_t ids_capacity,
+                               unsigned long long* keys, int nkeys, float* logits, hipStream_t stream);
 // Overwrites token/pos/step/ids_capacity.
 hipError_t launch_set_state(DecodeState* state, uint32_t token, int32_t pos, uint32_t step, uint32_t ids_capacity,
                             hipStream_t stream);
