@@ -143,6 +143,9 @@ struct rn_batch {
     uint32_t* ids = nullptr;
     int ids_steps = 0;
     bool has_logits = false;
+    int32_t* step = nullptr;            // the step of the running decode (its ids slot)
+    hipGraphExec_t step_graph = nullptr;  // one step, captured for graph_steps and this ids buffer
+    int graph_steps = 0;
 };
 
 // ---- the fixed scratch of rn_matrix_multiply_batch_noalloc ------------------------
@@ -1689,7 +1692,7 @@ int rn_batch_create(const rn_model* m, int count, int capacity, rn_batch** out) 
     const size_t ce = cache_elems(c, capacity) * count, d = c.d_model, f = c.ffn, n = count;
     const size_t total = 2 * align_up(ce * 2) + align_up(4 * n) + align_up(4 * n * d) * 2 + align_up(4 * n * 3 * d) +
                          align_up(4 * n * f) + align_up(4 * n * c.vocab) + align_up(n * (f > d ? f : d)) +
-                         align_up(4 * n) * 3;
+                         align_up(4 * n) * 3 + align_up(256);
     if (hipMalloc(&b->arena, total) != hipSuccess) {
         delete b;
         return fail(RN_ERR_MEMORY, "device allocation of %zu bytes failed", total);
@@ -1707,6 +1710,7 @@ int rn_batch_create(const rn_model* m, int count, int capacity, rn_batch** out) 
     b->sx = (float*)a.take(4 * n);
     b->tokens = (uint32_t*)a.take(4 * n);
     b->error = (int32_t*)a.take(4 * n);
+    b->step = (int32_t*)a.take(256);
     if (hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking) != hipSuccess ||
         hipMemsetAsync(b->arena, 0, total, b->stream) != hipSuccess || hipStreamSynchronize(b->stream) != hipSuccess) {
         if (b->stream) (void)hipStreamDestroy(b->stream);
@@ -1721,6 +1725,7 @@ int rn_batch_create(const rn_model* m, int count, int capacity, rn_batch** out) 
 int rn_batch_free(rn_batch* b) {
     if (!b) return RN_OK;
     if (b->stream) (void)hipStreamSynchronize(b->stream);
+    if (b->step_graph) (void)hipGraphExecDestroy(b->step_graph);
     if (b->ids) (void)hipFree(b->ids);
     (void)hipFree(b->arena);
     if (b->stream) (void)hipStreamDestroy(b->stream);
@@ -1763,8 +1768,10 @@ int rn_batch_set_cache(rn_batch* b, int sequence, int length, const uint16_t* ke
 
 // One step for every sequence: embed the current tokens, the layer stack with
 // M=count MFMA products and ragged attention, the final norm, the tied logits
-// product and a per-row argmax that becomes the next tokens.
-static int enqueue_batch_step(rn_batch* b, int steps, int step) {
+// product and a per-row argmax that becomes the next tokens. The step's ids
+// slot and the positions are read from the device (b->step, b->pos), so the
+// same launches serve every step: the step is captured once as a hipGraph.
+static int enqueue_batch_step(rn_batch* b, int steps) {
     const rn_model* m = b->model;
     const rn_config& c = m->cfg;
     const int n = b->count, d = c.d_model, f = c.ffn;
@@ -1808,8 +1815,8 @@ static int enqueue_batch_step(rn_batch* b, int steps, int step) {
     RN_HIP(launch_gemm(GemmParams{b->Xq, b->sx, m->embedding.W, m->embedding.sW, n, c.vocab, d, b->logits, c.vocab,
                                   nullptr, 0},
                        kGemmStore, kPlane, false, st));
-    RN_HIP(launch_argmax_rows(b->logits, n, c.vocab, b->tokens, b->ids, steps, step, st));
-    RN_HIP(launch_advance_positions(b->pos, n, 1, st));
+    RN_HIP(launch_argmax_rows(b->logits, n, c.vocab, b->tokens, b->ids, steps, 0, st, b->step));
+    RN_HIP(launch_advance_positions(b->pos, n, 1, st, b->step));
     return RN_OK;
 }
 
@@ -1830,12 +1837,44 @@ int rn_batch_decode_greedy(rn_batch* b, const uint32_t* first, int steps, uint32
         b->ids = nullptr;
         if (hipMalloc(&b->ids, 4 * (size_t)b->count * steps) != hipSuccess) return fail(RN_ERR_MEMORY, "id buffer");
         b->ids_steps = steps;
+        if (b->step_graph) RN_HIP(hipGraphExecDestroy(b->step_graph));
+        b->step_graph = nullptr;
     }
     RN_HIP(hipMemcpyAsync(b->tokens, first, 4 * (size_t)b->count, hipMemcpyHostToDevice, b->stream));
     RN_HIP(hipMemcpyAsync(b->pos, b->lengths.data(), 4 * (size_t)b->count, hipMemcpyHostToDevice, b->stream));
-    for (int step = 0; step < steps; ++step) {
-        int rc = enqueue_batch_step(b, steps, step);
-        if (rc) return rc;
+    RN_HIP(hipMemsetAsync(b->step, 0, sizeof(int32_t), b->stream));
+    // RN_DECODE_GRAPH=0 launches the step's kernels directly (same kernels,
+    // same arguments; for kernel-level tracing)
+    static const bool use_graph = [] {
+        const char* e = getenv("RN_DECODE_GRAPH");
+        return !(e && e[0] == '0');
+    }();
+    if (!use_graph) {
+        for (int step = 0; step < steps; ++step) {
+            int rc = enqueue_batch_step(b, steps);
+            if (rc) return rc;
+        }
+    } else {
+        if (b->step_graph && b->graph_steps != steps) {
+            RN_HIP(hipGraphExecDestroy(b->step_graph));
+            b->step_graph = nullptr;
+        }
+        if (!b->step_graph) {
+            hipGraph_t graph = nullptr;
+            RN_HIP(hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal));
+            const int rc = enqueue_batch_step(b, steps);
+            hipError_t e = hipStreamEndCapture(b->stream, &graph);
+            if (rc) {
+                if (graph) (void)hipGraphDestroy(graph);
+                return rc;
+            }
+            RN_HIP(e);
+            e = hipGraphInstantiate(&b->step_graph, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            RN_HIP(e);
+            b->graph_steps = steps;
+        }
+        for (int step = 0; step < steps; ++step) RN_HIP(hipGraphLaunch(b->step_graph, b->stream));
     }
     RN_HIP(hipMemcpyAsync(ids, b->ids, 4 * (size_t)b->count * steps, hipMemcpyDeviceToHost, b->stream));
     int32_t err = 0;

@@ -956,7 +956,7 @@ hipError_t launch_embed_rows(const uint32_t* tokens, int count, const int8_t* E,
 // One 1024-thread block a row; 16-byte loads, four in flight a thread, when
 // the row allows them.
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* logits, int n, uint32_t* tokens, uint32_t* ids,
-                                                           int steps, int step) {
+                                                           int steps, int step, const int32_t* step_dev) {
     __shared__ unsigned long long best_s[16];
     const float* row = logits + (size_t)blockIdx.x * n;
     const int tid = threadIdx.x;
@@ -1001,25 +1001,27 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* logits, 
         const float first = row[0];
         const uint32_t index = (first != first) ? 0u : argmax_index(k);
         tokens[blockIdx.x] = index;
-        if (ids != nullptr) ids[(size_t)blockIdx.x * steps + step] = index;
+        const int at = step_dev != nullptr ? *step_dev : step;
+        if (ids != nullptr && at >= 0 && at < steps) ids[(size_t)blockIdx.x * steps + at] = index;
     }
 }
 
 hipError_t launch_argmax_rows(const float* logits, int count, int n, uint32_t* tokens, uint32_t* ids, int steps,
-                              int step, hipStream_t stream) {
+                              int step, hipStream_t stream, const int32_t* step_dev) {
     if (count <= 0) return hipSuccess;
-    rn_launch(argmax_rows_kernel, dim3(count), dim3(1024), 0, stream, logits, n, tokens, ids, steps, step);
+    rn_launch(argmax_rows_kernel, dim3(count), dim3(1024), 0, stream, logits, n, tokens, ids, steps, step, step_dev);
     return hipGetLastError();
 }
 
-__global__ void advance_positions_kernel(int32_t* pos, int count, int by) {
+__global__ void advance_positions_kernel(int32_t* pos, int count, int by, int32_t* step) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < count) pos[i] = pos[i] + by;
+    if (step != nullptr && i == 0) *step = *step + 1;
 }
 
-hipError_t launch_advance_positions(int32_t* pos, int count, int by, hipStream_t stream) {
+hipError_t launch_advance_positions(int32_t* pos, int count, int by, hipStream_t stream, int32_t* step) {
     if (count <= 0) return hipSuccess;
-    rn_launch(advance_positions_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, pos, count, by);
+    rn_launch(advance_positions_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, pos, count, by, step);
     return hipGetLastError();
 }
 

@@ -217,9 +217,12 @@ hipError_t launch_quantise_strided(const float* x, size_t x_stride, int count, i
                                    hipStream_t stream);
 hipError_t launch_embed_rows(const uint32_t* tokens, int count, const int8_t* E, const float* sE, int d, int vocab,
                              float scale, float* X, int32_t* error, hipStream_t stream);
+// step_dev (nullable): the step is read from the device, so that a captured
+// step graph writes each replay's ids in its own slot.
 hipError_t launch_argmax_rows(const float* logits, int count, int n, uint32_t* tokens, uint32_t* ids, int steps,
-                              int step, hipStream_t stream);
-hipError_t launch_advance_positions(int32_t* pos, int count, int by, hipStream_t stream);
+                              int step, hipStream_t stream, const int32_t* step_dev = nullptr);
+// pos[i] += by for each sequence; thread 0 also moves *step on (nullable).
+hipError_t launch_advance_positions(int32_t* pos, int count, int by, hipStream_t stream, int32_t* step = nullptr);
 
 // ---- speech path (rn_whistle.hip) ---------------------------------------------
 // The stem's first convolution (kernel 3, stride 1, pad 1) + silu into h1 [F][d].
