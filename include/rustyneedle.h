@@ -345,6 +345,10 @@ int rn_silu(const float* x, float* y, int n, void* stream);
  * bit for bit to glibc's x86-64 expf. Exposed for parity checks. */
 int rn_libm_exp(const float* x, float* y, int n, void* stream);
 int rn_sigmoid(const float* x, float* y, int n, void* stream);
+/* f32::ln as the reference calls it (the C library's logf: the log-mel
+ * features, frontend.rs:96-99), elementwise on the device; equal bit for bit to
+ * this image's glibc logf on all 2^32 inputs. Exposed for parity checks. */
+int rn_libm_log(const float* x, float* y, int n, void* stream);
 
 /* ops::zero_centred_norm (ops.rs:44-50) for `count` rows of `n` floats on the
  * device (n a multiple of 8, <= 4096). */
@@ -576,6 +580,13 @@ int rn_whistle_stem(rn_whistle* whistle, const float* mel, float* out);
  * the encoded frames and every decoder layer's int8 key/value memory stay on
  * the device; `encoded` (nullable) receives [T][d]. Resets the decoder. */
 int rn_whistle_encode(rn_whistle* whistle, const float* mel, float* encoded);
+/* Whistle::encode from samples (lib.rs:155-161): Frontend::log_mel
+ * (frontend.rs:72-103) runs on the device and the stem reads its features in
+ * place, with no round trip through the host; then as rn_whistle_encode.
+ * samples: n host floats with n / hop == the model's frames; the front end's
+ * mels must be the model's. spread (nullable) receives Features::spread. */
+int rn_whistle_encode_samples(rn_whistle* whistle, const rn_frontend* frontend, const float* samples, int n,
+                              float* encoded, float* spread);
 /* The cross memory of the last encode: keys/values [dec_layers][T][heads][64]
  * int8, scales [dec_layers][T][heads]. */
 int rn_whistle_memory(const rn_whistle* whistle, int8_t* keys, float* key_scales, int8_t* values,

@@ -130,6 +130,18 @@ def libm_exp_array(x: np.ndarray, sigmoid: bool = False) -> np.ndarray:
     return y
 
 
+lib.ro_libm_log_array.restype = None
+lib.ro_libm_log_array.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+
+
+def libm_log_array(x: np.ndarray) -> np.ndarray:
+    """The C library's logf (f32::ln), elementwise."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib.ro_libm_log_array(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
 def silu(v: float) -> float:
     return lib.ro_silu(float(v))
 

@@ -49,6 +49,13 @@ void ro_libm_exp_array(const float* x, float* y, size_t n, int sigmoid) {
     for (size_t i = 0; i < n; ++i) y[i] = sigmoid ? 1.0f / (1.0f + expf(-x[i])) : expf(x[i]);
 }
 
+/* f32::ln over an array: the C library's logf, which the reference's f32::ln
+ * calls (frontend.rs:96-99). */
+void ro_libm_log_array(const float* x, float* y, size_t n) {
+#pragma omp parallel for schedule(static) num_threads(ro_get_threads())
+    for (size_t i = 0; i < n; ++i) y[i] = logf(x[i]);
+}
+
 /* ops.rs:32-42 — max is order-free (NaN operands are ignored like f32::max). */
 float ro_peak_magnitude(const float* x, int n) {
     float peak = 0.0f;

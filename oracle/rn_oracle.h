@@ -51,6 +51,7 @@ extern "C" {
 /* ---- scalar and vector primitives: crates/kernels/src/ops.rs ---------------- */
 float ro_fast_exp(float value);                                     /* ops.rs:82-90   */
 void ro_libm_exp_array(const float* x, float* y, size_t n, int sigmoid); /* f32::exp, ops.rs:68-71 */
+void ro_libm_log_array(const float* x, float* y, size_t n);              /* f32::ln, frontend.rs:96-99 */
 float ro_silu(float value);                                         /* ops.rs:73-76   */
 float ro_peak_magnitude(const float* x, int n);                     /* ops.rs:32-42   */
 float ro_int8_scale(const float* x, int n);                         /* ops.rs:103-110 */

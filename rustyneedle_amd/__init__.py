@@ -178,6 +178,7 @@ SIGNATURES = {
     "rn_silu": (_i, [_p, _p, _i, _p]),
     "rn_libm_exp": (_i, [_p, _p, _i, _p]),
     "rn_sigmoid": (_i, [_p, _p, _i, _p]),
+    "rn_libm_log": (_i, [_p, _p, _i, _p]),
     "rn_zero_centred_norm": (_i, [_p, _p, _i, _i, _p, _p]),
     "rn_attend_heads": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, _p]),
     "rn_model_create": (_i, [C.POINTER(Config), C.POINTER(WeightsHost), C.POINTER(_p)]),
@@ -214,6 +215,7 @@ SIGNATURES = {
     "rn_whistle_tables": (_i, [_p, _p, _p]),
     "rn_whistle_stem": (_i, [_p, _p, _p]),
     "rn_whistle_encode": (_i, [_p, _p, _p]),
+    "rn_whistle_encode_samples": (_i, [_p, _p, _p, _i, _p, _p]),
     "rn_whistle_memory": (_i, [_p, _p, _p, _p, _p]),
     "rn_whistle_reset": (_i, [_p]),
     "rn_whistle_push": (_i, [_p, _u32]),
@@ -621,6 +623,11 @@ def sigmoid(x: np.ndarray) -> np.ndarray:
     return _elementwise(lib.rn_sigmoid, x)
 
 
+def libm_log(x: np.ndarray) -> np.ndarray:
+    """f32::ln (the C library's logf) on the device."""
+    return _elementwise(lib.rn_libm_log, x)
+
+
 def quantise_int8(x: np.ndarray):
     x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
     count, cols = x.shape
@@ -1009,6 +1016,15 @@ class Whistle:
         out = np.empty((self.frames, self.config["d_model"]), np.float32) if copy_out else None
         check(lib.rn_whistle_encode(self.handle, _ptr(mel), _ptr(out) if copy_out else None))
         return out
+
+    def encode_samples(self, frontend: "Frontend", samples: np.ndarray, copy_out: bool = True):
+        """Whistle::encode from samples: the log-mel features stay on the device."""
+        x = np.ascontiguousarray(samples, dtype=np.float32)
+        out = np.empty((self.frames, self.config["d_model"]), np.float32) if copy_out else None
+        spread = C.c_float()
+        check(lib.rn_whistle_encode_samples(self.handle, frontend.handle, _ptr(x) if x.size else None, x.size,
+                                            _ptr(out) if copy_out else None, C.byref(spread)))
+        return out, np.float32(spread.value)
 
     def memory(self):
         c = self.config

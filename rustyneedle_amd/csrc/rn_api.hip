@@ -713,6 +713,12 @@ int rn_sigmoid(const float* x, float* y, int n, void* stream) {
     return RN_OK;
 }
 
+int rn_libm_log(const float* x, float* y, int n, void* stream) {
+    RN_REQUIRE(x && y && n >= 0, "bad argument");
+    RN_HIP(launch_fast_exp(x, y, n, 4, (hipStream_t)stream));
+    return RN_OK;
+}
+
 int rn_zero_centred_norm(const float* x, const float* gain, int count, int n, float* out, void* stream) {
     RN_REQUIRE(x && gain && out, "null argument");
     RN_REQUIRE(n > 0 && n % 8 == 0 && n <= 4096 && count >= 0, "n must be a multiple of 8 in 8..4096");
@@ -1972,6 +1978,8 @@ struct rn_whistle {
     int8_t *mem_k = nullptr, *mem_v = nullptr;
     float *mem_ks = nullptr, *mem_vs = nullptr;
     bool encoded_ready = false;
+    char* fe_buf = nullptr;  // rn_whistle_encode_samples: samples, features and spread (grown as needed)
+    size_t fe_bytes = 0;
     // the decoder session
     __half *kcache = nullptr, *vcache = nullptr;
     int capacity = 0, length = 0;
@@ -2262,6 +2270,7 @@ int rn_whistle_free(rn_whistle* w) {
         (void)hipStreamSynchronize(w->stream);
         (void)hipStreamDestroy(w->stream);
     }
+    if (w->fe_buf) (void)hipFree(w->fe_buf);
     (void)hipFree(w->arena);
     delete w;
     return RN_OK;
@@ -2291,12 +2300,19 @@ int rn_whistle_stream(const rn_whistle* w, void** stream) {
 // as the int8 product of conv2 with the im2col rows: row t is h1 rows 2t..2t+2
 // (frames 2t-1..2t+1), contiguous, so the rows are read in place with a
 // stride of two frames and quantised per row; silu, into w->X.
-static int whistle_stem(rn_whistle* w, const float* mel) {
+// The stem over host features (copied to the device first) or, with
+// `on_device`, over features already on the device ([frames][mels], the first
+// c.frames rows read).
+static int whistle_stem(rn_whistle* w, const float* mel, bool on_device = false) {
     const rn_whistle_config& c = w->cfg;
     const int d = c.d_model, T = w->T;
     hipStream_t st = w->stream;
-    RN_HIP(hipMemcpyAsync(w->mel, mel, 4 * (size_t)c.frames * c.mels, hipMemcpyHostToDevice, st));
-    RN_HIP(launch_stem(w->mel, w->conv1, c.frames, c.mels, d, w->h1 + d, st));
+    const float* src = mel;
+    if (!on_device) {
+        RN_HIP(hipMemcpyAsync(w->mel, mel, 4 * (size_t)c.frames * c.mels, hipMemcpyHostToDevice, st));
+        src = w->mel;
+    }
+    RN_HIP(launch_stem(src, w->conv1, c.frames, c.mels, d, w->h1 + d, st));
     RN_HIP(launch_quantise_strided(w->h1, 2 * (size_t)d, T, 3 * d, w->Xq, w->sx, st));
     RN_HIP(launch_gemm(GemmParams{w->Xq, w->sx, w->conv2.W, w->conv2.sW, T, d, 3 * d, w->X, d, nullptr, 0},
                        kGemmStoreSilu, kPanel, false, st));
@@ -2376,10 +2392,9 @@ static int whistle_memory(rn_whistle* w) {
     return RN_OK;
 }
 
-int rn_whistle_encode(rn_whistle* w, const float* mel, float* encoded) {
-    RN_REQUIRE(w && mel, "null argument");
+static int whistle_encode(rn_whistle* w, const float* mel, bool on_device, float* encoded) {
     const rn_whistle_config& c = w->cfg;
-    int rc = whistle_stem(w, mel);
+    int rc = whistle_stem(w, mel, on_device);
     if (rc) return rc;
     for (int l = 0; l < c.enc_layers; ++l) {
         rc = whistle_encoder_layer(w, l);
@@ -2395,6 +2410,44 @@ int rn_whistle_encode(rn_whistle* w, const float* mel, float* encoded) {
     w->length = 0;
     w->has_hidden = false;
     return RN_OK;
+}
+
+int rn_whistle_encode(rn_whistle* w, const float* mel, float* encoded) {
+    RN_REQUIRE(w && mel, "null argument");
+    return whistle_encode(w, mel, false, encoded);
+}
+
+// Whistle::encode from samples (lib.rs:155-161): Frontend::log_mel on the
+// device into a buffer the stem then reads in place, so the features make no
+// round trip through the host. The front end must give the model's frames
+// (valid = n / hop == frames) of its mels; the frame past the valid ones is
+// zero after the normalisation, as the stem's zero padding is.
+int rn_whistle_encode_samples(rn_whistle* w, const rn_frontend* f, const float* samples, int n, float* encoded,
+                              float* spread) {
+    RN_REQUIRE(w && f && (samples || n == 0), "null argument");
+    RN_REQUIRE(n >= 0, "n must be non-negative");
+    const rn_whistle_config& c = w->cfg;
+    RN_REQUIRE(f->p.mels == c.mels, "the front end has %d mels, the model %d", f->p.mels, c.mels);
+    RN_REQUIRE(n / f->p.hop == c.frames, "%d samples give %d valid frames, the model takes %d", n, n / f->p.hop,
+               c.frames);
+    const int nf = n / f->p.hop + 1;
+    const size_t sb = align_up(sizeof(float) * (size_t)n + 4), fb = align_up(sizeof(float) * (size_t)nf * c.mels);
+    const size_t need = sb + fb + align_up(4 * (1 + (size_t)c.mels));
+    if (w->fe_bytes < need) {
+        RN_HIP(hipStreamSynchronize(w->stream));
+        if (w->fe_buf) RN_HIP(hipFree(w->fe_buf));
+        w->fe_buf = nullptr;
+        w->fe_bytes = 0;
+        if (hipMalloc(&w->fe_buf, need) != hipSuccess) return fail(RN_ERR_MEMORY, "front-end buffer of %zu bytes", need);
+        w->fe_bytes = need;
+    }
+    float* ds = (float*)w->fe_buf;
+    float* dd = (float*)(w->fe_buf + sb);
+    float* dspread = (float*)(w->fe_buf + sb + fb);
+    if (n) RN_HIP(hipMemcpyAsync(ds, samples, sizeof(float) * (size_t)n, hipMemcpyHostToDevice, w->stream));
+    RN_HIP(launch_log_mel(f->p, ds, n, dd, dspread, w->stream));
+    if (spread) RN_HIP(hipMemcpyAsync(spread, dspread, sizeof(float), hipMemcpyDeviceToHost, w->stream));
+    return whistle_encode(w, dd, true, encoded);
 }
 
 int rn_whistle_memory(const rn_whistle* w, int8_t* keys, float* key_scales, int8_t* values, float* value_scales) {

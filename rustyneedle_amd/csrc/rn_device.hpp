@@ -82,6 +82,52 @@ __device__ __forceinline__ float libm_expf(float x) {
 // ops.rs:68-71 with the C library's expf.
 __device__ __forceinline__ float libm_sigmoid(float value) { return 1.0f / (1.0f + libm_expf(-value)); }
 
+// The (1/c, log c) pairs of the 16 subintervals of [0x1.66p-1, 0x1.66p0) in
+// which the mantissa of x is reduced (rounded to double, as published with the
+// method below).
+static __device__ __constant__ const double kLogfTable[16][2] = {
+    {0x1.661ec79f8f3bep+0, -0x1.57bf7808caadep-2}, {0x1.571ed4aaf883dp+0, -0x1.2bef0a7c06ddbp-2},
+    {0x1.49539f0f010bp+0, -0x1.01eae7f513a67p-2},  {0x1.3c995b0b80385p+0, -0x1.b31d8a68224e9p-3},
+    {0x1.30d190c8864a5p+0, -0x1.6574f0ac07758p-3}, {0x1.25e227b0b8eap+0, -0x1.1aa2bc79c81p-3},
+    {0x1.1bb4a4a1a343fp+0, -0x1.a4e76ce8c0e5ep-4}, {0x1.12358f08ae5bap+0, -0x1.1973c5a611cccp-4},
+    {0x1.0953f419900a7p+0, -0x1.252f438e10c1ep-5}, {0x1p+0, 0x0p+0},
+    {0x1.e608cfd9a47acp-1, 0x1.aa5aa5df25984p-5},  {0x1.ca4b31f026aap-1, 0x1.c5e53aa362eb4p-4},
+    {0x1.b2036576afce6p-1, 0x1.526e57720db08p-3},  {0x1.9c2d163a1aa2dp-1, 0x1.bc2860d22477p-3},
+    {0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2},  {0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2}};
+
+// The C library's logf, which the reference's f32::ln calls (the log-mel
+// features, frontend.rs:96-99): the method of ARM's optimized-routines logf
+// (Szabolcs Nagy, 2017), which glibc builds since 2.28. x = 2^k z with z in
+// [0x1.66p-1, 0x1.66p0) and c near the middle of z's subinterval;
+// log(x) = k ln2 + log(c) + log1p(r) with r = z/c - 1 = fma(z, 1/c, -1), the
+// log1p a cubic in r evaluated in double, one rounding to float at the end.
+// Equal to this image's glibc logf on every one of the 2^32 inputs.
+__device__ __forceinline__ float libm_logf(float x) {
+    uint32_t ix = __float_as_uint(x);
+    if (ix == 0x3f800000u) return 0.0f;                      // log(1) = +0 in every rounding mode
+    if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {    // subnormal, zero, negative, inf or NaN
+        if (ix * 2u == 0u) return -__builtin_inff();
+        if (ix == 0x7f800000u) return x;
+        if ((ix & 0x80000000u) || ix * 2u >= 0xff000000u) return __builtin_nanf("");
+        ix = __float_as_uint(x * 0x1p23f);                   // normalise a subnormal
+        ix -= 23u << 23;
+    }
+    const double ln2 = 0x1.62e42fefa39efp-1;
+    const double a0 = -0x1.00ea348b88334p-2, a1 = 0x1.5575b0be00b6ap-2, a2 = -0x1.ffffef20a4123p-2;
+    const uint32_t tmp = ix - 0x3f330000u;
+    const int i = (int)((tmp >> 19) % 16u);
+    const int k = (int32_t)tmp >> 23;
+    const uint32_t iz = ix - (tmp & (0x1ffu << 23));
+    const double z = (double)__uint_as_float(iz);
+    const double r = __builtin_fma(z, kLogfTable[i][0], -1.0);
+    const double y0 = kLogfTable[i][1] + (double)k * ln2;
+    const double r2 = r * r;
+    double y = a1 * r + a2;
+    y = a0 * r2 + y;
+    y = y * r2 + (y0 + r);
+    return (float)y;
+}
+
 // ops.rs:112-118 per element: round half to even, clamp to [-128, 127]; NaN -> 0.
 __device__ __forceinline__ int quantise_one(float value, float scale) {
     float q = __builtin_rintf(value / scale);

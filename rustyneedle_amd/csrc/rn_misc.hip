@@ -79,7 +79,8 @@ __global__ void fast_exp_kernel(const float* x, float* y, int n, int op) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const float v = x[i];
-    y[i] = op == 0 ? fast_exp(v) : op == 1 ? silu(v) : op == 2 ? libm_expf(v) : libm_sigmoid(v);
+    y[i] = op == 0 ? fast_exp(v) : op == 1 ? silu(v) : op == 2 ? libm_expf(v) : op == 3 ? libm_sigmoid(v)
+                                                                                   : libm_logf(v);
 }
 
 hipError_t launch_norm_rows(const float* x, const float* gain, int count, int n, float eps, float* out,
@@ -119,7 +120,7 @@ hipError_t launch_set_state(DecodeState* state, uint32_t token, int32_t pos, uin
 
 hipError_t launch_fast_exp(const float* x, float* y, int n, int op, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    if (op < 0 || op > 3) return hipErrorInvalidValue;
+    if (op < 0 || op > 4) return hipErrorInvalidValue;
     rn_launch(fast_exp_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, y, n, op);
     return hipGetLastError();
 }

@@ -856,7 +856,7 @@ __global__ __launch_bounds__(256) void log_mel_kernel(FrontendParams p, const fl
     for (int m = tid; m < p.mels; m += 256) {
         float row = 0.0f;
         for (int bin = 0; bin < bins; ++bin) row = row + power[bin] * p.mel_weights[(size_t)bin * p.mels + m];
-        data[(size_t)frame * p.mels + m] = logf(row + 5.9604645e-8f);  // FLOOR, frontend.rs:3
+        data[(size_t)frame * p.mels + m] = libm_logf(row + 5.9604645e-8f);  // FLOOR, frontend.rs:3
     }
 }
 
