@@ -739,6 +739,7 @@ lib.ro_n3_session_free.argtypes = [_p]
 lib.ro_n3_session_clone.restype = C.c_int
 lib.ro_n3_session_clone.argtypes = [_p, C.POINTER(_p)]
 lib.ro_n3_push.argtypes = [_p, C.c_uint32]
+lib.ro_n3_feed.argtypes = [_p, _p, _i]
 lib.ro_n3_logits.argtypes = [_p, _p]
 lib.ro_n3_pooled_readout.restype = C.c_int
 lib.ro_n3_pooled_readout.argtypes = [_p, C.c_int, _p]
@@ -803,8 +804,15 @@ class OracleNeedle3Session:
         lib.ro_n3_push(self.handle, int(token))
 
     def feed(self, tokens) -> None:
-        for t in tokens:
-            self.push(int(t))
+        """Session::feed (session.rs:56-70): chunks of 128 as prefills (the
+        projections and engram products through multiply_batch, which for 1-
+        and 3-bit matrices is the float tile), a short last chunk pushed; with
+        integer-path matrices equal to pushing every token."""
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).ravel())
+        if len(self) + t.size > self.capacity:
+            raise ValueError("session is full")
+        if t.size:
+            lib.ro_n3_feed(self.handle, _ptr(t), t.size)
 
     def greedy(self, first: int, steps: int) -> np.ndarray:
         """generator.rs:199-230 without grammar: push, logits, argmax (generator.rs:257-265)."""

@@ -125,6 +125,21 @@ void ro_cbm_rows(const ro_cbm* m, int first, int n, const float* rotated, float*
     }
 }
 
+/* The product of one token's rotated input as a batched prefill computes it:
+ * QuantisedMatrix::multiply_batch (matrix.rs:330-389) takes the integer paths
+ * of fill_rows for 2-, 4-bit and ternary matrices, and for the others the float
+ * tile (expand_row_scaled, then the eight-lane dot), whose result for a token
+ * does not depend on the other tokens of the batch. With batch == 0 this is
+ * ro_cbm_rows (multiply_vector / multiply_fused). */
+static void cbm_rows_as(const ro_cbm* m, int first, int n, const float* rotated, float* y, int batch) {
+    if (batch && !m->integer) {
+        ro_codebook_float_batch(m->packed + (size_t)first * m->row_bytes, m->norms + (size_t)first * m->groups, n,
+                                m->padded, m->group, m->bits, m->levels, rotated, 1, y);
+        return;
+    }
+    ro_cbm_rows(m, first, n, rotated, y);
+}
+
 void ro_cbm_dequantise_row(const ro_cbm* m, int row, float* out) {
     ro_codebook_dequantise_row(m->packed, m->norms, m->padded, m->columns, m->group, m->bits, m->levels, row, out);
 }
@@ -752,7 +767,8 @@ int ro_n3_session_clone(const ro_n3_session* s, ro_n3_session** out) {
 }
 
 /* engram.rs:66-112: contribute for one site */
-static void engram_contribute(ro_n3_session* s, int site, const int* indices, int position, float* key, float* value) {
+static void engram_contribute(ro_n3_session* s, int site, const int* indices, int position, float* key, float* value,
+                              int batch) {
     const ro_n3_model* m = s->m;
     const ro_n3_config* c = &m->config;
     const ro_n3_engram* g = &m->engrams[site];
@@ -771,8 +787,8 @@ static void engram_contribute(ro_n3_session* s, int site, const int* indices, in
     ro_cbm_prepare(&g->key, gathered, rotated);
     const int width = g->value.rows;
     float* raw = fbuf((size_t)width);
-    ro_cbm_rows(&g->key, 0, g->key.rows, rotated, key);
-    ro_cbm_rows(&g->value, 0, width, rotated, raw);
+    cbm_rows_as(&g->key, 0, g->key.rows, rotated, key, batch);    /* engram.rs:84 / contribute_batch :134-136 */
+    cbm_rows_as(&g->value, 0, width, rotated, raw, batch);
     const int keep = (c->engram_conv_taps - 1) * c->engram_dilation + 1;
     float* hist = s->engram_history[site];
     memmove(hist + width, hist, sizeof(float) * (size_t)(keep - 1) * width);
@@ -824,7 +840,7 @@ static void apply_rotary_at(const ro_n3_session* s, float* head, int qk, int pos
 }
 
 /* attention.rs:96-154 */
-static void attend(ro_n3_session* s, int layer, int position, const float* hidden, float* output) {
+static void attend(ro_n3_session* s, int layer, int position, const float* hidden, float* output, int batch) {
     const ro_n3_model* m = s->m;
     const ro_n3_config* c = &m->config;
     const ro_n3_layer* y = &m->layers[layer];
@@ -840,10 +856,11 @@ static void attend(ro_n3_session* s, int layer, int position, const float* hidde
     float* k = fbuf((size_t)kw);
     float* v = fbuf((size_t)vw);
     float* gate = fbuf((size_t)aw);
-    ro_cbm_rows(&y->q, 0, qw, rotated, q);
-    ro_cbm_rows(&y->k, 0, kw, rotated, k);
-    ro_cbm_rows(&y->v, 0, vw, rotated, v);
-    ro_cbm_rows(&y->gate, 0, aw, rotated, gate);
+    /* attention.rs:107-110 (multiply_fused) / attend_batch :233-240 (multiply_batch_fused) */
+    cbm_rows_as(&y->q, 0, qw, rotated, q, batch);
+    cbm_rows_as(&y->k, 0, kw, rotated, k, batch);
+    cbm_rows_as(&y->v, 0, vw, rotated, v, batch);
+    cbm_rows_as(&y->gate, 0, aw, rotated, gate, batch);
     if (c->conv_taps > 0) {
         float* h = cache->history;
         memmove(h + qkv, h, sizeof(float) * (size_t)(c->conv_taps - 1) * qkv);
@@ -895,7 +912,7 @@ static void attend(ro_n3_session* s, int layer, int position, const float* hidde
     ro_fake_quantise_int8(attended, aw);
     float* rotated_out = fbuf((size_t)y->out.padded);
     ro_cbm_prepare(&y->out, attended, rotated_out);
-    ro_cbm_rows(&y->out, 0, y->out.rows, rotated_out, output);
+    cbm_rows_as(&y->out, 0, y->out.rows, rotated_out, output, batch); /* attention.rs:152 / :359-366 */
     free(rotated_out);
     free(attended);
     free(qscales);
@@ -934,7 +951,10 @@ static void heads_observe(ro_n3_session* s) {
 }
 
 /* session.rs:76-148 */
-void ro_n3_push(ro_n3_session* s, uint32_t token) {
+/* One token of Session::push (batch == 0) or of Session::prefill (batch == 1):
+ * prefill.rs:10-99 runs the same per-token arithmetic as push_with except that
+ * the projections and the engram key and value go through multiply_batch. */
+static void n3_token(ro_n3_session* s, uint32_t token, int batch) {
     const ro_n3_model* m = s->m;
     const ro_n3_config* c = &m->config;
     const int d = c->d_model, lanes = c->lanes;
@@ -961,7 +981,7 @@ void ro_n3_push(ro_n3_session* s, uint32_t token) {
         if (!present) continue;
         ekey[e] = fbuf((size_t)m->engrams[e].key.rows);
         evalue[e] = fbuf((size_t)m->engrams[e].value.rows);
-        engram_contribute(s, e, indices, position, ekey[e], evalue[e]);
+        engram_contribute(s, e, indices, position, ekey[e], evalue[e], batch);
     }
 
     const int phi_padded = m->phi_pre.padded;
@@ -995,7 +1015,7 @@ void ro_n3_push(ro_n3_session* s, uint32_t token) {
                 break;
             }
         ro_zero_centred_norm(x, y->norm_in, d, normed);
-        attend(s, layer, position, normed, attended);
+        attend(s, layer, position, normed, attended, batch);
         norm_in_place(attended, y->post_norm, d);
         const float gate = libm_sigmoid(y->attention_gate);
         for (int i = 0; i < d; ++i) x[i] = x[i] + gate * attended[i];
@@ -1049,6 +1069,23 @@ void ro_n3_logits(const ro_n3_session* s, float* logits) {
     ro_cbm_rows(&m->embedding, 0, m->config.output_vocab, rotated, logits);
     free(rotated);
     free(q);
+}
+
+void ro_n3_push(ro_n3_session* s, uint32_t token) { n3_token(s, token, 0); }
+
+/* Session::feed (session.rs:56-70): at least BATCH_THRESHOLD (4) tokens go in
+ * chunks of PREFILL_CHUNK (128), each chunk of at least 4 as a prefill, a
+ * shorter last chunk pushed; fewer than 4 tokens are pushed. */
+void ro_n3_feed(ro_n3_session* s, const uint32_t* tokens, int count) {
+    const int threshold = 4, chunk = 128;
+    if (count < threshold) {
+        for (int i = 0; i < count; ++i) n3_token(s, tokens[i], 0);
+        return;
+    }
+    for (int i = 0; i < count; i += chunk) {
+        const int n = count - i < chunk ? count - i : chunk;
+        for (int j = 0; j < n; ++j) n3_token(s, tokens[i + j], n >= threshold);
+    }
 }
 
 static int head_index(const ro_n3_model* m, int code) {

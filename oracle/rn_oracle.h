@@ -358,6 +358,7 @@ int ro_n3_session_new(const ro_n3_model* m, int capacity, ro_n3_session** out);
 void ro_n3_session_free(ro_n3_session* s);
 int ro_n3_session_clone(const ro_n3_session* s, ro_n3_session** out);              /* session.rs:17 */
 void ro_n3_push(ro_n3_session* s, uint32_t token);                                  /* session.rs:76-148 */
+void ro_n3_feed(ro_n3_session* s, const uint32_t* tokens, int count);               /* session.rs:56-70 */
 void ro_n3_logits(const ro_n3_session* s, float* logits);                           /* session.rs:151-165 */
 int ro_n3_pooled_readout(const ro_n3_session* s, int code, float* pooled);          /* heads.rs:99-125 */
 int ro_n3_head_output(const ro_n3_session* s, int code, float* out);                /* heads.rs:127-136 */

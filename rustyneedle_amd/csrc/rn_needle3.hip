@@ -2559,10 +2559,12 @@ int n3_out_loads(int row_bytes) {
     return l;
 }
 
-// The three-kernel step needs integer-path formats whose rows start where the
-// reference takes the panel form (2-bit rows on panels of four), at most four
-// lanes, and rows that fit its LDS tiles.
-bool fused_applies(const rn_n3_model* m) {
+// The layer boundary kernel (tail, routing, block input) applies: integer-path
+// routing matrices whose rows start where the reference takes the panel form
+// (2-bit rows on panels of four), at most four lanes, vectors that fit its LDS
+// staging, and a stacked q/k/v/gate matrix whose prepared input fits it. The
+// batched feed needs this much; its products take either path.
+bool boundary_applies(const rn_n3_model* m) {
     const rn_geometry& g = m->g;
     const int L = (int)g.mhc_lanes;
     if (2 * L + L * L > kN3RouteRows || g.d_model > (uint32_t)kN3Hadamard) return false;
@@ -2594,11 +2596,21 @@ bool fused_applies(const rn_n3_model* m) {
         for (int f = 0; f < 6; ++f)
             if (!aligned(y.factors[f])) return false;
         if (y.rank == 8 && !aligned(y.cond_v)) return false;
+        if (y.qkvg->group > 256 || y.qkvg->cb.padded > kN3Hadamard) return false;
+    }
+    return true;
+}
+
+// The three-kernel step of a push needs, beyond the boundary kernel, the
+// attention and output kernels' formats: integer-path projections whose rows
+// fit their LDS tiles.
+bool fused_applies(const rn_n3_model* m) {
+    if (!boundary_applies(m)) return false;
+    auto aligned = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+    for (const N3Layer& y : m->layers) {
         if (!aligned(y.out->cb.packed) || !aligned(y.out->cb.norms) || !aligned(y.qkvg->cb.packed)) return false;
-        if (y.qkvg->group > 256 || y.out->group > 256) return false;
-        if (y.qkvg == nullptr || !integer_path(y.qkvg) || y.qkvg->cb.padded > kN3Hadamard ||
-            y.qkvg->cb.row_bytes > kN3HeadRowBytes)
-            return false;
+        if (y.out->group > 256) return false;
+        if (!integer_path(y.qkvg) || y.qkvg->cb.row_bytes > kN3HeadRowBytes) return false;
         if (!integer_path(y.out) || y.out->cb.padded > kN3MaxWidth || y.out->cb.row_bytes > kN3OutRowBytes ||
             y.out->cb.padded / y.out->group > 64 || y.out->cb.row_bytes % 16 != 0)
             return false;
@@ -2822,7 +2834,9 @@ int rn_n3_model_open(const rn_archive* archive, int depth, rn_n3_model** out) {
         }
         if (w.failed) return n3_fail(RN_ERR_ARGUMENT, "directory ends inside the probe heads");
         m->fused = fused_applies(m);
-        if (m->fused) N3_CALL(stack_routing_rows(m));
+        // the boundary kernel (pushes of the fused step and every batched feed)
+        // reads the routing rows from this stack
+        if (boundary_applies(m)) N3_CALL(stack_routing_rows(m));
         N3_REQUIRE(w.next == w.end, "%d tensors follow the heads (an audio encoder is not part of this model)",
                    w.end - w.next);
         return RN_OK;
@@ -3736,13 +3750,16 @@ int enqueue_run(rn_n3_session* s, const uint32_t* tokens, int count) {
     return RN_OK;
 }
 
-// A run of tokens can take the batched path: the one-launch boundary, integer
-// projections, and vectors on 16-byte boundaries.
+// A run of tokens can take the batched path: the one-launch boundary and
+// vectors on 16-byte boundaries (its products take either path, so float-path
+// projections run it too); RN_N3_PATH=stepwise keeps every token a push.
 bool run_applies(const rn_n3_session* s) {
     const rn_n3_model* m = s->m;
     const rn_geometry& g = m->g;
     const int d = (int)g.d_model;
-    if (!s->fused || d % 4 != 0) return false;
+    const char* path = getenv("RN_N3_PATH");
+    if ((path && strcmp(path, "stepwise") == 0) || !boundary_applies(m) || m->phi_stack == nullptr || d % 4 != 0)
+        return false;
     for (const N3Head& h : m->heads)
         if (h.width != d) return false;
     const int gathered = (int)(g.engram_order_count * heads_per_order(g) * g.engram_sub_dim);
@@ -3893,20 +3910,29 @@ int rn_n3_session_choose_allowed(rn_n3_session* s, const uint8_t* allowed, rn_ch
 // are pushed. With integer-path engram matrices the batched prefill runs each
 // token's arithmetic as a push does, so the chunk size changes nothing but
 // speed, and runs take up to kN3FeedChunk tokens (RN_N3_FEED_CHUNK, 4..256,
-// sets it). A 1- or 3-bit engram key or value matrix takes the float path,
-// whose batch tile (multiply_batch, matrix.rs:330-389) rounds differently from
-// its vector path: then the chunks are the reference's PREFILL_CHUNK of 128
-// (session.rs:11), so that the same tokens run batched and pushed as there.
+// sets it). A 1- or 3-bit projection, engram key or engram value matrix takes
+// the float path, whose batch tile (multiply_batch, matrix.rs:330-389) rounds
+// differently from its vector path: then the chunks are the reference's
+// PREFILL_CHUNK of 128 (session.rs:11), so that the same tokens run batched
+// and pushed as there.
 int rn_n3_session_feed(rn_n3_session* s, const uint32_t* tokens, int count) {
     constexpr int kBatchThreshold = 4, kPrefillChunk = 128;
     N3_REQUIRE(s && (tokens || count == 0), "null argument");
     N3_REQUIRE(count >= 0 && s->length + count <= s->capacity, "feed of %d tokens overflows the capacity", count);
     for (int i = 0; i < count; ++i) N3_REQUIRE(tokens[i] < s->m->g.vocab, "token %u outside the vocabulary", tokens[i]);
-    bool float_engram = false;
-    for (const N3Engram& e : s->m->engrams) float_engram |= !integer_path(e.key) || !integer_path(e.value);
-    int chunk = float_engram ? kPrefillChunk : kN3FeedChunk;
+    // the products whose batch arithmetic differs from their vector arithmetic
+    // (1- and 3-bit matrices: multiply_batch's float tile, matrix.rs:356-378):
+    // the projections (attend_batch) and the engram key and value
+    // (contribute_batch); then the runs are the reference's chunks
+    bool float_batch = false;
+    for (const N3Engram& e : s->m->engrams) float_batch |= !integer_path(e.key) || !integer_path(e.value);
+    for (int layer : s->m->active) {
+        const N3Layer& y = s->m->layers[(size_t)layer];
+        float_batch |= !integer_path(y.out) || (y.qkvg != nullptr && !integer_path(y.qkvg));
+    }
+    int chunk = float_batch ? kPrefillChunk : kN3FeedChunk;
     if (const char* e = getenv("RN_N3_FEED_CHUNK"))
-        if (!float_engram) chunk = std::min(kN3FeedChunk, std::max(kBatchThreshold, atoi(e)));
+        if (!float_batch) chunk = std::min(kN3FeedChunk, std::max(kBatchThreshold, atoi(e)));
     if (count < kBatchThreshold || !run_applies(s)) {
         for (int i = 0; i < count; ++i) N3_CALL(rn_n3_session_push(s, tokens[i]));
         return RN_OK;

@@ -41,9 +41,11 @@ BITS = dict(embedding=4, projection=2, lanes=2, tables=4, engram=2, probes=4, he
 KIND_HALF, KIND_SINGLE, KIND_CODEBOOK, KIND_RAW = 1, 2, 3, 4
 
 
-def synthetic_archive(geometry: dict, seed: int = 20261202) -> bytes:
+def synthetic_archive(geometry: dict, seed: int = 20261202, bits: Optional[dict] = None) -> bytes:
     """A .cact archive of the Needle 3 layout with seeded synthetic weights.
-    geometry["heads"] lists (code, probes_per_layer, queries, projection_rows)."""
+    geometry["heads"] lists (code, probes_per_layer, queries, projection_rows);
+    bits (default BITS) gives the width of each matrix kind."""
+    BITS = globals()["BITS"] if bits is None else bits
     g = dict(geometry)
     d, L, lanes, size = g["d_model"], g["num_layers"], g["mhc_lanes"], g["hada_n"]
     qk, vd, H, KV = g["qk_head_dim"], g["v_head_dim"], g["num_heads"], g["num_kv_heads"]

@@ -236,3 +236,30 @@ def test_choose_allowed_on_the_session(archive):
         gs.push(got[0])
         os_.push(want[0])
     _compare_all(gs, os_, gm, "after constrained steps")
+
+
+@pytest.mark.parametrize("path", ["fused"], indirect=True)
+def test_float_path_projections_feed_as_the_reference_prefills(path):
+    """3-bit projections and engram matrices take the float path, whose batch
+    tile (multiply_batch, matrix.rs:356-378) rounds differently from a push's
+    vector product (test_needle3_oracle.py shows the oracle's feed and pushes
+    differ there). Feeds of 21 tokens (a prefill), 2 (pushes) and 130 (a
+    prefill of 128, then 2 pushes: the reference's PREFILL_CHUNK,
+    session.rs:11, 56-70) run the batched path with the batch arithmetic and
+    match the oracle's prefill-faithful feed bit for bit after each; then
+    pushes and greedy tokens from the fed state."""
+    bits = dict(needle3.BITS, projection=3, engram=3)
+    archive = needle3.synthetic_archive(GEOMETRY, bits=bits)
+    gm, om = needle3.Model(archive), oracle.OracleNeedle3(archive)
+    gs, os_ = gm.session(200), om.session(200)
+    tokens = _tokens(153, seed=47)
+    for a, b in ((0, 21), (21, 23), (23, 153)):
+        print(f"needle3 3-bit projections: feed of tokens {a}..{b}", flush=True)
+        gs.feed(tokens[a:b])
+        os_.feed(tokens[a:b])
+        _compare_all(gs, os_, gm, f"3-bit after {b}")
+    for t in (5, 77):
+        gs.push(t)
+        os_.push(t)
+    assert gs.decode_greedy(9, 4).tolist() == os_.greedy(9, 4).tolist()
+    _compare_all(gs, os_, gm, "3-bit after pushes and greedy tokens")

@@ -278,3 +278,29 @@ def test_loading_errors(archive):
     with pytest.raises(ValueError):
         oracle.OracleNeedle3(archive[:-200])
     assert oracle.OracleNeedle3(archive, depth=2).active == [0, 3]
+
+
+def test_prefill_of_float_path_matrices_differs_from_pushes():
+    """Session::feed runs chunks of at least four tokens as prefills
+    (session.rs:56-70), whose projections and engram products go through
+    multiply_batch; for 1- and 3-bit matrices that is the float tile
+    (matrix.rs:356-378), which rounds differently from the vector product of a
+    push. With 3-bit projections and engram matrices the oracle's feed must
+    therefore differ from pushing the same tokens, while with the default
+    (2-bit) layout the two are equal bit for bit; a feed of fewer than four
+    tokens is pushes in both."""
+    from rustyneedle_amd import needle3
+    tokens = rn.synth_tokens(3, "needle3.tokens", needle3.NEEDLE3_SMALL["vocab"], (21,))
+    for bits, differs in ((dict(needle3.BITS, projection=3, engram=3), True), (needle3.BITS, False)):
+        om = oracle.OracleNeedle3(needle3.synthetic_archive(needle3.NEEDLE3_SMALL, bits=bits))
+        fed, pushed = om.session(64), om.session(64)
+        fed.feed(tokens)
+        for t in tokens:
+            pushed.push(int(t))
+        same = np.array_equal(fed.logits().view(np.uint32), pushed.logits().view(np.uint32))
+        assert same != differs, bits
+        short_fed, short_pushed = om.session(8), om.session(8)
+        short_fed.feed(tokens[:3])
+        for t in tokens[:3]:
+            short_pushed.push(int(t))
+        assert np.array_equal(short_fed.hidden().view(np.uint32), short_pushed.hidden().view(np.uint32))
