@@ -116,6 +116,13 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
         sw_s[c][g] = p.sW[(size_t)min(column(c), p.N - 1) * G + g];
     }
     if (AIN == kRowsCodes && threadIdx.x < BM) sx_s[threadIdx.x] = p.sx[min(m0 + (int)threadIdx.x, p.M - 1)];
+    // the residual add's current value of this thread's output, requested now
+    // rather than after the group chain (each output belongs to one thread)
+    float residual_in = 0.0f;
+    if constexpr (EPI == kGemmResidual) {
+        const int rr = min((int)threadIdx.x / BN, BM - 1), cc = (int)threadIdx.x - ((int)threadIdx.x / BN) * BN;
+        residual_in = p.Y[(size_t)min(m0 + rr, p.M - 1) * p.ldy + min(column(cc), p.N - 1)];
+    }
 #pragma unroll
     for (int q = 0; q < (kPieces + 1023) / 1024; ++q) {
         const int i = kFirst + threadIdx.x + 1024 * q;
@@ -238,7 +245,7 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
         if (m < p.M && n < p.N) {
             float* dst = p.Y + (size_t)m * p.ldy + n;
             if constexpr (EPI == kGemmResidual)
-                *dst = *dst + total;
+                *dst = residual_in + total;
             else if constexpr (EPI == kGemmStoreSilu)
                 *dst = silu(total);  // stem.rs:76,99: silu after the stage
             else

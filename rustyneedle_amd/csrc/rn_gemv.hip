@@ -117,13 +117,20 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int j = 0; j < NL; ++j)
         w[j] = *reinterpret_cast<const int4*>(sg.W + (size_t)row_load(load_row(j)) * K + load_chunk(j) * 16);
-    // 1c. lane r < ROWS holds the G scales of its row
+    // 1c. lane r < ROWS holds the G scales of its row, and for the residual
+    // add the row's current value, requested now rather than after the
+    // epilogue (each row belongs to one block, which reads it before writing it)
     float4 sv[G / 4];
     const bool mine = lane < ROWS && row_valid(lane);
     {
         const float4* src = reinterpret_cast<const float4*>(sg.sW + (size_t)row_load(min(lane, ROWS - 1)) * G);
 #pragma unroll
         for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
+    }
+    float residual_in = 0.0f;
+    if constexpr (EPI == kResidual) {
+        const int rr = row_load(min(lane, ROWS - 1));
+        residual_in = p.res != nullptr ? p.res[rr] : sg.y[rr];
     }
     // keep the scheduler from sinking those loads below the prologue
     __builtin_amdgcn_sched_barrier(0);
@@ -235,10 +242,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     if constexpr (EPI == kStore) {
         if (mine) sg.y[row_of(lane)] = total;
     } else if constexpr (EPI == kResidual) {
-        if (mine) {
-            const int r = row_of(lane);
-            sg.y[r] = (p.res != nullptr ? p.res[r] : sg.y[r]) + total;
-        }
+        if (mine) sg.y[row_of(lane)] = residual_in + total;
     } else if constexpr (EPI == kSilu) {
         const float up = lane_xor<H>(total);  // lane + H for the lanes below H (DPP / lane swap)
         if (lane < H && mine) sg.y[blk * H + lane] = silu(total) * up;
@@ -294,11 +298,14 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
                                               load_chunk(j) * 16);
     const bool mine = wave == 0 && lane < ROWS && r0 + lane < sg.rows;
     float4 sv[G / 4];
+    float residual_in = 0.0f;  // the row's current value, requested with the other loads
     {
-        const float4* src = reinterpret_cast<const float4*>(sg.sW + (size_t)min(r0 + min(lane, ROWS - 1), sg.rows - 1) * G);
+        const int rr = min(r0 + min(lane, ROWS - 1), sg.rows - 1);
+        const float4* src = reinterpret_cast<const float4*>(sg.sW + (size_t)rr * G);
         if (wave == 0) {
 #pragma unroll
             for (int i = 0; i < G / 4; ++i) sv[i] = src[i];
+            residual_in = p.res != nullptr ? p.res[rr] : sg.y[rr];
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -344,8 +351,7 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
                     total = total + (a[k] * s[k]) * sx;    // neon.rs:180
             }
         }
-        const int r = r0 + lane;
-        sg.y[r] = (p.res != nullptr ? p.res[r] : sg.y[r]) + total;
+        sg.y[r0 + lane] = residual_in + total;
     }
 }
 
