@@ -64,8 +64,8 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
     __shared__ float sw_s[BN][G + 1];
     __shared__ float sx_s[BM];
     __shared__ float tile[kSilu ? BM : 1][kSilu ? BN + 1 : 1];
-    // kRowsNormQuant: a wave's squares, run r (elements e = r mod 8) at r * (K / 8 + 1)
-    __shared__ float sq_s[AIN == kRowsNormQuant ? 16 : 1][AIN == kRowsNormQuant ? K + 8 : 1];
+    // kRowsNormQuant: a wave's squares, run r (elements e = r mod 8) at r * (K / 8 + 4)
+    __shared__ __align__(16) float sq_s[AIN == kRowsNormQuant ? 16 : 1][AIN == kRowsNormQuant ? K + 32 : 1];
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int mtiles = (p.M + BM - 1) / BM;
@@ -84,6 +84,10 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
         for (int rr = 0; rr < RPW; ++rr)
             load_floats<E>(p.Xf + (size_t)min(m0 + wave + 16 * rr, p.M - 1) * K + lane * E, xv[rr]);
     }
+    // the norm gains, requested with the rows (not after them: that load
+    // would then start only when the rows had arrived)
+    float gv[AIN == kRowsNormQuant ? E : 1];
+    if constexpr (AIN == kRowsNormQuant) load_floats<E>(p.gain + lane * E, gv);
 
     // output column of local column c (silu: first BN/2 gate rows, then the up rows)
     auto column = [&](int c) -> int {
@@ -142,27 +146,36 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
                 // the ordered 8-run sum of squares of norm_quantise_kernel (ops.rs:7-17),
                 // the gained values m = (1 + g) x and their peak beside it; the normed
                 // peak is fl(peak(|m|) * inverse) (rounding is monotone, inverse > 0)
-                constexpr int run = K / 8;
+                // (runs padded by four floats: 16-byte reads, and the eight
+                // summing lanes start on banks 4 apart)
+                constexpr int run = K / 8, stride = run + 4;
                 float* sq = sq_s[wave];
 #pragma unroll
                 for (int e = 0; e < E; ++e) {
                     const int ge = lane * E + e;
-                    sq[(ge & 7) * (run + 1) + (ge >> 3)] = v[e] * v[e];
+                    sq[(ge & 7) * stride + (ge >> 3)] = v[e] * v[e];
                 }
-                float g[E];
-                load_floats<E>(p.gain + lane * E, g);
 #pragma unroll
                 for (int e = 0; e < E; ++e) {
-                    v[e] = (1.0f + g[e]) * v[e];
+                    v[e] = (1.0f + gv[e]) * v[e];
                     peak = fmaxf(peak, fabsf(v[e]));
                 }
                 peak = wave_max(peak);
-                __syncthreads();
+                // a wave's own squares: DS operations of a wave complete in order
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 float part = 0.0f;
                 if (lane < 8) {
-                    const float* r = sq + lane * (run + 1);
-#pragma unroll 16
-                    for (int c = 0; c < run; ++c) part = part + r[c];
+                    const float4* r = reinterpret_cast<const float4*>(sq + lane * stride);
+#pragma unroll
+                    for (int c = 0; c < run / 4; ++c) {
+                        const float4 t = r[c];
+                        part = part + t.x;
+                        part = part + t.y;
+                        part = part + t.z;
+                        part = part + t.w;
+                    }
                 }
                 float total = sum_lanes_0_to_7(part);
                 total = total + 0.0f;  // the empty tail of the 8-lane sum
