@@ -114,10 +114,14 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
             piece[q] = *reinterpret_cast<const v4i*>(src + 16 * col);
         }
     }
-    // scales of the tile's columns and rows
-    for (int i = threadIdx.x; i < BN * G; i += 1024) {
-        const int c = i / G, g = i - c * G;
-        sw_s[c][g] = p.sW[(size_t)min(column(c), p.N - 1) * G + g];
+    // scales of the tile's columns (into registers; stored to LDS after the
+    // token rows are quantised, so that no wave waits for them before that)
+    constexpr int kScaleLoads = (BN * G + 1023) / 1024;
+    float swv[kScaleLoads];
+#pragma unroll
+    for (int q = 0; q < kScaleLoads; ++q) {
+        const int i = min((int)threadIdx.x + 1024 * q, BN * G - 1), c = i / G, g = i - c * G;
+        swv[q] = p.sW[(size_t)min(column(c), p.N - 1) * G + g];
     }
     if (AIN == kRowsCodes && threadIdx.x < BM) sx_s[threadIdx.x] = p.sx[min(m0 + (int)threadIdx.x, p.M - 1)];
     // the residual add's current value of this thread's output, requested now
@@ -127,14 +131,24 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
         const int rr = min((int)threadIdx.x / BN, BM - 1), cc = (int)threadIdx.x - ((int)threadIdx.x / BN) * BN;
         residual_in = p.Y[(size_t)min(m0 + rr, p.M - 1) * p.ldy + min(column(cc), p.N - 1)];
     }
+    // the operand pieces and scales into LDS: for float token rows after their
+    // quantisation below (which waits only for the rows), else now
+    auto store_pieces = [&]() {
 #pragma unroll
-    for (int q = 0; q < (kPieces + 1023) / 1024; ++q) {
-        const int i = kFirst + threadIdx.x + 1024 * q;
-        if (kPieces % 1024 == 0 || i < kFirst + kPieces) {
-            const int row = i / kRow16, col = i - row * kRow16;
-            *reinterpret_cast<v4i*>(&a_s[0][0] + (size_t)row * KP + 16 * col) = piece[q];
+        for (int q = 0; q < (kPieces + 1023) / 1024; ++q) {
+            const int i = kFirst + threadIdx.x + 1024 * q;
+            if (kPieces % 1024 == 0 || i < kFirst + kPieces) {
+                const int row = i / kRow16, col = i - row * kRow16;
+                *reinterpret_cast<v4i*>(&a_s[0][0] + (size_t)row * KP + 16 * col) = piece[q];
+            }
         }
-    }
+#pragma unroll
+        for (int q = 0; q < kScaleLoads; ++q) {
+            const int i = (int)threadIdx.x + 1024 * q;
+            if (i < BN * G) sw_s[i / G][i % G] = swv[q];
+        }
+    };
+    if constexpr (AIN == kRowsCodes) store_pieces();
     if constexpr (AIN != kRowsCodes) {
         // the token rows' codes and scales, one wave per row
 #pragma unroll
@@ -200,6 +214,7 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
             }
             if (lane == 0) sx_s[row] = scale;
         }
+        store_pieces();
     }
     __syncthreads();
 
