@@ -57,15 +57,16 @@ __device__ __forceinline__ void unpack_values(const typename ValuePiece<DPV>::T&
 // the last two across lanes (xor 1, xor 2; the four lanes of a row are one
 // DPP quad).
 __device__ __forceinline__ float score_row(const float* q16, const uint4& ka, const uint4& kb) {
-    float k[16];
-    unpack8(ka, k);
-    unpack8(kb, k + 8);
+    // dims 2w and 2w + 1 are the low and high halves of word w
+    const uint32_t w[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
     float part[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = s + q16[4 * j + i] * k[4 * j + i];
+        s = s + mul_f16<false>(q16[4 * j], w[2 * j]);
+        s = s + mul_f16<true>(q16[4 * j + 1], w[2 * j]);
+        s = s + mul_f16<false>(q16[4 * j + 2], w[2 * j + 1]);
+        s = s + mul_f16<true>(q16[4 * j + 3], w[2 * j + 1]);
         part[j] = s;
     }
     float s = (part[0] + part[1]) + (part[2] + part[3]);
@@ -294,11 +295,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 512 ? 
             if (base + kClasses * c + (64 / TPC) * wave >= nglobal) continue;
             const bool ok = pp < nglobal;
             const float e = scores[min(pp, last)];
-            float vv[DPV];
-            unpack_values<DPV>(vr[c], vv);
+            const uint32_t* vw = reinterpret_cast<const uint32_t*>(&vr[c]);
 #pragma unroll
             for (int i = 0; i < DPV; ++i) {
-                const float t = acc[i] + e * vv[i];
+                const float t = acc[i] + ((i & 1) ? mul_f16<true>(e, vw[i / 2]) : mul_f16<false>(e, vw[i / 2]));
                 acc[i] = ok ? t : acc[i];
             }
             const float tt = total + e;
@@ -885,12 +885,11 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
             const int pp = base + j + kClasses * c;
             const bool ok = pp < nglobal;
             const float e = scores[min(pp, last)];
-            const __half2 h01 = *reinterpret_cast<const __half2*>(&vr[c].x);
-            const __half2 h23 = *reinterpret_cast<const __half2*>(&vr[c].y);
-            const float vv[4] = {__low2float(h01), __high2float(h01), __low2float(h23), __high2float(h23)};
+            const float ev[4] = {mul_f16<false>(e, vr[c].x), mul_f16<true>(e, vr[c].x), mul_f16<false>(e, vr[c].y),
+                                 mul_f16<true>(e, vr[c].y)};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float t = a[i] + e * vv[i];
+                const float t = a[i] + ev[i];
                 a[i] = ok ? t : a[i];
             }
             const float tt = total + e;

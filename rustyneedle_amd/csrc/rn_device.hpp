@@ -267,6 +267,21 @@ __device__ __forceinline__ float sum_lanes_0_to_7(float s) {
     return total;
 }
 
+// x times the f16 in the low (HI false) or high half of `packed`, as one
+// v_fma_mix_f32 with a -0.0 addend instead of a conversion and a multiply.
+// The f16 operand widens exactly, and fma(x, h, -0) = RN(x h + (-0)) = RN(x h)
+// for every operand (a zero product keeps its sign: +0 + -0 = +0, -0 + -0 =
+// -0; NaN and infinities pass through), so the result is the product's bits.
+template <bool HI>
+__device__ __forceinline__ float mul_f16(float x, uint32_t packed) {
+    float d;
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(d) : "v"(x), "v"(packed), "v"(-0.0f));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(d) : "v"(x), "v"(packed), "v"(-0.0f));
+    return d;
+}
+
 // Four int8 x int8 products added to an int32 accumulator (v_dot4_i32_i8).
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
