@@ -349,6 +349,11 @@ int rn_sigmoid(const float* x, float* y, int n, void* stream);
  * features, frontend.rs:96-99), elementwise on the device; equal bit for bit to
  * this image's glibc logf on all 2^32 inputs. Exposed for parity checks. */
 int rn_libm_log(const float* x, float* y, int n, void* stream);
+/* The division-free reciprocal the fused Needle 3 step uses for the Sinkhorn
+ * normalisation (1.0f / total, ops.rs:198-217): v_rcp_f32 and one Newton step,
+ * elementwise on the device; equal to the IEEE division for every x in
+ * [2^-126, 2^126), the only inputs it is given. Exposed for that check. */
+int rn_reciprocal(const float* x, float* y, int n, void* stream);
 
 /* ops::zero_centred_norm (ops.rs:44-50) for `count` rows of `n` floats on the
  * device (n a multiple of 8, <= 4096). */

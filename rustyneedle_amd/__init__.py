@@ -179,6 +179,7 @@ SIGNATURES = {
     "rn_libm_exp": (_i, [_p, _p, _i, _p]),
     "rn_sigmoid": (_i, [_p, _p, _i, _p]),
     "rn_libm_log": (_i, [_p, _p, _i, _p]),
+    "rn_reciprocal": (_i, [_p, _p, _i, _p]),
     "rn_zero_centred_norm": (_i, [_p, _p, _i, _i, _p, _p]),
     "rn_attend_heads": (_i, [_p, _p, _p, _p, _i, _i, _i, _p, _p]),
     "rn_model_create": (_i, [C.POINTER(Config), C.POINTER(WeightsHost), C.POINTER(_p)]),
@@ -626,6 +627,12 @@ def sigmoid(x: np.ndarray) -> np.ndarray:
 def libm_log(x: np.ndarray) -> np.ndarray:
     """f32::ln (the C library's logf) on the device."""
     return _elementwise(lib.rn_libm_log, x)
+
+
+def reciprocal(x: np.ndarray) -> np.ndarray:
+    """The fused step's reciprocal (v_rcp_f32 and one Newton step) on the device;
+    the IEEE 1/x for x in [2^-126, 2^126)."""
+    return _elementwise(lib.rn_reciprocal, x)
 
 
 def quantise_int8(x: np.ndarray):

@@ -719,6 +719,12 @@ int rn_libm_log(const float* x, float* y, int n, void* stream) {
     return RN_OK;
 }
 
+int rn_reciprocal(const float* x, float* y, int n, void* stream) {
+    RN_REQUIRE(x && y && n >= 0, "bad argument");
+    RN_HIP(launch_fast_exp(x, y, n, 5, (hipStream_t)stream));
+    return RN_OK;
+}
+
 int rn_zero_centred_norm(const float* x, const float* gain, int count, int n, float* out, void* stream) {
     RN_REQUIRE(x && gain && out, "null argument");
     RN_REQUIRE(n > 0 && n % 8 == 0 && n <= 4096 && count >= 0, "n must be a multiple of 8 in 8..4096");

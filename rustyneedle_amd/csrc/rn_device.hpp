@@ -170,6 +170,17 @@ __device__ __forceinline__ void quotients(const float* v, float scale, float* y)
     }
 }
 
+// 1.0f / x correctly rounded, for x in [2^-126, 2^126) (positive normal with a
+// normal reciprocal): r = v_rcp_f32(x) (within one ulp), then one Newton step
+// with fused multiply-adds, r + r (1 - x r). Equal to the IEEE division on
+// every float of that range (all 2^31 - 2^25 of them, tests/test_reciprocal.py);
+// callers keep x inside it. Three dependent operations against the division's
+// nine.
+__device__ __forceinline__ float reciprocal_normal(float x) {
+    const float r = __builtin_amdgcn_rcpf(x);
+    return __builtin_fmaf(__builtin_fmaf(-x, r, 1.0f), r, r);
+}
+
 // ops.rs:103-110: peak / 127 (1.0 when the peak is not positive). The quotient
 // is formed without a division: q0 = peak * RN(1/127), then one fma correction
 // with the exact residual peak - 127 q0; the result equals the correctly

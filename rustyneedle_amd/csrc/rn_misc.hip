@@ -80,7 +80,7 @@ __global__ void fast_exp_kernel(const float* x, float* y, int n, int op) {
     if (i >= n) return;
     const float v = x[i];
     y[i] = op == 0 ? fast_exp(v) : op == 1 ? silu(v) : op == 2 ? libm_expf(v) : op == 3 ? libm_sigmoid(v)
-                                                                                   : libm_logf(v);
+                                   : op == 4 ? libm_logf(v) : reciprocal_normal(v);
 }
 
 hipError_t launch_norm_rows(const float* x, const float* gain, int count, int n, float eps, float* out,
@@ -120,7 +120,7 @@ hipError_t launch_set_state(DecodeState* state, uint32_t token, int32_t pos, uin
 
 hipError_t launch_fast_exp(const float* x, float* y, int n, int op, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    if (op < 0 || op > 4) return hipErrorInvalidValue;
+    if (op < 0 || op > 5) return hipErrorInvalidValue;
     rn_launch(fast_exp_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, y, n, op);
     return hipGetLastError();
 }

@@ -67,6 +67,15 @@ constexpr int kN3Hadamard = 1024;     // 32 x 32
 
 namespace {
 
+// A barrier of the block for its LDS traffic: this wave's LDS operations
+// complete, then s_barrier. Unlike __syncthreads it does not wait for the
+// wave's global loads, so loads into LDS (global_load_lds) issued earlier stay
+// in flight across it; a kernel reads such data only after an explicit vmcnt
+// wait and a barrier. For code whose threads share data through LDS only.
+__device__ __forceinline__ void n3_lds_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // The maximum over the block (every thread calls; all get the result). With
 // TAIL false the caller's next barrier must come before red is written again.
 template <bool TAIL = true>
@@ -112,43 +121,51 @@ __device__ __forceinline__ float n3_fold(float s, const float* a, const float* b
     return s;
 }
 
-// 0.0 + q[0].x + q[0].y + ... in order over `count` float4 values in LDS (a
-// chain of dependent adds): the next eight values' loads are issued before
-// the current eight's adds (two register sets in turn), so the chain waits on
-// the adds and not on the LDS.
-__device__ __forceinline__ float n3_chain4(const float4* q, int count) {
-    float s = 0.0f;
-    auto add8 = [&](const float4 (&v)[8]) {
+// s + q[0].x + q[0].y + ... in order over `count` float4 values in LDS (a
+// chain of dependent adds): three register sets of four values in turn, the
+// loads of the set two ahead issued before the current set's adds, so that the
+// chain waits on the adds and not on the LDS. The loads are issued
+// unconditionally (the last set again past the end) and kept ahead of the adds
+// by a scheduling barrier; at most twelve are in flight (the LDS counter
+// holds fifteen), so the wait before a set's adds leaves the eight newer ones
+// outstanding.
+__device__ __forceinline__ float n3_chain4(const float4* q, int count, float s = 0.0f) {
+    auto add4 = [&](const float4 (&v)[4]) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 4; ++j) {
             s = s + v[j].x;
             s = s + v[j].y;
             s = s + v[j].z;
             s = s + v[j].w;
         }
     };
-    const int full = count / 8 * 8;
+    const int full = count / 4 * 4, last = full - 4;
+    auto load4 = [&](float4 (&v)[4], int k) {
+        k = min(k, last);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = q[k + j];
+        __builtin_amdgcn_sched_barrier(0);  // issued here, ahead of the adds
+    };
     if (full > 0) {
-        float4 a[8], b[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = q[j];
+        // no scalar load in flight (those return out of order and would make
+        // every wait below a full one)
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        float4 a[4], b[4], c[4];
+        load4(a, 0);
+        load4(b, 4);
         for (int k = 0;;) {
-            const bool more = k + 8 < full;
-            if (more) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) b[j] = q[k + 8 + j];
-            }
-            add8(a);
-            k += 8;
-            if (!more) break;
-            const bool more2 = k + 8 < full;
-            if (more2) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) a[j] = q[k + 8 + j];
-            }
-            add8(b);
-            k += 8;
-            if (!more2) break;
+            load4(c, k + 8);
+            add4(a);
+            k += 4;
+            if (k >= full) break;
+            load4(a, k + 8);
+            add4(b);
+            k += 4;
+            if (k >= full) break;
+            load4(b, k + 8);
+            add4(c);
+            k += 4;
+            if (k >= full) break;
         }
     }
     for (int k = full; k < count; ++k) {
@@ -175,19 +192,19 @@ __device__ float n3_sum_of_squares(const float* v, int n, float* red, float* sq 
             const float x = v[i];
             sq[(i & 7) * stride + (i >> 3)] = x * x;
         }
-        __syncthreads();
+        n3_lds_sync();
         if (tid < 8) {
             red[tid] = n3_chain4(reinterpret_cast<const float4*>(sq + tid * stride), n8 / 4);
         }
     } else if (tid < 8) {
         red[tid] = n3_fold<true>(0.0f, v + tid, nullptr, n8, 8);
     }
-    __syncthreads();
+    n3_lds_sync();
     float total = 0.0f;
     for (int j = 0; j < 8; ++j) total = total + red[j];
     float tail = -0.0f;
     for (int i = n8 * 8; i < n; ++i) tail = tail + v[i] * v[i];
-    __syncthreads();
+    n3_lds_sync();
     return total + tail;
 }
 
@@ -205,7 +222,7 @@ __device__ void n3_norm_gain(const float* x, float gain, int n, float* out, floa
     const float inverse = 1.0f / sqrtf(mean_square + 1e-6f);
     const int i = threadIdx.x;
     if (i < n) out[i] = ((1.0f + gain) * x[i]) * inverse;
-    __syncthreads();
+    n3_lds_sync();
 }
 
 // ops.rs:60-66
@@ -841,6 +858,11 @@ __device__ __forceinline__ void n3_kronecker32(const float* x, const float* left
 // LDS of the block tail: six Hadamard-sized arrays, the rank-8 condition rows
 struct N3TailLds {
     float *xs, *a, *sc, *st, *mx, *modulation, *cv, *chains, *weights, *red;
+    // a staged tail's inputs, copied into LDS: attention, x and input [3][d];
+    // the six factors [6][1024]; the stream [lanes][d]; post [kMaxLanes] and
+    // residual [kMaxLanes^2]
+    float* tin;
+    const float *factors, *stream, *lane;
 };
 
 // A thread's elementwise Hadamard tensors, read at kernel start so that their
@@ -872,15 +894,26 @@ __device__ N3TailPre n3_tail_prefetch(const N3BlockOutParams& p) {
 // the pre-Hadamard norm, HadamardWeights::apply, the block delta, the lane
 // combine and the next cell; the next stream also into `keep` (LDS) when set.
 // 1024 threads (the Hadamard size).
-__device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* keep, const N3TailPre& pre,
-                        bool staged = false) {
+// STAGED: the inputs are LDS copies (l.tin, l.factors, l.stream, l.lane; cond_v
+// of rank 8 in l.cv), read as LDS (the pointers' address space is fixed per
+// instantiation), and the factors and cond_v may still be in flight (loads
+// into LDS) until the condition products.
+template <bool STAGED>
+__device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* keep, const N3TailPre& pre) {
     float *xs = l.xs, *a = l.a, *sc = l.sc, *st = l.st, *mx = l.mx, *modulation = l.modulation;
     float *cv = l.cv, *weights = l.weights, *red = l.red;
     float(*chains)[8] = reinterpret_cast<float(*)[8]>(l.chains);
     const int tid = threadIdx.x, d = p.d;
-    if (staged) {  // attention, x and (rank 8) cond_v already in LDS: work on them in place
-        a = const_cast<float*>(p.attention);
-        xs = const_cast<float*>(p.x);
+    const float* const input = STAGED ? l.tin + 2 * d : p.input;
+    const float* const stream = STAGED ? l.stream : p.stream;
+    const float* const post = STAGED ? l.lane : p.post;
+    const float* const residual = STAGED ? l.lane + kMaxLanes : p.residual;
+    const float* factor[6];
+#pragma unroll
+    for (int f = 0; f < 6; ++f) factor[f] = STAGED ? l.factors + f * kN3Hadamard : p.factors[f];
+    if (STAGED) {  // attention, x and (rank 8) cond_v already in LDS: work on them in place
+        a = l.tin;
+        xs = l.tin + d;
     } else {
         n3_copy(a, p.attention, d);
         n3_copy(xs, p.x, d);
@@ -889,54 +922,45 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
     }
     n3_norm_gain(a, pre.post_gain, d, a, red, st);
     if (tid < d) xs[tid] = xs[tid] + p.gate * a[tid];
-    __syncthreads();
+    n3_lds_sync();
     n3_norm_gain(xs, pre.pre_gain, d, a, red, st);  // a = pre
-    if (staged) {  // the factors and cond_v, copied into LDS as the tail began
+    if (STAGED) {  // the factors and cond_v, copied into LDS as the tail began
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
     // condition weights (hadamard.rs:57-79): the products value * factor by
-    // every thread (in place over cv), then the 32 chains (lane j of rank r:
-    // rows 4k + j in order) only add
+    // every thread, stored so that each of the 32 chains (lane j of rank r:
+    // rows 4k + j in order) reads its products as consecutive float4 values
+    // (chain c = 8 j + r at c * stride floats, stride the longest chain
+    // rounded up to four, plus four where the 8192 floats of cv allow, so
+    // that the 32 chains start in different banks); the chains then only add
+    // (n3_chain4, the last values of a chain of n % 4 != 0 one at a time)
     if (p.rank == 8) {
-        for (int e = tid; e < d * 8; e += blockDim.x) cv[e] = a[e >> 3] * cv[e];
-        __syncthreads();
-        if (tid < 32) {
-            const int j = tid >> 3, r = tid & 7, n = (d - j + 3) / 4;
-            const float* q = cv + j * 8 + r;
-            // 0.0 + q[0] + q[32] + ... in order; the next sixteen loads are
-            // issued before the current sixteen adds (two register sets in turn)
-            float sum = 0.0f;
-            const int full = n / 16 * 16;
-            if (full > 0) {
-                float ta[16], tb[16];
+        const int n4 = ((d + 3) / 4 + 3) / 4 * 4, stride = min(n4 + 4, kN3Hadamard / 4);
+        float pv[8];
 #pragma unroll
-                for (int u = 0; u < 16; ++u) ta[u] = q[u * 32];
-                for (int k = 0;;) {
-                    const bool more = k + 16 < full;
-                    if (more) {
-#pragma unroll
-                        for (int u = 0; u < 16; ++u) tb[u] = q[(k + 16 + u) * 32];
-                    }
-#pragma unroll
-                    for (int u = 0; u < 16; ++u) sum = sum + ta[u];
-                    k += 16;
-                    if (!more) break;
-                    const bool more2 = k + 16 < full;
-                    if (more2) {
-#pragma unroll
-                        for (int u = 0; u < 16; ++u) ta[u] = q[(k + 16 + u) * 32];
-                    }
-#pragma unroll
-                    for (int u = 0; u < 16; ++u) sum = sum + tb[u];
-                    k += 16;
-                    if (!more2) break;
-                }
-            }
-            for (int k = full; k < n; ++k) sum = sum + q[k * 32];
-            chains[j][r] = sum;
+        for (int k = 0; k < 8; ++k) {
+            const int e = tid + k * kN3Block;
+            pv[k] = e < d * 8 ? a[e >> 3] * cv[e] : 0.0f;
         }
-        __syncthreads();
+        n3_lds_sync();
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int e = tid + k * kN3Block;
+            if (e < d * 8) {
+                const int i = e >> 3, r = e & 7;
+                cv[((i & 3) * 8 + r) * stride + (i >> 2)] = pv[k];
+            }
+        }
+        n3_lds_sync();
+        if (tid < 32) {
+            const int j = tid >> 3, n = (d - j + 3) / 4;
+            const float* q = cv + tid * stride;
+            float sum = n3_chain4(reinterpret_cast<const float4*>(q), n / 4);
+            for (int k = n / 4 * 4; k < n; ++k) sum = sum + q[k];
+            chains[j][tid & 7] = sum;
+        }
+        n3_lds_sync();
         if (tid < 8) weights[tid] = (((0.0f + chains[0][tid]) + chains[1][tid]) + chains[2][tid]) + chains[3][tid];
     } else if (tid < p.rank) {
         float s = 0.0f;
@@ -944,16 +968,15 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
         weights[tid] = s;
     }
     __syncthreads();
-    if (tid == 0) {  // ops.rs:92-101
-        float peak = -INFINITY;
-        for (int r = 0; r < p.rank; ++r) peak = fmaxf(peak, weights[r]);
+    if (tid < 64) {  // ops.rs:92-101: the peak (order-free) and the exponentials by lane, the total in order
+        const int R = p.rank;
+        const float w = tid < R ? weights[tid] : -INFINITY;
+        const float peak = wave_max(w);
+        const float e = fast_exp(w - peak);
         float total = 0.0f;
-        for (int r = 0; r < p.rank; ++r) {
-            weights[r] = fast_exp(weights[r] - peak);
-            total = total + weights[r];
-        }
+        for (int r = 0; r < R; ++r) total = total + lane_float(e, r);
         const float inverse = 1.0f / total;
-        for (int r = 0; r < p.rank; ++r) weights[r] = weights[r] * inverse;
+        if (tid < R) weights[tid] = e * inverse;
     }
     __syncthreads();
     {
@@ -969,24 +992,24 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
         sc[tid] = (tid < d ? a[tid] : 0.0f) * pre.d1;
     }
     __syncthreads();
-    n3_kronecker32(sc, p.factors[0], p.factors[1], mx, st);
+    n3_kronecker32(sc, factor[0], factor[1], mx, st);
     sc[tid] = silu(((pre.d2 * modulation[tid]) * st[pre.perm1]) + pre.b2);
     __syncthreads();
-    n3_kronecker32(sc, p.factors[2], p.factors[3], mx, st);
+    n3_kronecker32(sc, factor[2], factor[3], mx, st);
     sc[tid] = st[pre.perm2] * pre.d3;
     __syncthreads();
-    n3_kronecker32(sc, p.factors[4], p.factors[5], mx, st);
+    n3_kronecker32(sc, factor[4], factor[5], mx, st);
     mx[tid] = st[tid] * pre.d4;  // mlp
     __syncthreads();
     // block output, delta (lanes.rs:100-104), combine (lanes.rs:86-98), cell
     for (int i = tid; i < d; i += blockDim.x) {
         const float xo = xs[i] + mx[i];
-        const float delta = xo - p.input[i];
+        const float delta = xo - input[i];
         float mean = 0.0f;
         for (int ln = 0; ln < p.lanes; ++ln) {
             float o = 0.0f;
-            for (int s = 0; s < p.lanes; ++s) o = o + p.residual[ln * p.lanes + s] * p.stream[(size_t)s * d + i];
-            o = o + p.post[ln] * delta;
+            for (int s = 0; s < p.lanes; ++s) o = o + residual[ln * p.lanes + s] * stream[(size_t)s * d + i];
+            o = o + post[ln] * delta;
             p.next[(size_t)ln * d + i] = o;
             if (keep) keep[(size_t)ln * d + i] = o;
             mean = mean + o / (float)p.lanes;
@@ -1002,10 +1025,10 @@ __global__ __launch_bounds__(kN3Block) void n3_block_out_kernel(N3BlockOutParams
     __shared__ float chains[32];
     __shared__ float weights[64];
     __shared__ float red[32];
-    __shared__ float cv[kN3Hadamard * 8];  // cond_v of rank 8
-    const N3TailLds l{xs, a, sc, st, mx, modulation, cv, chains, weights, red};
+    __shared__ __align__(16) float cv[kN3Hadamard * 8];  // cond_v of rank 8
+    const N3TailLds l{xs, a, sc, st, mx, modulation, cv, chains, weights, red, nullptr, nullptr, nullptr, nullptr};
     const N3TailPre pre = n3_tail_prefetch(p);
-    n3_tail(p, l, nullptr, pre);
+    n3_tail<false>(p, l, nullptr, pre);
 }
 
 // session.rs:141-144: lane mean and the final norm
@@ -1530,11 +1553,15 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
             float nv[8], av[8], sv[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
+                // loaded unconditionally (clamped), then zeroed past the
+                // groups: a conditional load becomes a branch with its own wait
                 const int g = min(g0 + k, G - 1);
                 const bool in = g0 + k < G;
-                nv[k] = in ? __half2float(__ushort_as_half(nm[r * G + g])) : 0.0f;
-                av[k] = in ? (float)acc[r * G + g] : 0.0f;
-                sv[k] = in ? xs[g] : 0.0f;
+                const float n_raw = __half2float(__ushort_as_half(nm[r * G + g]));
+                const float a_raw = (float)acc[r * G + g], s_raw = xs[g];
+                nv[k] = in ? n_raw : 0.0f;
+                av[k] = in ? a_raw : 0.0f;
+                sv[k] = in ? s_raw : 0.0f;
             }
             if (fma_form) {
 #pragma unroll
@@ -1774,13 +1801,13 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     }
     // the new position, and earlier positions past the staged ones
     for (int pp = early + tid; pp < count; pp += kN3AttendThreads) {
+        // the new position's key from LDS, another's from memory (values
+        // selected, so that no load is a flat one)
         int4 k[4];
-        float kscl;
-        if (pp == last) {
+        float kscl = scale_s[1];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) k[i] = reinterpret_cast<const int4*>(kc_s)[i];
-            kscl = scale_s[1];
-        } else {
+        for (int i = 0; i < 4; ++i) k[i] = reinterpret_cast<const int4*>(kc_s)[i];
+        if (pp != last) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) k[i] = reinterpret_cast<const int4*>(kbase + (size_t)pp * kN3Head)[i];
             kscl = ks[pp];
@@ -1844,9 +1871,13 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
             for (int j = 0; j < 16; ++j) {
                 const int pp = pp0 + 64 * j;
                 if (pp >= count) break;
-                const int packed = pp == last ? reinterpret_cast<const int*>(vc_s)[dg]
-                                   : pp < early ? reinterpret_cast<const int*>(val_s + (size_t)pp * kN3Head)[dg]
-                                                : *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head + 4 * dg);
+                // staged and new values read as LDS (values selected, not
+                // addresses, so that no load is a flat one); a later earlier
+                // position (past the staged ones) from memory
+                const int staged = reinterpret_cast<const int*>(val_s + (size_t)min(pp, kN3StagedPositions - 1) * kN3Head)[dg];
+                const int fresh = reinterpret_cast<const int*>(vc_s)[dg];
+                int packed = pp == last ? fresh : staged;
+                if (pp >= early && pp != last) packed = *reinterpret_cast<const int*>(vbase + (size_t)pp * kN3Head + 4 * dg);
                 const int wgt = pre_w ? wgt_s[pp] : (int)__builtin_roundf((c_s[pp] * value_scale(pp)) / scale);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) av[k] += wgt * (int)(int8_t)(packed >> (8 * k));
@@ -2000,7 +2031,6 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     __shared__ __align__(16) float rv[kN3MaxWidth];
     __shared__ int4 rq[kN3MaxWidth / 16];
     __shared__ float rs[64];
-    __shared__ int racc[kN3RouteRows * 64];
     __shared__ float ry[kN3RouteRows];
     __shared__ __align__(16) uint8_t pw[kN3RouteRows * kN3RouteRowBytes];
     __shared__ uint16_t pn[kN3RouteRows * 64];
@@ -2061,31 +2091,37 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     int4 v0 = make_int4(0, 0, 0, 0), v1 = make_int4(0, 0, 0, 0);
     if (wv < cn) v0 = chunk_src(wv)[lane];
     if (wv + 16 < cn) v1 = chunk_src(wv + 16)[lane];
-    if (p.tail) pre = n3_tail_prefetch(t);
-    // the layer's norms of phi_pre, phi_post and phi_res (rows one after another)
+    // the small tensors, one element a thread from a selected address, so
+    // that every load is issued before the first wait: the layer's norms of
+    // phi_pre, phi_post and phi_res (rows one after another); small_s (a_pre,
+    // a_post, a_res, then b_pre, b_post, b_res of the layer); the tail's post
+    // and residual
+    const int nsmall = 3 + 2 * L + L * L, nlane = L + L * L;
     uint16_t tn = 0;
+    float small_v = 0.0f, lane_v = 0.0f;
     if (p.route) {
         const int i = min(tid, route_rows * G - 1), r = i / G;
         const uint16_t* nsrc = r < L ? p.phi_pre.norms + (size_t)(layer * L + r) * G
                                      : r < 2 * L ? p.phi_post.norms + (size_t)(layer * L + r - L) * G
                                                  : p.phi_res.norms + (size_t)(layer * L * L + r - 2 * L) * G;
         tn = nsrc[i - r * G];
-        if (tid < L) {
-            small_s[3 + tid] = p.b_pre[layer * L + tid];
-            small_s[3 + L + tid] = p.b_post[layer * L + tid];
-        }
-        if (tid < L * L) small_s[3 + 2 * L + tid] = p.b_res[layer * L * L + tid];
-        if (tid == 0) {
-            small_s[0] = p.a_pre[layer];
-            small_s[1] = p.a_post[layer];
-            small_s[2] = p.a_res[layer];
-        }
+        const int j = min(tid, nsmall - 1);
+        const float* ssrc = j == 0 ? p.a_pre + layer
+                          : j == 1 ? p.a_post + layer
+                          : j == 2 ? p.a_res + layer
+                          : j < 3 + L ? p.b_pre + layer * L + (j - 3)
+                          : j < 3 + 2 * L ? p.b_post + layer * L + (j - 3 - L)
+                                          : p.b_res + layer * L * L + (j - 3 - 2 * L);
+        small_v = *ssrc;
     }
     if (p.tail) {
-        if (tid < L) lane_s[tid] = t.post[tid];
-        if (tid < L * L) lane_s[kMaxLanes + tid] = t.residual[tid];
+        const int j = min(tid, nlane - 1);
+        lane_v = *(j < L ? t.post + j : t.residual + (j - L));
+        pre = n3_tail_prefetch(t);
     }
     if (p.route && tid < route_rows * G) pn[tid] = tn;
+    if (p.route && tid < nsmall) small_s[tid] = small_v;
+    if (p.tail && tid < nlane) lane_s[tid < L ? tid : kMaxLanes + tid - L] = lane_v;
     if (wv < cn) chunk_dst(wv)[lane] = v0;
     if (wv + 16 < cn) chunk_dst(wv + 16)[lane] = v1;
     {
@@ -2102,19 +2138,9 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
                                                  16, 0, 0);
         }
     }
-    if (p.tail) {
-        // the tail reads its copies
-        for (int f = 0; f < 6; ++f) t.factors[f] = tailw_s + f * kN3Hadamard;
-        t.attention = tin_s;
-        t.x = tin_s + d;
-        t.input = tin_s + 2 * d;
-        t.stream = stream_s;
-        t.post = lane_s;
-        t.residual = lane_s + kMaxLanes;
-    }
-    __syncthreads();
-    const N3TailLds l{xs_, a_, sc_, st_, mx_, mod_, cv_, chains_, weights_, red};
-    if (p.tail) n3_tail(t, l, rv, pre, true);  // the next stream into rv, then into stream_s
+    n3_lds_sync();  // the factors, cond_v and routing rows stay in flight
+    const N3TailLds l{xs_, a_, sc_, st_, mx_, mod_, cv_, chains_, weights_, red, tin_s, tailw_s, stream_s, lane_s};
+    if (p.tail) n3_tail<true>(t, l, rv, pre);  // the next stream into rv, then into stream_s
     if (p.tail) {
         for (int i = tid; i < S; i += blockDim.x) stream_s[i] = rv[i];
         __syncthreads();
@@ -2149,13 +2175,22 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
         // (taps of the positions that exist, at most kN3MaxTaps, read first)
         const int i = min(tid, d - 1);
         const float r = p.raw[i];
+        // (every load issued unconditionally from a clamped index, then
+        // selected: a conditional load becomes a branch with its own wait)
         float gain[kN3MaxTaps], sample[kN3MaxTaps];
+        if (p.ntaps > 0) {
 #pragma unroll
-        for (int tap = 0; tap < kN3MaxTaps; ++tap) {
-            const int back = tap * p.dilation;
-            const bool on = tap < p.ntaps && p.position >= back;
-            gain[tap] = on ? p.taps[(size_t)tap * d + i] : 0.0f;
-            sample[tap] = (on && tap > 0) ? p.ring[(size_t)((p.position - back) % p.keep) * d + i] : r;
+            for (int tap = 0; tap < kN3MaxTaps; ++tap) {
+                const int back = tap * p.dilation;
+                const bool on = tap < p.ntaps && p.position >= back;
+                const float g_raw = p.taps[(size_t)min(tap, p.ntaps - 1) * d + i];
+                const float s_raw = p.ring[(size_t)((on ? p.position - back : p.position) % p.keep) * d + i];
+                gain[tap] = on ? g_raw : 0.0f;
+                sample[tap] = (on && tap > 0) ? s_raw : r;
+            }
+        } else {
+#pragma unroll
+            for (int tap = 0; tap < kN3MaxTaps; ++tap) gain[tap] = sample[tap] = 0.0f;
         }
         float v = 0.0f;
 #pragma unroll
@@ -2175,7 +2210,8 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the routing rows, copied into LDS at the start
     __syncthreads();
     // lanes.rs:56-63: the layer's rows of the three routing matrices
-    n3_rows(p.phi_pre, pw, pn, route_rows, rq, rs, racc, ry);
+    // (the rows' group sums in cv_, free after the tail: R * G <= 1024)
+    n3_rows(p.phi_pre, pw, pn, route_rows, rq, rs, reinterpret_cast<int*>(cv_), ry);
     // lanes.rs:64-83 (as lanes_route_kernel)
     const int own = p.slot % L, n = L * L;
     if (tid < 64) {
@@ -2218,13 +2254,13 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
                 float total = -0.0f;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) total = total + row_j(m, j);
-                m = m * (1.0f / fmaxf(total, 1.17549435e-38f));
+                m = m * reciprocal_normal(fmaxf(total, 1.17549435e-38f));
                 float col[4];
                 col4(m, col);
                 total = -0.0f;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) total = total + col[j];
-                m = m * (1.0f / fmaxf(total, 1.17549435e-38f));
+                m = m * reciprocal_normal(fmaxf(total, 1.17549435e-38f));
             }
         } else {
             float peak = -INFINITY;
@@ -2233,10 +2269,10 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
             for (int it = 0; it < 20; ++it) {
                 float total = -0.0f;
                 for (int j = 0; j < L; ++j) total = total + __shfl(m, r * L + j, 64);
-                m = m * (1.0f / fmaxf(total, 1.17549435e-38f));
+                m = m * reciprocal_normal(fmaxf(total, 1.17549435e-38f));
                 total = -0.0f;
                 for (int j = 0; j < L; ++j) total = total + __shfl(m, j * L + c, 64);
-                m = m * (1.0f / fmaxf(total, 1.17549435e-38f));
+                m = m * reciprocal_normal(fmaxf(total, 1.17549435e-38f));
             }
         }
         if (live) out_residual[i] = m;
@@ -2255,8 +2291,11 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
         if (tid < d) sc_[tid] = key_r;
         __syncthreads();
         n3_unit_rms(sc_, d, sc_, red, cv_);
-        if (tid == 0) {  // Iterator::sum: in order from -0.0
-            const float dot = n3_fold<false>(-0.0f, a_, sc_, d, 1);
+        // Iterator::sum: the products by every thread, then in order from -0.0
+        if (tid < d) st_[tid] = a_[tid] * sc_[tid];
+        __syncthreads();
+        if (tid == 0) {
+            const float dot = n3_chain4(reinterpret_cast<const float4*>(st_), d / 4, -0.0f);
             alpha_s = libm_sigmoid(dot / sqrtf((float)d));
         }
         __syncthreads();
