@@ -38,12 +38,12 @@ GEMV_UNIT_BYTES = 1_189_888    # one 2048x512 int8 matvec: W 1,048,576 + sW 131,
 DECODE_TOKENS = 64
 CONTEXT = 256
 KERNEL_NAMES = {
-    "qkv_attention": "qkv_attend_kernel<512,norm> (norm + a head's q/k/v rows + rotary + fp16 append + attention)",
+    "qkv_attention": "qkv_attend_kernel<512,norm> (norm + a head's q/k/v rows + rotary + fp16 append + attention; "
+                     "layer 0 first reduces the previous logits' argmax keys and gathers the embedding row)",
     "out": "gemv_kernel<512,2,quant,residual,panel> (out)",
     "gate_up": "gemv_kernel<512,8,norm,silu,panel> (gate/up)",
     "down": "gemv_splitk_kernel<2048,2,panel> (down, four waves over the columns)",
-    "logits": "gemv_kernel<512,8,norm,argmax,plane> (logits)",
-    "final": "argmax_finalize_kernel",
+    "logits": "gemv_kernel<512,8,norm,argmax,plane> (logits, block argmax keys, position advance)",
 }
 # Memory-side bytes per launch of each decode kernel, from two rocprofv3 --pmc
 # passes (FETCH_SIZE, WRITE_SIZE) over this workload with direct launches; the
@@ -51,12 +51,11 @@ KERNEL_NAMES = {
 # (FETCH x2.000, WRITE x1.000). Recorded in profiles/decode_b1_needle20_traffic.md;
 # they describe the kernels as built when measured and are re-measured with them.
 PMC_TRAFFIC = {
-    "qkv_attention": 1_723_332,
-    "out": 399_300,
-    "gate_up": 2_502_273,
-    "down": 1_345_535,
-    "logits": 4_913_429,
-    "final": 10_341,
+    "qkv_attention": 1_780_895,  # 20-launch mean: 19 x 1,776,640 (layers 1-19) + 1,861,734 (layer 0)
+    "out": 392_192,
+    "gate_up": 2_502_656,
+    "down": 1_345_536,
+    "logits": 4_915_405,
 }
 
 
