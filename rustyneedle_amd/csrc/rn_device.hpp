@@ -193,6 +193,12 @@ __device__ __forceinline__ float int8_scale_from_peak(float peak) {
     return peak > 0.0f ? (peak == __builtin_inff() ? peak : q) : 1.0f;
 }
 
+// The s_waitcnt immediate that waits until at most n (0..63) vector memory
+// operations of the wave are outstanding, and for nothing else (gfx9
+// encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 at their
+// maxima).
+constexpr unsigned vmcnt_imm(unsigned n) { return (n & 0xfu) | (((n >> 4) & 3u) << 14) | 0x0f70u; }
+
 // Cross-lane moves inside rows of 16 lanes (DPP: no LDS round trip). CTRL:
 // quad_perm [1,0,3,2] = 0xb1, quad_perm [2,3,0,1] = 0x4e, row_half_mirror =
 // 0x141, row_mirror = 0x140. A lane whose source is invalid keeps its value.

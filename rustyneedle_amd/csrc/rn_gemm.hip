@@ -468,22 +468,26 @@ __global__ __launch_bounds__(256) void gemm_chain_kernel(GemmParams p) {
 //
 // The chain kernel's arithmetic (a 16 x 16 x 32 i8 MFMA per sub-tile and group,
 // folded into the lane's running totals in group order), with every operand
-// byte of the block requested at once: the BM token rows and BN weight rows of
-// all K columns, and the tile's weight scales, go straight to LDS
-// (global_load_lds_dwordx4, no registers), so a block waits for one memory
-// round trip instead of one per K chunk, then runs its group chains back to
-// back from LDS. Rows are padded by 16 bytes, so the 16 rows of an MFMA
-// fragment read start on 16 different 16-byte bank slots.
+// byte of the block requested at once: the tile's weight scales, then the BM
+// token rows and BN weight rows in K chunks of 128 columns (four groups),
+// chunk by chunk, go straight to LDS (global_load_lds_dwordx4, no registers).
+// Every wave issues the same number of chunk loads, so the group chains of
+// chunk c start once the wave's loads of chunks 0..c are in (a counted vmcnt
+// wait, then an LDS barrier) while the later chunks are still arriving. A
+// chunk's rows are 128 bytes, their eight 16-byte pieces XOR-swizzled by the
+// row (piece p of row r at slot p ^ (r & 7)), so the rows of an MFMA fragment
+// read spread over the banks without padding.
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void global_void;
 
 template <int K, int BM, int BN>
 struct PanelShape {
-    static constexpr int kPitch = K + 16;             // LDS bytes per row
-    static constexpr int kSlotsPerRow = kPitch / 16;  // the last slot of a row is padding
-    static constexpr int kSlots = (BM + BN) * kSlotsPerRow;
+    static constexpr int kChunks = K / 128;               // K chunks of 128 columns
+    static constexpr int kChunkBytes = (BM + BN) * 128;    // a chunk's LDS image
+    static constexpr int kChunkRounds = kChunkBytes / 16 / 256;  // loads a wave issues per chunk
     static constexpr int kG = K / kGroup;
     static constexpr int kScaleSlots = BN * kG / 4;   // 16-byte pieces of the tile's weight scales
+    static_assert(K % 128 == 0 && (BM + BN) % 32 == 0, "whole chunks, whole load rounds");
 };
 
 template <int K, int SM, int SN, int WAVES_M, int EPI, int FORM>
@@ -491,13 +495,18 @@ __global__ __launch_bounds__(256) void gemm_panel_kernel(GemmParams p) {
     constexpr int WAVES_N = 4 / WAVES_M;
     constexpr int BM = WAVES_M * SM * 16, BN = WAVES_N * SN * 16;
     using S = PanelShape<K, BM, BN>;
-    constexpr int G = S::kG, PITCH = S::kPitch;
+    constexpr int G = S::kG;
     constexpr bool kSilu = EPI == kGemmSilu;
     constexpr bool kRope = EPI == kGemmRope;
     static_assert(!kSilu || SN == 2, "the gated FFN pairs gate and up sub-tiles");
     static_assert(!kRope || (SM == 1 && SN == 1 && WAVES_M == 2), "rotary: wave column 0 the first halves, 1 the second");
     static_assert(K % 32 == 0 && G % 4 == 0, "whole groups, scale quads");
-    __shared__ __align__(16) int8_t panel_s[(BM + BN) * PITCH];
+    // one array a chunk, so that the reads of a chunk are seen not to alias the
+    // later chunks' loads into LDS (which the compiler would otherwise wait for)
+    __shared__ __align__(16) int8_t chunk0_s[S::kChunkBytes], chunk1_s[S::kChunkBytes], chunk2_s[S::kChunkBytes];
+    __shared__ __align__(16) int8_t chunk3_s[S::kChunks > 3 ? S::kChunkBytes : 16];
+    static_assert(S::kChunks >= 3 && S::kChunks <= 4, "K of 384 or 512");
+    auto chunk_s = [&](int ch) -> int8_t* { return ch == 0 ? chunk0_s : ch == 1 ? chunk1_s : ch == 2 ? chunk2_s : chunk3_s; };
     __shared__ __align__(16) float sw_s[BN * G];
     __shared__ float pair_s[kRope ? BM : 1][kRope ? BN + 1 : 1];
 
@@ -529,22 +538,19 @@ __global__ __launch_bounds__(256) void gemm_panel_kernel(GemmParams p) {
         else return nt * BN + c < p.N;
     };
 
-    // 1. the panel: slot s of the LDS image is 16-byte piece s % kSlotsPerRow of
-    // tile row s / kSlotsPerRow (rows 0..BM-1 tokens, then BN weight rows; rows
-    // past the matrix repeat its last row; a padding slot repeats piece 0). A
-    // lane copies to slot (round base + lane): lanes past the image stay idle.
+    const int r16 = lane & 15, kq = lane >> 4;
+    // the rows' activation scales (register loads, issued before the panel's
+    // loads so that the counted waits below cover them)
+    float sx[SM][4];
 #pragma unroll
-    for (int q = 0; q < (S::kSlots + 255) / 256; ++q) {
-        const int sl = 256 * q + 64 * wave + lane;
-        if (sl < S::kSlots) {
-            const int row = sl / S::kSlotsPerRow, col = sl - row * S::kSlotsPerRow;
-            const int piece = col < S::kSlotsPerRow - 1 ? col : 0;
-            const int8_t* src = row < BM ? p.X + (size_t)min(m0 + row, p.M - 1) * K
-                                         : p.W + (size_t)min(weight_row(row - BM), p.N - 1) * K;
-            __builtin_amdgcn_global_load_lds((global_void*)(src + 16 * piece),
-                                             (lds_void*)(panel_s + 16 * (256 * q + 64 * wave)), 16, 0, 0);
-        }
-    }
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sx[i][r] = p.sx[min(m0 + wm * SM * 16 + i * 16 + 4 * kq + r, p.M - 1)];
+    // 1. the tile's weight scales, then the panel chunk by chunk: slot s of
+    // chunk c's image (tile row s / 8, rows 0..BM-1 tokens, then BN weight
+    // rows; rows past the matrix repeat its last row) holds 16-byte piece
+    // (s % 8) ^ (row & 7) of the row's columns 128 c .. 128 c + 127. A wave's
+    // lanes fill 64 consecutive slots per load.
 #pragma unroll
     for (int q = 0; q < (S::kScaleSlots + 255) / 256; ++q) {
         const int sl = 256 * q + 64 * wave + lane;
@@ -554,12 +560,17 @@ __global__ __launch_bounds__(256) void gemm_panel_kernel(GemmParams p) {
                                              (lds_void*)(sw_s + 4 * (256 * q + 64 * wave)), 16, 0, 0);
         }
     }
-    const int r16 = lane & 15, kq = lane >> 4;
-    float sx[SM][4];
 #pragma unroll
-    for (int i = 0; i < SM; ++i)
+    for (int ch = 0; ch < S::kChunks; ++ch)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sx[i][r] = p.sx[min(m0 + wm * SM * 16 + i * 16 + 4 * kq + r, p.M - 1)];
+        for (int q = 0; q < S::kChunkRounds; ++q) {
+            const int sl = 256 * q + 64 * wave + lane, row = sl >> 3, piece = (sl & 7) ^ (row & 7);
+            const int8_t* src = row < BM ? p.X + (size_t)min(m0 + row, p.M - 1) * K
+                                         : p.W + (size_t)min(weight_row(row - BM), p.N - 1) * K;
+            __builtin_amdgcn_global_load_lds((global_void*)(src + 128 * ch + 16 * piece),
+                                             (lds_void*)(chunk_s(ch) + 16 * (256 * q + 64 * wave)),
+                                             16, 0, 0);
+        }
     float total[SM][SN][4];
 #pragma unroll
     for (int i = 0; i < SM; ++i)
@@ -567,44 +578,61 @@ __global__ __launch_bounds__(256) void gemm_panel_kernel(GemmParams p) {
         for (int j = 0; j < SN; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) total[i][j][r] = 0.0f;
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's panel pieces are in LDS
-    __syncthreads();
 
-    // 2. the group chains, in group order
-    const int8_t* arow[SM];
-    const int8_t* brow[SN];
+    // 2. the group chains, in group order, a chunk at a time. Lane (r16, kq)
+    // reads bytes 8 kq .. 8 kq + 7 of a group of fragment row r16: piece
+    // 2 (g % 4) + kq / 2 of the chunk row, half kq % 2.
+    int arow[SM], brow[SN];
     const float* srow[SN];
 #pragma unroll
-    for (int i = 0; i < SM; ++i) arow[i] = panel_s + (wm * SM * 16 + i * 16 + r16) * PITCH + 8 * kq;
+    for (int i = 0; i < SM; ++i) arow[i] = (wm * SM * 16 + i * 16 + r16) * 128 + 8 * (kq & 1);
 #pragma unroll
     for (int j = 0; j < SN; ++j) {
-        brow[j] = panel_s + (BM + wn * SN * 16 + j * 16 + r16) * PITCH + 8 * kq;
+        brow[j] = (BM + wn * SN * 16 + j * 16 + r16) * 128 + 8 * (kq & 1);
         srow[j] = sw_s + (wn * SN * 16 + j * 16 + r16) * G;
     }
-#pragma unroll 4
-    for (int g = 0; g < G; ++g) {
-        long a[SM], b[SN];
-        float sv[SN];
+    int slot[4];
 #pragma unroll
-        for (int i = 0; i < SM; ++i) a[i] = *reinterpret_cast<const long*>(arow[i] + g * kGroup);
+    for (int gg = 0; gg < 4; ++gg) slot[gg] = ((2 * gg + (kq >> 1)) ^ (r16 & 7)) * 16;
 #pragma unroll
-        for (int j = 0; j < SN; ++j) {
-            b[j] = *reinterpret_cast<const long*>(brow[j] + g * kGroup);
-            sv[j] = srow[j][g];
+    for (int ch = 0; ch < S::kChunks; ++ch) {
+        // this wave's loads of chunks 0..ch are in (later chunks' loads, the
+        // newest, may still be outstanding); then every wave's
+        constexpr int kRounds = S::kChunkRounds;
+        switch (S::kChunks - 1 - ch) {
+            case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+            case 1: __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRounds)); break;
+            case 2: __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kRounds)); break;
+            default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * kRounds)); break;
         }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int8_t* chunk = chunk_s(ch);
 #pragma unroll
-        for (int i = 0; i < SM; ++i)
+        for (int gg = 0; gg < 4; ++gg) {
+            const int g = 4 * ch + gg;
+            long a[SM], b[SN];
+            float sv[SN];
+#pragma unroll
+            for (int i = 0; i < SM; ++i) a[i] = *reinterpret_cast<const long*>(chunk + arow[i] + slot[gg]);
 #pragma unroll
             for (int j = 0; j < SN; ++j) {
-                const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b[j], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if constexpr (FORM == kPanel)
-                        total[i][j][r] = fmaf((float)acc[r], sv[j] * sx[i][r], total[i][j][r]);  // panel.rs:184-188
-                    else
-                        total[i][j][r] = total[i][j][r] + ((float)acc[r] * sv[j]) * sx[i][r];  // neon.rs:180
-                }
+                b[j] = *reinterpret_cast<const long*>(chunk + brow[j] + slot[gg]);
+                sv[j] = srow[j][g];
             }
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+#pragma unroll
+                for (int j = 0; j < SN; ++j) {
+                    const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b[j], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if constexpr (FORM == kPanel)
+                            total[i][j][r] = fmaf((float)acc[r], sv[j] * sx[i][r], total[i][j][r]);  // panel.rs:184-188
+                        else
+                            total[i][j][r] = total[i][j][r] + ((float)acc[r] * sv[j]) * sx[i][r];  // neon.rs:180
+                    }
+                }
+        }
     }
 
     // 3. epilogue
@@ -685,8 +713,10 @@ static void launch_chain(const GemmParams& p, hipStream_t stream) {
 
 // Tile shape: the one with the most blocks among 64 x 64, 64 x 32, 32 x 64 and
 // 32 x 32 (not for the gated FFN, whose waves pair gate and up sub-tiles). The
-// chains are sequential over K, so blocks are the parallelism, and small tiles
-// measured faster than large ones at every size used here.
+// chains are VALU-bound, so blocks (waves) are the parallelism: small tiles
+// measured faster than large ones at every size used here, also with the
+// panel's loads overlapping the chains (64 x 64 re-reads less but ran the
+// 256-token gate/up product slower than 64 x 32).
 // Returns the chain shape to use (0-3), or -1 for the split kernel.
 template <int EPI>
 static int chain_pick(const GemmParams& p) {
