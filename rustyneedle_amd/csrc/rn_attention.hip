@@ -652,10 +652,16 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
                 // the previous step's greedy choice (generator.rs:257-265): the
                 // largest of the logits kernel's block keys (the lowest index
                 // among equal values); a NaN at index 0 is never displaced
+                // (the lane's sixteen keys of a round of 1024 requested before
+                // any compare, from clamped indices: a repeated key does not
+                // change the maximum; a loop of single loads waits for each)
                 uint64_t key = 0ull;
-                for (int i = lane; i < p.nkeys; i += 64) {
-                    const uint64_t k = p.keys[i];
-                    key = k > key ? k : key;
+                for (int base = 0; base < p.nkeys; base += 1024) {
+                    uint64_t kk[16];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) kk[i] = p.keys[min(base + lane + 64 * i, p.nkeys - 1)];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) key = kk[i] > key ? kk[i] : key;
                 }
                 key = wave_max_u64(key);
                 const float first = p.logits[0];

@@ -367,8 +367,16 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const unsigned lon
                                                               const float* logits, DecodeState* st, uint32_t* ids,
                                                               int mode) {
     __shared__ unsigned long long best_s[4];
+    // rounds of four keys a thread, all requested before any compare, from
+    // clamped indices (a repeated key does not change the maximum)
     uint64_t key = 0ull;
-    for (int i = threadIdx.x; i < nkeys; i += 256) key = keys[i] > key ? keys[i] : key;
+    for (int base = 0; base < nkeys; base += 4 * 256) {
+        uint64_t kk[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kk[j] = keys[min(base + (int)threadIdx.x + 256 * j, nkeys - 1)];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) key = kk[j] > key ? kk[j] : key;
+    }
     key = wave_max_u64(key);
     if ((threadIdx.x & 63) == 0) best_s[threadIdx.x >> 6] = key;
     __syncthreads();
