@@ -1031,26 +1031,28 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* logits, 
         key = k > key ? k : key;
     };
     if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
-        // rounds of four loads a thread, all requested before any compare,
-        // from clamped indices (a repeated element does not change the key)
         const float4* r4 = reinterpret_cast<const float4*>(row);
         const int n4 = n / 4;
-        for (int base = 0; base < n4; base += 4 * 1024) {
+        int i = tid;
+        for (; i + 3 * 1024 < n4; i += 4 * 1024) {
             float4 v[4];
-            int at[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = r4[i + j * 1024];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                at[j] = min(base + tid + j * 1024, n4 - 1);
-                v[j] = r4[at[j]];
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int e = 4 * at[j];
+                const int e = 4 * (i + j * 1024);
                 take(v[j].x, e);
                 take(v[j].y, e + 1);
                 take(v[j].z, e + 2);
                 take(v[j].w, e + 3);
             }
+        }
+        for (; i < n4; i += 1024) {
+            const float4 v = r4[i];
+            take(v.x, 4 * i);
+            take(v.y, 4 * i + 1);
+            take(v.z, 4 * i + 2);
+            take(v.w, 4 * i + 3);
         }
     } else {
         for (int i = tid; i < n; i += 1024) take(row[i], i);
