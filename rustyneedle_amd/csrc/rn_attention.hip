@@ -584,11 +584,11 @@ hipError_t launch_rope_append(const float* qkv, float* q_out, __half* kc, __half
 // loads and barriers off that chain:
 //   1. every load is requested at the start: wave 0 the input row (or the
 //      embedding row of the token times sqrt(d), session.rs:85-90) and the
-//      norm gains; waves 1-6 the head's weight rows and scales; every wave its
-//      share of the first KC x 128 key rows and 32 x VC value rows (clamped to
-//      the capacity, so that they need not wait for the position); once the
-//      position is known (one scalar load), waves 1-4 the rotary angles of
-//      their rows;
+//      norm gains; waves 1-6 the head's weight rows and scales; wave 7 the
+//      position (one scalar load) and then the rotary angles of that
+//      position, for the block through LDS; every wave its share of the first
+//      KC x 128 key rows and 32 x VC value rows (clamped to the capacity, so
+//      that they need not wait for the position);
 //   2. wave 0: zero-centred RMSNorm (eight-lane sum of ops.rs:7-17) and int8
 //      codes (ops.rs:103-118) into LDS (barrier 1);
 //   3. waves 1-6, 32 rows each, two lanes a row: each lane owns half a row's
@@ -603,7 +603,10 @@ hipError_t launch_rope_append(const float* qkv, float* q_out, __half* kc, __half
 //      (barrier 4), then the value sums in tree T3 (32 position classes, 4 dims
 //      per thread, barrier 5) and the class combine with one multiply by
 //      1/total.
-// The float results are identical to the separate product + attend_kernel path.
+// The block shares data through LDS only, so its barriers wait for LDS
+// operations and not for global loads or stores (the new cache rows it stores
+// are read from LDS). The float results are identical to the separate
+// product + attend_kernel path.
 template <int K, int PRO, int KC, int VC>
 __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
     constexpr int NT = 512;
@@ -624,6 +627,8 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
     __shared__ float total_s[kClasses];
     __shared__ float peak_s[NT / 64];
     __shared__ float sx_s;
+    __shared__ int pos_s;
+    __shared__ float rope_s[2][kHeadDim / 2];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = blockIdx.x;
     const int r = tid >> 2, li = tid & 3;     // score layout: key row slot, 16-dim quarter
@@ -639,9 +644,32 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
     const int dim = dim_of(lr);
     const int rot = (lr & 15) + 16 * sub;     // rotary pair index of this row
     const bool rows_wave = wave >= 1 && wave <= 6;
+    // The first pass of key and value rows does not wait for the position: a
+    // load that needed it would start only when the position's own load came
+    // back. The rows are clamped to the capacity instead; rows past the cached
+    // ones are read but never used. Each kind of wave issues them in its own
+    // branch: a distinct asm statement per branch (after the loads, and the
+    // zero `salt` before them) keeps the compiler from merging the copies below
+    // the branches, behind the product waves' wait for the position.
+    const int top = p.capacity - 1;
+    uint4 kr[KC][2];
+    uint2 vr[VC];
+    auto request_cache = [&](int salt) {
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            const __half* row = Kc + (size_t)min(r + KROWS * c, top) * kHeadDim + 16 * li + salt;
+            kr[c][0] = *reinterpret_cast<const uint4*>(row);
+            kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
+        }
+#pragma unroll
+        for (int c = 0; c < VC; ++c)
+            vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(j + kClasses * c, top) * kHeadDim + 4 * dq +
+                                                    salt);
+    };
+    int salt;
 
     // 1. requests: the prologue input first (wave 0), the weights and scales
-    // (waves 1-6), then everything that needs the position
+    // (waves 1-6), the position and the rotary angles (wave 7), the cache rows
     float v[E], gv[E];
     int4 w[HC];
     float sv[HG];
@@ -689,6 +717,9 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
             load_floats<E>(p.x + lane * E, v);
         }
         load_floats<E>(p.gain + lane * E, gv);
+        asm volatile("v_mov_b32 %0, 0 ; salt: prologue wave" : "=v"(salt));
+        request_cache(salt);
+        asm volatile("; requests issued: prologue wave" ::: "memory");
     } else if (rows_wave) {
         // load c covers chunk 64 c + lane of the wave's 32 rows taken slot by
         // slot: consecutive lanes read consecutive 16-byte chunks of a row
@@ -698,35 +729,27 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
             w[c] = *reinterpret_cast<const int4*>(p.W + slot_row(slot) * K + (chunk % CPR) * 16);
         }
         load_floats<HG>(p.sW + slot_row(lr) * G + hh * HG, sv);
+        asm volatile("v_mov_b32 %0, 0 ; salt: product wave" : "=v"(salt));
+        request_cache(salt);
+        asm volatile("; requests issued: product wave" ::: "memory");
+    } else {
+        // wave 7: the position (its wait is this wave's only work before the
+        // first barrier) and the rotary angles of the product waves' rows,
+        // both through LDS; then its cache rows
+        const int pos_in = p.state->pos;
+        const int pr = (pos_in < 0 || pos_in >= p.capacity) ? 0 : pos_in;
+        const int half = lane & (kHeadDim / 2 - 1);
+        const float angle_cos = p.rope_cos[(size_t)pr * (kHeadDim / 2) + half];
+        const float angle_sin = p.rope_sin[(size_t)pr * (kHeadDim / 2) + half];
+        asm volatile("v_mov_b32 %0, 0 ; salt: attention wave" : "=v"(salt));
+        request_cache(salt);
+        asm volatile("; requests issued: attention wave" ::: "memory");
+        if (lane < kHeadDim / 2) {
+            rope_s[0][lane] = angle_cos;
+            rope_s[1][lane] = angle_sin;
+        }
+        if (lane == 0) pos_s = pos_in;
     }
-    // The first pass of key and value rows does not wait for the position: a
-    // load that needed it would start only when the position's own load came
-    // back. The rows are clamped to the capacity instead; rows past the cached
-    // ones are read but never used. No branch around these loads (it would
-    // make later wait counts conservative).
-    const int top = p.capacity - 1;
-    uint4 kr[KC][2];
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-        const __half* row = Kc + (size_t)min(r + KROWS * c, top) * kHeadDim + 16 * li;
-        kr[c][0] = *reinterpret_cast<const uint4*>(row);
-        kr[c][1] = *reinterpret_cast<const uint4*>(row + 8);
-    }
-    uint2 vr[VC];
-#pragma unroll
-    for (int c = 0; c < VC; ++c)
-        vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(j + kClasses * c, top) * kHeadDim + 4 * dq);
-    const int pos = p.state->pos;
-    if (pos < 0 || pos >= p.capacity) {  // uniform over the block
-        if (tid == 0) atomicOr(&p.state->error, 2);
-        return;
-    }
-    float rc = 1.0f, rs = 0.0f;
-    if (rows_wave && section < 2) {
-        rc = p.rope_cos[(size_t)pos * (kHeadDim / 2) + rot];
-        rs = p.rope_sin[(size_t)pos * (kHeadDim / 2) + rot];
-    }
-    const int last_row = pos > 0 ? pos - 1 : 0;  // the last cached row (later passes clamp to it)
 
     // 2. wave 0: the norm and the int8 codes (DS operations of a wave complete
     // in order, so the squares need only a wave barrier)
@@ -769,7 +792,14 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
         for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)code_of_quotient(y[e]);
         if (lane == 0) sx_s = sx;
     }
-    __syncthreads();
+    lds_barrier();
+    // a position outside the cache is flagged; the block then runs on position 0
+    // and stores nothing (uniform over the block)
+    const int pos_in = pos_s;
+    const bool bad_pos = pos_in < 0 || pos_in >= p.capacity;
+    if (bad_pos && tid == 0) atomicOr(&p.state->error, 2);
+    const int pos = bad_pos ? 0 : pos_in;
+    const int last_row = pos > 0 ? pos - 1 : 0;  // the last cached row (later passes clamp to it)
 
     // 3. waves 1-6: a row's exact group sums inside its lane pair, the epilogue
     // chain over the even lane's groups continued by the odd lane, the rotary
@@ -813,21 +843,22 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
             if (section == 2) {
                 const __half vh = __float2half_rn(value);
                 new_s[1][dim] = vh;
-                const_cast<__half*>(Vc)[(size_t)pos * kHeadDim + dim] = vh;
+                if (!bad_pos) const_cast<__half*>(Vc)[(size_t)pos * kHeadDim + dim] = vh;
             } else {
                 // rotate-half: (a, b) = (dim i, dim i + 32) -> (a c - b s, b c + a s)
+                const float rc = rope_s[0][rot], rs = rope_s[1][rot];
                 const float rotated = lr < 16 ? value * rc - other * rs : value * rc + other * rs;
                 if (section == 0) {
                     q_s[dim] = rotated;
                 } else {
                     const __half kh = __float2half_rn(rotated);
                     new_s[0][dim] = kh;
-                    const_cast<__half*>(Kc)[(size_t)pos * kHeadDim + dim] = kh;
+                    if (!bad_pos) const_cast<__half*>(Kc)[(size_t)pos * kHeadDim + dim] = kh;
                 }
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // 4. scores (T2), KROWS key rows per pass, and each thread's peak
     const int nglobal = pos, length = pos + 1;
@@ -857,7 +888,7 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
             }
         }
     }
-    if (tid < 4) {
+    if (tid >= NT - 4) {  // the last wave: it holds the highest rows of every pass
         const uint4 ka = *reinterpret_cast<const uint4*>(&new_s[0][16 * li]);
         const uint4 kb = *reinterpret_cast<const uint4*>(&new_s[0][16 * li + 8]);
         const float s = score_row(q16, ka, kb) * inverse_root;
@@ -866,14 +897,14 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
     }
     m = wave_max(m);
     if (lane == 0) peak_s[wave] = m;
-    __syncthreads();
+    lds_barrier();
 
     // 5. the fast_exp weights (the peak is order-free)
     float peak = peak_s[0];
 #pragma unroll
     for (int w8 = 1; w8 < NT / 64; ++w8) peak = fmaxf(peak, peak_s[w8]);
     for (int pp = tid; pp < length; pp += NT) scores[pp] = fast_exp(scores[pp] - peak);
-    __syncthreads();
+    lds_barrier();
 
     // 6. weighted values (T3): thread (j, dq) walks positions j, j+32, ... in order
     float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -886,20 +917,36 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
                 vr[c] = *reinterpret_cast<const uint2*>(Vc + (size_t)min(base + j + kClasses * c, last_row) *
                                                         kHeadDim + 4 * dq);
         }
+        // slots below `whole` hold a live position in every class; slot
+        // `whole` (if any) in some; later slots in none (uniform tests). The
+        // weights are read from LDS before the tests, all at once.
+        const int whole = (nglobal - base) >> 5;
+        float ew[VC];
+#pragma unroll
+        for (int c = 0; c < VC; ++c) ew[c] = scores[min(base + j + kClasses * c, last)];
 #pragma unroll
         for (int c = 0; c < VC; ++c) {
             const int pp = base + j + kClasses * c;
-            const bool ok = pp < nglobal;
-            const float e = scores[min(pp, last)];
-            const float ev[4] = {mul_f16<false>(e, vr[c].x), mul_f16<true>(e, vr[c].x), mul_f16<false>(e, vr[c].y),
-                                 mul_f16<true>(e, vr[c].y)};
+            if (c < whole) {
+                const float e = ew[c];
+                a[0] = a[0] + mul_f16<false>(e, vr[c].x);
+                a[1] = a[1] + mul_f16<true>(e, vr[c].x);
+                a[2] = a[2] + mul_f16<false>(e, vr[c].y);
+                a[3] = a[3] + mul_f16<true>(e, vr[c].y);
+                total = total + e;
+            } else if (c == whole) {
+                const bool ok = pp < nglobal;
+                const float e = ew[c];
+                const float ev[4] = {mul_f16<false>(e, vr[c].x), mul_f16<true>(e, vr[c].x),
+                                     mul_f16<false>(e, vr[c].y), mul_f16<true>(e, vr[c].y)};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float t = a[i] + ev[i];
-                a[i] = ok ? t : a[i];
+                for (int i = 0; i < 4; ++i) {
+                    const float t = a[i] + ev[i];
+                    a[i] = ok ? t : a[i];
+                }
+                const float tt = total + e;
+                total = ok ? tt : total;
             }
-            const float tt = total + e;
-            total = ok ? tt : total;
         }
     }
     if (j == (nglobal & (kClasses - 1))) {  // the newest position closes its class
@@ -913,8 +960,8 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
     }
     *reinterpret_cast<float4*>(&part_s[j][4 * dq]) = make_float4(a[0], a[1], a[2], a[3]);
     if (dq == 0) total_s[j] = total;
-    __syncthreads();
-    if (tid < kHeadDim) {
+    lds_barrier();
+    if (tid < kHeadDim && !bad_pos) {
         float o = 0.0f, t = 0.0f;
 #pragma unroll
         for (int k = 0; k < kClasses; ++k) {

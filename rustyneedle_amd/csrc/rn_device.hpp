@@ -199,6 +199,16 @@ __device__ __forceinline__ float int8_scale_from_peak(float peak) {
 // maxima).
 constexpr unsigned vmcnt_imm(unsigned n) { return (n & 0xfu) | (((n >> 4) & 3u) << 14) | 0x0f70u; }
 
+// A barrier of the block for its LDS traffic: this wave's LDS operations
+// complete, then s_barrier. Unlike __syncthreads it does not wait for the
+// wave's global loads and stores, so loads (also into LDS, global_load_lds)
+// issued earlier stay in flight across it, and so do stores the block does not
+// read back; a kernel reads LDS-bound load data only after an explicit vmcnt
+// wait and a barrier. For code whose threads share data through LDS only.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Cross-lane moves inside rows of 16 lanes (DPP: no LDS round trip). CTRL:
 // quad_perm [1,0,3,2] = 0xb1, quad_perm [2,3,0,1] = 0x4e, row_half_mirror =
 // 0x141, row_mirror = 0x140. A lane whose source is invalid keeps its value.

@@ -138,21 +138,23 @@ hipError_t launch_attend_prefill(const AttendParams& p, int heads, int count, hi
 
 // Batch-1 decode: norm + the q/k/v rows of each head + rotary + fp16 append +
 // attention, one block per head (grid = heads, d_model = 64 heads).
+// The fields a block needs at its start come first: they share the first 64 bytes
+// of the argument segment, one scalar-cache line.
 struct QkvAttendParams {
     const int8_t* W;      // fused q/k/v codes [3 d][d]
     const float* sW;      // [3 d][d/32]
     const float* x;       // residual stream [d] (kNorm)
     const float* gain;    // norm gains [d]
+    __half* kc;           // this layer's cache [heads][capacity][64]
+    __half* vc;
+    DecodeState* state;   // token, pos, error flags
+    int capacity;
     float eps;
     const int8_t* embW;   // kEmbedNorm: embedding codes/scales, token from state
     const float* embS;
     float embed_scale;
     int vocab;
     float* x_out;         // kEmbedNorm: block 0 writes the embedded row
-    __half* kc;           // this layer's cache [heads][capacity][64]
-    __half* vc;
-    int capacity;
-    DecodeState* state;   // token, pos, error flags
     const float* rope_cos;
     const float* rope_sin;
     float* out;           // [d] attention output, head h at 64 h

@@ -67,15 +67,6 @@ constexpr int kN3Hadamard = 1024;     // 32 x 32
 
 namespace {
 
-// A barrier of the block for its LDS traffic: this wave's LDS operations
-// complete, then s_barrier. Unlike __syncthreads it does not wait for the
-// wave's global loads, so loads into LDS (global_load_lds) issued earlier stay
-// in flight across it; a kernel reads such data only after an explicit vmcnt
-// wait and a barrier. For code whose threads share data through LDS only.
-__device__ __forceinline__ void n3_lds_sync() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // The maximum over the block (every thread calls; all get the result). With
 // TAIL false the caller's next barrier must come before red is written again.
 template <bool TAIL = true>
@@ -192,19 +183,19 @@ __device__ float n3_sum_of_squares(const float* v, int n, float* red, float* sq 
             const float x = v[i];
             sq[(i & 7) * stride + (i >> 3)] = x * x;
         }
-        n3_lds_sync();
+        lds_barrier();
         if (tid < 8) {
             red[tid] = n3_chain4(reinterpret_cast<const float4*>(sq + tid * stride), n8 / 4);
         }
     } else if (tid < 8) {
         red[tid] = n3_fold<true>(0.0f, v + tid, nullptr, n8, 8);
     }
-    n3_lds_sync();
+    lds_barrier();
     float total = 0.0f;
     for (int j = 0; j < 8; ++j) total = total + red[j];
     float tail = -0.0f;
     for (int i = n8 * 8; i < n; ++i) tail = tail + v[i] * v[i];
-    n3_lds_sync();
+    lds_barrier();
     return total + tail;
 }
 
@@ -222,7 +213,7 @@ __device__ void n3_norm_gain(const float* x, float gain, int n, float* out, floa
     const float inverse = 1.0f / sqrtf(mean_square + 1e-6f);
     const int i = threadIdx.x;
     if (i < n) out[i] = ((1.0f + gain) * x[i]) * inverse;
-    n3_lds_sync();
+    lds_barrier();
 }
 
 // ops.rs:60-66
@@ -922,7 +913,7 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
     }
     n3_norm_gain(a, pre.post_gain, d, a, red, st);
     if (tid < d) xs[tid] = xs[tid] + p.gate * a[tid];
-    n3_lds_sync();
+    lds_barrier();
     n3_norm_gain(xs, pre.pre_gain, d, a, red, st);  // a = pre
     if (STAGED) {  // the factors and cond_v, copied into LDS as the tail began
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -943,7 +934,7 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
             const int e = tid + k * kN3Block;
             pv[k] = e < d * 8 ? a[e >> 3] * cv[e] : 0.0f;
         }
-        n3_lds_sync();
+        lds_barrier();
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int e = tid + k * kN3Block;
@@ -952,7 +943,7 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
                 cv[((i & 3) * 8 + r) * stride + (i >> 2)] = pv[k];
             }
         }
-        n3_lds_sync();
+        lds_barrier();
         if (tid < 32) {
             const int j = tid >> 3, n = (d - j + 3) / 4;
             const float* q = cv + tid * stride;
@@ -960,7 +951,7 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
             for (int k = n / 4 * 4; k < n; ++k) sum = sum + q[k];
             chains[j][tid & 7] = sum;
         }
-        n3_lds_sync();
+        lds_barrier();
         if (tid < 8) weights[tid] = (((0.0f + chains[0][tid]) + chains[1][tid]) + chains[2][tid]) + chains[3][tid];
     } else if (tid < p.rank) {
         float s = 0.0f;
@@ -2138,7 +2129,7 @@ __global__ __launch_bounds__(kN3Block) void n3_boundary_kernel(N3BoundaryParams 
                                                  16, 0, 0);
         }
     }
-    n3_lds_sync();  // the factors, cond_v and routing rows stay in flight
+    lds_barrier();  // the factors, cond_v and routing rows stay in flight
     const N3TailLds l{xs_, a_, sc_, st_, mx_, mod_, cv_, chains_, weights_, red, tin_s, tailw_s, stream_s, lane_s};
     if (p.tail) n3_tail<true>(t, l, rv, pre);  // the next stream into rv, then into stream_s
     if (p.tail) {
