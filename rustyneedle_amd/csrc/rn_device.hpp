@@ -209,6 +209,14 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// The same for the lanes of one wave (a one-wave block, or data a wave shares
+// with itself): its LDS writes are visible to its later LDS reads.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Cross-lane moves inside rows of 16 lanes (DPP: no LDS round trip). CTRL:
 // quad_perm [1,0,3,2] = 0xb1, quad_perm [2,3,0,1] = 0x4e, row_half_mirror =
 // 0x141, row_mirror = 0x140. A lane whose source is invalid keeps its value.

@@ -43,33 +43,6 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     __shared__ __align__(16) float sq_s[NORM ? K : 4];
 
     const int lane = threadIdx.x;
-    int si = 0;
-    for (int i = 1; i < p.nseg; ++i)
-        if ((int)blockIdx.x >= p.seg[i].block0) si = i;
-    const Segment sg = p.seg[si];
-    const int blk = (int)blockIdx.x - sg.block0;
-
-    auto row_of = [&](int rr) -> int {
-        if constexpr (EPI == kSilu) return rr < H ? blk * H + rr : p.half_rows + blk * H + (rr - H);
-        else return blk * ROWS + rr;
-    };
-    auto row_valid = [&](int rr) -> bool {
-        if constexpr (EPI == kSilu) return blk * H + (rr < H ? rr : rr - H) < p.half_rows;
-        else return blk * ROWS + rr < sg.rows;
-    };
-    // The row a lane loads from: past the end of the matrix it re-reads the last
-    // row (never stored), so loads need no condition.
-    auto row_load = [&](int rr) -> int {
-        if constexpr (EPI == kSilu) {
-            const int i = min(blk * H + (rr < H ? rr : rr - H), p.half_rows - 1);
-            return rr < H ? i : p.half_rows + i;
-        } else {
-            return min(blk * ROWS + rr, sg.rows - 1);
-        }
-    };
-    // load j of a lane covers chunk (64 j + lane) of the block's rows, in row-major order
-    auto load_row = [&](int j) -> int { return (64 * j + lane) / CPR; };
-    auto load_chunk = [&](int j) -> int { return (64 * j + lane) % CPR; };
 
     // Memory-level order matters: loads complete in issue order for the wait
     // counter, so the prologue inputs go first, then the weights, then the
@@ -110,6 +83,36 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         load_floats<E>(p.post_gain + lane * E, pg);
     }
     if constexpr (NORM) load_floats<E>(p.gain + lane * E, gv);
+
+    // the block's segment (after the input requests: its lookup reads further
+    // argument lines)
+    int si = 0;
+    for (int i = 1; i < p.nseg; ++i)
+        if ((int)blockIdx.x >= p.seg[i].block0) si = i;
+    const Segment sg = p.seg[si];
+    const int blk = (int)blockIdx.x - sg.block0;
+
+    auto row_of = [&](int rr) -> int {
+        if constexpr (EPI == kSilu) return rr < H ? blk * H + rr : p.half_rows + blk * H + (rr - H);
+        else return blk * ROWS + rr;
+    };
+    auto row_valid = [&](int rr) -> bool {
+        if constexpr (EPI == kSilu) return blk * H + (rr < H ? rr : rr - H) < p.half_rows;
+        else return blk * ROWS + rr < sg.rows;
+    };
+    // The row a lane loads from: past the end of the matrix it re-reads the last
+    // row (never stored), so loads need no condition.
+    auto row_load = [&](int rr) -> int {
+        if constexpr (EPI == kSilu) {
+            const int i = min(blk * H + (rr < H ? rr : rr - H), p.half_rows - 1);
+            return rr < H ? i : p.half_rows + i;
+        } else {
+            return min(blk * ROWS + rr, sg.rows - 1);
+        }
+    };
+    // load j of a lane covers chunk (64 j + lane) of the block's rows, in row-major order
+    auto load_row = [&](int j) -> int { return (64 * j + lane) / CPR; };
+    auto load_chunk = [&](int j) -> int { return (64 * j + lane) % CPR; };
 
     // 1b. weights: unconditional loads (a branch around a load would make the
     // wait counter unknowable and force a full wait)
@@ -153,17 +156,21 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
                 const int idx = lane * E + e;
                 sq_s[(idx % 8) * (K / 8) + idx / 8] = vals[e] * vals[e];
             }
-            __syncthreads();
+            wave_lds_sync();
             float s = 0.0f;
             if (lane < 8) {
+                // the whole run requested before the first add (one LDS round
+                // trip, not one per read)
                 const float4* run = reinterpret_cast<const float4*>(sq_s + lane * (K / 8));
+                float4 t[K / 32];
+#pragma unroll
+                for (int c = 0; c < K / 32; ++c) t[c] = run[c];
 #pragma unroll
                 for (int c = 0; c < K / 32; ++c) {
-                    const float4 t = run[c];
-                    s = s + t.x;
-                    s = s + t.y;
-                    s = s + t.z;
-                    s = s + t.w;
+                    s = s + t[c].x;
+                    s = s + t[c].y;
+                    s = s + t[c].z;
+                    s = s + t[c].w;
                 }
             }
             float total = sum_lanes_0_to_7(s);
@@ -184,7 +191,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
             if (blockIdx.x == 0)
 #pragma unroll
                 for (int e = 0; e < E; ++e) p.x_out[lane * E + e] = v[e];
-            __syncthreads();  // the runs are read before the next squares replace them
+            wave_lds_sync();  // the runs are read before the next squares replace them
         }
         if constexpr (NORM) {
             const float inverse = norm_inverse(v);
@@ -203,7 +210,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         quotients<E>(v, sx, y);
 #pragma unroll
         for (int e = 0; e < E; ++e) xq_s[lane * E + e] = (int8_t)code_of_quotient(y[e]);
-        __syncthreads();
+        wave_lds_sync();
 #pragma unroll
         for (int j = 0; j < NL; ++j) xc[j] = *reinterpret_cast<const int4*>(xq_s + load_chunk(j) * 16);
     }
@@ -215,7 +222,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         part = part + lane_xor_i<1>(part);  // the lane pair of a chunk (DPP)
         if ((lane & 1) == 0) acc_s[load_row(j) * G + load_chunk(j) / 2] = part;
     }
-    __syncthreads();
+    wave_lds_sync();
 
     // 4. sequential per-row epilogue (tree T4), one lane per row
     float total = 0.0f;
@@ -316,7 +323,7 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
     for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
     peak = wave_max(peak);
     if (lane == 0) peak_s[wave] = peak;
-    __syncthreads();
+    lds_barrier();
     peak = fmaxf(fmaxf(peak_s[0], peak_s[1]), fmaxf(peak_s[2], peak_s[3]));
     const float sx = int8_scale_from_peak(peak);
     float y[E];
@@ -324,9 +331,7 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
 #pragma unroll
     for (int e = 0; e < E; ++e) xq_s[wave * KW + lane * E + e] = (int8_t)code_of_quotient(y[e]);
     // the codes a lane dots were written by lanes of its own wave
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_lds_sync();
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
         const int4 xc = *reinterpret_cast<const int4*>(xq_s + wave * KW + load_chunk(j) * 16);
@@ -334,7 +339,7 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
         part = part + dpp_move<0xb1>(part);  // lane ^ 1 holds the other half of the group
         if ((lane & 1) == 0) acc_s[load_row(j) * G + wave * GW + load_chunk(j) / 2] = part;
     }
-    __syncthreads();
+    lds_barrier();
     if (mine) {
         const int4* arow = reinterpret_cast<const int4*>(acc_s + lane * G);
         float total = 0.0f;

@@ -70,27 +70,30 @@ struct Segment {
 };
 constexpr int kMaxSegments = 8;
 
+// The prologue's inputs come first: with the segment count they share the first
+// 64 bytes of the argument segment (one scalar-cache line), so a block requests
+// its input vector after one argument load.
 struct GemvParams {
-    Segment seg[kMaxSegments];
-    int nseg;
-    int half_rows;        // kSilu: ffn width (gate rows 0..half-1, up rows half..2*half-1)
     const float* x;       // input vector (kQuant/kNorm)
     const float* gain;    // zero-centred norm gains (kNorm/kEmbedNorm)
+    const float* attended;     // kCrossNorm: the cross-attention output and its post-norm gains
+    const float* post_gain;
+    DecodeState* state;   // kEmbedNorm: the token to embed
+    int nseg;
+    int half_rows;        // kSilu: ffn width (gate rows 0..half-1, up rows half..2*half-1)
     float eps;
+    float cross_gain;
     const int8_t* xq;     // kCodes: pre-quantised input
     const float* xs;
+    Segment seg[kMaxSegments];
     const int8_t* embW;   // kEmbedNorm: embedding codes/scales, the token comes from state
     const float* embS;
     float embed_scale;    // sqrt(d_model)
     int vocab;
     float* x_out;         // kEmbedNorm / kCrossNorm: block 0 writes the new residual row
     float* hidden_out;    // kNorm: block 0 writes the normed input (nullable)
-    DecodeState* state;   // kEmbedNorm: the token to embed
     unsigned long long* keys;  // kArgmax: one greedy key per block (argmax_key)
     DecodeState* advance;      // kArgmax: when set, block 0 moves pos and step on by one
-    const float* attended;     // kCrossNorm: the cross-attention output and its post-norm gains
-    const float* post_gain;
-    float cross_gain;
     const float* res;     // kResidual: the residual read (nullable: the stored row itself)
 };
 
