@@ -288,13 +288,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 512 ? 
                 vr[c] = *reinterpret_cast<const VPiece*>(V + (size_t)min(base + j + kClasses * c, rows - 1) * kHeadDim +
                                                          DPV * dg);
         }
+        // the weights of all slots are read from LDS before the slot tests (a
+        // read inside each test would be waited for before the next one)
+        float ew[VC];
+#pragma unroll
+        for (int c = 0; c < VC; ++c) ew[c] = scores[min(base + j + kClasses * c, last)];
 #pragma unroll
         for (int c = 0; c < VC; ++c) {
             const int pp = base + j + kClasses * c;
             // wave-uniform: the wave's classes hold no live position in this slot
             if (base + kClasses * c + (64 / TPC) * wave >= nglobal) continue;
             const bool ok = pp < nglobal;
-            const float e = scores[min(pp, last)];
+            const float e = ew[c];
             const uint32_t* vw = reinterpret_cast<const uint32_t*>(&vr[c]);
 #pragma unroll
             for (int i = 0; i < DPV; ++i) {

@@ -887,7 +887,7 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
                                                             int8_t* codes, float* scales, float* normed,
                                                             size_t x_stride) {
     constexpr int n = NV * 128;
-    extern __shared__ float sq_s[];  // [4][n + 8] when gain != nullptr
+    extern __shared__ float sq_s[];  // [4][n + 32] when gain != nullptr
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + wave;
     const bool live = row < count;
@@ -897,16 +897,17 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
     for (int i = 0; i < NV; ++i) v[i] = src[lane + 64 * i];
     float peak = 0.0f;
     if (gain != nullptr) {
-        // run r of the squares at sq[r * (run + 1)]: the 8 chain lanes read 8 banks
-        constexpr int run = n >> 3;
-        float* sq = sq_s + wave * (n + 8);
+        // run r of the squares at sq[r * (run + 4)]: 16-byte aligned runs whose
+        // 128-bit reads by the 8 chain lanes fall in distinct banks
+        constexpr int run = n >> 3, stride = run + 4;
+        float* sq = sq_s + wave * (n + 32);
         const float2* g2 = reinterpret_cast<const float2*>(gain);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int e = 2 * (lane + 64 * i);  // elements e, e+1; e % 8 is 0, 2, 4 or 6
             const int p = e & 7, c = e >> 3;
-            sq[(p + 0) * (run + 1) + c] = v[i].x * v[i].x;
-            sq[(p + 1) * (run + 1) + c] = v[i].y * v[i].y;
+            sq[(p + 0) * stride + c] = v[i].x * v[i].x;
+            sq[(p + 1) * stride + c] = v[i].y * v[i].y;
         }
         // the gained values and their peak while the squares are summed: the
         // normed value is fl(m * inverse) with inverse > 0 and rounding is
@@ -919,12 +920,26 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
             peak = fmaxf(peak, fmaxf(fabsf(v[i].x), fabsf(v[i].y)));
         }
         peak = wave_max(peak);
-        __syncthreads();
+        wave_lds_sync();  // each wave reads only its own row's squares
         float part = 0.0f;
         if (lane < 8) {
-            const float* r = sq + lane * (run + 1);
-#pragma unroll 16
-            for (int c = 0; c < run; ++c) part = part + r[c];
+            // the run in 128-bit reads, each group of CH requested before its adds
+            constexpr int R4 = run / 4, CH = R4 % 16 == 0 ? 16 : (R4 % 12 == 0 ? 12 : 4);
+            static_assert(R4 % CH == 0, "whole groups of reads");
+            const float4* r4 = reinterpret_cast<const float4*>(sq + lane * stride);
+#pragma unroll
+            for (int c0 = 0; c0 < R4; c0 += CH) {
+                float4 t[CH];
+#pragma unroll
+                for (int c = 0; c < CH; ++c) t[c] = r4[c0 + c];
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    part = part + t[c].x;
+                    part = part + t[c].y;
+                    part = part + t[c].z;
+                    part = part + t[c].w;
+                }
+            }
         }
         float total = sum_lanes_0_to_7(part);
         total = total + 0.0f;  // the empty tail of the 8-lane sum
@@ -960,7 +975,7 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
 hipError_t launch_norm_quantise(const float* x, const float* gain, int count, int n, float eps, int8_t* codes,
                                 float* scales, float* normed, hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    const size_t lds = gain != nullptr ? 4 * sizeof(float) * (size_t)(n + 8) : 0;
+    const size_t lds = gain != nullptr ? 4 * sizeof(float) * (size_t)(n + 32) : 0;
     const dim3 grid((count + 3) / 4), block(256);
 #define RN_NQ(NV) \
     rn_launch(norm_quantise_kernel<NV>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed, (size_t)n)
