@@ -783,13 +783,13 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
         }
         float total = sum_lanes_0_to_7(s);
         total = total + 0.0f;  // the (empty) tail of ops.rs:15-16
-        const float inverse = 1.0f / sqrtf(total / (float)K + p.eps);
+        const float inverse = reciprocal(sqrtf(total / (float)K + p.eps));
 #pragma unroll
         for (int e = 0; e < E; ++e) v[e] = ((1.0f + gv[e]) * v[e]) * inverse;
         float peak = 0.0f;
 #pragma unroll
         for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
-        peak = wave_max(peak);
+        peak = wave_max_nonneg(peak);
         const float sx = int8_scale_from_peak(peak);
         float y[E];
         quotients<E>(v, sx, y);

@@ -186,6 +186,14 @@ __device__ __forceinline__ float reciprocal_normal(float x) {
     return __builtin_fmaf(__builtin_fmaf(-x, r, 1.0f), r, r);
 }
 
+// 1.0f / x for every float: reciprocal_normal inside its range, the IEEE
+// division outside it (zero, infinity, NaN, the extremes), on the lanes that
+// need it.
+__device__ __forceinline__ float reciprocal(float x) {
+    if (__builtin_expect(x >= 0x1p-126f && x < 0x1p126f, 1)) return reciprocal_normal(x);
+    return 1.0f / x;
+}
+
 // ops.rs:103-110: peak / 127 (1.0 when the peak is not positive). The quotient
 // is formed without a division: q0 = peak * RN(1/127), then one fma correction
 // with the exact residual peak - 127 q0; the result equals the correctly
@@ -275,6 +283,23 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, __int_as_float(dpp_move<0x141>(__float_as_int(v))));
     v = fmaxf(v, __int_as_float(dpp_move<0x140>(__float_as_int(v))));
     return fmaxf(fmaxf(lane_float(v, 0), lane_float(v, 16)), fmaxf(lane_float(v, 32), lane_float(v, 48)));
+}
+
+// wave_max for values that are never negative or NaN (the peaks of |x| built
+// by fmaxf from 0, which drops NaN): their bit patterns order as the values
+// do, so the steps are integer maxima, which the compiler folds with their
+// lane moves into one DPP instruction each.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    // (bound_ctrl: a lane without a source would read 0, the identity of the
+    // maximum; these lane patterns give every lane a source)
+    uint32_t u = __float_as_uint(v);
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0xb1, 0xf, 0xf, true));
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x4e, 0xf, 0xf, true));
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x141, 0xf, 0xf, true));
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x140, 0xf, 0xf, true));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)u, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)u, 16),
+                   c = (uint32_t)__builtin_amdgcn_readlane((int)u, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)u, 48);
+    return __uint_as_float(max(max(a, b), max(c, d)));
 }
 
 template <int CTRL>

@@ -174,7 +174,7 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
                     v[e] = (1.0f + gv[e]) * v[e];
                     peak = fmaxf(peak, fabsf(v[e]));
                 }
-                peak = wave_max(peak);
+                peak = wave_max_nonneg(peak);
                 // a wave's own squares: DS operations of a wave complete in order
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
@@ -193,14 +193,14 @@ __global__ __launch_bounds__(1024) void gemm_split_kernel(GemmParams p) {
                 }
                 float total = sum_lanes_0_to_7(part);
                 total = total + 0.0f;  // the empty tail of the 8-lane sum
-                const float inverse = 1.0f / sqrtf(total / (float)K + p.eps);
+                const float inverse = reciprocal(sqrtf(total / (float)K + p.eps));
 #pragma unroll
                 for (int e = 0; e < E; ++e) v[e] = v[e] * inverse;
                 peak = peak * inverse;
             } else {
 #pragma unroll
                 for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
-                peak = wave_max(peak);
+                peak = wave_max_nonneg(peak);
             }
             const float scale = int8_scale_from_peak(peak);
             float y[E];
@@ -919,7 +919,7 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
             v[i].y = (1.0f + g.y) * v[i].y;
             peak = fmaxf(peak, fmaxf(fabsf(v[i].x), fabsf(v[i].y)));
         }
-        peak = wave_max(peak);
+        peak = wave_max_nonneg(peak);
         wave_lds_sync();  // each wave reads only its own row's squares
         float part = 0.0f;
         if (lane < 8) {
@@ -943,7 +943,7 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
         }
         float total = sum_lanes_0_to_7(part);
         total = total + 0.0f;  // the empty tail of the 8-lane sum
-        const float inverse = 1.0f / sqrtf(total / (float)n + eps);
+        const float inverse = reciprocal(sqrtf(total / (float)n + eps));
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             v[i].x = v[i].x * inverse;
@@ -954,7 +954,7 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
     } else {
 #pragma unroll
         for (int i = 0; i < NV; ++i) peak = fmaxf(peak, fmaxf(fabsf(v[i].x), fabsf(v[i].y)));
-        peak = wave_max(peak);
+        peak = wave_max_nonneg(peak);
     }
     const float scale = int8_scale_from_peak(peak);
     if (!live) return;  // the whole wave: one row per wave

@@ -176,7 +176,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
             float total = sum_lanes_0_to_7(s);
             total = total + 0.0f;  // the (empty) tail of ops.rs:15-16
             const float mean_square = total / (float)K;
-            return 1.0f / sqrtf(mean_square + p.eps);
+            return reciprocal(sqrtf(mean_square + p.eps));
         };
         if constexpr (PRO == kEmbedNorm) {
             if (blockIdx.x == 0)
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         float peak = 0.0f;
 #pragma unroll
         for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
-        peak = wave_max(peak);
+        peak = wave_max_nonneg(peak);
         sx = int8_scale_from_peak(peak);
         float y[E];
         quotients<E>(v, sx, y);
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(256) void gemv_splitk_kernel(GemvParams p) {
     float peak = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
-    peak = wave_max(peak);
+    peak = wave_max_nonneg(peak);
     if (lane == 0) peak_s[wave] = peak;
     lds_barrier();
     peak = fmaxf(fmaxf(peak_s[0], peak_s[1]), fmaxf(peak_s[2], peak_s[3]));

@@ -44,10 +44,10 @@ __global__ __launch_bounds__(256) void lanes_prologue_kernel(const float* stream
 #pragma unroll
     for (int j = 0; j < 8; ++j) total = total + lanes_s[j];
     total = total + 0.0f;  // the empty tail (n is a multiple of 8)
-    const float inverse = 1.0f / sqrtf(total / (float)n + 1e-6f);
+    const float inverse = reciprocal(sqrtf(total / (float)n + 1e-6f));
     float peak = 0.0f;
     for (int i = tid; i < n; i += kLaneThreads) peak = fmaxf(peak, fabsf(v[i] * inverse));
-    peak = wave_max(peak);
+    peak = wave_max_nonneg(peak);
     if (lane == 0) peak_s[wave] = peak;
     __syncthreads();
     peak = fmaxf(fmaxf(peak_s[0], peak_s[1]), fmaxf(peak_s[2], peak_s[3]));

@@ -34,7 +34,7 @@ __device__ void norm_row(const float* v, const float* gain, int n, float eps, fl
     for (int j = 0; j < 8; ++j) total = total + lanes_s[j];
     total = total + 0.0f;
     const float mean_square = total / (float)n;
-    const float inverse = 1.0f / sqrtf(mean_square + eps);
+    const float inverse = reciprocal(sqrtf(mean_square + eps));
     for (int i = lane; i < n; i += kRowThreads) out[i] = ((1.0f + gain[i]) * v[i]) * inverse;
 }
 
@@ -62,7 +62,7 @@ __global__ __launch_bounds__(64) void quantise_rows_kernel(const float* x, int n
     const float* row = x + (size_t)blockIdx.x * n;
     float peak = 0.0f;
     for (int i = threadIdx.x; i < n; i += kRowThreads) peak = fmaxf(peak, fabsf(row[i]));
-    peak = wave_max(peak);
+    peak = wave_max_nonneg(peak);
     const float scale = int8_scale_from_peak(peak);
     for (int i0 = 0; i0 < n; i0 += kRowThreads) {  // uniform trip count: every lane reaches the wave vote
         const int i = i0 + threadIdx.x;

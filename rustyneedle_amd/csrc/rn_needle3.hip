@@ -202,7 +202,7 @@ __device__ float n3_sum_of_squares(const float* v, int n, float* red, float* sq 
 // ops.rs:44-58: out = ((1 + gain) * x) * inverse (out may be x)
 __device__ void n3_norm(const float* x, const float* gain, int n, float* out, float* red, float* sq = nullptr) {
     const float mean_square = n3_sum_of_squares(x, n, red, sq) / (float)n;
-    const float inverse = 1.0f / sqrtf(mean_square + 1e-6f);
+    const float inverse = reciprocal(sqrtf(mean_square + 1e-6f));
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = ((1.0f + gain[i]) * x[i]) * inverse;
     __syncthreads();
 }
@@ -210,7 +210,7 @@ __device__ void n3_norm(const float* x, const float* gain, int n, float* out, fl
 // n3_norm for n <= blockDim.x with thread i's gain in a register
 __device__ void n3_norm_gain(const float* x, float gain, int n, float* out, float* red, float* sq) {
     const float mean_square = n3_sum_of_squares(x, n, red, sq) / (float)n;
-    const float inverse = 1.0f / sqrtf(mean_square + 1e-6f);
+    const float inverse = reciprocal(sqrtf(mean_square + 1e-6f));
     const int i = threadIdx.x;
     if (i < n) out[i] = ((1.0f + gain) * x[i]) * inverse;
     lds_barrier();
@@ -218,7 +218,7 @@ __device__ void n3_norm_gain(const float* x, float gain, int n, float* out, floa
 
 // ops.rs:60-66
 __device__ void n3_unit_rms(const float* x, int n, float* out, float* red, float* sq = nullptr) {
-    const float inverse = 1.0f / sqrtf(n3_sum_of_squares(x, n, red, sq) / (float)n + 1e-6f);
+    const float inverse = reciprocal(sqrtf(n3_sum_of_squares(x, n, red, sq) / (float)n + 1e-6f));
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inverse;
     __syncthreads();
 }
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(64) void n3_qkv_kernel(N3QkvParams p) {
         __syncthreads();
         float ss = 0.0f;
         for (int j = 0; j < 8; ++j) ss = ss + red[j];
-        const float inverse = 1.0f / sqrtf(ss / (float)kN3Head + 1e-6f);
+        const float inverse = reciprocal(sqrtf(ss / (float)kN3Head + 1e-6f));
         const float* gain = which == 0 ? p.q_norm : p.k_norm;
         v = ((1.0f + gain[lane]) * v) * inverse;
         __syncthreads();
@@ -1376,7 +1376,7 @@ __device__ void n3_norm_codes(const float* v, const float* gain, int n, float* r
     __syncthreads();
     float total = 0.0f;
     for (int j = 0; j < 8; ++j) total = total + red[j];
-    const float inverse = 1.0f / sqrtf(total / (float)n + 1e-6f);
+    const float inverse = reciprocal(sqrtf(total / (float)n + 1e-6f));
     float r = red[16 + min(lane, waves - 1)];
     r = fmaxf(r, lane_xor<1>(r));
     r = fmaxf(r, lane_xor<2>(r));
@@ -1743,7 +1743,7 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     if (wave < 2) {
         float ss = 0.0f;
         for (int j = 0; j < 8; ++j) ss = ss + red_s[which][j];
-        const float inverse = 1.0f / sqrtf(ss / (float)kN3Head + 1e-6f);
+        const float inverse = reciprocal(sqrtf(ss / (float)kN3Head + 1e-6f));
         v = ((1.0f + gain) * v) * inverse;
     }
     __syncthreads();

@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void head_codes_kernel(HeadCodesParams p) {
         for (int c = 0; c < 8; ++c) s = s + __shfl(sq, 8 * c + (lane & 7), kWave);
         float total = sum_lanes_0_to_7(s);
         total = total + 0.0f;
-        const float inverse = 1.0f / sqrtf(total / 64.0f + p.eps);
+        const float inverse = reciprocal(sqrtf(total / 64.0f + p.eps));
         v = ((1.0f + sec.gain[lane]) * v) * inverse;
     }
     if (sec.rotary) {
@@ -636,13 +636,13 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
         }
         float total = sum_lanes_0_to_7(s);
         total = total + 0.0f;  // the (empty) tail of ops.rs:15-16
-        const float inverse = 1.0f / sqrtf(total / (float)K + p.eps);
+        const float inverse = reciprocal(sqrtf(total / (float)K + p.eps));
 #pragma unroll
         for (int e = 0; e < E; ++e) v[e] = ((1.0f + gv[e]) * v[e]) * inverse;
         float peak = 0.0f;
 #pragma unroll
         for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
-        peak = wave_max(peak);
+        peak = wave_max_nonneg(peak);
         const float sx = int8_scale_from_peak(peak);
         float y[E];
         quotients<E>(v, sx, y);
@@ -706,7 +706,7 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
         for (int c = 0; c < 8; ++c) s = s + __shfl(sq, 8 * c + (lane & 7), kWave);
         float total = sum_lanes_0_to_7(s);
         total = total + 0.0f;
-        const float inverse = 1.0f / sqrtf(total / 64.0f + p.eps);
+        const float inverse = reciprocal(sqrtf(total / 64.0f + p.eps));
         q = ((1.0f + qgain) * q) * inverse;
         const float scale = int8_scale_from_peak(wave_max(fabsf(q)));
         float y;
