@@ -329,7 +329,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 512 ? 
             o = o + part_s[k][tid];
             t = t + total_s[k];
         }
-        const float inverse = 1.0f / t;
+        const float inverse = reciprocal(t);
         out[tid] = o * inverse;
     }
 }
@@ -525,7 +525,7 @@ __global__ __launch_bounds__(256) void attend_prefill_tile_kernel(AttendParams p
                 o = o + part_s[q][k][d];
                 t = t + total_s[q][k];
             }
-            const float inverse = 1.0f / t;
+            const float inverse = reciprocal(t);
             p.out[(size_t)(t0 + q) * p.d_model + h * kHeadDim + d] = o * inverse;
         }
     }
@@ -973,7 +973,7 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
             o = o + part_s[k][tid];
             t = t + total_s[k];
         }
-        p.out[h * kHeadDim + tid] = o * (1.0f / t);
+        p.out[h * kHeadDim + tid] = o * reciprocal(t);
     }
 }
 

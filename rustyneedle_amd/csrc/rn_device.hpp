@@ -79,8 +79,27 @@ __device__ __forceinline__ float libm_expf(float x) {
     return (float)(y * s);
 }
 
+// 1.0f / x correctly rounded, for x in [2^-126, 2^126) (positive normal with a
+// normal reciprocal): r = v_rcp_f32(x) (within one ulp), then one Newton step
+// with fused multiply-adds, r + r (1 - x r). Equal to the IEEE division on
+// every float of that range (all 2^31 - 2^25 of them, tests/test_reciprocal.py);
+// callers keep x inside it. Three dependent operations against the division's
+// nine.
+__device__ __forceinline__ float reciprocal_normal(float x) {
+    const float r = __builtin_amdgcn_rcpf(x);
+    return __builtin_fmaf(__builtin_fmaf(-x, r, 1.0f), r, r);
+}
+
+// 1.0f / x for every float: reciprocal_normal inside its range, the IEEE
+// division outside it (zero, infinity, NaN, the extremes), on the lanes that
+// need it.
+__device__ __forceinline__ float reciprocal(float x) {
+    if (__builtin_expect(x >= 0x1p-126f && x < 0x1p126f, 1)) return reciprocal_normal(x);
+    return 1.0f / x;
+}
+
 // ops.rs:68-71 with the C library's expf.
-__device__ __forceinline__ float libm_sigmoid(float value) { return 1.0f / (1.0f + libm_expf(-value)); }
+__device__ __forceinline__ float libm_sigmoid(float value) { return reciprocal(1.0f + libm_expf(-value)); }
 
 // The (1/c, log c) pairs of the 16 subintervals of [0x1.66p-1, 0x1.66p0) in
 // which the mantissa of x is reduced (rounded to double, as published with the
@@ -173,25 +192,6 @@ __device__ __forceinline__ void quotients(const float* v, float scale, float* y)
 #pragma unroll
         for (int e = 0; e < E; ++e) y[e] = v[e] / scale;
     }
-}
-
-// 1.0f / x correctly rounded, for x in [2^-126, 2^126) (positive normal with a
-// normal reciprocal): r = v_rcp_f32(x) (within one ulp), then one Newton step
-// with fused multiply-adds, r + r (1 - x r). Equal to the IEEE division on
-// every float of that range (all 2^31 - 2^25 of them, tests/test_reciprocal.py);
-// callers keep x inside it. Three dependent operations against the division's
-// nine.
-__device__ __forceinline__ float reciprocal_normal(float x) {
-    const float r = __builtin_amdgcn_rcpf(x);
-    return __builtin_fmaf(__builtin_fmaf(-x, r, 1.0f), r, r);
-}
-
-// 1.0f / x for every float: reciprocal_normal inside its range, the IEEE
-// division outside it (zero, infinity, NaN, the extremes), on the lanes that
-// need it.
-__device__ __forceinline__ float reciprocal(float x) {
-    if (__builtin_expect(x >= 0x1p-126f && x < 0x1p126f, 1)) return reciprocal_normal(x);
-    return 1.0f / x;
 }
 
 // ops.rs:103-110: peak / 127 (1.0 when the peak is not positive). The quotient

@@ -740,7 +740,7 @@ __global__ __launch_bounds__(256) void n3_attend_kernel(N3AttendParams p) {
         float total = (lanes_s[0] + lanes_s[1]) + (lanes_s[2] + lanes_s[3]);
         for (int pp = vector_count; pp < count; ++pp) total = total + c_s[pp];
         float o = cpeak > 0.0f ? (float)sum * scale : 0.0f;
-        o = o * (1.0f / total);
+        o = o * reciprocal(total);
         o = o * libm_sigmoid(gate[(size_t)h * kN3Head + tid]);
         out[(size_t)h * kN3Head + tid] = o;
     }
@@ -966,7 +966,7 @@ __device__ void n3_tail(const N3BlockOutParams& p, const N3TailLds& l, float* ke
         const float e = fast_exp(w - peak);
         float total = 0.0f;
         for (int r = 0; r < R; ++r) total = total + lane_float(e, r);
-        const float inverse = 1.0f / total;
+        const float inverse = reciprocal(total);
         if (tid < R) weights[tid] = e * inverse;
     }
     __syncthreads();
@@ -1150,7 +1150,7 @@ __global__ __launch_bounds__(256) void n3_readout_kernel(const float* weighted, 
     __shared__ float v[kN3MaxWidth];
     __shared__ float red[32];
     const int slot = blockIdx.x;
-    const float inverse = 1.0f / total[slot];
+    const float inverse = reciprocal(total[slot]);
     for (int i = threadIdx.x; i < width; i += blockDim.x) v[i] = weighted[(size_t)slot * width + i] * inverse;
     __syncthreads();
     n3_unit_rms(v, width, v, red);
@@ -1178,7 +1178,7 @@ __global__ __launch_bounds__(256) void n3_pool_kernel(const float* readouts, int
             w[s] = fast_exp(w[s] - peak);
             t = t + w[s];
         }
-        const float inverse = 1.0f / t;
+        const float inverse = reciprocal(t);
         for (int s = 0; s < slots; ++s) w[s] = w[s] * inverse;
     }
     __syncthreads();
@@ -1885,7 +1885,7 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         float total = (lanes_s[0] + lanes_s[1]) + (lanes_s[2] + lanes_s[3]);
         for (int pp = vector_count; pp < count; ++pp) total = total + c_s[pp];
         float o = cpeak > 0.0f ? (float)sum * scale : 0.0f;
-        o = o * (1.0f / total);
+        o = o * reciprocal(total);
         o = o * libm_sigmoid(y_s[192 + tid]);
         p.out[(size_t)h * kN3Head + tid] = o;
     }

@@ -242,7 +242,7 @@ __global__ __launch_bounds__(1024) void int8_attend_one_kernel(Int8AttendParams 
     float total = 0.0f;
 #pragma unroll
     for (int c = 0; c < 32; ++c) total = total + tot_s[c];
-    const float inverse = 1.0f / total;
+    const float inverse = reciprocal(total);
 #pragma unroll
     for (int c = 0; c < EP; ++c) {
         const int j = tid + NT * c;
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(512) void int8_attend_tile_kernel(Int8AttendParams 
         float total = 0.0f;
 #pragma unroll
         for (int c = 0; c < 32; ++c) total = total + tot_s[tid][c];
-        inv_s[tid] = 1.0f / total;
+        inv_s[tid] = reciprocal(total);
     }
     __syncthreads();
     {
@@ -761,7 +761,7 @@ __global__ __launch_bounds__(1024) void cross_attend_kernel(CrossAttendParams p)
         float total = 0.0f;
 #pragma unroll
         for (int c = 0; c < 32; ++c) total = total + lane_float(ct, c);
-        const float inverse = 1.0f / total;
+        const float inverse = reciprocal(total);
 #pragma unroll
         for (int k = 0; k < kCrossRows / kWave; ++k) {
             const int r = lane + kWave * k;
