@@ -69,12 +69,14 @@ namespace {
 
 // The maximum over the block (every thread calls; all get the result). With
 // TAIL false the caller's next barrier must come before red is written again.
-template <bool TAIL = true>
+// LDS: the barriers wait for LDS operations only (callers whose threads share
+// data through LDS only; global loads in flight stay in flight).
+template <bool TAIL = true, bool LDS = false>
 __device__ float n3_block_max(float v, float* red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = (blockDim.x + 63) >> 6;
     v = wave_max(v);
     if (lane == 0) red[wave] = v;
-    __syncthreads();
+    if constexpr (LDS) lds_barrier(); else __syncthreads();
     // the waves' maxima (at most 16) on a row of lanes (the rest repeat the
     // last), joined inside the row
     float r = red[min(lane, waves - 1)];
@@ -83,7 +85,9 @@ __device__ float n3_block_max(float v, float* red) {
     r = fmaxf(r, lane_xor<4>(r));
     r = fmaxf(r, lane_xor<8>(r));
     r = lane_float(r, 0);
-    if (TAIL) __syncthreads();
+    if (TAIL) {
+        if constexpr (LDS) lds_barrier(); else __syncthreads();
+    }
     return r;
 }
 
@@ -1474,7 +1478,7 @@ __device__ void n3_stage_rows(const CodebookParams& c, RowOf row_of, int R, uint
 // take the rows in turn, KR at a time. A group's runs sit on aligned lanes
 // and join by DPP. No branch inside the loops but uniform ones: groups past
 // the row's last add an exact zero (level, norm and scale all zero).
-template <int IB, int KR>
+template <int IB, int KR, bool LDS = false>
 __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R, const int4* xq,
                            const float* xs, int* acc, float* y) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
@@ -1535,7 +1539,7 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
             }
         }
     }
-    __syncthreads();
+    if constexpr (LDS) lds_barrier(); else __syncthreads();
     const bool fma_form = c.bits == 2;  // panel.rs:184-188; else neon.rs:158,180
     const float lscale = c.lscale;
     for (int r = threadIdx.x; r < R; r += blockDim.x) {
@@ -1564,27 +1568,30 @@ __device__ void n3_rows_ib(const CodebookParams& c, const uint8_t* w, const uint
         }
         y[r] = t;
     }
-    __syncthreads();
+    if constexpr (LDS) lds_barrier(); else __syncthreads();
 }
 
-template <int IB>
+template <int IB, bool LDS>
 __device__ __forceinline__ void n3_rows_kr(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R,
                                            const int4* xq, const float* xs, int* acc, float* y) {
     const int waves = blockDim.x >> 6, kr = (R + waves - 1) / waves;
     if (kr <= 1)
-        n3_rows_ib<IB, 1>(c, w, nm, R, xq, xs, acc, y);
+        n3_rows_ib<IB, 1, LDS>(c, w, nm, R, xq, xs, acc, y);
     else if (kr <= 2)
-        n3_rows_ib<IB, 2>(c, w, nm, R, xq, xs, acc, y);
+        n3_rows_ib<IB, 2, LDS>(c, w, nm, R, xq, xs, acc, y);
     else
-        n3_rows_ib<IB, 4>(c, w, nm, R, xq, xs, acc, y);
+        n3_rows_ib<IB, 4, LDS>(c, w, nm, R, xq, xs, acc, y);
 }
 
+// LDS: the barriers wait for LDS operations only (w, nm, xq, xs, acc and y in
+// LDS, or y in memory that no thread of the block reads back).
+template <bool LDS = false>
 __device__ void n3_rows(const CodebookParams& c, const uint8_t* w, const uint16_t* nm, int R, const int4* xq,
                         const float* xs, int* acc, float* y) {
     if (c.bits == 4)
-        n3_rows_kr<4>(c, w, nm, R, xq, xs, acc, y);
+        n3_rows_kr<4, LDS>(c, w, nm, R, xq, xs, acc, y);
     else
-        n3_rows_kr<2>(c, w, nm, R, xq, xs, acc, y);
+        n3_rows_kr<2, LDS>(c, w, nm, R, xq, xs, acc, y);
 }
 
 struct N3AttentionParams {
@@ -1614,7 +1621,11 @@ constexpr int kN3MaxTaps = 4;
 // block needs is issued first (its 256 projection rows and norms, the input
 // codes, the conv taps and ring samples, the norm gains and rotary row, and
 // the cached keys and values of the earlier positions, which no block writes
-// here); the new position's key and value come from LDS.
+// here); the new position's key and value come from LDS. Its threads share
+// data through LDS only (the cache rows and ring samples it stores are not read
+// back), so its barriers wait for LDS operations and leave global loads (the
+// staged values' LDS copies included, which each wave waits for itself before
+// the barrier that publishes them) in flight.
 __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3AttentionParams p) {
     __shared__ __align__(16) uint8_t w_s[256 * kN3HeadRowBytes];
     __shared__ uint16_t nm_s[256 * 16];
@@ -1640,7 +1651,12 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     // are four ranges of 64 (q rows, its kv head's k and v rows, gate rows),
     // staged one after another.
     const int chunks = p.qkvg.row_bytes / 16, per_range = 64 * chunks;
-    auto range_row = [&](int j) { return j == 0 ? h * 64 : j == 1 ? qw + kvh * 64 : j == 2 ? qw + kw + kvh * 64 : qw + 2 * kw + h * 64; };
+    // the first row of range rj: uniform steps added per lane (neither a branch
+    // nor a lookup table in memory)
+    const int row0 = h * 64, step1 = qw + kvh * 64 - row0, step2 = kw, step3 = kw + (h - kvh) * 64;
+    auto range_row = [&](int rj) {
+        return row0 + (rj >= 1 ? step1 : 0) + (rj >= 2 ? step2 : 0) + (rj >= 3 ? step3 : 0);
+    };
     int4 rw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1655,26 +1671,43 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         const int rj = (i >= per) + (i >= 2 * per) + (i >= 3 * per);
         rn[j] = p.qkvg.norms[(size_t)range_row(rj) * G + (i - rj * per)];
     }
-    int4 code = make_int4(0, 0, 0, 0);
-    if (tid < P / 16) code = p.codes[tid];
-    const float code_scale = tid < G ? p.code_scales[tid] : 0.0f;
+    // (the small inputs below are requested by the waves that use them only:
+    // every 16-byte request of a wave takes the CU's load path whether or not
+    // its lanes share an address)
+    int4 code_any = make_int4(0, 0, 0, 0);
+    float code_scale_any = 0.0f;
+    if (wave == 0) {
+        code_any = p.codes[min(tid, P / 16 - 1)];
+        code_scale_any = p.code_scales[min(tid, G - 1)];
+    }
     // conv taps, ring samples, norm gain and rotary row of waves 0, 1, 2 (q, k, v)
     const int which = wave < 3 ? wave : 0;
     const int head = which == 0 ? h : kvh;
     const int width = which == 0 ? qw : kw, off = which == 0 ? 0 : (which == 1 ? qw : qw + kw);
     const int col = head * kN3Head + lane;
-    const int ntap = min(p.ntaps, p.position + 1);
-    const float* const tap = which == 0 ? p.taps[0] : which == 1 ? p.taps[1] : p.taps[2];
-    float gains[kN3MaxTaps], samples[kN3MaxTaps];
-#pragma unroll
-    for (int t = 0; t < kN3MaxTaps; ++t) {
-        gains[t] = (wave < 3 && t < ntap) ? tap[(size_t)t * width + col] : 0.0f;
-        samples[t] = (wave < 3 && t >= 1 && t < ntap)
-                         ? p.hist[(size_t)((p.position - t) % p.ntaps) * width_all + off + col]
-                         : 0.0f;
-    }
-    const float gain = wave < 2 ? (which == 0 ? p.q_norm : p.k_norm)[lane] : 0.0f;
+    // (every wave requests them, from indices that exist: with no taps the
+    // loads read the norm gains instead and are not used; a load under a
+    // condition would be sunk into a branch and waited for there)
+    const bool has_taps = p.ntaps > 0;
+    const int ntap = has_taps ? min(p.ntaps, p.position + 1) : 0;
+    const float* const tap = !has_taps ? p.q_norm : which == 0 ? p.taps[0] : which == 1 ? p.taps[1] : p.taps[2];
+    const float* const ring = has_taps ? p.hist : p.q_norm;
+    float gains[kN3MaxTaps], samples[kN3MaxTaps];  // set and used by waves 0..2
+    // the norm gain and rotary row (used by waves 0 and 1): every wave
+    // requests them, unconditionally (a value chosen by a branch would bring
+    // the 1 + gain of its use into the branch, and its wait with it)
+    const float gain = (which == 0 ? p.q_norm : p.k_norm)[lane];
     const float cs = p.cos_row[lane & 31], sn = p.sin_row[lane & 31];
+    if (wave < 3) {
+#pragma unroll
+        for (int t = 0; t < kN3MaxTaps; ++t) {
+            const int tc = has_taps ? min(t, ntap - 1) : 0;
+            const float g = tap[has_taps ? (size_t)tc * width + col : (size_t)lane];
+            const float sm = ring[has_taps ? (size_t)((p.position - tc) % p.ntaps) * width_all + off + col : (size_t)lane];
+            gains[t] = g;    // used for t < ntap only
+            samples[t] = sm;  // used for 1 <= t < ntap only
+        }
+    }
     // the first 1024 earlier positions' keys and values as 16-byte units (unit u
     // = 1024 k + tid: quarter u % 4 of position u / 4, so a wave's request is 1
     // KB in a row and a position's four quarters sit on one quad), and each
@@ -1687,6 +1720,22 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     const float* ks = p.key_scales + (size_t)kvh * p.cap + p.first;
     const float* vsc = p.value_scales + (size_t)kvh * p.cap + p.first;
     const int early = min(last, kN3StagedPositions), clampp = max(last - 1, 0);
+    // ---- the head's projection rows (stored unconditionally: every index is
+    // inside w_s and nm_s, and units past the rows hold clamped copies that
+    // are never read; a store under a condition takes its load into a branch
+    // that waits for it alone)
+    static_assert(4 * kN3AttendThreads * 16 <= sizeof(w_s) && 4 * kN3AttendThreads <= 256 * 16, "staging fits");
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = j * kN3AttendThreads + tid;
+        reinterpret_cast<int4*>(w_s)[i] = rw[j];
+        nm_s[i] = rn[j];
+    }
+    if (tid < P / 16) xq[tid] = code_any;
+    if (tid < G) xs[tid] = code_scale_any;
+    // the keys are requested after the staged rows arrive (a wait counts
+    // loads in issue order: keys requested first would delay the rows), and
+    // stream in during the row products
     int4 ku[4];
     float ksr[4];
 #pragma unroll
@@ -1695,17 +1744,8 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         ku[k] = reinterpret_cast<const int4*>(kbase + (size_t)pos * kN3Head)[u & 3];
         ksr[k] = ks[pos];
     }
-    // ---- the head's projection rows
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = j * kN3AttendThreads + tid;
-        if (i < 256 * chunks) reinterpret_cast<int4*>(w_s)[i] = rw[j];
-        if (i < 256 * G) nm_s[i] = rn[j];
-    }
-    if (tid < P / 16) xq[tid] = code;
-    if (tid < G) xs[tid] = code_scale;
-    __syncthreads();
-    n3_rows(p.qkvg, w_s, nm_s, 256, xq, xs, acc, y_s);
+    lds_barrier();
+    n3_rows<true>(p.qkvg, w_s, nm_s, 256, xq, xs, acc, y_s);
     // the rows are done: the values of the staged positions are requested now
     // (they arrive during the next phases; w_s then takes them, [position][64],
     // and nm_s their scales)
@@ -1733,22 +1773,22 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         }
         v_s[which][lane] = v;
     }
-    __syncthreads();
+    lds_barrier();
     if (wave < 2 && lane < 8) {
         float s = 0.0f;
         for (int c = 0; c < kN3Head / 8; ++c) s = s + v_s[which][8 * c + lane] * v_s[which][8 * c + lane];
         red_s[which][lane] = s;
     }
-    __syncthreads();
+    lds_barrier();
     if (wave < 2) {
         float ss = 0.0f;
         for (int j = 0; j < 8; ++j) ss = ss + red_s[which][j];
         const float inverse = reciprocal(sqrtf(ss / (float)kN3Head + 1e-6f));
         v = ((1.0f + gain) * v) * inverse;
     }
-    __syncthreads();
+    lds_barrier();
     if (wave < 2) v_s[which][lane] = v;
-    __syncthreads();
+    lds_barrier();
     if (wave < 2) {
         const int half = kN3Head / 2;
         if (lane < half) {
@@ -1771,7 +1811,7 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
             if (lane == 0) (which == 1 ? p.key_scales : p.value_scales)[row] = scale;
         }
     }
-    __syncthreads();
+    lds_barrier();
     // ---- kernels/src/attention.rs:53-80 (as n3_attend_kernel)
     const float query_scale = scale_s[0] * (1.0f / sqrtf((float)kN3Head));
     float peak = -INFINITY;
@@ -1810,7 +1850,7 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
         c_s[pp] = c;
         peak = fmaxf(peak, c);
     }
-    peak = n3_block_max(peak, red);
+    peak = n3_block_max<true, true>(peak, red);
     // (a thread's first position is its own: its value scale is in vsr)
     auto value_scale = [&](int pp) {
         return pp == last ? scale_s[2] : pp == tid ? vsr : pp < early ? vsc_s[pp] : vsc[pp];
@@ -1823,7 +1863,7 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
     }
     if (tid < early) vsc_s[tid] = vsr;
     __builtin_amdgcn_s_waitcnt(0);  // this wave's value chunks are in LDS (published by the barriers below)
-    cpeak = n3_block_max(cpeak, red);
+    cpeak = n3_block_max<true, true>(cpeak, red);
     // the coefficients round((e * value scale) / scale), once a position
     // (quotients<1>: rounds as the division; in acc, free until the sums)
     const float scale = cpeak / 2047.0f;
@@ -1837,7 +1877,7 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
             wgt_s[pp] = (int)__builtin_roundf(y);
         }
     }
-    __syncthreads();
+    lds_barrier();
     const int vector_count = count - count % 4;
     if (tid < 4) {
         float s = 0.0f;
@@ -1875,10 +1915,10 @@ __global__ __launch_bounds__(kN3AttendThreads) void n3_attention_kernel(N3Attent
             }
         }
     }
-    __syncthreads();  // the coefficients are read: acc takes the sums
+    lds_barrier();  // the coefficients are read: acc takes the sums
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc[pc * kN3Head + 4 * dg + k] = av[k];
-    __syncthreads();
+    lds_barrier();
     if (tid < kN3Head) {
         int sum = 0;
         for (int c = 0; c < 64; ++c) sum += acc[c * kN3Head + tid];
