@@ -439,7 +439,7 @@ int rn_matrix_multiply_vector(const rn_matrix* m, const float* x, float* y, int3
     const int rpb = gemv_rows_per_block(m->rows, m->columns, kStore);
     const int blocks = (m->rows + rpb - 1) / rpb;
     p.nseg = 1;
-    p.seg[0] = Segment{m->W, m->sW, y, acc, m->rows, 0};
+    p.seg[0] = Segment{m->W, m->sW, y, acc, m->rows};
     p.x = x;
     RN_HIP(launch_gemv(p, m->columns, kQuant, kStore, m->form, rpb, blocks, (hipStream_t)stream));
     return RN_OK;
@@ -454,7 +454,7 @@ int rn_matrix_multiply_vector_rows(const rn_matrix* m, const float* x, float* y,
     GemvParams p{};
     const int blocks = (m->rows + rows_per_block - 1) / rows_per_block;
     p.nseg = 1;
-    p.seg[0] = Segment{m->W, m->sW, y, nullptr, m->rows, 0};
+    p.seg[0] = Segment{m->W, m->sW, y, nullptr, m->rows};
     p.x = x;
     RN_HIP(launch_gemv(p, m->columns, kQuant, kStore, m->form, rows_per_block, blocks, (hipStream_t)stream));
     return RN_OK;
@@ -490,13 +490,13 @@ int rn_matrix_multiply_fused(const rn_matrix* const* ms, int count, const float*
     const int rpb = gemv_rows_per_block(total_rows, first->columns, kStore);
     GemvParams p{};
     p.nseg = count;
-    int block = 0;
+    int blocks = 0;  // per segment (grid row): the widest segment's
     for (int i = 0; i < count; ++i) {
-        p.seg[i] = Segment{ms[i]->W, ms[i]->sW, ys[i], nullptr, ms[i]->rows, block};
-        block += (ms[i]->rows + rpb - 1) / rpb;
+        p.seg[i] = Segment{ms[i]->W, ms[i]->sW, ys[i], nullptr, ms[i]->rows};
+        blocks = std::max(blocks, (ms[i]->rows + rpb - 1) / rpb);
     }
     p.x = x;
-    RN_HIP(launch_gemv(p, first->columns, kQuant, kStore, first->form, rpb, block, (hipStream_t)stream));
+    RN_HIP(launch_gemv(p, first->columns, kQuant, kStore, first->form, rpb, blocks, (hipStream_t)stream));
     return RN_OK;
 }
 
@@ -1133,7 +1133,7 @@ static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) 
         {
             GemvParams p{};
             p.nseg = 1;
-            p.seg[0] = Segment{L.out.W, L.out.sW, s->x, nullptr, d, 0};
+            p.seg[0] = Segment{L.out.W, L.out.sW, s->x, nullptr, d};
             p.x = s->attn;
             const int rpb = gemv_rows_per_block(d, d, kResidual);
             RN_PROFILED(RN_PROFILE_OUT, launch_gemv(p, d, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
@@ -1141,7 +1141,7 @@ static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) 
         {
             GemvParams p{};
             p.nseg = 1;
-            p.seg[0] = Segment{L.gate_up.W, L.gate_up.sW, s->ffh, nullptr, 2 * c.ffn, 0};
+            p.seg[0] = Segment{L.gate_up.W, L.gate_up.sW, s->ffh, nullptr, 2 * c.ffn};
             p.half_rows = c.ffn;
             p.x = s->x;
             p.gain = L.norm_ffn;
@@ -1153,7 +1153,7 @@ static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) 
             // the 2048-wide input: four waves split the columns (quantise + product + residual)
             GemvParams p{};
             p.nseg = 1;
-            p.seg[0] = Segment{L.down.W, L.down.sW, s->x, nullptr, d, 0};
+            p.seg[0] = Segment{L.down.W, L.down.sW, s->x, nullptr, d};
             p.x = s->ffh;
             RN_PROFILED(RN_PROFILE_DOWN, launch_gemv_splitk(p, c.ffn, d, st));
         }
@@ -1167,7 +1167,7 @@ static int enqueue_step(rn_session* s, bool greedy, StepProbe* probe = nullptr) 
     // 0 moves the position on; the next step's first kernel reduces the keys.
     GemvParams p{};
     p.nseg = 1;
-    p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab, 0};
+    p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab};
     p.x = s->x;
     p.gain = m->norm_final;
     p.eps = c.norm_eps;
@@ -1220,7 +1220,7 @@ int rn_session_logits(rn_session* s, float* out) {
     const rn_config& c = m->cfg;
     GemvParams p{};
     p.nseg = 1;
-    p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab, 0};
+    p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab};
     p.x = s->hidden;
     const int rpb = gemv_rows_per_block(c.vocab, c.d_model, kStore);
     RN_HIP(launch_gemv(p, c.d_model, kQuant, kStore, kPlane, rpb, (c.vocab + rpb - 1) / rpb, s->stream));
@@ -1499,7 +1499,7 @@ int rn_session_choose_allowed(rn_session* s, const uint8_t* allowed, rn_choice* 
     Choice* choice = (Choice*)((char*)s->choice_buf + align_up((size_t)c.vocab));
     GemvParams p{};
     p.nseg = 1;
-    p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab, 0};
+    p.seg[0] = Segment{m->embedding.W, m->embedding.sW, s->logits, nullptr, c.vocab};
     p.x = s->hidden;
     const int rpb = gemv_rows_per_block(c.vocab, c.d_model, kStore);
     RN_HIP(launch_gemv(p, c.d_model, kQuant, kStore, kPlane, rpb, (c.vocab + rpb - 1) / rpb, s->stream));
@@ -2511,7 +2511,7 @@ static int enqueue_whistle_step(rn_whistle* w, bool greedy) {
         {
             GemvParams p{};
             p.nseg = 1;
-            p.seg[0] = Segment{L.out.W, L.out.sW, w->x, nullptr, d, 0};
+            p.seg[0] = Segment{L.out.W, L.out.sW, w->x, nullptr, d};
             p.x = w->attn;
             const int rpb = gemv_rows_per_block(d, d, kResidual);
             RN_HIP(launch_gemv(p, d, kQuant, kResidual, kPanel, rpb, (d + rpb - 1) / rpb, st));
@@ -2528,7 +2528,7 @@ static int enqueue_whistle_step(rn_whistle* w, bool greedy) {
         {
             GemvParams p{};
             p.nseg = 1;
-            p.seg[0] = Segment{L.cross_out.W, L.cross_out.sW, w->catt, nullptr, d, 0};
+            p.seg[0] = Segment{L.cross_out.W, L.cross_out.sW, w->catt, nullptr, d};
             p.x = w->cpart;
             const int rpb = gemv_rows_per_block(d, d, kStore);
             RN_HIP(launch_gemv(p, d, kClassSum, kStore, kPanel, rpb, (d + rpb - 1) / rpb, st));
@@ -2539,7 +2539,7 @@ static int enqueue_whistle_step(rn_whistle* w, bool greedy) {
             // by the other blocks of this launch), then the FFN norm
             GemvParams p{};
             p.nseg = 1;
-            p.seg[0] = Segment{L.gate_up.W, L.gate_up.sW, w->ffh, nullptr, 2 * f, 0};
+            p.seg[0] = Segment{L.gate_up.W, L.gate_up.sW, w->ffh, nullptr, 2 * f};
             p.half_rows = f;
             p.x = w->x;
             p.attended = w->catt;
@@ -2554,7 +2554,7 @@ static int enqueue_whistle_step(rn_whistle* w, bool greedy) {
         {
             GemvParams p{};
             p.nseg = 1;
-            p.seg[0] = Segment{L.down.W, L.down.sW, w->x, nullptr, d, 0};
+            p.seg[0] = Segment{L.down.W, L.down.sW, w->x, nullptr, d};
             p.res = w->x2;
             p.x = w->ffh;
             const int rpb = gemv_rows_per_block(d, f, kResidual);
@@ -2567,7 +2567,7 @@ static int enqueue_whistle_step(rn_whistle* w, bool greedy) {
     }
     GemvParams p{};
     p.nseg = 1;
-    p.seg[0] = Segment{w->embedding.W, w->embedding.sW, w->logits, nullptr, c.vocab, 0};
+    p.seg[0] = Segment{w->embedding.W, w->embedding.sW, w->logits, nullptr, c.vocab};
     p.x = w->x;
     p.gain = w->dec_norm;
     p.eps = c.norm_eps;
@@ -2611,7 +2611,7 @@ int rn_whistle_logits(rn_whistle* w, float* out) {
     const rn_whistle_config& c = w->cfg;
     GemvParams p{};
     p.nseg = 1;
-    p.seg[0] = Segment{w->embedding.W, w->embedding.sW, w->logits, nullptr, c.vocab, 0};
+    p.seg[0] = Segment{w->embedding.W, w->embedding.sW, w->logits, nullptr, c.vocab};
     p.x = w->hidden;
     const int rpb = gemv_rows_per_block(c.vocab, c.d_model, kStore);
     RN_HIP(launch_gemv(p, c.d_model, kQuant, kStore, kPlane, rpb, (c.vocab + rpb - 1) / rpb, w->stream));

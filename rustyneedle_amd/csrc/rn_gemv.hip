@@ -47,6 +47,13 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
     // Memory-level order matters: loads complete in issue order for the wait
     // counter, so the prologue inputs go first, then the weights, then the
     // row scales; the prologue then waits only for its own inputs.
+    // The block's segment is its grid row; a segment with fewer blocks than the
+    // grid's width leaves its last blocks with rows past its end, which load
+    // the last row again and store nothing. Its fields are read with the input
+    // pointers (one argument round trip).
+    const Segment sg = p.seg[blockIdx.y];
+    const int blk = (int)blockIdx.x;
+    __builtin_amdgcn_sched_barrier(0);
     // 1a. prologue inputs
     float v[E];
     float gv[NORM ? E : 1];
@@ -83,14 +90,9 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         load_floats<E>(p.post_gain + lane * E, pg);
     }
     if constexpr (NORM) load_floats<E>(p.gain + lane * E, gv);
+    // the inputs are requested before the weights
+    __builtin_amdgcn_sched_barrier(0);
 
-    // the block's segment (after the input requests: its lookup reads further
-    // argument lines)
-    int si = 0;
-    for (int i = 1; i < p.nseg; ++i)
-        if ((int)blockIdx.x >= p.seg[i].block0) si = i;
-    const Segment sg = p.seg[si];
-    const int blk = (int)blockIdx.x - sg.block0;
 
     auto row_of = [&](int rr) -> int {
         if constexpr (EPI == kSilu) return rr < H ? blk * H + rr : p.half_rows + blk * H + (rr - H);
@@ -429,7 +431,7 @@ hipError_t launch_greedy_start(DecodeState* state, uint32_t token, int32_t pos, 
 
 template <int K, int ROWS, int PRO, int EPI, int FORM>
 static hipError_t launch_one(const GemvParams& p, int blocks, hipStream_t stream) {
-    rn_launch((gemv_kernel<K, ROWS, PRO, EPI, FORM>), dim3(blocks), dim3(64), 0, stream, p);
+    rn_launch((gemv_kernel<K, ROWS, PRO, EPI, FORM>), dim3(blocks, p.nseg), dim3(64), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -66,26 +66,27 @@ struct Segment {
     float* y;          // store target (kStore/kSilu/kArgmax) or residual x (kResidual)
     int32_t* acc;      // nullable [rows][K/32]
     int rows;          // rows of W (kSilu: 2*half_rows)
-    int block0;        // first block of this segment
 };
 constexpr int kMaxSegments = 8;
+static_assert(sizeof(Segment) == 40, "the first segment, after 24 leading bytes, ends the first 64-byte line");
 
-// The prologue's inputs come first: with the segment count they share the first
-// 64 bytes of the argument segment (one scalar-cache line), so a block requests
-// its input vector after one argument load.
+// The prologue's input and the first segment share the first 64 bytes of the
+// argument segment (one scalar-cache line). Segment s is grid row y = s, so a
+// block reads its segment at an address known when it starts: it requests its
+// input vector and its weights after one argument load.
 struct GemvParams {
     const float* x;       // input vector (kQuant/kNorm)
     const float* gain;    // zero-centred norm gains (kNorm/kEmbedNorm)
+    int nseg;
+    int half_rows;        // kSilu: ffn width (gate rows 0..half-1, up rows half..2*half-1)
+    Segment seg[kMaxSegments];
     const float* attended;     // kCrossNorm: the cross-attention output and its post-norm gains
     const float* post_gain;
     DecodeState* state;   // kEmbedNorm: the token to embed
-    int nseg;
-    int half_rows;        // kSilu: ffn width (gate rows 0..half-1, up rows half..2*half-1)
     float eps;
     float cross_gain;
     const int8_t* xq;     // kCodes: pre-quantised input
     const float* xs;
-    Segment seg[kMaxSegments];
     const int8_t* embW;   // kEmbedNorm: embedding codes/scales, the token comes from state
     const float* embS;
     float embed_scale;    // sqrt(d_model)
@@ -97,7 +98,8 @@ struct GemvParams {
     const float* res;     // kResidual: the residual read (nullable: the stored row itself)
 };
 
-// Launch one batch-1 product. `columns` in {512, 1024, 2048}; returns
+// Launch one batch-1 product: `blocks` blocks for each of the p.nseg segments
+// (grid rows). `columns` in {384, 512, 1024, 1536, 2048}; returns
 // hipErrorInvalidValue for an unsupported combination.
 hipError_t launch_gemv(const GemvParams& p, int columns, int prologue, int epilogue, int form,
                        int rows_per_block, int blocks, hipStream_t stream);
