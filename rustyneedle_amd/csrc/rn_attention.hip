@@ -29,15 +29,6 @@ namespace rn {
 constexpr int kHeadDim = 64;
 constexpr int kClasses = 32;  // T3 position classes (p mod 32)
 
-__device__ __forceinline__ void unpack8(const uint4& raw, float* out) {
-    const __half2* h = reinterpret_cast<const __half2*>(&raw);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        out[2 * i] = __low2float(h[i]);
-        out[2 * i + 1] = __high2float(h[i]);
-    }
-}
-
 // DPV consecutive fp16 values of one value row: the load type and its floats
 template <int DPV> struct ValuePiece;
 template <> struct ValuePiece<8> { using T = uint4; };
@@ -432,22 +423,11 @@ __global__ __launch_bounds__(256) void attend_prefill_tile_kernel(AttendParams p
         for (int pass = 0; pass < kTileRows && c0 + pass < L; pass += NT / 4) {
             const int pp = c0 + pass + r;
             const uint4* kr = reinterpret_cast<const uint4*>(k_s + (pass + r) * kHeadDim + 16 * li);
-            float k[16];
-            unpack8(kr[0], k);
-            unpack8(kr[1], k + 8);
+            const uint4 ka = kr[0], kb = kr[1];
 #pragma unroll
             for (int q = 0; q < QT; ++q) {
-                float part[4];
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    float sum = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) sum = sum + qr[q][4 * jj + i] * k[4 * jj + i];
-                    part[jj] = sum;
-                }
-                float sc = (part[0] + part[1]) + (part[2] + part[3]);
-                sc = sc + __int_as_float(dpp_move<0xb1>(__float_as_int(sc)));  // lane ^ 1
-                sc = sc + __int_as_float(dpp_move<0x4e>(__float_as_int(sc)));  // lane ^ 2
+                // the fp16 keys multiply in place (v_fma_mix_f32: the exact product rounded once)
+                const float sc = score_row(qr[q], ka, kb);
                 if (li == 0 && pp < len[q]) scores[q * stride + pp] = sc * inverse_root;
             }
         }
@@ -483,26 +463,29 @@ __global__ __launch_bounds__(256) void attend_prefill_tile_kernel(AttendParams p
         // positions every query of the tile attends, then the tile's last QT - 1
         const int all = min(c0 + kTileRows, len[0]), end = min(c0 + kTileRows, L);
         int pp = c0 + j;
+        // e times the fp16 value by v_fma_mix_f32 (the exact product rounded once)
+        auto weigh = [&](float (&a)[8], float e, const uint4& raw) {
+            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                a[i] = a[i] + ((i & 1) ? mul_f16<true>(e, w[i / 2]) : mul_f16<false>(e, w[i / 2]));
+        };
         for (; pp < all; pp += kClasses) {
-            float vv[8];
-            unpack8(*reinterpret_cast<const uint4*>(v_s + (pp - c0) * kHeadDim + 8 * dg), vv);
+            const uint4 raw = *reinterpret_cast<const uint4*>(v_s + (pp - c0) * kHeadDim + 8 * dg);
 #pragma unroll
             for (int q = 0; q < QT; ++q) {
                 const float e = scores[q * stride + pp];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc[q][i] = acc[q][i] + e * vv[i];
+                weigh(acc[q], e, raw);
                 total[q] = total[q] + e;
             }
         }
         for (; pp < end; pp += kClasses) {
-            float vv[8];
-            unpack8(*reinterpret_cast<const uint4*>(v_s + (pp - c0) * kHeadDim + 8 * dg), vv);
+            const uint4 raw = *reinterpret_cast<const uint4*>(v_s + (pp - c0) * kHeadDim + 8 * dg);
 #pragma unroll
             for (int q = 0; q < QT; ++q) {
                 if (pp < len[q]) {
                     const float e = scores[q * stride + pp];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) acc[q][i] = acc[q][i] + e * vv[i];
+                    weigh(acc[q], e, raw);
                     total[q] = total[q] + e;
                 }
             }
