@@ -2,8 +2,8 @@
 checked against the defining divisions of ops.rs:103-118 in IEEE float32:
 
 - quotients: multiply by v_rcp_f32(scale), which is within 1 ulp of 1/scale, and
-  fall back to the division near a rounding boundary or for scales outside
-  [2^-100, 2^100]. Restated in numpy for each of the three reciprocals a 1-ulp
+  fall back to the division near a rounding boundary (|fract(y) - 0.5| at most
+  fma(|y|, 2^-21, 2^-30)) or for scales outside [2^-100, 2^100]. Restated in numpy for each of the three reciprocals a 1-ulp
   error allows, on random and adversarial inputs (quotients within a few ulps of
   every half-integer) for scales over sixty decades;
 - int8_scale_from_peak: peak / 127 as q0 = peak * RN(1/127) plus one fma
@@ -26,9 +26,14 @@ def reciprocal_rule(v: np.ndarray, s: np.float32, ulps: int = 0) -> np.ndarray:
     for _ in range(abs(ulps)):
         r = np.nextafter(r, f32(np.inf) if ulps > 0 else f32(-np.inf))
     y = (v * r).astype(f32)
-    h = (np.floor(y) + f32(0.5)).astype(f32)
-    thr = (np.abs(y) * f32(2.0 ** -21) + f32(2.0 ** -30)).astype(f32)
-    near = np.abs((y - h).astype(f32)) <= thr
+    # the device's test: d = v_fract_f32(y) - 0.5 (the fraction y - floor(y),
+    # held below 1.0 as v_fract_f32 holds it), against fma(|y|, 2^-21, 2^-30),
+    # one rounding (the float64 sum is exact: |y| * 2^-21 is a power-of-two
+    # scaling); for |y| >= 2^23 the fraction is 0 and d = -0.5, never near
+    frac = np.minimum((y - np.floor(y)).astype(f32), f32(np.nextafter(f32(1), f32(0))))
+    d = (frac - f32(0.5)).astype(f32)
+    thr = (np.abs(y).astype(np.float64) * 2.0 ** -21 + 2.0 ** -30).astype(f32)
+    near = np.abs(d) <= thr
     if not (f32(2.0 ** -100) <= s <= f32(2.0 ** 100)):
         near = np.ones_like(near)
     # per element: the device sends a whole wave to the division when any lane
