@@ -110,9 +110,12 @@ def test_multiply_vector_edge_inputs():
         assert np.array_equal(acc, acco[0]) and np.array_equal(y.view(np.uint32), yo[0].view(np.uint32))
 
 
-def test_multiply_fused_matches_separate():
+@pytest.mark.parametrize("rows", [(512, 128, 128, 512), (37, 1000, 200), (3, 2048)])
+def test_multiply_fused_matches_separate(rows):
+    # each matrix is a grid row of one launch; a matrix with fewer blocks than
+    # the widest leaves spare blocks, which must store nothing
     rng = np.random.default_rng(9)
-    mats = [_matrix(rng, r, 512) for r in (512, 128, 128, 512)]
+    mats = [_matrix(rng, r, 512) for r in rows]
     x = rng.standard_normal(512).astype(np.float32)
     qm = [rn.QuantisedMatrix(W, sW) for W, sW in mats]
     ys = rn.multiply_fused_host(qm, x)
