@@ -231,11 +231,19 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Cross-lane moves inside rows of 16 lanes (DPP: no LDS round trip). CTRL:
-// quad_perm [1,0,3,2] = 0xb1, quad_perm [2,3,0,1] = 0x4e, row_half_mirror =
-// 0x141, row_mirror = 0x140. A lane whose source is invalid keeps its value.
+// quad_perm [1,0,3,2] = 0xb1, quad_perm [2,3,0,1] = 0x4e, the quad broadcasts
+// 0x00, 0x55, 0xaa, 0xff, row_ror 4 / 8 / 12 = 0x124 / 0x128 / 0x12c,
+// row_half_mirror = 0x141, row_mirror = 0x140: every lane has a source lane in
+// its row, which must be active. The move carries no old value (a lane whose
+// source were disabled would read 0), so the compiler folds it into the
+// instruction that consumes it (v_add_f32_dpp and the like: no separate move
+// and no wait states between them).
 template <int CTRL>
 __device__ __forceinline__ int dpp_move(int v) {
-    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+    static_assert((CTRL >= 0x00 && CTRL <= 0xff) || CTRL == 0x124 || CTRL == 0x128 || CTRL == 0x12c ||
+                      CTRL == 0x140 || CTRL == 0x141,
+                  "controls whose every lane has a source in its row");
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
 }
 __device__ __forceinline__ float lane_float(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
