@@ -340,19 +340,26 @@ __device__ __forceinline__ float sum_lanes_0_to_7(float s) {
     return total;
 }
 
+// -0.0 in a register the compiler cannot see into: with a literal -0.0 it
+// would turn fma(x, h, -0) back into a conversion and a multiply.
+__device__ __forceinline__ float opaque_negative_zero() {
+    float z;
+    asm("v_mov_b32 %0, 0x80000000" : "=v"(z));
+    return z;
+}
+
 // x times the f16 in the low (HI false) or high half of `packed`, as one
-// v_fma_mix_f32 with a -0.0 addend instead of a conversion and a multiply.
+// v_fma_mix_f32 with a -0.0 addend instead of a conversion and a multiply (the
+// compiler selects it from the fma of the widened half, with op_sel for the
+// high half, and schedules it as its own instruction, not an opaque asm).
 // The f16 operand widens exactly, and fma(x, h, -0) = RN(x h + (-0)) = RN(x h)
 // for every operand (a zero product keeps its sign: +0 + -0 = +0, -0 + -0 =
-// -0; NaN and infinities pass through), so the result is the product's bits.
+// -0; NaN and infinities pass through), so the result is the product's bits
+// whichever instructions compute it.
 template <bool HI>
 __device__ __forceinline__ float mul_f16(float x, uint32_t packed) {
-    float d;
-    if constexpr (HI)
-        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(d) : "v"(x), "v"(packed), "v"(-0.0f));
-    else
-        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(d) : "v"(x), "v"(packed), "v"(-0.0f));
-    return d;
+    const unsigned short bits = HI ? (unsigned short)(packed >> 16) : (unsigned short)(packed & 0xffffu);
+    return __builtin_fmaf(x, __half2float(__ushort_as_half(bits)), opaque_negative_zero());
 }
 
 // Four int8 x int8 products added to an int32 accumulator (v_dot4_i32_i8).
