@@ -747,6 +747,17 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
             const int idx = lane * E + e;
             sq_s[(idx % 8) * (K / 8) + idx / 8] = v[e] * v[e];
         }
+        // the gained values m = (1 + g) x and their peak while the squares'
+        // LDS writes complete: the normed value is fl(m * inverse) with
+        // inverse > 0 and rounding is monotone, so the normed peak is
+        // fl(peak(|m|) * inverse)
+        float peak = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            v[e] = (1.0f + gv[e]) * v[e];
+            peak = fmaxf(peak, fabsf(v[e]));
+        }
+        peak = wave_max_nonneg(peak);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -768,12 +779,8 @@ __global__ __launch_bounds__(512) void qkv_attend_kernel(QkvAttendParams p) {
         total = total + 0.0f;  // the (empty) tail of ops.rs:15-16
         const float inverse = reciprocal(sqrtf(total / (float)K + p.eps));
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = ((1.0f + gv[e]) * v[e]) * inverse;
-        float peak = 0.0f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
-        peak = wave_max_nonneg(peak);
-        const float sx = int8_scale_from_peak(peak);
+        for (int e = 0; e < E; ++e) v[e] = v[e] * inverse;
+        const float sx = int8_scale_from_peak(peak * inverse);
         float y[E];
         quotients<E>(v, sx, y);
 #pragma unroll

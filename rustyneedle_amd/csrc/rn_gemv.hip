@@ -152,11 +152,24 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         // j, j+8, j+16, ... in index order. Squares are stored transposed
         // (strided lane j's run is contiguous) so each of the eight lanes reads
         // its run with 128-bit reads. Returns 1 / sqrt(mean square + eps).
-        auto norm_inverse = [&](const float* vals) -> float {
+        // GAINED: vals become the gained values m = (1 + g) x and *peak their
+        // wave peak |m|, formed while the squares' LDS writes complete (the
+        // normed value is fl(m * inverse) with inverse > 0 and rounding is
+        // monotone, so the normed peak is fl(peak(|m|) * inverse)).
+        auto norm_inverse = [&](float* vals, const float* gains, float* peak) -> float {
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 const int idx = lane * E + e;
                 sq_s[(idx % 8) * (K / 8) + idx / 8] = vals[e] * vals[e];
+            }
+            if (gains != nullptr) {
+                float pk = 0.0f;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    vals[e] = (1.0f + gains[e]) * vals[e];
+                    pk = fmaxf(pk, fabsf(vals[e]));
+                }
+                *peak = wave_max_nonneg(pk);
             }
             wave_lds_sync();
             float s = 0.0f;
@@ -187,7 +200,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
         }
         if constexpr (PRO == kCrossNorm) {
             // cross.rs:176-181: x += cross_gain * zero_centred_norm(attended, post_gain)
-            const float inverse = norm_inverse(av);
+            const float inverse = norm_inverse(av, nullptr, nullptr);
 #pragma unroll
             for (int e = 0; e < E; ++e) v[e] = v[e] + p.cross_gain * (((1.0f + pg[e]) * av[e]) * inverse);
             if (blockIdx.x == 0)
@@ -195,18 +208,20 @@ __global__ __launch_bounds__(64) void gemv_kernel(GemvParams p) {
                 for (int e = 0; e < E; ++e) p.x_out[lane * E + e] = v[e];
             wave_lds_sync();  // the runs are read before the next squares replace them
         }
+        float peak = 0.0f;
         if constexpr (NORM) {
-            const float inverse = norm_inverse(v);
+            const float inverse = norm_inverse(v, gv, &peak);
 #pragma unroll
-            for (int e = 0; e < E; ++e) v[e] = ((1.0f + gv[e]) * v[e]) * inverse;
+            for (int e = 0; e < E; ++e) v[e] = v[e] * inverse;
             if (p.hidden_out != nullptr && blockIdx.x == 0)
 #pragma unroll
                 for (int e = 0; e < E; ++e) p.hidden_out[lane * E + e] = v[e];
-        }
-        float peak = 0.0f;
+            peak = peak * inverse;
+        } else {
 #pragma unroll
-        for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
-        peak = wave_max_nonneg(peak);
+            for (int e = 0; e < E; ++e) peak = fmaxf(peak, fabsf(v[e]));
+            peak = wave_max_nonneg(peak);
+        }
         sx = int8_scale_from_peak(peak);
         float y[E];
         quotients<E>(v, sx, y);
