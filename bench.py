@@ -51,11 +51,11 @@ KERNEL_NAMES = {
 # (FETCH x2.000, WRITE x1.000). Recorded in profiles/decode_b1_needle20_traffic.md;
 # they describe the kernels as built when measured and are re-measured with them.
 PMC_TRAFFIC = {
-    "qkv_attention": 1_836_840,  # 20-launch mean: 19 x 1,832,668 (layers 1-19) + 1,916,111 (layer 0)
-    "out": 391_107,
-    "gate_up": 2_495_093,
-    "down": 1_338_156,
-    "logits": 4_891_084,
+    "qkv_attention": 1_833_616,  # 20-launch mean: 19 x 1,829,898 (layers 1-19) + 1,904,262 (layer 0)
+    "out": 378_887,
+    "gate_up": 2_493_441,
+    "down": 1_338_368,
+    "logits": 4_907_168,
 }
 
 
