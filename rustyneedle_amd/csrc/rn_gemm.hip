@@ -887,9 +887,9 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
                                                             int8_t* codes, float* scales, float* normed,
                                                             size_t x_stride) {
     constexpr int n = NV * 128;
-    extern __shared__ float sq_s[];  // [4][n + 32] when gain != nullptr
+    extern __shared__ float sq_s[];  // [waves][n + 32] when gain != nullptr
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + wave;
+    const int row = blockIdx.x * (blockDim.x >> 6) + wave;
     const bool live = row < count;
     const float2* src = reinterpret_cast<const float2*>(x + (size_t)(live ? row : count - 1) * x_stride);
     float2 v[NV];
@@ -975,8 +975,9 @@ __global__ __launch_bounds__(256) void norm_quantise_kernel(const float* x, cons
 hipError_t launch_norm_quantise(const float* x, const float* gain, int count, int n, float eps, int8_t* codes,
                                 float* scales, float* normed, hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    const size_t lds = gain != nullptr ? 4 * sizeof(float) * (size_t)(n + 32) : 0;
-    const dim3 grid((count + 3) / 4), block(256);
+    // one row a block: the rows' loads spread over as many CUs as there are rows
+    const size_t lds = gain != nullptr ? sizeof(float) * (size_t)(n + 32) : 0;
+    const dim3 grid(count), block(64);
 #define RN_NQ(NV) \
     rn_launch(norm_quantise_kernel<NV>, grid, block, lds, stream, x, gain, count, eps, codes, scales, normed, (size_t)n)
     switch (n) {
@@ -995,7 +996,7 @@ hipError_t launch_norm_quantise(const float* x, const float* gain, int count, in
 hipError_t launch_quantise_strided(const float* x, size_t x_stride, int count, int n, int8_t* codes, float* scales,
                                    hipStream_t stream) {
     if (count <= 0) return hipSuccess;
-    const dim3 grid((count + 3) / 4), block(256);
+    const dim3 grid(count), block(64);
     const float* no_gain = nullptr;
     float* no_normed = nullptr;
 #define RN_QS(NV) \
