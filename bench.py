@@ -413,14 +413,26 @@ def bench_needle3(rn, with_cpu: bool = True, context: int = 600, steps: int = 64
                                    "prefill of 4000 tokens about 1800 tokens/s; on an Apple M1 Max "
                                    "(docs/architecture.md, Performance)")
     if with_cpu:
+        # the reference's pool policy, min(cores - 1, 6) threads (pool.rs:48-52):
+        # the oracle splits its row products over them; one thread beside it
+        cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count() or 1
+        threads = max(1, min(cores - 1, 6))
+
+        def pushes(n_threads: int) -> float:
+            oracle.set_threads(n_threads)
+            cs = om.session(24)
+            t = time.perf_counter()
+            for tok in prompt[:16]:
+                cs.push(int(tok))
+            return (time.perf_counter() - t) / 16
+
+        single = pushes(1)
+        dt = pushes(threads)
         oracle.set_threads(1)
-        cs = om.session(24)
-        t = time.perf_counter()
-        for tok in prompt[:16]:
-            cs.push(int(tok))
-        dt = (time.perf_counter() - t) / 16
-        out["cpu"] = dict(ms_per_push=dt * 1e3, tokens_per_s=1.0 / dt, cores=1, kind="port",
-                          sample="16 pushes from an empty session, C oracle on one thread")
+        out["cpu"] = dict(ms_per_push=dt * 1e3, tokens_per_s=1.0 / dt, cores=threads, kind="port",
+                          single_thread_tokens_per_s=1.0 / single,
+                          sample=f"16 pushes from an empty session, C oracle on {threads} threads "
+                                 f"(row products split over them) of {cores} host cores")
     return out
 
 

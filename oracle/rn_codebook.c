@@ -141,7 +141,7 @@ void ro_codebook_product(const uint8_t* packed, const uint16_t* norms, int rows,
                          const float* xscales, int count, float* y, int32_t* acc) {
     const int ib = index_bits(bits), groups = padded / group;
     const size_t row_bytes = (size_t)padded * ib / 8;
-#pragma omp parallel for schedule(static) if ((size_t)rows * padded * count >= (1u << 22))
+#pragma omp parallel for schedule(static) num_threads(ro_get_threads()) if ((size_t)rows * padded * count >= (1u << 18))
     for (int r = 0; r < rows; ++r) {
         const uint8_t* row = packed + (size_t)r * row_bytes;
         for (int t = 0; t < count; ++t) {
@@ -218,7 +218,7 @@ void ro_codebook_float_vector(const uint8_t* packed, const uint16_t* norms, int 
                               const float levels[16], const float* rotated, int count, float* y) {
     const int ib = index_bits(bits), groups = padded / group;
     const size_t row_bytes = (size_t)padded * ib / 8;
-#pragma omp parallel for schedule(static) if ((size_t)rows * padded * count >= (1u << 22))
+#pragma omp parallel for schedule(static) num_threads(ro_get_threads()) if ((size_t)rows * padded * count >= (1u << 18))
     for (int r = 0; r < rows; ++r) {
         const uint8_t* row = packed + (size_t)r * row_bytes;
         for (int t = 0; t < count; ++t) {
@@ -240,7 +240,7 @@ void ro_codebook_float_batch(const uint8_t* packed, const uint16_t* norms, int r
                              const float levels[16], const float* rotated, int count, float* y) {
     const int ib = index_bits(bits), groups = padded / group;
     const size_t row_bytes = (size_t)padded * ib / 8;
-#pragma omp parallel for schedule(static) if ((size_t)rows * padded * count >= (1u << 22))
+#pragma omp parallel for schedule(static) num_threads(ro_get_threads()) if ((size_t)rows * padded * count >= (1u << 18))
     for (int r = 0; r < rows; ++r) {
         const uint8_t* row = packed + (size_t)r * row_bytes;
         float* w = (float*)malloc((size_t)padded * sizeof(float));
